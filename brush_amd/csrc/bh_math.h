@@ -1,0 +1,155 @@
+/*
+ * bh_math.h — reproducible scalar float primitives shared by the gfx950
+ * kernels and the CPU restatement.
+ *
+ * Why this exists: the rasterizer's integer outputs (visibility, per-splat
+ * tile counts, tile ids, sort keys, tile offsets) are decided by float
+ * comparisons that sit downstream of exp() and log() (sigmoid of the raw
+ * opacity, exp of the log-scales, ln(255 * opacity) power threshold,
+ * brush-render/src/kernels/project_forward.rs:82-133,
+ * brush-render/src/kernels/helpers.rs:87-97,241-280).  Vendor libm and the
+ * device math library each round exp/log their own way, so the only way for a
+ * CPU checker and the GPU to agree bit for bit is to evaluate both functions
+ * with the same sequence of correctly rounded IEEE-754 operations
+ * (+, -, *, /, fma).  Every function here uses only those, plus integer bit
+ * manipulation, and the translation units that include this header are
+ * compiled without floating-point contraction (-ffp-contract=off), so gcc on
+ * x86-64 (SSE, FLT_EVAL_METHOD == 0) and hipcc for gfx950 (IEEE mode,
+ * f32 denormals kept, correctly rounded division) produce identical bits.
+ *
+ * Methods:
+ *   bh_expf — Cody & Waite argument reduction x = n ln2 + r with a two-part
+ *             ln2 (hi part with 15 significant bits, so n*ln2_hi is exact for
+ *             |n| <= 2^8), then the degree-7 Taylor polynomial of e^r on
+ *             |r| <= ln2/2 (truncation error < 0.05 ulp), scaled by 2^n.
+ *   bh_logf — x = 2^e m with m in [sqrt(1/2), sqrt(2)), f = m - 1,
+ *             s = f / (2 + f), log(1+f) = 2 atanh(s) = f - s (f - R) with
+ *             R = sum_{k>=1} 2 s^{2k} / (2k+1) truncated after s^8 (the
+ *             rearrangement used by the classic BSD/fdlibm logf), plus e ln2.
+ * Both stay within 2 ulp of the correctly rounded result over all finite
+ * inputs (pinned on the CPU against float64 libm by tests/test_math.py).
+ *
+ * This header is plain C99 so the CPU restatement (gcc) can include it; under
+ * hipcc every function is callable from host and device.
+ */
+#ifndef BH_MATH_H
+#define BH_MATH_H
+
+#include <stdint.h>
+
+#if defined(__HIPCC__)
+#define BH_HD __host__ __device__ static inline
+#else
+#define BH_HD static inline
+#include <math.h>
+#endif
+
+#define BH_INF_BITS 0x7f800000u
+#define BH_NAN_BITS 0x7fc00000u
+
+BH_HD uint32_t bh_as_uint(float x) {
+    uint32_t u;
+    __builtin_memcpy(&u, &x, sizeof(u));
+    return u;
+}
+
+BH_HD float bh_as_float(uint32_t u) {
+    float x;
+    __builtin_memcpy(&x, &u, sizeof(x));
+    return x;
+}
+
+/* Bit-level finiteness: NaN and +-Inf have an all-ones exponent
+ * (brush-cube/src/lib.rs:626-630). */
+BH_HD int bh_is_finite(float x) { return ((bh_as_uint(x) >> 23) & 0xFFu) != 0xFFu; }
+
+/* min/max with a fixed NaN rule so both sides agree: the first operand is
+ * returned unless the second compares strictly smaller (larger). */
+BH_HD float bh_minf(float a, float b) { return (b < a) ? b : a; }
+BH_HD float bh_maxf(float a, float b) { return (b > a) ? b : a; }
+BH_HD float bh_clampf(float x, float lo, float hi) { return bh_minf(bh_maxf(x, lo), hi); }
+BH_HD float bh_absf(float x) { return bh_as_float(bh_as_uint(x) & 0x7fffffffu); }
+
+BH_HD float bh_fmaf(float a, float b, float c) {
+#if defined(__HIPCC__)
+    return __builtin_fmaf(a, b, c);
+#else
+    return fmaf(a, b, c);
+#endif
+}
+
+/* Multiply p by 2^n for n in [-150, 128] with IEEE rounding. */
+BH_HD float bh_scale_pow2(float p, int n) {
+    if (n > 127) {
+        p = p * 2.0f;
+        n -= 1;
+    }
+    if (n < -126) {
+        p = p * bh_as_float((uint32_t)(n + 24 + 127) << 23);
+        return p * 5.9604644775390625e-08f; /* 2^-24 */
+    }
+    return p * bh_as_float((uint32_t)(n + 127) << 23);
+}
+
+BH_HD float bh_expf(float x) {
+    if (!(x == x)) return x; /* NaN propagates */
+    if (x > 89.0f) return bh_as_float(BH_INF_BITS);
+    if (x < -104.0f) return 0.0f;
+    const float log2e = 1.44269502162933349609375f;
+    const float ln2_hi = 0.693145751953125f;        /* 0x3f317200 */
+    const float ln2_lo = 1.428606765330187045e-06f; /* 0x35bfbe8e */
+    const float shifter = 12582912.0f;              /* 1.5 * 2^23: round to nearest even */
+    float k = x * log2e;
+    float kr = (k + shifter) - shifter;
+    int n = (int)kr;
+    float r = bh_fmaf(kr, -ln2_hi, x);
+    r = bh_fmaf(kr, -ln2_lo, r);
+    /* e^r = sum r^i / i!, i = 0..7, Horner form */
+    float p = 1.98412698412698413e-04f; /* 1/5040 */
+    p = bh_fmaf(p, r, 1.38888888888888889e-03f); /* 1/720 */
+    p = bh_fmaf(p, r, 8.33333333333333333e-03f); /* 1/120 */
+    p = bh_fmaf(p, r, 4.16666666666666667e-02f); /* 1/24 */
+    p = bh_fmaf(p, r, 1.66666666666666667e-01f); /* 1/6 */
+    p = bh_fmaf(p, r, 0.5f);
+    p = bh_fmaf(p, r, 1.0f);
+    p = bh_fmaf(p, r, 1.0f);
+    return bh_scale_pow2(p, n);
+}
+
+BH_HD float bh_logf(float x) {
+    if (!(x == x)) return x;
+    if (x < 0.0f) return bh_as_float(BH_NAN_BITS);
+    if (x == 0.0f) return -bh_as_float(BH_INF_BITS);
+    uint32_t bits = bh_as_uint(x);
+    if (bits == BH_INF_BITS) return x;
+    int e = 0;
+    if (bits < 0x00800000u) { /* subnormal: renormalise exactly */
+        x = x * 33554432.0f;  /* 2^25 */
+        bits = bh_as_uint(x);
+        e = -25;
+    }
+    e += (int)(bits >> 23) - 127;
+    float m = bh_as_float((bits & 0x007fffffu) | 0x3f800000u); /* [1, 2) */
+    if (m > 1.41421353816986083984375f) {
+        m = m * 0.5f;
+        e += 1;
+    }
+    float f = m - 1.0f; /* exact */
+    float s = f / (2.0f + f);
+    float s2 = s * s;
+    float t = 2.22222222222222222e-01f;          /* 2/9 */
+    t = bh_fmaf(t, s2, 2.85714285714285714e-01f); /* 2/7 */
+    t = bh_fmaf(t, s2, 4.0e-01f);                 /* 2/5 */
+    t = bh_fmaf(t, s2, 6.66666666666666667e-01f); /* 2/3 */
+    float R = t * s2;
+    float logm = f - s * (f - R);
+    const float ln2_hi = 0.693145751953125f;
+    const float ln2_lo = 1.428606765330187045e-06f;
+    float ef = (float)e;
+    return ef * ln2_hi + (ef * ln2_lo + logm);
+}
+
+/* 1 / (1 + e^-x)  (brush-cube/src/lib.rs:620-623) */
+BH_HD float bh_sigmoidf(float x) { return 1.0f / (1.0f + bh_expf(-x)); }
+
+#endif /* BH_MATH_H */

@@ -1,0 +1,229 @@
+/*
+ * brush_hip.h — C ABI of the gfx950 differentiable tile rasterizer.
+ *
+ * This is the drop-in boundary for Brush's rasterizer path.  Each entry
+ * point replaces one operation of the reference's Burn backend extension and
+ * takes plain device pointers and sizes (no framework types), so a Rust
+ * `-sys` crate, Python ctypes or C++ can bind it.  Device pointers are
+ * ordinary HIP device allocations on the context's device; every call is
+ * stream-ordered on the context's stream.
+ *
+ * Layouts are the reference's row-major contiguous layouts
+ * (brush-render/src/render.rs:103-110):
+ *   transforms      f32 [N,10]  means xyz | quat wxyz | log-scales xyz
+ *                   (brush-render/src/gaussian_splats.rs:110-127)
+ *   sh_coeffs       f32 [N,C,3] C = (degree+1)^2, coefficient-major, rgb inner
+ *   raw_opacities   f32 [N]     logits
+ *   projected       f32 [V,10]  x y | conic c00 c01 c11 | opacity | r g b | depth
+ *                   (brush-render/src/kernels/helpers.rs:192-196)
+ *   v_combined      f32 [V,11]  dx dy | dc00 dc01 dc11 | dr dg db | dalpha |
+ *                   refine | ddepth
+ *                   (brush-render-bwd/src/kernels/rasterize_backwards.rs:28-40)
+ *   tile_offsets    u32 [TY,TX,2] [start, end) per 16x16 tile
+ *   out_img         f32 [H,W,4] (or [H,W,5] with depth) when BH_FLAG_BWD_INFO,
+ *                   otherwise u32 [H,W] packed r|g<<8|b<<16|a<<24
+ *
+ * Errors: every entry point returns a bh_status and never aborts.  The text
+ * of the last error on a context is available from bh_last_error().
+ * A context is externally synchronised: do not call into one context from two
+ * threads at once.
+ */
+#ifndef BRUSH_HIP_H
+#define BRUSH_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum bh_status {
+    BH_OK = 0,
+    BH_ERR_INVALID_ARG = 1, /* null pointer, zero image size, bad flag       */
+    BH_ERR_SHAPE = 2,       /* sizes inconsistent with each other            */
+    BH_ERR_OOM = 3,         /* device allocation failed                      */
+    BH_ERR_DEVICE = 4,      /* a HIP runtime call failed                     */
+    BH_ERR_INTERNAL = 5,    /* a kernel reported a broken invariant          */
+    BH_ERR_NOT_FINITE = 6   /* non-finite value where the reference panics   */
+} bh_status;
+
+/* Render flags.  BWD_INFO and SMOOTH_CUTOFF together encode the reference's
+ * RasterPass {Forward, Backward, BackwardSmoothCutoff}
+ * (brush-render/src/gaussian_splats.rs:43-66); RENDER_DEPTH is
+ * RasterizationMode::RgbaAndDepth (:24-40); MIP is SplatRenderMode::Mip. */
+#define BH_FLAG_BWD_INFO 1u
+#define BH_FLAG_SMOOTH_CUTOFF 2u
+#define BH_FLAG_RENDER_DEPTH 4u
+#define BH_FLAG_MIP 8u
+/* Backward-only flag: accumulate the refine weight lane (v_combined[:,9]). */
+#define BH_FLAG_REFINE_WEIGHT 16u
+
+#define BH_TILE_WIDTH 16u
+#define BH_PROJECTED_LANES 10u
+#define BH_COMPACT_GRAD_LANES 11u
+
+/* Mirrors ProjectUniforms (brush-render/src/kernels/types.rs:53-83 and
+ * brush-render/src/shaders.rs:19-67).  viewmat is the top 3 rows of the
+ * world-to-camera matrix, column-major: column i is viewmat[3i..3i+2], column 3
+ * is the translation.  Build it with the host helpers of the Python package
+ * (camera.rs:63-119,200-254 restated). */
+typedef struct bh_project_uniforms {
+    float viewmat[12];
+    float half_max_render_fov;
+    float fx, fy, cx, cy;
+    float lim_pos_x, lim_pos_y, lim_neg_x, lim_neg_y;
+    float camera_pos[3];
+    uint32_t img_w, img_h;
+    uint32_t tile_bw, tile_bh;
+    uint32_t sh_degree;
+    uint32_t total_splats;
+    uint32_t num_visible; /* filled in by the forward pass */
+} bh_project_uniforms;
+
+typedef struct bh_ctx bh_ctx;
+typedef struct bh_fwd_state bh_fwd_state;
+
+/* Device pointers and counts of one forward pass (RenderOutput and
+ * RenderAuxInner, brush-render/src/render_aux.rs:17-68).  Buffers sized by a
+ * count are allocated with max(count, 1) rows like the reference
+ * (render.rs:337,373).  They stay valid until bh_fwd_state_release(). */
+typedef struct bh_fwd_info {
+    uint32_t num_splats;
+    uint32_t num_visible;
+    uint32_t num_intersections;
+    uint32_t num_tiles;
+    uint32_t tile_bw, tile_bh;
+    uint32_t img_w, img_h;
+    uint32_t sh_degree;
+    uint32_t flags;
+    bh_project_uniforms uniforms;      /* num_visible filled in              */
+    const float* projected;            /* [V,10] in depth (compact) order    */
+    const uint32_t* global_from_compact_gid; /* [V] depth-sorted global ids  */
+    const float* depths;               /* [V] ascending view-space depths    */
+    const uint32_t* intersect_counts;  /* [N] tiles hit per global id        */
+    const uint32_t* cum_tiles_hit;     /* [V] inclusive scan, compact order  */
+    const uint32_t* tile_id_from_isect;      /* [M] tile-sorted tile ids     */
+    const uint32_t* compact_gid_from_isect;  /* [M] tile-sorted compact ids  */
+    const uint32_t* tile_offsets_pre;  /* [TY,TX,2] before rasterize shrinks */
+} bh_fwd_info;
+
+/* ---- context ------------------------------------------------------------ */
+
+/* Create a context on HIP device `device` with the null stream.
+ * No counterpart in the reference (the reference's device is a Burn
+ * WgpuDevice, brush-process/src/lib.rs:34-39). */
+bh_status bh_ctx_create(int device, bh_ctx** out);
+void bh_ctx_destroy(bh_ctx* ctx);
+/* Use `hip_stream` (a hipStream_t) for all later work.  If it differs from the
+ * current stream, the current stream is synchronised first so that cached
+ * workspace is not reused across streams. */
+bh_status bh_ctx_set_stream(bh_ctx* ctx, void* hip_stream);
+const char* bh_last_error(const bh_ctx* ctx);
+/* Kernel timing with HIP events on the context's stream (for benchmarking).
+ * When enabled, every launch is bracketed by events and its duration is
+ * accumulated per kernel name. */
+bh_status bh_ctx_set_timing(bh_ctx* ctx, int enable);
+typedef struct bh_kernel_timing {
+    char name[48];
+    uint32_t launches;
+    double total_ms;
+} bh_kernel_timing;
+/* Synchronises the stream, then copies up to `max` entries. */
+bh_status bh_ctx_read_timings(bh_ctx* ctx, bh_kernel_timing* out, int max, int* count);
+bh_status bh_ctx_reset_timings(bh_ctx* ctx);
+/* Bytes currently cached by the context's workspace pool. */
+uint64_t bh_ctx_workspace_bytes(const bh_ctx* ctx);
+
+/* ---- primitives ---------------------------------------------------------- */
+
+/* Stable LSD radix argsort of u32 keys carrying u32 values, considering the
+ * low `sorting_bits` (<= 32) bits.  Replaces brush-sort `radix_argsort`
+ * (crates/brush-sort/src/lib.rs:16-129).  Outputs are caller allocated and
+ * must not alias the inputs.  n == 0 is a no-op. */
+bh_status bh_radix_argsort(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t* vals_in,
+                           uint32_t n, uint32_t sorting_bits, uint32_t* keys_out,
+                           uint32_t* vals_out);
+
+/* Inclusive u32 prefix sum.  Replaces brush-prefix-sum `prefix_sum`
+ * (crates/brush-prefix-sum/src/lib.rs:11-87).  out may alias in. */
+bh_status bh_prefix_sum(bh_ctx* ctx, const uint32_t* in, uint32_t* out, uint32_t n);
+
+/* [start, end) of each tile's run in tile-sorted ids; ids >= num_tiles are
+ * sentinels and write nothing.  Replaces `get_tile_offsets`
+ * (brush-render/src/get_tile_offset.rs:10-62) together with its zero fill
+ * (brush-render/src/render.rs:396-400): every entry of tile_offsets[2*T] is
+ * written. */
+bh_status bh_get_tile_offsets(bh_ctx* ctx, const uint32_t* tile_id_from_isect,
+                              uint32_t num_intersections, uint32_t num_tiles,
+                              uint32_t* tile_offsets);
+
+/* ---- forward ------------------------------------------------------------- */
+
+/* Full forward render: project + cull, depth sort, scan, project visible
+ * (SH -> RGB), map to intersections, tile sort, tile offsets, blend.
+ * Replaces SplatRasterizerOps::render_with_rasterizer with the 16x16
+ * rasterizer (brush-render/src/render.rs:78-543; trait at
+ * brush-render/src/lib.rs:69-108).
+ *
+ * `u` supplies the camera part of ProjectUniforms; img_w/img_h must be > 0;
+ * tile_bw/tile_bh, sh_degree, total_splats are recomputed from the sizes.
+ * Caller-allocated outputs:
+ *   out_img       BWD_INFO: f32 [H,W,4] ([H,W,5] with RENDER_DEPTH)
+ *                 otherwise u32 [H,W] packed RGBA8
+ *   visible       f32 [N] (BWD_INFO only, else may be NULL)
+ *   max_radius    f32 [N]
+ *   tile_offsets  u32 [TY,TX,2]; with BWD_INFO the end of each tile is shrunk to
+ *                 one past the last splat that contributed (rasterize.rs:193-199)
+ * One blocking 16-byte device-to-host read per call sizes the count-dependent
+ * buffers (render.rs:308-330).  *state receives the forward state, which the
+ * caller releases with bh_fwd_state_release(). */
+bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* u, const float background[3],
+                            const float* transforms, const float* sh_coeffs,
+                            const float* raw_opacities, uint32_t num_splats, uint32_t sh_degree,
+                            uint32_t flags, void* out_img, float* visible, float* max_radius,
+                            uint32_t* tile_offsets, bh_fwd_state** state);
+
+bh_status bh_fwd_state_info(const bh_fwd_state* state, bh_fwd_info* out);
+/* Returns the state's buffers to the context pool (stream ordered). */
+void bh_fwd_state_release(bh_fwd_state* state);
+
+/* ---- backward ------------------------------------------------------------ */
+
+/* Rasterize backward.  Replaces SplatBwdOps::rasterize_bwd /
+ * rasterize_bwd_with_refine_weight (brush-render-bwd/src/burn_glue.rs:79-172,
+ * impl render_bwd.rs:90-238).  Inputs are the forward's out_img (f32),
+ * projected [V,10], tile-sorted compact_gid_from_isect, the post-rasterize
+ * tile_offsets, and the upstream gradient v_output (same shape as out_img).
+ * flags: BH_FLAG_SMOOTH_CUTOFF, BH_FLAG_REFINE_WEIGHT, BH_FLAG_RENDER_DEPTH.
+ * v_combined [max(V,1),11] is caller allocated; it is fully overwritten. */
+bh_status bh_rasterize_backward(bh_ctx* ctx, const float* out_img, const float* projected,
+                                const uint32_t* compact_gid_from_isect,
+                                const uint32_t* tile_offsets, uint32_t num_visible,
+                                const float background[3], uint32_t img_w, uint32_t img_h,
+                                const float* v_output, uint32_t flags, float* v_combined);
+
+/* Project backward.  Replaces SplatBwdOps::project_bwd
+ * (brush-render-bwd/src/burn_glue.rs:79-172, impl render_bwd.rs:298-447,
+ * kernel kernels/project_backwards.rs:101-263).  `u` is the forward's uniforms
+ * with num_visible filled in (bh_fwd_info.uniforms).  flags: BH_FLAG_MIP.
+ * Dense caller-allocated outputs, every element written:
+ *   v_transforms f32 [N,10], v_coeffs f32 [N,C,3], v_raw_opac f32 [N],
+ *   v_refine f32 [N]. */
+bh_status bh_project_backward(bh_ctx* ctx, const bh_project_uniforms* u, const float* transforms,
+                              const float* sh_coeffs, const float* raw_opacities,
+                              const uint32_t* global_from_compact_gid, const float* v_combined,
+                              uint32_t flags, float* v_transforms, float* v_coeffs,
+                              float* v_raw_opac, float* v_refine);
+
+/* ---- host/device copies (plumbing for bindings without a tensor library) */
+bh_status bh_copy_to_host(bh_ctx* ctx, void* dst_host, const void* src_device, uint64_t bytes);
+bh_status bh_copy_to_device(bh_ctx* ctx, void* dst_device, const void* src_host, uint64_t bytes);
+bh_status bh_device_alloc(bh_ctx* ctx, void** out, uint64_t bytes);
+bh_status bh_device_free(bh_ctx* ctx, void* ptr);
+bh_status bh_synchronize(bh_ctx* ctx);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BRUSH_HIP_H */

@@ -1,0 +1,1053 @@
+/*
+ * bh_oracle.c — CPU restatement of Brush's tile rasterizer (forward and
+ * backward).  TEST INFRASTRUCTURE ONLY: the parity checker for the gfx950
+ * kernels and the CPU baseline timed by bench.py.  The product never links it.
+ *
+ * All arithmetic is f32 in the reference's written order; build with
+ * -ffp-contract=off (oracle/Makefile).  Citations are to the reference tree
+ * (paths relative to crates/).
+ */
+#include "bh_oracle.h"
+
+#include <stdlib.h>
+#include <string.h>
+
+#include "../brush_amd/csrc/bh_math.h"
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+static int g_threads = 1;
+
+void or_set_threads(int n) { g_threads = n < 1 ? 1 : n; }
+
+int or_get_max_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
+/* ------------------------------------------------------------------------ */
+/* Small linear algebra (brush-cube/src/lib.rs:34-543).                      */
+/* ------------------------------------------------------------------------ */
+
+typedef struct { float x, y, z; } v3;
+typedef struct { float x, y; } v2;
+typedef struct { float w, x, y, z; } qt;
+/* column-major: cI_R = column I, row R */
+typedef struct { float c0x, c0y, c0z, c1x, c1y, c1z, c2x, c2y, c2z; } m3;
+typedef struct { v2 c0, c1, c2; } m23;
+typedef struct { float c00, c01, c11; } s2;
+typedef struct { float c00, c01, c02, c11, c12, c22; } s3;
+
+static v3 mk3(float x, float y, float z) { v3 r = {x, y, z}; return r; }
+static v2 mk2(float x, float y) { v2 r = {x, y}; return r; }
+static v3 add3(v3 a, v3 b) { return mk3(a.x + b.x, a.y + b.y, a.z + b.z); }
+static v3 sub3(v3 a, v3 b) { return mk3(a.x - b.x, a.y - b.y, a.z - b.z); }
+static v3 scl3(v3 a, float s) { return mk3(a.x * s, a.y * s, a.z * s); }
+static float dot3(v3 a, v3 b) { return a.x * b.x + a.y * b.y + a.z * b.z; }
+static float len3(v3 a) { return sqrtf(dot3(a, a)); }
+static int fin3(v3 a) { return bh_is_finite(a.x) && bh_is_finite(a.y) && bh_is_finite(a.z); }
+static v2 add2(v2 a, v2 b) { return mk2(a.x + b.x, a.y + b.y); }
+static v2 scl2(v2 a, float s) { return mk2(a.x * s, a.y * s); }
+static float dot2(v2 a, v2 b) { return a.x * b.x + a.y * b.y; }
+
+static float qdot(qt a, qt b) { return a.w * b.w + a.x * b.x + a.y * b.y + a.z * b.z; }
+static qt qscale(qt a, float s) { qt r = {a.w * s, a.x * s, a.y * s, a.z * s}; return r; }
+/* Quat::normalize (lib.rs:185-188) */
+static qt qnormalize(qt q) { return qscale(q, 1.0f / sqrtf(qdot(q, q))); }
+/* Quat::to_mat3 (lib.rs:190-216) */
+static m3 qmat(qt q) {
+    float x2 = q.x * q.x, y2 = q.y * q.y, z2 = q.z * q.z;
+    float xy = q.x * q.y, xz = q.x * q.z, yz = q.y * q.z;
+    float wx = q.w * q.x, wy = q.w * q.y, wz = q.w * q.z;
+    m3 m;
+    m.c0x = 1.0f - 2.0f * (y2 + z2);
+    m.c0y = 2.0f * (xy + wz);
+    m.c0z = 2.0f * (xz - wy);
+    m.c1x = 2.0f * (xy - wz);
+    m.c1y = 1.0f - 2.0f * (x2 + z2);
+    m.c1z = 2.0f * (yz + wx);
+    m.c2x = 2.0f * (xz + wy);
+    m.c2y = 2.0f * (yz - wx);
+    m.c2z = 1.0f - 2.0f * (x2 + y2);
+    return m;
+}
+static v3 col0(m3 m) { return mk3(m.c0x, m.c0y, m.c0z); }
+static v3 col1(m3 m) { return mk3(m.c1x, m.c1y, m.c1z); }
+static v3 col2(m3 m) { return mk3(m.c2x, m.c2y, m.c2z); }
+static v3 row0(m3 m) { return mk3(m.c0x, m.c1x, m.c2x); }
+static v3 row1(m3 m) { return mk3(m.c0y, m.c1y, m.c2y); }
+static v3 row2(m3 m) { return mk3(m.c0z, m.c1z, m.c2z); }
+static m3 from_cols(v3 a, v3 b, v3 c) {
+    m3 m = {a.x, a.y, a.z, b.x, b.y, b.z, c.x, c.y, c.z};
+    return m;
+}
+/* Mat3::mul_vec3 (lib.rs:262-268): col0*x + col1*y + col2*z */
+static v3 m3mulv(m3 m, v3 v) { return add3(add3(scl3(col0(m), v.x), scl3(col1(m), v.y)), scl3(col2(m), v.z)); }
+/* Mat3::transpose_mul_vec3 (lib.rs:270-273) */
+static v3 m3tmulv(m3 m, v3 v) { return mk3(dot3(col0(m), v), dot3(col1(m), v), dot3(col2(m), v)); }
+/* Mat3::mul_mat3 (lib.rs:275-282) */
+static m3 m3mul(m3 a, m3 b) { return from_cols(m3mulv(a, col0(b)), m3mulv(a, col1(b)), m3mulv(a, col2(b))); }
+/* Mat3::mul_diag (lib.rs:284-291) */
+static m3 m3diag(m3 m, v3 s) { return from_cols(scl3(col0(m), s.x), scl3(col1(m), s.y), scl3(col2(m), s.z)); }
+/* Mat3::outer_product_self (lib.rs:305-318) */
+static s3 m3outer(m3 m) {
+    v3 r0 = row0(m), r1 = row1(m), r2 = row2(m);
+    s3 s = {dot3(r0, r0), dot3(r0, r1), dot3(r0, r2), dot3(r1, r1), dot3(r1, r2), dot3(r2, r2)};
+    return s;
+}
+/* Mat2x3::mul_vec3 (lib.rs:341-347) */
+static v2 m23mulv(m23 m, v3 v) { return add2(add2(scl2(m.c0, v.x), scl2(m.c1, v.y)), scl2(m.c2, v.z)); }
+/* Mat2x3::mul_mat3 (lib.rs:332-339) */
+static m23 m23mul(m23 m, m3 n) {
+    m23 r = {m23mulv(m, col0(n)), m23mulv(m, col1(n)), m23mulv(m, col2(n))};
+    return r;
+}
+static v3 m23row0(m23 m) { return mk3(m.c0.x, m.c1.x, m.c2.x); }
+static v3 m23row1(m23 m) { return mk3(m.c0.y, m.c1.y, m.c2.y); }
+/* Mat2x3::gram_matrix (lib.rs:377-383) */
+static s2 m23gram(m23 m) {
+    s2 s;
+    s.c00 = m.c0.x * m.c0.x + m.c1.x * m.c1.x + m.c2.x * m.c2.x;
+    s.c01 = m.c0.x * m.c0.y + m.c1.x * m.c1.y + m.c2.x * m.c2.y;
+    s.c11 = m.c0.y * m.c0.y + m.c1.y * m.c1.y + m.c2.y * m.c2.y;
+    return s;
+}
+/* Sym2::mul_vec2 (lib.rs:405-408) */
+static v2 s2mulv(s2 s, v2 v) { return add2(scl2(mk2(s.c00, s.c01), v.x), scl2(mk2(s.c01, s.c11), v.y)); }
+/* Sym2::mul_mat2x3 (lib.rs:425-432) */
+static m23 s2mulm23(s2 s, m23 n) {
+    m23 r = {s2mulv(s, n.c0), s2mulv(s, n.c1), s2mulv(s, n.c2)};
+    return r;
+}
+/* Mat2x3::transpose_congruence_sym2 (lib.rs:357-370) */
+static s3 m23tcong(m23 m, s2 s) {
+    v2 sc0 = s2mulv(s, m.c0), sc1 = s2mulv(s, m.c1), sc2 = s2mulv(s, m.c2);
+    s3 r = {dot2(m.c0, sc0), dot2(m.c0, sc1), dot2(m.c0, sc2), dot2(m.c1, sc1), dot2(m.c1, sc2), dot2(m.c2, sc2)};
+    return r;
+}
+static s2 s2scale(s2 s, float f) { s2 r = {s.c00 * f, s.c01 * f, s.c11 * f}; return r; }
+static float s2maxabs(s2 s) { return bh_maxf(bh_maxf(bh_absf(s.c00), bh_absf(s.c11)), bh_absf(s.c01)); }
+/* Sym2::inverse (lib.rs:434-445) */
+static s2 s2inv(s2 s) {
+    float det = s.c00 * s.c11 - s.c01 * s.c01;
+    int inv = det > 0.0f;
+    float inv_det = inv ? 1.0f / det : 0.0f;
+    s2 r = {s.c11 * inv_det, -s.c01 * inv_det, s.c00 * inv_det};
+    return r;
+}
+/* Sym2::det2_strict (lib.rs:447-453) */
+static float s2det(s2 s) {
+    float ad = s.c00 * s.c11;
+    float bc = s.c01 * s.c01;
+    return ad - bc;
+}
+static int s2fin(s2 s) { return bh_is_finite(s.c00) && bh_is_finite(s.c11) && bh_is_finite(s.c01); }
+/* Sym3 rows and products (lib.rs:472-543) */
+static v3 s3row0(s3 s) { return mk3(s.c00, s.c01, s.c02); }
+static v3 s3row1(s3 s) { return mk3(s.c01, s.c11, s.c12); }
+static v3 s3row2(s3 s) { return mk3(s.c02, s.c12, s.c22); }
+static v3 s3mulv(s3 s, v3 v) { return add3(add3(scl3(s3row0(s), v.x), scl3(s3row1(s), v.y)), scl3(s3row2(s), v.z)); }
+static s3 s3scale(s3 s, float f) { s3 r = {s.c00 * f, s.c01 * f, s.c02 * f, s.c11 * f, s.c12 * f, s.c22 * f}; return r; }
+static m3 s3mulm3(s3 s, m3 m) { return from_cols(s3mulv(s, col0(m)), s3mulv(s, col1(m)), s3mulv(s, col2(m))); }
+static s3 s3cong(s3 s, m3 m) {
+    v3 sr0 = s3mulv(s, row0(m)), sr1 = s3mulv(s, row1(m)), sr2 = s3mulv(s, row2(m));
+    s3 r = {dot3(row0(m), sr0), dot3(row0(m), sr1), dot3(row0(m), sr2), dot3(row1(m), sr1), dot3(row1(m), sr2), dot3(row2(m), sr2)};
+    return r;
+}
+static s3 s3tcong(s3 s, m3 m) {
+    v3 sc0 = s3mulv(s, col0(m)), sc1 = s3mulv(s, col1(m)), sc2 = s3mulv(s, col2(m));
+    s3 r = {dot3(col0(m), sc0), dot3(col0(m), sc1), dot3(col0(m), sc2), dot3(col1(m), sc1), dot3(col1(m), sc2), dot3(col2(m), sc2)};
+    return r;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Camera / projection helpers                                               */
+/* ------------------------------------------------------------------------ */
+
+static m3 view_rot(const bh_project_uniforms* u) {
+    const float* v = u->viewmat;
+    m3 m = {v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7], v[8]};
+    return m;
+}
+/* world_to_cam (kernels/helpers.rs:477-482): R*mean + t */
+static v3 world_to_cam(const bh_project_uniforms* u, v3 mean) {
+    return add3(m3mulv(view_rot(u), mean), mk3(u->viewmat[9], u->viewmat[10], u->viewmat[11]));
+}
+/* project_pinhole (camera_model/pinhole.rs:24-30) */
+static void project_pinhole(const bh_project_uniforms* u, v3 p, float* ox, float* oy) {
+    float inv_z = 1.0f / p.z;
+    *ox = u->fx * p.x * inv_z + u->cx;
+    *oy = u->fy * p.y * inv_z + u->cy;
+}
+/* calculate_project_jacobian_pinhole (pinhole.rs:32-56) */
+static m23 jac_pinhole(const bh_project_uniforms* u, v3 p) {
+    float inv_z = 1.0f / p.z;
+    float dx = u->fx * inv_z;
+    float dy = u->fy * inv_z;
+    float cxl = bh_clampf(p.x * inv_z, u->lim_neg_x, u->lim_pos_x);
+    float cyl = bh_clampf(p.y * inv_z, u->lim_neg_y, u->lim_pos_y);
+    m23 m = {mk2(dx, 0.0f), mk2(0.0f, dy), mk2(-dx * cxl, -dy * cyl)};
+    return m;
+}
+/* calc_cov2d (kernels/helpers.rs:297-330) */
+static s2 calc_cov2d(const bh_project_uniforms* u, v3 scale, qt quat, v3 mean_c) {
+    m3 ns = m3diag(m3mul(view_rot(u), qmat(quat)), scale);
+    m23 jac = jac_pinhole(u, mean_c);
+    m23 v = m23mul(jac, ns);
+    s2 raw = m23gram(v);
+    float lim = 1.0e18f;
+    float max_abs = s2maxabs(raw);
+    float scale_down = max_abs > lim ? lim / max_abs : 1.0f;
+    return s2scale(raw, scale_down);
+}
+/* compensate_cov2d (kernels/helpers.rs:332-350) */
+static s2 compensate_cov2d(s2 c, uint32_t mip, float* comp) {
+    float blur = mip ? 0.1f : 0.3f;
+    s2 b = {c.c00 + blur, c.c01, c.c11 + blur};
+    float fc = 1.0f;
+    if (mip) {
+        float det_raw = bh_maxf(s2det(c), 0.0f);
+        float det_b = s2det(b);
+        fc = sqrtf(det_raw / det_b);
+    }
+    *comp = fc;
+    return b;
+}
+/* compute_bbox_extent (kernels/helpers.rs:227-241) */
+static void bbox_extent(s2 conic, float pt, float* ex, float* ey) {
+    float det = conic.c00 * conic.c11 - conic.c01 * conic.c01;
+    int degenerate = det <= 0.0f;
+    float inv_det = degenerate ? 0.0f : 1.0f / det;
+    float x = sqrtf(2.0f * pt * conic.c11 * inv_det);
+    float y = sqrtf(2.0f * pt * conic.c00 * inv_det);
+    *ex = degenerate ? -1.0f : x;
+    *ey = degenerate ? -1.0f : y;
+}
+typedef struct { uint32_t min_x, min_y, max_x, max_y; } tbox;
+/* get_bbox / get_tile_bbox (kernels/helpers.rs:260-295) */
+static tbox tile_bbox(float mx, float my, float ex, float ey, uint32_t bw, uint32_t bh) {
+    float cx = mx / 16.0f, cy = my / 16.0f, dx = ex / 16.0f, dy = ey / 16.0f;
+    float bwf = (float)bw, bhf = (float)bh;
+    tbox b;
+    b.min_x = (uint32_t)bh_clampf(cx - dx, 0.0f, bwf);
+    b.min_y = (uint32_t)bh_clampf(cy - dy, 0.0f, bhf);
+    b.max_x = (uint32_t)bh_clampf(cx + dx + 1.0f, 0.0f, bwf);
+    b.max_y = (uint32_t)bh_clampf(cy + dy + 1.0f, 0.0f, bhf);
+    return b;
+}
+/* calc_sigma (brush-cube/src/lib.rs:632-638) */
+static float calc_sigma(float px, float py, s2 c, float x, float y) {
+    float dx = px - x;
+    float dy = py - y;
+    return 0.5f * (c.c00 * dx * dx + c.c11 * dy * dy) + c.c01 * dx * dy;
+}
+/* will_primitive_contribute (kernels/helpers.rs:385-424), 16x16 tile rect */
+static int will_contribute(uint32_t tx, uint32_t ty, float mx, float my, s2 c, float pt) {
+    float min_x = (float)(tx * 16u), min_y = (float)(ty * 16u);
+    float max_x = min_x + 16.0f, max_y = min_y + 16.0f;
+    int x_left = mx < min_x, x_right = mx > max_x;
+    int in_x = !(x_left || x_right);
+    int y_above = my < min_y, y_below = my > max_y;
+    int in_y = !(y_above || y_below);
+    int hit = in_x && in_y;
+    if (!hit) {
+        float corner_x = x_left ? min_x : max_x;
+        float corner_y = y_above ? min_y : max_y;
+        float width = max_x - min_x;
+        float height = max_y - min_y;
+        float dxf = x_left ? width : -width;
+        float dyf = y_above ? height : -height;
+        float diff_x = mx - corner_x;
+        float diff_y = my - corner_y;
+        float tx_raw = (dxf * c.c00 * diff_x + dxf * c.c01 * diff_y) / (dxf * c.c00 * dxf);
+        float ty_raw = (dyf * c.c01 * diff_x + dyf * c.c11 * diff_y) / (dyf * c.c11 * dyf);
+        float tt_x = in_y ? 0.0f : bh_clampf(tx_raw, 0.0f, 1.0f);
+        float tt_y = in_x ? 0.0f : bh_clampf(ty_raw, 0.0f, 1.0f);
+        float px = corner_x + tt_x * dxf;
+        float py = corner_y + tt_y * dyf;
+        hit = calc_sigma(px, py, c, mx, my) <= pt;
+    }
+    return hit;
+}
+
+/* ------------------------------------------------------------------------ */
+/* project_forward (kernels/project_forward.rs:20-144)                       */
+/* Pinned by: fuzz cull cases (bench-test/tests/fuzz.rs:330-490), brute      */
+/* force tile enumeration, and the gsplat goldens through the full forward.  */
+/* ------------------------------------------------------------------------ */
+
+/* Returns 1 and fills outputs if the splat survives culling. */
+static int project_one(const bh_project_uniforms* u, const float* t, float raw_opac, uint32_t mip,
+                       uint32_t* count, float* radius, float* depth) {
+    v3 mean_c = world_to_cam(u, mk3(t[0], t[1], t[2]));
+    if (!(fin3(mean_c) && mean_c.z <= 1.0e10f)) return 0;
+    if (mean_c.z < 0.01f) return 0;
+    v3 scale = mk3(bh_expf(t[7]), bh_expf(t[8]), bh_expf(t[9]));
+    if (!fin3(scale)) return 0;
+    qt qu = {t[3], t[4], t[5], t[6]};
+    float qn = qdot(qu, qu);
+    if (!(qn >= 1.0e-6f && bh_is_finite(qn))) return 0;
+    if (!bh_is_finite(raw_opac)) return 0;
+    qt q = qnormalize(qu);
+    s2 raw_cov = calc_cov2d(u, scale, q, mean_c);
+    float comp;
+    s2 cov = compensate_cov2d(raw_cov, mip, &comp);
+    float opac = bh_sigmoidf(raw_opac) * comp;
+    if (!s2fin(cov)) return 0;
+    float mx, my;
+    project_pinhole(u, mean_c, &mx, &my);
+    if (!(opac >= 1.0f / 255.0f)) return 0;
+    float pt = bh_logf(opac * 255.0f);
+    s2 conic = s2inv(cov);
+    float ex, ey;
+    bbox_extent(conic, pt, &ex, &ey);
+    if (!(ex >= 0.0f && ey >= 0.0f)) return 0;
+    float wf = (float)u->img_w, hf = (float)u->img_h;
+    int on_screen = mx + ex > 0.0f && mx - ex < wf && my + ey > 0.0f && my - ey < hf;
+    if (!on_screen) return 0;
+    tbox bb = tile_bbox(mx, my, ex, ey, u->tile_bw, u->tile_bh);
+    uint32_t hits = 0;
+    for (uint32_t ty = bb.min_y; ty < bb.max_y; ty++)
+        for (uint32_t tx = bb.min_x; tx < bb.max_x; tx++)
+            if (will_contribute(tx, ty, mx, my, conic, pt)) hits++;
+    *count = hits;
+    *radius = bh_maxf(ex / wf, ey / hf);
+    *depth = mean_c.z;
+    return 1;
+}
+
+uint64_t or_project_forward(const bh_project_uniforms* u, const float* transforms,
+                            const float* raw_opac, uint32_t n, uint32_t mip,
+                            uint32_t* intersect_counts, float* max_radius, float* depths,
+                            uint8_t* visible_mask) {
+    uint64_t total = 0;
+#pragma omp parallel for schedule(dynamic, 4096) reduction(+ : total) num_threads(g_threads)
+    for (int64_t i = 0; i < (int64_t)n; i++) {
+        uint32_t c = 0;
+        float r = 0.0f, d = 0.0f;
+        int vis = project_one(u, transforms + (size_t)i * 10, raw_opac[i], mip, &c, &r, &d);
+        intersect_counts[i] = vis ? c : 0u;
+        max_radius[i] = vis ? r : 0.0f;
+        depths[i] = vis ? d : 0.0f;
+        visible_mask[i] = (uint8_t)vis;
+        total += vis ? c : 0u;
+    }
+    return total;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Stable sort: textbook bottom-up merge sort on (key & mask, value) pairs.  */
+/* Semantics of brush-sort radix_argsort (brush-sort/src/lib.rs:16-129): a   */
+/* stable ascending sort on the low `sorting_bits` key bits; the returned    */
+/* keys are the original keys.  Pinned by stability/permutation tests.       */
+/* ------------------------------------------------------------------------ */
+
+void or_stable_sort(uint32_t* keys, uint32_t* vals, uint64_t n, uint32_t sorting_bits) {
+    if (n < 2) return;
+    uint32_t mask = sorting_bits >= 32 ? 0xFFFFFFFFu : ((1u << sorting_bits) - 1u);
+    uint32_t* k2 = (uint32_t*)malloc(n * sizeof(uint32_t));
+    uint32_t* v2b = (uint32_t*)malloc(n * sizeof(uint32_t));
+    uint32_t *sk = keys, *sv = vals, *dk = k2, *dv = v2b;
+    for (uint64_t w = 1; w < n; w *= 2) {
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+        for (int64_t lo = 0; lo < (int64_t)n; lo += (int64_t)(2 * w)) {
+            uint64_t mid = (uint64_t)lo + w < n ? (uint64_t)lo + w : n;
+            uint64_t hi = (uint64_t)lo + 2 * w < n ? (uint64_t)lo + 2 * w : n;
+            uint64_t i = (uint64_t)lo, j = mid, o = (uint64_t)lo;
+            while (i < mid && j < hi) {
+                if ((sk[j] & mask) < (sk[i] & mask)) {
+                    dk[o] = sk[j]; dv[o] = sv[j]; j++;
+                } else {
+                    dk[o] = sk[i]; dv[o] = sv[i]; i++;
+                }
+                o++;
+            }
+            while (i < mid) { dk[o] = sk[i]; dv[o] = sv[i]; i++; o++; }
+            while (j < hi) { dk[o] = sk[j]; dv[o] = sv[j]; j++; o++; }
+        }
+        uint32_t* t;
+        t = sk; sk = dk; dk = t;
+        t = sv; sv = dv; dv = t;
+    }
+    if (sk != keys) {
+        memcpy(keys, sk, n * sizeof(uint32_t));
+        memcpy(vals, sv, n * sizeof(uint32_t));
+    }
+    free(k2);
+    free(v2b);
+}
+
+/* Inclusive scan (brush-prefix-sum/src/lib.rs:11-87). Closed form. */
+void or_prefix_sum(const uint32_t* in, uint32_t* out, uint64_t n) {
+    uint32_t acc = 0;
+    for (uint64_t i = 0; i < n; i++) {
+        acc += in[i];
+        out[i] = acc;
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* SH -> RGB (kernels/sh.rs:157-247). Coefficient k of channel ch is at      */
+/* base + 3k + ch.                                                           */
+/* ------------------------------------------------------------------------ */
+static v3 rd3(const float* c, uint32_t k) { return mk3(c[3 * k], c[3 * k + 1], c[3 * k + 2]); }
+
+static v3 sh_to_color(const float* c, uint32_t deg, v3 v) {
+    v3 color = scl3(rd3(c, 0), 0.2820948f);
+    if (deg >= 1) {
+        float f0a = 0.4886025f;
+        color = add3(color, scl3(rd3(c, 1), -f0a * v.y));
+        color = add3(color, scl3(rd3(c, 2), f0a * v.z));
+        color = add3(color, scl3(rd3(c, 3), -f0a * v.x));
+        if (deg >= 2) {
+            float z2 = v.z * v.z;
+            float f0b = -1.0925485f * v.z;
+            float f1a = 0.54627424f;
+            float fc1 = v.x * v.x - v.y * v.y;
+            float fs1 = 2.0f * v.x * v.y;
+            float p4 = f1a * fs1, p5 = f0b * v.y, p6 = 0.9461747f * z2 - 0.31539157f;
+            float p7 = f0b * v.x, p8 = f1a * fc1;
+            color = add3(color, scl3(rd3(c, 4), p4));
+            color = add3(color, scl3(rd3(c, 5), p5));
+            color = add3(color, scl3(rd3(c, 6), p6));
+            color = add3(color, scl3(rd3(c, 7), p7));
+            color = add3(color, scl3(rd3(c, 8), p8));
+            if (deg >= 3) {
+                float f0c = -2.285229f * z2 + 0.4570458f;
+                float f1b = 1.4453057f * v.z;
+                float f2a = -0.5900436f;
+                float fc2 = v.x * fc1 - v.y * fs1;
+                float fs2 = v.x * fs1 + v.y * fc1;
+                float p12 = v.z * (1.8658817f * z2 - 1.119529f);
+                float p9 = f2a * fs2, p10 = f1b * fs1, p11 = f0c * v.y;
+                float p13 = f0c * v.x, p14 = f1b * fc1, p15 = f2a * fc2;
+                color = add3(color, scl3(rd3(c, 9), p9));
+                color = add3(color, scl3(rd3(c, 10), p10));
+                color = add3(color, scl3(rd3(c, 11), p11));
+                color = add3(color, scl3(rd3(c, 12), p12));
+                color = add3(color, scl3(rd3(c, 13), p13));
+                color = add3(color, scl3(rd3(c, 14), p14));
+                color = add3(color, scl3(rd3(c, 15), p15));
+                if (deg >= 4) {
+                    float f0d = v.z * (-4.683326f * z2 + 2.0071396f);
+                    float f1c = 3.3116114f * z2 - 0.47308735f;
+                    float f2b = -1.7701308f * v.z;
+                    float f3a = 0.62583575f;
+                    float fc3 = v.x * fc2 - v.y * fs2;
+                    float fs3 = v.x * fs2 + v.y * fc2;
+                    float p20 = 1.9843135f * v.z * p12 - 1.0062306f * p6;
+                    float p16 = f3a * fs3, p17 = f2b * fs2, p18 = f1c * fs1, p19 = f0d * v.y;
+                    float p21 = f0d * v.x, p22 = f1c * fc1, p23 = f2b * fc2, p24 = f3a * fc3;
+                    color = add3(color, scl3(rd3(c, 16), p16));
+                    color = add3(color, scl3(rd3(c, 17), p17));
+                    color = add3(color, scl3(rd3(c, 18), p18));
+                    color = add3(color, scl3(rd3(c, 19), p19));
+                    color = add3(color, scl3(rd3(c, 20), p20));
+                    color = add3(color, scl3(rd3(c, 21), p21));
+                    color = add3(color, scl3(rd3(c, 22), p22));
+                    color = add3(color, scl3(rd3(c, 23), p23));
+                    color = add3(color, scl3(rd3(c, 24), p24));
+                }
+            }
+        }
+    }
+    return color;
+}
+
+/* ------------------------------------------------------------------------ */
+/* project_visible (kernels/project_visible.rs:22-89)                        */
+/* ------------------------------------------------------------------------ */
+void or_project_visible(const bh_project_uniforms* u, const float* transforms,
+                        const float* sh_coeffs, const float* raw_opac,
+                        const uint32_t* global_from_compact_gid, uint32_t num_visible,
+                        uint32_t sh_degree, uint32_t mip, float* projected) {
+    uint32_t nc = (sh_degree + 1) * (sh_degree + 1);
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+    for (int64_t ci = 0; ci < (int64_t)num_visible; ci++) {
+        uint32_t g = global_from_compact_gid[ci];
+        const float* t = transforms + (size_t)g * 10;
+        v3 mean = mk3(t[0], t[1], t[2]);
+        v3 scale = mk3(bh_expf(t[7]), bh_expf(t[8]), bh_expf(t[9]));
+        qt qu = {t[3], t[4], t[5], t[6]};
+        qt q = qnormalize(qu);
+        v3 mean_c = world_to_cam(u, mean);
+        s2 raw_cov = calc_cov2d(u, scale, q, mean_c);
+        float comp;
+        s2 cov = compensate_cov2d(raw_cov, mip, &comp);
+        float opac = bh_sigmoidf(raw_opac[g]) * comp;
+        s2 conic = s2inv(cov);
+        float mx, my;
+        project_pinhole(u, mean_c, &mx, &my);
+        v3 v = sub3(mean, mk3(u->camera_pos[0], u->camera_pos[1], u->camera_pos[2]));
+        v = scl3(v, 1.0f / len3(v));
+        v3 raw = sh_to_color(sh_coeffs + (size_t)g * nc * 3, sh_degree, v);
+        float cr = raw.x + 0.5f, cg = raw.y + 0.5f, cb = raw.z + 0.5f;
+        float* p = projected + (size_t)ci * 10;
+        p[0] = mx;
+        p[1] = my;
+        p[2] = conic.c00;
+        p[3] = conic.c01;
+        p[4] = conic.c11;
+        p[5] = opac;
+        p[6] = bh_clampf(bh_is_finite(cr) ? cr : 0.0f, -100.0f, 100.0f);
+        p[7] = bh_clampf(bh_is_finite(cg) ? cg : 0.0f, -100.0f, 100.0f);
+        p[8] = bh_clampf(bh_is_finite(cb) ? cb : 0.0f, -100.0f, 100.0f);
+        p[9] = mean_c.z;
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* map_gaussians_to_intersect (kernels/map_gaussians.rs:14-92)               */
+/* ------------------------------------------------------------------------ */
+void or_map_intersects(uint32_t tile_bw, uint32_t tile_bh, const float* projected,
+                       const uint32_t* cum, uint32_t num_visible,
+                       uint32_t* tile_id_from_isect, uint32_t* compact_gid_from_isect) {
+#pragma omp parallel for schedule(dynamic, 1024) num_threads(g_threads)
+    for (int64_t ci = 0; ci < (int64_t)num_visible; ci++) {
+        const float* p = projected + (size_t)ci * 10;
+        float mx = p[0], my = p[1];
+        s2 conic = {p[2], p[3], p[4]};
+        float pt = bh_logf(p[5] * 255.0f);
+        float ex, ey;
+        bbox_extent(conic, pt, &ex, &ey);
+        tbox bb = tile_bbox(mx, my, ex, ey, tile_bw, tile_bh);
+        uint32_t base = ci == 0 ? 0u : cum[ci - 1];
+        uint32_t budget = cum[ci] - base;
+        uint32_t hits = 0;
+        for (uint32_t ty = bb.min_y; ty < bb.max_y && hits < budget; ty++)
+            for (uint32_t tx = bb.min_x; tx < bb.max_x && hits < budget; tx++)
+                if (will_contribute(tx, ty, mx, my, conic, pt)) {
+                    tile_id_from_isect[base + hits] = tx + ty * tile_bw;
+                    compact_gid_from_isect[base + hits] = (uint32_t)ci;
+                    hits++;
+                }
+        for (uint32_t k = hits; k < budget; k++) {
+            tile_id_from_isect[base + k] = tile_bw * tile_bh;
+            compact_gid_from_isect[base + k] = (uint32_t)ci;
+        }
+    }
+}
+
+/* get_tile_offsets + zero fill (get_tile_offset.rs:10-62; render.rs:396-400). */
+void or_tile_offsets(const uint32_t* ids, uint64_t m, uint32_t num_tiles, uint32_t* offsets) {
+    memset(offsets, 0, (size_t)num_tiles * 2 * sizeof(uint32_t));
+    for (uint64_t i = 0; i < m; i++) {
+        uint32_t tid = ids[i];
+        if (i == 0) {
+            if (tid < num_tiles) offsets[2 * tid] = 0;
+        } else {
+            uint32_t prev = ids[i - 1];
+            if (tid != prev) {
+                if (prev < num_tiles) offsets[2 * prev + 1] = (uint32_t)i;
+                if (tid < num_tiles) offsets[2 * tid] = (uint32_t)i;
+            }
+        }
+        if (i == m - 1 && tid < num_tiles) offsets[2 * tid + 1] = (uint32_t)(i + 1);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Forward blend (kernels/rasterize.rs:24-200) with the alpha cutoff         */
+/* (kernels/helpers.rs:161-190).                                             */
+/* ------------------------------------------------------------------------ */
+static const float CUT_MID = 1.0f / 255.0f;
+static const float CUT_BAND = 1.0e-3f;
+
+static float cutoff_weight(float alpha) {
+    float t = bh_clampf((alpha - (CUT_MID - 0.5f * CUT_BAND)) / CUT_BAND, 0.0f, 1.0f);
+    return t * t * (3.0f - 2.0f * t);
+}
+static float cutoff_weight_deriv(float alpha) {
+    float low = CUT_MID - 0.5f * CUT_BAND;
+    float high = CUT_MID + 0.5f * CUT_BAND;
+    int inside = alpha > low && alpha < high;
+    float t = (alpha - low) / CUT_BAND;
+    return inside ? (6.0f * t - 6.0f * t * t) / CUT_BAND : 0.0f;
+}
+
+void or_rasterize(uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,
+                  const float* bg, const float* projected, const uint32_t* cgid_from_isect,
+                  const uint32_t* gfc, const uint32_t* off_pre, uint32_t flags, void* out_img,
+                  float* visible, uint32_t* off_post) {
+    int bwd_info = (flags & BH_FLAG_BWD_INFO) != 0;
+    int smooth = (flags & BH_FLAG_SMOOTH_CUTOFF) != 0;
+    int depth = bwd_info && (flags & BH_FLAG_RENDER_DEPTH) != 0;
+    uint32_t chans = depth ? 5u : 4u;
+    int64_t num_tiles = (int64_t)tile_bw * tile_bh;
+#pragma omp parallel for schedule(dynamic, 4) num_threads(g_threads)
+    for (int64_t tile = 0; tile < num_tiles; tile++) {
+        uint32_t lo = off_pre[2 * tile], hi = off_pre[2 * tile + 1];
+        uint32_t ox = (uint32_t)(tile % tile_bw) * 16u, oy = (uint32_t)(tile / tile_bw) * 16u;
+        uint32_t max_useful = lo;
+        for (uint32_t p = 0; p < 256; p++) {
+            uint32_t px = ox + (p & 15u), py = oy + (p >> 4);
+            if (px >= img_w || py >= img_h) continue;
+            float pcx = (float)px + 0.5f, pcy = (float)py + 0.5f;
+            float t_acc = 1.0f, r = 0.0f, g = 0.0f, b = 0.0f, d = 0.0f;
+            uint32_t last = lo;
+            for (uint32_t i = lo; i < hi; i++) {
+                const float* s = projected + (size_t)cgid_from_isect[i] * 10;
+                s2 conic = {s[2], s[3], s[4]};
+                float sigma = calc_sigma(pcx, pcy, conic, s[0], s[1]);
+                float alpha = bh_minf(0.999f, s[5] * bh_expf(-sigma));
+                float w = smooth ? cutoff_weight(alpha) : (alpha >= CUT_MID ? 1.0f : 0.0f);
+                if (sigma >= 0.0f && w > 0.0f) {
+                    float ae = alpha * w;
+                    float next_t = t_acc * (1.0f - ae);
+                    if (next_t <= 1.0e-4f) break;
+                    if (bwd_info) visible[gfc[cgid_from_isect[i]]] = 1.0f;
+                    float vis = ae * t_acc;
+                    r += bh_maxf(s[6], 0.0f) * vis;
+                    g += bh_maxf(s[7], 0.0f) * vis;
+                    b += bh_maxf(s[8], 0.0f) * vis;
+                    if (depth) d += s[9] * vis;
+                    t_acc = next_t;
+                    last = i + 1;
+                }
+            }
+            if (last > max_useful) max_useful = last;
+            float fr = r + t_acc * bg[0], fg = g + t_acc * bg[1], fb = b + t_acc * bg[2];
+            float fa = 1.0f - t_acc;
+            size_t pix = (size_t)py * img_w + px;
+            if (bwd_info) {
+                float* o = (float*)out_img + pix * chans;
+                o[0] = fr; o[1] = fg; o[2] = fb; o[3] = fa;
+                if (depth) o[4] = d;
+            } else {
+                uint32_t ur = (uint32_t)bh_clampf(fr * 255.0f, 0.0f, 255.0f);
+                uint32_t ug = (uint32_t)bh_clampf(fg * 255.0f, 0.0f, 255.0f);
+                uint32_t ub = (uint32_t)bh_clampf(fb * 255.0f, 0.0f, 255.0f);
+                uint32_t ua = (uint32_t)bh_clampf(fa * 255.0f, 0.0f, 255.0f);
+                ((uint32_t*)out_img)[pix] = ur | (ug << 8) | (ub << 16) | (ua << 24);
+            }
+        }
+        off_post[2 * tile] = lo;
+        off_post[2 * tile + 1] = bwd_info ? max_useful : hi;
+    }
+}
+
+/* Independent per-pixel walk over all depth-sorted projected splats, no tiles
+ * (brush-render/src/tests/raster_oracle.rs:48-98). */
+void or_rasterize_reference(const float* projected, uint32_t n, uint32_t w, uint32_t h,
+                            const float* bg, uint32_t smooth, float* out) {
+    for (uint32_t y = 0; y < h; y++)
+        for (uint32_t x = 0; x < w; x++) {
+            float pxc = (float)x + 0.5f, pyc = (float)y + 0.5f;
+            float t = 1.0f, r = 0.0f, g = 0.0f, b = 0.0f;
+            for (uint32_t i = 0; i < n; i++) {
+                const float* s = projected + (size_t)i * 10;
+                float dx = pxc - s[0], dy = pyc - s[1];
+                float sigma = 0.5f * (s[2] * dx * dx + s[4] * dy * dy) + s[3] * dx * dy;
+                float alpha = bh_minf(s[5] * bh_expf(-sigma), 0.999f);
+                float wgt = smooth ? cutoff_weight(alpha) : (alpha >= CUT_MID ? 1.0f : 0.0f);
+                if (sigma >= 0.0f && wgt > 0.0f) {
+                    float ea = alpha * wgt;
+                    float nt = t * (1.0f - ea);
+                    if (nt <= 1.0e-4f) break;
+                    float vis = ea * t;
+                    r += bh_maxf(s[6], 0.0f) * vis;
+                    g += bh_maxf(s[7], 0.0f) * vis;
+                    b += bh_maxf(s[8], 0.0f) * vis;
+                    t = nt;
+                }
+            }
+            float* o = out + ((size_t)y * w + x) * 4;
+            o[0] = r + bg[0] * t;
+            o[1] = g + bg[1] * t;
+            o[2] = b + bg[2] * t;
+            o[3] = 1.0f - t;
+        }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Rasterize backward (brush-render-bwd/src/kernels/rasterize_backwards.rs). */
+/* The reference replays each tile front to back: lane = splat, and each     */
+/* splat visits the tile's 256 pixels in row-major order, carrying per-pixel */
+/* state (rgb remaining, T) from splat to splat.  The per-(splat, tile)      */
+/* gradient is summed over pixels in that order, then added to v_combined.   */
+/* Here tiles are visited in row-major order; the GPU adds the per-tile      */
+/* sums with atomics, so the cross-tile sum order differs (tolerance).       */
+/* ------------------------------------------------------------------------ */
+void or_rasterize_backward(uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,
+                           const float* bg, const float* out_img, const float* projected,
+                           const uint32_t* cgid_from_isect, const uint32_t* offsets,
+                           uint32_t num_visible, const float* v_output, uint32_t flags,
+                           float* v_combined) {
+    int smooth = (flags & BH_FLAG_SMOOTH_CUTOFF) != 0;
+    int refine = (flags & BH_FLAG_REFINE_WEIGHT) != 0;
+    int depth = (flags & BH_FLAG_RENDER_DEPTH) != 0;
+    uint32_t chans = depth ? 5u : 4u;
+    memset(v_combined, 0, (size_t)(num_visible ? num_visible : 1) * 11 * sizeof(float));
+    float img_wf = (float)img_w, img_hf = (float)img_h;
+    int64_t num_tiles = (int64_t)tile_bw * tile_bh;
+#pragma omp parallel for schedule(dynamic, 2) num_threads(g_threads)
+    for (int64_t tile = 0; tile < num_tiles; tile++) {
+        uint32_t lo = offsets[2 * tile], hi = offsets[2 * tile + 1];
+        if (hi <= lo) continue;
+        uint32_t ox = (uint32_t)(tile % tile_bw) * 16u, oy = (uint32_t)(tile / tile_bw) * 16u;
+        float st[256][5];
+        for (uint32_t p = 0; p < 256; p++) {
+            uint32_t px = ox + (p & 15u), py = oy + (p >> 4);
+            if (px < img_w && py < img_h) {
+                const float* o = out_img + ((size_t)py * img_w + px) * chans;
+                float t_final = 1.0f - o[3];
+                st[p][0] = o[0] - t_final * bg[0];
+                st[p][1] = o[1] - t_final * bg[1];
+                st[p][2] = o[2] - t_final * bg[2];
+                st[p][3] = 1.0f;
+                st[p][4] = depth ? o[4] : 0.0f;
+            } else {
+                st[p][0] = st[p][1] = st[p][2] = st[p][3] = st[p][4] = 0.0f;
+            }
+        }
+        for (uint32_t i = lo; i < hi; i++) {
+            uint32_t cg = cgid_from_isect[i];
+            const float* s = projected + (size_t)cg * 10;
+            s2 c = {s[2], s[3], s[4]};
+            float cr = bh_maxf(s[6], 0.0f), cgc = bh_maxf(s[7], 0.0f), cb = bh_maxf(s[8], 0.0f);
+            float gr[11] = {0};
+            for (uint32_t p = 0; p < 256; p++) {
+                float sx = st[p][0], sy = st[p][1], sz = st[p][2], sw = st[p][3];
+                if (!(sw > 1.0e-4f)) continue;
+                uint32_t px = ox + (p & 15u), py = oy + (p >> 4);
+                float pcx = (float)px + 0.5f, pcy = (float)py + 0.5f;
+                float dx = s[0] - pcx, dy = s[1] - pcy;
+                float sigma = 0.5f * (c.c00 * dx * dx + c.c11 * dy * dy) + c.c01 * dx * dy;
+                float gaussian = bh_expf(-sigma);
+                float alpha = bh_minf(0.999f, s[5] * gaussian);
+                float w = smooth ? cutoff_weight(alpha) : (alpha >= CUT_MID ? 1.0f : 0.0f);
+                if (!(sigma >= 0.0f && w > 0.0f)) continue;
+                float ae = alpha * w;
+                float next_t = sw * (1.0f - ae);
+                if (next_t <= 1.0e-4f) {
+                    st[p][3] = 0.0f;
+                    continue;
+                }
+                float vis = ae * sw;
+                const float* vo = v_output + ((size_t)py * img_w + px) * chans;
+                float vox = vo[0], voy = vo[1], voz = vo[2], va = vo[3];
+                float final_a = out_img[((size_t)py * img_w + px) * chans + 3];
+                float t_final = 1.0f - final_a;
+                float vow = (va - (bg[0] * vox + bg[1] * voy + bg[2] * voz)) * t_final;
+                gr[5] += s[6] >= 0.0f ? vis * vox : 0.0f;
+                gr[6] += s[7] >= 0.0f ? vis * voy : 0.0f;
+                gr[7] += s[8] >= 0.0f ? vis * voz : 0.0f;
+                float ra = 1.0f / (1.0f - ae);
+                float dot_rgb = ((sw * cr - sx) * vox + (sw * cgc - sy) * voy + (sw * cb - sz) * voz) * ra;
+                float nrx = sx - vis * cr, nry = sy - vis * cgc, nrz = sz - vis * cb;
+                if (depth) {
+                    float vod = vo[4];
+                    float sd = st[p][4];
+                    gr[10] += vis * vod;
+                    st[p][4] = sd - vis * s[9];
+                }
+                float v_ae = dot_rgb + vow * ra;
+                float dw = smooth ? cutoff_weight_deriv(alpha) : 0.0f * alpha;
+                float v_alpha = v_ae * (w + alpha * dw);
+                float v_sigma = -alpha * v_alpha;
+                float vxy_x = v_sigma * (c.c00 * dx + c.c01 * dy);
+                float vxy_y = v_sigma * (c.c01 * dx + c.c11 * dy);
+                if (s[5] * gaussian <= 0.999f) {
+                    gr[2] += 0.5f * v_sigma * dx * dx;
+                    gr[3] += v_sigma * dx * dy;
+                    gr[4] += 0.5f * v_sigma * dy * dy;
+                    gr[0] += vxy_x;
+                    gr[1] += vxy_y;
+                    gr[8] += v_alpha * gaussian;
+                    if (refine) {
+                        float len = sqrtf(vxy_x * img_wf * vxy_x * img_wf + vxy_y * img_hf * vxy_y * img_hf);
+                        gr[9] += len / bh_maxf(final_a, 1.0e-5f);
+                    }
+                }
+                st[p][0] = nrx;
+                st[p][1] = nry;
+                st[p][2] = nrz;
+                st[p][3] = next_t;
+            }
+            float* out = v_combined + (size_t)cg * 11;
+            for (int k = 0; k < 11; k++) {
+                if (k == 9 && !refine) continue;
+                if (k == 10 && !depth) continue;
+                if (g_threads > 1) {
+#pragma omp atomic
+                    out[k] += gr[k];
+                } else {
+                    out[k] += gr[k];
+                }
+            }
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* project_backwards (brush-render-bwd/src/kernels/project_backwards.rs)     */
+/* ------------------------------------------------------------------------ */
+
+/* apply_normalize_vjp (:19-52) */
+static qt normalize_vjp(qt q, qt g) {
+    float lsq = qdot(q, q);
+    float l = sqrtf(lsq);
+    float inv = 1.0f / (l * lsq);
+    float cc0 = -q.w * q.x, cc1 = -q.x * q.y, cc2 = -q.y * q.w;
+    float cs0 = -q.w * q.z, cs1 = -q.x * q.z, cs2 = -q.y * q.z;
+    float sw = q.w * q.w, sx = q.x * q.x, sy = q.y * q.y, sz = q.z * q.z;
+    qt r;
+    r.w = ((lsq - sw) * g.w + cc0 * g.x + cc2 * g.y + cs0 * g.z) * inv;
+    r.x = (cc0 * g.w + (lsq - sx) * g.x + cc1 * g.y + cs1 * g.z) * inv;
+    r.y = (cc2 * g.w + cc1 * g.x + (lsq - sy) * g.y + cs2 * g.z) * inv;
+    r.z = (cs0 * g.w + cs1 * g.x + cs2 * g.y + (lsq - sz) * g.z) * inv;
+    return r;
+}
+/* quat_to_mat_vjp (:54-79) */
+static qt quat_to_mat_vjp(qt q, m3 v) {
+    float w_grad = q.x * (v.c1z - v.c2y) + q.y * (v.c2x - v.c0z) + q.z * (v.c0y - v.c1x);
+    float x_grad = -2.0f * q.x * (v.c1y + v.c2z) + q.y * (v.c0y + v.c1x) + q.z * (v.c0z + v.c2x) + q.w * (v.c1z - v.c2y);
+    float y_grad = q.x * (v.c0y + v.c1x) - 2.0f * q.y * (v.c0x + v.c2z) + q.z * (v.c1z + v.c2y) + q.w * (v.c2x - v.c0z);
+    float z_grad = q.x * (v.c0z + v.c2x) + q.y * (v.c1z + v.c2y) - 2.0f * q.z * (v.c0x + v.c1y) + q.w * (v.c0y - v.c1x);
+    qt r = {2.0f * w_grad, 2.0f * x_grad, 2.0f * y_grad, 2.0f * z_grad};
+    return r;
+}
+/* inverse2x2_vjp (:81-99) */
+static s2 inverse2x2_vjp(s2 m, s2 v) {
+    float t00 = -m.c00 * v.c00 + -m.c01 * v.c01;
+    float t01 = -m.c01 * v.c00 + -m.c11 * v.c01;
+    float t10 = -m.c00 * v.c01 + -m.c01 * v.c11;
+    float t11 = -m.c01 * v.c01 + -m.c11 * v.c11;
+    s2 r = {t00 * m.c00 + t10 * m.c01, t01 * m.c00 + t11 * m.c01, t01 * m.c01 + t11 * m.c11};
+    return r;
+}
+/* calculate_projection_vjp_pinhole (camera_model/pinhole.rs:58-123) */
+static v3 projection_vjp(const bh_project_uniforms* u, m23 J, v3 mean_c, s3 cov_c, s2 v_cov2d,
+                         v2 v_mean2d) {
+    float fx = u->fx, fy = u->fy;
+    float mx = mean_c.x, my = mean_c.y, mz = mean_c.z;
+    float inv_z = 1.0f / mz;
+    float mx_rz_raw = mx * inv_z, my_rz_raw = my * inv_z;
+    float mx_rz = bh_clampf(mx_rz_raw, u->lim_neg_x, u->lim_pos_x);
+    float my_rz = bh_clampf(my_rz_raw, u->lim_neg_y, u->lim_pos_y);
+    int in_x = mx_rz_raw <= u->lim_pos_x && mx_rz_raw >= u->lim_neg_x;
+    int in_y = my_rz_raw <= u->lim_pos_y && my_rz_raw >= u->lim_neg_y;
+    float inv_z2 = inv_z * inv_z;
+    float inv_z3 = inv_z2 * inv_z;
+    float v_mx = fx * inv_z * v_mean2d.x;
+    float v_my = fy * inv_z * v_mean2d.y;
+    float v_mz = -(fx * mx * v_mean2d.x + fy * my * v_mean2d.y) * inv_z2;
+    m23 tmp = s2mulm23(v_cov2d, J);
+    float vj00 = 2.0f * dot3(m23row0(tmp), s3row0(cov_c));
+    float vj11 = 2.0f * dot3(m23row1(tmp), s3row1(cov_c));
+    float vj20 = 2.0f * dot3(m23row0(tmp), s3row2(cov_c));
+    float vj21 = 2.0f * dot3(m23row1(tmp), s3row2(cov_c));
+    float tx = mz * mx_rz;
+    float ty = mz * my_rz;
+    if (in_x) v_mx += -fx * inv_z2 * vj20;
+    else v_mz += -fx * inv_z3 * vj20 * tx;
+    if (in_y) v_my += -fy * inv_z2 * vj21;
+    else v_mz += -fy * inv_z3 * vj21 * ty;
+    v_mz += -fx * inv_z2 * vj00 - fy * inv_z2 * vj11 + 2.0f * fx * tx * inv_z3 * vj20 + 2.0f * fy * ty * inv_z3 * vj21;
+    return mk3(v_mx, v_my, v_mz);
+}
+/* sh_coeffs_to_color_vjp (kernels/sh.rs:383-466) */
+static void wr3(float* o, uint32_t k, v3 v) {
+    o[3 * k] = v.x;
+    o[3 * k + 1] = v.y;
+    o[3 * k + 2] = v.z;
+}
+static void sh_color_vjp(float* o, uint32_t deg, v3 v, v3 vc) {
+    wr3(o, 0, scl3(vc, 0.2820948f));
+    if (deg >= 1) {
+        float f0a = 0.4886025f;
+        wr3(o, 1, scl3(vc, -f0a * v.y));
+        wr3(o, 2, scl3(vc, f0a * v.z));
+        wr3(o, 3, scl3(vc, -f0a * v.x));
+        if (deg >= 2) {
+            float z2 = v.z * v.z;
+            float f0b = -1.0925485f * v.z;
+            float f1a = 0.54627424f;
+            float fc1 = v.x * v.x - v.y * v.y;
+            float fs1 = 2.0f * v.x * v.y;
+            float p6 = 0.9461747f * z2 - 0.31539157f;
+            wr3(o, 4, scl3(vc, f1a * fs1));
+            wr3(o, 5, scl3(vc, f0b * v.y));
+            wr3(o, 6, scl3(vc, p6));
+            wr3(o, 7, scl3(vc, f0b * v.x));
+            wr3(o, 8, scl3(vc, f1a * fc1));
+            if (deg >= 3) {
+                float f0c = -2.285229f * z2 + 0.4570458f;
+                float f1b = 1.4453057f * v.z;
+                float f2a = -0.5900436f;
+                float fc2 = v.x * fc1 - v.y * fs1;
+                float fs2 = v.x * fs1 + v.y * fc1;
+                float p12 = v.z * (1.8658817f * z2 - 1.119529f);
+                wr3(o, 9, scl3(vc, f2a * fs2));
+                wr3(o, 10, scl3(vc, f1b * fs1));
+                wr3(o, 11, scl3(vc, f0c * v.y));
+                wr3(o, 12, scl3(vc, p12));
+                wr3(o, 13, scl3(vc, f0c * v.x));
+                wr3(o, 14, scl3(vc, f1b * fc1));
+                wr3(o, 15, scl3(vc, f2a * fc2));
+                if (deg >= 4) {
+                    float f0d = v.z * (-4.683326f * z2 + 2.0071396f);
+                    float f1c = 3.3116114f * z2 - 0.47308735f;
+                    float f2b = -1.7701308f * v.z;
+                    float f3a = 0.62583575f;
+                    float fc3 = v.x * fc2 - v.y * fs2;
+                    float fs3 = v.x * fs2 + v.y * fc2;
+                    float p20 = 1.9843135f * v.z * p12 + -1.0062306f * p6;
+                    wr3(o, 16, scl3(vc, f3a * fs3));
+                    wr3(o, 17, scl3(vc, f2b * fs2));
+                    wr3(o, 18, scl3(vc, f1c * fs1));
+                    wr3(o, 19, scl3(vc, f0d * v.y));
+                    wr3(o, 20, scl3(vc, p20));
+                    wr3(o, 21, scl3(vc, f0d * v.x));
+                    wr3(o, 22, scl3(vc, f1c * fc1));
+                    wr3(o, 23, scl3(vc, f2b * fc2));
+                    wr3(o, 24, scl3(vc, f3a * fc3));
+                }
+            }
+        }
+    }
+}
+/* sh_color_viewdir_vjp (kernels/sh.rs:249-381) */
+static v3 sh_viewdir_vjp(const float* c, uint32_t deg, v3 v, v3 vc) {
+    float gx = 0.0f, gy = 0.0f, gz = 0.0f;
+    if (deg >= 1) {
+        float f0a = 0.4886025f;
+        float s_n1 = dot3(rd3(c, 1), vc), s_z0 = dot3(rd3(c, 2), vc), s_p1 = dot3(rd3(c, 3), vc);
+        gx += -f0a * s_p1;
+        gy += -f0a * s_n1;
+        gz += f0a * s_z0;
+        if (deg >= 2) {
+            float z = v.z, x = v.x, y = v.y;
+            float c2 = -1.0925485f;
+            float f1a = 0.54627424f;
+            float s_n2 = dot3(rd3(c, 4), vc);
+            s_n1 = dot3(rd3(c, 5), vc);
+            s_z0 = dot3(rd3(c, 6), vc);
+            s_p1 = dot3(rd3(c, 7), vc);
+            float s_p2 = dot3(rd3(c, 8), vc);
+            gx += 2.0f * f1a * y * s_n2 + c2 * z * s_p1 + 2.0f * f1a * x * s_p2;
+            gy += 2.0f * f1a * x * s_n2 + c2 * z * s_n1 - 2.0f * f1a * y * s_p2;
+            gz += c2 * y * s_n1 + 2.0f * 0.9461747f * z * s_z0 + c2 * x * s_p1;
+            if (deg >= 3) {
+                float z2 = z * z, x2 = x * x, y2 = y * y;
+                float f2a = -0.5900436f;
+                float c1b = 1.4453057f;
+                float f1b = c1b * z;
+                float c0c = -2.285229f;
+                float f0c = c0c * z2 + 0.4570458f;
+                float f0c_dz = 2.0f * c0c * z;
+                float s_n3 = dot3(rd3(c, 9), vc);
+                s_n2 = dot3(rd3(c, 10), vc);
+                s_n1 = dot3(rd3(c, 11), vc);
+                s_z0 = dot3(rd3(c, 12), vc);
+                s_p1 = dot3(rd3(c, 13), vc);
+                s_p2 = dot3(rd3(c, 14), vc);
+                float s_p3 = dot3(rd3(c, 15), vc);
+                float d12_z = 3.0f * 1.8658817f * z2 - 1.119529f;
+                gx += f2a * 6.0f * x * y * s_n3 + 2.0f * f1b * y * s_n2 + f0c * s_p1 + 2.0f * f1b * x * s_p2 + f2a * 3.0f * (x2 - y2) * s_p3;
+                gy += f2a * 3.0f * (x2 - y2) * s_n3 + 2.0f * f1b * x * s_n2 + f0c * s_n1 + (-2.0f) * f1b * y * s_p2 + f2a * (-6.0f) * x * y * s_p3;
+                gz += 2.0f * c1b * x * y * s_n2 + f0c_dz * y * s_n1 + d12_z * s_z0 + f0c_dz * x * s_p1 + c1b * (x2 - y2) * s_p2;
+                if (deg >= 4) {
+                    float fc1 = x2 - y2;
+                    float fs1 = 2.0f * x * y;
+                    float fc2 = x * fc1 - y * fs1;
+                    float fs2 = x * fs1 + y * fc1;
+                    float f0d = z * (-4.683326f * z2 + 2.0071396f);
+                    float f0d_dz = -14.049978f * z2 + 2.0071396f;
+                    float f1c = 3.3116114f * z2 - 0.47308735f;
+                    float f1c_dz = 2.0f * 3.3116114f * z;
+                    float f2b_dz_const = -1.7701308f;
+                    float f2b = f2b_dz_const * z;
+                    float f3a = 0.62583575f;
+                    float p12 = z * (1.8658817f * z2 - 1.119529f);
+                    float dp12 = 3.0f * 1.8658817f * z2 - 1.119529f;
+                    float dp6 = 2.0f * 0.9461747f * z;
+                    float dp20 = 1.9843135f * (p12 + z * dp12) - 1.0062306f * dp6;
+                    float s_n4 = dot3(rd3(c, 16), vc);
+                    s_n3 = dot3(rd3(c, 17), vc);
+                    s_n2 = dot3(rd3(c, 18), vc);
+                    s_n1 = dot3(rd3(c, 19), vc);
+                    s_z0 = dot3(rd3(c, 20), vc);
+                    s_p1 = dot3(rd3(c, 21), vc);
+                    s_p2 = dot3(rd3(c, 22), vc);
+                    s_p3 = dot3(rd3(c, 23), vc);
+                    float s_p4 = dot3(rd3(c, 24), vc);
+                    gx += f3a * 4.0f * fs2 * s_n4 + f2b * 3.0f * fs1 * s_n3 + f1c * 2.0f * y * s_n2 + f0d * s_p1 + f1c * 2.0f * x * s_p2 + f2b * 3.0f * fc1 * s_p3 + f3a * 4.0f * fc2 * s_p4;
+                    gy += f3a * 4.0f * fc2 * s_n4 + f2b * 3.0f * fc1 * s_n3 + f1c * 2.0f * x * s_n2 + f0d * s_n1 + f1c * (-2.0f) * y * s_p2 + f2b * (-3.0f) * fs1 * s_p3 + f3a * (-4.0f) * fs2 * s_p4;
+                    gz += f2b_dz_const * fs2 * s_n3 + f1c_dz * fs1 * s_n2 + f0d_dz * y * s_n1 + dp20 * s_z0 + f0d_dz * x * s_p1 + f1c_dz * fc1 * s_p2 + f2b_dz_const * fc2 * s_p3;
+                }
+            }
+        }
+    }
+    return mk3(gx, gy, gz);
+}
+
+void or_project_backward(const bh_project_uniforms* u, const float* transforms,
+                         const float* sh_coeffs, const float* raw_opac,
+                         const uint32_t* gfc, uint32_t num_visible, uint32_t num_splats,
+                         uint32_t sh_degree, uint32_t mip, const float* v_combined,
+                         float* v_transforms, float* v_coeffs, float* v_raw_opac,
+                         float* v_refine) {
+    uint32_t nc = (sh_degree + 1) * (sh_degree + 1);
+    memset(v_transforms, 0, (size_t)num_splats * 10 * sizeof(float));
+    memset(v_coeffs, 0, (size_t)num_splats * nc * 3 * sizeof(float));
+    memset(v_raw_opac, 0, (size_t)num_splats * sizeof(float));
+    memset(v_refine, 0, (size_t)num_splats * sizeof(float));
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+    for (int64_t ci = 0; ci < (int64_t)num_visible; ci++) {
+        uint32_t g = gfc[ci];
+        const float* rg = v_combined + (size_t)ci * 11;
+        int any = 0;
+        for (int k = 0; k < 11; k++) any |= rg[k] != 0.0f;
+        if (!any) continue;
+        const float* t = transforms + (size_t)g * 10;
+        v3 mean = mk3(t[0], t[1], t[2]);
+        v3 scale = mk3(bh_expf(t[7]), bh_expf(t[8]), bh_expf(t[9]));
+        qt qu = {t[3], t[4], t[5], t[6]};
+        qt q = qnormalize(qu);
+        v3 uw = sub3(mean, mk3(u->camera_pos[0], u->camera_pos[1], u->camera_pos[2]));
+        float ulen = len3(uw);
+        v3 v = scl3(uw, 1.0f / ulen);
+        const float* coeffs = sh_coeffs + (size_t)g * nc * 3;
+        v3 vcol = mk3(rg[5], rg[6], rg[7]);
+        sh_color_vjp(v_coeffs + (size_t)g * nc * 3, sh_degree, v, vcol);
+        v3 vv = sh_viewdir_vjp(coeffs, sh_degree, v, vcol);
+        float vdot = dot3(v, vv);
+        v3 v_mean_sh = scl3(sub3(vv, scl3(v, vdot)), 1.0f / ulen);
+        v3 mean_c = world_to_cam(u, mean);
+        m3 r = qmat(q);
+        m3 m = m3diag(r, scale);
+        s2 raw_cov = calc_cov2d(u, scale, q, mean_c);
+        float comp;
+        s2 cov = compensate_cov2d(raw_cov, mip, &comp);
+        float sig = bh_sigmoidf(raw_opac[g]);
+        v_raw_opac[g] = comp * rg[8] * sig * (1.0f - sig);
+        float rc = bh_is_finite(rg[9]) ? rg[9] : 0.0f;
+        v_refine[g] = bh_clampf(rc, 0.0f, 1.0e32f);
+        s2 conic_inv = s2inv(cov);
+        s2 v_inv = {rg[2], rg[3] * 0.5f, rg[4]};
+        s2 v_cov2d = inverse2x2_vjp(conic_inv, v_inv);
+        s3 covar = m3outer(m);
+        m3 vr = view_rot(u);
+        s3 cov_c = s3cong(covar, vr);
+        m23 J = jac_pinhole(u, mean_c);
+        v3 v_mean_c = projection_vjp(u, J, mean_c, cov_c, v_cov2d, mk2(rg[0], rg[1]));
+        v_mean_c = mk3(v_mean_c.x, v_mean_c.y, v_mean_c.z + rg[10]);
+        s3 vcc = m23tcong(J, v_cov2d);
+        v3 v_mean = add3(m3tmulv(vr, v_mean_c), v_mean_sh);
+        m3 v_m = s3mulm3(s3scale(s3tcong(vcc, vr), 2.0f), m);
+        v3 v_scale = mk3(dot3(col0(r), col0(v_m)) * scale.x, dot3(col1(r), col1(v_m)) * scale.y,
+                         dot3(col2(r), col2(v_m)) * scale.z);
+        qt qg = quat_to_mat_vjp(q, m3diag(v_m, scale));
+        qt vq = normalize_vjp(qu, qg);
+        float* o = v_transforms + (size_t)g * 10;
+        o[0] = v_mean.x; o[1] = v_mean.y; o[2] = v_mean.z;
+        o[3] = vq.w; o[4] = vq.x; o[5] = vq.y; o[6] = vq.z;
+        o[7] = v_scale.x; o[8] = v_scale.y; o[9] = v_scale.z;
+    }
+}

@@ -1,0 +1,83 @@
+/*
+ * bh_oracle.h — CPU restatement of Brush's differentiable tile rasterizer.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the parity checker for the gfx950
+ * kernels and the timed CPU baseline of bench.py.  Nothing in the product
+ * (brush_amd/, include/) links it or calls it.
+ *
+ * Every function restates one piece of the reference in plain C11, in the
+ * reference's own float operation order (left-to-right as written in the
+ * CubeCL source, no contraction), so that integer outputs can be compared bit
+ * for bit.  exp/log come from brush_amd/csrc/bh_math.h, which the kernels use
+ * too; those two functions are pinned separately against float64 libm.
+ *
+ * Parity status per function (what pins each one is listed in the .c file
+ * above the function):
+ *   or_project_forward, or_project_visible, or_map_intersects,
+ *   or_stable_sort, or_prefix_sum, or_tile_offsets, or_rasterize,
+ *   or_rasterize_reference, or_rasterize_backward, or_project_backward:
+ *   pinned (see tests/test_oracle.py).
+ */
+#ifndef BH_ORACLE_H
+#define BH_ORACLE_H
+
+#include <stdint.h>
+#include "../include/brush_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Number of OpenMP threads the parallel loops may use (1 = sequential). */
+void or_set_threads(int n);
+int or_get_max_threads(void);
+
+uint64_t or_project_forward(const bh_project_uniforms* u, const float* transforms,
+                            const float* raw_opac, uint32_t n, uint32_t mip,
+                            uint32_t* intersect_counts, float* max_radius, float* depths,
+                            uint8_t* visible_mask);
+
+void or_stable_sort(uint32_t* keys, uint32_t* vals, uint64_t n, uint32_t sorting_bits);
+
+void or_prefix_sum(const uint32_t* in, uint32_t* out, uint64_t n);
+
+void or_project_visible(const bh_project_uniforms* u, const float* transforms,
+                        const float* sh_coeffs, const float* raw_opac,
+                        const uint32_t* global_from_compact_gid, uint32_t num_visible,
+                        uint32_t sh_degree, uint32_t mip, float* projected);
+
+void or_map_intersects(uint32_t tile_bw, uint32_t tile_bh, const float* projected,
+                       const uint32_t* cum_tiles_hit, uint32_t num_visible,
+                       uint32_t* tile_id_from_isect, uint32_t* compact_gid_from_isect);
+
+void or_tile_offsets(const uint32_t* tile_id_from_isect, uint64_t num_inter, uint32_t num_tiles,
+                     uint32_t* tile_offsets);
+
+void or_rasterize(uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,
+                  const float* background, const float* projected,
+                  const uint32_t* compact_gid_from_isect,
+                  const uint32_t* global_from_compact_gid, const uint32_t* tile_offsets_pre,
+                  uint32_t flags, void* out_img, float* visible, uint32_t* tile_offsets_post);
+
+void or_rasterize_reference(const float* projected, uint32_t num_splats, uint32_t img_w,
+                            uint32_t img_h, const float* background, uint32_t smooth_cutoff,
+                            float* out_rgba);
+
+void or_rasterize_backward(uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,
+                           const float* background, const float* out_img,
+                           const float* projected, const uint32_t* compact_gid_from_isect,
+                           const uint32_t* tile_offsets, uint32_t num_visible,
+                           const float* v_output, uint32_t flags, float* v_combined);
+
+void or_project_backward(const bh_project_uniforms* u, const float* transforms,
+                         const float* sh_coeffs, const float* raw_opac,
+                         const uint32_t* global_from_compact_gid, uint32_t num_visible,
+                         uint32_t num_splats, uint32_t sh_degree, uint32_t mip,
+                         const float* v_combined, float* v_transforms, float* v_coeffs,
+                         float* v_raw_opac, float* v_refine);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,260 @@
+"""ctypes wrapper and numpy orchestration of the CPU restatement (liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, ``__graft_entry__.smoke()`` and
+the ``cpu_baseline`` leg of bench.py, as the checker.  The product package
+(brush_amd) never imports this module.
+
+The forward pipeline mirrors render.rs:78-543: project_forward, compaction in
+global-id order, stable depth sort, gather + inclusive scan of tile counts,
+project_visible, map_gaussians_to_intersect, stable tile sort, tile offsets,
+rasterize.  Compaction in global-id order followed by a stable sort resolves
+equal depths by global id; the reference resolves them by atomic arrival
+order, which is not reproducible (brush-render/src/tests/mod.rs:443-451).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+
+FLAG_BWD_INFO = 1
+FLAG_SMOOTH_CUTOFF = 2
+FLAG_RENDER_DEPTH = 4
+FLAG_MIP = 8
+FLAG_REFINE_WEIGHT = 16
+
+
+class Uniforms(ctypes.Structure):
+    """bh_project_uniforms (include/brush_hip.h)."""
+
+    _fields_ = [
+        ("viewmat", ctypes.c_float * 12),
+        ("half_max_render_fov", ctypes.c_float),
+        ("fx", ctypes.c_float), ("fy", ctypes.c_float), ("cx", ctypes.c_float), ("cy", ctypes.c_float),
+        ("lim_pos_x", ctypes.c_float), ("lim_pos_y", ctypes.c_float),
+        ("lim_neg_x", ctypes.c_float), ("lim_neg_y", ctypes.c_float),
+        ("camera_pos", ctypes.c_float * 3),
+        ("img_w", ctypes.c_uint32), ("img_h", ctypes.c_uint32),
+        ("tile_bw", ctypes.c_uint32), ("tile_bh", ctypes.c_uint32),
+        ("sh_degree", ctypes.c_uint32),
+        ("total_splats", ctypes.c_uint32),
+        ("num_visible", ctypes.c_uint32),
+    ]
+
+
+def make_uniforms(d: dict) -> Uniforms:
+    u = Uniforms()
+    for i, v in enumerate(d["viewmat"]):
+        u.viewmat[i] = float(v)
+    for k in ("half_max_render_fov", "fx", "fy", "cx", "cy", "lim_pos_x", "lim_pos_y", "lim_neg_x", "lim_neg_y"):
+        setattr(u, k, float(d[k]))
+    for i in range(3):
+        u.camera_pos[i] = float(d["camera_pos"][i])
+    for k in ("img_w", "img_h", "tile_bw", "tile_bh", "sh_degree", "total_splats", "num_visible"):
+        setattr(u, k, int(d[k]))
+    return u
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            raise RuntimeError(f"{_LIB_PATH} is missing: run `make -C oracle` or __graft_entry__.build()")
+        L = ctypes.CDLL(_LIB_PATH)
+        P = ctypes.c_void_p
+        U32 = ctypes.c_uint32
+        U64 = ctypes.c_uint64
+        UP = ctypes.POINTER(Uniforms)
+        L.or_set_threads.argtypes = [ctypes.c_int]
+        L.or_get_max_threads.restype = ctypes.c_int
+        L.or_project_forward.argtypes = [UP, P, P, U32, U32, P, P, P, P]
+        L.or_project_forward.restype = U64
+        L.or_stable_sort.argtypes = [P, P, U64, U32]
+        L.or_prefix_sum.argtypes = [P, P, U64]
+        L.or_project_visible.argtypes = [UP, P, P, P, P, U32, U32, U32, P]
+        L.or_map_intersects.argtypes = [U32, U32, P, P, U32, P, P]
+        L.or_tile_offsets.argtypes = [P, U64, U32, P]
+        L.or_rasterize.argtypes = [U32, U32, U32, U32, P, P, P, P, P, U32, P, P, P]
+        L.or_rasterize_reference.argtypes = [P, U32, U32, U32, P, U32, P]
+        L.or_rasterize_backward.argtypes = [U32, U32, U32, U32, P, P, P, P, P, U32, P, U32, P]
+        L.or_project_backward.argtypes = [UP, P, P, P, P, U32, U32, U32, U32, P, P, P, P, P]
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def set_threads(n: int):
+    lib().or_set_threads(int(n))
+
+
+def max_threads() -> int:
+    return int(lib().or_get_max_threads())
+
+
+# ---- primitives ---------------------------------------------------------------
+
+def stable_sort(keys: np.ndarray, vals: np.ndarray, sorting_bits: int = 32):
+    k = np.ascontiguousarray(keys, dtype=np.uint32).copy()
+    v = np.ascontiguousarray(vals, dtype=np.uint32).copy()
+    lib().or_stable_sort(_p(k), _p(v), k.size, sorting_bits)
+    return k, v
+
+
+def prefix_sum(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.uint32)
+    out = np.empty_like(x)
+    lib().or_prefix_sum(_p(x), _p(out), x.size)
+    return out
+
+
+def tile_offsets(tile_ids: np.ndarray, num_tiles: int) -> np.ndarray:
+    ids = np.ascontiguousarray(tile_ids, dtype=np.uint32)
+    out = np.empty((num_tiles * 2,), dtype=np.uint32)
+    lib().or_tile_offsets(_p(ids), ids.size, num_tiles, _p(out))
+    return out
+
+
+def rasterize_reference(projected: np.ndarray, img_w: int, img_h: int, background, smooth: bool) -> np.ndarray:
+    proj = np.ascontiguousarray(projected, dtype=np.float32).reshape(-1, 10)
+    bg = np.asarray(background, dtype=np.float32)
+    out = np.empty((img_h, img_w, 4), dtype=np.float32)
+    lib().or_rasterize_reference(_p(proj), proj.shape[0], img_w, img_h, _p(bg), int(smooth), _p(out))
+    return out
+
+
+# ---- full forward / backward ----------------------------------------------------
+
+@dataclass
+class ForwardResult:
+    num_visible: int
+    num_intersections: int
+    intersect_counts: np.ndarray
+    max_radius: np.ndarray
+    depths_sorted: np.ndarray
+    global_from_compact_gid: np.ndarray
+    cum_tiles_hit: np.ndarray
+    projected: np.ndarray
+    tile_id_from_isect: np.ndarray
+    compact_gid_from_isect: np.ndarray
+    tile_offsets_pre: np.ndarray
+    tile_offsets: np.ndarray
+    out_img: np.ndarray
+    visible: np.ndarray
+    uniforms: dict
+
+
+def render_forward(uniforms: dict, transforms, sh_coeffs, raw_opac, flags: int = FLAG_BWD_INFO,
+                   background=(0.0, 0.0, 0.0)) -> ForwardResult:
+    L = lib()
+    transforms = np.ascontiguousarray(transforms, dtype=np.float32).reshape(-1, 10)
+    sh_coeffs = np.ascontiguousarray(sh_coeffs, dtype=np.float32)
+    raw_opac = np.ascontiguousarray(raw_opac, dtype=np.float32).reshape(-1)
+    n = transforms.shape[0]
+    nc = sh_coeffs.shape[1] if sh_coeffs.ndim == 3 else 1
+    deg = int(round(nc ** 0.5)) - 1
+    ud = dict(uniforms)
+    ud["total_splats"] = n
+    ud["sh_degree"] = deg
+    w, h = ud["img_w"], ud["img_h"]
+    tbw, tbh = ud["tile_bw"], ud["tile_bh"]
+    num_tiles = tbw * tbh
+    mip = int((flags & FLAG_MIP) != 0)
+    bwd_info = (flags & FLAG_BWD_INFO) != 0
+    depth = bwd_info and (flags & FLAG_RENDER_DEPTH) != 0
+    bg = np.asarray(background, dtype=np.float32)
+    u = make_uniforms(ud)
+
+    counts = np.zeros(n, np.uint32)
+    radius = np.zeros(n, np.float32)
+    depths = np.zeros(n, np.float32)
+    mask = np.zeros(n, np.uint8)
+    total = 0
+    if n:
+        total = L.or_project_forward(ctypes.byref(u), _p(transforms), _p(raw_opac), n, mip,
+                                     _p(counts), _p(radius), _p(depths), _p(mask))
+    vis_ids = np.nonzero(mask)[0].astype(np.uint32)
+    num_visible = int(vis_ids.size)
+    if total >= 2 ** 32:
+        raise OverflowError("more than 2^32 intersections")
+    dkeys = depths[vis_ids].view(np.uint32).copy()
+    dkeys, gfc = stable_sort(dkeys, vis_ids, 32)
+    depths_sorted = dkeys.view(np.float32)
+    compact_counts = counts[gfc]
+    cum = prefix_sum(compact_counts)
+    ud["num_visible"] = num_visible
+    u = make_uniforms(ud)
+    projected = np.zeros((max(num_visible, 1), 10), np.float32)
+    if num_visible:
+        L.or_project_visible(ctypes.byref(u), _p(transforms), _p(sh_coeffs), _p(raw_opac), _p(gfc),
+                             num_visible, deg, mip, _p(projected))
+    m = int(total)
+    tile_ids = np.zeros(max(m, 1), np.uint32)
+    cgids = np.zeros(max(m, 1), np.uint32)
+    if num_visible and m:
+        L.or_map_intersects(tbw, tbh, _p(projected), _p(cum), num_visible, _p(tile_ids), _p(cgids))
+    bits = int(num_tiles).bit_length()  # render.rs:392: 32 - leading_zeros(T)
+    if m:
+        tk, tv = stable_sort(tile_ids[:m], cgids[:m], bits)
+        tile_ids[:m] = tk
+        cgids[:m] = tv
+    off_pre = tile_offsets(tile_ids[:m], num_tiles)
+    off_post = np.zeros_like(off_pre)
+    if bwd_info:
+        out_img = np.zeros((h, w, 5 if depth else 4), np.float32)
+        visible = np.zeros(n, np.float32)
+    else:
+        out_img = np.zeros((h, w), np.uint32)
+        visible = np.zeros(1, np.float32)
+    gfc_arg = gfc if gfc.size else np.zeros(1, np.uint32)
+    L.or_rasterize(w, h, tbw, tbh, _p(bg), _p(projected), _p(cgids), _p(gfc_arg), _p(off_pre),
+                   flags, _p(out_img), _p(visible), _p(off_post))
+    return ForwardResult(num_visible, m, counts, radius, depths_sorted, gfc, cum, projected,
+                         tile_ids, cgids, off_pre.reshape(tbh, tbw, 2), off_post.reshape(tbh, tbw, 2),
+                         out_img, visible, ud)
+
+
+def rasterize_backward(fwd: ForwardResult, v_output: np.ndarray, flags: int = FLAG_REFINE_WEIGHT,
+                       background=(0.0, 0.0, 0.0)) -> np.ndarray:
+    ud = fwd.uniforms
+    bg = np.asarray(background, dtype=np.float32)
+    v_output = np.ascontiguousarray(v_output, dtype=np.float32)
+    v_comb = np.zeros((max(fwd.num_visible, 1), 11), np.float32)
+    lib().or_rasterize_backward(ud["img_w"], ud["img_h"], ud["tile_bw"], ud["tile_bh"], _p(bg),
+                                _p(np.ascontiguousarray(fwd.out_img)), _p(fwd.projected),
+                                _p(fwd.compact_gid_from_isect),
+                                _p(np.ascontiguousarray(fwd.tile_offsets).reshape(-1)),
+                                fwd.num_visible, _p(v_output), flags, _p(v_comb))
+    return v_comb
+
+
+def project_backward(fwd: ForwardResult, transforms, sh_coeffs, raw_opac, v_combined, mip: bool = False):
+    ud = fwd.uniforms
+    transforms = np.ascontiguousarray(transforms, dtype=np.float32).reshape(-1, 10)
+    sh_coeffs = np.ascontiguousarray(sh_coeffs, dtype=np.float32)
+    raw_opac = np.ascontiguousarray(raw_opac, dtype=np.float32).reshape(-1)
+    n = transforms.shape[0]
+    nc = sh_coeffs.shape[1]
+    deg = ud["sh_degree"]
+    v_t = np.empty((n, 10), np.float32)
+    v_c = np.empty((n, nc, 3), np.float32)
+    v_o = np.empty((n,), np.float32)
+    v_r = np.empty((n,), np.float32)
+    gfc = fwd.global_from_compact_gid if fwd.num_visible else np.zeros(1, np.uint32)
+    u = make_uniforms(ud)
+    lib().or_project_backward(ctypes.byref(u), _p(transforms), _p(sh_coeffs), _p(raw_opac), _p(gfc),
+                              fwd.num_visible, n, deg, int(mip),
+                              _p(np.ascontiguousarray(v_combined, dtype=np.float32)),
+                              _p(v_t), _p(v_c), _p(v_o), _p(v_r))
+    return v_t, v_c, v_o, v_r
