@@ -1,0 +1,567 @@
+// api.hip — C ABI of the gfx950 rasterizer (include/brush_hip.h).
+//
+// Host orchestration of the forward pass (crates/brush-render/src/render.rs:78-543
+// restated) and of the two backward operations
+// (crates/brush-render-bwd/src/render_bwd.rs:90-447 restated).  All work is
+// queued on the context's stream; the forward reads back one 24-byte block of
+// counters (visible count, intersection count, depth-key range, error flags).
+#include <hip/hip_runtime.h>
+#include <string.h>
+
+#include <algorithm>
+#include <new>
+#include <string>
+
+#include "bh_internal.h"
+
+struct bh_fwd_state {
+    bh_ctx* ctx;
+    bh_fwd_info info;
+    std::vector<void*> buffers;
+};
+
+namespace bh {
+
+static const size_t kAlign = 256;
+
+hipError_t Pool::alloc(void** out, size_t bytes) {
+    bytes = std::max<size_t>(kAlign, (bytes + kAlign - 1) / kAlign * kAlign);
+    size_t best = (size_t)-1;
+    for (size_t i = 0; i < free_blocks.size(); i++) {
+        const Block& b = free_blocks[i];
+        if (b.bytes >= bytes && b.bytes <= 2 * bytes + (1u << 20) &&
+            (best == (size_t)-1 || b.bytes < free_blocks[best].bytes))
+            best = i;
+    }
+    if (best != (size_t)-1) {
+        Block b = free_blocks[best];
+        free_blocks.erase(free_blocks.begin() + best);
+        cached_bytes -= b.bytes;
+        live[b.ptr] = b.bytes;
+        *out = b.ptr;
+        return hipSuccess;
+    }
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) {
+        // drop the cache and try once more
+        (void)hipGetLastError();
+        trim();
+        e = hipMalloc(&p, bytes);
+        if (e != hipSuccess) return e;
+    }
+    live[p] = bytes;
+    *out = p;
+    return hipSuccess;
+}
+
+void Pool::release(void* ptr) {
+    if (!ptr) return;
+    auto it = live.find(ptr);
+    if (it == live.end()) return;
+    free_blocks.push_back(Block{ptr, it->second});
+    cached_bytes += it->second;
+    live.erase(it);
+}
+
+void Pool::trim() {
+    for (auto& b : free_blocks) (void)hipFree(b.ptr);
+    free_blocks.clear();
+    cached_bytes = 0;
+}
+
+KernelTimer::KernelTimer(bh_ctx* c, const char* n) : ctx(c), name(n) {
+    if (!ctx->timing) return;
+    auto get = [&]() {
+        hipEvent_t e = nullptr;
+        if (!ctx->event_cache.empty()) {
+            e = ctx->event_cache.back();
+            ctx->event_cache.pop_back();
+        } else if (hipEventCreate(&e) != hipSuccess) {
+            e = nullptr;
+        }
+        return e;
+    };
+    e0 = get();
+    e1 = get();
+    if (e0) (void)hipEventRecord(e0, ctx->stream);
+}
+
+KernelTimer::~KernelTimer() {
+    if (!ctx->timing || !e0 || !e1) return;
+    (void)hipEventRecord(e1, ctx->stream);
+    ctx->pending.push_back(Timing{name, e0, e1});
+}
+
+bh_status set_error(bh_ctx* ctx, bh_status st, const std::string& msg) {
+    if (ctx) ctx->last_error = msg;
+    return st;
+}
+
+bh_status check_launch(bh_ctx* ctx, const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return set_error(ctx, BH_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
+    return BH_OK;
+}
+
+static bh_status hip_check(bh_ctx* ctx, hipError_t e, const char* what) {
+    if (e == hipSuccess) return BH_OK;
+    (void)hipGetLastError();
+    return set_error(ctx, e == hipErrorOutOfMemory ? BH_ERR_OOM : BH_ERR_DEVICE,
+                     std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// RAII set of pool buffers released (stream ordered) at scope exit.
+struct Scratch {
+    bh_ctx* ctx;
+    std::vector<void*> bufs;
+    explicit Scratch(bh_ctx* c) : ctx(c) {}
+    ~Scratch() {
+        for (void* p : bufs) ctx->pool.release(p);
+    }
+    template <class T>
+    bh_status get(T** out, size_t count) {
+        void* p = nullptr;
+        hipError_t e = ctx->pool.alloc(&p, std::max<size_t>(count, 1) * sizeof(T));
+        if (e != hipSuccess) return hip_check(ctx, e, "workspace allocation");
+        bufs.push_back(p);
+        *out = (T*)p;
+        return BH_OK;
+    }
+};
+
+static uint32_t bit_length(uint32_t x) { return x ? 32u - (uint32_t)__builtin_clz(x) : 0u; }
+
+static bh_status check_device_error(bh_ctx* ctx, uint32_t flags) {
+    if (flags & kErrSpin) return set_error(ctx, BH_ERR_INTERNAL, "a look-back spin exceeded its bound");
+    if (flags & kErrOverflow) return set_error(ctx, BH_ERR_INTERNAL, "a device count overflowed");
+    return BH_OK;
+}
+
+}  // namespace bh
+
+using namespace bh;
+
+#define BH_TRY(expr)                      \
+    do {                                  \
+        bh_status _st = (expr);           \
+        if (_st != BH_OK) return _st;     \
+    } while (0)
+
+extern "C" {
+
+bh_status bh_ctx_create(int device, bh_ctx** out) {
+    if (!out) return BH_ERR_INVALID_ARG;
+    *out = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || device < 0 || device >= count) {
+        (void)hipGetLastError();
+        return BH_ERR_DEVICE;
+    }
+    if (hipSetDevice(device) != hipSuccess) return BH_ERR_DEVICE;
+    bh_ctx* ctx = new (std::nothrow) bh_ctx();
+    if (!ctx) return BH_ERR_OOM;
+    ctx->device = device;
+    if (hipMalloc(&ctx->d_counters, 64) != hipSuccess || hipHostMalloc(&ctx->h_counters, 64) != hipSuccess) {
+        (void)hipGetLastError();
+        if (ctx->d_counters) (void)hipFree(ctx->d_counters);
+        delete ctx;
+        return BH_ERR_OOM;
+    }
+    *out = ctx;
+    return BH_OK;
+}
+
+void bh_ctx_destroy(bh_ctx* ctx) {
+    if (!ctx) return;
+    (void)hipStreamSynchronize(ctx->stream);
+    for (auto& t : ctx->pending) {
+        (void)hipEventDestroy(t.start);
+        (void)hipEventDestroy(t.stop);
+    }
+    for (auto e : ctx->event_cache) (void)hipEventDestroy(e);
+    ctx->pool.trim();
+    for (auto& kv : ctx->pool.live) (void)hipFree(kv.first);
+    (void)hipFree(ctx->d_counters);
+    (void)hipHostFree(ctx->h_counters);
+    delete ctx;
+}
+
+bh_status bh_ctx_set_stream(bh_ctx* ctx, void* hip_stream) {
+    if (!ctx) return BH_ERR_INVALID_ARG;
+    hipStream_t s = (hipStream_t)hip_stream;
+    if (s != ctx->stream) {
+        BH_TRY(hip_check(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize"));
+        ctx->stream = s;
+    }
+    return BH_OK;
+}
+
+const char* bh_last_error(const bh_ctx* ctx) { return ctx ? ctx->last_error.c_str() : "null context"; }
+
+bh_status bh_ctx_set_timing(bh_ctx* ctx, int enable) {
+    if (!ctx) return BH_ERR_INVALID_ARG;
+    ctx->timing = enable != 0;
+    return BH_OK;
+}
+
+static bh_status collect_timings(bh_ctx* ctx) {
+    BH_TRY(hip_check(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize"));
+    for (auto& t : ctx->pending) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, t.start, t.stop) != hipSuccess) {
+            (void)hipGetLastError();
+            ms = 0.0f;
+        }
+        auto it = std::find_if(ctx->totals.begin(), ctx->totals.end(),
+                               [&](const std::pair<std::string, TimingTotal>& kv) { return kv.first == t.name; });
+        if (it == ctx->totals.end()) {
+            ctx->totals.push_back({t.name, TimingTotal{}});
+            it = ctx->totals.end() - 1;
+        }
+        it->second.launches += 1;
+        it->second.total_ms += ms;
+        ctx->event_cache.push_back(t.start);
+        ctx->event_cache.push_back(t.stop);
+    }
+    ctx->pending.clear();
+    return BH_OK;
+}
+
+bh_status bh_ctx_read_timings(bh_ctx* ctx, bh_kernel_timing* out, int max, int* count) {
+    if (!ctx || !count) return BH_ERR_INVALID_ARG;
+    BH_TRY(collect_timings(ctx));
+    int n = 0;
+    for (auto& kv : ctx->totals) {
+        if (n >= max || !out) break;
+        memset(out[n].name, 0, sizeof(out[n].name));
+        strncpy(out[n].name, kv.first.c_str(), sizeof(out[n].name) - 1);
+        out[n].launches = kv.second.launches;
+        out[n].total_ms = kv.second.total_ms;
+        n++;
+    }
+    *count = out ? n : (int)ctx->totals.size();
+    return BH_OK;
+}
+
+bh_status bh_ctx_reset_timings(bh_ctx* ctx) {
+    if (!ctx) return BH_ERR_INVALID_ARG;
+    BH_TRY(collect_timings(ctx));
+    ctx->totals.clear();
+    return BH_OK;
+}
+
+uint64_t bh_ctx_workspace_bytes(const bh_ctx* ctx) {
+    if (!ctx) return 0;
+    uint64_t b = ctx->pool.cached_bytes;
+    for (auto& kv : ctx->pool.live) b += kv.second;
+    return b;
+}
+
+bh_status bh_radix_argsort(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t* vals_in, uint32_t n,
+                           uint32_t sorting_bits, uint32_t* keys_out, uint32_t* vals_out) {
+    if (!ctx) return BH_ERR_INVALID_ARG;
+    if (sorting_bits > 32) return set_error(ctx, BH_ERR_INVALID_ARG, "Can only sort up to 32 bits");
+    if (n == 0) return BH_OK;
+    if (!keys_in || !vals_in || !keys_out || !vals_out)
+        return set_error(ctx, BH_ERR_INVALID_ARG, "radix_argsort: null pointer");
+    if (keys_in == keys_out || vals_in == vals_out)
+        return set_error(ctx, BH_ERR_INVALID_ARG, "radix_argsort: outputs must not alias inputs");
+    // brush-sort runs ceil(bits/4) 4-bit passes, i.e. it orders by the low
+    // 4*ceil(bits/4) key bits; keep exactly that key width.
+    const uint32_t width = 4u * ((sorting_bits + 3u) / 4u);
+    if (width == 0) {
+        BH_TRY(hip_check(ctx, hipMemcpyAsync(keys_out, keys_in, (size_t)n * 4, hipMemcpyDeviceToDevice, ctx->stream),
+                         "copy"));
+        return hip_check(ctx, hipMemcpyAsync(vals_out, vals_in, (size_t)n * 4, hipMemcpyDeviceToDevice, ctx->stream),
+                         "copy");
+    }
+    const uint32_t passes = (width + 7u) / 8u;
+    const uint32_t mask = width >= 32 ? 0xFFFFFFFFu : ((1u << width) - 1u);
+    Scratch ws(ctx);
+    uint32_t *tk, *tv, *masked = nullptr;
+    void* scratch;
+    BH_TRY(ws.get(&tk, n));
+    BH_TRY(ws.get(&tv, n));
+    BH_TRY(ws.get((char**)&scratch, radix_sort_scratch_bytes(n, passes)));
+    if (mask != 0xFFFFFFFFu) {
+        // Sort (key & mask, index) then gather: the emitted keys must be the
+        // caller's original keys, including any bits above the key width.
+        uint32_t *perm, *sk;
+        BH_TRY(ws.get(&masked, n));
+        BH_TRY(ws.get(&perm, n));
+        BH_TRY(ws.get(&sk, n));
+        launch_mask_u32(ctx, keys_in, mask, n, masked);
+        BH_TRY(radix_sort_pairs(ctx, masked, nullptr, n, passes, 0u, 0xFFFFFFFFu, sk, perm, tk, tv, scratch));
+        launch_gather_pairs(ctx, keys_in, vals_in, perm, n, keys_out, vals_out);
+        return check_launch(ctx, "radix_argsort gather");
+    }
+    return radix_sort_pairs(ctx, keys_in, vals_in, n, passes, 0u, 0xFFFFFFFFu, keys_out, vals_out, tk, tv, scratch);
+}
+
+bh_status bh_prefix_sum(bh_ctx* ctx, const uint32_t* in, uint32_t* out, uint32_t n) {
+    if (!ctx) return BH_ERR_INVALID_ARG;
+    if (n == 0) return BH_OK;
+    if (!in || !out) return set_error(ctx, BH_ERR_INVALID_ARG, "prefix_sum: null pointer");
+    Scratch ws(ctx);
+    char* scratch;
+    BH_TRY(ws.get(&scratch, scan_scratch_bytes(n)));
+    return inclusive_scan(ctx, in, nullptr, out, n, scratch);
+}
+
+bh_status bh_get_tile_offsets(bh_ctx* ctx, const uint32_t* ids, uint32_t m, uint32_t num_tiles, uint32_t* offsets) {
+    if (!ctx) return BH_ERR_INVALID_ARG;
+    if (!offsets || (m && !ids)) return set_error(ctx, BH_ERR_INVALID_ARG, "get_tile_offsets: null pointer");
+    launch_tile_offsets(ctx, ids, m, num_tiles, offsets);
+    return check_launch(ctx, "get_tile_offsets");
+}
+
+bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const float background[3],
+                            const float* transforms, const float* sh_coeffs, const float* raw_opacities,
+                            uint32_t num_splats, uint32_t sh_degree, uint32_t flags, void* out_img, float* visible,
+                            float* max_radius, uint32_t* tile_offsets, bh_fwd_state** state_out) {
+    if (!ctx) return BH_ERR_INVALID_ARG;
+    if (!uin || !background || !state_out) return set_error(ctx, BH_ERR_INVALID_ARG, "render_forward: null argument");
+    *state_out = nullptr;
+    if (uin->img_w == 0 || uin->img_h == 0)
+        return set_error(ctx, BH_ERR_INVALID_ARG, "Can't render images with 0 size.");
+    if (sh_degree > 4) return set_error(ctx, BH_ERR_INVALID_ARG, "sh_degree must be <= 4");
+    const bool bwd = (flags & BH_FLAG_BWD_INFO) != 0;
+    const bool mip = (flags & BH_FLAG_MIP) != 0;
+    if (!out_img || !tile_offsets || (num_splats && (!transforms || !sh_coeffs || !raw_opacities || !max_radius)) ||
+        (bwd && num_splats && !visible))
+        return set_error(ctx, BH_ERR_INVALID_ARG, "render_forward: null buffer");
+
+    bh_project_uniforms u = *uin;
+    u.tile_bw = div_up(u.img_w, BH_TILE_WIDTH);
+    u.tile_bh = div_up(u.img_h, BH_TILE_WIDTH);
+    u.sh_degree = sh_degree;
+    u.total_splats = num_splats;
+    u.num_visible = 0;
+    const uint32_t num_tiles = u.tile_bw * u.tile_bh;
+
+    bh_fwd_state* st = new (std::nothrow) bh_fwd_state();
+    if (!st) return set_error(ctx, BH_ERR_OOM, "render_forward: host allocation");
+    st->ctx = ctx;
+    memset(&st->info, 0, sizeof(st->info));
+    auto sget = [&](void** p, size_t bytes) -> bh_status {
+        hipError_t e = ctx->pool.alloc(p, std::max<size_t>(bytes, 4));
+        if (e != hipSuccess) return hip_check(ctx, e, "state allocation");
+        st->buffers.push_back(*p);
+        return BH_OK;
+    };
+    auto fail = [&](bh_status s) {
+        for (void* p : st->buffers) ctx->pool.release(p);
+        delete st;
+        return s;
+    };
+#define BH_STRY(expr)                         \
+    do {                                      \
+        bh_status _st = (expr);               \
+        if (_st != BH_OK) return fail(_st);   \
+    } while (0)
+
+    Scratch ws(ctx);
+    uint32_t *counts = nullptr, *gfc = nullptr, *cum = nullptr, *tile_ids = nullptr, *cgids = nullptr,
+             *off_pre = nullptr;
+    float *projected = nullptr, *depths = nullptr;
+    BH_STRY(sget((void**)&counts, (size_t)num_splats * 4));
+    BH_STRY(sget((void**)&off_pre, (size_t)num_tiles * 8));
+
+    uint32_t num_visible = 0;
+    uint64_t num_isect = 0;
+    uint32_t kmin = 0, kmax = 0;
+    if (bwd && num_splats) launch_fill_u32(ctx, (uint32_t*)visible, 0u, num_splats);
+    if (num_splats) {
+        uint32_t* depth_keys;
+        BH_STRY(ws.get(&depth_keys, num_splats));
+        // counters: visible, flags, isect lo, isect hi, min key, max key
+        launch_fill_u32(ctx, ctx->d_counters, 0u, 4);
+        launch_fill_u32(ctx, ctx->d_counters + 4, 0xFFFFFFFFu, 1);
+        launch_fill_u32(ctx, ctx->d_counters + 5, 0u, 1);
+        launch_project_forward(ctx, u, transforms, raw_opacities, num_splats, mip, counts, max_radius, depth_keys,
+                               ctx->d_counters);
+        BH_STRY(check_launch(ctx, "project_forward"));
+        BH_STRY(hip_check(ctx, hipMemcpyAsync(ctx->h_counters, ctx->d_counters, 24, hipMemcpyDeviceToHost, ctx->stream),
+                          "count readback"));
+        BH_STRY(hip_check(ctx, hipStreamSynchronize(ctx->stream), "count readback"));
+        num_visible = ctx->h_counters[0];
+        num_isect = (uint64_t)ctx->h_counters[2] | ((uint64_t)ctx->h_counters[3] << 32);
+        kmin = ctx->h_counters[4];
+        kmax = ctx->h_counters[5];
+        BH_STRY(check_device_error(ctx, ctx->h_counters[1]));
+        if (num_isect > 0xFFFFFFFFull)
+            return fail(set_error(ctx, BH_ERR_SHAPE, "more than 2^32 - 1 tile intersections"));
+
+        BH_STRY(sget((void**)&gfc, (size_t)num_splats * 4));
+        if (num_visible) {
+            // depth sort: key' = min(bits - kmin, kmax - kmin + 1); culled splats
+            // (all-ones key) map to the cap and sort last.
+            const uint32_t cap = kmax - kmin + 1u;
+            const uint32_t passes = std::max<uint32_t>(1u, (bit_length(cap) + 7u) / 8u);
+            uint32_t *sk, *tk, *tv;
+            char* scr;
+            BH_STRY(ws.get(&sk, num_splats));
+            BH_STRY(ws.get(&tk, num_splats));
+            BH_STRY(ws.get(&tv, num_splats));
+            BH_STRY(ws.get(&scr, radix_sort_scratch_bytes(num_splats, passes)));
+            BH_STRY(radix_sort_pairs(ctx, depth_keys, nullptr, num_splats, passes, kmin, cap, sk, gfc, tk, tv, scr));
+        }
+    }
+    BH_STRY(sget((void**)&cum, (size_t)num_visible * 4));
+    BH_STRY(sget((void**)&projected, (size_t)std::max<uint32_t>(num_visible, 1) * 40));
+    BH_STRY(sget((void**)&depths, (size_t)num_visible * 4));
+    if (!gfc) BH_STRY(sget((void**)&gfc, 4));
+    const uint32_t m = (uint32_t)num_isect;
+    BH_STRY(sget((void**)&tile_ids, (size_t)std::max<uint32_t>(m, 1) * 4));
+    BH_STRY(sget((void**)&cgids, (size_t)std::max<uint32_t>(m, 1) * 4));
+    if (num_visible) {
+        char* scr;
+        BH_STRY(ws.get(&scr, scan_scratch_bytes(num_visible)));
+        BH_STRY(inclusive_scan(ctx, counts, gfc, cum, num_visible, scr));
+        launch_project_visible(ctx, u, transforms, sh_coeffs, raw_opacities, gfc, num_visible, sh_degree, mip,
+                               projected, depths);
+        BH_STRY(check_launch(ctx, "project_visible"));
+    } else {
+        launch_fill_u32(ctx, (uint32_t*)projected, 0u, 10);
+    }
+    if (m) {
+        uint32_t *ut, *uc, *tk, *tv;
+        char* scr;
+        BH_STRY(ws.get(&ut, m));
+        BH_STRY(ws.get(&uc, m));
+        BH_STRY(ws.get(&tk, m));
+        BH_STRY(ws.get(&tv, m));
+        launch_map_intersects(ctx, u.tile_bw, u.tile_bh, projected, cum, num_visible, ut, uc);
+        BH_STRY(check_launch(ctx, "map_intersects"));
+        // tile sort over bits(num_tiles) bits (render.rs:392-395)
+        const uint32_t bits = bit_length(num_tiles);
+        const uint32_t passes = std::max<uint32_t>(1u, (bits + 7u) / 8u);
+        BH_STRY(ws.get(&scr, radix_sort_scratch_bytes(m, passes)));
+        BH_STRY(radix_sort_pairs(ctx, ut, uc, m, passes, 0u, 0xFFFFFFFFu, tile_ids, cgids, tk, tv, scr));
+    } else {
+        launch_fill_u32(ctx, tile_ids, 0u, 1);
+        launch_fill_u32(ctx, cgids, 0u, 1);
+    }
+    launch_tile_offsets(ctx, tile_ids, m, num_tiles, off_pre);
+    launch_rasterize(ctx, u.img_w, u.img_h, u.tile_bw, u.tile_bh, background, num_visible, projected, cgids, gfc,
+                     off_pre, flags,
+                     out_img, visible, tile_offsets);
+    BH_STRY(check_launch(ctx, "rasterize"));
+#undef BH_STRY
+
+    u.num_visible = num_visible;
+    bh_fwd_info& in = st->info;
+    in.num_splats = num_splats;
+    in.num_visible = num_visible;
+    in.num_intersections = m;
+    in.num_tiles = num_tiles;
+    in.tile_bw = u.tile_bw;
+    in.tile_bh = u.tile_bh;
+    in.img_w = u.img_w;
+    in.img_h = u.img_h;
+    in.sh_degree = sh_degree;
+    in.flags = flags;
+    in.uniforms = u;
+    in.projected = projected;
+    in.global_from_compact_gid = gfc;
+    in.depths = depths;
+    in.intersect_counts = counts;
+    in.cum_tiles_hit = cum;
+    in.tile_id_from_isect = tile_ids;
+    in.compact_gid_from_isect = cgids;
+    in.tile_offsets_pre = off_pre;
+    *state_out = st;
+    return BH_OK;
+}
+
+bh_status bh_fwd_state_info(const bh_fwd_state* state, bh_fwd_info* out) {
+    if (!state || !out) return BH_ERR_INVALID_ARG;
+    *out = state->info;
+    return BH_OK;
+}
+
+void bh_fwd_state_release(bh_fwd_state* state) {
+    if (!state) return;
+    for (void* p : state->buffers) state->ctx->pool.release(p);
+    delete state;
+}
+
+bh_status bh_rasterize_backward(bh_ctx* ctx, const float* out_img, const float* projected,
+                                const uint32_t* compact_gid_from_isect, const uint32_t* tile_offsets,
+                                uint32_t num_visible, const float background[3], uint32_t img_w, uint32_t img_h,
+                                const float* v_output, uint32_t flags, float* v_combined) {
+    if (!ctx) return BH_ERR_INVALID_ARG;
+    if (img_w == 0 || img_h == 0) return set_error(ctx, BH_ERR_INVALID_ARG, "Can't render images with 0 size.");
+    if (!out_img || !projected || !compact_gid_from_isect || !tile_offsets || !background || !v_output ||
+        !v_combined)
+        return set_error(ctx, BH_ERR_INVALID_ARG, "rasterize_backward: null argument");
+    const uint32_t tbw = div_up(img_w, BH_TILE_WIDTH), tbh = div_up(img_h, BH_TILE_WIDTH);
+    launch_fill_u32(ctx, (uint32_t*)v_combined, 0u, (uint64_t)std::max<uint32_t>(num_visible, 1) * 11);
+    if (num_visible)
+        launch_rasterize_backward(ctx, img_w, img_h, tbw, tbh, background, num_visible, out_img, projected,
+                                  compact_gid_from_isect, tile_offsets, v_output, flags, v_combined);
+    return check_launch(ctx, "rasterize_backward");
+}
+
+bh_status bh_project_backward(bh_ctx* ctx, const bh_project_uniforms* u, const float* transforms,
+                              const float* sh_coeffs, const float* raw_opacities,
+                              const uint32_t* global_from_compact_gid, const float* v_combined, uint32_t flags,
+                              float* v_transforms, float* v_coeffs, float* v_raw_opac, float* v_refine) {
+    if (!ctx) return BH_ERR_INVALID_ARG;
+    if (!u) return set_error(ctx, BH_ERR_INVALID_ARG, "project_backward: null uniforms");
+    const uint32_t n = u->total_splats;
+    if (n == 0) return BH_OK;
+    if (u->sh_degree > 4) return set_error(ctx, BH_ERR_INVALID_ARG, "sh_degree must be <= 4");
+    if (u->num_visible > n) return set_error(ctx, BH_ERR_SHAPE, "num_visible > total_splats");
+    if (!transforms || !sh_coeffs || !raw_opacities || !v_combined || !v_transforms || !v_coeffs || !v_raw_opac ||
+        !v_refine || (u->num_visible && !global_from_compact_gid))
+        return set_error(ctx, BH_ERR_INVALID_ARG, "project_backward: null argument");
+    Scratch ws(ctx);
+    uint32_t* cfg;
+    BH_TRY(ws.get(&cfg, n));
+    launch_invert_permutation(ctx, global_from_compact_gid, u->num_visible, n, cfg);
+    launch_project_backward(ctx, *u, transforms, sh_coeffs, raw_opacities, cfg, n, u->sh_degree,
+                            (flags & BH_FLAG_MIP) != 0, v_combined, v_transforms, v_coeffs, v_raw_opac, v_refine);
+    return check_launch(ctx, "project_backward");
+}
+
+bh_status bh_copy_to_host(bh_ctx* ctx, void* dst, const void* src, uint64_t bytes) {
+    if (!ctx || (bytes && (!dst || !src))) return BH_ERR_INVALID_ARG;
+    if (!bytes) return BH_OK;
+    BH_TRY(hip_check(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream), "copy to host"));
+    return hip_check(ctx, hipStreamSynchronize(ctx->stream), "copy to host");
+}
+
+bh_status bh_copy_to_device(bh_ctx* ctx, void* dst, const void* src, uint64_t bytes) {
+    if (!ctx || (bytes && (!dst || !src))) return BH_ERR_INVALID_ARG;
+    if (!bytes) return BH_OK;
+    BH_TRY(hip_check(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream), "copy to device"));
+    return hip_check(ctx, hipStreamSynchronize(ctx->stream), "copy to device");
+}
+
+bh_status bh_copy_device(bh_ctx* ctx, void* dst, const void* src, uint64_t bytes) {
+    if (!ctx || (bytes && (!dst || !src))) return BH_ERR_INVALID_ARG;
+    if (!bytes) return BH_OK;
+    return hip_check(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream), "copy on device");
+}
+
+bh_status bh_device_alloc(bh_ctx* ctx, void** out, uint64_t bytes) {
+    if (!ctx || !out) return BH_ERR_INVALID_ARG;
+    *out = nullptr;
+    return hip_check(ctx, hipMalloc(out, std::max<uint64_t>(bytes, 4)), "hipMalloc");
+}
+
+bh_status bh_device_free(bh_ctx* ctx, void* ptr) {
+    if (!ctx) return BH_ERR_INVALID_ARG;
+    if (!ptr) return BH_OK;
+    return hip_check(ctx, hipFree(ptr), "hipFree");
+}
+
+bh_status bh_synchronize(bh_ctx* ctx) {
+    if (!ctx) return BH_ERR_INVALID_ARG;
+    return hip_check(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+}
+
+}  // extern "C"

@@ -1,0 +1,132 @@
+// bh_internal.h — context, workspace pool and launch helpers shared by the
+// C-ABI implementation and the kernel translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/brush_hip.h"
+
+namespace bh {
+
+// Stream-ordered caching pool.  Every allocation is used on the context's
+// single stream, so a block returned to the pool can be handed out again
+// immediately: later kernels on the stream are ordered after earlier users.
+struct Pool {
+    struct Block {
+        void* ptr;
+        size_t bytes;
+    };
+    std::vector<Block> free_blocks;
+    std::map<void*, size_t> live;
+    size_t cached_bytes = 0;
+
+    hipError_t alloc(void** out, size_t bytes);
+    void release(void* ptr);
+    void trim();  // hipFree everything in the free list
+};
+
+struct Timing {
+    std::string name;
+    hipEvent_t start, stop;
+};
+
+struct TimingTotal {
+    uint32_t launches = 0;
+    double total_ms = 0.0;
+};
+
+}  // namespace bh
+
+struct bh_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string last_error;
+    bh::Pool pool;
+    bool timing = false;
+    std::vector<bh::Timing> pending;
+    std::vector<hipEvent_t> event_cache;
+    std::vector<std::pair<std::string, bh::TimingTotal>> totals;
+    // small device scratch: [0] num_visible, [1] error flags,
+    // [2..3] num_intersections (u64), [4] min depth key, [5] max depth key
+    uint32_t* d_counters = nullptr;
+    uint32_t* h_counters = nullptr;  // pinned
+};
+
+namespace bh {
+
+constexpr uint32_t kErrSpin = 1u;      // a look-back spin hit its bound
+constexpr uint32_t kErrOverflow = 2u;  // a count exceeded its field
+
+// Scoped timing of one kernel launch on the context's stream.
+struct KernelTimer {
+    bh_ctx* ctx;
+    const char* name;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    KernelTimer(bh_ctx* c, const char* n);
+    ~KernelTimer();
+};
+
+bh_status set_error(bh_ctx* ctx, bh_status st, const std::string& msg);
+bh_status check_launch(bh_ctx* ctx, const char* what);
+
+inline uint32_t div_up(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
+
+// ---- kernel launchers implemented in the .hip translation units ----------------
+
+// fill.hip
+void launch_fill_u32(bh_ctx* ctx, uint32_t* p, uint32_t value, uint64_t count);
+
+// sort.hip
+size_t radix_sort_scratch_bytes(uint32_t n, uint32_t passes);
+// Stable sort of (key', value) pairs by the low 8*passes bits of
+// key' = min(key - key_sub, key_cap).  vals_in == nullptr means vals = index.
+// The transformed keys are what the sort emits.  tmp_* are n-element buffers.
+bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t* vals_in, uint32_t n,
+                           uint32_t passes, uint32_t key_sub, uint32_t key_cap, uint32_t* keys_out,
+                           uint32_t* vals_out, uint32_t* tmp_keys, uint32_t* tmp_vals, void* scratch);
+// out[i] = in[i] & mask
+void launch_mask_u32(bh_ctx* ctx, const uint32_t* in, uint32_t mask, uint32_t n, uint32_t* out);
+// keys_out[i] = keys_in[perm[i]], vals_out[i] = vals_in[perm[i]]
+void launch_gather_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t* vals_in, const uint32_t* perm,
+                         uint32_t n, uint32_t* keys_out, uint32_t* vals_out);
+size_t scan_scratch_bytes(uint32_t n);
+// Inclusive scan of in[i] (or in[gather[i]] when gather != nullptr).
+bh_status inclusive_scan(bh_ctx* ctx, const uint32_t* in, const uint32_t* gather, uint32_t* out, uint32_t n,
+                         void* scratch);
+
+// project.hip
+void launch_project_forward(bh_ctx* ctx, const bh_project_uniforms& u, const float* transforms,
+                            const float* raw_opac, uint32_t n, bool mip, uint32_t* intersect_counts,
+                            float* max_radius, uint32_t* depth_keys, uint32_t* counters);
+void launch_project_visible(bh_ctx* ctx, const bh_project_uniforms& u, const float* transforms, const float* sh,
+                            const float* raw_opac, const uint32_t* gfc, uint32_t num_visible, uint32_t sh_degree,
+                            bool mip, float* projected, float* depths);
+void launch_map_intersects(bh_ctx* ctx, uint32_t tile_bw, uint32_t tile_bh, const float* projected,
+                           const uint32_t* cum, uint32_t num_visible, uint32_t* tile_ids, uint32_t* cgids);
+
+// raster.hip
+void launch_tile_offsets(bh_ctx* ctx, const uint32_t* tile_ids, uint32_t m, uint32_t num_tiles,
+                         uint32_t* offsets);
+void launch_rasterize(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,
+                      const float* bg, uint32_t num_visible, const float* projected, const uint32_t* cgids, const uint32_t* gfc,
+                      const uint32_t* off_pre, uint32_t flags, void* out_img, float* visible,
+                      uint32_t* off_post);
+
+// backward.hip
+void launch_rasterize_backward(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,
+                               const float* bg, uint32_t num_visible, const float* out_img, const float* projected,
+                               const uint32_t* cgids, const uint32_t* offsets, const float* v_output,
+                               uint32_t flags, float* v_combined);
+void launch_invert_permutation(bh_ctx* ctx, const uint32_t* gfc, uint32_t num_visible, uint32_t n,
+                               uint32_t* compact_from_global);
+void launch_project_backward(bh_ctx* ctx, const bh_project_uniforms& u, const float* transforms, const float* sh,
+                             const float* raw_opac, const uint32_t* compact_from_global, uint32_t n,
+                             uint32_t sh_degree, bool mip, const float* v_combined, float* v_transforms,
+                             float* v_coeffs, float* v_raw_opac, float* v_refine);
+
+}  // namespace bh

@@ -1,0 +1,540 @@
+// bh_splat_math.h — per-splat math of the rasterizer for gfx950 kernels.
+//
+// Restates the reference's cube-side math (crates/brush-cube/src/lib.rs,
+// crates/brush-render/src/kernels/{helpers,sh,camera_model/pinhole}.rs,
+// crates/brush-render-bwd/src/kernels/project_backwards.rs).  Expressions keep
+// the reference's evaluation order and are compiled without contraction
+// (-ffp-contract=off), so the integer decisions derived from them (culling,
+// tile counts, tile ids) are reproducible bit for bit on a CPU.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/brush_hip.h"
+#include "bh_math.h"
+
+#define BH_DEV __device__ __forceinline__
+
+namespace bh {
+
+struct V3 {
+    float x, y, z;
+};
+struct V2 {
+    float x, y;
+};
+struct Q4 {
+    float w, x, y, z;
+};
+// 3x3, column-major: cI_R is column I, row R.
+struct M3 {
+    float c0x, c0y, c0z, c1x, c1y, c1z, c2x, c2y, c2z;
+};
+struct M23 {
+    V2 c0, c1, c2;
+};
+struct S2 {
+    float c00, c01, c11;
+};
+struct S3 {
+    float c00, c01, c02, c11, c12, c22;
+};
+
+BH_DEV V3 v3(float x, float y, float z) { return V3{x, y, z}; }
+BH_DEV V2 v2(float x, float y) { return V2{x, y}; }
+BH_DEV V3 operator+(V3 a, V3 b) { return v3(a.x + b.x, a.y + b.y, a.z + b.z); }
+BH_DEV V3 operator-(V3 a, V3 b) { return v3(a.x - b.x, a.y - b.y, a.z - b.z); }
+BH_DEV V3 operator*(V3 a, float s) { return v3(a.x * s, a.y * s, a.z * s); }
+BH_DEV float dot(V3 a, V3 b) { return a.x * b.x + a.y * b.y + a.z * b.z; }
+BH_DEV bool finite3(V3 a) { return bh_is_finite(a.x) && bh_is_finite(a.y) && bh_is_finite(a.z); }
+BH_DEV V2 operator+(V2 a, V2 b) { return v2(a.x + b.x, a.y + b.y); }
+BH_DEV V2 operator*(V2 a, float s) { return v2(a.x * s, a.y * s); }
+BH_DEV float dot(V2 a, V2 b) { return a.x * b.x + a.y * b.y; }
+
+BH_DEV float qdot(Q4 a, Q4 b) { return a.w * b.w + a.x * b.x + a.y * b.y + a.z * b.z; }
+// Quat::normalize (lib.rs:185-188)
+BH_DEV Q4 qnormalize(Q4 q) {
+    float s = 1.0f / sqrtf(qdot(q, q));
+    return Q4{q.w * s, q.x * s, q.y * s, q.z * s};
+}
+// Quat::to_mat3 (lib.rs:190-216)
+BH_DEV M3 qmat(Q4 q) {
+    float x2 = q.x * q.x, y2 = q.y * q.y, z2 = q.z * q.z;
+    float xy = q.x * q.y, xz = q.x * q.z, yz = q.y * q.z;
+    float wx = q.w * q.x, wy = q.w * q.y, wz = q.w * q.z;
+    M3 m;
+    m.c0x = 1.0f - 2.0f * (y2 + z2);
+    m.c0y = 2.0f * (xy + wz);
+    m.c0z = 2.0f * (xz - wy);
+    m.c1x = 2.0f * (xy - wz);
+    m.c1y = 1.0f - 2.0f * (x2 + z2);
+    m.c1z = 2.0f * (yz + wx);
+    m.c2x = 2.0f * (xz + wy);
+    m.c2y = 2.0f * (yz - wx);
+    m.c2z = 1.0f - 2.0f * (x2 + y2);
+    return m;
+}
+BH_DEV V3 col0(const M3& m) { return v3(m.c0x, m.c0y, m.c0z); }
+BH_DEV V3 col1(const M3& m) { return v3(m.c1x, m.c1y, m.c1z); }
+BH_DEV V3 col2(const M3& m) { return v3(m.c2x, m.c2y, m.c2z); }
+BH_DEV V3 row0(const M3& m) { return v3(m.c0x, m.c1x, m.c2x); }
+BH_DEV V3 row1(const M3& m) { return v3(m.c0y, m.c1y, m.c2y); }
+BH_DEV V3 row2(const M3& m) { return v3(m.c0z, m.c1z, m.c2z); }
+BH_DEV M3 from_cols(V3 a, V3 b, V3 c) { return M3{a.x, a.y, a.z, b.x, b.y, b.z, c.x, c.y, c.z}; }
+// Mat3::mul_vec3 (lib.rs:262-268)
+BH_DEV V3 mulv(const M3& m, V3 v) { return col0(m) * v.x + col1(m) * v.y + col2(m) * v.z; }
+// Mat3::transpose_mul_vec3 (lib.rs:270-273)
+BH_DEV V3 tmulv(const M3& m, V3 v) { return v3(dot(col0(m), v), dot(col1(m), v), dot(col2(m), v)); }
+// Mat3::mul_mat3 (lib.rs:275-282)
+BH_DEV M3 mul(const M3& a, const M3& b) { return from_cols(mulv(a, col0(b)), mulv(a, col1(b)), mulv(a, col2(b))); }
+// Mat3::mul_diag (lib.rs:284-291)
+BH_DEV M3 mul_diag(const M3& m, V3 s) { return from_cols(col0(m) * s.x, col1(m) * s.y, col2(m) * s.z); }
+// Mat3::outer_product_self (lib.rs:305-318)
+BH_DEV S3 outer_self(const M3& m) {
+    V3 r0 = row0(m), r1 = row1(m), r2 = row2(m);
+    return S3{dot(r0, r0), dot(r0, r1), dot(r0, r2), dot(r1, r1), dot(r1, r2), dot(r2, r2)};
+}
+// Mat2x3::mul_vec3 / mul_mat3 / rows / gram_matrix (lib.rs:330-384)
+BH_DEV V2 mulv(const M23& m, V3 v) { return m.c0 * v.x + m.c1 * v.y + m.c2 * v.z; }
+BH_DEV M23 mul(const M23& m, const M3& n) { return M23{mulv(m, col0(n)), mulv(m, col1(n)), mulv(m, col2(n))}; }
+BH_DEV V3 row0(const M23& m) { return v3(m.c0.x, m.c1.x, m.c2.x); }
+BH_DEV V3 row1(const M23& m) { return v3(m.c0.y, m.c1.y, m.c2.y); }
+BH_DEV S2 gram(const M23& m) {
+    S2 s;
+    s.c00 = m.c0.x * m.c0.x + m.c1.x * m.c1.x + m.c2.x * m.c2.x;
+    s.c01 = m.c0.x * m.c0.y + m.c1.x * m.c1.y + m.c2.x * m.c2.y;
+    s.c11 = m.c0.y * m.c0.y + m.c1.y * m.c1.y + m.c2.y * m.c2.y;
+    return s;
+}
+// Sym2 (lib.rs:395-458)
+BH_DEV V2 mulv(const S2& s, V2 v) { return v2(s.c00, s.c01) * v.x + v2(s.c01, s.c11) * v.y; }
+BH_DEV M23 mul(const S2& s, const M23& n) { return M23{mulv(s, n.c0), mulv(s, n.c1), mulv(s, n.c2)}; }
+BH_DEV S2 scale(const S2& s, float f) { return S2{s.c00 * f, s.c01 * f, s.c11 * f}; }
+BH_DEV float max_abs(const S2& s) { return bh_maxf(bh_maxf(bh_absf(s.c00), bh_absf(s.c11)), bh_absf(s.c01)); }
+BH_DEV S2 inverse(const S2& s) {
+    float det = s.c00 * s.c11 - s.c01 * s.c01;
+    bool inv = det > 0.0f;
+    float inv_det = inv ? 1.0f / det : 0.0f;
+    return S2{s.c11 * inv_det, -s.c01 * inv_det, s.c00 * inv_det};
+}
+BH_DEV float det_strict(const S2& s) {
+    float ad = s.c00 * s.c11;
+    float bc = s.c01 * s.c01;
+    return ad - bc;
+}
+BH_DEV bool finite2(const S2& s) { return bh_is_finite(s.c00) && bh_is_finite(s.c11) && bh_is_finite(s.c01); }
+// Mat2x3::transpose_congruence_sym2 (lib.rs:357-370)
+BH_DEV S3 tcong(const M23& m, const S2& s) {
+    V2 sc0 = mulv(s, m.c0), sc1 = mulv(s, m.c1), sc2 = mulv(s, m.c2);
+    return S3{dot(m.c0, sc0), dot(m.c0, sc1), dot(m.c0, sc2), dot(m.c1, sc1), dot(m.c1, sc2), dot(m.c2, sc2)};
+}
+// Sym3 (lib.rs:472-543)
+BH_DEV V3 srow0(const S3& s) { return v3(s.c00, s.c01, s.c02); }
+BH_DEV V3 srow1(const S3& s) { return v3(s.c01, s.c11, s.c12); }
+BH_DEV V3 srow2(const S3& s) { return v3(s.c02, s.c12, s.c22); }
+BH_DEV V3 mulv(const S3& s, V3 v) { return srow0(s) * v.x + srow1(s) * v.y + srow2(s) * v.z; }
+BH_DEV S3 scale(const S3& s, float f) { return S3{s.c00 * f, s.c01 * f, s.c02 * f, s.c11 * f, s.c12 * f, s.c22 * f}; }
+BH_DEV M3 mul(const S3& s, const M3& m) { return from_cols(mulv(s, col0(m)), mulv(s, col1(m)), mulv(s, col2(m))); }
+BH_DEV S3 cong(const S3& s, const M3& m) {
+    V3 sr0 = mulv(s, row0(m)), sr1 = mulv(s, row1(m)), sr2 = mulv(s, row2(m));
+    return S3{dot(row0(m), sr0), dot(row0(m), sr1), dot(row0(m), sr2), dot(row1(m), sr1), dot(row1(m), sr2), dot(row2(m), sr2)};
+}
+BH_DEV S3 tcong(const S3& s, const M3& m) {
+    V3 sc0 = mulv(s, col0(m)), sc1 = mulv(s, col1(m)), sc2 = mulv(s, col2(m));
+    return S3{dot(col0(m), sc0), dot(col0(m), sc1), dot(col0(m), sc2), dot(col1(m), sc1), dot(col1(m), sc2), dot(col2(m), sc2)};
+}
+
+// ---- camera -----------------------------------------------------------------
+
+BH_DEV M3 view_rot(const bh_project_uniforms& u) {
+    const float* v = u.viewmat;
+    return M3{v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7], v[8]};
+}
+// world_to_cam (kernels/helpers.rs:477-482)
+BH_DEV V3 world_to_cam(const bh_project_uniforms& u, V3 mean) {
+    return mulv(view_rot(u), mean) + v3(u.viewmat[9], u.viewmat[10], u.viewmat[11]);
+}
+// project_pinhole (camera_model/pinhole.rs:24-30)
+BH_DEV V2 project_pinhole(const bh_project_uniforms& u, V3 p) {
+    float inv_z = 1.0f / p.z;
+    return v2(u.fx * p.x * inv_z + u.cx, u.fy * p.y * inv_z + u.cy);
+}
+// calculate_project_jacobian_pinhole (pinhole.rs:32-56)
+BH_DEV M23 jacobian(const bh_project_uniforms& u, V3 p) {
+    float inv_z = 1.0f / p.z;
+    float dx = u.fx * inv_z;
+    float dy = u.fy * inv_z;
+    float cxl = bh_clampf(p.x * inv_z, u.lim_neg_x, u.lim_pos_x);
+    float cyl = bh_clampf(p.y * inv_z, u.lim_neg_y, u.lim_pos_y);
+    return M23{v2(dx, 0.0f), v2(0.0f, dy), v2(-dx * cxl, -dy * cyl)};
+}
+// calc_cov2d (kernels/helpers.rs:297-330)
+BH_DEV S2 calc_cov2d(const bh_project_uniforms& u, V3 sc, Q4 q, V3 mean_c) {
+    M3 ns = mul_diag(mul(view_rot(u), qmat(q)), sc);
+    M23 jac = jacobian(u, mean_c);
+    S2 raw = gram(mul(jac, ns));
+    const float lim = 1.0e18f;
+    float ma = max_abs(raw);
+    float down = ma > lim ? lim / ma : 1.0f;
+    return scale(raw, down);
+}
+// compensate_cov2d (kernels/helpers.rs:332-350)
+template <bool MIP>
+BH_DEV S2 compensate_cov2d(const S2& c, float& comp) {
+    const float blur = MIP ? 0.1f : 0.3f;
+    S2 b{c.c00 + blur, c.c01, c.c11 + blur};
+    comp = 1.0f;
+    if (MIP) {
+        float det_raw = bh_maxf(det_strict(c), 0.0f);
+        float det_b = det_strict(b);
+        comp = sqrtf(det_raw / det_b);
+    }
+    return b;
+}
+// compute_bbox_extent (kernels/helpers.rs:227-241)
+BH_DEV V2 bbox_extent(const S2& conic, float pt) {
+    float det = conic.c00 * conic.c11 - conic.c01 * conic.c01;
+    bool degenerate = det <= 0.0f;
+    float inv_det = degenerate ? 0.0f : 1.0f / det;
+    float ex = sqrtf(2.0f * pt * conic.c11 * inv_det);
+    float ey = sqrtf(2.0f * pt * conic.c00 * inv_det);
+    return v2(degenerate ? -1.0f : ex, degenerate ? -1.0f : ey);
+}
+struct TileBox {
+    uint32_t min_x, min_y, max_x, max_y;
+};
+// get_bbox / get_tile_bbox (kernels/helpers.rs:260-295), 16x16 tiles
+BH_DEV TileBox tile_bbox(V2 m, V2 e, uint32_t bw, uint32_t bh) {
+    float cx = m.x / 16.0f, cy = m.y / 16.0f, dx = e.x / 16.0f, dy = e.y / 16.0f;
+    float bwf = (float)bw, bhf = (float)bh;
+    TileBox b;
+    b.min_x = (uint32_t)bh_clampf(cx - dx, 0.0f, bwf);
+    b.min_y = (uint32_t)bh_clampf(cy - dy, 0.0f, bhf);
+    b.max_x = (uint32_t)bh_clampf(cx + dx + 1.0f, 0.0f, bwf);
+    b.max_y = (uint32_t)bh_clampf(cy + dy + 1.0f, 0.0f, bhf);
+    return b;
+}
+// calc_sigma (brush-cube/src/lib.rs:632-638)
+BH_DEV float calc_sigma(float px, float py, const S2& c, float x, float y) {
+    float dx = px - x;
+    float dy = py - y;
+    return 0.5f * (c.c00 * dx * dx + c.c11 * dy * dy) + c.c01 * dx * dy;
+}
+// will_primitive_contribute (kernels/helpers.rs:385-424) on the 16x16 rect of tile (tx, ty)
+BH_DEV bool will_contribute(uint32_t tx, uint32_t ty, V2 m, const S2& c, float pt) {
+    float min_x = (float)(tx * 16u), min_y = (float)(ty * 16u);
+    float max_x = min_x + 16.0f, max_y = min_y + 16.0f;
+    bool x_left = m.x < min_x, x_right = m.x > max_x;
+    bool in_x = !(x_left || x_right);
+    bool y_above = m.y < min_y, y_below = m.y > max_y;
+    bool in_y = !(y_above || y_below);
+    bool hit = in_x && in_y;
+    if (!hit) {
+        float corner_x = x_left ? min_x : max_x;
+        float corner_y = y_above ? min_y : max_y;
+        float width = max_x - min_x;
+        float height = max_y - min_y;
+        float dxf = x_left ? width : -width;
+        float dyf = y_above ? height : -height;
+        float diff_x = m.x - corner_x;
+        float diff_y = m.y - corner_y;
+        float tx_raw = (dxf * c.c00 * diff_x + dxf * c.c01 * diff_y) / (dxf * c.c00 * dxf);
+        float ty_raw = (dyf * c.c01 * diff_x + dyf * c.c11 * diff_y) / (dyf * c.c11 * dyf);
+        float tt_x = in_y ? 0.0f : bh_clampf(tx_raw, 0.0f, 1.0f);
+        float tt_y = in_x ? 0.0f : bh_clampf(ty_raw, 0.0f, 1.0f);
+        float px = corner_x + tt_x * dxf;
+        float py = corner_y + tt_y * dyf;
+        hit = calc_sigma(px, py, c, m.x, m.y) <= pt;
+    }
+    return hit;
+}
+
+// ---- alpha cutoff (kernels/helpers.rs:161-190) --------------------------------
+constexpr float kCutMid = 1.0f / 255.0f;
+constexpr float kCutBand = 1.0e-3f;
+BH_DEV float cutoff_weight(float alpha) {
+    float t = bh_clampf((alpha - (kCutMid - 0.5f * kCutBand)) / kCutBand, 0.0f, 1.0f);
+    return t * t * (3.0f - 2.0f * t);
+}
+BH_DEV float cutoff_weight_deriv(float alpha) {
+    const float low = kCutMid - 0.5f * kCutBand;
+    const float high = kCutMid + 0.5f * kCutBand;
+    bool inside = alpha > low && alpha < high;
+    float t = (alpha - low) / kCutBand;
+    return inside ? (6.0f * t - 6.0f * t * t) / kCutBand : 0.0f;
+}
+
+// ---- spherical harmonics (kernels/sh.rs) --------------------------------------
+// Coefficient k of a splat's row, channel-interleaved: row[3k + ch].
+BH_DEV V3 rd3(const float* c, int k) { return v3(c[3 * k], c[3 * k + 1], c[3 * k + 2]); }
+
+// sh_coeffs_to_color (sh.rs:151-247); `c` points at the splat's SH row.
+template <int DEG>
+BH_DEV V3 sh_to_color(const float* c, V3 v) {
+    V3 color = rd3(c, 0) * 0.2820948f;
+    if (DEG >= 1) {
+        const float f0a = 0.4886025f;
+        color = color + rd3(c, 1) * (-f0a * v.y);
+        color = color + rd3(c, 2) * (f0a * v.z);
+        color = color + rd3(c, 3) * (-f0a * v.x);
+        if (DEG >= 2) {
+            float z2 = v.z * v.z;
+            float f0b = -1.0925485f * v.z;
+            const float f1a = 0.54627424f;
+            float fc1 = v.x * v.x - v.y * v.y;
+            float fs1 = 2.0f * v.x * v.y;
+            float p4 = f1a * fs1, p5 = f0b * v.y, p6 = 0.9461747f * z2 - 0.31539157f;
+            float p7 = f0b * v.x, p8 = f1a * fc1;
+            color = color + rd3(c, 4) * p4;
+            color = color + rd3(c, 5) * p5;
+            color = color + rd3(c, 6) * p6;
+            color = color + rd3(c, 7) * p7;
+            color = color + rd3(c, 8) * p8;
+            if (DEG >= 3) {
+                float f0c = -2.285229f * z2 + 0.4570458f;
+                float f1b = 1.4453057f * v.z;
+                const float f2a = -0.5900436f;
+                float fc2 = v.x * fc1 - v.y * fs1;
+                float fs2 = v.x * fs1 + v.y * fc1;
+                float p12 = v.z * (1.8658817f * z2 - 1.119529f);
+                color = color + rd3(c, 9) * (f2a * fs2);
+                color = color + rd3(c, 10) * (f1b * fs1);
+                color = color + rd3(c, 11) * (f0c * v.y);
+                color = color + rd3(c, 12) * p12;
+                color = color + rd3(c, 13) * (f0c * v.x);
+                color = color + rd3(c, 14) * (f1b * fc1);
+                color = color + rd3(c, 15) * (f2a * fc2);
+                if (DEG >= 4) {
+                    float f0d = v.z * (-4.683326f * z2 + 2.0071396f);
+                    float f1c = 3.3116114f * z2 - 0.47308735f;
+                    float f2b = -1.7701308f * v.z;
+                    const float f3a = 0.62583575f;
+                    float fc3 = v.x * fc2 - v.y * fs2;
+                    float fs3 = v.x * fs2 + v.y * fc2;
+                    float p20 = 1.9843135f * v.z * p12 - 1.0062306f * p6;
+                    color = color + rd3(c, 16) * (f3a * fs3);
+                    color = color + rd3(c, 17) * (f2b * fs2);
+                    color = color + rd3(c, 18) * (f1c * fs1);
+                    color = color + rd3(c, 19) * (f0d * v.y);
+                    color = color + rd3(c, 20) * p20;
+                    color = color + rd3(c, 21) * (f0d * v.x);
+                    color = color + rd3(c, 22) * (f1c * fc1);
+                    color = color + rd3(c, 23) * (f2b * fc2);
+                    color = color + rd3(c, 24) * (f3a * fc3);
+                }
+            }
+        }
+    }
+    return color;
+}
+
+// Evaluate the SH basis functions (the factors of sh_coeffs_to_color_vjp,
+// sh.rs:383-466) into basis[0..(DEG+1)^2).
+template <int DEG>
+BH_DEV void sh_basis(V3 v, float* basis) {
+    basis[0] = 0.2820948f;
+    if (DEG >= 1) {
+        const float f0a = 0.4886025f;
+        basis[1] = -f0a * v.y;
+        basis[2] = f0a * v.z;
+        basis[3] = -f0a * v.x;
+        if (DEG >= 2) {
+            float z2 = v.z * v.z;
+            float f0b = -1.0925485f * v.z;
+            const float f1a = 0.54627424f;
+            float fc1 = v.x * v.x - v.y * v.y;
+            float fs1 = 2.0f * v.x * v.y;
+            float p6 = 0.9461747f * z2 - 0.31539157f;
+            basis[4] = f1a * fs1;
+            basis[5] = f0b * v.y;
+            basis[6] = p6;
+            basis[7] = f0b * v.x;
+            basis[8] = f1a * fc1;
+            if (DEG >= 3) {
+                float f0c = -2.285229f * z2 + 0.4570458f;
+                float f1b = 1.4453057f * v.z;
+                const float f2a = -0.5900436f;
+                float fc2 = v.x * fc1 - v.y * fs1;
+                float fs2 = v.x * fs1 + v.y * fc1;
+                float p12 = v.z * (1.8658817f * z2 - 1.119529f);
+                basis[9] = f2a * fs2;
+                basis[10] = f1b * fs1;
+                basis[11] = f0c * v.y;
+                basis[12] = p12;
+                basis[13] = f0c * v.x;
+                basis[14] = f1b * fc1;
+                basis[15] = f2a * fc2;
+                if (DEG >= 4) {
+                    float f0d = v.z * (-4.683326f * z2 + 2.0071396f);
+                    float f1c = 3.3116114f * z2 - 0.47308735f;
+                    float f2b = -1.7701308f * v.z;
+                    const float f3a = 0.62583575f;
+                    float fc3 = v.x * fc2 - v.y * fs2;
+                    float fs3 = v.x * fs2 + v.y * fc2;
+                    basis[16] = f3a * fs3;
+                    basis[17] = f2b * fs2;
+                    basis[18] = f1c * fs1;
+                    basis[19] = f0d * v.y;
+                    basis[20] = 1.9843135f * v.z * p12 + -1.0062306f * p6;
+                    basis[21] = f0d * v.x;
+                    basis[22] = f1c * fc1;
+                    basis[23] = f2b * fc2;
+                    basis[24] = f3a * fc3;
+                }
+            }
+        }
+    }
+}
+
+// sh_color_viewdir_vjp (sh.rs:249-381)
+template <int DEG>
+BH_DEV V3 sh_viewdir_vjp(const float* c, V3 v, V3 vc) {
+    float gx = 0.0f, gy = 0.0f, gz = 0.0f;
+    if (DEG >= 1) {
+        const float f0a = 0.4886025f;
+        float s_n1 = dot(rd3(c, 1), vc), s_z0 = dot(rd3(c, 2), vc), s_p1 = dot(rd3(c, 3), vc);
+        gx += -f0a * s_p1;
+        gy += -f0a * s_n1;
+        gz += f0a * s_z0;
+        if (DEG >= 2) {
+            float z = v.z, x = v.x, y = v.y;
+            const float c2 = -1.0925485f;
+            const float f1a = 0.54627424f;
+            float s_n2 = dot(rd3(c, 4), vc);
+            s_n1 = dot(rd3(c, 5), vc);
+            s_z0 = dot(rd3(c, 6), vc);
+            s_p1 = dot(rd3(c, 7), vc);
+            float s_p2 = dot(rd3(c, 8), vc);
+            gx += 2.0f * f1a * y * s_n2 + c2 * z * s_p1 + 2.0f * f1a * x * s_p2;
+            gy += 2.0f * f1a * x * s_n2 + c2 * z * s_n1 - 2.0f * f1a * y * s_p2;
+            gz += c2 * y * s_n1 + 2.0f * 0.9461747f * z * s_z0 + c2 * x * s_p1;
+            if (DEG >= 3) {
+                float z2 = z * z, x2 = x * x, y2 = y * y;
+                const float f2a = -0.5900436f;
+                const float c1b = 1.4453057f;
+                float f1b = c1b * z;
+                const float c0c = -2.285229f;
+                float f0c = c0c * z2 + 0.4570458f;
+                float f0c_dz = 2.0f * c0c * z;
+                float s_n3 = dot(rd3(c, 9), vc);
+                s_n2 = dot(rd3(c, 10), vc);
+                s_n1 = dot(rd3(c, 11), vc);
+                s_z0 = dot(rd3(c, 12), vc);
+                s_p1 = dot(rd3(c, 13), vc);
+                s_p2 = dot(rd3(c, 14), vc);
+                float s_p3 = dot(rd3(c, 15), vc);
+                float d12_z = 3.0f * 1.8658817f * z2 - 1.119529f;
+                gx += f2a * 6.0f * x * y * s_n3 + 2.0f * f1b * y * s_n2 + f0c * s_p1 + 2.0f * f1b * x * s_p2 +
+                      f2a * 3.0f * (x2 - y2) * s_p3;
+                gy += f2a * 3.0f * (x2 - y2) * s_n3 + 2.0f * f1b * x * s_n2 + f0c * s_n1 + (-2.0f) * f1b * y * s_p2 +
+                      f2a * (-6.0f) * x * y * s_p3;
+                gz += 2.0f * c1b * x * y * s_n2 + f0c_dz * y * s_n1 + d12_z * s_z0 + f0c_dz * x * s_p1 +
+                      c1b * (x2 - y2) * s_p2;
+                if (DEG >= 4) {
+                    float fc1 = x2 - y2;
+                    float fs1 = 2.0f * x * y;
+                    float fc2 = x * fc1 - y * fs1;
+                    float fs2 = x * fs1 + y * fc1;
+                    float f0d = z * (-4.683326f * z2 + 2.0071396f);
+                    float f0d_dz = -14.049978f * z2 + 2.0071396f;
+                    float f1c = 3.3116114f * z2 - 0.47308735f;
+                    float f1c_dz = 2.0f * 3.3116114f * z;
+                    const float f2b_dz = -1.7701308f;
+                    float f2b = f2b_dz * z;
+                    const float f3a = 0.62583575f;
+                    float p12 = z * (1.8658817f * z2 - 1.119529f);
+                    float dp12 = 3.0f * 1.8658817f * z2 - 1.119529f;
+                    float dp6 = 2.0f * 0.9461747f * z;
+                    float dp20 = 1.9843135f * (p12 + z * dp12) - 1.0062306f * dp6;
+                    float s_n4 = dot(rd3(c, 16), vc);
+                    s_n3 = dot(rd3(c, 17), vc);
+                    s_n2 = dot(rd3(c, 18), vc);
+                    s_n1 = dot(rd3(c, 19), vc);
+                    s_z0 = dot(rd3(c, 20), vc);
+                    s_p1 = dot(rd3(c, 21), vc);
+                    s_p2 = dot(rd3(c, 22), vc);
+                    s_p3 = dot(rd3(c, 23), vc);
+                    float s_p4 = dot(rd3(c, 24), vc);
+                    gx += f3a * 4.0f * fs2 * s_n4 + f2b * 3.0f * fs1 * s_n3 + f1c * 2.0f * y * s_n2 + f0d * s_p1 +
+                          f1c * 2.0f * x * s_p2 + f2b * 3.0f * fc1 * s_p3 + f3a * 4.0f * fc2 * s_p4;
+                    gy += f3a * 4.0f * fc2 * s_n4 + f2b * 3.0f * fc1 * s_n3 + f1c * 2.0f * x * s_n2 + f0d * s_n1 +
+                          f1c * (-2.0f) * y * s_p2 + f2b * (-3.0f) * fs1 * s_p3 + f3a * (-4.0f) * fs2 * s_p4;
+                    gz += f2b_dz * fs2 * s_n3 + f1c_dz * fs1 * s_n2 + f0d_dz * y * s_n1 + dp20 * s_z0 +
+                          f0d_dz * x * s_p1 + f1c_dz * fc1 * s_p2 + f2b_dz * fc2 * s_p3;
+                }
+            }
+        }
+    }
+    return v3(gx, gy, gz);
+}
+
+// ---- projection backward pieces (project_backwards.rs) -------------------------
+
+// apply_normalize_vjp (:19-52)
+BH_DEV Q4 normalize_vjp(Q4 q, Q4 g) {
+    float lsq = qdot(q, q);
+    float l = sqrtf(lsq);
+    float inv = 1.0f / (l * lsq);
+    float cc0 = -q.w * q.x, cc1 = -q.x * q.y, cc2 = -q.y * q.w;
+    float cs0 = -q.w * q.z, cs1 = -q.x * q.z, cs2 = -q.y * q.z;
+    float sw = q.w * q.w, sx = q.x * q.x, sy = q.y * q.y, sz = q.z * q.z;
+    Q4 r;
+    r.w = ((lsq - sw) * g.w + cc0 * g.x + cc2 * g.y + cs0 * g.z) * inv;
+    r.x = (cc0 * g.w + (lsq - sx) * g.x + cc1 * g.y + cs1 * g.z) * inv;
+    r.y = (cc2 * g.w + cc1 * g.x + (lsq - sy) * g.y + cs2 * g.z) * inv;
+    r.z = (cs0 * g.w + cs1 * g.x + cs2 * g.y + (lsq - sz) * g.z) * inv;
+    return r;
+}
+// quat_to_mat_vjp (:54-79)
+BH_DEV Q4 quat_to_mat_vjp(Q4 q, const M3& v) {
+    float w_grad = q.x * (v.c1z - v.c2y) + q.y * (v.c2x - v.c0z) + q.z * (v.c0y - v.c1x);
+    float x_grad = -2.0f * q.x * (v.c1y + v.c2z) + q.y * (v.c0y + v.c1x) + q.z * (v.c0z + v.c2x) + q.w * (v.c1z - v.c2y);
+    float y_grad = q.x * (v.c0y + v.c1x) - 2.0f * q.y * (v.c0x + v.c2z) + q.z * (v.c1z + v.c2y) + q.w * (v.c2x - v.c0z);
+    float z_grad = q.x * (v.c0z + v.c2x) + q.y * (v.c1z + v.c2y) - 2.0f * q.z * (v.c0x + v.c1y) + q.w * (v.c0y - v.c1x);
+    return Q4{2.0f * w_grad, 2.0f * x_grad, 2.0f * y_grad, 2.0f * z_grad};
+}
+// inverse2x2_vjp (:81-99)
+BH_DEV S2 inverse2x2_vjp(const S2& m, const S2& v) {
+    float t00 = -m.c00 * v.c00 + -m.c01 * v.c01;
+    float t01 = -m.c01 * v.c00 + -m.c11 * v.c01;
+    float t10 = -m.c00 * v.c01 + -m.c01 * v.c11;
+    float t11 = -m.c01 * v.c01 + -m.c11 * v.c11;
+    return S2{t00 * m.c00 + t10 * m.c01, t01 * m.c00 + t11 * m.c01, t01 * m.c01 + t11 * m.c11};
+}
+// calculate_projection_vjp_pinhole (camera_model/pinhole.rs:58-123)
+BH_DEV V3 projection_vjp(const bh_project_uniforms& u, const M23& J, V3 mean_c, const S3& cov_c, const S2& v_cov2d,
+                         V2 v_mean2d) {
+    float fx = u.fx, fy = u.fy;
+    float mx = mean_c.x, my = mean_c.y, mz = mean_c.z;
+    float inv_z = 1.0f / mz;
+    float mx_rz_raw = mx * inv_z, my_rz_raw = my * inv_z;
+    float mx_rz = bh_clampf(mx_rz_raw, u.lim_neg_x, u.lim_pos_x);
+    float my_rz = bh_clampf(my_rz_raw, u.lim_neg_y, u.lim_pos_y);
+    bool in_x = mx_rz_raw <= u.lim_pos_x && mx_rz_raw >= u.lim_neg_x;
+    bool in_y = my_rz_raw <= u.lim_pos_y && my_rz_raw >= u.lim_neg_y;
+    float inv_z2 = inv_z * inv_z;
+    float inv_z3 = inv_z2 * inv_z;
+    float v_mx = fx * inv_z * v_mean2d.x;
+    float v_my = fy * inv_z * v_mean2d.y;
+    float v_mz = -(fx * mx * v_mean2d.x + fy * my * v_mean2d.y) * inv_z2;
+    M23 tmp = mul(v_cov2d, J);
+    float vj00 = 2.0f * dot(row0(tmp), srow0(cov_c));
+    float vj11 = 2.0f * dot(row1(tmp), srow1(cov_c));
+    float vj20 = 2.0f * dot(row0(tmp), srow2(cov_c));
+    float vj21 = 2.0f * dot(row1(tmp), srow2(cov_c));
+    float tx = mz * mx_rz;
+    float ty = mz * my_rz;
+    if (in_x)
+        v_mx += -fx * inv_z2 * vj20;
+    else
+        v_mz += -fx * inv_z3 * vj20 * tx;
+    if (in_y)
+        v_my += -fy * inv_z2 * vj21;
+    else
+        v_mz += -fy * inv_z3 * vj21 * ty;
+    v_mz += -fx * inv_z2 * vj00 - fy * inv_z2 * vj11 + 2.0f * fx * tx * inv_z3 * vj20 + 2.0f * fy * ty * inv_z3 * vj21;
+    return v3(v_mx, v_my, v_mz);
+}
+
+}  // namespace bh

@@ -1,0 +1,279 @@
+// project.hip — per-splat projection kernels for gfx950.
+//
+//   project_forward   cull, 2D covariance and conic, power threshold, extent,
+//                     contributing-tile count, max radius, depth key
+//                     (crates/brush-render/src/kernels/project_forward.rs:20-144)
+//   project_visible   depth-ordered projected rows with SH -> RGB
+//                     (crates/brush-render/src/kernels/project_visible.rs:22-89)
+//   map_intersects    (tile id, compact id) pairs for every contributing tile
+//                     (crates/brush-render/src/kernels/map_gaussians.rs:14-92)
+//
+// Differences in organisation from the reference: project_forward does not
+// compact visible splats with an atomic slot counter (whose order depends on
+// scheduling); it writes a depth key per global id (all ones when culled) and
+// the depth sort over all ids yields the compact order, with equal depths in
+// global-id order.  Counters are aggregated per wave before the atomics.
+#include <hip/hip_runtime.h>
+
+#include "bh_internal.h"
+#include "bh_splat_math.h"
+
+namespace bh {
+
+struct ProjectOut {
+    uint32_t hits;
+    float radius;
+    float depth;
+};
+
+// The cull-and-count body of project_forward_kernel; returns false if culled.
+template <bool MIP>
+__device__ bool project_one(const bh_project_uniforms& u, const float* t, float raw_opac, ProjectOut& o) {
+    V3 mean_c = world_to_cam(u, v3(t[0], t[1], t[2]));
+    if (!(finite3(mean_c) && mean_c.z <= 1.0e10f)) return false;
+    if (mean_c.z < 0.01f) return false;
+    V3 sc = v3(bh_expf(t[7]), bh_expf(t[8]), bh_expf(t[9]));
+    if (!finite3(sc)) return false;
+    Q4 qu{t[3], t[4], t[5], t[6]};
+    float qn = qdot(qu, qu);
+    if (!(qn >= 1.0e-6f && bh_is_finite(qn))) return false;
+    if (!bh_is_finite(raw_opac)) return false;
+    Q4 q = qnormalize(qu);
+    S2 raw_cov = calc_cov2d(u, sc, q, mean_c);
+    float comp;
+    S2 cov = compensate_cov2d<MIP>(raw_cov, comp);
+    float opac = bh_sigmoidf(raw_opac) * comp;
+    if (!finite2(cov)) return false;
+    V2 m = project_pinhole(u, mean_c);
+    if (!(opac >= 1.0f / 255.0f)) return false;
+    float pt = bh_logf(opac * 255.0f);
+    S2 conic = inverse(cov);
+    V2 e = bbox_extent(conic, pt);
+    if (!(e.x >= 0.0f && e.y >= 0.0f)) return false;
+    float wf = (float)u.img_w, hf = (float)u.img_h;
+    bool on_screen = m.x + e.x > 0.0f && m.x - e.x < wf && m.y + e.y > 0.0f && m.y - e.y < hf;
+    if (!on_screen) return false;
+    TileBox bb = tile_bbox(m, e, u.tile_bw, u.tile_bh);
+    uint32_t hits = 0;
+    for (uint32_t ty = bb.min_y; ty < bb.max_y; ty++)
+        for (uint32_t tx = bb.min_x; tx < bb.max_x; tx++)
+            if (will_contribute(tx, ty, m, conic, pt)) hits++;
+    o.hits = hits;
+    o.radius = bh_maxf(e.x / wf, e.y / hf);
+    o.depth = mean_c.z;
+    return true;
+}
+
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = min(v, (uint32_t)__shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor(v, o, 64));
+    return v;
+}
+
+template <bool MIP>
+__global__ __launch_bounds__(256) void project_forward_kernel(bh_project_uniforms u,
+                                                               const float* __restrict__ transforms,
+                                                               const float* __restrict__ raw_opac, uint32_t n,
+                                                               uint32_t* __restrict__ counts,
+                                                               float* __restrict__ max_radius,
+                                                               uint32_t* __restrict__ depth_keys,
+                                                               uint32_t* __restrict__ counters) {
+    const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
+    bool vis = false;
+    ProjectOut o{0u, 0.0f, 0.0f};
+    if (gid < n) {
+        const float2* row = reinterpret_cast<const float2*>(transforms + (size_t)gid * 10);
+        float t[10];
+#pragma unroll
+        for (int i = 0; i < 5; i++) {
+            float2 p = row[i];
+            t[2 * i] = p.x;
+            t[2 * i + 1] = p.y;
+        }
+        vis = project_one<MIP>(u, t, raw_opac[gid], o);
+        counts[gid] = vis ? o.hits : 0u;
+        max_radius[gid] = vis ? o.radius : 0.0f;
+        depth_keys[gid] = vis ? bh_as_uint(o.depth) : 0xFFFFFFFFu;
+    }
+    uint64_t vmask = __ballot(vis);
+    uint64_t hits = wave_sum_u64(vis ? (uint64_t)o.hits : 0ull);
+    uint32_t kmin = wave_min_u32(vis ? bh_as_uint(o.depth) : 0xFFFFFFFFu);
+    uint32_t kmax = wave_max_u32(vis ? bh_as_uint(o.depth) : 0u);
+    if ((threadIdx.x & 63) == 0 && vmask) {
+        atomicAdd(&counters[0], (uint32_t)__popcll(vmask));
+        atomicAdd(reinterpret_cast<unsigned long long*>(counters + 2), (unsigned long long)hits);
+        atomicMin(&counters[4], kmin);
+        atomicMax(&counters[5], kmax);
+    }
+}
+
+void launch_project_forward(bh_ctx* ctx, const bh_project_uniforms& u, const float* transforms,
+                            const float* raw_opac, uint32_t n, bool mip, uint32_t* intersect_counts,
+                            float* max_radius, uint32_t* depth_keys, uint32_t* counters) {
+    if (n == 0) return;
+    KernelTimer t(ctx, "project_forward");
+    uint32_t blocks = div_up(n, 256);
+    if (mip)
+        project_forward_kernel<true><<<blocks, 256, 0, ctx->stream>>>(u, transforms, raw_opac, n, intersect_counts,
+                                                                       max_radius, depth_keys, counters);
+    else
+        project_forward_kernel<false><<<blocks, 256, 0, ctx->stream>>>(u, transforms, raw_opac, n, intersect_counts,
+                                                                        max_radius, depth_keys, counters);
+}
+
+// ---- project_visible ------------------------------------------------------------
+
+template <int NC>
+__device__ __forceinline__ void load_sh_row(const float* __restrict__ sh, uint32_t gid, float* c) {
+    const float* row = sh + (size_t)gid * (3 * NC);
+    if ((3 * NC) % 4 == 0) {
+        const float4* r4 = reinterpret_cast<const float4*>(row);
+#pragma unroll
+        for (int i = 0; i < (3 * NC) / 4; i++) {
+            float4 q = r4[i];
+            c[4 * i] = q.x;
+            c[4 * i + 1] = q.y;
+            c[4 * i + 2] = q.z;
+            c[4 * i + 3] = q.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 3 * NC; i++) c[i] = row[i];
+    }
+}
+
+template <int DEG, bool MIP>
+__global__ __launch_bounds__(256) void project_visible_kernel(bh_project_uniforms u,
+                                                               const float* __restrict__ transforms,
+                                                               const float* __restrict__ sh,
+                                                               const float* __restrict__ raw_opac,
+                                                               const uint32_t* __restrict__ gfc, uint32_t num_visible,
+                                                               uint32_t num_splats, float* __restrict__ projected,
+                                                               float* __restrict__ depths) {
+    constexpr int NC = (DEG + 1) * (DEG + 1);
+    const uint32_t c = blockIdx.x * 256u + threadIdx.x;
+    if (c >= num_visible) return;
+    const uint32_t gid = min(gfc[c], num_splats - 1u);
+    const float2* row = reinterpret_cast<const float2*>(transforms + (size_t)gid * 10);
+    float t[10];
+#pragma unroll
+    for (int i = 0; i < 5; i++) {
+        float2 p = row[i];
+        t[2 * i] = p.x;
+        t[2 * i + 1] = p.y;
+    }
+    float coeffs[3 * NC];
+    load_sh_row<NC>(sh, gid, coeffs);
+    V3 mean = v3(t[0], t[1], t[2]);
+    V3 sc = v3(bh_expf(t[7]), bh_expf(t[8]), bh_expf(t[9]));
+    Q4 q = qnormalize(Q4{t[3], t[4], t[5], t[6]});
+    V3 mean_c = world_to_cam(u, mean);
+    S2 raw_cov = calc_cov2d(u, sc, q, mean_c);
+    float comp;
+    S2 cov = compensate_cov2d<MIP>(raw_cov, comp);
+    float opac = bh_sigmoidf(raw_opac[gid]) * comp;
+    S2 conic = inverse(cov);
+    V2 m = project_pinhole(u, mean_c);
+    V3 v = mean - v3(u.camera_pos[0], u.camera_pos[1], u.camera_pos[2]);
+    v = v * (1.0f / sqrtf(dot(v, v)));
+    V3 raw = sh_to_color<DEG>(coeffs, v);
+    float cr = raw.x + 0.5f, cg = raw.y + 0.5f, cb = raw.z + 0.5f;
+    float out[10];
+    out[0] = m.x;
+    out[1] = m.y;
+    out[2] = conic.c00;
+    out[3] = conic.c01;
+    out[4] = conic.c11;
+    out[5] = opac;
+    out[6] = bh_clampf(bh_is_finite(cr) ? cr : 0.0f, -100.0f, 100.0f);
+    out[7] = bh_clampf(bh_is_finite(cg) ? cg : 0.0f, -100.0f, 100.0f);
+    out[8] = bh_clampf(bh_is_finite(cb) ? cb : 0.0f, -100.0f, 100.0f);
+    out[9] = mean_c.z;
+    float2* dst = reinterpret_cast<float2*>(projected + (size_t)c * 10);
+#pragma unroll
+    for (int i = 0; i < 5; i++) dst[i] = make_float2(out[2 * i], out[2 * i + 1]);
+    depths[c] = mean_c.z;
+}
+
+template <int DEG>
+static void launch_pv(bh_ctx* ctx, bool mip, uint32_t blocks, const bh_project_uniforms& u, const float* transforms,
+                      const float* sh, const float* raw_opac, const uint32_t* gfc, uint32_t num_visible,
+                      float* projected, float* depths) {
+    if (mip)
+        project_visible_kernel<DEG, true><<<blocks, 256, 0, ctx->stream>>>(u, transforms, sh, raw_opac, gfc,
+                                                                           num_visible, u.total_splats, projected,
+                                                                           depths);
+    else
+        project_visible_kernel<DEG, false><<<blocks, 256, 0, ctx->stream>>>(u, transforms, sh, raw_opac, gfc,
+                                                                            num_visible, u.total_splats, projected,
+                                                                            depths);
+}
+
+void launch_project_visible(bh_ctx* ctx, const bh_project_uniforms& u, const float* transforms, const float* sh,
+                            const float* raw_opac, const uint32_t* gfc, uint32_t num_visible, uint32_t sh_degree,
+                            bool mip, float* projected, float* depths) {
+    if (num_visible == 0) return;
+    KernelTimer t(ctx, "project_visible");
+    uint32_t blocks = div_up(num_visible, 256);
+    switch (sh_degree) {
+        case 0: launch_pv<0>(ctx, mip, blocks, u, transforms, sh, raw_opac, gfc, num_visible, projected, depths); break;
+        case 1: launch_pv<1>(ctx, mip, blocks, u, transforms, sh, raw_opac, gfc, num_visible, projected, depths); break;
+        case 2: launch_pv<2>(ctx, mip, blocks, u, transforms, sh, raw_opac, gfc, num_visible, projected, depths); break;
+        case 3: launch_pv<3>(ctx, mip, blocks, u, transforms, sh, raw_opac, gfc, num_visible, projected, depths); break;
+        default: launch_pv<4>(ctx, mip, blocks, u, transforms, sh, raw_opac, gfc, num_visible, projected, depths); break;
+    }
+}
+
+// ---- map_intersects ----------------------------------------------------------------
+
+__global__ __launch_bounds__(256) void map_intersects_kernel(uint32_t tile_bw, uint32_t tile_bh,
+                                                              const float* __restrict__ projected,
+                                                              const uint32_t* __restrict__ cum, uint32_t num_visible,
+                                                              uint32_t* __restrict__ tile_ids,
+                                                              uint32_t* __restrict__ cgids) {
+    const uint32_t c = blockIdx.x * 256u + threadIdx.x;
+    if (c >= num_visible) return;
+    const float2* row = reinterpret_cast<const float2*>(projected + (size_t)c * 10);
+    float2 p0 = row[0], p1 = row[1], p2 = row[2];
+    V2 m = v2(p0.x, p0.y);
+    S2 conic{p1.x, p1.y, p2.x};
+    float opac = p2.y;
+    float pt = bh_logf(opac * 255.0f);
+    V2 e = bbox_extent(conic, pt);
+    TileBox bb = tile_bbox(m, e, tile_bw, tile_bh);
+    uint32_t base = c == 0 ? 0u : cum[c - 1];
+    uint32_t budget = cum[c] - base;
+    uint32_t hits = 0;
+    for (uint32_t ty = bb.min_y; ty < bb.max_y && hits < budget; ty++)
+        for (uint32_t tx = bb.min_x; tx < bb.max_x && hits < budget; tx++)
+            if (will_contribute(tx, ty, m, conic, pt)) {
+                tile_ids[base + hits] = tx + ty * tile_bw;
+                cgids[base + hits] = c;
+                hits++;
+            }
+    // sentinel padding of an unused budget (map_gaussians.rs:171-180)
+    for (uint32_t k = hits; k < budget; k++) {
+        tile_ids[base + k] = tile_bw * tile_bh;
+        cgids[base + k] = c;
+    }
+}
+
+void launch_map_intersects(bh_ctx* ctx, uint32_t tile_bw, uint32_t tile_bh, const float* projected,
+                           const uint32_t* cum, uint32_t num_visible, uint32_t* tile_ids, uint32_t* cgids) {
+    if (num_visible == 0) return;
+    KernelTimer t(ctx, "map_intersects");
+    map_intersects_kernel<<<div_up(num_visible, 256), 256, 0, ctx->stream>>>(tile_bw, tile_bh, projected, cum,
+                                                                               num_visible, tile_ids, cgids);
+}
+
+}  // namespace bh

@@ -1,0 +1,177 @@
+// raster.hip — tile offsets and the forward front-to-back blend for gfx950.
+//
+//   tile_offsets  [start, end) of each tile's run in the tile-sorted list
+//                 (crates/brush-render/src/get_tile_offset.rs:10-62)
+//   rasterize     one 256-thread workgroup (four wave64s) per 16x16 tile, one
+//                 pixel per lane, splat batches of 256 staged in LDS, the
+//                 whole-tile early exit decided by a workgroup vote
+//                 (crates/brush-render/src/kernels/rasterize.rs:24-200).
+//
+// With BWD_INFO the kernel also marks contributing splats visible — once per
+// (splat, tile) batch through an LDS flag instead of once per pixel — and
+// shrinks each tile's end to one past the last splat any pixel consumed.
+#include <hip/hip_runtime.h>
+
+#include "bh_internal.h"
+#include "bh_splat_math.h"
+
+namespace bh {
+
+__global__ __launch_bounds__(256) void tile_offsets_kernel(const uint32_t* __restrict__ ids, uint32_t m,
+                                                            uint32_t num_tiles, uint32_t* __restrict__ off) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= m) return;
+    const uint32_t tid = ids[i];
+    if (i == 0) {
+        if (tid < num_tiles) off[2 * tid] = 0;
+    } else {
+        const uint32_t prev = ids[i - 1];
+        if (tid != prev) {
+            if (prev < num_tiles) off[2 * prev + 1] = i;
+            if (tid < num_tiles) off[2 * tid] = i;
+        }
+    }
+    if (i == m - 1 && tid < num_tiles) off[2 * tid + 1] = i + 1;
+}
+
+void launch_tile_offsets(bh_ctx* ctx, const uint32_t* tile_ids, uint32_t m, uint32_t num_tiles,
+                         uint32_t* offsets) {
+    launch_fill_u32(ctx, offsets, 0u, (uint64_t)num_tiles * 2);
+    if (m == 0) return;
+    KernelTimer t(ctx, "tile_offsets");
+    tile_offsets_kernel<<<div_up(m, 256), 256, 0, ctx->stream>>>(tile_ids, m, num_tiles, offsets);
+}
+
+template <bool BWD_INFO, bool SMOOTH, bool DEPTH>
+__global__ __launch_bounds__(256) void rasterize_kernel(uint32_t img_w, uint32_t img_h, uint32_t tile_bw, float bg_r,
+                                                         float bg_g, float bg_b, uint32_t num_visible,
+                                                         const float* __restrict__ projected,
+                                                         const uint32_t* __restrict__ cgids,
+                                                         const uint32_t* __restrict__ gfc,
+                                                         const uint32_t* __restrict__ off_pre,
+                                                         void* __restrict__ out_img, float* __restrict__ visible,
+                                                         uint32_t* __restrict__ off_post) {
+    __shared__ float4 s_xyco[256];  // x, y, conic c00, conic c01
+    __shared__ float2 s_c11a[256];  // conic c11, opacity
+    __shared__ float4 s_rgbd[256];  // r, g, b, depth
+    __shared__ uint32_t s_gid[BWD_INFO ? 256 : 1];
+    __shared__ uint32_t s_contrib[BWD_INFO ? 256 : 1];
+    __shared__ uint32_t s_max_useful;
+
+    const uint32_t tile = blockIdx.x;
+    const uint32_t tx = tile % tile_bw, ty = tile / tile_bw;
+    const uint32_t t = threadIdx.x;
+    const uint32_t px = tx * 16u + (t & 15u), py = ty * 16u + (t >> 4);
+    const bool inside = px < img_w && py < img_h;
+    const uint32_t lo = off_pre[2 * tile], hi = off_pre[2 * tile + 1];
+    if (t == 0) s_max_useful = lo;
+    __syncthreads();
+
+    const float pcx = (float)px + 0.5f, pcy = (float)py + 0.5f;
+    float t_acc = 1.0f, pr = 0.0f, pg = 0.0f, pb = 0.0f, pd = 0.0f;
+    bool done = !inside;
+    uint32_t last = lo;
+
+    for (uint32_t batch = lo; batch < hi; batch += 256u) {
+        if (__syncthreads_count(done) == 256) break;
+        const uint32_t cnt = min(256u, hi - batch);
+        if (t < cnt) {
+            const uint32_t c = min(cgids[batch + t], num_visible - 1u);
+            const float2* row = reinterpret_cast<const float2*>(projected + (size_t)c * 10);
+            float2 a = row[0], b = row[1], cc = row[2], d = row[3], e = row[4];
+            s_xyco[t] = make_float4(a.x, a.y, b.x, b.y);
+            s_c11a[t] = make_float2(cc.x, cc.y);
+            s_rgbd[t] = make_float4(d.x, d.y, e.x, e.y);
+            if (BWD_INFO) {
+                s_gid[t] = gfc[c];
+                s_contrib[t] = 0u;
+            }
+        }
+        __syncthreads();
+        if (!done) {
+            for (uint32_t j = 0; j < cnt; j++) {
+                const float4 xc = s_xyco[j];
+                const float2 ca = s_c11a[j];
+                const S2 conic{xc.z, xc.w, ca.x};
+                const float sigma = calc_sigma(pcx, pcy, conic, xc.x, xc.y);
+                const float alpha = bh_minf(0.999f, ca.y * bh_expf(-sigma));
+                const float w = SMOOTH ? cutoff_weight(alpha) : (alpha >= kCutMid ? 1.0f : 0.0f);
+                if (sigma >= 0.0f && w > 0.0f) {
+                    const float ae = alpha * w;
+                    const float next_t = t_acc * (1.0f - ae);
+                    if (next_t <= 1.0e-4f) {
+                        done = true;
+                        break;
+                    }
+                    if (BWD_INFO) s_contrib[j] = 1u;
+                    const float vis = ae * t_acc;
+                    const float4 col = s_rgbd[j];
+                    pr += bh_maxf(col.x, 0.0f) * vis;
+                    pg += bh_maxf(col.y, 0.0f) * vis;
+                    pb += bh_maxf(col.z, 0.0f) * vis;
+                    if (DEPTH) pd += col.w * vis;
+                    t_acc = next_t;
+                    last = batch + j + 1u;
+                }
+            }
+        }
+        __syncthreads();
+        if (BWD_INFO && t < cnt && s_contrib[t]) visible[s_gid[t]] = 1.0f;
+    }
+
+    if (inside) {
+        const float fr = pr + t_acc * bg_r, fg = pg + t_acc * bg_g, fb = pb + t_acc * bg_b;
+        const float fa = 1.0f - t_acc;
+        const size_t pix = (size_t)py * img_w + px;
+        if (BWD_INFO) {
+            if (DEPTH) {
+                float* o = (float*)out_img + pix * 5;
+                o[0] = fr;
+                o[1] = fg;
+                o[2] = fb;
+                o[3] = fa;
+                o[4] = pd;
+            } else {
+                reinterpret_cast<float4*>(out_img)[pix] = make_float4(fr, fg, fb, fa);
+            }
+        } else {
+            const uint32_t ur = (uint32_t)bh_clampf(fr * 255.0f, 0.0f, 255.0f);
+            const uint32_t ug = (uint32_t)bh_clampf(fg * 255.0f, 0.0f, 255.0f);
+            const uint32_t ub = (uint32_t)bh_clampf(fb * 255.0f, 0.0f, 255.0f);
+            const uint32_t ua = (uint32_t)bh_clampf(fa * 255.0f, 0.0f, 255.0f);
+            reinterpret_cast<uint32_t*>(out_img)[pix] = ur | (ug << 8) | (ub << 16) | (ua << 24);
+        }
+    }
+    if (BWD_INFO) atomicMax(&s_max_useful, last);
+    __syncthreads();
+    if (t == 0) {
+        off_post[2 * tile] = lo;
+        off_post[2 * tile + 1] = BWD_INFO ? s_max_useful : hi;
+    }
+}
+
+void launch_rasterize(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,
+                      const float* bg, uint32_t num_visible, const float* projected, const uint32_t* cgids, const uint32_t* gfc,
+                      const uint32_t* off_pre, uint32_t flags, void* out_img, float* visible, uint32_t* off_post) {
+    const uint32_t num_tiles = tile_bw * tile_bh;
+    if (num_tiles == 0) return;
+    const bool bwd = (flags & BH_FLAG_BWD_INFO) != 0;
+    const bool smooth = (flags & BH_FLAG_SMOOTH_CUTOFF) != 0;
+    const bool depth = bwd && (flags & BH_FLAG_RENDER_DEPTH) != 0;
+    const uint32_t nv = num_visible > 0 ? num_visible : 1u;
+    KernelTimer t(ctx, "rasterize");
+#define BH_RASTER(B, S, D)                                                                                      \
+    rasterize_kernel<B, S, D><<<num_tiles, 256, 0, ctx->stream>>>(img_w, img_h, tile_bw, bg[0], bg[1], bg[2], \
+                                                                  nv, projected, cgids, gfc, off_pre, out_img, \
+                                                                  visible, off_post)
+    if (!bwd) {
+        if (smooth) BH_RASTER(false, true, false); else BH_RASTER(false, false, false);
+    } else if (depth) {
+        if (smooth) BH_RASTER(true, true, true); else BH_RASTER(true, false, true);
+    } else {
+        if (smooth) BH_RASTER(true, true, false); else BH_RASTER(true, false, false);
+    }
+#undef BH_RASTER
+}
+
+}  // namespace bh

@@ -1,0 +1,362 @@
+// sort.hip — fill, inclusive scan and stable radix sort for gfx950.
+//
+// Radix sort: LSD with 8-bit digits in the "onesweep" organisation
+// (Adinets & Merrill, 2022): one histogram pass computes the digit counts of
+// every pass up front, then each digit pass reads keys and values once and
+// writes them once.  A partition of 4096 pairs is ranked stably inside the
+// workgroup with wave64 ballots (an 8-ballot match of the digit gives each
+// lane its peers; a per-wave running count orders slots), the block's digit
+// counts are published to a look-back status array, and the pairs are written
+// from LDS in digit order so each digit's run is a contiguous write.
+//
+// Forward progress of the look-back: partition ids come from an atomic
+// counter taken when a workgroup starts, so a workgroup only ever waits on
+// partitions owned by workgroups that are already resident.  The spin is
+// bounded; on exhaustion the kernel raises an error flag that the host turns
+// into BH_ERR_INTERNAL, and the kernel still completes.
+//
+// Replaces brush-sort (crates/brush-sort/src/lib.rs:16-129, which runs five
+// kernels per 4-bit pass with a single-workgroup scan) and brush-prefix-sum
+// (crates/brush-prefix-sum/src/lib.rs:11-87, a multi-level Hillis-Steele scan).
+#include <hip/hip_runtime.h>
+
+#include "bh_internal.h"
+
+namespace bh {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kItems = 16;
+constexpr int kPart = kThreads * kItems;  // 4096
+constexpr int kRadix = 256;
+constexpr uint64_t kFlagAgg = 1ull << 62;
+constexpr uint64_t kFlagPrefix = 2ull << 62;
+constexpr uint32_t kSpinLimit = 1u << 24;
+
+__global__ void fill_u32_kernel(uint32_t* p, uint32_t value, uint64_t count) {
+    uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (; i < count; i += stride) p[i] = value;
+}
+
+void launch_fill_u32(bh_ctx* ctx, uint32_t* p, uint32_t value, uint64_t count) {
+    if (count == 0) return;
+    KernelTimer t(ctx, "fill");
+    uint32_t blocks = (uint32_t)std::min<uint64_t>((count + 255) / 256, 4096);
+    fill_u32_kernel<<<blocks, 256, 0, ctx->stream>>>(p, value, count);
+}
+
+__device__ __forceinline__ uint64_t status_load(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void status_store(uint64_t* p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Sum of the values published by partitions [0, part) for one status column.
+// Walks backwards accumulating aggregates until an inclusive prefix is found.
+__device__ uint32_t look_back(const uint64_t* status, uint32_t part, uint32_t stride, uint32_t col,
+                              uint32_t* err) {
+    uint32_t excl = 0;
+    int64_t p = (int64_t)part - 1;
+    uint32_t spins = 0;
+    while (p >= 0) {
+        uint64_t s = status_load(status + (uint64_t)p * stride + col);
+        uint64_t flag = s & (3ull << 62);
+        if (flag == 0) {
+            if (++spins >= kSpinLimit) {
+                atomicOr(err, kErrSpin);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+            continue;
+        }
+        excl += (uint32_t)s;
+        if (flag == kFlagPrefix) break;
+        p--;
+    }
+    return excl;
+}
+
+// Exclusive scan of one value per thread over a 256-thread block.
+__device__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* s_wave_tot, uint32_t* total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint32_t x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        uint32_t y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
+    }
+    if (lane == 63) s_wave_tot[wave] = x;
+    __syncthreads();
+    uint32_t off = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) {
+        uint32_t t = s_wave_tot[w];
+        if (w < wave) off += t;
+        tot += t;
+    }
+    __syncthreads();
+    *total = tot;
+    return off + x - v;
+}
+
+// ---- histogram of all digit passes -------------------------------------------
+
+__global__ __launch_bounds__(kThreads) void radix_hist_kernel(const uint32_t* __restrict__ keys, uint32_t n,
+                                                               uint32_t passes, uint32_t key_sub, uint32_t key_cap,
+                                                               uint32_t* __restrict__ hist) {
+    __shared__ uint32_t sh[4 * kRadix];
+    for (int i = threadIdx.x; i < 4 * kRadix; i += kThreads) sh[i] = 0;
+    __syncthreads();
+    for (uint32_t idx = blockIdx.x * kThreads + threadIdx.x; idx < n; idx += gridDim.x * kThreads) {
+        uint32_t k = min(keys[idx] - key_sub, key_cap);
+        for (uint32_t p = 0; p < passes; p++) atomicAdd(&sh[p * kRadix + ((k >> (8 * p)) & 255u)], 1u);
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < passes * kRadix; i += kThreads)
+        if (sh[i]) atomicAdd(&hist[i], sh[i]);
+}
+
+// ---- one digit pass ------------------------------------------------------------
+
+template <bool FIRST>
+__global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __restrict__ keys_in,
+                                                             const uint32_t* __restrict__ vals_in,
+                                                             uint32_t* __restrict__ keys_out,
+                                                             uint32_t* __restrict__ vals_out, uint32_t n,
+                                                             uint32_t shift, uint32_t key_sub, uint32_t key_cap,
+                                                             const uint32_t* __restrict__ hist, uint64_t* status,
+                                                             uint32_t* part_counter, uint32_t* err) {
+    __shared__ uint32_t s_wave_hist[kWaves][kRadix];
+    __shared__ uint32_t s_local_start[kRadix];
+    __shared__ uint32_t s_global_off[kRadix];
+    __shared__ uint32_t s_keys[kPart];
+    __shared__ uint32_t s_vals[kPart];
+    __shared__ uint32_t s_tot[kWaves];
+    __shared__ uint32_t s_part;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid == 0) s_part = atomicAdd(part_counter, 1u);
+    for (int i = tid; i < kWaves * kRadix; i += kThreads) (&s_wave_hist[0][0])[i] = 0;
+    __syncthreads();
+    const uint32_t part = s_part;
+    const uint64_t base = (uint64_t)part * kPart;
+    const uint64_t wave_base = base + (uint64_t)wave * (64 * kItems);
+
+    uint32_t k[kItems], v[kItems], rank[kItems];
+#pragma unroll
+    for (int j = 0; j < kItems; j++) {
+        uint64_t idx = wave_base + (uint64_t)j * 64 + lane;
+        bool valid = idx < n;
+        uint32_t kk = valid ? keys_in[idx] : 0u;
+        if (FIRST) kk = min(kk - key_sub, key_cap);
+        k[j] = kk;
+        v[j] = valid ? (vals_in ? vals_in[idx] : (uint32_t)idx) : 0u;
+    }
+    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+#pragma unroll
+    for (int j = 0; j < kItems; j++) {
+        uint64_t idx = wave_base + (uint64_t)j * 64 + lane;
+        bool valid = idx < n;
+        uint32_t d = (k[j] >> shift) & 255u;
+        uint64_t peers = __ballot(valid);
+#pragma unroll
+        for (int b = 0; b < 8; b++) {
+            bool bit = (d >> b) & 1u;
+            uint64_t bal = __ballot(bit);
+            peers &= bit ? bal : ~bal;
+        }
+        uint32_t prefix = 0;
+        if (valid) prefix = s_wave_hist[wave][d];
+        rank[j] = prefix + (uint32_t)__popcll(peers & lt_mask);
+        // the highest lane of each peer group advances the wave's running count
+        if (valid && (peers >> lane) == 1ull) s_wave_hist[wave][d] = prefix + (uint32_t)__popcll(peers);
+    }
+    __syncthreads();
+
+    // per-digit counts of the partition and each wave's offset inside them
+    const uint32_t d = tid;
+    uint32_t c[kWaves];
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) c[w] = s_wave_hist[w][d];
+    uint32_t total = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) {
+        s_wave_hist[w][d] = total;
+        total += c[w];
+    }
+    uint64_t* my_status = status + (uint64_t)part * kRadix + d;
+    uint32_t excl = 0;
+    if (part == 0) {
+        status_store(my_status, kFlagPrefix | total);
+    } else {
+        status_store(my_status, kFlagAgg | total);
+        excl = look_back(status, part, kRadix, d, err);
+        status_store(my_status, kFlagPrefix | (uint64_t)(excl + total));
+    }
+    uint32_t tot_dummy;
+    uint32_t bin_base = block_exclusive_scan(hist[d], s_tot, &tot_dummy);
+    uint32_t local_start = block_exclusive_scan(total, s_tot, &tot_dummy);
+    s_local_start[d] = local_start;
+    s_global_off[d] = bin_base + excl;
+    __syncthreads();
+
+#pragma unroll
+    for (int j = 0; j < kItems; j++) {
+        uint64_t idx = wave_base + (uint64_t)j * 64 + lane;
+        if (idx < n) {
+            uint32_t dd = (k[j] >> shift) & 255u;
+            uint32_t pos = s_local_start[dd] + s_wave_hist[wave][dd] + rank[j];
+            s_keys[pos] = k[j];
+            s_vals[pos] = v[j];
+        }
+    }
+    __syncthreads();
+    const uint32_t count = (uint32_t)min<uint64_t>((uint64_t)kPart, (uint64_t)n - base);
+    for (uint32_t i = tid; i < count; i += kThreads) {
+        uint32_t key = s_keys[i];
+        uint32_t dd = (key >> shift) & 255u;
+        uint32_t g = s_global_off[dd] + (i - s_local_start[dd]);
+        if (g < n) {  // always true unless a look-back gave up (reported through err)
+            keys_out[g] = key;
+            vals_out[g] = s_vals[i];
+        }
+    }
+}
+
+// scratch layout: hist[passes*256] | counters[passes] (padded to 8 words) | status[passes][parts][256] (u64)
+size_t radix_sort_scratch_bytes(uint32_t n, uint32_t passes) {
+    uint64_t parts = div_up(n, kPart);
+    return (size_t)(4 * kRadix + 8) * 4 + (size_t)passes * parts * kRadix * 8;
+}
+
+bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t* vals_in, uint32_t n,
+                           uint32_t passes, uint32_t key_sub, uint32_t key_cap, uint32_t* keys_out,
+                           uint32_t* vals_out, uint32_t* tmp_keys, uint32_t* tmp_vals, void* scratch) {
+    if (n == 0) return BH_OK;
+    if (passes == 0) passes = 1;
+    if (passes > 4) return set_error(ctx, BH_ERR_INVALID_ARG, "radix sort: more than 32 key bits");
+    uint32_t parts = div_up(n, kPart);
+    uint32_t* hist = (uint32_t*)scratch;
+    uint32_t* counters = hist + 4 * kRadix;
+    uint64_t* status = (uint64_t*)(counters + 8);
+    size_t words = (size_t)(4 * kRadix + 8) + (size_t)passes * parts * kRadix * 2;
+    launch_fill_u32(ctx, hist, 0u, words);
+    {
+        KernelTimer t(ctx, "radix_hist");
+        uint32_t blocks = std::min<uint32_t>(div_up(n, kThreads * 16), 2048);
+        radix_hist_kernel<<<blocks, kThreads, 0, ctx->stream>>>(keys_in, n, passes, key_sub, key_cap, hist);
+    }
+    const uint32_t* src_k = keys_in;
+    const uint32_t* src_v = vals_in;
+    for (uint32_t p = 0; p < passes; p++) {
+        // the last pass lands in the output buffers
+        bool to_out = ((passes - 1 - p) % 2) == 0;
+        uint32_t* dk = to_out ? keys_out : tmp_keys;
+        uint32_t* dv = to_out ? vals_out : tmp_vals;
+        uint64_t* st = status + (uint64_t)p * parts * kRadix;
+        KernelTimer t(ctx, "radix_onesweep");
+        if (p == 0)
+            onesweep_kernel<true><<<parts, kThreads, 0, ctx->stream>>>(src_k, src_v, dk, dv, n, 0, key_sub, key_cap,
+                                                                        hist, st, counters + p, ctx->d_counters + 1);
+        else
+            onesweep_kernel<false><<<parts, kThreads, 0, ctx->stream>>>(
+                src_k, src_v, dk, dv, n, 8 * p, 0, 0xFFFFFFFFu, hist + p * kRadix, st, counters + p, ctx->d_counters + 1);
+        src_k = dk;
+        src_v = dv;
+    }
+    return check_launch(ctx, "radix sort");
+}
+
+__global__ void mask_u32_kernel(const uint32_t* __restrict__ in, uint32_t mask, uint32_t n,
+                                uint32_t* __restrict__ out) {
+    uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i < n) out[i] = in[i] & mask;
+}
+
+void launch_mask_u32(bh_ctx* ctx, const uint32_t* in, uint32_t mask, uint32_t n, uint32_t* out) {
+    if (n == 0) return;
+    KernelTimer t(ctx, "mask");
+    mask_u32_kernel<<<div_up(n, 256), 256, 0, ctx->stream>>>(in, mask, n, out);
+}
+
+__global__ void gather_pairs_kernel(const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
+                                    const uint32_t* __restrict__ perm, uint32_t n, uint32_t* __restrict__ keys_out,
+                                    uint32_t* __restrict__ vals_out) {
+    uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i < n) {
+        uint32_t j = perm[i];
+        keys_out[i] = keys_in[j];
+        vals_out[i] = vals_in[j];
+    }
+}
+
+void launch_gather_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t* vals_in, const uint32_t* perm,
+                         uint32_t n, uint32_t* keys_out, uint32_t* vals_out) {
+    if (n == 0) return;
+    KernelTimer t(ctx, "gather_pairs");
+    gather_pairs_kernel<<<div_up(n, 256), 256, 0, ctx->stream>>>(keys_in, vals_in, perm, n, keys_out, vals_out);
+}
+
+// ---- single-pass inclusive scan ----------------------------------------------------
+
+__global__ __launch_bounds__(kThreads) void scan_kernel(const uint32_t* __restrict__ in,
+                                                         const uint32_t* __restrict__ gather,
+                                                         uint32_t* __restrict__ out, uint32_t n, uint64_t* status,
+                                                         uint32_t* part_counter, uint32_t* err) {
+    __shared__ uint32_t s_tot[kWaves];
+    __shared__ uint32_t s_part;
+    __shared__ uint32_t s_prefix;
+    const int tid = threadIdx.x;
+    if (tid == 0) s_part = atomicAdd(part_counter, 1u);
+    __syncthreads();
+    const uint32_t part = s_part;
+    const uint64_t first = (uint64_t)part * kPart + (uint64_t)tid * kItems;
+    uint32_t x[kItems];
+    uint32_t run = 0;
+#pragma unroll
+    for (int j = 0; j < kItems; j++) {
+        uint64_t idx = first + j;
+        uint32_t val = 0;
+        if (idx < n) val = gather ? in[gather[idx]] : in[idx];
+        run += val;
+        x[j] = run;
+    }
+    uint32_t block_total;
+    uint32_t thread_excl = block_exclusive_scan(run, s_tot, &block_total);
+    if (tid == 0) {
+        uint32_t excl = 0;
+        if (part == 0) {
+            status_store(status, kFlagPrefix | block_total);
+        } else {
+            status_store(status + part, kFlagAgg | block_total);
+            excl = look_back(status, part, 1, 0, err);
+            status_store(status + part, kFlagPrefix | (uint64_t)(excl + block_total));
+        }
+        s_prefix = excl;
+    }
+    __syncthreads();
+    const uint32_t add = s_prefix + thread_excl;
+#pragma unroll
+    for (int j = 0; j < kItems; j++) {
+        uint64_t idx = first + j;
+        if (idx < n) out[idx] = x[j] + add;
+    }
+}
+
+size_t scan_scratch_bytes(uint32_t n) { return 64 + (size_t)div_up(n, kPart) * 8; }
+
+bh_status inclusive_scan(bh_ctx* ctx, const uint32_t* in, const uint32_t* gather, uint32_t* out, uint32_t n,
+                         void* scratch) {
+    if (n == 0) return BH_OK;
+    uint32_t parts = div_up(n, kPart);
+    uint32_t* counter = (uint32_t*)scratch;
+    uint64_t* status = (uint64_t*)((char*)scratch + 64);
+    launch_fill_u32(ctx, counter, 0u, 16 + (size_t)parts * 2);
+    KernelTimer t(ctx, "scan");
+    scan_kernel<<<parts, kThreads, 0, ctx->stream>>>(in, gather, out, n, status, counter, ctx->d_counters + 1);
+    return check_launch(ctx, "scan");
+}
+
+}  // namespace bh

@@ -218,6 +218,8 @@ bh_status bh_project_backward(bh_ctx* ctx, const bh_project_uniforms* u, const f
 /* ---- host/device copies (plumbing for bindings without a tensor library) */
 bh_status bh_copy_to_host(bh_ctx* ctx, void* dst_host, const void* src_device, uint64_t bytes);
 bh_status bh_copy_to_device(bh_ctx* ctx, void* dst_device, const void* src_host, uint64_t bytes);
+/* Stream-ordered device-to-device copy (does not synchronise). */
+bh_status bh_copy_device(bh_ctx* ctx, void* dst_device, const void* src_device, uint64_t bytes);
 bh_status bh_device_alloc(bh_ctx* ctx, void** out, uint64_t bytes);
 bh_status bh_device_free(bh_ctx* ctx, void* ptr);
 bh_status bh_synchronize(bh_ctx* ctx);

@@ -1,0 +1,300 @@
+"""GPU parity: every HIP kernel against the CPU restatement on identical inputs.
+
+Integer outputs (visibility, tile counts, sorted tile ids and compact ids,
+tile offsets before and after the blend) and the projected rows are compared
+bit for bit; so is the image, because the blend uses the same reproducible
+exp() as the checker.  Gradients are compared to a relative tolerance of 1e-3
+(rasterize backward sums per-tile partials with float atomics, whose order
+varies); project backward fed the same v_combined is compared bit for bit.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.helpers import (assert_bits_equal, compare_forward, gpu_forward, gsplat_case, random_scene,
+                           raster_oracle_scene, rel_close, uniforms_for)
+from brush_amd.synthetic import CONFIGS, generate_splats, generate_v_output
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(gpu):
+    return gpu
+
+
+# ---- primitives ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n,bits", [(1, 32), (255, 8), (4096, 13), (4097, 32), (65537, 4), (100000, 0),
+                                    (300001, 17), (1 << 20, 32)])
+def test_radix_argsort_matches_stable_sort(gpu, n, bits):
+    import torch
+    from brush_amd import _lib
+
+    print(f"[case] radix_argsort n={n} bits={bits}", flush=True)
+    rng = np.random.default_rng(n * 7 + bits)
+    keys = rng.integers(0, 2**32, size=n, dtype=np.uint64).astype(np.uint32)
+    if bits and bits < 32:
+        keys[: n // 2] &= np.uint32((1 << bits) - 1)  # many keys inside the width, some with high bits
+    vals = np.arange(n, dtype=np.uint32)
+    ctx = _lib.context()
+    tk = torch.from_numpy(keys.view(np.int32)).to(gpu)
+    tv = torch.from_numpy(vals.view(np.int32)).to(gpu)
+    ok = torch.empty_like(tk)
+    ov = torch.empty_like(tv)
+    ctx.check(_lib.lib().bh_radix_argsort(ctx.handle, _lib.ptr(tk), _lib.ptr(tv), n, bits, _lib.ptr(ok),
+                                          _lib.ptr(ov)))
+    # brush-sort orders by the low 4*ceil(bits/4) bits
+    width = 4 * ((bits + 3) // 4)
+    ek, ev = O.stable_sort(keys, vals, width)
+    assert_bits_equal("keys", ok.cpu().numpy().view(np.uint32), ek)
+    assert_bits_equal("vals", ov.cpu().numpy().view(np.uint32), ev)
+
+
+@pytest.mark.parametrize("n", [4, 255, 256, 257, 1024, 4095, 4096, 4097, 41000, 1 << 20, 3_000_001])
+def test_prefix_sum_closed_form(gpu, n):
+    import torch
+    from brush_amd import _lib
+
+    print(f"[case] prefix_sum n={n}", flush=True)
+    rng = np.random.default_rng(n)
+    x = rng.integers(0, 64, size=n).astype(np.uint32)
+    ctx = _lib.context()
+    tx = torch.from_numpy(x.view(np.int32)).to(gpu)
+    out = torch.empty_like(tx)
+    ctx.check(_lib.lib().bh_prefix_sum(ctx.handle, _lib.ptr(tx), _lib.ptr(out), n))
+    assert_bits_equal("scan", out.cpu().numpy().view(np.uint32), np.cumsum(x, dtype=np.uint64).astype(np.uint32))
+
+
+def test_tile_offsets_run_length_fixture(gpu):
+    """get_tile_offset.rs:88-129: runs [31,1,223,1,1791,1,17,0] + 13 sentinel rows."""
+    import torch
+    from brush_amd import _lib
+
+    runs = [31, 1, 223, 1, 1791, 1, 17, 0]
+    ids, expected = [], np.zeros(16, np.uint32)
+    for t, r in enumerate(runs):
+        if r == 0:
+            continue
+        expected[2 * t] = len(ids)
+        ids += [t] * r
+        expected[2 * t + 1] = len(ids)
+    ids += [8] * 13
+    ids = np.array(ids, np.uint32)
+    ctx = _lib.context()
+    ti = torch.from_numpy(ids.view(np.int32)).to(gpu)
+    off = torch.full((16,), -1, dtype=torch.int32, device=gpu)
+    ctx.check(_lib.lib().bh_get_tile_offsets(ctx.handle, _lib.ptr(ti), ids.size, 8, _lib.ptr(off)))
+    assert_bits_equal("offsets", off.cpu().numpy().view(np.uint32), expected)
+
+
+# ---- forward ----------------------------------------------------------------------------------
+
+def test_gsplat_goldens_forward(gpu):
+    for name in ["tiny_case", "basic_case"]:
+        print(f"[case] gsplat {name}", flush=True)
+        cam, (w, h), tr, sh, opac, ref = gsplat_case(name)
+        u = uniforms_for(cam, w, h, tr.shape[0], 3)
+        g = gpu_forward(u, tr, sh, opac, O.FLAG_BWD_INFO)
+        o = O.render_forward(u, tr, sh, opac, O.FLAG_BWD_INFO)
+        compare_forward(g, o)
+        err = np.abs(g["out_img"] - ref)
+        assert np.all(err < 1e-5 + 1e-2 * np.abs(ref)), f"{name} vs gsplat: max err {err.max()}"
+
+
+@pytest.mark.parametrize("size", [(23, 19), (15, 7), (16, 8), (17, 9), (9, 17)])
+@pytest.mark.parametrize("flags", [1, 3])
+def test_raster_oracle_scene(gpu, size, flags):
+    """raster_oracle.rs:271-397 scenes and sizes, hard and smooth cutoff."""
+    print(f"[case] raster_oracle size={size} flags={flags}", flush=True)
+    cam, tr, sh, opac, bg = raster_oracle_scene()
+    w, h = size
+    u = uniforms_for(cam, w, h, 6, 0)
+    g = gpu_forward(u, tr, sh, opac, flags, bg)
+    o = O.render_forward(u, tr, sh, opac, flags, bg)
+    compare_forward(g, o)
+    ref = O.rasterize_reference(o.projected[: o.num_visible], w, h, bg, bool(flags & 2))
+    assert np.max(np.abs(g["out_img"] - ref)) <= 2e-5
+
+
+@pytest.mark.parametrize("seed,n,deg,flags", [(1, 1000, 0, 1), (2, 5000, 3, 1), (3, 3000, 1, 9), (4, 2000, 2, 5),
+                                              (5, 4000, 4, 1), (6, 2500, 3, 0), (7, 20000, 3, 3)])
+def test_random_scene_forward(gpu, seed, n, deg, flags):
+    print(f"[case] random forward seed={seed} n={n} deg={deg} flags={flags}", flush=True)
+    tr, sh, opac = random_scene(1000 + seed, n, deg, log_scale=(-3.0, 0.6))
+    from brush_amd.camera import Camera
+
+    cam = Camera.from_focal((0.1, -0.2, -3.0), (0.0, 0.0, 0.0, 1.0), 70.0, 97, 75)
+    u = uniforms_for(cam, 97, 75, n, deg)
+    g = gpu_forward(u, tr, sh, opac, flags, (0.1, 0.2, 0.3))
+    o = O.render_forward(u, tr, sh, opac, flags, (0.1, 0.2, 0.3))
+    compare_forward(g, o)
+
+
+def test_config0_forward_full_size(gpu):
+    """BASELINE config 0 (100k splats, SH0, 256x256) bit for bit."""
+    w = CONFIGS[0]
+    print(f"[case] config0 forward {w.name}", flush=True)
+    tr, sh, opac = generate_splats(w)
+    u = uniforms_for(w.camera(), w.img_w, w.img_h, w.n, w.sh_degree)
+    g = gpu_forward(u, tr, sh, opac, O.FLAG_BWD_INFO)
+    o = O.render_forward(u, tr, sh, opac, O.FLAG_BWD_INFO)
+    compare_forward(g, o)
+
+
+def test_empty_and_culled_scenes(gpu):
+    """render.rs:145-253 empty contract; fuzz.rs:330-448 all-bad geometry."""
+    from brush_amd.camera import Camera
+
+    cam = Camera((0.0, 0.0, -3.0), (0.0, 0.0, 0.0, 1.0), 0.5, 0.5)
+    u = uniforms_for(cam, 64, 64, 0, 0)
+    for flags in (0, 1):
+        g = gpu_forward(u, np.zeros((0, 10), np.float32), np.zeros((0, 1, 3), np.float32),
+                        np.zeros((0,), np.float32), flags, (0.25, 0.5, 0.75))
+        assert g["num_visible"] == 0 and g["num_intersections"] == 0
+        if flags:
+            assert np.all(g["out_img"][..., :3] == np.array([0.25, 0.5, 0.75], np.float32))
+            assert np.all(g["out_img"][..., 3] == 0)
+        else:
+            expect = (63) | (127 << 8) | (191 << 16)
+            assert np.all(g["out_img"] == expect)
+        assert np.all(g["tile_offsets"] == 0)
+    n = 16
+    base_tr = np.tile(np.array([0, 0, 3, 1, 0, 0, 0, 0, 0, 0], np.float32), (n, 1))
+    cases = {
+        "nan_positions": lambda t: t.__setitem__((slice(None), slice(0, 3)), np.nan),
+        "inf_positions": lambda t: t.__setitem__((slice(None), 0), np.inf),
+        "zero_quats": lambda t: t.__setitem__((slice(None), slice(3, 7)), 0.0),
+        "nan_quats": lambda t: t.__setitem__((slice(None), 4), np.nan),
+        "nan_scales": lambda t: t.__setitem__((slice(None), 8), np.nan),
+        "inf_scales": lambda t: t.__setitem__((slice(None), slice(7, 10)), 120.0),
+        "behind_camera": lambda t: t.__setitem__((slice(None), 2), -3.5),
+    }
+    for name, poison in cases.items():
+        tr = base_tr.copy()
+        poison(tr)
+        sh = np.full((n, 1, 3), 0.5, np.float32)
+        opac = np.zeros(n, np.float32)
+        g = gpu_forward(u, tr, sh, opac, 1)
+        assert g["num_visible"] == 0 and g["num_intersections"] == 0, name
+    g = gpu_forward(u, base_tr, np.full((n, 1, 3), 0.5, np.float32), np.full(n, np.nan, np.float32), 1)
+    assert g["num_visible"] == 0
+
+
+def test_extreme_but_valid_stays_visible(gpu):
+    """fuzz.rs:450-490."""
+    from brush_amd.camera import Camera
+
+    cam = Camera((0.0, 0.0, -3.0), (0.0, 0.0, 0.0, 1.0), 0.5, 0.5)
+    n = 4
+    u = uniforms_for(cam, 64, 64, n, 0)
+    for ls in [-30.0, -10.0, 0.0, 10.0, 20.0, 30.0, 40.0]:
+        tr = np.tile(np.array([0, 0, 3, 1, 0, 0, 0, ls, ls, ls], np.float32), (n, 1))
+        g = gpu_forward(u, tr, np.full((n, 1, 3), 0.5, np.float32), np.full(n, 2.0, np.float32), 0)
+        o = O.render_forward(u, tr, np.full((n, 1, 3), 0.5, np.float32), np.full(n, 2.0, np.float32), 0)
+        assert g["num_visible"] == n, f"log_scale={ls} over-culled"
+        compare_forward(g, o)
+
+
+def test_poison_fuzz_single_slot(gpu):
+    """fuzz.rs:267-302: every (slot, poison) combination, counts match the checker."""
+    from brush_amd.camera import Camera
+
+    poisons = [np.nan, -np.nan, np.inf, -np.inf, 0.0, -0.0, 1.1754944e-38, 5.877472e-39, 1e-40, 1.1920929e-07,
+               1e38, -1e38, 3.4028235e38, -3.4028235e38, 1e20, -1e20, 1.0, -1.0, 0.01, 1e10, 1.0 / 255.0, 16.0]
+    cam = Camera((0.0, 0.0, -3.0), (0.0, 0.0, 0.0, 1.0), 0.5, 0.5)
+    n = 120
+    u = uniforms_for(cam, 48, 48, n, 0)
+    for slot in range(14):
+        for p in poisons:
+            tr = np.tile(np.array([0, 0, 3, 1, 0, 0, 0, -1, -1, -1], np.float32), (n, 1))
+            sh = np.full((n, 1, 3), 0.5, np.float32)
+            opac = np.full(n, 2.0, np.float32)
+            if slot < 10:
+                tr[0, slot] = p
+            elif slot < 13:
+                sh[0, 0, slot - 10] = p
+            else:
+                opac[0] = p
+            g = gpu_forward(u, tr, sh, opac, 0)
+            o = O.render_forward(u, tr, sh, opac, 0)
+            assert g["num_visible"] == o.num_visible, (slot, p)
+            assert g["num_intersections"] == o.num_intersections, (slot, p)
+            assert_bits_equal(f"img slot={slot} p={p}", g["out_img"], o.out_img)
+
+
+# ---- backward -----------------------------------------------------------------------------------
+
+def _gpu_backward(g, v_output, flags_bwd, bg, tr, sh, opac, mode_mip=False):
+    import torch
+    from brush_amd import render as R
+
+    out = g["out"]
+    dev = out.out_img.device
+    vo = torch.from_numpy(np.ascontiguousarray(v_output)).to(dev)
+    v_comb = R.rasterize_bwd(out.out_img, out.projected_splats, out.compact_gid_from_isect, out.aux.tile_offsets,
+                             bg, out.aux.img_size, vo, bool(flags_bwd & 2), bool(flags_bwd & 4),
+                             bool(flags_bwd & 16))
+    return v_comb
+
+
+@pytest.mark.parametrize("seed,n,deg,flags", [(11, 800, 3, 1), (12, 3000, 0, 1), (13, 2000, 3, 3),
+                                              (14, 1500, 2, 5), (15, 1200, 1, 9)])
+def test_backward_matches_checker(gpu, seed, n, deg, flags):
+    import torch
+    from brush_amd import render as R
+    from brush_amd.camera import Camera
+
+    print(f"[case] backward seed={seed} n={n} deg={deg} flags={flags}", flush=True)
+    tr, sh, opac = random_scene(2000 + seed, n, deg, log_scale=(-3.0, 0.6))
+    cam = Camera.from_focal((0.1, -0.2, -3.0), (0.0, 0.0, 0.0, 1.0), 70.0, 61, 53)
+    u = uniforms_for(cam, 61, 53, n, deg)
+    bg = (0.1, 0.2, 0.3)
+    g = gpu_forward(u, tr, sh, opac, flags, bg)
+    o = O.render_forward(u, tr, sh, opac, flags, bg)
+    compare_forward(g, o)
+    chans = 5 if flags & 4 else 4
+    rng = np.random.default_rng(seed)
+    v_out = rng.standard_normal((53, 61, chans)).astype(np.float32)
+    bflags = (flags & 6) | 16
+    vc_gpu = _gpu_backward(g, v_out, bflags, bg, tr, sh, opac).cpu().numpy()
+    vc_ref = O.rasterize_backward(o, v_out, bflags, bg)
+    rel_close("v_combined", vc_gpu[: o.num_visible], vc_ref[: o.num_visible], rtol=1e-3, atol_frac=1e-5)
+    # project backward fed the checker's v_combined: deterministic per splat, bit for bit
+    dev = gpu
+    mode = R.SplatRenderMode.Mip if flags & 8 else R.SplatRenderMode.Default
+    grads = R.project_bwd(torch.from_numpy(tr).to(dev), torch.from_numpy(sh).to(dev), torch.from_numpy(opac).to(dev),
+                          g["out"].global_from_compact_gid, g["out"].project_uniforms, mode,
+                          torch.from_numpy(vc_ref).to(dev))
+    vt, vcoef, vo, vr = O.project_backward(o, tr, sh, opac, vc_ref, mip=bool(flags & 8))
+    assert_bits_equal("v_transforms", grads.v_transforms.cpu().numpy(), vt)
+    assert_bits_equal("v_coeffs", grads.v_coeffs.cpu().numpy(), vcoef)
+    assert_bits_equal("v_raw_opac", grads.v_raw_opac.cpu().numpy(), vo)
+    assert_bits_equal("v_refine", grads.v_refine_weight.cpu().numpy(), vr)
+
+
+def test_autograd_end_to_end(gpu):
+    """render_splats_diff + loss.backward() vs the checker's full backward."""
+    import torch
+    from brush_amd import render as R
+    from brush_amd.camera import Camera
+
+    n, deg = 2000, 3
+    tr, sh, opac = random_scene(3001, n, deg, log_scale=(-3.0, 0.6))
+    cam = Camera.from_focal((0.0, 0.1, -3.0), (0.0, 0.0, 0.0, 1.0), 80.0, 64, 48)
+    t = torch.from_numpy(tr).to(gpu).requires_grad_(True)
+    s = torch.from_numpy(sh).to(gpu).requires_grad_(True)
+    op = torch.from_numpy(opac).to(gpu).requires_grad_(True)
+    splats = R.Splats(t, s, op)
+    res = R.render_splats_diff(splats, cam, (64, 48), (0.0, 0.0, 0.0))
+    rng = np.random.default_rng(5)
+    w = torch.from_numpy(rng.standard_normal((48, 64, 4)).astype(np.float32)).to(gpu)
+    loss = (res.img * w).sum()
+    loss.backward()
+    u = uniforms_for(cam, 64, 48, n, deg)
+    o = O.render_forward(u, tr, sh, opac, O.FLAG_BWD_INFO)
+    vc = O.rasterize_backward(o, w.cpu().numpy(), O.FLAG_REFINE_WEIGHT)
+    vt, vcoef, vo, vr = O.project_backward(o, tr, sh, opac, vc)
+    rel_close("v_transforms", t.grad.cpu().numpy(), vt, rtol=1e-3, atol_frac=1e-4)
+    rel_close("v_coeffs", s.grad.cpu().numpy(), vcoef, rtol=1e-3, atol_frac=1e-4)
+    rel_close("v_raw_opac", op.grad.cpu().numpy(), vo, rtol=1e-3, atol_frac=1e-4)
+    rel_close("refine", res._cfg.refine_weight.cpu().numpy(), vr, rtol=1e-3, atol_frac=1e-4)
