@@ -1,0 +1,228 @@
+"""Benchmark: forward + backward rasterization on one MI355X.
+
+One step = the differentiable render of BASELINE.json's north-star workload
+(config 1: 1M SH-degree-3 splats at 1920x1080, f = 1100, camera at distance 4)
+followed by its backward for a fixed upstream image gradient ~ N(0, 1):
+project + cull, depth sort, scan, project_visible, map, tile sort, tile
+offsets, blend, rasterize backward and project backward, all through
+libbrush_hip.so.  Inputs are resident in HBM before the timed region.
+
+Prints one JSON line (the driver's contract).  ``roofline`` reports the kernel
+with the largest share of the step, its algorithmic bytes per launch divided by
+its mean launch time (HIP events on the library's stream), against 8 TB/s.
+``cpu_baseline`` times the C restatement (oracle/liboracle.so) on the box's
+host cores over a bounded sample of the same scene.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def algorithmic_bytes(name: str, n: int, v: int, m: int, m_post: int, t: int, p: int, c: int,
+                      depth_passes: int, tile_passes: int) -> float:
+    """Compulsory HBM bytes of one launch: every input read once, every output
+    written once (counts per launch; sort passes are separate launches)."""
+    if name == "project_forward":
+        return 44.0 * n + 12.0 * n                      # transforms+opac in; count, radius, depth key out
+    if name == "project_visible":
+        return v * (4 + 40 + 12 * c + 4) + v * (40 + 4)  # gid, transforms, SH row, opac in; row, depth out
+    if name == "scan":
+        return 12.0 * v                                  # gid + gathered count in, cum out
+    if name == "map_intersects":
+        return 24.0 * v + 8.0 * v + 8.0 * m              # x,y,conic,opac + cum in; (tile, id) pairs out
+    if name == "tile_offsets":
+        return 4.0 * m + 8.0 * t
+    if name == "rasterize":
+        return 44.0 * m + 16.0 * p + 4.0 * v + 16.0 * t  # id+row per isect, image, visible, offsets
+    if name == "rasterize_backward":
+        return 44.0 * m_post + 32.0 * p + 40.0 * m_post  # id+row, image+grad image, atomics per isect
+    if name == "project_backward":
+        return (40 + 12 * c + 4 + 4) * n + 44.0 * v + (40 + 12 * c + 8) * n
+    if name == "invert_permutation":
+        return 8.0 * v
+    return 0.0
+
+
+def sort_bytes_per_launch(name: str, passes: float, n: int, m: int) -> float:
+    """Algorithmic bytes of one launch of a sort kernel: every onesweep pass reads
+    and writes (u32 key, u32 value) once; the depth sort's first pass generates
+    its values (global ids) instead of reading them; the histogram reads keys."""
+    if name == "depth_sort_hist":
+        return 4.0 * n
+    if name == "tile_sort_hist":
+        return 4.0 * m
+    if name == "depth_sort_onesweep":
+        return (16.0 * passes - 4.0) * n / max(passes, 1.0)
+    if name == "tile_sort_onesweep":
+        return 16.0 * m
+    return 0.0
+
+
+def cpu_baseline(workload, transforms, sh, opac, v_out, min_seconds: float = 10.0, max_reps: int = 20) -> dict:
+    """Times the C restatement (oracle/liboracle.so, OpenMP over splats and
+    tiles) on the same full workload, repeated until ``min_seconds`` of CPU
+    work; reports the median repetition in Mpix/s."""
+    from brush_amd.camera import project_uniforms
+    from oracle import oracle as O
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
+    threads = max(1, min(threads, os.cpu_count() or 1))
+    O.set_threads(threads)
+    w = workload
+    u = project_uniforms(w.camera(), w.img_w, w.img_h, w.n, w.sh_degree)
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < max_reps and (time.perf_counter() - t_start < min_seconds or len(times) < 2):
+        t0 = time.perf_counter()
+        fwd = O.render_forward(u, transforms, sh, opac, O.FLAG_BWD_INFO)
+        vc = O.rasterize_backward(fwd, v_out, O.FLAG_REFINE_WEIGHT)
+        O.project_backward(fwd, transforms, sh, opac, vc)
+        times.append(time.perf_counter() - t0)
+    dt = float(np.median(times))
+    px = w.img_w * w.img_h
+    return {"value": round(px / dt / 1e6, 4), "unit": "Mpix/s", "cores": threads, "kind": "port",
+            "ms_per_step": round(dt * 1000.0, 2), "reps": len(times),
+            "sample": f"the full {w.name} fwd+bwd step ({w.n} splats, {w.img_w}x{w.img_h}), median of "
+                      f"{len(times)} repetitions"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=1)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget in seconds (0 = skip)")
+    ap.add_argument("--no-timing", action="store_true", help="do not bracket kernels with HIP events")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
+              "(the rasterizer path is single-GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from brush_amd import _lib
+    from brush_amd import render as R
+    from brush_amd.synthetic import CONFIGS, generate_splats, generate_v_output
+
+    w = CONFIGS[args.config]
+    t_gen = time.perf_counter()
+    tr, sh, opac = generate_splats(w)
+    v_out = generate_v_output(w)
+    t_gen = time.perf_counter() - t_gen
+    dev = torch.device("cuda:0")
+    t = torch.from_numpy(tr).to(dev).requires_grad_(True)
+    s = torch.from_numpy(sh).to(dev).requires_grad_(True)
+    o = torch.from_numpy(opac).to(dev).requires_grad_(True)
+    vo = torch.from_numpy(v_out).to(dev)
+    splats = R.Splats(t, s, o)
+    cam = w.camera()
+    img_size = (w.img_w, w.img_h)
+    ctx = _lib.context(0)
+
+    stats = {}
+
+    def step():
+        t.grad = None
+        s.grad = None
+        o.grad = None
+        res = R.render_splats_diff(splats, cam, img_size, (0.0, 0.0, 0.0))
+        res.img.backward(vo)
+        stats["num_visible"] = res.num_visible
+        stats["num_intersections"] = res.aux.num_intersections
+        stats["out"] = res
+        return res
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    res = stats["out"]
+    m_post = int((res.aux.tile_offsets[..., 1].long() - res.aux.tile_offsets[..., 0].long()).sum().item())
+    stats.pop("out")
+    del res
+
+    ctx.reset_timings()
+    ctx.set_timing(not args.no_timing)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    timings = ctx.read_timings() if not args.no_timing else {}
+    ctx.set_timing(False)
+    ms = (t1 - t0) * 1000.0 / args.steps
+    pixels = w.img_w * w.img_h
+    mpix = pixels / (ms / 1000.0) / 1e6
+
+    n, v, m = w.n, stats["num_visible"], stats["num_intersections"]
+    tiles = ((w.img_w + 15) // 16) * ((w.img_h + 15) // 16)
+    c = w.num_coeffs
+    kernels = {}
+    for name, (launches, total) in timings.items():
+        per_step_launches = launches / args.steps
+        avg = total / max(launches, 1)
+        if name.endswith("_onesweep") or name.endswith("_hist"):
+            b = sort_bytes_per_launch(name, per_step_launches, n, m)
+        else:
+            b = algorithmic_bytes(name, n, v, m, m_post, tiles, pixels, c, 0, 0)
+        kernels[name] = {"launches_per_step": round(per_step_launches, 2), "avg_ms": round(avg, 4),
+                         "ms_per_step": round(total / args.steps, 4),
+                         "gb_s": round(b / (avg / 1000.0) / 1e9, 1) if b and avg > 0 else None}
+    dominant = max(kernels.items(), key=lambda kv: kv[1]["ms_per_step"])[0] if kernels else None
+    roofline = None
+    if dominant:
+        kd = kernels[dominant]
+        achieved = kd["gb_s"] or 0.0
+        roofline = {"bound": "hbm", "kernel": dominant, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None}
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        try:
+            cpu = cpu_baseline(w, tr, sh, opac, v_out, args.cpu_seconds)
+        except Exception as e:  # the baseline is reported, never required
+            cpu = {"error": str(e)}
+
+    line = {
+        "metric": "fwd+bwd rasterize ms & Mpix/s, 1M Gaussians SH3 @1080p; % HBM roofline",
+        "value": round(mpix, 2),
+        "unit": "Mpix/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded SplitMix64 generator, brush_amd/synthetic.py)",
+        "config": {"workload": w.name, "splats": w.n, "sh_degree": w.sh_degree, "img": [w.img_w, w.img_h],
+                   "focal": w.focal, "distance": w.distance, "num_visible": v, "num_intersections": m,
+                   "num_intersections_post_raster": m_post,
+                   "sort": "two-stage: depth sort of visible splats, then stable tile-id sort of (tile, depth-rank) "
+                           "pairs (equivalent to a 64-bit tile|depth key sort)",
+                   "parallelism": "single GPU"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "kernels": kernels,
+        "event_timing": not args.no_timing,
+        "input_gen_s": round(t_gen, 2),
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

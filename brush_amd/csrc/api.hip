@@ -406,7 +406,8 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
             BH_STRY(ws.get(&tk, num_splats));
             BH_STRY(ws.get(&tv, num_splats));
             BH_STRY(ws.get(&scr, radix_sort_scratch_bytes(num_splats, passes)));
-            BH_STRY(radix_sort_pairs(ctx, depth_keys, nullptr, num_splats, passes, kmin, cap, sk, gfc, tk, tv, scr));
+            BH_STRY(radix_sort_pairs(ctx, depth_keys, nullptr, num_splats, passes, kmin, cap, sk, gfc, tk, tv, scr,
+                                     "depth_sort"));
         }
     }
     BH_STRY(sget((void**)&cum, (size_t)num_visible * 4));
@@ -439,7 +440,7 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
         const uint32_t bits = bit_length(num_tiles);
         const uint32_t passes = std::max<uint32_t>(1u, (bits + 7u) / 8u);
         BH_STRY(ws.get(&scr, radix_sort_scratch_bytes(m, passes)));
-        BH_STRY(radix_sort_pairs(ctx, ut, uc, m, passes, 0u, 0xFFFFFFFFu, tile_ids, cgids, tk, tv, scr));
+        BH_STRY(radix_sort_pairs(ctx, ut, uc, m, passes, 0u, 0xFFFFFFFFu, tile_ids, cgids, tk, tv, scr, "tile_sort"));
     } else {
         launch_fill_u32(ctx, tile_ids, 0u, 1);
         launch_fill_u32(ctx, cgids, 0u, 1);

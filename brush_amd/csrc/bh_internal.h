@@ -88,7 +88,8 @@ size_t radix_sort_scratch_bytes(uint32_t n, uint32_t passes);
 // The transformed keys are what the sort emits.  tmp_* are n-element buffers.
 bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t* vals_in, uint32_t n,
                            uint32_t passes, uint32_t key_sub, uint32_t key_cap, uint32_t* keys_out,
-                           uint32_t* vals_out, uint32_t* tmp_keys, uint32_t* tmp_vals, void* scratch);
+                           uint32_t* vals_out, uint32_t* tmp_keys, uint32_t* tmp_vals, void* scratch,
+                           const char* tag = "radix");
 // out[i] = in[i] & mask
 void launch_mask_u32(bh_ctx* ctx, const uint32_t* in, uint32_t mask, uint32_t n, uint32_t* out);
 // keys_out[i] = keys_in[perm[i]], vals_out[i] = vals_in[perm[i]]

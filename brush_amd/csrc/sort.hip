@@ -233,7 +233,9 @@ size_t radix_sort_scratch_bytes(uint32_t n, uint32_t passes) {
 
 bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t* vals_in, uint32_t n,
                            uint32_t passes, uint32_t key_sub, uint32_t key_cap, uint32_t* keys_out,
-                           uint32_t* vals_out, uint32_t* tmp_keys, uint32_t* tmp_vals, void* scratch) {
+                           uint32_t* vals_out, uint32_t* tmp_keys, uint32_t* tmp_vals, void* scratch,
+                           const char* tag) {
+    const std::string hist_name = std::string(tag) + "_hist", pass_name = std::string(tag) + "_onesweep";
     if (n == 0) return BH_OK;
     if (passes == 0) passes = 1;
     if (passes > 4) return set_error(ctx, BH_ERR_INVALID_ARG, "radix sort: more than 32 key bits");
@@ -244,7 +246,7 @@ bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t*
     size_t words = (size_t)(4 * kRadix + 8) + (size_t)passes * parts * kRadix * 2;
     launch_fill_u32(ctx, hist, 0u, words);
     {
-        KernelTimer t(ctx, "radix_hist");
+        KernelTimer t(ctx, hist_name.c_str());
         uint32_t blocks = std::min<uint32_t>(div_up(n, kThreads * 16), 2048);
         radix_hist_kernel<<<blocks, kThreads, 0, ctx->stream>>>(keys_in, n, passes, key_sub, key_cap, hist);
     }
@@ -256,7 +258,7 @@ bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t*
         uint32_t* dk = to_out ? keys_out : tmp_keys;
         uint32_t* dv = to_out ? vals_out : tmp_vals;
         uint64_t* st = status + (uint64_t)p * parts * kRadix;
-        KernelTimer t(ctx, "radix_onesweep");
+        KernelTimer t(ctx, pass_name.c_str());
         if (p == 0)
             onesweep_kernel<true><<<parts, kThreads, 0, ctx->stream>>>(src_k, src_v, dk, dv, n, 0, key_sub, key_cap,
                                                                         hist, st, counters + p, ctx->d_counters + 1);
