@@ -374,14 +374,14 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
     uint32_t kmin = 0, kmax = 0;
     if (bwd && num_splats) launch_fill_u32(ctx, (uint32_t*)visible, 0u, num_splats);
     if (num_splats) {
-        uint32_t* depth_keys;
+        uint32_t *depth_keys, *partials;
         BH_STRY(ws.get(&depth_keys, num_splats));
-        // counters: visible, flags, isect lo, isect hi, min key, max key
-        launch_fill_u32(ctx, ctx->d_counters, 0u, 4);
-        launch_fill_u32(ctx, ctx->d_counters + 4, 0xFFFFFFFFu, 1);
-        launch_fill_u32(ctx, ctx->d_counters + 5, 0u, 1);
+        BH_STRY(ws.get((char**)&partials, project_partials_bytes(num_splats)));
+        // counters: visible, flags, isect lo, isect hi, min key, max key; the
+        // reduction kernel writes all but the flags word
+        launch_fill_u32(ctx, ctx->d_counters + 1, 0u, 1);
         launch_project_forward(ctx, u, transforms, raw_opacities, num_splats, mip, counts, max_radius, depth_keys,
-                               ctx->d_counters);
+                               partials, ctx->d_counters);
         BH_STRY(check_launch(ctx, "project_forward"));
         BH_STRY(hip_check(ctx, hipMemcpyAsync(ctx->h_counters, ctx->d_counters, 24, hipMemcpyDeviceToHost, ctx->stream),
                           "count readback"));

@@ -1,17 +1,17 @@
 // backward.hip — rasterize backward and project backward for gfx950.
 //
-// rasterize_backward: one wave64 workgroup per 16x16 tile.  Lane j owns splat j
-// of a 64-splat batch and walks the tile's 256 pixels in row-major order; at
-// step i lane j handles pixel i - j, so pixel p is visited front to back by
-// the batch's splats on consecutive steps and its transmittance / remaining
-// colour state in LDS is always up to date (the diagonal replay of
-// crates/brush-render-bwd/src/kernels/rasterize_backwards.rs:79-443, re-laid
-// out for 64-wide waves: the reference batches 32 splats to match a 32-lane
-// SIMD group).  The per-pixel upstream terms (dL/drgb, the alpha term
-// (v_a - bg . v_rgb) T_final, final alpha) are computed once per pixel into
-// LDS instead of per (splat, pixel) pair.  Each lane accumulates its splat's
-// gradient for the whole tile in registers and adds it to v_combined with one
-// hardware float atomic per lane per batch.
+// rasterize_backward: one 256-thread workgroup per 16x16 tile, one pixel per
+// lane (each wave64 owns a 16x4 strip).  Every pixel replays the tile's
+// splats front to back with the same per-pair arithmetic as the reference's
+// replay (crates/brush-render-bwd/src/kernels/rasterize_backwards.rs:79-443,
+// where instead a 32-lane workgroup owns 32 splats and walks the pixels on a
+// diagonal); the transmittance / remaining-colour state never leaves the
+// lane's registers.  Splats are staged in LDS in batches of 64.  For each
+// splat a wave that had any contributing pixel sums the 9-11 gradient lanes
+// across its 64 pixels with DPP adds (six steps to lane 63); the four strips'
+// partials are added in LDS in strip order and each (splat, tile) pair costs
+// one hardware float atomic per gradient lane.  A wave whose 64 pixels have
+// all saturated stops evaluating splats.
 //
 // project_backward: one thread per *global* id, so every dense output row is
 // written exactly once (zeros for culled splats or splats without gradient)
@@ -25,140 +25,181 @@
 
 namespace bh {
 
+// Sum of x over the wave, left in lane 63 (other lanes hold partial sums):
+// inclusive Hillis-Steele steps inside each 16-lane row, then the row
+// broadcasts, all as DPP adds.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float x) {
+    return x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xF, true));
+}
+__device__ __forceinline__ float wave_sum_lane63(float x) {
+    x = dpp_add<0x111, 0xF>(x);  // row_shr:1
+    x = dpp_add<0x112, 0xF>(x);  // row_shr:2
+    x = dpp_add<0x114, 0xF>(x);  // row_shr:4
+    x = dpp_add<0x118, 0xF>(x);  // row_shr:8
+    x = dpp_add<0x142, 0xA>(x);  // row_bcast:15 into rows 1 and 3
+    x = dpp_add<0x143, 0xC>(x);  // row_bcast:31 into rows 2 and 3
+    return x;
+}
+
+constexpr uint32_t kBwdBatch = 64;
+
 template <bool SMOOTH, bool REFINE, bool DEPTH>
-__global__ __launch_bounds__(64) void rasterize_backward_kernel(
+__global__ __launch_bounds__(256) void rasterize_backward_kernel(
     uint32_t img_w, uint32_t img_h, uint32_t tile_bw, float bg_r, float bg_g, float bg_b, uint32_t num_visible,
     const float* __restrict__ out_img, const float* __restrict__ projected, const uint32_t* __restrict__ cgids,
     const uint32_t* __restrict__ offsets, const float* __restrict__ v_output, float* __restrict__ v_combined) {
     constexpr uint32_t CH = DEPTH ? 5u : 4u;
-    __shared__ float4 s_state[256];  // remaining r, g, b; transmittance
-    __shared__ float4 s_vout[256];   // dL/dr, dL/dg, dL/db, (v_a - bg . v_rgb) * T_final
-    __shared__ float s_final_a[256];
-    __shared__ float s_state_d[DEPTH ? 256 : 1];
-    __shared__ float s_vod[DEPTH ? 256 : 1];
+    constexpr int NG = 11;
+    __shared__ float4 s_xyco[kBwdBatch];  // x, y, conic c00, c01
+    __shared__ float4 s_crgb[kBwdBatch];  // conic c11, opacity, r, g
+    __shared__ float4 s_bd[kBwdBatch];    // b, depth, sigma cutoff
+    __shared__ uint32_t s_cid[kBwdBatch];
+    __shared__ float s_grad[4][kBwdBatch][NG + 1];  // per-wave partials; [NG] flags "wave contributed"
 
     const uint32_t tile = blockIdx.x;
     const uint32_t ox = (tile % tile_bw) * 16u, oy = (tile / tile_bw) * 16u;
-    const uint32_t lane = threadIdx.x;
-    for (uint32_t p = lane; p < 256u; p += 64u) {
-        const uint32_t px = ox + (p & 15u), py = oy + (p >> 4);
-        if (px < img_w && py < img_h) {
-            const size_t pix = (size_t)py * img_w + px;
-            const float* o = out_img + pix * CH;
-            const float* vo = v_output + pix * CH;
-            const float final_a = o[3];
-            const float t_final = 1.0f - final_a;
-            s_state[p] = make_float4(o[0] - t_final * bg_r, o[1] - t_final * bg_g, o[2] - t_final * bg_b, 1.0f);
-            const float vox = vo[0], voy = vo[1], voz = vo[2], va = vo[3];
-            const float vow = (va - (bg_r * vox + bg_g * voy + bg_b * voz)) * t_final;
-            s_vout[p] = make_float4(vox, voy, voz, vow);
-            s_final_a[p] = final_a;
-            if (DEPTH) {
-                s_state_d[p] = o[4];
-                s_vod[p] = vo[4];
-            }
-        } else {
-            s_state[p] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            s_vout[p] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            s_final_a[p] = 0.0f;
-            if (DEPTH) {
-                s_state_d[p] = 0.0f;
-                s_vod[p] = 0.0f;
-            }
+    const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
+    const uint32_t px = ox + (t & 15u), py = oy + (t >> 4);
+    const bool inside = px < img_w && py < img_h;
+    const float pcx = (float)px + 0.5f, pcy = (float)py + 0.5f;
+
+    // Pixel state of the front-to-back replay (rasterize_backwards.rs:193-250):
+    // remaining colour (final minus background pre-roll) and transmittance.
+    float sx = 0.0f, sy = 0.0f, sz = 0.0f, sw = 0.0f, sd = 0.0f;
+    float vox = 0.0f, voy = 0.0f, voz = 0.0f, vow = 0.0f, vod = 0.0f, final_a = 0.0f;
+    if (inside) {
+        const size_t pix = (size_t)py * img_w + px;
+        const float* o = out_img + pix * CH;
+        const float* vo = v_output + pix * CH;
+        final_a = o[3];
+        const float t_final = 1.0f - final_a;
+        sx = o[0] - t_final * bg_r;
+        sy = o[1] - t_final * bg_g;
+        sz = o[2] - t_final * bg_b;
+        sw = 1.0f;
+        vox = vo[0];
+        voy = vo[1];
+        voz = vo[2];
+        vow = (vo[3] - (bg_r * vox + bg_g * voy + bg_b * voz)) * t_final;
+        if (DEPTH) {
+            sd = o[4];
+            vod = vo[4];
         }
     }
     const uint32_t lo = offsets[2 * tile], hi = offsets[2 * tile + 1];
     const float img_wf = (float)img_w, img_hf = (float)img_h;
-    __syncthreads();
+    const float inv_final_a = __builtin_amdgcn_rcpf(bh_maxf(final_a, 1.0e-5f));
+    bool wave_live = __ballot(sw > 1.0e-4f) != 0ull;
 
-    for (uint32_t b = lo; b < hi; b += 64u) {
-        const uint32_t idx = b + lane;
-        const bool active = idx < hi;
-        uint32_t c = 0;
-        float s[10];
-#pragma unroll
-        for (int k = 0; k < 10; k++) s[k] = 0.0f;
-        if (active) {
-            c = min(cgids[idx], num_visible - 1u);
+    for (uint32_t b = lo; b < hi; b += kBwdBatch) {
+        const uint32_t cnt = min(kBwdBatch, hi - b);
+        if (t < cnt) {
+            const uint32_t c = min(cgids[b + t], num_visible - 1u);
             const float2* row = reinterpret_cast<const float2*>(projected + (size_t)c * 10);
-#pragma unroll
-            for (int k = 0; k < 5; k++) {
-                float2 q = row[k];
-                s[2 * k] = q.x;
-                s[2 * k + 1] = q.y;
-            }
+            const float2 r0 = row[0], r1 = row[1], r2 = row[2], r3 = row[3], r4 = row[4];
+            s_xyco[t] = make_float4(r0.x, r0.y, r1.x, r1.y);
+            s_crgb[t] = make_float4(r2.x, r2.y, r3.x, r3.y);
+            s_bd[t] = make_float4(r4.x, r4.y, sigma_cutoff<SMOOTH>(r2.y), 0.0f);
+            s_cid[t] = c;
         }
-        const S2 conic{s[2], s[3], s[4]};
-        const float opac = s[5];
-        const float cr = bh_maxf(s[6], 0.0f), cgc = bh_maxf(s[7], 0.0f), cb = bh_maxf(s[8], 0.0f);
-        float g[11];
+        for (uint32_t e = t; e < 4u * kBwdBatch; e += 256u) (&s_grad[0][0][0])[e * (NG + 1) + NG] = 0.0f;
+        __syncthreads();
+        for (uint32_t j = 0; wave_live && j < cnt; j++) {
+            const float4 xc = s_xyco[j];
+            const float4 cr4 = s_crgb[j];
+            const float4 bd = s_bd[j];
+            const S2 conic{xc.z, xc.w, cr4.x};
+            const float opac = cr4.y;
+            float g[NG];
 #pragma unroll
-        for (int k = 0; k < 11; k++) g[k] = 0.0f;
-        const uint32_t cnt = min(64u, hi - b);
-        const uint32_t iters = cnt + 255u;
-        for (uint32_t i = 0; i < iters; i++) {
-            const int p = (int)i - (int)lane;
-            if (active && p >= 0 && p < 256) {
-                const float4 st = s_state[p];
-                if (st.w > 1.0e-4f) {
-                    const uint32_t px = ox + ((uint32_t)p & 15u), py = oy + ((uint32_t)p >> 4);
-                    const float pcx = (float)px + 0.5f, pcy = (float)py + 0.5f;
-                    const float dx = s[0] - pcx, dy = s[1] - pcy;
-                    const float sigma = 0.5f * (conic.c00 * dx * dx + conic.c11 * dy * dy) + conic.c01 * dx * dy;
-                    const float gaussian = bh_expf(-sigma);
-                    const float alpha = bh_minf(0.999f, opac * gaussian);
-                    const float w = SMOOTH ? cutoff_weight(alpha) : (alpha >= kCutMid ? 1.0f : 0.0f);
-                    if (sigma >= 0.0f && w > 0.0f) {
-                        const float ae = alpha * w;
-                        const float next_t = st.w * (1.0f - ae);
-                        if (next_t <= 1.0e-4f) {
-                            s_state[p].w = 0.0f;
-                        } else {
-                            const float vis = ae * st.w;
-                            const float4 vo = s_vout[p];
-                            g[5] += s[6] >= 0.0f ? vis * vo.x : 0.0f;
-                            g[6] += s[7] >= 0.0f ? vis * vo.y : 0.0f;
-                            g[7] += s[8] >= 0.0f ? vis * vo.z : 0.0f;
-                            const float ra = 1.0f / (1.0f - ae);
-                            const float dot_rgb =
-                                ((st.w * cr - st.x) * vo.x + (st.w * cgc - st.y) * vo.y + (st.w * cb - st.z) * vo.z) * ra;
-                            const float nrx = st.x - vis * cr, nry = st.y - vis * cgc, nrz = st.z - vis * cb;
-                            if (DEPTH) {
-                                g[10] += vis * s_vod[p];
-                                s_state_d[p] = s_state_d[p] - vis * s[9];
-                            }
-                            const float v_ae = dot_rgb + vo.w * ra;
-                            const float dw = SMOOTH ? cutoff_weight_deriv(alpha) : 0.0f * alpha;
-                            const float v_alpha = v_ae * (w + alpha * dw);
-                            const float v_sigma = -alpha * v_alpha;
-                            const float vxy_x = v_sigma * (conic.c00 * dx + conic.c01 * dy);
-                            const float vxy_y = v_sigma * (conic.c01 * dx + conic.c11 * dy);
-                            if (opac * gaussian <= 0.999f) {
-                                g[2] += 0.5f * v_sigma * dx * dx;
-                                g[3] += v_sigma * dx * dy;
-                                g[4] += 0.5f * v_sigma * dy * dy;
-                                g[0] += vxy_x;
-                                g[1] += vxy_y;
-                                g[8] += v_alpha * gaussian;
-                                if (REFINE) {
-                                    const float len = sqrtf(vxy_x * img_wf * vxy_x * img_wf + vxy_y * img_hf * vxy_y * img_hf);
-                                    g[9] += len / bh_maxf(s_final_a[p], 1.0e-5f);
-                                }
-                            }
-                            s_state[p] = make_float4(nrx, nry, nrz, next_t);
+            for (int k = 0; k < NG; k++) g[k] = 0.0f;
+            bool contrib = false;
+            const float dx = xc.x - pcx, dy = xc.y - pcy;
+            const float sigma = 0.5f * (conic.c00 * dx * dx + conic.c11 * dy * dy) + conic.c01 * dx * dy;
+            if (sw > 1.0e-4f && sigma >= 0.0f && !(sigma > bd.z)) {
+                const float gaussian = bh_expf(-sigma);
+                const float alpha = bh_minf(0.999f, opac * gaussian);
+                const float w = SMOOTH ? cutoff_weight(alpha) : (alpha >= kCutMid ? 1.0f : 0.0f);
+                if (sigma >= 0.0f && w > 0.0f) {
+                    const float ae = alpha * w;
+                    const float next_t = sw * (1.0f - ae);
+                    if (next_t <= 1.0e-4f) {
+                        sw = 0.0f;
+                    } else {
+                        contrib = true;
+                        const float cr = bh_maxf(cr4.z, 0.0f), cgc = bh_maxf(cr4.w, 0.0f), cb = bh_maxf(bd.x, 0.0f);
+                        const float vis = ae * sw;
+                        g[5] = cr4.z >= 0.0f ? vis * vox : 0.0f;
+                        g[6] = cr4.w >= 0.0f ? vis * voy : 0.0f;
+                        g[7] = bd.x >= 0.0f ? vis * voz : 0.0f;
+                        // gradient-only quantities: hardware reciprocal / sqrt (1 ulp)
+                        const float ra = __builtin_amdgcn_rcpf(1.0f - ae);
+                        const float dot_rgb = ((sw * cr - sx) * vox + (sw * cgc - sy) * voy + (sw * cb - sz) * voz) * ra;
+                        const float nrx = sx - vis * cr, nry = sy - vis * cgc, nrz = sz - vis * cb;
+                        if (DEPTH) {
+                            g[10] = vis * vod;
+                            sd = sd - vis * bd.y;
                         }
+                        const float v_ae = dot_rgb + vow * ra;
+                        const float dw = SMOOTH ? cutoff_weight_deriv(alpha) : 0.0f * alpha;
+                        const float v_alpha = v_ae * (w + alpha * dw);
+                        const float v_sigma = -alpha * v_alpha;
+                        const float vxy_x = v_sigma * (conic.c00 * dx + conic.c01 * dy);
+                        const float vxy_y = v_sigma * (conic.c01 * dx + conic.c11 * dy);
+                        if (opac * gaussian <= 0.999f) {
+                            g[2] = 0.5f * v_sigma * dx * dx;
+                            g[3] = v_sigma * dx * dy;
+                            g[4] = 0.5f * v_sigma * dy * dy;
+                            g[0] = vxy_x;
+                            g[1] = vxy_y;
+                            g[8] = v_alpha * gaussian;
+                            if (REFINE) {
+                                const float len = __builtin_amdgcn_sqrtf(vxy_x * img_wf * vxy_x * img_wf +
+                                                                         vxy_y * img_hf * vxy_y * img_hf);
+                                g[9] = len * inv_final_a;
+                            }
+                        }
+                        sx = nrx;
+                        sy = nry;
+                        sz = nrz;
+                        sw = next_t;
                     }
                 }
             }
-            __syncthreads();
-        }
-        if (active) {
-            float* out = v_combined + (size_t)c * 11;
+            if (__ballot(contrib) != 0ull) {
 #pragma unroll
-            for (int k = 0; k < 9; k++) unsafeAtomicAdd(out + k, g[k]);
-            if (REFINE) unsafeAtomicAdd(out + 9, g[9]);
-            if (DEPTH) unsafeAtomicAdd(out + 10, g[10]);
+                for (int k = 0; k < NG; k++) {
+                    if ((k == 9 && !REFINE) || (k == 10 && !DEPTH)) continue;
+                    g[k] = wave_sum_lane63(g[k]);
+                }
+                if (lane == 63u) {
+#pragma unroll
+                    for (int k = 0; k < NG; k++) s_grad[wave][j][k] = g[k];
+                    s_grad[wave][j][NG] = 1.0f;
+                }
+            }
+            wave_live = __ballot(sw > 1.0e-4f) != 0ull;
         }
+        __syncthreads();
+        // per splat: the four strips' partials, added in strip order
+        for (uint32_t e = t; e < (uint32_t)NG * kBwdBatch; e += 256u) {
+            const uint32_t k = e / kBwdBatch, j = e % kBwdBatch;
+            const bool used = k < 9u || (REFINE && k == 9u) || (DEPTH && k == 10u);
+            if (used && j < cnt) {
+                float sum = 0.0f;
+                bool any = false;
+#pragma unroll
+                for (int w = 0; w < 4; w++) {
+                    if (s_grad[w][j][NG] != 0.0f) {
+                        sum = any ? sum + s_grad[w][j][k] : s_grad[w][j][k];
+                        any = true;
+                    }
+                }
+                if (any) unsafeAtomicAdd(v_combined + (size_t)s_cid[j] * NG + k, sum);
+            }
+        }
+        __syncthreads();
     }
 }
 
@@ -172,7 +213,7 @@ void launch_rasterize_backward(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint
     const bool depth = (flags & BH_FLAG_RENDER_DEPTH) != 0;
     KernelTimer t(ctx, "rasterize_backward");
 #define BH_RB(S, R, D)                                                                                          \
-    rasterize_backward_kernel<S, R, D><<<num_tiles, 64, 0, ctx->stream>>>(img_w, img_h, tile_bw, bg[0], bg[1], \
+    rasterize_backward_kernel<S, R, D><<<num_tiles, 256, 0, ctx->stream>>>(img_w, img_h, tile_bw, bg[0], bg[1], \
                                                                           bg[2], num_visible, out_img,          \
                                                                           projected, cgids, offsets, v_output,  \
                                                                           v_combined)

@@ -239,10 +239,11 @@ BH_DEV bool will_contribute(uint32_t tx, uint32_t ty, V2 m, const S2& c, float p
         float dyf = y_above ? height : -height;
         float diff_x = m.x - corner_x;
         float diff_y = m.y - corner_y;
-        float tx_raw = (dxf * c.c00 * diff_x + dxf * c.c01 * diff_y) / (dxf * c.c00 * dxf);
-        float ty_raw = (dyf * c.c01 * diff_x + dyf * c.c11 * diff_y) / (dyf * c.c11 * dyf);
-        float tt_x = in_y ? 0.0f : bh_clampf(tx_raw, 0.0f, 1.0f);
-        float tt_y = in_x ? 0.0f : bh_clampf(ty_raw, 0.0f, 1.0f);
+        // each quotient only matters off its own row/column: skip the
+        // division where the reference's select discards it
+        float tt_x = 0.0f, tt_y = 0.0f;
+        if (!in_y) tt_x = bh_clampf((dxf * c.c00 * diff_x + dxf * c.c01 * diff_y) / (dxf * c.c00 * dxf), 0.0f, 1.0f);
+        if (!in_x) tt_y = bh_clampf((dyf * c.c01 * diff_x + dyf * c.c11 * diff_y) / (dyf * c.c11 * dyf), 0.0f, 1.0f);
         float px = corner_x + tt_x * dxf;
         float py = corner_y + tt_y * dyf;
         hit = calc_sigma(px, py, c, m.x, m.y) <= pt;
@@ -263,6 +264,19 @@ BH_DEV float cutoff_weight_deriv(float alpha) {
     bool inside = alpha > low && alpha < high;
     float t = (alpha - low) / kCutBand;
     return inside ? (6.0f * t - 6.0f * t * t) / kCutBand : 0.0f;
+}
+
+// Largest sigma at which a splat of opacity `opac` can still pass the alpha
+// cutoff, plus a margin.  For sigma above it, opac * exp(-sigma) rounds below
+// the cutoff (1/255, or the lower edge of the smooth band) with certainty:
+// exp and log are within 2 ulp and the margin of 1e-3 exceeds their combined
+// relative error by three orders of magnitude.  Callers use it to skip the
+// exp of pairs that cannot contribute; every pair that can is evaluated
+// exactly as before.
+template <bool SMOOTH>
+BH_DEV float sigma_cutoff(float opac) {
+    const float alpha_min = SMOOTH ? (kCutMid - 0.5f * kCutBand) : kCutMid;
+    return bh_logf(opac / alpha_min) + 1.0e-3f;
 }
 
 // ---- spherical harmonics (kernels/sh.rs) --------------------------------------

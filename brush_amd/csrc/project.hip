@@ -87,7 +87,9 @@ __global__ __launch_bounds__(256) void project_forward_kernel(bh_project_uniform
                                                                uint32_t* __restrict__ counts,
                                                                float* __restrict__ max_radius,
                                                                uint32_t* __restrict__ depth_keys,
-                                                               uint32_t* __restrict__ counters) {
+                                                               uint32_t* __restrict__ partials) {
+    __shared__ uint32_t s_vis[4], s_kmin[4], s_kmax[4];
+    __shared__ unsigned long long s_hits[4];
     const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
     bool vis = false;
     ProjectOut o{0u, 0.0f, 0.0f};
@@ -105,30 +107,99 @@ __global__ __launch_bounds__(256) void project_forward_kernel(bh_project_uniform
         max_radius[gid] = vis ? o.radius : 0.0f;
         depth_keys[gid] = vis ? bh_as_uint(o.depth) : 0xFFFFFFFFu;
     }
+    // per-block totals (no same-address atomics): wave shuffles, then LDS
+    const uint32_t wave = threadIdx.x >> 6;
     uint64_t vmask = __ballot(vis);
     uint64_t hits = wave_sum_u64(vis ? (uint64_t)o.hits : 0ull);
     uint32_t kmin = wave_min_u32(vis ? bh_as_uint(o.depth) : 0xFFFFFFFFu);
     uint32_t kmax = wave_max_u32(vis ? bh_as_uint(o.depth) : 0u);
-    if ((threadIdx.x & 63) == 0 && vmask) {
-        atomicAdd(&counters[0], (uint32_t)__popcll(vmask));
-        atomicAdd(reinterpret_cast<unsigned long long*>(counters + 2), (unsigned long long)hits);
-        atomicMin(&counters[4], kmin);
-        atomicMax(&counters[5], kmax);
+    if ((threadIdx.x & 63) == 0) {
+        s_vis[wave] = (uint32_t)__popcll(vmask);
+        s_hits[wave] = hits;
+        s_kmin[wave] = kmin;
+        s_kmax[wave] = kmax;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t v = 0, mn = 0xFFFFFFFFu, mx = 0u;
+        unsigned long long h = 0;
+        for (int w = 0; w < 4; w++) {
+            v += s_vis[w];
+            h += s_hits[w];
+            mn = min(mn, s_kmin[w]);
+            mx = max(mx, s_kmax[w]);
+        }
+        uint32_t* out = partials + (size_t)blockIdx.x * 8;
+        out[0] = v;
+        out[1] = (uint32_t)h;
+        out[2] = (uint32_t)(h >> 32);
+        out[3] = mn;
+        out[4] = mx;
     }
 }
 
+// Folds the per-block totals of project_forward into the context counters
+// ([0] visible, [2..3] intersections, [4] min depth key, [5] max depth key).
+__global__ __launch_bounds__(1024) void project_reduce_kernel(const uint32_t* __restrict__ partials,
+                                                              uint32_t num_blocks, uint32_t* __restrict__ counters) {
+    __shared__ uint32_t s_v[16], s_mn[16], s_mx[16];
+    __shared__ unsigned long long s_h[16];
+    uint32_t v = 0, mn = 0xFFFFFFFFu, mx = 0u;
+    unsigned long long h = 0;
+    for (uint32_t i = threadIdx.x; i < num_blocks; i += 1024u) {
+        const uint32_t* p = partials + (size_t)i * 8;
+        v += p[0];
+        h += (unsigned long long)p[1] | ((unsigned long long)p[2] << 32);
+        mn = min(mn, p[3]);
+        mx = max(mx, p[4]);
+    }
+    v = (uint32_t)wave_sum_u64(v);
+    h = wave_sum_u64(h);
+    mn = wave_min_u32(mn);
+    mx = wave_max_u32(mx);
+    const uint32_t wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        s_v[wave] = v;
+        s_h[wave] = h;
+        s_mn[wave] = mn;
+        s_mx[wave] = mx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 16; w++) {
+            v += s_v[w];
+            h += s_h[w];
+            mn = min(mn, s_mn[w]);
+            mx = max(mx, s_mx[w]);
+        }
+        counters[0] = v;
+        counters[2] = (uint32_t)h;
+        counters[3] = (uint32_t)(h >> 32);
+        counters[4] = mn;
+        counters[5] = mx;
+    }
+}
+
+size_t project_partials_bytes(uint32_t n) { return (size_t)div_up(n, 256) * 8 * sizeof(uint32_t); }
+
 void launch_project_forward(bh_ctx* ctx, const bh_project_uniforms& u, const float* transforms,
                             const float* raw_opac, uint32_t n, bool mip, uint32_t* intersect_counts,
-                            float* max_radius, uint32_t* depth_keys, uint32_t* counters) {
+                            float* max_radius, uint32_t* depth_keys, uint32_t* partials, uint32_t* counters) {
     if (n == 0) return;
-    KernelTimer t(ctx, "project_forward");
     uint32_t blocks = div_up(n, 256);
-    if (mip)
-        project_forward_kernel<true><<<blocks, 256, 0, ctx->stream>>>(u, transforms, raw_opac, n, intersect_counts,
-                                                                       max_radius, depth_keys, counters);
-    else
-        project_forward_kernel<false><<<blocks, 256, 0, ctx->stream>>>(u, transforms, raw_opac, n, intersect_counts,
-                                                                        max_radius, depth_keys, counters);
+    {
+        KernelTimer t(ctx, "project_forward");
+        if (mip)
+            project_forward_kernel<true><<<blocks, 256, 0, ctx->stream>>>(u, transforms, raw_opac, n,
+                                                                           intersect_counts, max_radius, depth_keys,
+                                                                           partials);
+        else
+            project_forward_kernel<false><<<blocks, 256, 0, ctx->stream>>>(u, transforms, raw_opac, n,
+                                                                            intersect_counts, max_radius, depth_keys,
+                                                                            partials);
+    }
+    KernelTimer t(ctx, "project_reduce");
+    project_reduce_kernel<<<1, 1024, 0, ctx->stream>>>(partials, blocks, counters);
 }
 
 // ---- project_visible ------------------------------------------------------------

@@ -52,7 +52,7 @@ __global__ __launch_bounds__(256) void rasterize_kernel(uint32_t img_w, uint32_t
                                                          void* __restrict__ out_img, float* __restrict__ visible,
                                                          uint32_t* __restrict__ off_post) {
     __shared__ float4 s_xyco[256];  // x, y, conic c00, conic c01
-    __shared__ float2 s_c11a[256];  // conic c11, opacity
+    __shared__ float4 s_c11a[256];  // conic c11, opacity, sigma cutoff
     __shared__ float4 s_rgbd[256];  // r, g, b, depth
     __shared__ uint32_t s_gid[BWD_INFO ? 256 : 1];
     __shared__ uint32_t s_contrib[BWD_INFO ? 256 : 1];
@@ -80,7 +80,7 @@ __global__ __launch_bounds__(256) void rasterize_kernel(uint32_t img_w, uint32_t
             const float2* row = reinterpret_cast<const float2*>(projected + (size_t)c * 10);
             float2 a = row[0], b = row[1], cc = row[2], d = row[3], e = row[4];
             s_xyco[t] = make_float4(a.x, a.y, b.x, b.y);
-            s_c11a[t] = make_float2(cc.x, cc.y);
+            s_c11a[t] = make_float4(cc.x, cc.y, sigma_cutoff<SMOOTH>(cc.y), 0.0f);
             s_rgbd[t] = make_float4(d.x, d.y, e.x, e.y);
             if (BWD_INFO) {
                 s_gid[t] = gfc[c];
@@ -91,9 +91,10 @@ __global__ __launch_bounds__(256) void rasterize_kernel(uint32_t img_w, uint32_t
         if (!done) {
             for (uint32_t j = 0; j < cnt; j++) {
                 const float4 xc = s_xyco[j];
-                const float2 ca = s_c11a[j];
+                const float4 ca = s_c11a[j];
                 const S2 conic{xc.z, xc.w, ca.x};
                 const float sigma = calc_sigma(pcx, pcy, conic, xc.x, xc.y);
+                if (!(sigma >= 0.0f) || sigma > ca.z) continue;  // cannot contribute
                 const float alpha = bh_minf(0.999f, ca.y * bh_expf(-sigma));
                 const float w = SMOOTH ? cutoff_weight(alpha) : (alpha >= kCutMid ? 1.0f : 0.0f);
                 if (sigma >= 0.0f && w > 0.0f) {

@@ -670,8 +670,10 @@ void or_rasterize_reference(const float* projected, uint32_t n, uint32_t w, uint
 /* splat visits the tile's 256 pixels in row-major order, carrying per-pixel */
 /* state (rgb remaining, T) from splat to splat.  The per-(splat, tile)      */
 /* gradient is summed over pixels in that order, then added to v_combined.   */
-/* Here tiles are visited in row-major order; the GPU adds the per-tile      */
-/* sums with atomics, so the cross-tile sum order differs (tolerance).       */
+/* Here tiles are visited in row-major order.  The per-(splat, tile) sum is  */
+/* formed as the GPU forms it: over each 64-pixel strip (tile rows 4k..4k+3) */
+/* in pixel order, then strip 0 + strip 1 + strip 2 + strip 3.  The GPU adds */
+/* the per-tile sums with atomics, so only the cross-tile order differs.     */
 /* ------------------------------------------------------------------------ */
 void or_rasterize_backward(uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,
                            const float* bg, const float* out_img, const float* projected,
@@ -710,8 +712,9 @@ void or_rasterize_backward(uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uin
             const float* s = projected + (size_t)cg * 10;
             s2 c = {s[2], s[3], s[4]};
             float cr = bh_maxf(s[6], 0.0f), cgc = bh_maxf(s[7], 0.0f), cb = bh_maxf(s[8], 0.0f);
-            float gr[11] = {0};
+            float gs[4][11] = {{0}};
             for (uint32_t p = 0; p < 256; p++) {
+                float* gr = gs[p >> 6];
                 float sx = st[p][0], sy = st[p][1], sz = st[p][2], sw = st[p][3];
                 if (!(sw > 1.0e-4f)) continue;
                 uint32_t px = ox + (p & 15u), py = oy + (p >> 4);
@@ -769,6 +772,8 @@ void or_rasterize_backward(uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uin
                 st[p][2] = nrz;
                 st[p][3] = next_t;
             }
+            float gr[11];
+            for (int k = 0; k < 11; k++) gr[k] = ((gs[0][k] + gs[1][k]) + gs[2][k]) + gs[3][k];
             float* out = v_combined + (size_t)cg * 11;
             for (int k = 0; k < 11; k++) {
                 if (k == 9 && !refine) continue;

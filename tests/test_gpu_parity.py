@@ -298,3 +298,23 @@ def test_autograd_end_to_end(gpu):
     rel_close("v_coeffs", s.grad.cpu().numpy(), vcoef, rtol=1e-3, atol_frac=1e-4)
     rel_close("v_raw_opac", op.grad.cpu().numpy(), vo, rtol=1e-3, atol_frac=1e-4)
     rel_close("refine", res._cfg.refine_weight.cpu().numpy(), vr, rtol=1e-3, atol_frac=1e-4)
+
+
+@pytest.mark.parametrize("flags", [1, 3])
+def test_alpha_cutoff_boundary_scene(gpu, flags):
+    """Low opacities put many (splat, pixel) pairs right at alpha = 1/255 (and
+    inside the smooth band): the blend's early reject must not change any
+    decision, so image and post-blend tile ends stay bit-exact."""
+    from brush_amd.camera import Camera
+
+    print(f"[case] cutoff boundary flags={flags}", flush=True)
+    tr, sh, opac = random_scene(4242 + flags, 6000, 1, log_scale=(-2.5, 0.5), opac=(-4.8, 0.6))
+    cam = Camera.from_focal((0.0, 0.0, -3.0), (0.0, 0.0, 0.0, 1.0), 60.0, 80, 64)
+    u = uniforms_for(cam, 80, 64, tr.shape[0], 1)
+    g = gpu_forward(u, tr, sh, opac, flags, (0.2, 0.1, 0.0))
+    o = O.render_forward(u, tr, sh, opac, flags, (0.2, 0.1, 0.0))
+    compare_forward(g, o)
+    v_out = np.random.default_rng(flags).standard_normal((64, 80, 4)).astype(np.float32)
+    vc_gpu = _gpu_backward(g, v_out, (flags & 2) | 16, (0.2, 0.1, 0.0), tr, sh, opac).cpu().numpy()
+    vc_ref = O.rasterize_backward(o, v_out, (flags & 2) | 16, (0.2, 0.1, 0.0))
+    rel_close("v_combined", vc_gpu[: o.num_visible], vc_ref[: o.num_visible], rtol=1e-3, atol_frac=1e-5)
