@@ -22,6 +22,14 @@ static int g_threads = 1;
 
 void or_set_threads(int n) { g_threads = n < 1 ? 1 : n; }
 
+void or_expf(const float* in, float* out, uint64_t n) {
+    for (uint64_t i = 0; i < n; i++) out[i] = bh_expf(in[i]);
+}
+
+void or_logf(const float* in, float* out, uint64_t n) {
+    for (uint64_t i = 0; i < n; i++) out[i] = bh_logf(in[i]);
+}
+
 int or_get_max_threads(void) {
 #ifdef _OPENMP
     return omp_get_max_threads();

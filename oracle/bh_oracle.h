@@ -30,6 +30,9 @@ extern "C" {
 
 /* Number of OpenMP threads the parallel loops may use (1 = sequential). */
 void or_set_threads(int n);
+/* Element-wise bh_expf / bh_logf, for pinning them against libm. */
+void or_expf(const float* in, float* out, uint64_t n);
+void or_logf(const float* in, float* out, uint64_t n);
 int or_get_max_threads(void);
 
 uint64_t or_project_forward(const bh_project_uniforms* u, const float* transforms,

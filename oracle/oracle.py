@@ -74,6 +74,8 @@ def lib():
         U64 = ctypes.c_uint64
         UP = ctypes.POINTER(Uniforms)
         L.or_set_threads.argtypes = [ctypes.c_int]
+        L.or_expf.argtypes = [P, P, U64]
+        L.or_logf.argtypes = [P, P, U64]
         L.or_get_max_threads.restype = ctypes.c_int
         L.or_project_forward.argtypes = [UP, P, P, U32, U32, P, P, P, P]
         L.or_project_forward.restype = U64
@@ -101,6 +103,20 @@ def set_threads(n: int):
 
 def max_threads() -> int:
     return int(lib().or_get_max_threads())
+
+
+def expf(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().or_expf(_p(x), _p(out), x.size)
+    return out
+
+
+def logf(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().or_logf(_p(x), _p(out), x.size)
+    return out
 
 
 # ---- primitives ---------------------------------------------------------------

@@ -1,0 +1,421 @@
+"""Pins the CPU restatement (oracle/) before it is trusted as the GPU checker.
+
+Every check here is independent of the kernels: the reference's own known
+answers and fixtures, float64 libm, closed forms, geometry derived in float64,
+brute force and finite differences.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.helpers import gsplat_case, random_scene, raster_oracle_scene, uniforms_for
+from brush_amd.camera import Camera
+
+
+# ---- exp / log ---------------------------------------------------------------------------------
+
+def _ulp_err(got, ref):
+    got = got.astype(np.float64)
+    with np.errstate(over="ignore"):
+        ref_f = ref.astype(np.float32)
+    finite = np.isfinite(ref_f)
+    ulp = np.spacing(np.abs(ref_f).astype(np.float32)).astype(np.float64)
+    ulp = np.maximum(ulp, 1.401298464324817e-45)
+    err = np.where(finite, np.abs(got - ref) / ulp, np.where(got == ref_f, 0.0, np.inf))
+    return err
+
+
+def test_expf_within_2ulp_of_libm():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.uniform(-104.0, 89.0, 2_000_000), rng.uniform(-2.0, 2.0, 1_000_000),
+                        np.array([0.0, -0.0, 1e-30, -1e-30, 88.72, -87.3, -103.0])]).astype(np.float32)
+    got = O.expf(x)
+    ref = np.exp(x.astype(np.float64))
+    assert np.max(_ulp_err(got, ref)) <= 2.0
+    assert np.isnan(O.expf(np.array([np.nan], np.float32)))[0]
+    assert O.expf(np.array([np.inf], np.float32))[0] == np.inf
+    assert O.expf(np.array([-np.inf], np.float32))[0] == 0.0
+
+
+def test_logf_within_2ulp_of_libm():
+    rng = np.random.default_rng(1)
+    bits = rng.integers(1, 0x7F800000, size=2_000_000, dtype=np.uint64).astype(np.uint32)
+    x = np.concatenate([bits.view(np.float32), rng.uniform(0.5, 2.0, 500_000).astype(np.float32),
+                        np.array([1.0, 255.0, 1.0 / 255.0, 1e-40], np.float32)])
+    got = O.logf(x)
+    ref = np.log(x.astype(np.float64))
+    assert np.max(_ulp_err(got, ref)) <= 2.0
+    assert O.logf(np.array([1.0], np.float32))[0] == 0.0
+    assert np.isnan(O.logf(np.array([-1.0], np.float32)))[0]
+    assert O.logf(np.array([0.0], np.float32))[0] == -np.inf
+
+
+# ---- blend: the reference's known answers -------------------------------------------------------
+
+def test_raster_reference_known_answers():
+    """raster_oracle.rs:111-159."""
+    one = np.array([0.5, 0.5, 1.0, 0.0, 1.0, 0.5, 1.0, 0.5, -1.0, 0.0], np.float32)
+    img = O.rasterize_reference(one, 1, 1, (0.2, 0.4, 0.6), False)
+    np.testing.assert_allclose(img.reshape(-1), [0.6, 0.45, 0.3, 0.5], atol=1e-6)
+    two = np.array([0.5, 0.5, 1.0, 0.0, 1.0, 0.999, 1.0, 0.0, 0.0, 0.0,
+                    0.5, 0.5, 1.0, 0.0, 1.0, 0.999, 0.0, 1.0, 0.0, 0.0], np.float32)
+    img = O.rasterize_reference(two, 1, 1, (0.0, 0.0, 0.0), False)
+    np.testing.assert_allclose(img.reshape(-1), [0.999, 0.0, 0.0, 0.999], atol=1e-6)
+    mid = np.float32(1.0) / np.float32(255.0)
+    cut = np.array([0.5, 0.5, 1.0, 0.0, 1.0, mid, 1.0, 0.0, 0.0, 0.0], np.float32)
+    hard = O.rasterize_reference(cut, 1, 1, (0.0, 0.0, 0.0), False)
+    smooth = O.rasterize_reference(cut, 1, 1, (0.0, 0.0, 0.0), True)
+    np.testing.assert_allclose(hard.reshape(-1), [mid, 0, 0, mid], atol=1e-7)
+    np.testing.assert_allclose(smooth.reshape(-1), [mid * 0.5, 0, 0, mid * 0.5], atol=1e-7)
+
+
+@pytest.mark.parametrize("size", [(23, 19), (15, 7), (16, 8), (17, 9), (9, 17)])
+@pytest.mark.parametrize("flags", [1, 3])
+def test_tiled_blend_matches_per_pixel_walk(size, flags):
+    """raster_oracle.rs:271-397: the tiled pipeline equals a walk over all
+    depth-sorted splats per pixel (no tiles) to 2e-5."""
+    cam, tr, sh, opac, bg = raster_oracle_scene()
+    w, h = size
+    u = uniforms_for(cam, w, h, 6, 0)
+    r = O.render_forward(u, tr, sh, opac, flags, bg)
+    assert r.num_visible == 6
+    ref = O.rasterize_reference(r.projected[: r.num_visible], w, h, bg, bool(flags & 2))
+    assert np.max(np.abs(r.out_img - ref)) <= 2e-5
+
+
+def test_gsplat_goldens():
+    """brush-bench-test/src/reference.rs:28-150: gsplat renders of tiny_case and
+    basic_case, compared at 1e-5 absolute + 1 % relative."""
+    for name in ["tiny_case", "basic_case"]:
+        cam, (w, h), tr, sh, opac, ref = gsplat_case(name)
+        r = O.render_forward(uniforms_for(cam, w, h, tr.shape[0], 3), tr, sh, opac, O.FLAG_BWD_INFO)
+        err = np.abs(r.out_img - ref)
+        assert np.all(err < 1e-5 + 1e-2 * np.abs(ref)), f"{name}: max err {err.max()}"
+
+
+# ---- primitives --------------------------------------------------------------------------------
+
+def test_tile_offsets_run_length_fixture():
+    """get_tile_offset.rs:88-129."""
+    runs = [31, 1, 223, 1, 1791, 1, 17, 0]
+    ids, expected = [], np.zeros(16, np.uint32)
+    for t, r in enumerate(runs):
+        if r == 0:
+            continue
+        expected[2 * t] = len(ids)
+        ids += [t] * r
+        expected[2 * t + 1] = len(ids)
+    ids += [8] * 13
+    np.testing.assert_array_equal(O.tile_offsets(np.array(ids, np.uint32), 8), expected)
+
+
+@pytest.mark.parametrize("bits", [0, 1, 4, 7, 8, 13, 17, 24, 31, 32])
+def test_stable_sort_matches_numpy(bits):
+    """brush-sort/src/lib.rs:170-241: stability at every bit width."""
+    rng = np.random.default_rng(bits)
+    n = 20_000
+    keys = rng.integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32)
+    keys[::3] &= np.uint32(7)  # plenty of ties
+    vals = np.arange(n, dtype=np.uint32)
+    k, v = O.stable_sort(keys, vals, bits)
+    mask = np.uint32(0xFFFFFFFF) if bits >= 32 else np.uint32((1 << bits) - 1)
+    order = np.argsort(keys & mask, kind="stable")
+    np.testing.assert_array_equal(v, order.astype(np.uint32))
+    np.testing.assert_array_equal(k, keys[order])
+
+
+@pytest.mark.parametrize("n", [4, 255, 256, 257, 1024, 41000])
+def test_prefix_sum_closed_form(n):
+    """brush-prefix-sum/src/lib.rs:109-220."""
+    x = np.random.default_rng(n).integers(0, 1000, n).astype(np.uint32)
+    np.testing.assert_array_equal(O.prefix_sum(x), np.cumsum(x, dtype=np.uint64).astype(np.uint32))
+
+
+# ---- project + cull ----------------------------------------------------------------------------
+
+STD_CAM = Camera((0.0, 0.0, -3.0), (0.0, 0.0, 0.0, 1.0), 0.5, 0.5)
+
+
+@pytest.mark.parametrize("case", ["nan_positions", "inf_positions", "nan_quats", "zero_quats", "nan_scales",
+                                  "inf_scales", "nan_opac"])
+def test_bad_geometry_fully_culled(case):
+    """fuzz.rs:330-448."""
+    n = 16
+    rng = np.random.default_rng(7)
+    tr = np.tile(np.array([0, 0, 3, 1, 0, 0, 0, 0, 0, 0], np.float32), (n, 1))
+    opac = np.zeros(n, np.float32)
+    if case == "nan_positions":
+        tr[:, 0:3] = np.nan
+    elif case == "inf_positions":
+        tr[:, 0:3] = np.where(np.arange(3) % 2 == 0, np.inf, -np.inf)
+    elif case == "nan_quats":
+        tr[:, 3:7] = rng.uniform(-1, 1, (n, 4))
+        tr[np.arange(n), 3 + rng.integers(0, 4, n)] = np.nan
+    elif case == "zero_quats":
+        tr[:, 3:7] = 0.0
+    elif case == "nan_scales":
+        tr[:, 7:10] = rng.uniform(-4, 4, (n, 3))
+        tr[np.arange(n), 7 + rng.integers(0, 3, n)] = np.nan
+    elif case == "inf_scales":
+        tr[:, 7:10] = 120.0
+    elif case == "nan_opac":
+        opac[:] = np.nan
+    r = O.render_forward(uniforms_for(STD_CAM, 64, 64, n, 0), tr, np.full((n, 1, 3), 0.5, np.float32), opac, 0)
+    assert r.num_visible == 0 and r.num_intersections == 0
+
+
+def test_extreme_but_valid_stays_visible():
+    """fuzz.rs:450-490."""
+    n = 4
+    u = uniforms_for(STD_CAM, 64, 64, n, 0)
+    for ls in [-30.0, -10.0, 0.0, 10.0, 20.0, 30.0, 40.0]:
+        tr = np.tile(np.array([0, 0, 3, 1, 0, 0, 0, ls, ls, ls], np.float32), (n, 1))
+        r = O.render_forward(u, tr, np.full((n, 1, 3), 0.5, np.float32), np.full(n, 2.0, np.float32), 0)
+        assert r.num_visible == n, f"log_scale={ls} over-culled"
+    for mag in [1e10, 1e25, 3.4028235e38 / 2]:
+        tr = np.tile(np.array([0, 0, 3, 1, 0, 0, 0, -1, -1, -1], np.float32), (n, 1))
+        sh = np.tile(np.array([mag, -mag, mag], np.float32), (n, 1)).reshape(n, 1, 3)
+        r = O.render_forward(u, tr, sh, np.full(n, 3.0, np.float32), 0)
+        assert r.num_visible == n, f"colour magnitude {mag} over-culled"
+
+
+def test_near_plane_and_behind_camera_culled():
+    """tests/mod.rs:41-93: splats with view depth < 0.01 render nothing."""
+    n = 8
+    tr = np.tile(np.array([0, 0, 0, 1, 0, 0, 0, -1, -1, -1], np.float32), (n, 1))
+    tr[:, 2] = np.linspace(-3.5, -2.995, n)  # camera at z = -3: depths -0.5 .. 0.005
+    r = O.render_forward(uniforms_for(STD_CAM, 32, 32, n, 0), tr, np.full((n, 1, 3), 0.5, np.float32),
+                         np.full(n, 4.0, np.float32), O.FLAG_BWD_INFO)
+    assert r.num_visible == 0
+    assert np.all(r.out_img == 0.0)
+
+
+def _tile_hits_float64(mx, my, c00, c01, c11, pt, tbw, tbh):
+    """Tiles whose 16x16 rect holds a point with Mahalanobis power <= pt, from
+    a float64 re-derivation of the edge test: the power restricted to the
+    rect's nearest edge line is minimised at dx = -c01 dy / c00 (horizontal
+    edge) or dy = -c01 dx / c11 (vertical edge)."""
+    out = set()
+    for ty in range(tbh):
+        for tx in range(tbw):
+            x0, y0, x1, y1 = tx * 16.0, ty * 16.0, tx * 16.0 + 16.0, ty * 16.0 + 16.0
+            in_x = x0 <= mx <= x1
+            in_y = y0 <= my <= y1
+            if in_x and in_y:
+                out.add((tx, ty))
+                continue
+            cx = x0 if mx < x0 else x1
+            cy = y0 if my < y0 else y1
+            dxf = 16.0 if mx < x0 else -16.0
+            dyf = 16.0 if my < y0 else -16.0
+            # minimiser along the edge through the nearest corner
+            tt_x = 0.0 if in_y else min(max((c00 * (mx - cx) + c01 * (my - cy)) / (c00 * dxf), 0.0), 1.0)
+            tt_y = 0.0 if in_x else min(max((c01 * (mx - cx) + c11 * (my - cy)) / (c11 * dyf), 0.0), 1.0)
+            px, py = cx + tt_x * dxf, cy + tt_y * dyf
+            dx, dy = px - mx, py - my
+            if 0.5 * (c00 * dx * dx + c11 * dy * dy) + c01 * dx * dy <= pt:
+                out.add((tx, ty))
+    return out
+
+
+def test_tile_predicate_against_float64_geometry():
+    """will_primitive_contribute (helpers.rs:385-424) and the counts of
+    project_forward agree with a float64 re-derivation on random anisotropic
+    splats, except within 1e-4 of the power threshold."""
+    rng = np.random.default_rng(11)
+    n = 300
+    tr = np.zeros((n, 10), np.float32)
+    tr[:, 0:2] = rng.uniform(-0.6, 0.6, (n, 2))
+    tr[:, 2] = rng.uniform(-0.5, 0.5, n)
+    q = rng.standard_normal((n, 4))
+    tr[:, 3:7] = q / np.linalg.norm(q, axis=1, keepdims=True)
+    tr[:, 7:10] = rng.uniform(-4.0, -1.5, (n, 3))
+    opac = rng.uniform(-3.0, 4.0, n).astype(np.float32)
+    cam = Camera.from_focal((0.0, 0.0, -3.0), (0.0, 0.0, 0.0, 1.0), 120.0, 112, 96)
+    u = uniforms_for(cam, 112, 96, n, 0)
+    r = O.render_forward(u, tr, np.full((n, 1, 3), 0.5, np.float32), opac, O.FLAG_BWD_INFO)
+    tbw, tbh = u["tile_bw"], u["tile_bh"]
+    by_splat = {}
+    for t, c in zip(r.tile_id_from_isect[: r.num_intersections], r.compact_gid_from_isect[: r.num_intersections]):
+        by_splat.setdefault(int(c), set()).add((int(t) % tbw, int(t) // tbw))
+    mismatches = 0
+    for c in range(r.num_visible):
+        p = r.projected[c].astype(np.float64)
+        pt = math.log(p[5] * 255.0)
+        ref = _tile_hits_float64(p[0], p[1], p[2], p[3], p[4], pt, tbw, tbh)
+        got = by_splat.get(c, set())
+        for tile in got ^ ref:
+            tx, ty = tile
+            # allow disagreement only for tiles whose decision sits on the threshold
+            near = _tile_hits_float64(p[0], p[1], p[2], p[3], p[4], pt * (1 + 1e-4) + 1e-4, tbw, tbh) - \
+                _tile_hits_float64(p[0], p[1], p[2], p[3], p[4], pt * (1 - 1e-4) - 1e-4, tbw, tbh)
+            assert tile in near, f"splat {c}: tile {tile} decided differently ({tile in got} vs {tile in ref})"
+            mismatches += 1
+        assert len(got) == r.intersect_counts[r.global_from_compact_gid[c]]
+    assert mismatches <= 3
+
+
+def test_no_pixel_contribution_outside_counted_tiles():
+    """Every pixel centre where a splat's alpha reaches 1/255 lies in a tile the
+    splat was binned to (the binning is conservative), so the tiled blend
+    equals the per-pixel walk (tests/mod.rs:475-605)."""
+    rng = np.random.default_rng(5)
+    n = 400
+    tr = np.zeros((n, 10), np.float32)
+    tr[:, 0:3] = rng.uniform(-0.8, 0.8, (n, 3))
+    q = rng.standard_normal((n, 4))
+    tr[:, 3:7] = q / np.linalg.norm(q, axis=1, keepdims=True)
+    tr[:, 7:10] = rng.uniform(-3.5, -1.0, (n, 3))
+    opac = rng.uniform(-4.0, 3.0, n).astype(np.float32)
+    cam = Camera.from_focal((0.0, 0.0, -3.0), (0.0, 0.0, 0.0, 1.0), 100.0, 96, 80)
+    u = uniforms_for(cam, 96, 80, n, 0)
+    r = O.render_forward(u, tr, np.full((n, 1, 3), 0.5, np.float32), opac, O.FLAG_BWD_INFO)
+    tbw = u["tile_bw"]
+    binned = set(zip(r.tile_id_from_isect[: r.num_intersections].tolist(),
+                     r.compact_gid_from_isect[: r.num_intersections].tolist()))
+    ys, xs = np.mgrid[0:80, 0:96]
+    pcx, pcy = xs + 0.5, ys + 0.5
+    mid = np.float32(1.0) / np.float32(255.0)
+    for c in range(r.num_visible):
+        p = r.projected[c]
+        dx = (pcx - p[0]).astype(np.float32)
+        dy = (pcy - p[1]).astype(np.float32)
+        sigma = np.float32(0.5) * (p[2] * dx * dx + p[4] * dy * dy) + p[3] * dx * dy
+        alpha = np.minimum(np.float32(0.999), p[5] * O.expf(-sigma))
+        hit = (alpha >= mid) & (sigma >= 0)
+        for y, x in zip(*np.nonzero(hit)):
+            assert ((x // 16) + (y // 16) * tbw, c) in binned, f"splat {c} pixel ({x},{y}) not binned"
+    ref = O.rasterize_reference(r.projected[: r.num_visible], 96, 80, (0, 0, 0), False)
+    assert np.max(np.abs(r.out_img - ref)) <= 2e-5
+
+
+def test_large_rotated_splats_cover_every_tile():
+    """tests/mod.rs:476-530 (fewer splats): big anisotropic splats at the
+    origin leave no tile empty."""
+    rng = np.random.default_rng(3)
+    n = 256
+    tr = np.zeros((n, 10), np.float32)
+    tr[:, 3:7] = rng.uniform(-1, 1, (n, 4))
+    tr[:, 7:10] = rng.uniform(1.0, 3.0, (n, 3))
+    cam = Camera((0.0, 0.0, -5.0), (0.0, 0.0, 0.0, 1.0), 0.5, 0.5)
+    O.set_threads(4)
+    try:
+        r = O.render_forward(uniforms_for(cam, 128, 128, n, 0), tr, np.full((n, 1, 3), 0.5, np.float32),
+                             np.full(n, -4.0, np.float32), O.FLAG_BWD_INFO)
+    finally:
+        O.set_threads(1)
+    alpha = r.out_img[..., 3].reshape(8, 16, 8, 16).mean(axis=(1, 3))
+    assert np.all(alpha > 1e-3)
+    assert r.num_visible == n
+
+
+# ---- backward ---------------------------------------------------------------------------------
+
+def _fd_scene():
+    rng = np.random.default_rng(21)
+    n = 10
+    tr = np.zeros((n, 10), np.float32)
+    tr[:, 0:2] = rng.uniform(-0.35, 0.35, (n, 2))
+    # depths 0.06 apart, so no perturbation below reorders the splats
+    tr[:, 2] = rng.permutation(np.linspace(-0.3, 0.3, n))
+    q = rng.standard_normal((n, 4))
+    tr[:, 3:7] = q / np.linalg.norm(q, axis=1, keepdims=True)
+    tr[:, 7:10] = rng.uniform(-2.3, -1.6, (n, 3))
+    sh = (rng.standard_normal((n, 4, 3)) * 0.3).astype(np.float32)
+    sh[:, 0, :] += 0.4
+    opac = rng.uniform(-1.0, 0.0, n).astype(np.float32)
+    cam = Camera.from_focal((0.05, -0.03, -3.0), (0.0, 0.0, 0.0, 1.0), 50.0, 40, 32)
+    return tr, sh, opac, cam
+
+
+def _loss(u, tr, sh, opac, weights, bg):
+    r = O.render_forward(u, tr, sh, opac, O.FLAG_BWD_INFO | O.FLAG_SMOOTH_CUTOFF, bg)
+    return float(np.sum(r.out_img.astype(np.float64) * weights))
+
+
+def test_backward_matches_finite_differences():
+    """finite_diff.rs:530-595 with the C^1 smooth cutoff: analytic gradients of
+    sum(W * image) against central differences of the forward."""
+    tr, sh, opac, cam = _fd_scene()
+    n = tr.shape[0]
+    u = uniforms_for(cam, 40, 32, n, 1)
+    bg = (0.1, 0.2, 0.3)
+    weights = np.random.default_rng(9).standard_normal((32, 40, 4)).astype(np.float32)
+    fwd = O.render_forward(u, tr, sh, opac, O.FLAG_BWD_INFO | O.FLAG_SMOOTH_CUTOFF, bg)
+    assert fwd.num_visible == n
+    vc = O.rasterize_backward(fwd, weights, O.FLAG_SMOOTH_CUTOFF, bg)
+    vt, vcoef, vo, _ = O.project_backward(fwd, tr, sh, opac, vc)
+    checks = []
+    for i in range(n):
+        for k in range(10):
+            checks.append(("t", i, k))
+        checks.append(("o", i, 0))
+        for k in (0, 1, 5, 11):
+            checks.append(("c", i, k))
+    worst = 0.0
+    for kind, i, k in checks:
+        eps = 1e-3
+        arrs = {"t": tr, "c": sh, "o": opac}
+        base = arrs[kind]
+        plus, minus = base.copy(), base.copy()
+        if kind == "t":
+            plus[i, k] += eps
+            minus[i, k] -= eps
+        elif kind == "c":
+            plus[i, k // 3, k % 3] += eps
+            minus[i, k // 3, k % 3] -= eps
+        else:
+            plus[i] += eps
+            minus[i] -= eps
+        args_p = {"t": (plus, sh, opac), "c": (tr, plus, opac), "o": (tr, sh, plus)}[kind]
+        args_m = {"t": (minus, sh, opac), "c": (tr, minus, opac), "o": (tr, sh, minus)}[kind]
+        fd = (_loss(u, *args_p, weights, bg) - _loss(u, *args_m, weights, bg)) / (2 * eps)
+        an = {"t": lambda: vt[i, k], "c": lambda: vcoef[i, k // 3, k % 3], "o": lambda: vo[i]}[kind]()
+        tol = 0.02 * abs(fd) + 0.02
+        worst = max(worst, abs(an - fd) / (abs(fd) + 1.0))
+        assert abs(an - fd) <= tol, f"{kind}[{i},{k}]: analytic {an} vs finite difference {fd}"
+    assert worst < 0.05
+
+
+def test_refine_toggle_and_hidden_splat_identities():
+    """finite_diff.rs:220-259 (the refine-weight lane does not change model
+    gradients) and :1019 (a splat behind a saturated stack gets exactly zero
+    gradient); culled splats get exactly zero dense rows."""
+    cam = Camera.from_focal((0.0, 0.0, -3.0), (0.0, 0.0, 0.0, 1.0), 60.0, 32, 32)
+    tr = np.array([
+        [0, 0, -0.2, 1, 0, 0, 0, 1.0, 1.0, 1.0],      # large and opaque, in front
+        [0, 0, -0.1, 1, 0, 0, 0, 1.0, 1.0, 1.0],      # large and opaque: saturates every pixel
+        [0, 0, 0.3, 1, 0, 0, 0, -3.0, -3.0, -3.0],    # small, hidden behind the stack
+        [0, 0, -9.0, 1, 0, 0, 0, -1.0, -1.0, -1.0],   # behind the camera: culled
+    ], np.float32)
+    sh = np.full((4, 1, 3), 0.4, np.float32)
+    opac = np.array([12.0, 12.0, 2.0, 2.0], np.float32)
+    u = uniforms_for(cam, 32, 32, 4, 0)
+    fwd = O.render_forward(u, tr, sh, opac, O.FLAG_BWD_INFO)
+    assert fwd.num_visible == 3
+    weights = np.random.default_rng(2).standard_normal((32, 32, 4)).astype(np.float32)
+    vc_r = O.rasterize_backward(fwd, weights, O.FLAG_REFINE_WEIGHT)
+    vc_n = O.rasterize_backward(fwd, weights, 0)
+    np.testing.assert_array_equal(vc_r[:, :9], vc_n[:, :9])
+    assert np.all(vc_n[:, 9] == 0)
+    hidden = int(np.nonzero(fwd.global_from_compact_gid == 2)[0][0])
+    assert np.all(vc_r[hidden] == 0.0)
+    vt, vcoef, vo, vr = O.project_backward(fwd, tr, sh, opac, vc_r)
+    for g in (2, 3):
+        assert np.all(vt[g] == 0) and np.all(vcoef[g] == 0) and vo[g] == 0 and vr[g] == 0
+    assert np.all(np.isfinite(vt)) and np.any(vt[0] != 0)
+
+
+def test_backward_gradients_finite_on_random_scenes():
+    """fuzz.rs:492-551."""
+    for seed in range(4):
+        tr, sh, opac = random_scene(77 + seed, 300, 2, log_scale=(-2.5, 0.8))
+        cam = Camera.from_focal((0.0, 0.0, -3.0), (0.0, 0.0, 0.0, 1.0), 50.0, 48, 40)
+        u = uniforms_for(cam, 48, 40, 300, 2)
+        fwd = O.render_forward(u, tr, sh, opac, O.FLAG_BWD_INFO)
+        vc = O.rasterize_backward(fwd, np.full((40, 48, 4), 1.0 / (40 * 48 * 4), np.float32), O.FLAG_REFINE_WEIGHT)
+        out = O.project_backward(fwd, tr, sh, opac, vc)
+        for a in out:
+            assert np.all(np.isfinite(a))
