@@ -8,9 +8,9 @@
 // diagonal); the transmittance / remaining-colour state never leaves the
 // lane's registers.  Splats are staged in LDS in batches of 64.  For each
 // splat a wave that had any contributing pixel sums the 9-11 gradient lanes
-// across its 64 pixels with DPP adds (six steps to lane 63); the four strips'
-// partials are added in LDS in strip order and each (splat, tile) pair costs
-// one hardware float atomic per gradient lane.  A wave whose 64 pixels have
+// over each 16-pixel row with DPP adds; the 16 row partials are added in LDS
+// in row order and each (splat, tile) pair costs one hardware float atomic
+// per gradient lane.  A wave whose 64 pixels have
 // all saturated stops evaluating splats.
 //
 // project_backward: one thread per *global* id, so every dense output row is
@@ -25,24 +25,23 @@
 
 namespace bh {
 
-// Sum of x over the wave, left in lane 63 (other lanes hold partial sums):
-// inclusive Hillis-Steele steps inside each 16-lane row, then the row
-// broadcasts, all as DPP adds.
-template <int CTRL, int ROW_MASK>
+// Sum of x over each 16-lane row of the wave, left in the row's last lane
+// (inclusive Hillis-Steele steps as DPP adds).
+template <int CTRL>
 __device__ __forceinline__ float dpp_add(float x) {
-    return x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xF, true));
+    return x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
 }
-__device__ __forceinline__ float wave_sum_lane63(float x) {
-    x = dpp_add<0x111, 0xF>(x);  // row_shr:1
-    x = dpp_add<0x112, 0xF>(x);  // row_shr:2
-    x = dpp_add<0x114, 0xF>(x);  // row_shr:4
-    x = dpp_add<0x118, 0xF>(x);  // row_shr:8
-    x = dpp_add<0x142, 0xA>(x);  // row_bcast:15 into rows 1 and 3
-    x = dpp_add<0x143, 0xC>(x);  // row_bcast:31 into rows 2 and 3
+__device__ __forceinline__ float row_sum_last_lane(float x) {
+    x = dpp_add<0x111>(x);  // row_shr:1
+    x = dpp_add<0x112>(x);  // row_shr:2
+    x = dpp_add<0x114>(x);  // row_shr:4
+    x = dpp_add<0x118>(x);  // row_shr:8
     return x;
 }
 
-constexpr uint32_t kBwdBatch = 64;
+constexpr uint32_t kBwdBatch = 32;
+constexpr int kNG = 11;
+constexpr int kRows = 16;  // 16-pixel rows per tile = partial sums per splat
 
 template <bool SMOOTH, bool REFINE, bool DEPTH>
 __global__ __launch_bounds__(256) void rasterize_backward_kernel(
@@ -50,16 +49,18 @@ __global__ __launch_bounds__(256) void rasterize_backward_kernel(
     const float* __restrict__ out_img, const float* __restrict__ projected, const uint32_t* __restrict__ cgids,
     const uint32_t* __restrict__ offsets, const float* __restrict__ v_output, float* __restrict__ v_combined) {
     constexpr uint32_t CH = DEPTH ? 5u : 4u;
-    constexpr int NG = 11;
+    constexpr int NG = kNG;
     __shared__ float4 s_xyco[kBwdBatch];  // x, y, conic c00, c01
     __shared__ float4 s_crgb[kBwdBatch];  // conic c11, opacity, r, g
     __shared__ float4 s_bd[kBwdBatch];    // b, depth, sigma cutoff
     __shared__ uint32_t s_cid[kBwdBatch];
-    __shared__ float s_grad[4][kBwdBatch][NG + 1];  // per-wave partials; [NG] flags "wave contributed"
+    __shared__ uint32_t s_strips[kBwdBatch];  // strips of the tile each splat may touch
+    // per (pixel row, splat): partial gradient; lane NG flags a contribution
+    __shared__ float s_grad[kRows][kBwdBatch][NG + 1];
 
     const uint32_t tile = blockIdx.x;
     const uint32_t ox = (tile % tile_bw) * 16u, oy = (tile / tile_bw) * 16u;
-    const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
+    const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6, row = t >> 4;
     const uint32_t px = ox + (t & 15u), py = oy + (t >> 4);
     const bool inside = px < img_w && py < img_h;
     const float pcx = (float)px + 0.5f, pcy = (float)py + 0.5f;
@@ -96,93 +97,98 @@ __global__ __launch_bounds__(256) void rasterize_backward_kernel(
         const uint32_t cnt = min(kBwdBatch, hi - b);
         if (t < cnt) {
             const uint32_t c = min(cgids[b + t], num_visible - 1u);
-            const float2* row = reinterpret_cast<const float2*>(projected + (size_t)c * 10);
-            const float2 r0 = row[0], r1 = row[1], r2 = row[2], r3 = row[3], r4 = row[4];
+            const float2* prow = reinterpret_cast<const float2*>(projected + (size_t)c * 10);
+            const float2 r0 = prow[0], r1 = prow[1], r2 = prow[2], r3 = prow[3], r4 = prow[4];
+            const float cut = sigma_cutoff<SMOOTH>(r2.y);
             s_xyco[t] = make_float4(r0.x, r0.y, r1.x, r1.y);
             s_crgb[t] = make_float4(r2.x, r2.y, r3.x, r3.y);
-            s_bd[t] = make_float4(r4.x, r4.y, sigma_cutoff<SMOOTH>(r2.y), 0.0f);
+            s_bd[t] = make_float4(r4.x, r4.y, cut, 0.0f);
             s_cid[t] = c;
+            s_strips[t] = strip_mask(r0.x, r0.y, S2{r1.x, r1.y, r2.x}, cut, ox, oy);
         }
-        for (uint32_t e = t; e < 4u * kBwdBatch; e += 256u) (&s_grad[0][0][0])[e * (NG + 1) + NG] = 0.0f;
+        for (uint32_t e = t; e < (uint32_t)kRows * kBwdBatch; e += 256u) (&s_grad[0][0][0])[e * (NG + 1) + NG] = 0.0f;
         __syncthreads();
-        for (uint32_t j = 0; wave_live && j < cnt; j++) {
+        // splats of the batch that may touch this wave's strip, in order
+        uint64_t todo = __ballot(lane < cnt && ((s_strips[lane] >> wave) & 1u));
+        while (wave_live && todo) {
+            const uint32_t j = (uint32_t)__builtin_ctzll(todo);
+            todo &= todo - 1ull;
             const float4 xc = s_xyco[j];
             const float4 cr4 = s_crgb[j];
             const float4 bd = s_bd[j];
             const S2 conic{xc.z, xc.w, cr4.x};
             const float opac = cr4.y;
-            float g[NG];
-#pragma unroll
-            for (int k = 0; k < NG; k++) g[k] = 0.0f;
-            bool contrib = false;
             const float dx = xc.x - pcx, dy = xc.y - pcy;
             const float sigma = 0.5f * (conic.c00 * dx * dx + conic.c11 * dy * dy) + conic.c01 * dx * dy;
-            if (sw > 1.0e-4f && sigma >= 0.0f && !(sigma > bd.z)) {
-                const float gaussian = bh_expf(-sigma);
-                const float alpha = bh_minf(0.999f, opac * gaussian);
-                const float w = SMOOTH ? cutoff_weight(alpha) : (alpha >= kCutMid ? 1.0f : 0.0f);
-                if (sigma >= 0.0f && w > 0.0f) {
-                    const float ae = alpha * w;
-                    const float next_t = sw * (1.0f - ae);
-                    if (next_t <= 1.0e-4f) {
-                        sw = 0.0f;
-                    } else {
-                        contrib = true;
-                        const float cr = bh_maxf(cr4.z, 0.0f), cgc = bh_maxf(cr4.w, 0.0f), cb = bh_maxf(bd.x, 0.0f);
-                        const float vis = ae * sw;
-                        g[5] = cr4.z >= 0.0f ? vis * vox : 0.0f;
-                        g[6] = cr4.w >= 0.0f ? vis * voy : 0.0f;
-                        g[7] = bd.x >= 0.0f ? vis * voz : 0.0f;
-                        // gradient-only quantities: hardware reciprocal / sqrt (1 ulp)
-                        const float ra = __builtin_amdgcn_rcpf(1.0f - ae);
-                        const float dot_rgb = ((sw * cr - sx) * vox + (sw * cgc - sy) * voy + (sw * cb - sz) * voz) * ra;
-                        const float nrx = sx - vis * cr, nry = sy - vis * cgc, nrz = sz - vis * cb;
-                        if (DEPTH) {
-                            g[10] = vis * vod;
-                            sd = sd - vis * bd.y;
-                        }
-                        const float v_ae = dot_rgb + vow * ra;
-                        const float dw = SMOOTH ? cutoff_weight_deriv(alpha) : 0.0f * alpha;
-                        const float v_alpha = v_ae * (w + alpha * dw);
-                        const float v_sigma = -alpha * v_alpha;
-                        const float vxy_x = v_sigma * (conic.c00 * dx + conic.c01 * dy);
-                        const float vxy_y = v_sigma * (conic.c01 * dx + conic.c11 * dy);
-                        if (opac * gaussian <= 0.999f) {
-                            g[2] = 0.5f * v_sigma * dx * dx;
-                            g[3] = v_sigma * dx * dy;
-                            g[4] = 0.5f * v_sigma * dy * dy;
-                            g[0] = vxy_x;
-                            g[1] = vxy_y;
-                            g[8] = v_alpha * gaussian;
-                            if (REFINE) {
-                                const float len = __builtin_amdgcn_sqrtf(vxy_x * img_wf * vxy_x * img_wf +
-                                                                         vxy_y * img_hf * vxy_y * img_hf);
-                                g[9] = len * inv_final_a;
-                            }
-                        }
-                        sx = nrx;
-                        sy = nry;
-                        sz = nrz;
-                        sw = next_t;
-                    }
-                }
+            const bool maybe = sw > 1.0e-4f && sigma >= 0.0f && !(sigma > bd.z);
+            if (__ballot(maybe) == 0ull) continue;
+            // lanes outside `maybe` compute values that the selects below discard
+            const float gaussian = bh_expf_neg(-sigma);
+            const float alpha = bh_minf(0.999f, opac * gaussian);
+            const float w = SMOOTH ? cutoff_weight(alpha) : (alpha >= kCutMid ? 1.0f : 0.0f);
+            const bool pass = maybe && w > 0.0f;
+            const float ae = alpha * w;
+            const float next_t = sw * (1.0f - ae);
+            const bool saturate = pass && next_t <= 1.0e-4f;
+            const bool contrib = pass && !saturate;
+            if (saturate) sw = 0.0f;
+            if (__ballot(contrib) == 0ull) {
+                wave_live = __ballot(sw > 1.0e-4f) != 0ull;
+                continue;
             }
-            if (__ballot(contrib) != 0ull) {
+            const float cr = bh_maxf(cr4.z, 0.0f), cgc = bh_maxf(cr4.w, 0.0f), cb = bh_maxf(bd.x, 0.0f);
+            const float vis = ae * sw;
+            float g[NG];
+            g[5] = cr4.z >= 0.0f ? vis * vox : 0.0f;
+            g[6] = cr4.w >= 0.0f ? vis * voy : 0.0f;
+            g[7] = bd.x >= 0.0f ? vis * voz : 0.0f;
+            // gradient-only quantities: hardware reciprocal / sqrt (1 ulp)
+            const float ra = __builtin_amdgcn_rcpf(1.0f - ae);
+            const float dot_rgb = ((sw * cr - sx) * vox + (sw * cgc - sy) * voy + (sw * cb - sz) * voz) * ra;
+            const float v_ae = dot_rgb + vow * ra;
+            const float dw = SMOOTH ? cutoff_weight_deriv(alpha) : 0.0f * alpha;
+            const float v_alpha = v_ae * (w + alpha * dw);
+            const float v_sigma = -alpha * v_alpha;
+            const float vxy_x = v_sigma * (conic.c00 * dx + conic.c01 * dy);
+            const float vxy_y = v_sigma * (conic.c01 * dx + conic.c11 * dy);
+            const bool unclamped = opac * gaussian <= 0.999f;
+            g[2] = 0.5f * v_sigma * dx * dx;
+            g[3] = v_sigma * dx * dy;
+            g[4] = 0.5f * v_sigma * dy * dy;
+            g[0] = vxy_x;
+            g[1] = vxy_y;
+            g[8] = v_alpha * gaussian;
+            g[9] = REFINE ? __builtin_amdgcn_sqrtf(vxy_x * img_wf * vxy_x * img_wf + vxy_y * img_hf * vxy_y * img_hf) *
+                                inv_final_a
+                          : 0.0f;
+            g[10] = DEPTH ? vis * vod : 0.0f;
 #pragma unroll
-                for (int k = 0; k < NG; k++) {
-                    if ((k == 9 && !REFINE) || (k == 10 && !DEPTH)) continue;
-                    g[k] = wave_sum_lane63(g[k]);
-                }
-                if (lane == 63u) {
+            for (int k = 0; k < NG; k++) {
+                const bool keep = contrib && (k >= 5 ? (k != 9 || unclamped) : unclamped) && (k != 8 || unclamped);
+                g[k] = keep ? g[k] : 0.0f;
+            }
+            if (contrib) {
+                sx = sx - vis * cr;
+                sy = sy - vis * cgc;
+                sz = sz - vis * cb;
+                if (DEPTH) sd = sd - vis * bd.y;
+                sw = next_t;
+            }
 #pragma unroll
-                    for (int k = 0; k < NG; k++) s_grad[wave][j][k] = g[k];
-                    s_grad[wave][j][NG] = 1.0f;
-                }
+            for (int k = 0; k < NG; k++) {
+                if ((k == 9 && !REFINE) || (k == 10 && !DEPTH)) continue;
+                g[k] = row_sum_last_lane(g[k]);
+            }
+            if ((t & 15u) == 15u) {
+                float* dst = &s_grad[row][j][0];
+#pragma unroll
+                for (int k = 0; k < NG; k++) dst[k] = g[k];
+                dst[NG] = 1.0f;
             }
             wave_live = __ballot(sw > 1.0e-4f) != 0ull;
         }
         __syncthreads();
-        // per splat: the four strips' partials, added in strip order
+        // per splat: the 16 row partials, added in row order
         for (uint32_t e = t; e < (uint32_t)NG * kBwdBatch; e += 256u) {
             const uint32_t k = e / kBwdBatch, j = e % kBwdBatch;
             const bool used = k < 9u || (REFINE && k == 9u) || (DEPTH && k == 10u);
@@ -190,9 +196,9 @@ __global__ __launch_bounds__(256) void rasterize_backward_kernel(
                 float sum = 0.0f;
                 bool any = false;
 #pragma unroll
-                for (int w = 0; w < 4; w++) {
-                    if (s_grad[w][j][NG] != 0.0f) {
-                        sum = any ? sum + s_grad[w][j][k] : s_grad[w][j][k];
+                for (int r = 0; r < kRows; r++) {
+                    if (s_grad[r][j][NG] != 0.0f) {
+                        sum = any ? sum + s_grad[r][j][k] : s_grad[r][j][k];
                         any = true;
                     }
                 }

@@ -149,6 +149,31 @@ BH_HD float bh_logf(float x) {
     return ef * ln2_hi + (ef * ln2_lo + logm);
 }
 
+/* bh_expf for x in [-87, 0] (every argument the blend kernels evaluate:
+ * x = -sigma with 0 <= sigma <= ln(255) + small): the same operations as
+ * bh_expf without the NaN / overflow / subnormal branches, which cannot
+ * trigger in that range, so the result is bit-identical there. */
+BH_HD float bh_expf_neg(float x) {
+    const float log2e = 1.44269502162933349609375f;
+    const float ln2_hi = 0.693145751953125f;
+    const float ln2_lo = 1.428606765330187045e-06f;
+    const float shifter = 12582912.0f;
+    float k = x * log2e;
+    float kr = (k + shifter) - shifter;
+    int n = (int)kr;
+    float r = bh_fmaf(kr, -ln2_hi, x);
+    r = bh_fmaf(kr, -ln2_lo, r);
+    float p = 1.98412698412698413e-04f;
+    p = bh_fmaf(p, r, 1.38888888888888889e-03f);
+    p = bh_fmaf(p, r, 8.33333333333333333e-03f);
+    p = bh_fmaf(p, r, 4.16666666666666667e-02f);
+    p = bh_fmaf(p, r, 1.66666666666666667e-01f);
+    p = bh_fmaf(p, r, 0.5f);
+    p = bh_fmaf(p, r, 1.0f);
+    p = bh_fmaf(p, r, 1.0f);
+    return p * bh_as_float((uint32_t)(n + 127) << 23);
+}
+
 /* 1 / (1 + e^-x)  (brush-cube/src/lib.rs:620-623) */
 BH_HD float bh_sigmoidf(float x) { return 1.0f / (1.0f + bh_expf(-x)); }
 

@@ -279,6 +279,50 @@ BH_DEV float sigma_cutoff(float opac) {
     return bh_logf(opac / alpha_min) + 1.0e-3f;
 }
 
+// Lower bound on the power 0.5 d^T C d (d = p - m) over the pixel centres of
+// the rectangle [x0, x1] x [y0, y1]: 0 if m lies inside, otherwise the least
+// of the four clamped edge minimisers (the power restricted to a horizontal
+// edge is minimised at dx = -c01 dy / c00, to a vertical one at
+// dy = -c01 dx / c11).  A splat whose bound exceeds its sigma_cutoff by more
+// than the float error of evaluating the power (1e-5 of the largest term
+// magnitude in the rectangle; the evaluation error is below 1e-6 of it) can
+// contribute to no pixel of the rectangle.
+BH_DEV bool may_touch_rect(float mx, float my, const S2& c, float cutoff, float x0, float y0, float x1, float y1) {
+    if (mx >= x0 && mx <= x1 && my >= y0 && my <= y1) return true;
+    float best = 3.0e38f;
+    const float ey[2] = {y0, y1};
+    const float ex[2] = {x0, x1};
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const float dy = ey[k] - my;
+        const float dx = bh_clampf(mx - c.c01 * dy / c.c00, x0, x1) - mx;
+        best = bh_minf(best, 0.5f * (c.c00 * dx * dx + c.c11 * dy * dy) + c.c01 * dx * dy);
+    }
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const float dx = ex[k] - mx;
+        const float dy = bh_clampf(my - c.c01 * dx / c.c11, y0, y1) - my;
+        best = bh_minf(best, 0.5f * (c.c00 * dx * dx + c.c11 * dy * dy) + c.c01 * dx * dy);
+    }
+    const float mdx = bh_maxf(bh_absf(x0 - mx), bh_absf(x1 - mx));
+    const float mdy = bh_maxf(bh_absf(y0 - my), bh_absf(y1 - my));
+    const float mag = c.c00 * mdx * mdx + c.c11 * mdy * mdy + 2.0f * bh_absf(c.c01) * mdx * mdy;
+    return !(best > cutoff + 1.0e-5f * mag + 1.0e-6f);
+}
+
+// 4-bit mask of the 16x4 pixel strips (tile rows 4k..4k+3) of the tile with
+// pixel origin (ox, oy) that a splat may touch.
+BH_DEV uint32_t strip_mask(float mx, float my, const S2& c, float cutoff, uint32_t ox, uint32_t oy) {
+    uint32_t m = 0;
+    const float x0 = (float)ox + 0.5f, x1 = (float)ox + 15.5f;
+#pragma unroll
+    for (uint32_t k = 0; k < 4; k++) {
+        const float y0 = (float)(oy + 4u * k) + 0.5f;
+        if (may_touch_rect(mx, my, c, cutoff, x0, y0, x1, y0 + 3.0f)) m |= 1u << k;
+    }
+    return m;
+}
+
 // ---- spherical harmonics (kernels/sh.rs) --------------------------------------
 // Coefficient k of a splat's row, channel-interleaved: row[3k + ch].
 BH_DEV V3 rd3(const float* c, int k) { return v3(c[3 * k], c[3 * k + 1], c[3 * k + 2]); }

@@ -56,6 +56,7 @@ __global__ __launch_bounds__(256) void rasterize_kernel(uint32_t img_w, uint32_t
     __shared__ float4 s_rgbd[256];  // r, g, b, depth
     __shared__ uint32_t s_gid[BWD_INFO ? 256 : 1];
     __shared__ uint32_t s_contrib[BWD_INFO ? 256 : 1];
+    __shared__ uint32_t s_strips[256];  // strips of the tile each splat may touch
     __shared__ uint32_t s_max_useful;
 
     const uint32_t tile = blockIdx.x;
@@ -79,8 +80,10 @@ __global__ __launch_bounds__(256) void rasterize_kernel(uint32_t img_w, uint32_t
             const uint32_t c = min(cgids[batch + t], num_visible - 1u);
             const float2* row = reinterpret_cast<const float2*>(projected + (size_t)c * 10);
             float2 a = row[0], b = row[1], cc = row[2], d = row[3], e = row[4];
+            const float cut = sigma_cutoff<SMOOTH>(cc.y);
             s_xyco[t] = make_float4(a.x, a.y, b.x, b.y);
-            s_c11a[t] = make_float4(cc.x, cc.y, sigma_cutoff<SMOOTH>(cc.y), 0.0f);
+            s_c11a[t] = make_float4(cc.x, cc.y, cut, 0.0f);
+            s_strips[t] = strip_mask(a.x, a.y, S2{b.x, b.y, cc.x}, cut, tx * 16u, ty * 16u);
             s_rgbd[t] = make_float4(d.x, d.y, e.x, e.y);
             if (BWD_INFO) {
                 s_gid[t] = gfc[c];
@@ -88,8 +91,14 @@ __global__ __launch_bounds__(256) void rasterize_kernel(uint32_t img_w, uint32_t
             }
         }
         __syncthreads();
-        if (!done) {
-            for (uint32_t j = 0; j < cnt; j++) {
+        const uint32_t wave = t >> 6, lane = t & 63u;
+        for (uint32_t q = 0; q < cnt; q += 64u) {
+            // splats of this 64-chunk that may touch this wave's strip, in order
+            uint64_t todo = __ballot(q + lane < cnt && ((s_strips[q + lane] >> wave) & 1u));
+            if (__ballot(!done) == 0ull) todo = 0ull;
+            while (todo && !done) {
+                const uint32_t j = q + (uint32_t)__builtin_ctzll(todo);
+                todo &= todo - 1ull;
                 const float4 xc = s_xyco[j];
                 const float4 ca = s_c11a[j];
                 const S2 conic{xc.z, xc.w, ca.x};
