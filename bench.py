@@ -27,6 +27,24 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "cfg1_hbm_traffic.md")
+
+
+def measured_traffic(kernel: str, workload: str):
+    """HBM bytes per launch of ``kernel`` from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (lines ``traffic <kernel> <bytes>``), or
+    None when that summary does not cover this workload or kernel."""
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+    except OSError:
+        return None
+    if f"workload: {workload}" not in text:
+        return None
+    for line in text.splitlines():
+        f = line.split()
+        if len(f) == 3 and f[0] == "traffic" and f[1] == kernel:
+            return int(f[2])
+    return None
 
 
 def algorithmic_bytes(name: str, n: int, v: int, m: int, m_post: int, t: int, p: int, c: int,
@@ -105,6 +123,9 @@ def main():
     ap.add_argument("--config", type=int, default=1)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget in seconds (0 = skip)")
     ap.add_argument("--no-timing", action="store_true", help="do not bracket kernels with HIP events")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="before warm-up, run one plain device copy of this many MiB (the known-size reference "
+                         "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
@@ -144,6 +165,15 @@ def main():
         stats["num_intersections"] = res.aux.num_intersections
         stats["out"] = res
         return res
+
+    if args.calibrate_copy_mib > 0:
+        words = args.calibrate_copy_mib * (1 << 18)
+        src = torch.ones(words, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     for _ in range(args.warmup):
         step()
@@ -187,7 +217,7 @@ def main():
         kd = kernels[dominant]
         achieved = kd["gb_s"] or 0.0
         roofline = {"bound": "hbm", "kernel": dominant, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None}
+                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dominant, w.name)}
 
     cpu = None
     if args.cpu_seconds > 0:
