@@ -1,0 +1,139 @@
+// bh_tile_walk.h — wave-cooperative walk over the tile bounding boxes of 64 splats.
+//
+// The reference tests a splat's bounding-box tiles in a loop run by the
+// splat's own thread (project_forward.rs:105-118, map_gaussians.rs:56-79), so
+// a wave waits for its largest splat while most lanes idle.  Here a wave
+// flattens the (splat, bbox tile) items of its 64 splats into one list, in
+// splat order and, within a splat, in the reference's row-major tile order,
+// and tests 64 items per step.  Per step, every lane finds the splat that owns
+// its item (a scatter of segment starts into LDS and a max-scan), fetches that
+// splat's record from LDS and evaluates the same tile predicate.  Hits are
+// tallied per splat by the last lane of each splat's run in the step; passing
+// items come out in exactly the order the per-splat loops would emit them, so
+// the map kernel writes them contiguously.
+#pragma once
+
+#include "bh_splat_math.h"
+
+namespace bh {
+
+// One splat's walk record in LDS (48 bytes, three 16-byte reads).
+struct WalkRec {
+    float4 a;  // mean x, mean y, conic c00, conic c01
+    float4 b;  // conic c11, power threshold, 1 / bbox width, end item index (bits)
+    uint4 c;   // bbox min_x, bbox min_y, bbox width, first item index
+};
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, ROW_MASK, 0xF, true);
+}
+
+// Inclusive wave64 scans: shifts within 16-lane rows, then row broadcasts of
+// lanes 15 and 31 into the following rows.
+__device__ __forceinline__ uint32_t wave_incl_add_u32(uint32_t x) {
+    x += dpp_u32<0x111, 0xF>(x);  // row_shr:1
+    x += dpp_u32<0x112, 0xF>(x);  // row_shr:2
+    x += dpp_u32<0x114, 0xF>(x);  // row_shr:4
+    x += dpp_u32<0x118, 0xF>(x);  // row_shr:8
+    x += dpp_u32<0x142, 0xA>(x);  // row_bcast:15 into rows 1 and 3
+    x += dpp_u32<0x143, 0xC>(x);  // row_bcast:31 into rows 2 and 3
+    return x;
+}
+__device__ __forceinline__ uint32_t wave_incl_max_u32(uint32_t x) {
+    x = max(x, dpp_u32<0x111, 0xF>(x));
+    x = max(x, dpp_u32<0x112, 0xF>(x));
+    x = max(x, dpp_u32<0x114, 0xF>(x));
+    x = max(x, dpp_u32<0x118, 0xF>(x));
+    x = max(x, dpp_u32<0x142, 0xA>(x));
+    x = max(x, dpp_u32<0x143, 0xC>(x));
+    return x;
+}
+
+// Orders this wave's LDS writes before its later LDS reads as seen by the
+// compiler: without it, a lane's read of a slot it wrote itself may be
+// forwarded from its own store even when another lane of the wave overwrote
+// the slot in between.  Wavefront scope: no instruction is emitted.
+__device__ __forceinline__ void wave_lds_fence() {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
+__device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+// Items (bbox tiles) of a splat whose box is bb; zero for an empty box.
+__device__ __forceinline__ uint32_t bbox_items(const TileBox& bb) {
+    return (bb.max_x > bb.min_x && bb.max_y > bb.min_y) ? (bb.max_x - bb.min_x) * (bb.max_y - bb.min_y) : 0u;
+}
+
+// Cooperative walk of one wave.  Every lane of the wave must call it (it uses
+// wave-wide DPP and ballots).  `items` is this lane's bbox tile count (0 for a
+// culled or absent splat); m, conic, pt, bb describe its splat.  `rec`,
+// `owner_slot` and `hits` are this wave's 64-entry LDS arrays.
+//
+// Returns the number of passing tiles of this lane's splat.  With WRITE, the
+// passing items are stored at out_base + (passing items before it in walk
+// order): tile id tx + ty * tile_bw into tile_ids and id_base + owner lane into
+// ids, skipping positions >= out_end.
+template <bool WRITE>
+__device__ uint32_t wave_tile_walk(uint32_t lane, uint32_t items, V2 m, const S2& conic, float pt,
+                                   const TileBox& bb, WalkRec* rec, uint32_t* owner_slot, uint32_t* hits,
+                                   uint32_t tile_bw, uint32_t out_base, uint32_t out_end, uint32_t id_base,
+                                   uint32_t* __restrict__ tile_ids, uint32_t* __restrict__ ids) {
+    const uint32_t incl = wave_incl_add_u32(items);
+    const uint32_t start = incl - items;
+    const uint32_t total = __builtin_amdgcn_readlane(incl, 63);
+    const uint32_t bw = bb.max_x - bb.min_x;
+    rec[lane].a = make_float4(m.x, m.y, conic.c00, conic.c01);
+    rec[lane].b = make_float4(conic.c11, pt, items ? 1.0f / (float)bw : 0.0f, __uint_as_float(incl));
+    rec[lane].c = make_uint4(bb.min_x, bb.min_y, bw, start);
+    hits[lane] = 0u;
+    wave_lds_fence();
+    uint32_t written = 0;  // passing items of earlier steps (wave uniform)
+    for (uint32_t base = 0; base < total; base += 64u) {
+        // owner of item base + lane: the splat with the largest start <= item
+        owner_slot[lane] = 0u;
+        const bool in_window = items != 0u && start < base + 64u && incl > base;
+        if (in_window) owner_slot[start > base ? start - base : 0u] = lane + 1u;
+        wave_lds_fence();
+        const uint32_t owner = wave_incl_max_u32(owner_slot[lane]) - 1u;
+        const uint32_t item = base + lane;
+        const bool valid = item < total;
+        const WalkRec r = rec[owner & 63u];
+        const uint32_t local = item - r.c.w;
+        // row = local / width through the float reciprocal, then one exact
+        // correction step either way
+        uint32_t row = (uint32_t)(((float)local + 0.5f) * r.b.z);
+        int32_t col = (int32_t)(local - row * r.c.z);
+        if (col < 0) {
+            row -= 1u;
+            col += (int32_t)r.c.z;
+        } else if ((uint32_t)col >= r.c.z) {
+            row += 1u;
+            col -= (int32_t)r.c.z;
+        }
+        const uint32_t tx = r.c.x + (uint32_t)col, ty = r.c.y + row;
+        const bool pass = valid && will_contribute(tx, ty, v2(r.a.x, r.a.y), S2{r.a.z, r.a.w, r.b.x}, r.b.y);
+        const uint64_t pmask = __ballot(pass);
+        // the last lane of each splat's run in this step adds the run's hits
+        const uint32_t run_lo = r.c.w > base ? r.c.w - base : 0u;
+        const uint32_t before_run = (uint32_t)__popcll(pmask & ((1ull << run_lo) - 1ull));
+        const uint32_t through_me = lanes_below(pmask) + (pass ? 1u : 0u);
+        const bool last_of_run = valid && (lane == 63u || item + 1u == __float_as_uint(r.b.w));
+        if (last_of_run) hits[owner & 63u] += through_me - before_run;
+        if (WRITE && pass) {
+            const uint32_t pos = out_base + written + lanes_below(pmask);
+            if (pos < out_end) {
+                tile_ids[pos] = tx + ty * tile_bw;
+                ids[pos] = id_base + owner;
+            }
+        }
+        written += (uint32_t)__popcll(pmask);
+        wave_lds_fence();
+    }
+    return hits[lane];
+}
+
+}  // namespace bh

@@ -17,18 +17,24 @@
 
 #include "bh_internal.h"
 #include "bh_splat_math.h"
+#include "bh_tile_walk.h"
 
 namespace bh {
 
-struct ProjectOut {
-    uint32_t hits;
+// The cull part of project_forward_kernel (project_forward.rs:20-118): returns
+// false if the splat is culled, else its screen mean, conic, power threshold
+// and tile box.  The tile count is done by the wave-cooperative walk.
+struct Projected {
+    V2 m;
+    S2 conic;
+    float pt;
+    TileBox bb;
     float radius;
     float depth;
 };
 
-// The cull-and-count body of project_forward_kernel; returns false if culled.
 template <bool MIP>
-__device__ bool project_one(const bh_project_uniforms& u, const float* t, float raw_opac, ProjectOut& o) {
+__device__ bool project_cull(const bh_project_uniforms& u, const float* t, float raw_opac, Projected& o) {
     V3 mean_c = world_to_cam(u, v3(t[0], t[1], t[2]));
     if (!(finite3(mean_c) && mean_c.z <= 1.0e10f)) return false;
     if (mean_c.z < 0.01f) return false;
@@ -53,12 +59,10 @@ __device__ bool project_one(const bh_project_uniforms& u, const float* t, float 
     float wf = (float)u.img_w, hf = (float)u.img_h;
     bool on_screen = m.x + e.x > 0.0f && m.x - e.x < wf && m.y + e.y > 0.0f && m.y - e.y < hf;
     if (!on_screen) return false;
-    TileBox bb = tile_bbox(m, e, u.tile_bw, u.tile_bh);
-    uint32_t hits = 0;
-    for (uint32_t ty = bb.min_y; ty < bb.max_y; ty++)
-        for (uint32_t tx = bb.min_x; tx < bb.max_x; tx++)
-            if (will_contribute(tx, ty, m, conic, pt)) hits++;
-    o.hits = hits;
+    o.m = m;
+    o.conic = conic;
+    o.pt = pt;
+    o.bb = tile_bbox(m, e, u.tile_bw, u.tile_bh);
     o.radius = bh_maxf(e.x / wf, e.y / hf);
     o.depth = mean_c.z;
     return true;
@@ -90,32 +94,40 @@ __global__ __launch_bounds__(256) void project_forward_kernel(bh_project_uniform
                                                                uint32_t* __restrict__ partials) {
     __shared__ uint32_t s_vis[4], s_kmin[4], s_kmax[4];
     __shared__ unsigned long long s_hits[4];
+    __shared__ WalkRec s_rec[4][64];
+    __shared__ uint32_t s_slot[4][64], s_count[4][64];
     const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     bool vis = false;
-    ProjectOut o{0u, 0.0f, 0.0f};
+    Projected p{v2(0.0f, 0.0f), S2{0.0f, 0.0f, 0.0f}, 0.0f, TileBox{0u, 0u, 0u, 0u}, 0.0f, 0.0f};
     if (gid < n) {
         const float2* row = reinterpret_cast<const float2*>(transforms + (size_t)gid * 10);
         float t[10];
 #pragma unroll
         for (int i = 0; i < 5; i++) {
-            float2 p = row[i];
-            t[2 * i] = p.x;
-            t[2 * i + 1] = p.y;
+            float2 q = row[i];
+            t[2 * i] = q.x;
+            t[2 * i + 1] = q.y;
         }
-        vis = project_one<MIP>(u, t, raw_opac[gid], o);
-        counts[gid] = vis ? o.hits : 0u;
-        max_radius[gid] = vis ? o.radius : 0.0f;
-        depth_keys[gid] = vis ? bh_as_uint(o.depth) : 0xFFFFFFFFu;
+        vis = project_cull<MIP>(u, t, raw_opac[gid], p);
+    }
+    // count_contributing_tiles (project_forward.rs:120-128) for the whole wave
+    const uint32_t hits = wave_tile_walk<false>(lane, vis ? bbox_items(p.bb) : 0u, p.m, p.conic, p.pt, p.bb,
+                                                s_rec[wave], s_slot[wave], s_count[wave], u.tile_bw, 0u, 0u, 0u,
+                                                nullptr, nullptr);
+    if (gid < n) {
+        counts[gid] = vis ? hits : 0u;
+        max_radius[gid] = vis ? p.radius : 0.0f;
+        depth_keys[gid] = vis ? bh_as_uint(p.depth) : 0xFFFFFFFFu;
     }
     // per-block totals (no same-address atomics): wave shuffles, then LDS
-    const uint32_t wave = threadIdx.x >> 6;
     uint64_t vmask = __ballot(vis);
-    uint64_t hits = wave_sum_u64(vis ? (uint64_t)o.hits : 0ull);
-    uint32_t kmin = wave_min_u32(vis ? bh_as_uint(o.depth) : 0xFFFFFFFFu);
-    uint32_t kmax = wave_max_u32(vis ? bh_as_uint(o.depth) : 0u);
-    if ((threadIdx.x & 63) == 0) {
+    uint64_t hsum = wave_sum_u64(vis ? (uint64_t)hits : 0ull);
+    uint32_t kmin = wave_min_u32(vis ? bh_as_uint(p.depth) : 0xFFFFFFFFu);
+    uint32_t kmax = wave_max_u32(vis ? bh_as_uint(p.depth) : 0u);
+    if (lane == 0) {
         s_vis[wave] = (uint32_t)__popcll(vmask);
-        s_hits[wave] = hits;
+        s_hits[wave] = hsum;
         s_kmin[wave] = kmin;
         s_kmax[wave] = kmax;
     }
@@ -312,28 +324,52 @@ __global__ __launch_bounds__(256) void map_intersects_kernel(uint32_t tile_bw, u
                                                               const uint32_t* __restrict__ cum, uint32_t num_visible,
                                                               uint32_t* __restrict__ tile_ids,
                                                               uint32_t* __restrict__ cgids) {
+    __shared__ WalkRec s_rec[4][64];
+    __shared__ uint32_t s_slot[4][64], s_count[4][64];
     const uint32_t c = blockIdx.x * 256u + threadIdx.x;
-    if (c >= num_visible) return;
-    const float2* row = reinterpret_cast<const float2*>(projected + (size_t)c * 10);
-    float2 p0 = row[0], p1 = row[1], p2 = row[2];
-    V2 m = v2(p0.x, p0.y);
-    S2 conic{p1.x, p1.y, p2.x};
-    float opac = p2.y;
-    float pt = bh_logf(opac * 255.0f);
-    V2 e = bbox_extent(conic, pt);
-    TileBox bb = tile_bbox(m, e, tile_bw, tile_bh);
-    uint32_t base = c == 0 ? 0u : cum[c - 1];
-    uint32_t budget = cum[c] - base;
-    uint32_t hits = 0;
-    for (uint32_t ty = bb.min_y; ty < bb.max_y && hits < budget; ty++)
-        for (uint32_t tx = bb.min_x; tx < bb.max_x && hits < budget; tx++)
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t c0 = c - lane;  // first compact id of this wave
+    if (c0 >= num_visible) return;  // the whole wave is past the end
+    const bool active = c < num_visible;
+    V2 m = v2(0.0f, 0.0f);
+    S2 conic{0.0f, 0.0f, 0.0f};
+    float pt = 0.0f;
+    TileBox bb{0u, 0u, 0u, 0u};
+    uint32_t base = 0, budget = 0;
+    if (active) {
+        const float2* row = reinterpret_cast<const float2*>(projected + (size_t)c * 10);
+        float2 p0 = row[0], p1 = row[1], p2 = row[2];
+        m = v2(p0.x, p0.y);
+        conic = S2{p1.x, p1.y, p2.x};
+        pt = bh_logf(p2.y * 255.0f);
+        bb = tile_bbox(m, bbox_extent(conic, pt), tile_bw, tile_bh);
+        base = c == 0 ? 0u : cum[c - 1];
+        budget = cum[c] - base;
+    }
+    // The wave's splats own the contiguous output range [cum[c0 - 1], cum[last]);
+    // the walk emits their tiles in that order.
+    const uint32_t last = min(c0 + 63u, num_visible - 1u);
+    const uint32_t out_base = c0 == 0 ? 0u : cum[c0 - 1];
+    const uint32_t out_end = cum[last];
+    const uint32_t hits = wave_tile_walk<true>(lane, active ? bbox_items(bb) : 0u, m, conic, pt, bb, s_rec[wave],
+                                               s_slot[wave], s_count[wave], tile_bw, out_base, out_end, c0, tile_ids,
+                                               cgids);
+    if (__ballot(active && hits != budget) == 0ull) return;
+    // A recount that disagrees with the forward counts (it cannot for identical
+    // rows) falls back to the reference's per-splat loop, which clamps to the
+    // budget and pads with the sentinel tile (map_gaussians.rs:56-91), and
+    // rewrites the wave's whole output range.
+    __threadfence();
+    if (!active) return;
+    uint32_t k = 0;
+    for (uint32_t ty = bb.min_y; ty < bb.max_y && k < budget; ty++)
+        for (uint32_t tx = bb.min_x; tx < bb.max_x && k < budget; tx++)
             if (will_contribute(tx, ty, m, conic, pt)) {
-                tile_ids[base + hits] = tx + ty * tile_bw;
-                cgids[base + hits] = c;
-                hits++;
+                tile_ids[base + k] = tx + ty * tile_bw;
+                cgids[base + k] = c;
+                k++;
             }
-    // sentinel padding of an unused budget (map_gaussians.rs:171-180)
-    for (uint32_t k = hits; k < budget; k++) {
+    for (; k < budget; k++) {
         tile_ids[base + k] = tile_bw * tile_bh;
         cgids[base + k] = c;
     }
