@@ -1,17 +1,20 @@
 // backward.hip — rasterize backward and project backward for gfx950.
 //
-// rasterize_backward: one 256-thread workgroup per 16x16 tile, one pixel per
-// lane (each wave64 owns a 16x4 strip).  Every pixel replays the tile's
-// splats front to back with the same per-pair arithmetic as the reference's
-// replay (crates/brush-render-bwd/src/kernels/rasterize_backwards.rs:79-443,
-// where instead a 32-lane workgroup owns 32 splats and walks the pixels on a
+// rasterize_backward: one single-wave workgroup per 8x8 pixel block of a
+// 16x16 tile, one pixel per lane.  Every pixel replays the tile's splats front
+// to back with the same per-pair arithmetic as the reference's replay
+// (crates/brush-render-bwd/src/kernels/rasterize_backwards.rs:79-443, where
+// instead a 32-lane workgroup owns 32 splats and walks the pixels on a
 // diagonal); the transmittance / remaining-colour state never leaves the
-// lane's registers.  Splats are staged in LDS in batches of 64.  For each
-// splat a wave that had any contributing pixel sums the 9-11 gradient lanes
-// over each 16-pixel row with DPP adds; the 16 row partials are added in LDS
-// in row order and each (splat, tile) pair costs one hardware float atomic
-// per gradient lane.  A wave whose 64 pixels have
-// all saturated stops evaluating splats.
+// lane's registers.  Each wave stages the tile's splats in LDS in batches of
+// 64 and keeps those that may touch its block (a ballot of a conservative
+// rectangle test), so the four blocks of a tile run independently, without
+// workgroup barriers, and a block whose 64 pixels have all saturated stops.
+// For a splat with any contributing pixel the wave sums its 9-11 gradient
+// lanes over all 64 pixels with a transposed reduction (permlane32 and
+// permlane16 swaps fold four lanes into one register, then four DPP row
+// steps), which leaves up to four different gradient lanes in lanes 15, 31,
+// 47 and 63, so one float-atomic instruction adds four of them.
 //
 // project_backward: one thread per *global* id, so every dense output row is
 // written exactly once (zeros for culled splats or splats without gradient)
@@ -22,6 +25,7 @@
 
 #include "bh_internal.h"
 #include "bh_splat_math.h"
+#include "bh_tile_walk.h"
 
 namespace bh {
 
@@ -39,29 +43,49 @@ __device__ __forceinline__ float row_sum_last_lane(float x) {
     return x;
 }
 
-constexpr uint32_t kBwdBatch = 32;
+// Transposed wave reduction.  psum32(a, b): rows 0-1 (lanes 0-31) hold a
+// summed over lanes i and i + 32, rows 2-3 hold b likewise.  psum16(p, q) of
+// two such values: row 0 holds p's rows 0+1, row 1 q's rows 0+1, row 2 p's
+// rows 2+3 and row 3 q's rows 2+3.  Two levels fold four values into one
+// register with one swap and one add per pair.
+__device__ __forceinline__ float psum32(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float psum16(float p, float q) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(p), __float_as_uint(q), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 constexpr int kNG = 11;
-constexpr int kRows = 16;  // 16-pixel rows per tile = partial sums per splat
+
+// One workgroup (a single wave) per 8x8 pixel block of a 16x16 tile.  The
+// dispatcher deals workgroups to the eight XCDs in turn, so the four blocks of
+// a tile are given ids that agree modulo 8 and share an L2.
+__device__ __forceinline__ void block_of_workgroup(uint32_t g, uint32_t& tile, uint32_t& blk) {
+    const uint32_t slot = g >> 3;
+    tile = ((slot >> 2) << 3) | (g & 7u);
+    blk = slot & 3u;
+}
 
 template <bool SMOOTH, bool REFINE, bool DEPTH>
-__global__ __launch_bounds__(256) void rasterize_backward_kernel(
-    uint32_t img_w, uint32_t img_h, uint32_t tile_bw, float bg_r, float bg_g, float bg_b, uint32_t num_visible,
-    const float* __restrict__ out_img, const float* __restrict__ projected, const uint32_t* __restrict__ cgids,
-    const uint32_t* __restrict__ offsets, const float* __restrict__ v_output, float* __restrict__ v_combined) {
+__global__ __launch_bounds__(64) void rasterize_backward_kernel(
+    uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t num_tiles, float bg_r, float bg_g, float bg_b,
+    uint32_t num_visible, const float* __restrict__ out_img, const float* __restrict__ projected,
+    const uint32_t* __restrict__ cgids, const uint32_t* __restrict__ offsets, const float* __restrict__ v_output,
+    float* __restrict__ v_combined) {
     constexpr uint32_t CH = DEPTH ? 5u : 4u;
-    constexpr int NG = kNG;
-    __shared__ float4 s_xyco[kBwdBatch];  // x, y, conic c00, c01
-    __shared__ float4 s_crgb[kBwdBatch];  // conic c11, opacity, r, g
-    __shared__ float4 s_bd[kBwdBatch];    // b, depth, sigma cutoff
-    __shared__ uint32_t s_cid[kBwdBatch];
-    __shared__ uint32_t s_strips[kBwdBatch];  // strips of the tile each splat may touch
-    // per (pixel row, splat): partial gradient; lane NG flags a contribution
-    __shared__ float s_grad[kRows][kBwdBatch][NG + 1];
+    __shared__ float4 s_xyco[64];  // x, y, conic c00, c01
+    __shared__ float4 s_crgb[64];  // conic c11, opacity, r, g
+    __shared__ float4 s_bd[64];    // b, depth, sigma cutoff
+    __shared__ uint32_t s_cid[64];
 
-    const uint32_t tile = blockIdx.x;
-    const uint32_t ox = (tile % tile_bw) * 16u, oy = (tile / tile_bw) * 16u;
-    const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6, row = t >> 4;
-    const uint32_t px = ox + (t & 15u), py = oy + (t >> 4);
+    uint32_t tile, blk;
+    block_of_workgroup(blockIdx.x, tile, blk);
+    if (tile >= num_tiles) return;
+    const uint32_t lane = threadIdx.x;
+    const uint32_t ox = (tile % tile_bw) * 16u + (blk & 1u) * 8u, oy = (tile / tile_bw) * 16u + (blk >> 1) * 8u;
+    const uint32_t px = ox + (lane & 7u), py = oy + (lane >> 3);
     const bool inside = px < img_w && py < img_h;
     const float pcx = (float)px + 0.5f, pcy = (float)py + 0.5f;
 
@@ -91,26 +115,27 @@ __global__ __launch_bounds__(256) void rasterize_backward_kernel(
     const uint32_t lo = offsets[2 * tile], hi = offsets[2 * tile + 1];
     const float img_wf = (float)img_w, img_hf = (float)img_h;
     const float inv_final_a = __builtin_amdgcn_rcpf(bh_maxf(final_a, 1.0e-5f));
+    const float bx0 = (float)ox + 0.5f, by0 = (float)oy + 0.5f;
     bool wave_live = __ballot(sw > 1.0e-4f) != 0ull;
 
-    for (uint32_t b = lo; b < hi; b += kBwdBatch) {
-        const uint32_t cnt = min(kBwdBatch, hi - b);
-        if (t < cnt) {
-            const uint32_t c = min(cgids[b + t], num_visible - 1u);
+    for (uint32_t b = lo; wave_live && b < hi; b += 64u) {
+        const uint32_t cnt = min(64u, hi - b);
+        bool touch = false;
+        if (lane < cnt) {
+            const uint32_t c = min(cgids[b + lane], num_visible - 1u);
             const float2* prow = reinterpret_cast<const float2*>(projected + (size_t)c * 10);
             const float2 r0 = prow[0], r1 = prow[1], r2 = prow[2], r3 = prow[3], r4 = prow[4];
             const float cut = sigma_cutoff<SMOOTH>(r2.y);
-            s_xyco[t] = make_float4(r0.x, r0.y, r1.x, r1.y);
-            s_crgb[t] = make_float4(r2.x, r2.y, r3.x, r3.y);
-            s_bd[t] = make_float4(r4.x, r4.y, cut, 0.0f);
-            s_cid[t] = c;
-            s_strips[t] = strip_mask(r0.x, r0.y, S2{r1.x, r1.y, r2.x}, cut, ox, oy);
+            s_xyco[lane] = make_float4(r0.x, r0.y, r1.x, r1.y);
+            s_crgb[lane] = make_float4(r2.x, r2.y, r3.x, r3.y);
+            s_bd[lane] = make_float4(r4.x, r4.y, cut, 0.0f);
+            s_cid[lane] = c;
+            touch = may_touch_rect(r0.x, r0.y, S2{r1.x, r1.y, r2.x}, cut, bx0, by0, bx0 + 7.0f, by0 + 7.0f);
         }
-        for (uint32_t e = t; e < (uint32_t)kRows * kBwdBatch; e += 256u) (&s_grad[0][0][0])[e * (NG + 1) + NG] = 0.0f;
-        __syncthreads();
-        // splats of the batch that may touch this wave's strip, in order
-        uint64_t todo = __ballot(lane < cnt && ((s_strips[lane] >> wave) & 1u));
-        while (wave_live && todo) {
+        // splats of the batch that may touch this block, in order
+        uint64_t todo = __ballot(touch);
+        wave_lds_fence();
+        while (todo) {
             const uint32_t j = (uint32_t)__builtin_ctzll(todo);
             todo &= todo - 1ull;
             const float4 xc = s_xyco[j];
@@ -134,11 +159,12 @@ __global__ __launch_bounds__(256) void rasterize_backward_kernel(
             if (saturate) sw = 0.0f;
             if (__ballot(contrib) == 0ull) {
                 wave_live = __ballot(sw > 1.0e-4f) != 0ull;
+                if (!wave_live) break;
                 continue;
             }
             const float cr = bh_maxf(cr4.z, 0.0f), cgc = bh_maxf(cr4.w, 0.0f), cb = bh_maxf(bd.x, 0.0f);
             const float vis = ae * sw;
-            float g[NG];
+            float g[12];
             g[5] = cr4.z >= 0.0f ? vis * vox : 0.0f;
             g[6] = cr4.w >= 0.0f ? vis * voy : 0.0f;
             g[7] = bd.x >= 0.0f ? vis * voz : 0.0f;
@@ -162,8 +188,9 @@ __global__ __launch_bounds__(256) void rasterize_backward_kernel(
                                 inv_final_a
                           : 0.0f;
             g[10] = DEPTH ? vis * vod : 0.0f;
+            g[11] = 0.0f;
 #pragma unroll
-            for (int k = 0; k < NG; k++) {
+            for (int k = 0; k < kNG; k++) {
                 const bool keep = contrib && (k >= 5 ? (k != 9 || unclamped) : unclamped) && (k != 8 || unclamped);
                 g[k] = keep ? g[k] : 0.0f;
             }
@@ -174,38 +201,25 @@ __global__ __launch_bounds__(256) void rasterize_backward_kernel(
                 if (DEPTH) sd = sd - vis * bd.y;
                 sw = next_t;
             }
-#pragma unroll
-            for (int k = 0; k < NG; k++) {
-                if ((k == 9 && !REFINE) || (k == 10 && !DEPTH)) continue;
-                g[k] = row_sum_last_lane(g[k]);
-            }
-            if ((t & 15u) == 15u) {
-                float* dst = &s_grad[row][j][0];
-#pragma unroll
-                for (int k = 0; k < NG; k++) dst[k] = g[k];
-                dst[NG] = 1.0f;
+            // whole-wave sums: rows of q0 hold lanes 0, 2, 1, 3; of q1 lanes 4, 6,
+            // 5, 7; of q2 lanes 8, 10, 9, 11 (8, 8, 9, 9 without depth)
+            const float q0 = row_sum_last_lane(psum16(psum32(g[0], g[1]), psum32(g[2], g[3])));
+            const float q1 = row_sum_last_lane(psum16(psum32(g[4], g[5]), psum32(g[6], g[7])));
+            const float p4 = psum32(g[8], g[9]);
+            const float q2 = row_sum_last_lane(DEPTH ? psum16(p4, psum32(g[10], g[11])) : psum16(p4, p4));
+            if ((lane & 15u) == 15u) {
+                const uint32_t row = lane >> 4;
+                const uint32_t k = (row & 1u) * 2u + (row >> 1);
+                float* dst = v_combined + (size_t)s_cid[j] * kNG;
+                unsafeAtomicAdd(dst + k, q0);
+                unsafeAtomicAdd(dst + 4u + k, q1);
+                const bool want = DEPTH ? (k == 0u || (k == 1u && REFINE) || k == 2u) : (k == 0u || (row == 2u && REFINE));
+                if (want) unsafeAtomicAdd(dst + (DEPTH ? 8u + k : 8u + (row >> 1)), q2);
             }
             wave_live = __ballot(sw > 1.0e-4f) != 0ull;
+            if (!wave_live) break;
         }
-        __syncthreads();
-        // per splat: the 16 row partials, added in row order
-        for (uint32_t e = t; e < (uint32_t)NG * kBwdBatch; e += 256u) {
-            const uint32_t k = e / kBwdBatch, j = e % kBwdBatch;
-            const bool used = k < 9u || (REFINE && k == 9u) || (DEPTH && k == 10u);
-            if (used && j < cnt) {
-                float sum = 0.0f;
-                bool any = false;
-#pragma unroll
-                for (int r = 0; r < kRows; r++) {
-                    if (s_grad[r][j][NG] != 0.0f) {
-                        sum = any ? sum + s_grad[r][j][k] : s_grad[r][j][k];
-                        any = true;
-                    }
-                }
-                if (any) unsafeAtomicAdd(v_combined + (size_t)s_cid[j] * NG + k, sum);
-            }
-        }
-        __syncthreads();
+        wave_lds_fence();
     }
 }
 
@@ -217,12 +231,13 @@ void launch_rasterize_backward(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint
     const bool smooth = (flags & BH_FLAG_SMOOTH_CUTOFF) != 0;
     const bool refine = (flags & BH_FLAG_REFINE_WEIGHT) != 0;
     const bool depth = (flags & BH_FLAG_RENDER_DEPTH) != 0;
+    const uint32_t groups = div_up(num_tiles, 8) * 32u;
     KernelTimer t(ctx, "rasterize_backward");
-#define BH_RB(S, R, D)                                                                                          \
-    rasterize_backward_kernel<S, R, D><<<num_tiles, 256, 0, ctx->stream>>>(img_w, img_h, tile_bw, bg[0], bg[1], \
-                                                                          bg[2], num_visible, out_img,          \
-                                                                          projected, cgids, offsets, v_output,  \
-                                                                          v_combined)
+#define BH_RB(S, R, D)                                                                                            \
+    rasterize_backward_kernel<S, R, D><<<groups, 64, 0, ctx->stream>>>(img_w, img_h, tile_bw, num_tiles, bg[0], \
+                                                                       bg[1], bg[2], num_visible, out_img,       \
+                                                                       projected, cgids, offsets, v_output,      \
+                                                                       v_combined)
     if (smooth) {
         if (refine) {
             if (depth) BH_RB(true, true, true); else BH_RB(true, true, false);

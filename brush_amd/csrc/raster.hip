@@ -2,18 +2,22 @@
 //
 //   tile_offsets  [start, end) of each tile's run in the tile-sorted list
 //                 (crates/brush-render/src/get_tile_offset.rs:10-62)
-//   rasterize     one 256-thread workgroup (four wave64s) per 16x16 tile, one
-//                 pixel per lane, splat batches of 256 staged in LDS, the
-//                 whole-tile early exit decided by a workgroup vote
+//   rasterize     one single-wave workgroup per 8x8 pixel block of a 16x16
+//                 tile, one pixel per lane; each wave stages the tile's splats
+//                 in LDS in batches of 64, keeps those that may touch its block
+//                 (ballot of a conservative rectangle test) and stops when its
+//                 64 pixels have saturated
 //                 (crates/brush-render/src/kernels/rasterize.rs:24-200).
 //
 // With BWD_INFO the kernel also marks contributing splats visible — once per
-// (splat, tile) batch through an LDS flag instead of once per pixel — and
-// shrinks each tile's end to one past the last splat any pixel consumed.
+// (splat, block) through a ballot instead of once per pixel — and shrinks each
+// tile's end to one past the last splat any pixel consumed (an atomic max over
+// the tile's four blocks).
 #include <hip/hip_runtime.h>
 
 #include "bh_internal.h"
 #include "bh_splat_math.h"
+#include "bh_tile_walk.h"
 
 namespace bh {
 
@@ -42,91 +46,97 @@ void launch_tile_offsets(bh_ctx* ctx, const uint32_t* tile_ids, uint32_t m, uint
     tile_offsets_kernel<<<div_up(m, 256), 256, 0, ctx->stream>>>(tile_ids, m, num_tiles, offsets);
 }
 
-template <bool BWD_INFO, bool SMOOTH, bool DEPTH>
-__global__ __launch_bounds__(256) void rasterize_kernel(uint32_t img_w, uint32_t img_h, uint32_t tile_bw, float bg_r,
-                                                         float bg_g, float bg_b, uint32_t num_visible,
-                                                         const float* __restrict__ projected,
-                                                         const uint32_t* __restrict__ cgids,
-                                                         const uint32_t* __restrict__ gfc,
-                                                         const uint32_t* __restrict__ off_pre,
-                                                         void* __restrict__ out_img, float* __restrict__ visible,
-                                                         uint32_t* __restrict__ off_post) {
-    __shared__ float4 s_xyco[256];  // x, y, conic c00, conic c01
-    __shared__ float4 s_c11a[256];  // conic c11, opacity, sigma cutoff
-    __shared__ float4 s_rgbd[256];  // r, g, b, depth
-    __shared__ uint32_t s_gid[BWD_INFO ? 256 : 1];
-    __shared__ uint32_t s_contrib[BWD_INFO ? 256 : 1];
-    __shared__ uint32_t s_strips[256];  // strips of the tile each splat may touch
-    __shared__ uint32_t s_max_useful;
+// One workgroup (a single wave) per 8x8 pixel block of a 16x16 tile; the four
+// blocks of a tile get workgroup ids that agree modulo 8, which the dispatcher
+// places on one XCD (shared L2 for the tile's splat rows).
+__device__ __forceinline__ void raster_block_of_workgroup(uint32_t g, uint32_t& tile, uint32_t& blk) {
+    const uint32_t slot = g >> 3;
+    tile = ((slot >> 2) << 3) | (g & 7u);
+    blk = slot & 3u;
+}
 
-    const uint32_t tile = blockIdx.x;
-    const uint32_t tx = tile % tile_bw, ty = tile / tile_bw;
-    const uint32_t t = threadIdx.x;
-    const uint32_t px = tx * 16u + (t & 15u), py = ty * 16u + (t >> 4);
+template <bool BWD_INFO, bool SMOOTH, bool DEPTH>
+__global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t img_h, uint32_t tile_bw,
+                                                        uint32_t num_tiles, float bg_r, float bg_g, float bg_b,
+                                                        uint32_t num_visible, const float* __restrict__ projected,
+                                                        const uint32_t* __restrict__ cgids,
+                                                        const uint32_t* __restrict__ gfc,
+                                                        const uint32_t* __restrict__ off_pre,
+                                                        void* __restrict__ out_img, float* __restrict__ visible,
+                                                        uint32_t* __restrict__ off_post) {
+    __shared__ float4 s_xyco[64];  // x, y, conic c00, conic c01
+    __shared__ float4 s_c11a[64];  // conic c11, opacity, sigma cutoff
+    __shared__ float4 s_rgbd[64];  // r, g, b, depth
+
+    uint32_t tile, blk;
+    raster_block_of_workgroup(blockIdx.x, tile, blk);
+    if (tile >= num_tiles) return;
+    const uint32_t lane = threadIdx.x;
+    const uint32_t ox = (tile % tile_bw) * 16u + (blk & 1u) * 8u, oy = (tile / tile_bw) * 16u + (blk >> 1) * 8u;
+    const uint32_t px = ox + (lane & 7u), py = oy + (lane >> 3);
     const bool inside = px < img_w && py < img_h;
     const uint32_t lo = off_pre[2 * tile], hi = off_pre[2 * tile + 1];
-    if (t == 0) s_max_useful = lo;
-    __syncthreads();
-
     const float pcx = (float)px + 0.5f, pcy = (float)py + 0.5f;
+    const float bx0 = (float)ox + 0.5f, by0 = (float)oy + 0.5f;
     float t_acc = 1.0f, pr = 0.0f, pg = 0.0f, pb = 0.0f, pd = 0.0f;
     bool done = !inside;
     uint32_t last = lo;
 
-    for (uint32_t batch = lo; batch < hi; batch += 256u) {
-        if (__syncthreads_count(done) == 256) break;
-        const uint32_t cnt = min(256u, hi - batch);
-        if (t < cnt) {
-            const uint32_t c = min(cgids[batch + t], num_visible - 1u);
-            const float2* row = reinterpret_cast<const float2*>(projected + (size_t)c * 10);
-            float2 a = row[0], b = row[1], cc = row[2], d = row[3], e = row[4];
+    for (uint32_t batch = lo; batch < hi; batch += 64u) {
+        if (__ballot(!done) == 0ull) break;
+        const uint32_t cnt = min(64u, hi - batch);
+        bool touch = false;
+        uint32_t my_c = 0;
+        if (lane < cnt) {
+            my_c = min(cgids[batch + lane], num_visible - 1u);
+            const float2* row = reinterpret_cast<const float2*>(projected + (size_t)my_c * 10);
+            const float2 a = row[0], b = row[1], cc = row[2], d = row[3], e = row[4];
             const float cut = sigma_cutoff<SMOOTH>(cc.y);
-            s_xyco[t] = make_float4(a.x, a.y, b.x, b.y);
-            s_c11a[t] = make_float4(cc.x, cc.y, cut, 0.0f);
-            s_strips[t] = strip_mask(a.x, a.y, S2{b.x, b.y, cc.x}, cut, tx * 16u, ty * 16u);
-            s_rgbd[t] = make_float4(d.x, d.y, e.x, e.y);
-            if (BWD_INFO) {
-                s_gid[t] = gfc[c];
-                s_contrib[t] = 0u;
-            }
+            s_xyco[lane] = make_float4(a.x, a.y, b.x, b.y);
+            s_c11a[lane] = make_float4(cc.x, cc.y, cut, 0.0f);
+            s_rgbd[lane] = make_float4(d.x, d.y, e.x, e.y);
+            touch = may_touch_rect(a.x, a.y, S2{b.x, b.y, cc.x}, cut, bx0, by0, bx0 + 7.0f, by0 + 7.0f);
         }
-        __syncthreads();
-        const uint32_t wave = t >> 6, lane = t & 63u;
-        for (uint32_t q = 0; q < cnt; q += 64u) {
-            // splats of this 64-chunk that may touch this wave's strip, in order
-            uint64_t todo = __ballot(q + lane < cnt && ((s_strips[q + lane] >> wave) & 1u));
-            if (__ballot(!done) == 0ull) todo = 0ull;
-            while (todo && !done) {
-                const uint32_t j = q + (uint32_t)__builtin_ctzll(todo);
-                todo &= todo - 1ull;
+        // splats of the batch that may touch this block, in order
+        uint64_t todo = __ballot(touch);
+        uint64_t used = 0ull;  // splats some pixel of the block blended
+        wave_lds_fence();
+        while (todo) {
+            const uint32_t j = (uint32_t)__builtin_ctzll(todo);
+            todo &= todo - 1ull;
+            bool contrib = false;
+            if (!done) {
                 const float4 xc = s_xyco[j];
                 const float4 ca = s_c11a[j];
                 const S2 conic{xc.z, xc.w, ca.x};
                 const float sigma = calc_sigma(pcx, pcy, conic, xc.x, xc.y);
-                if (!(sigma >= 0.0f) || sigma > ca.z) continue;  // cannot contribute
-                const float alpha = bh_minf(0.999f, ca.y * bh_expf(-sigma));
-                const float w = SMOOTH ? cutoff_weight(alpha) : (alpha >= kCutMid ? 1.0f : 0.0f);
-                if (sigma >= 0.0f && w > 0.0f) {
-                    const float ae = alpha * w;
-                    const float next_t = t_acc * (1.0f - ae);
-                    if (next_t <= 1.0e-4f) {
-                        done = true;
-                        break;
+                if (sigma >= 0.0f && !(sigma > ca.z)) {
+                    const float alpha = bh_minf(0.999f, ca.y * bh_expf(-sigma));
+                    const float w = SMOOTH ? cutoff_weight(alpha) : (alpha >= kCutMid ? 1.0f : 0.0f);
+                    if (w > 0.0f) {
+                        const float ae = alpha * w;
+                        const float next_t = t_acc * (1.0f - ae);
+                        if (next_t <= 1.0e-4f) {
+                            done = true;
+                        } else {
+                            contrib = true;
+                            const float vis = ae * t_acc;
+                            const float4 col = s_rgbd[j];
+                            pr += bh_maxf(col.x, 0.0f) * vis;
+                            pg += bh_maxf(col.y, 0.0f) * vis;
+                            pb += bh_maxf(col.z, 0.0f) * vis;
+                            if (DEPTH) pd += col.w * vis;
+                            t_acc = next_t;
+                            last = batch + j + 1u;
+                        }
                     }
-                    if (BWD_INFO) s_contrib[j] = 1u;
-                    const float vis = ae * t_acc;
-                    const float4 col = s_rgbd[j];
-                    pr += bh_maxf(col.x, 0.0f) * vis;
-                    pg += bh_maxf(col.y, 0.0f) * vis;
-                    pb += bh_maxf(col.z, 0.0f) * vis;
-                    if (DEPTH) pd += col.w * vis;
-                    t_acc = next_t;
-                    last = batch + j + 1u;
                 }
             }
+            if (BWD_INFO && __ballot(contrib) != 0ull) used |= 1ull << j;
+            if (__ballot(!done) == 0ull) break;
         }
-        __syncthreads();
-        if (BWD_INFO && t < cnt && s_contrib[t]) visible[s_gid[t]] = 1.0f;
+        if (BWD_INFO && ((used >> lane) & 1ull)) visible[gfc[my_c]] = 1.0f;
+        wave_lds_fence();
     }
 
     if (inside) {
@@ -152,11 +162,18 @@ __global__ __launch_bounds__(256) void rasterize_kernel(uint32_t img_w, uint32_t
             reinterpret_cast<uint32_t*>(out_img)[pix] = ur | (ug << 8) | (ub << 16) | (ua << 24);
         }
     }
-    if (BWD_INFO) atomicMax(&s_max_useful, last);
-    __syncthreads();
-    if (t == 0) {
+    // post-raster tile end: one past the last splat any pixel of the tile
+    // blended (the caller zero-filled off_post; every block of the tile adds
+    // its own maximum)
+    if (BWD_INFO) {
+        uint32_t m = last;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, o, 64));
+        if (lane == 0) atomicMax(&off_post[2 * tile + 1], m);
+    }
+    if (lane == 0 && blk == 0) {
         off_post[2 * tile] = lo;
-        off_post[2 * tile + 1] = BWD_INFO ? s_max_useful : hi;
+        if (!BWD_INFO) off_post[2 * tile + 1] = hi;
     }
 }
 
@@ -169,11 +186,13 @@ void launch_rasterize(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile
     const bool smooth = (flags & BH_FLAG_SMOOTH_CUTOFF) != 0;
     const bool depth = bwd && (flags & BH_FLAG_RENDER_DEPTH) != 0;
     const uint32_t nv = num_visible > 0 ? num_visible : 1u;
+    if (bwd) launch_fill_u32(ctx, off_post, 0u, (uint64_t)num_tiles * 2);
+    const uint32_t groups = div_up(num_tiles, 8) * 32u;
     KernelTimer t(ctx, "rasterize");
-#define BH_RASTER(B, S, D)                                                                                      \
-    rasterize_kernel<B, S, D><<<num_tiles, 256, 0, ctx->stream>>>(img_w, img_h, tile_bw, bg[0], bg[1], bg[2], \
-                                                                  nv, projected, cgids, gfc, off_pre, out_img, \
-                                                                  visible, off_post)
+#define BH_RASTER(B, S, D)                                                                                         \
+    rasterize_kernel<B, S, D><<<groups, 64, 0, ctx->stream>>>(img_w, img_h, tile_bw, num_tiles, bg[0], bg[1],    \
+                                                              bg[2], nv, projected, cgids, gfc, off_pre, out_img, \
+                                                              visible, off_post)
     if (!bwd) {
         if (smooth) BH_RASTER(false, true, false); else BH_RASTER(false, false, false);
     } else if (depth) {
