@@ -104,35 +104,34 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
         while (todo) {
             const uint32_t j = (uint32_t)__builtin_ctzll(todo);
             todo &= todo - 1ull;
-            bool contrib = false;
-            if (!done) {
-                const float4 xc = s_xyco[j];
-                const float4 ca = s_c11a[j];
-                const S2 conic{xc.z, xc.w, ca.x};
-                const float sigma = calc_sigma(pcx, pcy, conic, xc.x, xc.y);
-                if (sigma >= 0.0f && !(sigma > ca.z)) {
-                    const float alpha = bh_minf(0.999f, ca.y * bh_expf(-sigma));
-                    const float w = SMOOTH ? cutoff_weight(alpha) : (alpha >= kCutMid ? 1.0f : 0.0f);
-                    if (w > 0.0f) {
-                        const float ae = alpha * w;
-                        const float next_t = t_acc * (1.0f - ae);
-                        if (next_t <= 1.0e-4f) {
-                            done = true;
-                        } else {
-                            contrib = true;
-                            const float vis = ae * t_acc;
-                            const float4 col = s_rgbd[j];
-                            pr += bh_maxf(col.x, 0.0f) * vis;
-                            pg += bh_maxf(col.y, 0.0f) * vis;
-                            pb += bh_maxf(col.z, 0.0f) * vis;
-                            if (DEPTH) pd += col.w * vis;
-                            t_acc = next_t;
-                            last = batch + j + 1u;
-                        }
-                    }
-                }
+            const float4 xc = s_xyco[j];
+            const float4 ca = s_c11a[j];
+            const S2 conic{xc.z, xc.w, ca.x};
+            const float sigma = calc_sigma(pcx, pcy, conic, xc.x, xc.y);
+            const bool maybe = !done && sigma >= 0.0f && !(sigma > ca.z);
+            if (__ballot(maybe) == 0ull) continue;
+            // Branch-free from here: lanes outside `maybe` compute values the
+            // selects discard.  0 <= sigma <= cutoff < 6 where it matters, the
+            // range in which bh_expf_neg equals bh_expf bit for bit.
+            const float alpha = bh_minf(0.999f, ca.y * bh_expf_neg(-sigma));
+            const float w = SMOOTH ? cutoff_weight(alpha) : (alpha >= kCutMid ? 1.0f : 0.0f);
+            const bool pass = maybe && w > 0.0f;
+            const float ae = alpha * w;
+            const float next_t = t_acc * (1.0f - ae);
+            const bool saturate = pass && next_t <= 1.0e-4f;
+            const bool contrib = pass && !saturate;
+            done = done || saturate;
+            if (__ballot(contrib) != 0ull) {
+                const float vis = ae * t_acc;
+                const float4 col = s_rgbd[j];
+                pr = contrib ? pr + bh_maxf(col.x, 0.0f) * vis : pr;
+                pg = contrib ? pg + bh_maxf(col.y, 0.0f) * vis : pg;
+                pb = contrib ? pb + bh_maxf(col.z, 0.0f) * vis : pb;
+                if (DEPTH) pd = contrib ? pd + col.w * vis : pd;
+                t_acc = contrib ? next_t : t_acc;
+                last = contrib ? batch + j + 1u : last;
+                if (BWD_INFO) used |= 1ull << j;
             }
-            if (BWD_INFO && __ballot(contrib) != 0ull) used |= 1ull << j;
             if (__ballot(!done) == 0ull) break;
         }
         if (BWD_INFO && ((used >> lane) & 1ull)) visible[gfc[my_c]] = 1.0f;
