@@ -123,6 +123,8 @@ def main():
     ap.add_argument("--config", type=int, default=1)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget in seconds (0 = skip)")
     ap.add_argument("--no-timing", action="store_true", help="do not bracket kernels with HIP events")
+    ap.add_argument("--profile-steps", type=int, default=5,
+                    help="untimed steps with every kernel bracketed by events (per-kernel table)")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="before warm-up, run one plain device copy of this many MiB (the known-size reference "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
@@ -183,41 +185,61 @@ def main():
     stats.pop("out")
     del res
 
+    n, v, m = w.n, stats["num_visible"], stats["num_intersections"]
+    tiles = ((w.img_w + 15) // 16) * ((w.img_h + 15) // 16)
+    c = w.num_coeffs
+    pixels = w.img_w * w.img_h
+
+    def kernel_table(timings: dict, steps: int) -> dict:
+        table = {}
+        for name, (launches, total) in timings.items():
+            per_step_launches = launches / steps
+            avg = total / max(launches, 1)
+            if name.endswith("_onesweep") or name.endswith("_hist"):
+                b = sort_bytes_per_launch(name, per_step_launches, n, m)
+            else:
+                b = algorithmic_bytes(name, n, v, m, m_post, tiles, pixels, c, 0, 0)
+            table[name] = {"launches_per_step": round(per_step_launches, 2), "avg_ms": round(avg, 4),
+                           "ms_per_step": round(total / steps, 4),
+                           "algorithmic_mb": round(b / 1e6, 2) if b else None,
+                           "gb_s": round(b / (avg / 1000.0) / 1e9, 1) if b and avg > 0 else None}
+        return table
+
+    # Per-kernel breakdown: a short untimed pass with every launch bracketed by
+    # HIP events (events on every launch add ~0.15 ms per step, so the timed
+    # region below brackets only the dominant kernel).
+    kernels, dominant = {}, None
+    if not args.no_timing:
+        ctx.reset_timings()
+        ctx.set_timing(True)
+        for _ in range(args.profile_steps):
+            step()
+        torch.cuda.synchronize()
+        kernels = kernel_table(ctx.read_timings(), args.profile_steps)
+        ctx.set_timing(False)
+        dominant = max(kernels.items(), key=lambda kv: kv[1]["ms_per_step"])[0] if kernels else None
+
     ctx.reset_timings()
-    ctx.set_timing(not args.no_timing)
+    ctx.set_timing(dominant is not None, only=dominant)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    timings = ctx.read_timings() if not args.no_timing else {}
+    timed = kernel_table(ctx.read_timings(), args.steps) if dominant else {}
     ctx.set_timing(False)
     ms = (t1 - t0) * 1000.0 / args.steps
-    pixels = w.img_w * w.img_h
     mpix = pixels / (ms / 1000.0) / 1e6
 
-    n, v, m = w.n, stats["num_visible"], stats["num_intersections"]
-    tiles = ((w.img_w + 15) // 16) * ((w.img_h + 15) // 16)
-    c = w.num_coeffs
-    kernels = {}
-    for name, (launches, total) in timings.items():
-        per_step_launches = launches / args.steps
-        avg = total / max(launches, 1)
-        if name.endswith("_onesweep") or name.endswith("_hist"):
-            b = sort_bytes_per_launch(name, per_step_launches, n, m)
-        else:
-            b = algorithmic_bytes(name, n, v, m, m_post, tiles, pixels, c, 0, 0)
-        kernels[name] = {"launches_per_step": round(per_step_launches, 2), "avg_ms": round(avg, 4),
-                         "ms_per_step": round(total / args.steps, 4),
-                         "gb_s": round(b / (avg / 1000.0) / 1e9, 1) if b and avg > 0 else None}
-    dominant = max(kernels.items(), key=lambda kv: kv[1]["ms_per_step"])[0] if kernels else None
     roofline = None
-    if dominant:
-        kd = kernels[dominant]
+    if dominant and dominant in timed:
+        kd = timed[dominant]
         achieved = kd["gb_s"] or 0.0
         roofline = {"bound": "hbm", "kernel": dominant, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dominant, w.name)}
+                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dominant, w.name),
+                    "avg_ms": kd["avg_ms"], "algorithmic_mb": kd["algorithmic_mb"],
+                    "timed_launches": int(round(kd["launches_per_step"] * args.steps))}
 
     cpu = None
     if args.cpu_seconds > 0:

@@ -35,6 +35,7 @@ TILE_WIDTH = 16
 # Every symbol include/brush_hip.h declares (checked by the CPU test suite).
 EXPORTED = [
     "bh_ctx_create", "bh_ctx_destroy", "bh_ctx_set_stream", "bh_last_error", "bh_ctx_set_timing",
+    "bh_ctx_set_timing_filter",
     "bh_ctx_read_timings", "bh_ctx_reset_timings", "bh_ctx_workspace_bytes", "bh_radix_argsort",
     "bh_prefix_sum", "bh_get_tile_offsets", "bh_render_forward", "bh_fwd_state_info",
     "bh_fwd_state_release", "bh_rasterize_backward", "bh_project_backward", "bh_copy_to_host",
@@ -144,6 +145,7 @@ def lib() -> ctypes.CDLL:
         "bh_ctx_set_stream": (S, [P, P]),
         "bh_last_error": (ctypes.c_char_p, [P]),
         "bh_ctx_set_timing": (S, [P, I]),
+        "bh_ctx_set_timing_filter": (S, [P, ctypes.c_char_p]),
         "bh_ctx_read_timings": (S, [P, ctypes.POINTER(KernelTiming), I, ctypes.POINTER(I)]),
         "bh_ctx_reset_timings": (S, [P]),
         "bh_ctx_workspace_bytes": (U64, [P]),
@@ -194,7 +196,10 @@ class Context:
             self.check(lib().bh_ctx_set_stream(self.handle, ctypes.c_void_p(s)), "bh_ctx_set_stream")
             self._stream = s
 
-    def set_timing(self, enable: bool):
+    def set_timing(self, enable: bool, only: str | None = None):
+        """Bracket kernel launches with HIP events; ``only`` restricts this to
+        the kernel of that name."""
+        self.check(lib().bh_ctx_set_timing_filter(self.handle, (only or "").encode()), "bh_ctx_set_timing_filter")
         self.check(lib().bh_ctx_set_timing(self.handle, int(enable)), "bh_ctx_set_timing")
 
     def reset_timings(self):

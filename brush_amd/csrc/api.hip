@@ -72,6 +72,7 @@ void Pool::trim() {
 
 KernelTimer::KernelTimer(bh_ctx* c, const char* n) : ctx(c), name(n) {
     if (!ctx->timing) return;
+    if (!ctx->timing_filter.empty() && ctx->timing_filter != n) return;
     auto get = [&]() {
         hipEvent_t e = nullptr;
         if (!ctx->event_cache.empty()) {
@@ -88,7 +89,7 @@ KernelTimer::KernelTimer(bh_ctx* c, const char* n) : ctx(c), name(n) {
 }
 
 KernelTimer::~KernelTimer() {
-    if (!ctx->timing || !e0 || !e1) return;
+    if (!e0 || !e1) return;
     (void)hipEventRecord(e1, ctx->stream);
     ctx->pending.push_back(Timing{name, e0, e1});
 }
@@ -206,6 +207,12 @@ bh_status bh_ctx_set_timing(bh_ctx* ctx, int enable) {
     return BH_OK;
 }
 
+bh_status bh_ctx_set_timing_filter(bh_ctx* ctx, const char* name) {
+    if (!ctx) return BH_ERR_INVALID_ARG;
+    ctx->timing_filter = name ? name : "";
+    return BH_OK;
+}
+
 static bh_status collect_timings(bh_ctx* ctx) {
     BH_TRY(hip_check(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize"));
     for (auto& t : ctx->pending) {
@@ -277,14 +284,13 @@ bh_status bh_radix_argsort(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t*
         return hip_check(ctx, hipMemcpyAsync(vals_out, vals_in, (size_t)n * 4, hipMemcpyDeviceToDevice, ctx->stream),
                          "copy");
     }
-    const uint32_t passes = (width + 7u) / 8u;
     const uint32_t mask = width >= 32 ? 0xFFFFFFFFu : ((1u << width) - 1u);
     Scratch ws(ctx);
     uint32_t *tk, *tv, *masked = nullptr;
     void* scratch;
     BH_TRY(ws.get(&tk, n));
     BH_TRY(ws.get(&tv, n));
-    BH_TRY(ws.get((char**)&scratch, radix_sort_scratch_bytes(n, passes)));
+    BH_TRY(ws.get((char**)&scratch, radix_sort_scratch_bytes(n, width)));
     if (mask != 0xFFFFFFFFu) {
         // Sort (key & mask, index) then gather: the emitted keys must be the
         // caller's original keys, including any bits above the key width.
@@ -293,11 +299,11 @@ bh_status bh_radix_argsort(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t*
         BH_TRY(ws.get(&perm, n));
         BH_TRY(ws.get(&sk, n));
         launch_mask_u32(ctx, keys_in, mask, n, masked);
-        BH_TRY(radix_sort_pairs(ctx, masked, nullptr, n, passes, 0u, 0xFFFFFFFFu, sk, perm, tk, tv, scratch));
+        BH_TRY(radix_sort_pairs(ctx, masked, nullptr, n, width, 0u, 0xFFFFFFFFu, sk, perm, tk, tv, scratch));
         launch_gather_pairs(ctx, keys_in, vals_in, perm, n, keys_out, vals_out);
         return check_launch(ctx, "radix_argsort gather");
     }
-    return radix_sort_pairs(ctx, keys_in, vals_in, n, passes, 0u, 0xFFFFFFFFu, keys_out, vals_out, tk, tv, scratch);
+    return radix_sort_pairs(ctx, keys_in, vals_in, n, width, 0u, 0xFFFFFFFFu, keys_out, vals_out, tk, tv, scratch);
 }
 
 bh_status bh_prefix_sum(bh_ctx* ctx, const uint32_t* in, uint32_t* out, uint32_t n) {
@@ -399,14 +405,14 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
             // depth sort: key' = min(bits - kmin, kmax - kmin + 1); culled splats
             // (all-ones key) map to the cap and sort last.
             const uint32_t cap = kmax - kmin + 1u;
-            const uint32_t passes = std::max<uint32_t>(1u, (bit_length(cap) + 7u) / 8u);
+            const uint32_t key_bits = std::max<uint32_t>(1u, bit_length(cap));
             uint32_t *sk, *tk, *tv;
             char* scr;
             BH_STRY(ws.get(&sk, num_splats));
             BH_STRY(ws.get(&tk, num_splats));
             BH_STRY(ws.get(&tv, num_splats));
-            BH_STRY(ws.get(&scr, radix_sort_scratch_bytes(num_splats, passes)));
-            BH_STRY(radix_sort_pairs(ctx, depth_keys, nullptr, num_splats, passes, kmin, cap, sk, gfc, tk, tv, scr,
+            BH_STRY(ws.get(&scr, radix_sort_scratch_bytes(num_splats, key_bits)));
+            BH_STRY(radix_sort_pairs(ctx, depth_keys, nullptr, num_splats, key_bits, kmin, cap, sk, gfc, tk, tv, scr,
                                      "depth_sort"));
         }
     }
@@ -438,9 +444,8 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
         BH_STRY(check_launch(ctx, "map_intersects"));
         // tile sort over bits(num_tiles) bits (render.rs:392-395)
         const uint32_t bits = bit_length(num_tiles);
-        const uint32_t passes = std::max<uint32_t>(1u, (bits + 7u) / 8u);
-        BH_STRY(ws.get(&scr, radix_sort_scratch_bytes(m, passes)));
-        BH_STRY(radix_sort_pairs(ctx, ut, uc, m, passes, 0u, 0xFFFFFFFFu, tile_ids, cgids, tk, tv, scr, "tile_sort"));
+        BH_STRY(ws.get(&scr, radix_sort_scratch_bytes(m, bits)));
+        BH_STRY(radix_sort_pairs(ctx, ut, uc, m, bits, 0u, 0xFFFFFFFFu, tile_ids, cgids, tk, tv, scr, "tile_sort"));
     } else {
         launch_fill_u32(ctx, tile_ids, 0u, 1);
         launch_fill_u32(ctx, cgids, 0u, 1);

@@ -48,6 +48,7 @@ struct bh_ctx {
     std::string last_error;
     bh::Pool pool;
     bool timing = false;
+    std::string timing_filter;  // empty: time every kernel
     std::vector<bh::Timing> pending;
     std::vector<hipEvent_t> event_cache;
     std::vector<std::pair<std::string, bh::TimingTotal>> totals;
@@ -82,12 +83,13 @@ inline uint32_t div_up(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) /
 void launch_fill_u32(bh_ctx* ctx, uint32_t* p, uint32_t value, uint64_t count);
 
 // sort.hip
-size_t radix_sort_scratch_bytes(uint32_t n, uint32_t passes);
-// Stable sort of (key', value) pairs by the low 8*passes bits of
-// key' = min(key - key_sub, key_cap).  vals_in == nullptr means vals = index.
-// The transformed keys are what the sort emits.  tmp_* are n-element buffers.
+size_t radix_sort_scratch_bytes(uint32_t n, uint32_t key_bits);
+// Stable sort of (key', value) pairs by the low key_bits bits of
+// key' = min(key - key_sub, key_cap), in ceil(key_bits / 8) passes of equal
+// digit width.  vals_in == nullptr means vals = index.  The transformed keys
+// are what the sort emits.  tmp_* are n-element buffers.
 bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t* vals_in, uint32_t n,
-                           uint32_t passes, uint32_t key_sub, uint32_t key_cap, uint32_t* keys_out,
+                           uint32_t key_bits, uint32_t key_sub, uint32_t key_cap, uint32_t* keys_out,
                            uint32_t* vals_out, uint32_t* tmp_keys, uint32_t* tmp_vals, void* scratch,
                            const char* tag = "radix");
 // out[i] = in[i] & mask

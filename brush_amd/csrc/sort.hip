@@ -54,26 +54,40 @@ __device__ __forceinline__ void status_store(uint64_t* p, uint64_t v) {
 }
 
 // Sum of the values published by partitions [0, part) for one status column.
-// Walks backwards accumulating aggregates until an inclusive prefix is found.
+// Walks backwards accumulating aggregates until an inclusive prefix is found,
+// reading four predecessors per round trip (the loads are independent).
 __device__ uint32_t look_back(const uint64_t* status, uint32_t part, uint32_t stride, uint32_t col,
                               uint32_t* err) {
     uint32_t excl = 0;
     int64_t p = (int64_t)part - 1;
     uint32_t spins = 0;
     while (p >= 0) {
-        uint64_t s = status_load(status + (uint64_t)p * stride + col);
-        uint64_t flag = s & (3ull << 62);
-        if (flag == 0) {
-            if (++spins >= kSpinLimit) {
-                atomicOr(err, kErrSpin);
-                break;
+        uint64_t s[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) s[i] = p - i >= 0 ? status_load(status + (uint64_t)(p - i) * stride + col) : 0ull;
+        bool stalled = false, found = false;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            if (stalled || found || p - i < 0) continue;
+            const uint64_t flag = s[i] & (3ull << 62);
+            if (flag == 0) {
+                stalled = true;  // wait for this one, keeping what was summed
+                p -= i;
+                continue;
             }
-            __builtin_amdgcn_s_sleep(1);
+            excl += (uint32_t)s[i];
+            if (flag == kFlagPrefix) found = true;
+        }
+        if (found) break;
+        if (!stalled) {
+            p -= 4;
             continue;
         }
-        excl += (uint32_t)s;
-        if (flag == kFlagPrefix) break;
-        p--;
+        if (++spins >= kSpinLimit) {
+            atomicOr(err, kErrSpin);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
     }
     return excl;
 }
@@ -101,38 +115,80 @@ __device__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* s_wave_tot, uint3
     return off + x - v;
 }
 
+// Digit layout of a sort by the low `key_bits` bits: ceil(key_bits / 8)
+// passes of equal width (13 bits -> 7 + 6), so every pass has at most 256
+// buckets and the runs each partition writes per bucket are as long as the
+// bit count allows.
+struct DigitPlan {
+    uint32_t key_bits, passes, width;
+    uint32_t shift(uint32_t p) const { return p * width; }
+    uint32_t bits(uint32_t p) const { return p * width >= key_bits ? 0u : min(width, key_bits - p * width); }
+};
+static DigitPlan digit_plan(uint32_t key_bits) {
+    DigitPlan d;
+    d.key_bits = key_bits;
+    d.passes = key_bits == 0 ? 1u : (key_bits + 7u) / 8u;
+    d.width = key_bits == 0 ? 1u : (key_bits + d.passes - 1u) / d.passes;
+    return d;
+}
+
 // ---- histogram of all digit passes -------------------------------------------
 
+// Each wave counts into its own LDS copy (less contention on the few buckets
+// of a narrow digit); a modest grid keeps the global atomics on the 256 *
+// passes bucket words few.
 __global__ __launch_bounds__(kThreads) void radix_hist_kernel(const uint32_t* __restrict__ keys, uint32_t n,
-                                                               uint32_t passes, uint32_t key_sub, uint32_t key_cap,
-                                                               uint32_t* __restrict__ hist) {
-    __shared__ uint32_t sh[4 * kRadix];
-    for (int i = threadIdx.x; i < 4 * kRadix; i += kThreads) sh[i] = 0;
+                                                               uint32_t passes, uint32_t width, uint32_t key_sub,
+                                                               uint32_t key_cap, uint32_t* __restrict__ hist) {
+    __shared__ uint32_t sh[kWaves][4 * kRadix];
+    const uint32_t wave = threadIdx.x >> 6;
+    for (int i = threadIdx.x; i < kWaves * 4 * kRadix; i += kThreads) (&sh[0][0])[i] = 0;
     __syncthreads();
-    for (uint32_t idx = blockIdx.x * kThreads + threadIdx.x; idx < n; idx += gridDim.x * kThreads) {
-        uint32_t k = min(keys[idx] - key_sub, key_cap);
-        for (uint32_t p = 0; p < passes; p++) atomicAdd(&sh[p * kRadix + ((k >> (8 * p)) & 255u)], 1u);
+    const uint32_t mask = (1u << width) - 1u;
+    uint32_t* mine = sh[wave];
+    // 16-byte loads when the keys are 16-byte aligned (every internal buffer
+    // is); a caller's misaligned view is counted one key at a time
+    const bool vec = (reinterpret_cast<uintptr_t>(keys) & 15u) == 0u;
+    const uint32_t n4 = vec ? n / 4u : 0u;
+    const uint4* k4 = reinterpret_cast<const uint4*>(keys);
+    for (uint32_t idx = blockIdx.x * kThreads + threadIdx.x; idx < n4; idx += gridDim.x * kThreads) {
+        const uint4 q = k4[idx];
+        const uint32_t kk[4] = {min(q.x - key_sub, key_cap), min(q.y - key_sub, key_cap), min(q.z - key_sub, key_cap),
+                                min(q.w - key_sub, key_cap)};
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            for (uint32_t p = 0; p < passes; p++) atomicAdd(&mine[p * kRadix + ((kk[e] >> (p * width)) & mask)], 1u);
+    }
+    // the keys after the last full group of four
+    for (uint32_t idx = n4 * 4u + blockIdx.x * kThreads + threadIdx.x; idx < n; idx += gridDim.x * kThreads) {
+        const uint32_t kk = min(keys[idx] - key_sub, key_cap);
+        for (uint32_t p = 0; p < passes; p++) atomicAdd(&mine[p * kRadix + ((kk >> (p * width)) & mask)], 1u);
     }
     __syncthreads();
-    for (uint32_t i = threadIdx.x; i < passes * kRadix; i += kThreads)
-        if (sh[i]) atomicAdd(&hist[i], sh[i]);
+    for (uint32_t i = threadIdx.x; i < passes * kRadix; i += kThreads) {
+        uint32_t c = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) c += sh[w][i];
+        if (c) atomicAdd(&hist[i], c);
+    }
 }
 
 // ---- one digit pass ------------------------------------------------------------
 
-template <bool FIRST>
+template <bool FIRST, int ITEMS>
 __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __restrict__ keys_in,
                                                              const uint32_t* __restrict__ vals_in,
                                                              uint32_t* __restrict__ keys_out,
                                                              uint32_t* __restrict__ vals_out, uint32_t n,
-                                                             uint32_t shift, uint32_t key_sub, uint32_t key_cap,
-                                                             const uint32_t* __restrict__ hist, uint64_t* status,
-                                                             uint32_t* part_counter, uint32_t* err) {
+                                                             uint32_t shift, uint32_t digit_bits, uint32_t key_sub,
+                                                             uint32_t key_cap, const uint32_t* __restrict__ hist,
+                                                             uint64_t* status, uint32_t* part_counter,
+                                                             uint32_t* err) {
+    constexpr int PART = kThreads * ITEMS;
     __shared__ uint32_t s_wave_hist[kWaves][kRadix];
     __shared__ uint32_t s_local_start[kRadix];
     __shared__ uint32_t s_global_off[kRadix];
-    __shared__ uint32_t s_keys[kPart];
-    __shared__ uint32_t s_vals[kPart];
+    __shared__ uint32_t s_buf[PART];  // keys, then values, in digit order
     __shared__ uint32_t s_tot[kWaves];
     __shared__ uint32_t s_part;
 
@@ -141,12 +197,13 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
     for (int i = tid; i < kWaves * kRadix; i += kThreads) (&s_wave_hist[0][0])[i] = 0;
     __syncthreads();
     const uint32_t part = s_part;
-    const uint64_t base = (uint64_t)part * kPart;
-    const uint64_t wave_base = base + (uint64_t)wave * (64 * kItems);
+    const uint64_t base = (uint64_t)part * PART;
+    const uint64_t wave_base = base + (uint64_t)wave * (64 * ITEMS);
+    const uint32_t dmask = (1u << digit_bits) - 1u;
 
-    uint32_t k[kItems], v[kItems], rank[kItems];
+    uint32_t k[ITEMS], v[ITEMS], pos[ITEMS];
 #pragma unroll
-    for (int j = 0; j < kItems; j++) {
+    for (int j = 0; j < ITEMS; j++) {
         uint64_t idx = wave_base + (uint64_t)j * 64 + lane;
         bool valid = idx < n;
         uint32_t kk = valid ? keys_in[idx] : 0u;
@@ -156,20 +213,19 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
     }
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 #pragma unroll
-    for (int j = 0; j < kItems; j++) {
+    for (int j = 0; j < ITEMS; j++) {
         uint64_t idx = wave_base + (uint64_t)j * 64 + lane;
         bool valid = idx < n;
-        uint32_t d = (k[j] >> shift) & 255u;
+        uint32_t d = (k[j] >> shift) & dmask;
         uint64_t peers = __ballot(valid);
-#pragma unroll
-        for (int b = 0; b < 8; b++) {
+        for (uint32_t b = 0; b < digit_bits; b++) {
             bool bit = (d >> b) & 1u;
             uint64_t bal = __ballot(bit);
             peers &= bit ? bal : ~bal;
         }
         uint32_t prefix = 0;
         if (valid) prefix = s_wave_hist[wave][d];
-        rank[j] = prefix + (uint32_t)__popcll(peers & lt_mask);
+        pos[j] = prefix + (uint32_t)__popcll(peers & lt_mask);
         // the highest lane of each peer group advances the wave's running count
         if (valid && (peers >> lane) == 1ull) s_wave_hist[wave][d] = prefix + (uint32_t)__popcll(peers);
     }
@@ -202,69 +258,98 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
     s_global_off[d] = bin_base + excl;
     __syncthreads();
 
+    // keys into LDS in digit order, then out; the destination of each LDS slot
+    // is kept for the values
 #pragma unroll
-    for (int j = 0; j < kItems; j++) {
+    for (int j = 0; j < ITEMS; j++) {
         uint64_t idx = wave_base + (uint64_t)j * 64 + lane;
-        if (idx < n) {
-            uint32_t dd = (k[j] >> shift) & 255u;
-            uint32_t pos = s_local_start[dd] + s_wave_hist[wave][dd] + rank[j];
-            s_keys[pos] = k[j];
-            s_vals[pos] = v[j];
+        uint32_t dd = (k[j] >> shift) & dmask;
+        pos[j] = s_local_start[dd] + s_wave_hist[wave][dd] + pos[j];
+        if (idx < n) s_buf[pos[j]] = k[j];
+    }
+    __syncthreads();
+    const uint32_t count = (uint32_t)min<uint64_t>((uint64_t)PART, (uint64_t)n - base);
+    uint32_t dst[ITEMS];
+#pragma unroll
+    for (int j = 0; j < ITEMS; j++) {
+        const uint32_t i = (uint32_t)(j * kThreads + tid);
+        dst[j] = 0xFFFFFFFFu;
+        if (i < count) {
+            const uint32_t key = s_buf[i];
+            const uint32_t dd = (key >> shift) & dmask;
+            const uint32_t g = s_global_off[dd] + (i - s_local_start[dd]);
+            if (g < n) {  // always true unless a look-back gave up (reported through err)
+                keys_out[g] = key;
+                dst[j] = g;
+            }
         }
     }
     __syncthreads();
-    const uint32_t count = (uint32_t)min<uint64_t>((uint64_t)kPart, (uint64_t)n - base);
-    for (uint32_t i = tid; i < count; i += kThreads) {
-        uint32_t key = s_keys[i];
-        uint32_t dd = (key >> shift) & 255u;
-        uint32_t g = s_global_off[dd] + (i - s_local_start[dd]);
-        if (g < n) {  // always true unless a look-back gave up (reported through err)
-            keys_out[g] = key;
-            vals_out[g] = s_vals[i];
-        }
+#pragma unroll
+    for (int j = 0; j < ITEMS; j++) {
+        uint64_t idx = wave_base + (uint64_t)j * 64 + lane;
+        if (idx < n) s_buf[pos[j]] = v[j];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < ITEMS; j++) {
+        const uint32_t i = (uint32_t)(j * kThreads + tid);
+        if (dst[j] != 0xFFFFFFFFu) vals_out[dst[j]] = s_buf[i];
     }
 }
 
-// scratch layout: hist[passes*256] | counters[passes] (padded to 8 words) | status[passes][parts][256] (u64)
-size_t radix_sort_scratch_bytes(uint32_t n, uint32_t passes) {
-    uint64_t parts = div_up(n, kPart);
-    return (size_t)(4 * kRadix + 8) * 4 + (size_t)passes * parts * kRadix * 8;
+// Partitions of 4096 pairs (smaller partitions measured slower: more
+// look-back traffic for the same data).
+static uint32_t sort_part(uint32_t) { return (uint32_t)kPart; }
+
+// scratch layout: hist[4*256] | counters[8] | status[passes][parts][256] (u64)
+size_t radix_sort_scratch_bytes(uint32_t n, uint32_t key_bits) {
+    const uint64_t parts = div_up(n, sort_part(n));
+    return (size_t)(4 * kRadix + 8) * 4 + (size_t)digit_plan(key_bits).passes * parts * kRadix * 8;
 }
 
 bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t* vals_in, uint32_t n,
-                           uint32_t passes, uint32_t key_sub, uint32_t key_cap, uint32_t* keys_out,
+                           uint32_t key_bits, uint32_t key_sub, uint32_t key_cap, uint32_t* keys_out,
                            uint32_t* vals_out, uint32_t* tmp_keys, uint32_t* tmp_vals, void* scratch,
                            const char* tag) {
     const std::string hist_name = std::string(tag) + "_hist", pass_name = std::string(tag) + "_onesweep";
     if (n == 0) return BH_OK;
-    if (passes == 0) passes = 1;
-    if (passes > 4) return set_error(ctx, BH_ERR_INVALID_ARG, "radix sort: more than 32 key bits");
-    uint32_t parts = div_up(n, kPart);
+    if (key_bits > 32) return set_error(ctx, BH_ERR_INVALID_ARG, "radix sort: more than 32 key bits");
+    const DigitPlan plan = digit_plan(key_bits);
+    const uint32_t part_size = sort_part(n);
+    const uint32_t parts = div_up(n, part_size);
     uint32_t* hist = (uint32_t*)scratch;
     uint32_t* counters = hist + 4 * kRadix;
     uint64_t* status = (uint64_t*)(counters + 8);
-    size_t words = (size_t)(4 * kRadix + 8) + (size_t)passes * parts * kRadix * 2;
+    size_t words = (size_t)(4 * kRadix + 8) + (size_t)plan.passes * parts * kRadix * 2;
     launch_fill_u32(ctx, hist, 0u, words);
     {
         KernelTimer t(ctx, hist_name.c_str());
-        uint32_t blocks = std::min<uint32_t>(div_up(n, kThreads * 16), 2048);
-        radix_hist_kernel<<<blocks, kThreads, 0, ctx->stream>>>(keys_in, n, passes, key_sub, key_cap, hist);
+        uint32_t blocks = std::min<uint32_t>(div_up(div_up(n, 4), kThreads * 8), 512);
+        radix_hist_kernel<<<blocks, kThreads, 0, ctx->stream>>>(keys_in, n, plan.passes, plan.width, key_sub, key_cap,
+                                                                hist);
     }
     const uint32_t* src_k = keys_in;
     const uint32_t* src_v = vals_in;
-    for (uint32_t p = 0; p < passes; p++) {
+    for (uint32_t p = 0; p < plan.passes; p++) {
         // the last pass lands in the output buffers
-        bool to_out = ((passes - 1 - p) % 2) == 0;
+        bool to_out = ((plan.passes - 1 - p) % 2) == 0;
         uint32_t* dk = to_out ? keys_out : tmp_keys;
         uint32_t* dv = to_out ? vals_out : tmp_vals;
         uint64_t* st = status + (uint64_t)p * parts * kRadix;
+        const uint32_t sh = plan.shift(p), bits = plan.bits(p);
+        const uint32_t sub = p == 0 ? key_sub : 0u, cap = p == 0 ? key_cap : 0xFFFFFFFFu;
         KernelTimer t(ctx, pass_name.c_str());
-        if (p == 0)
-            onesweep_kernel<true><<<parts, kThreads, 0, ctx->stream>>>(src_k, src_v, dk, dv, n, 0, key_sub, key_cap,
-                                                                        hist, st, counters + p, ctx->d_counters + 1);
-        else
-            onesweep_kernel<false><<<parts, kThreads, 0, ctx->stream>>>(
-                src_k, src_v, dk, dv, n, 8 * p, 0, 0xFFFFFFFFu, hist + p * kRadix, st, counters + p, ctx->d_counters + 1);
+#define BH_PASS(F, I)                                                                                               \
+    onesweep_kernel<F, I><<<parts, kThreads, 0, ctx->stream>>>(src_k, src_v, dk, dv, n, sh, bits, sub, cap,        \
+                                                               hist + p * kRadix, st, counters + p,                \
+                                                               ctx->d_counters + 1)
+        if (part_size == (uint32_t)kPart) {
+            if (p == 0) BH_PASS(true, kItems); else BH_PASS(false, kItems);
+        } else {
+            if (p == 0) BH_PASS(true, 4); else BH_PASS(false, 4);
+        }
+#undef BH_PASS
         src_k = dk;
         src_v = dv;
     }

@@ -123,6 +123,10 @@ const char* bh_last_error(const bh_ctx* ctx);
  * When enabled, every launch is bracketed by events and its duration is
  * accumulated per kernel name. */
 bh_status bh_ctx_set_timing(bh_ctx* ctx, int enable);
+/* Restricts timing to launches of the kernel called `name` (NULL or "" times
+ * every kernel), so that a benchmark can time one kernel without bracketing the
+ * others with events. */
+bh_status bh_ctx_set_timing_filter(bh_ctx* ctx, const char* name);
 typedef struct bh_kernel_timing {
     char name[48];
     uint32_t launches;
