@@ -38,7 +38,7 @@ EXPORTED = [
     "bh_ctx_set_timing_filter",
     "bh_ctx_read_timings", "bh_ctx_reset_timings", "bh_ctx_workspace_bytes", "bh_radix_argsort",
     "bh_prefix_sum", "bh_get_tile_offsets", "bh_render_forward", "bh_fwd_state_info",
-    "bh_fwd_state_release", "bh_rasterize_backward", "bh_project_backward", "bh_copy_to_host",
+    "bh_fwd_state_release", "bh_rasterize_backward", "bh_render_backward", "bh_project_backward", "bh_copy_to_host",
     "bh_copy_to_device", "bh_copy_device", "bh_device_alloc", "bh_device_free", "bh_synchronize",
 ]
 
@@ -156,6 +156,7 @@ def lib() -> ctypes.CDLL:
         "bh_fwd_state_info": (S, [P, ctypes.POINTER(FwdInfo)]),
         "bh_fwd_state_release": (None, [P]),
         "bh_rasterize_backward": (S, [P, P, P, P, P, U32, P, U32, U32, P, U32, P]),
+        "bh_render_backward": (S, [P, P, P, P, P, P, P, P, P, U32, P, P, P, P]),
         "bh_project_backward": (S, [P, UP, P, P, P, P, P, U32, P, P, P, P]),
         "bh_copy_to_host": (S, [P, P, P, U64]),
         "bh_copy_to_device": (S, [P, P, P, U64]),

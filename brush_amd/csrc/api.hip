@@ -507,7 +507,7 @@ bh_status bh_rasterize_backward(bh_ctx* ctx, const float* out_img, const float* 
     launch_fill_u32(ctx, (uint32_t*)v_combined, 0u, (uint64_t)std::max<uint32_t>(num_visible, 1) * 11);
     if (num_visible)
         launch_rasterize_backward(ctx, img_w, img_h, tbw, tbh, background, num_visible, out_img, projected,
-                                  compact_gid_from_isect, tile_offsets, v_output, flags, v_combined);
+                                  compact_gid_from_isect, tile_offsets, v_output, flags, nullptr, v_combined);
     return check_launch(ctx, "rasterize_backward");
 }
 
@@ -530,6 +530,37 @@ bh_status bh_project_backward(bh_ctx* ctx, const bh_project_uniforms* u, const f
     launch_invert_permutation(ctx, global_from_compact_gid, u->num_visible, n, cfg);
     launch_project_backward(ctx, *u, transforms, sh_coeffs, raw_opacities, cfg, n, u->sh_degree,
                             (flags & BH_FLAG_MIP) != 0, v_combined, v_transforms, v_coeffs, v_raw_opac, v_refine);
+    return check_launch(ctx, "project_backward");
+}
+
+bh_status bh_render_backward(bh_ctx* ctx, const bh_fwd_state* state, const float* out_img,
+                             const uint32_t* tile_offsets, const float background[3], const float* transforms,
+                             const float* sh_coeffs, const float* raw_opacities, const float* v_output, uint32_t flags,
+                             float* v_transforms, float* v_coeffs, float* v_raw_opac, float* v_refine) {
+    if (!ctx) return BH_ERR_INVALID_ARG;
+    if (!state) return set_error(ctx, BH_ERR_INVALID_ARG, "render_backward: null forward state");
+    const bh_fwd_info& in = state->info;
+    if (!(in.flags & BH_FLAG_BWD_INFO))
+        return set_error(ctx, BH_ERR_INVALID_ARG, "render_backward: the forward ran without BH_FLAG_BWD_INFO");
+    const uint32_t n = in.num_splats;
+    if (n == 0) return BH_OK;
+    if (!out_img || !tile_offsets || !background || !transforms || !sh_coeffs || !raw_opacities || !v_output ||
+        !v_transforms || !v_coeffs || !v_raw_opac || !v_refine)
+        return set_error(ctx, BH_ERR_INVALID_ARG, "render_backward: null argument");
+    // gradient lanes accumulated per global id, so project backward reads
+    // them in order (no inverse permutation, no gathered rows)
+    Scratch ws(ctx);
+    float* rows;
+    BH_TRY(ws.get(&rows, (size_t)n * 11));
+    launch_fill_u32(ctx, (uint32_t*)rows, 0u, (uint64_t)n * 11);
+    const uint32_t raster_flags = flags & (BH_FLAG_SMOOTH_CUTOFF | BH_FLAG_REFINE_WEIGHT | BH_FLAG_RENDER_DEPTH);
+    if (in.num_visible)
+        launch_rasterize_backward(ctx, in.img_w, in.img_h, in.tile_bw, in.tile_bh, background, in.num_visible, out_img,
+                                  in.projected, in.compact_gid_from_isect, tile_offsets, v_output, raster_flags,
+                                  in.global_from_compact_gid, rows);
+    BH_TRY(check_launch(ctx, "rasterize_backward"));
+    launch_project_backward(ctx, in.uniforms, transforms, sh_coeffs, raw_opacities, nullptr, n, in.sh_degree,
+                            (in.flags & BH_FLAG_MIP) != 0, rows, v_transforms, v_coeffs, v_raw_opac, v_refine);
     return check_launch(ctx, "project_backward");
 }
 

@@ -73,7 +73,7 @@ __global__ __launch_bounds__(64) void rasterize_backward_kernel(
     uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t num_tiles, float bg_r, float bg_g, float bg_b,
     uint32_t num_visible, const float* __restrict__ out_img, const float* __restrict__ projected,
     const uint32_t* __restrict__ cgids, const uint32_t* __restrict__ offsets, const float* __restrict__ v_output,
-    float* __restrict__ v_combined) {
+    const uint32_t* __restrict__ row_of, float* __restrict__ v_combined) {
     constexpr uint32_t CH = DEPTH ? 5u : 4u;
     __shared__ float4 s_xyco[64];  // x, y, conic c00, c01
     __shared__ float4 s_crgb[64];  // conic c11, opacity, r, g
@@ -129,7 +129,7 @@ __global__ __launch_bounds__(64) void rasterize_backward_kernel(
             s_xyco[lane] = make_float4(r0.x, r0.y, r1.x, r1.y);
             s_crgb[lane] = make_float4(r2.x, r2.y, r3.x, r3.y);
             s_bd[lane] = make_float4(r4.x, r4.y, cut, 0.0f);
-            s_cid[lane] = c;
+            s_cid[lane] = row_of ? row_of[c] : c;
             touch = may_touch_rect(r0.x, r0.y, S2{r1.x, r1.y, r2.x}, cut, bx0, by0, bx0 + 7.0f, by0 + 7.0f);
         }
         // splats of the batch that may touch this block, in order
@@ -172,8 +172,8 @@ __global__ __launch_bounds__(64) void rasterize_backward_kernel(
             const float ra = __builtin_amdgcn_rcpf(1.0f - ae);
             const float dot_rgb = ((sw * cr - sx) * vox + (sw * cgc - sy) * voy + (sw * cb - sz) * voz) * ra;
             const float v_ae = dot_rgb + vow * ra;
-            const float dw = SMOOTH ? cutoff_weight_deriv(alpha) : 0.0f * alpha;
-            const float v_alpha = v_ae * (w + alpha * dw);
+            // with the hard cutoff the weight is a step and its derivative 0
+            const float v_alpha = SMOOTH ? v_ae * (w + alpha * cutoff_weight_deriv(alpha)) : v_ae * w;
             const float v_sigma = -alpha * v_alpha;
             const float vxy_x = v_sigma * (conic.c00 * dx + conic.c01 * dy);
             const float vxy_y = v_sigma * (conic.c01 * dx + conic.c11 * dy);
@@ -225,7 +225,8 @@ __global__ __launch_bounds__(64) void rasterize_backward_kernel(
 
 void launch_rasterize_backward(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,
                                const float* bg, uint32_t num_visible, const float* out_img, const float* projected, const uint32_t* cgids,
-                               const uint32_t* offsets, const float* v_output, uint32_t flags, float* v_combined) {
+                               const uint32_t* offsets, const float* v_output, uint32_t flags,
+                               const uint32_t* row_of, float* v_combined) {
     const uint32_t num_tiles = tile_bw * tile_bh;
     if (num_tiles == 0 || num_visible == 0) return;
     const bool smooth = (flags & BH_FLAG_SMOOTH_CUTOFF) != 0;
@@ -237,7 +238,7 @@ void launch_rasterize_backward(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint
     rasterize_backward_kernel<S, R, D><<<groups, 64, 0, ctx->stream>>>(img_w, img_h, tile_bw, num_tiles, bg[0], \
                                                                        bg[1], bg[2], num_visible, out_img,       \
                                                                        projected, cgids, offsets, v_output,      \
-                                                                       v_combined)
+                                                                       row_of, v_combined)
     if (smooth) {
         if (refine) {
             if (depth) BH_RB(true, true, true); else BH_RB(true, true, false);
@@ -287,41 +288,17 @@ __device__ __forceinline__ void store_row(float* __restrict__ dst, const float* 
     }
 }
 
+// The projection VJP of one splat with gradient lanes rg, written to its dense
+// rows (project_backwards.rs:101-263).
 template <int DEG, bool MIP>
-__global__ __launch_bounds__(256) void project_backward_kernel(
-    bh_project_uniforms u, const float* __restrict__ transforms, const float* __restrict__ sh,
-    const float* __restrict__ raw_opac, const uint32_t* __restrict__ cfg, uint32_t n,
-    const float* __restrict__ v_combined, float* __restrict__ v_transforms, float* __restrict__ v_coeffs,
-    float* __restrict__ v_raw_opac, float* __restrict__ v_refine) {
+__device__ void project_backward_one(const bh_project_uniforms& u, const float* __restrict__ transforms,
+                                     const float* __restrict__ sh, const float* __restrict__ raw_opac, uint32_t gid,
+                                     const float* rg, float* __restrict__ v_transforms, float* __restrict__ v_coeffs,
+                                     float* __restrict__ v_raw_opac, float* __restrict__ v_refine) {
     constexpr int NC = (DEG + 1) * (DEG + 1);
-    const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
-    if (gid >= n) return;
-    const uint32_t c = cfg[gid];
-    float rg[11];
-#pragma unroll
-    for (int k = 0; k < 11; k++) rg[k] = 0.0f;
-    bool any = false;
-    if (c != 0xFFFFFFFFu) {
-        const float* src = v_combined + (size_t)c * 11;
-#pragma unroll
-        for (int k = 0; k < 11; k++) {
-            rg[k] = src[k];
-            any = any || rg[k] != 0.0f;
-        }
-    }
     float2* vt = reinterpret_cast<float2*>(v_transforms + (size_t)gid * 10);
     float* vc_row = v_coeffs + (size_t)gid * (3 * NC);
     float vcoef[3 * NC];
-    if (!any) {
-#pragma unroll
-        for (int k = 0; k < 5; k++) vt[k] = make_float2(0.0f, 0.0f);
-#pragma unroll
-        for (int k = 0; k < 3 * NC; k++) vcoef[k] = 0.0f;
-        store_row<NC>(vc_row, vcoef);
-        v_raw_opac[gid] = 0.0f;
-        v_refine[gid] = 0.0f;
-        return;
-    }
     const float2* row = reinterpret_cast<const float2*>(transforms + (size_t)gid * 10);
     float t[10];
 #pragma unroll
@@ -402,6 +379,77 @@ __global__ __launch_bounds__(256) void project_backward_kernel(
     vt[2] = make_float2(vq.x, vq.y);
     vt[3] = make_float2(vq.z, v_scale.x);
     vt[4] = make_float2(v_scale.y, v_scale.z);
+}
+
+// Zero-fills floats [begin, end) of p with the block's threads, 16 bytes per
+// store where p + begin is 16-byte aligned.
+__device__ __forceinline__ void block_zero(float* __restrict__ p, size_t begin, size_t end) {
+    float* q = p + begin;
+    const size_t count = end - begin;
+    size_t head = 0;
+    if ((reinterpret_cast<uintptr_t>(q) & 15u) == 0u) {
+        float4* q4 = reinterpret_cast<float4*>(q);
+        head = count / 4u * 4u;
+        for (size_t i = threadIdx.x; i < count / 4u; i += blockDim.x) q4[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    for (size_t i = head + threadIdx.x; i < count; i += blockDim.x) q[i] = 0.0f;
+}
+
+// Each block first zero-fills its 256 dense output rows with contiguous stores
+// (rows without gradient — culled splats, splats behind saturated pixels —
+// are most rows), then compacts the ids that have gradient into an LDS list
+// and runs the VJP over that list with every lane busy, overwriting their
+// rows.  cfg == nullptr: v_combined holds one row per global id (the fused
+// backward), else v_combined[cfg[gid]].
+template <int DEG, bool MIP>
+__global__ __launch_bounds__(256) void project_backward_kernel(
+    bh_project_uniforms u, const float* __restrict__ transforms, const float* __restrict__ sh,
+    const float* __restrict__ raw_opac, const uint32_t* __restrict__ cfg, uint32_t n,
+    const float* __restrict__ v_combined, float* __restrict__ v_transforms, float* __restrict__ v_coeffs,
+    float* __restrict__ v_raw_opac, float* __restrict__ v_refine) {
+    constexpr int NC = (DEG + 1) * (DEG + 1);
+    __shared__ uint32_t s_gid[256];
+    __shared__ uint32_t s_row[256];
+    __shared__ uint32_t s_count[4];
+    const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
+    const uint32_t gid = blockIdx.x * 256u + t;
+    const uint32_t c = gid < n ? (cfg ? cfg[gid] : gid) : 0xFFFFFFFFu;
+    bool any = false;
+    if (c != 0xFFFFFFFFu) {
+        const float* src = v_combined + (size_t)c * 11;
+#pragma unroll
+        for (int k = 0; k < 11; k++) any = any || src[k] != 0.0f;
+    }
+    const size_t g0 = (size_t)blockIdx.x * 256u, g1 = min<size_t>(g0 + 256u, n);
+    block_zero(v_transforms, g0 * 10u, g1 * 10u);
+    block_zero(v_coeffs, g0 * (3u * NC), g1 * (3u * NC));
+    block_zero(v_raw_opac, g0, g1);
+    block_zero(v_refine, g0, g1);
+    // compact the ids with gradient: per-wave ballot, then wave offsets
+    const uint64_t mask = __ballot(any);
+    if (lane == 0) s_count[wave] = (uint32_t)__popcll(mask);
+    __syncthreads();
+    uint32_t before = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        before += (uint32_t)w < wave ? s_count[w] : 0u;
+        total += s_count[w];
+    }
+    if (any) {
+        const uint32_t slot = before + lanes_below(mask);
+        s_gid[slot] = gid;
+        s_row[slot] = c;
+    }
+    __syncthreads();
+    for (uint32_t i = t; i < total; i += 256u) {
+        const uint32_t g = s_gid[i];
+        const float* src = v_combined + (size_t)s_row[i] * 11;
+        float rg[11];
+#pragma unroll
+        for (int k = 0; k < 11; k++) rg[k] = src[k];
+        project_backward_one<DEG, MIP>(u, transforms, sh, raw_opac, g, rg, v_transforms, v_coeffs, v_raw_opac,
+                                       v_refine);
+    }
 }
 
 template <int DEG>

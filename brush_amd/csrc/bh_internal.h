@@ -125,9 +125,10 @@ void launch_rasterize(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile
 void launch_rasterize_backward(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,
                                const float* bg, uint32_t num_visible, const float* out_img, const float* projected,
                                const uint32_t* cgids, const uint32_t* offsets, const float* v_output,
-                               uint32_t flags, float* v_combined);
+                               uint32_t flags, const uint32_t* row_of, float* v_combined);
 void launch_invert_permutation(bh_ctx* ctx, const uint32_t* gfc, uint32_t num_visible, uint32_t n,
                                uint32_t* compact_from_global);
+// compact_from_global == nullptr: v_combined is indexed by global id.
 void launch_project_backward(bh_ctx* ctx, const bh_project_uniforms& u, const float* transforms, const float* sh,
                              const float* raw_opac, const uint32_t* compact_from_global, uint32_t n,
                              uint32_t sh_degree, bool mip, const float* v_combined, float* v_transforms,

@@ -431,23 +431,36 @@ class _RenderSplatsFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, v_img):
+        """rasterize_bwd followed by project_bwd in one library call
+        (bh_render_backward); the intermediate gradient lanes stay in library
+        workspace, as v_combined stays inside RenderBackwards::backward."""
         cfg = ctx.cfg
         transforms, sh_coeffs, raw_opac, out_img, tile_offsets = ctx.saved_tensors
         out = cfg.output
-        info = out.state.info
-        with torch.cuda.device(out_img.device):
+        n = transforms.shape[0]
+        dev = transforms.device
+        nc = sh_coeffs.shape[1]
+        v_t = torch.empty((n, 10), dtype=torch.float32, device=dev)
+        v_c = torch.empty((n, nc, 3), dtype=torch.float32, device=dev)
+        v_o = torch.empty((n,), dtype=torch.float32, device=dev)
+        v_r = torch.empty((n,), dtype=torch.float32, device=dev)
+        flags = 0
+        if cfg.raster_pass.smooth_cutoff:
+            flags |= _lib.FLAG_SMOOTH_CUTOFF
+        if cfg.raster_mode.render_depth:
+            flags |= _lib.FLAG_RENDER_DEPTH
+        if cfg.compute_refine_weight:
+            flags |= _lib.FLAG_REFINE_WEIGHT
+        bg = (ctypes.c_float * 3)(*[float(x) for x in cfg.background])
+        with torch.cuda.device(dev):
             c = context()
-            v_comb = _rasterize_bwd_ptrs(
-                c, out_img, ctypes.c_void_p(info.projected), ctypes.c_void_p(info.compact_gid_from_isect),
-                tile_offsets, int(info.num_visible), cfg.background, cfg.img_size, v_img.contiguous(),
-                cfg.raster_pass.smooth_cutoff, cfg.raster_mode.render_depth, cfg.compute_refine_weight)
-            grads = _project_bwd_ptrs(c, transforms.detach().contiguous(), sh_coeffs.detach().contiguous(),
-                                      raw_opac.detach().contiguous(),
-                                      ctypes.c_void_p(info.global_from_compact_gid), out.project_uniforms,
-                                      cfg.render_mode, v_comb)
-        cfg.refine_weight = grads.v_refine_weight
-        cfg.v_combined = v_comb
-        return grads.v_transforms, grads.v_coeffs, grads.v_raw_opac, None
+            st = lib().bh_render_backward(c.handle, out.state.handle, ptr(out_img), ptr(tile_offsets), bg,
+                                          ptr(transforms.detach().contiguous()),
+                                          ptr(sh_coeffs.detach().contiguous()), ptr(raw_opac.detach().contiguous()),
+                                          ptr(v_img.contiguous()), flags, ptr(v_t), ptr(v_c), ptr(v_o), ptr(v_r))
+            c.check(st, "render_backward")
+        cfg.refine_weight = v_r
+        return v_t, v_c, v_o, None
 
 
 def render_splats_diff(splats: Splats, camera: Camera, img_size, background=(0.0, 0.0, 0.0),

@@ -206,6 +206,20 @@ bh_status bh_rasterize_backward(bh_ctx* ctx, const float* out_img, const float* 
                                 const float background[3], uint32_t img_w, uint32_t img_h,
                                 const float* v_output, uint32_t flags, float* v_combined);
 
+/* Both backward operations of one forward state in one call: the backward of
+ * RenderBackwards (brush-render-bwd/src/burn_glue.rs:292-378), which runs
+ * rasterize_bwd then project_bwd and keeps v_combined internal.  Here the
+ * gradient lanes are accumulated per global id in library workspace, so
+ * project backward reads them in order.  `state` comes from a forward with
+ * BH_FLAG_BWD_INFO; out_img and tile_offsets are that forward's outputs;
+ * flags: BH_FLAG_SMOOTH_CUTOFF, BH_FLAG_REFINE_WEIGHT, BH_FLAG_RENDER_DEPTH
+ * (BH_FLAG_MIP follows the forward).  Outputs as bh_project_backward. */
+bh_status bh_render_backward(bh_ctx* ctx, const bh_fwd_state* state, const float* out_img,
+                             const uint32_t* tile_offsets, const float background[3],
+                             const float* transforms, const float* sh_coeffs,
+                             const float* raw_opacities, const float* v_output, uint32_t flags,
+                             float* v_transforms, float* v_coeffs, float* v_raw_opac, float* v_refine);
+
 /* Project backward.  Replaces SplatBwdOps::project_bwd
  * (brush-render-bwd/src/burn_glue.rs:79-172, impl render_bwd.rs:298-447,
  * kernel kernels/project_backwards.rs:101-263).  `u` is the forward's uniforms

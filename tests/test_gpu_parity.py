@@ -272,32 +272,68 @@ def test_backward_matches_checker(gpu, seed, n, deg, flags):
     assert_bits_equal("v_refine", grads.v_refine_weight.cpu().numpy(), vr)
 
 
-def test_autograd_end_to_end(gpu):
-    """render_splats_diff + loss.backward() vs the checker's full backward."""
+@pytest.mark.parametrize("smooth,depth,mip,refine", [(False, False, False, True), (True, False, False, True),
+                                                      (False, True, False, False), (True, True, True, True),
+                                                      (False, False, True, False)])
+def test_autograd_end_to_end(gpu, smooth, depth, mip, refine):
+    """render_splats_diff + loss.backward() (the fused bh_render_backward, which
+    accumulates the gradient lanes per global id) vs the checker's rasterize
+    backward followed by project backward, for every backward flag."""
     import torch
     from brush_amd import render as R
     from brush_amd.camera import Camera
 
+    print(f"[case] autograd smooth={smooth} depth={depth} mip={mip} refine={refine}", flush=True)
     n, deg = 2000, 3
     tr, sh, opac = random_scene(3001, n, deg, log_scale=(-3.0, 0.6))
     cam = Camera.from_focal((0.0, 0.1, -3.0), (0.0, 0.0, 0.0, 1.0), 80.0, 64, 48)
     t = torch.from_numpy(tr).to(gpu).requires_grad_(True)
     s = torch.from_numpy(sh).to(gpu).requires_grad_(True)
     op = torch.from_numpy(opac).to(gpu).requires_grad_(True)
-    splats = R.Splats(t, s, op)
-    res = R.render_splats_diff(splats, cam, (64, 48), (0.0, 0.0, 0.0))
+    splats = R.Splats(t, s, op, render_mip=mip)
+    rpass = R.RasterPass.BackwardSmoothCutoff if smooth else R.RasterPass.Backward
+    rmode = R.RasterizationMode.RgbaAndDepth if depth else R.RasterizationMode.Rgba
+    res = R.render_splats_diff(splats, cam, (64, 48), (0.1, 0.0, 0.2), compute_refine_weight=refine,
+                               raster_pass=rpass, raster_mode=rmode)
+    chans = 5 if depth else 4
     rng = np.random.default_rng(5)
-    w = torch.from_numpy(rng.standard_normal((48, 64, 4)).astype(np.float32)).to(gpu)
+    w = torch.from_numpy(rng.standard_normal((48, 64, chans)).astype(np.float32)).to(gpu)
     loss = (res.img * w).sum()
     loss.backward()
     u = uniforms_for(cam, 64, 48, n, deg)
-    o = O.render_forward(u, tr, sh, opac, O.FLAG_BWD_INFO)
-    vc = O.rasterize_backward(o, w.cpu().numpy(), O.FLAG_REFINE_WEIGHT)
-    vt, vcoef, vo, vr = O.project_backward(o, tr, sh, opac, vc)
+    fflags = O.FLAG_BWD_INFO | (O.FLAG_SMOOTH_CUTOFF if smooth else 0) | (O.FLAG_RENDER_DEPTH if depth else 0) | \
+        (O.FLAG_MIP if mip else 0)
+    o = O.render_forward(u, tr, sh, opac, fflags, (0.1, 0.0, 0.2))
+    compare_forward(gpu_forward(u, tr, sh, opac, fflags, (0.1, 0.0, 0.2)), o)
+    bflags = (fflags & 6) | (O.FLAG_REFINE_WEIGHT if refine else 0)
+    vc = O.rasterize_backward(o, w.cpu().numpy(), bflags, (0.1, 0.0, 0.2))
+    vt, vcoef, vo, vr = O.project_backward(o, tr, sh, opac, vc, mip=mip)
     rel_close("v_transforms", t.grad.cpu().numpy(), vt, rtol=1e-3, atol_frac=1e-4)
     rel_close("v_coeffs", s.grad.cpu().numpy(), vcoef, rtol=1e-3, atol_frac=1e-4)
     rel_close("v_raw_opac", op.grad.cpu().numpy(), vo, rtol=1e-3, atol_frac=1e-4)
     rel_close("refine", res._cfg.refine_weight.cpu().numpy(), vr, rtol=1e-3, atol_frac=1e-4)
+    if not refine:
+        assert not res._cfg.refine_weight.any().item()
+
+
+def test_autograd_fully_culled_scene(gpu):
+    """A scene whose splats are all behind the camera: the fused backward
+    writes exactly-zero dense gradients (render.rs:145-253 empty contract)."""
+    import torch
+    from brush_amd import render as R
+    from brush_amd.camera import Camera
+
+    tr, sh, opac = random_scene(3002, 500, 1)
+    tr[:, 2] = -10.0  # z of every mean behind a camera at z = -3 looking down +z
+    cam = Camera.from_focal((0.0, 0.0, -3.0), (0.0, 0.0, 0.0, 1.0), 50.0, 40, 30)
+    t = torch.from_numpy(tr).to(gpu).requires_grad_(True)
+    s = torch.from_numpy(sh).to(gpu).requires_grad_(True)
+    op = torch.from_numpy(opac).to(gpu).requires_grad_(True)
+    res = R.render_splats_diff(R.Splats(t, s, op), cam, (40, 30))
+    assert res.num_visible == 0
+    res.img.sum().backward()
+    for g in (t.grad, s.grad, op.grad, res._cfg.refine_weight):
+        assert g is not None and not g.any().item()
 
 
 @pytest.mark.parametrize("flags", [1, 3])
