@@ -33,16 +33,24 @@ constexpr uint64_t kFlagAgg = 1ull << 62;
 constexpr uint64_t kFlagPrefix = 2ull << 62;
 constexpr uint32_t kSpinLimit = 1u << 24;
 
+// p[0, count) = value: 16-byte stores from the first 16-byte boundary, single
+// words for the unaligned head and the tail.
 __global__ void fill_u32_kernel(uint32_t* p, uint32_t value, uint64_t count) {
-    uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-    for (; i < count; i += stride) p[i] = value;
+    const uint64_t tid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    const uint64_t head = min<uint64_t>(count, ((16u - (reinterpret_cast<uintptr_t>(p) & 15u)) & 15u) / 4u);
+    if (tid < head) p[tid] = value;
+    const uint64_t quads = (count - head) / 4u;
+    uint4* q = reinterpret_cast<uint4*>(p + head);
+    const uint4 v4 = make_uint4(value, value, value, value);
+    for (uint64_t i = tid; i < quads; i += stride) q[i] = v4;
+    for (uint64_t i = head + quads * 4u + tid; i < count; i += stride) p[i] = value;
 }
 
 void launch_fill_u32(bh_ctx* ctx, uint32_t* p, uint32_t value, uint64_t count) {
     if (count == 0) return;
     KernelTimer t(ctx, "fill");
-    uint32_t blocks = (uint32_t)std::min<uint64_t>((count + 255) / 256, 4096);
+    uint32_t blocks = (uint32_t)std::min<uint64_t>((count / 4 + 255) / 256 + 1, 2048);
     fill_u32_kernel<<<blocks, 256, 0, ctx->stream>>>(p, value, count);
 }
 
