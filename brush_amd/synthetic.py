@@ -23,6 +23,8 @@ Generator contract (stable across releases, so fixtures stay valid):
 from __future__ import annotations
 
 import math
+import os
+from concurrent.futures import ThreadPoolExecutor
 from dataclasses import dataclass
 
 import numpy as np
@@ -125,7 +127,7 @@ def generate_splats(w: Workload, n: int | None = None, chunk: int = 1 << 16):
     sh_sigma = np.full((c, 3), w.rest_sigma)
     sh_sigma[0, :] = w.dc_sigma
     sh_sigma = sh_sigma.reshape(-1)
-    for s in range(0, n, chunk):
+    def fill(s):
         e = min(n, s + chunk)
         m = e - s
         idx = (np.arange(s, e, dtype=np.uint64) * np.uint64(per))[:, None] + np.arange(per, dtype=np.uint64)[None, :]
@@ -149,6 +151,17 @@ def generate_splats(w: Workload, n: int | None = None, chunk: int = 1 << 16):
         transforms[s:e, 7:10] = log_scales
         opac[s:e] = w.opac_mu + w.opac_sigma * nrm[:, 7]
         sh[s:e] = (nrm[:, 8:] * sh_sigma[None, :]).reshape(m, c, 3)
+
+    # every chunk depends only on its own indices: fill them on a thread pool
+    # (numpy releases the GIL in these array operations)
+    starts = list(range(0, n, chunk))
+    workers = max(1, min(len(starts), os.cpu_count() or 1, 16))
+    if workers == 1:
+        for s in starts:
+            fill(s)
+    else:
+        with ThreadPoolExecutor(max_workers=workers) as pool:
+            list(pool.map(fill, starts))
     return transforms, sh, opac
 
 

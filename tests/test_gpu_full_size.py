@@ -1,0 +1,180 @@
+"""GPU parity at BASELINE.json's full sizes.
+
+Config 1 (the north-star workload, 1M SH3 splats at 1920x1080) is compared
+with the CPU restatement bit for bit through the forward and to the gradient
+tolerance through the backward.  Configs 2 (3M clustered splats, tens of
+millions of tile intersections) and 3 (6M splats at 3840x2160, forward only)
+are checked through properties that do not need a full CPU run:
+
+* the tile sort: tile ids non-decreasing, compact ids increasing inside each
+  tile, every compact id appearing exactly as often as its splat's tile count,
+  tile offsets equal to the runs;
+* the depth sort: depths non-decreasing, global ids a permutation of the
+  visible splats;
+* per-splat outputs (tile count, max radius, projected row, the list of tiles
+  a splat lands in) depend on the splat alone, so the CPU restatement run on a
+  random subset of splats must reproduce them bit for bit;
+* the image is finite with alpha in [0, 1]; gradients are finite.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.helpers import assert_bits_equal, compare_forward, gpu_forward, rel_close, uniforms_for
+from brush_amd.synthetic import CONFIGS, generate_splats, generate_v_output  # noqa: F401
+
+pytestmark = pytest.mark.gpu
+
+_splats = {}
+
+
+def _scene(k):
+    """The config's splats, generated once per test session."""
+    if k not in _splats:
+        _splats.clear()
+        _splats[k] = generate_splats(CONFIGS[k])
+    return _splats[k]
+
+
+def _check_sort_structure(g, num_tiles):
+    v, m = g["num_visible"], g["num_intersections"]
+    tiles = g["tile_id_from_isect"].astype(np.int64)
+    cg = g["compact_gid_from_isect"].astype(np.int64)
+    assert tiles.shape == (m,) and cg.shape == (m,)
+    assert m == 0 or tiles.max() < num_tiles, "sentinel or out-of-range tile id"
+    d = np.diff(tiles)
+    assert np.all(d >= 0), "tile ids not sorted"
+    same = d == 0
+    assert np.all(np.diff(cg)[same] > 0), "compact ids not increasing inside a tile"
+    gfc = g["global_from_compact_gid"].astype(np.int64)
+    counts = g["intersect_counts"].astype(np.int64)
+    assert np.array_equal(np.bincount(cg, minlength=v)[:v], counts[gfc]), "per-splat entry counts"
+    assert counts.sum() == m
+    depths = g["depths"]
+    assert np.all(np.diff(depths) >= 0), "depths not sorted"
+    assert gfc.size == v and (v == 0 or gfc.max() < counts.size), "global ids out of range"
+    assert np.unique(gfc).size == v, "global ids repeat"
+    # tile offsets are the runs (empty tiles [0, 0])
+    t = np.arange(num_tiles)
+    start = np.searchsorted(tiles, t, "left")
+    end = np.searchsorted(tiles, t, "right")
+    empty = start == end
+    start[empty] = 0
+    end[empty] = 0
+    pre = g["tile_offsets_pre"].reshape(-1, 2).astype(np.int64)
+    assert np.array_equal(pre[:, 0], start) and np.array_equal(pre[:, 1], end), "tile offsets"
+    post = g["tile_offsets"].reshape(-1, 2).astype(np.int64)
+    assert np.array_equal(post[:, 0], start), "post-raster tile starts"
+    assert np.all(post[:, 1] <= end) and np.all(post[:, 1] >= post[:, 0]), "post-raster tile ends"
+
+
+def _check_subset(g, u, tr, sh, opac, flags, seed, size=20000):
+    """Per-splat outputs of a random subset against the restatement run on that subset."""
+    n = tr.shape[0]
+    rng = np.random.default_rng(seed)
+    sub = np.sort(rng.choice(n, size=min(size, n), replace=False))
+    o = O.render_forward(u, tr[sub], sh[sub], opac[sub], flags)
+    assert_bits_equal("subset intersect_counts", g["intersect_counts"][sub], o.intersect_counts)
+    assert_bits_equal("subset max_radius", g["max_radius"][sub], o.max_radius)
+    # projected rows: GPU row of global id x sits at its compact position
+    gfc = g["global_from_compact_gid"].astype(np.int64)
+    pos = np.full(n, -1, np.int64)
+    pos[gfc] = np.arange(gfc.size)
+    sub_vis = sub[o.global_from_compact_gid.astype(np.int64)]  # global ids, in the subset's depth order
+    assert np.all(pos[sub_vis] >= 0), "a splat visible on its own is culled in the full scene"
+    assert_bits_equal("subset projected rows", g["projected"][pos[sub_vis]], o.projected[: o.num_visible])
+    # the tiles each subset splat lands in
+    in_sub = np.zeros(n, bool)
+    in_sub[sub] = True
+    cg = g["compact_gid_from_isect"].astype(np.int64)
+    gids = gfc[cg]
+    keep = in_sub[gids]
+    got = np.lexsort((g["tile_id_from_isect"][keep], gids[keep]))
+    got_pairs = np.stack([gids[keep][got], g["tile_id_from_isect"][keep][got].astype(np.int64)], 1)
+    m = o.num_intersections
+    o_g = sub[o.global_from_compact_gid.astype(np.int64)[o.compact_gid_from_isect[:m].astype(np.int64)]]
+    o_t = o.tile_id_from_isect[:m].astype(np.int64)
+    ref = np.lexsort((o_t, o_g))
+    ref_pairs = np.stack([o_g[ref], o_t[ref]], 1)
+    assert np.array_equal(got_pairs, ref_pairs), "(splat, tile) pairs of the subset"
+
+
+def _check_image(img):
+    assert np.all(np.isfinite(img)), "non-finite pixels"
+    a = img[..., 3]
+    assert a.min() >= 0.0 and a.max() <= 1.0
+    assert img[..., :3].min() >= 0.0
+
+
+def test_config1_full_size_forward_and_backward(gpu):
+    """The north-star workload bit for bit (forward) and to rtol 1e-3 (gradients)."""
+    import torch
+    from brush_amd import render as R
+
+    w_id = 1
+    w = CONFIGS[w_id]
+    print(f"[case] {w.name} forward + backward", flush=True)
+    tr, sh, opac = _scene(w_id)
+    cam = w.camera()
+    u = uniforms_for(cam, w.img_w, w.img_h, w.n, w.sh_degree)
+    g = gpu_forward(u, tr, sh, opac, O.FLAG_BWD_INFO)
+    o = O.render_forward(u, tr, sh, opac, O.FLAG_BWD_INFO)
+    compare_forward(g, o)
+    del g
+    t = torch.from_numpy(tr).to(gpu).requires_grad_(True)
+    s = torch.from_numpy(sh).to(gpu).requires_grad_(True)
+    op = torch.from_numpy(opac).to(gpu).requires_grad_(True)
+    res = R.render_splats_diff(R.Splats(t, s, op), cam, (w.img_w, w.img_h))
+    v_out = generate_v_output(w)
+    res.img.backward(torch.from_numpy(v_out).to(gpu))
+    vc = O.rasterize_backward(o, v_out, O.FLAG_REFINE_WEIGHT)
+    vt, vcoef, vo, vr = O.project_backward(o, tr, sh, opac, vc)
+    rel_close("v_transforms", t.grad.cpu().numpy(), vt, rtol=1e-3, atol_frac=1e-4)
+    rel_close("v_coeffs", s.grad.cpu().numpy(), vcoef, rtol=1e-3, atol_frac=1e-4)
+    rel_close("v_raw_opac", op.grad.cpu().numpy(), vo, rtol=1e-3, atol_frac=1e-4)
+    rel_close("refine", res._cfg.refine_weight.cpu().numpy(), vr, rtol=1e-3, atol_frac=1e-4)
+
+
+def test_config2_clustered_full_size(gpu):
+    """3M clustered splats at 1280x720: the high-overlap intersect / sort stress."""
+    import torch
+    from brush_amd import render as R
+
+    w_id = 2
+    w = CONFIGS[w_id]
+    print(f"[case] {w.name} forward + backward", flush=True)
+    tr, sh, opac = _scene(w_id)
+    cam = w.camera()
+    u = uniforms_for(cam, w.img_w, w.img_h, w.n, w.sh_degree)
+    g = gpu_forward(u, tr, sh, opac, O.FLAG_BWD_INFO)
+    print(f"[case] {w.name}: visible={g['num_visible']} intersections={g['num_intersections']}", flush=True)
+    assert g["num_intersections"] > 20_000_000
+    _check_sort_structure(g, u["tile_bw"] * u["tile_bh"])
+    _check_subset(g, u, tr, sh, opac, O.FLAG_BWD_INFO, seed=2)
+    _check_image(g["out_img"])
+    del g
+    t = torch.from_numpy(tr).to(gpu).requires_grad_(True)
+    s = torch.from_numpy(sh).to(gpu).requires_grad_(True)
+    op = torch.from_numpy(opac).to(gpu).requires_grad_(True)
+    res = R.render_splats_diff(R.Splats(t, s, op), cam, (w.img_w, w.img_h))
+    res.img.backward(torch.from_numpy(generate_v_output(w)).to(gpu))
+    for name, grad in (("v_transforms", t.grad), ("v_coeffs", s.grad), ("v_raw_opac", op.grad)):
+        assert bool(torch.isfinite(grad).all()), name
+        assert bool((grad != 0).any()), name
+
+
+@pytest.mark.parametrize("pose", [0, 7])
+def test_config3_4k_forward_full_size(gpu, pose):
+    """6M splats at 3840x2160, forward only (packed RGBA8), two of the eight poses."""
+    w_id = 3
+    w = CONFIGS[w_id]
+    print(f"[case] {w.name} pose {pose}", flush=True)
+    tr, sh, opac = _scene(w_id)
+    cam = w.camera(pose, 8)
+    u = uniforms_for(cam, w.img_w, w.img_h, w.n, w.sh_degree)
+    g = gpu_forward(u, tr, sh, opac, 0)
+    print(f"[case] {w.name} pose {pose}: visible={g['num_visible']} intersections={g['num_intersections']}",
+          flush=True)
+    _check_sort_structure(g, u["tile_bw"] * u["tile_bh"])
+    _check_subset(g, u, tr, sh, opac, 0, seed=30 + pose, size=10000)
+    assert g["out_img"].shape == (w.img_h, w.img_w)
