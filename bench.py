@@ -1,17 +1,26 @@
-"""Benchmark: forward + backward rasterization on one MI355X.
+"""Benchmark: the rasterizer on one MI355X.
 
-One step = the differentiable render of BASELINE.json's north-star workload
-(config 1: 1M SH-degree-3 splats at 1920x1080, f = 1100, camera at distance 4)
-followed by its backward for a fixed upstream image gradient ~ N(0, 1):
-project + cull, depth sort, scan, project_visible, map, tile sort, tile
-offsets, blend, rasterize backward and project backward, all through
-libbrush_hip.so.  Inputs are resident in HBM before the timed region.
+The default run is BASELINE.json's north-star workload, config 1: one step is
+the differentiable render of 1M SH-degree-3 splats at 1920x1080 (f = 1100,
+camera at distance 4) followed by its backward for a fixed upstream image
+gradient ~ N(0, 1): project + cull, depth sort, scan, project_visible, map,
+tile sort, tile offsets, blend, rasterize backward and project backward, all
+through libbrush_hip.so.  Inputs are resident in HBM before the timed region.
+
+``--config 0|2`` times the same forward + backward on those workloads,
+``--config 3`` the forward-only render of the eight 3840x2160 poses (one step =
+eight views), ``--config 4`` one full training step (render, L1 + SSIM loss,
+backward, AdamScaled on every splat parameter) at 1600x1064.
 
 Prints one JSON line (the driver's contract).  ``roofline`` reports the kernel
-with the largest share of the step, its algorithmic bytes per launch divided by
-its mean launch time (HIP events on the library's stream), against 8 TB/s.
-``cpu_baseline`` times the C restatement (oracle/liboracle.so) on the box's
-host cores over a bounded sample of the same scene.
+with the largest share of the step: its algorithmic bytes per launch divided by
+its mean launch time (HIP events on the library's stream, recorded in the timed
+region around that kernel only), against 8 TB/s; ``traffic`` is the HBM bytes
+per launch that rocprofv3 FETCH_SIZE / WRITE_SIZE measured for it
+(profiles/cfg1_hbm_traffic.md).  ``kernels`` is a per-kernel table from a short
+separate pass with every launch bracketed by events.  ``cpu_baseline`` times the
+C restatement (oracle/liboracle.so) on the box's host cores over a bounded
+sample of the same workload.
 """
 from __future__ import annotations
 
@@ -28,6 +37,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "cfg1_hbm_traffic.md")
+METRIC_CFG1 = "fwd+bwd rasterize ms & Mpix/s, 1M Gaussians SH3 @1080p; % HBM roofline"
 
 
 def measured_traffic(kernel: str, workload: str):
@@ -47,8 +57,7 @@ def measured_traffic(kernel: str, workload: str):
     return None
 
 
-def algorithmic_bytes(name: str, n: int, v: int, m: int, m_post: int, t: int, p: int, c: int,
-                      depth_passes: int, tile_passes: int) -> float:
+def algorithmic_bytes(name: str, n: int, v: int, m: int, m_post: int, t: int, p: int, c: int) -> float:
     """Compulsory HBM bytes of one launch: every input read once, every output
     written once (counts per launch; sort passes are separate launches)."""
     if name == "project_forward":
@@ -62,13 +71,21 @@ def algorithmic_bytes(name: str, n: int, v: int, m: int, m_post: int, t: int, p:
     if name == "tile_offsets":
         return 4.0 * m + 8.0 * t
     if name == "rasterize":
-        return 44.0 * m + 16.0 * p + 4.0 * v + 16.0 * t  # id+row per isect, image, visible, offsets
+        return 44.0 * m_post + 16.0 * p + 4.0 * v + 16.0 * t  # id+row per used isect, image, visible, offsets
     if name == "rasterize_backward":
         return 44.0 * m_post + 32.0 * p + 40.0 * m_post  # id+row, image+grad image, atomics per isect
     if name == "project_backward":
-        return (40 + 12 * c + 4 + 4) * n + 44.0 * v + (40 + 12 * c + 8) * n
-    if name == "invert_permutation":
-        return 8.0 * v
+        # gradient lanes [N, 11] in, dense rows out; parameters read for the
+        # splats that have gradient (the visible ones, an upper bound)
+        return 44.0 * n + (40 + 12 * c + 4) * v + (40 + 12 * c + 8) * n
+    if name == "image_loss_forward":
+        return 28.0 * p                                  # RGB + packed GT in, RGB map out
+    if name == "image_loss_backward":
+        return 44.0 * p                                  # RGB, GT, chain in; RGBA gradient out
+    if name == "adam_step":
+        # three launches per step (transforms, SH with per-row second moment,
+        # opacity): the mean per launch
+        return (28.0 * 10 * n + (20.0 * 3 * c + 8.0) * n + 28.0 * n) / 3.0
     return 0.0
 
 
@@ -87,10 +104,12 @@ def sort_bytes_per_launch(name: str, passes: float, n: int, m: int) -> float:
     return 0.0
 
 
-def cpu_baseline(workload, transforms, sh, opac, v_out, min_seconds: float = 10.0, max_reps: int = 20) -> dict:
+def cpu_baseline(mode: str, workload, transforms, sh, opac, v_out, gt, min_seconds: float = 10.0,
+                 max_reps: int = 20) -> dict:
     """Times the C restatement (oracle/liboracle.so, OpenMP over splats and
     tiles) on the same full workload, repeated until ``min_seconds`` of CPU
-    work; reports the median repetition in Mpix/s."""
+    work; reports the median repetition in Mpix/s.  Forward-only workloads
+    time one pose per repetition."""
     from brush_amd.camera import project_uniforms
     from oracle import oracle as O
 
@@ -98,20 +117,43 @@ def cpu_baseline(workload, transforms, sh, opac, v_out, min_seconds: float = 10.
     threads = max(1, min(threads, os.cpu_count() or 1))
     O.set_threads(threads)
     w = workload
-    u = project_uniforms(w.camera(), w.img_w, w.img_h, w.n, w.sh_degree)
+    u = project_uniforms(w.camera(0, 8 if mode == "forward" else 1), w.img_w, w.img_h, w.n, w.sh_degree)
+    h, wd = w.img_h, w.img_w
+    p = [transforms.copy(), sh.copy(), opac.copy()] if mode == "train" else None
+    m1 = [np.zeros_like(x) for x in p] if p else None
+    m2 = [np.zeros_like(p[0]), np.zeros((w.n,), np.float32), np.zeros_like(p[2])] if p else None
     times = []
     t_start = time.perf_counter()
     while len(times) < max_reps and (time.perf_counter() - t_start < min_seconds or len(times) < 2):
         t0 = time.perf_counter()
-        fwd = O.render_forward(u, transforms, sh, opac, O.FLAG_BWD_INFO)
-        vc = O.rasterize_backward(fwd, v_out, O.FLAG_REFINE_WEIGHT)
-        O.project_backward(fwd, transforms, sh, opac, vc)
+        if mode == "forward":
+            O.render_forward(u, transforms, sh, opac, 0)
+        elif mode == "fwd_bwd":
+            fwd = O.render_forward(u, transforms, sh, opac, O.FLAG_BWD_INFO)
+            vc = O.rasterize_backward(fwd, v_out, O.FLAG_REFINE_WEIGHT)
+            O.project_backward(fwd, transforms, sh, opac, vc)
+        else:
+            fwd = O.render_forward(u, p[0], p[1], p[2], O.FLAG_BWD_INFO)
+            cfg = O.loss_config(0.8, -0.2)
+            O.image_loss_forward(fwd.out_img, 3, gt, cfg)
+            chain = np.full((h, wd, 3), np.float32(1.0 / (3 * h * wd)), np.float32)
+            v_img = O.image_loss_backward(fwd.out_img, 3, gt, cfg, chain)
+            vc = O.rasterize_backward(fwd, v_img, O.FLAG_REFINE_WEIGHT)
+            vt, vcoef, vo, _ = O.project_backward(fwd, p[0], p[1], p[2], vc)
+            step = len(times) + 1
+            sc_t = np.array([1.6e-4] * 3 + [2e-3] * 4 + [7e-3] * 3, np.float32)
+            sc_c = np.repeat(np.array([1.0] + [0.1] * (w.num_coeffs - 1), np.float32), 3)
+            O.adam_scaled_step(p[0], vt, m1[0], m2[0], sc_t, False, 1.0, step)
+            O.adam_scaled_step(p[1], vcoef, m1[1], m2[1], sc_c, True, 2.5e-3, step)
+            O.adam_scaled_step(p[2], vo, m1[2], m2[2], None, False, 0.012, step)
         times.append(time.perf_counter() - t0)
     dt = float(np.median(times))
     px = w.img_w * w.img_h
+    what = {"forward": "forward-only render of one pose", "fwd_bwd": "fwd+bwd step",
+            "train": "training step (render, loss, backward, Adam)"}[mode]
     return {"value": round(px / dt / 1e6, 4), "unit": "Mpix/s", "cores": threads, "kind": "port",
             "ms_per_step": round(dt * 1000.0, 2), "reps": len(times),
-            "sample": f"the full {w.name} fwd+bwd step ({w.n} splats, {w.img_w}x{w.img_h}), median of "
+            "sample": f"the full {w.name} {what} ({w.n} splats, {w.img_w}x{w.img_h}), median of "
                       f"{len(times)} repetitions"}
 
 
@@ -138,35 +180,58 @@ def main():
 
     from brush_amd import _lib
     from brush_amd import render as R
-    from brush_amd.synthetic import CONFIGS, generate_splats, generate_v_output
+    from brush_amd.synthetic import CONFIGS, generate_splats, generate_target, generate_v_output
 
     w = CONFIGS[args.config]
+    mode = "train" if args.config == 4 else ("forward" if w.forward_only else "fwd_bwd")
+    poses = 8 if mode == "forward" else 1
     t_gen = time.perf_counter()
     tr, sh, opac = generate_splats(w)
-    v_out = generate_v_output(w)
+    v_out = generate_v_output(w) if mode == "fwd_bwd" else None
+    gt = generate_target(w) if mode == "train" else None
     t_gen = time.perf_counter() - t_gen
     dev = torch.device("cuda:0")
-    t = torch.from_numpy(tr).to(dev).requires_grad_(True)
-    s = torch.from_numpy(sh).to(dev).requires_grad_(True)
-    o = torch.from_numpy(opac).to(dev).requires_grad_(True)
-    vo = torch.from_numpy(v_out).to(dev)
+    t = torch.from_numpy(tr).to(dev).requires_grad_(mode == "fwd_bwd")
+    s = torch.from_numpy(sh).to(dev).requires_grad_(mode == "fwd_bwd")
+    o = torch.from_numpy(opac).to(dev).requires_grad_(mode == "fwd_bwd")
+    vo = torch.from_numpy(v_out).to(dev) if v_out is not None else None
+    gt_dev = torch.from_numpy(gt.view(np.int32)).to(dev) if gt is not None else None
     splats = R.Splats(t, s, o)
-    cam = w.camera()
+    cams = [w.camera(k, poses) for k in range(poses)]
     img_size = (w.img_w, w.img_h)
     ctx = _lib.context(0)
+    trainer = None
+    if mode == "train":
+        from brush_amd.train import SplatTrainer
 
-    stats = {}
+        trainer = SplatTrainer()
+
+    stats = {"num_visible": 0, "num_intersections": 0}
 
     def step():
-        t.grad = None
-        s.grad = None
-        o.grad = None
-        res = R.render_splats_diff(splats, cam, img_size, (0.0, 0.0, 0.0))
-        res.img.backward(vo)
-        stats["num_visible"] = res.num_visible
-        stats["num_intersections"] = res.aux.num_intersections
-        stats["out"] = res
-        return res
+        if mode == "fwd_bwd":
+            t.grad = None
+            s.grad = None
+            o.grad = None
+            res = R.render_splats_diff(splats, cams[0], img_size, (0.0, 0.0, 0.0))
+            res.img.backward(vo)
+            stats["num_visible"] = res.num_visible
+            stats["num_intersections"] = res.aux.num_intersections
+            stats["tile_offsets"] = res.aux.tile_offsets
+        elif mode == "forward":
+            vis = isect = 0
+            for cam in cams:
+                out = R.render(cam, img_size, t, s, o, raster_pass=R.RasterPass.Forward)
+                vis += out.aux.num_visible
+                isect += out.aux.num_intersections
+                stats["tile_offsets"] = out.aux.tile_offsets
+                out.state.release()
+            stats["num_visible"] = vis / poses
+            stats["num_intersections"] = isect / poses
+        else:
+            res = trainer.step(splats, cams[0], gt_dev)
+            stats["num_visible"] = res["num_visible"]
+            stats["loss"] = res["loss"]
 
     if args.calibrate_copy_mib > 0:
         words = args.calibrate_copy_mib * (1 << 18)
@@ -180,12 +245,18 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    res = stats["out"]
-    m_post = int((res.aux.tile_offsets[..., 1].long() - res.aux.tile_offsets[..., 0].long()).sum().item())
-    stats.pop("out")
-    del res
+    m_post = 0
+    if "tile_offsets" in stats:
+        to = stats.pop("tile_offsets")
+        m_post = int((to[..., 1].long() - to[..., 0].long()).sum().item())
+    if mode == "train":
+        # the training step's intersection count: one forward at the current parameters
+        out = R.render(cams[0], img_size, t, s, o, raster_pass=R.RasterPass.Backward)
+        stats["num_intersections"] = out.aux.num_intersections
+        m_post = int((out.aux.tile_offsets[..., 1].long() - out.aux.tile_offsets[..., 0].long()).sum().item())
+        out.state.release()
 
-    n, v, m = w.n, stats["num_visible"], stats["num_intersections"]
+    n, v, m = w.n, int(stats["num_visible"]), int(stats["num_intersections"])
     tiles = ((w.img_w + 15) // 16) * ((w.img_h + 15) // 16)
     c = w.num_coeffs
     pixels = w.img_w * w.img_h
@@ -196,9 +267,9 @@ def main():
             per_step_launches = launches / steps
             avg = total / max(launches, 1)
             if name.endswith("_onesweep") or name.endswith("_hist"):
-                b = sort_bytes_per_launch(name, per_step_launches, n, m)
+                b = sort_bytes_per_launch(name, per_step_launches / poses, n, m)
             else:
-                b = algorithmic_bytes(name, n, v, m, m_post, tiles, pixels, c, 0, 0)
+                b = algorithmic_bytes(name, n, v, m, m_post, tiles, pixels, c)
             table[name] = {"launches_per_step": round(per_step_launches, 2), "avg_ms": round(avg, 4),
                            "ms_per_step": round(total / steps, 4),
                            "algorithmic_mb": round(b / 1e6, 2) if b else None,
@@ -230,7 +301,7 @@ def main():
     timed = kernel_table(ctx.read_timings(), args.steps) if dominant else {}
     ctx.set_timing(False)
     ms = (t1 - t0) * 1000.0 / args.steps
-    mpix = pixels / (ms / 1000.0) / 1e6
+    mpix = pixels * poses / (ms / 1000.0) / 1e6
 
     roofline = None
     if dominant and dominant in timed:
@@ -244,12 +315,23 @@ def main():
     cpu = None
     if args.cpu_seconds > 0:
         try:
-            cpu = cpu_baseline(w, tr, sh, opac, v_out, args.cpu_seconds)
+            cpu = cpu_baseline(mode, w, tr, sh, opac, v_out, gt, args.cpu_seconds)
         except Exception as e:  # the baseline is reported, never required
             cpu = {"error": str(e)}
 
+    metric = {"fwd_bwd": METRIC_CFG1 if args.config == 1 else f"fwd+bwd rasterize ms & Mpix/s, {w.name}",
+              "forward": f"forward render ms per view & Mpix/s, {w.name} ({poses} poses per step)",
+              "train": f"training step ms & Mpix/s (render, L1+SSIM, backward, AdamScaled), {w.name}"}[mode]
+    config = {"workload": w.name, "splats": w.n, "sh_degree": w.sh_degree, "img": [w.img_w, w.img_h],
+              "focal": round(w.focal, 3), "distance": w.distance, "num_visible": v, "num_intersections": m,
+              "num_intersections_post_raster": m_post, "poses": poses,
+              "sort": "two-stage: depth sort of visible splats, then stable tile-id sort of (tile, depth-rank) "
+                      "pairs (equivalent to a 64-bit tile|depth key sort)",
+              "parallelism": "single GPU"}
+    if mode == "train":
+        config["loss"] = round(float(stats["loss"].item()), 6)
     line = {
-        "metric": "fwd+bwd rasterize ms & Mpix/s, 1M Gaussians SH3 @1080p; % HBM roofline",
+        "metric": metric,
         "value": round(mpix, 2),
         "unit": "Mpix/s",
         "n_gpus": 1,
@@ -261,12 +343,7 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded SplitMix64 generator, brush_amd/synthetic.py)",
-        "config": {"workload": w.name, "splats": w.n, "sh_degree": w.sh_degree, "img": [w.img_w, w.img_h],
-                   "focal": w.focal, "distance": w.distance, "num_visible": v, "num_intersections": m,
-                   "num_intersections_post_raster": m_post,
-                   "sort": "two-stage: depth sort of visible splats, then stable tile-id sort of (tile, depth-rank) "
-                           "pairs (equivalent to a 64-bit tile|depth key sort)",
-                   "parallelism": "single GPU"},
+        "config": config,
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": kernels,

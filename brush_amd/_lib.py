@@ -38,7 +38,8 @@ EXPORTED = [
     "bh_ctx_set_timing_filter",
     "bh_ctx_read_timings", "bh_ctx_reset_timings", "bh_ctx_workspace_bytes", "bh_radix_argsort",
     "bh_prefix_sum", "bh_get_tile_offsets", "bh_render_forward", "bh_fwd_state_info",
-    "bh_fwd_state_release", "bh_rasterize_backward", "bh_render_backward", "bh_project_backward", "bh_copy_to_host",
+    "bh_fwd_state_release", "bh_rasterize_backward", "bh_render_backward", "bh_project_backward",
+    "bh_image_loss_forward", "bh_image_loss_backward", "bh_adam_scaled_step", "bh_copy_to_host",
     "bh_copy_to_device", "bh_copy_device", "bh_device_alloc", "bh_device_free", "bh_synchronize",
 ]
 
@@ -116,6 +117,19 @@ class FwdInfo(ctypes.Structure):
     ]
 
 
+class ImageLossConfig(ctypes.Structure):
+    """bh_image_loss_config (include/brush_hip.h)."""
+
+    _fields_ = [("l1_weight", ctypes.c_float), ("ssim_weight", ctypes.c_float), ("composite", ctypes.c_uint32),
+                ("background", ctypes.c_float * 3), ("mask", ctypes.c_uint32)]
+
+
+class AdamConfig(ctypes.Structure):
+    """bh_adam_config (include/brush_hip.h)."""
+
+    _fields_ = [("beta_1", ctypes.c_float), ("beta_2", ctypes.c_float), ("epsilon", ctypes.c_float)]
+
+
 class KernelTiming(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char * 48), ("launches", ctypes.c_uint32), ("total_ms", ctypes.c_double)]
 
@@ -157,6 +171,10 @@ def lib() -> ctypes.CDLL:
         "bh_fwd_state_release": (None, [P]),
         "bh_rasterize_backward": (S, [P, P, P, P, P, U32, P, U32, U32, P, U32, P]),
         "bh_render_backward": (S, [P, P, P, P, P, P, P, P, P, U32, P, P, P, P]),
+        "bh_image_loss_forward": (S, [P, P, U32, U32, P, U32, U32, ctypes.POINTER(ImageLossConfig), P]),
+        "bh_image_loss_backward": (S, [P, P, U32, U32, P, U32, U32, ctypes.POINTER(ImageLossConfig), P, P]),
+        "bh_adam_scaled_step": (S, [P, P, P, P, P, P, U32, U32, U32, ctypes.c_float, U32,
+                                    ctypes.POINTER(AdamConfig)]),
         "bh_project_backward": (S, [P, UP, P, P, P, P, P, U32, P, P, P, P]),
         "bh_copy_to_host": (S, [P, P, P, U64]),
         "bh_copy_to_device": (S, [P, P, P, U64]),

@@ -564,6 +564,47 @@ bh_status bh_render_backward(bh_ctx* ctx, const bh_fwd_state* state, const float
     return check_launch(ctx, "project_backward");
 }
 
+static bh_status check_loss_args(bh_ctx* ctx, const float* pred, uint32_t pred_stride, uint32_t channels,
+                                 const uint32_t* gt, uint32_t w, uint32_t h, const bh_image_loss_config* cfg) {
+    if (w == 0 || h == 0) return set_error(ctx, BH_ERR_INVALID_ARG, "image loss: zero image size");
+    if (channels != 3 && channels != 4) return set_error(ctx, BH_ERR_SHAPE, "image loss: channels must be 3 or 4");
+    if (pred_stride < channels) return set_error(ctx, BH_ERR_SHAPE, "image loss: pred_stride < channels");
+    if (!pred || !gt || !cfg) return set_error(ctx, BH_ERR_INVALID_ARG, "image loss: null argument");
+    return BH_OK;
+}
+
+bh_status bh_image_loss_forward(bh_ctx* ctx, const float* pred, uint32_t pred_stride, uint32_t channels,
+                                const uint32_t* gt_packed, uint32_t img_w, uint32_t img_h,
+                                const bh_image_loss_config* cfg, float* loss_map) {
+    if (!ctx) return BH_ERR_INVALID_ARG;
+    BH_TRY(check_loss_args(ctx, pred, pred_stride, channels, gt_packed, img_w, img_h, cfg));
+    if (!loss_map) return set_error(ctx, BH_ERR_INVALID_ARG, "image loss: null loss map");
+    launch_image_loss_forward(ctx, pred, pred_stride, channels, gt_packed, img_w, img_h, *cfg, loss_map);
+    return check_launch(ctx, "image_loss_forward");
+}
+
+bh_status bh_image_loss_backward(bh_ctx* ctx, const float* pred, uint32_t pred_stride, uint32_t channels,
+                                 const uint32_t* gt_packed, uint32_t img_w, uint32_t img_h,
+                                 const bh_image_loss_config* cfg, const float* dl_dmap, float* dl_dpred) {
+    if (!ctx) return BH_ERR_INVALID_ARG;
+    BH_TRY(check_loss_args(ctx, pred, pred_stride, channels, gt_packed, img_w, img_h, cfg));
+    if (!dl_dmap || !dl_dpred) return set_error(ctx, BH_ERR_INVALID_ARG, "image loss: null gradient buffer");
+    launch_image_loss_backward(ctx, pred, pred_stride, channels, gt_packed, img_w, img_h, *cfg, dl_dmap, dl_dpred);
+    return check_launch(ctx, "image_loss_backward");
+}
+
+bh_status bh_adam_scaled_step(bh_ctx* ctx, float* param, const float* grad, float* moment_1, float* moment_2,
+                              const float* scaling, uint32_t rows, uint32_t row_len, uint32_t reduce_moment_2,
+                              float lr, uint32_t time, const bh_adam_config* cfg) {
+    if (!ctx) return BH_ERR_INVALID_ARG;
+    if (!cfg) return set_error(ctx, BH_ERR_INVALID_ARG, "adam: null config");
+    if (time == 0) return set_error(ctx, BH_ERR_INVALID_ARG, "adam: time counts steps from 1");
+    if ((uint64_t)rows * row_len == 0) return BH_OK;
+    if (!param || !grad || !moment_1 || !moment_2) return set_error(ctx, BH_ERR_INVALID_ARG, "adam: null buffer");
+    return launch_adam_step(ctx, param, grad, moment_1, moment_2, scaling, rows, row_len, reduce_moment_2 != 0, lr,
+                            time, *cfg);
+}
+
 bh_status bh_copy_to_host(bh_ctx* ctx, void* dst, const void* src, uint64_t bytes) {
     if (!ctx || (bytes && (!dst || !src))) return BH_ERR_INVALID_ARG;
     if (!bytes) return BH_OK;

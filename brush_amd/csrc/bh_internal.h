@@ -40,6 +40,19 @@ struct TimingTotal {
     double total_ms = 0.0;
 };
 
+// loss.hip
+void launch_image_loss_forward(bh_ctx* ctx, const float* pred, uint32_t stride, uint32_t channels,
+                               const uint32_t* gt, uint32_t w, uint32_t h, const bh_image_loss_config& cfg,
+                               float* map);
+void launch_image_loss_backward(bh_ctx* ctx, const float* pred, uint32_t stride, uint32_t channels,
+                                const uint32_t* gt, uint32_t w, uint32_t h, const bh_image_loss_config& cfg,
+                                const float* dl_dmap, float* dl_dpred);
+
+// adam.hip
+bh_status launch_adam_step(bh_ctx* ctx, float* param, const float* grad, float* m1, float* m2,
+                           const float* scaling, uint32_t rows, uint32_t row_len, bool reduce, float lr,
+                           uint32_t time, const bh_adam_config& cfg);
+
 }  // namespace bh
 
 struct bh_ctx {

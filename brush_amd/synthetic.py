@@ -171,3 +171,17 @@ def generate_v_output(w: Workload, channels: int = 4) -> np.ndarray:
     idx = np.arange(2 * count, dtype=np.uint64)
     z = splitmix64(w.seed + 1000, idx)
     return _normal(z[0::2], z[1::2]).astype(np.float32).reshape(w.img_h, w.img_w, channels)
+
+
+def generate_target(w: Workload, block: int = 8) -> np.ndarray:
+    """The training target of config 4: RGB uniform in [0, 1], constant over
+    block x block pixel squares, drawn with SplitMix64 from seed + 2000 (one
+    draw per block and channel, row-major over blocks), quantised like a
+    decoded 8-bit image (round(x * 255)) and packed RGBA8 with alpha 255
+    (r in the low byte).  Returns uint32 [H, W]."""
+    bh, bw = (w.img_h + block - 1) // block, (w.img_w + block - 1) // block
+    z = splitmix64(w.seed + 2000, np.arange(bh * bw * 3, dtype=np.uint64))
+    rgb = _uniform(z).reshape(bh, bw, 3)
+    q = np.round(rgb * 255.0).astype(np.uint32)
+    q = np.repeat(np.repeat(q, block, axis=0), block, axis=1)[: w.img_h, : w.img_w]
+    return (q[..., 0] | (q[..., 1] << 8) | (q[..., 2] << 16) | np.uint32(255 << 24)).astype(np.uint32)

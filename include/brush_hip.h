@@ -107,6 +107,25 @@ typedef struct bh_fwd_info {
     const uint32_t* tile_offsets_pre;  /* [TY,TX,2] before rasterize shrinks */
 } bh_fwd_info;
 
+/* Image loss configuration: brush-loss ImageLossConfig
+ * (crates/brush-loss/src/lib.rs:927-941).  composite != 0 composites GT over
+ * `background` (gt + (1 - gt.a) * bg); mask != 0 multiplies the loss map by
+ * gt.a. */
+typedef struct bh_image_loss_config {
+    float l1_weight;
+    float ssim_weight;
+    uint32_t composite;
+    float background[3];
+    uint32_t mask;
+} bh_image_loss_config;
+
+/* AdamScaledConfig (crates/brush-train/src/adam_scaled.rs:57-69). */
+typedef struct bh_adam_config {
+    float beta_1;
+    float beta_2;
+    float epsilon;
+} bh_adam_config;
+
 /* ---- context ------------------------------------------------------------ */
 
 /* Create a context on HIP device `device` with the null stream.
@@ -219,6 +238,37 @@ bh_status bh_render_backward(bh_ctx* ctx, const bh_fwd_state* state, const float
                              const float* transforms, const float* sh_coeffs,
                              const float* raw_opacities, const float* v_output, uint32_t flags,
                              float* v_transforms, float* v_coeffs, float* v_raw_opac, float* v_refine);
+
+/* ---- training: image loss and optimizer ------------------------------------ */
+
+/* Fused L1 + SSIM loss map.  Replaces LossOps::image_loss_forward
+ * (crates/brush-loss/src/lib.rs:946-963; kernels lib.rs:228-555).
+ * pred: f32 [H, W, pred_stride] of which the first `channels` (3 or 4) are
+ * compared; gt_packed: u32 [H, W] RGBA8 (r in the low byte).  loss_map:
+ * f32 [H, W, channels].  With channels == 4 the alpha channel of the map is
+ * |pred.a - gt.a|.  ssim_weight == 0 selects the L1-only path. */
+bh_status bh_image_loss_forward(bh_ctx* ctx, const float* pred, uint32_t pred_stride, uint32_t channels,
+                                const uint32_t* gt_packed, uint32_t img_w, uint32_t img_h,
+                                const bh_image_loss_config* cfg, float* loss_map);
+/* VJP of bh_image_loss_forward.  Replaces LossOps::image_loss_backward
+ * (lib.rs:952-957; kernels lib.rs:280-893).  dl_dmap: f32 [H, W, channels];
+ * dl_dpred: f32 [H, W, pred_stride], every element written (zeros in the
+ * channels past `channels`), so it can be fed to the rasterizer's backward
+ * as the gradient of an RGBA render. */
+bh_status bh_image_loss_backward(bh_ctx* ctx, const float* pred, uint32_t pred_stride, uint32_t channels,
+                                 const uint32_t* gt_packed, uint32_t img_w, uint32_t img_h,
+                                 const bh_image_loss_config* cfg, const float* dl_dmap, float* dl_dpred);
+/* One AdamScaled step on a [rows, row_len] parameter, in place.  Replaces
+ * AdamScaled::step (crates/brush-train/src/adam_scaled.rs:216-383).
+ * moment_1 has the parameter's shape; moment_2 has it too, or [rows] when
+ * reduce_moment_2 != 0 (mean of grad^2 over each row, the SH setting of
+ * train.rs:966-990).  scaling: per-column factors [row_len] or NULL; the
+ * decrement is step * (scaling[col] * lr).  time is the step count including
+ * this step (1 on the first step, when the moments are initialised from the
+ * gradient and their previous contents are ignored). */
+bh_status bh_adam_scaled_step(bh_ctx* ctx, float* param, const float* grad, float* moment_1, float* moment_2,
+                              const float* scaling, uint32_t rows, uint32_t row_len, uint32_t reduce_moment_2,
+                              float lr, uint32_t time, const bh_adam_config* cfg);
 
 /* Project backward.  Replaces SplatBwdOps::project_bwd
  * (brush-render-bwd/src/burn_glue.rs:79-172, impl render_bwd.rs:298-447,

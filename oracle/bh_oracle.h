@@ -15,8 +15,10 @@
  * above the function):
  *   or_project_forward, or_project_visible, or_map_intersects,
  *   or_stable_sort, or_prefix_sum, or_tile_offsets, or_rasterize,
- *   or_rasterize_reference, or_rasterize_backward, or_project_backward:
- *   pinned (see tests/test_oracle.py).
+ *   or_rasterize_reference, or_rasterize_backward, or_project_backward,
+ *   or_gauss_taps, or_image_loss_forward, or_image_loss_backward,
+ *   or_adam_scaled_step: pinned (see tests/test_oracle.py and
+ *   tests/test_oracle_train.py).
  */
 #ifndef BH_ORACLE_H
 #define BH_ORACLE_H
@@ -78,6 +80,17 @@ void or_project_backward(const bh_project_uniforms* u, const float* transforms,
                          uint32_t num_splats, uint32_t sh_degree, uint32_t mip,
                          const float* v_combined, float* v_transforms, float* v_coeffs,
                          float* v_raw_opac, float* v_refine);
+
+/* bh_oracle_train.c: the image loss and the optimizer step. */
+void or_gauss_taps(float* taps6);
+void or_image_loss_forward(const float* pred, uint32_t stride, uint32_t channels, const uint32_t* gt,
+                           uint32_t w, uint32_t h, const bh_image_loss_config* cfg, float* map);
+void or_image_loss_backward(const float* pred, uint32_t stride, uint32_t channels, const uint32_t* gt,
+                            uint32_t w, uint32_t h, const bh_image_loss_config* cfg, const float* dl_dmap,
+                            float* dl_dpred);
+void or_adam_scaled_step(float* param, const float* grad, float* m1, float* m2, const float* scaling,
+                         uint32_t rows, uint32_t row_len, uint32_t reduce, float lr, uint32_t time,
+                         const bh_adam_config* cfg);
 
 #ifdef __cplusplus
 }

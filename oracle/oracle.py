@@ -47,6 +47,30 @@ class Uniforms(ctypes.Structure):
     ]
 
 
+class LossConfig(ctypes.Structure):
+    """bh_image_loss_config (include/brush_hip.h)."""
+
+    _fields_ = [("l1_weight", ctypes.c_float), ("ssim_weight", ctypes.c_float), ("composite", ctypes.c_uint32),
+                ("background", ctypes.c_float * 3), ("mask", ctypes.c_uint32)]
+
+
+class AdamConfig(ctypes.Structure):
+    """bh_adam_config (include/brush_hip.h)."""
+
+    _fields_ = [("beta_1", ctypes.c_float), ("beta_2", ctypes.c_float), ("epsilon", ctypes.c_float)]
+
+
+def loss_config(l1_weight: float, ssim_weight: float, composite_bg=None, mask: bool = False) -> LossConfig:
+    c = LossConfig()
+    c.l1_weight = l1_weight
+    c.ssim_weight = ssim_weight
+    c.composite = 0 if composite_bg is None else 1
+    for i in range(3):
+        c.background[i] = 0.0 if composite_bg is None else float(composite_bg[i])
+    c.mask = 1 if mask else 0
+    return c
+
+
 def make_uniforms(d: dict) -> Uniforms:
     u = Uniforms()
     for i, v in enumerate(d["viewmat"]):
@@ -88,6 +112,11 @@ def lib():
         L.or_rasterize_reference.argtypes = [P, U32, U32, U32, P, U32, P]
         L.or_rasterize_backward.argtypes = [U32, U32, U32, U32, P, P, P, P, P, U32, P, U32, P]
         L.or_project_backward.argtypes = [UP, P, P, P, P, U32, U32, U32, U32, P, P, P, P, P]
+        L.or_gauss_taps.argtypes = [P]
+        L.or_image_loss_forward.argtypes = [P, U32, U32, P, U32, U32, ctypes.POINTER(LossConfig), P]
+        L.or_image_loss_backward.argtypes = [P, U32, U32, P, U32, U32, ctypes.POINTER(LossConfig), P, P]
+        L.or_adam_scaled_step.argtypes = [P, P, P, P, P, U32, U32, U32, ctypes.c_float, U32,
+                                          ctypes.POINTER(AdamConfig)]
         _lib = L
     return _lib
 
@@ -274,3 +303,46 @@ def project_backward(fwd: ForwardResult, transforms, sh_coeffs, raw_opac, v_comb
                               _p(np.ascontiguousarray(v_combined, dtype=np.float32)),
                               _p(v_t), _p(v_c), _p(v_o), _p(v_r))
     return v_t, v_c, v_o, v_r
+
+
+# ---- training step: image loss and AdamScaled (bh_oracle_train.c) ----------------------------------
+
+def gauss_taps() -> np.ndarray:
+    t = np.zeros(6, np.float32)
+    lib().or_gauss_taps(_p(t))
+    return t
+
+
+def image_loss_forward(pred: np.ndarray, channels: int, gt_packed: np.ndarray, cfg: LossConfig) -> np.ndarray:
+    """pred f32 [H, W, stride], gt u32 [H, W] -> loss map f32 [H, W, channels]."""
+    pred = np.ascontiguousarray(pred, dtype=np.float32)
+    h, w, stride = pred.shape
+    gt = np.ascontiguousarray(gt_packed, dtype=np.uint32)
+    out = np.empty((h, w, channels), np.float32)
+    lib().or_image_loss_forward(_p(pred), stride, channels, _p(gt), w, h, ctypes.byref(cfg), _p(out))
+    return out
+
+
+def image_loss_backward(pred: np.ndarray, channels: int, gt_packed: np.ndarray, cfg: LossConfig,
+                        dl_dmap: np.ndarray) -> np.ndarray:
+    """-> dl_dpred f32 [H, W, stride] (zeros past `channels`)."""
+    pred = np.ascontiguousarray(pred, dtype=np.float32)
+    h, w, stride = pred.shape
+    gt = np.ascontiguousarray(gt_packed, dtype=np.uint32)
+    dmap = np.ascontiguousarray(dl_dmap, dtype=np.float32)
+    out = np.empty((h, w, stride), np.float32)
+    lib().or_image_loss_backward(_p(pred), stride, channels, _p(gt), w, h, ctypes.byref(cfg), _p(dmap), _p(out))
+    return out
+
+
+def adam_scaled_step(param: np.ndarray, grad: np.ndarray, m1: np.ndarray, m2: np.ndarray, scaling, reduce: bool,
+                     lr: float, time: int, beta_1: float = 0.9, beta_2: float = 0.999, epsilon: float = 1e-15):
+    """In place on param, m1, m2 (f32, C-contiguous); param viewed as [rows, row_len]."""
+    rows = param.shape[0]
+    row_len = int(np.prod(param.shape[1:])) if param.ndim > 1 else 1
+    cfg = AdamConfig()
+    cfg.beta_1, cfg.beta_2, cfg.epsilon = beta_1, beta_2, epsilon
+    sc = None if scaling is None else np.ascontiguousarray(scaling, dtype=np.float32).reshape(-1)
+    g = np.ascontiguousarray(grad, dtype=np.float32)
+    lib().or_adam_scaled_step(_p(param), _p(g), _p(m1), _p(m2), _p(sc) if sc is not None else None, rows, row_len,
+                              int(reduce), float(lr), int(time), ctypes.byref(cfg))
