@@ -86,7 +86,8 @@ def test_image_loss_autograd(gpu):
 
 @pytest.mark.parametrize("shape,reduce,scaled", [((5000, 10), False, True), ((3000, 16, 3), True, True),
                                                   ((100000,), False, False), ((777, 9, 3), True, False),
-                                                  ((1, 1), False, False)])
+                                                  ((1, 1), False, False), ((1001, 7), False, True),
+                                                  ((40, 700), True, True), ((3, 5), True, False)])
 def test_adam_matches_checker(gpu, shape, reduce, scaled):
     import torch
     from brush_amd.train import AdamScaled, AdamState
