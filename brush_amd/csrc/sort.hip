@@ -9,11 +9,15 @@
 // counts are published to a look-back status array, and the pairs are written
 // from LDS in digit order so each digit's run is a contiguous write.
 //
-// Forward progress of the look-back: partition ids come from an atomic
-// counter taken when a workgroup starts, so a workgroup only ever waits on
-// partitions owned by workgroups that are already resident.  The spin is
-// bounded; on exhaustion the kernel raises an error flag that the host turns
-// into BH_ERR_INTERNAL, and the kernel still completes.
+// Forward progress of the look-back: a partition is its workgroup's id, and a
+// workgroup only waits on lower ids.  Workgroups go to the XCDs round robin
+// and each XCD dispatches its share in increasing id order, so whenever some
+// partition waits, every lower partition already has a resident workgroup or
+// has finished (an atomic ticket per workgroup gives the same guarantee
+// without relying on dispatch order, but serialises workgroup starts on one
+// counter: measured 14 us of a 93 us tile-sort pass).  The spin is bounded;
+// on exhaustion the kernel raises an error flag that the host turns into
+// BH_ERR_INTERNAL, and the kernel still completes.
 //
 // Replaces brush-sort (crates/brush-sort/src/lib.rs:16-129, which runs five
 // kernels per 4-bit pass with a single-workgroup scan) and brush-prefix-sum
@@ -21,6 +25,7 @@
 #include <hip/hip_runtime.h>
 
 #include "bh_internal.h"
+#include "bh_lookback.h"
 
 namespace bh {
 
@@ -29,10 +34,6 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kItems = 16;
 constexpr int kPart = kThreads * kItems;  // 4096
 constexpr int kRadix = 256;
-constexpr uint64_t kFlagAgg = 1ull << 62;
-constexpr uint64_t kFlagPrefix = 2ull << 62;
-constexpr uint32_t kSpinLimit = 1u << 24;
-
 // p[0, count) = value: 16-byte stores from the first 16-byte boundary, single
 // words for the unaligned head and the tail.
 __global__ void fill_u32_kernel(uint32_t* p, uint32_t value, uint64_t count) {
@@ -54,74 +55,6 @@ void launch_fill_u32(bh_ctx* ctx, uint32_t* p, uint32_t value, uint64_t count) {
     fill_u32_kernel<<<blocks, 256, 0, ctx->stream>>>(p, value, count);
 }
 
-__device__ __forceinline__ uint64_t status_load(const uint64_t* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void status_store(uint64_t* p, uint64_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Sum of the values published by partitions [0, part) for one status column.
-// Walks backwards accumulating aggregates until an inclusive prefix is found,
-// reading four predecessors per round trip (the loads are independent).
-__device__ uint32_t look_back(const uint64_t* status, uint32_t part, uint32_t stride, uint32_t col,
-                              uint32_t* err) {
-    uint32_t excl = 0;
-    int64_t p = (int64_t)part - 1;
-    uint32_t spins = 0;
-    while (p >= 0) {
-        uint64_t s[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) s[i] = p - i >= 0 ? status_load(status + (uint64_t)(p - i) * stride + col) : 0ull;
-        bool stalled = false, found = false;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            if (stalled || found || p - i < 0) continue;
-            const uint64_t flag = s[i] & (3ull << 62);
-            if (flag == 0) {
-                stalled = true;  // wait for this one, keeping what was summed
-                p -= i;
-                continue;
-            }
-            excl += (uint32_t)s[i];
-            if (flag == kFlagPrefix) found = true;
-        }
-        if (found) break;
-        if (!stalled) {
-            p -= 4;
-            continue;
-        }
-        if (++spins >= kSpinLimit) {
-            atomicOr(err, kErrSpin);
-            break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-    }
-    return excl;
-}
-
-// Exclusive scan of one value per thread over a 256-thread block.
-__device__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* s_wave_tot, uint32_t* total) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    uint32_t x = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        uint32_t y = __shfl_up(x, o, 64);
-        if (lane >= o) x += y;
-    }
-    if (lane == 63) s_wave_tot[wave] = x;
-    __syncthreads();
-    uint32_t off = 0, tot = 0;
-#pragma unroll
-    for (int w = 0; w < kWaves; w++) {
-        uint32_t t = s_wave_tot[w];
-        if (w < wave) off += t;
-        tot += t;
-    }
-    __syncthreads();
-    *total = tot;
-    return off + x - v;
-}
 
 // Digit layout of a sort by the low `key_bits` bits: ceil(key_bits / 8)
 // passes of equal width (13 bits -> 7 + 6), so every pass has at most 256
@@ -190,21 +123,18 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
                                                              uint32_t* __restrict__ vals_out, uint32_t n,
                                                              uint32_t shift, uint32_t digit_bits, uint32_t key_sub,
                                                              uint32_t key_cap, const uint32_t* __restrict__ hist,
-                                                             uint64_t* status, uint32_t* part_counter,
-                                                             uint32_t* err) {
+                                                             uint64_t* status, uint32_t* err) {
     constexpr int PART = kThreads * ITEMS;
     __shared__ uint32_t s_wave_hist[kWaves][kRadix];
     __shared__ uint32_t s_local_start[kRadix];
     __shared__ uint32_t s_global_off[kRadix];
     __shared__ uint32_t s_buf[PART];  // keys, then values, in digit order
     __shared__ uint32_t s_tot[kWaves];
-    __shared__ uint32_t s_part;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (tid == 0) s_part = atomicAdd(part_counter, 1u);
     for (int i = tid; i < kWaves * kRadix; i += kThreads) (&s_wave_hist[0][0])[i] = 0;
     __syncthreads();
-    const uint32_t part = s_part;
+    const uint32_t part = blockIdx.x;
     const uint64_t base = (uint64_t)part * PART;
     const uint64_t wave_base = base + (uint64_t)wave * (64 * ITEMS);
     const uint32_t dmask = (1u << digit_bits) - 1u;
@@ -260,8 +190,8 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
         status_store(my_status, kFlagPrefix | (uint64_t)(excl + total));
     }
     uint32_t tot_dummy;
-    uint32_t bin_base = block_exclusive_scan(hist[d], s_tot, &tot_dummy);
-    uint32_t local_start = block_exclusive_scan(total, s_tot, &tot_dummy);
+    uint32_t bin_base = block_exclusive_scan<kThreads>(hist[d], s_tot, &tot_dummy);
+    uint32_t local_start = block_exclusive_scan<kThreads>(total, s_tot, &tot_dummy);
     s_local_start[d] = local_start;
     s_global_off[d] = bin_base + excl;
     __syncthreads();
@@ -310,10 +240,10 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
 // look-back traffic for the same data).
 static uint32_t sort_part(uint32_t) { return (uint32_t)kPart; }
 
-// scratch layout: hist[4*256] | counters[8] | status[passes][parts][256] (u64)
+// scratch layout: hist[4*256] | status[passes][parts][256] (u64)
 size_t radix_sort_scratch_bytes(uint32_t n, uint32_t key_bits) {
     const uint64_t parts = div_up(n, sort_part(n));
-    return (size_t)(4 * kRadix + 8) * 4 + (size_t)digit_plan(key_bits).passes * parts * kRadix * 8;
+    return (size_t)(4 * kRadix) * 4 + (size_t)digit_plan(key_bits).passes * parts * kRadix * 8;
 }
 
 bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t* vals_in, uint32_t n,
@@ -327,9 +257,8 @@ bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t*
     const uint32_t part_size = sort_part(n);
     const uint32_t parts = div_up(n, part_size);
     uint32_t* hist = (uint32_t*)scratch;
-    uint32_t* counters = hist + 4 * kRadix;
-    uint64_t* status = (uint64_t*)(counters + 8);
-    size_t words = (size_t)(4 * kRadix + 8) + (size_t)plan.passes * parts * kRadix * 2;
+    uint64_t* status = (uint64_t*)(hist + 4 * kRadix);
+    size_t words = (size_t)(4 * kRadix) + (size_t)plan.passes * parts * kRadix * 2;
     launch_fill_u32(ctx, hist, 0u, words);
     {
         KernelTimer t(ctx, hist_name.c_str());
@@ -350,8 +279,7 @@ bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t*
         KernelTimer t(ctx, pass_name.c_str());
 #define BH_PASS(F, I)                                                                                               \
     onesweep_kernel<F, I><<<parts, kThreads, 0, ctx->stream>>>(src_k, src_v, dk, dv, n, sh, bits, sub, cap,        \
-                                                               hist + p * kRadix, st, counters + p,                \
-                                                               ctx->d_counters + 1)
+                                                               hist + p * kRadix, st, ctx->d_counters + 1)
         if (part_size == (uint32_t)kPart) {
             if (p == 0) BH_PASS(true, kItems); else BH_PASS(false, kItems);
         } else {
@@ -399,14 +327,11 @@ void launch_gather_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t* v
 __global__ __launch_bounds__(kThreads) void scan_kernel(const uint32_t* __restrict__ in,
                                                          const uint32_t* __restrict__ gather,
                                                          uint32_t* __restrict__ out, uint32_t n, uint64_t* status,
-                                                         uint32_t* part_counter, uint32_t* err) {
+                                                         uint32_t* err) {
     __shared__ uint32_t s_tot[kWaves];
-    __shared__ uint32_t s_part;
     __shared__ uint32_t s_prefix;
     const int tid = threadIdx.x;
-    if (tid == 0) s_part = atomicAdd(part_counter, 1u);
-    __syncthreads();
-    const uint32_t part = s_part;
+    const uint32_t part = blockIdx.x;
     const uint64_t first = (uint64_t)part * kPart + (uint64_t)tid * kItems;
     uint32_t x[kItems];
     uint32_t run = 0;
@@ -419,7 +344,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const uint32_t* __restri
         x[j] = run;
     }
     uint32_t block_total;
-    uint32_t thread_excl = block_exclusive_scan(run, s_tot, &block_total);
+    uint32_t thread_excl = block_exclusive_scan<kThreads>(run, s_tot, &block_total);
     if (tid == 0) {
         uint32_t excl = 0;
         if (part == 0) {
@@ -446,11 +371,10 @@ bh_status inclusive_scan(bh_ctx* ctx, const uint32_t* in, const uint32_t* gather
                          void* scratch) {
     if (n == 0) return BH_OK;
     uint32_t parts = div_up(n, kPart);
-    uint32_t* counter = (uint32_t*)scratch;
     uint64_t* status = (uint64_t*)((char*)scratch + 64);
-    launch_fill_u32(ctx, counter, 0u, 16 + (size_t)parts * 2);
+    launch_fill_u32(ctx, (uint32_t*)status, 0u, (size_t)parts * 2);
     KernelTimer t(ctx, "scan");
-    scan_kernel<<<parts, kThreads, 0, ctx->stream>>>(in, gather, out, n, status, counter, ctx->d_counters + 1);
+    scan_kernel<<<parts, kThreads, 0, ctx->stream>>>(in, gather, out, n, status, ctx->d_counters + 1);
     return check_launch(ctx, "scan");
 }
 
