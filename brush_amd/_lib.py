@@ -65,6 +65,8 @@ class Uniforms(ctypes.Structure):
         ("sh_degree", ctypes.c_uint32),
         ("total_splats", ctypes.c_uint32),
         ("num_visible", ctypes.c_uint32),
+        ("camera_model", ctypes.c_uint32),
+        ("camera_params", ctypes.c_float * 8),
     ]
 
     @staticmethod
@@ -78,6 +80,9 @@ class Uniforms(ctypes.Structure):
             u.camera_pos[i] = float(d["camera_pos"][i])
         for k in ("img_w", "img_h", "tile_bw", "tile_bh", "sh_degree", "total_splats", "num_visible"):
             setattr(u, k, int(d.get(k, 0)))
+        u.camera_model = int(d.get("camera_model", 0))
+        for i, v in enumerate(d.get("camera_params", ())):
+            u.camera_params[i] = float(v)
         return u
 
     def to_dict(self) -> dict:
@@ -90,6 +95,7 @@ class Uniforms(ctypes.Structure):
             camera_pos=[float(x) for x in self.camera_pos],
             img_w=self.img_w, img_h=self.img_h, tile_bw=self.tile_bw, tile_bh=self.tile_bh,
             sh_degree=self.sh_degree, total_splats=self.total_splats, num_visible=self.num_visible,
+            camera_model=self.camera_model, camera_params=[float(x) for x in self.camera_params],
         )
 
 

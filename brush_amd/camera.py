@@ -1,16 +1,17 @@
-"""Pinhole camera and ProjectUniforms construction.
+"""Camera, camera models and ProjectUniforms construction.
 
 Restates the host side of the reference's projection setup:
 ``Camera`` (brush-render/src/camera.rs:11-82), ``fov_to_focal`` /
-``focal_to_fov`` (camera.rs:84-119, pinhole branch),
-``calculate_jacobian_clamp_limits`` (camera.rs:200-254, pinhole branch),
+``focal_to_fov`` (camera.rs:84-195, every model),
+``calculate_jacobian_clamp_limits`` (camera.rs:197-254),
 ``calc_tile_bounds`` (render.rs:30-47) and the uniform packing of
-``render_with_rasterizer`` (render.rs:116-136).  Scalar arithmetic follows the
-reference's types: f64 for fov/focal conversion, f32 elsewhere (numpy float32
-scalars give IEEE single-precision rounding per operation).
-
-Other camera models (Kannala-Brandt, radial-tangential, thin-prism fisheye)
-are not part of this build.
+``render_with_rasterizer`` (render.rs:116-136).  The camera models
+(kernels/camera_model/mod.rs:34-41) are ``Pinhole``, ``KannalaBrandt4``,
+``RadialTangential8`` and ``ThinPrismFisheye``; the kernels receive the model
+id and its coefficients through the uniforms.  Scalar arithmetic follows the
+reference's types: f64 for fov/focal conversion and the distortion inverses,
+f32 elsewhere (numpy float32 scalars give IEEE single-precision rounding per
+operation).
 """
 from __future__ import annotations
 
@@ -24,14 +25,165 @@ TILE_WIDTH = 16
 f32 = np.float32
 
 
-def fov_to_focal(fov: float, pixels: int) -> float:
-    """camera.rs:84-101 (pinhole): r_pix / tan(fov / 2), in f64."""
-    return (pixels / 2.0) / math.tan(fov / 2.0)
+@dataclass(frozen=True)
+class Pinhole:
+    """camera_model/pinhole.rs."""
+
+    model_id = 0
+
+    def params(self):
+        return [0.0] * 8
 
 
-def focal_to_fov(focal: float, pixels: int) -> float:
-    """camera.rs:103-119 (pinhole): 2 atan(r_pix / focal), in f64."""
-    return 2.0 * math.atan((pixels / 2.0) / focal)
+@dataclass(frozen=True)
+class KannalaBrandt4:
+    """camera_model/kannala_brandt_4.rs:11-16: d(theta) = theta (1 + k1 theta^2 + ... + k4 theta^8)."""
+
+    k1: float = 0.0
+    k2: float = 0.0
+    k3: float = 0.0
+    k4: float = 0.0
+    model_id = 1
+
+    def params(self):
+        return [self.k1, self.k2, self.k3, self.k4, 0.0, 0.0, 0.0, 0.0]
+
+
+@dataclass(frozen=True)
+class RadialTangential8:
+    """camera_model/radial_tangential_8.rs:12-21: rational radial (k1..k3 over
+    k4..k6) plus tangential p1, p2."""
+
+    k1: float = 0.0
+    k2: float = 0.0
+    k3: float = 0.0
+    k4: float = 0.0
+    k5: float = 0.0
+    k6: float = 0.0
+    p1: float = 0.0
+    p2: float = 0.0
+    model_id = 2
+
+    def params(self):
+        return [self.k1, self.k2, self.k3, self.k4, self.k5, self.k6, self.p1, self.p2]
+
+
+@dataclass(frozen=True)
+class ThinPrismFisheye:
+    """camera_model/thin_prism_fisheye.rs:23-30: KB4 plus tangential (p1, p2)
+    and thin prism (sx1, sy1)."""
+
+    kb4: KannalaBrandt4 = KannalaBrandt4()
+    p1: float = 0.0
+    p2: float = 0.0
+    sx1: float = 0.0
+    sy1: float = 0.0
+    model_id = 3
+
+    def params(self):
+        k = self.kb4
+        return [k.k1, k.k2, k.k3, k.k4, self.p1, self.p2, self.sx1, self.sy1]
+
+
+PINHOLE = Pinhole()
+
+
+def _f32_coeffs(model):
+    """The model's coefficients as the f32 values the reference stores, in f64."""
+    return [float(f32(v)) for v in model.params()]
+
+
+def kb4_d(theta: float, model) -> float:
+    """camera.rs:121-130: theta + k1 theta^3 + k2 theta^5 + k3 theta^7 + k4 theta^9 (f64)."""
+    k1, k2, k3, k4 = _f32_coeffs(model)[:4]
+    t2 = theta * theta
+    t3 = t2 * theta
+    t5 = t3 * t2
+    t7 = t5 * t2
+    t9 = t7 * t2
+    return theta + k1 * t3 + k2 * t5 + k3 * t7 + k4 * t9
+
+
+def kb4_dd_dtheta(theta: float, model) -> float:
+    """camera.rs:132-143."""
+    k1, k2, k3, k4 = _f32_coeffs(model)[:4]
+    t2 = theta * theta
+    t4 = t2 * t2
+    t6 = t4 * t2
+    t8 = t6 * t2
+    return 1.0 + 3.0 * k1 * t2 + 5.0 * k2 * t4 + 7.0 * k3 * t6 + 9.0 * k4 * t8
+
+
+def kb4_invert_d(target: float, model) -> float:
+    """camera.rs:145-168: Newton on d(theta) = target over [0, pi]."""
+    if target <= 0.0:
+        return 0.0
+    theta = min(target, math.pi - 1e-6)
+    for _ in range(50):
+        fv = kb4_d(theta, model) - target
+        fp = kb4_dd_dtheta(theta, model)
+        if abs(fp) < 1e-12:
+            break
+        nxt = min(max(theta - fv / fp, 0.0), math.pi)
+        if abs(nxt - theta) < 1e-12:
+            theta = nxt
+            break
+        theta = nxt
+    return theta
+
+
+def rt8_radial(r: float, model: RadialTangential8) -> float:
+    """camera.rs:170-179: (1 + k1 r^2 + k2 r^4 + k3 r^6) / (1 + k4 r^2 + k5 r^4 + k6 r^6)."""
+    k1, k2, k3, k4, k5, k6 = _f32_coeffs(model)[:6]
+    r2 = r * r
+    r4 = r2 * r2
+    r6 = r4 * r2
+    return (1.0 + k1 * r2 + k2 * r4 + k3 * r6) / (1.0 + k4 * r2 + k5 * r4 + k6 * r6)
+
+
+def rt8_undistort_radius(r_d: float, model: RadialTangential8) -> float:
+    """camera.rs:181-195: fixed point r = r_d / radial(r)."""
+    r = r_d
+    for _ in range(30):
+        factor = rt8_radial(r, model)
+        if abs(factor) < 1e-12:
+            break
+        r_new = r_d / factor
+        if abs(r_new - r) < 1e-12:
+            r = r_new
+            break
+        r = r_new
+    return r
+
+
+def fov_to_focal(fov: float, pixels: int, model=PINHOLE) -> float:
+    """camera.rs:84-101: r_pix / projection(fov / 2), in f64."""
+    half = fov / 2.0
+    r_pix = pixels / 2.0
+    if isinstance(model, KannalaBrandt4):
+        proj = kb4_d(half, model)
+    elif isinstance(model, ThinPrismFisheye):
+        proj = kb4_d(half, model.kb4)
+    elif isinstance(model, RadialTangential8):
+        r = math.tan(half)
+        proj = r * rt8_radial(r, model)
+    else:
+        proj = math.tan(half)
+    return r_pix / proj
+
+
+def focal_to_fov(focal: float, pixels: int, model=PINHOLE) -> float:
+    """camera.rs:103-119, in f64."""
+    r_norm = (pixels / 2.0) / focal
+    if isinstance(model, KannalaBrandt4):
+        half = kb4_invert_d(r_norm, model)
+    elif isinstance(model, ThinPrismFisheye):
+        half = kb4_invert_d(r_norm, model.kb4)
+    elif isinstance(model, RadialTangential8):
+        half = math.atan(rt8_undistort_radius(r_norm, model))
+    else:
+        half = math.atan(r_norm)
+    return 2.0 * half
 
 
 def quat_to_mat3(q_xyzw) -> np.ndarray:
@@ -84,21 +236,25 @@ class Camera:
     fov_x: float = 0.5
     fov_y: float = 0.5
     center_uv: tuple = (0.5, 0.5)
+    camera_model: object = PINHOLE
 
     @staticmethod
-    def from_focal(position, rotation, focal: float, img_w: int, img_h: int, center_uv=(0.5, 0.5)):
-        """A camera whose pinhole focal length is ``focal`` pixels on both axes."""
+    def from_focal(position, rotation, focal: float, img_w: int, img_h: int, center_uv=(0.5, 0.5),
+                   camera_model=PINHOLE):
+        """A camera whose focal length is ``focal`` pixels on both axes."""
         return Camera(
             tuple(position),
             tuple(rotation),
-            focal_to_fov(focal, img_w),
-            focal_to_fov(focal, img_h),
+            focal_to_fov(focal, img_w, camera_model),
+            focal_to_fov(focal, img_h, camera_model),
             tuple(center_uv),
+            camera_model,
         )
 
     def focal(self, img_w: int, img_h: int):
         """camera.rs:49-54: f64 focal cast to f32."""
-        return f32(fov_to_focal(self.fov_x, img_w)), f32(fov_to_focal(self.fov_y, img_h))
+        return (f32(fov_to_focal(self.fov_x, img_w, self.camera_model)),
+                f32(fov_to_focal(self.fov_y, img_h, self.camera_model)))
 
     def center(self, img_w: int, img_h: int):
         """camera.rs:56-61."""
@@ -115,14 +271,22 @@ def tile_bounds(img_w: int, img_h: int):
     return (img_w + TILE_WIDTH - 1) // TILE_WIDTH, (img_h + TILE_WIDTH - 1) // TILE_WIDTH
 
 
-def jacobian_clamp_limits(img_w: int, img_h: int, fx, fy, cx, cy):
-    """camera.rs:200-254, pinhole branch, f32."""
+def jacobian_clamp_limits(img_w: int, img_h: int, fx, fy, cx, cy, model=PINHOLE):
+    """camera.rs:197-254, f32: the pinhole margins (1.15 W - c) / f and
+    (-0.15 W - c) / f; for RT8 each edge is undistorted (in f64) to the bound
+    on the undistorted coordinate; the fisheye models are not clamped (zeros)."""
+    if isinstance(model, (KannalaBrandt4, ThinPrismFisheye)):
+        z = f32(0.0)
+        return z, z, z, z
     w, h = f32(img_w), f32(img_h)
-    lim_pos_x = (f32(1.15) * w - cx) / fx
-    lim_pos_y = (f32(1.15) * h - cy) / fy
-    lim_neg_x = (f32(-0.15) * w - cx) / fx
-    lim_neg_y = (f32(-0.15) * h - cy) / fy
-    return lim_pos_x, lim_pos_y, lim_neg_x, lim_neg_y
+    edges = ((f32(1.15) * w - cx) / fx, (f32(1.15) * h - cy) / fy,
+             (f32(-0.15) * w - cx) / fx, (f32(-0.15) * h - cy) / fy)
+    if isinstance(model, RadialTangential8):
+        def undistort(edge):
+            mag = f32(rt8_undistort_radius(abs(float(edge)), model))
+            return mag * (f32(1.0) if edge >= 0 else f32(-1.0))
+        edges = tuple(undistort(e) for e in edges)
+    return edges
 
 
 def project_uniforms(camera: Camera, img_w: int, img_h: int, total_splats: int, sh_degree: int) -> dict:
@@ -139,7 +303,7 @@ def project_uniforms(camera: Camera, img_w: int, img_h: int, total_splats: int, 
     viewmat = np.concatenate([rot[:, 0], rot[:, 1], rot[:, 2], trans]).astype(np.float32)
     hyp = f32(math.hypot(float(f32(camera.fov_x)), float(f32(camera.fov_y))))
     half_fov = min(hyp * f32(1.05), f32(2.0 * math.pi - 1e-6)) * f32(0.5)
-    lims = jacobian_clamp_limits(img_w, img_h, fx, fy, cx, cy)
+    lims = jacobian_clamp_limits(img_w, img_h, fx, fy, cx, cy, camera.camera_model)
     tbw, tbh = tile_bounds(img_w, img_h)
     return dict(
         viewmat=viewmat,
@@ -152,6 +316,8 @@ def project_uniforms(camera: Camera, img_w: int, img_h: int, total_splats: int, 
         sh_degree=int(sh_degree),
         total_splats=int(total_splats),
         num_visible=0,
+        camera_model=int(camera.camera_model.model_id),
+        camera_params=[float(f32(v)) for v in camera.camera_model.params()],
     )
 
 

@@ -333,6 +333,7 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
     if (uin->img_w == 0 || uin->img_h == 0)
         return set_error(ctx, BH_ERR_INVALID_ARG, "Can't render images with 0 size.");
     if (sh_degree > 4) return set_error(ctx, BH_ERR_INVALID_ARG, "sh_degree must be <= 4");
+    if (uin->camera_model > BH_CAMERA_TPF) return set_error(ctx, BH_ERR_INVALID_ARG, "unknown camera model");
     const bool bwd = (flags & BH_FLAG_BWD_INFO) != 0;
     const bool mip = (flags & BH_FLAG_MIP) != 0;
     if (!out_img || !tile_offsets || (num_splats && (!transforms || !sh_coeffs || !raw_opacities || !max_radius)) ||
@@ -520,6 +521,7 @@ bh_status bh_project_backward(bh_ctx* ctx, const bh_project_uniforms* u, const f
     const uint32_t n = u->total_splats;
     if (n == 0) return BH_OK;
     if (u->sh_degree > 4) return set_error(ctx, BH_ERR_INVALID_ARG, "sh_degree must be <= 4");
+    if (u->camera_model > BH_CAMERA_TPF) return set_error(ctx, BH_ERR_INVALID_ARG, "unknown camera model");
     if (u->num_visible > n) return set_error(ctx, BH_ERR_SHAPE, "num_visible > total_splats");
     if (!transforms || !sh_coeffs || !raw_opacities || !v_combined || !v_transforms || !v_coeffs || !v_raw_opac ||
         !v_refine || (u->num_visible && !global_from_compact_gid))

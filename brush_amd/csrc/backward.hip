@@ -290,7 +290,7 @@ __device__ __forceinline__ void store_row(float* __restrict__ dst, const float* 
 
 // The projection VJP of one splat with gradient lanes rg, written to its dense
 // rows (project_backwards.rs:101-263).
-template <int DEG, bool MIP>
+template <int DEG, bool MIP, int CAM>
 __device__ void project_backward_one(const bh_project_uniforms& u, const float* __restrict__ transforms,
                                      const float* __restrict__ sh, const float* __restrict__ raw_opac, uint32_t gid,
                                      const float* rg, float* __restrict__ v_transforms, float* __restrict__ v_coeffs,
@@ -351,7 +351,7 @@ __device__ void project_backward_one(const bh_project_uniforms& u, const float* 
     const V3 mean_c = world_to_cam(u, mean);
     const M3 r = qmat(q);
     const M3 m = mul_diag(r, sc);
-    const S2 raw_cov = calc_cov2d(u, sc, q, mean_c);
+    const S2 raw_cov = calc_cov2d<CAM>(u, sc, q, mean_c);
     float comp;
     const S2 cov = compensate_cov2d<MIP>(raw_cov, comp);
     const float sig = bh_sigmoidf(raw_opac[gid]);
@@ -364,8 +364,8 @@ __device__ void project_backward_one(const bh_project_uniforms& u, const float* 
     const S3 covar = outer_self(m);
     const M3 vr = view_rot(u);
     const S3 cov_c = cong(covar, vr);
-    const M23 J = jacobian(u, mean_c);
-    V3 v_mean_c = projection_vjp(u, J, mean_c, cov_c, v_cov2d, v2(rg[0], rg[1]));
+    const M23 J = jacobian<CAM>(u, mean_c);
+    V3 v_mean_c = projection_vjp<CAM>(u, J, mean_c, cov_c, v_cov2d, v2(rg[0], rg[1]));
     v_mean_c = v3(v_mean_c.x, v_mean_c.y, v_mean_c.z + rg[10]);
     const S3 vcc = tcong(J, v_cov2d);
     const V3 v_mean = tmulv(vr, v_mean_c) + v_mean_sh;
@@ -401,7 +401,7 @@ __device__ __forceinline__ void block_zero(float* __restrict__ p, size_t begin, 
 // and runs the VJP over that list with every lane busy, overwriting their
 // rows.  cfg == nullptr: v_combined holds one row per global id (the fused
 // backward), else v_combined[cfg[gid]].
-template <int DEG, bool MIP>
+template <int DEG, bool MIP, int CAM>
 __global__ __launch_bounds__(256) void project_backward_kernel(
     bh_project_uniforms u, const float* __restrict__ transforms, const float* __restrict__ sh,
     const float* __restrict__ raw_opac, const uint32_t* __restrict__ cfg, uint32_t n,
@@ -447,22 +447,39 @@ __global__ __launch_bounds__(256) void project_backward_kernel(
         float rg[11];
 #pragma unroll
         for (int k = 0; k < 11; k++) rg[k] = src[k];
-        project_backward_one<DEG, MIP>(u, transforms, sh, raw_opac, g, rg, v_transforms, v_coeffs, v_raw_opac,
-                                       v_refine);
+        project_backward_one<DEG, MIP, CAM>(u, transforms, sh, raw_opac, g, rg, v_transforms, v_coeffs,
+                                            v_raw_opac, v_refine);
     }
+}
+
+template <int DEG, bool MIP>
+static void launch_pb_cam(bh_ctx* ctx, const bh_project_uniforms& u, const float* transforms, const float* sh,
+                          const float* raw_opac, const uint32_t* cfg, uint32_t n, const float* v_combined,
+                          float* v_transforms, float* v_coeffs, float* v_raw_opac, float* v_refine) {
+    const uint32_t blocks = div_up(n, 256);
+#define BH_PB(C)                                                                                                  \
+    project_backward_kernel<DEG, MIP, C><<<blocks, 256, 0, ctx->stream>>>(u, transforms, sh, raw_opac, cfg, n,     \
+                                                                          v_combined, v_transforms, v_coeffs,     \
+                                                                          v_raw_opac, v_refine)
+    switch (u.camera_model) {
+        case kCamKB4: BH_PB(kCamKB4); break;
+        case kCamRT8: BH_PB(kCamRT8); break;
+        case kCamTPF: BH_PB(kCamTPF); break;
+        default: BH_PB(kCamPinhole); break;
+    }
+#undef BH_PB
 }
 
 template <int DEG>
 static void launch_pb(bh_ctx* ctx, bool mip, const bh_project_uniforms& u, const float* transforms, const float* sh,
                       const float* raw_opac, const uint32_t* cfg, uint32_t n, const float* v_combined,
                       float* v_transforms, float* v_coeffs, float* v_raw_opac, float* v_refine) {
-    uint32_t blocks = div_up(n, 256);
     if (mip)
-        project_backward_kernel<DEG, true><<<blocks, 256, 0, ctx->stream>>>(
-            u, transforms, sh, raw_opac, cfg, n, v_combined, v_transforms, v_coeffs, v_raw_opac, v_refine);
+        launch_pb_cam<DEG, true>(ctx, u, transforms, sh, raw_opac, cfg, n, v_combined, v_transforms, v_coeffs,
+                                 v_raw_opac, v_refine);
     else
-        project_backward_kernel<DEG, false><<<blocks, 256, 0, ctx->stream>>>(
-            u, transforms, sh, raw_opac, cfg, n, v_combined, v_transforms, v_coeffs, v_raw_opac, v_refine);
+        launch_pb_cam<DEG, false>(ctx, u, transforms, sh, raw_opac, cfg, n, v_combined, v_transforms, v_coeffs,
+                                  v_raw_opac, v_refine);
 }
 
 void launch_project_backward(bh_ctx* ctx, const bh_project_uniforms& u, const float* transforms, const float* sh,

@@ -26,8 +26,15 @@
  *             s = f / (2 + f), log(1+f) = 2 atanh(s) = f - s (f - R) with
  *             R = sum_{k>=1} 2 s^{2k} / (2k+1) truncated after s^8 (the
  *             rearrangement used by the classic BSD/fdlibm logf), plus e ln2.
- * Both stay within 2 ulp of the correctly rounded result over all finite
- * inputs (pinned on the CPU against float64 libm by tests/test_math.py).
+ *   bh_atan2f — t = min(|y|,|x|) / max(|y|,|x|) in [0, 1]; with the nearest
+ *             centre c = tan(k pi / 12), k = 0..3, atan(t) = atan(c) +
+ *             atan((t - c) / (1 + t c)) leaves |s| <= tan(pi/24); atan(s) is
+ *             the Taylor series through s^13 (truncation below 1e-13
+ *             relative); atan(c) of the f32 c and the quadrant fix-ups
+ *             (pi/2 - a when |y| > |x|, pi - a when x < 0) use two-part
+ *             constants; sign of y.
+ * All stay within 2 ulp of the correctly rounded result over all finite
+ * inputs (pinned on the CPU against float64 libm by the oracle tests).
  *
  * This header is plain C99 so the CPU restatement (gcc) can include it; under
  * hipcc every function is callable from host and device.
@@ -176,5 +183,52 @@ BH_HD float bh_expf_neg(float x) {
 
 /* 1 / (1 + e^-x)  (brush-cube/src/lib.rs:620-623) */
 BH_HD float bh_sigmoidf(float x) { return 1.0f / (1.0f + bh_expf(-x)); }
+
+/* atan2 (the fisheye camera models' theta = atan2(r, z),
+ * brush-render/src/kernels/camera_model/kannala_brandt_4.rs:38 and
+ * project_forward.rs:55-62), IEEE special cases included. */
+BH_HD float bh_atan2f(float y, float x) {
+    if (!(x == x) || !(y == y)) return x + y;
+    const int xneg = (int)(bh_as_uint(x) >> 31), yneg = (int)(bh_as_uint(y) >> 31);
+    const float ax = bh_absf(x), ay = bh_absf(y);
+    const float pi_hi = 3.14159274101257324f, pi_lo = -8.74227766e-08f;
+    const float pi2_hi = 1.57079637050628662f, pi2_lo = -4.37113883e-08f;
+    const float inf = bh_as_float(BH_INF_BITS);
+    float a;
+    if (ay == 0.0f) {
+        a = xneg ? pi_hi : 0.0f;
+    } else if (ax == 0.0f) {
+        a = pi2_hi;
+    } else if (ax == inf || ay == inf) {
+        if (ax == inf && ay == inf) a = xneg ? 2.35619449615478516f : 0.785398185253143311f;
+        else if (ay == inf) a = pi2_hi;
+        else a = xneg ? pi_hi : 0.0f;
+    } else {
+        const int swap = ay > ax;
+        const float t = swap ? ax / ay : ay / ax; /* [0, 1] */
+        /* nearest centre c_k = tan(k pi / 12), atan(c_k) as hi + lo for the f32 c_k */
+        float c = 0.0f, at_hi = 0.0f, at_lo = 0.0f;
+        if (t > 0.767327011f) {
+            c = 1.0f, at_hi = 0.785398185253143311f, at_lo = -2.18556941e-08f;
+        } else if (t > 0.414213568f) {
+            c = 0.577350259f, at_hi = 0.523598790168762207f, at_lo = -2.23422756e-08f;
+        } else if (t > 0.131652504f) {
+            c = 0.267949194f, at_hi = 0.261799395084381104f, at_lo = -6.08637896e-09f;
+        }
+        const float s = c == 0.0f ? t : (t - c) / bh_fmaf(t, c, 1.0f); /* |s| <= tan(pi/24) */
+        const float z = s * s;
+        float p = 7.69230769e-02f;               /* 1/13 */
+        p = bh_fmaf(p, z, -9.09090909e-02f);     /* -1/11 */
+        p = bh_fmaf(p, z, 1.11111111e-01f);      /* 1/9 */
+        p = bh_fmaf(p, z, -1.42857143e-01f);     /* -1/7 */
+        p = bh_fmaf(p, z, 2.0e-01f);             /* 1/5 */
+        p = bh_fmaf(p, z, -3.33333333e-01f);     /* -1/3 */
+        const float at = bh_fmaf(s * z, p, s);
+        a = at_hi + (at + at_lo);
+        if (swap) a = (pi2_hi - a) + pi2_lo;
+        if (xneg) a = (pi_hi - a) + pi_lo;
+    }
+    return yneg ? -a : a;
+}
 
 #endif /* BH_MATH_H */

@@ -161,7 +161,7 @@ BH_DEV V2 project_pinhole(const bh_project_uniforms& u, V3 p) {
     return v2(u.fx * p.x * inv_z + u.cx, u.fy * p.y * inv_z + u.cy);
 }
 // calculate_project_jacobian_pinhole (pinhole.rs:32-56)
-BH_DEV M23 jacobian(const bh_project_uniforms& u, V3 p) {
+BH_DEV M23 jacobian_pinhole(const bh_project_uniforms& u, V3 p) {
     float inv_z = 1.0f / p.z;
     float dx = u.fx * inv_z;
     float dy = u.fy * inv_z;
@@ -169,10 +169,180 @@ BH_DEV M23 jacobian(const bh_project_uniforms& u, V3 p) {
     float cyl = bh_clampf(p.y * inv_z, u.lim_neg_y, u.lim_pos_y);
     return M23{v2(dx, 0.0f), v2(0.0f, dy), v2(-dx * cxl, -dy * cyl)};
 }
+// ---- camera models (kernels/camera_model/*.rs) --------------------------------
+// The model is a template parameter (the reference makes it a comptime
+// parameter of every projection kernel); its coefficients come from
+// u.camera_params in the reference's struct order.  Each function restates the
+// reference's expression term by term, so both sides round alike.
+enum : int { kCamPinhole = 0, kCamKB4 = 1, kCamRT8 = 2, kCamTPF = 3 };
+
+// project_kb4 (kannala_brandt_4.rs:18-52); also the radial part of TPF
+BH_DEV V2 project_kb4(const bh_project_uniforms& u, V3 p) {
+    const float* k = u.camera_params;
+    const float x = p.x, y = p.y, z = p.z;
+    const float inv_z = 1.0f / z;
+    const float pin_u = u.fx * x * inv_z + u.cx, pin_v = u.fy * y * inv_z + u.cy;
+    const float r = sqrtf(x * x + y * y);
+    const float theta = bh_atan2f(r, z);
+    const float t2 = theta * theta, t4 = t2 * t2, t6 = t2 * t4, t8 = t4 * t4;
+    const float d = theta * (1.0f + k[0] * t2 + k[1] * t4 + k[2] * t6 + k[3] * t8);
+    const float inv_r = 1.0f / r;
+    const float fish_u = u.fx * (d * x * inv_r) + u.cx, fish_v = u.fy * (d * y * inv_r) + u.cy;
+    const bool near_axis = r < 1e-6f;
+    return v2(near_axis ? pin_u : fish_u, near_axis ? pin_v : fish_v);
+}
+
+// calculate_project_jacobian_kb4 (kannala_brandt_4.rs:54-136): no clamp
+BH_DEV M23 jacobian_kb4(const bh_project_uniforms& u, V3 p) {
+    const float* k = u.camera_params;
+    const float fx = u.fx, fy = u.fy;
+    const float x = p.x, y = p.y, z = p.z;
+    const float inv_z = 1.0f / z;
+    const float x2 = x * x, y2 = y * y, xy = x * y;
+    const float r2 = x2 + y2;
+    const float r = sqrtf(r2);
+    const float inv_r = 1.0f / r;
+    const float inv_r3 = inv_r * inv_r * inv_r;
+    const float rho2 = r2 + z * z;
+    const float inv_rho2 = 1.0f / rho2;
+    const float inv_rho2_r = inv_rho2 * inv_r;
+    const float theta = bh_atan2f(r, z);
+    const float t2 = theta * theta, t4 = t2 * t2, t6 = t4 * t2, t8 = t4 * t4;
+    const float d = theta * (1.0f + k[0] * t2 + k[1] * t4 + k[2] * t6 + k[3] * t8);
+    const float dd = 1.0f + 3.0f * k[0] * t2 + 5.0f * k[1] * t4 + 7.0f * k[2] * t6 + 9.0f * k[3] * t8;
+    const float dth_dx = x * z * inv_rho2_r, dth_dy = y * z * inv_rho2_r, dth_dz = -r * inv_rho2;
+    const float dd_dx = dd * dth_dx, dd_dy = dd * dth_dy, dd_dz = dd * dth_dz;
+    const float xr = x * inv_r, dxr_dx = y2 * inv_r3, dxr_dy = -xy * inv_r3;
+    const float du_dx = fx * (dd_dx * xr + d * dxr_dx);
+    const float du_dy = fx * (dd_dy * xr + d * dxr_dy);
+    const float du_dz = fx * (dd_dz * xr);
+    const float yr = y * inv_r, dyr_dx = -xy * inv_r3, dyr_dy = x2 * inv_r3;
+    const float dv_dx = fy * (dd_dx * yr + d * dyr_dx);
+    const float dv_dy = fy * (dd_dy * yr + d * dyr_dy);
+    const float dv_dz = fy * (dd_dz * yr);
+    const bool near_axis = r < 1e-6f;
+    const float pdx = fx * inv_z, pdy = fy * inv_z;
+    const float p_du_dz = -pdx * x * inv_z, p_dv_dz = -pdy * y * inv_z;
+    return M23{v2(near_axis ? pdx : du_dx, near_axis ? 0.0f : dv_dx),
+               v2(near_axis ? 0.0f : du_dy, near_axis ? pdy : dv_dy),
+               v2(near_axis ? p_du_dz : du_dz, near_axis ? p_dv_dz : dv_dz)};
+}
+
+// project_rt8 (radial_tangential_8.rs:24-69)
+BH_DEV V2 project_rt8(const bh_project_uniforms& u, V3 p) {
+    const float* k = u.camera_params;
+    const float p1 = k[6], p2 = k[7];
+    const float xn = p.x / p.z, yn = p.y / p.z;
+    const float xn2 = xn * xn, yn2 = yn * yn;
+    const float r2 = xn2 + yn2, r4 = r2 * r2, r6 = r4 * r2;
+    const float d = (1.0f + k[0] * r2 + k[1] * r4 + k[2] * r6) / (1.0f + k[3] * r2 + k[4] * r4 + k[5] * r6);
+    const float xy = xn * yn;
+    const float xd = xn * d + 2.0f * p1 * xy + p2 * (r2 + 2.0f * xn2);
+    const float yd = yn * d + 2.0f * p2 * xy + p1 * (r2 + 2.0f * yn2);
+    return v2(u.fx * xd + u.cx, u.fy * yd + u.cy);
+}
+
+// calculate_project_jacobian_rt8 (radial_tangential_8.rs:71-146): evaluated at
+// the clamped normalised coordinate like the pinhole Jacobian
+BH_DEV M23 jacobian_rt8(const bh_project_uniforms& u, V3 p) {
+    const float* k = u.camera_params;
+    const float p1 = k[6], p2 = k[7];
+    const float fx = u.fx, fy = u.fy;
+    const float z = p.z;
+    const float inv_z = 1.0f / z, inv_z2 = inv_z * inv_z;
+    const float xn = bh_clampf(p.x * inv_z, u.lim_neg_x, u.lim_pos_x);
+    const float yn = bh_clampf(p.y * inv_z, u.lim_neg_y, u.lim_pos_y);
+    const float xc = xn * z, yc = yn * z;
+    const float r2 = xn * xn + yn * yn, r4 = r2 * r2, r6 = r4 * r2;
+    const float n_poly = 1.0f + k[0] * r2 + k[1] * r4 + k[2] * r6;
+    const float dn_poly = 1.0f + k[3] * r2 + k[4] * r4 + k[5] * r6;
+    const float np_poly = k[0] + 2.0f * k[1] * r2 + 3.0f * k[2] * r4;
+    const float dnp_poly = k[3] + 2.0f * k[4] * r2 + 3.0f * k[5] * r4;
+    const float inv_dn = 1.0f / dn_poly, inv_dn2 = inv_dn * inv_dn;
+    const float rv = n_poly * inv_dn;
+    const float rpv = (np_poly * dn_poly - n_poly * dnp_poly) * inv_dn2;
+    const float d00 = rv + 2.0f * xn * xn * rpv + 2.0f * p1 * yn + 6.0f * p2 * xn;
+    const float d01 = 2.0f * xn * yn * rpv + 2.0f * p1 * xn + 2.0f * p2 * yn;
+    const float d10 = d01;
+    const float d11 = rv + 2.0f * yn * yn * rpv + 6.0f * p1 * yn + 2.0f * p2 * xn;
+    return M23{v2(fx * d00 * inv_z, fy * d10 * inv_z), v2(fx * d01 * inv_z, fy * d11 * inv_z),
+               v2(-fx * (d00 * xc + d01 * yc) * inv_z2, -fy * (d10 * xc + d11 * yc) * inv_z2)};
+}
+
+// thin_prism_polys (thin_prism_fisheye.rs:37-63): N_u, N_v and their x, y
+// derivatives in camera-space x, y (the model divides them by z^2)
+struct PrismPolys {
+    float nu, nv, dnu_dx, dnu_dy, dnv_dx, dnv_dy;
+};
+BH_DEV PrismPolys thin_prism_polys(const bh_project_uniforms& u, float x, float y) {
+    const float p1 = u.camera_params[4], p2 = u.camera_params[5];
+    const float sx1 = u.camera_params[6], sy1 = u.camera_params[7];
+    const float x2 = x * x, y2 = y * y, xy = x * y, r2 = x2 + y2;
+    PrismPolys o;
+    o.nu = 2.0f * p1 * xy + p2 * (3.0f * x2 + y2) + sx1 * r2;
+    o.nv = 2.0f * p2 * xy + p1 * (x2 + 3.0f * y2) + sy1 * r2;
+    o.dnu_dx = 2.0f * (p1 * y + (3.0f * p2 + sx1) * x);
+    o.dnu_dy = 2.0f * (p1 * x + (p2 + sx1) * y);
+    o.dnv_dx = 2.0f * (p2 * y + (p1 + sy1) * x);
+    o.dnv_dy = 2.0f * (p2 * x + (3.0f * p1 + sy1) * y);
+    return o;
+}
+
+// project_tpf (thin_prism_fisheye.rs:65-81)
+BH_DEV V2 project_tpf(const bh_project_uniforms& u, V3 p) {
+    const V2 kb = project_kb4(u, p);
+    const float inv_z = 1.0f / p.z, inv_z2 = inv_z * inv_z;
+    const PrismPolys t = thin_prism_polys(u, p.x, p.y);
+    return v2(kb.x + u.fx * t.nu * inv_z2, kb.y + u.fy * t.nv * inv_z2);
+}
+
+// calculate_project_jacobian_tpf (thin_prism_fisheye.rs:83-114)
+BH_DEV M23 jacobian_tpf(const bh_project_uniforms& u, V3 p) {
+    const M23 kb = jacobian_kb4(u, p);
+    const float fx = u.fx, fy = u.fy;
+    const float inv_z = 1.0f / p.z, inv_z2 = inv_z * inv_z, inv_z3 = inv_z2 * inv_z;
+    const PrismPolys t = thin_prism_polys(u, p.x, p.y);
+    const float add_du_dx = fx * t.dnu_dx * inv_z2, add_du_dy = fx * t.dnu_dy * inv_z2;
+    const float add_du_dz = -2.0f * fx * t.nu * inv_z3;
+    const float add_dv_dx = fy * t.dnv_dx * inv_z2, add_dv_dy = fy * t.dnv_dy * inv_z2;
+    const float add_dv_dz = -2.0f * fy * t.nv * inv_z3;
+    return M23{v2(kb.c0.x + add_du_dx, kb.c0.y + add_dv_dx), v2(kb.c1.x + add_du_dy, kb.c1.y + add_dv_dy),
+               v2(kb.c2.x + add_du_dz, kb.c2.y + add_dv_dz)};
+}
+
+// project (camera_model/mod.rs:50-62)
+template <int CAM>
+BH_DEV V2 project_point(const bh_project_uniforms& u, V3 p) {
+    if (CAM == kCamKB4) return project_kb4(u, p);
+    if (CAM == kCamRT8) return project_rt8(u, p);
+    if (CAM == kCamTPF) return project_tpf(u, p);
+    return project_pinhole(u, p);
+}
+
+// calculate_project_jacobian (camera_model/mod.rs:64-80)
+template <int CAM>
+BH_DEV M23 jacobian(const bh_project_uniforms& u, V3 p) {
+    if (CAM == kCamKB4) return jacobian_kb4(u, p);
+    if (CAM == kCamRT8) return jacobian_rt8(u, p);
+    if (CAM == kCamTPF) return jacobian_tpf(u, p);
+    return jacobian_pinhole(u, p);
+}
+
+// The depth cull of project_forward (project_forward.rs:49-62): pinhole drops
+// z < 0.01; the other models drop splats whose view angle exceeds
+// half_max_render_fov.
+template <int CAM>
+BH_DEV bool depth_culled(const bh_project_uniforms& u, V3 mean_c) {
+    if (CAM == kCamPinhole) return mean_c.z < 0.01f;
+    const float r = sqrtf(mean_c.x * mean_c.x + mean_c.y * mean_c.y);
+    return bh_atan2f(r, mean_c.z) > u.half_max_render_fov;
+}
+
 // calc_cov2d (kernels/helpers.rs:297-330)
+template <int CAM>
 BH_DEV S2 calc_cov2d(const bh_project_uniforms& u, V3 sc, Q4 q, V3 mean_c) {
     M3 ns = mul_diag(mul(view_rot(u), qmat(q)), sc);
-    M23 jac = jacobian(u, mean_c);
+    M23 jac = jacobian<CAM>(u, mean_c);
     S2 raw = gram(mul(jac, ns));
     const float lim = 1.0e18f;
     float ma = max_abs(raw);
@@ -561,7 +731,7 @@ BH_DEV S2 inverse2x2_vjp(const S2& m, const S2& v) {
     return S2{t00 * m.c00 + t10 * m.c01, t01 * m.c00 + t11 * m.c01, t01 * m.c01 + t11 * m.c11};
 }
 // calculate_projection_vjp_pinhole (camera_model/pinhole.rs:58-123)
-BH_DEV V3 projection_vjp(const bh_project_uniforms& u, const M23& J, V3 mean_c, const S3& cov_c, const S2& v_cov2d,
+BH_DEV V3 projection_vjp_pinhole(const bh_project_uniforms& u, const M23& J, V3 mean_c, const S3& cov_c, const S2& v_cov2d,
                          V2 v_mean2d) {
     float fx = u.fx, fy = u.fy;
     float mx = mean_c.x, my = mean_c.y, mz = mean_c.z;
@@ -593,6 +763,260 @@ BH_DEV V3 projection_vjp(const bh_project_uniforms& u, const M23& J, V3 mean_c, 
         v_mz += -fy * inv_z3 * vj21 * ty;
     v_mz += -fx * inv_z2 * vj00 - fy * inv_z2 * vj11 + 2.0f * fx * tx * inv_z3 * vj20 + 2.0f * fy * ty * inv_z3 * vj21;
     return v3(v_mx, v_my, v_mz);
+}
+
+// 2 (v_cov2d J) cov_c, the six entries (row u, row v) x (column 0..2)
+struct VJ6 {
+    float u0, u1, u2, v0, v1, v2;
+};
+BH_DEV VJ6 cov_jacobian_grad(const M23& J, const S3& cov_c, const S2& v_cov2d) {
+    const M23 tmp = mul(v_cov2d, J);
+    VJ6 o;
+    o.u0 = 2.0f * dot(row0(tmp), srow0(cov_c));
+    o.u1 = 2.0f * dot(row0(tmp), srow1(cov_c));
+    o.u2 = 2.0f * dot(row0(tmp), srow2(cov_c));
+    o.v0 = 2.0f * dot(row1(tmp), srow0(cov_c));
+    o.v1 = 2.0f * dot(row1(tmp), srow1(cov_c));
+    o.v2 = 2.0f * dot(row1(tmp), srow2(cov_c));
+    return o;
+}
+
+// calculate_projection_vjp_kb4 (kannala_brandt_4.rs:138-337): J^T v_mean2d
+// plus the contraction of 2 (v_cov2d J) cov_c with the second derivatives of
+// the projection
+BH_DEV V3 projection_vjp_kb4(const bh_project_uniforms& u, const M23& J, V3 mean_c, const S3& cov_c,
+                             const S2& v_cov2d, V2 v_mean2d) {
+    const float* k = u.camera_params;
+    const float fx = u.fx, fy = u.fy;
+    const float mx = mean_c.x, my = mean_c.y, mz = mean_c.z;
+    const float r2 = mx * mx + my * my;
+    const float r = bh_maxf(sqrtf(r2), 1.0e-8f);
+    const float rho2 = r2 + mz * mz;
+    const float theta = bh_atan2f(r, mz);
+    const float th2 = theta * theta, th4 = th2 * th2, th6 = th4 * th2, th8 = th4 * th4;
+    const float theta_d = theta * (1.0f + k[0] * th2 + k[1] * th4 + k[2] * th6 + k[3] * th8);
+    const float p1 = 1.0f + 3.0f * k[0] * th2 + 5.0f * k[1] * th4 + 7.0f * k[2] * th6 + 9.0f * k[3] * th8;
+    const float p2 = 6.0f * k[0] * theta + 20.0f * k[1] * theta * th2 + 42.0f * k[2] * theta * th4 +
+                     72.0f * k[3] * theta * th6;
+    const float inv_r = 1.0f / r;
+    const float inv_r3 = inv_r * inv_r * inv_r;
+    const float inv_r5 = inv_r3 * inv_r * inv_r;
+    const float inv_rho2 = 1.0f / rho2;
+    const float inv_rho2_sq = inv_rho2 * inv_rho2;
+    const float inv_rho2_r = inv_rho2 * inv_r;
+    const float dth_x = mx * mz * inv_rho2_r, dth_y = my * mz * inv_rho2_r, dth_z = -r * inv_rho2;
+    const float xr = mx * inv_r, yr = my * inv_r;
+    const float dxr_x = my * my * inv_r3, dxr_y = -mx * my * inv_r3;
+    const float dyr_x = dxr_y, dyr_y = mx * mx * inv_r3;
+    const float dg_x = p1 * dth_x, dg_y = p1 * dth_y, dg_z = p1 * dth_z;
+    float v_mx = dot(v_mean2d, J.c0);
+    float v_my = dot(v_mean2d, J.c1);
+    float v_mz = dot(v_mean2d, J.c2);
+    const VJ6 vj = cov_jacobian_grad(J, cov_c, v_cov2d);
+    const float three_r2_z2 = 3.0f * r2 + mz * mz;
+    const float r2_minus_z2 = r2 - mz * mz;
+    const float h_th_00 = mz * (r2 * rho2 - mx * mx * three_r2_z2) * inv_r3 * inv_rho2_sq;
+    const float h_th_11 = mz * (r2 * rho2 - my * my * three_r2_z2) * inv_r3 * inv_rho2_sq;
+    const float h_th_01 = -mx * my * mz * three_r2_z2 * inv_r3 * inv_rho2_sq;
+    const float h_th_02 = mx * r2_minus_z2 * inv_r * inv_rho2_sq;
+    const float h_th_12 = my * r2_minus_z2 * inv_r * inv_rho2_sq;
+    const float h_th_22 = 2.0f * mz * r * inv_rho2_sq;
+    const float two_x2_my2 = 2.0f * mx * mx - my * my;
+    const float two_y2_mx2 = 2.0f * my * my - mx * mx;
+    const float h_xr_00 = -3.0f * mx * my * my * inv_r5;
+    const float h_xr_01 = my * two_x2_my2 * inv_r5;
+    const float h_xr_11 = mx * two_y2_mx2 * inv_r5;
+    const float h_yr_00 = my * two_x2_my2 * inv_r5;
+    const float h_yr_01 = mx * two_y2_mx2 * inv_r5;
+    const float h_yr_11 = -3.0f * mx * mx * my * inv_r5;
+    {  // (j, k) = (0, 0)
+        const float d2g = p2 * dth_x * dth_x + p1 * h_th_00;
+        const float d_ju = fx * (d2g * xr + dg_x * dxr_x + dg_x * dxr_x + theta_d * h_xr_00);
+        const float d_jv = fy * (d2g * yr + dg_x * dyr_x + dg_x * dyr_x + theta_d * h_yr_00);
+        v_mx += vj.u0 * d_ju + vj.v0 * d_jv;
+    }
+    {  // (1, 0)
+        const float d2g = p2 * dth_y * dth_x + p1 * h_th_01;
+        const float d_ju = fx * (d2g * xr + dg_y * dxr_x + dg_x * dxr_y + theta_d * h_xr_01);
+        const float d_jv = fy * (d2g * yr + dg_y * dyr_x + dg_x * dyr_y + theta_d * h_yr_01);
+        v_mx += vj.u1 * d_ju + vj.v1 * d_jv;
+    }
+    {  // (2, 0)
+        const float d2g = p2 * dth_z * dth_x + p1 * h_th_02;
+        const float d_ju = fx * (d2g * xr + dg_x * 0.0f + dg_z * dxr_x);
+        const float d_jv = fy * (d2g * yr + dg_x * 0.0f + dg_z * dyr_x);
+        v_mx += vj.u2 * d_ju + vj.v2 * d_jv;
+    }
+    {  // (0, 1)
+        const float d2g = p2 * dth_x * dth_y + p1 * h_th_01;
+        const float d_ju = fx * (d2g * xr + dg_x * dxr_y + dg_y * dxr_x + theta_d * h_xr_01);
+        const float d_jv = fy * (d2g * yr + dg_x * dyr_y + dg_y * dyr_x + theta_d * h_yr_01);
+        v_my += vj.u0 * d_ju + vj.v0 * d_jv;
+    }
+    {  // (1, 1)
+        const float d2g = p2 * dth_y * dth_y + p1 * h_th_11;
+        const float d_ju = fx * (d2g * xr + dg_y * dxr_y + dg_y * dxr_y + theta_d * h_xr_11);
+        const float d_jv = fy * (d2g * yr + dg_y * dyr_y + dg_y * dyr_y + theta_d * h_yr_11);
+        v_my += vj.u1 * d_ju + vj.v1 * d_jv;
+    }
+    {  // (2, 1)
+        const float d2g = p2 * dth_z * dth_y + p1 * h_th_12;
+        const float d_ju = fx * (d2g * xr + dg_y * 0.0f + dg_z * dxr_y);
+        const float d_jv = fy * (d2g * yr + dg_y * 0.0f + dg_z * dyr_y);
+        v_my += vj.u2 * d_ju + vj.v2 * d_jv;
+    }
+    {  // (0, 2)
+        const float d2g = p2 * dth_x * dth_z + p1 * h_th_02;
+        const float d_ju = fx * (d2g * xr + dg_z * dxr_x + dg_x * 0.0f);
+        const float d_jv = fy * (d2g * yr + dg_z * dyr_x + dg_x * 0.0f);
+        v_mz += vj.u0 * d_ju + vj.v0 * d_jv;
+    }
+    {  // (1, 2)
+        const float d2g = p2 * dth_y * dth_z + p1 * h_th_12;
+        const float d_ju = fx * (d2g * xr + dg_z * dxr_y + dg_y * 0.0f);
+        const float d_jv = fy * (d2g * yr + dg_z * dyr_y + dg_y * 0.0f);
+        v_mz += vj.u1 * d_ju + vj.v1 * d_jv;
+    }
+    {  // (2, 2)
+        const float d2g = p2 * dth_z * dth_z + p1 * h_th_22;
+        const float d_ju = fx * (d2g * xr);
+        const float d_jv = fy * (d2g * yr);
+        v_mz += vj.u2 * d_ju + vj.v2 * d_jv;
+    }
+    return v3(v_mx, v_my, v_mz);
+}
+
+// calculate_projection_vjp_rt8 (radial_tangential_8.rs:148-377): the Jacobian
+// is routed through the clamp of the normalised coordinate (surrogate point)
+BH_DEV V3 projection_vjp_rt8(const bh_project_uniforms& u, V3 mean_c, const S3& cov_c, const S2& v_cov2d,
+                             V2 v_mean2d) {
+    const float* k = u.camera_params;
+    const float p1 = k[6], p2 = k[7];
+    const float fx = u.fx, fy = u.fy;
+    const float mx = mean_c.x, my = mean_c.y, mz = mean_c.z;
+    const float inv_z = 1.0f / mz;
+    const float mx_rz_raw = mx * inv_z, my_rz_raw = my * inv_z;
+    const float mx_rz = bh_clampf(mx_rz_raw, u.lim_neg_x, u.lim_pos_x);
+    const float my_rz = bh_clampf(my_rz_raw, u.lim_neg_y, u.lim_pos_y);
+    const bool in_x = mx_rz_raw <= u.lim_pos_x && mx_rz_raw >= u.lim_neg_x;
+    const bool in_y = my_rz_raw <= u.lim_pos_y && my_rz_raw >= u.lim_neg_y;
+    const float xc = mx_rz * mz, yc = my_rz * mz;
+    const float inv_z2 = inv_z * inv_z, inv_z3 = inv_z2 * inv_z;
+    const float x = xc * inv_z, y = yc * inv_z;
+    const float r2 = x * x + y * y, r4 = r2 * r2;
+    const float n_poly = 1.0f + k[0] * r2 + k[1] * r4 + k[2] * r2 * r4;
+    const float dn_poly = 1.0f + k[3] * r2 + k[4] * r4 + k[5] * r2 * r4;
+    const float np_poly = k[0] + 2.0f * k[1] * r2 + 3.0f * k[2] * r4;
+    const float dnp_poly = k[3] + 2.0f * k[4] * r2 + 3.0f * k[5] * r4;
+    const float npp_poly = 2.0f * k[1] + 6.0f * k[2] * r2;
+    const float dnpp_poly = 2.0f * k[4] + 6.0f * k[5] * r2;
+    const float inv_dn = 1.0f / dn_poly, inv_dn2 = inv_dn * inv_dn, inv_dn3 = inv_dn2 * inv_dn;
+    const float rr = n_poly * inv_dn;
+    const float rrp = (np_poly * dn_poly - n_poly * dnp_poly) * inv_dn2;
+    const float rrpp = (npp_poly * dn_poly * dn_poly - 2.0f * np_poly * dn_poly * dnp_poly -
+                        n_poly * dnpp_poly * dn_poly + 2.0f * n_poly * dnp_poly * dnp_poly) *
+                       inv_dn3;
+    const float rx = 2.0f * x * rrp, ry = 2.0f * y * rrp;
+    const float rpx = 2.0f * x * rrpp, rpy = 2.0f * y * rrpp;
+    const float d00 = rr + 2.0f * x * x * rrp + 2.0f * p1 * y + 6.0f * p2 * x;
+    const float d01 = 2.0f * x * y * rrp + 2.0f * p1 * x + 2.0f * p2 * y;
+    const float d10 = d01;
+    const float d11 = rr + 2.0f * y * y * rrp + 6.0f * p1 * y + 2.0f * p2 * x;
+    const float js00 = fx * d00 * inv_z, js01 = fx * d01 * inv_z;
+    const float js02 = -fx * (d00 * xc + d01 * yc) * inv_z2;
+    const float js10 = fy * d10 * inv_z, js11 = fy * d11 * inv_z;
+    const float js12 = -fy * (d10 * xc + d11 * yc) * inv_z2;
+    const float je00 = in_x ? js00 : 0.0f, je10 = in_x ? js10 : 0.0f;
+    const float je01 = in_y ? js01 : 0.0f, je11 = in_y ? js11 : 0.0f;
+    const float je02 = (in_x ? 0.0f : mx_rz * js00) + (in_y ? 0.0f : my_rz * js01) + js02;
+    const float je12 = (in_x ? 0.0f : mx_rz * js10) + (in_y ? 0.0f : my_rz * js11) + js12;
+    float v_mx = je00 * v_mean2d.x + je10 * v_mean2d.y;
+    float v_my = je01 * v_mean2d.x + je11 * v_mean2d.y;
+    float v_mz = je02 * v_mean2d.x + je12 * v_mean2d.y;
+    const VJ6 ve = cov_jacobian_grad(M23{v2(je00, je10), v2(je01, je11), v2(je02, je12)}, cov_c, v_cov2d);
+    const float vs_u0 = in_x ? ve.u0 : mx_rz * ve.u2, vs_v0 = in_x ? ve.v0 : mx_rz * ve.v2;
+    const float vs_u1 = in_y ? ve.u1 : my_rz * ve.u2, vs_v1 = in_y ? ve.v1 : my_rz * ve.v2;
+    const float vs_u2 = ve.u2, vs_v2 = ve.v2;
+    const float dd00_dx = rx + 4.0f * x * rrp + 2.0f * x * x * rpx + 6.0f * p2;
+    const float dd00_dy = ry + 2.0f * x * x * rpy + 2.0f * p1;
+    const float dd01_dx = 2.0f * y * rrp + 2.0f * x * y * rpx + 2.0f * p1;
+    const float dd01_dy = 2.0f * x * rrp + 2.0f * x * y * rpy + 2.0f * p2;
+    const float dd10_dx = dd01_dx, dd10_dy = dd01_dy;
+    const float dd11_dx = rx + 2.0f * y * y * rpx + 2.0f * p2;
+    const float dd11_dy = ry + 4.0f * y * rrp + 2.0f * y * y * rpy + 6.0f * p1;
+    const float dd00_dxc = dd00_dx * inv_z, dd00_dyc = dd00_dy * inv_z;
+    const float dd00_dz = -(xc * dd00_dx + yc * dd00_dy) * inv_z2;
+    const float dd01_dxc = dd01_dx * inv_z, dd01_dyc = dd01_dy * inv_z;
+    const float dd01_dz = -(xc * dd01_dx + yc * dd01_dy) * inv_z2;
+    const float dd10_dxc = dd10_dx * inv_z, dd10_dyc = dd10_dy * inv_z;
+    const float dd10_dz = -(xc * dd10_dx + yc * dd10_dy) * inv_z2;
+    const float dd11_dxc = dd11_dx * inv_z, dd11_dyc = dd11_dy * inv_z;
+    const float dd11_dz = -(xc * dd11_dx + yc * dd11_dy) * inv_z2;
+    const float djs00_dxc = fx * dd00_dxc * inv_z, djs00_dyc = fx * dd00_dyc * inv_z;
+    const float djs00_dz = fx * (dd00_dz * inv_z - d00 * inv_z2);
+    const float djs01_dxc = fx * dd01_dxc * inv_z, djs01_dyc = fx * dd01_dyc * inv_z;
+    const float djs01_dz = fx * (dd01_dz * inv_z - d01 * inv_z2);
+    const float djs10_dxc = fy * dd10_dxc * inv_z, djs10_dyc = fy * dd10_dyc * inv_z;
+    const float djs10_dz = fy * (dd10_dz * inv_z - d10 * inv_z2);
+    const float djs11_dxc = fy * dd11_dxc * inv_z, djs11_dyc = fy * dd11_dyc * inv_z;
+    const float djs11_dz = fy * (dd11_dz * inv_z - d11 * inv_z2);
+    const float djs02_dxc = -fx * (dd00_dxc * xc + d00 + dd01_dxc * yc) * inv_z2;
+    const float djs02_dyc = -fx * (dd00_dyc * xc + dd01_dyc * yc + d01) * inv_z2;
+    const float djs02_dz = -fx * ((dd00_dz * xc + dd01_dz * yc) * inv_z2 - 2.0f * (d00 * xc + d01 * yc) * inv_z3);
+    const float djs12_dxc = -fy * (dd10_dxc * xc + d10 + dd11_dxc * yc) * inv_z2;
+    const float djs12_dyc = -fy * (dd10_dyc * xc + dd11_dyc * yc + d11) * inv_z2;
+    const float djs12_dz = -fy * ((dd10_dz * xc + dd11_dz * yc) * inv_z2 - 2.0f * (d10 * xc + d11 * yc) * inv_z3);
+    const float c_xc = vs_u0 * djs00_dxc + vs_u1 * djs01_dxc + vs_u2 * djs02_dxc + vs_v0 * djs10_dxc +
+                       vs_v1 * djs11_dxc + vs_v2 * djs12_dxc;
+    const float c_yc = vs_u0 * djs00_dyc + vs_u1 * djs01_dyc + vs_u2 * djs02_dyc + vs_v0 * djs10_dyc +
+                       vs_v1 * djs11_dyc + vs_v2 * djs12_dyc;
+    const float c_z = vs_u0 * djs00_dz + vs_u1 * djs01_dz + vs_u2 * djs02_dz + vs_v0 * djs10_dz +
+                      vs_v1 * djs11_dz + vs_v2 * djs12_dz;
+    if (in_x) v_mx += c_xc;
+    if (in_y) v_my += c_yc;
+    v_mz += c_z;
+    if (!in_x) v_mz += mx_rz * c_xc;
+    if (!in_y) v_mz += my_rz * c_yc;
+    return v3(v_mx, v_my, v_mz);
+}
+
+// calculate_projection_vjp_tpf (thin_prism_fisheye.rs:116-203): the KB4 VJP
+// with the full Jacobian plus the tangential / thin-prism Hessian terms
+BH_DEV V3 projection_vjp_tpf(const bh_project_uniforms& u, const M23& J, V3 mean_c, const S3& cov_c,
+                             const S2& v_cov2d, V2 v_mean2d) {
+    const V3 kb = projection_vjp_kb4(u, J, mean_c, cov_c, v_cov2d, v_mean2d);
+    const float p1 = u.camera_params[4], p2 = u.camera_params[5];
+    const float sx1 = u.camera_params[6], sy1 = u.camera_params[7];
+    const float fx = u.fx, fy = u.fy;
+    const float inv_z = 1.0f / mean_c.z;
+    const float inv_z2 = inv_z * inv_z, inv_z3 = inv_z2 * inv_z, inv_z4 = inv_z2 * inv_z2;
+    const PrismPolys t = thin_prism_polys(u, mean_c.x, mean_c.y);
+    const float d2nu_dxx = 6.0f * p2 + 2.0f * sx1, d2nu_dyy = 2.0f * p2 + 2.0f * sx1, d2nu_dxy = 2.0f * p1;
+    const float d2nv_dxx = 2.0f * p1 + 2.0f * sy1, d2nv_dyy = 6.0f * p1 + 2.0f * sy1, d2nv_dxy = 2.0f * p2;
+    const float h_u_00 = d2nu_dxx * inv_z2, h_u_01 = d2nu_dxy * inv_z2, h_u_11 = d2nu_dyy * inv_z2;
+    const float h_u_02 = -2.0f * t.dnu_dx * inv_z3, h_u_12 = -2.0f * t.dnu_dy * inv_z3;
+    const float h_u_22 = 6.0f * t.nu * inv_z4;
+    const float h_v_00 = d2nv_dxx * inv_z2, h_v_01 = d2nv_dxy * inv_z2, h_v_11 = d2nv_dyy * inv_z2;
+    const float h_v_02 = -2.0f * t.dnv_dx * inv_z3, h_v_12 = -2.0f * t.dnv_dy * inv_z3;
+    const float h_v_22 = 6.0f * t.nv * inv_z4;
+    const VJ6 vj = cov_jacobian_grad(J, cov_c, v_cov2d);
+    const float v_mx = fx * (vj.u0 * h_u_00 + vj.u1 * h_u_01 + vj.u2 * h_u_02) +
+                       fy * (vj.v0 * h_v_00 + vj.v1 * h_v_01 + vj.v2 * h_v_02);
+    const float v_my = fx * (vj.u0 * h_u_01 + vj.u1 * h_u_11 + vj.u2 * h_u_12) +
+                       fy * (vj.v0 * h_v_01 + vj.v1 * h_v_11 + vj.v2 * h_v_12);
+    const float v_mz = fx * (vj.u0 * h_u_02 + vj.u1 * h_u_12 + vj.u2 * h_u_22) +
+                       fy * (vj.v0 * h_v_02 + vj.v1 * h_v_12 + vj.v2 * h_v_22);
+    return v3(kb.x + v_mx, kb.y + v_my, kb.z + v_mz);
+}
+
+// calculate_projection_vjp (camera_model/mod.rs:82-126)
+template <int CAM>
+BH_DEV V3 projection_vjp(const bh_project_uniforms& u, const M23& J, V3 mean_c, const S3& cov_c, const S2& v_cov2d,
+                         V2 v_mean2d) {
+    if (CAM == kCamKB4) return projection_vjp_kb4(u, J, mean_c, cov_c, v_cov2d, v_mean2d);
+    if (CAM == kCamRT8) return projection_vjp_rt8(u, mean_c, cov_c, v_cov2d, v_mean2d);
+    if (CAM == kCamTPF) return projection_vjp_tpf(u, J, mean_c, cov_c, v_cov2d, v_mean2d);
+    return projection_vjp_pinhole(u, J, mean_c, cov_c, v_cov2d, v_mean2d);
 }
 
 }  // namespace bh

@@ -33,11 +33,11 @@ struct Projected {
     float depth;
 };
 
-template <bool MIP>
+template <bool MIP, int CAM>
 __device__ bool project_cull(const bh_project_uniforms& u, const float* t, float raw_opac, Projected& o) {
     V3 mean_c = world_to_cam(u, v3(t[0], t[1], t[2]));
     if (!(finite3(mean_c) && mean_c.z <= 1.0e10f)) return false;
-    if (mean_c.z < 0.01f) return false;
+    if (depth_culled<CAM>(u, mean_c)) return false;
     V3 sc = v3(bh_expf(t[7]), bh_expf(t[8]), bh_expf(t[9]));
     if (!finite3(sc)) return false;
     Q4 qu{t[3], t[4], t[5], t[6]};
@@ -45,12 +45,12 @@ __device__ bool project_cull(const bh_project_uniforms& u, const float* t, float
     if (!(qn >= 1.0e-6f && bh_is_finite(qn))) return false;
     if (!bh_is_finite(raw_opac)) return false;
     Q4 q = qnormalize(qu);
-    S2 raw_cov = calc_cov2d(u, sc, q, mean_c);
+    S2 raw_cov = calc_cov2d<CAM>(u, sc, q, mean_c);
     float comp;
     S2 cov = compensate_cov2d<MIP>(raw_cov, comp);
     float opac = bh_sigmoidf(raw_opac) * comp;
     if (!finite2(cov)) return false;
-    V2 m = project_pinhole(u, mean_c);
+    V2 m = project_point<CAM>(u, mean_c);
     if (!(opac >= 1.0f / 255.0f)) return false;
     float pt = bh_logf(opac * 255.0f);
     S2 conic = inverse(cov);
@@ -84,7 +84,7 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     return v;
 }
 
-template <bool MIP>
+template <bool MIP, int CAM>
 __global__ __launch_bounds__(256) void project_forward_kernel(bh_project_uniforms u,
                                                                const float* __restrict__ transforms,
                                                                const float* __restrict__ raw_opac, uint32_t n,
@@ -109,7 +109,7 @@ __global__ __launch_bounds__(256) void project_forward_kernel(bh_project_uniform
             t[2 * i] = q.x;
             t[2 * i + 1] = q.y;
         }
-        vis = project_cull<MIP>(u, t, raw_opac[gid], p);
+        vis = project_cull<MIP, CAM>(u, t, raw_opac[gid], p);
     }
     // count_contributing_tiles (project_forward.rs:120-128) for the whole wave
     const uint32_t hits = wave_tile_walk<false>(lane, vis ? bbox_items(p.bb) : 0u, p.m, p.conic, p.pt, p.bb,
@@ -194,6 +194,22 @@ __global__ __launch_bounds__(1024) void project_reduce_kernel(const uint32_t* __
 
 size_t project_partials_bytes(uint32_t n) { return (size_t)div_up(n, 256) * 8 * sizeof(uint32_t); }
 
+template <bool MIP>
+static void launch_pf(bh_ctx* ctx, uint32_t blocks, const bh_project_uniforms& u, const float* transforms,
+                      const float* raw_opac, uint32_t n, uint32_t* intersect_counts, float* max_radius,
+                      uint32_t* depth_keys, uint32_t* partials) {
+#define BH_PF(C)                                                                                                 \
+    project_forward_kernel<MIP, C><<<blocks, 256, 0, ctx->stream>>>(u, transforms, raw_opac, n, intersect_counts, \
+                                                                    max_radius, depth_keys, partials)
+    switch (u.camera_model) {
+        case kCamKB4: BH_PF(kCamKB4); break;
+        case kCamRT8: BH_PF(kCamRT8); break;
+        case kCamTPF: BH_PF(kCamTPF); break;
+        default: BH_PF(kCamPinhole); break;
+    }
+#undef BH_PF
+}
+
 void launch_project_forward(bh_ctx* ctx, const bh_project_uniforms& u, const float* transforms,
                             const float* raw_opac, uint32_t n, bool mip, uint32_t* intersect_counts,
                             float* max_radius, uint32_t* depth_keys, uint32_t* partials, uint32_t* counters) {
@@ -202,13 +218,11 @@ void launch_project_forward(bh_ctx* ctx, const bh_project_uniforms& u, const flo
     {
         KernelTimer t(ctx, "project_forward");
         if (mip)
-            project_forward_kernel<true><<<blocks, 256, 0, ctx->stream>>>(u, transforms, raw_opac, n,
-                                                                           intersect_counts, max_radius, depth_keys,
-                                                                           partials);
+            launch_pf<true>(ctx, blocks, u, transforms, raw_opac, n, intersect_counts, max_radius, depth_keys,
+                            partials);
         else
-            project_forward_kernel<false><<<blocks, 256, 0, ctx->stream>>>(u, transforms, raw_opac, n,
-                                                                            intersect_counts, max_radius, depth_keys,
-                                                                            partials);
+            launch_pf<false>(ctx, blocks, u, transforms, raw_opac, n, intersect_counts, max_radius, depth_keys,
+                             partials);
     }
     KernelTimer t(ctx, "project_reduce");
     project_reduce_kernel<<<1, 1024, 0, ctx->stream>>>(partials, blocks, counters);
@@ -235,7 +249,7 @@ __device__ __forceinline__ void load_sh_row(const float* __restrict__ sh, uint32
     }
 }
 
-template <int DEG, bool MIP>
+template <int DEG, bool MIP, int CAM>
 __global__ __launch_bounds__(256) void project_visible_kernel(bh_project_uniforms u,
                                                                const float* __restrict__ transforms,
                                                                const float* __restrict__ sh,
@@ -261,12 +275,12 @@ __global__ __launch_bounds__(256) void project_visible_kernel(bh_project_uniform
     V3 sc = v3(bh_expf(t[7]), bh_expf(t[8]), bh_expf(t[9]));
     Q4 q = qnormalize(Q4{t[3], t[4], t[5], t[6]});
     V3 mean_c = world_to_cam(u, mean);
-    S2 raw_cov = calc_cov2d(u, sc, q, mean_c);
+    S2 raw_cov = calc_cov2d<CAM>(u, sc, q, mean_c);
     float comp;
     S2 cov = compensate_cov2d<MIP>(raw_cov, comp);
     float opac = bh_sigmoidf(raw_opac[gid]) * comp;
     S2 conic = inverse(cov);
-    V2 m = project_pinhole(u, mean_c);
+    V2 m = project_point<CAM>(u, mean_c);
     V3 v = mean - v3(u.camera_pos[0], u.camera_pos[1], u.camera_pos[2]);
     v = v * (1.0f / sqrtf(dot(v, v)));
     V3 raw = sh_to_color<DEG>(coeffs, v);
@@ -288,18 +302,31 @@ __global__ __launch_bounds__(256) void project_visible_kernel(bh_project_uniform
     depths[c] = mean_c.z;
 }
 
+template <int DEG, bool MIP>
+static void launch_pv_cam(bh_ctx* ctx, uint32_t blocks, const bh_project_uniforms& u, const float* transforms,
+                          const float* sh, const float* raw_opac, const uint32_t* gfc, uint32_t num_visible,
+                          float* projected, float* depths) {
+#define BH_PV(C)                                                                                              \
+    project_visible_kernel<DEG, MIP, C><<<blocks, 256, 0, ctx->stream>>>(u, transforms, sh, raw_opac, gfc,     \
+                                                                         num_visible, u.total_splats, projected, \
+                                                                         depths)
+    switch (u.camera_model) {
+        case kCamKB4: BH_PV(kCamKB4); break;
+        case kCamRT8: BH_PV(kCamRT8); break;
+        case kCamTPF: BH_PV(kCamTPF); break;
+        default: BH_PV(kCamPinhole); break;
+    }
+#undef BH_PV
+}
+
 template <int DEG>
 static void launch_pv(bh_ctx* ctx, bool mip, uint32_t blocks, const bh_project_uniforms& u, const float* transforms,
                       const float* sh, const float* raw_opac, const uint32_t* gfc, uint32_t num_visible,
                       float* projected, float* depths) {
     if (mip)
-        project_visible_kernel<DEG, true><<<blocks, 256, 0, ctx->stream>>>(u, transforms, sh, raw_opac, gfc,
-                                                                           num_visible, u.total_splats, projected,
-                                                                           depths);
+        launch_pv_cam<DEG, true>(ctx, blocks, u, transforms, sh, raw_opac, gfc, num_visible, projected, depths);
     else
-        project_visible_kernel<DEG, false><<<blocks, 256, 0, ctx->stream>>>(u, transforms, sh, raw_opac, gfc,
-                                                                            num_visible, u.total_splats, projected,
-                                                                            depths);
+        launch_pv_cam<DEG, false>(ctx, blocks, u, transforms, sh, raw_opac, gfc, num_visible, projected, depths);
 }
 
 void launch_project_visible(bh_ctx* ctx, const bh_project_uniforms& u, const float* transforms, const float* sh,

@@ -78,7 +78,19 @@ typedef struct bh_project_uniforms {
     uint32_t sh_degree;
     uint32_t total_splats;
     uint32_t num_visible; /* filled in by the forward pass */
+    /* CameraModel (brush-render/src/kernels/camera_model/mod.rs:34-41): one of
+     * BH_CAMERA_* and its coefficients, in the order of the reference's
+     * parameter structs: KB4 k1..k4; RT8 k1..k6, p1, p2; TPF k1..k4, p1, p2,
+     * sx1, sy1 (kannala_brandt_4.rs:11-16, radial_tangential_8.rs:12-21,
+     * thin_prism_fisheye.rs:23-30).  Unused entries are ignored. */
+    uint32_t camera_model;
+    float camera_params[8];
 } bh_project_uniforms;
+
+#define BH_CAMERA_PINHOLE 0u
+#define BH_CAMERA_KB4 1u /* Kannala-Brandt 4 (equidistant fisheye) */
+#define BH_CAMERA_RT8 2u /* radial-tangential with 6 radial + 2 tangential */
+#define BH_CAMERA_TPF 3u /* thin-prism fisheye: KB4 + tangential + thin prism */
 
 typedef struct bh_ctx bh_ctx;
 typedef struct bh_fwd_state bh_fwd_state;

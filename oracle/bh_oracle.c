@@ -202,10 +202,178 @@ static m23 jac_pinhole(const bh_project_uniforms* u, v3 p) {
     m23 m = {mk2(dx, 0.0f), mk2(0.0f, dy), mk2(-dx * cxl, -dy * cyl)};
     return m;
 }
+/* ---- camera models (kernels/camera_model/{kannala_brandt_4,
+ * radial_tangential_8,thin_prism_fisheye}.rs).  u->camera_params holds the
+ * coefficients in the reference's struct order: KB4 k1..k4, RT8 k1..k6 p1 p2,
+ * TPF k1..k4 p1 p2 sx1 sy1. */
+static m23 mkm23(float a00, float a10, float a01, float a11, float a02, float a12) {
+    m23 m = {mk2(a00, a10), mk2(a01, a11), mk2(a02, a12)};
+    return m;
+}
+/* project_kb4 (kannala_brandt_4.rs:18-52) */
+static v2 kb4_project(const bh_project_uniforms* u, v3 p) {
+    const float* k = u->camera_params;
+    float inv_z = 1.0f / p.z;
+    float pu = u->fx * p.x * inv_z + u->cx;
+    float pv = u->fy * p.y * inv_z + u->cy;
+    float r = sqrtf(p.x * p.x + p.y * p.y);
+    float th = bh_atan2f(r, p.z);
+    float th2 = th * th;
+    float th4 = th2 * th2;
+    float th6 = th2 * th4;
+    float th8 = th4 * th4;
+    float d = th * (1.0f + k[0] * th2 + k[1] * th4 + k[2] * th6 + k[3] * th8);
+    float inv_r = 1.0f / r;
+    float fu = u->fx * (d * p.x * inv_r) + u->cx;
+    float fv = u->fy * (d * p.y * inv_r) + u->cy;
+    if (r < 1e-6f) return mk2(pu, pv);
+    return mk2(fu, fv);
+}
+/* calculate_project_jacobian_kb4 (kannala_brandt_4.rs:54-136) */
+static m23 kb4_jacobian(const bh_project_uniforms* u, v3 p) {
+    const float* k = u->camera_params;
+    float fx = u->fx, fy = u->fy, x = p.x, y = p.y, z = p.z;
+    float inv_z = 1.0f / z;
+    float x2 = x * x, y2 = y * y, xy = x * y;
+    float r2 = x2 + y2;
+    float r = sqrtf(r2);
+    float inv_r = 1.0f / r;
+    float inv_r3 = inv_r * inv_r * inv_r;
+    float rho2 = r2 + z * z;
+    float inv_rho2 = 1.0f / rho2;
+    float inv_rho2_r = inv_rho2 * inv_r;
+    float th = bh_atan2f(r, z);
+    float th2 = th * th, th4 = th2 * th2, th6 = th4 * th2, th8 = th4 * th4;
+    float d = th * (1.0f + k[0] * th2 + k[1] * th4 + k[2] * th6 + k[3] * th8);
+    float ddt = 1.0f + 3.0f * k[0] * th2 + 5.0f * k[1] * th4 + 7.0f * k[2] * th6 + 9.0f * k[3] * th8;
+    float dth_dx = x * z * inv_rho2_r;
+    float dth_dy = y * z * inv_rho2_r;
+    float dth_dz = -r * inv_rho2;
+    float dd_dx = ddt * dth_dx, dd_dy = ddt * dth_dy, dd_dz = ddt * dth_dz;
+    float xr = x * inv_r;
+    float dxr_dx = y2 * inv_r3;
+    float dxr_dy = -xy * inv_r3;
+    float yr = y * inv_r;
+    float dyr_dx = -xy * inv_r3;
+    float dyr_dy = x2 * inv_r3;
+    if (r < 1e-6f) {
+        float ddx = fx * inv_z, ddy = fy * inv_z;
+        return mkm23(ddx, 0.0f, 0.0f, ddy, -ddx * x * inv_z, -ddy * y * inv_z);
+    }
+    return mkm23(fx * (dd_dx * xr + d * dxr_dx), fy * (dd_dx * yr + d * dyr_dx), fx * (dd_dy * xr + d * dxr_dy),
+                 fy * (dd_dy * yr + d * dyr_dy), fx * (dd_dz * xr), fy * (dd_dz * yr));
+}
+/* project_rt8 (radial_tangential_8.rs:24-69) */
+static v2 rt8_project(const bh_project_uniforms* u, v3 p) {
+    const float* k = u->camera_params;
+    float p1 = k[6], p2 = k[7];
+    float xn = p.x / p.z, yn = p.y / p.z;
+    float xn2 = xn * xn, yn2 = yn * yn;
+    float r2 = xn2 + yn2;
+    float r4 = r2 * r2;
+    float r6 = r4 * r2;
+    float d = (1.0f + k[0] * r2 + k[1] * r4 + k[2] * r6) / (1.0f + k[3] * r2 + k[4] * r4 + k[5] * r6);
+    float xy = xn * yn;
+    float xd = xn * d + 2.0f * p1 * xy + p2 * (r2 + 2.0f * xn2);
+    float yd = yn * d + 2.0f * p2 * xy + p1 * (r2 + 2.0f * yn2);
+    return mk2(u->fx * xd + u->cx, u->fy * yd + u->cy);
+}
+/* radial term R(r2) = N/Dn and R', R'' with respect to r2 (both RT8 paths) */
+typedef struct { float n, dn, np, dnp; } rt8_polys;
+/* calculate_project_jacobian_rt8 (radial_tangential_8.rs:71-146) */
+static m23 rt8_jacobian(const bh_project_uniforms* u, v3 p) {
+    const float* k = u->camera_params;
+    float p1 = k[6], p2 = k[7], fx = u->fx, fy = u->fy, z = p.z;
+    float inv_z = 1.0f / z;
+    float inv_z2 = inv_z * inv_z;
+    float xn = bh_clampf(p.x * inv_z, u->lim_neg_x, u->lim_pos_x);
+    float yn = bh_clampf(p.y * inv_z, u->lim_neg_y, u->lim_pos_y);
+    float xc = xn * z, yc = yn * z;
+    float r2 = xn * xn + yn * yn;
+    float r4 = r2 * r2;
+    float r6 = r4 * r2;
+    float n = 1.0f + k[0] * r2 + k[1] * r4 + k[2] * r6;
+    float dn = 1.0f + k[3] * r2 + k[4] * r4 + k[5] * r6;
+    float np = k[0] + 2.0f * k[1] * r2 + 3.0f * k[2] * r4;
+    float dnp = k[3] + 2.0f * k[4] * r2 + 3.0f * k[5] * r4;
+    float inv_dn = 1.0f / dn;
+    float inv_dn2 = inv_dn * inv_dn;
+    float rv = n * inv_dn;
+    float rp = (np * dn - n * dnp) * inv_dn2;
+    float d00 = rv + 2.0f * xn * xn * rp + 2.0f * p1 * yn + 6.0f * p2 * xn;
+    float d01 = 2.0f * xn * yn * rp + 2.0f * p1 * xn + 2.0f * p2 * yn;
+    float d10 = d01;
+    float d11 = rv + 2.0f * yn * yn * rp + 6.0f * p1 * yn + 2.0f * p2 * xn;
+    return mkm23(fx * d00 * inv_z, fy * d10 * inv_z, fx * d01 * inv_z, fy * d11 * inv_z,
+                 -fx * (d00 * xc + d01 * yc) * inv_z2, -fy * (d10 * xc + d11 * yc) * inv_z2);
+}
+/* thin_prism_polys (thin_prism_fisheye.rs:37-63): out = Nu, Nv, dNu/dx,
+ * dNu/dy, dNv/dx, dNv/dy at camera-space (x, y) */
+static void tpf_polys(const bh_project_uniforms* u, float x, float y, float* o) {
+    float p1 = u->camera_params[4], p2 = u->camera_params[5];
+    float sx1 = u->camera_params[6], sy1 = u->camera_params[7];
+    float x2 = x * x, y2 = y * y, xy = x * y;
+    float r2 = x2 + y2;
+    o[0] = 2.0f * p1 * xy + p2 * (3.0f * x2 + y2) + sx1 * r2;
+    o[1] = 2.0f * p2 * xy + p1 * (x2 + 3.0f * y2) + sy1 * r2;
+    o[2] = 2.0f * (p1 * y + (3.0f * p2 + sx1) * x);
+    o[3] = 2.0f * (p1 * x + (p2 + sx1) * y);
+    o[4] = 2.0f * (p2 * y + (p1 + sy1) * x);
+    o[5] = 2.0f * (p2 * x + (3.0f * p1 + sy1) * y);
+}
+/* project_tpf (thin_prism_fisheye.rs:65-81) */
+static v2 tpf_project(const bh_project_uniforms* u, v3 p) {
+    v2 kb = kb4_project(u, p);
+    float inv_z = 1.0f / p.z;
+    float inv_z2 = inv_z * inv_z;
+    float t[6];
+    tpf_polys(u, p.x, p.y, t);
+    return mk2(kb.x + u->fx * t[0] * inv_z2, kb.y + u->fy * t[1] * inv_z2);
+}
+/* calculate_project_jacobian_tpf (thin_prism_fisheye.rs:83-114) */
+static m23 tpf_jacobian(const bh_project_uniforms* u, v3 p) {
+    m23 kb = kb4_jacobian(u, p);
+    float fx = u->fx, fy = u->fy;
+    float inv_z = 1.0f / p.z;
+    float inv_z2 = inv_z * inv_z;
+    float inv_z3 = inv_z2 * inv_z;
+    float t[6];
+    tpf_polys(u, p.x, p.y, t);
+    return mkm23(kb.c0.x + fx * t[2] * inv_z2, kb.c0.y + fy * t[4] * inv_z2, kb.c1.x + fx * t[3] * inv_z2,
+                 kb.c1.y + fy * t[5] * inv_z2, kb.c2.x + -2.0f * fx * t[0] * inv_z3,
+                 kb.c2.y + -2.0f * fy * t[1] * inv_z3);
+}
+/* project (camera_model/mod.rs:50-62) */
+static void project_point(const bh_project_uniforms* u, v3 p, float* ox, float* oy) {
+    v2 r;
+    switch (u->camera_model) {
+        case BH_CAMERA_KB4: r = kb4_project(u, p); break;
+        case BH_CAMERA_RT8: r = rt8_project(u, p); break;
+        case BH_CAMERA_TPF: r = tpf_project(u, p); break;
+        default: project_pinhole(u, p, ox, oy); return;
+    }
+    *ox = r.x;
+    *oy = r.y;
+}
+/* calculate_project_jacobian (camera_model/mod.rs:64-80) */
+static m23 cam_jacobian(const bh_project_uniforms* u, v3 p) {
+    switch (u->camera_model) {
+        case BH_CAMERA_KB4: return kb4_jacobian(u, p);
+        case BH_CAMERA_RT8: return rt8_jacobian(u, p);
+        case BH_CAMERA_TPF: return tpf_jacobian(u, p);
+        default: return jac_pinhole(u, p);
+    }
+}
+/* the depth cull of project_forward (project_forward.rs:49-62) */
+static int depth_culled(const bh_project_uniforms* u, v3 mean_c) {
+    if (u->camera_model == BH_CAMERA_PINHOLE) return mean_c.z < 0.01f;
+    float r = sqrtf(mean_c.x * mean_c.x + mean_c.y * mean_c.y);
+    return bh_atan2f(r, mean_c.z) > u->half_max_render_fov;
+}
 /* calc_cov2d (kernels/helpers.rs:297-330) */
 static s2 calc_cov2d(const bh_project_uniforms* u, v3 scale, qt quat, v3 mean_c) {
     m3 ns = m3diag(m3mul(view_rot(u), qmat(quat)), scale);
-    m23 jac = jac_pinhole(u, mean_c);
+    m23 jac = cam_jacobian(u, mean_c);
     m23 v = m23mul(jac, ns);
     s2 raw = m23gram(v);
     float lim = 1.0e18f;
@@ -294,7 +462,7 @@ static int project_one(const bh_project_uniforms* u, const float* t, float raw_o
                        uint32_t* count, float* radius, float* depth) {
     v3 mean_c = world_to_cam(u, mk3(t[0], t[1], t[2]));
     if (!(fin3(mean_c) && mean_c.z <= 1.0e10f)) return 0;
-    if (mean_c.z < 0.01f) return 0;
+    if (depth_culled(u, mean_c)) return 0;
     v3 scale = mk3(bh_expf(t[7]), bh_expf(t[8]), bh_expf(t[9]));
     if (!fin3(scale)) return 0;
     qt qu = {t[3], t[4], t[5], t[6]};
@@ -308,7 +476,7 @@ static int project_one(const bh_project_uniforms* u, const float* t, float raw_o
     float opac = bh_sigmoidf(raw_opac) * comp;
     if (!s2fin(cov)) return 0;
     float mx, my;
-    project_pinhole(u, mean_c, &mx, &my);
+    project_point(u, mean_c, &mx, &my);
     if (!(opac >= 1.0f / 255.0f)) return 0;
     float pt = bh_logf(opac * 255.0f);
     s2 conic = s2inv(cov);
@@ -490,7 +658,7 @@ void or_project_visible(const bh_project_uniforms* u, const float* transforms,
         float opac = bh_sigmoidf(raw_opac[g]) * comp;
         s2 conic = s2inv(cov);
         float mx, my;
-        project_pinhole(u, mean_c, &mx, &my);
+        project_point(u, mean_c, &mx, &my);
         v3 v = sub3(mean, mk3(u->camera_pos[0], u->camera_pos[1], u->camera_pos[2]));
         v = scl3(v, 1.0f / len3(v));
         v3 raw = sh_to_color(sh_coeffs + (size_t)g * nc * 3, sh_degree, v);
@@ -835,7 +1003,7 @@ static s2 inverse2x2_vjp(s2 m, s2 v) {
     return r;
 }
 /* calculate_projection_vjp_pinhole (camera_model/pinhole.rs:58-123) */
-static v3 projection_vjp(const bh_project_uniforms* u, m23 J, v3 mean_c, s3 cov_c, s2 v_cov2d,
+static v3 pinhole_projection_vjp(const bh_project_uniforms* u, m23 J, v3 mean_c, s3 cov_c, s2 v_cov2d,
                          v2 v_mean2d) {
     float fx = u->fx, fy = u->fy;
     float mx = mean_c.x, my = mean_c.y, mz = mean_c.z;
@@ -863,6 +1031,246 @@ static v3 projection_vjp(const bh_project_uniforms* u, m23 J, v3 mean_c, s3 cov_
     else v_mz += -fy * inv_z3 * vj21 * ty;
     v_mz += -fx * inv_z2 * vj00 - fy * inv_z2 * vj11 + 2.0f * fx * tx * inv_z3 * vj20 + 2.0f * fy * ty * inv_z3 * vj21;
     return mk3(v_mx, v_my, v_mz);
+}
+/* 2 (v_cov2d J) cov_c as rows u (o[0..2]) and v (o[3..5]) */
+static void cov_jac_grad(m23 J, s3 cov_c, s2 v_cov2d, float* o) {
+    m23 tmp = s2mulm23(v_cov2d, J);
+    o[0] = 2.0f * dot3(m23row0(tmp), s3row0(cov_c));
+    o[1] = 2.0f * dot3(m23row0(tmp), s3row1(cov_c));
+    o[2] = 2.0f * dot3(m23row0(tmp), s3row2(cov_c));
+    o[3] = 2.0f * dot3(m23row1(tmp), s3row0(cov_c));
+    o[4] = 2.0f * dot3(m23row1(tmp), s3row1(cov_c));
+    o[5] = 2.0f * dot3(m23row1(tmp), s3row2(cov_c));
+}
+/* calculate_projection_vjp_kb4 (kannala_brandt_4.rs:138-337) */
+static v3 kb4_projection_vjp(const bh_project_uniforms* u, m23 J, v3 mean_c, s3 cov_c, s2 v_cov2d, v2 v_mean2d) {
+    const float* k = u->camera_params;
+    float fx = u->fx, fy = u->fy, mx = mean_c.x, my = mean_c.y, mz = mean_c.z;
+    float r2 = mx * mx + my * my;
+    float r = bh_maxf(sqrtf(r2), 1.0e-8f);
+    float rho2 = r2 + mz * mz;
+    float th = bh_atan2f(r, mz);
+    float th2 = th * th, th4 = th2 * th2, th6 = th4 * th2, th8 = th4 * th4;
+    float theta_d = th * (1.0f + k[0] * th2 + k[1] * th4 + k[2] * th6 + k[3] * th8);
+    float p1 = 1.0f + 3.0f * k[0] * th2 + 5.0f * k[1] * th4 + 7.0f * k[2] * th6 + 9.0f * k[3] * th8;
+    float p2 = 6.0f * k[0] * th + 20.0f * k[1] * th * th2 + 42.0f * k[2] * th * th4 + 72.0f * k[3] * th * th6;
+    float inv_r = 1.0f / r;
+    float inv_r3 = inv_r * inv_r * inv_r;
+    float inv_r5 = inv_r3 * inv_r * inv_r;
+    float inv_rho2 = 1.0f / rho2;
+    float inv_rho2_sq = inv_rho2 * inv_rho2;
+    float inv_rho2_r = inv_rho2 * inv_r;
+    float dth_x = mx * mz * inv_rho2_r, dth_y = my * mz * inv_rho2_r, dth_z = -r * inv_rho2;
+    float xr = mx * inv_r, yr = my * inv_r;
+    float dxr_x = my * my * inv_r3, dxr_y = -mx * my * inv_r3;
+    float dyr_x = dxr_y, dyr_y = mx * mx * inv_r3;
+    float dg_x = p1 * dth_x, dg_y = p1 * dth_y, dg_z = p1 * dth_z;
+    float v_mx = dot2(v_mean2d, J.c0), v_my = dot2(v_mean2d, J.c1), v_mz = dot2(v_mean2d, J.c2);
+    float vj[6];
+    cov_jac_grad(J, cov_c, v_cov2d, vj);
+    float three_r2_z2 = 3.0f * r2 + mz * mz;
+    float r2_minus_z2 = r2 - mz * mz;
+    float h00 = mz * (r2 * rho2 - mx * mx * three_r2_z2) * inv_r3 * inv_rho2_sq;
+    float h11 = mz * (r2 * rho2 - my * my * three_r2_z2) * inv_r3 * inv_rho2_sq;
+    float h01 = -mx * my * mz * three_r2_z2 * inv_r3 * inv_rho2_sq;
+    float h02 = mx * r2_minus_z2 * inv_r * inv_rho2_sq;
+    float h12 = my * r2_minus_z2 * inv_r * inv_rho2_sq;
+    float h22 = 2.0f * mz * r * inv_rho2_sq;
+    float two_x2_my2 = 2.0f * mx * mx - my * my;
+    float two_y2_mx2 = 2.0f * my * my - mx * mx;
+    float hx00 = -3.0f * mx * my * my * inv_r5;
+    float hx01 = my * two_x2_my2 * inv_r5;
+    float hx11 = mx * two_y2_mx2 * inv_r5;
+    float hy00 = my * two_x2_my2 * inv_r5;
+    float hy01 = mx * two_y2_mx2 * inv_r5;
+    float hy11 = -3.0f * mx * mx * my * inv_r5;
+    float d2g, du, dv;
+    /* d/dx: j = 0, 1, 2 */
+    d2g = p2 * dth_x * dth_x + p1 * h00;
+    du = fx * (d2g * xr + dg_x * dxr_x + dg_x * dxr_x + theta_d * hx00);
+    dv = fy * (d2g * yr + dg_x * dyr_x + dg_x * dyr_x + theta_d * hy00);
+    v_mx += vj[0] * du + vj[3] * dv;
+    d2g = p2 * dth_y * dth_x + p1 * h01;
+    du = fx * (d2g * xr + dg_y * dxr_x + dg_x * dxr_y + theta_d * hx01);
+    dv = fy * (d2g * yr + dg_y * dyr_x + dg_x * dyr_y + theta_d * hy01);
+    v_mx += vj[1] * du + vj[4] * dv;
+    d2g = p2 * dth_z * dth_x + p1 * h02;
+    du = fx * (d2g * xr + dg_x * 0.0f + dg_z * dxr_x);
+    dv = fy * (d2g * yr + dg_x * 0.0f + dg_z * dyr_x);
+    v_mx += vj[2] * du + vj[5] * dv;
+    /* d/dy */
+    d2g = p2 * dth_x * dth_y + p1 * h01;
+    du = fx * (d2g * xr + dg_x * dxr_y + dg_y * dxr_x + theta_d * hx01);
+    dv = fy * (d2g * yr + dg_x * dyr_y + dg_y * dyr_x + theta_d * hy01);
+    v_my += vj[0] * du + vj[3] * dv;
+    d2g = p2 * dth_y * dth_y + p1 * h11;
+    du = fx * (d2g * xr + dg_y * dxr_y + dg_y * dxr_y + theta_d * hx11);
+    dv = fy * (d2g * yr + dg_y * dyr_y + dg_y * dyr_y + theta_d * hy11);
+    v_my += vj[1] * du + vj[4] * dv;
+    d2g = p2 * dth_z * dth_y + p1 * h12;
+    du = fx * (d2g * xr + dg_y * 0.0f + dg_z * dxr_y);
+    dv = fy * (d2g * yr + dg_y * 0.0f + dg_z * dyr_y);
+    v_my += vj[2] * du + vj[5] * dv;
+    /* d/dz */
+    d2g = p2 * dth_x * dth_z + p1 * h02;
+    du = fx * (d2g * xr + dg_z * dxr_x + dg_x * 0.0f);
+    dv = fy * (d2g * yr + dg_z * dyr_x + dg_x * 0.0f);
+    v_mz += vj[0] * du + vj[3] * dv;
+    d2g = p2 * dth_y * dth_z + p1 * h12;
+    du = fx * (d2g * xr + dg_z * dxr_y + dg_y * 0.0f);
+    dv = fy * (d2g * yr + dg_z * dyr_y + dg_y * 0.0f);
+    v_mz += vj[1] * du + vj[4] * dv;
+    d2g = p2 * dth_z * dth_z + p1 * h22;
+    du = fx * (d2g * xr);
+    dv = fy * (d2g * yr);
+    v_mz += vj[2] * du + vj[5] * dv;
+    return mk3(v_mx, v_my, v_mz);
+}
+/* calculate_projection_vjp_rt8 (radial_tangential_8.rs:148-377) */
+static v3 rt8_projection_vjp(const bh_project_uniforms* u, v3 mean_c, s3 cov_c, s2 v_cov2d, v2 v_mean2d) {
+    const float* k = u->camera_params;
+    float p1 = k[6], p2 = k[7], fx = u->fx, fy = u->fy;
+    float mx = mean_c.x, my = mean_c.y, mz = mean_c.z;
+    float inv_z = 1.0f / mz;
+    float rx_raw = mx * inv_z, ry_raw = my * inv_z;
+    float mx_rz = bh_clampf(rx_raw, u->lim_neg_x, u->lim_pos_x);
+    float my_rz = bh_clampf(ry_raw, u->lim_neg_y, u->lim_pos_y);
+    int in_x = rx_raw <= u->lim_pos_x && rx_raw >= u->lim_neg_x;
+    int in_y = ry_raw <= u->lim_pos_y && ry_raw >= u->lim_neg_y;
+    float xc = mx_rz * mz, yc = my_rz * mz;
+    float inv_z2 = inv_z * inv_z;
+    float inv_z3 = inv_z2 * inv_z;
+    float x = xc * inv_z, y = yc * inv_z;
+    float r2 = x * x + y * y;
+    float r4 = r2 * r2;
+    float n = 1.0f + k[0] * r2 + k[1] * r4 + k[2] * r2 * r4;
+    float dn = 1.0f + k[3] * r2 + k[4] * r4 + k[5] * r2 * r4;
+    float np = k[0] + 2.0f * k[1] * r2 + 3.0f * k[2] * r4;
+    float dnp = k[3] + 2.0f * k[4] * r2 + 3.0f * k[5] * r4;
+    float npp = 2.0f * k[1] + 6.0f * k[2] * r2;
+    float dnpp = 2.0f * k[4] + 6.0f * k[5] * r2;
+    float inv_dn = 1.0f / dn;
+    float inv_dn2 = inv_dn * inv_dn;
+    float inv_dn3 = inv_dn2 * inv_dn;
+    float rr = n * inv_dn;
+    float rrp = (np * dn - n * dnp) * inv_dn2;
+    float rrpp = (npp * dn * dn - 2.0f * np * dn * dnp - n * dnpp * dn + 2.0f * n * dnp * dnp) * inv_dn3;
+    float rx = 2.0f * x * rrp, ry = 2.0f * y * rrp;
+    float rpx = 2.0f * x * rrpp, rpy = 2.0f * y * rrpp;
+    float d00 = rr + 2.0f * x * x * rrp + 2.0f * p1 * y + 6.0f * p2 * x;
+    float d01 = 2.0f * x * y * rrp + 2.0f * p1 * x + 2.0f * p2 * y;
+    float d10 = d01;
+    float d11 = rr + 2.0f * y * y * rrp + 6.0f * p1 * y + 2.0f * p2 * x;
+    float js00 = fx * d00 * inv_z, js01 = fx * d01 * inv_z, js02 = -fx * (d00 * xc + d01 * yc) * inv_z2;
+    float js10 = fy * d10 * inv_z, js11 = fy * d11 * inv_z, js12 = -fy * (d10 * xc + d11 * yc) * inv_z2;
+    float je00 = in_x ? js00 : 0.0f, je10 = in_x ? js10 : 0.0f;
+    float je01 = in_y ? js01 : 0.0f, je11 = in_y ? js11 : 0.0f;
+    float je02 = (in_x ? 0.0f : mx_rz * js00) + (in_y ? 0.0f : my_rz * js01) + js02;
+    float je12 = (in_x ? 0.0f : mx_rz * js10) + (in_y ? 0.0f : my_rz * js11) + js12;
+    float v_mx = je00 * v_mean2d.x + je10 * v_mean2d.y;
+    float v_my = je01 * v_mean2d.x + je11 * v_mean2d.y;
+    float v_mz = je02 * v_mean2d.x + je12 * v_mean2d.y;
+    float ve[6];
+    cov_jac_grad(mkm23(je00, je10, je01, je11, je02, je12), cov_c, v_cov2d, ve);
+    float su0 = in_x ? ve[0] : mx_rz * ve[2], sv0 = in_x ? ve[3] : mx_rz * ve[5];
+    float su1 = in_y ? ve[1] : my_rz * ve[2], sv1 = in_y ? ve[4] : my_rz * ve[5];
+    float su2 = ve[2], sv2 = ve[5];
+    float a00x = rx + 4.0f * x * rrp + 2.0f * x * x * rpx + 6.0f * p2;
+    float a00y = ry + 2.0f * x * x * rpy + 2.0f * p1;
+    float a01x = 2.0f * y * rrp + 2.0f * x * y * rpx + 2.0f * p1;
+    float a01y = 2.0f * x * rrp + 2.0f * x * y * rpy + 2.0f * p2;
+    float a10x = a01x, a10y = a01y;
+    float a11x = rx + 2.0f * y * y * rpx + 2.0f * p2;
+    float a11y = ry + 4.0f * y * rrp + 2.0f * y * y * rpy + 6.0f * p1;
+    float b00xc = a00x * inv_z, b00yc = a00y * inv_z, b00z = -(xc * a00x + yc * a00y) * inv_z2;
+    float b01xc = a01x * inv_z, b01yc = a01y * inv_z, b01z = -(xc * a01x + yc * a01y) * inv_z2;
+    float b10xc = a10x * inv_z, b10yc = a10y * inv_z, b10z = -(xc * a10x + yc * a10y) * inv_z2;
+    float b11xc = a11x * inv_z, b11yc = a11y * inv_z, b11z = -(xc * a11x + yc * a11y) * inv_z2;
+    float j00xc = fx * b00xc * inv_z, j00yc = fx * b00yc * inv_z, j00z = fx * (b00z * inv_z - d00 * inv_z2);
+    float j01xc = fx * b01xc * inv_z, j01yc = fx * b01yc * inv_z, j01z = fx * (b01z * inv_z - d01 * inv_z2);
+    float j10xc = fy * b10xc * inv_z, j10yc = fy * b10yc * inv_z, j10z = fy * (b10z * inv_z - d10 * inv_z2);
+    float j11xc = fy * b11xc * inv_z, j11yc = fy * b11yc * inv_z, j11z = fy * (b11z * inv_z - d11 * inv_z2);
+    float j02xc = -fx * (b00xc * xc + d00 + b01xc * yc) * inv_z2;
+    float j02yc = -fx * (b00yc * xc + b01yc * yc + d01) * inv_z2;
+    float j02z = -fx * ((b00z * xc + b01z * yc) * inv_z2 - 2.0f * (d00 * xc + d01 * yc) * inv_z3);
+    float j12xc = -fy * (b10xc * xc + d10 + b11xc * yc) * inv_z2;
+    float j12yc = -fy * (b10yc * xc + b11yc * yc + d11) * inv_z2;
+    float j12z = -fy * ((b10z * xc + b11z * yc) * inv_z2 - 2.0f * (d10 * xc + d11 * yc) * inv_z3);
+    float c_xc = su0 * j00xc + su1 * j01xc + su2 * j02xc + sv0 * j10xc + sv1 * j11xc + sv2 * j12xc;
+    float c_yc = su0 * j00yc + su1 * j01yc + su2 * j02yc + sv0 * j10yc + sv1 * j11yc + sv2 * j12yc;
+    float c_z = su0 * j00z + su1 * j01z + su2 * j02z + sv0 * j10z + sv1 * j11z + sv2 * j12z;
+    if (in_x) v_mx += c_xc;
+    if (in_y) v_my += c_yc;
+    v_mz += c_z;
+    if (!in_x) v_mz += mx_rz * c_xc;
+    if (!in_y) v_mz += my_rz * c_yc;
+    return mk3(v_mx, v_my, v_mz);
+}
+/* calculate_projection_vjp_tpf (thin_prism_fisheye.rs:116-203) */
+static v3 tpf_projection_vjp(const bh_project_uniforms* u, m23 J, v3 mean_c, s3 cov_c, s2 v_cov2d, v2 v_mean2d) {
+    v3 kb = kb4_projection_vjp(u, J, mean_c, cov_c, v_cov2d, v_mean2d);
+    float p1 = u->camera_params[4], p2 = u->camera_params[5];
+    float sx1 = u->camera_params[6], sy1 = u->camera_params[7];
+    float fx = u->fx, fy = u->fy;
+    float inv_z = 1.0f / mean_c.z;
+    float inv_z2 = inv_z * inv_z;
+    float inv_z3 = inv_z2 * inv_z;
+    float inv_z4 = inv_z2 * inv_z2;
+    float t[6];
+    tpf_polys(u, mean_c.x, mean_c.y, t);
+    float hu00 = (6.0f * p2 + 2.0f * sx1) * inv_z2, hu01 = (2.0f * p1) * inv_z2, hu11 = (2.0f * p2 + 2.0f * sx1) * inv_z2;
+    float hu02 = -2.0f * t[2] * inv_z3, hu12 = -2.0f * t[3] * inv_z3, hu22 = 6.0f * t[0] * inv_z4;
+    float hv00 = (2.0f * p1 + 2.0f * sy1) * inv_z2, hv01 = (2.0f * p2) * inv_z2, hv11 = (6.0f * p1 + 2.0f * sy1) * inv_z2;
+    float hv02 = -2.0f * t[4] * inv_z3, hv12 = -2.0f * t[5] * inv_z3, hv22 = 6.0f * t[1] * inv_z4;
+    float vj[6];
+    cov_jac_grad(J, cov_c, v_cov2d, vj);
+    float ax = fx * (vj[0] * hu00 + vj[1] * hu01 + vj[2] * hu02) + fy * (vj[3] * hv00 + vj[4] * hv01 + vj[5] * hv02);
+    float ay = fx * (vj[0] * hu01 + vj[1] * hu11 + vj[2] * hu12) + fy * (vj[3] * hv01 + vj[4] * hv11 + vj[5] * hv12);
+    float az = fx * (vj[0] * hu02 + vj[1] * hu12 + vj[2] * hu22) + fy * (vj[3] * hv02 + vj[4] * hv12 + vj[5] * hv22);
+    return mk3(kb.x + ax, kb.y + ay, kb.z + az);
+}
+/* calculate_projection_vjp (camera_model/mod.rs:82-126) */
+static v3 cam_projection_vjp(const bh_project_uniforms* u, m23 J, v3 mean_c, s3 cov_c, s2 v_cov2d, v2 v_mean2d) {
+    switch (u->camera_model) {
+        case BH_CAMERA_KB4: return kb4_projection_vjp(u, J, mean_c, cov_c, v_cov2d, v_mean2d);
+        case BH_CAMERA_RT8: return rt8_projection_vjp(u, mean_c, cov_c, v_cov2d, v_mean2d);
+        case BH_CAMERA_TPF: return tpf_projection_vjp(u, J, mean_c, cov_c, v_cov2d, v_mean2d);
+        default: return pinhole_projection_vjp(u, J, mean_c, cov_c, v_cov2d, v_mean2d);
+    }
+}
+
+/* Test hooks: the camera models on their own. */
+void or_atan2f(const float* y, const float* x, float* out, uint64_t n) {
+    for (uint64_t i = 0; i < n; i++) out[i] = bh_atan2f(y[i], x[i]);
+}
+void or_camera_project(const bh_project_uniforms* u, const float* pts, uint64_t n, float* out, uint8_t* culled) {
+    for (uint64_t i = 0; i < n; i++) {
+        v3 p = mk3(pts[3 * i], pts[3 * i + 1], pts[3 * i + 2]);
+        project_point(u, p, &out[2 * i], &out[2 * i + 1]);
+        culled[i] = (uint8_t)depth_culled(u, p);
+    }
+}
+void or_camera_jacobian(const bh_project_uniforms* u, const float* pts, uint64_t n, float* out) {
+    for (uint64_t i = 0; i < n; i++) {
+        m23 J = cam_jacobian(u, mk3(pts[3 * i], pts[3 * i + 1], pts[3 * i + 2]));
+        float* o = out + 6 * i;
+        o[0] = J.c0.x; o[1] = J.c1.x; o[2] = J.c2.x;
+        o[3] = J.c0.y; o[4] = J.c1.y; o[5] = J.c2.y;
+    }
+}
+/* cov_c rows c00 c01 c02 c11 c12 c22; v_cov2d c00 c01 c11 */
+void or_camera_vjp(const bh_project_uniforms* u, const float* mean_c, const float* cov_c, const float* v_cov2d,
+                   const float* v_mean2d, uint64_t n, float* out) {
+    for (uint64_t i = 0; i < n; i++) {
+        v3 m = mk3(mean_c[3 * i], mean_c[3 * i + 1], mean_c[3 * i + 2]);
+        const float* c = cov_c + 6 * i;
+        s3 cc = {c[0], c[1], c[2], c[3], c[4], c[5]};
+        s2 vc = {v_cov2d[3 * i], v_cov2d[3 * i + 1], v_cov2d[3 * i + 2]};
+        v3 g = cam_projection_vjp(u, cam_jacobian(u, m), m, cc, vc, mk2(v_mean2d[2 * i], v_mean2d[2 * i + 1]));
+        out[3 * i] = g.x;
+        out[3 * i + 1] = g.y;
+        out[3 * i + 2] = g.z;
+    }
 }
 /* sh_coeffs_to_color_vjp (kernels/sh.rs:383-466) */
 static void wr3(float* o, uint32_t k, v3 v) {
@@ -1048,8 +1456,8 @@ void or_project_backward(const bh_project_uniforms* u, const float* transforms,
         s3 covar = m3outer(m);
         m3 vr = view_rot(u);
         s3 cov_c = s3cong(covar, vr);
-        m23 J = jac_pinhole(u, mean_c);
-        v3 v_mean_c = projection_vjp(u, J, mean_c, cov_c, v_cov2d, mk2(rg[0], rg[1]));
+        m23 J = cam_jacobian(u, mean_c);
+        v3 v_mean_c = cam_projection_vjp(u, J, mean_c, cov_c, v_cov2d, mk2(rg[0], rg[1]));
         v_mean_c = mk3(v_mean_c.x, v_mean_c.y, v_mean_c.z + rg[10]);
         s3 vcc = m23tcong(J, v_cov2d);
         v3 v_mean = add3(m3tmulv(vr, v_mean_c), v_mean_sh);

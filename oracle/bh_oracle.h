@@ -35,6 +35,13 @@ void or_set_threads(int n);
 /* Element-wise bh_expf / bh_logf, for pinning them against libm. */
 void or_expf(const float* in, float* out, uint64_t n);
 void or_logf(const float* in, float* out, uint64_t n);
+void or_atan2f(const float* y, const float* x, float* out, uint64_t n);
+/* camera models on their own (test hooks): projection and depth cull,
+ * Jacobian rows (du/dx du/dy du/dz dv/dx dv/dy dv/dz), projection VJP */
+void or_camera_project(const bh_project_uniforms* u, const float* pts, uint64_t n, float* out, uint8_t* culled);
+void or_camera_jacobian(const bh_project_uniforms* u, const float* pts, uint64_t n, float* out);
+void or_camera_vjp(const bh_project_uniforms* u, const float* mean_c, const float* cov_c, const float* v_cov2d,
+                   const float* v_mean2d, uint64_t n, float* out);
 int or_get_max_threads(void);
 
 uint64_t or_project_forward(const bh_project_uniforms* u, const float* transforms,

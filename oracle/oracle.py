@@ -44,6 +44,8 @@ class Uniforms(ctypes.Structure):
         ("sh_degree", ctypes.c_uint32),
         ("total_splats", ctypes.c_uint32),
         ("num_visible", ctypes.c_uint32),
+        ("camera_model", ctypes.c_uint32),
+        ("camera_params", ctypes.c_float * 8),
     ]
 
 
@@ -81,6 +83,9 @@ def make_uniforms(d: dict) -> Uniforms:
         u.camera_pos[i] = float(d["camera_pos"][i])
     for k in ("img_w", "img_h", "tile_bw", "tile_bh", "sh_degree", "total_splats", "num_visible"):
         setattr(u, k, int(d[k]))
+    u.camera_model = int(d.get("camera_model", 0))
+    for i, v in enumerate(d.get("camera_params", ())):
+        u.camera_params[i] = float(v)
     return u
 
 
@@ -100,6 +105,10 @@ def lib():
         L.or_set_threads.argtypes = [ctypes.c_int]
         L.or_expf.argtypes = [P, P, U64]
         L.or_logf.argtypes = [P, P, U64]
+        L.or_atan2f.argtypes = [P, P, P, U64]
+        L.or_camera_project.argtypes = [UP, P, U64, P, P]
+        L.or_camera_jacobian.argtypes = [UP, P, U64, P]
+        L.or_camera_vjp.argtypes = [UP, P, P, P, P, U64, P]
         L.or_get_max_threads.restype = ctypes.c_int
         L.or_project_forward.argtypes = [UP, P, P, U32, U32, P, P, P, P]
         L.or_project_forward.restype = U64
@@ -138,6 +147,45 @@ def expf(x: np.ndarray) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.float32)
     out = np.empty_like(x)
     lib().or_expf(_p(x), _p(out), x.size)
+    return out
+
+
+def atan2f(y: np.ndarray, x: np.ndarray) -> np.ndarray:
+    y = np.ascontiguousarray(y, dtype=np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(y)
+    lib().or_atan2f(_p(y), _p(x), _p(out), y.size)
+    return out
+
+
+def camera_project(uniforms: dict, pts: np.ndarray):
+    """(screen points [n, 2], depth-culled mask [n]) of camera-space points
+    through the uniforms' camera model."""
+    u = make_uniforms(uniforms)
+    pts = np.ascontiguousarray(pts, dtype=np.float32).reshape(-1, 3)
+    out = np.empty((pts.shape[0], 2), np.float32)
+    culled = np.empty(pts.shape[0], np.uint8)
+    lib().or_camera_project(ctypes.byref(u), _p(pts), pts.shape[0], _p(out), _p(culled))
+    return out, culled.astype(bool)
+
+
+def camera_jacobian(uniforms: dict, pts: np.ndarray) -> np.ndarray:
+    """[n, 2, 3] projection Jacobians (rows u, v; columns x, y, z)."""
+    u = make_uniforms(uniforms)
+    pts = np.ascontiguousarray(pts, dtype=np.float32).reshape(-1, 3)
+    out = np.empty((pts.shape[0], 2, 3), np.float32)
+    lib().or_camera_jacobian(ctypes.byref(u), _p(pts), pts.shape[0], _p(out))
+    return out
+
+
+def camera_vjp(uniforms: dict, mean_c, cov_c, v_cov2d, v_mean2d) -> np.ndarray:
+    """[n, 3] projection VJP: cov_c [n, 6] (c00 c01 c02 c11 c12 c22), v_cov2d
+    [n, 3] (c00 c01 c11), v_mean2d [n, 2]."""
+    u = make_uniforms(uniforms)
+    a = [np.ascontiguousarray(x, dtype=np.float32) for x in (mean_c, cov_c, v_cov2d, v_mean2d)]
+    n = a[0].reshape(-1, 3).shape[0]
+    out = np.empty((n, 3), np.float32)
+    lib().or_camera_vjp(ctypes.byref(u), _p(a[0]), _p(a[1]), _p(a[2]), _p(a[3]), n, _p(out))
     return out
 
 
