@@ -27,6 +27,7 @@ FLAG_SMOOTH_CUTOFF = 2
 FLAG_RENDER_DEPTH = 4
 FLAG_MIP = 8
 FLAG_REFINE_WEIGHT = 16
+FLAG_TILE_16X8 = 32
 
 PROJECTED_LANES = 10
 COMPACT_GRAD_LANES = 11

@@ -266,9 +266,9 @@ class Camera:
         return affine_inverse(rot, np.asarray(self.position, dtype=np.float32))
 
 
-def tile_bounds(img_w: int, img_h: int):
-    """render.rs:30-47 for 16x16 tiles."""
-    return (img_w + TILE_WIDTH - 1) // TILE_WIDTH, (img_h + TILE_WIDTH - 1) // TILE_WIDTH
+def tile_bounds(img_w: int, img_h: int, tile_h: int = TILE_WIDTH):
+    """render.rs:30-47 (calc_tile_bounds_for_dims) for 16 x tile_h tiles."""
+    return (img_w + TILE_WIDTH - 1) // TILE_WIDTH, (img_h + tile_h - 1) // tile_h
 
 
 def jacobian_clamp_limits(img_w: int, img_h: int, fx, fy, cx, cy, model=PINHOLE):

@@ -341,8 +341,11 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
         return set_error(ctx, BH_ERR_INVALID_ARG, "render_forward: null buffer");
 
     bh_project_uniforms u = *uin;
+    // calc_tile_bounds_for_dims (render.rs:36-47): 16x16 tiles, or 16x8 for the
+    // candidate rasterizer
+    const uint32_t tile_h = (flags & BH_FLAG_TILE_16X8) ? 8u : BH_TILE_WIDTH;
     u.tile_bw = div_up(u.img_w, BH_TILE_WIDTH);
-    u.tile_bh = div_up(u.img_h, BH_TILE_WIDTH);
+    u.tile_bh = div_up(u.img_h, tile_h);
     u.sh_degree = sh_degree;
     u.total_splats = num_splats;
     u.num_visible = 0;
@@ -387,7 +390,7 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
         // counters: visible, flags, isect lo, isect hi, min key, max key; the
         // reduction kernel writes all but the flags word
         launch_fill_u32(ctx, ctx->d_counters + 1, 0u, 1);
-        launch_project_forward(ctx, u, transforms, raw_opacities, num_splats, mip, counts, max_radius, depth_keys,
+        launch_project_forward(ctx, u, transforms, raw_opacities, num_splats, mip, tile_h, counts, max_radius, depth_keys,
                                partials, ctx->d_counters);
         BH_STRY(check_launch(ctx, "project_forward"));
         BH_STRY(hip_check(ctx, hipMemcpyAsync(ctx->h_counters, ctx->d_counters, 24, hipMemcpyDeviceToHost, ctx->stream),
@@ -441,7 +444,7 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
         BH_STRY(ws.get(&uc, m));
         BH_STRY(ws.get(&tk, m));
         BH_STRY(ws.get(&tv, m));
-        launch_map_intersects(ctx, u.tile_bw, u.tile_bh, projected, cum, num_visible, ut, uc);
+        launch_map_intersects(ctx, u.tile_bw, u.tile_bh, tile_h, projected, cum, num_visible, ut, uc);
         BH_STRY(check_launch(ctx, "map_intersects"));
         // tile sort over bits(num_tiles) bits (render.rs:392-395)
         const uint32_t bits = bit_length(num_tiles);
@@ -504,7 +507,8 @@ bh_status bh_rasterize_backward(bh_ctx* ctx, const float* out_img, const float* 
     if (!out_img || !projected || !compact_gid_from_isect || !tile_offsets || !background || !v_output ||
         !v_combined)
         return set_error(ctx, BH_ERR_INVALID_ARG, "rasterize_backward: null argument");
-    const uint32_t tbw = div_up(img_w, BH_TILE_WIDTH), tbh = div_up(img_h, BH_TILE_WIDTH);
+    const uint32_t tbw = div_up(img_w, BH_TILE_WIDTH);
+    const uint32_t tbh = div_up(img_h, (flags & BH_FLAG_TILE_16X8) ? 8u : BH_TILE_WIDTH);
     launch_fill_u32(ctx, (uint32_t*)v_combined, 0u, (uint64_t)std::max<uint32_t>(num_visible, 1) * 11);
     if (num_visible)
         launch_rasterize_backward(ctx, img_w, img_h, tbw, tbh, background, num_visible, out_img, projected,
@@ -555,7 +559,8 @@ bh_status bh_render_backward(bh_ctx* ctx, const bh_fwd_state* state, const float
     float* rows;
     BH_TRY(ws.get(&rows, (size_t)n * 11));
     launch_fill_u32(ctx, (uint32_t*)rows, 0u, (uint64_t)n * 11);
-    const uint32_t raster_flags = flags & (BH_FLAG_SMOOTH_CUTOFF | BH_FLAG_REFINE_WEIGHT | BH_FLAG_RENDER_DEPTH);
+    const uint32_t raster_flags =
+        (flags & (BH_FLAG_SMOOTH_CUTOFF | BH_FLAG_REFINE_WEIGHT | BH_FLAG_RENDER_DEPTH)) | (in.flags & BH_FLAG_TILE_16X8);
     if (in.num_visible)
         launch_rasterize_backward(ctx, in.img_w, in.img_h, in.tile_bw, in.tile_bh, background, in.num_visible, out_img,
                                   in.projected, in.compact_gid_from_isect, tile_offsets, v_output, raster_flags,

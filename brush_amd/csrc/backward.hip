@@ -62,13 +62,15 @@ constexpr int kNG = 11;
 // One workgroup (a single wave) per 8x8 pixel block of a 16x16 tile.  The
 // dispatcher deals workgroups to the eight XCDs in turn, so the four blocks of
 // a tile are given ids that agree modulo 8 and share an L2.
+template <int TH>
 __device__ __forceinline__ void block_of_workgroup(uint32_t g, uint32_t& tile, uint32_t& blk) {
+    constexpr uint32_t BPT = 2u * (uint32_t)TH / 8u;
     const uint32_t slot = g >> 3;
-    tile = ((slot >> 2) << 3) | (g & 7u);
-    blk = slot & 3u;
+    tile = ((slot / BPT) << 3) | (g & 7u);
+    blk = slot % BPT;
 }
 
-template <bool SMOOTH, bool REFINE, bool DEPTH>
+template <bool SMOOTH, bool REFINE, bool DEPTH, int TH>
 __global__ __launch_bounds__(64) void rasterize_backward_kernel(
     uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t num_tiles, float bg_r, float bg_g, float bg_b,
     uint32_t num_visible, const float* __restrict__ out_img, const float* __restrict__ projected,
@@ -81,10 +83,11 @@ __global__ __launch_bounds__(64) void rasterize_backward_kernel(
     __shared__ uint32_t s_cid[64];
 
     uint32_t tile, blk;
-    block_of_workgroup(blockIdx.x, tile, blk);
+    block_of_workgroup<TH>(blockIdx.x, tile, blk);
     if (tile >= num_tiles) return;
     const uint32_t lane = threadIdx.x;
-    const uint32_t ox = (tile % tile_bw) * 16u + (blk & 1u) * 8u, oy = (tile / tile_bw) * 16u + (blk >> 1) * 8u;
+    const uint32_t ox = (tile % tile_bw) * 16u + (blk & 1u) * 8u;
+    const uint32_t oy = (tile / tile_bw) * (uint32_t)TH + (blk >> 1) * 8u;
     const uint32_t px = ox + (lane & 7u), py = oy + (lane >> 3);
     const bool inside = px < img_w && py < img_h;
     const float pcx = (float)px + 0.5f, pcy = (float)py + 0.5f;
@@ -232,13 +235,20 @@ void launch_rasterize_backward(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint
     const bool smooth = (flags & BH_FLAG_SMOOTH_CUTOFF) != 0;
     const bool refine = (flags & BH_FLAG_REFINE_WEIGHT) != 0;
     const bool depth = (flags & BH_FLAG_RENDER_DEPTH) != 0;
-    const uint32_t groups = div_up(num_tiles, 8) * 32u;
+    const bool fine = (flags & BH_FLAG_TILE_16X8) != 0;
+    const uint32_t groups = div_up(num_tiles, 8) * (fine ? 16u : 32u);
     KernelTimer t(ctx, "rasterize_backward");
-#define BH_RB(S, R, D)                                                                                            \
-    rasterize_backward_kernel<S, R, D><<<groups, 64, 0, ctx->stream>>>(img_w, img_h, tile_bw, num_tiles, bg[0], \
-                                                                       bg[1], bg[2], num_visible, out_img,       \
-                                                                       projected, cgids, offsets, v_output,      \
-                                                                       row_of, v_combined)
+#define BH_RB_T(S, R, D, T)                                                                                      \
+    rasterize_backward_kernel<S, R, D, T><<<groups, 64, 0, ctx->stream>>>(                                       \
+        img_w, img_h, tile_bw, num_tiles, bg[0], bg[1], bg[2], num_visible, out_img, projected, cgids, offsets, \
+        v_output, row_of, v_combined)
+#define BH_RB(S, R, D) \
+    do {               \
+        if (fine)      \
+            BH_RB_T(S, R, D, 8); \
+        else           \
+            BH_RB_T(S, R, D, 16); \
+    } while (0)
     if (smooth) {
         if (refine) {
             if (depth) BH_RB(true, true, true); else BH_RB(true, true, false);
@@ -252,6 +262,7 @@ void launch_rasterize_backward(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint
             if (depth) BH_RB(false, false, true); else BH_RB(false, false, false);
         }
     }
+#undef BH_RB_T
 #undef BH_RB
 }
 

@@ -374,9 +374,11 @@ BH_DEV V2 bbox_extent(const S2& conic, float pt) {
 struct TileBox {
     uint32_t min_x, min_y, max_x, max_y;
 };
-// get_bbox / get_tile_bbox (kernels/helpers.rs:260-295), 16x16 tiles
+// get_bbox / get_tile_bbox (kernels/helpers.rs:99-148) for 16 x TH tiles
+// (TH = 16, or 8 for the rasterizer's 16x8 candidate tiles)
+template <int TH = 16>
 BH_DEV TileBox tile_bbox(V2 m, V2 e, uint32_t bw, uint32_t bh) {
-    float cx = m.x / 16.0f, cy = m.y / 16.0f, dx = e.x / 16.0f, dy = e.y / 16.0f;
+    float cx = m.x / 16.0f, cy = m.y / (float)TH, dx = e.x / 16.0f, dy = e.y / (float)TH;
     float bwf = (float)bw, bhf = (float)bh;
     TileBox b;
     b.min_x = (uint32_t)bh_clampf(cx - dx, 0.0f, bwf);
@@ -391,10 +393,12 @@ BH_DEV float calc_sigma(float px, float py, const S2& c, float x, float y) {
     float dy = py - y;
     return 0.5f * (c.c00 * dx * dx + c.c11 * dy * dy) + c.c01 * dx * dy;
 }
-// will_primitive_contribute (kernels/helpers.rs:385-424) on the 16x16 rect of tile (tx, ty)
+// will_primitive_contribute (kernels/helpers.rs:241-280) on the 16 x TH rect
+// of tile (tx, ty) (tile_rect, helpers.rs:96-111)
+template <int TH = 16>
 BH_DEV bool will_contribute(uint32_t tx, uint32_t ty, V2 m, const S2& c, float pt) {
-    float min_x = (float)(tx * 16u), min_y = (float)(ty * 16u);
-    float max_x = min_x + 16.0f, max_y = min_y + 16.0f;
+    float min_x = (float)(tx * 16u), min_y = (float)(ty * (uint32_t)TH);
+    float max_x = min_x + 16.0f, max_y = min_y + (float)TH;
     bool x_left = m.x < min_x, x_right = m.x > max_x;
     bool in_x = !(x_left || x_right);
     bool y_above = m.y < min_y, y_below = m.y > max_y;

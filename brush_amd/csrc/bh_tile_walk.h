@@ -68,7 +68,7 @@ __device__ __forceinline__ uint32_t bbox_items(const TileBox& bb) {
     return (bb.max_x > bb.min_x && bb.max_y > bb.min_y) ? (bb.max_x - bb.min_x) * (bb.max_y - bb.min_y) : 0u;
 }
 
-// Cooperative walk of one wave.  Every lane of the wave must call it (it uses
+// Cooperative walk of one wave over 16 x TH tiles.  Every lane of the wave must call it (it uses
 // wave-wide DPP and ballots).  `items` is this lane's bbox tile count (0 for a
 // culled or absent splat); m, conic, pt, bb describe its splat.  `rec`,
 // `owner_slot` and `hits` are this wave's 64-entry LDS arrays.
@@ -77,7 +77,7 @@ __device__ __forceinline__ uint32_t bbox_items(const TileBox& bb) {
 // passing items are stored at out_base + (passing items before it in walk
 // order): tile id tx + ty * tile_bw into tile_ids and id_base + owner lane into
 // ids, skipping positions >= out_end.
-template <bool WRITE>
+template <bool WRITE, int TH = 16>
 __device__ uint32_t wave_tile_walk(uint32_t lane, uint32_t items, V2 m, const S2& conic, float pt,
                                    const TileBox& bb, WalkRec* rec, uint32_t* owner_slot, uint32_t* hits,
                                    uint32_t tile_bw, uint32_t out_base, uint32_t out_end, uint32_t id_base,
@@ -115,7 +115,7 @@ __device__ uint32_t wave_tile_walk(uint32_t lane, uint32_t items, V2 m, const S2
             col -= (int32_t)r.c.z;
         }
         const uint32_t tx = r.c.x + (uint32_t)col, ty = r.c.y + row;
-        const bool pass = valid && will_contribute(tx, ty, v2(r.a.x, r.a.y), S2{r.a.z, r.a.w, r.b.x}, r.b.y);
+        const bool pass = valid && will_contribute<TH>(tx, ty, v2(r.a.x, r.a.y), S2{r.a.z, r.a.w, r.b.x}, r.b.y);
         const uint64_t pmask = __ballot(pass);
         // the last lane of each splat's run in this step adds the run's hits
         const uint32_t run_lo = r.c.w > base ? r.c.w - base : 0u;

@@ -33,7 +33,7 @@ struct Projected {
     float depth;
 };
 
-template <bool MIP, int CAM>
+template <bool MIP, int CAM, int TH>
 __device__ bool project_cull(const bh_project_uniforms& u, const float* t, float raw_opac, Projected& o) {
     V3 mean_c = world_to_cam(u, v3(t[0], t[1], t[2]));
     if (!(finite3(mean_c) && mean_c.z <= 1.0e10f)) return false;
@@ -62,7 +62,7 @@ __device__ bool project_cull(const bh_project_uniforms& u, const float* t, float
     o.m = m;
     o.conic = conic;
     o.pt = pt;
-    o.bb = tile_bbox(m, e, u.tile_bw, u.tile_bh);
+    o.bb = tile_bbox<TH>(m, e, u.tile_bw, u.tile_bh);
     o.radius = bh_maxf(e.x / wf, e.y / hf);
     o.depth = mean_c.z;
     return true;
@@ -84,7 +84,7 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     return v;
 }
 
-template <bool MIP, int CAM>
+template <bool MIP, int CAM, int TH>
 __global__ __launch_bounds__(256) void project_forward_kernel(bh_project_uniforms u,
                                                                const float* __restrict__ transforms,
                                                                const float* __restrict__ raw_opac, uint32_t n,
@@ -109,10 +109,10 @@ __global__ __launch_bounds__(256) void project_forward_kernel(bh_project_uniform
             t[2 * i] = q.x;
             t[2 * i + 1] = q.y;
         }
-        vis = project_cull<MIP, CAM>(u, t, raw_opac[gid], p);
+        vis = project_cull<MIP, CAM, TH>(u, t, raw_opac[gid], p);
     }
     // count_contributing_tiles (project_forward.rs:120-128) for the whole wave
-    const uint32_t hits = wave_tile_walk<false>(lane, vis ? bbox_items(p.bb) : 0u, p.m, p.conic, p.pt, p.bb,
+    const uint32_t hits = wave_tile_walk<false, TH>(lane, vis ? bbox_items(p.bb) : 0u, p.m, p.conic, p.pt, p.bb,
                                                 s_rec[wave], s_slot[wave], s_count[wave], u.tile_bw, 0u, 0u, 0u,
                                                 nullptr, nullptr);
     if (gid < n) {
@@ -194,13 +194,14 @@ __global__ __launch_bounds__(1024) void project_reduce_kernel(const uint32_t* __
 
 size_t project_partials_bytes(uint32_t n) { return (size_t)div_up(n, 256) * 8 * sizeof(uint32_t); }
 
-template <bool MIP>
+template <bool MIP, int TH>
 static void launch_pf(bh_ctx* ctx, uint32_t blocks, const bh_project_uniforms& u, const float* transforms,
                       const float* raw_opac, uint32_t n, uint32_t* intersect_counts, float* max_radius,
                       uint32_t* depth_keys, uint32_t* partials) {
-#define BH_PF(C)                                                                                                 \
-    project_forward_kernel<MIP, C><<<blocks, 256, 0, ctx->stream>>>(u, transforms, raw_opac, n, intersect_counts, \
-                                                                    max_radius, depth_keys, partials)
+#define BH_PF(C)                                                                                      \
+    project_forward_kernel<MIP, C, TH><<<blocks, 256, 0, ctx->stream>>>(u, transforms, raw_opac, n,    \
+                                                                        intersect_counts, max_radius, \
+                                                                        depth_keys, partials)
     switch (u.camera_model) {
         case kCamKB4: BH_PF(kCamKB4); break;
         case kCamRT8: BH_PF(kCamRT8); break;
@@ -211,18 +212,20 @@ static void launch_pf(bh_ctx* ctx, uint32_t blocks, const bh_project_uniforms& u
 }
 
 void launch_project_forward(bh_ctx* ctx, const bh_project_uniforms& u, const float* transforms,
-                            const float* raw_opac, uint32_t n, bool mip, uint32_t* intersect_counts,
+                            const float* raw_opac, uint32_t n, bool mip, uint32_t tile_h, uint32_t* intersect_counts,
                             float* max_radius, uint32_t* depth_keys, uint32_t* partials, uint32_t* counters) {
     if (n == 0) return;
     uint32_t blocks = div_up(n, 256);
     {
         KernelTimer t(ctx, "project_forward");
-        if (mip)
-            launch_pf<true>(ctx, blocks, u, transforms, raw_opac, n, intersect_counts, max_radius, depth_keys,
-                            partials);
-        else
-            launch_pf<false>(ctx, blocks, u, transforms, raw_opac, n, intersect_counts, max_radius, depth_keys,
-                             partials);
+#define BH_PFM(M, T) \
+    launch_pf<M, T>(ctx, blocks, u, transforms, raw_opac, n, intersect_counts, max_radius, depth_keys, partials)
+        if (tile_h == 8) {
+            if (mip) BH_PFM(true, 8); else BH_PFM(false, 8);
+        } else {
+            if (mip) BH_PFM(true, 16); else BH_PFM(false, 16);
+        }
+#undef BH_PFM
     }
     KernelTimer t(ctx, "project_reduce");
     project_reduce_kernel<<<1, 1024, 0, ctx->stream>>>(partials, blocks, counters);
@@ -346,6 +349,7 @@ void launch_project_visible(bh_ctx* ctx, const bh_project_uniforms& u, const flo
 
 // ---- map_intersects ----------------------------------------------------------------
 
+template <int TH>
 __global__ __launch_bounds__(256) void map_intersects_kernel(uint32_t tile_bw, uint32_t tile_bh,
                                                               const float* __restrict__ projected,
                                                               const uint32_t* __restrict__ cum, uint32_t num_visible,
@@ -369,7 +373,7 @@ __global__ __launch_bounds__(256) void map_intersects_kernel(uint32_t tile_bw, u
         m = v2(p0.x, p0.y);
         conic = S2{p1.x, p1.y, p2.x};
         pt = bh_logf(p2.y * 255.0f);
-        bb = tile_bbox(m, bbox_extent(conic, pt), tile_bw, tile_bh);
+        bb = tile_bbox<TH>(m, bbox_extent(conic, pt), tile_bw, tile_bh);
         base = c == 0 ? 0u : cum[c - 1];
         budget = cum[c] - base;
     }
@@ -378,7 +382,7 @@ __global__ __launch_bounds__(256) void map_intersects_kernel(uint32_t tile_bw, u
     const uint32_t last = min(c0 + 63u, num_visible - 1u);
     const uint32_t out_base = c0 == 0 ? 0u : cum[c0 - 1];
     const uint32_t out_end = cum[last];
-    const uint32_t hits = wave_tile_walk<true>(lane, active ? bbox_items(bb) : 0u, m, conic, pt, bb, s_rec[wave],
+    const uint32_t hits = wave_tile_walk<true, TH>(lane, active ? bbox_items(bb) : 0u, m, conic, pt, bb, s_rec[wave],
                                                s_slot[wave], s_count[wave], tile_bw, out_base, out_end, c0, tile_ids,
                                                cgids);
     if (__ballot(active && hits != budget) == 0ull) return;
@@ -391,7 +395,7 @@ __global__ __launch_bounds__(256) void map_intersects_kernel(uint32_t tile_bw, u
     uint32_t k = 0;
     for (uint32_t ty = bb.min_y; ty < bb.max_y && k < budget; ty++)
         for (uint32_t tx = bb.min_x; tx < bb.max_x && k < budget; tx++)
-            if (will_contribute(tx, ty, m, conic, pt)) {
+            if (will_contribute<TH>(tx, ty, m, conic, pt)) {
                 tile_ids[base + k] = tx + ty * tile_bw;
                 cgids[base + k] = c;
                 k++;
@@ -402,12 +406,17 @@ __global__ __launch_bounds__(256) void map_intersects_kernel(uint32_t tile_bw, u
     }
 }
 
-void launch_map_intersects(bh_ctx* ctx, uint32_t tile_bw, uint32_t tile_bh, const float* projected,
+void launch_map_intersects(bh_ctx* ctx, uint32_t tile_bw, uint32_t tile_bh, uint32_t tile_h, const float* projected,
                            const uint32_t* cum, uint32_t num_visible, uint32_t* tile_ids, uint32_t* cgids) {
     if (num_visible == 0) return;
     KernelTimer t(ctx, "map_intersects");
-    map_intersects_kernel<<<div_up(num_visible, 256), 256, 0, ctx->stream>>>(tile_bw, tile_bh, projected, cum,
-                                                                               num_visible, tile_ids, cgids);
+    const uint32_t blocks = div_up(num_visible, 256);
+    if (tile_h == 8)
+        map_intersects_kernel<8><<<blocks, 256, 0, ctx->stream>>>(tile_bw, tile_bh, projected, cum, num_visible,
+                                                                 tile_ids, cgids);
+    else
+        map_intersects_kernel<16><<<blocks, 256, 0, ctx->stream>>>(tile_bw, tile_bh, projected, cum, num_visible,
+                                                                  tile_ids, cgids);
 }
 
 }  // namespace bh

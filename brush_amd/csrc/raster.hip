@@ -46,16 +46,18 @@ void launch_tile_offsets(bh_ctx* ctx, const uint32_t* tile_ids, uint32_t m, uint
     tile_offsets_kernel<<<div_up(m, 256), 256, 0, ctx->stream>>>(tile_ids, m, num_tiles, offsets);
 }
 
-// One workgroup (a single wave) per 8x8 pixel block of a 16x16 tile; the four
-// blocks of a tile get workgroup ids that agree modulo 8, which the dispatcher
-// places on one XCD (shared L2 for the tile's splat rows).
+// One workgroup (a single wave) per 8x8 pixel block of a 16 x TH tile; the
+// 2 * TH / 8 blocks of a tile get workgroup ids that agree modulo 8, which the
+// dispatcher places on one XCD (shared L2 for the tile's splat rows).
+template <int TH>
 __device__ __forceinline__ void raster_block_of_workgroup(uint32_t g, uint32_t& tile, uint32_t& blk) {
+    constexpr uint32_t BPT = 2u * (uint32_t)TH / 8u;
     const uint32_t slot = g >> 3;
-    tile = ((slot >> 2) << 3) | (g & 7u);
-    blk = slot & 3u;
+    tile = ((slot / BPT) << 3) | (g & 7u);
+    blk = slot % BPT;
 }
 
-template <bool BWD_INFO, bool SMOOTH, bool DEPTH>
+template <bool BWD_INFO, bool SMOOTH, bool DEPTH, int TH>
 __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t img_h, uint32_t tile_bw,
                                                         uint32_t num_tiles, float bg_r, float bg_g, float bg_b,
                                                         uint32_t num_visible, const float* __restrict__ projected,
@@ -69,10 +71,11 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
     __shared__ float4 s_rgbd[64];  // r, g, b, depth
 
     uint32_t tile, blk;
-    raster_block_of_workgroup(blockIdx.x, tile, blk);
+    raster_block_of_workgroup<TH>(blockIdx.x, tile, blk);
     if (tile >= num_tiles) return;
     const uint32_t lane = threadIdx.x;
-    const uint32_t ox = (tile % tile_bw) * 16u + (blk & 1u) * 8u, oy = (tile / tile_bw) * 16u + (blk >> 1) * 8u;
+    const uint32_t ox = (tile % tile_bw) * 16u + (blk & 1u) * 8u;
+    const uint32_t oy = (tile / tile_bw) * (uint32_t)TH + (blk >> 1) * 8u;
     const uint32_t px = ox + (lane & 7u), py = oy + (lane >> 3);
     const bool inside = px < img_w && py < img_h;
     const uint32_t lo = off_pre[2 * tile], hi = off_pre[2 * tile + 1];
@@ -186,12 +189,21 @@ void launch_rasterize(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile
     const bool depth = bwd && (flags & BH_FLAG_RENDER_DEPTH) != 0;
     const uint32_t nv = num_visible > 0 ? num_visible : 1u;
     if (bwd) launch_fill_u32(ctx, off_post, 0u, (uint64_t)num_tiles * 2);
-    const uint32_t groups = div_up(num_tiles, 8) * 32u;
+    const bool fine = (flags & BH_FLAG_TILE_16X8) != 0;
+    // 8 tiles per group of workgroup ids, 4 (16x16) or 2 (16x8) blocks per tile
+    const uint32_t groups = div_up(num_tiles, 8) * (fine ? 16u : 32u);
     KernelTimer t(ctx, "rasterize");
-#define BH_RASTER(B, S, D)                                                                                         \
-    rasterize_kernel<B, S, D><<<groups, 64, 0, ctx->stream>>>(img_w, img_h, tile_bw, num_tiles, bg[0], bg[1],    \
-                                                              bg[2], nv, projected, cgids, gfc, off_pre, out_img, \
-                                                              visible, off_post)
+#define BH_RASTER_T(B, S, D, T)                                                                                    \
+    rasterize_kernel<B, S, D, T><<<groups, 64, 0, ctx->stream>>>(img_w, img_h, tile_bw, num_tiles, bg[0], bg[1], \
+                                                                 bg[2], nv, projected, cgids, gfc, off_pre,       \
+                                                                 out_img, visible, off_post)
+#define BH_RASTER(B, S, D) \
+    do {                   \
+        if (fine)          \
+            BH_RASTER_T(B, S, D, 8); \
+        else               \
+            BH_RASTER_T(B, S, D, 16); \
+    } while (0)
     if (!bwd) {
         if (smooth) BH_RASTER(false, true, false); else BH_RASTER(false, false, false);
     } else if (depth) {
@@ -200,6 +212,7 @@ void launch_rasterize(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile
         if (smooth) BH_RASTER(true, true, false); else BH_RASTER(true, false, false);
     }
 #undef BH_RASTER
+#undef BH_RASTER_T
 }
 
 }  // namespace bh

@@ -64,6 +64,25 @@ class RasterPass(enum.Enum):
         return self is RasterPass.BackwardSmoothCutoff
 
 
+class Rasterizer(enum.Enum):
+    """gaussian_splats.rs:68-101: Legacy 16x16 tiles, Candidate 16x8 tiles.
+    The forward and the backward of one render must use the same one."""
+    Legacy = 16
+    Candidate = 8
+
+    @property
+    def tile_width(self) -> int:
+        return 16
+
+    @property
+    def tile_height(self) -> int:
+        return self.value
+
+    @property
+    def flag(self) -> int:
+        return _lib.FLAG_TILE_16X8 if self is Rasterizer.Candidate else 0
+
+
 class TextureMode(enum.Enum):
     """gaussian_splats.rs:103-108"""
     Packed = 0
@@ -200,8 +219,10 @@ class RenderOutput:
 def render(camera: Camera, img_size, transforms: torch.Tensor, sh_coeffs: torch.Tensor,
            raw_opacities: torch.Tensor, render_mode: SplatRenderMode = SplatRenderMode.Default,
            raster_mode: RasterizationMode = RasterizationMode.Rgba, background=(0.0, 0.0, 0.0),
-           raster_pass: RasterPass = RasterPass.Forward, uniforms: dict | None = None) -> RenderOutput:
-    """SplatOps::render with the 16x16 rasterizer (render.rs:78-543).
+           raster_pass: RasterPass = RasterPass.Forward, uniforms: dict | None = None,
+           rasterizer: Rasterizer = Rasterizer.Legacy) -> RenderOutput:
+    """SplatOps::render (render.rs:78-543); ``rasterizer`` picks 16x16 or 16x8
+    tiles (the reference's render_with_rasterizer, lib.rs:93-108).
 
     ``uniforms`` may supply a precomputed ``project_uniforms`` dict instead of
     deriving it from ``camera``.
@@ -225,13 +246,13 @@ def render(camera: Camera, img_size, transforms: torch.Tensor, sh_coeffs: torch.
 
     ud = dict(uniforms) if uniforms is not None else project_uniforms(camera, img_w, img_h, n, degree)
     ud["img_w"], ud["img_h"] = img_w, img_h
-    ud["tile_bw"], ud["tile_bh"] = tile_bounds(img_w, img_h)
+    ud["tile_bw"], ud["tile_bh"] = tile_bounds(img_w, img_h, rasterizer.tile_height)
     u = Uniforms.from_dict(ud)
-    flags = _flags(render_mode, raster_mode, raster_pass)
+    flags = _flags(render_mode, raster_mode, raster_pass) | rasterizer.flag
     depth = (flags & _lib.FLAG_RENDER_DEPTH) != 0
     with torch.cuda.device(device):
         ctx = context(device.index if device.index is not None else torch.cuda.current_device())
-        tbw, tbh = tile_bounds(img_w, img_h)
+        tbw, tbh = tile_bounds(img_w, img_h, rasterizer.tile_height)
         if raster_pass.bwd_info:
             out_img = torch.empty((img_h, img_w, 5 if depth else 4), dtype=torch.float32, device=device)
             visible = torch.empty((n,), dtype=torch.float32, device=device)
@@ -265,11 +286,11 @@ class SplatGrads:
 
 
 def _rasterize_bwd_ptrs(ctx, out_img, projected_p, cgids_p, tile_offsets, num_visible, background, img_size,
-                        v_output, smooth_cutoff, render_depth, compute_refine_weight):
+                        v_output, smooth_cutoff, render_depth, compute_refine_weight, rasterizer=Rasterizer.Legacy):
     img_w, img_h = int(img_size[0]), int(img_size[1])
     v_combined = torch.empty((max(num_visible, 1), _lib.COMPACT_GRAD_LANES), dtype=torch.float32,
                              device=out_img.device)
-    flags = 0
+    flags = rasterizer.flag
     if smooth_cutoff:
         flags |= _lib.FLAG_SMOOTH_CUTOFF
     if render_depth:
@@ -285,14 +306,14 @@ def _rasterize_bwd_ptrs(ctx, out_img, projected_p, cgids_p, tile_offsets, num_vi
 
 def rasterize_bwd(out_img, projected_splats, compact_gid_from_isect, tile_offsets, background, img_size, v_output,
                   smooth_cutoff: bool = False, render_depth: bool = False,
-                  compute_refine_weight: bool = True) -> torch.Tensor:
+                  compute_refine_weight: bool = True, rasterizer: Rasterizer = Rasterizer.Legacy) -> torch.Tensor:
     """SplatBwdOps::rasterize_bwd(_with_refine_weight) -> v_combined [V, 11]
-    (render_bwd.rs:90-238)."""
+    (render_bwd.rs:90-238); ``rasterizer`` must be the forward's."""
     chans = 5 if render_depth else 4
     if out_img.dim() != 3 or out_img.shape[2] != chans or tuple(v_output.shape) != tuple(out_img.shape):
         raise ValueError("out_img and v_output must both be [H, W, 4] ([H, W, 5] with depth)")
     img_w, img_h = int(img_size[0]), int(img_size[1])
-    tbw, tbh = tile_bounds(img_w, img_h)
+    tbw, tbh = tile_bounds(img_w, img_h, rasterizer.tile_height)
     if tuple(tile_offsets.shape) != (tbh, tbw, 2):
         raise ValueError(f"tile offsets must be [{tbh}, {tbw}, 2], got {tuple(tile_offsets.shape)}")
     num_visible = projected_splats.shape[0]
@@ -301,7 +322,7 @@ def rasterize_bwd(out_img, projected_splats, compact_gid_from_isect, tile_offset
         return _rasterize_bwd_ptrs(ctx, out_img.contiguous(), ptr(projected_splats.contiguous()),
                                    ptr(compact_gid_from_isect.contiguous()), tile_offsets.contiguous(), num_visible,
                                    background, img_size, v_output.contiguous(), smooth_cutoff, render_depth,
-                                   compute_refine_weight)
+                                   compute_refine_weight, rasterizer)
 
 
 def _project_bwd_ptrs(ctx, transforms, sh_coeffs, raw_opac, gfc_p, uniforms: dict, render_mode, v_combined):
@@ -405,7 +426,9 @@ class SplatOutputDiff:
 
 
 class _DiffConfig:
-    def __init__(self, camera, img_size, background, render_mode, raster_mode, raster_pass, compute_refine_weight):
+    def __init__(self, camera, img_size, background, render_mode, raster_mode, raster_pass, compute_refine_weight,
+                 rasterizer=None):
+        self.rasterizer = rasterizer or Rasterizer.Legacy
         self.camera = camera
         self.img_size = img_size
         self.background = background
@@ -423,7 +446,7 @@ class _RenderSplatsFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, transforms, sh_coeffs, raw_opac, cfg: _DiffConfig):
         out = render(cfg.camera, cfg.img_size, transforms.detach(), sh_coeffs.detach(), raw_opac.detach(),
-                     cfg.render_mode, cfg.raster_mode, cfg.background, cfg.raster_pass)
+                     cfg.render_mode, cfg.raster_mode, cfg.background, cfg.raster_pass, rasterizer=cfg.rasterizer)
         cfg.output = out
         ctx.cfg = cfg
         ctx.save_for_backward(transforms, sh_coeffs, raw_opac, out.out_img, out.aux.tile_offsets)
@@ -465,13 +488,15 @@ class _RenderSplatsFn(torch.autograd.Function):
 
 def render_splats_diff(splats: Splats, camera: Camera, img_size, background=(0.0, 0.0, 0.0),
                        compute_refine_weight: bool = True, raster_pass: RasterPass = RasterPass.Backward,
-                       raster_mode: RasterizationMode = RasterizationMode.Rgba) -> SplatOutputDiff:
+                       raster_mode: RasterizationMode = RasterizationMode.Rgba,
+                       rasterizer: Rasterizer = Rasterizer.Legacy) -> SplatOutputDiff:
     """Differentiable render (brush_render_bwd::render_splats and
     render_splats_with_pass, burn_glue.rs:476-483, 548-573)."""
     if not raster_pass.bwd_info:
         raise ValueError("render_splats_with_pass requires a Backward variant")
     mode = SplatRenderMode.Mip if splats.render_mip else SplatRenderMode.Default
-    cfg = _DiffConfig(camera, img_size, background, mode, raster_mode, raster_pass, compute_refine_weight)
+    cfg = _DiffConfig(camera, img_size, background, mode, raster_mode, raster_pass, compute_refine_weight,
+                      rasterizer)
     img = _RenderSplatsFn.apply(splats.transforms, splats.sh_coeffs, splats.raw_opacities, cfg)
     aux = cfg.output.aux
     res = SplatOutputDiff(img, aux.num_visible, aux.visible, aux.max_radius, aux)
@@ -486,8 +511,9 @@ def render_splats_diff(splats: Splats, camera: Camera, img_size, background=(0.0
 
 def render_splats_for_training(splats: Splats, camera: Camera, img_size, background=(0.0, 0.0, 0.0),
                                compute_refine_weight: bool = True,
-                               rasterization_mode: RasterizationMode = RasterizationMode.Rgba) -> SplatOutputDiff:
+                               rasterization_mode: RasterizationMode = RasterizationMode.Rgba,
+                               rasterizer: Rasterizer = Rasterizer.Legacy) -> SplatOutputDiff:
     """burn_glue.rs:518-546 (deferred SH gradients are an Apple-only path and
     are not offered)."""
     return render_splats_diff(splats, camera, img_size, background, compute_refine_weight, RasterPass.Backward,
-                              rasterization_mode)
+                              rasterization_mode, rasterizer)

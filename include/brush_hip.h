@@ -57,6 +57,10 @@ typedef enum bh_status {
 #define BH_FLAG_MIP 8u
 /* Backward-only flag: accumulate the refine weight lane (v_combined[:,9]). */
 #define BH_FLAG_REFINE_WEIGHT 16u
+/* Rasterizer::Candidate (brush-render/src/gaussian_splats.rs:68-101): 16x8
+ * tiles instead of 16x16 (tile grid ceil(W/16) x ceil(H/8)).  Pass it to the
+ * forward and to every backward entry point of that forward. */
+#define BH_FLAG_TILE_16X8 32u
 
 #define BH_TILE_WIDTH 16u
 #define BH_PROJECTED_LANES 10u

@@ -406,8 +406,8 @@ static void bbox_extent(s2 conic, float pt, float* ex, float* ey) {
 }
 typedef struct { uint32_t min_x, min_y, max_x, max_y; } tbox;
 /* get_bbox / get_tile_bbox (kernels/helpers.rs:260-295) */
-static tbox tile_bbox(float mx, float my, float ex, float ey, uint32_t bw, uint32_t bh) {
-    float cx = mx / 16.0f, cy = my / 16.0f, dx = ex / 16.0f, dy = ey / 16.0f;
+static tbox tile_bbox(float mx, float my, float ex, float ey, uint32_t bw, uint32_t bh, uint32_t th) {
+    float cx = mx / 16.0f, cy = my / (float)th, dx = ex / 16.0f, dy = ey / (float)th;
     float bwf = (float)bw, bhf = (float)bh;
     tbox b;
     b.min_x = (uint32_t)bh_clampf(cx - dx, 0.0f, bwf);
@@ -423,9 +423,9 @@ static float calc_sigma(float px, float py, s2 c, float x, float y) {
     return 0.5f * (c.c00 * dx * dx + c.c11 * dy * dy) + c.c01 * dx * dy;
 }
 /* will_primitive_contribute (kernels/helpers.rs:385-424), 16x16 tile rect */
-static int will_contribute(uint32_t tx, uint32_t ty, float mx, float my, s2 c, float pt) {
-    float min_x = (float)(tx * 16u), min_y = (float)(ty * 16u);
-    float max_x = min_x + 16.0f, max_y = min_y + 16.0f;
+static int will_contribute(uint32_t tx, uint32_t ty, uint32_t th, float mx, float my, s2 c, float pt) {
+    float min_x = (float)(tx * 16u), min_y = (float)(ty * th);
+    float max_x = min_x + 16.0f, max_y = min_y + (float)th;
     int x_left = mx < min_x, x_right = mx > max_x;
     int in_x = !(x_left || x_right);
     int y_above = my < min_y, y_below = my > max_y;
@@ -458,7 +458,7 @@ static int will_contribute(uint32_t tx, uint32_t ty, float mx, float my, s2 c, f
 /* ------------------------------------------------------------------------ */
 
 /* Returns 1 and fills outputs if the splat survives culling. */
-static int project_one(const bh_project_uniforms* u, const float* t, float raw_opac, uint32_t mip,
+static int project_one(const bh_project_uniforms* u, const float* t, float raw_opac, uint32_t mip, uint32_t th,
                        uint32_t* count, float* radius, float* depth) {
     v3 mean_c = world_to_cam(u, mk3(t[0], t[1], t[2]));
     if (!(fin3(mean_c) && mean_c.z <= 1.0e10f)) return 0;
@@ -486,11 +486,11 @@ static int project_one(const bh_project_uniforms* u, const float* t, float raw_o
     float wf = (float)u->img_w, hf = (float)u->img_h;
     int on_screen = mx + ex > 0.0f && mx - ex < wf && my + ey > 0.0f && my - ey < hf;
     if (!on_screen) return 0;
-    tbox bb = tile_bbox(mx, my, ex, ey, u->tile_bw, u->tile_bh);
+    tbox bb = tile_bbox(mx, my, ex, ey, u->tile_bw, u->tile_bh, th);
     uint32_t hits = 0;
     for (uint32_t ty = bb.min_y; ty < bb.max_y; ty++)
         for (uint32_t tx = bb.min_x; tx < bb.max_x; tx++)
-            if (will_contribute(tx, ty, mx, my, conic, pt)) hits++;
+            if (will_contribute(tx, ty, th, mx, my, conic, pt)) hits++;
     *count = hits;
     *radius = bh_maxf(ex / wf, ey / hf);
     *depth = mean_c.z;
@@ -498,7 +498,7 @@ static int project_one(const bh_project_uniforms* u, const float* t, float raw_o
 }
 
 uint64_t or_project_forward(const bh_project_uniforms* u, const float* transforms,
-                            const float* raw_opac, uint32_t n, uint32_t mip,
+                            const float* raw_opac, uint32_t n, uint32_t mip, uint32_t tile_h,
                             uint32_t* intersect_counts, float* max_radius, float* depths,
                             uint8_t* visible_mask) {
     uint64_t total = 0;
@@ -506,7 +506,7 @@ uint64_t or_project_forward(const bh_project_uniforms* u, const float* transform
     for (int64_t i = 0; i < (int64_t)n; i++) {
         uint32_t c = 0;
         float r = 0.0f, d = 0.0f;
-        int vis = project_one(u, transforms + (size_t)i * 10, raw_opac[i], mip, &c, &r, &d);
+        int vis = project_one(u, transforms + (size_t)i * 10, raw_opac[i], mip, tile_h, &c, &r, &d);
         intersect_counts[i] = vis ? c : 0u;
         max_radius[i] = vis ? r : 0.0f;
         depths[i] = vis ? d : 0.0f;
@@ -680,7 +680,7 @@ void or_project_visible(const bh_project_uniforms* u, const float* transforms,
 /* ------------------------------------------------------------------------ */
 /* map_gaussians_to_intersect (kernels/map_gaussians.rs:14-92)               */
 /* ------------------------------------------------------------------------ */
-void or_map_intersects(uint32_t tile_bw, uint32_t tile_bh, const float* projected,
+void or_map_intersects(uint32_t tile_bw, uint32_t tile_bh, uint32_t tile_h, const float* projected,
                        const uint32_t* cum, uint32_t num_visible,
                        uint32_t* tile_id_from_isect, uint32_t* compact_gid_from_isect) {
 #pragma omp parallel for schedule(dynamic, 1024) num_threads(g_threads)
@@ -691,13 +691,13 @@ void or_map_intersects(uint32_t tile_bw, uint32_t tile_bh, const float* projecte
         float pt = bh_logf(p[5] * 255.0f);
         float ex, ey;
         bbox_extent(conic, pt, &ex, &ey);
-        tbox bb = tile_bbox(mx, my, ex, ey, tile_bw, tile_bh);
+        tbox bb = tile_bbox(mx, my, ex, ey, tile_bw, tile_bh, tile_h);
         uint32_t base = ci == 0 ? 0u : cum[ci - 1];
         uint32_t budget = cum[ci] - base;
         uint32_t hits = 0;
         for (uint32_t ty = bb.min_y; ty < bb.max_y && hits < budget; ty++)
             for (uint32_t tx = bb.min_x; tx < bb.max_x && hits < budget; tx++)
-                if (will_contribute(tx, ty, mx, my, conic, pt)) {
+                if (will_contribute(tx, ty, tile_h, mx, my, conic, pt)) {
                     tile_id_from_isect[base + hits] = tx + ty * tile_bw;
                     compact_gid_from_isect[base + hits] = (uint32_t)ci;
                     hits++;
@@ -755,12 +755,13 @@ void or_rasterize(uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t til
     int depth = bwd_info && (flags & BH_FLAG_RENDER_DEPTH) != 0;
     uint32_t chans = depth ? 5u : 4u;
     int64_t num_tiles = (int64_t)tile_bw * tile_bh;
+    const uint32_t th = (flags & BH_FLAG_TILE_16X8) ? 8u : 16u;
 #pragma omp parallel for schedule(dynamic, 4) num_threads(g_threads)
     for (int64_t tile = 0; tile < num_tiles; tile++) {
         uint32_t lo = off_pre[2 * tile], hi = off_pre[2 * tile + 1];
-        uint32_t ox = (uint32_t)(tile % tile_bw) * 16u, oy = (uint32_t)(tile / tile_bw) * 16u;
+        uint32_t ox = (uint32_t)(tile % tile_bw) * 16u, oy = (uint32_t)(tile / tile_bw) * th;
         uint32_t max_useful = lo;
-        for (uint32_t p = 0; p < 256; p++) {
+        for (uint32_t p = 0; p < 16u * th; p++) {
             uint32_t px = ox + (p & 15u), py = oy + (p >> 4);
             if (px >= img_w || py >= img_h) continue;
             float pcx = (float)px + 0.5f, pcy = (float)py + 0.5f;
@@ -863,13 +864,14 @@ void or_rasterize_backward(uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uin
     memset(v_combined, 0, (size_t)(num_visible ? num_visible : 1) * 11 * sizeof(float));
     float img_wf = (float)img_w, img_hf = (float)img_h;
     int64_t num_tiles = (int64_t)tile_bw * tile_bh;
+    const uint32_t th = (flags & BH_FLAG_TILE_16X8) ? 8u : 16u;
 #pragma omp parallel for schedule(dynamic, 2) num_threads(g_threads)
     for (int64_t tile = 0; tile < num_tiles; tile++) {
         uint32_t lo = offsets[2 * tile], hi = offsets[2 * tile + 1];
         if (hi <= lo) continue;
-        uint32_t ox = (uint32_t)(tile % tile_bw) * 16u, oy = (uint32_t)(tile / tile_bw) * 16u;
+        uint32_t ox = (uint32_t)(tile % tile_bw) * 16u, oy = (uint32_t)(tile / tile_bw) * th;
         float st[256][5];
-        for (uint32_t p = 0; p < 256; p++) {
+        for (uint32_t p = 0; p < 16u * th; p++) {
             uint32_t px = ox + (p & 15u), py = oy + (p >> 4);
             if (px < img_w && py < img_h) {
                 const float* o = out_img + ((size_t)py * img_w + px) * chans;
@@ -889,7 +891,7 @@ void or_rasterize_backward(uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uin
             s2 c = {s[2], s[3], s[4]};
             float cr = bh_maxf(s[6], 0.0f), cgc = bh_maxf(s[7], 0.0f), cb = bh_maxf(s[8], 0.0f);
             float gs[4][11] = {{0}};
-            for (uint32_t p = 0; p < 256; p++) {
+            for (uint32_t p = 0; p < 16u * th; p++) {
                 float* gr = gs[p >> 6];
                 float sx = st[p][0], sy = st[p][1], sz = st[p][2], sw = st[p][3];
                 if (!(sw > 1.0e-4f)) continue;

@@ -44,8 +44,9 @@ void or_camera_vjp(const bh_project_uniforms* u, const float* mean_c, const floa
                    const float* v_mean2d, uint64_t n, float* out);
 int or_get_max_threads(void);
 
+/* tile_h: 16, or 8 for 16x8 tiles (BH_FLAG_TILE_16X8); u->tile_bh must match */
 uint64_t or_project_forward(const bh_project_uniforms* u, const float* transforms,
-                            const float* raw_opac, uint32_t n, uint32_t mip,
+                            const float* raw_opac, uint32_t n, uint32_t mip, uint32_t tile_h,
                             uint32_t* intersect_counts, float* max_radius, float* depths,
                             uint8_t* visible_mask);
 
@@ -58,7 +59,7 @@ void or_project_visible(const bh_project_uniforms* u, const float* transforms,
                         const uint32_t* global_from_compact_gid, uint32_t num_visible,
                         uint32_t sh_degree, uint32_t mip, float* projected);
 
-void or_map_intersects(uint32_t tile_bw, uint32_t tile_bh, const float* projected,
+void or_map_intersects(uint32_t tile_bw, uint32_t tile_bh, uint32_t tile_h, const float* projected,
                        const uint32_t* cum_tiles_hit, uint32_t num_visible,
                        uint32_t* tile_id_from_isect, uint32_t* compact_gid_from_isect);
 

@@ -27,6 +27,7 @@ FLAG_SMOOTH_CUTOFF = 2
 FLAG_RENDER_DEPTH = 4
 FLAG_MIP = 8
 FLAG_REFINE_WEIGHT = 16
+FLAG_TILE_16X8 = 32
 
 
 class Uniforms(ctypes.Structure):
@@ -110,12 +111,12 @@ def lib():
         L.or_camera_jacobian.argtypes = [UP, P, U64, P]
         L.or_camera_vjp.argtypes = [UP, P, P, P, P, U64, P]
         L.or_get_max_threads.restype = ctypes.c_int
-        L.or_project_forward.argtypes = [UP, P, P, U32, U32, P, P, P, P]
+        L.or_project_forward.argtypes = [UP, P, P, U32, U32, U32, P, P, P, P]
         L.or_project_forward.restype = U64
         L.or_stable_sort.argtypes = [P, P, U64, U32]
         L.or_prefix_sum.argtypes = [P, P, U64]
         L.or_project_visible.argtypes = [UP, P, P, P, P, U32, U32, U32, P]
-        L.or_map_intersects.argtypes = [U32, U32, P, P, U32, P, P]
+        L.or_map_intersects.argtypes = [U32, U32, U32, P, P, U32, P, P]
         L.or_tile_offsets.argtypes = [P, U64, U32, P]
         L.or_rasterize.argtypes = [U32, U32, U32, U32, P, P, P, P, P, U32, P, P, P]
         L.or_rasterize_reference.argtypes = [P, U32, U32, U32, P, U32, P]
@@ -261,6 +262,9 @@ def render_forward(uniforms: dict, transforms, sh_coeffs, raw_opac, flags: int =
     ud["total_splats"] = n
     ud["sh_degree"] = deg
     w, h = ud["img_w"], ud["img_h"]
+    # calc_tile_bounds_for_dims (render.rs:36-47): 16x16 tiles, or 16x8
+    th = 8 if flags & FLAG_TILE_16X8 else 16
+    ud["tile_bw"], ud["tile_bh"], ud["tile_h"] = (w + 15) // 16, (h + th - 1) // th, th
     tbw, tbh = ud["tile_bw"], ud["tile_bh"]
     num_tiles = tbw * tbh
     mip = int((flags & FLAG_MIP) != 0)
@@ -275,7 +279,7 @@ def render_forward(uniforms: dict, transforms, sh_coeffs, raw_opac, flags: int =
     mask = np.zeros(n, np.uint8)
     total = 0
     if n:
-        total = L.or_project_forward(ctypes.byref(u), _p(transforms), _p(raw_opac), n, mip,
+        total = L.or_project_forward(ctypes.byref(u), _p(transforms), _p(raw_opac), n, mip, th,
                                      _p(counts), _p(radius), _p(depths), _p(mask))
     vis_ids = np.nonzero(mask)[0].astype(np.uint32)
     num_visible = int(vis_ids.size)
@@ -296,7 +300,7 @@ def render_forward(uniforms: dict, transforms, sh_coeffs, raw_opac, flags: int =
     tile_ids = np.zeros(max(m, 1), np.uint32)
     cgids = np.zeros(max(m, 1), np.uint32)
     if num_visible and m:
-        L.or_map_intersects(tbw, tbh, _p(projected), _p(cum), num_visible, _p(tile_ids), _p(cgids))
+        L.or_map_intersects(tbw, tbh, th, _p(projected), _p(cum), num_visible, _p(tile_ids), _p(cgids))
     bits = int(num_tiles).bit_length()  # render.rs:392: 32 - leading_zeros(T)
     if m:
         tk, tv = stable_sort(tile_ids[:m], cgids[:m], bits)
@@ -324,6 +328,8 @@ def rasterize_backward(fwd: ForwardResult, v_output: np.ndarray, flags: int = FL
     bg = np.asarray(background, dtype=np.float32)
     v_output = np.ascontiguousarray(v_output, dtype=np.float32)
     v_comb = np.zeros((max(fwd.num_visible, 1), 11), np.float32)
+    if ud.get("tile_h", 16) == 8:
+        flags |= FLAG_TILE_16X8
     lib().or_rasterize_backward(ud["img_w"], ud["img_h"], ud["tile_bw"], ud["tile_bh"], _p(bg),
                                 _p(np.ascontiguousarray(fwd.out_img)), _p(fwd.projected),
                                 _p(fwd.compact_gid_from_isect),

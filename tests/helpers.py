@@ -91,8 +91,9 @@ def gpu_forward(uniforms: dict, tr, sh, opac, flags: int, background=(0.0, 0.0, 
         raster_pass = R.RasterPass.BackwardSmoothCutoff if flags & 2 else R.RasterPass.Backward
     mode = R.SplatRenderMode.Mip if flags & 8 else R.SplatRenderMode.Default
     rmode = R.RasterizationMode.RgbaAndDepth if flags & 4 else R.RasterizationMode.Rgba
+    rasterizer = R.Rasterizer.Candidate if flags & 32 else R.Rasterizer.Legacy
     out = R.render(None, (uniforms["img_w"], uniforms["img_h"]), t, s, o, mode, rmode, background, raster_pass,
-                   uniforms=uniforms)
+                   uniforms=uniforms, rasterizer=rasterizer)
     u32 = lambda x: x.cpu().numpy().view(np.uint32)
     res = dict(
         out=out,

@@ -192,15 +192,15 @@ def test_near_plane_and_behind_camera_culled():
     assert np.all(r.out_img == 0.0)
 
 
-def _tile_hits_float64(mx, my, c00, c01, c11, pt, tbw, tbh):
-    """Tiles whose 16x16 rect holds a point with Mahalanobis power <= pt, from
-    a float64 re-derivation of the edge test: the power restricted to the
+def _tile_hits_float64(mx, my, c00, c01, c11, pt, tbw, tbh, th=16):
+    """Tiles whose 16 x th rect holds a point with Mahalanobis power <= pt,
+    from a float64 re-derivation of the edge test: the power restricted to the
     rect's nearest edge line is minimised at dx = -c01 dy / c00 (horizontal
     edge) or dy = -c01 dx / c11 (vertical edge)."""
     out = set()
     for ty in range(tbh):
         for tx in range(tbw):
-            x0, y0, x1, y1 = tx * 16.0, ty * 16.0, tx * 16.0 + 16.0, ty * 16.0 + 16.0
+            x0, y0, x1, y1 = tx * 16.0, ty * float(th), tx * 16.0 + 16.0, ty * float(th) + th
             in_x = x0 <= mx <= x1
             in_y = y0 <= my <= y1
             if in_x and in_y:
@@ -209,7 +209,7 @@ def _tile_hits_float64(mx, my, c00, c01, c11, pt, tbw, tbh):
             cx = x0 if mx < x0 else x1
             cy = y0 if my < y0 else y1
             dxf = 16.0 if mx < x0 else -16.0
-            dyf = 16.0 if my < y0 else -16.0
+            dyf = float(th) if my < y0 else -float(th)
             # minimiser along the edge through the nearest corner
             tt_x = 0.0 if in_y else min(max((c00 * (mx - cx) + c01 * (my - cy)) / (c00 * dxf), 0.0), 1.0)
             tt_y = 0.0 if in_x else min(max((c01 * (mx - cx) + c11 * (my - cy)) / (c11 * dyf), 0.0), 1.0)
@@ -220,10 +220,12 @@ def _tile_hits_float64(mx, my, c00, c01, c11, pt, tbw, tbh):
     return out
 
 
-def test_tile_predicate_against_float64_geometry():
-    """will_primitive_contribute (helpers.rs:385-424) and the counts of
+@pytest.mark.parametrize("th", [16, 8])
+def test_tile_predicate_against_float64_geometry(th):
+    """will_primitive_contribute (helpers.rs:241-280) and the counts of
     project_forward agree with a float64 re-derivation on random anisotropic
-    splats, except within 1e-4 of the power threshold."""
+    splats, except within 1e-4 of the power threshold; 16x16 tiles and the
+    16x8 candidate tiles."""
     rng = np.random.default_rng(11)
     n = 300
     tr = np.zeros((n, 10), np.float32)
@@ -235,8 +237,10 @@ def test_tile_predicate_against_float64_geometry():
     opac = rng.uniform(-3.0, 4.0, n).astype(np.float32)
     cam = Camera.from_focal((0.0, 0.0, -3.0), (0.0, 0.0, 0.0, 1.0), 120.0, 112, 96)
     u = uniforms_for(cam, 112, 96, n, 0)
-    r = O.render_forward(u, tr, np.full((n, 1, 3), 0.5, np.float32), opac, O.FLAG_BWD_INFO)
-    tbw, tbh = u["tile_bw"], u["tile_bh"]
+    flags = O.FLAG_BWD_INFO | (O.FLAG_TILE_16X8 if th == 8 else 0)
+    r = O.render_forward(u, tr, np.full((n, 1, 3), 0.5, np.float32), opac, flags)
+    tbw, tbh = r.uniforms["tile_bw"], r.uniforms["tile_bh"]
+    assert tbh == -(-96 // th)
     by_splat = {}
     for t, c in zip(r.tile_id_from_isect[: r.num_intersections], r.compact_gid_from_isect[: r.num_intersections]):
         by_splat.setdefault(int(c), set()).add((int(t) % tbw, int(t) // tbw))
@@ -244,23 +248,24 @@ def test_tile_predicate_against_float64_geometry():
     for c in range(r.num_visible):
         p = r.projected[c].astype(np.float64)
         pt = math.log(p[5] * 255.0)
-        ref = _tile_hits_float64(p[0], p[1], p[2], p[3], p[4], pt, tbw, tbh)
+        ref = _tile_hits_float64(p[0], p[1], p[2], p[3], p[4], pt, tbw, tbh, th)
         got = by_splat.get(c, set())
         for tile in got ^ ref:
             tx, ty = tile
             # allow disagreement only for tiles whose decision sits on the threshold
-            near = _tile_hits_float64(p[0], p[1], p[2], p[3], p[4], pt * (1 + 1e-4) + 1e-4, tbw, tbh) - \
-                _tile_hits_float64(p[0], p[1], p[2], p[3], p[4], pt * (1 - 1e-4) - 1e-4, tbw, tbh)
+            near = _tile_hits_float64(p[0], p[1], p[2], p[3], p[4], pt * (1 + 1e-4) + 1e-4, tbw, tbh, th) - \
+                _tile_hits_float64(p[0], p[1], p[2], p[3], p[4], pt * (1 - 1e-4) - 1e-4, tbw, tbh, th)
             assert tile in near, f"splat {c}: tile {tile} decided differently ({tile in got} vs {tile in ref})"
             mismatches += 1
         assert len(got) == r.intersect_counts[r.global_from_compact_gid[c]]
     assert mismatches <= 3
 
 
-def test_no_pixel_contribution_outside_counted_tiles():
+@pytest.mark.parametrize("th", [16, 8])
+def test_no_pixel_contribution_outside_counted_tiles(th):
     """Every pixel centre where a splat's alpha reaches 1/255 lies in a tile the
     splat was binned to (the binning is conservative), so the tiled blend
-    equals the per-pixel walk (tests/mod.rs:475-605)."""
+    equals the per-pixel walk (tests/mod.rs:475-605); 16x16 and 16x8 tiles."""
     rng = np.random.default_rng(5)
     n = 400
     tr = np.zeros((n, 10), np.float32)
@@ -271,8 +276,9 @@ def test_no_pixel_contribution_outside_counted_tiles():
     opac = rng.uniform(-4.0, 3.0, n).astype(np.float32)
     cam = Camera.from_focal((0.0, 0.0, -3.0), (0.0, 0.0, 0.0, 1.0), 100.0, 96, 80)
     u = uniforms_for(cam, 96, 80, n, 0)
-    r = O.render_forward(u, tr, np.full((n, 1, 3), 0.5, np.float32), opac, O.FLAG_BWD_INFO)
-    tbw = u["tile_bw"]
+    r = O.render_forward(u, tr, np.full((n, 1, 3), 0.5, np.float32), opac,
+                         O.FLAG_BWD_INFO | (O.FLAG_TILE_16X8 if th == 8 else 0))
+    tbw = r.uniforms["tile_bw"]
     binned = set(zip(r.tile_id_from_isect[: r.num_intersections].tolist(),
                      r.compact_gid_from_isect[: r.num_intersections].tolist()))
     ys, xs = np.mgrid[0:80, 0:96]
@@ -286,7 +292,7 @@ def test_no_pixel_contribution_outside_counted_tiles():
         alpha = np.minimum(np.float32(0.999), p[5] * O.expf(-sigma))
         hit = (alpha >= mid) & (sigma >= 0)
         for y, x in zip(*np.nonzero(hit)):
-            assert ((x // 16) + (y // 16) * tbw, c) in binned, f"splat {c} pixel ({x},{y}) not binned"
+            assert ((x // 16) + (y // th) * tbw, c) in binned, f"splat {c} pixel ({x},{y}) not binned"
     ref = O.rasterize_reference(r.projected[: r.num_visible], 96, 80, (0, 0, 0), False)
     assert np.max(np.abs(r.out_img - ref)) <= 2e-5
 
@@ -419,3 +425,29 @@ def test_backward_gradients_finite_on_random_scenes():
         out = O.project_backward(fwd, tr, sh, opac, vc)
         for a in out:
             assert np.all(np.isfinite(a))
+
+
+# ---- 16x8 candidate tiles ---------------------------------------------------------------------
+
+@pytest.mark.parametrize("seed,flags", [(1, 1), (2, 3), (3, 5), (4, 9), (5, 0)])
+def test_candidate_tiles_render_the_same_image(seed, flags):
+    """The tile shape only decides which lists a pixel walks; the binning is
+    conservative and every list is in depth order, so the 16x8 rasterizer
+    (gaussian_splats.rs:68-101) gives the 16x16 image bit for bit, the same
+    visibility, and gradients equal up to the order of float sums."""
+    tr, sh, opac = random_scene(300 + seed, 1500, 2, log_scale=(-3.0, 0.6))
+    cam = Camera.from_focal((0.1, -0.1, -3.0), (0.0, 0.0, 0.0, 1.0), 60.0, 71, 53)
+    u = uniforms_for(cam, 71, 53, tr.shape[0], 2)
+    a = O.render_forward(u, tr, sh, opac, flags, (0.1, 0.2, 0.3))
+    b = O.render_forward(u, tr, sh, opac, flags | O.FLAG_TILE_16X8, (0.1, 0.2, 0.3))
+    assert b.uniforms["tile_bh"] == 7 and a.uniforms["tile_bh"] == 4
+    assert np.array_equal(a.out_img.view(np.uint32), b.out_img.view(np.uint32))
+    assert a.num_visible == b.num_visible
+    assert np.array_equal(a.global_from_compact_gid, b.global_from_compact_gid)
+    if flags & 1:
+        assert np.array_equal(a.visible, b.visible)
+        v_out = np.random.default_rng(seed).standard_normal(a.out_img.shape).astype(np.float32)
+        ga = O.rasterize_backward(a, v_out, (flags & 6) | O.FLAG_REFINE_WEIGHT, (0.1, 0.2, 0.3))
+        gb = O.rasterize_backward(b, v_out, (flags & 6) | O.FLAG_REFINE_WEIGHT, (0.1, 0.2, 0.3))
+        scale = np.abs(ga).max(axis=0) + 1e-12
+        assert np.max(np.abs(ga - gb) / scale) < 1e-4
