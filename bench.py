@@ -167,6 +167,8 @@ def main():
     ap.add_argument("--no-timing", action="store_true", help="do not bracket kernels with HIP events")
     ap.add_argument("--profile-steps", type=int, default=5,
                     help="untimed steps with every kernel bracketed by events (per-kernel table)")
+    ap.add_argument("--rasterizer", choices=["legacy", "candidate"], default="legacy",
+                    help="16x16 tiles (the reference's product path) or the 16x8 candidate tiles")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="before warm-up, run one plain device copy of this many MiB (the known-size reference "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
@@ -197,6 +199,7 @@ def main():
     vo = torch.from_numpy(v_out).to(dev) if v_out is not None else None
     gt_dev = torch.from_numpy(gt.view(np.int32)).to(dev) if gt is not None else None
     splats = R.Splats(t, s, o)
+    rasterizer = R.Rasterizer.Candidate if args.rasterizer == "candidate" else R.Rasterizer.Legacy
     cams = [w.camera(k, poses) for k in range(poses)]
     img_size = (w.img_w, w.img_h)
     ctx = _lib.context(0)
@@ -204,7 +207,7 @@ def main():
     if mode == "train":
         from brush_amd.train import SplatTrainer
 
-        trainer = SplatTrainer()
+        trainer = SplatTrainer(rasterizer=rasterizer)
 
     stats = {"num_visible": 0, "num_intersections": 0}
 
@@ -213,7 +216,7 @@ def main():
             t.grad = None
             s.grad = None
             o.grad = None
-            res = R.render_splats_diff(splats, cams[0], img_size, (0.0, 0.0, 0.0))
+            res = R.render_splats_diff(splats, cams[0], img_size, (0.0, 0.0, 0.0), rasterizer=rasterizer)
             res.img.backward(vo)
             stats["num_visible"] = res.num_visible
             stats["num_intersections"] = res.aux.num_intersections
@@ -221,7 +224,7 @@ def main():
         elif mode == "forward":
             vis = isect = 0
             for cam in cams:
-                out = R.render(cam, img_size, t, s, o, raster_pass=R.RasterPass.Forward)
+                out = R.render(cam, img_size, t, s, o, raster_pass=R.RasterPass.Forward, rasterizer=rasterizer)
                 vis += out.aux.num_visible
                 isect += out.aux.num_intersections
                 stats["tile_offsets"] = out.aux.tile_offsets
@@ -251,13 +254,13 @@ def main():
         m_post = int((to[..., 1].long() - to[..., 0].long()).sum().item())
     if mode == "train":
         # the training step's intersection count: one forward at the current parameters
-        out = R.render(cams[0], img_size, t, s, o, raster_pass=R.RasterPass.Backward)
+        out = R.render(cams[0], img_size, t, s, o, raster_pass=R.RasterPass.Backward, rasterizer=rasterizer)
         stats["num_intersections"] = out.aux.num_intersections
         m_post = int((out.aux.tile_offsets[..., 1].long() - out.aux.tile_offsets[..., 0].long()).sum().item())
         out.state.release()
 
     n, v, m = w.n, int(stats["num_visible"]), int(stats["num_intersections"])
-    tiles = ((w.img_w + 15) // 16) * ((w.img_h + 15) // 16)
+    tiles = ((w.img_w + 15) // 16) * ((w.img_h + rasterizer.tile_height - 1) // rasterizer.tile_height)
     c = w.num_coeffs
     pixels = w.img_w * w.img_h
 
@@ -327,7 +330,8 @@ def main():
               "num_intersections_post_raster": m_post, "poses": poses,
               "sort": "two-stage: depth sort of visible splats, then stable tile-id sort of (tile, depth-rank) "
                       "pairs (equivalent to a 64-bit tile|depth key sort)",
-              "parallelism": "single GPU"}
+              "parallelism": "single GPU",
+              "tiles": f"16x{rasterizer.tile_height}"}
     if mode == "train":
         config["loss"] = round(float(stats["loss"].item()), 6)
     line = {

@@ -27,7 +27,7 @@ from . import _lib
 from ._lib import context, lib, ptr
 from .camera import Camera
 from .loss import ImageLossConfig, image_loss_backward_raw, image_loss_forward_raw
-from .render import RasterizationMode, RasterPass, SplatRenderMode, Splats, render
+from .render import RasterizationMode, Rasterizer, RasterPass, SplatRenderMode, Splats, render
 
 
 @dataclass
@@ -96,6 +96,7 @@ class TrainConfig:
 class SplatTrainer:
     config: TrainConfig = field(default_factory=TrainConfig)
     background: tuple = (0.0, 0.0, 0.0)
+    rasterizer: Rasterizer = Rasterizer.Legacy
 
     def __post_init__(self):
         # train.rs:141-143: epsilon 1e-15
@@ -121,7 +122,7 @@ class SplatTrainer:
         t, s, o = splats.transforms, splats.sh_coeffs, splats.raw_opacities
         mode = SplatRenderMode.Mip if splats.render_mip else SplatRenderMode.Default
         out = render(camera, (w, h), t.detach(), s.detach(), o.detach(), mode, RasterizationMode.Rgba,
-                     self.background, RasterPass.Backward)
+                     self.background, RasterPass.Backward, rasterizer=self.rasterizer)
         img = out.out_img  # [H, W, 4]
         loss_cfg = ImageLossConfig(1.0 - cfg.ssim_weight, -cfg.ssim_weight)
         rgb = img[..., :3]
