@@ -7,6 +7,9 @@ gradient ~ N(0, 1): project + cull, depth sort, scan, project_visible, map,
 tile sort, tile offsets, blend, rasterize backward and project backward, all
 through libbrush_hip.so.  Inputs are resident in HBM before the timed region.
 
+``--workload ply`` times PLY import/export instead: decode of a resident
+1M-splat SH-3 vertex element and export encode (bench_ply).
+
 ``--config 0|2`` times the same forward + backward on those workloads,
 ``--config 3`` the forward-only render of the eight 3840x2160 poses (one step =
 eight views), ``--config 4`` one full training step (render, L1 + SSIM loss,
@@ -37,15 +40,16 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "cfg1_hbm_traffic.md")
+PLY_TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "ply_hbm_traffic.md")
 METRIC_CFG1 = "fwd+bwd rasterize ms & Mpix/s, 1M Gaussians SH3 @1080p; % HBM roofline"
 
 
-def measured_traffic(kernel: str, workload: str):
+def measured_traffic(kernel: str, workload: str, profile: str = TRAFFIC_PROFILE):
     """HBM bytes per launch of ``kernel`` from the committed rocprofv3
     FETCH_SIZE / WRITE_SIZE summary (lines ``traffic <kernel> <bytes>``), or
     None when that summary does not cover this workload or kernel."""
     try:
-        text = open(TRAFFIC_PROFILE).read()
+        text = open(profile).read()
     except OSError:
         return None
     if f"workload: {workload}" not in text:
@@ -157,6 +161,139 @@ def cpu_baseline(mode: str, workload, transforms, sh, opac, v_out, gt, min_secon
                       f"{len(times)} repetitions"}
 
 
+PLY_METRIC = "PLY import+export splats/s: decode of a resident 3DGS vertex element + export encode, 1M SH3"
+
+
+def _ply_workload(n: int, seed: int = 7):
+    """A 3DGS-layout PLY (x y z nx ny nz f_dc_0..2 f_rest_0..44 opacity
+    scale_0..2 rot_0..3, 62 float32 properties) of n seeded splats."""
+    rng = np.random.default_rng(seed)
+    names = ["x", "y", "z", "nx", "ny", "nz"] + [f"f_dc_{k}" for k in range(3)] + \
+        [f"f_rest_{k}" for k in range(45)] + ["opacity"] + [f"scale_{k}" for k in range(3)] + \
+        [f"rot_{k}" for k in range(4)]
+    rows = rng.standard_normal((n, len(names)), dtype=np.float32)
+    head = "ply\nformat binary_little_endian 1.0\nelement vertex %d\n" % n
+    head += "".join(f"property float {k}\n" for k in names) + "end_header\n"
+    return head.encode() + rows.tobytes(), len(names) * 4
+
+
+def bench_ply(args):
+    """--workload ply: one step decodes the vertex element of a 1M-splat
+    SH-degree-3 PLY already resident in HBM (bh_ply_decode_rows) and encodes
+    the decoded splats back into export rows (bh_ply_encode_rows)."""
+    import torch
+
+    from brush_amd import _lib
+    from brush_amd import serde as S
+
+    n = 1 << 20
+    dev = torch.device("cuda:0")
+    if args.calibrate_copy_mib > 0:  # the first device copy of the run: rocprofv3 counter calibration
+        src = torch.ones(args.calibrate_copy_mib * (1 << 18), dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+    data, row_bytes = _ply_workload(n)
+    header = S.parse_header(data[:1 << 16])
+    layout = S.vertex_layout(header.get_element("vertex"))
+    body = np.frombuffer(data, np.uint8, n * row_bytes, header.data_offset)
+    rows = torch.from_numpy(body.copy()).to(dev)
+    out = (torch.empty((n, 10), dtype=torch.float32, device=dev),
+           torch.empty((n, layout.num_coeffs, 3), dtype=torch.float32, device=dev),
+           torch.empty((n,), dtype=torch.float32, device=dev))
+    export = torch.empty((n, 11 + 3 * layout.num_coeffs), dtype=torch.float32, device=dev)
+    ctx = _lib.context(0)
+
+    def step():
+        d = S.decode_rows(rows, layout, n, out=out)
+        ctx.check(_lib.lib().bh_ply_encode_rows(ctx.handle, _lib.ptr(d.transforms), _lib.ptr(d.sh), _lib.ptr(d.opac),
+                                                n, layout.num_coeffs, _lib.ptr(export)), "ply_encode_rows")
+
+    out_bytes = n * (10 + 3 * layout.num_coeffs + 1) * 4
+    algo = {"ply_decode_rows": n * row_bytes + out_bytes,
+            "ply_encode_rows": out_bytes + n * (11 + 3 * layout.num_coeffs) * 4}
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    kernels = {}
+    ctx.reset_timings()
+    ctx.set_timing(True)
+    for _ in range(max(args.profile_steps, 1)):
+        step()
+    torch.cuda.synchronize()
+    for name, (launches, total) in ctx.read_timings().items():
+        avg = total / max(launches, 1)
+        kernels[name] = {"avg_ms": round(avg, 4), "algorithmic_mb": round(algo[name] / 1e6, 2),
+                         "gb_s": round(algo[name] / (avg / 1000.0) / 1e9, 1)}
+    ctx.set_timing(False)
+    dominant = max(kernels.items(), key=lambda kv: kv[1]["avg_ms"])[0]
+    ctx.reset_timings()
+    ctx.set_timing(True, only=dominant)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    launches, total = ctx.read_timings()[dominant]
+    ctx.set_timing(False)
+    ms = (t1 - t0) * 1000.0 / args.steps
+    avg = total / max(launches, 1)
+    achieved = round(algo[dominant] / (avg / 1000.0) / 1e9, 1)
+    roofline = {"bound": "hbm", "kernel": dominant, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": measured_traffic(dominant, "ply_1M_sh3", PLY_TRAFFIC_PROFILE),
+                "avg_ms": round(avg, 4), "algorithmic_mb": round(algo[dominant] / 1e6, 2),
+                "timed_launches": int(launches)}
+    # the path a caller with a file in host memory takes (PCIe included)
+    torch.cuda.synchronize()
+    h0 = time.perf_counter()
+    S.load_splat_from_ply(data)
+    torch.cuda.synchronize()
+    host_ms = (time.perf_counter() - h0) * 1000.0
+    cpu = None
+    if args.cpu_seconds > 0:
+        try:
+            from oracle import ply_oracle as P
+
+            sample_n = 1 << 17
+            sample, _ = _ply_workload(sample_n, seed=8)
+            done, c0 = 0, time.perf_counter()
+            while time.perf_counter() - c0 < args.cpu_seconds:
+                m = P.load_splat_from_ply(sample)
+                tt, shh, oo = m.data.with_defaults()
+                P.export_rows(tt, shh, oo)
+                done += sample_n
+            el = time.perf_counter() - c0
+            cpu = {"value": round(done / el, 1), "unit": "splats/s", "cores": 1, "kind": "port",
+                   "sample": f"numpy restatement (oracle/ply_oracle.py): import of a {sample_n}-splat SH3 PLY "
+                             f"from host bytes plus export rows, repeated {done // sample_n}x in {el:.1f} s"}
+        except Exception as e:  # reported, never required
+            cpu = {"error": str(e)}
+    line = {
+        "metric": PLY_METRIC,
+        "value": round(n / (ms / 1000.0), 1),
+        "unit": "splats/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded numpy rows in the 3DGS PLY layout)",
+        "config": {"workload": "ply_1M_sh3", "splats": n, "row_bytes": row_bytes, "sh_degree": 3,
+                   "host_inclusive_load_ms": round(host_ms, 2), "parallelism": "single GPU"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "kernels": kernels,
+    }
+    print(json.dumps(line))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -172,11 +309,17 @@ def main():
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="before warm-up, run one plain device copy of this many MiB (the known-size reference "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
+    ap.add_argument("--workload", choices=["raster", "ply"], default="raster",
+                    help="raster: the rasterizer (BASELINE.json's metric); ply: PLY import/export rows")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
               "(the rasterizer path is single-GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
         sys.exit(2)
+
+    if args.workload == "ply":
+        bench_ply(args)
+        return
 
     import torch
 

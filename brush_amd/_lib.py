@@ -42,6 +42,7 @@ EXPORTED = [
     "bh_fwd_state_release", "bh_rasterize_backward", "bh_render_backward", "bh_project_backward",
     "bh_image_loss_forward", "bh_image_loss_backward", "bh_adam_scaled_step", "bh_copy_to_host",
     "bh_copy_to_device", "bh_copy_device", "bh_device_alloc", "bh_device_free", "bh_synchronize",
+    "bh_ply_decode_rows", "bh_ply_decode_compressed", "bh_ply_encode_rows",
 ]
 
 
@@ -137,6 +138,27 @@ class AdamConfig(ctypes.Structure):
     _fields_ = [("beta_1", ctypes.c_float), ("beta_2", ctypes.c_float), ("epsilon", ctypes.c_float)]
 
 
+PLY_CONST, PLY_I8, PLY_U8, PLY_I16, PLY_U16, PLY_I32, PLY_U32, PLY_F32, PLY_F64 = range(9)
+PLY_OP_PLAIN, PLY_OP_COLOR = 0, 1
+PLY_BIG_ENDIAN = 1
+
+
+class PlyColumn(ctypes.Structure):
+    """bh_ply_column (include/brush_hip.h)."""
+
+    _fields_ = [("offset", ctypes.c_uint32), ("type", ctypes.c_uint16), ("op", ctypes.c_uint16),
+                ("konst", ctypes.c_float)]
+
+
+class PlyCompressedLayout(ctypes.Structure):
+    """bh_ply_compressed_layout (include/brush_hip.h)."""
+
+    _fields_ = [("vertex_row_bytes", ctypes.c_uint32), ("position_offset", ctypes.c_uint32),
+                ("scale_offset", ctypes.c_uint32), ("rotation_offset", ctypes.c_uint32),
+                ("color_offset", ctypes.c_uint32), ("sh_row_bytes", ctypes.c_uint32),
+                ("sh_rest_count", ctypes.c_uint32), ("sh_offsets", ctypes.c_uint16 * 72)]
+
+
 class KernelTiming(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char * 48), ("launches", ctypes.c_uint32), ("total_ms", ctypes.c_double)]
 
@@ -183,6 +205,10 @@ def lib() -> ctypes.CDLL:
         "bh_adam_scaled_step": (S, [P, P, P, P, P, P, U32, U32, U32, ctypes.c_float, U32,
                                     ctypes.POINTER(AdamConfig)]),
         "bh_project_backward": (S, [P, UP, P, P, P, P, P, U32, P, P, P, P]),
+        "bh_ply_decode_rows": (S, [P, P, U64, U32, U64, U32, U32, ctypes.POINTER(PlyColumn), U32, P, P, P]),
+        "bh_ply_decode_compressed": (S, [P, P, U64, P, U64, P, U64, U64, U32, U32,
+                                         ctypes.POINTER(PlyCompressedLayout), P, P, P]),
+        "bh_ply_encode_rows": (S, [P, P, P, P, U64, U32, P]),
         "bh_copy_to_host": (S, [P, P, P, U64]),
         "bh_copy_to_device": (S, [P, P, P, U64]),
         "bh_copy_device": (S, [P, P, P, U64]),

@@ -12,7 +12,7 @@ import time
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libbrush_hip.so")
-SOURCES = ["api.hip", "sort.hip", "project.hip", "raster.hip", "backward.hip", "loss.hip", "adam.hip"]
+SOURCES = ["api.hip", "sort.hip", "project.hip", "raster.hip", "backward.hip", "loss.hip", "adam.hip", "ply.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 FLAGS = [

@@ -612,6 +612,70 @@ bh_status bh_adam_scaled_step(bh_ctx* ctx, float* param, const float* grad, floa
                             time, *cfg);
 }
 
+static bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0u; }
+
+bh_status bh_ply_decode_rows(bh_ctx* ctx, const uint8_t* rows, uint64_t rows_bytes, uint32_t row_bytes,
+                             uint64_t num_rows, uint32_t subsample, uint32_t flags, const bh_ply_column* columns,
+                             uint32_t num_coeffs, float* transforms, float* sh_coeffs, float* raw_opac) {
+    if (!ctx) return BH_ERR_INVALID_ARG;
+    if (subsample == 0) return set_error(ctx, BH_ERR_INVALID_ARG, "ply: subsample must be greater than zero");
+    if (num_rows == 0) return BH_OK;
+    if (!rows || !columns || !transforms || !sh_coeffs || !raw_opac)
+        return set_error(ctx, BH_ERR_INVALID_ARG, "ply: null buffer");
+    if (row_bytes == 0) return set_error(ctx, BH_ERR_INVALID_ARG, "ply: empty rows");
+    if (!aligned4(rows)) return set_error(ctx, BH_ERR_INVALID_ARG, "ply: rows must be 4-byte aligned");
+    if (rows_bytes < (num_rows * row_bytes + 3u) / 4u * 4u)
+        return set_error(ctx, BH_ERR_INVALID_ARG, "ply: rows_bytes below num_rows * row_bytes (rounded up to 4)");
+    const uint64_t n_out = (num_rows + subsample - 1) / subsample;
+    return launch_ply_decode_rows(ctx, rows, rows_bytes, row_bytes, n_out, subsample, flags, columns, num_coeffs,
+                                  transforms, sh_coeffs, raw_opac);
+}
+
+bh_status bh_ply_decode_compressed(bh_ctx* ctx, const float* chunks, uint64_t num_chunks, const uint8_t* vertex_rows,
+                                   uint64_t vertex_bytes, const uint8_t* sh_rows, uint64_t sh_bytes,
+                                   uint64_t num_rows, uint32_t subsample, uint32_t flags,
+                                   const bh_ply_compressed_layout* layout, float* transforms, float* sh_coeffs,
+                                   float* raw_opac) {
+    if (!ctx) return BH_ERR_INVALID_ARG;
+    if (subsample == 0) return set_error(ctx, BH_ERR_INVALID_ARG, "ply: subsample must be greater than zero");
+    if (!layout) return set_error(ctx, BH_ERR_INVALID_ARG, "ply: null layout");
+    if (num_rows == 0) return BH_OK;
+    const bh_ply_compressed_layout& L = *layout;
+    if (!chunks || !vertex_rows || !transforms || !sh_coeffs || !raw_opac)
+        return set_error(ctx, BH_ERR_INVALID_ARG, "ply: null buffer");
+    if (num_chunks < (num_rows + 255u) / 256u)
+        return set_error(ctx, BH_ERR_INVALID_ARG, "ply: fewer chunk rows than ceil(num_rows / 256)");
+    const uint32_t offs[4] = {L.position_offset, L.scale_offset, L.rotation_offset, L.color_offset};
+    for (uint32_t o : offs)
+        if ((uint64_t)o + 4u > L.vertex_row_bytes)
+            return set_error(ctx, BH_ERR_INVALID_ARG, "ply: packed word outside the vertex row");
+    if (!aligned4(vertex_rows) || vertex_bytes < num_rows * L.vertex_row_bytes)
+        return set_error(ctx, BH_ERR_INVALID_ARG, "ply: vertex rows unaligned or shorter than num_rows rows");
+    if (L.sh_row_bytes == 0) {
+        if (L.sh_rest_count != 0) return set_error(ctx, BH_ERR_INVALID_ARG, "ply: SH rest count without sh rows");
+    } else {
+        const uint32_t rc = L.sh_rest_count;
+        if (!(rc == 0 || rc == 9 || rc == 24 || rc == 45 || rc == 72))
+            return set_error(ctx, BH_ERR_INVALID_ARG, "ply: Unsupported SH rest property count");
+        if (!sh_rows || sh_bytes < num_rows * L.sh_row_bytes)
+            return set_error(ctx, BH_ERR_INVALID_ARG, "ply: sh rows missing or shorter than num_rows rows");
+        for (uint32_t k = 0; k < rc; k++)
+            if (L.sh_offsets[k] >= L.sh_row_bytes)
+                return set_error(ctx, BH_ERR_INVALID_ARG, "ply: SH property outside the sh row");
+    }
+    const uint64_t n_out = (num_rows + subsample - 1) / subsample;
+    return launch_ply_decode_compressed(ctx, chunks, vertex_rows, sh_rows, n_out, subsample, flags, L, transforms,
+                                        sh_coeffs, raw_opac);
+}
+
+bh_status bh_ply_encode_rows(bh_ctx* ctx, const float* transforms, const float* sh_coeffs, const float* raw_opac,
+                             uint64_t n, uint32_t num_coeffs, float* rows) {
+    if (!ctx) return BH_ERR_INVALID_ARG;
+    if (n == 0) return BH_OK;
+    if (!transforms || !sh_coeffs || !raw_opac || !rows) return set_error(ctx, BH_ERR_INVALID_ARG, "ply: null buffer");
+    return launch_ply_encode_rows(ctx, transforms, sh_coeffs, raw_opac, n, num_coeffs, rows);
+}
+
 bh_status bh_copy_to_host(bh_ctx* ctx, void* dst, const void* src, uint64_t bytes) {
     if (!ctx || (bytes && (!dst || !src))) return BH_ERR_INVALID_ARG;
     if (!bytes) return BH_OK;

@@ -53,6 +53,17 @@ bh_status launch_adam_step(bh_ctx* ctx, float* param, const float* grad, float* 
                            const float* scaling, uint32_t rows, uint32_t row_len, bool reduce, float lr,
                            uint32_t time, const bh_adam_config& cfg);
 
+// ply.hip
+bh_status launch_ply_decode_rows(bh_ctx* ctx, const uint8_t* rows, uint64_t rows_bytes, uint32_t row_bytes,
+                                 uint64_t n_out, uint32_t subsample, uint32_t flags, const bh_ply_column* columns,
+                                 uint32_t num_coeffs, float* transforms, float* sh, float* opac);
+bh_status launch_ply_decode_compressed(bh_ctx* ctx, const float* chunks, const uint8_t* vrows, const uint8_t* srows,
+                                       uint64_t n_out, uint32_t subsample, uint32_t flags,
+                                       const bh_ply_compressed_layout& layout, float* transforms, float* sh,
+                                       float* opac);
+bh_status launch_ply_encode_rows(bh_ctx* ctx, const float* transforms, const float* sh, const float* opac, uint64_t n,
+                                 uint32_t num_coeffs, float* rows);
+
 }  // namespace bh
 
 struct bh_ctx {

@@ -356,14 +356,37 @@ def project_bwd(transforms, sh_coeffs, raw_opac, global_from_compact_gid, projec
 
 # ---- splat container and entry points ---------------------------------------------------
 
+def fold_min_scale(transforms: torch.Tensor, raw_opac: torch.Tensor, f: torch.Tensor):
+    """gaussian_splats.rs:139-164, the Mip-Splatting 3D filter: scales become
+    sqrt(s^2 + f^2) and the opacity is scaled by sqrt(det(s^2)/det(s^2 + f^2))
+    over the three axes, clamped to [1e-6, 1 - 1e-6] and turned back into a
+    logit.  Differentiable in transforms and raw_opac; ``f`` [N] is a constant."""
+    n = transforms.shape[0]
+    f = f.detach().to(transforms.device, torch.float32)
+    s2 = (transforms[:, 7:10] * 2.0).exp()
+    s2f = s2 + (f * f).reshape(n, 1)
+    new_log = s2f.log() * 0.5
+    out = torch.cat([transforms[:, 0:7], new_log], dim=1)
+
+    def det(t):
+        return t[:, 0:1] * t[:, 1:2] * t[:, 2:3]
+
+    coef = (det(s2) / det(s2f)).sqrt().reshape(n)
+    opac = (torch.sigmoid(raw_opac) * coef).clamp(1e-6, 1.0 - 1e-6)
+    return out, (opac / (1.0 - opac)).log()
+
+
 @dataclass
 class Splats:
     """gaussian_splats.rs:110-127: transforms [N,10] (means | quat wxyz |
-    log-scales), sh_coeffs [N,C,3], raw_opacities [N] (logits)."""
+    log-scales), sh_coeffs [N,C,3], raw_opacities [N] (logits), and an
+    optional frozen per-splat world-space scale floor ``min_scale`` [N] that
+    every render folds in (fold_min_scale) and export bakes."""
     transforms: torch.Tensor
     sh_coeffs: torch.Tensor
     raw_opacities: torch.Tensor
     render_mip: bool = False
+    min_scale: torch.Tensor | None = None
 
     @staticmethod
     def from_tensor_data(means, rotation, log_scales, sh_coeffs, raw_opacity, mode=SplatRenderMode.Default):
@@ -388,11 +411,34 @@ class Splats:
     def log_scales(self):
         return self.transforms[:, 7:10]
 
+    def with_min_scale(self, f: torch.Tensor) -> "Splats":
+        """gaussian_splats.rs:241-247"""
+        if f.shape != (self.num_splats(),):
+            raise ValueError(f"min_scale must be [{self.num_splats()}], got {tuple(f.shape)}")
+        return Splats(self.transforms, self.sh_coeffs, self.raw_opacities, self.render_mip, f)
+
+    def folded(self):
+        """(transforms, raw_opacities) with the min-scale floor folded in."""
+        if self.min_scale is None:
+            return self.transforms, self.raw_opacities
+        return fold_min_scale(self.transforms, self.raw_opacities, self.min_scale)
+
     def scales(self):
-        return self.log_scales().exp()
+        """gaussian_splats.rs:279-292: with the floor folded in."""
+        return self.folded()[0][:, 7:10].exp()
 
     def opacities(self):
-        return torch.sigmoid(self.raw_opacities)
+        """gaussian_splats.rs:261-277: with the floor's energy compensation."""
+        return torch.sigmoid(self.folded()[1])
+
+    def bake_min_scale(self) -> "Splats":
+        """gaussian_splats.rs:294-307: fold the floor into the parameters and
+        drop it; the result renders identically."""
+        if self.min_scale is None:
+            return self
+        with torch.no_grad():
+            t, o = self.folded()
+        return Splats(t.contiguous(), self.sh_coeffs, o.contiguous(), self.render_mip, None)
 
 
 def render_splats(splats: Splats, camera: Camera, img_size, background=(0.0, 0.0, 0.0),
@@ -400,14 +446,15 @@ def render_splats(splats: Splats, camera: Camera, img_size, background=(0.0, 0.0
     """Non-differentiable render (gaussian_splats.rs:417-437, 468-549):
     returns (image, RenderAux).  Float mode renders with the backward
     bookkeeping (f32 RGBA); Packed mode returns packed RGBA8 in an int32 [H, W]."""
-    transforms = splats.transforms
-    if splat_scale is not None:
-        transforms = transforms.clone()
-        transforms[:, 7:10] += math.log(splat_scale)
+    with torch.no_grad():
+        transforms, raw_opacities = splats.folded()  # gaussian_splats.rs:484-491
+        if splat_scale is not None:
+            transforms = transforms.clone()
+            transforms[:, 7:10] += math.log(splat_scale)
     raster_pass = RasterPass.Backward if texture_mode is TextureMode.Float else RasterPass.Forward
     mode = SplatRenderMode.Mip if splats.render_mip else SplatRenderMode.Default
     out = render(camera, img_size, transforms.detach(), splats.sh_coeffs.detach(),
-                 splats.raw_opacities.detach(), mode, RasterizationMode.Rgba, background, raster_pass)
+                 raw_opacities.detach(), mode, RasterizationMode.Rgba, background, raster_pass)
     return out.out_img, out.aux
 
 
@@ -497,7 +544,8 @@ def render_splats_diff(splats: Splats, camera: Camera, img_size, background=(0.0
     mode = SplatRenderMode.Mip if splats.render_mip else SplatRenderMode.Default
     cfg = _DiffConfig(camera, img_size, background, mode, raster_mode, raster_pass, compute_refine_weight,
                       rasterizer)
-    img = _RenderSplatsFn.apply(splats.transforms, splats.sh_coeffs, splats.raw_opacities, cfg)
+    transforms, raw_opacities = splats.folded()  # burn_glue.rs:631-641, differentiable through the fold
+    img = _RenderSplatsFn.apply(transforms, splats.sh_coeffs, raw_opacities, cfg)
     aux = cfg.output.aux
     res = SplatOutputDiff(img, aux.num_visible, aux.visible, aux.max_radius, aux)
     res._cfg = cfg

@@ -27,7 +27,7 @@ from . import _lib
 from ._lib import context, lib, ptr
 from .camera import Camera
 from .loss import ImageLossConfig, image_loss_backward_raw, image_loss_forward_raw
-from .render import RasterizationMode, Rasterizer, RasterPass, SplatRenderMode, Splats, render
+from .render import RasterizationMode, Rasterizer, RasterPass, SplatRenderMode, Splats, fold_min_scale, render
 
 
 @dataclass
@@ -121,7 +121,15 @@ class SplatTrainer:
         h, w = gt_packed.shape
         t, s, o = splats.transforms, splats.sh_coeffs, splats.raw_opacities
         mode = SplatRenderMode.Mip if splats.render_mip else SplatRenderMode.Default
-        out = render(camera, (w, h), t.detach(), s.detach(), o.detach(), mode, RasterizationMode.Rgba,
+        rt, ro = t, o
+        if splats.min_scale is not None:
+            # the render sees the folded floor (burn_glue.rs:631-641); its
+            # gradients are chained back through the fold after the backward
+            with torch.enable_grad():
+                t_leaf = t.detach().requires_grad_()
+                o_leaf = o.detach().requires_grad_()
+                rt, ro = fold_min_scale(t_leaf, o_leaf, splats.min_scale)
+        out = render(camera, (w, h), rt.detach(), s.detach(), ro.detach(), mode, RasterizationMode.Rgba,
                      self.background, RasterPass.Backward, rasterizer=self.rasterizer)
         img = out.out_img  # [H, W, 4]
         loss_cfg = ImageLossConfig(1.0 - cfg.ssim_weight, -cfg.ssim_weight)
@@ -140,9 +148,12 @@ class SplatTrainer:
         bg = (ctypes.c_float * 3)(*[float(x) for x in self.background])
         with torch.cuda.device(t.device):
             ctx = context()
+            rt_c, ro_c = rt.detach().contiguous(), ro.detach().contiguous()
             ctx.check(lib().bh_render_backward(ctx.handle, out.state.handle, ptr(img), ptr(out.aux.tile_offsets),
-                                               bg, ptr(t), ptr(s), ptr(o), ptr(v_img), flags, ptr(v_t), ptr(v_c),
-                                               ptr(v_o), ptr(v_r)), "render_backward")
+                                               bg, ptr(rt_c), ptr(s), ptr(ro_c), ptr(v_img), flags, ptr(v_t),
+                                               ptr(v_c), ptr(v_o), ptr(v_r)), "render_backward")
+        if splats.min_scale is not None:
+            v_t, v_o = torch.autograd.grad([rt, ro], [t_leaf, o_leaf], [v_t, v_o])
         # optimizer (train.rs:966-1051); the per-column scales live on the device
         lr_t = (cfg.lr_mean,) * 3 + (cfg.lr_rotation,) * 4 + (cfg.lr_scale,) * 3
         if self._lr_t != lr_t:

@@ -299,6 +299,88 @@ bh_status bh_project_backward(bh_ctx* ctx, const bh_project_uniforms* u, const f
                               uint32_t flags, float* v_transforms, float* v_coeffs,
                               float* v_raw_opac, float* v_refine);
 
+/* ---- PLY rows (brush-serde) ------------------------------------------------ */
+
+/* Scalar types of PLY properties (the header's char .. double). */
+#define BH_PLY_I8 1u
+#define BH_PLY_U8 2u
+#define BH_PLY_I16 3u
+#define BH_PLY_U16 4u
+#define BH_PLY_I32 5u
+#define BH_PLY_U32 6u
+#define BH_PLY_F32 7u
+#define BH_PLY_F64 8u
+/* A column with no property in the file: the value is `konst`. */
+#define BH_PLY_CONST 0u
+/* Column ops: PLAIN converts the value to f32 (Rust `as f32`); COLOR is a
+ * red/green/blue override: u8 / 255, u16 / 65535 or f32 as is
+ * (ply_gaussian.rs:35-56), then rgb_to_sh, (c - 0.5) / SH_C0 (sh.rs:20-31). */
+#define BH_PLY_OP_PLAIN 0u
+#define BH_PLY_OP_COLOR 1u
+/* flags */
+#define BH_PLY_BIG_ENDIAN 1u
+
+/* Where one output value comes from in a vertex row. */
+typedef struct bh_ply_column {
+    uint32_t offset; /* byte offset of the property in the row */
+    uint16_t type;   /* BH_PLY_* scalar type, or BH_PLY_CONST */
+    uint16_t op;     /* BH_PLY_OP_* */
+    float konst;     /* value of a BH_PLY_CONST column */
+} bh_ply_column;
+
+/* Decode the rows of a standard PLY vertex element straight into the splat
+ * layout.  Replaces the row visitor of parse_ply
+ * (crates/brush-serde/src/import.rs:341-502) with SplatData::into_splats
+ * (import.rs:76-91) fused in: the caller resolves the header into
+ * 11 + 3 * num_coeffs columns, in output order
+ *   x y z rot_0..3 scale_0..2 | opacity | sh[c][channel] for c < num_coeffs,
+ * with the into_splats defaults as BH_PLY_CONST columns.
+ * rows: device copy of the element's bytes (binary little- or big-endian per
+ * flags; an ASCII file is first converted by the host), 4-byte aligned,
+ * rows_bytes >= num_rows * row_bytes.  Row k * subsample becomes splat k for
+ * k < ceil(num_rows / subsample); num_coeffs is 1, 4, 9, 16 or 25; rows are
+ * at most 32 KiB.  Outputs (device, every element written):
+ * transforms f32 [n,10], sh_coeffs f32 [n,num_coeffs,3], raw_opac f32 [n]. */
+bh_status bh_ply_decode_rows(bh_ctx* ctx, const uint8_t* rows, uint64_t rows_bytes, uint32_t row_bytes,
+                             uint64_t num_rows, uint32_t subsample, uint32_t flags,
+                             const bh_ply_column* columns, uint32_t num_coeffs, float* transforms,
+                             float* sh_coeffs, float* raw_opac);
+
+/* The SuperSplat compressed layout (import.rs:504-720, quant.rs:1-71). */
+typedef struct bh_ply_compressed_layout {
+    uint32_t vertex_row_bytes;
+    uint32_t position_offset; /* byte offsets of the four packed u32 words */
+    uint32_t scale_offset;
+    uint32_t rotation_offset;
+    uint32_t color_offset;
+    uint32_t sh_row_bytes;    /* bytes of one `sh` row; 0 without an sh element */
+    uint32_t sh_rest_count;   /* 0, 9, 24, 45 or 72 u8 properties */
+    uint16_t sh_offsets[72];  /* byte offset of f_rest_k in an sh row */
+} bh_ply_compressed_layout;
+
+/* Decode a compressed PLY.  Replaces parse_compressed_ply
+ * (import.rs:504-720).  chunks: device f32 [num_chunks, 18] holding each
+ * chunk row's min_x max_x min_y max_y min_z max_z min_scale_x max_scale_x
+ * min_scale_y max_scale_y min_scale_z max_scale_z min_r max_r min_g max_g
+ * min_b max_b; num_chunks >= ceil(num_rows / 256).  vertex_rows / sh_rows:
+ * device copies of the vertex and sh elements (sh_rows may be NULL when
+ * layout->sh_row_bytes is 0), 4-byte aligned.  Outputs as bh_ply_decode_rows
+ * with num_coeffs = 1 + sh_rest_count / 3. */
+bh_status bh_ply_decode_compressed(bh_ctx* ctx, const float* chunks, uint64_t num_chunks,
+                                   const uint8_t* vertex_rows, uint64_t vertex_bytes, const uint8_t* sh_rows,
+                                   uint64_t sh_bytes, uint64_t num_rows, uint32_t subsample, uint32_t flags,
+                                   const bh_ply_compressed_layout* layout, float* transforms, float* sh_coeffs,
+                                   float* raw_opac);
+
+/* Encode splats as the rows of an exported PLY.  Replaces read_splat_data
+ * (crates/brush-serde/src/export.rs:83-178): per splat, 11 + 3 * num_coeffs
+ * f32 values x y z scale_0..2 opacity rot_0..3 f_dc_0..2 f_rest_*, the
+ * quaternion divided by max(|q|, 1e-12) and the rest coefficients
+ * channel-major.  rows: device f32 [n, 11 + 3 * num_coeffs] (little-endian,
+ * ready to follow the header). */
+bh_status bh_ply_encode_rows(bh_ctx* ctx, const float* transforms, const float* sh_coeffs,
+                             const float* raw_opac, uint64_t n, uint32_t num_coeffs, float* rows);
+
 /* ---- host/device copies (plumbing for bindings without a tensor library) */
 bh_status bh_copy_to_host(bh_ctx* ctx, void* dst_host, const void* src_device, uint64_t bytes);
 bh_status bh_copy_to_device(bh_ctx* ctx, void* dst_device, const void* src_host, uint64_t bytes);

@@ -50,6 +50,9 @@ def test_null_arguments_return_status_codes():
     assert L.bh_rasterize_backward(null, null, null, null, null, 0, null, 1, 1, null, 0, null) == 1
     assert L.bh_project_backward(null, None, null, null, null, null, null, 0, null, null, null, null) == 1
     assert L.bh_fwd_state_info(null, None) == 1
+    assert L.bh_ply_decode_rows(null, null, 0, 4, 1, 1, 0, None, 1, null, null, null) == 1
+    assert L.bh_ply_decode_compressed(null, null, 0, null, 0, null, 0, 1, 1, 0, None, null, null, null) == 1
+    assert L.bh_ply_encode_rows(null, null, null, null, 1, 1, null) == 1
     assert L.bh_last_error(null) == b"null context"
     L.bh_fwd_state_release(null)
     L.bh_ctx_destroy(null)

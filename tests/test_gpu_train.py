@@ -187,3 +187,57 @@ def test_config4_training_steps_reduce_the_loss(gpu):
     assert losses[-1] < losses[0]
     for t in (splats.transforms, splats.sh_coeffs, splats.raw_opacities):
         assert bool(torch.isfinite(t).all())
+
+
+def test_min_scale_floor_in_render_and_training(gpu):
+    """Splats.min_scale (gaussian_splats.rs:139-164): both render paths render
+    the folded splat, and the trainer's gradients are the restatement's chain
+    at the folded parameters pulled back through the fold (rtol 1e-3)."""
+    import torch
+    from brush_amd import render as R
+    from brush_amd.camera import Camera
+    from brush_amd.train import SplatTrainer
+
+    n, deg, W, H = 2000, 1, 72, 56
+    tr, sh, op = random_scene(4202, n, deg, log_scale=(-4.0, -1.0))
+    cam = Camera.from_focal((0.0, 0.1, -3.0), (0.0, 0.0, 0.0, 1.0), 90.0, W, H)
+    f = np.random.default_rng(5).uniform(0.002, 0.03, n).astype(np.float32)
+    t_d, s_d, o_d, f_d = (torch.from_numpy(a.copy()).to(gpu) for a in (tr, sh, op, f))
+    floored = R.Splats(t_d.clone(), s_d.clone(), o_d.clone(), min_scale=f_d)
+    ft, fo = R.fold_min_scale(t_d, o_d, f_d)
+    plain = R.Splats(ft.contiguous(), s_d.clone(), fo.contiguous())
+    img_a, _ = R.render_splats(floored, cam, (W, H))
+    img_b, _ = R.render_splats(plain, cam, (W, H))
+    assert torch.equal(img_a, img_b)
+    # differentiable path: gradients reach the unfolded leaves through the fold
+    leaves = [t_d.clone().requires_grad_(), s_d.clone().requires_grad_(), o_d.clone().requires_grad_()]
+    out = R.render_splats_diff(R.Splats(*leaves, min_scale=f_d), cam, (W, H))
+    v_img = torch.randn(out.img.shape, device=gpu, generator=torch.Generator(device=gpu).manual_seed(3))
+    out.img.backward(v_img)
+    ref = [t_d.clone().requires_grad_(), o_d.clone().requires_grad_()]
+    rt, ro = R.fold_min_scale(ref[0], ref[1], f_d)
+    out2 = R.render_splats_diff(R.Splats(rt, s_d.clone().requires_grad_(), ro), cam, (W, H))
+    out2.img.backward(v_img)
+    rel_close("v_transforms (diff)", leaves[0].grad.cpu().numpy(), ref[0].grad.cpu().numpy(), rtol=1e-3,
+              atol_frac=1e-4)
+    rel_close("v_raw_opac (diff)", leaves[2].grad.cpu().numpy(), ref[1].grad.cpu().numpy(), rtol=1e-3,
+              atol_frac=1e-4)
+    # the training step
+    rng = np.random.default_rng(13)
+    gt = _pack(np.concatenate([rng.integers(0, 256, (H, W, 3), dtype=np.uint8),
+                               np.full((H, W, 1), 255, np.uint8)], -1))
+    trainer = SplatTrainer()
+    res = trainer.step(R.Splats(t_d.clone(), s_d.clone(), o_d.clone(), min_scale=f_d), cam, _i32(gt).to(gpu),
+                       record_grads=True)
+    u = uniforms_for(cam, W, H, n, deg)
+    (vt_f, vcoef, vo_f, _), _ = _oracle_step_grads(u, ft.cpu().numpy(), sh, fo.cpu().numpy(), gt,
+                                                   trainer.config.ssim_weight)
+    pt, po = t_d.clone().requires_grad_(), o_d.clone().requires_grad_()
+    qt, qo = R.fold_min_scale(pt, po, f_d)
+    want_t, want_o = torch.autograd.grad([qt, qo], [pt, po], [torch.from_numpy(vt_f).to(gpu),
+                                                               torch.from_numpy(vo_f).to(gpu)])
+    rel_close("v_transforms (train)", res["v_transforms"].cpu().numpy(), want_t.cpu().numpy(), rtol=1e-3,
+              atol_frac=1e-4)
+    rel_close("v_raw_opac (train)", res["v_raw_opac"].cpu().numpy(), want_o.cpu().numpy(), rtol=1e-3,
+              atol_frac=1e-4)
+    rel_close("v_coeffs (train)", res["v_coeffs"].cpu().numpy(), vcoef, rtol=1e-3, atol_frac=1e-4)
