@@ -382,14 +382,31 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
     uint32_t num_visible = 0;
     uint64_t num_isect = 0;
     uint32_t kmin = 0, kmax = 0;
-    if (bwd && num_splats) launch_fill_u32(ctx, (uint32_t*)visible, 0u, num_splats);
+    // Everything the forward needs zeroed, in one launch: the counters' flags
+    // word (the reduction kernel writes the others), the visible mask, the
+    // depth sort's histograms and look-back status (sized for 32 key bits,
+    // which covers the key range found later), the scan's status (sized for
+    // N >= V), and both tile-offset arrays (empty tiles stay [0, 0]).
+    char *depth_scr = nullptr, *scan_scr = nullptr;
+    if (num_splats) {
+        BH_STRY(ws.get(&depth_scr, radix_sort_scratch_bytes(num_splats, 32)));
+        BH_STRY(ws.get(&scan_scr, scan_scratch_bytes(num_splats)));
+    }
+    {
+        const FillRange zero[] = {
+            {ctx->d_counters + 1, 0u, num_splats ? 1u : 0u},
+            {(uint32_t*)visible, 0u, bwd ? (uint64_t)num_splats : 0u},
+            {(uint32_t*)depth_scr, 0u, num_splats ? radix_sort_zeroed_words(num_splats, 32) : 0u},
+            {(uint32_t*)(scan_scr + 64), 0u, num_splats ? scan_zeroed_words(num_splats) : 0u},
+            {off_pre, 0u, (uint64_t)num_tiles * 2},
+            {tile_offsets, 0u, bwd ? (uint64_t)num_tiles * 2 : 0u},
+        };
+        launch_fill_multi(ctx, zero, (int)(sizeof(zero) / sizeof(zero[0])));
+    }
     if (num_splats) {
         uint32_t *depth_keys, *partials;
         BH_STRY(ws.get(&depth_keys, num_splats));
         BH_STRY(ws.get((char**)&partials, project_partials_bytes(num_splats)));
-        // counters: visible, flags, isect lo, isect hi, min key, max key; the
-        // reduction kernel writes all but the flags word
-        launch_fill_u32(ctx, ctx->d_counters + 1, 0u, 1);
         launch_project_forward(ctx, u, transforms, raw_opacities, num_splats, mip, tile_h, counts, max_radius, depth_keys,
                                partials, ctx->d_counters);
         BH_STRY(check_launch(ctx, "project_forward"));
@@ -411,13 +428,11 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
             const uint32_t cap = kmax - kmin + 1u;
             const uint32_t key_bits = std::max<uint32_t>(1u, bit_length(cap));
             uint32_t *sk, *tk, *tv;
-            char* scr;
             BH_STRY(ws.get(&sk, num_splats));
             BH_STRY(ws.get(&tk, num_splats));
             BH_STRY(ws.get(&tv, num_splats));
-            BH_STRY(ws.get(&scr, radix_sort_scratch_bytes(num_splats, key_bits)));
-            BH_STRY(radix_sort_pairs(ctx, depth_keys, nullptr, num_splats, key_bits, kmin, cap, sk, gfc, tk, tv, scr,
-                                     "depth_sort"));
+            BH_STRY(radix_sort_pairs(ctx, depth_keys, nullptr, num_splats, key_bits, kmin, cap, sk, gfc, tk, tv,
+                                     depth_scr, "depth_sort", true));
         }
     }
     BH_STRY(sget((void**)&cum, (size_t)num_visible * 4));
@@ -428,9 +443,7 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
     BH_STRY(sget((void**)&tile_ids, (size_t)std::max<uint32_t>(m, 1) * 4));
     BH_STRY(sget((void**)&cgids, (size_t)std::max<uint32_t>(m, 1) * 4));
     if (num_visible) {
-        char* scr;
-        BH_STRY(ws.get(&scr, scan_scratch_bytes(num_visible)));
-        BH_STRY(inclusive_scan(ctx, counts, gfc, cum, num_visible, scr));
+        BH_STRY(inclusive_scan(ctx, counts, gfc, cum, num_visible, scan_scr, true));
         launch_project_visible(ctx, u, transforms, sh_coeffs, raw_opacities, gfc, num_visible, sh_degree, mip,
                                projected, depths);
         BH_STRY(check_launch(ctx, "project_visible"));
@@ -454,10 +467,9 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
         launch_fill_u32(ctx, tile_ids, 0u, 1);
         launch_fill_u32(ctx, cgids, 0u, 1);
     }
-    launch_tile_offsets(ctx, tile_ids, m, num_tiles, off_pre);
+    launch_tile_offsets(ctx, tile_ids, m, num_tiles, off_pre, true);
     launch_rasterize(ctx, u.img_w, u.img_h, u.tile_bw, u.tile_bh, background, num_visible, projected, cgids, gfc,
-                     off_pre, flags,
-                     out_img, visible, tile_offsets);
+                     off_pre, flags, out_img, visible, tile_offsets, true);
     BH_STRY(check_launch(ctx, "rasterize"));
 #undef BH_STRY
 

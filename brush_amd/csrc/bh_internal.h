@@ -105,6 +105,14 @@ inline uint32_t div_up(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) /
 
 // fill.hip
 void launch_fill_u32(bh_ctx* ctx, uint32_t* p, uint32_t value, uint64_t count);
+// Several fills in one launch (at most kMaxFillRanges; empty ranges allowed).
+struct FillRange {
+    uint32_t* p;
+    uint32_t value;
+    uint64_t count;
+};
+constexpr int kMaxFillRanges = 8;
+void launch_fill_multi(bh_ctx* ctx, const FillRange* ranges, int k);
 
 // sort.hip
 size_t radix_sort_scratch_bytes(uint32_t n, uint32_t key_bits);
@@ -112,10 +120,14 @@ size_t radix_sort_scratch_bytes(uint32_t n, uint32_t key_bits);
 // key' = min(key - key_sub, key_cap), in ceil(key_bits / 8) passes of equal
 // digit width.  vals_in == nullptr means vals = index.  The transformed keys
 // are what the sort emits.  tmp_* are n-element buffers.
+// The first radix_sort_zeroed_words(n, key_bits) words of `scratch` must be
+// zero when the sort starts; with scratch_zeroed the caller has done that
+// (it may size the fill for 32 key bits, which covers any key_bits).
+size_t radix_sort_zeroed_words(uint32_t n, uint32_t key_bits);
 bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t* vals_in, uint32_t n,
                            uint32_t key_bits, uint32_t key_sub, uint32_t key_cap, uint32_t* keys_out,
                            uint32_t* vals_out, uint32_t* tmp_keys, uint32_t* tmp_vals, void* scratch,
-                           const char* tag = "radix");
+                           const char* tag = "radix", bool scratch_zeroed = false);
 // out[i] = in[i] & mask
 void launch_mask_u32(bh_ctx* ctx, const uint32_t* in, uint32_t mask, uint32_t n, uint32_t* out);
 // keys_out[i] = keys_in[perm[i]], vals_out[i] = vals_in[perm[i]]
@@ -123,8 +135,11 @@ void launch_gather_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t* v
                          uint32_t n, uint32_t* keys_out, uint32_t* vals_out);
 size_t scan_scratch_bytes(uint32_t n);
 // Inclusive scan of in[i] (or in[gather[i]] when gather != nullptr).
+// The first scan_zeroed_words(n) words of `scratch` past its 64-byte header
+// must be zero; with status_zeroed the caller has done that.
+size_t scan_zeroed_words(uint32_t n);
 bh_status inclusive_scan(bh_ctx* ctx, const uint32_t* in, const uint32_t* gather, uint32_t* out, uint32_t n,
-                         void* scratch);
+                         void* scratch, bool status_zeroed = false);
 
 // project.hip
 size_t project_partials_bytes(uint32_t n);
@@ -139,11 +154,11 @@ void launch_map_intersects(bh_ctx* ctx, uint32_t tile_bw, uint32_t tile_bh, uint
 
 // raster.hip
 void launch_tile_offsets(bh_ctx* ctx, const uint32_t* tile_ids, uint32_t m, uint32_t num_tiles,
-                         uint32_t* offsets);
+                         uint32_t* offsets, bool zeroed = false);
 void launch_rasterize(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,
                       const float* bg, uint32_t num_visible, const float* projected, const uint32_t* cgids, const uint32_t* gfc,
                       const uint32_t* off_pre, uint32_t flags, void* out_img, float* visible,
-                      uint32_t* off_post);
+                      uint32_t* off_post, bool off_post_zeroed = false);
 
 // backward.hip
 void launch_rasterize_backward(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,

@@ -21,29 +21,44 @@
 
 namespace bh {
 
+// Four consecutive ids per thread (one 16-byte load when the quad lies in
+// range and `ids` is 16-byte aligned), each compared with its predecessor:
+// a change of id at i ends the previous tile's run and starts the next one.
 __global__ __launch_bounds__(256) void tile_offsets_kernel(const uint32_t* __restrict__ ids, uint32_t m,
                                                             uint32_t num_tiles, uint32_t* __restrict__ off) {
-    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
-    if (i >= m) return;
-    const uint32_t tid = ids[i];
-    if (i == 0) {
-        if (tid < num_tiles) off[2 * tid] = 0;
+    const uint32_t i0 = (blockIdx.x * 256u + threadIdx.x) * 4u;
+    if (i0 >= m) return;
+    uint32_t v[4];
+    if (i0 + 4u <= m && (reinterpret_cast<uintptr_t>(ids) & 15u) == 0u) {
+        const uint4 q = reinterpret_cast<const uint4*>(ids)[i0 / 4u];
+        v[0] = q.x, v[1] = q.y, v[2] = q.z, v[3] = q.w;
     } else {
-        const uint32_t prev = ids[i - 1];
-        if (tid != prev) {
+#pragma unroll
+        for (uint32_t k = 0; k < 4u; k++) v[k] = i0 + k < m ? ids[i0 + k] : 0u;
+    }
+    uint32_t prev = i0 > 0 ? ids[i0 - 1] : 0u;
+#pragma unroll
+    for (uint32_t k = 0; k < 4u; k++) {
+        const uint32_t i = i0 + k;
+        if (i >= m) break;
+        const uint32_t tid = v[k];
+        if (i == 0) {
+            if (tid < num_tiles) off[2 * tid] = 0;
+        } else if (tid != prev) {
             if (prev < num_tiles) off[2 * prev + 1] = i;
             if (tid < num_tiles) off[2 * tid] = i;
         }
+        if (i == m - 1 && tid < num_tiles) off[2 * tid + 1] = i + 1;
+        prev = tid;
     }
-    if (i == m - 1 && tid < num_tiles) off[2 * tid + 1] = i + 1;
 }
 
 void launch_tile_offsets(bh_ctx* ctx, const uint32_t* tile_ids, uint32_t m, uint32_t num_tiles,
-                         uint32_t* offsets) {
-    launch_fill_u32(ctx, offsets, 0u, (uint64_t)num_tiles * 2);
+                         uint32_t* offsets, bool zeroed) {
+    if (!zeroed) launch_fill_u32(ctx, offsets, 0u, (uint64_t)num_tiles * 2);
     if (m == 0) return;
     KernelTimer t(ctx, "tile_offsets");
-    tile_offsets_kernel<<<div_up(m, 256), 256, 0, ctx->stream>>>(tile_ids, m, num_tiles, offsets);
+    tile_offsets_kernel<<<div_up(div_up(m, 4), 256), 256, 0, ctx->stream>>>(tile_ids, m, num_tiles, offsets);
 }
 
 // One workgroup (a single wave) per 8x8 pixel block of a 16 x TH tile; the
@@ -181,14 +196,15 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
 
 void launch_rasterize(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,
                       const float* bg, uint32_t num_visible, const float* projected, const uint32_t* cgids, const uint32_t* gfc,
-                      const uint32_t* off_pre, uint32_t flags, void* out_img, float* visible, uint32_t* off_post) {
+                      const uint32_t* off_pre, uint32_t flags, void* out_img, float* visible, uint32_t* off_post,
+                      bool off_post_zeroed) {
     const uint32_t num_tiles = tile_bw * tile_bh;
     if (num_tiles == 0) return;
     const bool bwd = (flags & BH_FLAG_BWD_INFO) != 0;
     const bool smooth = (flags & BH_FLAG_SMOOTH_CUTOFF) != 0;
     const bool depth = bwd && (flags & BH_FLAG_RENDER_DEPTH) != 0;
     const uint32_t nv = num_visible > 0 ? num_visible : 1u;
-    if (bwd) launch_fill_u32(ctx, off_post, 0u, (uint64_t)num_tiles * 2);
+    if (bwd && !off_post_zeroed) launch_fill_u32(ctx, off_post, 0u, (uint64_t)num_tiles * 2);
     const bool fine = (flags & BH_FLAG_TILE_16X8) != 0;
     // 8 tiles per group of workgroup ids, 4 (16x16) or 2 (16x8) blocks per tile
     const uint32_t groups = div_up(num_tiles, 8) * (fine ? 16u : 32u);

@@ -55,6 +55,48 @@ void launch_fill_u32(bh_ctx* ctx, uint32_t* p, uint32_t value, uint64_t count) {
     fill_u32_kernel<<<blocks, 256, 0, ctx->stream>>>(p, value, count);
 }
 
+struct FillRanges {
+    FillRange r[kMaxFillRanges];
+    int k;
+};
+
+// Every range filled by the whole grid in turn (the range index is uniform),
+// each as fill_u32_kernel fills one.
+__global__ void fill_multi_kernel(FillRanges ranges) {
+    const uint64_t tid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (int j = 0; j < ranges.k; j++) {
+        uint32_t* p = ranges.r[j].p;
+        const uint32_t value = ranges.r[j].value;
+        const uint64_t count = ranges.r[j].count;
+        const uint64_t head = min<uint64_t>(count, ((16u - (reinterpret_cast<uintptr_t>(p) & 15u)) & 15u) / 4u);
+        if (tid < head) p[tid] = value;
+        const uint64_t quads = (count - head) / 4u;
+        uint4* q = reinterpret_cast<uint4*>(p + head);
+        const uint4 v4 = make_uint4(value, value, value, value);
+        for (uint64_t i = tid; i < quads; i += stride) q[i] = v4;
+        for (uint64_t i = head + quads * 4u + tid; i < count; i += stride) p[i] = value;
+    }
+}
+
+void launch_fill_multi(bh_ctx* ctx, const FillRange* ranges, int k) {
+    FillRanges fr{};
+    uint64_t total = 0;
+    for (int j = 0; j < k; j++) {
+        if (ranges[j].count == 0 || !ranges[j].p) continue;
+        if (fr.k == kMaxFillRanges) {  // more than one launch holds
+            launch_fill_multi(ctx, ranges + j, k - j);
+            break;
+        }
+        fr.r[fr.k++] = ranges[j];
+        total += ranges[j].count;
+    }
+    if (fr.k == 0) return;
+    KernelTimer t(ctx, "fill");
+    const uint32_t blocks = (uint32_t)std::min<uint64_t>((total / 4 + 255) / 256 + 1, 2048);
+    fill_multi_kernel<<<blocks, 256, 0, ctx->stream>>>(fr);
+}
+
 
 // Digit layout of a sort by the low `key_bits` bits: ceil(key_bits / 8)
 // passes of equal width (13 bits -> 7 + 6), so every pass has at most 256
@@ -246,10 +288,15 @@ size_t radix_sort_scratch_bytes(uint32_t n, uint32_t key_bits) {
     return (size_t)(4 * kRadix) * 4 + (size_t)digit_plan(key_bits).passes * parts * kRadix * 8;
 }
 
+size_t radix_sort_zeroed_words(uint32_t n, uint32_t key_bits) {
+    const uint64_t parts = div_up(n, sort_part(n));
+    return (size_t)(4 * kRadix) + (size_t)digit_plan(key_bits).passes * parts * kRadix * 2;
+}
+
 bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t* vals_in, uint32_t n,
                            uint32_t key_bits, uint32_t key_sub, uint32_t key_cap, uint32_t* keys_out,
                            uint32_t* vals_out, uint32_t* tmp_keys, uint32_t* tmp_vals, void* scratch,
-                           const char* tag) {
+                           const char* tag, bool scratch_zeroed) {
     const std::string hist_name = std::string(tag) + "_hist", pass_name = std::string(tag) + "_onesweep";
     if (n == 0) return BH_OK;
     if (key_bits > 32) return set_error(ctx, BH_ERR_INVALID_ARG, "radix sort: more than 32 key bits");
@@ -258,8 +305,7 @@ bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t*
     const uint32_t parts = div_up(n, part_size);
     uint32_t* hist = (uint32_t*)scratch;
     uint64_t* status = (uint64_t*)(hist + 4 * kRadix);
-    size_t words = (size_t)(4 * kRadix) + (size_t)plan.passes * parts * kRadix * 2;
-    launch_fill_u32(ctx, hist, 0u, words);
+    if (!scratch_zeroed) launch_fill_u32(ctx, hist, 0u, radix_sort_zeroed_words(n, key_bits));
     {
         KernelTimer t(ctx, hist_name.c_str());
         uint32_t blocks = std::min<uint32_t>(div_up(div_up(n, 4), kThreads * 8), 512);
@@ -367,12 +413,14 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const uint32_t* __restri
 
 size_t scan_scratch_bytes(uint32_t n) { return 64 + (size_t)div_up(n, kPart) * 8; }
 
+size_t scan_zeroed_words(uint32_t n) { return (size_t)div_up(n, kPart) * 2; }
+
 bh_status inclusive_scan(bh_ctx* ctx, const uint32_t* in, const uint32_t* gather, uint32_t* out, uint32_t n,
-                         void* scratch) {
+                         void* scratch, bool status_zeroed) {
     if (n == 0) return BH_OK;
     uint32_t parts = div_up(n, kPart);
     uint64_t* status = (uint64_t*)((char*)scratch + 64);
-    launch_fill_u32(ctx, (uint32_t*)status, 0u, (size_t)parts * 2);
+    if (!status_zeroed) launch_fill_u32(ctx, (uint32_t*)status, 0u, scan_zeroed_words(n));
     KernelTimer t(ctx, "scan");
     scan_kernel<<<parts, kThreads, 0, ctx->stream>>>(in, gather, out, n, status, ctx->d_counters + 1);
     return check_launch(ctx, "scan");
