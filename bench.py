@@ -65,13 +65,17 @@ def algorithmic_bytes(name: str, n: int, v: int, m: int, m_post: int, t: int, p:
     """Compulsory HBM bytes of one launch: every input read once, every output
     written once (counts per launch; sort passes are separate launches)."""
     if name == "project_forward":
-        return 44.0 * n + 12.0 * n                      # transforms+opac in; count, radius, depth key out
+        # transforms+opac in; count, radius, depth key out; the visible
+        # splats' SH rows in and their projected rows (48 B of each 64-B slot) out
+        return 44.0 * n + 12.0 * n + v * (12 * c + 48)
     if name == "project_visible":
-        return v * (4 + 40 + 12 * c + 4) + v * (40 + 4)  # gid, transforms, SH row, opac in; row, depth out
+        # (only without intersections; otherwise map_intersects orders the rows)
+        return v * (4 + 48) + v * (40 + 4)               # gid + row slot in; ordered row, depth out
     if name == "scan":
         return 12.0 * v                                  # gid + gathered count in, cum out
     if name == "map_intersects":
-        return 24.0 * v + 8.0 * v + 8.0 * m              # x,y,conic,opac + cum in; (tile, id) pairs out
+        # gid + global-id row slot + cum in; ordered row + depth out; (tile, id) pairs out
+        return (4.0 + 48.0 + 8.0) * v + 44.0 * v + 8.0 * m
     if name == "tile_offsets":
         return 4.0 * m + 8.0 * t
     if name == "rasterize":

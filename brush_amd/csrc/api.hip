@@ -388,6 +388,7 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
     // which covers the key range found later), the scan's status (sized for
     // N >= V), and both tile-offset arrays (empty tiles stay [0, 0]).
     char *depth_scr = nullptr, *scan_scr = nullptr;
+    float* vis_rows = nullptr;
     if (num_splats) {
         BH_STRY(ws.get(&depth_scr, radix_sort_scratch_bytes(num_splats, 32)));
         BH_STRY(ws.get(&scan_scr, scan_scratch_bytes(num_splats)));
@@ -407,8 +408,9 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
         uint32_t *depth_keys, *partials;
         BH_STRY(ws.get(&depth_keys, num_splats));
         BH_STRY(ws.get((char**)&partials, project_partials_bytes(num_splats)));
-        launch_project_forward(ctx, u, transforms, raw_opacities, num_splats, mip, tile_h, counts, max_radius, depth_keys,
-                               partials, ctx->d_counters);
+        BH_STRY(ws.get(&vis_rows, (size_t)num_splats * 16));
+        launch_project_forward(ctx, u, transforms, raw_opacities, sh_coeffs, sh_degree, num_splats, mip, tile_h, counts,
+                               max_radius, depth_keys, vis_rows, partials, ctx->d_counters);
         BH_STRY(check_launch(ctx, "project_forward"));
         BH_STRY(hip_check(ctx, hipMemcpyAsync(ctx->h_counters, ctx->d_counters, 24, hipMemcpyDeviceToHost, ctx->stream),
                           "count readback"));
@@ -444,8 +446,8 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
     BH_STRY(sget((void**)&cgids, (size_t)std::max<uint32_t>(m, 1) * 4));
     if (num_visible) {
         BH_STRY(inclusive_scan(ctx, counts, gfc, cum, num_visible, scan_scr, true));
-        launch_project_visible(ctx, u, transforms, sh_coeffs, raw_opacities, gfc, num_visible, sh_degree, mip,
-                               projected, depths);
+        // with intersections, map_intersects orders the rows as it reads them
+        if (num_isect == 0) launch_project_visible(ctx, vis_rows, gfc, num_visible, num_splats, projected, depths);
         BH_STRY(check_launch(ctx, "project_visible"));
     } else {
         launch_fill_u32(ctx, (uint32_t*)projected, 0u, 10);
@@ -457,7 +459,8 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
         BH_STRY(ws.get(&uc, m));
         BH_STRY(ws.get(&tk, m));
         BH_STRY(ws.get(&tv, m));
-        launch_map_intersects(ctx, u.tile_bw, u.tile_bh, tile_h, projected, cum, num_visible, ut, uc);
+        launch_map_intersects(ctx, u.tile_bw, u.tile_bh, tile_h, vis_rows, gfc, num_splats, cum, num_visible, projected,
+                              depths, ut, uc);
         BH_STRY(check_launch(ctx, "map_intersects"));
         // tile sort over bits(num_tiles) bits (render.rs:392-395)
         const uint32_t bits = bit_length(num_tiles);

@@ -143,14 +143,19 @@ bh_status inclusive_scan(bh_ctx* ctx, const uint32_t* in, const uint32_t* gather
 
 // project.hip
 size_t project_partials_bytes(uint32_t n);
+// Also writes each visible splat's projected row into rows [n, 16] (its
+// global-id slot), for launch_project_visible to order by depth.
 void launch_project_forward(bh_ctx* ctx, const bh_project_uniforms& u, const float* transforms,
-                            const float* raw_opac, uint32_t n, bool mip, uint32_t tile_h, uint32_t* intersect_counts,
-                            float* max_radius, uint32_t* depth_keys, uint32_t* partials, uint32_t* counters);
-void launch_project_visible(bh_ctx* ctx, const bh_project_uniforms& u, const float* transforms, const float* sh,
-                            const float* raw_opac, const uint32_t* gfc, uint32_t num_visible, uint32_t sh_degree,
-                            bool mip, float* projected, float* depths);
-void launch_map_intersects(bh_ctx* ctx, uint32_t tile_bw, uint32_t tile_bh, uint32_t tile_h, const float* projected,
-                           const uint32_t* cum, uint32_t num_visible, uint32_t* tile_ids, uint32_t* cgids);
+                            const float* raw_opac, const float* sh, uint32_t sh_degree, uint32_t n, bool mip,
+                            uint32_t tile_h, uint32_t* intersect_counts, float* max_radius, uint32_t* depth_keys,
+                            float* rows, uint32_t* partials, uint32_t* counters);
+void launch_project_visible(bh_ctx* ctx, const float* rows, const uint32_t* gfc, uint32_t num_visible,
+                            uint32_t num_splats, float* projected, float* depths);
+// Also writes compact rows `projected` [V,10] and `depths` [V] from the
+// global-id rows of launch_project_forward.
+void launch_map_intersects(bh_ctx* ctx, uint32_t tile_bw, uint32_t tile_bh, uint32_t tile_h, const float* rows,
+                           const uint32_t* gfc, uint32_t num_splats, const uint32_t* cum, uint32_t num_visible,
+                           float* projected, float* depths, uint32_t* tile_ids, uint32_t* cgids);
 
 // raster.hip
 void launch_tile_offsets(bh_ctx* ctx, const uint32_t* tile_ids, uint32_t m, uint32_t num_tiles,

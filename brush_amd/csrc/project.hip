@@ -4,7 +4,9 @@
 //                     contributing-tile count, max radius, depth key
 //                     (crates/brush-render/src/kernels/project_forward.rs:20-144)
 //   project_visible   depth-ordered projected rows with SH -> RGB
-//                     (crates/brush-render/src/kernels/project_visible.rs:22-89)
+//                     (crates/brush-render/src/kernels/project_visible.rs:22-89):
+//                     project_forward computes each visible splat's row in
+//                     global-id order, project_gather_kernel orders them
 //   map_intersects    (tile id, compact id) pairs for every contributing tile
 //                     (crates/brush-render/src/kernels/map_gaussians.rs:14-92)
 //
@@ -31,6 +33,7 @@ struct Projected {
     TileBox bb;
     float radius;
     float depth;
+    float opac;
 };
 
 template <bool MIP, int CAM, int TH>
@@ -65,6 +68,7 @@ __device__ bool project_cull(const bh_project_uniforms& u, const float* t, float
     o.bb = tile_bbox<TH>(m, e, u.tile_bw, u.tile_bh);
     o.radius = bh_maxf(e.x / wf, e.y / hf);
     o.depth = mean_c.z;
+    o.opac = opac;
     return true;
 }
 
@@ -84,13 +88,59 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     return v;
 }
 
-template <bool MIP, int CAM, int TH>
+template <int NC>
+__device__ __forceinline__ void load_sh_row(const float* __restrict__ sh, uint32_t gid, float* c) {
+    const float* row = sh + (size_t)gid * (3 * NC);
+    if ((3 * NC) % 4 == 0) {
+        const float4* r4 = reinterpret_cast<const float4*>(row);
+#pragma unroll
+        for (int i = 0; i < (3 * NC) / 4; i++) {
+            float4 q = r4[i];
+            c[4 * i] = q.x;
+            c[4 * i + 1] = q.y;
+            c[4 * i + 2] = q.z;
+            c[4 * i + 3] = q.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 3 * NC; i++) c[i] = row[i];
+    }
+}
+
+// A visible splat's projected row (project_visible.rs:22-89) in its global-id
+// slot: 16 floats, x y c00 c01 | c11 opac r g | b depth - - | - - - -.
+// project_forward reads the parameters and SH rows in global-id order
+// (coalesced), so the depth-ordered rows cost one aligned 64-byte gather each
+// (project_gather_kernel) instead of three scattered parameter reads.
+template <int DEG>
+__device__ __forceinline__ void write_visible_row(const bh_project_uniforms& u, const float* __restrict__ sh,
+                                                  uint32_t gid, V3 mean, const Projected& p,
+                                                  float4* __restrict__ rows) {
+    constexpr int NC = (DEG + 1) * (DEG + 1);
+    float coeffs[3 * NC];
+    load_sh_row<NC>(sh, gid, coeffs);
+    V3 v = mean - v3(u.camera_pos[0], u.camera_pos[1], u.camera_pos[2]);
+    v = v * (1.0f / sqrtf(dot(v, v)));
+    V3 raw = sh_to_color<DEG>(coeffs, v);
+    const float cr = raw.x + 0.5f, cg = raw.y + 0.5f, cb = raw.z + 0.5f;
+    const float r = bh_clampf(bh_is_finite(cr) ? cr : 0.0f, -100.0f, 100.0f);
+    const float g = bh_clampf(bh_is_finite(cg) ? cg : 0.0f, -100.0f, 100.0f);
+    const float b = bh_clampf(bh_is_finite(cb) ? cb : 0.0f, -100.0f, 100.0f);
+    float4* dst = rows + (size_t)gid * 4;
+    dst[0] = make_float4(p.m.x, p.m.y, p.conic.c00, p.conic.c01);
+    dst[1] = make_float4(p.conic.c11, p.opac, r, g);
+    dst[2] = make_float4(b, p.depth, 0.0f, 0.0f);
+}
+
+template <bool MIP, int CAM, int TH, int DEG>
 __global__ __launch_bounds__(256) void project_forward_kernel(bh_project_uniforms u,
                                                                const float* __restrict__ transforms,
-                                                               const float* __restrict__ raw_opac, uint32_t n,
+                                                               const float* __restrict__ raw_opac,
+                                                               const float* __restrict__ sh, uint32_t n,
                                                                uint32_t* __restrict__ counts,
                                                                float* __restrict__ max_radius,
                                                                uint32_t* __restrict__ depth_keys,
+                                                               float4* __restrict__ rows,
                                                                uint32_t* __restrict__ partials) {
     __shared__ uint32_t s_vis[4], s_kmin[4], s_kmax[4];
     __shared__ unsigned long long s_hits[4];
@@ -99,7 +149,7 @@ __global__ __launch_bounds__(256) void project_forward_kernel(bh_project_uniform
     const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     bool vis = false;
-    Projected p{v2(0.0f, 0.0f), S2{0.0f, 0.0f, 0.0f}, 0.0f, TileBox{0u, 0u, 0u, 0u}, 0.0f, 0.0f};
+    Projected p{v2(0.0f, 0.0f), S2{0.0f, 0.0f, 0.0f}, 0.0f, TileBox{0u, 0u, 0u, 0u}, 0.0f, 0.0f, 0.0f};
     if (gid < n) {
         const float2* row = reinterpret_cast<const float2*>(transforms + (size_t)gid * 10);
         float t[10];
@@ -110,6 +160,7 @@ __global__ __launch_bounds__(256) void project_forward_kernel(bh_project_uniform
             t[2 * i + 1] = q.y;
         }
         vis = project_cull<MIP, CAM, TH>(u, t, raw_opac[gid], p);
+        if (vis) write_visible_row<DEG>(u, sh, gid, v3(t[0], t[1], t[2]), p, rows);
     }
     // count_contributing_tiles (project_forward.rs:120-128) for the whole wave
     const uint32_t hits = wave_tile_walk<false, TH>(lane, vis ? bbox_items(p.bb) : 0u, p.m, p.conic, p.pt, p.bb,
@@ -194,14 +245,14 @@ __global__ __launch_bounds__(1024) void project_reduce_kernel(const uint32_t* __
 
 size_t project_partials_bytes(uint32_t n) { return (size_t)div_up(n, 256) * 8 * sizeof(uint32_t); }
 
-template <bool MIP, int TH>
+template <bool MIP, int TH, int DEG>
 static void launch_pf(bh_ctx* ctx, uint32_t blocks, const bh_project_uniforms& u, const float* transforms,
-                      const float* raw_opac, uint32_t n, uint32_t* intersect_counts, float* max_radius,
-                      uint32_t* depth_keys, uint32_t* partials) {
-#define BH_PF(C)                                                                                      \
-    project_forward_kernel<MIP, C, TH><<<blocks, 256, 0, ctx->stream>>>(u, transforms, raw_opac, n,    \
-                                                                        intersect_counts, max_radius, \
-                                                                        depth_keys, partials)
+                      const float* raw_opac, const float* sh, uint32_t n, uint32_t* intersect_counts,
+                      float* max_radius, uint32_t* depth_keys, float4* rows, uint32_t* partials) {
+#define BH_PF(C)                                                                                             \
+    project_forward_kernel<MIP, C, TH, DEG><<<blocks, 256, 0, ctx->stream>>>(u, transforms, raw_opac, sh, n, \
+                                                                             intersect_counts, max_radius,   \
+                                                                             depth_keys, rows, partials)
     switch (u.camera_model) {
         case kCamKB4: BH_PF(kCamKB4); break;
         case kCamRT8: BH_PF(kCamRT8); break;
@@ -211,21 +262,42 @@ static void launch_pf(bh_ctx* ctx, uint32_t blocks, const bh_project_uniforms& u
 #undef BH_PF
 }
 
+template <int DEG>
+static void launch_pf_deg(bh_ctx* ctx, uint32_t blocks, const bh_project_uniforms& u, const float* transforms,
+                          const float* raw_opac, const float* sh, uint32_t n, bool mip, uint32_t tile_h,
+                          uint32_t* intersect_counts, float* max_radius, uint32_t* depth_keys, float4* rows,
+                          uint32_t* partials) {
+#define BH_PFM(M, T)                                                                                               \
+    launch_pf<M, T, DEG>(ctx, blocks, u, transforms, raw_opac, sh, n, intersect_counts, max_radius, depth_keys, rows, \
+                         partials)
+    if (tile_h == 8) {
+        if (mip) BH_PFM(true, 8); else BH_PFM(false, 8);
+    } else {
+        if (mip) BH_PFM(true, 16); else BH_PFM(false, 16);
+    }
+#undef BH_PFM
+}
+
 void launch_project_forward(bh_ctx* ctx, const bh_project_uniforms& u, const float* transforms,
-                            const float* raw_opac, uint32_t n, bool mip, uint32_t tile_h, uint32_t* intersect_counts,
-                            float* max_radius, uint32_t* depth_keys, uint32_t* partials, uint32_t* counters) {
+                            const float* raw_opac, const float* sh, uint32_t sh_degree, uint32_t n, bool mip,
+                            uint32_t tile_h, uint32_t* intersect_counts, float* max_radius, uint32_t* depth_keys,
+                            float* rows, uint32_t* partials, uint32_t* counters) {
     if (n == 0) return;
     uint32_t blocks = div_up(n, 256);
     {
         KernelTimer t(ctx, "project_forward");
-#define BH_PFM(M, T) \
-    launch_pf<M, T>(ctx, blocks, u, transforms, raw_opac, n, intersect_counts, max_radius, depth_keys, partials)
-        if (tile_h == 8) {
-            if (mip) BH_PFM(true, 8); else BH_PFM(false, 8);
-        } else {
-            if (mip) BH_PFM(true, 16); else BH_PFM(false, 16);
+        float4* r4 = reinterpret_cast<float4*>(rows);
+#define BH_PFD(D) \
+    launch_pf_deg<D>(ctx, blocks, u, transforms, raw_opac, sh, n, mip, tile_h, intersect_counts, max_radius, depth_keys, \
+                     r4, partials)
+        switch (sh_degree) {
+            case 0: BH_PFD(0); break;
+            case 1: BH_PFD(1); break;
+            case 2: BH_PFD(2); break;
+            case 3: BH_PFD(3); break;
+            default: BH_PFD(4); break;
         }
-#undef BH_PFM
+#undef BH_PFD
     }
     KernelTimer t(ctx, "project_reduce");
     project_reduce_kernel<<<1, 1024, 0, ctx->stream>>>(partials, blocks, counters);
@@ -233,126 +305,48 @@ void launch_project_forward(bh_ctx* ctx, const bh_project_uniforms& u, const flo
 
 // ---- project_visible ------------------------------------------------------------
 
-template <int NC>
-__device__ __forceinline__ void load_sh_row(const float* __restrict__ sh, uint32_t gid, float* c) {
-    const float* row = sh + (size_t)gid * (3 * NC);
-    if ((3 * NC) % 4 == 0) {
-        const float4* r4 = reinterpret_cast<const float4*>(row);
-#pragma unroll
-        for (int i = 0; i < (3 * NC) / 4; i++) {
-            float4 q = r4[i];
-            c[4 * i] = q.x;
-            c[4 * i + 1] = q.y;
-            c[4 * i + 2] = q.z;
-            c[4 * i + 3] = q.w;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 3 * NC; i++) c[i] = row[i];
-    }
-}
-
-template <int DEG, bool MIP, int CAM>
-__global__ __launch_bounds__(256) void project_visible_kernel(bh_project_uniforms u,
-                                                               const float* __restrict__ transforms,
-                                                               const float* __restrict__ sh,
-                                                               const float* __restrict__ raw_opac,
-                                                               const uint32_t* __restrict__ gfc, uint32_t num_visible,
-                                                               uint32_t num_splats, float* __restrict__ projected,
-                                                               float* __restrict__ depths) {
-    constexpr int NC = (DEG + 1) * (DEG + 1);
+// The depth-ordered projected rows and depths: compact id c takes the row
+// project_forward wrote in the slot of global id gfc[c].  map_intersects does
+// this itself; this kernel serves forwards with visible splats but no
+// intersections.
+__global__ __launch_bounds__(256) void project_gather_kernel(const float4* __restrict__ rows,
+                                                              const uint32_t* __restrict__ gfc, uint32_t num_visible,
+                                                              uint32_t num_splats, float* __restrict__ projected,
+                                                              float* __restrict__ depths) {
     const uint32_t c = blockIdx.x * 256u + threadIdx.x;
     if (c >= num_visible) return;
     const uint32_t gid = min(gfc[c], num_splats - 1u);
-    const float2* row = reinterpret_cast<const float2*>(transforms + (size_t)gid * 10);
-    float t[10];
-#pragma unroll
-    for (int i = 0; i < 5; i++) {
-        float2 p = row[i];
-        t[2 * i] = p.x;
-        t[2 * i + 1] = p.y;
-    }
-    float coeffs[3 * NC];
-    load_sh_row<NC>(sh, gid, coeffs);
-    V3 mean = v3(t[0], t[1], t[2]);
-    V3 sc = v3(bh_expf(t[7]), bh_expf(t[8]), bh_expf(t[9]));
-    Q4 q = qnormalize(Q4{t[3], t[4], t[5], t[6]});
-    V3 mean_c = world_to_cam(u, mean);
-    S2 raw_cov = calc_cov2d<CAM>(u, sc, q, mean_c);
-    float comp;
-    S2 cov = compensate_cov2d<MIP>(raw_cov, comp);
-    float opac = bh_sigmoidf(raw_opac[gid]) * comp;
-    S2 conic = inverse(cov);
-    V2 m = project_point<CAM>(u, mean_c);
-    V3 v = mean - v3(u.camera_pos[0], u.camera_pos[1], u.camera_pos[2]);
-    v = v * (1.0f / sqrtf(dot(v, v)));
-    V3 raw = sh_to_color<DEG>(coeffs, v);
-    float cr = raw.x + 0.5f, cg = raw.y + 0.5f, cb = raw.z + 0.5f;
-    float out[10];
-    out[0] = m.x;
-    out[1] = m.y;
-    out[2] = conic.c00;
-    out[3] = conic.c01;
-    out[4] = conic.c11;
-    out[5] = opac;
-    out[6] = bh_clampf(bh_is_finite(cr) ? cr : 0.0f, -100.0f, 100.0f);
-    out[7] = bh_clampf(bh_is_finite(cg) ? cg : 0.0f, -100.0f, 100.0f);
-    out[8] = bh_clampf(bh_is_finite(cb) ? cb : 0.0f, -100.0f, 100.0f);
-    out[9] = mean_c.z;
+    const float4* r = rows + (size_t)gid * 4;
+    const float4 a = r[0], b = r[1], d = r[2];
     float2* dst = reinterpret_cast<float2*>(projected + (size_t)c * 10);
-#pragma unroll
-    for (int i = 0; i < 5; i++) dst[i] = make_float2(out[2 * i], out[2 * i + 1]);
-    depths[c] = mean_c.z;
+    dst[0] = make_float2(a.x, a.y);
+    dst[1] = make_float2(a.z, a.w);
+    dst[2] = make_float2(b.x, b.y);
+    dst[3] = make_float2(b.z, b.w);
+    dst[4] = make_float2(d.x, d.y);
+    depths[c] = d.y;
 }
 
-template <int DEG, bool MIP>
-static void launch_pv_cam(bh_ctx* ctx, uint32_t blocks, const bh_project_uniforms& u, const float* transforms,
-                          const float* sh, const float* raw_opac, const uint32_t* gfc, uint32_t num_visible,
-                          float* projected, float* depths) {
-#define BH_PV(C)                                                                                              \
-    project_visible_kernel<DEG, MIP, C><<<blocks, 256, 0, ctx->stream>>>(u, transforms, sh, raw_opac, gfc,     \
-                                                                         num_visible, u.total_splats, projected, \
-                                                                         depths)
-    switch (u.camera_model) {
-        case kCamKB4: BH_PV(kCamKB4); break;
-        case kCamRT8: BH_PV(kCamRT8); break;
-        case kCamTPF: BH_PV(kCamTPF); break;
-        default: BH_PV(kCamPinhole); break;
-    }
-#undef BH_PV
-}
-
-template <int DEG>
-static void launch_pv(bh_ctx* ctx, bool mip, uint32_t blocks, const bh_project_uniforms& u, const float* transforms,
-                      const float* sh, const float* raw_opac, const uint32_t* gfc, uint32_t num_visible,
-                      float* projected, float* depths) {
-    if (mip)
-        launch_pv_cam<DEG, true>(ctx, blocks, u, transforms, sh, raw_opac, gfc, num_visible, projected, depths);
-    else
-        launch_pv_cam<DEG, false>(ctx, blocks, u, transforms, sh, raw_opac, gfc, num_visible, projected, depths);
-}
-
-void launch_project_visible(bh_ctx* ctx, const bh_project_uniforms& u, const float* transforms, const float* sh,
-                            const float* raw_opac, const uint32_t* gfc, uint32_t num_visible, uint32_t sh_degree,
-                            bool mip, float* projected, float* depths) {
+void launch_project_visible(bh_ctx* ctx, const float* rows, const uint32_t* gfc, uint32_t num_visible,
+                            uint32_t num_splats, float* projected, float* depths) {
     if (num_visible == 0) return;
     KernelTimer t(ctx, "project_visible");
-    uint32_t blocks = div_up(num_visible, 256);
-    switch (sh_degree) {
-        case 0: launch_pv<0>(ctx, mip, blocks, u, transforms, sh, raw_opac, gfc, num_visible, projected, depths); break;
-        case 1: launch_pv<1>(ctx, mip, blocks, u, transforms, sh, raw_opac, gfc, num_visible, projected, depths); break;
-        case 2: launch_pv<2>(ctx, mip, blocks, u, transforms, sh, raw_opac, gfc, num_visible, projected, depths); break;
-        case 3: launch_pv<3>(ctx, mip, blocks, u, transforms, sh, raw_opac, gfc, num_visible, projected, depths); break;
-        default: launch_pv<4>(ctx, mip, blocks, u, transforms, sh, raw_opac, gfc, num_visible, projected, depths); break;
-    }
+    project_gather_kernel<<<div_up(num_visible, 256), 256, 0, ctx->stream>>>(
+        reinterpret_cast<const float4*>(rows), gfc, num_visible, num_splats, projected, depths);
 }
 
 // ---- map_intersects ----------------------------------------------------------------
 
+// Each lane takes its splat's row from the global-id slot project_forward
+// filled (gfc[c]), stores it as compact row c of `projected` (with its
+// depth), and walks its tiles with it.
 template <int TH>
 __global__ __launch_bounds__(256) void map_intersects_kernel(uint32_t tile_bw, uint32_t tile_bh,
-                                                              const float* __restrict__ projected,
+                                                              const float4* __restrict__ rows,
+                                                              const uint32_t* __restrict__ gfc, uint32_t num_splats,
                                                               const uint32_t* __restrict__ cum, uint32_t num_visible,
+                                                              float* __restrict__ projected,
+                                                              float* __restrict__ depths,
                                                               uint32_t* __restrict__ tile_ids,
                                                               uint32_t* __restrict__ cgids) {
     __shared__ WalkRec s_rec[4][64];
@@ -368,11 +362,18 @@ __global__ __launch_bounds__(256) void map_intersects_kernel(uint32_t tile_bw, u
     TileBox bb{0u, 0u, 0u, 0u};
     uint32_t base = 0, budget = 0;
     if (active) {
-        const float2* row = reinterpret_cast<const float2*>(projected + (size_t)c * 10);
-        float2 p0 = row[0], p1 = row[1], p2 = row[2];
-        m = v2(p0.x, p0.y);
-        conic = S2{p1.x, p1.y, p2.x};
-        pt = bh_logf(p2.y * 255.0f);
+        const float4* r = rows + (size_t)min(gfc[c], num_splats - 1u) * 4;
+        const float4 a = r[0], b = r[1], d = r[2];
+        float2* dst = reinterpret_cast<float2*>(projected + (size_t)c * 10);
+        dst[0] = make_float2(a.x, a.y);
+        dst[1] = make_float2(a.z, a.w);
+        dst[2] = make_float2(b.x, b.y);
+        dst[3] = make_float2(b.z, b.w);
+        dst[4] = make_float2(d.x, d.y);
+        depths[c] = d.y;
+        m = v2(a.x, a.y);
+        conic = S2{a.z, a.w, b.x};
+        pt = bh_logf(b.y * 255.0f);
         bb = tile_bbox<TH>(m, bbox_extent(conic, pt), tile_bw, tile_bh);
         base = c == 0 ? 0u : cum[c - 1];
         budget = cum[c] - base;
@@ -406,17 +407,19 @@ __global__ __launch_bounds__(256) void map_intersects_kernel(uint32_t tile_bw, u
     }
 }
 
-void launch_map_intersects(bh_ctx* ctx, uint32_t tile_bw, uint32_t tile_bh, uint32_t tile_h, const float* projected,
-                           const uint32_t* cum, uint32_t num_visible, uint32_t* tile_ids, uint32_t* cgids) {
+void launch_map_intersects(bh_ctx* ctx, uint32_t tile_bw, uint32_t tile_bh, uint32_t tile_h, const float* rows,
+                           const uint32_t* gfc, uint32_t num_splats, const uint32_t* cum, uint32_t num_visible,
+                           float* projected, float* depths, uint32_t* tile_ids, uint32_t* cgids) {
     if (num_visible == 0) return;
     KernelTimer t(ctx, "map_intersects");
     const uint32_t blocks = div_up(num_visible, 256);
+    const float4* r4 = reinterpret_cast<const float4*>(rows);
     if (tile_h == 8)
-        map_intersects_kernel<8><<<blocks, 256, 0, ctx->stream>>>(tile_bw, tile_bh, projected, cum, num_visible,
-                                                                 tile_ids, cgids);
+        map_intersects_kernel<8><<<blocks, 256, 0, ctx->stream>>>(tile_bw, tile_bh, r4, gfc, num_splats, cum,
+                                                                 num_visible, projected, depths, tile_ids, cgids);
     else
-        map_intersects_kernel<16><<<blocks, 256, 0, ctx->stream>>>(tile_bw, tile_bh, projected, cum, num_visible,
-                                                                  tile_ids, cgids);
+        map_intersects_kernel<16><<<blocks, 256, 0, ctx->stream>>>(tile_bw, tile_bh, r4, gfc, num_splats, cum,
+                                                                  num_visible, projected, depths, tile_ids, cgids);
 }
 
 }  // namespace bh
