@@ -78,7 +78,9 @@ KernelTimer::KernelTimer(bh_ctx* c, const char* n) : ctx(c), name(n) {
         if (!ctx->event_cache.empty()) {
             e = ctx->event_cache.back();
             ctx->event_cache.pop_back();
-        } else if (hipEventCreate(&e) != hipSuccess) {
+        } else if (hipEventCreateWithFlags(&e, hipEventDisableSystemFence) != hipSuccess) {
+            // timing-only events: no system-scope fence (cache writeback and
+            // invalidate) that would slow the kernels after the timed one
             e = nullptr;
         }
         return e;
