@@ -111,14 +111,12 @@ __device__ __forceinline__ void load_sh_row(const float* __restrict__ sh, uint32
 // slot: 16 floats, x y c00 c01 | c11 opac r g | b depth - - | - - - -.
 // project_forward reads the parameters and SH rows in global-id order
 // (coalesced), so the depth-ordered rows cost one aligned 64-byte gather each
-// (project_gather_kernel) instead of three scattered parameter reads.
+// (in map_intersects) instead of three scattered parameter reads.  The SH row
+// is loaded before the tile walk and used after it, so the walk hides the
+// load latency.
 template <int DEG>
-__device__ __forceinline__ void write_visible_row(const bh_project_uniforms& u, const float* __restrict__ sh,
-                                                  uint32_t gid, V3 mean, const Projected& p,
-                                                  float4* __restrict__ rows) {
-    constexpr int NC = (DEG + 1) * (DEG + 1);
-    float coeffs[3 * NC];
-    load_sh_row<NC>(sh, gid, coeffs);
+__device__ __forceinline__ void write_row_from_coeffs(const bh_project_uniforms& u, const float* coeffs, uint32_t gid,
+                                                      V3 mean, const Projected& p, float4* __restrict__ rows) {
     V3 v = mean - v3(u.camera_pos[0], u.camera_pos[1], u.camera_pos[2]);
     v = v * (1.0f / sqrtf(dot(v, v)));
     V3 raw = sh_to_color<DEG>(coeffs, v);
@@ -149,6 +147,7 @@ __global__ __launch_bounds__(256) void project_forward_kernel(bh_project_uniform
     const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     bool vis = false;
+    V3 mean = v3(0.0f, 0.0f, 0.0f);
     Projected p{v2(0.0f, 0.0f), S2{0.0f, 0.0f, 0.0f}, 0.0f, TileBox{0u, 0u, 0u, 0u}, 0.0f, 0.0f, 0.0f};
     if (gid < n) {
         const float2* row = reinterpret_cast<const float2*>(transforms + (size_t)gid * 10);
@@ -160,8 +159,11 @@ __global__ __launch_bounds__(256) void project_forward_kernel(bh_project_uniform
             t[2 * i + 1] = q.y;
         }
         vis = project_cull<MIP, CAM, TH>(u, t, raw_opac[gid], p);
-        if (vis) write_visible_row<DEG>(u, sh, gid, v3(t[0], t[1], t[2]), p, rows);
+        mean = v3(t[0], t[1], t[2]);
     }
+    constexpr int NC = (DEG + 1) * (DEG + 1);
+    float coeffs[3 * NC];
+    if (vis) load_sh_row<NC>(sh, gid, coeffs);
     // count_contributing_tiles (project_forward.rs:120-128) for the whole wave
     const uint32_t hits = wave_tile_walk<false, TH>(lane, vis ? bbox_items(p.bb) : 0u, p.m, p.conic, p.pt, p.bb,
                                                 s_rec[wave], s_slot[wave], s_count[wave], u.tile_bw, 0u, 0u, 0u,
@@ -171,6 +173,7 @@ __global__ __launch_bounds__(256) void project_forward_kernel(bh_project_uniform
         max_radius[gid] = vis ? p.radius : 0.0f;
         depth_keys[gid] = vis ? bh_as_uint(p.depth) : 0xFFFFFFFFu;
     }
+    if (vis) write_row_from_coeffs<DEG>(u, coeffs, gid, mean, p, rows);
     // per-block totals (no same-address atomics): wave shuffles, then LDS
     uint64_t vmask = __ballot(vis);
     uint64_t hsum = wave_sum_u64(vis ? (uint64_t)hits : 0ull);
