@@ -24,8 +24,20 @@ namespace bh {
 
 static const size_t kAlign = 256;
 
-hipError_t Pool::alloc(void** out, size_t bytes) {
+// Requests above 1 MiB are rounded up to a size class of 1/8 of their power
+// of two (at most 12.5 % over), so a buffer whose size creeps up from call to
+// call (the intersection count of a scene that is being trained) keeps
+// reusing one block instead of missing the cache and allocating every call.
+static size_t size_class(size_t bytes) {
     bytes = std::max<size_t>(kAlign, (bytes + kAlign - 1) / kAlign * kAlign);
+    if (bytes <= ((size_t)1 << 20)) return bytes;
+    size_t top = (size_t)1 << (63 - __builtin_clzll((unsigned long long)bytes));
+    const size_t step = top / 8;
+    return (bytes + step - 1) / step * step;
+}
+
+hipError_t Pool::alloc(void** out, size_t bytes) {
+    bytes = size_class(bytes);
     size_t best = (size_t)-1;
     for (size_t i = 0; i < free_blocks.size(); i++) {
         const Block& b = free_blocks[i];

@@ -383,3 +383,28 @@ def test_needle_splats_strip_culling(gpu, flags):
     vc_gpu = _gpu_backward(g, v_out, (flags & 2) | 16, (0.0, 0.0, 0.0), tr, sh, opac).cpu().numpy()
     vc_ref = O.rasterize_backward(o, v_out, (flags & 2) | 16)
     rel_close("v_combined", vc_gpu[: o.num_visible], vc_ref[: o.num_visible], rtol=1e-3, atol_frac=1e-5)
+
+
+def test_workspace_stops_growing_when_sizes_creep(gpu):
+    """A scene that grows a little from call to call (as a trained scene's
+    intersection count does) reuses the library's cached workspace: after
+    the first calls, the pool holds no more memory than it did."""
+    import torch
+    from brush_amd import _lib
+    from brush_amd import render as R
+    from brush_amd.camera import Camera
+
+    tr, sh, op = random_scene(9090, 60000, 1, log_scale=(-3.0, 0.5))
+    cam = Camera.from_focal((0.0, 0.0, -3.0), (0.0, 0.0, 0.0, 1.0), 300.0, 256, 256)
+    sizes = []
+    for k in range(12):
+        n = 50000 + 500 * k  # more splats, more intersections, every call
+        t = torch.from_numpy(tr[:n].copy()).to(gpu)
+        s = torch.from_numpy(sh[:n].copy()).to(gpu)
+        o = torch.from_numpy(op[:n].copy()).to(gpu)
+        out = R.render(cam, (256, 256), t, s, o, raster_pass=R.RasterPass.Backward)
+        out.state.release()
+        torch.cuda.synchronize()
+        sizes.append(_lib.context(0).workspace_bytes())
+    print(f"[case] workspace bytes per call {sizes}", flush=True)
+    assert sizes[-1] <= sizes[4], sizes
