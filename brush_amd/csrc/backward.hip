@@ -78,8 +78,8 @@ __global__ __launch_bounds__(64) void rasterize_backward_kernel(
     const uint32_t* __restrict__ row_of, float* __restrict__ v_combined) {
     constexpr uint32_t CH = DEPTH ? 5u : 4u;
     __shared__ float4 s_xyco[64];  // x, y, conic c00, c01
-    __shared__ float4 s_crgb[64];  // conic c11, opacity, r, g
-    __shared__ float4 s_bd[64];    // b, depth, sigma cutoff
+    __shared__ float4 s_crgb[64];  // conic c11, opacity, r, g (staged_colour)
+    __shared__ float4 s_bd[64];    // b (staged_colour), depth, sigma cutoff
     __shared__ uint32_t s_cid[64];
 
     uint32_t tile, blk;
@@ -130,8 +130,8 @@ __global__ __launch_bounds__(64) void rasterize_backward_kernel(
             const float2 r0 = prow[0], r1 = prow[1], r2 = prow[2], r3 = prow[3], r4 = prow[4];
             const float cut = sigma_cutoff<SMOOTH>(r2.y);
             s_xyco[lane] = make_float4(r0.x, r0.y, r1.x, r1.y);
-            s_crgb[lane] = make_float4(r2.x, r2.y, r3.x, r3.y);
-            s_bd[lane] = make_float4(r4.x, r4.y, cut, 0.0f);
+            s_crgb[lane] = make_float4(r2.x, r2.y, staged_colour(r3.x), staged_colour(r3.y));
+            s_bd[lane] = make_float4(staged_colour(r4.x), r4.y, cut, 0.0f);
             s_cid[lane] = row_of ? row_of[c] : c;
             touch = may_touch_rect(r0.x, r0.y, S2{r1.x, r1.y, r2.x}, cut, bx0, by0, bx0 + 7.0f, by0 + 7.0f);
         }
@@ -155,7 +155,7 @@ __global__ __launch_bounds__(64) void rasterize_backward_kernel(
             const float alpha = bh_minf(0.999f, opac * gaussian);
             const float w = SMOOTH ? cutoff_weight(alpha) : (alpha >= kCutMid ? 1.0f : 0.0f);
             const bool pass = maybe && w > 0.0f;
-            const float ae = alpha * w;
+            const float ae = SMOOTH ? alpha * w : (alpha >= kCutMid ? alpha : 0.0f);
             const float next_t = sw * (1.0f - ae);
             const bool saturate = pass && next_t <= 1.0e-4f;
             const bool contrib = pass && !saturate;
@@ -165,38 +165,44 @@ __global__ __launch_bounds__(64) void rasterize_backward_kernel(
                 if (!wave_live) break;
                 continue;
             }
-            const float cr = bh_maxf(cr4.z, 0.0f), cgc = bh_maxf(cr4.w, 0.0f), cb = bh_maxf(bd.x, 0.0f);
+            // staged colours: max(c, 0) in value, the c >= 0 gate in the sign bit
+            const float cr = cr4.z, cgc = cr4.w, cb = bd.x;
             const float vis = ae * sw;
             float g[12];
-            g[5] = cr4.z >= 0.0f ? vis * vox : 0.0f;
-            g[6] = cr4.w >= 0.0f ? vis * voy : 0.0f;
-            g[7] = bd.x >= 0.0f ? vis * voz : 0.0f;
+            g[5] = contrib && colour_gate(cr) ? vis * vox : 0.0f;
+            g[6] = contrib && colour_gate(cgc) ? vis * voy : 0.0f;
+            g[7] = contrib && colour_gate(cb) ? vis * voz : 0.0f;
             // gradient-only quantities: hardware reciprocal / sqrt (1 ulp)
             const float ra = __builtin_amdgcn_rcpf(1.0f - ae);
             const float dot_rgb = ((sw * cr - sx) * vox + (sw * cgc - sy) * voy + (sw * cb - sz) * voz) * ra;
             const float v_ae = dot_rgb + vow * ra;
-            // with the hard cutoff the weight is a step and its derivative 0
+            // with the hard cutoff the weight is a step and its derivative 0.
+            // The position, conic, opacity and refine lanes are gated on
+            // contributing and unclamped (o G <= 0.999) pairs.  Lanes outside
+            // `maybe` may hold any alpha and gaussian: a sigma far below zero
+            // (rounding on a nearly singular conic) overflows the exponential's
+            // range reduction into inf or a negative value.  So the selects sit
+            // on v_sigma and on the opacity lane; a zero v_sigma then zeroes the
+            // position, conic and refine lanes (up to the sign of a zero), whose
+            // other factors dx, dy and the conic (|c| <= 10: every 2D covariance
+            // carries a blur of at least 0.1 on its diagonal) are finite.
+            const bool unclamped = opac * gaussian <= 0.999f;
+            const bool gate = contrib && unclamped;
             const float v_alpha = SMOOTH ? v_ae * (w + alpha * cutoff_weight_deriv(alpha)) : v_ae * w;
-            const float v_sigma = -alpha * v_alpha;
+            const float v_sigma = gate ? -alpha * v_alpha : 0.0f;
             const float vxy_x = v_sigma * (conic.c00 * dx + conic.c01 * dy);
             const float vxy_y = v_sigma * (conic.c01 * dx + conic.c11 * dy);
-            const bool unclamped = opac * gaussian <= 0.999f;
             g[2] = 0.5f * v_sigma * dx * dx;
             g[3] = v_sigma * dx * dy;
             g[4] = 0.5f * v_sigma * dy * dy;
             g[0] = vxy_x;
             g[1] = vxy_y;
-            g[8] = v_alpha * gaussian;
+            g[8] = gate ? v_alpha * gaussian : 0.0f;
             g[9] = REFINE ? __builtin_amdgcn_sqrtf(vxy_x * img_wf * vxy_x * img_wf + vxy_y * img_hf * vxy_y * img_hf) *
                                 inv_final_a
                           : 0.0f;
-            g[10] = DEPTH ? vis * vod : 0.0f;
+            g[10] = DEPTH && contrib ? vis * vod : 0.0f;
             g[11] = 0.0f;
-#pragma unroll
-            for (int k = 0; k < kNG; k++) {
-                const bool keep = contrib && (k >= 5 ? (k != 9 || unclamped) : unclamped) && (k != 8 || unclamped);
-                g[k] = keep ? g[k] : 0.0f;
-            }
             if (contrib) {
                 sx = sx - vis * cr;
                 sy = sy - vis * cgc;

@@ -440,6 +440,13 @@ BH_DEV float cutoff_weight_deriv(float alpha) {
     return inside ? (6.0f * t - 6.0f * t * t) / kCutBand : 0.0f;
 }
 
+// A colour channel as the blend kernels stage it: negative values become -0
+// and -0 becomes +0, others stay.  Added into a non-negative sum it acts as
+// max(c, 0) bit for bit, and its sign bit is the gradient gate of the
+// reference (v_rgb only where c >= 0, rasterize_backwards.rs:330-338).
+BH_DEV float staged_colour(float c) { return c < 0.0f ? -0.0f : c + 0.0f; }
+BH_DEV bool colour_gate(float staged) { return (bh_as_uint(staged) >> 31) == 0u; }
+
 // Largest sigma at which a splat of opacity `opac` can still pass the alpha
 // cutoff, plus a margin.  For sigma above it, opac * exp(-sigma) rounds below
 // the cutoff (1/255, or the lower edge of the smooth band) with certainty:

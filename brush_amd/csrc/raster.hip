@@ -83,7 +83,7 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
                                                         uint32_t* __restrict__ off_post) {
     __shared__ float4 s_xyco[64];  // x, y, conic c00, conic c01
     __shared__ float4 s_c11a[64];  // conic c11, opacity, sigma cutoff
-    __shared__ float4 s_rgbd[64];  // r, g, b, depth
+    __shared__ float4 s_rgbd[64];  // r, g, b (staged_colour), depth
 
     uint32_t tile, blk;
     raster_block_of_workgroup<TH>(blockIdx.x, tile, blk);
@@ -112,7 +112,7 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
             const float cut = sigma_cutoff<SMOOTH>(cc.y);
             s_xyco[lane] = make_float4(a.x, a.y, b.x, b.y);
             s_c11a[lane] = make_float4(cc.x, cc.y, cut, 0.0f);
-            s_rgbd[lane] = make_float4(d.x, d.y, e.x, e.y);
+            s_rgbd[lane] = make_float4(staged_colour(d.x), staged_colour(d.y), staged_colour(e.x), e.y);
             touch = may_touch_rect(a.x, a.y, S2{b.x, b.y, cc.x}, cut, bx0, by0, bx0 + 7.0f, by0 + 7.0f);
         }
         // splats of the batch that may touch this block, in order
@@ -132,9 +132,10 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
             // selects discard.  0 <= sigma <= cutoff < 6 where it matters, the
             // range in which bh_expf_neg equals bh_expf bit for bit.
             const float alpha = bh_minf(0.999f, ca.y * bh_expf_neg(-sigma));
+            // the hard cutoff's weight is a step: alpha * w is a select
             const float w = SMOOTH ? cutoff_weight(alpha) : (alpha >= kCutMid ? 1.0f : 0.0f);
             const bool pass = maybe && w > 0.0f;
-            const float ae = alpha * w;
+            const float ae = SMOOTH ? alpha * w : (alpha >= kCutMid ? alpha : 0.0f);
             const float next_t = t_acc * (1.0f - ae);
             const bool saturate = pass && next_t <= 1.0e-4f;
             const bool contrib = pass && !saturate;
@@ -142,9 +143,9 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
             if (__ballot(contrib) != 0ull) {
                 const float vis = ae * t_acc;
                 const float4 col = s_rgbd[j];
-                pr = contrib ? pr + bh_maxf(col.x, 0.0f) * vis : pr;
-                pg = contrib ? pg + bh_maxf(col.y, 0.0f) * vis : pg;
-                pb = contrib ? pb + bh_maxf(col.z, 0.0f) * vis : pb;
+                pr = contrib ? pr + col.x * vis : pr;
+                pg = contrib ? pg + col.y * vis : pg;
+                pb = contrib ? pb + col.z * vis : pb;
                 if (DEPTH) pd = contrib ? pd + col.w * vis : pd;
                 t_acc = contrib ? next_t : t_acc;
                 last = contrib ? batch + j + 1u : last;

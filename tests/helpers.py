@@ -64,10 +64,18 @@ def assert_bits_equal(name, a, b):
 
 
 def rel_close(name, got, want, rtol=1e-3, atol_frac=1e-5):
-    """|got - want| <= rtol * |want| + atol, atol = atol_frac * max|want|."""
+    """|got - want| <= rtol * |want| + atol, atol = atol_frac * max|want| over
+    the finite entries; a non-finite entry must match exactly (NaN where NaN,
+    inf of the same sign), so a NaN on either side fails the check."""
     got = np.asarray(got, dtype=np.float64)
     want = np.asarray(want, dtype=np.float64)
     assert got.shape == want.shape, f"{name}: shape {got.shape} vs {want.shape}"
+    gf, wf = np.isfinite(got), np.isfinite(want)
+    odd = np.nonzero(((gf != wf) | (~gf & ~wf & ~((got == want) | (np.isnan(got) & np.isnan(want))))).reshape(-1))[0]
+    assert odd.size == 0, (f"{name}: {odd.size}/{got.size} non-finite mismatches, first at {odd[:3]}: "
+                           f"{got.reshape(-1)[odd[:3]]} vs {want.reshape(-1)[odd[:3]]}")
+    got = np.where(gf, got, 0.0)
+    want = np.where(wf, want, 0.0)
     scale = float(np.max(np.abs(want))) if want.size else 0.0
     atol = atol_frac * scale + 1e-30
     err = np.abs(got - want)
