@@ -98,12 +98,13 @@ def algorithmic_bytes(name: str, n: int, v: int, m: int, m_post: int, t: int, p:
 
 
 def sort_bytes_per_launch(name: str, passes: float, n: int, m: int) -> float:
-    """Algorithmic bytes of one launch of a sort kernel: every onesweep pass reads
+    """Algorithmic bytes of one launch of a sort kernel: every digit pass reads
     and writes (u32 key, u32 value) once; the depth sort's first pass generates
-    its values (global ids) instead of reading them; the histogram reads keys."""
-    if name == "depth_sort_hist":
+    its values (global ids) instead of reading them; each pass's upsweep reads
+    the keys (the offset scan's few counters are not counted)."""
+    if name == "depth_sort_up":
         return 4.0 * n
-    if name == "tile_sort_hist":
+    if name == "tile_sort_up":
         return 4.0 * m
     if name == "depth_sort_onesweep":
         return (16.0 * passes - 4.0) * n / max(passes, 1.0)
@@ -418,7 +419,7 @@ def main():
         for name, (launches, total) in timings.items():
             per_step_launches = launches / steps
             avg = total / max(launches, 1)
-            if name.endswith("_onesweep") or name.endswith("_hist"):
+            if name.endswith(("_onesweep", "_up", "_scan")):
                 b = sort_bytes_per_launch(name, per_step_launches / poses, n, m)
             else:
                 b = algorithmic_bytes(name, n, v, m, m_post, tiles, pixels, c)

@@ -37,7 +37,8 @@ TILE_WIDTH = 16
 EXPORTED = [
     "bh_ctx_create", "bh_ctx_destroy", "bh_ctx_set_stream", "bh_last_error", "bh_ctx_set_timing",
     "bh_ctx_set_timing_filter",
-    "bh_ctx_read_timings", "bh_ctx_reset_timings", "bh_ctx_workspace_bytes", "bh_radix_argsort",
+    "bh_ctx_read_timings", "bh_ctx_reset_timings", "bh_ctx_workspace_bytes", "bh_ctx_release_workspace",
+    "bh_radix_argsort",
     "bh_prefix_sum", "bh_get_tile_offsets", "bh_render_forward", "bh_fwd_state_info",
     "bh_fwd_state_release", "bh_rasterize_backward", "bh_render_backward", "bh_project_backward",
     "bh_image_loss_forward", "bh_image_loss_backward", "bh_adam_scaled_step", "bh_copy_to_host",
@@ -192,6 +193,7 @@ def lib() -> ctypes.CDLL:
         "bh_ctx_read_timings": (S, [P, ctypes.POINTER(KernelTiming), I, ctypes.POINTER(I)]),
         "bh_ctx_reset_timings": (S, [P]),
         "bh_ctx_workspace_bytes": (U64, [P]),
+        "bh_ctx_release_workspace": (S, [P]),
         "bh_radix_argsort": (S, [P, P, P, U32, U32, P, P]),
         "bh_prefix_sum": (S, [P, P, P, U32]),
         "bh_get_tile_offsets": (S, [P, P, U32, U32, P]),
@@ -265,6 +267,10 @@ class Context:
 
     def workspace_bytes(self) -> int:
         return int(lib().bh_ctx_workspace_bytes(self.handle))
+
+    def release_workspace(self) -> None:
+        """Frees the cached workspace blocks no forward state holds."""
+        self.check(lib().bh_ctx_release_workspace(self.handle), "bh_ctx_release_workspace")
 
     def __del__(self):
         try:

@@ -25,9 +25,12 @@ namespace bh {
 static const size_t kAlign = 256;
 
 // Requests above 1 MiB are rounded up to a size class of 1/8 of their power
-// of two (at most 12.5 % over), so a buffer whose size creeps up from call to
-// call (the intersection count of a scene that is being trained) keeps
-// reusing one block instead of missing the cache and allocating every call.
+// of two (at most 12.5 % over), and a request that misses the cache allocates
+// a block with 25 % headroom (the cache serves requests down to half a
+// block's size), so a buffer whose size creeps up from call to call (the
+// intersection count of a scene that is being trained, the per-splat arrays of
+// a scene that densifies) keeps reusing one block instead of missing the cache
+// and allocating every call.
 static size_t size_class(size_t bytes) {
     bytes = std::max<size_t>(kAlign, (bytes + kAlign - 1) / kAlign * kAlign);
     if (bytes <= ((size_t)1 << 20)) return bytes;
@@ -54,15 +57,21 @@ hipError_t Pool::alloc(void** out, size_t bytes) {
         return hipSuccess;
     }
     void* p = nullptr;
-    hipError_t e = hipMalloc(&p, bytes);
+    size_t got = size_class(bytes + bytes / 4);
+    hipError_t e = hipMalloc(&p, got);
     if (e != hipSuccess) {
-        // drop the cache and try once more
+        // drop the cache and try once more, then without headroom
         (void)hipGetLastError();
         trim();
-        e = hipMalloc(&p, bytes);
-        if (e != hipSuccess) return e;
+        e = hipMalloc(&p, got);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            got = bytes;
+            e = hipMalloc(&p, got);
+            if (e != hipSuccess) return e;
+        }
     }
-    live[p] = bytes;
+    live[p] = got;
     *out = p;
     return hipSuccess;
 }
@@ -278,6 +287,13 @@ uint64_t bh_ctx_workspace_bytes(const bh_ctx* ctx) {
     uint64_t b = ctx->pool.cached_bytes;
     for (auto& kv : ctx->pool.live) b += kv.second;
     return b;
+}
+
+bh_status bh_ctx_release_workspace(bh_ctx* ctx) {
+    if (!ctx) return BH_ERR_INVALID_ARG;
+    BH_TRY(hip_check(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize"));
+    ctx->pool.trim();
+    return BH_OK;
 }
 
 bh_status bh_radix_argsort(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t* vals_in, uint32_t n,

@@ -1,23 +1,24 @@
 // sort.hip — fill, inclusive scan and stable radix sort for gfx950.
 //
-// Radix sort: LSD with 8-bit digits in the "onesweep" organisation
-// (Adinets & Merrill, 2022): one histogram pass computes the digit counts of
-// every pass up front, then each digit pass reads keys and values once and
-// writes them once.  A partition of 4096 pairs is ranked stably inside the
-// workgroup with wave64 ballots (an 8-ballot match of the digit gives each
-// lane its peers; a per-wave running count orders slots), the block's digit
-// counts are published to a look-back status array, and the pairs are written
-// from LDS in digit order so each digit's run is a contiguous write.
+// Radix sort: LSD with digits of at most 8 bits, each pass in three kernels
+// (reduce-then-scan).  An upsweep counts the digits of every partition of 4096
+// keys; a small scan turns the counts into each partition's output offset per
+// digit (digit totals below it plus the same digit in earlier partitions);
+// the digit pass then ranks a partition's pairs stably inside the workgroup
+// with wave64 ballots (an 8-ballot match of the digit gives each lane its
+// peers; a per-wave running count orders slots) and writes them from LDS in
+// digit order, so each digit's run is a contiguous write.  No workgroup waits
+// on another: a decoupled look-back over the ~2500 partitions of a tile sort
+// was measured to cost 31 of a pass's 76 us (a chain that advances a few
+// partitions per coherent round trip), more than the extra read of the keys.
 //
-// Forward progress of the look-back: a partition is its workgroup's id, and a
-// workgroup only waits on lower ids.  Workgroups go to the XCDs round robin
-// and each XCD dispatches its share in increasing id order, so whenever some
-// partition waits, every lower partition already has a resident workgroup or
-// has finished (an atomic ticket per workgroup gives the same guarantee
-// without relying on dispatch order, but serialises workgroup starts on one
-// counter: measured 14 us of a 93 us tile-sort pass).  The spin is bounded;
-// on exhaustion the kernel raises an error flag that the host turns into
-// BH_ERR_INTERNAL, and the kernel still completes.
+// The inclusive scan below keeps a decoupled look-back.  A partition is
+// its workgroup's id and waits only on lower ids.  Workgroups go
+// to the XCDs round robin and each XCD dispatches its share in increasing id
+// order, so whenever some partition waits, every lower partition already has
+// a resident workgroup or has finished.  The spin is bounded; on exhaustion
+// the kernel raises an error flag that the host turns into BH_ERR_INTERNAL,
+// and the kernel still completes.
 //
 // Replaces brush-sort (crates/brush-sort/src/lib.rs:16-129, which runs five
 // kernels per 4-bit pass with a single-workgroup scan) and brush-prefix-sum
@@ -115,68 +116,181 @@ static DigitPlan digit_plan(uint32_t key_bits) {
     return d;
 }
 
-// ---- histogram of all digit passes -------------------------------------------
+// Offset geometry of a sort: `parts` partitions of 256 * `items` pairs,
+// `radix` counters per partition (2^width), and partitions grouped into
+// `blocks` of `rows` (a power of two >= sqrt(parts)) for the offset scan, so
+// that both the block sums every scan workgroup reads and the rows it walks
+// stay short.  Partitions are as large as still gives about four workgroups
+// per CU: 4096 pairs from 4M keys, 1024 for a 1M-key depth sort (4096 would
+// leave it 245 workgroups for 256 CUs).
+struct ScanPlan {
+    uint32_t items, parts, rows, blocks, radix;
+};
+static ScanPlan scan_plan(uint32_t n, const DigitPlan& d) {
+    ScanPlan s;
+    s.items = n >= (4096u << 10) ? 16u : n >= (2048u << 10) ? 8u : 4u;
+    s.parts = div_up(n, (uint64_t)kThreads * s.items);
+    s.rows = 16;
+    while ((uint64_t)s.rows * s.rows < s.parts) s.rows *= 2;
+    s.blocks = div_up(s.parts, s.rows);
+    s.radix = 1u << d.width;
+    return s;
+}
 
-// Each wave counts into its own LDS copy (less contention on the few buckets
-// of a narrow digit); a modest grid keeps the global atomics on the 256 *
-// passes bucket words few.
-__global__ __launch_bounds__(kThreads) void radix_hist_kernel(const uint32_t* __restrict__ keys, uint32_t n,
-                                                               uint32_t passes, uint32_t width, uint32_t key_sub,
-                                                               uint32_t key_cap, uint32_t* __restrict__ hist) {
-    __shared__ uint32_t sh[kWaves][4 * kRadix];
-    const uint32_t wave = threadIdx.x >> 6;
-    for (int i = threadIdx.x; i < kWaves * 4 * kRadix; i += kThreads) (&sh[0][0])[i] = 0;
+// ---- reduce-then-scan: digit counts of each partition ----------------------------
+
+// One workgroup per partition: the digit counts of its keys (per-wave LDS
+// copies, 16-byte loads for a whole aligned partition) go to its row of
+// `counts` and are added to its block's sums.
+template <bool FIRST, int ITEMS>
+__global__ __launch_bounds__(kThreads) void radix_upsweep_kernel(const uint32_t* __restrict__ keys, uint32_t n,
+                                                                  uint32_t shift, uint32_t digit_bits,
+                                                                  uint32_t key_sub, uint32_t key_cap, uint32_t radix,
+                                                                  uint32_t rows, uint32_t* __restrict__ counts,
+                                                                  uint32_t* __restrict__ blk) {
+    __shared__ uint32_t s_hist[kWaves][kRadix];
+    const int tid = threadIdx.x, wave = tid >> 6;
+    for (int i = tid; i < kWaves * kRadix; i += kThreads) (&s_hist[0][0])[i] = 0;
     __syncthreads();
-    const uint32_t mask = (1u << width) - 1u;
-    uint32_t* mine = sh[wave];
-    // 16-byte loads when the keys are 16-byte aligned (every internal buffer
-    // is); a caller's misaligned view is counted one key at a time
-    const bool vec = (reinterpret_cast<uintptr_t>(keys) & 15u) == 0u;
-    const uint32_t n4 = vec ? n / 4u : 0u;
-    const uint4* k4 = reinterpret_cast<const uint4*>(keys);
-    for (uint32_t idx = blockIdx.x * kThreads + threadIdx.x; idx < n4; idx += gridDim.x * kThreads) {
-        const uint4 q = k4[idx];
-        const uint32_t kk[4] = {min(q.x - key_sub, key_cap), min(q.y - key_sub, key_cap), min(q.z - key_sub, key_cap),
-                                min(q.w - key_sub, key_cap)};
+    constexpr int PART = kThreads * ITEMS;
+    const uint32_t part = blockIdx.x;
+    const uint64_t base = (uint64_t)part * PART;
+    const uint32_t dmask = (1u << digit_bits) - 1u;
+    uint32_t* mine = s_hist[wave];
+    if (base + PART <= n && (reinterpret_cast<uintptr_t>(keys) & 15u) == 0u) {
+        const uint4* k4 = reinterpret_cast<const uint4*>(keys + base);
+        uint4 q[ITEMS / 4];
 #pragma unroll
-        for (int e = 0; e < 4; e++)
-            for (uint32_t p = 0; p < passes; p++) atomicAdd(&mine[p * kRadix + ((kk[e] >> (p * width)) & mask)], 1u);
-    }
-    // the keys after the last full group of four
-    for (uint32_t idx = n4 * 4u + blockIdx.x * kThreads + threadIdx.x; idx < n; idx += gridDim.x * kThreads) {
-        const uint32_t kk = min(keys[idx] - key_sub, key_cap);
-        for (uint32_t p = 0; p < passes; p++) atomicAdd(&mine[p * kRadix + ((kk >> (p * width)) & mask)], 1u);
+        for (int j = 0; j < ITEMS / 4; j++) q[j] = k4[j * kThreads + tid];
+#pragma unroll
+        for (int j = 0; j < ITEMS / 4; j++) {
+            const uint32_t kk[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t k = FIRST ? min(kk[e] - key_sub, key_cap) : kk[e];
+                atomicAdd(&mine[(k >> shift) & dmask], 1u);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < ITEMS; j++) {
+            const uint64_t idx = base + (uint64_t)j * kThreads + tid;
+            if (idx < n) {
+                const uint32_t k = FIRST ? min(keys[idx] - key_sub, key_cap) : keys[idx];
+                atomicAdd(&mine[(k >> shift) & dmask], 1u);
+            }
+        }
     }
     __syncthreads();
-    for (uint32_t i = threadIdx.x; i < passes * kRadix; i += kThreads) {
+    if ((uint32_t)tid < radix) {
         uint32_t c = 0;
 #pragma unroll
-        for (int w = 0; w < kWaves; w++) c += sh[w][i];
-        if (c) atomicAdd(&hist[i], c);
+        for (int w = 0; w < kWaves; w++) c += s_hist[w][tid];
+        counts[(size_t)part * radix + tid] = c;
+        if (c) atomicAdd(&blk[(size_t)(part / rows) * radix + tid], c);
+    }
+}
+
+// counts[q][d] becomes the output position of partition q's first pair of
+// digit d: the totals of the digits below d plus the counts of digit d in the
+// partitions before q.  One workgroup of 1024 threads per block of `rows`
+// partitions; each digit column is shared by 1024 / radix thread groups, which
+// split the block sums and the block's rows between them, so a thread issues
+// its few loads together (a handful of memory round trips in all).
+constexpr int kScanThreads = 1024;
+__global__ __launch_bounds__(kScanThreads) void radix_scan_kernel(uint32_t* __restrict__ counts,
+                                                                   const uint32_t* __restrict__ blk, uint32_t parts,
+                                                                   uint32_t rows, uint32_t blocks, uint32_t radix) {
+    __shared__ uint32_t s_tot[kScanThreads / 64];
+    __shared__ uint32_t s_all[kScanThreads];     // a thread's share of its digit's total
+    __shared__ uint32_t s_before[kScanThreads];  // ... of the blocks before this one
+    __shared__ uint32_t s_rows[kScanThreads];    // ... of this block's rows
+    __shared__ uint32_t s_base[kRadix];
+    constexpr int kChunk = 16;
+    const uint32_t tid = threadIdx.x, b = blockIdx.x;
+    const uint32_t d = tid & (radix - 1u), grp = tid / radix, groups = kScanThreads / radix;
+    // block sums: group g reads blocks g, g + groups, ...
+    uint32_t all = 0, before = 0;
+    for (uint32_t q0 = grp; q0 < blocks; q0 += groups * kChunk) {
+        uint32_t x[kChunk];
+#pragma unroll
+        for (int i = 0; i < kChunk; i++) {
+            const uint32_t q = q0 + i * groups;
+            x[i] = q < blocks ? blk[(size_t)q * radix + d] : 0u;
+        }
+#pragma unroll
+        for (int i = 0; i < kChunk; i++) {
+            all += x[i];
+            before += q0 + i * groups < b ? x[i] : 0u;
+        }
+    }
+    // this block's rows: group g takes a contiguous run of them
+    const uint32_t r0 = b * rows, r1 = min(parts, r0 + rows);
+    const uint32_t sub = (rows + groups - 1u) / groups;
+    const uint32_t lo = min(r1, r0 + grp * sub), hi = min(r1, lo + sub);
+    uint32_t mine = 0;
+    for (uint32_t q0 = lo; q0 < hi; q0 += kChunk) {
+        uint32_t x[kChunk];
+#pragma unroll
+        for (int i = 0; i < kChunk; i++) x[i] = q0 + i < hi ? counts[(size_t)(q0 + i) * radix + d] : 0u;
+#pragma unroll
+        for (int i = 0; i < kChunk; i++) mine += x[i];
+    }
+    s_all[tid] = all;
+    s_before[tid] = before;
+    s_rows[tid] = mine;
+    __syncthreads();
+    uint32_t total = 0, pre = 0;
+    if (grp == 0) {
+        for (uint32_t g = 0; g < groups; g++) {
+            total += s_all[g * radix + d];
+            pre += s_before[g * radix + d];
+        }
+    }
+    uint32_t dummy;
+    const uint32_t bin_base = block_exclusive_scan<kScanThreads>(grp == 0 ? total : 0u, s_tot, &dummy);
+    if (grp == 0) s_base[d] = bin_base + pre;
+    __syncthreads();
+    uint32_t run = s_base[d];
+    for (uint32_t g = 0; g < grp; g++) run += s_rows[g * radix + d];
+    for (uint32_t q0 = lo; q0 < hi; q0 += kChunk) {
+        uint32_t x[kChunk];
+#pragma unroll
+        for (int i = 0; i < kChunk; i++) x[i] = q0 + i < hi ? counts[(size_t)(q0 + i) * radix + d] : 0u;
+#pragma unroll
+        for (int i = 0; i < kChunk; i++) {
+            if (q0 + i < hi) counts[(size_t)(q0 + i) * radix + d] = run;
+            run += x[i];
+        }
     }
 }
 
 // ---- one digit pass ------------------------------------------------------------
 
+// One workgroup per partition of 256 * ITEMS pairs: stable ranking inside the
+// partition, then every pair written to offs[part][digit] + its rank among the
+// partition's pairs of that digit, through LDS in digit order.
 template <bool FIRST, int ITEMS>
 __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __restrict__ keys_in,
                                                              const uint32_t* __restrict__ vals_in,
                                                              uint32_t* __restrict__ keys_out,
                                                              uint32_t* __restrict__ vals_out, uint32_t n,
                                                              uint32_t shift, uint32_t digit_bits, uint32_t key_sub,
-                                                             uint32_t key_cap, const uint32_t* __restrict__ hist,
-                                                             uint64_t* status, uint32_t* err) {
-    constexpr int PART = kThreads * ITEMS;
+                                                             uint32_t key_cap, uint32_t radix,
+                                                             const uint32_t* __restrict__ offs) {
     __shared__ uint32_t s_wave_hist[kWaves][kRadix];
     __shared__ uint32_t s_local_start[kRadix];
     __shared__ uint32_t s_global_off[kRadix];
+    constexpr int PART = kThreads * ITEMS;
     __shared__ uint32_t s_buf[PART];  // keys, then values, in digit order
     __shared__ uint32_t s_tot[kWaves];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t part = blockIdx.x;
+    // this partition's output offset of digit `tid`, loaded while the pairs are ranked
+    const uint32_t my_off = (uint32_t)tid < radix ? offs[(size_t)part * radix + tid] : 0u;
     for (int i = tid; i < kWaves * kRadix; i += kThreads) (&s_wave_hist[0][0])[i] = 0;
     __syncthreads();
-    const uint32_t part = blockIdx.x;
     const uint64_t base = (uint64_t)part * PART;
     const uint64_t wave_base = base + (uint64_t)wave * (64 * ITEMS);
     const uint32_t dmask = (1u << digit_bits) - 1u;
@@ -222,20 +336,10 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
         s_wave_hist[w][d] = total;
         total += c[w];
     }
-    uint64_t* my_status = status + (uint64_t)part * kRadix + d;
-    uint32_t excl = 0;
-    if (part == 0) {
-        status_store(my_status, kFlagPrefix | total);
-    } else {
-        status_store(my_status, kFlagAgg | total);
-        excl = look_back(status, part, kRadix, d, err);
-        status_store(my_status, kFlagPrefix | (uint64_t)(excl + total));
-    }
     uint32_t tot_dummy;
-    uint32_t bin_base = block_exclusive_scan<kThreads>(hist[d], s_tot, &tot_dummy);
-    uint32_t local_start = block_exclusive_scan<kThreads>(total, s_tot, &tot_dummy);
+    const uint32_t local_start = block_exclusive_scan<kThreads>(total, s_tot, &tot_dummy);
     s_local_start[d] = local_start;
-    s_global_off[d] = bin_base + excl;
+    s_global_off[d] = my_off;
     __syncthreads();
 
     // keys into LDS in digit order, then out; the destination of each LDS slot
@@ -258,7 +362,7 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
             const uint32_t key = s_buf[i];
             const uint32_t dd = (key >> shift) & dmask;
             const uint32_t g = s_global_off[dd] + (i - s_local_start[dd]);
-            if (g < n) {  // always true unless a look-back gave up (reported through err)
+            if (g < n) {  // always true: the offsets partition [0, n)
                 keys_out[g] = key;
                 dst[j] = g;
             }
@@ -278,40 +382,33 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
     }
 }
 
-// Partitions of 4096 pairs (smaller partitions measured slower: more
-// look-back traffic for the same data).
-static uint32_t sort_part(uint32_t) { return (uint32_t)kPart; }
-
-// scratch layout: hist[4*256] | status[passes][parts][256] (u64)
+// scratch layout: block sums blk[passes][blocks][radix] (zeroed before the
+// sort) | offsets counts[parts][radix] (rewritten by every pass)
 size_t radix_sort_scratch_bytes(uint32_t n, uint32_t key_bits) {
-    const uint64_t parts = div_up(n, sort_part(n));
-    return (size_t)(4 * kRadix) * 4 + (size_t)digit_plan(key_bits).passes * parts * kRadix * 8;
+    const DigitPlan plan = digit_plan(key_bits);
+    const ScanPlan sp = scan_plan(n, plan);
+    return ((size_t)plan.passes * sp.blocks + sp.parts) * sp.radix * 4;
 }
 
 size_t radix_sort_zeroed_words(uint32_t n, uint32_t key_bits) {
-    const uint64_t parts = div_up(n, sort_part(n));
-    return (size_t)(4 * kRadix) + (size_t)digit_plan(key_bits).passes * parts * kRadix * 2;
+    const DigitPlan plan = digit_plan(key_bits);
+    const ScanPlan sp = scan_plan(n, plan);
+    return (size_t)plan.passes * sp.blocks * sp.radix;
 }
 
 bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t* vals_in, uint32_t n,
                            uint32_t key_bits, uint32_t key_sub, uint32_t key_cap, uint32_t* keys_out,
                            uint32_t* vals_out, uint32_t* tmp_keys, uint32_t* tmp_vals, void* scratch,
                            const char* tag, bool scratch_zeroed) {
-    const std::string hist_name = std::string(tag) + "_hist", pass_name = std::string(tag) + "_onesweep";
+    const std::string up_name = std::string(tag) + "_up", scan_name = std::string(tag) + "_scan",
+                      pass_name = std::string(tag) + "_onesweep";
     if (n == 0) return BH_OK;
     if (key_bits > 32) return set_error(ctx, BH_ERR_INVALID_ARG, "radix sort: more than 32 key bits");
     const DigitPlan plan = digit_plan(key_bits);
-    const uint32_t part_size = sort_part(n);
-    const uint32_t parts = div_up(n, part_size);
-    uint32_t* hist = (uint32_t*)scratch;
-    uint64_t* status = (uint64_t*)(hist + 4 * kRadix);
-    if (!scratch_zeroed) launch_fill_u32(ctx, hist, 0u, radix_sort_zeroed_words(n, key_bits));
-    {
-        KernelTimer t(ctx, hist_name.c_str());
-        uint32_t blocks = std::min<uint32_t>(div_up(div_up(n, 4), kThreads * 8), 512);
-        radix_hist_kernel<<<blocks, kThreads, 0, ctx->stream>>>(keys_in, n, plan.passes, plan.width, key_sub, key_cap,
-                                                                hist);
-    }
+    const ScanPlan sp = scan_plan(n, plan);
+    uint32_t* blk = (uint32_t*)scratch;
+    uint32_t* offs = blk + (size_t)plan.passes * sp.blocks * sp.radix;
+    if (!scratch_zeroed) launch_fill_u32(ctx, blk, 0u, radix_sort_zeroed_words(n, key_bits));
     const uint32_t* src_k = keys_in;
     const uint32_t* src_v = vals_in;
     for (uint32_t p = 0; p < plan.passes; p++) {
@@ -319,19 +416,43 @@ bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t*
         bool to_out = ((plan.passes - 1 - p) % 2) == 0;
         uint32_t* dk = to_out ? keys_out : tmp_keys;
         uint32_t* dv = to_out ? vals_out : tmp_vals;
-        uint64_t* st = status + (uint64_t)p * parts * kRadix;
+        uint32_t* pblk = blk + (size_t)p * sp.blocks * sp.radix;
         const uint32_t sh = plan.shift(p), bits = plan.bits(p);
         const uint32_t sub = p == 0 ? key_sub : 0u, cap = p == 0 ? key_cap : 0xFFFFFFFFu;
-        KernelTimer t(ctx, pass_name.c_str());
-#define BH_PASS(F, I)                                                                                               \
-    onesweep_kernel<F, I><<<parts, kThreads, 0, ctx->stream>>>(src_k, src_v, dk, dv, n, sh, bits, sub, cap,        \
-                                                               hist + p * kRadix, st, ctx->d_counters + 1)
-        if (part_size == (uint32_t)kPart) {
-            if (p == 0) BH_PASS(true, kItems); else BH_PASS(false, kItems);
-        } else {
-            if (p == 0) BH_PASS(true, 4); else BH_PASS(false, 4);
-        }
-#undef BH_PASS
+        const dim3 grid(sp.parts), block(kThreads);
+#define BH_SORT_PASS(I)                                                                                          \
+    do {                                                                                                        \
+        {                                                                                                       \
+            KernelTimer t(ctx, up_name.c_str());                                                                \
+            if (p == 0)                                                                                         \
+                radix_upsweep_kernel<true, I><<<grid, block, 0, ctx->stream>>>(src_k, n, sh, bits, sub, cap,   \
+                                                                               sp.radix, sp.rows, offs, pblk); \
+            else                                                                                                \
+                radix_upsweep_kernel<false, I><<<grid, block, 0, ctx->stream>>>(src_k, n, sh, bits, sub, cap,  \
+                                                                                sp.radix, sp.rows, offs, pblk); \
+        }                                                                                                       \
+        {                                                                                                       \
+            KernelTimer t(ctx, scan_name.c_str());                                                              \
+            radix_scan_kernel<<<sp.blocks, kScanThreads, 0, ctx->stream>>>(offs, pblk, sp.parts, sp.rows,       \
+                                                                           sp.blocks, sp.radix);               \
+        }                                                                                                       \
+        {                                                                                                       \
+            KernelTimer t(ctx, pass_name.c_str());                                                              \
+            if (p == 0)                                                                                         \
+                onesweep_kernel<true, I><<<grid, block, 0, ctx->stream>>>(src_k, src_v, dk, dv, n, sh, bits,   \
+                                                                          sub, cap, sp.radix, offs);           \
+            else                                                                                                \
+                onesweep_kernel<false, I><<<grid, block, 0, ctx->stream>>>(src_k, src_v, dk, dv, n, sh, bits,  \
+                                                                           sub, cap, sp.radix, offs);          \
+        }                                                                                                       \
+    } while (0)
+        if (sp.items == 16)
+            BH_SORT_PASS(16);
+        else if (sp.items == 8)
+            BH_SORT_PASS(8);
+        else
+            BH_SORT_PASS(4);
+#undef BH_SORT_PASS
         src_k = dk;
         src_v = dv;
     }

@@ -172,6 +172,11 @@ bh_status bh_ctx_read_timings(bh_ctx* ctx, bh_kernel_timing* out, int max, int* 
 bh_status bh_ctx_reset_timings(bh_ctx* ctx);
 /* Bytes currently cached by the context's workspace pool. */
 uint64_t bh_ctx_workspace_bytes(const bh_ctx* ctx);
+/* Synchronises the stream, then frees every cached workspace block that no
+ * forward state holds (the counterpart of a caching allocator's empty-cache
+ * call; no counterpart in the reference, whose buffers belong to Burn's
+ * allocator).  Later calls allocate again as needed. */
+bh_status bh_ctx_release_workspace(bh_ctx* ctx);
 
 /* ---- primitives ---------------------------------------------------------- */
 

@@ -25,7 +25,7 @@ def _dev(gpu):
 # ---- primitives ---------------------------------------------------------------------------
 
 @pytest.mark.parametrize("n,bits", [(1, 32), (255, 8), (4096, 13), (4097, 32), (65537, 4), (100000, 0),
-                                    (300001, 17), (1 << 20, 32)])
+                                    (300001, 17), (1 << 20, 32), (3_000_017, 24), (5_000_001, 13)])
 def test_radix_argsort_matches_stable_sort(gpu, n, bits):
     import torch
     from brush_amd import _lib
@@ -396,6 +396,8 @@ def test_workspace_stops_growing_when_sizes_creep(gpu):
 
     tr, sh, op = random_scene(9090, 60000, 1, log_scale=(-3.0, 0.5))
     cam = Camera.from_focal((0.0, 0.0, -3.0), (0.0, 0.0, 0.0, 1.0), 300.0, 256, 256)
+    # start from an empty pool: what earlier tests cached would serve some sizes
+    _lib.context(0).release_workspace()
     sizes = []
     for k in range(12):
         n = 50000 + 500 * k  # more splats, more intersections, every call
