@@ -158,7 +158,6 @@ struct Scratch {
 static uint32_t bit_length(uint32_t x) { return x ? 32u - (uint32_t)__builtin_clz(x) : 0u; }
 
 static bh_status check_device_error(bh_ctx* ctx, uint32_t flags) {
-    if (flags & kErrSpin) return set_error(ctx, BH_ERR_INTERNAL, "a look-back spin exceeded its bound");
     if (flags & kErrOverflow) return set_error(ctx, BH_ERR_INTERNAL, "a device count overflowed");
     return BH_OK;
 }
@@ -343,7 +342,7 @@ bh_status bh_prefix_sum(bh_ctx* ctx, const uint32_t* in, uint32_t* out, uint32_t
     Scratch ws(ctx);
     char* scratch;
     BH_TRY(ws.get(&scratch, scan_scratch_bytes(n)));
-    return inclusive_scan(ctx, in, nullptr, out, n, scratch);
+    return inclusive_scan(ctx, in, out, n, scratch);
 }
 
 bh_status bh_get_tile_offsets(bh_ctx* ctx, const uint32_t* ids, uint32_t m, uint32_t num_tiles, uint32_t* offsets) {
@@ -411,12 +410,12 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
 
     uint32_t num_visible = 0;
     uint64_t num_isect = 0;
+    uint32_t* counts_sorted = nullptr;
     uint32_t kmin = 0, kmax = 0;
     // Everything the forward needs zeroed, in one launch: the counters' flags
     // word (the reduction kernel writes the others), the visible mask, the
-    // depth sort's histograms and look-back status (sized for 32 key bits,
-    // which covers the key range found later), the scan's status (sized for
-    // N >= V), and both tile-offset arrays (empty tiles stay [0, 0]).
+    // depth sort's block sums (sized for 32 key bits, which covers the key
+    // range found later), and both tile-offset arrays (empty tiles stay [0, 0]).
     char *depth_scr = nullptr, *scan_scr = nullptr;
     float* vis_rows = nullptr;
     if (num_splats) {
@@ -428,7 +427,6 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
             {ctx->d_counters + 1, 0u, num_splats ? 1u : 0u},
             {(uint32_t*)visible, 0u, bwd ? (uint64_t)num_splats : 0u},
             {(uint32_t*)depth_scr, 0u, num_splats ? radix_sort_zeroed_words(num_splats, 32) : 0u},
-            {(uint32_t*)(scan_scr + 64), 0u, num_splats ? scan_zeroed_words(num_splats) : 0u},
             {off_pre, 0u, (uint64_t)num_tiles * 2},
             {tile_offsets, 0u, bwd ? (uint64_t)num_tiles * 2 : 0u},
         };
@@ -459,12 +457,15 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
             // (all-ones key) map to the cap and sort last.
             const uint32_t cap = kmax - kmin + 1u;
             const uint32_t key_bits = std::max<uint32_t>(1u, bit_length(cap));
+            // the last pass also gathers each splat's tile count in depth order,
+            // so the scan below reads them contiguously
             uint32_t *sk, *tk, *tv;
             BH_STRY(ws.get(&sk, num_splats));
             BH_STRY(ws.get(&tk, num_splats));
             BH_STRY(ws.get(&tv, num_splats));
+            BH_STRY(ws.get(&counts_sorted, num_splats));
             BH_STRY(radix_sort_pairs(ctx, depth_keys, nullptr, num_splats, key_bits, kmin, cap, sk, gfc, tk, tv,
-                                     depth_scr, "depth_sort", true));
+                                     depth_scr, "depth_sort", true, counts, counts_sorted));
         }
     }
     BH_STRY(sget((void**)&cum, (size_t)num_visible * 4));
@@ -475,7 +476,7 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
     BH_STRY(sget((void**)&tile_ids, (size_t)std::max<uint32_t>(m, 1) * 4));
     BH_STRY(sget((void**)&cgids, (size_t)std::max<uint32_t>(m, 1) * 4));
     if (num_visible) {
-        BH_STRY(inclusive_scan(ctx, counts, gfc, cum, num_visible, scan_scr, true));
+        BH_STRY(inclusive_scan(ctx, counts_sorted, cum, num_visible, scan_scr));
         // with intersections, map_intersects orders the rows as it reads them
         if (num_isect == 0) launch_project_visible(ctx, vis_rows, gfc, num_visible, num_splats, projected, depths);
         BH_STRY(check_launch(ctx, "project_visible"));
@@ -489,13 +490,15 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
         BH_STRY(ws.get(&uc, m));
         BH_STRY(ws.get(&tk, m));
         BH_STRY(ws.get(&tv, m));
-        launch_map_intersects(ctx, u.tile_bw, u.tile_bh, tile_h, vis_rows, gfc, num_splats, cum, num_visible, projected,
-                              depths, ut, uc);
-        BH_STRY(check_launch(ctx, "map_intersects"));
-        // tile sort over bits(num_tiles) bits (render.rs:392-395)
+        // tile sort over bits(num_tiles) bits (render.rs:392-395); the map
+        // kernel zeroes the sort's scratch
         const uint32_t bits = bit_length(num_tiles);
         BH_STRY(ws.get(&scr, radix_sort_scratch_bytes(m, bits)));
-        BH_STRY(radix_sort_pairs(ctx, ut, uc, m, bits, 0u, 0xFFFFFFFFu, tile_ids, cgids, tk, tv, scr, "tile_sort"));
+        launch_map_intersects(ctx, u.tile_bw, u.tile_bh, tile_h, vis_rows, gfc, num_splats, cum, num_visible, projected,
+                              depths, ut, uc, (uint32_t*)scr, (uint32_t)radix_sort_zeroed_words(m, bits));
+        BH_STRY(check_launch(ctx, "map_intersects"));
+        BH_STRY(radix_sort_pairs(ctx, ut, uc, m, bits, 0u, 0xFFFFFFFFu, tile_ids, cgids, tk, tv, scr, "tile_sort",
+                                 true));
     } else {
         launch_fill_u32(ctx, tile_ids, 0u, 1);
         launch_fill_u32(ctx, cgids, 0u, 1);

@@ -84,7 +84,6 @@ struct bh_ctx {
 
 namespace bh {
 
-constexpr uint32_t kErrSpin = 1u;      // a look-back spin hit its bound
 constexpr uint32_t kErrOverflow = 2u;  // a count exceeded its field
 
 // Scoped timing of one kernel launch on the context's stream.
@@ -124,22 +123,21 @@ size_t radix_sort_scratch_bytes(uint32_t n, uint32_t key_bits);
 // zero when the sort starts; with scratch_zeroed the caller has done that
 // (it may size the fill for 32 key bits, which covers any key_bits).
 size_t radix_sort_zeroed_words(uint32_t n, uint32_t key_bits);
+// With gather_out, the last pass also writes gather_out[i] =
+// gather_src[vals_out[i]] (an n-element buffer).
 bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t* vals_in, uint32_t n,
                            uint32_t key_bits, uint32_t key_sub, uint32_t key_cap, uint32_t* keys_out,
                            uint32_t* vals_out, uint32_t* tmp_keys, uint32_t* tmp_vals, void* scratch,
-                           const char* tag = "radix", bool scratch_zeroed = false);
+                           const char* tag = "radix", bool scratch_zeroed = false,
+                           const uint32_t* gather_src = nullptr, uint32_t* gather_out = nullptr);
 // out[i] = in[i] & mask
 void launch_mask_u32(bh_ctx* ctx, const uint32_t* in, uint32_t mask, uint32_t n, uint32_t* out);
 // keys_out[i] = keys_in[perm[i]], vals_out[i] = vals_in[perm[i]]
 void launch_gather_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t* vals_in, const uint32_t* perm,
                          uint32_t n, uint32_t* keys_out, uint32_t* vals_out);
 size_t scan_scratch_bytes(uint32_t n);
-// Inclusive scan of in[i] (or in[gather[i]] when gather != nullptr).
-// The first scan_zeroed_words(n) words of `scratch` past its 64-byte header
-// must be zero; with status_zeroed the caller has done that.
-size_t scan_zeroed_words(uint32_t n);
-bh_status inclusive_scan(bh_ctx* ctx, const uint32_t* in, const uint32_t* gather, uint32_t* out, uint32_t n,
-                         void* scratch, bool status_zeroed = false);
+// Inclusive scan of in[0, n); out may alias in.
+bh_status inclusive_scan(bh_ctx* ctx, const uint32_t* in, uint32_t* out, uint32_t n, void* scratch);
 
 // project.hip
 size_t project_partials_bytes(uint32_t n);
@@ -152,10 +150,12 @@ void launch_project_forward(bh_ctx* ctx, const bh_project_uniforms& u, const flo
 void launch_project_visible(bh_ctx* ctx, const float* rows, const uint32_t* gfc, uint32_t num_visible,
                             uint32_t num_splats, float* projected, float* depths);
 // Also writes compact rows `projected` [V,10] and `depths` [V] from the
-// global-id rows of launch_project_forward.
+// global-id rows of launch_project_forward, and zeroes zero[0, zero_words)
+// (the tile sort's scratch).
 void launch_map_intersects(bh_ctx* ctx, uint32_t tile_bw, uint32_t tile_bh, uint32_t tile_h, const float* rows,
                            const uint32_t* gfc, uint32_t num_splats, const uint32_t* cum, uint32_t num_visible,
-                           float* projected, float* depths, uint32_t* tile_ids, uint32_t* cgids);
+                           float* projected, float* depths, uint32_t* tile_ids, uint32_t* cgids, uint32_t* zero,
+                           uint32_t zero_words);
 
 // raster.hip
 void launch_tile_offsets(bh_ctx* ctx, const uint32_t* tile_ids, uint32_t m, uint32_t num_tiles,

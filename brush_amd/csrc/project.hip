@@ -351,10 +351,13 @@ __global__ __launch_bounds__(256) void map_intersects_kernel(uint32_t tile_bw, u
                                                               float* __restrict__ projected,
                                                               float* __restrict__ depths,
                                                               uint32_t* __restrict__ tile_ids,
-                                                              uint32_t* __restrict__ cgids) {
+                                                              uint32_t* __restrict__ cgids,
+                                                              uint32_t* __restrict__ zero, uint32_t zero_words) {
     __shared__ WalkRec s_rec[4][64];
     __shared__ uint32_t s_slot[4][64], s_count[4][64];
     const uint32_t c = blockIdx.x * 256u + threadIdx.x;
+    // the tile sort's zeroed scratch, cleared here instead of by a launch of its own
+    for (uint32_t i = c; i < zero_words; i += gridDim.x * 256u) zero[i] = 0u;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t c0 = c - lane;  // first compact id of this wave
     if (c0 >= num_visible) return;  // the whole wave is past the end
@@ -412,17 +415,20 @@ __global__ __launch_bounds__(256) void map_intersects_kernel(uint32_t tile_bw, u
 
 void launch_map_intersects(bh_ctx* ctx, uint32_t tile_bw, uint32_t tile_bh, uint32_t tile_h, const float* rows,
                            const uint32_t* gfc, uint32_t num_splats, const uint32_t* cum, uint32_t num_visible,
-                           float* projected, float* depths, uint32_t* tile_ids, uint32_t* cgids) {
+                           float* projected, float* depths, uint32_t* tile_ids, uint32_t* cgids, uint32_t* zero,
+                           uint32_t zero_words) {
     if (num_visible == 0) return;
     KernelTimer t(ctx, "map_intersects");
     const uint32_t blocks = div_up(num_visible, 256);
     const float4* r4 = reinterpret_cast<const float4*>(rows);
     if (tile_h == 8)
         map_intersects_kernel<8><<<blocks, 256, 0, ctx->stream>>>(tile_bw, tile_bh, r4, gfc, num_splats, cum,
-                                                                 num_visible, projected, depths, tile_ids, cgids);
+                                                                 num_visible, projected, depths, tile_ids, cgids, zero,
+                                                                 zero_words);
     else
         map_intersects_kernel<16><<<blocks, 256, 0, ctx->stream>>>(tile_bw, tile_bh, r4, gfc, num_splats, cum,
-                                                                  num_visible, projected, depths, tile_ids, cgids);
+                                                                  num_visible, projected, depths, tile_ids, cgids, zero,
+                                                                  zero_words);
 }
 
 }  // namespace bh

@@ -12,13 +12,8 @@
 // was measured to cost 31 of a pass's 76 us (a chain that advances a few
 // partitions per coherent round trip), more than the extra read of the keys.
 //
-// The inclusive scan below keeps a decoupled look-back.  A partition is
-// its workgroup's id and waits only on lower ids.  Workgroups go
-// to the XCDs round robin and each XCD dispatches its share in increasing id
-// order, so whenever some partition waits, every lower partition already has
-// a resident workgroup or has finished.  The spin is bounded; on exhaustion
-// the kernel raises an error flag that the host turns into BH_ERR_INTERNAL,
-// and the kernel still completes.
+// The inclusive scan is reduce-then-scan as well (partition sums, then the
+// in-partition scan plus the sums before it).
 //
 // Replaces brush-sort (crates/brush-sort/src/lib.rs:16-129, which runs five
 // kernels per 4-bit pass with a single-workgroup scan) and brush-prefix-sum
@@ -26,15 +21,38 @@
 #include <hip/hip_runtime.h>
 
 #include "bh_internal.h"
-#include "bh_lookback.h"
 
 namespace bh {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-constexpr int kItems = 16;
-constexpr int kPart = kThreads * kItems;  // 4096
 constexpr int kRadix = 256;
+
+// Exclusive scan of one value per thread over a block of THREADS threads
+// (a multiple of 64); *total receives the block's sum.
+template <int THREADS>
+__device__ inline uint32_t block_exclusive_scan(uint32_t v, uint32_t* s_wave_tot, uint32_t* total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint32_t x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        uint32_t y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
+    }
+    if (lane == 63) s_wave_tot[wave] = x;
+    __syncthreads();
+    uint32_t off = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < THREADS / 64; w++) {
+        uint32_t t = s_wave_tot[w];
+        if (w < wave) off += t;
+        tot += t;
+    }
+    __syncthreads();
+    *total = tot;
+    return off + x - v;
+}
+
 // p[0, count) = value: 16-byte stores from the first 16-byte boundary, single
 // words for the unaligned head and the tail.
 __global__ void fill_u32_kernel(uint32_t* p, uint32_t value, uint64_t count) {
@@ -120,15 +138,16 @@ static DigitPlan digit_plan(uint32_t key_bits) {
 // `radix` counters per partition (2^width), and partitions grouped into
 // `blocks` of `rows` (a power of two >= sqrt(parts)) for the offset scan, so
 // that both the block sums every scan workgroup reads and the rows it walks
-// stay short.  Partitions are as large as still gives about four workgroups
-// per CU: 4096 pairs from 4M keys, 1024 for a 1M-key depth sort (4096 would
-// leave it 245 workgroups for 256 CUs).
+// stay short.  Partitions hold 2048 pairs from 2M keys (the 10M-pair tile
+// sort of a 1080p frame: 4096-pair partitions need 112 VGPRs, four waves per
+// SIMD, and measured 10 us per frame slower) and 1024 below (a 1M-key depth
+// sort in 4096-pair partitions would have 245 workgroups for 256 CUs).
 struct ScanPlan {
     uint32_t items, parts, rows, blocks, radix;
 };
 static ScanPlan scan_plan(uint32_t n, const DigitPlan& d) {
     ScanPlan s;
-    s.items = n >= (4096u << 10) ? 16u : n >= (2048u << 10) ? 8u : 4u;
+    s.items = n >= (2048u << 10) ? 8u : 4u;
     s.parts = div_up(n, (uint64_t)kThreads * s.items);
     s.rows = 16;
     while ((uint64_t)s.rows * s.rows < s.parts) s.rows *= 2;
@@ -195,8 +214,10 @@ __global__ __launch_bounds__(kThreads) void radix_upsweep_kernel(const uint32_t*
 // digit d: the totals of the digits below d plus the counts of digit d in the
 // partitions before q.  One workgroup of 1024 threads per block of `rows`
 // partitions; each digit column is shared by 1024 / radix thread groups, which
-// split the block sums and the block's rows between them, so a thread issues
-// its few loads together (a handful of memory round trips in all).
+// split the block sums and the block's rows between them.  A thread issues the
+// loads of its first 16 block sums and 16 rows together and keeps the rows in
+// registers for the stores, so a common sort (up to 16 of each per thread)
+// costs one memory round trip; larger ones loop over further chunks.
 constexpr int kScanThreads = 1024;
 __global__ __launch_bounds__(kScanThreads) void radix_scan_kernel(uint32_t* __restrict__ counts,
                                                                    const uint32_t* __restrict__ blk, uint32_t parts,
@@ -206,36 +227,35 @@ __global__ __launch_bounds__(kScanThreads) void radix_scan_kernel(uint32_t* __re
     __shared__ uint32_t s_before[kScanThreads];  // ... of the blocks before this one
     __shared__ uint32_t s_rows[kScanThreads];    // ... of this block's rows
     __shared__ uint32_t s_base[kRadix];
-    constexpr int kChunk = 16;
+    constexpr uint32_t kChunk = 16;
     const uint32_t tid = threadIdx.x, b = blockIdx.x;
     const uint32_t d = tid & (radix - 1u), grp = tid / radix, groups = kScanThreads / radix;
-    // block sums: group g reads blocks g, g + groups, ...
-    uint32_t all = 0, before = 0;
-    for (uint32_t q0 = grp; q0 < blocks; q0 += groups * kChunk) {
-        uint32_t x[kChunk];
-#pragma unroll
-        for (int i = 0; i < kChunk; i++) {
-            const uint32_t q = q0 + i * groups;
-            x[i] = q < blocks ? blk[(size_t)q * radix + d] : 0u;
-        }
-#pragma unroll
-        for (int i = 0; i < kChunk; i++) {
-            all += x[i];
-            before += q0 + i * groups < b ? x[i] : 0u;
-        }
-    }
-    // this block's rows: group g takes a contiguous run of them
+    // block sums: group g reads blocks g, g + groups, ...; this block's rows:
+    // group g takes a contiguous run of them
     const uint32_t r0 = b * rows, r1 = min(parts, r0 + rows);
     const uint32_t sub = (rows + groups - 1u) / groups;
     const uint32_t lo = min(r1, r0 + grp * sub), hi = min(r1, lo + sub);
-    uint32_t mine = 0;
-    for (uint32_t q0 = lo; q0 < hi; q0 += kChunk) {
-        uint32_t x[kChunk];
+    uint32_t xb[kChunk], xr[kChunk];
 #pragma unroll
-        for (int i = 0; i < kChunk; i++) x[i] = q0 + i < hi ? counts[(size_t)(q0 + i) * radix + d] : 0u;
-#pragma unroll
-        for (int i = 0; i < kChunk; i++) mine += x[i];
+    for (uint32_t i = 0; i < kChunk; i++) {
+        const uint32_t q = grp + i * groups;
+        xb[i] = q < blocks ? blk[(size_t)q * radix + d] : 0u;
     }
+#pragma unroll
+    for (uint32_t i = 0; i < kChunk; i++) xr[i] = lo + i < hi ? counts[(size_t)(lo + i) * radix + d] : 0u;
+    uint32_t all = 0, before = 0, mine = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < kChunk; i++) {
+        all += xb[i];
+        before += grp + i * groups < b ? xb[i] : 0u;
+        mine += xr[i];
+    }
+    for (uint32_t q = grp + kChunk * groups; q < blocks; q += groups) {
+        const uint32_t x = blk[(size_t)q * radix + d];
+        all += x;
+        before += q < b ? x : 0u;
+    }
+    for (uint32_t q = lo + kChunk; q < hi; q++) mine += counts[(size_t)q * radix + d];
     s_all[tid] = all;
     s_before[tid] = before;
     s_rows[tid] = mine;
@@ -253,15 +273,15 @@ __global__ __launch_bounds__(kScanThreads) void radix_scan_kernel(uint32_t* __re
     __syncthreads();
     uint32_t run = s_base[d];
     for (uint32_t g = 0; g < grp; g++) run += s_rows[g * radix + d];
-    for (uint32_t q0 = lo; q0 < hi; q0 += kChunk) {
-        uint32_t x[kChunk];
 #pragma unroll
-        for (int i = 0; i < kChunk; i++) x[i] = q0 + i < hi ? counts[(size_t)(q0 + i) * radix + d] : 0u;
-#pragma unroll
-        for (int i = 0; i < kChunk; i++) {
-            if (q0 + i < hi) counts[(size_t)(q0 + i) * radix + d] = run;
-            run += x[i];
-        }
+    for (uint32_t i = 0; i < kChunk; i++) {
+        if (lo + i < hi) counts[(size_t)(lo + i) * radix + d] = run;
+        run += xr[i];
+    }
+    for (uint32_t q = lo + kChunk; q < hi; q++) {
+        const uint32_t x = counts[(size_t)q * radix + d];
+        counts[(size_t)q * radix + d] = run;
+        run += x;
     }
 }
 
@@ -269,15 +289,20 @@ __global__ __launch_bounds__(kScanThreads) void radix_scan_kernel(uint32_t* __re
 
 // One workgroup per partition of 256 * ITEMS pairs: stable ranking inside the
 // partition, then every pair written to offs[part][digit] + its rank among the
-// partition's pairs of that digit, through LDS in digit order.
-template <bool FIRST, int ITEMS>
+// partition's pairs of that digit, through LDS in digit order.  With GATHER,
+// each output value v also writes gather_out[g] = gather_src[v]: the gather
+// loads are issued with the pair loads (their latency hides behind the
+// ranking) and go out through LDS like the values.
+template <bool FIRST, int ITEMS, bool GATHER>
 __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __restrict__ keys_in,
                                                              const uint32_t* __restrict__ vals_in,
                                                              uint32_t* __restrict__ keys_out,
                                                              uint32_t* __restrict__ vals_out, uint32_t n,
                                                              uint32_t shift, uint32_t digit_bits, uint32_t key_sub,
                                                              uint32_t key_cap, uint32_t radix,
-                                                             const uint32_t* __restrict__ offs) {
+                                                             const uint32_t* __restrict__ offs,
+                                                             const uint32_t* __restrict__ gather_src,
+                                                             uint32_t* __restrict__ gather_out) {
     __shared__ uint32_t s_wave_hist[kWaves][kRadix];
     __shared__ uint32_t s_local_start[kRadix];
     __shared__ uint32_t s_global_off[kRadix];
@@ -304,6 +329,11 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
         if (FIRST) kk = min(kk - key_sub, key_cap);
         k[j] = kk;
         v[j] = valid ? (vals_in ? vals_in[idx] : (uint32_t)idx) : 0u;
+    }
+    uint32_t gv[GATHER ? ITEMS : 1];
+    if (GATHER) {
+#pragma unroll
+        for (int j = 0; j < ITEMS; j++) gv[j] = wave_base + (uint64_t)j * 64 + lane < n ? gather_src[v[j]] : 0u;
     }
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 #pragma unroll
@@ -380,6 +410,20 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
         const uint32_t i = (uint32_t)(j * kThreads + tid);
         if (dst[j] != 0xFFFFFFFFu) vals_out[dst[j]] = s_buf[i];
     }
+    if (GATHER) {
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < ITEMS; j++) {
+            uint64_t idx = wave_base + (uint64_t)j * 64 + lane;
+            if (idx < n) s_buf[pos[j]] = gv[j];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < ITEMS; j++) {
+            const uint32_t i = (uint32_t)(j * kThreads + tid);
+            if (dst[j] != 0xFFFFFFFFu) gather_out[dst[j]] = s_buf[i];
+        }
+    }
 }
 
 // scratch layout: block sums blk[passes][blocks][radix] (zeroed before the
@@ -396,10 +440,23 @@ size_t radix_sort_zeroed_words(uint32_t n, uint32_t key_bits) {
     return (size_t)plan.passes * sp.blocks * sp.radix;
 }
 
+template <bool FIRST, int ITEMS>
+static void launch_digit_pass(bh_ctx* ctx, uint32_t parts, const uint32_t* src_k, const uint32_t* src_v,
+                              uint32_t* dk, uint32_t* dv, uint32_t n, uint32_t sh, uint32_t bits, uint32_t sub,
+                              uint32_t cap, uint32_t radix, const uint32_t* offs, const uint32_t* gs, uint32_t* go) {
+    if (go)
+        onesweep_kernel<FIRST, ITEMS, true><<<parts, kThreads, 0, ctx->stream>>>(src_k, src_v, dk, dv, n, sh, bits, sub,
+                                                                              cap, radix, offs, gs, go);
+    else
+        onesweep_kernel<FIRST, ITEMS, false><<<parts, kThreads, 0, ctx->stream>>>(src_k, src_v, dk, dv, n, sh, bits,
+                                                                               sub, cap, radix, offs, gs, go);
+}
+
 bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t* vals_in, uint32_t n,
                            uint32_t key_bits, uint32_t key_sub, uint32_t key_cap, uint32_t* keys_out,
                            uint32_t* vals_out, uint32_t* tmp_keys, uint32_t* tmp_vals, void* scratch,
-                           const char* tag, bool scratch_zeroed) {
+                           const char* tag, bool scratch_zeroed, const uint32_t* gather_src,
+                           uint32_t* gather_out) {
     const std::string up_name = std::string(tag) + "_up", scan_name = std::string(tag) + "_scan",
                       pass_name = std::string(tag) + "_onesweep";
     if (n == 0) return BH_OK;
@@ -419,6 +476,9 @@ bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t*
         uint32_t* pblk = blk + (size_t)p * sp.blocks * sp.radix;
         const uint32_t sh = plan.shift(p), bits = plan.bits(p);
         const uint32_t sub = p == 0 ? key_sub : 0u, cap = p == 0 ? key_cap : 0xFFFFFFFFu;
+        const bool last = p + 1 == plan.passes;
+        const uint32_t* gs = last ? gather_src : nullptr;
+        uint32_t* go = last ? gather_out : nullptr;
         const dim3 grid(sp.parts), block(kThreads);
 #define BH_SORT_PASS(I)                                                                                          \
     do {                                                                                                        \
@@ -439,16 +499,14 @@ bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t*
         {                                                                                                       \
             KernelTimer t(ctx, pass_name.c_str());                                                              \
             if (p == 0)                                                                                         \
-                onesweep_kernel<true, I><<<grid, block, 0, ctx->stream>>>(src_k, src_v, dk, dv, n, sh, bits,   \
-                                                                          sub, cap, sp.radix, offs);           \
+                launch_digit_pass<true, I>(ctx, sp.parts, src_k, src_v, dk, dv, n, sh, bits, sub, cap, sp.radix,  \
+                                           offs, gs, go);                                                       \
             else                                                                                                \
-                onesweep_kernel<false, I><<<grid, block, 0, ctx->stream>>>(src_k, src_v, dk, dv, n, sh, bits,  \
-                                                                           sub, cap, sp.radix, offs);          \
+                launch_digit_pass<false, I>(ctx, sp.parts, src_k, src_v, dk, dv, n, sh, bits, sub, cap,          \
+                                            sp.radix, offs, gs, go);                                            \
         }                                                                                                       \
     } while (0)
-        if (sp.items == 16)
-            BH_SORT_PASS(16);
-        else if (sp.items == 8)
+        if (sp.items == 8)
             BH_SORT_PASS(8);
         else
             BH_SORT_PASS(4);
@@ -489,61 +547,102 @@ void launch_gather_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t* v
     gather_pairs_kernel<<<div_up(n, 256), 256, 0, ctx->stream>>>(keys_in, vals_in, perm, n, keys_out, vals_out);
 }
 
-// ---- single-pass inclusive scan ----------------------------------------------------
+// ---- inclusive scan (reduce-then-scan) -------------------------------------------
 
-__global__ __launch_bounds__(kThreads) void scan_kernel(const uint32_t* __restrict__ in,
-                                                         const uint32_t* __restrict__ gather,
-                                                         uint32_t* __restrict__ out, uint32_t n, uint64_t* status,
-                                                         uint32_t* err) {
+// A partition is 256 threads x 4 * `chunks` consecutive values, with `chunks`
+// chosen so that there are at most 4096 partitions: one reduce kernel writes
+// each partition's sum, then the scan kernel adds the sums of the partitions
+// before it (at most 16 loads per thread, issued with the value loads) to the
+// in-partition scan.  The values are read twice, the second time mostly from
+// cache.  `out` may alias `in`: every value is read by the thread that writes
+// it, before it writes it.  (The forward's scan of tile counts in depth order
+// reads counts that the depth sort's last pass gathered, so no scan kernel
+// gathers: a gather in each of the two kernels measured 25 us at 1M splats.)
+struct ScanGeom {
+    uint32_t chunks, part, parts;
+};
+static ScanGeom scan_geom(uint32_t n) {
+    ScanGeom g;
+    g.chunks = std::max<uint32_t>(1u, div_up(n, (uint64_t)4096 * kThreads * 4));
+    g.part = kThreads * 4u * g.chunks;
+    g.parts = div_up(n, g.part);
+    return g;
+}
+
+__device__ __forceinline__ uint32_t scan_value(const uint32_t* in, uint64_t idx, uint32_t n) {
+    return idx < n ? in[idx] : 0u;
+}
+
+__global__ __launch_bounds__(kThreads) void scan_reduce_kernel(const uint32_t* in, uint32_t n, uint32_t chunks,
+                                                                uint32_t* __restrict__ sums) {
     __shared__ uint32_t s_tot[kWaves];
-    __shared__ uint32_t s_prefix;
-    const int tid = threadIdx.x;
-    const uint32_t part = blockIdx.x;
-    const uint64_t first = (uint64_t)part * kPart + (uint64_t)tid * kItems;
-    uint32_t x[kItems];
+    const uint64_t first = ((uint64_t)blockIdx.x * kThreads + threadIdx.x) * 4u * chunks;
     uint32_t run = 0;
+    for (uint32_t c = 0; c < chunks; c++) {
+        uint32_t x[4];
 #pragma unroll
-    for (int j = 0; j < kItems; j++) {
-        uint64_t idx = first + j;
-        uint32_t val = 0;
-        if (idx < n) val = gather ? in[gather[idx]] : in[idx];
-        run += val;
-        x[j] = run;
+        for (int j = 0; j < 4; j++) x[j] = scan_value(in, first + c * 4u + j, n);
+        run += x[0] + x[1] + x[2] + x[3];
     }
-    uint32_t block_total;
-    uint32_t thread_excl = block_exclusive_scan<kThreads>(run, s_tot, &block_total);
-    if (tid == 0) {
-        uint32_t excl = 0;
-        if (part == 0) {
-            status_store(status, kFlagPrefix | block_total);
-        } else {
-            status_store(status + part, kFlagAgg | block_total);
-            excl = look_back(status, part, 1, 0, err);
-            status_store(status + part, kFlagPrefix | (uint64_t)(excl + block_total));
+    uint32_t total;
+    (void)block_exclusive_scan<kThreads>(run, s_tot, &total);
+    if (threadIdx.x == 0) sums[blockIdx.x] = total;
+}
+
+__global__ __launch_bounds__(kThreads) void scan_down_kernel(const uint32_t* in, uint32_t* out, uint32_t n,
+                                                              uint32_t chunks, const uint32_t* __restrict__ sums) {
+    __shared__ uint32_t s_tot[kWaves];
+    const uint32_t part = blockIdx.x, tid = threadIdx.x;
+    const uint64_t first = ((uint64_t)part * kThreads + tid) * 4u * chunks;
+    // the sums of the partitions before this one (part < 4096: 16 per thread)
+    uint32_t prev[16];
+#pragma unroll
+    for (uint32_t i = 0; i < 16; i++) {
+        const uint32_t q = tid + i * kThreads;
+        prev[i] = q < part ? sums[q] : 0u;
+    }
+    uint32_t run = 0;
+    for (uint32_t c = 0; c < chunks; c++) {
+        uint32_t x[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) x[j] = scan_value(in, first + c * 4u + j, n);
+        run += x[0] + x[1] + x[2] + x[3];
+    }
+    uint32_t before = 0;
+#pragma unroll
+    for (int i = 0; i < 16; i++) before += prev[i];
+    uint32_t part_excl;
+    (void)block_exclusive_scan<kThreads>(before, s_tot, &part_excl);
+    uint32_t dummy;
+    uint32_t acc = part_excl + block_exclusive_scan<kThreads>(run, s_tot, &dummy);
+    for (uint32_t c = 0; c < chunks; c++) {
+        uint32_t x[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) x[j] = scan_value(in, first + c * 4u + j, n);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            acc += x[j];
+            if (first + c * 4u + j < n) out[first + c * 4u + j] = acc;
         }
-        s_prefix = excl;
-    }
-    __syncthreads();
-    const uint32_t add = s_prefix + thread_excl;
-#pragma unroll
-    for (int j = 0; j < kItems; j++) {
-        uint64_t idx = first + j;
-        if (idx < n) out[idx] = x[j] + add;
     }
 }
 
-size_t scan_scratch_bytes(uint32_t n) { return 64 + (size_t)div_up(n, kPart) * 8; }
+// at most 4096 partition sums for any n (so a caller may size it for an upper
+// bound of n)
+size_t scan_scratch_bytes(uint32_t) { return (size_t)4096 * 4; }
 
-size_t scan_zeroed_words(uint32_t n) { return (size_t)div_up(n, kPart) * 2; }
-
-bh_status inclusive_scan(bh_ctx* ctx, const uint32_t* in, const uint32_t* gather, uint32_t* out, uint32_t n,
-                         void* scratch, bool status_zeroed) {
+bh_status inclusive_scan(bh_ctx* ctx, const uint32_t* in, uint32_t* out, uint32_t n, void* scratch) {
     if (n == 0) return BH_OK;
-    uint32_t parts = div_up(n, kPart);
-    uint64_t* status = (uint64_t*)((char*)scratch + 64);
-    if (!status_zeroed) launch_fill_u32(ctx, (uint32_t*)status, 0u, scan_zeroed_words(n));
-    KernelTimer t(ctx, "scan");
-    scan_kernel<<<parts, kThreads, 0, ctx->stream>>>(in, gather, out, n, status, ctx->d_counters + 1);
+    const ScanGeom g = scan_geom(n);
+    uint32_t* sums = (uint32_t*)scratch;
+    {
+        KernelTimer t(ctx, "scan_reduce");
+        scan_reduce_kernel<<<g.parts, kThreads, 0, ctx->stream>>>(in, n, g.chunks, sums);
+    }
+    {
+        KernelTimer t(ctx, "scan");
+        scan_down_kernel<<<g.parts, kThreads, 0, ctx->stream>>>(in, out, n, g.chunks, sums);
+    }
     return check_launch(ctx, "scan");
 }
 

@@ -50,7 +50,7 @@ def test_radix_argsort_matches_stable_sort(gpu, n, bits):
     assert_bits_equal("vals", ov.cpu().numpy().view(np.uint32), ev)
 
 
-@pytest.mark.parametrize("n", [4, 255, 256, 257, 1024, 4095, 4096, 4097, 41000, 1 << 20, 3_000_001])
+@pytest.mark.parametrize("n", [4, 255, 256, 257, 1024, 4095, 4096, 4097, 41000, 1 << 20, 3_000_001, 9_000_001])
 def test_prefix_sum_closed_form(gpu, n):
     import torch
     from brush_amd import _lib
