@@ -165,51 +165,58 @@ __global__ __launch_bounds__(64) void rasterize_backward_kernel(
                 if (!wave_live) break;
                 continue;
             }
-            // staged colours: max(c, 0) in value, the c >= 0 gate in the sign bit
-            const float cr = cr4.z, cgc = cr4.w, cb = bd.x;
-            const float vis = ae * sw;
             float g[12];
-            g[5] = contrib && colour_gate(cr) ? vis * vox : 0.0f;
-            g[6] = contrib && colour_gate(cgc) ? vis * voy : 0.0f;
-            g[7] = contrib && colour_gate(cb) ? vis * voz : 0.0f;
-            // gradient-only quantities: hardware reciprocal / sqrt (1 ulp)
-            const float ra = __builtin_amdgcn_rcpf(1.0f - ae);
-            const float dot_rgb = ((sw * cr - sx) * vox + (sw * cgc - sy) * voy + (sw * cb - sz) * voz) * ra;
-            const float v_ae = dot_rgb + vow * ra;
-            // with the hard cutoff the weight is a step and its derivative 0.
-            // The position, conic, opacity and refine lanes are gated on
-            // contributing and unclamped (o G <= 0.999) pairs.  Lanes outside
-            // `maybe` may hold any alpha and gaussian: a sigma far below zero
-            // (rounding on a nearly singular conic) overflows the exponential's
-            // range reduction into inf or a negative value.  So the selects sit
-            // on v_sigma and on the opacity lane; a zero v_sigma then zeroes the
-            // position, conic and refine lanes (up to the sign of a zero), whose
-            // other factors dx, dy and the conic (|c| <= 10: every 2D covariance
-            // carries a blur of at least 0.1 on its diagonal) are finite.
-            const bool unclamped = opac * gaussian <= 0.999f;
-            const bool gate = contrib && unclamped;
-            const float v_alpha = SMOOTH ? v_ae * (w + alpha * cutoff_weight_deriv(alpha)) : v_ae * w;
-            const float v_sigma = gate ? -alpha * v_alpha : 0.0f;
-            const float vxy_x = v_sigma * (conic.c00 * dx + conic.c01 * dy);
-            const float vxy_y = v_sigma * (conic.c01 * dx + conic.c11 * dy);
-            g[2] = 0.5f * v_sigma * dx * dx;
-            g[3] = v_sigma * dx * dy;
-            g[4] = 0.5f * v_sigma * dy * dy;
-            g[0] = vxy_x;
-            g[1] = vxy_y;
-            g[8] = gate ? v_alpha * gaussian : 0.0f;
-            g[9] = REFINE ? __builtin_amdgcn_sqrtf(vxy_x * img_wf * vxy_x * img_wf + vxy_y * img_hf * vxy_y * img_hf) *
-                                inv_final_a
-                          : 0.0f;
-            g[10] = DEPTH && contrib ? vis * vod : 0.0f;
-            g[11] = 0.0f;
-            if (contrib) {
-                sx = sx - vis * cr;
-                sy = sy - vis * cgc;
-                sz = sz - vis * cb;
-                if (DEPTH) sd = sd - vis * bd.y;
-                sw = next_t;
+            {
+#pragma clang fp contract(fast)
+                // Gradient-only arithmetic and the remaining-colour state, which
+                // feeds only gradients: products and sums fuse into FMAs here.
+                // The replay's decisions above (alpha, transmittance, saturation)
+                // stay uncontracted, bit for bit the forward's.
+                // staged colours: max(c, 0) in value, the c >= 0 gate in the sign bit
+                const float cr = cr4.z, cgc = cr4.w, cb = bd.x;
+                const float vis = ae * sw;
+                g[5] = contrib && colour_gate(cr) ? vis * vox : 0.0f;
+                g[6] = contrib && colour_gate(cgc) ? vis * voy : 0.0f;
+                g[7] = contrib && colour_gate(cb) ? vis * voz : 0.0f;
+                // gradient-only quantities: hardware reciprocal / sqrt (1 ulp)
+                const float ra = __builtin_amdgcn_rcpf(1.0f - ae);
+                const float dot_rgb = ((sw * cr - sx) * vox + (sw * cgc - sy) * voy + (sw * cb - sz) * voz) * ra;
+                const float v_ae = dot_rgb + vow * ra;
+                // with the hard cutoff the weight is a step and its derivative 0.
+                // The position, conic, opacity and refine lanes are gated on
+                // contributing and unclamped (o G <= 0.999) pairs.  Lanes outside
+                // `maybe` may hold any alpha and gaussian: a sigma far below zero
+                // (rounding on a nearly singular conic) overflows the exponential's
+                // range reduction into inf or a negative value.  So the selects sit
+                // on v_sigma and on the opacity lane; a zero v_sigma then zeroes the
+                // position, conic and refine lanes (up to the sign of a zero), whose
+                // other factors dx, dy and the conic (|c| <= 10: every 2D covariance
+                // carries a blur of at least 0.1 on its diagonal) are finite.
+                const bool unclamped = opac * gaussian <= 0.999f;
+                const bool gate = contrib && unclamped;
+                const float v_alpha = SMOOTH ? v_ae * (w + alpha * cutoff_weight_deriv(alpha)) : v_ae * w;
+                const float v_sigma = gate ? -alpha * v_alpha : 0.0f;
+                const float vxy_x = v_sigma * (conic.c00 * dx + conic.c01 * dy);
+                const float vxy_y = v_sigma * (conic.c01 * dx + conic.c11 * dy);
+                g[2] = 0.5f * v_sigma * dx * dx;
+                g[3] = v_sigma * dx * dy;
+                g[4] = 0.5f * v_sigma * dy * dy;
+                g[0] = vxy_x;
+                g[1] = vxy_y;
+                g[8] = gate ? v_alpha * gaussian : 0.0f;
+                g[9] = REFINE ? __builtin_amdgcn_sqrtf(vxy_x * img_wf * vxy_x * img_wf + vxy_y * img_hf * vxy_y * img_hf) *
+                                    inv_final_a
+                              : 0.0f;
+                g[10] = DEPTH && contrib ? vis * vod : 0.0f;
+                g[11] = 0.0f;
+                if (contrib) {
+                    sx = sx - vis * cr;
+                    sy = sy - vis * cgc;
+                    sz = sz - vis * cb;
+                    if (DEPTH) sd = sd - vis * bd.y;
+                }
             }
+            if (contrib) sw = next_t;
             // whole-wave sums: rows of q0 hold lanes 0, 2, 1, 3; of q1 lanes 4, 6,
             // 5, 7; of q2 lanes 8, 10, 9, 11 (8, 8, 9, 9 without depth)
             const float q0 = row_sum_last_lane(psum16(psum32(g[0], g[1]), psum32(g[2], g[3])));
