@@ -218,15 +218,19 @@ __global__ __launch_bounds__(64) void rasterize_backward_kernel(
             }
             if (contrib) sw = next_t;
             // whole-wave sums: rows of q0 hold lanes 0, 2, 1, 3; of q1 lanes 4, 6,
-            // 5, 7; of q2 lanes 8, 10, 9, 11 (8, 8, 9, 9 without depth)
+            // 5, 7; of q2 lanes 8, 10, 9, 11 (8, 8, 9, 9 without depth, of which
+            // one lane each is added: two lanes of one atomic instruction on one
+            // address measured 124 us per frame slower)
             const float q0 = row_sum_last_lane(psum16(psum32(g[0], g[1]), psum32(g[2], g[3])));
             const float q1 = row_sum_last_lane(psum16(psum32(g[4], g[5]), psum32(g[6], g[7])));
             const float p4 = psum32(g[8], g[9]);
             const float q2 = row_sum_last_lane(DEPTH ? psum16(p4, psum32(g[10], g[11])) : psum16(p4, p4));
+            // the splat's gradient row: wave-uniform, so its address is scalar
+            const uint32_t cid = __builtin_amdgcn_readfirstlane(s_cid[j]);
+            float* dst = v_combined + (size_t)cid * kNG;
             if ((lane & 15u) == 15u) {
                 const uint32_t row = lane >> 4;
                 const uint32_t k = (row & 1u) * 2u + (row >> 1);
-                float* dst = v_combined + (size_t)s_cid[j] * kNG;
                 unsafeAtomicAdd(dst + k, q0);
                 unsafeAtomicAdd(dst + 4u + k, q1);
                 const bool want = DEPTH ? (k == 0u || (k == 1u && REFINE) || k == 2u) : (k == 0u || (row == 2u && REFINE));
