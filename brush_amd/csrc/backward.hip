@@ -228,13 +228,19 @@ __global__ __launch_bounds__(64) void rasterize_backward_kernel(
             // the splat's gradient row: wave-uniform, so its address is scalar
             const uint32_t cid = __builtin_amdgcn_readfirstlane(s_cid[j]);
             float* dst = v_combined + (size_t)cid * kNG;
-            if ((lane & 15u) == 15u) {
+            // one atomic instruction for all three sums: q1's and q2's row totals
+            // move from lane 15 of each row to lanes 14 and 13 (DPP row_shl),
+            // so lanes 13-15 of a row add to three distinct words of the row
+            const float q1s = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(q1), 0x101, 0xF, 0xF, true));
+            const float q2s = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(q2), 0x102, 0xF, 0xF, true));
+            const uint32_t r = lane & 15u;
+            if (r >= 13u) {
                 const uint32_t row = lane >> 4;
                 const uint32_t k = (row & 1u) * 2u + (row >> 1);
-                unsafeAtomicAdd(dst + k, q0);
-                unsafeAtomicAdd(dst + 4u + k, q1);
                 const bool want = DEPTH ? (k == 0u || (k == 1u && REFINE) || k == 2u) : (k == 0u || (row == 2u && REFINE));
-                if (want) unsafeAtomicAdd(dst + (DEPTH ? 8u + k : 8u + (row >> 1)), q2);
+                const uint32_t off = r == 15u ? k : r == 14u ? 4u + k : (DEPTH ? 8u + k : 8u + (row >> 1));
+                const float val = r == 15u ? q0 : r == 14u ? q1s : q2s;
+                if (r != 13u || want) unsafeAtomicAdd(dst + off, val);
             }
             wave_live = __ballot(sw > 1.0e-4f) != 0ull;
             if (!wave_live) break;
