@@ -321,7 +321,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
-              "(the rasterizer path is single-GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
+              "(the rasterizer path is single-GPU: several GPUs would each render their own views "
+              "of a replicated scene and all-reduce the splat gradients)", file=sys.stderr)
         sys.exit(2)
 
     if args.workload == "ply":
