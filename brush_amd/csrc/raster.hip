@@ -94,6 +94,15 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
     const uint32_t px = ox + (lane & 7u), py = oy + (lane >> 3);
     const bool inside = px < img_w && py < img_h;
     const uint32_t lo = off_pre[2 * tile], hi = off_pre[2 * tile + 1];
+    // Long blocks first: the wave priority rises with the tile's candidate
+    // count (work is concentrated in few tiles; see the backward kernel).
+    const uint32_t len = hi - lo;
+    if (len >= 6144u)
+        __builtin_amdgcn_s_setprio(3);
+    else if (len >= 3072u)
+        __builtin_amdgcn_s_setprio(2);
+    else if (len >= 1024u)
+        __builtin_amdgcn_s_setprio(1);
     const float pcx = (float)px + 0.5f, pcy = (float)py + 0.5f;
     const float bx0 = (float)ox + 0.5f, by0 = (float)oy + 0.5f;
     float t_acc = 1.0f, pr = 0.0f, pg = 0.0f, pb = 0.0f, pd = 0.0f;
