@@ -504,8 +504,14 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
         launch_fill_u32(ctx, cgids, 0u, 1);
     }
     launch_tile_offsets(ctx, tile_ids, m, num_tiles, off_pre, true);
+    // the blend kernel starts the tiles with the most candidates first
+    uint32_t* order = nullptr;
+    if (m) {
+        BH_STRY(ws.get(&order, num_tiles));
+        launch_tile_order(ctx, off_pre, num_tiles, order);
+    }
     launch_rasterize(ctx, u.img_w, u.img_h, u.tile_bw, u.tile_bh, background, num_visible, projected, cgids, gfc,
-                     off_pre, flags, out_img, visible, tile_offsets, true);
+                     off_pre, order, flags, out_img, visible, tile_offsets, true);
     BH_STRY(check_launch(ctx, "rasterize"));
 #undef BH_STRY
 
@@ -560,7 +566,7 @@ bh_status bh_rasterize_backward(bh_ctx* ctx, const float* out_img, const float* 
     launch_fill_u32(ctx, (uint32_t*)v_combined, 0u, (uint64_t)std::max<uint32_t>(num_visible, 1) * 11);
     if (num_visible)
         launch_rasterize_backward(ctx, img_w, img_h, tbw, tbh, background, num_visible, out_img, projected,
-                                  compact_gid_from_isect, tile_offsets, v_output, flags, nullptr, v_combined);
+                                  compact_gid_from_isect, tile_offsets, v_output, flags, nullptr, nullptr, v_combined);
     return check_launch(ctx, "rasterize_backward");
 }
 
@@ -609,10 +615,15 @@ bh_status bh_render_backward(bh_ctx* ctx, const bh_fwd_state* state, const float
     launch_fill_u32(ctx, (uint32_t*)rows, 0u, (uint64_t)n * 11);
     const uint32_t raster_flags =
         (flags & (BH_FLAG_SMOOTH_CUTOFF | BH_FLAG_REFINE_WEIGHT | BH_FLAG_RENDER_DEPTH)) | (in.flags & BH_FLAG_TILE_16X8);
-    if (in.num_visible)
+    if (in.num_visible) {
+        // the longest tiles (most splats the forward blended) start first
+        uint32_t* order;
+        BH_TRY(ws.get(&order, in.num_tiles));
+        launch_tile_order(ctx, tile_offsets, in.num_tiles, order);
         launch_rasterize_backward(ctx, in.img_w, in.img_h, in.tile_bw, in.tile_bh, background, in.num_visible, out_img,
                                   in.projected, in.compact_gid_from_isect, tile_offsets, v_output, raster_flags,
-                                  in.global_from_compact_gid, rows);
+                                  in.global_from_compact_gid, order, rows);
+    }
     BH_TRY(check_launch(ctx, "rasterize_backward"));
     launch_project_backward(ctx, in.uniforms, transforms, sh_coeffs, raw_opacities, nullptr, n, in.sh_degree,
                             (in.flags & BH_FLAG_MIP) != 0, rows, v_transforms, v_coeffs, v_raw_opac, v_refine);

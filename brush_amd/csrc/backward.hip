@@ -75,7 +75,7 @@ __global__ __launch_bounds__(64) void rasterize_backward_kernel(
     uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t num_tiles, float bg_r, float bg_g, float bg_b,
     uint32_t num_visible, const float* __restrict__ out_img, const float* __restrict__ projected,
     const uint32_t* __restrict__ cgids, const uint32_t* __restrict__ offsets, const float* __restrict__ v_output,
-    const uint32_t* __restrict__ row_of, float* __restrict__ v_combined) {
+    const uint32_t* __restrict__ row_of, const uint32_t* __restrict__ order, float* __restrict__ v_combined) {
     constexpr uint32_t CH = DEPTH ? 5u : 4u;
     __shared__ float4 s_xyco[64];  // x, y, conic c00, c01
     __shared__ float4 s_crgb[64];  // conic c11, opacity, r, g (staged_colour)
@@ -85,6 +85,7 @@ __global__ __launch_bounds__(64) void rasterize_backward_kernel(
     uint32_t tile, blk;
     block_of_workgroup<TH>(blockIdx.x, tile, blk);
     if (tile >= num_tiles) return;
+    if (order) tile = order[tile];
     const uint32_t lane = threadIdx.x;
     const uint32_t ox = (tile % tile_bw) * 16u + (blk & 1u) * 8u;
     const uint32_t oy = (tile / tile_bw) * (uint32_t)TH + (blk >> 1) * 8u;
@@ -263,7 +264,7 @@ __global__ __launch_bounds__(64) void rasterize_backward_kernel(
 void launch_rasterize_backward(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,
                                const float* bg, uint32_t num_visible, const float* out_img, const float* projected, const uint32_t* cgids,
                                const uint32_t* offsets, const float* v_output, uint32_t flags,
-                               const uint32_t* row_of, float* v_combined) {
+                               const uint32_t* row_of, const uint32_t* order, float* v_combined) {
     const uint32_t num_tiles = tile_bw * tile_bh;
     if (num_tiles == 0 || num_visible == 0) return;
     const bool smooth = (flags & BH_FLAG_SMOOTH_CUTOFF) != 0;
@@ -275,7 +276,7 @@ void launch_rasterize_backward(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint
 #define BH_RB_T(S, R, D, T)                                                                                      \
     rasterize_backward_kernel<S, R, D, T><<<groups, 64, 0, ctx->stream>>>(                                       \
         img_w, img_h, tile_bw, num_tiles, bg[0], bg[1], bg[2], num_visible, out_img, projected, cgids, offsets, \
-        v_output, row_of, v_combined)
+        v_output, row_of, order, v_combined)
 #define BH_RB(S, R, D) \
     do {               \
         if (fine)      \

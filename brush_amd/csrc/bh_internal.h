@@ -160,16 +160,19 @@ void launch_map_intersects(bh_ctx* ctx, uint32_t tile_bw, uint32_t tile_bh, uint
 // raster.hip
 void launch_tile_offsets(bh_ctx* ctx, const uint32_t* tile_ids, uint32_t m, uint32_t num_tiles,
                          uint32_t* offsets, bool zeroed = false);
+// order[num_tiles]: the tiles by descending load (launch_tile_order), or
+// nullptr for tile-id order.
+void launch_tile_order(bh_ctx* ctx, const uint32_t* offsets, uint32_t num_tiles, uint32_t* order);
 void launch_rasterize(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,
                       const float* bg, uint32_t num_visible, const float* projected, const uint32_t* cgids, const uint32_t* gfc,
-                      const uint32_t* off_pre, uint32_t flags, void* out_img, float* visible,
+                      const uint32_t* off_pre, const uint32_t* order, uint32_t flags, void* out_img, float* visible,
                       uint32_t* off_post, bool off_post_zeroed = false);
 
 // backward.hip
 void launch_rasterize_backward(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,
                                const float* bg, uint32_t num_visible, const float* out_img, const float* projected,
                                const uint32_t* cgids, const uint32_t* offsets, const float* v_output,
-                               uint32_t flags, const uint32_t* row_of, float* v_combined);
+                               uint32_t flags, const uint32_t* row_of, const uint32_t* order, float* v_combined);
 void launch_invert_permutation(bh_ctx* ctx, const uint32_t* gfc, uint32_t num_visible, uint32_t n,
                                uint32_t* compact_from_global);
 // compact_from_global == nullptr: v_combined is indexed by global id.

@@ -72,6 +72,51 @@ __device__ __forceinline__ void raster_block_of_workgroup(uint32_t g, uint32_t& 
     blk = slot % BPT;
 }
 
+// Dispatch order of the tiles: by descending splat count, in buckets of a
+// quarter octave (exact order inside a bucket is not needed), so the longest
+// blocks start first.  One workgroup; order[i] is the i-th tile to dispatch.
+__device__ __forceinline__ uint32_t tile_load_bucket(const uint32_t* __restrict__ offsets, uint32_t t) {
+    const uint32_t lo = offsets[2 * t], hi = offsets[2 * t + 1];
+    const uint32_t c = hi > lo ? hi - lo : 0u;
+    uint32_t b = c;
+    if (c >= 4u) {
+        const uint32_t msb = 31u - (uint32_t)__builtin_clz(c);
+        b = msb * 4u + ((c >> (msb - 2u)) & 3u);
+    }
+    return 127u - min(b, 127u);
+}
+
+__global__ __launch_bounds__(1024) void tile_order_kernel(const uint32_t* __restrict__ offsets, uint32_t num_tiles,
+                                                          uint32_t* __restrict__ order) {
+    __shared__ uint32_t s_cur[128];
+    const uint32_t t = threadIdx.x;
+    if (t < 128u) s_cur[t] = 0u;
+    __syncthreads();
+    for (uint32_t i = t; i < num_tiles; i += 1024u) atomicAdd(&s_cur[tile_load_bucket(offsets, i)], 1u);
+    __syncthreads();
+    if (t < 64u) {
+        // exclusive scan of the 128 bucket sizes, two per lane
+        const uint32_t a = s_cur[2u * t], b = s_cur[2u * t + 1u];
+        uint32_t x = a + b;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t y = __shfl_up(x, o, 64);
+            if ((int)t >= o) x += y;
+        }
+        const uint32_t excl = x - a - b;
+        s_cur[2u * t] = excl;
+        s_cur[2u * t + 1u] = excl + a;
+    }
+    __syncthreads();
+    for (uint32_t i = t; i < num_tiles; i += 1024u) order[atomicAdd(&s_cur[tile_load_bucket(offsets, i)], 1u)] = i;
+}
+
+void launch_tile_order(bh_ctx* ctx, const uint32_t* offsets, uint32_t num_tiles, uint32_t* order) {
+    if (num_tiles == 0) return;
+    KernelTimer t(ctx, "tile_order");
+    tile_order_kernel<<<1, 1024, 0, ctx->stream>>>(offsets, num_tiles, order);
+}
+
 template <bool BWD_INFO, bool SMOOTH, bool DEPTH, int TH>
 __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t img_h, uint32_t tile_bw,
                                                         uint32_t num_tiles, float bg_r, float bg_g, float bg_b,
@@ -79,6 +124,7 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
                                                         const uint32_t* __restrict__ cgids,
                                                         const uint32_t* __restrict__ gfc,
                                                         const uint32_t* __restrict__ off_pre,
+                                                        const uint32_t* __restrict__ order,
                                                         void* __restrict__ out_img, float* __restrict__ visible,
                                                         uint32_t* __restrict__ off_post) {
     __shared__ float4 s_xyco[64];  // x, y, conic c00, conic c01
@@ -88,6 +134,7 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
     uint32_t tile, blk;
     raster_block_of_workgroup<TH>(blockIdx.x, tile, blk);
     if (tile >= num_tiles) return;
+    if (order) tile = order[tile];
     const uint32_t lane = threadIdx.x;
     const uint32_t ox = (tile % tile_bw) * 16u + (blk & 1u) * 8u;
     const uint32_t oy = (tile / tile_bw) * (uint32_t)TH + (blk >> 1) * 8u;
@@ -206,8 +253,8 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
 
 void launch_rasterize(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,
                       const float* bg, uint32_t num_visible, const float* projected, const uint32_t* cgids, const uint32_t* gfc,
-                      const uint32_t* off_pre, uint32_t flags, void* out_img, float* visible, uint32_t* off_post,
-                      bool off_post_zeroed) {
+                      const uint32_t* off_pre, const uint32_t* order, uint32_t flags, void* out_img, float* visible,
+                      uint32_t* off_post, bool off_post_zeroed) {
     const uint32_t num_tiles = tile_bw * tile_bh;
     if (num_tiles == 0) return;
     const bool bwd = (flags & BH_FLAG_BWD_INFO) != 0;
@@ -221,7 +268,7 @@ void launch_rasterize(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile
     KernelTimer t(ctx, "rasterize");
 #define BH_RASTER_T(B, S, D, T)                                                                                    \
     rasterize_kernel<B, S, D, T><<<groups, 64, 0, ctx->stream>>>(img_w, img_h, tile_bw, num_tiles, bg[0], bg[1], \
-                                                                 bg[2], nv, projected, cgids, gfc, off_pre,       \
+                                                                 bg[2], nv, projected, cgids, gfc, off_pre, order, \
                                                                  out_img, visible, off_post)
 #define BH_RASTER(B, S, D) \
     do {                   \
