@@ -158,6 +158,9 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
 
     for (uint32_t batch = lo; batch < hi; batch += 64u) {
         if (__ballot(!done) == 0ull) break;
+        // a block still blending after 256 candidates is one of the long ones
+        // whatever its candidate count said: top priority from here on
+        if (batch - lo == 256u) __builtin_amdgcn_s_setprio(3);
         const uint32_t cnt = min(64u, hi - batch);
         bool touch = false;
         uint32_t my_c = 0;
