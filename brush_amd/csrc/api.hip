@@ -612,14 +612,15 @@ bh_status bh_render_backward(bh_ctx* ctx, const bh_fwd_state* state, const float
     Scratch ws(ctx);
     float* rows;
     BH_TRY(ws.get(&rows, (size_t)n * 11));
-    launch_fill_u32(ctx, (uint32_t*)rows, 0u, (uint64_t)n * 11);
     const uint32_t raster_flags =
         (flags & (BH_FLAG_SMOOTH_CUTOFF | BH_FLAG_REFINE_WEIGHT | BH_FLAG_RENDER_DEPTH)) | (in.flags & BH_FLAG_TILE_16X8);
+    if (!in.num_visible) launch_fill_u32(ctx, (uint32_t*)rows, 0u, (uint64_t)n * 11);
     if (in.num_visible) {
-        // the longest tiles (most splats the forward blended) start first
+        // the longest tiles (most splats the forward blended) start first;
+        // the order is computed while the gradient rows are zeroed
         uint32_t* order;
         BH_TRY(ws.get(&order, in.num_tiles));
-        launch_tile_order(ctx, tile_offsets, in.num_tiles, order);
+        launch_zero_and_tile_order(ctx, (uint32_t*)rows, (uint64_t)n * 11, tile_offsets, in.num_tiles, order);
         launch_rasterize_backward(ctx, in.img_w, in.img_h, in.tile_bw, in.tile_bh, background, in.num_visible, out_img,
                                   in.projected, in.compact_gid_from_isect, tile_offsets, v_output, raster_flags,
                                   in.global_from_compact_gid, order, rows);

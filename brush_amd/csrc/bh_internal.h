@@ -163,6 +163,9 @@ void launch_tile_offsets(bh_ctx* ctx, const uint32_t* tile_ids, uint32_t m, uint
 // order[num_tiles]: the tiles by descending load (launch_tile_order), or
 // nullptr for tile-id order.
 void launch_tile_order(bh_ctx* ctx, const uint32_t* offsets, uint32_t num_tiles, uint32_t* order);
+// p[0, words) = 0 (p 16-byte aligned) and the tile order, in one launch.
+void launch_zero_and_tile_order(bh_ctx* ctx, uint32_t* p, uint64_t words, const uint32_t* offsets,
+                                uint32_t num_tiles, uint32_t* order);
 void launch_rasterize(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,
                       const float* bg, uint32_t num_visible, const float* projected, const uint32_t* cgids, const uint32_t* gfc,
                       const uint32_t* off_pre, const uint32_t* order, uint32_t flags, void* out_img, float* visible,

@@ -86,8 +86,8 @@ __device__ __forceinline__ uint32_t tile_load_bucket(const uint32_t* __restrict_
     return 127u - min(b, 127u);
 }
 
-__global__ __launch_bounds__(1024) void tile_order_kernel(const uint32_t* __restrict__ offsets, uint32_t num_tiles,
-                                                          uint32_t* __restrict__ order) {
+__device__ __forceinline__ void tile_order_block(const uint32_t* __restrict__ offsets, uint32_t num_tiles,
+                                                 uint32_t* __restrict__ order) {
     __shared__ uint32_t s_cur[128];
     const uint32_t t = threadIdx.x;
     if (t < 128u) s_cur[t] = 0u;
@@ -111,10 +111,45 @@ __global__ __launch_bounds__(1024) void tile_order_kernel(const uint32_t* __rest
     for (uint32_t i = t; i < num_tiles; i += 1024u) order[atomicAdd(&s_cur[tile_load_bucket(offsets, i)], 1u)] = i;
 }
 
+__global__ __launch_bounds__(1024) void tile_order_kernel(const uint32_t* __restrict__ offsets, uint32_t num_tiles,
+                                                          uint32_t* __restrict__ order) {
+    tile_order_block(offsets, num_tiles, order);
+}
+
+// The tile order in the first workgroup (dispatched first, so it starts at
+// once) while the others zero p[0, words): the backward's gradient rows and
+// its order are independent, and the order's single workgroup (~12 us of
+// latency) runs beside the fill.
+__global__ __launch_bounds__(1024) void zero_and_tile_order_kernel(uint32_t* __restrict__ p, uint64_t words,
+                                                                   const uint32_t* __restrict__ offsets,
+                                                                   uint32_t num_tiles, uint32_t* __restrict__ order) {
+    if (blockIdx.x == 0u) {
+        tile_order_block(offsets, num_tiles, order);
+        return;
+    }
+    const uint64_t b = blockIdx.x - 1u;
+    const uint64_t stride = (uint64_t)(gridDim.x - 1u) * 1024u;
+    const uint64_t quads = words / 4u;
+    uint4* q = reinterpret_cast<uint4*>(p);
+    for (uint64_t i = b * 1024u + threadIdx.x; i < quads; i += stride) q[i] = make_uint4(0u, 0u, 0u, 0u);
+    for (uint64_t i = quads * 4u + b * 1024u + threadIdx.x; i < words; i += stride) p[i] = 0u;
+}
+
 void launch_tile_order(bh_ctx* ctx, const uint32_t* offsets, uint32_t num_tiles, uint32_t* order) {
     if (num_tiles == 0) return;
     KernelTimer t(ctx, "tile_order");
     tile_order_kernel<<<1, 1024, 0, ctx->stream>>>(offsets, num_tiles, order);
+}
+
+void launch_zero_and_tile_order(bh_ctx* ctx, uint32_t* p, uint64_t words, const uint32_t* offsets,
+                                uint32_t num_tiles, uint32_t* order) {
+    if (num_tiles == 0) {
+        launch_fill_u32(ctx, p, 0u, words);
+        return;
+    }
+    KernelTimer t(ctx, "zero_and_tile_order");
+    const uint32_t fill_blocks = (uint32_t)std::min<uint64_t>((words / 4u + 1023u) / 1024u + 1u, 1024u);
+    zero_and_tile_order_kernel<<<fill_blocks + 1u, 1024, 0, ctx->stream>>>(p, words, offsets, num_tiles, order);
 }
 
 template <bool BWD_INFO, bool SMOOTH, bool DEPTH, int TH>
