@@ -128,6 +128,8 @@ __device__ __forceinline__ void write_row_from_coeffs(const bh_project_uniforms&
     dst[0] = make_float4(p.m.x, p.m.y, p.conic.c00, p.conic.c01);
     dst[1] = make_float4(p.conic.c11, p.opac, r, g);
     dst[2] = make_float4(b, p.depth, 0.0f, 0.0f);
+    // the whole 64-byte slot: 48 of 64 bytes per slot cost partial-line writes
+    dst[3] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 }
 
 template <bool MIP, int CAM, int TH, int DEG>
