@@ -66,15 +66,15 @@ def algorithmic_bytes(name: str, n: int, v: int, m: int, m_post: int, t: int, p:
     written once (counts per launch; sort passes are separate launches)."""
     if name == "project_forward":
         # transforms+opac in; count, radius, depth key out; the visible
-        # splats' SH rows in and their whole 64-B row slots out
-        return 44.0 * n + 12.0 * n + v * (12 * c + 64)
+        # splats' SH rows in and their 48-B row slots out
+        return 44.0 * n + 12.0 * n + v * (12 * c + 48)
     if name == "project_visible":
         # (only without intersections; otherwise map_intersects orders the rows)
         return v * (4 + 48) + v * (40 + 4)               # gid + row slot in; ordered row, depth out
     if name == "scan":
         return 12.0 * v                                  # gid + gathered count in, cum out
     if name == "map_intersects":
-        # gid + global-id row slot (48 B of 64) + cum in; ordered row + depth out; (tile, id) pairs out
+        # gid + global-id row slot (48 B) + cum in; ordered row + depth out; (tile, id) pairs out
         return (4.0 + 48.0 + 8.0) * v + 44.0 * v + 8.0 * m
     if name == "tile_offsets":
         return 4.0 * m + 8.0 * t

@@ -436,7 +436,7 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
         uint32_t *depth_keys, *partials;
         BH_STRY(ws.get(&depth_keys, num_splats));
         BH_STRY(ws.get((char**)&partials, project_partials_bytes(num_splats)));
-        BH_STRY(ws.get(&vis_rows, (size_t)num_splats * 16));
+        BH_STRY(ws.get(&vis_rows, (size_t)num_splats * 12));
         launch_project_forward(ctx, u, transforms, raw_opacities, sh_coeffs, sh_degree, num_splats, mip, tile_h, counts,
                                max_radius, depth_keys, vis_rows, partials, ctx->d_counters);
         BH_STRY(check_launch(ctx, "project_forward"));

@@ -108,7 +108,9 @@ __device__ __forceinline__ void load_sh_row(const float* __restrict__ sh, uint32
 }
 
 // A visible splat's projected row (project_visible.rs:22-89) in its global-id
-// slot: 16 floats, x y c00 c01 | c11 opac r g | b depth - - | - - - -.
+// slot: 12 floats, x y c00 c01 | c11 opac r g | b depth - -.  Slots are packed
+// (48 bytes): a wave's stores cover whole lines, where 48 bytes of a 64-byte
+// slot cost partial-line writes.
 // project_forward reads the parameters and SH rows in global-id order
 // (coalesced), so the depth-ordered rows cost one aligned 64-byte gather each
 // (in map_intersects) instead of three scattered parameter reads.  The SH row
@@ -124,12 +126,10 @@ __device__ __forceinline__ void write_row_from_coeffs(const bh_project_uniforms&
     const float r = bh_clampf(bh_is_finite(cr) ? cr : 0.0f, -100.0f, 100.0f);
     const float g = bh_clampf(bh_is_finite(cg) ? cg : 0.0f, -100.0f, 100.0f);
     const float b = bh_clampf(bh_is_finite(cb) ? cb : 0.0f, -100.0f, 100.0f);
-    float4* dst = rows + (size_t)gid * 4;
+    float4* dst = rows + (size_t)gid * 3;
     dst[0] = make_float4(p.m.x, p.m.y, p.conic.c00, p.conic.c01);
     dst[1] = make_float4(p.conic.c11, p.opac, r, g);
     dst[2] = make_float4(b, p.depth, 0.0f, 0.0f);
-    // the whole 64-byte slot: 48 of 64 bytes per slot cost partial-line writes
-    dst[3] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 }
 
 template <bool MIP, int CAM, int TH, int DEG>
@@ -321,7 +321,7 @@ __global__ __launch_bounds__(256) void project_gather_kernel(const float4* __res
     const uint32_t c = blockIdx.x * 256u + threadIdx.x;
     if (c >= num_visible) return;
     const uint32_t gid = min(gfc[c], num_splats - 1u);
-    const float4* r = rows + (size_t)gid * 4;
+    const float4* r = rows + (size_t)gid * 3;
     const float4 a = r[0], b = r[1], d = r[2];
     float2* dst = reinterpret_cast<float2*>(projected + (size_t)c * 10);
     dst[0] = make_float2(a.x, a.y);
@@ -370,7 +370,7 @@ __global__ __launch_bounds__(256) void map_intersects_kernel(uint32_t tile_bw, u
     TileBox bb{0u, 0u, 0u, 0u};
     uint32_t base = 0, budget = 0;
     if (active) {
-        const float4* r = rows + (size_t)min(gfc[c], num_splats - 1u) * 4;
+        const float4* r = rows + (size_t)min(gfc[c], num_splats - 1u) * 3;
         const float4 a = r[0], b = r[1], d = r[2];
         float2* dst = reinterpret_cast<float2*>(projected + (size_t)c * 10);
         dst[0] = make_float2(a.x, a.y);
