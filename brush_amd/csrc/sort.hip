@@ -118,13 +118,17 @@ void launch_fill_multi(bh_ctx* ctx, const FillRange* ranges, int k) {
 
 
 // Digit layout of a sort by the low `key_bits` bits: ceil(key_bits / 8)
-// passes of equal width (13 bits -> 7 + 6), so every pass has at most 256
+// passes of near-equal width, so every pass has at most 256
 // buckets and the runs each partition writes per bucket are as long as the
 // bit count allows.
+// The narrower digits come first: the first pass reads the unsorted input
+// and writes the shortest runs, so it gets the fewest buckets (13 bits -> 6 + 7).
 struct DigitPlan {
     uint32_t key_bits, passes, width;
-    uint32_t shift(uint32_t p) const { return p * width; }
-    uint32_t bits(uint32_t p) const { return p * width >= key_bits ? 0u : min(width, key_bits - p * width); }
+    // passes [0, narrow) have width - 1 bits, the others width
+    uint32_t narrow() const { return passes * width - key_bits; }
+    uint32_t bits(uint32_t p) const { return key_bits == 0 ? 0u : (p < narrow() ? width - 1u : width); }
+    uint32_t shift(uint32_t p) const { return p * width - min(p, narrow()); }
 };
 static DigitPlan digit_plan(uint32_t key_bits) {
     DigitPlan d;
