@@ -86,13 +86,50 @@ __device__ __forceinline__ uint32_t tile_load_bucket(const uint32_t* __restrict_
     return 127u - min(b, 127u);
 }
 
+// Adds one to s[b] for each lane of the (fully active) wave whose b is a
+// bucket (b <= 127) and returns the lane's previous count.  Empty tiles, most
+// of the image, all fall in bucket 127: the wave adds those in one atomic from
+// its first such lane and hands out consecutive slots, since same-address
+// atomics of one instruction serialise in LDS.
+__device__ __forceinline__ uint32_t bucket_add(uint32_t* s, uint32_t b) {
+    const uint64_t e = __ballot(b == 127u);
+    const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(e >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)e, 0u));
+    uint32_t r = 0u;
+    if (b < 127u)
+        r = atomicAdd(&s[b], 1u);
+    else if (b == 127u && rank == 0u)
+        r = atomicAdd(&s[127], (uint32_t)__popcll(e));
+    const int leader = e ? __ffsll((unsigned long long)e) - 1 : 0;
+    const uint32_t base = (uint32_t)__shfl((int)r, leader, 64);
+    return b == 127u ? base + rank : r;
+}
+
+// Every lane of the workgroup runs each call (the loops below have uniform
+// trip counts), so the wave-wide ballot and shuffle in bucket_add see all 64
+// lanes.  The first 16 x 1024 tiles' buckets stay in registers between the
+// count and the scatter, and their loads are all issued before the first
+// atomic: the two passes cost one memory round trip, not one per tile.
 __device__ __forceinline__ void tile_order_block(const uint32_t* __restrict__ offsets, uint32_t num_tiles,
                                                  uint32_t* __restrict__ order) {
+    constexpr uint32_t K = 16u;
+    constexpr uint32_t NONE = 0xFFFFFFFFu;
     __shared__ uint32_t s_cur[128];
     const uint32_t t = threadIdx.x;
     if (t < 128u) s_cur[t] = 0u;
+    uint32_t bk[K];
+#pragma unroll
+    for (uint32_t k = 0; k < K; ++k) {
+        const uint32_t i = k * 1024u + t;
+        bk[k] = i < num_tiles ? tile_load_bucket(offsets, i) : NONE;
+    }
     __syncthreads();
-    for (uint32_t i = t; i < num_tiles; i += 1024u) atomicAdd(&s_cur[tile_load_bucket(offsets, i)], 1u);
+#pragma unroll
+    for (uint32_t k = 0; k < K; ++k)
+        if (k * 1024u < num_tiles) bucket_add(s_cur, bk[k]);
+    for (uint32_t b0 = K * 1024u; b0 < num_tiles; b0 += 1024u) {
+        const uint32_t i = b0 + t;
+        bucket_add(s_cur, i < num_tiles ? tile_load_bucket(offsets, i) : NONE);
+    }
     __syncthreads();
     if (t < 64u) {
         // exclusive scan of the 128 bucket sizes, two per lane
@@ -108,7 +145,19 @@ __device__ __forceinline__ void tile_order_block(const uint32_t* __restrict__ of
         s_cur[2u * t + 1u] = excl + a;
     }
     __syncthreads();
-    for (uint32_t i = t; i < num_tiles; i += 1024u) order[atomicAdd(&s_cur[tile_load_bucket(offsets, i)], 1u)] = i;
+#pragma unroll
+    for (uint32_t k = 0; k < K; ++k) {
+        if (k * 1024u < num_tiles) {
+            const uint32_t pos = bucket_add(s_cur, bk[k]);
+            if (bk[k] != NONE) order[pos] = k * 1024u + t;
+        }
+    }
+    for (uint32_t b0 = K * 1024u; b0 < num_tiles; b0 += 1024u) {
+        const uint32_t i = b0 + t;
+        const uint32_t b = i < num_tiles ? tile_load_bucket(offsets, i) : NONE;
+        const uint32_t pos = bucket_add(s_cur, b);
+        if (b != NONE) order[pos] = i;
+    }
 }
 
 __global__ __launch_bounds__(1024) void tile_order_kernel(const uint32_t* __restrict__ offsets, uint32_t num_tiles,
