@@ -8,6 +8,7 @@ import os
 import subprocess
 import sys
 import time
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
@@ -32,20 +33,40 @@ FLAGS = [
 ]
 
 
+def _run(cmd):
+    return subprocess.run(cmd, capture_output=True, text=True)
+
+
 def build(verbose: bool = True) -> str:
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    tmp = OUT + ".tmp"
-    cmd = [HIPCC, *FLAGS, "-o", tmp, *srcs]
+    """Compiles every translation unit to an object in parallel (each one is
+    self-contained: no relocatable device code), then links the library."""
+    objdir = os.path.join(HERE, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    compile_flags = [f for f in FLAGS if f != "-shared"]
+    jobs = []
+    for src in SOURCES:
+        obj = os.path.join(objdir, src.replace(".hip", ".o"))
+        jobs.append((obj, [HIPCC, *compile_flags, "-c", "-o", obj, os.path.join(CSRC, src)]))
     t0 = time.time()
     if verbose:
-        print("[build]", " ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
+        print("[build]", " ".join(jobs[0][1][:-4]), "-c <source>", flush=True)
+    workers = max(1, min(len(jobs), os.cpu_count() or 1, 16))
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        results = list(pool.map(_run, [cmd for _, cmd in jobs]))
+    stderr = []
+    for (obj, cmd), res in zip(jobs, results):
+        stderr.append(res.stderr)
+        if res.returncode != 0:
+            sys.stderr.write(res.stdout + res.stderr)
+            raise RuntimeError(f"hipcc failed to compile {cmd[-1]}")
+    tmp = OUT + ".tmp"
+    res = _run([HIPCC, "--offload-arch=gfx950", "-fPIC", "-shared", "-o", tmp, *[obj for obj, _ in jobs]])
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError("hipcc failed to build libbrush_hip.so")
+        raise RuntimeError("hipcc failed to link libbrush_hip.so")
     os.replace(tmp, OUT)
     if verbose:
-        warn = [l for l in res.stderr.splitlines() if "warning" in l and "packed-fp32-ops" not in l]
+        warn = [l for e in stderr for l in e.splitlines() if "warning" in l and "packed-fp32-ops" not in l]
         for l in warn[:20]:
             print("[build]", l)
         print(f"[build] {OUT} ({time.time() - t0:.1f} s)", flush=True)
