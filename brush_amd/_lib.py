@@ -38,7 +38,7 @@ EXPORTED = [
     "bh_ctx_create", "bh_ctx_destroy", "bh_ctx_set_stream", "bh_last_error", "bh_ctx_set_timing",
     "bh_ctx_set_timing_filter",
     "bh_ctx_read_timings", "bh_ctx_reset_timings", "bh_ctx_workspace_bytes", "bh_ctx_release_workspace",
-    "bh_radix_argsort",
+    "bh_radix_argsort", "bh_radix_argsort_noalloc",
     "bh_prefix_sum", "bh_get_tile_offsets", "bh_render_forward", "bh_fwd_state_info",
     "bh_fwd_state_release", "bh_rasterize_backward", "bh_render_backward", "bh_project_backward",
     "bh_image_loss_forward", "bh_image_loss_backward", "bh_adam_scaled_step", "bh_copy_to_host",
@@ -195,6 +195,7 @@ def lib() -> ctypes.CDLL:
         "bh_ctx_workspace_bytes": (U64, [P]),
         "bh_ctx_release_workspace": (S, [P]),
         "bh_radix_argsort": (S, [P, P, P, U32, U32, P, P]),
+        "bh_radix_argsort_noalloc": (S, [P, P, P, U32, U32, P, P]),
         "bh_prefix_sum": (S, [P, P, P, U32]),
         "bh_get_tile_offsets": (S, [P, P, U32, U32, P]),
         "bh_render_forward": (S, [P, UP, P, P, P, P, U32, U32, U32, P, P, P, P, PP]),

@@ -9,6 +9,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <new>
 #include <string>
 
@@ -136,6 +137,12 @@ static bh_status hip_check(bh_ctx* ctx, hipError_t e, const char* what) {
                      std::string(what) + ": " + hipGetErrorString(e));
 }
 
+#define BH_TRY(expr)                      \
+    do {                                  \
+        bh_status _st = (expr);           \
+        if (_st != BH_OK) return _st;     \
+    } while (0)
+
 // RAII set of pool buffers released (stream ordered) at scope exit.
 struct Scratch {
     bh_ctx* ctx;
@@ -155,7 +162,93 @@ struct Scratch {
     }
 };
 
+// Workspace of bh_radix_argsort_noalloc: a fixed device array instead of the
+// pool.  Each GPU the library runs on holds its own copy until the process
+// ends.  In host code `scratch` names a host-side stand-in, never the device
+// memory: its device address is looked up once per device
+// (hipGetSymbolAddress, with that device current) and only that address is
+// handed to kernels.  Every call on one device shares the array, so calls that
+// overlap on one device race; each call clears what must start at zero.
+constexpr size_t kNoAllocScratchBytes = (size_t)48 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mutex;
+static void* g_scratch_addr[kMaxDevices];
+
+// The device address of `scratch` on `device`, which must be current.
+static hipError_t noalloc_scratch_address(int device, void** out) {
+    *out = nullptr;
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_addr[device]) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            return e;
+        }
+        g_scratch_addr[device] = ptr;
+    }
+    *out = g_scratch_addr[device];
+    return hipSuccess;
+}
+
+// Hands out 256-byte aligned pieces of a fixed device region, front to back.
+struct Bump {
+    bh_ctx* ctx;
+    char* base;
+    size_t cap, used = 0;
+    Bump(bh_ctx* c, void* b, size_t n) : ctx(c), base((char*)b), cap(n) {}
+    template <class T>
+    bh_status get(T** out, size_t count) {
+        const size_t bytes = (std::max<size_t>(count, 1) * sizeof(T) + kAlign - 1) / kAlign * kAlign;
+        if (bytes > cap - used)
+            return set_error(ctx, BH_ERR_INVALID_ARG, "radix_argsort_noalloc: workspace exceeds the fixed scratch");
+        *out = (T*)(base + used);
+        used += bytes;
+        return BH_OK;
+    }
+};
+
 static uint32_t bit_length(uint32_t x) { return x ? 32u - (uint32_t)__builtin_clz(x) : 0u; }
+
+// bh_radix_argsort's body over a workspace provider (the pool, or the fixed
+// scratch of the allocation-free entry point).
+template <class Ws>
+static bh_status radix_argsort_with(bh_ctx* ctx, Ws& ws, const uint32_t* keys_in, const uint32_t* vals_in,
+                                    uint32_t n, uint32_t sorting_bits, uint32_t* keys_out, uint32_t* vals_out) {
+    // brush-sort runs ceil(bits/4) 4-bit passes, i.e. it orders by the low
+    // 4*ceil(bits/4) key bits; keep exactly that key width.
+    const uint32_t width = 4u * ((sorting_bits + 3u) / 4u);
+    if (width == 0) {
+        bh_status st = hip_check(
+            ctx, hipMemcpyAsync(keys_out, keys_in, (size_t)n * 4, hipMemcpyDeviceToDevice, ctx->stream), "copy");
+        if (st != BH_OK) return st;
+        return hip_check(ctx, hipMemcpyAsync(vals_out, vals_in, (size_t)n * 4, hipMemcpyDeviceToDevice, ctx->stream),
+                         "copy");
+    }
+    const uint32_t mask = width >= 32 ? 0xFFFFFFFFu : ((1u << width) - 1u);
+    uint32_t *tk, *tv, *masked = nullptr;
+    void* digit_scratch;
+    BH_TRY(ws.get(&tk, n));
+    BH_TRY(ws.get(&tv, n));
+    BH_TRY(ws.get((char**)&digit_scratch, radix_sort_scratch_bytes(n, width)));
+    if (mask != 0xFFFFFFFFu) {
+        // Sort (key & mask, index) then gather: the emitted keys must be the
+        // caller's original keys, including any bits above the key width.
+        uint32_t *perm, *sk;
+        BH_TRY(ws.get(&masked, n));
+        BH_TRY(ws.get(&perm, n));
+        BH_TRY(ws.get(&sk, n));
+        launch_mask_u32(ctx, keys_in, mask, n, masked);
+        BH_TRY(radix_sort_pairs(ctx, masked, nullptr, n, width, 0u, 0xFFFFFFFFu, sk, perm, tk, tv, digit_scratch));
+        launch_gather_pairs(ctx, keys_in, vals_in, perm, n, keys_out, vals_out);
+        return check_launch(ctx, "radix_argsort gather");
+    }
+    return radix_sort_pairs(ctx, keys_in, vals_in, n, width, 0u, 0xFFFFFFFFu, keys_out, vals_out, tk, tv,
+                            digit_scratch);
+}
 
 static bh_status check_device_error(bh_ctx* ctx, uint32_t flags) {
     if (flags & kErrOverflow) return set_error(ctx, BH_ERR_INTERNAL, "a device count overflowed");
@@ -165,12 +258,6 @@ static bh_status check_device_error(bh_ctx* ctx, uint32_t flags) {
 }  // namespace bh
 
 using namespace bh;
-
-#define BH_TRY(expr)                      \
-    do {                                  \
-        bh_status _st = (expr);           \
-        if (_st != BH_OK) return _st;     \
-    } while (0)
 
 extern "C" {
 
@@ -186,6 +273,9 @@ bh_status bh_ctx_create(int device, bh_ctx** out) {
     bh_ctx* ctx = new (std::nothrow) bh_ctx();
     if (!ctx) return BH_ERR_OOM;
     ctx->device = device;
+    // the allocation-free entry point's scratch on this device (looked up
+    // once per device; a failure only disables that entry point)
+    if (noalloc_scratch_address(device, &ctx->noalloc_scratch) != hipSuccess) ctx->noalloc_scratch = nullptr;
     if (hipMalloc(&ctx->d_counters, 64) != hipSuccess || hipHostMalloc(&ctx->h_counters, 64) != hipSuccess) {
         (void)hipGetLastError();
         if (ctx->d_counters) (void)hipFree(ctx->d_counters);
@@ -304,35 +394,27 @@ bh_status bh_radix_argsort(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t*
         return set_error(ctx, BH_ERR_INVALID_ARG, "radix_argsort: null pointer");
     if (keys_in == keys_out || vals_in == vals_out)
         return set_error(ctx, BH_ERR_INVALID_ARG, "radix_argsort: outputs must not alias inputs");
-    // brush-sort runs ceil(bits/4) 4-bit passes, i.e. it orders by the low
-    // 4*ceil(bits/4) key bits; keep exactly that key width.
-    const uint32_t width = 4u * ((sorting_bits + 3u) / 4u);
-    if (width == 0) {
-        BH_TRY(hip_check(ctx, hipMemcpyAsync(keys_out, keys_in, (size_t)n * 4, hipMemcpyDeviceToDevice, ctx->stream),
-                         "copy"));
-        return hip_check(ctx, hipMemcpyAsync(vals_out, vals_in, (size_t)n * 4, hipMemcpyDeviceToDevice, ctx->stream),
-                         "copy");
-    }
-    const uint32_t mask = width >= 32 ? 0xFFFFFFFFu : ((1u << width) - 1u);
     Scratch ws(ctx);
-    uint32_t *tk, *tv, *masked = nullptr;
-    void* scratch;
-    BH_TRY(ws.get(&tk, n));
-    BH_TRY(ws.get(&tv, n));
-    BH_TRY(ws.get((char**)&scratch, radix_sort_scratch_bytes(n, width)));
-    if (mask != 0xFFFFFFFFu) {
-        // Sort (key & mask, index) then gather: the emitted keys must be the
-        // caller's original keys, including any bits above the key width.
-        uint32_t *perm, *sk;
-        BH_TRY(ws.get(&masked, n));
-        BH_TRY(ws.get(&perm, n));
-        BH_TRY(ws.get(&sk, n));
-        launch_mask_u32(ctx, keys_in, mask, n, masked);
-        BH_TRY(radix_sort_pairs(ctx, masked, nullptr, n, width, 0u, 0xFFFFFFFFu, sk, perm, tk, tv, scratch));
-        launch_gather_pairs(ctx, keys_in, vals_in, perm, n, keys_out, vals_out);
-        return check_launch(ctx, "radix_argsort gather");
-    }
-    return radix_sort_pairs(ctx, keys_in, vals_in, n, width, 0u, 0xFFFFFFFFu, keys_out, vals_out, tk, tv, scratch);
+    return radix_argsort_with(ctx, ws, keys_in, vals_in, n, sorting_bits, keys_out, vals_out);
+}
+
+bh_status bh_radix_argsort_noalloc(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t* vals_in, uint32_t n,
+                                   uint32_t sorting_bits, uint32_t* keys_out, uint32_t* vals_out) {
+    if (!ctx) return BH_ERR_INVALID_ARG;
+    if (sorting_bits > 32) return set_error(ctx, BH_ERR_INVALID_ARG, "Can only sort up to 32 bits");
+    if (n == 0) return BH_OK;
+    if (!keys_in || !vals_in || !keys_out || !vals_out)
+        return set_error(ctx, BH_ERR_INVALID_ARG, "radix_argsort_noalloc: null pointer");
+    if (keys_in == keys_out || vals_in == vals_out)
+        return set_error(ctx, BH_ERR_INVALID_ARG, "radix_argsort_noalloc: outputs must not alias inputs");
+    if (n > BH_NOALLOC_SORT_MAX_KEYS)
+        return set_error(ctx, BH_ERR_INVALID_ARG,
+                         "radix_argsort_noalloc: n = " + std::to_string(n) + " exceeds the fixed scratch's maximum of " +
+                             std::to_string(BH_NOALLOC_SORT_MAX_KEYS) + " keys");
+    if (!ctx->noalloc_scratch)
+        return set_error(ctx, BH_ERR_DEVICE, "radix_argsort_noalloc: the device scratch could not be located");
+    Bump ws(ctx, ctx->noalloc_scratch, kNoAllocScratchBytes);
+    return radix_argsort_with(ctx, ws, keys_in, vals_in, n, sorting_bits, keys_out, vals_out);
 }
 
 bh_status bh_prefix_sum(bh_ctx* ctx, const uint32_t* in, uint32_t* out, uint32_t n) {
@@ -340,9 +422,9 @@ bh_status bh_prefix_sum(bh_ctx* ctx, const uint32_t* in, uint32_t* out, uint32_t
     if (n == 0) return BH_OK;
     if (!in || !out) return set_error(ctx, BH_ERR_INVALID_ARG, "prefix_sum: null pointer");
     Scratch ws(ctx);
-    char* scratch;
-    BH_TRY(ws.get(&scratch, scan_scratch_bytes(n)));
-    return inclusive_scan(ctx, in, out, n, scratch);
+    char* sums;
+    BH_TRY(ws.get(&sums, scan_scratch_bytes(n)));
+    return inclusive_scan(ctx, in, out, n, sums);
 }
 
 bh_status bh_get_tile_offsets(bh_ctx* ctx, const uint32_t* ids, uint32_t m, uint32_t num_tiles, uint32_t* offsets) {

@@ -80,6 +80,9 @@ struct bh_ctx {
     // [2..3] num_intersections (u64), [4] min depth key, [5] max depth key
     uint32_t* d_counters = nullptr;
     uint32_t* h_counters = nullptr;  // pinned
+    // device address of the allocation-free entry point's fixed scratch on
+    // this context's device (null when it could not be located)
+    void* noalloc_scratch = nullptr;
 };
 
 namespace bh {

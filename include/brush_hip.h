@@ -188,6 +188,19 @@ bh_status bh_radix_argsort(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t*
                            uint32_t n, uint32_t sorting_bits, uint32_t* keys_out,
                            uint32_t* vals_out);
 
+/* bh_radix_argsort without any allocation: no hipMalloc, hipFree or
+ * allocating library call, for callers that cannot allocate (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid it).  It has no
+ * counterpart in the reference.  Same arguments, results and errors as
+ * bh_radix_argsort, for n <= BH_NOALLOC_SORT_MAX_KEYS (larger n returns
+ * BH_ERR_INVALID_ARG).  The workspace is a fixed 48 MiB device array of the
+ * library, one per GPU, held until the process ends; every call on one GPU
+ * shares it, so calls that overlap on one GPU (from any context or stream)
+ * race. */
+#define BH_NOALLOC_SORT_MAX_KEYS 2097152u
+bh_status bh_radix_argsort_noalloc(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t* vals_in, uint32_t n,
+                                   uint32_t sorting_bits, uint32_t* keys_out, uint32_t* vals_out);
+
 /* Inclusive u32 prefix sum.  Replaces brush-prefix-sum `prefix_sum`
  * (crates/brush-prefix-sum/src/lib.rs:11-87).  out may alias in. */
 bh_status bh_prefix_sum(bh_ctx* ctx, const uint32_t* in, uint32_t* out, uint32_t n);
