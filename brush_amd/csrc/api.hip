@@ -19,6 +19,9 @@ struct bh_fwd_state {
     bh_ctx* ctx;
     bh_fwd_info info;
     std::vector<void*> buffers;
+    // the blend's record of contributing pairs (forward with BWD_INFO and
+    // intersections), read by bh_render_backward
+    bh::SplatRecord record;
 };
 
 namespace bh {
@@ -592,8 +595,17 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
         BH_STRY(ws.get(&order, num_tiles));
         launch_tile_order(ctx, off_pre, num_tiles, order);
     }
+    SplatRecord rec;
+    if (bwd) {
+        // which pairs the blend used, for the fused backward.  Every BWD_INFO
+        // blend writes block_end for every block (also with no intersections),
+        // so the buffers exist whenever BWD_INFO is set.
+        const uint32_t bpt = 2u * tile_h / 8u;
+        BH_STRY(sget((void**)&rec.masks, std::max<size_t>(record_masks(m, bpt), 1) * sizeof(uint2)));
+        BH_STRY(sget((void**)&rec.block_end, (size_t)num_tiles * bpt * 4));
+    }
     launch_rasterize(ctx, u.img_w, u.img_h, u.tile_bw, u.tile_bh, background, num_visible, projected, cgids, gfc,
-                     off_pre, order, flags, out_img, visible, tile_offsets, true);
+                     off_pre, order, flags, out_img, visible, tile_offsets, true, rec);
     BH_STRY(check_launch(ctx, "rasterize"));
 #undef BH_STRY
 
@@ -618,6 +630,7 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
     in.tile_id_from_isect = tile_ids;
     in.compact_gid_from_isect = cgids;
     in.tile_offsets_pre = off_pre;
+    st->record = rec;
     *state_out = st;
     return BH_OK;
 }
@@ -684,6 +697,13 @@ bh_status bh_render_backward(bh_ctx* ctx, const bh_fwd_state* state, const float
     const bh_fwd_info& in = state->info;
     if (!(in.flags & BH_FLAG_BWD_INFO))
         return set_error(ctx, BH_ERR_INVALID_ARG, "render_backward: the forward ran without BH_FLAG_BWD_INFO");
+    // the cutoff and the image layout belong to the forward (burn_glue.rs:326-328
+    // takes them from the forward state): a caller that asks for others is
+    // rejected before anything is launched
+    const uint32_t fwd_owned = BH_FLAG_SMOOTH_CUTOFF | BH_FLAG_RENDER_DEPTH;
+    if ((flags & fwd_owned) != (in.flags & fwd_owned))
+        return set_error(ctx, BH_ERR_INVALID_ARG,
+                         "render_backward: BH_FLAG_SMOOTH_CUTOFF / BH_FLAG_RENDER_DEPTH differ from the forward's");
     const uint32_t n = in.num_splats;
     if (n == 0) return BH_OK;
     if (!out_img || !tile_offsets || !background || !transforms || !sh_coeffs || !raw_opacities || !v_output ||
@@ -694,18 +714,20 @@ bh_status bh_render_backward(bh_ctx* ctx, const bh_fwd_state* state, const float
     Scratch ws(ctx);
     float* rows;
     BH_TRY(ws.get(&rows, (size_t)n * 11));
-    const uint32_t raster_flags =
-        (flags & (BH_FLAG_SMOOTH_CUTOFF | BH_FLAG_REFINE_WEIGHT | BH_FLAG_RENDER_DEPTH)) | (in.flags & BH_FLAG_TILE_16X8);
-    if (!in.num_visible) launch_fill_u32(ctx, (uint32_t*)rows, 0u, (uint64_t)n * 11);
-    if (in.num_visible) {
+    const uint32_t raster_flags = (in.flags & (fwd_owned | BH_FLAG_TILE_16X8)) | (flags & BH_FLAG_REFINE_WEIGHT);
+    if (in.num_visible && in.num_intersections && state->record.masks) {
         // the longest tiles (most splats the forward blended) start first;
         // the order is computed while the gradient rows are zeroed
         uint32_t* order;
         BH_TRY(ws.get(&order, in.num_tiles));
         launch_zero_and_tile_order(ctx, (uint32_t*)rows, (uint64_t)n * 11, tile_offsets, in.num_tiles, order);
-        launch_rasterize_backward(ctx, in.img_w, in.img_h, in.tile_bw, in.tile_bh, background, in.num_visible, out_img,
-                                  in.projected, in.compact_gid_from_isect, tile_offsets, v_output, raster_flags,
-                                  in.global_from_compact_gid, order, rows);
+        launch_rasterize_backward_recorded(ctx, in.img_w, in.img_h, in.tile_bw, in.tile_bh, background, in.num_visible,
+                                           out_img, in.projected, in.compact_gid_from_isect, in.tile_offsets_pre,
+                                           state->record, v_output, raster_flags, in.global_from_compact_gid, order,
+                                           rows);
+    } else {
+        // no intersections: no pixel blended a splat, every gradient is zero
+        launch_fill_u32(ctx, (uint32_t*)rows, 0u, (uint64_t)n * 11);
     }
     BH_TRY(check_launch(ctx, "rasterize_backward"));
     launch_project_backward(ctx, in.uniforms, transforms, sh_coeffs, raw_opacities, nullptr, n, in.sh_degree,

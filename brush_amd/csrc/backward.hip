@@ -25,7 +25,13 @@
 
 #include "bh_internal.h"
 #include "bh_splat_math.h"
+#include "bh_splat_record.h"
 #include "bh_tile_walk.h"
+
+// Splats queued in LDS before the recorded backward sums them (1-3).
+#ifndef BH_RECORDED_SLOTS
+#define BH_RECORDED_SLOTS 2
+#endif
 
 namespace bh {
 
@@ -299,6 +305,268 @@ void launch_rasterize_backward(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint
     }
 #undef BH_RB_T
 #undef BH_RB
+}
+
+// ---- fused rasterize backward from the forward's record ----------------------------
+
+// The fused backward (bh_render_backward) reads the pairs the forward recorded
+// (bh_splat_record.h) instead of replaying the forward's decisions: per 8x8
+// block it visits only splats some pixel blended, and a pixel takes part only
+// where its own bit is set.  The per-pair arithmetic is the reference's
+// (rasterize_backwards.rs:308-441); because no decision depends on it, alpha
+// comes from the hardware exp2 (1 ulp) instead of the bit-exact exp the forward
+// needs, and the transmittance and remaining colour are carried with FMA
+// contraction.
+//
+// A splat's 9-11 gradient lanes are summed over the wave through LDS: every
+// lane writes its values into rows of 64 (one row per gradient lane), and once
+// NSLOT splats are queued, LPR lanes sum each row (a float4 loop over their
+// segment and one or two DPP adds) and one lane per row adds the total to the
+// splat's gradient row in HBM.  That costs about one VALU add per value where
+// a DPP / permlane transposed reduction costs about four, and it issues one
+// atomic instruction per NSLOT splats.
+template <bool SMOOTH, bool REFINE, bool DEPTH, int TH, int NSLOT>
+__global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
+    uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t num_tiles, float bg_r, float bg_g, float bg_b,
+    uint32_t num_visible, const float* __restrict__ out_img, const float* __restrict__ projected,
+    const uint32_t* __restrict__ cgids, const uint32_t* __restrict__ off_pre, SplatRecord rec,
+    const float* __restrict__ v_output, const uint32_t* __restrict__ row_of, const uint32_t* __restrict__ order,
+    float* __restrict__ v_rows) {
+    constexpr uint32_t CH = DEPTH ? 5u : 4u;
+    constexpr uint32_t BPT = 2u * (uint32_t)TH / 8u;
+    constexpr int K = 9 + (REFINE ? 1 : 0) + (DEPTH ? 1 : 0);  // gradient lanes summed per splat
+    constexpr int R = NSLOT * K;                                // LDS rows in use
+    constexpr int RPAD = R <= 16 ? 16 : (R <= 32 ? 32 : 64);
+    constexpr int LPR = 64 / RPAD;  // lanes that sum one row
+    constexpr int SEG = 64 / LPR;   // values each of them sums
+    constexpr int SSTR = SEG + 4;   // segment stride in floats (padded against bank conflicts)
+    constexpr int RS = LPR * SSTR;  // row stride in floats
+    static_assert(R <= 64 && SEG % 4 == 0, "flush geometry");
+    __shared__ float4 s_geo[64];   // x, y, conic c00, c01
+    __shared__ float4 s_op[64];    // conic c11, opacity, max(r, 0), max(g, 0)
+    __shared__ float4 s_gate[64];  // max(b, 0), the colour gradient gates (1 where c >= 0, else 0)
+    __shared__ uint32_t s_row[64];
+    __shared__ float4 s_red4[(R * RS + 3) / 4];
+    __shared__ uint32_t s_slot[NSLOT];
+    float* s_red = reinterpret_cast<float*>(s_red4);
+
+    uint32_t tile, blk;
+    block_of_workgroup<TH>(blockIdx.x, tile, blk);
+    if (tile >= num_tiles) return;
+    if (order) tile = order[tile];
+    const uint32_t lo = off_pre[2 * tile], hi = off_pre[2 * tile + 1];
+    const uint32_t end = rec.block_end[tile * BPT + blk];
+    if (end <= lo) return;
+    const uint32_t lane = threadIdx.x;
+    const uint32_t ox = (tile % tile_bw) * 16u + (blk & 1u) * 8u;
+    const uint32_t oy = (tile / tile_bw) * (uint32_t)TH + (blk >> 1) * 8u;
+    const uint32_t px = ox + (lane & 7u), py = oy + (lane >> 3);
+    const bool inside = px < img_w && py < img_h;
+    const float pcx = (float)px + 0.5f, pcy = (float)py + 0.5f;
+
+    // remaining colour (final minus background pre-roll) and transmittance
+    // (rasterize_backwards.rs:193-250)
+    float sx = 0.0f, sy = 0.0f, sz = 0.0f, sw = 0.0f;
+    float vox = 0.0f, voy = 0.0f, voz = 0.0f, vow = 0.0f, vod = 0.0f, final_a = 0.0f;
+    if (inside) {
+        const size_t pix = (size_t)py * img_w + px;
+        const float* o = out_img + pix * CH;
+        const float* vo = v_output + pix * CH;
+        final_a = o[3];
+        const float t_final = 1.0f - final_a;
+        sx = o[0] - t_final * bg_r;
+        sy = o[1] - t_final * bg_g;
+        sz = o[2] - t_final * bg_b;
+        sw = 1.0f;
+        vox = vo[0];
+        voy = vo[1];
+        voz = vo[2];
+        vow = (vo[3] - (bg_r * vox + bg_g * voy + bg_b * voz)) * t_final;
+        if (DEPTH) vod = vo[4];
+    }
+    // long blocks first (work sits in few tiles; see the replay kernel above)
+    const uint32_t len = end - lo;
+    if (len >= 256u)
+        __builtin_amdgcn_s_setprio(3);
+    else if (len >= 128u)
+        __builtin_amdgcn_s_setprio(2);
+    else if (len >= 64u)
+        __builtin_amdgcn_s_setprio(1);
+    const float w2 = (float)img_w * (float)img_w, h2 = (float)img_h * (float)img_h;
+    const float inv_final_a = __builtin_amdgcn_rcpf(bh_maxf(final_a, 1.0e-5f));
+    const size_t rbase = record_base<BPT>(blk, lo, hi) - lo;
+    // where this lane's value goes in a row, and the row segment it sums
+    const uint32_t wcol = (lane / SEG) * SSTR + (lane % SEG);
+    const uint32_t frow = lane / LPR, fq = lane % LPR;
+
+    // sums the queued slots' rows and adds them to the splats' gradient rows
+    auto flush = [&](uint32_t nslots) {
+        wave_lds_fence();
+        float acc = 0.0f;
+        if (frow < nslots * (uint32_t)K) {
+            const float4* src = reinterpret_cast<const float4*>(s_red + frow * RS + fq * SSTR);
+            float4 v = src[0];
+            acc = (v.x + v.y) + (v.z + v.w);
+#pragma unroll
+            for (int q = 1; q < SEG / 4; ++q) {
+                v = src[q];
+                acc += (v.x + v.y) + (v.z + v.w);
+            }
+        }
+        // the LPR lanes of a row are one pair or one quad of lanes
+        if (LPR >= 2) acc = dpp_add<0xB1>(acc);  // quad_perm [1, 0, 3, 2]
+        if (LPR >= 4) acc = dpp_add<0x4E>(acc);  // quad_perm [2, 3, 0, 1]
+        if (fq == 0u && frow < nslots * (uint32_t)K && acc != 0.0f) {
+            const uint32_t slot = frow / (uint32_t)K, k = frow % (uint32_t)K;
+            const uint32_t dst_lane = k < 9u ? k : (k == 9u && REFINE ? 9u : 10u);
+            unsafeAtomicAdd(v_rows + (size_t)s_slot[slot] * kNG + dst_lane, acc);
+        }
+        wave_lds_fence();
+    };
+
+    uint32_t nslot = 0;
+    for (uint32_t b = lo; b < end; b += 64u) {
+        const uint32_t cnt = min(64u, end - b);
+        // lane j: the pixels that blended candidate b + j
+        uint2 mask = make_uint2(0u, 0u);
+        if (lane < cnt) mask = rec.masks[rbase + b + lane];
+        const bool any = (mask.x | mask.y) != 0u;
+        if (any) {
+            const uint32_t c = min(cgids[b + lane], num_visible - 1u);
+            const float2* prow = reinterpret_cast<const float2*>(projected + (size_t)c * 10);
+            const float2 r0 = prow[0], r1 = prow[1], r2 = prow[2], r3 = prow[3], r4 = prow[4];
+            s_geo[lane] = make_float4(r0.x, r0.y, r1.x, r1.y);
+            s_op[lane] = make_float4(r2.x, r2.y, bh_maxf(r3.x, 0.0f), bh_maxf(r3.y, 0.0f));
+            s_gate[lane] = make_float4(bh_maxf(r4.x, 0.0f), r3.x >= 0.0f ? 1.0f : 0.0f, r3.y >= 0.0f ? 1.0f : 0.0f,
+                                       r4.x >= 0.0f ? 1.0f : 0.0f);
+            s_row[lane] = row_of[c];
+        }
+        uint64_t todo = __ballot(any);
+        wave_lds_fence();
+        while (todo) {
+            const uint32_t j = (uint32_t)__builtin_ctzll(todo);
+            todo &= todo - 1ull;
+            // candidate j's mask, read into scalar registers, is the lane condition
+            // (readlane returns a signed int: widen through uint32_t, never by
+            // sign extension)
+            const uint64_t mj = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(mask.y, j) << 32) |
+                                (uint64_t)(uint32_t)__builtin_amdgcn_readlane(mask.x, j);
+            const bool contrib = __builtin_amdgcn_inverse_ballot_w64(mj);
+            const float4 geo = s_geo[j];
+            const float4 op = s_op[j];
+            const float4 gt = s_gate[j];
+            float g[K];
+            {
+#pragma clang fp contract(fast)
+                const float c00 = geo.z, c01 = geo.w, c11 = op.x, opac = op.y;
+                const float dx = geo.x - pcx, dy = geo.y - pcy;
+                const float dxx = dx * dx, dyy = dy * dy, dxy = dx * dy;
+                const float sigma = 0.5f * (c00 * dxx + c11 * dyy) + c01 * dxy;
+                const float gauss = __builtin_amdgcn_exp2f(sigma * -1.44269504088896341f);
+                const float og = opac * gauss;
+                const float alpha = bh_minf(0.999f, og);
+                float w = 1.0f, ae = alpha;
+                if (SMOOTH) {
+                    w = cutoff_weight(alpha);
+                    ae = alpha * w;
+                }
+                ae = contrib ? ae : 0.0f;
+                const float vis = ae * sw;
+                g[5] = vis * vox * gt.y;
+                g[6] = vis * voy * gt.z;
+                g[7] = vis * voz * gt.w;
+                const float one_minus = 1.0f - ae;
+                const float ra = __builtin_amdgcn_rcpf(one_minus);
+                const float cr = op.z, cg = op.w, cb = gt.x;
+                const float dot_rgb = ((sw * cr - sx) * vox + (sw * cg - sy) * voy + (sw * cb - sz) * voz) * ra;
+                const float v_ae = dot_rgb + vow * ra;
+                const float v_alpha = SMOOTH ? v_ae * (w + alpha * cutoff_weight_deriv(alpha)) : v_ae;
+                // position, conic, opacity and refine lanes: contributing and
+                // unclamped pairs (o G <= 0.999); the selects sit on v_sigma and
+                // on the opacity lane, so other lanes' values never reach a sum
+                const bool gate = contrib && og <= 0.999f;
+                const float v_sigma = gate ? -alpha * v_alpha : 0.0f;
+                const float vxy_x = v_sigma * (c00 * dx + c01 * dy);
+                const float vxy_y = v_sigma * (c01 * dx + c11 * dy);
+                const float hv = 0.5f * v_sigma;
+                g[0] = vxy_x;
+                g[1] = vxy_y;
+                g[2] = hv * dxx;
+                g[3] = v_sigma * dxy;
+                g[4] = hv * dyy;
+                g[8] = gate ? v_alpha * gauss : 0.0f;
+                if (REFINE)
+                    g[9] = __builtin_amdgcn_sqrtf(vxy_x * vxy_x * w2 + vxy_y * vxy_y * h2) * inv_final_a;
+                if (DEPTH) g[K - 1] = vis * vod;
+                sx = sx - vis * cr;
+                sy = sy - vis * cg;
+                sz = sz - vis * cb;
+                sw = sw * one_minus;
+            }
+            float* dst = s_red + nslot * (uint32_t)(K * RS) + wcol;
+#pragma unroll
+            for (int k = 0; k < K; ++k) dst[k * RS] = g[k];
+            if (lane == 0u) s_slot[nslot] = s_row[j];
+            if (++nslot == (uint32_t)NSLOT) {
+                flush(NSLOT);
+                nslot = 0;
+            }
+        }
+        wave_lds_fence();
+    }
+    if (nslot) flush(nslot);
+}
+
+template <int NSLOT>
+static void launch_recorded(bh_ctx* ctx, uint32_t groups, bool smooth, bool refine, bool depth, bool fine,
+                            uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t num_tiles, const float* bg,
+                            uint32_t num_visible, const float* out_img, const float* projected, const uint32_t* cgids,
+                            const uint32_t* off_pre, const SplatRecord& rec, const float* v_output,
+                            const uint32_t* row_of, const uint32_t* order, float* v_rows) {
+#define BH_RBR_T(S, R, D, T)                                                                                     \
+    rasterize_backward_recorded_kernel<S, R, D, T, NSLOT><<<groups, 64, 0, ctx->stream>>>(                       \
+        img_w, img_h, tile_bw, num_tiles, bg[0], bg[1], bg[2], num_visible, out_img, projected, cgids, off_pre, \
+        rec, v_output, row_of, order, v_rows)
+#define BH_RBR(S, R, D)              \
+    do {                             \
+        if (fine)                    \
+            BH_RBR_T(S, R, D, 8);    \
+        else                         \
+            BH_RBR_T(S, R, D, 16);   \
+    } while (0)
+    if (smooth) {
+        if (refine) {
+            if (depth) BH_RBR(true, true, true); else BH_RBR(true, true, false);
+        } else {
+            if (depth) BH_RBR(true, false, true); else BH_RBR(true, false, false);
+        }
+    } else {
+        if (refine) {
+            if (depth) BH_RBR(false, true, true); else BH_RBR(false, true, false);
+        } else {
+            if (depth) BH_RBR(false, false, true); else BH_RBR(false, false, false);
+        }
+    }
+#undef BH_RBR
+#undef BH_RBR_T
+}
+
+void launch_rasterize_backward_recorded(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile_bw,
+                                        uint32_t tile_bh, const float* bg, uint32_t num_visible, const float* out_img,
+                                        const float* projected, const uint32_t* cgids, const uint32_t* off_pre,
+                                        const SplatRecord& rec, const float* v_output, uint32_t flags,
+                                        const uint32_t* row_of, const uint32_t* order, float* v_rows) {
+    const uint32_t num_tiles = tile_bw * tile_bh;
+    if (num_tiles == 0 || num_visible == 0 || !rec.masks) return;
+    const bool smooth = (flags & BH_FLAG_SMOOTH_CUTOFF) != 0;
+    const bool refine = (flags & BH_FLAG_REFINE_WEIGHT) != 0;
+    const bool depth = (flags & BH_FLAG_RENDER_DEPTH) != 0;
+    const bool fine = (flags & BH_FLAG_TILE_16X8) != 0;
+    const uint32_t groups = div_up(num_tiles, 8) * (fine ? 16u : 32u);
+    KernelTimer t(ctx, "rasterize_backward");
+    launch_recorded<BH_RECORDED_SLOTS>(ctx, groups, smooth, refine, depth, fine, img_w, img_h, tile_bw, num_tiles,
+                                       bg, num_visible, out_img, projected, cgids, off_pre, rec, v_output, row_of,
+                                       order, v_rows);
 }
 
 // ---- project backward ---------------------------------------------------------------

@@ -10,6 +10,7 @@
 #include <vector>
 
 #include "../../include/brush_hip.h"
+#include "bh_splat_record.h"
 
 namespace bh {
 
@@ -169,16 +170,25 @@ void launch_tile_order(bh_ctx* ctx, const uint32_t* offsets, uint32_t num_tiles,
 // p[0, words) = 0 (p 16-byte aligned) and the tile order, in one launch.
 void launch_zero_and_tile_order(bh_ctx* ctx, uint32_t* p, uint64_t words, const uint32_t* offsets,
                                 uint32_t num_tiles, uint32_t* order);
+// With BWD_INFO and rec.masks set, the blend also records its contributing
+// pairs for the fused backward (bh_splat_record.h).
 void launch_rasterize(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,
                       const float* bg, uint32_t num_visible, const float* projected, const uint32_t* cgids, const uint32_t* gfc,
                       const uint32_t* off_pre, const uint32_t* order, uint32_t flags, void* out_img, float* visible,
-                      uint32_t* off_post, bool off_post_zeroed = false);
+                      uint32_t* off_post, bool off_post_zeroed = false, SplatRecord rec = SplatRecord{});
 
 // backward.hip
 void launch_rasterize_backward(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,
                                const float* bg, uint32_t num_visible, const float* out_img, const float* projected,
                                const uint32_t* cgids, const uint32_t* offsets, const float* v_output,
                                uint32_t flags, const uint32_t* row_of, const uint32_t* order, float* v_combined);
+// The fused backward's rasterize step from the forward's record; v_rows is
+// indexed by row_of[compact id] (the global id).
+void launch_rasterize_backward_recorded(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile_bw,
+                                        uint32_t tile_bh, const float* bg, uint32_t num_visible, const float* out_img,
+                                        const float* projected, const uint32_t* cgids, const uint32_t* off_pre,
+                                        const SplatRecord& rec, const float* v_output, uint32_t flags,
+                                        const uint32_t* row_of, const uint32_t* order, float* v_rows);
 void launch_invert_permutation(bh_ctx* ctx, const uint32_t* gfc, uint32_t num_visible, uint32_t n,
                                uint32_t* compact_from_global);
 // compact_from_global == nullptr: v_combined is indexed by global id.

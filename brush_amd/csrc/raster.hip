@@ -12,11 +12,16 @@
 // With BWD_INFO the kernel also marks contributing splats visible — once per
 // (splat, block) through a ballot instead of once per pixel — and shrinks each
 // tile's end to one past the last splat any pixel consumed (an atomic max over
-// the tile's four blocks).
+// the tile's four blocks).  It also records which pairs contributed, for the
+// fused backward (bh_splat_record.h): per block and candidate, the 64-bit mask
+// of the block's pixels that blended it (the ballot of the blend decision,
+// moved into the candidate's lane), and per block the end of the candidates its
+// pixels consumed.
 #include <hip/hip_runtime.h>
 
 #include "bh_internal.h"
 #include "bh_splat_math.h"
+#include "bh_splat_record.h"
 #include "bh_tile_walk.h"
 
 namespace bh {
@@ -59,6 +64,15 @@ void launch_tile_offsets(bh_ctx* ctx, const uint32_t* tile_ids, uint32_t m, uint
     if (m == 0) return;
     KernelTimer t(ctx, "tile_offsets");
     tile_offsets_kernel<<<div_up(div_up(m, 4), 256), 256, 0, ctx->stream>>>(tile_ids, m, num_tiles, offsets);
+}
+
+// v_writelane_b32: writes the wave-uniform `value` into lane `lane` of `old`,
+// the other lanes keep theirs.  This compiler exposes no builtin for it, so the
+// declaration binds to the LLVM intrinsic, which also places the lane select
+// where the constant bus allows.
+extern "C" __device__ int bh_llvm_writelane(int value, int lane, int old) __asm("llvm.amdgcn.writelane.i32");
+__device__ __forceinline__ uint32_t write_lane(uint32_t old, uint32_t value, uint32_t lane) {
+    return (uint32_t)bh_llvm_writelane((int)value, (int)lane, (int)old);
 }
 
 // One workgroup (a single wave) per 8x8 pixel block of a 16 x TH tile; the
@@ -210,7 +224,7 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
                                                         const uint32_t* __restrict__ off_pre,
                                                         const uint32_t* __restrict__ order,
                                                         void* __restrict__ out_img, float* __restrict__ visible,
-                                                        uint32_t* __restrict__ off_post) {
+                                                        uint32_t* __restrict__ off_post, SplatRecord rec) {
     __shared__ float4 s_xyco[64];  // x, y, conic c00, conic c01
     __shared__ float4 s_c11a[64];  // conic c11, opacity, sigma cutoff
     __shared__ float4 s_rgbd[64];  // r, g, b (staged_colour), depth
@@ -239,6 +253,11 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
     float t_acc = 1.0f, pr = 0.0f, pg = 0.0f, pb = 0.0f, pd = 0.0f;
     bool done = !inside;
     uint32_t last = lo;
+    // a forward with BWD_INFO always records its pairs (the launcher passes
+    // the record buffers whenever there are intersections)
+    constexpr uint32_t BPT = 2u * (uint32_t)TH / 8u;
+    constexpr bool record = BWD_INFO;
+    const size_t rbase = record ? record_base<BPT>(blk, lo, hi) : 0;
 
     for (uint32_t batch = lo; batch < hi; batch += 64u) {
         if (__ballot(!done) == 0ull) break;
@@ -261,6 +280,7 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
         // splats of the batch that may touch this block, in order
         uint64_t todo = __ballot(touch);
         uint64_t used = 0ull;  // splats some pixel of the block blended
+        uint32_t mask_lo = 0u, mask_hi = 0u;  // pixels that blended this lane's candidate
         wave_lds_fence();
         while (todo) {
             const uint32_t j = (uint32_t)__builtin_ctzll(todo);
@@ -283,7 +303,8 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
             const bool saturate = pass && next_t <= 1.0e-4f;
             const bool contrib = pass && !saturate;
             done = done || saturate;
-            if (__ballot(contrib) != 0ull) {
+            const uint64_t blended = __ballot(contrib);
+            if (blended != 0ull) {
                 const float vis = ae * t_acc;
                 const float4 col = s_rgbd[j];
                 pr = contrib ? pr + col.x * vis : pr;
@@ -293,10 +314,16 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
                 t_acc = contrib ? next_t : t_acc;
                 last = contrib ? batch + j + 1u : last;
                 if (BWD_INFO) used |= 1ull << j;
+                if (record) {
+                    // the ballot (scalar) goes into candidate j's lane
+                    mask_lo = write_lane(mask_lo, (uint32_t)blended, j);
+                    mask_hi = write_lane(mask_hi, (uint32_t)(blended >> 32), j);
+                }
             }
             if (__ballot(!done) == 0ull) break;
         }
         if (BWD_INFO && ((used >> lane) & 1ull)) visible[gfc[my_c]] = 1.0f;
+        if (record && lane < cnt) rec.masks[rbase + (batch - lo) + lane] = make_uint2(mask_lo, mask_hi);
         wave_lds_fence();
     }
 
@@ -331,6 +358,7 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, o, 64));
         if (lane == 0) atomicMax(&off_post[2 * tile + 1], m);
+        if (record && lane == 0) rec.block_end[tile * BPT + blk] = m;
     }
     if (lane == 0 && blk == 0) {
         off_post[2 * tile] = lo;
@@ -341,13 +369,16 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
 void launch_rasterize(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,
                       const float* bg, uint32_t num_visible, const float* projected, const uint32_t* cgids, const uint32_t* gfc,
                       const uint32_t* off_pre, const uint32_t* order, uint32_t flags, void* out_img, float* visible,
-                      uint32_t* off_post, bool off_post_zeroed) {
+                      uint32_t* off_post, bool off_post_zeroed, SplatRecord rec) {
     const uint32_t num_tiles = tile_bw * tile_bh;
     if (num_tiles == 0) return;
     const bool bwd = (flags & BH_FLAG_BWD_INFO) != 0;
     const bool smooth = (flags & BH_FLAG_SMOOTH_CUTOFF) != 0;
     const bool depth = bwd && (flags & BH_FLAG_RENDER_DEPTH) != 0;
     const uint32_t nv = num_visible > 0 ? num_visible : 1u;
+    // a BWD_INFO blend writes its record (block ends always, masks with
+    // intersections): never launch it without the buffers
+    if (bwd && (!rec.masks || !rec.block_end)) return;
     if (bwd && !off_post_zeroed) launch_fill_u32(ctx, off_post, 0u, (uint64_t)num_tiles * 2);
     const bool fine = (flags & BH_FLAG_TILE_16X8) != 0;
     // 8 tiles per group of workgroup ids, 4 (16x16) or 2 (16x8) blocks per tile
@@ -356,7 +387,7 @@ void launch_rasterize(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile
 #define BH_RASTER_T(B, S, D, T)                                                                                    \
     rasterize_kernel<B, S, D, T><<<groups, 64, 0, ctx->stream>>>(img_w, img_h, tile_bw, num_tiles, bg[0], bg[1], \
                                                                  bg[2], nv, projected, cgids, gfc, off_pre, order, \
-                                                                 out_img, visible, off_post)
+                                                                 out_img, visible, off_post, rec)
 #define BH_RASTER(B, S, D) \
     do {                   \
         if (fine)          \
