@@ -29,6 +29,9 @@ FLAG_MIP = 8
 FLAG_REFINE_WEIGHT = 16
 FLAG_TILE_16X8 = 32
 
+DEBUG_POISON = 1
+DEBUG_VALIDATE = 2
+
 PROJECTED_LANES = 10
 COMPACT_GRAD_LANES = 11
 TILE_WIDTH = 16
@@ -38,6 +41,7 @@ EXPORTED = [
     "bh_ctx_create", "bh_ctx_destroy", "bh_ctx_set_stream", "bh_last_error", "bh_ctx_set_timing",
     "bh_ctx_set_timing_filter",
     "bh_ctx_read_timings", "bh_ctx_reset_timings", "bh_ctx_workspace_bytes", "bh_ctx_release_workspace",
+    "bh_ctx_set_debug",
     "bh_radix_argsort", "bh_radix_argsort_noalloc",
     "bh_prefix_sum", "bh_get_tile_offsets", "bh_render_forward", "bh_fwd_state_info",
     "bh_fwd_state_release", "bh_rasterize_backward", "bh_render_backward", "bh_project_backward",
@@ -193,6 +197,7 @@ def lib() -> ctypes.CDLL:
         "bh_ctx_read_timings": (S, [P, ctypes.POINTER(KernelTiming), I, ctypes.POINTER(I)]),
         "bh_ctx_reset_timings": (S, [P]),
         "bh_ctx_workspace_bytes": (U64, [P]),
+        "bh_ctx_set_debug": (S, [P, U32]),
         "bh_ctx_release_workspace": (S, [P]),
         "bh_radix_argsort": (S, [P, P, P, U32, U32, P, P]),
         "bh_radix_argsort_noalloc": (S, [P, P, P, U32, U32, P, P]),
@@ -265,6 +270,13 @@ class Context:
         n = ctypes.c_int(0)
         self.check(lib().bh_ctx_read_timings(self.handle, arr, 64, ctypes.byref(n)), "bh_ctx_read_timings")
         return {arr[i].name.decode(): (int(arr[i].launches), float(arr[i].total_ms)) for i in range(n.value)}
+
+    def set_debug(self, poison: bool = False, validate: bool = False):
+        """BH_DEBUG_POISON: workspace blocks start as 0xFF bytes;
+        BH_DEBUG_VALIDATE: NaN / Inf splat parameters (forward) and gradients
+        (fused backward) raise BH_ERR_NOT_FINITE."""
+        flags = (DEBUG_POISON if poison else 0) | (DEBUG_VALIDATE if validate else 0)
+        self.check(lib().bh_ctx_set_debug(self.handle, flags), "bh_ctx_set_debug")
 
     def workspace_bytes(self) -> int:
         return int(lib().bh_ctx_workspace_bytes(self.handle))

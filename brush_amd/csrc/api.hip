@@ -146,6 +146,13 @@ static bh_status hip_check(bh_ctx* ctx, hipError_t e, const char* what) {
         if (_st != BH_OK) return _st;     \
     } while (0)
 
+// BH_DEBUG_POISON: a block handed out is first filled with 0xFF bytes (stream
+// ordered, so before any kernel that uses it).  Blocks are at least 4-byte
+// sized pool allocations, so rounding the byte count up to words stays inside.
+static void poison(bh_ctx* ctx, void* p, size_t bytes) {
+    if (ctx->debug & BH_DEBUG_POISON) launch_fill_u32(ctx, (uint32_t*)p, 0xFFFFFFFFu, (bytes + 3) / 4);
+}
+
 // RAII set of pool buffers released (stream ordered) at scope exit.
 struct Scratch {
     bh_ctx* ctx;
@@ -157,13 +164,43 @@ struct Scratch {
     template <class T>
     bh_status get(T** out, size_t count) {
         void* p = nullptr;
-        hipError_t e = ctx->pool.alloc(&p, std::max<size_t>(count, 1) * sizeof(T));
+        const size_t bytes = std::max<size_t>(count, 1) * sizeof(T);
+        hipError_t e = ctx->pool.alloc(&p, bytes);
         if (e != hipSuccess) return hip_check(ctx, e, "workspace allocation");
         bufs.push_back(p);
+        poison(ctx, p, bytes);
         *out = (T*)p;
         return BH_OK;
     }
 };
+
+// BH_DEBUG_VALIDATE: the first NaN or infinity of each array, reported as the
+// reference's validation names it (validation.rs:6-84).  names[j] is the
+// array's name, or nullptr for the transforms, whose columns are the means,
+// rotations and log-scales.
+static bh_status check_finite(bh_ctx* ctx, const char* what, const FiniteArrays& a, const char* const* names) {
+    Scratch ws(ctx);
+    unsigned long long* first;
+    BH_TRY(ws.get(&first, kMaxFiniteArrays));
+    launch_first_non_finite(ctx, a, first);
+    BH_TRY(check_launch(ctx, "validation"));
+    unsigned long long h[kMaxFiniteArrays];
+    BH_TRY(hip_check(ctx, hipMemcpyAsync(h, first, sizeof(h), hipMemcpyDeviceToHost, ctx->stream), "validation"));
+    BH_TRY(hip_check(ctx, hipStreamSynchronize(ctx->stream), "validation"));
+    for (int j = 0; j < a.k; j++) {
+        if (h[j] == ~0ull) continue;
+        std::string name = names[j] ? names[j] : "";
+        if (!names[j]) {
+            const uint64_t col = h[j] % 10u;
+            name = col < 3u ? "means" : col < 7u ? "rotations" : "log_scales";
+        }
+        return set_error(ctx, BH_ERR_NOT_FINITE,
+                         std::string(what) + ": tensor '" + name + "' has a NaN or Inf (first @ flat index " +
+                             std::to_string(h[j]) + ")");
+    }
+    return BH_OK;
+}
+
 
 // Workspace of bh_radix_argsort_noalloc: a fixed device array instead of the
 // pool.  Each GPU the library runs on holds its own copy until the process
@@ -210,6 +247,7 @@ struct Bump {
             return set_error(ctx, BH_ERR_INVALID_ARG, "radix_argsort_noalloc: workspace exceeds the fixed scratch");
         *out = (T*)(base + used);
         used += bytes;
+        poison(ctx, *out, bytes);
         return BH_OK;
     }
 };
@@ -374,6 +412,14 @@ bh_status bh_ctx_reset_timings(bh_ctx* ctx) {
     return BH_OK;
 }
 
+bh_status bh_ctx_set_debug(bh_ctx* ctx, uint32_t flags) {
+    if (!ctx) return BH_ERR_INVALID_ARG;
+    if (flags & ~(BH_DEBUG_POISON | BH_DEBUG_VALIDATE))
+        return set_error(ctx, BH_ERR_INVALID_ARG, "set_debug: unknown flag");
+    ctx->debug = flags;
+    return BH_OK;
+}
+
 uint64_t bh_ctx_workspace_bytes(const bh_ctx* ctx) {
     if (!ctx) return 0;
     uint64_t b = ctx->pool.cached_bytes;
@@ -454,6 +500,19 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
         (bwd && num_splats && !visible))
         return set_error(ctx, BH_ERR_INVALID_ARG, "render_forward: null buffer");
 
+    if ((ctx->debug & BH_DEBUG_VALIDATE) && num_splats) {
+        // Splats::validate_values (gaussian_splats.rs:322-380): NaN / Inf in a
+        // parameter fails the render before anything is drawn
+        const uint32_t nc = (sh_degree + 1u) * (sh_degree + 1u);
+        FiniteArrays a{};
+        a.p[0] = transforms, a.n[0] = (uint64_t)num_splats * 10u;
+        a.p[1] = sh_coeffs, a.n[1] = (uint64_t)num_splats * nc * 3u;
+        a.p[2] = raw_opacities, a.n[2] = num_splats;
+        a.k = 3;
+        const char* names[] = {nullptr, "sh_coeffs", "raw_opacity"};
+        BH_TRY(check_finite(ctx, "render", a, names));
+    }
+
     bh_project_uniforms u = *uin;
     // calc_tile_bounds_for_dims (render.rs:36-47): 16x16 tiles, or 16x8 for the
     // candidate rasterizer
@@ -473,6 +532,7 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
         hipError_t e = ctx->pool.alloc(p, std::max<size_t>(bytes, 4));
         if (e != hipSuccess) return hip_check(ctx, e, "state allocation");
         st->buffers.push_back(*p);
+        poison(ctx, *p, std::max<size_t>(bytes, 4));
         return BH_OK;
     };
     auto fail = [&](bh_status s) {
@@ -732,7 +792,19 @@ bh_status bh_render_backward(bh_ctx* ctx, const bh_fwd_state* state, const float
     BH_TRY(check_launch(ctx, "rasterize_backward"));
     launch_project_backward(ctx, in.uniforms, transforms, sh_coeffs, raw_opacities, nullptr, n, in.sh_degree,
                             (in.flags & BH_FLAG_MIP) != 0, rows, v_transforms, v_coeffs, v_raw_opac, v_refine);
-    return check_launch(ctx, "project_backward");
+    BH_TRY(check_launch(ctx, "project_backward"));
+    if (ctx->debug & BH_DEBUG_VALIDATE) {
+        // Splats::bwd_validate (gaussian_splats.rs:384-415)
+        const uint32_t nc = (in.sh_degree + 1u) * (in.sh_degree + 1u);
+        FiniteArrays a{};
+        a.p[0] = v_transforms, a.n[0] = (uint64_t)n * 10u;
+        a.p[1] = v_coeffs, a.n[1] = (uint64_t)n * nc * 3u;
+        a.p[2] = v_raw_opac, a.n[2] = n;
+        a.k = 3;
+        const char* names[] = {"gradient_transforms", "gradient_sh_coeffs", "gradient_raw_opacities"};
+        BH_TRY(check_finite(ctx, "render_backward", a, names));
+    }
+    return BH_OK;
 }
 
 static bh_status check_loss_args(bh_ctx* ctx, const float* pred, uint32_t pred_stride, uint32_t channels,

@@ -312,11 +312,12 @@ void launch_rasterize_backward(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint
 // The fused backward (bh_render_backward) reads the pairs the forward recorded
 // (bh_splat_record.h) instead of replaying the forward's decisions: per 8x8
 // block it visits only splats some pixel blended, and a pixel takes part only
-// where its own bit is set.  The per-pair arithmetic is the reference's
-// (rasterize_backwards.rs:308-441); because no decision depends on it, alpha
-// comes from the hardware exp2 (1 ulp) instead of the bit-exact exp the forward
-// needs, and the transmittance and remaining colour are carried with FMA
-// contraction.
+// where its own bit is set, so no cutoff test is evaluated.  The per-pair
+// arithmetic is the reference's (rasterize_backwards.rs:308-441): alpha,
+// transmittance and remaining colour exactly as the forward computed them (the
+// remaining colour is the final colour minus these contributions, and an alpha
+// one ulp off would leave it inconsistent deep in a stack), the gradient-only
+// products with FMA contraction.
 //
 // A splat's 9-11 gradient lanes are summed over the wave through LDS: every
 // lane writes its values into rows of 64 (one row per gradient lane), and once
@@ -455,54 +456,60 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
             const float4 geo = s_geo[j];
             const float4 op = s_op[j];
             const float4 gt = s_gate[j];
+            const float c00 = geo.z, c01 = geo.w, c11 = op.x, opac = op.y;
+            const float cr = op.z, cg = op.w, cb = gt.x;
+            // The replay state -- alpha, transmittance and remaining colour --
+            // is computed exactly as the forward computed it (its sigma, its
+            // exp, no contraction): the remaining colour is the forward's final
+            // colour minus these contributions, and deep in a stack it is a
+            // small difference of nearly equal numbers, which an alpha off by
+            // an ulp would make inconsistent.
+            const float sigma = calc_sigma(pcx, pcy, S2{c00, c01, c11}, geo.x, geo.y);
+            const float gauss = bh_expf_neg(-sigma);
+            const float og = opac * gauss;
+            const float alpha = bh_minf(0.999f, og);
+            float w = 1.0f, ae = alpha;
+            if (SMOOTH) {
+                w = cutoff_weight(alpha);
+                ae = alpha * w;
+            }
+            ae = contrib ? ae : 0.0f;
+            const float vis = ae * sw;
+            const float one_minus = 1.0f - ae;
+            // position, conic, opacity and refine lanes: contributing and
+            // unclamped pairs (o G <= 0.999); the selects sit on v_sigma and on
+            // the opacity lane, so other lanes' values never reach a sum
+            const bool gate = contrib && og <= 0.999f;
             float g[K];
             {
 #pragma clang fp contract(fast)
-                const float c00 = geo.z, c01 = geo.w, c11 = op.x, opac = op.y;
+                // gradient-only arithmetic: products and sums fuse into FMAs
                 const float dx = geo.x - pcx, dy = geo.y - pcy;
-                const float dxx = dx * dx, dyy = dy * dy, dxy = dx * dy;
-                const float sigma = 0.5f * (c00 * dxx + c11 * dyy) + c01 * dxy;
-                const float gauss = __builtin_amdgcn_exp2f(sigma * -1.44269504088896341f);
-                const float og = opac * gauss;
-                const float alpha = bh_minf(0.999f, og);
-                float w = 1.0f, ae = alpha;
-                if (SMOOTH) {
-                    w = cutoff_weight(alpha);
-                    ae = alpha * w;
-                }
-                ae = contrib ? ae : 0.0f;
-                const float vis = ae * sw;
                 g[5] = vis * vox * gt.y;
                 g[6] = vis * voy * gt.z;
                 g[7] = vis * voz * gt.w;
-                const float one_minus = 1.0f - ae;
                 const float ra = __builtin_amdgcn_rcpf(one_minus);
-                const float cr = op.z, cg = op.w, cb = gt.x;
                 const float dot_rgb = ((sw * cr - sx) * vox + (sw * cg - sy) * voy + (sw * cb - sz) * voz) * ra;
                 const float v_ae = dot_rgb + vow * ra;
                 const float v_alpha = SMOOTH ? v_ae * (w + alpha * cutoff_weight_deriv(alpha)) : v_ae;
-                // position, conic, opacity and refine lanes: contributing and
-                // unclamped pairs (o G <= 0.999); the selects sit on v_sigma and
-                // on the opacity lane, so other lanes' values never reach a sum
-                const bool gate = contrib && og <= 0.999f;
                 const float v_sigma = gate ? -alpha * v_alpha : 0.0f;
                 const float vxy_x = v_sigma * (c00 * dx + c01 * dy);
                 const float vxy_y = v_sigma * (c01 * dx + c11 * dy);
-                const float hv = 0.5f * v_sigma;
                 g[0] = vxy_x;
                 g[1] = vxy_y;
-                g[2] = hv * dxx;
-                g[3] = v_sigma * dxy;
-                g[4] = hv * dyy;
+                g[2] = 0.5f * v_sigma * dx * dx;
+                g[3] = v_sigma * dx * dy;
+                g[4] = 0.5f * v_sigma * dy * dy;
                 g[8] = gate ? v_alpha * gauss : 0.0f;
                 if (REFINE)
                     g[9] = __builtin_amdgcn_sqrtf(vxy_x * vxy_x * w2 + vxy_y * vxy_y * h2) * inv_final_a;
                 if (DEPTH) g[K - 1] = vis * vod;
-                sx = sx - vis * cr;
-                sy = sy - vis * cg;
-                sz = sz - vis * cb;
-                sw = sw * one_minus;
             }
+            // the reference's state update (rasterize_backwards.rs:356-358, 432-435)
+            sx = sx - vis * cr;
+            sy = sy - vis * cg;
+            sz = sz - vis * cb;
+            sw = sw * one_minus;
             float* dst = s_red + nslot * (uint32_t)(K * RS) + wcol;
 #pragma unroll
             for (int k = 0; k < K; ++k) dst[k * RS] = g[k];

@@ -84,6 +84,8 @@ struct bh_ctx {
     // device address of the allocation-free entry point's fixed scratch on
     // this context's device (null when it could not be located)
     void* noalloc_scratch = nullptr;
+    // BH_DEBUG_* flags (bh_ctx_set_debug)
+    uint32_t debug = 0;
 };
 
 namespace bh {
@@ -116,6 +118,15 @@ struct FillRange {
 };
 constexpr int kMaxFillRanges = 8;
 void launch_fill_multi(bh_ctx* ctx, const FillRange* ranges, int k);
+// Debug validation: first[j] (u64, ~0 when none) = the index of the first NaN
+// or infinity in float array j; first holds kMaxFiniteArrays entries.
+constexpr int kMaxFiniteArrays = 4;
+struct FiniteArrays {
+    const float* p[kMaxFiniteArrays];
+    uint64_t n[kMaxFiniteArrays];
+    int k;
+};
+void launch_first_non_finite(bh_ctx* ctx, const FiniteArrays& a, unsigned long long* first);
 
 // sort.hip
 size_t radix_sort_scratch_bytes(uint32_t n, uint32_t key_bits);

@@ -116,6 +116,29 @@ void launch_fill_multi(bh_ctx* ctx, const FillRange* ranges, int k) {
     fill_multi_kernel<<<blocks, 256, 0, ctx->stream>>>(fr);
 }
 
+// ---- debug validation: the first non-finite value of each array ----------------------
+
+// first[i] = the smallest index of a NaN or infinite value in array i (or
+// stays ~0 when it holds none): one grid-stride pass, atomics only on a hit.
+__global__ void first_non_finite_kernel(FiniteArrays a, unsigned long long* __restrict__ first) {
+    const uint64_t tid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (int j = 0; j < a.k; j++) {
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(a.p[j]);
+        for (uint64_t i = tid; i < a.n[j]; i += stride)
+            if ((p[i] & 0x7F800000u) == 0x7F800000u) atomicMin(&first[j], (unsigned long long)i);
+    }
+}
+
+void launch_first_non_finite(bh_ctx* ctx, const FiniteArrays& a, unsigned long long* first) {
+    launch_fill_u32(ctx, reinterpret_cast<uint32_t*>(first), 0xFFFFFFFFu, 2u * kMaxFiniteArrays);
+    uint64_t total = 0;
+    for (int j = 0; j < a.k; j++) total += a.n[j];
+    if (total == 0) return;
+    KernelTimer t(ctx, "first_non_finite");
+    const uint32_t blocks = (uint32_t)std::min<uint64_t>((total + 255) / 256, 4096);
+    first_non_finite_kernel<<<blocks, 256, 0, ctx->stream>>>(a, first);
+}
 
 // Digit layout of a sort by the low `key_bits` bits: ceil(key_bits / 8)
 // passes of near-equal width, so every pass has at most 256

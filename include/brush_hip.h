@@ -170,6 +170,22 @@ typedef struct bh_kernel_timing {
 /* Synchronises the stream, then copies up to `max` entries. */
 bh_status bh_ctx_read_timings(bh_ctx* ctx, bh_kernel_timing* out, int max, int* count);
 bh_status bh_ctx_reset_timings(bh_ctx* ctx);
+/* Debug modes (off by default; not for benchmarking).
+ * BH_DEBUG_POISON: every workspace block the library hands out (pool blocks,
+ *   forward-state buffers, the allocation-free sort's scratch) is first filled
+ *   with 0xFF bytes (NaN as f32, 0xFFFFFFFF as u32), so a missed initialisation
+ *   shows up in the results instead of reading zeros left by an earlier call;
+ *   the reference noises its uninitialised test tensors the same way
+ *   (crates/brush-cube/src/host.rs:52-65).
+ * BH_DEBUG_VALIDATE: bh_render_forward returns BH_ERR_NOT_FINITE when a splat
+ *   parameter is NaN or infinite, and bh_render_backward when a gradient it
+ *   produced is, naming the array and the first index; the reference panics
+ *   there under its debug validation (Splats::validate_values / bwd_validate,
+ *   crates/brush-render/src/gaussian_splats.rs:322-415, validation.rs:6-84).
+ *   Costs one pass over the inputs (outputs) and one host synchronisation. */
+#define BH_DEBUG_POISON 1u
+#define BH_DEBUG_VALIDATE 2u
+bh_status bh_ctx_set_debug(bh_ctx* ctx, uint32_t flags);
 /* Bytes currently cached by the context's workspace pool. */
 uint64_t bh_ctx_workspace_bytes(const bh_ctx* ctx);
 /* Synchronises the stream, then frees every cached workspace block that no

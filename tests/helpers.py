@@ -6,6 +6,7 @@ import math
 import numpy as np
 
 from brush_amd.camera import Camera, focal_to_fov, fov_to_focal, project_uniforms
+from oracle import oracle as O
 from brush_amd.synthetic import CONFIGS, Workload, generate_splats, generate_v_output, splitmix64
 
 
@@ -83,6 +84,51 @@ def rel_close(name, got, want, rtol=1e-3, atol_frac=1e-5):
     bad = np.nonzero(err.reshape(-1) > tol.reshape(-1))[0]
     assert bad.size == 0, (f"{name}: {bad.size}/{got.size} outside rtol={rtol} atol={atol:.3g}; worst "
                            f"{err.reshape(-1)[bad[:3]]} at {bad[:3]} (want {want.reshape(-1)[bad[:3]]})")
+
+
+def gradient_term_magnitudes(o, tr, sh, opac, vc, mip: bool = False, rel: float = 3e-5, draws: int = 3,
+                             seed: int = 0):
+    """For each dense gradient entry (transforms, SH coefficients, raw
+    opacities), how far it moves when the gradient lanes v_combined move by
+    `rel` relative noise, the size of the differences between two correct f32
+    summations of a lane in different orders.  Project backward turns conic
+    lanes of 1e4-1e6 into scale and rotation gradients of order 1-100 through
+    intermediates that cancel, so a few entries amplify lane differences of
+    1e-7 into percent-level changes (the CPU restatement and the GPU's
+    replay path, whose lanes agree to 7 digits, differ there); for a
+    well-conditioned entry the movement is ~rel * |entry|.  The maximum over a
+    few random perturbations."""
+    base = [x.astype(np.float64) for x in O.project_backward(o, tr, sh, opac, vc, mip)[:3]]
+    sens = [np.zeros(x.shape) for x in base]
+    rng = np.random.default_rng(seed)
+    for _ in range(draws):
+        noise = rng.uniform(-1.0, 1.0, vc.shape)
+        vp = (vc.astype(np.float64) * (1.0 + rel * noise)).astype(np.float32)
+        out = O.project_backward(o, tr, sh, opac, vp, mip)[:3]
+        for s_, x, b in zip(sens, out, base):
+            np.maximum(s_, np.abs(x.astype(np.float64) - b), out=s_)
+    return sens
+
+
+def grad_close(name, got, want, magnitude, rtol=1e-3, atol_frac=1e-4, cond=1.0):
+    """rel_close with the float error of cancellation allowed for: |got - want|
+    <= rtol |want| + atol_frac max|want| + cond * magnitude, with `magnitude`
+    the entry's sensitivity to f32 summation differences in its lanes
+    (gradient_term_magnitudes).  For a well-conditioned entry that is ~3e-5
+    |want| and the bound stays rtol relative; it widens only where the entry
+    is a small difference of large intermediates."""
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    assert got.shape == want.shape, f"{name}: shape {got.shape} vs {want.shape}"
+    assert np.array_equal(np.isfinite(got), np.isfinite(want)), f"{name}: non-finite entries differ"
+    gf = np.isfinite(got)
+    got, want, magnitude = got[gf], want[gf], np.asarray(magnitude, np.float64)[gf]
+    scale = float(np.max(np.abs(want))) if want.size else 0.0
+    tol = rtol * np.abs(want) + atol_frac * scale + cond * magnitude + 1e-30
+    err = np.abs(got - want)
+    bad = np.nonzero(err > tol)[0]
+    assert bad.size == 0, (f"{name}: {bad.size}/{got.size} outside; worst {err[bad[:3]]} at {bad[:3]} "
+                           f"(want {want[bad[:3]]}, term magnitude {magnitude[bad[:3]]})")
 
 
 def gpu_forward(uniforms: dict, tr, sh, opac, flags: int, background=(0.0, 0.0, 0.0), device="cuda:0"):

@@ -1,10 +1,11 @@
 """GPU parity at BASELINE.json's full sizes.
 
-Config 1 (the north-star workload, 1M SH3 splats at 1920x1080) is compared
-with the CPU restatement bit for bit through the forward and to the gradient
-tolerance through the backward.  Configs 2 (3M clustered splats, tens of
-millions of tile intersections) and 3 (6M splats at 3840x2160, forward only)
-are checked through properties that do not need a full CPU run:
+Configs 0 (100k SH0 splats at 256x256), 1 (the north-star workload, 1M SH3
+splats at 1920x1080) and 2 (3M clustered splats, 93M tile intersections) are
+compared with the CPU restatement bit for bit through the forward and to the
+gradient tolerance through the backward, every splat.  All configs, and config
+3 (6M splats at 3840x2160, forward only, all eight poses), are also checked
+through properties that do not need the CPU run:
 
 * the tile sort: tile ids non-decreasing, compact ids increasing inside each
   tile, every compact id appearing exactly as often as its splat's tile count,
@@ -20,12 +21,23 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
-from tests.helpers import assert_bits_equal, compare_forward, gpu_forward, rel_close, uniforms_for
+from tests.helpers import (assert_bits_equal, compare_forward, gpu_forward, grad_close, gradient_term_magnitudes,
+                           rel_close, uniforms_for)
 from brush_amd.synthetic import CONFIGS, generate_splats, generate_v_output  # noqa: F401
 
 pytestmark = pytest.mark.gpu
 
 _splats = {}
+
+
+@pytest.fixture(autouse=True, scope="module")
+def _oracle_threads():
+    """The restatement runs these sizes on the box's CPU share (16 threads)."""
+    import os
+
+    O.set_threads(max(1, min(16, os.cpu_count() or 1)))
+    yield
+    O.set_threads(1)
 
 
 def _scene(k):
@@ -106,12 +118,13 @@ def _check_image(img):
     assert img[..., :3].min() >= 0.0
 
 
-def test_config1_full_size_forward_and_backward(gpu):
-    """The north-star workload bit for bit (forward) and to rtol 1e-3 (gradients)."""
+@pytest.mark.parametrize("w_id", [0, 1])
+def test_full_size_forward_and_backward(gpu, w_id):
+    """Configs 0 and 1 (the north-star workload) bit for bit (forward) and to
+    rtol 1e-3 (gradients, every splat)."""
     import torch
     from brush_amd import render as R
 
-    w_id = 1
     w = CONFIGS[w_id]
     print(f"[case] {w.name} forward + backward", flush=True)
     tr, sh, opac = _scene(w_id)
@@ -120,7 +133,24 @@ def test_config1_full_size_forward_and_backward(gpu):
     g = gpu_forward(u, tr, sh, opac, O.FLAG_BWD_INFO)
     o = O.render_forward(u, tr, sh, opac, O.FLAG_BWD_INFO)
     compare_forward(g, o)
+    _check_sort_structure(g, u["tile_bw"] * u["tile_bh"])
     del g
+    _compare_gradients(gpu, w, cam, tr, sh, opac, o)
+
+
+def _compare_gradients(gpu, w, cam, tr, sh, opac, o):
+    """The fused backward of render_splats_diff against the restatement's
+    rasterize + project backward, for the config's upstream gradient, to
+    rtol 1e-3 plus the entry's sensitivity to f32 summation differences in its
+    lanes (grad_close / gradient_term_magnitudes): in the clustered config a
+    few scale and rotation gradients are small differences of conic terms
+    1e4-1e5 times larger, where two correct f32 evaluations (the restatement
+    and the GPU's replay path, whose lanes agree to 7 digits) differ by
+    percents, and a float64 evaluation puts the restatement itself up to 1 %
+    away."""
+    import torch
+    from brush_amd import render as R
+
     t = torch.from_numpy(tr).to(gpu).requires_grad_(True)
     s = torch.from_numpy(sh).to(gpu).requires_grad_(True)
     op = torch.from_numpy(opac).to(gpu).requires_grad_(True)
@@ -129,16 +159,18 @@ def test_config1_full_size_forward_and_backward(gpu):
     res.img.backward(torch.from_numpy(v_out).to(gpu))
     vc = O.rasterize_backward(o, v_out, O.FLAG_REFINE_WEIGHT)
     vt, vcoef, vo, vr = O.project_backward(o, tr, sh, opac, vc)
-    rel_close("v_transforms", t.grad.cpu().numpy(), vt, rtol=1e-3, atol_frac=1e-4)
-    rel_close("v_coeffs", s.grad.cpu().numpy(), vcoef, rtol=1e-3, atol_frac=1e-4)
-    rel_close("v_raw_opac", op.grad.cpu().numpy(), vo, rtol=1e-3, atol_frac=1e-4)
+    mt, mc, mo = gradient_term_magnitudes(o, tr, sh, opac, vc)
+    grad_close("v_transforms", t.grad.cpu().numpy(), vt, mt)
+    grad_close("v_coeffs", s.grad.cpu().numpy(), vcoef, mc)
+    grad_close("v_raw_opac", op.grad.cpu().numpy(), vo, mo)
     rel_close("refine", res._cfg.refine_weight.cpu().numpy(), vr, rtol=1e-3, atol_frac=1e-4)
 
 
 def test_config2_clustered_full_size(gpu):
-    """3M clustered splats at 1280x720: the high-overlap intersect / sort stress."""
-    import torch
-    from brush_amd import render as R
+    """3M clustered splats at 1280x720: the high-overlap intersect / sort
+    stress, against the restatement bit for bit (forward) and to rtol 1e-3
+    (gradients, every splat)."""
+    import gc
 
     w_id = 2
     w = CONFIGS[w_id]
@@ -150,22 +182,17 @@ def test_config2_clustered_full_size(gpu):
     print(f"[case] {w.name}: visible={g['num_visible']} intersections={g['num_intersections']}", flush=True)
     assert g["num_intersections"] > 20_000_000
     _check_sort_structure(g, u["tile_bw"] * u["tile_bh"])
-    _check_subset(g, u, tr, sh, opac, O.FLAG_BWD_INFO, seed=2)
     _check_image(g["out_img"])
+    o = O.render_forward(u, tr, sh, opac, O.FLAG_BWD_INFO)
+    compare_forward(g, o)
     del g
-    t = torch.from_numpy(tr).to(gpu).requires_grad_(True)
-    s = torch.from_numpy(sh).to(gpu).requires_grad_(True)
-    op = torch.from_numpy(opac).to(gpu).requires_grad_(True)
-    res = R.render_splats_diff(R.Splats(t, s, op), cam, (w.img_w, w.img_h))
-    res.img.backward(torch.from_numpy(generate_v_output(w)).to(gpu))
-    for name, grad in (("v_transforms", t.grad), ("v_coeffs", s.grad), ("v_raw_opac", op.grad)):
-        assert bool(torch.isfinite(grad).all()), name
-        assert bool((grad != 0).any()), name
+    gc.collect()
+    _compare_gradients(gpu, w, cam, tr, sh, opac, o)
 
 
-@pytest.mark.parametrize("pose", [0, 7])
+@pytest.mark.parametrize("pose", list(range(8)))
 def test_config3_4k_forward_full_size(gpu, pose):
-    """6M splats at 3840x2160, forward only (packed RGBA8), two of the eight poses."""
+    """6M splats at 3840x2160, forward only (packed RGBA8), each of the eight poses."""
     w_id = 3
     w = CONFIGS[w_id]
     print(f"[case] {w.name} pose {pose}", flush=True)

@@ -1,0 +1,379 @@
+"""GPU robustness: the reference's stress, invariance and validation tests
+(crates/brush-render/src/tests/mod.rs), the debug modes of the C ABI, and
+frames with more than 16384 tiles.
+
+* determinism: the same scene renders bit for bit the same, also with every
+  workspace block poisoned (0xFF bytes) before use (mod.rs:310-332;
+  brush-cube/src/host.rs:52-65 noises uninitialised test tensors);
+* invariance: appending culled splats, or prepending a culled prefix that
+  shifts every global id, leaves the render bit for bit the same
+  (mod.rs:334-410), and the culled splats get exactly zero gradients;
+* stress: 120k fullscreen splats render deterministically with no dropped
+  tile, 200k large splats leave no tile empty, 30M splats render
+  (mod.rs:96-142, 412-605);
+* validation: BH_DEBUG_VALIDATE turns a NaN or Inf parameter into
+  BH_ERR_NOT_FINITE naming the tensor, where the reference panics
+  (mod.rs:607-641; gaussian_splats.rs:322-415), and likewise non-finite
+  gradients;
+* the fused backward takes the cutoff and depth flags from its forward and
+  rejects a caller that passes others, before launching anything;
+* more than 16384 tiles (the tile-order kernel keeps the first 16384 tiles'
+  buckets in registers and loops over the rest): 3840x2160 with 16x16 tiles
+  and 2048x1080 with 16x8 tiles, forward bit for bit and gradients against
+  the CPU restatement.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from brush_amd.camera import Camera
+from oracle import oracle as O
+from tests.helpers import (compare_forward, gpu_forward, grad_close, gradient_term_magnitudes, random_scene,
+                           rel_close, uniforms_for)
+
+pytestmark = pytest.mark.gpu
+
+STATUS_NOT_FINITE = 6
+STATUS_INVALID_ARG = 1
+
+
+def rng_scene(n, mean_range, log_scale_range, opacity_range, seed):
+    """The reference's rng_scene (mod.rs:180-236): SplitMix64 uniforms, per
+    splat means, a non-normalised quaternion, log-scales, SH DC in [0, 1] and a
+    raw opacity, drawn in that order."""
+    k = np.arange(1, n * 14 + 1, dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        z = np.uint64(seed) + k * np.uint64(0x9E3779B97F4A7C15)
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        z = z ^ (z >> np.uint64(31))
+    u = (z.astype(np.float64) / float(2**64 - 1)).astype(np.float32).reshape(n, 14)
+
+    def span(x, lo, hi):
+        return (np.float32(lo) + x * np.float32(hi - lo)).astype(np.float32)
+
+    tr = np.empty((n, 10), np.float32)
+    tr[:, 0:3] = span(u[:, 0:3], -mean_range, mean_range)
+    tr[:, 3:7] = span(u[:, 3:7], -1.0, 1.0)
+    tr[:, 7:10] = span(u[:, 7:10], *log_scale_range)
+    sh = span(u[:, 10:13], 0.0, 1.0).reshape(n, 1, 3)
+    opac = span(u[:, 13], *opacity_range)
+    return tr, sh, opac
+
+
+def _cam():
+    return Camera((0.0, 0.0, -5.0), (0.0, 0.0, 0.0, 1.0), 0.5, 0.5)
+
+
+def _diff_render(gpu, tr, sh, opac, cam, size, v_out):
+    """render_splats_diff forward + fused backward; returns (image, grads)."""
+    import torch
+    from brush_amd import render as R
+
+    t = torch.from_numpy(np.ascontiguousarray(tr)).to(gpu).requires_grad_(True)
+    s = torch.from_numpy(np.ascontiguousarray(sh)).to(gpu).requires_grad_(True)
+    o = torch.from_numpy(np.ascontiguousarray(opac)).to(gpu).requires_grad_(True)
+    res = R.render_splats_diff(R.Splats(t, s, o), cam, size)
+    res.img.backward(torch.from_numpy(v_out).to(gpu))
+    torch.cuda.synchronize()
+    return (res.img.detach().cpu().numpy(),
+            (t.grad.cpu().numpy(), s.grad.cpu().numpy(), o.grad.cpu().numpy()))
+
+
+def _magnitudes(tr, sh, opac, cam, size, v_out):
+    """gradient_term_magnitudes of the scene, from the CPU restatement."""
+    u = uniforms_for(cam, size[0], size[1], tr.shape[0], 0)
+    o = O.render_forward(u, tr, sh, opac, O.FLAG_BWD_INFO)
+    vc = O.rasterize_backward(o, v_out, O.FLAG_REFINE_WEIGHT)
+    return gradient_term_magnitudes(o, tr, sh, opac, vc)
+
+
+def _forward_arrays(u, tr, sh, opac):
+    g = gpu_forward(u, tr, sh, opac, O.FLAG_BWD_INFO)
+    g.pop("out")
+    return g
+
+
+def _assert_same(a: dict, b: dict):
+    for k, v in a.items():
+        if isinstance(v, np.ndarray):
+            assert np.array_equal(v.view(np.uint8), b[k].view(np.uint8)), k
+        else:
+            assert v == b[k], k
+
+
+@pytest.fixture
+def debug_ctx(gpu):
+    from brush_amd import _lib
+
+    ctx = _lib.context()
+    yield ctx
+    ctx.set_debug()
+
+
+def test_render_is_deterministic_with_poisoned_workspace(gpu, debug_ctx):
+    """mod.rs:310-332 (20k large splats at 256x256, rendered twice) with every
+    workspace block of the second and third render poisoned: every forward
+    output bit for bit the same, gradients the same up to the order of float
+    atomics (and finite), the allocation-free sort unchanged."""
+    import torch
+    from brush_amd import _lib
+
+    print("[case] determinism with poisoned workspace", flush=True)
+    tr, sh, opac = rng_scene(20_000, 2.0, (0.5, 3.0), (-1.0, 2.0), 0xA11CE)
+    cam = _cam()
+    u = uniforms_for(cam, 256, 256, tr.shape[0], 0)
+    v_out = np.random.default_rng(5).standard_normal((256, 256, 4)).astype(np.float32)
+    debug_ctx.set_debug()
+    f0 = _forward_arrays(u, tr, sh, opac)
+    img0, g0 = _diff_render(gpu, tr, sh, opac, cam, (256, 256), v_out)
+    mags = _magnitudes(tr, sh, opac, cam, (256, 256), v_out)
+    debug_ctx.set_debug(poison=True)
+    for rep in range(2):
+        f1 = _forward_arrays(u, tr, sh, opac)
+        _assert_same(f0, f1)
+        img1, g1 = _diff_render(gpu, tr, sh, opac, cam, (256, 256), v_out)
+        assert np.array_equal(img0.view(np.uint32), img1.view(np.uint32))
+        for name, a, b, m in zip(("v_transforms", "v_coeffs", "v_raw_opac"), g0, g1, mags):
+            assert np.all(np.isfinite(b)), name
+            grad_close(name, b, a, m, rtol=1e-4, atol_frac=1e-6)
+    # the allocation-free sort's fixed scratch is poisoned too
+    n = 300_001
+    keys = np.random.default_rng(9).integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32)
+    tk = torch.from_numpy(keys.view(np.int32)).to(gpu)
+    tv = torch.arange(n, dtype=torch.int32, device=gpu)
+    outs = []
+    for fn in ("bh_radix_argsort", "bh_radix_argsort_noalloc"):
+        ok, ov = torch.empty_like(tk), torch.empty_like(tv)
+        debug_ctx.check(getattr(_lib.lib(), fn)(debug_ctx.handle, _lib.ptr(tk), _lib.ptr(tv), n, 32, _lib.ptr(ok),
+                                                _lib.ptr(ov)), fn)
+        outs.append((ok.cpu().numpy(), ov.cpu().numpy()))
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+
+
+@pytest.mark.parametrize("where", ["appended", "prefix"])
+def test_culled_splats_do_not_perturb_render(gpu, where):
+    """mod.rs:334-410: culled splats (opacity far below 1/255, behind the
+    camera, far off screen) appended after, or prepended before (shifting
+    every global id) the visible scene leave the image bit for bit the same;
+    the visible splats' gradients are unchanged and the culled splats' are
+    exactly zero."""
+    print(f"[case] culled splats {where}", flush=True)
+    cam = _cam()
+    if where == "appended":
+        vis = rng_scene(5_000, 1.5, (0.0, 2.5), (0.0, 3.0), 0xBEEF)
+        hid = rng_scene(20_000, 1.0, (-1.0, 1.0), (-20.0, -20.0), 0xDEAD)
+        hid[0][1::3, 0:3] = [0.0, 0.0, 1000.0]   # behind the camera after the view transform
+        hid[0][2::3, 0:3] = [1e6, 1e6, 10.0]     # far off screen
+        parts = (vis, hid)
+    else:
+        vis = rng_scene(4_000, 1.5, (0.0, 2.5), (0.0, 3.0), 0xC0FFEE)
+        hid = rng_scene(50_000, 1.0, (-1.0, 1.0), (-20.0, -20.0), 0xF00D)
+        parts = (hid, vis)
+    tr, sh, op = (np.concatenate([p[i] for p in parts]) for i in range(3))
+    v_out = np.random.default_rng(11).standard_normal((256, 256, 4)).astype(np.float32)
+    img_v, g_v = _diff_render(gpu, *vis, cam, (256, 256), v_out)
+    img_c, g_c = _diff_render(gpu, tr, sh, op, cam, (256, 256), v_out)
+    assert np.array_equal(img_v.view(np.uint32), img_c.view(np.uint32)), "culled splats changed the render"
+    mags = _magnitudes(*vis, cam, (256, 256), v_out)
+    nv = vis[0].shape[0]
+    sl = slice(0, nv) if where == "appended" else slice(tr.shape[0] - nv, tr.shape[0])
+    hs = slice(nv, tr.shape[0]) if where == "appended" else slice(0, tr.shape[0] - nv)
+    for name, a, b, m in zip(("v_transforms", "v_coeffs", "v_raw_opac"), g_v, g_c, mags):
+        grad_close(name, b[sl], a, m, rtol=1e-4, atol_frac=1e-6)
+        assert np.all(b[hs] == 0.0), f"{name}: culled splats got gradients"
+
+
+def _tiles_alpha_sums(img, tile=16):
+    h, w = img.shape[:2]
+    a = img[: h // tile * tile, : w // tile * tile, 3]
+    return a.reshape(h // tile, tile, w // tile, tile).sum(axis=(1, 3))
+
+
+def test_mega_stress_fullscreen_splats(gpu):
+    """mod.rs:412-475: 120k fullscreen-sized splats at 512x512 (~120M tile
+    intersections) render bit for bit the same before and after an unrelated
+    render, and no tile is dropped."""
+    print("[case] mega stress", flush=True)
+    cam = _cam()
+    tr, sh, opac = rng_scene(120_000, 0.1, (3.5, 4.0), (-3.0, -1.5), 0x5EED)
+    u = uniforms_for(cam, 512, 512, tr.shape[0], 0)
+    a = gpu_forward(u, tr, sh, opac, O.FLAG_BWD_INFO)
+    print(f"[case] mega stress: intersections={a['num_intersections']}", flush=True)
+    assert a["num_intersections"] > 50_000_000
+    filler = rng_scene(100, 0.5, (-1.0, 0.5), (0.0, 1.0), 0xFACE)
+    gpu_forward(uniforms_for(cam, 512, 512, 100, 0), *filler, O.FLAG_BWD_INFO)
+    b = gpu_forward(u, tr, sh, opac, O.FLAG_BWD_INFO)
+    assert np.array_equal(a["out_img"].view(np.uint32), b["out_img"].view(np.uint32))
+    assert np.array_equal(a["tile_offsets"], b["tile_offsets"])
+    assert np.all(_tiles_alpha_sums(a["out_img"]) > 1e-3), "dropped tile"
+
+
+def test_many_large_splats_leave_no_tile_empty(gpu):
+    """mod.rs:531-605: 200k large splats at 128x128: a finite image with
+    alpha in every tile."""
+    print("[case] 200k large splats", flush=True)
+    rng = np.random.default_rng(0x200)
+    n = 200_000
+    tr = np.empty((n, 10), np.float32)
+    tr[:, 0:3] = rng.uniform(-0.5, 0.5, (n, 3))
+    tr[:, 3:7] = rng.uniform(-1.0, 1.0, (n, 4))
+    tr[:, 7:10] = rng.uniform(-1.0, 2.5, (n, 3))
+    sh = rng.uniform(0.0, 1.0, (n, 1, 3)).astype(np.float32)
+    opac = rng.uniform(-2.0, 2.0, n).astype(np.float32)
+    g = gpu_forward(uniforms_for(_cam(), 128, 128, n, 0), tr, sh, opac, O.FLAG_BWD_INFO)
+    assert np.all(np.isfinite(g["out_img"]))
+    assert int(np.sum(_tiles_alpha_sums(g["out_img"]) < 1e-4)) == 0, "dropped tiles"
+
+
+def test_renders_30m_splats(gpu):
+    """mod.rs:96-142: 30M splats in front of the camera at 64x64 (past any 1D
+    launch limit): some survive projection, the image is finite and not empty,
+    and the tile-count total equals the intersection count."""
+    import torch
+    from brush_amd import render as R
+
+    print("[case] 30M splats", flush=True)
+    n = 30_000_000
+    g = torch.Generator(device=gpu).manual_seed(30)
+
+    def uni(shape, lo, hi):
+        return torch.rand(shape, generator=g, device=gpu, dtype=torch.float32) * (hi - lo) + lo
+
+    tr = torch.cat([uni((n, 3), -2.0, 2.0), uni((n, 4), -1.0, 1.0), uni((n, 3), -4.0, -2.0)], 1).contiguous()
+    sh = uni((n, 1, 3), 0.0, 1.0).contiguous()
+    op = uni((n,), -2.0, 2.0).contiguous()
+    cam = _cam()
+    out = R.render(cam, (64, 64), tr, sh, op, raster_pass=R.RasterPass.Backward)
+    try:
+        assert out.aux.num_visible > 0, "30M splats in front of the camera, none survived projection"
+        img = out.out_img.cpu().numpy()
+        assert np.all(np.isfinite(img))
+        assert np.any(img[..., 3] > 1e-3), "30M splats rendered to an empty image"
+        total = int(out.intersect_counts.to(torch.int64).sum().item())
+        assert total == out.aux.num_intersections
+    finally:
+        out.state.release()
+
+
+_POISONS = [
+    ("means", lambda t, s, o: t.__setitem__((3, 1), np.nan)),
+    ("rotations", lambda t, s, o: t.__setitem__((5, 4), np.inf)),
+    ("log_scales", lambda t, s, o: t.__setitem__((7, 9), np.nan)),
+    ("sh_coeffs", lambda t, s, o: s.__setitem__((2, 0, 1), -np.inf)),
+    ("raw_opacity", lambda t, s, o: o.__setitem__(9, np.nan)),
+]
+
+
+@pytest.mark.parametrize("name,poison", _POISONS, ids=[p[0] for p in _POISONS])
+def test_validation_rejects_non_finite_parameters(gpu, debug_ctx, name, poison):
+    """mod.rs:607-641: with BH_DEBUG_VALIDATE a NaN / Inf parameter fails the
+    render with BH_ERR_NOT_FINITE naming the tensor (the reference panics);
+    without it the splat is culled and the render goes on."""
+    from brush_amd._lib import BrushHipError
+
+    print(f"[case] validation {name}", flush=True)
+    n = 16
+    tr = np.zeros((n, 10), np.float32)
+    tr[:, 0] = np.linspace(-0.5, 0.5, n)
+    tr[:, 3] = 1.0
+    sh = np.ones((n, 1, 3), np.float32)
+    opac = np.zeros(n, np.float32)
+    poison(tr, sh, opac)
+    u = uniforms_for(Camera((0.0, 0.0, -3.0), (0.0, 0.0, 0.0, 1.0), 0.5, 0.5), 32, 32, n, 0)
+    debug_ctx.set_debug()
+    gpu_forward(u, tr, sh, opac, O.FLAG_BWD_INFO)
+    debug_ctx.set_debug(validate=True)
+    with pytest.raises(BrushHipError) as e:
+        gpu_forward(u, tr, sh, opac, O.FLAG_BWD_INFO)
+    assert e.value.status == STATUS_NOT_FINITE
+    assert f"'{name}'" in str(e.value)
+
+
+def test_validation_rejects_non_finite_gradients(gpu, debug_ctx):
+    """Splats::bwd_validate (gaussian_splats.rs:384-415): a NaN upstream
+    gradient on a covered pixel gives NaN parameter gradients, which the fused
+    backward reports as BH_ERR_NOT_FINITE under BH_DEBUG_VALIDATE."""
+    from brush_amd._lib import BrushHipError
+
+    print("[case] validation of gradients", flush=True)
+    tr, sh, opac = random_scene(41, 500, 1, log_scale=(-2.5, 0.5))
+    cam = Camera.from_focal((0.0, 0.0, -3.0), (0.0, 0.0, 0.0, 1.0), 40.0, 48, 40)
+    v_out = np.zeros((40, 48, 4), np.float32)
+    v_out[20, 24, 0] = np.nan
+    debug_ctx.set_debug(validate=True)
+    _diff_render(gpu, tr, sh, opac, cam, (48, 40), np.zeros_like(v_out))
+    with pytest.raises(BrushHipError) as e:
+        _diff_render(gpu, tr, sh, opac, cam, (48, 40), v_out)
+    assert e.value.status == STATUS_NOT_FINITE and "'gradient_" in str(e.value)
+
+
+@pytest.mark.parametrize("fwd_flags,bwd_flags", [(1, 2), (1, 4), (3, 0), (5, 0), (1, 6)])
+def test_render_backward_rejects_flags_of_another_forward(gpu, fwd_flags, bwd_flags):
+    """The cutoff and the image layout belong to the forward (burn_glue.rs:
+    326-328): bh_render_backward with a SMOOTH_CUTOFF or RENDER_DEPTH flag the
+    forward did not have (or without one it had) returns BH_ERR_INVALID_ARG,
+    and the gradient buffers are left untouched (nothing was launched)."""
+    import torch
+    from brush_amd import _lib
+    from brush_amd import render as R
+
+    print(f"[case] backward flags {bwd_flags} after forward flags {fwd_flags}", flush=True)
+    tr, sh, opac = random_scene(43, 300, 0, log_scale=(-2.5, 0.5))
+    cam = Camera.from_focal((0.0, 0.0, -3.0), (0.0, 0.0, 0.0, 1.0), 40.0, 32, 32)
+    t = torch.from_numpy(tr).to(gpu)
+    s = torch.from_numpy(sh).to(gpu)
+    o = torch.from_numpy(opac).to(gpu)
+    rp = R.RasterPass.BackwardSmoothCutoff if fwd_flags & 2 else R.RasterPass.Backward
+    rm = R.RasterizationMode.RgbaAndDepth if fwd_flags & 4 else R.RasterizationMode.Rgba
+    out = R.render(cam, (32, 32), t, s, o, R.SplatRenderMode.Default, rm, (0.0, 0.0, 0.0), rp)
+    n = tr.shape[0]
+    grads = [torch.full(shape, 7.0, device=gpu) for shape in ((n, 10), (n, 1, 3), (n,), (n,))]
+    v_out = torch.ones_like(out.out_img)
+    ctx = _lib.context()
+    bg = (ctypes.c_float * 3)(0.0, 0.0, 0.0)
+    st = _lib.lib().bh_render_backward(ctx.handle, out.state.handle, _lib.ptr(out.out_img),
+                                       _lib.ptr(out.aux.tile_offsets), bg, _lib.ptr(t), _lib.ptr(s), _lib.ptr(o),
+                                       _lib.ptr(v_out), bwd_flags, *[_lib.ptr(x) for x in grads])
+    torch.cuda.synchronize()
+    assert st == STATUS_INVALID_ARG
+    assert "differ from the forward" in _lib.lib().bh_last_error(ctx.handle).decode()
+    for x in grads:
+        assert bool((x == 7.0).all())
+    out.state.release()
+
+
+@pytest.mark.parametrize("tile16x8", [False, True])
+def test_more_than_16384_tiles(gpu, tile16x8):
+    """Frames with more tiles than the tile-order kernel keeps in registers
+    (16 x 1024): 3840x2160 with 16x16 tiles (32400 tiles) and 2048x1080 with
+    16x8 tiles (17280 tiles).  Forward bit for bit, every tile's offsets
+    before and after the blend, and the fused backward to rtol 1e-3, against
+    the CPU restatement."""
+    w, h = (2048, 1080) if tile16x8 else (3840, 2160)
+    print(f"[case] {w}x{h} tiles 16x{8 if tile16x8 else 16}", flush=True)
+    tr, sh, opac = random_scene(57, 20_000, 1, mean_range=1.2, log_scale=(-3.5, 0.6))
+    cam = Camera.from_focal((0.0, 0.0, -3.0), (0.0, 0.0, 0.0, 1.0), 0.45 * w, w, h)
+    u = uniforms_for(cam, w, h, tr.shape[0], 1)
+    flags = O.FLAG_BWD_INFO | (O.FLAG_TILE_16X8 if tile16x8 else 0)
+    o = O.render_forward(u, tr, sh, opac, flags)
+    g = gpu_forward(u, tr, sh, opac, flags)
+    assert o.uniforms["tile_bw"] * o.uniforms["tile_bh"] > 16384
+    compare_forward(g, o)
+    import torch
+    from brush_amd import render as R
+
+    rasterizer = R.Rasterizer.Candidate if tile16x8 else R.Rasterizer.Legacy
+    t = torch.from_numpy(tr).to(gpu).requires_grad_(True)
+    s = torch.from_numpy(sh).to(gpu).requires_grad_(True)
+    op = torch.from_numpy(opac).to(gpu).requires_grad_(True)
+    res = R.render_splats_diff(R.Splats(t, s, op), cam, (w, h), rasterizer=rasterizer)
+    v_out = np.random.default_rng(3).standard_normal((h, w, 4)).astype(np.float32)
+    res.img.backward(torch.from_numpy(v_out).to(gpu))
+    vc = O.rasterize_backward(o, v_out, O.FLAG_REFINE_WEIGHT)
+    vt, vcoef, vo, _ = O.project_backward(o, tr, sh, opac, vc)
+    mt, mc, mo = gradient_term_magnitudes(o, tr, sh, opac, vc)
+    grad_close("v_transforms", t.grad.cpu().numpy(), vt, mt)
+    grad_close("v_coeffs", s.grad.cpu().numpy(), vcoef, mc)
+    grad_close("v_raw_opac", op.grad.cpu().numpy(), vo, mo)
