@@ -61,9 +61,12 @@ def measured_traffic(kernel: str, workload: str, profile: str = TRAFFIC_PROFILE)
     return None
 
 
-def algorithmic_bytes(name: str, n: int, v: int, m: int, m_post: int, t: int, p: int, c: int) -> float:
+def algorithmic_bytes(name: str, n: int, v: int, m: int, m_post: int, t: int, p: int, c: int,
+                      contributing: int | None = None) -> float:
     """Compulsory HBM bytes of one launch: every input read once, every output
-    written once (counts per launch; sort passes are separate launches)."""
+    written once (counts per launch; sort passes are separate launches).
+    ``contributing`` is the number of splats some pixel blended (the forward's
+    visible mask), the ones with a gradient."""
     if name == "project_forward":
         # transforms+opac in; count, radius, depth key out; the visible
         # splats' SH rows in and their 48-B row slots out
@@ -83,9 +86,11 @@ def algorithmic_bytes(name: str, n: int, v: int, m: int, m_post: int, t: int, p:
     if name == "rasterize_backward":
         return 44.0 * m_post + 32.0 * p + 40.0 * m_post  # id+row, image+grad image, atomics per isect
     if name == "project_backward":
-        # gradient lanes [N, 11] in, dense rows out; parameters read for the
-        # splats that have gradient (the visible ones, an upper bound)
-        return 44.0 * n + (40 + 12 * c + 4) * v + (40 + 12 * c + 8) * n
+        # gradient lanes [N, 11] in, dense rows out (transforms, SH, opacity,
+        # refine); the parameters are read only for the splats with a
+        # gradient, those some pixel blended
+        k = v if contributing is None else contributing
+        return 44.0 * n + (40 + 12 * c + 4) * k + (40 + 12 * c + 8) * n
     if name == "image_loss_forward":
         return 28.0 * p                                  # RGB + packed GT in, RGB map out
     if name == "image_loss_backward":
@@ -113,17 +118,38 @@ def sort_bytes_per_launch(name: str, passes: float, n: int, m: int) -> float:
     return 0.0
 
 
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(mode: str, workload, transforms, sh, opac, v_out, gt, min_seconds: float = 10.0,
                  max_reps: int = 20) -> dict:
     """Times the C restatement (oracle/liboracle.so, OpenMP over splats and
-    tiles) on the same full workload, repeated until ``min_seconds`` of CPU
-    work; reports the median repetition in Mpix/s.  Forward-only workloads
-    time one pose per repetition."""
+    tiles) on the same full workload on the host cores it may use, then on one
+    core; each repeated until about ``min_seconds`` / 2 of CPU work (at least
+    one repetition); reports the median repetition in Mpix/s.  Forward-only
+    workloads time one pose per repetition."""
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
+    threads = max(1, min(threads, os.cpu_count() or 1))
+    multi = _cpu_run(mode, workload, transforms, sh, opac, v_out, gt, threads, min_seconds / 2.0, max_reps)
+    single = _cpu_run(mode, workload, transforms, sh, opac, v_out, gt, 1, min_seconds / 2.0, max_reps)
+    out = dict(multi)
+    out["cpu_model"] = cpu_model()
+    out["single_thread"] = {"value": single["value"], "ms_per_step": single["ms_per_step"], "reps": single["reps"],
+                            "cores": 1}
+    return out
+
+
+def _cpu_run(mode, workload, transforms, sh, opac, v_out, gt, threads, min_seconds, max_reps) -> dict:
     from brush_amd.camera import project_uniforms
     from oracle import oracle as O
 
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
-    threads = max(1, min(threads, os.cpu_count() or 1))
     O.set_threads(threads)
     w = workload
     u = project_uniforms(w.camera(0, 8 if mode == "forward" else 1), w.img_w, w.img_h, w.n, w.sh_degree)
@@ -133,7 +159,7 @@ def cpu_baseline(mode: str, workload, transforms, sh, opac, v_out, gt, min_secon
     m2 = [np.zeros_like(p[0]), np.zeros((w.n,), np.float32), np.zeros_like(p[2])] if p else None
     times = []
     t_start = time.perf_counter()
-    while len(times) < max_reps and (time.perf_counter() - t_start < min_seconds or len(times) < 2):
+    while len(times) < max_reps and (time.perf_counter() - t_start < min_seconds or len(times) < 1):
         t0 = time.perf_counter()
         if mode == "forward":
             O.render_forward(u, transforms, sh, opac, 0)
@@ -162,8 +188,8 @@ def cpu_baseline(mode: str, workload, transforms, sh, opac, v_out, gt, min_secon
             "train": "training step (render, loss, backward, Adam)"}[mode]
     return {"value": round(px / dt / 1e6, 4), "unit": "Mpix/s", "cores": threads, "kind": "port",
             "ms_per_step": round(dt * 1000.0, 2), "reps": len(times),
-            "sample": f"the full {w.name} {what} ({w.n} splats, {w.img_w}x{w.img_h}), median of "
-                      f"{len(times)} repetitions"}
+            "sample": f"the C restatement of the reference algorithm (oracle/, not the reference binary) on the "
+                      f"full {w.name} {what} ({w.n} splats, {w.img_w}x{w.img_h}), median of {len(times)} repetitions"}
 
 
 PLY_METRIC = "PLY import+export splats/s: decode of a resident 3DGS vertex element + export encode, 1M SH3"
@@ -372,6 +398,7 @@ def main():
             stats["num_visible"] = res.num_visible
             stats["num_intersections"] = res.aux.num_intersections
             stats["tile_offsets"] = res.aux.tile_offsets
+            stats["visible_mask"] = res.visible
         elif mode == "forward":
             vis = isect = 0
             for cam in cams:
@@ -403,6 +430,9 @@ def main():
     if "tile_offsets" in stats:
         to = stats.pop("tile_offsets")
         m_post = int((to[..., 1].long() - to[..., 0].long()).sum().item())
+    contributing = None
+    if "visible_mask" in stats:
+        contributing = int((stats.pop("visible_mask") > 0).sum().item())
     if mode == "train":
         # the training step's intersection count: one forward at the current parameters
         out = R.render(cams[0], img_size, t, s, o, raster_pass=R.RasterPass.Backward, rasterizer=rasterizer)
@@ -423,7 +453,7 @@ def main():
             if name.endswith(("_onesweep", "_up", "_scan")):
                 b = sort_bytes_per_launch(name, per_step_launches / poses, n, m)
             else:
-                b = algorithmic_bytes(name, n, v, m, m_post, tiles, pixels, c)
+                b = algorithmic_bytes(name, n, v, m, m_post, tiles, pixels, c, contributing)
             table[name] = {"launches_per_step": round(per_step_launches, 2), "avg_ms": round(avg, 4),
                            "ms_per_step": round(total / steps, 4),
                            "algorithmic_mb": round(b / 1e6, 2) if b else None,
@@ -479,6 +509,7 @@ def main():
     config = {"workload": w.name, "splats": w.n, "sh_degree": w.sh_degree, "img": [w.img_w, w.img_h],
               "focal": round(w.focal, 3), "distance": w.distance, "num_visible": v, "num_intersections": m,
               "num_intersections_post_raster": m_post, "poses": poses,
+              "num_contributing": contributing,
               "sort": "two-stage: depth sort of visible splats, then stable tile-id sort of (tile, depth-rank) "
                       "pairs (equivalent to a 64-bit tile|depth key sort)",
               "parallelism": "single GPU",

@@ -31,6 +31,7 @@ FLAG_TILE_16X8 = 32
 
 DEBUG_POISON = 1
 DEBUG_VALIDATE = 2
+DEBUG_EXACT_SIZES = 4
 
 PROJECTED_LANES = 10
 COMPACT_GRAD_LANES = 11
@@ -271,11 +272,15 @@ class Context:
         self.check(lib().bh_ctx_read_timings(self.handle, arr, 64, ctypes.byref(n)), "bh_ctx_read_timings")
         return {arr[i].name.decode(): (int(arr[i].launches), float(arr[i].total_ms)) for i in range(n.value)}
 
-    def set_debug(self, poison: bool = False, validate: bool = False):
+    def set_debug(self, poison: bool = False, validate: bool = False, exact_sizes: bool = False):
         """BH_DEBUG_POISON: workspace blocks start as 0xFF bytes;
         BH_DEBUG_VALIDATE: NaN / Inf splat parameters (forward) and gradients
-        (fused backward) raise BH_ERR_NOT_FINITE."""
-        flags = (DEBUG_POISON if poison else 0) | (DEBUG_VALIDATE if validate else 0)
+        (fused backward) raise BH_ERR_NOT_FINITE;
+        BH_DEBUG_EXACT_SIZES: every forward waits for its counts before it
+        queues the launches that depend on them (no plan from the previous
+        forward)."""
+        flags = ((DEBUG_POISON if poison else 0) | (DEBUG_VALIDATE if validate else 0)
+                 | (DEBUG_EXACT_SIZES if exact_sizes else 0))
         self.check(lib().bh_ctx_set_debug(self.handle, flags), "bh_ctx_set_debug")
 
     def workspace_bytes(self) -> int:

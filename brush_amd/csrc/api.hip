@@ -317,9 +317,11 @@ bh_status bh_ctx_create(int device, bh_ctx** out) {
     // the allocation-free entry point's scratch on this device (looked up
     // once per device; a failure only disables that entry point)
     if (noalloc_scratch_address(device, &ctx->noalloc_scratch) != hipSuccess) ctx->noalloc_scratch = nullptr;
-    if (hipMalloc(&ctx->d_counters, 64) != hipSuccess || hipHostMalloc(&ctx->h_counters, 64) != hipSuccess) {
+    if (hipMalloc(&ctx->d_counters, 64) != hipSuccess || hipHostMalloc(&ctx->h_counters, 64) != hipSuccess ||
+        hipEventCreateWithFlags(&ctx->counters_ready, hipEventDisableTiming) != hipSuccess) {
         (void)hipGetLastError();
         if (ctx->d_counters) (void)hipFree(ctx->d_counters);
+        if (ctx->h_counters) (void)hipHostFree(ctx->h_counters);
         delete ctx;
         return BH_ERR_OOM;
     }
@@ -339,6 +341,7 @@ void bh_ctx_destroy(bh_ctx* ctx) {
     for (auto& kv : ctx->pool.live) (void)hipFree(kv.first);
     (void)hipFree(ctx->d_counters);
     (void)hipHostFree(ctx->h_counters);
+    (void)hipEventDestroy(ctx->counters_ready);
     delete ctx;
 }
 
@@ -414,7 +417,7 @@ bh_status bh_ctx_reset_timings(bh_ctx* ctx) {
 
 bh_status bh_ctx_set_debug(bh_ctx* ctx, uint32_t flags) {
     if (!ctx) return BH_ERR_INVALID_ARG;
-    if (flags & ~(BH_DEBUG_POISON | BH_DEBUG_VALIDATE))
+    if (flags & ~(BH_DEBUG_POISON | BH_DEBUG_VALIDATE | BH_DEBUG_EXACT_SIZES))
         return set_error(ctx, BH_ERR_INVALID_ARG, "set_debug: unknown flag");
     ctx->debug = flags;
     return BH_OK;
@@ -547,126 +550,190 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
     } while (0)
 
     Scratch ws(ctx);
-    uint32_t *counts = nullptr, *gfc = nullptr, *cum = nullptr, *tile_ids = nullptr, *cgids = nullptr,
-             *off_pre = nullptr;
-    float *projected = nullptr, *depths = nullptr;
+    uint32_t *counts = nullptr, *off_pre = nullptr;
     BH_STRY(sget((void**)&counts, (size_t)num_splats * 4));
     BH_STRY(sget((void**)&off_pre, (size_t)num_tiles * 8));
 
-    uint32_t num_visible = 0;
-    uint64_t num_isect = 0;
-    uint32_t* counts_sorted = nullptr;
-    uint32_t kmin = 0, kmax = 0;
-    // Everything the forward needs zeroed, in one launch: the counters' flags
-    // word (the reduction kernel writes the others), the visible mask, the
-    // depth sort's block sums (sized for 32 key bits, which covers the key
-    // range found later), and both tile-offset arrays (empty tiles stay [0, 0]).
+    // The launches after project_forward depend on its counts (visible
+    // splats, intersections, depth-key range).  A plan sizes them: the counts
+    // themselves, read back first (the reference's order, render.rs:309-329),
+    // or the previous forward's plan on this context, with the kernels reading
+    // the actual counts from ctx->d_counters.  The host then reads the counts
+    // only after everything is queued, while the GPU works, and queues the
+    // exact launches again in the rare case that they do not fit the plan.
+    struct Plan {
+        bool device;          // kernels read the counts from ctx->d_counters
+        uint32_t v;           // visible splats (a capacity when device)
+        uint32_t m;           // intersections (a capacity when device)
+        uint32_t key_bits;    // depth-key bits the depth sort covers
+        uint32_t kmin, kcap;  // the depth keys' transform (host plan)
+    };
+    const bool planned = num_splats && ctx->plan_valid && !(ctx->debug & BH_DEBUG_EXACT_SIZES);
+
     char *depth_scr = nullptr, *scan_scr = nullptr;
+    uint32_t* depth_keys = nullptr;
     float* vis_rows = nullptr;
     if (num_splats) {
         BH_STRY(ws.get(&depth_scr, radix_sort_scratch_bytes(num_splats, 32)));
         BH_STRY(ws.get(&scan_scr, scan_scratch_bytes(num_splats)));
     }
-    {
+    // Everything the forward needs zeroed, in one launch: the counters' flags
+    // word (the reduction kernel writes the others), the visible mask, the
+    // depth sort's block sums (sized for 32 key bits, which covers the key
+    // range found later), and both tile-offset arrays (empty tiles stay [0, 0]).
+    auto zero_outputs = [&](bool counters) {
         const FillRange zero[] = {
-            {ctx->d_counters + 1, 0u, num_splats ? 1u : 0u},
+            {ctx->d_counters + 1, 0u, counters && num_splats ? 1u : 0u},
             {(uint32_t*)visible, 0u, bwd ? (uint64_t)num_splats : 0u},
             {(uint32_t*)depth_scr, 0u, num_splats ? radix_sort_zeroed_words(num_splats, 32) : 0u},
             {off_pre, 0u, (uint64_t)num_tiles * 2},
             {tile_offsets, 0u, bwd ? (uint64_t)num_tiles * 2 : 0u},
         };
         launch_fill_multi(ctx, zero, (int)(sizeof(zero) / sizeof(zero[0])));
-    }
-    if (num_splats) {
-        uint32_t *depth_keys, *partials;
-        BH_STRY(ws.get(&depth_keys, num_splats));
-        BH_STRY(ws.get((char**)&partials, project_partials_bytes(num_splats)));
-        BH_STRY(ws.get(&vis_rows, (size_t)num_splats * 12));
-        launch_project_forward(ctx, u, transforms, raw_opacities, sh_coeffs, sh_degree, num_splats, mip, tile_h, counts,
-                               max_radius, depth_keys, vis_rows, partials, ctx->d_counters);
-        BH_STRY(check_launch(ctx, "project_forward"));
-        BH_STRY(hip_check(ctx, hipMemcpyAsync(ctx->h_counters, ctx->d_counters, 24, hipMemcpyDeviceToHost, ctx->stream),
-                          "count readback"));
-        BH_STRY(hip_check(ctx, hipStreamSynchronize(ctx->stream), "count readback"));
+    };
+    zero_outputs(true);
+
+    uint32_t num_visible = 0, kmin = 0, kmax = 0;
+    uint64_t num_isect = 0;
+    auto read_counts = [&]() -> bh_status {
+        BH_TRY(hip_check(ctx, hipEventSynchronize(ctx->counters_ready), "count readback"));
         num_visible = ctx->h_counters[0];
         num_isect = (uint64_t)ctx->h_counters[2] | ((uint64_t)ctx->h_counters[3] << 32);
         kmin = ctx->h_counters[4];
         kmax = ctx->h_counters[5];
-        BH_STRY(check_device_error(ctx, ctx->h_counters[1]));
+        BH_TRY(check_device_error(ctx, ctx->h_counters[1]));
         if (num_isect > 0xFFFFFFFFull)
-            return fail(set_error(ctx, BH_ERR_SHAPE, "more than 2^32 - 1 tile intersections"));
+            return set_error(ctx, BH_ERR_SHAPE, "more than 2^32 - 1 tile intersections");
+        return BH_OK;
+    };
+    if (num_splats) {
+        uint32_t* partials;
+        BH_STRY(ws.get(&depth_keys, num_splats));
+        BH_STRY(ws.get((char**)&partials, project_partials_bytes(num_splats)));
+        BH_STRY(ws.get(&vis_rows, (size_t)num_splats * 12));
+        launch_project_forward(ctx, u, transforms, raw_opacities, sh_coeffs, sh_degree, num_splats, mip, tile_h, counts,
+                               max_radius, depth_keys, vis_rows, partials, ctx->d_counters,
+                               planned ? ctx->plan_isect_cap : 0u);
+        BH_STRY(check_launch(ctx, "project_forward"));
+        BH_STRY(hip_check(ctx, hipMemcpyAsync(ctx->h_counters, ctx->d_counters, 32, hipMemcpyDeviceToHost, ctx->stream),
+                          "count readback"));
+        BH_STRY(hip_check(ctx, hipEventRecord(ctx->counters_ready, ctx->stream), "count readback"));
+    }
 
-        BH_STRY(sget((void**)&gfc, (size_t)num_splats * 4));
-        if (num_visible) {
-            // depth sort: key' = min(bits - kmin, kmax - kmin + 1); culled splats
-            // (all-ones key) map to the cap and sort last.
-            const uint32_t cap = kmax - kmin + 1u;
-            const uint32_t key_bits = std::max<uint32_t>(1u, bit_length(cap));
-            // the last pass also gathers each splat's tile count in depth order,
-            // so the scan below reads them contiguously
-            uint32_t *sk, *tk, *tv;
-            BH_STRY(ws.get(&sk, num_splats));
-            BH_STRY(ws.get(&tk, num_splats));
-            BH_STRY(ws.get(&tv, num_splats));
-            BH_STRY(ws.get(&counts_sorted, num_splats));
-            BH_STRY(radix_sort_pairs(ctx, depth_keys, nullptr, num_splats, key_bits, kmin, cap, sk, gfc, tk, tv,
-                                     depth_scr, "depth_sort", true, counts, counts_sorted));
-        }
-    }
-    BH_STRY(sget((void**)&cum, (size_t)num_visible * 4));
-    BH_STRY(sget((void**)&projected, (size_t)std::max<uint32_t>(num_visible, 1) * 40));
-    BH_STRY(sget((void**)&depths, (size_t)num_visible * 4));
-    if (!gfc) BH_STRY(sget((void**)&gfc, 4));
-    const uint32_t m = (uint32_t)num_isect;
-    BH_STRY(sget((void**)&tile_ids, (size_t)std::max<uint32_t>(m, 1) * 4));
-    BH_STRY(sget((void**)&cgids, (size_t)std::max<uint32_t>(m, 1) * 4));
-    if (num_visible) {
-        BH_STRY(inclusive_scan(ctx, counts_sorted, cum, num_visible, scan_scr));
-        // with intersections, map_intersects orders the rows as it reads them
-        if (num_isect == 0) launch_project_visible(ctx, vis_rows, gfc, num_visible, num_splats, projected, depths);
-        BH_STRY(check_launch(ctx, "project_visible"));
-    } else {
-        launch_fill_u32(ctx, (uint32_t*)projected, 0u, 10);
-    }
-    if (m) {
-        uint32_t *ut, *uc, *tk, *tv;
-        char* scr;
-        BH_STRY(ws.get(&ut, m));
-        BH_STRY(ws.get(&uc, m));
-        BH_STRY(ws.get(&tk, m));
-        BH_STRY(ws.get(&tv, m));
-        // tile sort over bits(num_tiles) bits (render.rs:392-395); the map
-        // kernel zeroes the sort's scratch
-        const uint32_t bits = bit_length(num_tiles);
-        BH_STRY(ws.get(&scr, radix_sort_scratch_bytes(m, bits)));
-        launch_map_intersects(ctx, u.tile_bw, u.tile_bh, tile_h, vis_rows, gfc, num_splats, cum, num_visible, projected,
-                              depths, ut, uc, (uint32_t*)scr, (uint32_t)radix_sort_zeroed_words(m, bits));
-        BH_STRY(check_launch(ctx, "map_intersects"));
-        BH_STRY(radix_sort_pairs(ctx, ut, uc, m, bits, 0u, 0xFFFFFFFFu, tile_ids, cgids, tk, tv, scr, "tile_sort",
-                                 true));
-    } else {
-        launch_fill_u32(ctx, tile_ids, 0u, 1);
-        launch_fill_u32(ctx, cgids, 0u, 1);
-    }
-    launch_tile_offsets(ctx, tile_ids, m, num_tiles, off_pre, true);
-    // the blend kernel starts the tiles with the most candidates first
-    uint32_t* order = nullptr;
-    if (m) {
-        BH_STRY(ws.get(&order, num_tiles));
-        launch_tile_order(ctx, off_pre, num_tiles, order);
-    }
+    uint32_t *gfc = nullptr, *cum = nullptr, *tile_ids = nullptr, *cgids = nullptr;
+    float *projected = nullptr, *depths = nullptr;
     SplatRecord rec;
-    if (bwd) {
-        // which pairs the blend used, for the fused backward.  Every BWD_INFO
-        // blend writes block_end for every block (also with no intersections),
-        // so the buffers exist whenever BWD_INFO is set.
-        const uint32_t bpt = 2u * tile_h / 8u;
-        BH_STRY(sget((void**)&rec.masks, std::max<size_t>(record_masks(m, bpt), 1) * sizeof(uint2)));
-        BH_STRY(sget((void**)&rec.block_end, (size_t)num_tiles * bpt * 4));
+    auto enqueue = [&](const Plan& p) -> bh_status {
+        const uint32_t* dc = p.device ? ctx->d_counters : nullptr;
+        uint32_t* counts_sorted = nullptr;
+        BH_TRY(sget((void**)&gfc, (size_t)std::max<uint32_t>(num_splats, 1u) * 4));
+        if (p.v) {
+            // depth sort: key' = min(bits - kmin, kmax - kmin + 1); culled splats
+            // (all-ones key) map to the cap and sort last.  The last pass also
+            // gathers each splat's tile count in depth order, so the scan below
+            // reads them contiguously.  A plan with more key bits than the
+            // range needs sorts the same: its extra passes see digit 0 only.
+            uint32_t *sk, *tk, *tv;
+            BH_TRY(ws.get(&sk, num_splats));
+            BH_TRY(ws.get(&tk, num_splats));
+            BH_TRY(ws.get(&tv, num_splats));
+            BH_TRY(ws.get(&counts_sorted, num_splats));
+            SortDevice dev;
+            if (dc) dev.key_sub = dc + 4, dev.key_cap = dc + 6;
+            BH_TRY(radix_sort_pairs(ctx, depth_keys, nullptr, num_splats, p.key_bits, p.kmin, p.kcap, sk, gfc, tk, tv,
+                                    depth_scr, "depth_sort", true, counts, counts_sorted, dev));
+        }
+        BH_TRY(sget((void**)&cum, (size_t)p.v * 4));
+        BH_TRY(sget((void**)&projected, (size_t)std::max<uint32_t>(p.v, 1u) * 40));
+        BH_TRY(sget((void**)&depths, (size_t)p.v * 4));
+        BH_TRY(sget((void**)&tile_ids, (size_t)std::max<uint32_t>(p.m, 1u) * 4));
+        BH_TRY(sget((void**)&cgids, (size_t)std::max<uint32_t>(p.m, 1u) * 4));
+        if (p.v) {
+            BH_TRY(inclusive_scan(ctx, counts_sorted, cum, p.v, scan_scr, dc));
+            // with intersections (and always under a device plan, which sizes
+            // them for at least one), map_intersects orders the rows as it reads them
+            if (p.m == 0) launch_project_visible(ctx, vis_rows, gfc, p.v, num_splats, projected, depths);
+            BH_TRY(check_launch(ctx, "project_visible"));
+        } else {
+            launch_fill_u32(ctx, (uint32_t*)projected, 0u, 10);
+        }
+        if (p.m) {
+            uint32_t *ut, *uc, *tk, *tv;
+            char* scr;
+            BH_TRY(ws.get(&ut, p.m));
+            BH_TRY(ws.get(&uc, p.m));
+            BH_TRY(ws.get(&tk, p.m));
+            BH_TRY(ws.get(&tv, p.m));
+            // tile sort over bits(num_tiles) bits (render.rs:392-395); the map
+            // kernel zeroes the sort's scratch
+            const uint32_t bits = bit_length(num_tiles);
+            BH_TRY(ws.get(&scr, radix_sort_scratch_bytes(p.m, bits)));
+            launch_map_intersects(ctx, u.tile_bw, u.tile_bh, tile_h, vis_rows, gfc, num_splats, cum, p.v, projected,
+                                  depths, ut, uc, (uint32_t*)scr, (uint32_t)radix_sort_zeroed_words(p.m, bits), dc);
+            BH_TRY(check_launch(ctx, "map_intersects"));
+            SortDevice dev;
+            if (dc) dev.n = dc + 7;
+            BH_TRY(radix_sort_pairs(ctx, ut, uc, p.m, bits, 0u, 0xFFFFFFFFu, tile_ids, cgids, tk, tv, scr, "tile_sort",
+                                    true, nullptr, nullptr, dev));
+        } else {
+            launch_fill_u32(ctx, tile_ids, 0u, 1);
+            launch_fill_u32(ctx, cgids, 0u, 1);
+        }
+        launch_tile_offsets(ctx, tile_ids, p.m, num_tiles, off_pre, true, dc ? dc + 7 : nullptr);
+        // the blend kernel starts the tiles with the most candidates first
+        uint32_t* order = nullptr;
+        if (p.m) {
+            BH_TRY(ws.get(&order, num_tiles));
+            launch_tile_order(ctx, off_pre, num_tiles, order);
+        }
+        rec = SplatRecord{};
+        if (bwd) {
+            // which pairs the blend used, for the fused backward.  Every BWD_INFO
+            // blend writes block_end for every block (also with no intersections),
+            // so the buffers exist whenever BWD_INFO is set.
+            const uint32_t bpt = 2u * tile_h / 8u;
+            BH_TRY(sget((void**)&rec.masks, std::max<size_t>(record_masks(p.m, bpt), 1) * sizeof(uint2)));
+            BH_TRY(sget((void**)&rec.block_end, (size_t)num_tiles * bpt * 4));
+        }
+        launch_rasterize(ctx, u.img_w, u.img_h, u.tile_bw, u.tile_bh, background, p.v, projected, cgids, gfc, off_pre,
+                         order, flags, out_img, visible, tile_offsets, true, rec);
+        return check_launch(ctx, "rasterize");
+    };
+    auto exact_plan = [&]() {
+        Plan p{false, num_visible, (uint32_t)num_isect, 0u, kmin, kmax - kmin + 1u};
+        if (num_visible) p.key_bits = std::max<uint32_t>(1u, bit_length(p.kcap));
+        return p;
+    };
+
+    const size_t state_mark = st->buffers.size();
+    if (planned) {
+        const Plan p{true, num_splats, ctx->plan_isect_cap, ctx->plan_key_bits, 0u, 0u};
+        BH_STRY(enqueue(p));
+        BH_STRY(read_counts());
+        const Plan exact = exact_plan();
+        // a plan with no visible splat leaves the projected rows unwritten:
+        // the exact launches write the zero row that case has
+        if (num_visible == 0 || exact.m > p.m || exact.key_bits > p.key_bits) {
+            // the exact launches reuse (stream ordered) the plan's buffers
+            for (size_t i = state_mark; i < st->buffers.size(); i++) ctx->pool.release(st->buffers[i]);
+            st->buffers.resize(state_mark);
+            zero_outputs(false);
+            BH_STRY(enqueue(exact));
+        }
+    } else {
+        if (num_splats) BH_STRY(read_counts());
+        BH_STRY(enqueue(exact_plan()));
     }
-    launch_rasterize(ctx, u.img_w, u.img_h, u.tile_bw, u.tile_bh, background, num_visible, projected, cgids, gfc,
-                     off_pre, order, flags, out_img, visible, tile_offsets, true, rec);
-    BH_STRY(check_launch(ctx, "rasterize"));
+    if (num_splats) {
+        // the next forward's plan: this key width, and room for 1/8 more
+        // intersections (kept while within twice what is needed)
+        if (num_visible) ctx->plan_key_bits = exact_plan().key_bits;
+        const uint64_t want = num_isect + num_isect / 8 + 4096;
+        if (!ctx->plan_valid || num_isect > ctx->plan_isect_cap || (uint64_t)ctx->plan_isect_cap > 2 * want)
+            ctx->plan_isect_cap = (uint32_t)std::min<uint64_t>((want + 4095) / 4096 * 4096, 0xFFFFF000ull);
+        ctx->plan_valid = true;
+    }
+    const uint32_t m = (uint32_t)num_isect;
 #undef BH_STRY
 
     u.num_visible = num_visible;

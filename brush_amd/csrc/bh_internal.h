@@ -78,9 +78,17 @@ struct bh_ctx {
     std::vector<hipEvent_t> event_cache;
     std::vector<std::pair<std::string, bh::TimingTotal>> totals;
     // small device scratch: [0] num_visible, [1] error flags,
-    // [2..3] num_intersections (u64), [4] min depth key, [5] max depth key
+    // [2..3] num_intersections (u64), [4] min depth key, [5] max depth key,
+    // [6] depth key cap, [7] intersections when they fit the planned capacity
     uint32_t* d_counters = nullptr;
     uint32_t* h_counters = nullptr;  // pinned
+    hipEvent_t counters_ready = nullptr;  // recorded after the counters' copy to h_counters
+    // The forward's plan for the launches that depend on its counts, taken
+    // from the previous forward on this context: the depth key width and the
+    // intersection capacity (valid once a forward with splats has run).
+    bool plan_valid = false;
+    uint32_t plan_key_bits = 32;
+    uint32_t plan_isect_cap = 0;
     // device address of the allocation-free entry point's fixed scratch on
     // this context's device (null when it could not be located)
     void* noalloc_scratch = nullptr;
@@ -130,6 +138,16 @@ void launch_first_non_finite(bh_ctx* ctx, const FiniteArrays& a, unsigned long l
 
 // sort.hip
 size_t radix_sort_scratch_bytes(uint32_t n, uint32_t key_bits);
+// Sort inputs the kernels read from device memory instead of the host
+// arguments (null: the host argument).  With `n`, the host n is a capacity
+// that sizes the grid and the scratch, and the sort covers the first
+// min(n, *dev.n) pairs; with key_sub / key_cap, the first pass's key
+// transform takes its two constants from there.
+struct SortDevice {
+    const uint32_t* n = nullptr;
+    const uint32_t* key_sub = nullptr;
+    const uint32_t* key_cap = nullptr;
+};
 // Stable sort of (key', value) pairs by the low key_bits bits of
 // key' = min(key - key_sub, key_cap), in ceil(key_bits / 8) passes of equal
 // digit width.  vals_in == nullptr means vals = index.  The transformed keys
@@ -144,15 +162,18 @@ bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t*
                            uint32_t key_bits, uint32_t key_sub, uint32_t key_cap, uint32_t* keys_out,
                            uint32_t* vals_out, uint32_t* tmp_keys, uint32_t* tmp_vals, void* scratch,
                            const char* tag = "radix", bool scratch_zeroed = false,
-                           const uint32_t* gather_src = nullptr, uint32_t* gather_out = nullptr);
+                           const uint32_t* gather_src = nullptr, uint32_t* gather_out = nullptr,
+                           const SortDevice& dev = SortDevice{});
 // out[i] = in[i] & mask
 void launch_mask_u32(bh_ctx* ctx, const uint32_t* in, uint32_t mask, uint32_t n, uint32_t* out);
 // keys_out[i] = keys_in[perm[i]], vals_out[i] = vals_in[perm[i]]
 void launch_gather_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t* vals_in, const uint32_t* perm,
                          uint32_t n, uint32_t* keys_out, uint32_t* vals_out);
 size_t scan_scratch_bytes(uint32_t n);
-// Inclusive scan of in[0, n); out may alias in.
-bh_status inclusive_scan(bh_ctx* ctx, const uint32_t* in, uint32_t* out, uint32_t n, void* scratch);
+// Inclusive scan of in[0, n); out may alias in.  With dev_n, n is a capacity
+// and the scan covers in[0, min(n, *dev_n)).
+bh_status inclusive_scan(bh_ctx* ctx, const uint32_t* in, uint32_t* out, uint32_t n, void* scratch,
+                         const uint32_t* dev_n = nullptr);
 
 // project.hip
 size_t project_partials_bytes(uint32_t n);
@@ -161,20 +182,23 @@ size_t project_partials_bytes(uint32_t n);
 void launch_project_forward(bh_ctx* ctx, const bh_project_uniforms& u, const float* transforms,
                             const float* raw_opac, const float* sh, uint32_t sh_degree, uint32_t n, bool mip,
                             uint32_t tile_h, uint32_t* intersect_counts, float* max_radius, uint32_t* depth_keys,
-                            float* rows, uint32_t* partials, uint32_t* counters);
+                            float* rows, uint32_t* partials, uint32_t* counters, uint32_t isect_cap = 0);
 void launch_project_visible(bh_ctx* ctx, const float* rows, const uint32_t* gfc, uint32_t num_visible,
                             uint32_t num_splats, float* projected, float* depths);
 // Also writes compact rows `projected` [V,10] and `depths` [V] from the
 // global-id rows of launch_project_forward, and zeroes zero[0, zero_words)
-// (the tile sort's scratch).
+// (the tile sort's scratch).  With dev (the context counters after
+// project_forward), num_visible is a capacity: the kernel reads the visible
+// count from dev[0] and writes intersections only when they fit the buffers.
 void launch_map_intersects(bh_ctx* ctx, uint32_t tile_bw, uint32_t tile_bh, uint32_t tile_h, const float* rows,
                            const uint32_t* gfc, uint32_t num_splats, const uint32_t* cum, uint32_t num_visible,
                            float* projected, float* depths, uint32_t* tile_ids, uint32_t* cgids, uint32_t* zero,
-                           uint32_t zero_words);
+                           uint32_t zero_words, const uint32_t* dev = nullptr);
 
 // raster.hip
+// With dev_m, m is a capacity and the ids are tile_ids[0, min(m, *dev_m)).
 void launch_tile_offsets(bh_ctx* ctx, const uint32_t* tile_ids, uint32_t m, uint32_t num_tiles,
-                         uint32_t* offsets, bool zeroed = false);
+                         uint32_t* offsets, bool zeroed = false, const uint32_t* dev_m = nullptr);
 // order[num_tiles]: the tiles by descending load (launch_tile_order), or
 // nullptr for tile-id order.
 void launch_tile_order(bh_ctx* ctx, const uint32_t* offsets, uint32_t num_tiles, uint32_t* order);

@@ -207,9 +207,13 @@ __global__ __launch_bounds__(256) void project_forward_kernel(bh_project_uniform
 }
 
 // Folds the per-block totals of project_forward into the context counters
-// ([0] visible, [2..3] intersections, [4] min depth key, [5] max depth key).
+// ([0] visible, [2..3] intersections, [4] min depth key, [5] max depth key),
+// and writes what launches sized before the host reads them take from there:
+// [6] the depth sort's key cap (max - min + 1) and [7] the intersection
+// count when it fits `isect_cap` (else 0).
 __global__ __launch_bounds__(1024) void project_reduce_kernel(const uint32_t* __restrict__ partials,
-                                                              uint32_t num_blocks, uint32_t* __restrict__ counters) {
+                                                              uint32_t num_blocks, uint32_t isect_cap,
+                                                              uint32_t* __restrict__ counters) {
     __shared__ uint32_t s_v[16], s_mn[16], s_mx[16];
     __shared__ unsigned long long s_h[16];
     uint32_t v = 0, mn = 0xFFFFFFFFu, mx = 0u;
@@ -245,6 +249,8 @@ __global__ __launch_bounds__(1024) void project_reduce_kernel(const uint32_t* __
         counters[3] = (uint32_t)(h >> 32);
         counters[4] = mn;
         counters[5] = mx;
+        counters[6] = mx - mn + 1u;
+        counters[7] = h <= (unsigned long long)isect_cap ? (uint32_t)h : 0u;
     }
 }
 
@@ -286,7 +292,7 @@ static void launch_pf_deg(bh_ctx* ctx, uint32_t blocks, const bh_project_uniform
 void launch_project_forward(bh_ctx* ctx, const bh_project_uniforms& u, const float* transforms,
                             const float* raw_opac, const float* sh, uint32_t sh_degree, uint32_t n, bool mip,
                             uint32_t tile_h, uint32_t* intersect_counts, float* max_radius, uint32_t* depth_keys,
-                            float* rows, uint32_t* partials, uint32_t* counters) {
+                            float* rows, uint32_t* partials, uint32_t* counters, uint32_t isect_cap) {
     if (n == 0) return;
     uint32_t blocks = div_up(n, 256);
     {
@@ -305,7 +311,7 @@ void launch_project_forward(bh_ctx* ctx, const bh_project_uniforms& u, const flo
 #undef BH_PFD
     }
     KernelTimer t(ctx, "project_reduce");
-    project_reduce_kernel<<<1, 1024, 0, ctx->stream>>>(partials, blocks, counters);
+    project_reduce_kernel<<<1, 1024, 0, ctx->stream>>>(partials, blocks, isect_cap, counters);
 }
 
 // ---- project_visible ------------------------------------------------------------
@@ -344,7 +350,11 @@ void launch_project_visible(bh_ctx* ctx, const float* rows, const uint32_t* gfc,
 
 // Each lane takes its splat's row from the global-id slot project_forward
 // filled (gfc[c]), stores it as compact row c of `projected` (with its
-// depth), and walks its tiles with it.
+// depth), and walks its tiles with it.  With `dev` (the context counters),
+// num_visible is a capacity and the visible count is dev[0]; the
+// intersections are written only when their count fits the output
+// (dev[7] == dev[2..3], set by project_reduce), so every store stays inside
+// buffers sized for the capacity.
 template <int TH>
 __global__ __launch_bounds__(256) void map_intersects_kernel(uint32_t tile_bw, uint32_t tile_bh,
                                                               const float4* __restrict__ rows,
@@ -354,13 +364,19 @@ __global__ __launch_bounds__(256) void map_intersects_kernel(uint32_t tile_bw, u
                                                               float* __restrict__ depths,
                                                               uint32_t* __restrict__ tile_ids,
                                                               uint32_t* __restrict__ cgids,
-                                                              uint32_t* __restrict__ zero, uint32_t zero_words) {
+                                                              uint32_t* __restrict__ zero, uint32_t zero_words,
+                                                              const uint32_t* __restrict__ dev) {
     __shared__ WalkRec s_rec[4][64];
     __shared__ uint32_t s_slot[4][64], s_count[4][64];
     const uint32_t c = blockIdx.x * 256u + threadIdx.x;
     // the tile sort's zeroed scratch, cleared here instead of by a launch of its own
     for (uint32_t i = c; i < zero_words; i += gridDim.x * 256u) zero[i] = 0u;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    bool emit = true;
+    if (dev) {
+        num_visible = min(num_visible, dev[0]);
+        emit = dev[3] == 0u && dev[7] == dev[2];
+    }
     const uint32_t c0 = c - lane;  // first compact id of this wave
     if (c0 >= num_visible) return;  // the whole wave is past the end
     const bool active = c < num_visible;
@@ -379,6 +395,7 @@ __global__ __launch_bounds__(256) void map_intersects_kernel(uint32_t tile_bw, u
         dst[3] = make_float2(b.z, b.w);
         dst[4] = make_float2(d.x, d.y);
         depths[c] = d.y;
+        if (!emit) return;
         m = v2(a.x, a.y);
         conic = S2{a.z, a.w, b.x};
         pt = bh_logf(b.y * 255.0f);
@@ -386,6 +403,7 @@ __global__ __launch_bounds__(256) void map_intersects_kernel(uint32_t tile_bw, u
         base = c == 0 ? 0u : cum[c - 1];
         budget = cum[c] - base;
     }
+    if (!emit) return;  // uniform over the grid
     // The wave's splats own the contiguous output range [cum[c0 - 1], cum[last]);
     // the walk emits their tiles in that order.
     const uint32_t last = min(c0 + 63u, num_visible - 1u);
@@ -418,7 +436,7 @@ __global__ __launch_bounds__(256) void map_intersects_kernel(uint32_t tile_bw, u
 void launch_map_intersects(bh_ctx* ctx, uint32_t tile_bw, uint32_t tile_bh, uint32_t tile_h, const float* rows,
                            const uint32_t* gfc, uint32_t num_splats, const uint32_t* cum, uint32_t num_visible,
                            float* projected, float* depths, uint32_t* tile_ids, uint32_t* cgids, uint32_t* zero,
-                           uint32_t zero_words) {
+                           uint32_t zero_words, const uint32_t* dev) {
     if (num_visible == 0) return;
     KernelTimer t(ctx, "map_intersects");
     const uint32_t blocks = div_up(num_visible, 256);
@@ -426,11 +444,11 @@ void launch_map_intersects(bh_ctx* ctx, uint32_t tile_bw, uint32_t tile_bh, uint
     if (tile_h == 8)
         map_intersects_kernel<8><<<blocks, 256, 0, ctx->stream>>>(tile_bw, tile_bh, r4, gfc, num_splats, cum,
                                                                  num_visible, projected, depths, tile_ids, cgids, zero,
-                                                                 zero_words);
+                                                                 zero_words, dev);
     else
         map_intersects_kernel<16><<<blocks, 256, 0, ctx->stream>>>(tile_bw, tile_bh, r4, gfc, num_splats, cum,
                                                                   num_visible, projected, depths, tile_ids, cgids, zero,
-                                                                  zero_words);
+                                                                  zero_words, dev);
 }
 
 }  // namespace bh

@@ -30,7 +30,9 @@ namespace bh {
 // range and `ids` is 16-byte aligned), each compared with its predecessor:
 // a change of id at i ends the previous tile's run and starts the next one.
 __global__ __launch_bounds__(256) void tile_offsets_kernel(const uint32_t* __restrict__ ids, uint32_t m,
-                                                            uint32_t num_tiles, uint32_t* __restrict__ off) {
+                                                            uint32_t num_tiles, uint32_t* __restrict__ off,
+                                                            const uint32_t* __restrict__ dev_m) {
+    if (dev_m) m = min(m, *dev_m);
     const uint32_t i0 = (blockIdx.x * 256u + threadIdx.x) * 4u;
     if (i0 >= m) return;
     uint32_t v[4];
@@ -59,11 +61,12 @@ __global__ __launch_bounds__(256) void tile_offsets_kernel(const uint32_t* __res
 }
 
 void launch_tile_offsets(bh_ctx* ctx, const uint32_t* tile_ids, uint32_t m, uint32_t num_tiles,
-                         uint32_t* offsets, bool zeroed) {
+                         uint32_t* offsets, bool zeroed, const uint32_t* dev_m) {
     if (!zeroed) launch_fill_u32(ctx, offsets, 0u, (uint64_t)num_tiles * 2);
     if (m == 0) return;
     KernelTimer t(ctx, "tile_offsets");
-    tile_offsets_kernel<<<div_up(div_up(m, 4), 256), 256, 0, ctx->stream>>>(tile_ids, m, num_tiles, offsets);
+    tile_offsets_kernel<<<div_up(div_up(m, 4), 256), 256, 0, ctx->stream>>>(tile_ids, m, num_tiles, offsets,
+                                                                         dev_m);
 }
 
 // v_writelane_b32: writes the wave-uniform `value` into lane `lane` of `old`,

@@ -193,9 +193,14 @@ __global__ __launch_bounds__(kThreads) void radix_upsweep_kernel(const uint32_t*
                                                                   uint32_t shift, uint32_t digit_bits,
                                                                   uint32_t key_sub, uint32_t key_cap, uint32_t radix,
                                                                   uint32_t rows, uint32_t* __restrict__ counts,
-                                                                  uint32_t* __restrict__ blk) {
+                                                                  uint32_t* __restrict__ blk, SortDevice dev) {
     __shared__ uint32_t s_hist[kWaves][kRadix];
     const int tid = threadIdx.x, wave = tid >> 6;
+    if (dev.n) n = min(n, *dev.n);
+    if (FIRST && dev.key_sub) {
+        key_sub = *dev.key_sub;
+        key_cap = *dev.key_cap;
+    }
     for (int i = tid; i < kWaves * kRadix; i += kThreads) (&s_hist[0][0])[i] = 0;
     __syncthreads();
     constexpr int PART = kThreads * ITEMS;
@@ -340,7 +345,7 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
                                                              uint32_t key_cap, uint32_t radix,
                                                              const uint32_t* __restrict__ offs,
                                                              const uint32_t* __restrict__ gather_src,
-                                                             uint32_t* __restrict__ gather_out) {
+                                                             uint32_t* __restrict__ gather_out, SortDevice dev) {
     __shared__ uint32_t s_wave_hist[kWaves][kRadix];
     __shared__ uint32_t s_local_start[kRadix];
     __shared__ uint32_t s_global_off[kRadix];
@@ -350,6 +355,14 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t part = xcd_partition(blockIdx.x, gridDim.x);
+    if (dev.n) n = min(n, *dev.n);
+    if (FIRST && dev.key_sub) {
+        key_sub = *dev.key_sub;
+        key_cap = *dev.key_cap;
+    }
+    // a partition past a device-held count has no pairs (the grid is sized
+    // for the capacity); the upsweep wrote its counts as zeros
+    if ((uint64_t)part * (kThreads * ITEMS) >= n) return;
     // this partition's output offset of digit `tid`, loaded while the pairs are ranked
     const uint32_t my_off = (uint32_t)tid < radix ? offs[(size_t)part * radix + tid] : 0u;
     for (int i = tid; i < kWaves * kRadix; i += kThreads) (&s_wave_hist[0][0])[i] = 0;
@@ -481,20 +494,21 @@ size_t radix_sort_zeroed_words(uint32_t n, uint32_t key_bits) {
 template <bool FIRST, int ITEMS>
 static void launch_digit_pass(bh_ctx* ctx, uint32_t parts, const uint32_t* src_k, const uint32_t* src_v,
                               uint32_t* dk, uint32_t* dv, uint32_t n, uint32_t sh, uint32_t bits, uint32_t sub,
-                              uint32_t cap, uint32_t radix, const uint32_t* offs, const uint32_t* gs, uint32_t* go) {
+                              uint32_t cap, uint32_t radix, const uint32_t* offs, const uint32_t* gs, uint32_t* go,
+                              const SortDevice& dev) {
     if (go)
         onesweep_kernel<FIRST, ITEMS, true><<<parts, kThreads, 0, ctx->stream>>>(src_k, src_v, dk, dv, n, sh, bits, sub,
-                                                                              cap, radix, offs, gs, go);
+                                                                              cap, radix, offs, gs, go, dev);
     else
         onesweep_kernel<FIRST, ITEMS, false><<<parts, kThreads, 0, ctx->stream>>>(src_k, src_v, dk, dv, n, sh, bits,
-                                                                               sub, cap, radix, offs, gs, go);
+                                                                               sub, cap, radix, offs, gs, go, dev);
 }
 
 bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t* vals_in, uint32_t n,
                            uint32_t key_bits, uint32_t key_sub, uint32_t key_cap, uint32_t* keys_out,
                            uint32_t* vals_out, uint32_t* tmp_keys, uint32_t* tmp_vals, void* scratch,
                            const char* tag, bool scratch_zeroed, const uint32_t* gather_src,
-                           uint32_t* gather_out) {
+                           uint32_t* gather_out, const SortDevice& dev) {
     const std::string up_name = std::string(tag) + "_up", scan_name = std::string(tag) + "_scan",
                       pass_name = std::string(tag) + "_onesweep";
     if (n == 0) return BH_OK;
@@ -524,10 +538,12 @@ bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t*
             KernelTimer t(ctx, up_name.c_str());                                                                \
             if (p == 0)                                                                                         \
                 radix_upsweep_kernel<true, I><<<grid, block, 0, ctx->stream>>>(src_k, n, sh, bits, sub, cap,   \
-                                                                               sp.radix, sp.rows, offs, pblk); \
+                                                                               sp.radix, sp.rows, offs, pblk,  \
+                                                                               dev);                           \
             else                                                                                                \
                 radix_upsweep_kernel<false, I><<<grid, block, 0, ctx->stream>>>(src_k, n, sh, bits, sub, cap,  \
-                                                                                sp.radix, sp.rows, offs, pblk); \
+                                                                                sp.radix, sp.rows, offs, pblk, \
+                                                                                dev);                          \
         }                                                                                                       \
         {                                                                                                       \
             KernelTimer t(ctx, scan_name.c_str());                                                              \
@@ -538,10 +554,10 @@ bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t*
             KernelTimer t(ctx, pass_name.c_str());                                                              \
             if (p == 0)                                                                                         \
                 launch_digit_pass<true, I>(ctx, sp.parts, src_k, src_v, dk, dv, n, sh, bits, sub, cap, sp.radix,  \
-                                           offs, gs, go);                                                       \
+                                           offs, gs, go, dev);                                                  \
             else                                                                                                \
                 launch_digit_pass<false, I>(ctx, sp.parts, src_k, src_v, dk, dv, n, sh, bits, sub, cap,          \
-                                            sp.radix, offs, gs, go);                                            \
+                                            sp.radix, offs, gs, go, dev);                                       \
         }                                                                                                       \
     } while (0)
         if (sp.items == 8)
@@ -612,8 +628,10 @@ __device__ __forceinline__ uint32_t scan_value(const uint32_t* in, uint64_t idx,
 }
 
 __global__ __launch_bounds__(kThreads) void scan_reduce_kernel(const uint32_t* in, uint32_t n, uint32_t chunks,
-                                                                uint32_t* __restrict__ sums) {
+                                                                uint32_t* __restrict__ sums,
+                                                                const uint32_t* __restrict__ dev_n) {
     __shared__ uint32_t s_tot[kWaves];
+    if (dev_n) n = min(n, *dev_n);
     const uint64_t first = ((uint64_t)blockIdx.x * kThreads + threadIdx.x) * 4u * chunks;
     uint32_t run = 0;
     for (uint32_t c = 0; c < chunks; c++) {
@@ -628,8 +646,10 @@ __global__ __launch_bounds__(kThreads) void scan_reduce_kernel(const uint32_t* i
 }
 
 __global__ __launch_bounds__(kThreads) void scan_down_kernel(const uint32_t* in, uint32_t* out, uint32_t n,
-                                                              uint32_t chunks, const uint32_t* __restrict__ sums) {
+                                                              uint32_t chunks, const uint32_t* __restrict__ sums,
+                                                              const uint32_t* __restrict__ dev_n) {
     __shared__ uint32_t s_tot[kWaves];
+    if (dev_n) n = min(n, *dev_n);
     const uint32_t part = blockIdx.x, tid = threadIdx.x;
     const uint64_t first = ((uint64_t)part * kThreads + tid) * 4u * chunks;
     // the sums of the partitions before this one (part < 4096: 16 per thread)
@@ -669,17 +689,18 @@ __global__ __launch_bounds__(kThreads) void scan_down_kernel(const uint32_t* in,
 // bound of n)
 size_t scan_scratch_bytes(uint32_t) { return (size_t)4096 * 4; }
 
-bh_status inclusive_scan(bh_ctx* ctx, const uint32_t* in, uint32_t* out, uint32_t n, void* scratch) {
+bh_status inclusive_scan(bh_ctx* ctx, const uint32_t* in, uint32_t* out, uint32_t n, void* scratch,
+                         const uint32_t* dev_n) {
     if (n == 0) return BH_OK;
     const ScanGeom g = scan_geom(n);
     uint32_t* sums = (uint32_t*)scratch;
     {
         KernelTimer t(ctx, "scan_reduce");
-        scan_reduce_kernel<<<g.parts, kThreads, 0, ctx->stream>>>(in, n, g.chunks, sums);
+        scan_reduce_kernel<<<g.parts, kThreads, 0, ctx->stream>>>(in, n, g.chunks, sums, dev_n);
     }
     {
         KernelTimer t(ctx, "scan");
-        scan_down_kernel<<<g.parts, kThreads, 0, ctx->stream>>>(in, out, n, g.chunks, sums);
+        scan_down_kernel<<<g.parts, kThreads, 0, ctx->stream>>>(in, out, n, g.chunks, sums, dev_n);
     }
     return check_launch(ctx, "scan");
 }

@@ -182,9 +182,18 @@ bh_status bh_ctx_reset_timings(bh_ctx* ctx);
  *   produced is, naming the array and the first index; the reference panics
  *   there under its debug validation (Splats::validate_values / bwd_validate,
  *   crates/brush-render/src/gaussian_splats.rs:322-415, validation.rs:6-84).
- *   Costs one pass over the inputs (outputs) and one host synchronisation. */
+ *   Costs one pass over the inputs (outputs) and one host synchronisation.
+ * BH_DEBUG_EXACT_SIZES: bh_render_forward waits for its counts (visible
+ *   splats, intersections, depth-key range) before it queues the launches that
+ *   depend on them, as the reference does (render.rs:309-329).  By default a
+ *   forward after the first on a context queues those launches sized from the
+ *   previous forward's counts (buffers for that many intersections, plus
+ *   1/8), with the kernels reading the actual counts from device memory, and
+ *   checks the counts only after queueing; when they do not fit it queues the
+ *   exact launches again before it returns.  Both give identical results. */
 #define BH_DEBUG_POISON 1u
 #define BH_DEBUG_VALIDATE 2u
+#define BH_DEBUG_EXACT_SIZES 4u
 bh_status bh_ctx_set_debug(bh_ctx* ctx, uint32_t flags);
 /* Bytes currently cached by the context's workspace pool. */
 uint64_t bh_ctx_workspace_bytes(const bh_ctx* ctx);

@@ -49,6 +49,30 @@ def random_scene(seed: int, n: int, sh_degree: int = 3, mean_range=1.0, log_scal
     return generate_splats(w)
 
 
+def rng_scene(n, mean_range, log_scale_range, opacity_range, seed):
+    """The reference's rng_scene (crates/brush-render/src/tests/mod.rs:180-236): SplitMix64 uniforms, per
+    splat means, a non-normalised quaternion, log-scales, SH DC in [0, 1] and a
+    raw opacity, drawn in that order."""
+    k = np.arange(1, n * 14 + 1, dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        z = np.uint64(seed) + k * np.uint64(0x9E3779B97F4A7C15)
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        z = z ^ (z >> np.uint64(31))
+    u = (z.astype(np.float64) / float(2**64 - 1)).astype(np.float32).reshape(n, 14)
+
+    def span(x, lo, hi):
+        return (np.float32(lo) + x * np.float32(hi - lo)).astype(np.float32)
+
+    tr = np.empty((n, 10), np.float32)
+    tr[:, 0:3] = span(u[:, 0:3], -mean_range, mean_range)
+    tr[:, 3:7] = span(u[:, 3:7], -1.0, 1.0)
+    tr[:, 7:10] = span(u[:, 7:10], *log_scale_range)
+    sh = span(u[:, 10:13], 0.0, 1.0).reshape(n, 1, 3)
+    opac = span(u[:, 13], *opacity_range)
+    return tr, sh, opac
+
+
 def uniforms_for(cam: Camera, w: int, h: int, n: int, deg: int) -> dict:
     return project_uniforms(cam, w, h, n, deg)
 

@@ -30,36 +30,12 @@ import pytest
 from brush_amd.camera import Camera
 from oracle import oracle as O
 from tests.helpers import (compare_forward, gpu_forward, grad_close, gradient_term_magnitudes, random_scene,
-                           rel_close, uniforms_for)
+                           rel_close, rng_scene, uniforms_for)
 
 pytestmark = pytest.mark.gpu
 
 STATUS_NOT_FINITE = 6
 STATUS_INVALID_ARG = 1
-
-
-def rng_scene(n, mean_range, log_scale_range, opacity_range, seed):
-    """The reference's rng_scene (mod.rs:180-236): SplitMix64 uniforms, per
-    splat means, a non-normalised quaternion, log-scales, SH DC in [0, 1] and a
-    raw opacity, drawn in that order."""
-    k = np.arange(1, n * 14 + 1, dtype=np.uint64)
-    with np.errstate(over="ignore"):
-        z = np.uint64(seed) + k * np.uint64(0x9E3779B97F4A7C15)
-        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
-        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
-        z = z ^ (z >> np.uint64(31))
-    u = (z.astype(np.float64) / float(2**64 - 1)).astype(np.float32).reshape(n, 14)
-
-    def span(x, lo, hi):
-        return (np.float32(lo) + x * np.float32(hi - lo)).astype(np.float32)
-
-    tr = np.empty((n, 10), np.float32)
-    tr[:, 0:3] = span(u[:, 0:3], -mean_range, mean_range)
-    tr[:, 3:7] = span(u[:, 3:7], -1.0, 1.0)
-    tr[:, 7:10] = span(u[:, 7:10], *log_scale_range)
-    sh = span(u[:, 10:13], 0.0, 1.0).reshape(n, 1, 3)
-    opac = span(u[:, 13], *opacity_range)
-    return tr, sh, opac
 
 
 def _cam():
