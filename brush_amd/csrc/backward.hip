@@ -28,11 +28,6 @@
 #include "bh_splat_record.h"
 #include "bh_tile_walk.h"
 
-// Splats queued in LDS before the recorded backward sums them (1-3).
-#ifndef BH_RECORDED_SLOTS
-#define BH_RECORDED_SLOTS 2
-#endif
-
 namespace bh {
 
 // Sum of x over each 16-lane row of the wave, left in the row's last lane
@@ -313,19 +308,32 @@ void launch_rasterize_backward(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint
 // (bh_splat_record.h) instead of replaying the forward's decisions: per 8x8
 // block it visits only splats some pixel blended, and a pixel takes part only
 // where its own bit is set, so no cutoff test is evaluated.  The per-pair
-// arithmetic is the reference's (rasterize_backwards.rs:308-441): alpha,
-// transmittance and remaining colour exactly as the forward computed them (the
-// remaining colour is the final colour minus these contributions, and an alpha
-// one ulp off would leave it inconsistent deep in a stack), the gradient-only
-// products with FMA contraction.
+// arithmetic is the reference's (rasterize_backwards.rs:308-441), rearranged
+// so that every factor that is constant over a splat is applied once, after
+// the sum over the block's pixels, instead of once per pixel:
+//   * alpha and transmittance exactly as the forward computed them (its sigma,
+//     its exp, no contraction): the remaining colour below is the forward's
+//     final colour minus these contributions, and deep in a stack it is a
+//     small difference of nearly equal numbers, which an alpha off by an ulp
+//     would make inconsistent;
+//   * the remaining colour S enters the gradient only through the dot product
+//     S . v_out, so a pixel carries that one number (D = S . v_out, updated as
+//     D -= vis (c . v_out)) instead of the three channels of S;
+//   * the 2D-mean gradient v_sigma (C d) is linear in the conic, so the block
+//     sums v_sigma dx and v_sigma dy and the conic multiplies the two sums;
+//     the conic lanes sum v_sigma dx dx, dx dy, dy dy and take their factor
+//     0.5 after the sum; the colour lanes sum vis v_out and take the colour
+//     gates (v_rgb only where c >= 0) after the sum;
+//   * the refine weight |(W vx, H vy)| / A is not linear and stays per pixel.
+// The gradient-only products use FMA contraction.
 //
-// A splat's 9-11 gradient lanes are summed over the wave through LDS: every
-// lane writes its values into rows of 64 (one row per gradient lane), and once
-// NSLOT splats are queued, LPR lanes sum each row (a float4 loop over their
-// segment and one or two DPP adds) and one lane per row adds the total to the
-// splat's gradient row in HBM.  That costs about one VALU add per value where
-// a DPP / permlane transposed reduction costs about four, and it issues one
-// atomic instruction per NSLOT splats.
+// A splat's K gradient sums are formed through LDS: every lane writes its K
+// values into rows of 64 (one row per sum), and once NSLOT splats are queued,
+// two lanes per row sum its halves (a float4 loop) and one lane per row
+// applies the splat's factor and adds the total to the splat's gradient row
+// in HBM: about one VALU add per value and one atomic instruction per NSLOT
+// splats.  A slot's rows start at an even row, so its two mean rows lie in
+// one lane quad and a quad permute brings each the other's total.
 template <bool SMOOTH, bool REFINE, bool DEPTH, int TH, int NSLOT>
 __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
     uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t num_tiles, float bg_r, float bg_g, float bg_b,
@@ -335,20 +343,23 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
     float* __restrict__ v_rows) {
     constexpr uint32_t CH = DEPTH ? 5u : 4u;
     constexpr uint32_t BPT = 2u * (uint32_t)TH / 8u;
-    constexpr int K = 9 + (REFINE ? 1 : 0) + (DEPTH ? 1 : 0);  // gradient lanes summed per splat
-    constexpr int R = NSLOT * K;                                // LDS rows in use
-    constexpr int RPAD = R <= 16 ? 16 : (R <= 32 ? 32 : 64);
-    constexpr int LPR = 64 / RPAD;  // lanes that sum one row
-    constexpr int SEG = 64 / LPR;   // values each of them sums
-    constexpr int SSTR = SEG + 4;   // segment stride in floats (padded against bank conflicts)
-    constexpr int RS = LPR * SSTR;  // row stride in floats
-    static_assert(R <= 64 && SEG % 4 == 0, "flush geometry");
+    // sums per splat: v_sigma dx, v_sigma dy, v_sigma dx dx, v_sigma dx dy,
+    // v_sigma dy dy, vis v_r, vis v_g, vis v_b, the opacity lane, (refine), (depth)
+    constexpr int K = 9 + (REFINE ? 1 : 0) + (DEPTH ? 1 : 0);
+    constexpr int KP = (K + 1) & ~1;  // rows per slot (even)
+    constexpr int R = NSLOT * KP;     // rows in use
+    static_assert(NSLOT >= 1 && NSLOT <= 2 && R <= 32, "flush geometry: two slots of at most 16 rows");
+    // the batch's candidates
     __shared__ float4 s_geo[64];   // x, y, conic c00, c01
     __shared__ float4 s_op[64];    // conic c11, opacity, max(r, 0), max(g, 0)
-    __shared__ float4 s_gate[64];  // max(b, 0), the colour gradient gates (1 where c >= 0, else 0)
-    __shared__ uint32_t s_row[64];
-    __shared__ float4 s_red4[(R * RS + 3) / 4];
-    __shared__ uint32_t s_slot[NSLOT];
+    __shared__ float s_cb[64];     // max(b, 0)
+    __shared__ uint32_t s_gate[64];  // colour gates: bit c where channel c >= 0
+    __shared__ uint32_t s_row[64];   // gradient row (global id)
+    // R rows of two 32-float halves, each padded by 4 floats: a row's stores
+    // and the summing lanes' 16-byte reads are free of bank conflicts
+    constexpr int SSTR = 36;      // half-row stride in floats
+    constexpr int RS = 2 * SSTR;  // row stride in floats
+    __shared__ float4 s_red4[R * RS / 4];
     float* s_red = reinterpret_cast<float*>(s_red4);
 
     uint32_t tile, blk;
@@ -365,9 +376,9 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
     const bool inside = px < img_w && py < img_h;
     const float pcx = (float)px + 0.5f, pcy = (float)py + 0.5f;
 
-    // remaining colour (final minus background pre-roll) and transmittance
+    // transmittance and D = (final colour minus background pre-roll) . v_out
     // (rasterize_backwards.rs:193-250)
-    float sx = 0.0f, sy = 0.0f, sz = 0.0f, sw = 0.0f;
+    float sw = 0.0f, dsum = 0.0f;
     float vox = 0.0f, voy = 0.0f, voz = 0.0f, vow = 0.0f, vod = 0.0f, final_a = 0.0f;
     if (inside) {
         const size_t pix = (size_t)py * img_w + px;
@@ -375,15 +386,16 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
         const float* vo = v_output + pix * CH;
         final_a = o[3];
         const float t_final = 1.0f - final_a;
-        sx = o[0] - t_final * bg_r;
-        sy = o[1] - t_final * bg_g;
-        sz = o[2] - t_final * bg_b;
+        const float sx = o[0] - t_final * bg_r;
+        const float sy = o[1] - t_final * bg_g;
+        const float sz = o[2] - t_final * bg_b;
         sw = 1.0f;
         vox = vo[0];
         voy = vo[1];
         voz = vo[2];
         vow = (vo[3] - (bg_r * vox + bg_g * voy + bg_b * voz)) * t_final;
         if (DEPTH) vod = vo[4];
+        dsum = sx * vox + sy * voy + sz * voz;
     }
     // long blocks first (work sits in few tiles; see the replay kernel above)
     const uint32_t len = end - lo;
@@ -393,78 +405,119 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
         __builtin_amdgcn_s_setprio(2);
     else if (len >= 64u)
         __builtin_amdgcn_s_setprio(1);
-    const float w2 = (float)img_w * (float)img_w, h2 = (float)img_h * (float)img_h;
+    const float wf = (float)img_w, hf = (float)img_h;
     const float inv_final_a = __builtin_amdgcn_rcpf(bh_maxf(final_a, 1.0e-5f));
     const size_t rbase = record_base<BPT>(blk, lo, hi) - lo;
-    // where this lane's value goes in a row, and the row segment it sums
-    const uint32_t wcol = (lane / SEG) * SSTR + (lane % SEG);
-    const uint32_t frow = lane / LPR, fq = lane % LPR;
+    // where this lane's value goes in a row; the row and half a summing lane
+    // sums, and what multiplies its total: its own total times c00 (a slot's
+    // v_sigma dx row), c11 (its v_sigma dy row), 0.5 (the dx dx and dy dy
+    // rows), the colour gate (a colour row) or 1, plus the quad partner row's
+    // total times c01 (the two mean rows)
+    const uint32_t wcol = (lane >> 5) * SSTR + (lane & 31u);
+    const uint32_t frow = lane >> 1, fq = lane & 1u;
+    const uint32_t fslot = frow / (uint32_t)KP, fk = frow % (uint32_t)KP;
+    const float4* fsrc = reinterpret_cast<const float4*>(s_red + frow * RS + fq * SSTR);
+    const float fconst = (fk == 2u || fk == 4u) ? 0.5f : 1.0f;
+    const uint32_t fgate = fk >= 5u && fk <= 7u ? 1u << (fk - 5u) : 0u;
+    const uint32_t fdst = fk < 9u ? fk : (fk == 9u && REFINE ? 9u : 10u);
 
-    // sums the queued slots' rows and adds them to the splats' gradient rows
+    // Sums the queued slots' rows, applies each splat's factors and adds the
+    // totals to the splats' gradient rows.  A slot holds the candidate index
+    // of its splat in the current batch (the staging arrays outlive the
+    // slot: pending slots are flushed before the next batch is staged).
+    uint32_t slot_j0 = 0, slot_j1 = 0;
     auto flush = [&](uint32_t nslots) {
         wave_lds_fence();
+        const bool active = fslot < nslots && fk < (uint32_t)K;
+        // every lane reads its slot's splat (a valid candidate index either way)
+        const uint32_t js = fslot == 0u ? slot_j0 : slot_j1;
+        const float4 geo = s_geo[js];
+        const float c11 = s_op[js].x;
+        const uint32_t gates = s_gate[js], row = s_row[js];
         float acc = 0.0f;
-        if (frow < nslots * (uint32_t)K) {
-            const float4* src = reinterpret_cast<const float4*>(s_red + frow * RS + fq * SSTR);
-            float4 v = src[0];
+        if (active) {
+            float4 v = fsrc[0];
             acc = (v.x + v.y) + (v.z + v.w);
 #pragma unroll
-            for (int q = 1; q < SEG / 4; ++q) {
-                v = src[q];
+            for (int q = 1; q < 8; ++q) {
+                v = fsrc[q];
                 acc += (v.x + v.y) + (v.z + v.w);
             }
         }
-        // the LPR lanes of a row are one pair or one quad of lanes
-        if (LPR >= 2) acc = dpp_add<0xB1>(acc);  // quad_perm [1, 0, 3, 2]
-        if (LPR >= 4) acc = dpp_add<0x4E>(acc);  // quad_perm [2, 3, 0, 1]
-        if (fq == 0u && frow < nslots * (uint32_t)K && acc != 0.0f) {
-            const uint32_t slot = frow / (uint32_t)K, k = frow % (uint32_t)K;
-            const uint32_t dst_lane = k < 9u ? k : (k == 9u && REFINE ? 9u : 10u);
-            unsafeAtomicAdd(v_rows + (size_t)s_slot[slot] * kNG + dst_lane, acc);
+        acc = dpp_add<0xB1>(acc);  // quad_perm [1, 0, 3, 2]: the row's two halves
+        // quad_perm [2, 3, 0, 1]: the other row of the lane quad (a slot's
+        // v_sigma dx row for its v_sigma dy row and back)
+        const float other = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc), 0x4E, 0xF, 0xF, true));
+        if (active && fq == 0u) {
+            const float fsel = fk == 0u ? geo.z : c11;
+            const float fself = fk < 2u ? fsel : (fgate ? ((gates & fgate) ? 1.0f : 0.0f) : fconst);
+            const float v = fself * acc + (fk < 2u ? geo.w * other : 0.0f);
+            if (v != 0.0f) unsafeAtomicAdd(v_rows + (size_t)row * kNG + fdst, v);
         }
         wave_lds_fence();
     };
 
+    // lane j of a batch: the pixels that blended candidate b + j, and its id.
+    // Every load below is unconditional (indices clamped into the block's
+    // range), so the compiler's wait counts are exact: a batch's ids are read
+    // right after the previous batch's rows and arrive while it is evaluated.
+    const uint32_t last = end - 1u;
+    uint2 mask_n = rec.masks[rbase + min(lo + lane, last)];
+    uint32_t cid_n = cgids[min(lo + lane, last)];
     uint32_t nslot = 0;
     for (uint32_t b = lo; b < end; b += 64u) {
-        const uint32_t cnt = min(64u, end - b);
-        // lane j: the pixels that blended candidate b + j
-        uint2 mask = make_uint2(0u, 0u);
-        if (lane < cnt) mask = rec.masks[rbase + b + lane];
+        const uint2 mask = b + lane <= last ? mask_n : make_uint2(0u, 0u);
+        const uint32_t c = min(cid_n, num_visible - 1u);
+        const float2* prow = reinterpret_cast<const float2*>(projected + (size_t)c * 10);
+        const float2 r0 = prow[0], r1 = prow[1], r2 = prow[2], r3 = prow[3], r4 = prow[4];
+        const uint32_t grow = row_of[c];
+        // keep the issue order: these rows, then the next batch's ids, then
+        // their uses (the wait for the rows must not cover the ids)
+        __asm__ volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        const uint32_t bn = min(b + 64u + lane, last);
+        mask_n = rec.masks[rbase + bn];
+        cid_n = cgids[bn];
+        __asm__ volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
         const bool any = (mask.x | mask.y) != 0u;
-        if (any) {
-            const uint32_t c = min(cgids[b + lane], num_visible - 1u);
-            const float2* prow = reinterpret_cast<const float2*>(projected + (size_t)c * 10);
-            const float2 r0 = prow[0], r1 = prow[1], r2 = prow[2], r3 = prow[3], r4 = prow[4];
-            s_geo[lane] = make_float4(r0.x, r0.y, r1.x, r1.y);
-            s_op[lane] = make_float4(r2.x, r2.y, bh_maxf(r3.x, 0.0f), bh_maxf(r3.y, 0.0f));
-            s_gate[lane] = make_float4(bh_maxf(r4.x, 0.0f), r3.x >= 0.0f ? 1.0f : 0.0f, r3.y >= 0.0f ? 1.0f : 0.0f,
-                                       r4.x >= 0.0f ? 1.0f : 0.0f);
-            s_row[lane] = row_of[c];
-        }
+        // every lane stages (a candidate without pixels is never read), so
+        // the row loads stay ahead of the barrier above
+        s_geo[lane] = make_float4(r0.x, r0.y, r1.x, r1.y);
+        s_op[lane] = make_float4(r2.x, r2.y, bh_maxf(r3.x, 0.0f), bh_maxf(r3.y, 0.0f));
+        s_cb[lane] = bh_maxf(r4.x, 0.0f);
+        s_gate[lane] = (r3.x >= 0.0f ? 1u : 0u) | (r3.y >= 0.0f ? 2u : 0u) | (r4.x >= 0.0f ? 4u : 0u);
+        s_row[lane] = grow;
         uint64_t todo = __ballot(any);
         wave_lds_fence();
+        // the next candidate's parameters are read while the current one is
+        // evaluated
+        uint32_t jn = todo ? (uint32_t)__builtin_ctzll(todo) : 0u;
+        float4 geo_n = s_geo[jn], op_n = s_op[jn];
+        float cb_n = s_cb[jn];
         while (todo) {
-            const uint32_t j = (uint32_t)__builtin_ctzll(todo);
+            const uint32_t j = jn;
+            const float4 geo = geo_n, op = op_n;
+            const float cb = cb_n;
             todo &= todo - 1ull;
+            if (todo) {
+                jn = (uint32_t)__builtin_ctzll(todo);
+                geo_n = s_geo[jn];
+                op_n = s_op[jn];
+                cb_n = s_cb[jn];
+            }
             // candidate j's mask, read into scalar registers, is the lane condition
             // (readlane returns a signed int: widen through uint32_t, never by
             // sign extension)
             const uint64_t mj = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(mask.y, j) << 32) |
                                 (uint64_t)(uint32_t)__builtin_amdgcn_readlane(mask.x, j);
             const bool contrib = __builtin_amdgcn_inverse_ballot_w64(mj);
-            const float4 geo = s_geo[j];
-            const float4 op = s_op[j];
-            const float4 gt = s_gate[j];
             const float c00 = geo.z, c01 = geo.w, c11 = op.x, opac = op.y;
-            const float cr = op.z, cg = op.w, cb = gt.x;
-            // The replay state -- alpha, transmittance and remaining colour --
-            // is computed exactly as the forward computed it (its sigma, its
-            // exp, no contraction): the remaining colour is the forward's final
-            // colour minus these contributions, and deep in a stack it is a
-            // small difference of nearly equal numbers, which an alpha off by
-            // an ulp would make inconsistent.
-            const float sigma = calc_sigma(pcx, pcy, S2{c00, c01, c11}, geo.x, geo.y);
+            const float cr = op.z, cg = op.w;
+            // d = mean - pixel centre; the forward's sigma, whose products are
+            // even in the sign of d, bit for bit
+            const float dx = geo.x - pcx, dy = geo.y - pcy;
+            const float sigma = calc_sigma(geo.x, geo.y, S2{c00, c01, c11}, pcx, pcy);
             const float gauss = bh_expf_neg(-sigma);
             const float og = opac * gauss;
             const float alpha = bh_minf(0.999f, og);
@@ -484,56 +537,87 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
             {
 #pragma clang fp contract(fast)
                 // gradient-only arithmetic: products and sums fuse into FMAs
-                const float dx = geo.x - pcx, dy = geo.y - pcy;
-                g[5] = vis * vox * gt.y;
-                g[6] = vis * voy * gt.z;
-                g[7] = vis * voz * gt.w;
                 const float ra = __builtin_amdgcn_rcpf(one_minus);
-                const float dot_rgb = ((sw * cr - sx) * vox + (sw * cg - sy) * voy + (sw * cb - sz) * voz) * ra;
-                const float v_ae = dot_rgb + vow * ra;
+                const float cv = cr * vox + cg * voy + cb * voz;
+                // ((T c - S) . v_out + v_ow) / (1 - alpha)
+                const float v_ae = (sw * cv - dsum + vow) * ra;
                 const float v_alpha = SMOOTH ? v_ae * (w + alpha * cutoff_weight_deriv(alpha)) : v_ae;
                 const float v_sigma = gate ? -alpha * v_alpha : 0.0f;
-                const float vxy_x = v_sigma * (c00 * dx + c01 * dy);
-                const float vxy_y = v_sigma * (c01 * dx + c11 * dy);
-                g[0] = vxy_x;
-                g[1] = vxy_y;
-                g[2] = 0.5f * v_sigma * dx * dx;
-                g[3] = v_sigma * dx * dy;
-                g[4] = 0.5f * v_sigma * dy * dy;
+                const float t = v_sigma * dx, u = v_sigma * dy;
+                g[0] = t;
+                g[1] = u;
+                g[2] = t * dx;
+                g[3] = t * dy;
+                g[4] = u * dy;
+                g[5] = vis * vox;
+                g[6] = vis * voy;
+                g[7] = vis * voz;
                 g[8] = gate ? v_alpha * gauss : 0.0f;
-                if (REFINE)
-                    g[9] = __builtin_amdgcn_sqrtf(vxy_x * vxy_x * w2 + vxy_y * vxy_y * h2) * inv_final_a;
+                if (REFINE) {
+                    const float ax = wf * (c00 * t + c01 * u), ay = hf * (c01 * t + c11 * u);
+                    g[9] = __builtin_amdgcn_sqrtf(ax * ax + ay * ay) * inv_final_a;
+                }
                 if (DEPTH) g[K - 1] = vis * vod;
+                // the reference's state update (rasterize_backwards.rs:356-358,
+                // 432-435) as D -= vis (c . v_out)
+                dsum = dsum - vis * cv;
             }
-            // the reference's state update (rasterize_backwards.rs:356-358, 432-435)
-            sx = sx - vis * cr;
-            sy = sy - vis * cg;
-            sz = sz - vis * cb;
             sw = sw * one_minus;
-            float* dst = s_red + nslot * (uint32_t)(K * RS) + wcol;
+            float* dst = s_red + nslot * (uint32_t)(KP * RS) + wcol;
 #pragma unroll
             for (int k = 0; k < K; ++k) dst[k * RS] = g[k];
-            if (lane == 0u) s_slot[nslot] = s_row[j];
+            if (nslot == 0u) {
+                slot_j0 = j;
+            } else {
+                slot_j1 = j;
+            }
             if (++nslot == (uint32_t)NSLOT) {
                 flush(NSLOT);
                 nslot = 0;
             }
         }
+        // the next batch overwrites the staging arrays the slots refer to
+        if (nslot) {
+            flush(nslot);
+            nslot = 0;
+        }
         wave_lds_fence();
     }
-    if (nslot) flush(nslot);
 }
 
-template <int NSLOT>
-static void launch_recorded(bh_ctx* ctx, uint32_t groups, bool smooth, bool refine, bool depth, bool fine,
-                            uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t num_tiles, const float* bg,
-                            uint32_t num_visible, const float* out_img, const float* projected, const uint32_t* cgids,
-                            const uint32_t* off_pre, const SplatRecord& rec, const float* v_output,
-                            const uint32_t* row_of, const uint32_t* order, float* v_rows) {
-#define BH_RBR_T(S, R, D, T)                                                                                     \
-    rasterize_backward_recorded_kernel<S, R, D, T, NSLOT><<<groups, 64, 0, ctx->stream>>>(                       \
-        img_w, img_h, tile_bw, num_tiles, bg[0], bg[1], bg[2], num_visible, out_img, projected, cgids, off_pre, \
-        rec, v_output, row_of, order, v_rows)
+
+template <bool S, bool R, bool D, int T>
+static void launch_recorded_t(bh_ctx* ctx, uint32_t groups, uint32_t img_w, uint32_t img_h, uint32_t tile_bw,
+                              uint32_t num_tiles, const float* bg, uint32_t num_visible, const float* out_img,
+                              const float* projected, const uint32_t* cgids, const uint32_t* off_pre,
+                              const SplatRecord& rec, const float* v_output, const uint32_t* row_of,
+                              const uint32_t* order, float* v_rows) {
+#ifdef BH_RECORDED_SLOTS
+    constexpr int NS = BH_RECORDED_SLOTS;
+#else
+    constexpr int NS = 2;
+#endif
+    rasterize_backward_recorded_kernel<S, R, D, T, NS><<<groups, 64, 0, ctx->stream>>>(
+        img_w, img_h, tile_bw, num_tiles, bg[0], bg[1], bg[2], num_visible, out_img, projected, cgids, off_pre, rec,
+        v_output, row_of, order, v_rows);
+}
+
+void launch_rasterize_backward_recorded(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile_bw,
+                                        uint32_t tile_bh, const float* bg, uint32_t num_visible, const float* out_img,
+                                        const float* projected, const uint32_t* cgids, const uint32_t* off_pre,
+                                        const SplatRecord& rec, const float* v_output, uint32_t flags,
+                                        const uint32_t* row_of, const uint32_t* order, float* v_rows) {
+    const uint32_t num_tiles = tile_bw * tile_bh;
+    if (num_tiles == 0 || num_visible == 0 || !rec.masks) return;
+    const bool smooth = (flags & BH_FLAG_SMOOTH_CUTOFF) != 0;
+    const bool refine = (flags & BH_FLAG_REFINE_WEIGHT) != 0;
+    const bool depth = (flags & BH_FLAG_RENDER_DEPTH) != 0;
+    const bool fine = (flags & BH_FLAG_TILE_16X8) != 0;
+    const uint32_t groups = div_up(num_tiles, 8) * (fine ? 16u : 32u);
+    KernelTimer t(ctx, "rasterize_backward");
+#define BH_RBR_T(S, R, D, T)                                                                                      \
+    launch_recorded_t<S, R, D, T>(ctx, groups, img_w, img_h, tile_bw, num_tiles, bg, num_visible, out_img,       \
+                                  projected, cgids, off_pre, rec, v_output, row_of, order, v_rows)
 #define BH_RBR(S, R, D)              \
     do {                             \
         if (fine)                    \
@@ -556,24 +640,6 @@ static void launch_recorded(bh_ctx* ctx, uint32_t groups, bool smooth, bool refi
     }
 #undef BH_RBR
 #undef BH_RBR_T
-}
-
-void launch_rasterize_backward_recorded(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile_bw,
-                                        uint32_t tile_bh, const float* bg, uint32_t num_visible, const float* out_img,
-                                        const float* projected, const uint32_t* cgids, const uint32_t* off_pre,
-                                        const SplatRecord& rec, const float* v_output, uint32_t flags,
-                                        const uint32_t* row_of, const uint32_t* order, float* v_rows) {
-    const uint32_t num_tiles = tile_bw * tile_bh;
-    if (num_tiles == 0 || num_visible == 0 || !rec.masks) return;
-    const bool smooth = (flags & BH_FLAG_SMOOTH_CUTOFF) != 0;
-    const bool refine = (flags & BH_FLAG_REFINE_WEIGHT) != 0;
-    const bool depth = (flags & BH_FLAG_RENDER_DEPTH) != 0;
-    const bool fine = (flags & BH_FLAG_TILE_16X8) != 0;
-    const uint32_t groups = div_up(num_tiles, 8) * (fine ? 16u : 32u);
-    KernelTimer t(ctx, "rasterize_backward");
-    launch_recorded<BH_RECORDED_SLOTS>(ctx, groups, smooth, refine, depth, fine, img_w, img_h, tile_bw, num_tiles,
-                                       bg, num_visible, out_img, projected, cgids, off_pre, rec, v_output, row_of,
-                                       order, v_rows);
 }
 
 // ---- project backward ---------------------------------------------------------------
