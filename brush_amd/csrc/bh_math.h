@@ -85,6 +85,24 @@ BH_HD float bh_fmaf(float a, float b, float c) {
 #endif
 }
 
+/* Round to the nearest integer, ties to even (exact). */
+BH_HD float bh_rintf(float x) {
+#if defined(__HIPCC__)
+    return __builtin_rintf(x);
+#else
+    return rintf(x);
+#endif
+}
+
+/* p * 2^n (exact while the result is a normal number). */
+BH_HD float bh_ldexpf(float p, int n) {
+#if defined(__HIPCC__)
+    return __builtin_ldexpf(p, n);
+#else
+    return ldexpf(p, n);
+#endif
+}
+
 /* Multiply p by 2^n for n in [-150, 128] with IEEE rounding. */
 BH_HD float bh_scale_pow2(float p, int n) {
     if (n > 127) {
@@ -159,14 +177,16 @@ BH_HD float bh_logf(float x) {
 /* bh_expf for x in [-87, 0] (every argument the blend kernels evaluate:
  * x = -sigma with 0 <= sigma <= ln(255) + small): the same operations as
  * bh_expf without the NaN / overflow / subnormal branches, which cannot
- * trigger in that range, so the result is bit-identical there. */
+ * trigger in that range, so the result is bit-identical there.  The
+ * round-to-integer is a single rint (equal to the shifter sum for
+ * |k| < 2^22) and the scaling a single ldexp (equal to the multiply by the
+ * constructed 2^n while e^x is a normal number, x >= -87). */
 BH_HD float bh_expf_neg(float x) {
     const float log2e = 1.44269502162933349609375f;
     const float ln2_hi = 0.693145751953125f;
     const float ln2_lo = 1.428606765330187045e-06f;
-    const float shifter = 12582912.0f;
     float k = x * log2e;
-    float kr = (k + shifter) - shifter;
+    float kr = bh_rintf(k);
     int n = (int)kr;
     float r = bh_fmaf(kr, -ln2_hi, x);
     r = bh_fmaf(kr, -ln2_lo, r);
@@ -178,7 +198,7 @@ BH_HD float bh_expf_neg(float x) {
     p = bh_fmaf(p, r, 0.5f);
     p = bh_fmaf(p, r, 1.0f);
     p = bh_fmaf(p, r, 1.0f);
-    return p * bh_as_float((uint32_t)(n + 127) << 23);
+    return bh_ldexpf(p, n);
 }
 
 /* 1 / (1 + e^-x)  (brush-cube/src/lib.rs:620-623) */

@@ -254,7 +254,8 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
     const float pcx = (float)px + 0.5f, pcy = (float)py + 0.5f;
     const float bx0 = (float)ox + 0.5f, by0 = (float)oy + 0.5f;
     float t_acc = 1.0f, pr = 0.0f, pg = 0.0f, pb = 0.0f, pd = 0.0f;
-    bool done = !inside;
+    // pixels whose transmittance has saturated (or that lie outside the image)
+    uint64_t done_m = __builtin_amdgcn_ballot_w64(!inside);
     uint32_t last = lo;
     // a forward with BWD_INFO always records its pairs (the launcher passes
     // the record buffers whenever there are intersections)
@@ -262,60 +263,88 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
     constexpr bool record = BWD_INFO;
     const size_t rbase = record ? record_base<BPT>(blk, lo, hi) : 0;
 
+    // A batch's global accesses are ordered so that a wait never covers a
+    // later one: its candidate ids were read before the previous batch was
+    // blended; its rows (and, with BWD_INFO, the splats' global ids) are read
+    // first, then the previous batch's record and visibility stores go out,
+    // then the next batch's ids are read, so they arrive while this batch is
+    // blended.  The reads are unconditional, at indices clamped into the
+    // tile's run.
+    const uint32_t lastc = hi - 1u;
+    uint32_t cid_n = 0u;
+    if (hi > lo) cid_n = cgids[min(lo + lane, lastc)];
+    // the previous batch's stores, deferred
+    bool pend_vis = false, pend_mask = false;
+    uint32_t pend_gid = 0u;
+    size_t pend_at = 0;
+    uint32_t mask_lo = 0u, mask_hi = 0u;  // pixels that blended this lane's candidate
     for (uint32_t batch = lo; batch < hi; batch += 64u) {
-        if (__ballot(!done) == 0ull) break;
+        if (done_m == ~0ull) break;
         // a block still blending after 256 candidates is one of the long ones
         // whatever its candidate count said: top priority from here on
         if (batch - lo == 256u) __builtin_amdgcn_s_setprio(3);
         const uint32_t cnt = min(64u, hi - batch);
-        bool touch = false;
-        uint32_t my_c = 0;
-        if (lane < cnt) {
-            my_c = min(cgids[batch + lane], num_visible - 1u);
-            const float2* row = reinterpret_cast<const float2*>(projected + (size_t)my_c * 10);
-            const float2 a = row[0], b = row[1], cc = row[2], d = row[3], e = row[4];
-            const float cut = sigma_cutoff<SMOOTH>(cc.y);
-            s_xyco[lane] = make_float4(a.x, a.y, b.x, b.y);
-            s_c11a[lane] = make_float4(cc.x, cc.y, cut, 0.0f);
-            s_rgbd[lane] = make_float4(staged_colour(d.x), staged_colour(d.y), staged_colour(e.x), e.y);
-            touch = may_touch_rect(a.x, a.y, S2{b.x, b.y, cc.x}, cut, bx0, by0, bx0 + 7.0f, by0 + 7.0f);
-        }
+        const uint32_t my_c = min(cid_n, num_visible - 1u);
+        const float2* row = reinterpret_cast<const float2*>(projected + (size_t)my_c * 10);
+        const float2 a = row[0], b = row[1], cc = row[2], d = row[3], e = row[4];
+        const uint32_t my_gid = BWD_INFO ? gfc[my_c] : 0u;
+        __asm__ volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        if (BWD_INFO && pend_vis) visible[pend_gid] = 1.0f;
+        if (record && pend_mask) rec.masks[pend_at] = make_uint2(mask_lo, mask_hi);
+        __asm__ volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        cid_n = cgids[min(batch + 64u + lane, lastc)];
+        __asm__ volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        const float cut = sigma_cutoff<SMOOTH>(cc.y);
+        s_xyco[lane] = make_float4(a.x, a.y, b.x, b.y);
+        s_c11a[lane] = make_float4(cc.x, cc.y, cut, 0.0f);
+        s_rgbd[lane] = make_float4(staged_colour(d.x), staged_colour(d.y), staged_colour(e.x), e.y);
+        const bool touch = lane < cnt && may_touch_rect(a.x, a.y, S2{b.x, b.y, cc.x}, cut, bx0, by0, bx0 + 7.0f,
+                                                        by0 + 7.0f);
         // splats of the batch that may touch this block, in order
-        uint64_t todo = __ballot(touch);
+        uint64_t todo = __builtin_amdgcn_ballot_w64(touch);
         uint64_t used = 0ull;  // splats some pixel of the block blended
-        uint32_t mask_lo = 0u, mask_hi = 0u;  // pixels that blended this lane's candidate
+        mask_lo = 0u;
+        mask_hi = 0u;
         wave_lds_fence();
-        while (todo) {
-            const uint32_t j = (uint32_t)__builtin_ctzll(todo);
-            todo &= todo - 1ull;
-            const float4 xc = s_xyco[j];
-            const float4 ca = s_c11a[j];
+        // One candidate front to back; true once every pixel of the block is
+        // done.  The loop below reads the next candidate's parameters while
+        // the current one is evaluated, two register sets in turn.
+        auto blend_one = [&](uint32_t j, const float4& xc, const float4& ca, const float4& col) -> bool {
             const S2 conic{xc.z, xc.w, ca.x};
             const float sigma = calc_sigma(pcx, pcy, conic, xc.x, xc.y);
-            const bool maybe = !done && sigma >= 0.0f && !(sigma > ca.z);
-            if (__ballot(maybe) == 0ull) continue;
+            // lane conditions are kept as wave masks (scalar registers), each
+            // the ballot of a single comparison
+            const uint64_t maybe_m = __builtin_amdgcn_ballot_w64(sigma >= 0.0f) &
+                                     __builtin_amdgcn_ballot_w64(!(sigma > ca.z)) & ~done_m;
+            if (maybe_m == 0ull) return false;
             // Branch-free from here: lanes outside `maybe` compute values the
             // selects discard.  0 <= sigma <= cutoff < 6 where it matters, the
             // range in which bh_expf_neg equals bh_expf bit for bit.
             const float alpha = bh_minf(0.999f, ca.y * bh_expf_neg(-sigma));
             // the hard cutoff's weight is a step: alpha * w is a select
             const float w = SMOOTH ? cutoff_weight(alpha) : (alpha >= kCutMid ? 1.0f : 0.0f);
-            const bool pass = maybe && w > 0.0f;
             const float ae = SMOOTH ? alpha * w : (alpha >= kCutMid ? alpha : 0.0f);
             const float next_t = t_acc * (1.0f - ae);
-            const bool saturate = pass && next_t <= 1.0e-4f;
-            const bool contrib = pass && !saturate;
-            done = done || saturate;
-            const uint64_t blended = __ballot(contrib);
+            const uint64_t pass_m = maybe_m & __builtin_amdgcn_ballot_w64(w > 0.0f);
+            const uint64_t sat_m = __builtin_amdgcn_ballot_w64(next_t <= 1.0e-4f) & pass_m;
+            const uint64_t blended = pass_m & ~sat_m;
+            const bool contrib = __builtin_amdgcn_inverse_ballot_w64(blended);
+            done_m |= sat_m;
             if (blended != 0ull) {
-                const float vis = ae * t_acc;
-                const float4 col = s_rgbd[j];
-                pr = contrib ? pr + col.x * vis : pr;
-                pg = contrib ? pg + col.y * vis : pg;
-                pb = contrib ? pb + col.z * vis : pb;
-                if (DEPTH) pd = contrib ? pd + col.w * vis : pd;
+                // vis is zero outside `contrib`: adding col * 0 (a signed zero;
+                // colours are finite) leaves a sum that is >= +0 unchanged
+                const float vis = contrib ? ae * t_acc : 0.0f;
+                pr = pr + col.x * vis;
+                pg = pg + col.y * vis;
+                pb = pb + col.z * vis;
+                if (DEPTH) pd = pd + col.w * vis;
                 t_acc = contrib ? next_t : t_acc;
-                last = contrib ? batch + j + 1u : last;
+                // the block's last blended candidate (the tile end is the
+                // maximum over its pixels, the same for every lane)
+                last = batch + j + 1u;
                 if (BWD_INFO) used |= 1ull << j;
                 if (record) {
                     // the ballot (scalar) goes into candidate j's lane
@@ -323,12 +352,43 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
                     mask_hi = write_lane(mask_hi, (uint32_t)(blended >> 32), j);
                 }
             }
-            if (__ballot(!done) == 0ull) break;
+            return done_m == ~0ull;
+        };
+        if (todo) {
+            uint32_t ja = (uint32_t)__builtin_ctzll(todo);
+            todo &= todo - 1ull;
+            float4 xa = s_xyco[ja], caa = s_c11a[ja], cola = s_rgbd[ja];
+            while (true) {
+                const bool has_b = todo != 0ull;
+                uint32_t jb = 0u;
+                float4 xb, cab, colb;
+                if (has_b) {
+                    jb = (uint32_t)__builtin_ctzll(todo);
+                    todo &= todo - 1ull;
+                    xb = s_xyco[jb];
+                    cab = s_c11a[jb];
+                    colb = s_rgbd[jb];
+                }
+                if (blend_one(ja, xa, caa, cola) || !has_b) break;
+                const bool has_a = todo != 0ull;
+                if (has_a) {
+                    ja = (uint32_t)__builtin_ctzll(todo);
+                    todo &= todo - 1ull;
+                    xa = s_xyco[ja];
+                    caa = s_c11a[ja];
+                    cola = s_rgbd[ja];
+                }
+                if (blend_one(jb, xb, cab, colb) || !has_a) break;
+            }
         }
-        if (BWD_INFO && ((used >> lane) & 1ull)) visible[gfc[my_c]] = 1.0f;
-        if (record && lane < cnt) rec.masks[rbase + (batch - lo) + lane] = make_uint2(mask_lo, mask_hi);
+        pend_vis = BWD_INFO && ((used >> lane) & 1ull);
+        pend_gid = my_gid;
+        pend_mask = record && lane < cnt;
+        pend_at = rbase + (batch - lo) + lane;
         wave_lds_fence();
     }
+    if (BWD_INFO && pend_vis) visible[pend_gid] = 1.0f;
+    if (record && pend_mask) rec.masks[pend_at] = make_uint2(mask_lo, mask_hi);
 
     if (inside) {
         const float fr = pr + t_acc * bg_r, fg = pg + t_acc * bg_g, fb = pb + t_acc * bg_b;
@@ -357,9 +417,7 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
     // blended (the caller zero-filled off_post; every block of the tile adds
     // its own maximum)
     if (BWD_INFO) {
-        uint32_t m = last;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, o, 64));
+        const uint32_t m = last;  // wave-uniform: one past the block's last blended candidate
         if (lane == 0) atomicMax(&off_post[2 * tile + 1], m);
         if (record && lane == 0) rec.block_end[tile * BPT + blk] = m;
     }

@@ -26,6 +26,11 @@ void or_expf(const float* in, float* out, uint64_t n) {
     for (uint64_t i = 0; i < n; i++) out[i] = bh_expf(in[i]);
 }
 
+/* the blend kernels' exponential (bh_math.h), for its equality check */
+void or_expf_neg(const float* in, float* out, uint64_t n) {
+    for (uint64_t i = 0; i < n; i++) out[i] = bh_expf_neg(in[i]);
+}
+
 void or_logf(const float* in, float* out, uint64_t n) {
     for (uint64_t i = 0; i < n; i++) out[i] = bh_logf(in[i]);
 }

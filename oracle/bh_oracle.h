@@ -34,6 +34,7 @@ extern "C" {
 void or_set_threads(int n);
 /* Element-wise bh_expf / bh_logf, for pinning them against libm. */
 void or_expf(const float* in, float* out, uint64_t n);
+void or_expf_neg(const float* in, float* out, uint64_t n);
 void or_logf(const float* in, float* out, uint64_t n);
 void or_atan2f(const float* y, const float* x, float* out, uint64_t n);
 /* camera models on their own (test hooks): projection and depth cull,

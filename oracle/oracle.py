@@ -105,6 +105,7 @@ def lib():
         UP = ctypes.POINTER(Uniforms)
         L.or_set_threads.argtypes = [ctypes.c_int]
         L.or_expf.argtypes = [P, P, U64]
+        L.or_expf_neg.argtypes = [P, P, U64]
         L.or_logf.argtypes = [P, P, U64]
         L.or_atan2f.argtypes = [P, P, P, U64]
         L.or_camera_project.argtypes = [UP, P, U64, P, P]
@@ -148,6 +149,14 @@ def expf(x: np.ndarray) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.float32)
     out = np.empty_like(x)
     lib().or_expf(_p(x), _p(out), x.size)
+    return out
+
+
+def expf_neg(x: np.ndarray) -> np.ndarray:
+    """The blend kernels' exponential for arguments in [-87, 0]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().or_expf_neg(_p(x), _p(out), x.size)
     return out
 
 

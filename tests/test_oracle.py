@@ -39,6 +39,19 @@ def test_expf_within_2ulp_of_libm():
     assert O.expf(np.array([-np.inf], np.float32))[0] == 0.0
 
 
+def test_expf_neg_equals_expf_bit_for_bit():
+    """The blend kernels evaluate e^-sigma with bh_expf_neg (one rint and one
+    ldexp in place of the shifter sum and the constructed power of two); on
+    [-87, 0] it must equal bh_expf bit for bit, or blend decisions would
+    differ from the restatement's."""
+    rng = np.random.default_rng(7)
+    lo_bits = np.float32(-87.0).view(np.uint32)
+    bits = rng.integers(0x80000000, int(lo_bits) + 1, size=4_000_000, dtype=np.uint64).astype(np.uint32)
+    dense = -np.arange(0, 1 << 21, dtype=np.float32) * np.float32(3.0e-6)  # [-6.3, 0], the cutoff range
+    x = np.concatenate([bits.view(np.float32), dense, np.array([0.0, -0.0, -87.0, -1e-30], np.float32)])
+    assert np.array_equal(O.expf_neg(x).view(np.uint32), O.expf(x).view(np.uint32))
+
+
 def test_logf_within_2ulp_of_libm():
     rng = np.random.default_rng(1)
     bits = rng.integers(1, 0x7F800000, size=2_000_000, dtype=np.uint64).astype(np.uint32)
