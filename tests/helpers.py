@@ -110,24 +110,39 @@ def rel_close(name, got, want, rtol=1e-3, atol_frac=1e-5):
                            f"{err.reshape(-1)[bad[:3]]} at {bad[:3]} (want {want.reshape(-1)[bad[:3]]})")
 
 
+# lanes of v_combined that are sums of the same per-pixel terms times
+# different pixel offsets: 2D mean (0-1), conic (2-4), colour (5-7), opacity,
+# refine, depth
+LANE_GROUPS = ((0, 2), (2, 5), (5, 8), (8, 9), (9, 10), (10, 11))
+
+
 def gradient_term_magnitudes(o, tr, sh, opac, vc, mip: bool = False, rel: float = 3e-5, draws: int = 3,
                              seed: int = 0):
     """For each dense gradient entry (transforms, SH coefficients, raw
     opacities), how far it moves when the gradient lanes v_combined move by
-    `rel` relative noise, the size of the differences between two correct f32
-    summations of a lane in different orders.  Project backward turns conic
-    lanes of 1e4-1e6 into scale and rotation gradients of order 1-100 through
-    intermediates that cancel, so a few entries amplify lane differences of
-    1e-7 into percent-level changes (the CPU restatement and the GPU's
-    replay path, whose lanes agree to 7 digits, differ there); for a
+    the differences between two correct f32 summations of a lane in different
+    orders: `rel` noise relative to the largest lane of the lane's group.  A
+    lane's summation error scales with the size of its terms, and the lanes
+    of a group are sums of the same per-pixel terms (v_sigma times dx dx,
+    dx dy, dy dy for the conic lanes), so a lane that is a small difference of
+    large terms carries the error of its group's large lanes.  Project
+    backward turns conic lanes of 1e4-1e6 into scale and rotation gradients
+    of order 1-100 through intermediates that cancel, so a few entries amplify
+    lane differences of 1e-7 into percent-level changes (the CPU restatement
+    and the GPU, whose lanes agree to 7 digits, differ there); for a
     well-conditioned entry the movement is ~rel * |entry|.  The maximum over a
     few random perturbations."""
     base = [x.astype(np.float64) for x in O.project_backward(o, tr, sh, opac, vc, mip)[:3]]
     sens = [np.zeros(x.shape) for x in base]
     rng = np.random.default_rng(seed)
+    vc64 = vc.astype(np.float64)
+    scale = np.empty_like(vc64)
+    for a, b in LANE_GROUPS:
+        if a < vc64.shape[1]:
+            scale[:, a:b] = np.max(np.abs(vc64[:, a:b]), axis=1, keepdims=True)
     for _ in range(draws):
         noise = rng.uniform(-1.0, 1.0, vc.shape)
-        vp = (vc.astype(np.float64) * (1.0 + rel * noise)).astype(np.float32)
+        vp = (vc64 + rel * noise * scale).astype(np.float32)
         out = O.project_backward(o, tr, sh, opac, vp, mip)[:3]
         for s_, x, b in zip(sens, out, base):
             np.maximum(s_, np.abs(x.astype(np.float64) - b), out=s_)
