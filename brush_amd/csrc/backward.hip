@@ -28,6 +28,11 @@
 #include "bh_splat_record.h"
 #include "bh_tile_walk.h"
 
+// Candidates staged per batch by the recorded backward (32 or 64).
+#ifndef BH_BWD_BATCH
+#define BH_BWD_BATCH 64
+#endif
+
 namespace bh {
 
 // Sum of x over each 16-lane row of the wave, left in the row's last lane
@@ -350,11 +355,15 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
     constexpr int R = NSLOT * KP;     // rows in use
     static_assert(NSLOT >= 1 && NSLOT <= 2 && R <= 32, "flush geometry: two slots of at most 16 rows");
     // the batch's candidates
-    __shared__ float4 s_geo[64];   // x, y, conic c00, c01
-    __shared__ float4 s_op[64];    // conic c11, opacity, max(r, 0), max(g, 0)
-    __shared__ float s_cb[64];     // max(b, 0)
-    __shared__ uint32_t s_gate[64];  // colour gates: bit c where channel c >= 0
-    __shared__ uint32_t s_row[64];   // gradient row (global id)
+    // the batch's candidates (a batch of BATCH candidates; a smaller batch
+    // takes less LDS, so more blocks fit a CU)
+    constexpr uint32_t BATCH = BH_BWD_BATCH;
+    static_assert(BATCH == 32 || BATCH == 64, "batch of 32 or 64 candidates");
+    __shared__ float4 s_geo[BATCH];   // x, y, conic c00, c01
+    __shared__ float4 s_op[BATCH];    // conic c11, opacity, max(r, 0), max(g, 0)
+    __shared__ float s_cb[BATCH];     // max(b, 0)
+    __shared__ uint32_t s_gate[BATCH];  // colour gates: bit c where channel c >= 0
+    __shared__ uint32_t s_row[BATCH];   // gradient row (global id)
     // R rows of two 32-float halves, each padded by 4 floats: a row's stores
     // and the summing lanes' 16-byte reads are free of bank conflicts
     constexpr int SSTR = 36;      // half-row stride in floats
@@ -417,9 +426,13 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
     const uint32_t frow = lane >> 1, fq = lane & 1u;
     const uint32_t fslot = frow / (uint32_t)KP, fk = frow % (uint32_t)KP;
     const float4* fsrc = reinterpret_cast<const float4*>(s_red + frow * RS + fq * SSTR);
-    const float fconst = (fk == 2u || fk == 4u) ? 0.5f : 1.0f;
+    // the factors as weights of c00, c11, c01 and a constant (exact products
+    // by 0 and 1: a splat's conic is finite)
+    const float f00 = fk == 0u ? 1.0f : 0.0f, f11 = fk == 1u ? 1.0f : 0.0f, f01 = fk < 2u ? 1.0f : 0.0f;
     const uint32_t fgate = fk >= 5u && fk <= 7u ? 1u << (fk - 5u) : 0u;
+    const float fconst = fk < 2u || fgate ? 0.0f : ((fk == 2u || fk == 4u) ? 0.5f : 1.0f);
     const uint32_t fdst = fk < 9u ? fk : (fk == 9u && REFINE ? 9u : 10u);
+    const bool fwriter = fq == 0u;
 
     // Sums the queued slots' rows, applies each splat's factors and adds the
     // totals to the splats' gradient rows.  A slot holds the candidate index
@@ -448,12 +461,10 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
         // quad_perm [2, 3, 0, 1]: the other row of the lane quad (a slot's
         // v_sigma dx row for its v_sigma dy row and back)
         const float other = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc), 0x4E, 0xF, 0xF, true));
-        if (active && fq == 0u) {
-            const float fsel = fk == 0u ? geo.z : c11;
-            const float fself = fk < 2u ? fsel : (fgate ? ((gates & fgate) ? 1.0f : 0.0f) : fconst);
-            const float v = fself * acc + (fk < 2u ? geo.w * other : 0.0f);
-            if (v != 0.0f) unsafeAtomicAdd(v_rows + (size_t)row * kNG + fdst, v);
-        }
+        const float fg = (gates & fgate) ? 1.0f : 0.0f;
+        const float fself = f00 * geo.z + (f11 * c11 + (fconst + fg));
+        const float v = fself * acc + (f01 * geo.w) * other;
+        if (active && fwriter && v != 0.0f) unsafeAtomicAdd(v_rows + (size_t)row * kNG + fdst, v);
         wave_lds_fence();
     };
 
@@ -462,11 +473,12 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
     // range), so the compiler's wait counts are exact: a batch's ids are read
     // right after the previous batch's rows and arrive while it is evaluated.
     const uint32_t last = end - 1u;
-    uint2 mask_n = rec.masks[rbase + min(lo + lane, last)];
-    uint32_t cid_n = cgids[min(lo + lane, last)];
+    const uint32_t bl = lane & (BATCH - 1u);  // lanes >= BATCH repeat a load and stage nothing
+    uint2 mask_n = rec.masks[rbase + min(lo + bl, last)];
+    uint32_t cid_n = cgids[min(lo + bl, last)];
     uint32_t nslot = 0;
-    for (uint32_t b = lo; b < end; b += 64u) {
-        const uint2 mask = b + lane <= last ? mask_n : make_uint2(0u, 0u);
+    for (uint32_t b = lo; b < end; b += BATCH) {
+        const uint2 mask = lane < BATCH && b + lane <= last ? mask_n : make_uint2(0u, 0u);
         const uint32_t c = min(cid_n, num_visible - 1u);
         const float2* prow = reinterpret_cast<const float2*>(projected + (size_t)c * 10);
         const float2 r0 = prow[0], r1 = prow[1], r2 = prow[2], r3 = prow[3], r4 = prow[4];
@@ -475,37 +487,27 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
         // their uses (the wait for the rows must not cover the ids)
         __asm__ volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
-        const uint32_t bn = min(b + 64u + lane, last);
+        const uint32_t bn = min(b + BATCH + bl, last);
         mask_n = rec.masks[rbase + bn];
         cid_n = cgids[bn];
         __asm__ volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
         const bool any = (mask.x | mask.y) != 0u;
-        // every lane stages (a candidate without pixels is never read), so
+        // every lane stages (a candidate without pixels is never read; lanes
+        // bl and bl + 32 of a 32-candidate batch store the same values), so
         // the row loads stay ahead of the barrier above
-        s_geo[lane] = make_float4(r0.x, r0.y, r1.x, r1.y);
-        s_op[lane] = make_float4(r2.x, r2.y, bh_maxf(r3.x, 0.0f), bh_maxf(r3.y, 0.0f));
-        s_cb[lane] = bh_maxf(r4.x, 0.0f);
-        s_gate[lane] = (r3.x >= 0.0f ? 1u : 0u) | (r3.y >= 0.0f ? 2u : 0u) | (r4.x >= 0.0f ? 4u : 0u);
-        s_row[lane] = grow;
-        uint64_t todo = __ballot(any);
+        s_geo[bl] = make_float4(r0.x, r0.y, r1.x, r1.y);
+        s_op[bl] = make_float4(r2.x, r2.y, bh_maxf(r3.x, 0.0f), bh_maxf(r3.y, 0.0f));
+        s_cb[bl] = bh_maxf(r4.x, 0.0f);
+        s_gate[bl] = (r3.x >= 0.0f ? 1u : 0u) | (r3.y >= 0.0f ? 2u : 0u) | (r4.x >= 0.0f ? 4u : 0u);
+        s_row[bl] = grow;
+        uint64_t todo = __builtin_amdgcn_ballot_w64(any);
         wave_lds_fence();
-        // the next candidate's parameters are read while the current one is
-        // evaluated
-        uint32_t jn = todo ? (uint32_t)__builtin_ctzll(todo) : 0u;
-        float4 geo_n = s_geo[jn], op_n = s_op[jn];
-        float cb_n = s_cb[jn];
-        while (todo) {
-            const uint32_t j = jn;
-            const float4 geo = geo_n, op = op_n;
-            const float cb = cb_n;
-            todo &= todo - 1ull;
-            if (todo) {
-                jn = (uint32_t)__builtin_ctzll(todo);
-                geo_n = s_geo[jn];
-                op_n = s_op[jn];
-                cb_n = s_cb[jn];
-            }
+        // One candidate: its gradient values into a slot, flushed when the
+        // slots are full.  The loop below reads the next candidate's
+        // parameters while the current one is evaluated, two register sets
+        // in turn.
+        auto eval_one = [&](uint32_t j, const float4& geo, const float4& op, float cb) {
             // candidate j's mask, read into scalar registers, is the lane condition
             // (readlane returns a signed int: widen through uint32_t, never by
             // sign extension)
@@ -574,6 +576,37 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
             if (++nslot == (uint32_t)NSLOT) {
                 flush(NSLOT);
                 nslot = 0;
+            }
+        };
+        if (todo) {
+            uint32_t ja = (uint32_t)__builtin_ctzll(todo);
+            todo &= todo - 1ull;
+            float4 geoa = s_geo[ja], opa = s_op[ja];
+            float cba = s_cb[ja];
+            while (true) {
+                const bool has_b = todo != 0ull;
+                uint32_t jb = 0u;
+                float4 geob, opb;
+                float cbb = 0.0f;
+                if (has_b) {
+                    jb = (uint32_t)__builtin_ctzll(todo);
+                    todo &= todo - 1ull;
+                    geob = s_geo[jb];
+                    opb = s_op[jb];
+                    cbb = s_cb[jb];
+                }
+                eval_one(ja, geoa, opa, cba);
+                if (!has_b) break;
+                const bool has_a = todo != 0ull;
+                if (has_a) {
+                    ja = (uint32_t)__builtin_ctzll(todo);
+                    todo &= todo - 1ull;
+                    geoa = s_geo[ja];
+                    opa = s_op[ja];
+                    cba = s_cb[ja];
+                }
+                eval_one(jb, geob, opb, cbb);
+                if (!has_a) break;
             }
         }
         // the next batch overwrites the staging arrays the slots refer to

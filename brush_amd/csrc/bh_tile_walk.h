@@ -63,6 +63,36 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
     return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
 }
 
+// The power will_contribute (bh_splat_math.h) compares with the threshold,
+// evaluated without branches: both edge quotients and the power at the
+// clamped edge point are computed for every lane and the predicate's selects
+// pick them, so `power <= pt` is the predicate's decision bit for bit (a splat
+// whose mean lies in the tile gets -1, which passes).  Tile widths 16 and TH
+// are exact differences of the tile's float edges for tile columns < 2^20.
+template <int TH>
+__device__ __forceinline__ float tile_power(uint32_t tx, uint32_t ty, V2 m, const S2& c) {
+    const float min_x = (float)(tx * 16u), min_y = (float)(ty * (uint32_t)TH);
+    const float max_x = min_x + 16.0f, max_y = min_y + (float)TH;
+    const bool x_left = m.x < min_x, x_right = m.x > max_x;
+    const bool in_x = !(x_left || x_right);
+    const bool y_above = m.y < min_y, y_below = m.y > max_y;
+    const bool in_y = !(y_above || y_below);
+    const float corner_x = x_left ? min_x : max_x;
+    const float corner_y = y_above ? min_y : max_y;
+    const float dxf = x_left ? 16.0f : -16.0f;
+    const float dyf = y_above ? (float)TH : -(float)TH;
+    const float diff_x = m.x - corner_x;
+    const float diff_y = m.y - corner_y;
+    const float qx = bh_clampf((dxf * c.c00 * diff_x + dxf * c.c01 * diff_y) / (dxf * c.c00 * dxf), 0.0f, 1.0f);
+    const float qy = bh_clampf((dyf * c.c01 * diff_x + dyf * c.c11 * diff_y) / (dyf * c.c11 * dyf), 0.0f, 1.0f);
+    const float tt_x = in_y ? 0.0f : qx;
+    const float tt_y = in_x ? 0.0f : qy;
+    const float px = corner_x + tt_x * dxf;
+    const float py = corner_y + tt_y * dyf;
+    const float power = calc_sigma(px, py, c, m.x, m.y);
+    return (in_x && in_y) ? -1.0f : power;
+}
+
 // Items (bbox tiles) of a splat whose box is bb; zero for an empty box.
 __device__ __forceinline__ uint32_t bbox_items(const TileBox& bb) {
     return (bb.max_x > bb.min_x && bb.max_y > bb.min_y) ? (bb.max_x - bb.min_x) * (bb.max_y - bb.min_y) : 0u;
@@ -104,19 +134,18 @@ __device__ uint32_t wave_tile_walk(uint32_t lane, uint32_t items, V2 m, const S2
         const WalkRec r = rec[owner & 63u];
         const uint32_t local = item - r.c.w;
         // row = local / width through the float reciprocal, then one exact
-        // correction step either way
+        // correction step either way (selects, no branches)
         uint32_t row = (uint32_t)(((float)local + 0.5f) * r.b.z);
         int32_t col = (int32_t)(local - row * r.c.z);
-        if (col < 0) {
-            row -= 1u;
-            col += (int32_t)r.c.z;
-        } else if ((uint32_t)col >= r.c.z) {
-            row += 1u;
-            col -= (int32_t)r.c.z;
-        }
+        const bool under = col < 0;
+        const bool over = !under && (uint32_t)col >= r.c.z;
+        row = under ? row - 1u : (over ? row + 1u : row);
+        col = under ? col + (int32_t)r.c.z : (over ? col - (int32_t)r.c.z : col);
         const uint32_t tx = r.c.x + (uint32_t)col, ty = r.c.y + row;
-        const bool pass = valid && will_contribute<TH>(tx, ty, v2(r.a.x, r.a.y), S2{r.a.z, r.a.w, r.b.x}, r.b.y);
-        const uint64_t pmask = __ballot(pass);
+        // will_contribute as one comparison; the lane conditions stay wave masks
+        const float power = tile_power<TH>(tx, ty, v2(r.a.x, r.a.y), S2{r.a.z, r.a.w, r.b.x});
+        const uint64_t pmask = __builtin_amdgcn_ballot_w64(power <= r.b.y) & __builtin_amdgcn_ballot_w64(valid);
+        const bool pass = __builtin_amdgcn_inverse_ballot_w64(pmask);
         // the last lane of each splat's run in this step adds the run's hits
         const uint32_t run_lo = r.c.w > base ? r.c.w - base : 0u;
         const uint32_t before_run = (uint32_t)__popcll(pmask & ((1ull << run_lo) - 1ull));
