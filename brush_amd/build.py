@@ -30,7 +30,25 @@ FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall",
     "-Wno-unused-function",
+    # per-kernel VGPRs, LDS, occupancy and scratch, checked below
+    "-Rpass-analysis=kernel-resource-usage",
 ]
+
+
+def kernel_resources(stderr: str) -> dict:
+    """Parses the compiler's kernel-resource-usage remarks into
+    {kernel: {field: value}} (fields as the compiler names them)."""
+    out, cur = {}, None
+    for line in stderr.splitlines():
+        if "remark:" not in line:
+            continue
+        text = line.split("remark:", 1)[1].split("[-Rpass", 1)[0].strip()
+        if text.startswith("Function Name:"):
+            cur = out.setdefault(text.split(":", 1)[1].strip(), {})
+        elif cur is not None and ":" in text:
+            k, v = text.rsplit(":", 1)
+            cur[k.strip()] = v.strip()
+    return out
 
 
 def _run(cmd):
@@ -59,6 +77,19 @@ def build(verbose: bool = True) -> str:
         if res.returncode != 0:
             sys.stderr.write(res.stdout + res.stderr)
             raise RuntimeError(f"hipcc failed to compile {cmd[-1]}")
+    # A kernel that spills to scratch (private memory) runs several times
+    # slower; none of this library's kernels needs scratch, so one that does
+    # is a build error (a captured lambda variable that lost SROA was one).
+    res = {}
+    for e in stderr:
+        res.update(kernel_resources(e))
+    scratch = {k: v.get("ScratchSize [bytes/lane]") for k, v in res.items()
+               if v.get("ScratchSize [bytes/lane]", "0") != "0"}
+    if scratch:
+        raise RuntimeError(f"kernels use scratch memory: {scratch}")
+    with open(os.path.join(objdir, "kernel_resources.txt"), "w") as f:
+        for k in sorted(res):
+            f.write(k + " " + " | ".join(f"{a}={b}" for a, b in res[k].items()) + "\n")
     tmp = OUT + ".tmp"
     res = _run([HIPCC, "--offload-arch=gfx950", "-fPIC", "-shared", "-o", tmp, *[obj for obj, _ in jobs]])
     if res.returncode != 0:
@@ -66,7 +97,8 @@ def build(verbose: bool = True) -> str:
         raise RuntimeError("hipcc failed to link libbrush_hip.so")
     os.replace(tmp, OUT)
     if verbose:
-        warn = [l for e in stderr for l in e.splitlines() if "warning" in l and "packed-fp32-ops" not in l]
+        warn = [l for e in stderr for l in e.splitlines()
+                if "warning" in l and "packed-fp32-ops" not in l and "remark" not in l]
         for l in warn[:20]:
             print("[build]", l)
         print(f"[build] {OUT} ({time.time() - t0:.1f} s)", flush=True)

@@ -32,6 +32,10 @@
 #ifndef BH_BWD_BATCH
 #define BH_BWD_BATCH 64
 #endif
+// Most splats the recorded backward queues before summing their rows (1-3).
+#ifndef BH_RECORDED_SLOTS
+#define BH_RECORDED_SLOTS 2
+#endif
 
 namespace bh {
 
@@ -353,7 +357,7 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
     constexpr int K = 9 + (REFINE ? 1 : 0) + (DEPTH ? 1 : 0);
     constexpr int KP = (K + 1) & ~1;  // rows per slot (even)
     constexpr int R = NSLOT * KP;     // rows in use
-    static_assert(NSLOT >= 1 && NSLOT <= 2 && R <= 32, "flush geometry: two slots of at most 16 rows");
+    static_assert(NSLOT >= 1 && NSLOT <= 3 && R <= 32, "flush geometry: up to three slots, at most 32 rows");
     // the batch's candidates
     // the batch's candidates (a batch of BATCH candidates; a smaller batch
     // takes less LDS, so more blocks fit a CU)
@@ -438,12 +442,12 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
     // totals to the splats' gradient rows.  A slot holds the candidate index
     // of its splat in the current batch (the staging arrays outlive the
     // slot: pending slots are flushed before the next batch is staged).
-    uint32_t slot_j0 = 0, slot_j1 = 0;
+    uint32_t slot_js = 0;  // queued candidate indices, six bits a slot
     auto flush = [&](uint32_t nslots) {
         wave_lds_fence();
         const bool active = fslot < nslots && fk < (uint32_t)K;
         // every lane reads its slot's splat (a valid candidate index either way)
-        const uint32_t js = fslot == 0u ? slot_j0 : slot_j1;
+        const uint32_t js = (slot_js >> (6u * fslot)) & 63u;
         const float4 geo = s_geo[js];
         const float c11 = s_op[js].x;
         const uint32_t gates = s_gate[js], row = s_row[js];
@@ -568,14 +572,11 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
             float* dst = s_red + nslot * (uint32_t)(KP * RS) + wcol;
 #pragma unroll
             for (int k = 0; k < K; ++k) dst[k * RS] = g[k];
-            if (nslot == 0u) {
-                slot_j0 = j;
-            } else {
-                slot_j1 = j;
-            }
+            slot_js |= j << (6u * nslot);
             if (++nslot == (uint32_t)NSLOT) {
                 flush(NSLOT);
                 nslot = 0;
+                slot_js = 0;
             }
         };
         if (todo) {
@@ -613,6 +614,7 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
         if (nslot) {
             flush(nslot);
             nslot = 0;
+            slot_js = 0;
         }
         wave_lds_fence();
     }
@@ -625,11 +627,9 @@ static void launch_recorded_t(bh_ctx* ctx, uint32_t groups, uint32_t img_w, uint
                               const float* projected, const uint32_t* cgids, const uint32_t* off_pre,
                               const SplatRecord& rec, const float* v_output, const uint32_t* row_of,
                               const uint32_t* order, float* v_rows) {
-#ifdef BH_RECORDED_SLOTS
-    constexpr int NS = BH_RECORDED_SLOTS;
-#else
-    constexpr int NS = 2;
-#endif
+    // slots per flush: as many as fit 32 rows, up to BH_RECORDED_SLOTS
+    constexpr int KP = (9 + (R ? 1 : 0) + (D ? 1 : 0) + 1) & ~1;
+    constexpr int NS = (32 / KP) < BH_RECORDED_SLOTS ? (32 / KP) : BH_RECORDED_SLOTS;
     rasterize_backward_recorded_kernel<S, R, D, T, NS><<<groups, 64, 0, ctx->stream>>>(
         img_w, img_h, tile_bw, num_tiles, bg[0], bg[1], bg[2], num_visible, out_img, projected, cgids, off_pre, rec,
         v_output, row_of, order, v_rows);
