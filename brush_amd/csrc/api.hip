@@ -629,17 +629,21 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
         BH_TRY(sget((void**)&gfc, (size_t)std::max<uint32_t>(num_splats, 1u) * 4));
         if (p.v) {
             // depth sort: key' = min(bits - kmin, kmax - kmin + 1); culled splats
-            // (all-ones key) map to the cap and sort last.  The last pass also
-            // gathers each splat's tile count in depth order, so the scan below
-            // reads them contiguously.  A plan with more key bits than the
-            // range needs sorts the same: its extra passes see digit 0 only.
+            // (all-ones key) map to the cap, and the first pass drops them, so
+            // the later passes sort only the visible splats (render.rs:339-346
+            // sorts the visible depths).  The last pass also gathers each
+            // splat's tile count in depth order, so the scan below reads them
+            // contiguously.  A plan with more key bits than the range needs
+            // sorts the same: its extra passes see digit 0 only.
             uint32_t *sk, *tk, *tv;
             BH_TRY(ws.get(&sk, num_splats));
             BH_TRY(ws.get(&tk, num_splats));
             BH_TRY(ws.get(&tv, num_splats));
             BH_TRY(ws.get(&counts_sorted, num_splats));
             SortDevice dev;
-            if (dc) dev.key_sub = dc + 4, dev.key_cap = dc + 6;
+            if (dc) dev.key_sub = dc + 4, dev.key_cap = dc + 6, dev.n_rest = dc + 0;
+            dev.drop_capped = true;
+            dev.n_rest_host = p.v;
             BH_TRY(radix_sort_pairs(ctx, depth_keys, nullptr, num_splats, p.key_bits, p.kmin, p.kcap, sk, gfc, tk, tv,
                                     depth_scr, "depth_sort", true, counts, counts_sorted, dev));
         }

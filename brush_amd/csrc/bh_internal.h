@@ -147,6 +147,13 @@ struct SortDevice {
     const uint32_t* n = nullptr;
     const uint32_t* key_sub = nullptr;
     const uint32_t* key_cap = nullptr;
+    // with drop_capped: the pairs left after the first pass (a capacity's
+    // actual count; the host value is n_rest)
+    const uint32_t* n_rest = nullptr;
+    // the first pass drops every pair whose transformed key equals key_cap
+    // (the depth sort's culled splats), so later passes sort n_rest pairs
+    bool drop_capped = false;
+    uint32_t n_rest_host = 0;
 };
 // Stable sort of (key', value) pairs by the low key_bits bits of
 // key' = min(key - key_sub, key_cap), in ceil(key_bits / 8) passes of equal

@@ -208,6 +208,8 @@ __global__ __launch_bounds__(kThreads) void radix_upsweep_kernel(const uint32_t*
     const uint64_t base = (uint64_t)part * PART;
     const uint32_t dmask = (1u << digit_bits) - 1u;
     uint32_t* mine = s_hist[wave];
+    // the first pass of a dropping sort does not count capped keys
+    const bool drop = FIRST && dev.drop_capped;
     if (base + PART <= n && (reinterpret_cast<uintptr_t>(keys) & 15u) == 0u) {
         const uint4* k4 = reinterpret_cast<const uint4*>(keys + base);
         uint4 q[ITEMS / 4];
@@ -219,7 +221,7 @@ __global__ __launch_bounds__(kThreads) void radix_upsweep_kernel(const uint32_t*
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const uint32_t k = FIRST ? min(kk[e] - key_sub, key_cap) : kk[e];
-                atomicAdd(&mine[(k >> shift) & dmask], 1u);
+                if (!(drop && k == key_cap)) atomicAdd(&mine[(k >> shift) & dmask], 1u);
             }
         }
     } else {
@@ -228,7 +230,7 @@ __global__ __launch_bounds__(kThreads) void radix_upsweep_kernel(const uint32_t*
             const uint64_t idx = base + (uint64_t)j * kThreads + tid;
             if (idx < n) {
                 const uint32_t k = FIRST ? min(keys[idx] - key_sub, key_cap) : keys[idx];
-                atomicAdd(&mine[(k >> shift) & dmask], 1u);
+                if (!(drop && k == key_cap)) atomicAdd(&mine[(k >> shift) & dmask], 1u);
             }
         }
     }
@@ -372,25 +374,29 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
     const uint32_t dmask = (1u << digit_bits) - 1u;
 
     uint32_t k[ITEMS], v[ITEMS], pos[ITEMS];
+    // the first pass of a dropping sort neither ranks nor writes capped keys
+    const bool drop = FIRST && dev.drop_capped;
+    uint32_t kept = 0;  // bit j: item j is a pair of this pass
 #pragma unroll
     for (int j = 0; j < ITEMS; j++) {
         uint64_t idx = wave_base + (uint64_t)j * 64 + lane;
         bool valid = idx < n;
         uint32_t kk = valid ? keys_in[idx] : 0u;
         if (FIRST) kk = min(kk - key_sub, key_cap);
+        if (drop && kk == key_cap) valid = false;
+        if (valid) kept |= 1u << j;
         k[j] = kk;
         v[j] = valid ? (vals_in ? vals_in[idx] : (uint32_t)idx) : 0u;
     }
     uint32_t gv[GATHER ? ITEMS : 1];
     if (GATHER) {
 #pragma unroll
-        for (int j = 0; j < ITEMS; j++) gv[j] = wave_base + (uint64_t)j * 64 + lane < n ? gather_src[v[j]] : 0u;
+        for (int j = 0; j < ITEMS; j++) gv[j] = (kept >> j) & 1u ? gather_src[v[j]] : 0u;
     }
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 #pragma unroll
     for (int j = 0; j < ITEMS; j++) {
-        uint64_t idx = wave_base + (uint64_t)j * 64 + lane;
-        bool valid = idx < n;
+        const bool valid = (kept >> j) & 1u;
         uint32_t d = (k[j] >> shift) & dmask;
         uint64_t peers = __ballot(valid);
         for (uint32_t b = 0; b < digit_bits; b++) {
@@ -417,8 +423,8 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
         s_wave_hist[w][d] = total;
         total += c[w];
     }
-    uint32_t tot_dummy;
-    const uint32_t local_start = block_exclusive_scan<kThreads>(total, s_tot, &tot_dummy);
+    uint32_t count;  // the partition's pairs (dropped keys excluded)
+    const uint32_t local_start = block_exclusive_scan<kThreads>(total, s_tot, &count);
     s_local_start[d] = local_start;
     s_global_off[d] = my_off;
     __syncthreads();
@@ -427,13 +433,11 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
     // is kept for the values
 #pragma unroll
     for (int j = 0; j < ITEMS; j++) {
-        uint64_t idx = wave_base + (uint64_t)j * 64 + lane;
         uint32_t dd = (k[j] >> shift) & dmask;
         pos[j] = s_local_start[dd] + s_wave_hist[wave][dd] + pos[j];
-        if (idx < n) s_buf[pos[j]] = k[j];
+        if ((kept >> j) & 1u) s_buf[pos[j]] = k[j];
     }
     __syncthreads();
-    const uint32_t count = (uint32_t)min<uint64_t>((uint64_t)PART, (uint64_t)n - base);
     uint32_t dst[ITEMS];
 #pragma unroll
     for (int j = 0; j < ITEMS; j++) {
@@ -451,10 +455,8 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
     }
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < ITEMS; j++) {
-        uint64_t idx = wave_base + (uint64_t)j * 64 + lane;
-        if (idx < n) s_buf[pos[j]] = v[j];
-    }
+    for (int j = 0; j < ITEMS; j++)
+        if ((kept >> j) & 1u) s_buf[pos[j]] = v[j];
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < ITEMS; j++) {
@@ -464,10 +466,8 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
     if (GATHER) {
         __syncthreads();
 #pragma unroll
-        for (int j = 0; j < ITEMS; j++) {
-            uint64_t idx = wave_base + (uint64_t)j * 64 + lane;
-            if (idx < n) s_buf[pos[j]] = gv[j];
-        }
+        for (int j = 0; j < ITEMS; j++)
+            if ((kept >> j) & 1u) s_buf[pos[j]] = gv[j];
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < ITEMS; j++) {
@@ -520,7 +520,14 @@ bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t*
     if (!scratch_zeroed) launch_fill_u32(ctx, blk, 0u, radix_sort_zeroed_words(n, key_bits));
     const uint32_t* src_k = keys_in;
     const uint32_t* src_v = vals_in;
+    // a dropping sort: the first pass sees n pairs, the later ones n_rest
+    SortDevice dev_rest = dev;
+    dev_rest.drop_capped = false;
+    if (dev.drop_capped && dev.n_rest) dev_rest.n = dev.n_rest;
+    const uint32_t n_first = n, n_later = dev.drop_capped ? std::min(n, dev.n_rest_host) : n;
     for (uint32_t p = 0; p < plan.passes; p++) {
+        const SortDevice& pdev = p == 0 ? dev : dev_rest;
+        n = p == 0 ? n_first : n_later;
         // the last pass lands in the output buffers
         bool to_out = ((plan.passes - 1 - p) % 2) == 0;
         uint32_t* dk = to_out ? keys_out : tmp_keys;
@@ -539,11 +546,11 @@ bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t*
             if (p == 0)                                                                                         \
                 radix_upsweep_kernel<true, I><<<grid, block, 0, ctx->stream>>>(src_k, n, sh, bits, sub, cap,   \
                                                                                sp.radix, sp.rows, offs, pblk,  \
-                                                                               dev);                           \
+                                                                               pdev);                          \
             else                                                                                                \
                 radix_upsweep_kernel<false, I><<<grid, block, 0, ctx->stream>>>(src_k, n, sh, bits, sub, cap,  \
                                                                                 sp.radix, sp.rows, offs, pblk, \
-                                                                                dev);                          \
+                                                                                pdev);                         \
         }                                                                                                       \
         {                                                                                                       \
             KernelTimer t(ctx, scan_name.c_str());                                                              \
@@ -554,10 +561,10 @@ bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t*
             KernelTimer t(ctx, pass_name.c_str());                                                              \
             if (p == 0)                                                                                         \
                 launch_digit_pass<true, I>(ctx, sp.parts, src_k, src_v, dk, dv, n, sh, bits, sub, cap, sp.radix,  \
-                                           offs, gs, go, dev);                                                  \
+                                           offs, gs, go, pdev);                                                 \
             else                                                                                                \
                 launch_digit_pass<false, I>(ctx, sp.parts, src_k, src_v, dk, dv, n, sh, bits, sub, cap,          \
-                                            sp.radix, offs, gs, go, dev);                                       \
+                                            sp.radix, offs, gs, go, pdev);                                      \
         }                                                                                                       \
     } while (0)
         if (sp.items == 8)

@@ -8,6 +8,8 @@ frames with more than 16384 tiles.
 * invariance: appending culled splats, or prepending a culled prefix that
   shifts every global id, leaves the render bit for bit the same
   (mod.rs:334-410), and the culled splats get exactly zero gradients;
+* a 90 % culled scene sorts only its visible splats and renders bit for bit
+  as the restatement, with counts read back first and from a plan;
 * stress: 120k fullscreen splats render deterministically with no dropped
   tile, 200k large splats leave no tile empty, 30M splats render
   (mod.rs:96-142, 412-605);
@@ -159,6 +161,31 @@ def test_culled_splats_do_not_perturb_render(gpu, where):
     for name, a, b, m in zip(("v_transforms", "v_coeffs", "v_raw_opac"), g_v, g_c, mags):
         grad_close(name, b[sl], a, m, rtol=1e-4, atol_frac=1e-6)
         assert np.all(b[hs] == 0.0), f"{name}: culled splats got gradients"
+
+
+def test_mostly_culled_scene_sorts_only_visible(gpu):
+    """The depth sort covers only the visible splats (render.rs:339-346): its
+    first pass drops the culled ones.  A scene whose splats are 90 % culled
+    (behind the camera, far off screen, transparent), interleaved with the
+    visible ones so that culled global ids fall in every sort partition,
+    renders bit for bit as the CPU restatement, on a fresh context (counts
+    read back first) and again on the same context (launches queued from the
+    previous forward's plan, the visible count read on the device)."""
+    print("[case] 90 % culled scene", flush=True)
+    cam = _cam()
+    vis = rng_scene(12_000, 1.5, (0.0, 2.5), (0.0, 3.0), 0xA11CE)
+    hid = rng_scene(108_000, 1.0, (-1.0, 1.0), (-1.0, 3.0), 0xB0B)
+    hid[0][0::3, 0:3] = [0.0, 0.0, -1000.0]  # behind the camera
+    hid[0][1::3, 0:3] = [1e6, 1e6, 10.0]     # far off screen
+    hid[2][2::3] = -20.0                     # opacity far below 1/255
+    order = np.random.default_rng(5).permutation(120_000)
+    tr, sh, op = (np.concatenate([vis[i], hid[i]])[order] for i in range(3))
+    u = uniforms_for(cam, 256, 256, tr.shape[0], 0)
+    o = O.render_forward(u, tr, sh, op, O.FLAG_BWD_INFO)
+    assert 10_000 <= o.num_visible <= 13_000, o.num_visible
+    for run in range(2):
+        g = gpu_forward(u, tr, sh, op, O.FLAG_BWD_INFO)
+        compare_forward(g, o)
 
 
 def _tiles_alpha_sums(img, tile=16):
