@@ -14,7 +14,9 @@ import os
 import torch  # noqa: F401  (must precede loading libbrush_hip.so)
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libbrush_hip.so")
+# BH_LIB_PATH selects another build of the same sources (the sanitizer build
+# of the host code, tests/test_sanitizers.py)
+LIB_PATH = os.environ.get("BH_LIB_PATH") or os.path.join(HERE, "libbrush_hip.so")
 
 OK = 0
 STATUS_NAMES = {

@@ -20,7 +20,9 @@ from dataclasses import dataclass
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+# BH_ORACLE_LIB selects another build of the same sources (the sanitizer
+# build, tests/test_sanitizers.py)
+_LIB_PATH = os.environ.get("BH_ORACLE_LIB") or os.path.join(_HERE, "liboracle.so")
 
 FLAG_BWD_INFO = 1
 FLAG_SMOOTH_CUTOFF = 2
