@@ -61,6 +61,32 @@ def measured_traffic(kernel: str, workload: str, profile: str = TRAFFIC_PROFILE)
     return None
 
 
+VALU_PROFILE = os.path.join(ROOT, "profiles", "cfg1_valu_counters.md")
+SIMDS = 1024          # 256 CUs x 4 SIMDs
+CLOCK_GHZ = 2.4       # peak engine clock
+CYCLES_PER_VALU = 4   # a wave64 FP32 instruction on a 16-lane SIMD (packed FP32 off)
+
+
+def measured_valu(kernel: str, workload: str, profile: str = VALU_PROFILE):
+    """VALU instructions per launch of ``kernel`` from the committed SQ counter
+    summary (table rows `| `kernel` | busy us | VGPRs | LDS | waves | VALU (M) |`),
+    or None when the summary does not cover this workload or kernel."""
+    try:
+        text = open(profile).read()
+    except OSError:
+        return None
+    if f"workload: {workload}" not in text:
+        return None
+    for line in text.splitlines():
+        f = [c.strip() for c in line.split("|")]
+        if len(f) > 6 and f[1] == f"`{kernel}`":
+            try:
+                return float(f[6]) * 1e6
+            except ValueError:
+                return None
+    return None
+
+
 def algorithmic_bytes(name: str, n: int, v: int, m: int, m_post: int, t: int, p: int, c: int,
                       contributing: int | None = None) -> float:
     """Compulsory HBM bytes of one launch: every input read once, every output
@@ -495,6 +521,15 @@ def main():
                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dominant, w.name),
                     "avg_ms": kd["avg_ms"], "algorithmic_mb": kd["algorithmic_mb"],
                     "timed_launches": int(round(kd["launches_per_step"] * args.steps))}
+        # the blend kernels are bound by VALU issue, not HBM: the dominant
+        # kernel's instructions per launch (committed SQ counter summary) over
+        # the issue slots of its live-measured duration
+        valu = measured_valu(dominant, w.name)
+        if valu and kd["avg_ms"]:
+            slots = kd["avg_ms"] * 1e-3 * CLOCK_GHZ * 1e9 * SIMDS / CYCLES_PER_VALU
+            roofline["valu"] = {"instructions": int(valu), "issue_frac": round(valu / slots, 3),
+                                "model": f"{CYCLES_PER_VALU} cycles per wave64 instruction, {SIMDS} SIMDs, "
+                                         f"{CLOCK_GHZ} GHz"}
 
     cpu = None
     if args.cpu_seconds > 0:
