@@ -23,6 +23,8 @@
 // render_bwd.rs:338-350 restated).
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "bh_internal.h"
 #include "bh_splat_math.h"
 #include "bh_splat_record.h"
@@ -31,10 +33,6 @@
 // Candidates staged per batch by the recorded backward (32 or 64).
 #ifndef BH_BWD_BATCH
 #define BH_BWD_BATCH 64
-#endif
-// Most splats the recorded backward queues before summing their rows (1-3).
-#ifndef BH_RECORDED_SLOTS
-#define BH_RECORDED_SLOTS 2
 #endif
 
 namespace bh {
@@ -153,7 +151,9 @@ __global__ __launch_bounds__(64) void rasterize_backward_kernel(
             const float cut = sigma_cutoff<SMOOTH>(r2.y);
             s_xyco[lane] = make_float4(r0.x, r0.y, r1.x, r1.y);
             s_crgb[lane] = make_float4(r2.x, r2.y, staged_colour(r3.x), staged_colour(r3.y));
-            s_bd[lane] = make_float4(staged_colour(r4.x), r4.y, cut, 0.0f);
+            // the cutoff on the power in base 2 (power log2(e); the cutoff's
+            // margin of 1e-3 covers the rounding)
+            s_bd[lane] = make_float4(staged_colour(r4.x), r4.y, kLog2e * cut, 0.0f);
             s_cid[lane] = row_of ? row_of[c] : c;
             touch = may_touch_rect(r0.x, r0.y, S2{r1.x, r1.y, r2.x}, cut, bx0, by0, bx0 + 7.0f, by0 + 7.0f);
         }
@@ -169,11 +169,14 @@ __global__ __launch_bounds__(64) void rasterize_backward_kernel(
             const S2 conic{xc.z, xc.w, cr4.x};
             const float opac = cr4.y;
             const float dx = xc.x - pcx, dy = xc.y - pcy;
-            const float sigma = 0.5f * (conic.c00 * dx * dx + conic.c11 * dy * dy) + conic.c01 * dx * dy;
-            const bool maybe = sw > 1.0e-4f && sigma >= 0.0f && !(sigma > bd.z);
+            // the forward's Gaussian (bh_math.h: the power in base 2)
+            float ka, kb, kc;
+            bh_conic_log2(conic.c00, conic.c01, conic.c11, &ka, &kb, &kc);
+            const float power = bh_power_log2(ka, kb, kc, dx, dy);
+            const bool maybe = sw > 1.0e-4f && power >= 0.0f && !(power > bd.z);
             if (__ballot(maybe) == 0ull) continue;
             // lanes outside `maybe` compute values that the selects below discard
-            const float gaussian = bh_expf_neg(-sigma);
+            const float gaussian = bh_exp2_neg(-power);
             const float alpha = bh_minf(0.999f, opac * gaussian);
             const float w = SMOOTH ? cutoff_weight(alpha) : (alpha >= kCutMid ? 1.0f : 0.0f);
             const bool pass = maybe && w > 0.0f;
@@ -320,11 +323,14 @@ void launch_rasterize_backward(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint
 // arithmetic is the reference's (rasterize_backwards.rs:308-441), rearranged
 // so that every factor that is constant over a splat is applied once, after
 // the sum over the block's pixels, instead of once per pixel:
-//   * alpha and transmittance exactly as the forward computed them (its sigma,
-//     its exp, no contraction): the remaining colour below is the forward's
-//     final colour minus these contributions, and deep in a stack it is a
-//     small difference of nearly equal numbers, which an alpha off by an ulp
-//     would make inconsistent;
+//   * alpha and transmittance exactly as the forward computed them (the
+//     power in base 2 from the same scaled conic, the same exponential, no
+//     contraction): the remaining colour below is the forward's final colour
+//     minus these contributions, and deep in a stack it is a small difference
+//     of nearly equal numbers, which an alpha off by an ulp would make
+//     inconsistent (with the hardware exp2, a few ulp from the forward's
+//     Gaussian, config 2's clustered scene put a scale gradient at three
+//     times its tolerance);
 //   * the remaining colour S enters the gradient only through the dot product
 //     S . v_out, so a pixel carries that one number (D = S . v_out, updated as
 //     D -= vis (c . v_out)) instead of the three channels of S;
@@ -337,13 +343,15 @@ void launch_rasterize_backward(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint
 // The gradient-only products use FMA contraction.
 //
 // A splat's K gradient sums are formed through LDS: every lane writes its K
-// values into rows of 64 (one row per sum), and once NSLOT splats are queued,
-// two lanes per row sum its halves (a float4 loop) and one lane per row
-// applies the splat's factor and adds the total to the splat's gradient row
-// in HBM: about one VALU add per value and one atomic instruction per NSLOT
-// splats.  A slot's rows start at an even row, so its two mean rows lie in
-// one lane quad and a quad permute brings each the other's total.
-template <bool SMOOTH, bool REFINE, bool DEPTH, int TH, int NSLOT>
+// values into rows of 64 (one row per sum), and once two splats are queued
+// (the candidate loop alternates two register sets, set a filling slot 0 and
+// set b slot 1), two lanes per row sum its halves (a float4 loop) and one
+// lane per row applies the splat's factor and adds the total to the splat's
+// gradient row in HBM: about one VALU add per value and one atomic
+// instruction per two splats.  A slot's rows start at an even row, so its two
+// mean rows lie in one lane quad and a quad permute brings each the other's
+// total.
+template <bool SMOOTH, bool REFINE, bool DEPTH, int TH>
 __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
     uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t num_tiles, float bg_r, float bg_g, float bg_b,
     uint32_t num_visible, const float* __restrict__ out_img, const float* __restrict__ projected,
@@ -356,15 +364,18 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
     // v_sigma dy dy, vis v_r, vis v_g, vis v_b, the opacity lane, (refine), (depth)
     constexpr int K = 9 + (REFINE ? 1 : 0) + (DEPTH ? 1 : 0);
     constexpr int KP = (K + 1) & ~1;  // rows per slot (even)
-    constexpr int R = NSLOT * KP;     // rows in use
-    static_assert(NSLOT >= 1 && NSLOT <= 3 && R <= 32, "flush geometry: up to three slots, at most 32 rows");
-    // the batch's candidates
+    constexpr int R = 2 * KP;         // rows in use: two slots
+    static_assert(R <= 32, "flush geometry: two slots of at most 16 rows");
+    // the conic from its scaled form (bh_conic_log2): c00 = 2 ln2 a,
+    // c01 = ln2 b, c11 = 2 ln2 c
+    constexpr float kLn2 = 0.69314718055994530942f;
+    constexpr float kTwoLn2 = 1.38629436111989061883f;
     // the batch's candidates (a batch of BATCH candidates; a smaller batch
     // takes less LDS, so more blocks fit a CU)
     constexpr uint32_t BATCH = BH_BWD_BATCH;
     static_assert(BATCH == 32 || BATCH == 64, "batch of 32 or 64 candidates");
-    __shared__ float4 s_geo[BATCH];   // x, y, conic c00, c01
-    __shared__ float4 s_op[BATCH];    // conic c11, opacity, max(r, 0), max(g, 0)
+    __shared__ float4 s_geo[BATCH];   // x, y, scaled conic a, b (bh_conic_log2)
+    __shared__ float4 s_op[BATCH];    // scaled conic c, opacity, max(r, 0), max(g, 0)
     __shared__ float s_cb[BATCH];     // max(b, 0)
     __shared__ uint32_t s_gate[BATCH];  // colour gates: bit c where channel c >= 0
     __shared__ uint32_t s_row[BATCH];   // gradient row (global id)
@@ -419,7 +430,8 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
     else if (len >= 64u)
         __builtin_amdgcn_s_setprio(1);
     const float wf = (float)img_w, hf = (float)img_h;
-    const float inv_final_a = __builtin_amdgcn_rcpf(bh_maxf(final_a, 1.0e-5f));
+    // the refine weight |(W vx, H vy)| / A with (vx, vy) = v_sigma ln2 (gx, gy)
+    const float refine_scale = kLn2 * __builtin_amdgcn_rcpf(bh_maxf(final_a, 1.0e-5f));
     const size_t rbase = record_base<BPT>(blk, lo, hi) - lo;
     // where this lane's value goes in a row; the row and half a summing lane
     // sums, and what multiplies its total: its own total times c00 (a slot's
@@ -430,9 +442,10 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
     const uint32_t frow = lane >> 1, fq = lane & 1u;
     const uint32_t fslot = frow / (uint32_t)KP, fk = frow % (uint32_t)KP;
     const float4* fsrc = reinterpret_cast<const float4*>(s_red + frow * RS + fq * SSTR);
-    // the factors as weights of c00, c11, c01 and a constant (exact products
-    // by 0 and 1: a splat's conic is finite)
-    const float f00 = fk == 0u ? 1.0f : 0.0f, f11 = fk == 1u ? 1.0f : 0.0f, f01 = fk < 2u ? 1.0f : 0.0f;
+    // the factors as weights of the staged a, c, b and a constant (exact
+    // products by 0: a splat's conic is finite)
+    const float f00 = fk == 0u ? kTwoLn2 : 0.0f, f11 = fk == 1u ? kTwoLn2 : 0.0f;
+    const float f01 = fk < 2u ? kLn2 : 0.0f;
     const uint32_t fgate = fk >= 5u && fk <= 7u ? 1u << (fk - 5u) : 0u;
     const float fconst = fk < 2u || fgate ? 0.0f : ((fk == 2u || fk == 4u) ? 0.5f : 1.0f);
     const uint32_t fdst = fk < 9u ? fk : (fk == 9u && REFINE ? 9u : 10u);
@@ -442,7 +455,7 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
     // totals to the splats' gradient rows.  A slot holds the candidate index
     // of its splat in the current batch (the staging arrays outlive the
     // slot: pending slots are flushed before the next batch is staged).
-    uint32_t slot_js = 0;  // queued candidate indices, six bits a slot
+    uint32_t slot_js = 0;  // queued candidate indices: slot 0 in bits 0-5, slot 1 in bits 6-11
     auto flush = [&](uint32_t nslots) {
         wave_lds_fence();
         const bool active = fslot < nslots && fk < (uint32_t)K;
@@ -480,7 +493,6 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
     const uint32_t bl = lane & (BATCH - 1u);  // lanes >= BATCH repeat a load and stage nothing
     uint2 mask_n = rec.masks[rbase + min(lo + bl, last)];
     uint32_t cid_n = cgids[min(lo + bl, last)];
-    uint32_t nslot = 0;
     for (uint32_t b = lo; b < end; b += BATCH) {
         const uint2 mask = lane < BATCH && b + lane <= last ? mask_n : make_uint2(0u, 0u);
         const uint32_t c = min(cid_n, num_visible - 1u);
@@ -500,31 +512,33 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
         // every lane stages (a candidate without pixels is never read; lanes
         // bl and bl + 32 of a 32-candidate batch store the same values), so
         // the row loads stay ahead of the barrier above
-        s_geo[bl] = make_float4(r0.x, r0.y, r1.x, r1.y);
-        s_op[bl] = make_float4(r2.x, r2.y, bh_maxf(r3.x, 0.0f), bh_maxf(r3.y, 0.0f));
+        float ka, kb, kc;
+        bh_conic_log2(r1.x, r1.y, r2.x, &ka, &kb, &kc);
+        s_geo[bl] = make_float4(r0.x, r0.y, ka, kb);
+        s_op[bl] = make_float4(kc, r2.y, bh_maxf(r3.x, 0.0f), bh_maxf(r3.y, 0.0f));
         s_cb[bl] = bh_maxf(r4.x, 0.0f);
         s_gate[bl] = (r3.x >= 0.0f ? 1u : 0u) | (r3.y >= 0.0f ? 2u : 0u) | (r4.x >= 0.0f ? 4u : 0u);
         s_row[bl] = grow;
         uint64_t todo = __builtin_amdgcn_ballot_w64(any);
         wave_lds_fence();
-        // One candidate: its gradient values into a slot, flushed when the
-        // slots are full.  The loop below reads the next candidate's
+        // One candidate: its gradient values into slot SLOT (0 for register
+        // set a, 1 for set b).  The loop below reads the next candidate's
         // parameters while the current one is evaluated, two register sets
-        // in turn.
-        auto eval_one = [&](uint32_t j, const float4& geo, const float4& op, float cb) {
+        // in turn, and sums the two slots after every set-b candidate.
+        auto eval_one = [&](auto slot, uint32_t j, const float4& geo, const float4& op, float cb) {
+            constexpr uint32_t SLOT = decltype(slot)::value;
             // candidate j's mask, read into scalar registers, is the lane condition
             // (readlane returns a signed int: widen through uint32_t, never by
             // sign extension)
             const uint64_t mj = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(mask.y, j) << 32) |
                                 (uint64_t)(uint32_t)__builtin_amdgcn_readlane(mask.x, j);
             const bool contrib = __builtin_amdgcn_inverse_ballot_w64(mj);
-            const float c00 = geo.z, c01 = geo.w, c11 = op.x, opac = op.y;
+            const float ka = geo.z, kb = geo.w, kc = op.x, opac = op.y;
             const float cr = op.z, cg = op.w;
-            // d = mean - pixel centre; the forward's sigma, whose products are
-            // even in the sign of d, bit for bit
+            // d = mean - pixel centre; the forward's power and Gaussian, bit
+            // for bit
             const float dx = geo.x - pcx, dy = geo.y - pcy;
-            const float sigma = calc_sigma(geo.x, geo.y, S2{c00, c01, c11}, pcx, pcy);
-            const float gauss = bh_expf_neg(-sigma);
+            const float gauss = bh_exp2_neg(-bh_power_log2(ka, kb, kc, dx, dy));
             const float og = opac * gauss;
             const float alpha = bh_minf(0.999f, og);
             float w = 1.0f, ae = alpha;
@@ -559,26 +573,34 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
                 g[6] = vis * voy;
                 g[7] = vis * voz;
                 g[8] = gate ? v_alpha * gauss : 0.0f;
-                if (REFINE) {
-                    const float ax = wf * (c00 * t + c01 * u), ay = hf * (c01 * t + c11 * u);
-                    g[9] = __builtin_amdgcn_sqrtf(ax * ax + ay * ay) * inv_final_a;
+                if constexpr (REFINE) {
+                    // (vx, vy) = v_sigma C d = v_sigma ln2 (gx, gy) with
+                    // gx = 2 a dx + b dy = q + a dx (q = a dx + b dy of the
+                    // power) and gy = b dx + 2 c dy
+                    const float q = bh_fmaf(ka, dx, kb * dy);
+                    const float cdy = kc * dy;
+                    const float gx = bh_fmaf(ka, dx, q), gy = bh_fmaf(kb, dx, cdy + cdy);
+                    const float ax = wf * gx, ay = hf * gy;
+                    g[9] = (__builtin_fabsf(v_sigma) * refine_scale) * __builtin_amdgcn_sqrtf(ax * ax + ay * ay);
                 }
-                if (DEPTH) g[K - 1] = vis * vod;
+                if constexpr (DEPTH) g[K - 1] = vis * vod;
                 // the reference's state update (rasterize_backwards.rs:356-358,
                 // 432-435) as D -= vis (c . v_out)
                 dsum = dsum - vis * cv;
             }
             sw = sw * one_minus;
-            float* dst = s_red + nslot * (uint32_t)(KP * RS) + wcol;
+            float* dst = s_red + SLOT * (uint32_t)(KP * RS) + wcol;
 #pragma unroll
             for (int k = 0; k < K; ++k) dst[k * RS] = g[k];
-            slot_js |= j << (6u * nslot);
-            if (++nslot == (uint32_t)NSLOT) {
-                flush(NSLOT);
-                nslot = 0;
-                slot_js = 0;
-            }
+            if (SLOT == 0u)
+                slot_js = j;
+            else
+                slot_js |= j << 6;
         };
+        using Slot0 = std::integral_constant<uint32_t, 0u>;
+        using Slot1 = std::integral_constant<uint32_t, 1u>;
+        // an odd count leaves the batch's last candidate alone in slot 0
+        const bool odd = (__builtin_popcountll(todo) & 1) != 0;
         if (todo) {
             uint32_t ja = (uint32_t)__builtin_ctzll(todo);
             todo &= todo - 1ull;
@@ -596,7 +618,7 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
                     opb = s_op[jb];
                     cbb = s_cb[jb];
                 }
-                eval_one(ja, geoa, opa, cba);
+                eval_one(Slot0{}, ja, geoa, opa, cba);
                 if (!has_b) break;
                 const bool has_a = todo != 0ull;
                 if (has_a) {
@@ -606,16 +628,14 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
                     opa = s_op[ja];
                     cba = s_cb[ja];
                 }
-                eval_one(jb, geob, opb, cbb);
+                eval_one(Slot1{}, jb, geob, opb, cbb);
+                flush(2u);
                 if (!has_a) break;
             }
         }
-        // the next batch overwrites the staging arrays the slots refer to
-        if (nslot) {
-            flush(nslot);
-            nslot = 0;
-            slot_js = 0;
-        }
+        // sum it before the next batch overwrites the staging arrays the
+        // slots refer to
+        if (odd) flush(1u);
         wave_lds_fence();
     }
 }
@@ -627,10 +647,7 @@ static void launch_recorded_t(bh_ctx* ctx, uint32_t groups, uint32_t img_w, uint
                               const float* projected, const uint32_t* cgids, const uint32_t* off_pre,
                               const SplatRecord& rec, const float* v_output, const uint32_t* row_of,
                               const uint32_t* order, float* v_rows) {
-    // slots per flush: as many as fit 32 rows, up to BH_RECORDED_SLOTS
-    constexpr int KP = (9 + (R ? 1 : 0) + (D ? 1 : 0) + 1) & ~1;
-    constexpr int NS = (32 / KP) < BH_RECORDED_SLOTS ? (32 / KP) : BH_RECORDED_SLOTS;
-    rasterize_backward_recorded_kernel<S, R, D, T, NS><<<groups, 64, 0, ctx->stream>>>(
+    rasterize_backward_recorded_kernel<S, R, D, T><<<groups, 64, 0, ctx->stream>>>(
         img_w, img_h, tile_bw, num_tiles, bg[0], bg[1], bg[2], num_visible, out_img, projected, cgids, off_pre, rec,
         v_output, row_of, order, v_rows);
 }

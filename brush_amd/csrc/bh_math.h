@@ -35,6 +35,9 @@
  *             constants; sign of y.
  * All stay within 2 ulp of the correctly rounded result over all finite
  * inputs (pinned on the CPU against float64 libm by the oracle tests).
+ *   bh_exp2_neg — the splat Gaussian's 2^x (see its comment): rint, a
+ *             degree-5 minimax polynomial of 2^f on [-1/2, 1/2], ldexp;
+ *             within 3 ulp of 2^x on [-126, 1].
  *
  * This header is plain C99 so the CPU restatement (gcc) can include it; under
  * hipcc every function is callable from host and device.
@@ -174,31 +177,49 @@ BH_HD float bh_logf(float x) {
     return ef * ln2_hi + (ef * ln2_lo + logm);
 }
 
-/* bh_expf for x in [-87, 0] (every argument the blend kernels evaluate:
- * x = -sigma with 0 <= sigma <= ln(255) + small): the same operations as
- * bh_expf without the NaN / overflow / subnormal branches, which cannot
- * trigger in that range, so the result is bit-identical there.  The
- * round-to-integer is a single rint (equal to the shifter sum for
- * |k| < 2^22) and the scaling a single ldexp (equal to the multiply by the
- * constructed 2^n while e^x is a normal number, x >= -87). */
-BH_HD float bh_expf_neg(float x) {
-    const float log2e = 1.44269502162933349609375f;
-    const float ln2_hi = 0.693145751953125f;
-    const float ln2_lo = 1.428606765330187045e-06f;
-    float k = x * log2e;
-    float kr = bh_rintf(k);
-    int n = (int)kr;
-    float r = bh_fmaf(kr, -ln2_hi, x);
-    r = bh_fmaf(kr, -ln2_lo, r);
-    float p = 1.98412698412698413e-04f;
-    p = bh_fmaf(p, r, 1.38888888888888889e-03f);
-    p = bh_fmaf(p, r, 8.33333333333333333e-03f);
-    p = bh_fmaf(p, r, 4.16666666666666667e-02f);
-    p = bh_fmaf(p, r, 1.66666666666666667e-01f);
-    p = bh_fmaf(p, r, 0.5f);
-    p = bh_fmaf(p, r, 1.0f);
-    p = bh_fmaf(p, r, 1.0f);
-    return bh_ldexpf(p, n);
+/* The splat Gaussian e^-sigma, sigma = (c00 dx^2 + c11 dy^2) / 2 + c01 dx dy
+ * (brush-cube/src/lib.rs:632-638, kernels/rasterize.rs), evaluated in base 2.
+ * The conic is scaled once per splat (bh_conic_log2: a = c00 log2(e) / 2,
+ * b = c01 log2(e), c = c11 log2(e) / 2), so a pixel's exponent
+ * sigma log2(e) = dx (a dx + b dy) + (c dy) dy costs three products and
+ * two fmas (bh_power_log2), and 2^-y needs no ln 2 reduction (bh_exp2_neg): with
+ * n = rint(y) and f = y - n in [-1/2, 1/2] (exact), 2^f is a degree-5
+ * polynomial fitted for least maximum relative error on [-1/2, 1/2]
+ * (6.9e-8 before rounding, within 3 ulp of 2^f in float), scaled by 2^n.
+ * Against e^-sigma of the unscaled power this differs by the rounding of the
+ * scaled conic and exponent, a few ulp of the result; the blend, its replay
+ * and the CPU restatement all evaluate alpha this way, so their decisions
+ * agree bit for bit. */
+BH_HD void bh_conic_log2(float c00, float c01, float c11, float* a, float* b, float* c) {
+    const float half_log2e = 0.72134752044448170368f; /* log2(e) / 2 */
+    const float log2e = 1.44269504088896340736f;
+    *a = half_log2e * c00;
+    *b = log2e * c01;
+    *c = half_log2e * c11;
+}
+
+BH_HD float bh_power_log2(float a, float b, float c, float dx, float dy) {
+    const float q = bh_fmaf(a, dx, b * dy);
+    return bh_fmaf(dx, q, (c * dy) * dy);
+}
+
+/* 2^x for x in [-126, 1] (x = -power: the power is >= 0 where it is used,
+ * up to rounding); below -200 the result is 0 and NaN stays NaN. */
+BH_HD float bh_exp2_neg(float x) {
+#if !defined(__HIPCC__)
+    /* the CPU restatement never converts an out-of-range n (on the GPU the
+     * conversion saturates and ldexp gives 0 for x < -200 as well) */
+    if (!(x >= -200.0f)) return x == x ? 0.0f : x;
+#endif
+    const float n = bh_rintf(x);
+    const float f = x - n;
+    float p = 1.33523193e-03f;
+    p = bh_fmaf(p, f, 9.67188086e-03f);
+    p = bh_fmaf(p, f, 5.55045046e-02f);
+    p = bh_fmaf(p, f, 2.40222305e-01f);
+    p = bh_fmaf(p, f, 6.93147242e-01f);
+    p = bh_fmaf(p, f, 1.0f);
+    return bh_ldexpf(p, (int)n);
 }
 
 /* 1 / (1 + e^-x)  (brush-cube/src/lib.rs:620-623) */

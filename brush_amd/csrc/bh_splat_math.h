@@ -459,6 +459,11 @@ BH_DEV float sigma_cutoff(float opac) {
     const float alpha_min = SMOOTH ? (kCutMid - 0.5f * kCutBand) : kCutMid;
     return bh_logf(opac / alpha_min) + 1.0e-3f;
 }
+// log2(e) in float: the blend kernels compare the power in base 2
+// (bh_power_log2) with kLog2e * sigma_cutoff, whose margin of 1e-3 (1.4e-3 in
+// base 2) still exceeds the rounding of the scaled conic, power and product
+// by three orders of magnitude.
+constexpr float kLog2e = 1.44269504088896340736f;
 
 // Lower bound on the power 0.5 d^T C d (d = p - m) over the pixel centres of
 // the rectangle [x0, x1] x [y0, y1]: 0 if m lies inside, otherwise the least

@@ -228,8 +228,9 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
                                                         const uint32_t* __restrict__ order,
                                                         void* __restrict__ out_img, float* __restrict__ visible,
                                                         uint32_t* __restrict__ off_post, SplatRecord rec) {
-    __shared__ float4 s_xyco[64];  // x, y, conic c00, conic c01
-    __shared__ float4 s_c11a[64];  // conic c11, opacity, sigma cutoff
+    // the conic scaled for the power in base 2 (bh_conic_log2: a, b, c)
+    __shared__ float4 s_xyco[64];  // x, y, a, b
+    __shared__ float4 s_c11a[64];  // c, opacity, cutoff on the power in base 2
     __shared__ float4 s_rgbd[64];  // r, g, b (staged_colour), depth
 
     uint32_t tile, blk;
@@ -298,8 +299,11 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
         __asm__ volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
         const float cut = sigma_cutoff<SMOOTH>(cc.y);
-        s_xyco[lane] = make_float4(a.x, a.y, b.x, b.y);
-        s_c11a[lane] = make_float4(cc.x, cc.y, cut, 0.0f);
+        float ka, kb, kc;
+        bh_conic_log2(b.x, b.y, cc.x, &ka, &kb, &kc);
+        s_xyco[lane] = make_float4(a.x, a.y, ka, kb);
+        // the cutoff's margin of 1e-3 covers the rounding of the scaled power
+        s_c11a[lane] = make_float4(kc, cc.y, kLog2e * cut, 0.0f);
         s_rgbd[lane] = make_float4(staged_colour(d.x), staged_colour(d.y), staged_colour(e.x), e.y);
         const bool touch = lane < cnt && may_touch_rect(a.x, a.y, S2{b.x, b.y, cc.x}, cut, bx0, by0, bx0 + 7.0f,
                                                         by0 + 7.0f);
@@ -313,17 +317,16 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
         // done.  The loop below reads the next candidate's parameters while
         // the current one is evaluated, two register sets in turn.
         auto blend_one = [&](uint32_t j, const float4& xc, const float4& ca, const float4& col) -> bool {
-            const S2 conic{xc.z, xc.w, ca.x};
-            const float sigma = calc_sigma(pcx, pcy, conic, xc.x, xc.y);
+            // the power sigma log2(e) of the pixel (bh_math.h)
+            const float power = bh_power_log2(xc.z, xc.w, ca.x, xc.x - pcx, xc.y - pcy);
             // lane conditions are kept as wave masks (scalar registers), each
             // the ballot of a single comparison
-            const uint64_t maybe_m = __builtin_amdgcn_ballot_w64(sigma >= 0.0f) &
-                                     __builtin_amdgcn_ballot_w64(!(sigma > ca.z)) & ~done_m;
+            const uint64_t maybe_m = __builtin_amdgcn_ballot_w64(power >= 0.0f) &
+                                     __builtin_amdgcn_ballot_w64(!(power > ca.z)) & ~done_m;
             if (maybe_m == 0ull) return false;
             // Branch-free from here: lanes outside `maybe` compute values the
-            // selects discard.  0 <= sigma <= cutoff < 6 where it matters, the
-            // range in which bh_expf_neg equals bh_expf bit for bit.
-            const float alpha = bh_minf(0.999f, ca.y * bh_expf_neg(-sigma));
+            // selects discard.
+            const float alpha = bh_minf(0.999f, ca.y * bh_exp2_neg(-power));
             // the hard cutoff's weight is a step: alpha * w is a select
             const float w = SMOOTH ? cutoff_weight(alpha) : (alpha >= kCutMid ? 1.0f : 0.0f);
             const float ae = SMOOTH ? alpha * w : (alpha >= kCutMid ? alpha : 0.0f);

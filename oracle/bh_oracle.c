@@ -26,9 +26,18 @@ void or_expf(const float* in, float* out, uint64_t n) {
     for (uint64_t i = 0; i < n; i++) out[i] = bh_expf(in[i]);
 }
 
-/* the blend kernels' exponential (bh_math.h), for its equality check */
-void or_expf_neg(const float* in, float* out, uint64_t n) {
-    for (uint64_t i = 0; i < n; i++) out[i] = bh_expf_neg(in[i]);
+/* the splat Gaussian in base 2 (bh_math.h), for its pins */
+void or_exp2_neg(const float* in, float* out, uint64_t n) {
+    for (uint64_t i = 0; i < n; i++) out[i] = bh_exp2_neg(in[i]);
+}
+
+void or_power_log2(const float* c00, const float* c01, const float* c11, const float* dx, const float* dy,
+                   float* out, uint64_t n) {
+    for (uint64_t i = 0; i < n; i++) {
+        float a, b, c;
+        bh_conic_log2(c00[i], c01[i], c11[i], &a, &b, &c);
+        out[i] = bh_power_log2(a, b, c, dx[i], dy[i]);
+    }
 }
 
 void or_logf(const float* in, float* out, uint64_t n) {
@@ -774,11 +783,13 @@ void or_rasterize(uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t til
             uint32_t last = lo;
             for (uint32_t i = lo; i < hi; i++) {
                 const float* s = projected + (size_t)cgid_from_isect[i] * 10;
-                s2 conic = {s[2], s[3], s[4]};
-                float sigma = calc_sigma(pcx, pcy, conic, s[0], s[1]);
-                float alpha = bh_minf(0.999f, s[5] * bh_expf(-sigma));
+                /* e^-sigma in base 2 (bh_math.h: bh_power_log2, bh_exp2_neg) */
+                float ca, cb, cc;
+                bh_conic_log2(s[2], s[3], s[4], &ca, &cb, &cc);
+                float power = bh_power_log2(ca, cb, cc, s[0] - pcx, s[1] - pcy);
+                float alpha = bh_minf(0.999f, s[5] * bh_exp2_neg(-power));
                 float w = smooth ? cutoff_weight(alpha) : (alpha >= CUT_MID ? 1.0f : 0.0f);
-                if (sigma >= 0.0f && w > 0.0f) {
+                if (power >= 0.0f && w > 0.0f) {
                     float ae = alpha * w;
                     float next_t = t_acc * (1.0f - ae);
                     if (next_t <= 1.0e-4f) break;
@@ -823,11 +834,12 @@ void or_rasterize_reference(const float* projected, uint32_t n, uint32_t w, uint
             float t = 1.0f, r = 0.0f, g = 0.0f, b = 0.0f;
             for (uint32_t i = 0; i < n; i++) {
                 const float* s = projected + (size_t)i * 10;
-                float dx = pxc - s[0], dy = pyc - s[1];
-                float sigma = 0.5f * (s[2] * dx * dx + s[4] * dy * dy) + s[3] * dx * dy;
-                float alpha = bh_minf(s[5] * bh_expf(-sigma), 0.999f);
+                float ca, cb, cc;
+                bh_conic_log2(s[2], s[3], s[4], &ca, &cb, &cc);
+                float power = bh_power_log2(ca, cb, cc, s[0] - pxc, s[1] - pyc);
+                float alpha = bh_minf(s[5] * bh_exp2_neg(-power), 0.999f);
                 float wgt = smooth ? cutoff_weight(alpha) : (alpha >= CUT_MID ? 1.0f : 0.0f);
-                if (sigma >= 0.0f && wgt > 0.0f) {
+                if (power >= 0.0f && wgt > 0.0f) {
                     float ea = alpha * wgt;
                     float nt = t * (1.0f - ea);
                     if (nt <= 1.0e-4f) break;
@@ -894,6 +906,8 @@ void or_rasterize_backward(uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uin
             uint32_t cg = cgid_from_isect[i];
             const float* s = projected + (size_t)cg * 10;
             s2 c = {s[2], s[3], s[4]};
+            float ca, cbc, cc;
+            bh_conic_log2(c.c00, c.c01, c.c11, &ca, &cbc, &cc);
             float cr = bh_maxf(s[6], 0.0f), cgc = bh_maxf(s[7], 0.0f), cb = bh_maxf(s[8], 0.0f);
             float gs[4][11] = {{0}};
             for (uint32_t p = 0; p < 16u * th; p++) {
@@ -903,11 +917,11 @@ void or_rasterize_backward(uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uin
                 uint32_t px = ox + (p & 15u), py = oy + (p >> 4);
                 float pcx = (float)px + 0.5f, pcy = (float)py + 0.5f;
                 float dx = s[0] - pcx, dy = s[1] - pcy;
-                float sigma = 0.5f * (c.c00 * dx * dx + c.c11 * dy * dy) + c.c01 * dx * dy;
-                float gaussian = bh_expf(-sigma);
+                float power = bh_power_log2(ca, cbc, cc, dx, dy);
+                float gaussian = bh_exp2_neg(-power);
                 float alpha = bh_minf(0.999f, s[5] * gaussian);
                 float w = smooth ? cutoff_weight(alpha) : (alpha >= CUT_MID ? 1.0f : 0.0f);
-                if (!(sigma >= 0.0f && w > 0.0f)) continue;
+                if (!(power >= 0.0f && w > 0.0f)) continue;
                 float ae = alpha * w;
                 float next_t = sw * (1.0f - ae);
                 if (next_t <= 1.0e-4f) {

@@ -34,7 +34,9 @@ extern "C" {
 void or_set_threads(int n);
 /* Element-wise bh_expf / bh_logf, for pinning them against libm. */
 void or_expf(const float* in, float* out, uint64_t n);
-void or_expf_neg(const float* in, float* out, uint64_t n);
+void or_exp2_neg(const float* in, float* out, uint64_t n);
+void or_power_log2(const float* c00, const float* c01, const float* c11, const float* dx, const float* dy,
+                   float* out, uint64_t n);
 void or_logf(const float* in, float* out, uint64_t n);
 void or_atan2f(const float* y, const float* x, float* out, uint64_t n);
 /* camera models on their own (test hooks): projection and depth cull,

@@ -107,7 +107,8 @@ def lib():
         UP = ctypes.POINTER(Uniforms)
         L.or_set_threads.argtypes = [ctypes.c_int]
         L.or_expf.argtypes = [P, P, U64]
-        L.or_expf_neg.argtypes = [P, P, U64]
+        L.or_exp2_neg.argtypes = [P, P, U64]
+        L.or_power_log2.argtypes = [P, P, P, P, P, P, U64]
         L.or_logf.argtypes = [P, P, U64]
         L.or_atan2f.argtypes = [P, P, P, U64]
         L.or_camera_project.argtypes = [UP, P, U64, P, P]
@@ -154,11 +155,23 @@ def expf(x: np.ndarray) -> np.ndarray:
     return out
 
 
-def expf_neg(x: np.ndarray) -> np.ndarray:
-    """The blend kernels' exponential for arguments in [-87, 0]."""
+def exp2_neg(x: np.ndarray) -> np.ndarray:
+    """2^x as the blend kernels evaluate the splat Gaussian (bh_math.h
+    bh_exp2_neg; arguments in [-126, 1])."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     out = np.empty_like(x)
-    lib().or_expf_neg(_p(x), _p(out), x.size)
+    lib().or_exp2_neg(_p(x), _p(out), x.size)
+    return out
+
+
+def power_log2(c00, c01, c11, dx, dy) -> np.ndarray:
+    """sigma log2(e) of pixel offsets (dx, dy) = mean - pixel centre, from the
+    conic scaled as the blend kernels scale it (bh_conic_log2, bh_power_log2);
+    arguments broadcast."""
+    arrs = np.broadcast_arrays(*[np.asarray(a, dtype=np.float32) for a in (c00, c01, c11, dx, dy)])
+    arrs = [np.ascontiguousarray(a) for a in arrs]
+    out = np.empty_like(arrs[0])
+    lib().or_power_log2(*[_p(a) for a in arrs], _p(out), out.size)
     return out
 
 

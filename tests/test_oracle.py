@@ -39,17 +39,60 @@ def test_expf_within_2ulp_of_libm():
     assert O.expf(np.array([-np.inf], np.float32))[0] == 0.0
 
 
-def test_expf_neg_equals_expf_bit_for_bit():
-    """The blend kernels evaluate e^-sigma with bh_expf_neg (one rint and one
-    ldexp in place of the shifter sum and the constructed power of two); on
-    [-87, 0] it must equal bh_expf bit for bit, or blend decisions would
-    differ from the restatement's."""
+def test_exp2_neg_within_3ulp_of_exp2():
+    """The splat Gaussian's 2^x (bh_exp2_neg: rint, degree-5 minimax
+    polynomial of 2^f on [-1/2, 1/2], ldexp) against float64 exp2 over the
+    arguments the blend evaluates ([-126, 1]; the alpha cutoff sits near
+    -log2(255 / opacity) > -9), exact at the integers, 0 below -200 and NaN
+    for NaN."""
     rng = np.random.default_rng(7)
-    lo_bits = np.float32(-87.0).view(np.uint32)
-    bits = rng.integers(0x80000000, int(lo_bits) + 1, size=4_000_000, dtype=np.uint64).astype(np.uint32)
-    dense = -np.arange(0, 1 << 21, dtype=np.float32) * np.float32(3.0e-6)  # [-6.3, 0], the cutoff range
-    x = np.concatenate([bits.view(np.float32), dense, np.array([0.0, -0.0, -87.0, -1e-30], np.float32)])
-    assert np.array_equal(O.expf_neg(x).view(np.uint32), O.expf(x).view(np.uint32))
+    lo_bits = np.float32(-126.0).view(np.uint32)
+    bits = rng.integers(0x80000000, int(lo_bits) + 1, size=3_000_000, dtype=np.uint64).astype(np.uint32)
+    dense = -np.arange(0, 1 << 22, dtype=np.float32) * np.float32(2.2e-6)  # [-9.2, 0]
+    halves = np.arange(-252, 3, dtype=np.float32) * np.float32(0.5)
+    x = np.concatenate([bits.view(np.float32), dense, rng.uniform(0.0, 1.0, 100_000).astype(np.float32), halves,
+                        np.array([0.0, -0.0, 1.0, -1e-30, np.nextafter(np.float32(-0.5), np.float32(0))],
+                                 np.float32)])
+    got = O.exp2_neg(x)
+    assert np.max(_ulp_err(got, np.exp2(x.astype(np.float64)))) <= 3.0
+    ints = -np.arange(0, 127, dtype=np.float32)
+    assert np.array_equal(O.exp2_neg(ints), np.exp2(ints.astype(np.float64)).astype(np.float32))
+    assert np.all(O.exp2_neg(np.array([-200.5, -1e30, -np.inf], np.float32)) == 0.0)
+    assert np.isnan(O.exp2_neg(np.array([np.nan], np.float32)))[0]
+
+
+def test_power_log2_is_sigma_times_log2e():
+    """bh_power_log2 of the scaled conic against log2(e) * sigma evaluated in
+    float64 from the same float32 conic and offsets, to a few ulp of the
+    terms' magnitude: a wrong scale (log2 e against log2(e) / 2 on the cross
+    term), a swapped coefficient or a lost sign breaks it.  Composed with
+    bh_exp2_neg it is e^-sigma over the cutoff range to that error times ln 2
+    plus the exponential's 3 ulp."""
+    rng = np.random.default_rng(11)
+    n = 400_000
+    # conics of 2D covariances with a blur: random rotation and scales
+    th = rng.uniform(0, np.pi, n)
+    s1, s2 = np.exp(rng.uniform(-1, 5, n)), np.exp(rng.uniform(-1, 5, n))
+    cs, sn = np.cos(th), np.sin(th)
+    cov = np.stack([cs * cs * s1 + sn * sn * s2 + 0.3, cs * sn * (s1 - s2), sn * sn * s1 + cs * cs * s2 + 0.3], 1)
+    det = cov[:, 0] * cov[:, 2] - cov[:, 1] ** 2
+    c00, c01, c11 = (cov[:, 2] / det).astype(np.float32), (-cov[:, 1] / det).astype(np.float32), \
+        (cov[:, 0] / det).astype(np.float32)
+    r = np.sqrt(rng.uniform(0, 20, n) / np.maximum(c00, c11))
+    dx = (r * rng.normal(size=n)).astype(np.float32)
+    dy = (r * rng.normal(size=n)).astype(np.float32)
+    got = O.power_log2(c00, c01, c11, dx, dy).astype(np.float64)
+    a, b, c, x, y = (v.astype(np.float64) for v in (c00, c01, c11, dx, dy))
+    sigma = 0.5 * (a * x * x + c * y * y) + b * x * y
+    mag = 0.5 * (a * x * x + c * y * y) + np.abs(b * x * y)
+    assert np.all(np.abs(got - np.log2(np.e) * sigma) <= 2.0 ** -20 * mag + 1e-30)
+    band = (sigma >= 0) & (sigma <= 6.0)
+    g = O.exp2_neg(-got.astype(np.float32)[band]).astype(np.float64)
+    # the power's error (a few ulp of the terms, which cancel where the
+    # cross term is large) times ln 2, plus the exponential's 3 ulp
+    assert np.all(np.abs(g / np.exp(-sigma[band]) - 1.0) <= np.log(2.0) * 2.0 ** -20 * mag[band] + 4e-7)
+    # the offsets' sign does not change a bit
+    assert np.array_equal(O.power_log2(c00, c01, c11, -dx, -dy).view(np.uint32), got.astype(np.float32).view(np.uint32))
 
 
 def test_logf_within_2ulp_of_libm():
@@ -299,11 +342,11 @@ def test_no_pixel_contribution_outside_counted_tiles(th):
     mid = np.float32(1.0) / np.float32(255.0)
     for c in range(r.num_visible):
         p = r.projected[c]
-        dx = (pcx - p[0]).astype(np.float32)
-        dy = (pcy - p[1]).astype(np.float32)
-        sigma = np.float32(0.5) * (p[2] * dx * dx + p[4] * dy * dy) + p[3] * dx * dy
-        alpha = np.minimum(np.float32(0.999), p[5] * O.expf(-sigma))
-        hit = (alpha >= mid) & (sigma >= 0)
+        dx = (p[0] - pcx).astype(np.float32)
+        dy = (p[1] - pcy).astype(np.float32)
+        power = O.power_log2(p[2], p[3], p[4], dx, dy)
+        alpha = np.minimum(np.float32(0.999), p[5] * O.exp2_neg(-power))
+        hit = (alpha >= mid) & (power >= 0)
         for y, x in zip(*np.nonzero(hit)):
             assert ((x // 16) + (y // th) * tbw, c) in binned, f"splat {c} pixel ({x},{y}) not binned"
     ref = O.rasterize_reference(r.projected[: r.num_visible], 96, 80, (0, 0, 0), False)
