@@ -376,9 +376,10 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
     static_assert(BATCH == 32 || BATCH == 64, "batch of 32 or 64 candidates");
     __shared__ float4 s_geo[BATCH];   // x, y, scaled conic a, b (bh_conic_log2)
     __shared__ float4 s_op[BATCH];    // scaled conic c, opacity, max(r, 0), max(g, 0)
-    __shared__ float s_cb[BATCH];     // max(b, 0)
-    __shared__ uint32_t s_gate[BATCH];  // colour gates: bit c where channel c >= 0
-    __shared__ uint32_t s_row[BATCH];   // gradient row (global id)
+    // max(b, 0) (bits), colour gates (bit c where channel c >= 0), gradient
+    // row (global id): the candidate's three 16-byte records share one
+    // address
+    __shared__ uint4 s_aux[BATCH];
     // R rows of two 32-float halves, each padded by 4 floats: a row's stores
     // and the summing lanes' 16-byte reads are free of bank conflicts
     constexpr int SSTR = 36;      // half-row stride in floats
@@ -439,6 +440,18 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
     // rows), the colour gate (a colour row) or 1, plus the quad partner row's
     // total times c01 (the two mean rows)
     const uint32_t wcol = (lane >> 5) * SSTR + (lane & 31u);
+    // byte offsets of this lane's column in rows 0, 4 and 8 of each slot: a
+    // row store's offset from them fits the 8-bit dword offsets of paired
+    // LDS stores (rows 72 floats apart); kept in registers (opaque to the
+    // compiler, which would otherwise rebuild them with an add per store pair)
+    uint32_t wbase[2][3];
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+        for (int gr = 0; gr < 3; ++gr) {
+            wbase[sl][gr] = ((uint32_t)(sl * KP + 4 * gr) * RS + wcol) * 4u;
+            __asm__ volatile("" : "+v"(wbase[sl][gr]));
+        }
     const uint32_t frow = lane >> 1, fq = lane & 1u;
     const uint32_t fslot = frow / (uint32_t)KP, fk = frow % (uint32_t)KP;
     const float4* fsrc = reinterpret_cast<const float4*>(s_red + frow * RS + fq * SSTR);
@@ -463,7 +476,8 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
         const uint32_t js = (slot_js >> (6u * fslot)) & 63u;
         const float4 geo = s_geo[js];
         const float c11 = s_op[js].x;
-        const uint32_t gates = s_gate[js], row = s_row[js];
+        const uint4 aux = s_aux[js];
+        const uint32_t gates = aux.y, row = aux.z;
         float acc = 0.0f;
         if (active) {
             float4 v = fsrc[0];
@@ -516,9 +530,8 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
         bh_conic_log2(r1.x, r1.y, r2.x, &ka, &kb, &kc);
         s_geo[bl] = make_float4(r0.x, r0.y, ka, kb);
         s_op[bl] = make_float4(kc, r2.y, bh_maxf(r3.x, 0.0f), bh_maxf(r3.y, 0.0f));
-        s_cb[bl] = bh_maxf(r4.x, 0.0f);
-        s_gate[bl] = (r3.x >= 0.0f ? 1u : 0u) | (r3.y >= 0.0f ? 2u : 0u) | (r4.x >= 0.0f ? 4u : 0u);
-        s_row[bl] = grow;
+        s_aux[bl] = make_uint4(__float_as_uint(bh_maxf(r4.x, 0.0f)),
+                               (r3.x >= 0.0f ? 1u : 0u) | (r3.y >= 0.0f ? 2u : 0u) | (r4.x >= 0.0f ? 4u : 0u), grow, 0u);
         uint64_t todo = __builtin_amdgcn_ballot_w64(any);
         wave_lds_fence();
         // One candidate: its gradient values into slot SLOT (0 for register
@@ -589,9 +602,9 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
                 dsum = dsum - vis * cv;
             }
             sw = sw * one_minus;
-            float* dst = s_red + SLOT * (uint32_t)(KP * RS) + wcol;
 #pragma unroll
-            for (int k = 0; k < K; ++k) dst[k * RS] = g[k];
+            for (int k = 0; k < K; ++k)
+                *reinterpret_cast<float*>(reinterpret_cast<char*>(s_red) + wbase[SLOT][k >> 2] + (k & 3) * RS * 4) = g[k];
             if (SLOT == 0u)
                 slot_js = j;
             else
@@ -605,7 +618,7 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
             uint32_t ja = (uint32_t)__builtin_ctzll(todo);
             todo &= todo - 1ull;
             float4 geoa = s_geo[ja], opa = s_op[ja];
-            float cba = s_cb[ja];
+            float cba = __uint_as_float(s_aux[ja].x);
             while (true) {
                 const bool has_b = todo != 0ull;
                 uint32_t jb = 0u;
@@ -616,7 +629,7 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
                     todo &= todo - 1ull;
                     geob = s_geo[jb];
                     opb = s_op[jb];
-                    cbb = s_cb[jb];
+                    cbb = __uint_as_float(s_aux[jb].x);
                 }
                 eval_one(Slot0{}, ja, geoa, opa, cba);
                 if (!has_b) break;
@@ -626,7 +639,7 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
                     todo &= todo - 1ull;
                     geoa = s_geo[ja];
                     opa = s_op[ja];
-                    cba = s_cb[ja];
+                    cba = __uint_as_float(s_aux[ja].x);
                 }
                 eval_one(Slot1{}, jb, geob, opb, cbb);
                 flush(2u);

@@ -309,7 +309,6 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
                                                         by0 + 7.0f);
         // splats of the batch that may touch this block, in order
         uint64_t todo = __builtin_amdgcn_ballot_w64(touch);
-        uint64_t used = 0ull;  // splats some pixel of the block blended
         mask_lo = 0u;
         mask_hi = 0u;
         wave_lds_fence();
@@ -323,7 +322,7 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
             // the ballot of a single comparison
             const uint64_t maybe_m = __builtin_amdgcn_ballot_w64(power >= 0.0f) &
                                      __builtin_amdgcn_ballot_w64(!(power > ca.z)) & ~done_m;
-            if (maybe_m == 0ull) return false;
+            if (maybe_m == 0ull) return done_m == ~0ull;
             // Branch-free from here: lanes outside `maybe` compute values the
             // selects discard.
             const float alpha = bh_minf(0.999f, ca.y * bh_exp2_neg(-power));
@@ -345,10 +344,6 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
                 pb = pb + col.z * vis;
                 if (DEPTH) pd = pd + col.w * vis;
                 t_acc = contrib ? next_t : t_acc;
-                // the block's last blended candidate (the tile end is the
-                // maximum over its pixels, the same for every lane)
-                last = batch + j + 1u;
-                if (BWD_INFO) used |= 1ull << j;
                 if (record) {
                     // the ballot (scalar) goes into candidate j's lane
                     mask_lo = write_lane(mask_lo, (uint32_t)blended, j);
@@ -372,7 +367,10 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
                     cab = s_c11a[jb];
                     colb = s_rgbd[jb];
                 }
-                if (blend_one(ja, xa, caa, cola) || !has_b) break;
+                // the wave's done test once per two candidates: after a, b's
+                // masks exclude the done pixels anyway
+                blend_one(ja, xa, caa, cola);
+                if (!has_b) break;
                 const bool has_a = todo != 0ull;
                 if (has_a) {
                     ja = (uint32_t)__builtin_ctzll(todo);
@@ -384,7 +382,14 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
                 if (blend_one(jb, xb, cab, colb) || !has_a) break;
             }
         }
-        pend_vis = BWD_INFO && ((used >> lane) & 1ull);
+        if (BWD_INFO) {
+            // the splats some pixel of the block blended (lane j: candidate
+            // batch + j) and the block's last one (the tile end is the
+            // maximum over its pixels, the same for every lane)
+            const uint64_t used = __builtin_amdgcn_ballot_w64((mask_lo | mask_hi) != 0u);
+            if (used) last = batch + 64u - (uint32_t)__builtin_clzll(used);
+            pend_vis = (used >> lane) & 1ull;
+        }
         pend_gid = my_gid;
         pend_mask = record && lane < cnt;
         pend_at = rbase + (batch - lo) + lane;
