@@ -495,6 +495,14 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
     *state_out = nullptr;
     if (uin->img_w == 0 || uin->img_h == 0)
         return set_error(ctx, BH_ERR_INVALID_ARG, "Can't render images with 0 size.");
+    {
+        // the tile walks split a box's flattened tile index into row and
+        // column through a float reciprocal, exact below 2^21 tiles an image
+        const uint64_t tiles = (uint64_t)div_up(uin->img_w, BH_TILE_WIDTH) *
+                               div_up(uin->img_h, (flags & BH_FLAG_TILE_16X8) ? 8u : BH_TILE_WIDTH);
+        if (tiles >= (1ull << 21))
+            return set_error(ctx, BH_ERR_INVALID_ARG, "render_forward: images are limited to 2^21 tiles");
+    }
     if (sh_degree > 4) return set_error(ctx, BH_ERR_INVALID_ARG, "sh_degree must be <= 4");
     if (uin->camera_model > BH_CAMERA_TPF) return set_error(ctx, BH_ERR_INVALID_ARG, "unknown camera model");
     const bool bwd = (flags & BH_FLAG_BWD_INFO) != 0;

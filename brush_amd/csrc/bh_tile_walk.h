@@ -17,12 +17,27 @@
 
 namespace bh {
 
-// One splat's walk record in LDS (48 bytes, three 16-byte reads).
+// One splat's walk record in LDS (64 bytes, four reads).
 struct WalkRec {
     float4 a;  // mean x, mean y, conic c00, conic c01
     float4 b;  // conic c11, power threshold, 1 / bbox width, end item index (bits)
     uint4 c;   // bbox min_x, bbox min_y, bbox width, first item index
+    float4 d;  // the predicate's divisors' reciprocals 1 / (16^2 c00), 1 / (TH^2 c11)
 };
+
+// RN(num / den) from y = RN(1 / den) for den > 0 and num < den (quotient
+// below 1, so nothing overflows): q0 = RN(num y) is within an ulp of the
+// quotient, the residual num - den q0 is exact in one fma, and RN(q0 + r y)
+// is the correctly rounded quotient (Markstein's theorem for a correctly
+// rounded reciprocal and a faithful first quotient; the quotient's
+// correctly rounded value is what the reference's division gives).  Below the
+// normal range the result can differ from the division in the last place of
+// a subnormal, which the predicate then adds to a tile edge that absorbs it.
+__device__ __forceinline__ float div_by_recip(float num, float den, float y) {
+    const float q0 = num * y;
+    const float r = __builtin_fmaf(-den, q0, num);
+    return __builtin_fmaf(r, y, q0);
+}
 
 template <int CTRL, int ROW_MASK>
 __device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
@@ -70,7 +85,7 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
 // whose mean lies in the tile gets -1, which passes).  Tile widths 16 and TH
 // are exact differences of the tile's float edges for tile columns < 2^20.
 template <int TH>
-__device__ __forceinline__ float tile_power(uint32_t tx, uint32_t ty, V2 m, const S2& c) {
+__device__ __forceinline__ float tile_power(uint32_t tx, uint32_t ty, V2 m, const S2& c, float rx, float ry) {
     const float min_x = (float)(tx * 16u), min_y = (float)(ty * (uint32_t)TH);
     const float max_x = min_x + 16.0f, max_y = min_y + (float)TH;
     const bool x_left = m.x < min_x, x_right = m.x > max_x;
@@ -83,8 +98,13 @@ __device__ __forceinline__ float tile_power(uint32_t tx, uint32_t ty, V2 m, cons
     const float dyf = y_above ? (float)TH : -(float)TH;
     const float diff_x = m.x - corner_x;
     const float diff_y = m.y - corner_y;
-    const float qx = bh_clampf((dxf * c.c00 * diff_x + dxf * c.c01 * diff_y) / (dxf * c.c00 * dxf), 0.0f, 1.0f);
-    const float qy = bh_clampf((dyf * c.c01 * diff_x + dyf * c.c11 * diff_y) / (dyf * c.c11 * dyf), 0.0f, 1.0f);
+    // the reference's quotients (dxf c00 dx + dxf c01 dy) / (dxf c00 dxf),
+    // their divisors 16^2 c00 and TH^2 c11 for either sign of dxf, dyf; a
+    // quotient at or above 1 clamps to 1 either way
+    const float nx = dxf * c.c00 * diff_x + dxf * c.c01 * diff_y, dnx = dxf * c.c00 * dxf;
+    const float ny = dyf * c.c01 * diff_x + dyf * c.c11 * diff_y, dny = dyf * c.c11 * dyf;
+    const float qx = nx >= dnx ? 1.0f : bh_maxf(div_by_recip(nx, dnx, rx), 0.0f);
+    const float qy = ny >= dny ? 1.0f : bh_maxf(div_by_recip(ny, dny, ry), 0.0f);
     const float tt_x = in_y ? 0.0f : qx;
     const float tt_y = in_x ? 0.0f : qy;
     const float px = corner_x + tt_x * dxf;
@@ -119,6 +139,8 @@ __device__ uint32_t wave_tile_walk(uint32_t lane, uint32_t items, V2 m, const S2
     rec[lane].a = make_float4(m.x, m.y, conic.c00, conic.c01);
     rec[lane].b = make_float4(conic.c11, pt, items ? 1.0f / (float)bw : 0.0f, __uint_as_float(incl));
     rec[lane].c = make_uint4(bb.min_x, bb.min_y, bw, start);
+    rec[lane].d = make_float4(items ? 1.0f / (256.0f * conic.c00) : 0.0f,
+                              items ? 1.0f / ((float)(TH * TH) * conic.c11) : 0.0f, 0.0f, 0.0f);
     hits[lane] = 0u;
     wave_lds_fence();
     uint32_t written = 0;  // passing items of earlier steps (wave uniform)
@@ -133,17 +155,17 @@ __device__ uint32_t wave_tile_walk(uint32_t lane, uint32_t items, V2 m, const S2
         const bool valid = item < total;
         const WalkRec r = rec[owner & 63u];
         const uint32_t local = item - r.c.w;
-        // row = local / width through the float reciprocal, then one exact
-        // correction step either way (selects, no branches)
-        uint32_t row = (uint32_t)(((float)local + 0.5f) * r.b.z);
-        int32_t col = (int32_t)(local - row * r.c.z);
-        const bool under = col < 0;
-        const bool over = !under && (uint32_t)col >= r.c.z;
-        row = under ? row - 1u : (over ? row + 1u : row);
-        col = under ? col + (int32_t)r.c.z : (over ? col - (int32_t)r.c.z : col);
-        const uint32_t tx = r.c.x + (uint32_t)col, ty = r.c.y + row;
+        // row = local / width, exactly, through the float reciprocal: with
+        // w = width and 1/w rounded, (local + 0.5) / w lies at least 0.5 / w
+        // from an integer and the two roundings move it by less than
+        // (row + 1) 2^-23, below 0.5 / w while (row + 1) w < 2^22 (a box
+        // holds at most tile_bw * tile_bh < 2^21 tiles: bh_render_forward
+        // rejects larger images)
+        const uint32_t row = (uint32_t)(((float)local + 0.5f) * r.b.z);
+        const uint32_t col = local - row * r.c.z;
+        const uint32_t tx = r.c.x + col, ty = r.c.y + row;
         // will_contribute as one comparison; the lane conditions stay wave masks
-        const float power = tile_power<TH>(tx, ty, v2(r.a.x, r.a.y), S2{r.a.z, r.a.w, r.b.x});
+        const float power = tile_power<TH>(tx, ty, v2(r.a.x, r.a.y), S2{r.a.z, r.a.w, r.b.x}, r.d.x, r.d.y);
         const uint64_t pmask = __builtin_amdgcn_ballot_w64(power <= r.b.y) & __builtin_amdgcn_ballot_w64(valid);
         const bool pass = __builtin_amdgcn_inverse_ballot_w64(pmask);
         // the last lane of each splat's run in this step adds the run's hits

@@ -133,7 +133,7 @@ __device__ __forceinline__ void write_row_from_coeffs(const bh_project_uniforms&
 }
 
 template <bool MIP, int CAM, int TH, int DEG>
-__global__ __launch_bounds__(256) void project_forward_kernel(bh_project_uniforms u,
+__global__ __launch_bounds__(256, DEG >= 4 ? 4 : 5) void project_forward_kernel(bh_project_uniforms u,
                                                                const float* __restrict__ transforms,
                                                                const float* __restrict__ raw_opac,
                                                                const float* __restrict__ sh, uint32_t n,

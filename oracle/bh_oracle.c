@@ -40,6 +40,18 @@ void or_power_log2(const float* c00, const float* c01, const float* c11, const f
     }
 }
 
+/* The tile walks' quotient (brush_amd/csrc/bh_tile_walk.h div_by_recip):
+ * RN(num / den) from y = RN(1 / den) as q0 = RN(num y), r = fma(-den, q0, num),
+ * RN(fma(r, y, q0)), for the test that pins it against the division. */
+void or_div_by_recip(const float* num, const float* den, float* out, uint64_t n) {
+    for (uint64_t i = 0; i < n; i++) {
+        const float y = 1.0f / den[i];
+        const float q0 = num[i] * y;
+        const float r = fmaf(-den[i], q0, num[i]);
+        out[i] = fmaf(r, y, q0);
+    }
+}
+
 void or_logf(const float* in, float* out, uint64_t n) {
     for (uint64_t i = 0; i < n; i++) out[i] = bh_logf(in[i]);
 }

@@ -35,6 +35,7 @@ void or_set_threads(int n);
 /* Element-wise bh_expf / bh_logf, for pinning them against libm. */
 void or_expf(const float* in, float* out, uint64_t n);
 void or_exp2_neg(const float* in, float* out, uint64_t n);
+void or_div_by_recip(const float* num, const float* den, float* out, uint64_t n);
 void or_power_log2(const float* c00, const float* c01, const float* c11, const float* dx, const float* dy,
                    float* out, uint64_t n);
 void or_logf(const float* in, float* out, uint64_t n);

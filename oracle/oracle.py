@@ -108,6 +108,7 @@ def lib():
         L.or_set_threads.argtypes = [ctypes.c_int]
         L.or_expf.argtypes = [P, P, U64]
         L.or_exp2_neg.argtypes = [P, P, U64]
+        L.or_div_by_recip.argtypes = [P, P, P, U64]
         L.or_power_log2.argtypes = [P, P, P, P, P, P, U64]
         L.or_logf.argtypes = [P, P, U64]
         L.or_atan2f.argtypes = [P, P, P, U64]
@@ -161,6 +162,15 @@ def exp2_neg(x: np.ndarray) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.float32)
     out = np.empty_like(x)
     lib().or_exp2_neg(_p(x), _p(out), x.size)
+    return out
+
+
+def div_by_recip(num, den) -> np.ndarray:
+    """The tile walks' quotient from a rounded reciprocal (bh_tile_walk.h
+    div_by_recip), for its pin against the division."""
+    num, den = (np.ascontiguousarray(a, dtype=np.float32) for a in np.broadcast_arrays(num, den))
+    out = np.empty_like(num)
+    lib().or_div_by_recip(_p(num), _p(den), _p(out), out.size)
     return out
 
 

@@ -507,3 +507,59 @@ def test_candidate_tiles_render_the_same_image(seed, flags):
         gb = O.rasterize_backward(b, v_out, (flags & 6) | O.FLAG_REFINE_WEIGHT, (0.1, 0.2, 0.3))
         scale = np.abs(ga).max(axis=0) + 1e-12
         assert np.max(np.abs(ga - gb) / scale) < 1e-4
+
+
+def test_walk_quotient_by_reciprocal_is_the_division():
+    """The tile walks replace the predicate's divisions (the reference's
+    (dxf c00 dx + dxf c01 dy) / (dxf c00 dxf), helpers.rs:243-290) by a
+    quotient from the divisor's rounded reciprocal and one fma correction
+    (bh_tile_walk.h div_by_recip).  For quotients below 1 (larger ones clamp
+    to 1 without it) it must equal the IEEE division bit for bit wherever the
+    quotient is a normal number: random divisors 16^2 c00 / 8^2 c11 over
+    twelve decades, numerators spread over the quotient's range and packed
+    next to the divisor's multiples by powers of two, divisors with all-ones
+    and all-zeros mantissas."""
+    rng = np.random.default_rng(21)
+    n = 3_000_000
+    c = np.exp(rng.uniform(np.log(1e-6), np.log(1e6), n)).astype(np.float32)
+    den = (c * rng.choice(np.array([256.0, 64.0], np.float32), n)).astype(np.float32)
+    q = np.concatenate([rng.uniform(-4.0, 1.0, n // 3), np.exp(rng.uniform(np.log(1e-30), 0.0, n // 3)),
+                        1.0 - np.exp(rng.uniform(np.log(1e-9), 0.0, n - 2 * (n // 3)))])
+    num = (q * den.astype(np.float64)).astype(np.float32)
+    # divisors whose mantissa is all ones or all zeros, numerators one ulp
+    # either side of 2^-k times the divisor
+    e = rng.integers(-20, 20, 200_000)
+    mant = rng.choice(np.array([0x7FFFFF, 0x0, 0x400000, 0x7FFFFE, 0x1], np.uint32), e.size)
+    den2 = ((e.astype(np.int64) + 127).astype(np.uint32) << 23 | mant).view(np.float32)
+    k = rng.integers(0, 24, e.size)
+    base = (den2.astype(np.float64) * np.exp2(-k.astype(np.float64))).astype(np.float32)
+    num2 = np.concatenate([np.nextafter(base, np.float32(np.inf)), np.nextafter(base, np.float32(-np.inf)), base])
+    num = np.concatenate([num, num2])
+    den = np.concatenate([den, den2, den2, den2])
+    keep = num < den
+    num, den = num[keep], den[keep]
+    want = num / den  # float32 IEEE division
+    got = O.div_by_recip(num, den)
+    normal = np.abs(want) >= np.float32(2.0 ** -126)
+    assert np.array_equal(got[normal].view(np.uint32), want[normal].view(np.uint32))
+    assert np.all(np.abs(got[~normal].astype(np.float64) - want[~normal]) <= 2.0 ** -149)
+
+
+def test_walk_row_of_flattened_tile_is_exact():
+    """The tile walks split a box item l into row l / w and column through the
+    float reciprocal of the box width, with no correction step
+    (bh_tile_walk.h): (uint)((l + 0.5) * RN(1 / w)) must be l / w for every
+    width and item below 2^21 (bh_render_forward rejects images of 2^21 tiles
+    or more)."""
+    one, half = np.float32(1.0), np.float32(0.5)
+    l_small = np.arange(0, 1 << 16, dtype=np.uint32)
+    lf_small = l_small.astype(np.float32) + half
+    for w in range(1, 4097):
+        r = one / np.float32(w)
+        assert np.array_equal((lf_small * r).astype(np.uint32), l_small // np.uint32(w)), w
+    rng = np.random.default_rng(5)
+    for w in np.unique(np.concatenate([rng.integers(4097, 1 << 21, 2000), 1 << np.arange(12, 21)])):
+        l = np.concatenate([rng.integers(0, 1 << 21, 4000), np.arange(w - 2, min(1 << 21, 64 * w), w)]).astype(np.uint32)
+        l = l[l < (1 << 21)]
+        r = one / np.float32(w)
+        assert np.array_equal(((l.astype(np.float32) + half) * r).astype(np.uint32), l // np.uint32(w)), w
