@@ -328,7 +328,10 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
             const float alpha = bh_minf(0.999f, ca.y * bh_exp2_neg(-power));
             // the hard cutoff's weight is a step: alpha * w is a select
             const float w = SMOOTH ? cutoff_weight(alpha) : (alpha >= kCutMid ? 1.0f : 0.0f);
-            const float ae = SMOOTH ? alpha * w : (alpha >= kCutMid ? alpha : 0.0f);
+            // with the hard cutoff alpha * w is alpha wherever it is used: the
+            // lanes below the cutoff are outside `pass`, so their next_t and
+            // vis never reach a mask, a sum or the transmittance
+            const float ae = SMOOTH ? alpha * w : alpha;
             const float next_t = t_acc * (1.0f - ae);
             const uint64_t pass_m = maybe_m & __builtin_amdgcn_ballot_w64(w > 0.0f);
             const uint64_t sat_m = __builtin_amdgcn_ballot_w64(next_t <= 1.0e-4f) & pass_m;
@@ -357,28 +360,22 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
             todo &= todo - 1ull;
             float4 xa = s_xyco[ja], caa = s_c11a[ja], cola = s_rgbd[ja];
             while (true) {
+                // the next candidate's parameters, read unconditionally (slot
+                // 0 when the list is empty: read, never blended)
                 const bool has_b = todo != 0ull;
-                uint32_t jb = 0u;
-                float4 xb, cab, colb;
-                if (has_b) {
-                    jb = (uint32_t)__builtin_ctzll(todo);
-                    todo &= todo - 1ull;
-                    xb = s_xyco[jb];
-                    cab = s_c11a[jb];
-                    colb = s_rgbd[jb];
-                }
+                const uint32_t jb = has_b ? (uint32_t)__builtin_ctzll(todo) : 0u;
+                todo &= todo - 1ull;
+                const float4 xb = s_xyco[jb], cab = s_c11a[jb], colb = s_rgbd[jb];
                 // the wave's done test once per two candidates: after a, b's
                 // masks exclude the done pixels anyway
                 blend_one(ja, xa, caa, cola);
                 if (!has_b) break;
                 const bool has_a = todo != 0ull;
-                if (has_a) {
-                    ja = (uint32_t)__builtin_ctzll(todo);
-                    todo &= todo - 1ull;
-                    xa = s_xyco[ja];
-                    caa = s_c11a[ja];
-                    cola = s_rgbd[ja];
-                }
+                ja = has_a ? (uint32_t)__builtin_ctzll(todo) : 0u;
+                todo &= todo - 1ull;
+                xa = s_xyco[ja];
+                caa = s_c11a[ja];
+                cola = s_rgbd[ja];
                 if (blend_one(jb, xb, cab, colb) || !has_a) break;
             }
         }
