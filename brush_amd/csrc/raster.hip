@@ -338,20 +338,21 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
             const uint64_t blended = pass_m & ~sat_m;
             const bool contrib = __builtin_amdgcn_inverse_ballot_w64(blended);
             done_m |= sat_m;
-            if (blended != 0ull) {
-                // vis is zero outside `contrib`: adding col * 0 (a signed zero;
-                // colours are finite) leaves a sum that is >= +0 unchanged
-                const float vis = contrib ? ae * t_acc : 0.0f;
-                pr = pr + col.x * vis;
-                pg = pg + col.y * vis;
-                pb = pb + col.z * vis;
-                if (DEPTH) pd = pd + col.w * vis;
-                t_acc = contrib ? next_t : t_acc;
-                if (record) {
-                    // the ballot (scalar) goes into candidate j's lane
-                    mask_lo = write_lane(mask_lo, (uint32_t)blended, j);
-                    mask_hi = write_lane(mask_hi, (uint32_t)(blended >> 32), j);
-                }
+            // unconditional (a candidate past the pre-test nearly always
+            // blends some pixel): vis is zero outside `contrib`, and adding
+            // col * 0 (a signed zero; colours are finite) leaves a sum that is
+            // >= +0 unchanged; an empty ballot written into lane j leaves its
+            // record empty
+            const float vis = contrib ? ae * t_acc : 0.0f;
+            pr = pr + col.x * vis;
+            pg = pg + col.y * vis;
+            pb = pb + col.z * vis;
+            if (DEPTH) pd = pd + col.w * vis;
+            t_acc = contrib ? next_t : t_acc;
+            if (record) {
+                // the ballot (scalar) goes into candidate j's lane
+                mask_lo = write_lane(mask_lo, (uint32_t)blended, j);
+                mask_hi = write_lane(mask_hi, (uint32_t)(blended >> 32), j);
             }
             return done_m == ~0ull;
         };
@@ -364,7 +365,7 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
                 // 0 when the list is empty: read, never blended)
                 const bool has_b = todo != 0ull;
                 const uint32_t jb = has_b ? (uint32_t)__builtin_ctzll(todo) : 0u;
-                todo &= todo - 1ull;
+                todo &= ~(1ull << jb);
                 const float4 xb = s_xyco[jb], cab = s_c11a[jb], colb = s_rgbd[jb];
                 // the wave's done test once per two candidates: after a, b's
                 // masks exclude the done pixels anyway
@@ -372,7 +373,7 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
                 if (!has_b) break;
                 const bool has_a = todo != 0ull;
                 ja = has_a ? (uint32_t)__builtin_ctzll(todo) : 0u;
-                todo &= todo - 1ull;
+                todo &= ~(1ull << ja);
                 xa = s_xyco[ja];
                 caa = s_c11a[ja];
                 cola = s_rgbd[ja];

@@ -130,9 +130,18 @@ def gradient_term_magnitudes(o, tr, sh, opac, vc, mip: bool = False, rel: float 
     of order 1-100 through intermediates that cancel, so a few entries amplify
     lane differences of 1e-7 into percent-level changes (the CPU restatement
     and the GPU, whose lanes agree to 7 digits, differ there); for a
-    well-conditioned entry the movement is ~rel * |entry|.  The maximum over a
-    few random perturbations."""
+    well-conditioned entry the movement is ~rel * |entry|.
+
+    Two parts, added: the first-order worst case over that box of lane errors
+    (each lane moved by +rel * scale alone, the entries' absolute changes
+    summed over the lanes: a deterministic bound for errors of either sign in
+    every lane), and the largest movement under a few random perturbations of
+    the same size, which also carries the entry's own float32 evaluation noise
+    (for the ill-conditioned entries that noise, not the linear response,
+    dominates; two correct GPU runs differ there by half of the random part
+    alone)."""
     base = [x.astype(np.float64) for x in O.project_backward(o, tr, sh, opac, vc, mip)[:3]]
+    box = [np.zeros(x.shape) for x in base]
     sens = [np.zeros(x.shape) for x in base]
     rng = np.random.default_rng(seed)
     vc64 = vc.astype(np.float64)
@@ -140,13 +149,19 @@ def gradient_term_magnitudes(o, tr, sh, opac, vc, mip: bool = False, rel: float 
     for a, b in LANE_GROUPS:
         if a < vc64.shape[1]:
             scale[:, a:b] = np.max(np.abs(vc64[:, a:b]), axis=1, keepdims=True)
+    for lane in range(vc.shape[1]):
+        vp = vc64.copy()
+        vp[:, lane] += rel * scale[:, lane]
+        out = O.project_backward(o, tr, sh, opac, vp.astype(np.float32), mip)[:3]
+        for s_, x, b in zip(box, out, base):
+            s_ += np.abs(x.astype(np.float64) - b)
     for _ in range(draws):
         noise = rng.uniform(-1.0, 1.0, vc.shape)
         vp = (vc64 + rel * noise * scale).astype(np.float32)
         out = O.project_backward(o, tr, sh, opac, vp, mip)[:3]
         for s_, x, b in zip(sens, out, base):
             np.maximum(s_, np.abs(x.astype(np.float64) - b), out=s_)
-    return sens
+    return [s_ + b_ for s_, b_ in zip(sens, box)]
 
 
 def grad_close(name, got, want, magnitude, rtol=1e-3, atol_frac=1e-4, cond=1.0):
