@@ -845,12 +845,18 @@ __device__ __forceinline__ void block_zero(float* __restrict__ p, size_t begin, 
     for (size_t i = head + threadIdx.x; i < count; i += blockDim.x) q[i] = 0.0f;
 }
 
-// Each block first zero-fills its 256 dense output rows with contiguous stores
-// (rows without gradient — culled splats, splats behind saturated pixels —
-// are most rows), then compacts the ids that have gradient into an LDS list
-// and runs the VJP over that list with every lane busy, overwriting their
-// rows.  cfg == nullptr: v_combined holds one row per global id (the fused
-// backward), else v_combined[cfg[gid]].
+// Each block owns PB_SPLATS consecutive global ids.  It reads their gradient
+// lanes and compacts the ids that have gradient into an LDS list, zero-fills
+// its dense output rows with contiguous stores (rows without gradient --
+// culled splats, splats behind saturated pixels -- are most rows), and then
+// runs the VJP over the list with every lane busy, overwriting those rows.
+// One block covers four times the ids one pass of its threads reads, so the
+// VJP's latency (its rows' loads, then a dependent chain) is paid once per
+// 1024 ids and ~1000 blocks are all resident at once.  cfg == nullptr:
+// v_combined holds one row per global id (the fused backward), else
+// v_combined[cfg[gid]].
+constexpr uint32_t PB_SPLATS = 1024u;
+
 template <int DEG, bool MIP, int CAM>
 __global__ __launch_bounds__(256) void project_backward_kernel(
     bh_project_uniforms u, const float* __restrict__ transforms, const float* __restrict__ sh,
@@ -858,38 +864,61 @@ __global__ __launch_bounds__(256) void project_backward_kernel(
     const float* __restrict__ v_combined, float* __restrict__ v_transforms, float* __restrict__ v_coeffs,
     float* __restrict__ v_raw_opac, float* __restrict__ v_refine) {
     constexpr int NC = (DEG + 1) * (DEG + 1);
-    __shared__ uint32_t s_gid[256];
-    __shared__ uint32_t s_row[256];
-    __shared__ uint32_t s_count[4];
+    constexpr uint32_t PASSES = PB_SPLATS / 256u;
+    __shared__ uint32_t s_gid[PB_SPLATS];
+    __shared__ uint32_t s_row[PB_SPLATS];
+    __shared__ uint32_t s_count[PASSES][4];
     const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
-    const uint32_t gid = blockIdx.x * 256u + t;
-    const uint32_t c = gid < n ? (cfg ? cfg[gid] : gid) : 0xFFFFFFFFu;
-    bool any = false;
-    if (c != 0xFFFFFFFFu) {
-        const float* src = v_combined + (size_t)c * 11;
+    const size_t g0 = (size_t)blockIdx.x * PB_SPLATS, g1 = min<size_t>(g0 + PB_SPLATS, n);
+    // every pass's lanes read first (the loads of all passes in flight
+    // together), then the ballots
+    uint32_t cs[PASSES];
+    bool any[PASSES];
 #pragma unroll
-        for (int k = 0; k < 11; k++) any = any || src[k] != 0.0f;
+    for (uint32_t p = 0; p < PASSES; ++p) {
+        const size_t gid = g0 + p * 256u + t;
+        cs[p] = gid < n ? (cfg ? cfg[gid] : (uint32_t)gid) : 0xFFFFFFFFu;
     }
-    const size_t g0 = (size_t)blockIdx.x * 256u, g1 = min<size_t>(g0 + 256u, n);
+#pragma unroll
+    for (uint32_t p = 0; p < PASSES; ++p) {
+        bool a = false;
+        if (cs[p] != 0xFFFFFFFFu) {
+            const float* src = v_combined + (size_t)cs[p] * 11;
+#pragma unroll
+            for (int k = 0; k < 11; k++) a = a || src[k] != 0.0f;
+        }
+        any[p] = a;
+    }
+    uint64_t masks[PASSES];
+#pragma unroll
+    for (uint32_t p = 0; p < PASSES; ++p) {
+        masks[p] = __ballot(any[p]);
+        if (lane == 0) s_count[p][wave] = (uint32_t)__popcll(masks[p]);
+    }
     block_zero(v_transforms, g0 * 10u, g1 * 10u);
     block_zero(v_coeffs, g0 * (3u * NC), g1 * (3u * NC));
     block_zero(v_raw_opac, g0, g1);
     block_zero(v_refine, g0, g1);
-    // compact the ids with gradient: per-wave ballot, then wave offsets
-    const uint64_t mask = __ballot(any);
-    if (lane == 0) s_count[wave] = (uint32_t)__popcll(mask);
     __syncthreads();
-    uint32_t before = 0, total = 0;
+    // compact the ids with gradient: list order = pass, wave, lane
+    uint32_t base = 0;
 #pragma unroll
-    for (int w = 0; w < 4; w++) {
-        before += (uint32_t)w < wave ? s_count[w] : 0u;
-        total += s_count[w];
+    for (uint32_t p = 0; p < PASSES; ++p) {
+        uint32_t before = base;
+#pragma unroll
+        for (uint32_t w = 0; w < 4u; w++) {
+            before += w < wave ? s_count[p][w] : 0u;
+            base += s_count[p][w];
+        }
+        if (any[p]) {
+            const uint32_t slot = before + lanes_below(masks[p]);
+            s_gid[slot] = (uint32_t)(g0 + p * 256u + t);
+            s_row[slot] = cs[p];
+        }
     }
-    if (any) {
-        const uint32_t slot = before + lanes_below(mask);
-        s_gid[slot] = gid;
-        s_row[slot] = c;
-    }
+    const uint32_t total = base;
+    // the zero-fill's stores precede the list's stores to the same rows
+    // (the barrier's workgroup release), and the list is complete
     __syncthreads();
     for (uint32_t i = t; i < total; i += 256u) {
         const uint32_t g = s_gid[i];
@@ -906,7 +935,7 @@ template <int DEG, bool MIP>
 static void launch_pb_cam(bh_ctx* ctx, const bh_project_uniforms& u, const float* transforms, const float* sh,
                           const float* raw_opac, const uint32_t* cfg, uint32_t n, const float* v_combined,
                           float* v_transforms, float* v_coeffs, float* v_raw_opac, float* v_refine) {
-    const uint32_t blocks = div_up(n, 256);
+    const uint32_t blocks = div_up(n, PB_SPLATS);
 #define BH_PB(C)                                                                                                  \
     project_backward_kernel<DEG, MIP, C><<<blocks, 256, 0, ctx->stream>>>(u, transforms, sh, raw_opac, cfg, n,     \
                                                                           v_combined, v_transforms, v_coeffs,     \
