@@ -344,10 +344,12 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
             // >= +0 unchanged; an empty ballot written into lane j leaves its
             // record empty
             const float vis = contrib ? ae * t_acc : 0.0f;
-            pr = pr + col.x * vis;
-            pg = pg + col.y * vis;
-            pb = pb + col.z * vis;
-            if (DEPTH) pd = pd + col.w * vis;
+            // the accumulation as one fma per channel, as the restatement
+            // evaluates it
+            pr = __builtin_fmaf(col.x, vis, pr);
+            pg = __builtin_fmaf(col.y, vis, pg);
+            pb = __builtin_fmaf(col.z, vis, pb);
+            if (DEPTH) pd = __builtin_fmaf(col.w, vis, pd);
             t_acc = contrib ? next_t : t_acc;
             if (record) {
                 // the ballot (scalar) goes into candidate j's lane

@@ -807,10 +807,13 @@ void or_rasterize(uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t til
                     if (next_t <= 1.0e-4f) break;
                     if (bwd_info) visible[gfc[cgid_from_isect[i]]] = 1.0f;
                     float vis = ae * t_acc;
-                    r += bh_maxf(s[6], 0.0f) * vis;
-                    g += bh_maxf(s[7], 0.0f) * vis;
-                    b += bh_maxf(s[8], 0.0f) * vis;
-                    if (depth) d += s[9] * vis;
+                    /* pix_out += color * vis (rasterize.rs) as one fma a channel:
+                     * the WGSL leaves contraction to the platform's shader
+                     * compiler; this restatement and the kernels fix it as fma */
+                    r = fmaf(bh_maxf(s[6], 0.0f), vis, r);
+                    g = fmaf(bh_maxf(s[7], 0.0f), vis, g);
+                    b = fmaf(bh_maxf(s[8], 0.0f), vis, b);
+                    if (depth) d = fmaf(s[9], vis, d);
                     t_acc = next_t;
                     last = i + 1;
                 }
@@ -856,9 +859,9 @@ void or_rasterize_reference(const float* projected, uint32_t n, uint32_t w, uint
                     float nt = t * (1.0f - ea);
                     if (nt <= 1.0e-4f) break;
                     float vis = ea * t;
-                    r += bh_maxf(s[6], 0.0f) * vis;
-                    g += bh_maxf(s[7], 0.0f) * vis;
-                    b += bh_maxf(s[8], 0.0f) * vis;
+                    r = fmaf(bh_maxf(s[6], 0.0f), vis, r);
+                    g = fmaf(bh_maxf(s[7], 0.0f), vis, g);
+                    b = fmaf(bh_maxf(s[8], 0.0f), vis, b);
                     t = nt;
                 }
             }
