@@ -7,10 +7,11 @@
 // splat order and, within a splat, in the reference's row-major tile order,
 // and tests 64 items per step.  Per step, every lane finds the splat that owns
 // its item (a scatter of segment starts into LDS and a max-scan), fetches that
-// splat's record from LDS and evaluates the same tile predicate.  Hits are
-// tallied per splat by the last lane of each splat's run in the step; passing
-// items come out in exactly the order the per-splat loops would emit them, so
-// the map kernel writes them contiguously.
+// splat's record from LDS and evaluates the same tile predicate.  The lane
+// holding a splat's last item records the wave's running count of passing
+// items through it, and a splat's hits are the difference of two such
+// prefixes.  Passing items come out in exactly the order the per-splat loops
+// would emit them, so the map kernel writes them contiguously.
 #pragma once
 
 #include "bh_splat_math.h"
@@ -121,7 +122,7 @@ __device__ __forceinline__ uint32_t bbox_items(const TileBox& bb) {
 // Cooperative walk of one wave over 16 x TH tiles.  Every lane of the wave must call it (it uses
 // wave-wide DPP and ballots).  `items` is this lane's bbox tile count (0 for a
 // culled or absent splat); m, conic, pt, bb describe its splat.  `rec`,
-// `owner_slot` and `hits` are this wave's 64-entry LDS arrays.
+// `owner_slot` and `ends` are this wave's 64-entry LDS arrays.
 //
 // Returns the number of passing tiles of this lane's splat.  With WRITE, the
 // passing items are stored at out_base + (passing items before it in walk
@@ -129,7 +130,7 @@ __device__ __forceinline__ uint32_t bbox_items(const TileBox& bb) {
 // ids, skipping positions >= out_end.
 template <bool WRITE, int TH = 16>
 __device__ uint32_t wave_tile_walk(uint32_t lane, uint32_t items, V2 m, const S2& conic, float pt,
-                                   const TileBox& bb, WalkRec* rec, uint32_t* owner_slot, uint32_t* hits,
+                                   const TileBox& bb, WalkRec* rec, uint32_t* owner_slot, uint32_t* ends,
                                    uint32_t tile_bw, uint32_t out_base, uint32_t out_end, uint32_t id_base,
                                    uint32_t* __restrict__ tile_ids, uint32_t* __restrict__ ids) {
     const uint32_t incl = wave_incl_add_u32(items);
@@ -141,7 +142,7 @@ __device__ uint32_t wave_tile_walk(uint32_t lane, uint32_t items, V2 m, const S2
     rec[lane].c = make_uint4(bb.min_x, bb.min_y, bw, start);
     rec[lane].d = make_float4(items ? 1.0f / (256.0f * conic.c00) : 0.0f,
                               items ? 1.0f / ((float)(TH * TH) * conic.c11) : 0.0f, 0.0f, 0.0f);
-    hits[lane] = 0u;
+    ends[lane] = 0u;
     wave_lds_fence();
     uint32_t written = 0;  // passing items of earlier steps (wave uniform)
     for (uint32_t base = 0; base < total; base += 64u) {
@@ -162,29 +163,32 @@ __device__ uint32_t wave_tile_walk(uint32_t lane, uint32_t items, V2 m, const S2
         // holds at most tile_bw * tile_bh < 2^21 tiles: bh_render_forward
         // rejects larger images)
         const uint32_t row = (uint32_t)(((float)local + 0.5f) * r.b.z);
-        const uint32_t col = local - row * r.c.z;
+        const uint32_t col = local - __umul24(row, r.c.z);  // both factors and the product < 2^21
         const uint32_t tx = r.c.x + col, ty = r.c.y + row;
         // will_contribute as one comparison; the lane conditions stay wave masks
         const float power = tile_power<TH>(tx, ty, v2(r.a.x, r.a.y), S2{r.a.z, r.a.w, r.b.x}, r.d.x, r.d.y);
         const uint64_t pmask = __builtin_amdgcn_ballot_w64(power <= r.b.y) & __builtin_amdgcn_ballot_w64(valid);
         const bool pass = __builtin_amdgcn_inverse_ballot_w64(pmask);
-        // the last lane of each splat's run in this step adds the run's hits
-        const uint32_t run_lo = r.c.w > base ? r.c.w - base : 0u;
-        const uint32_t before_run = (uint32_t)__popcll(pmask & ((1ull << run_lo) - 1ull));
-        const uint32_t through_me = lanes_below(pmask) + (pass ? 1u : 0u);
-        const bool last_of_run = valid && (lane == 63u || item + 1u == __float_as_uint(r.b.w));
-        if (last_of_run) hits[owner & 63u] += through_me - before_run;
+        // the wave's passing items up to and including this one, kept at a
+        // splat's last item
+        const uint32_t below = lanes_below(pmask);
+        if (valid && item + 1u == __float_as_uint(r.b.w)) ends[owner & 63u] = written + below + (pass ? 1u : 0u);
         if (WRITE && pass) {
-            const uint32_t pos = out_base + written + lanes_below(pmask);
+            const uint32_t pos = out_base + written + below;
             if (pos < out_end) {
-                tile_ids[pos] = tx + ty * tile_bw;
+                tile_ids[pos] = tx + __umul24(ty, tile_bw);  // a tile id < 2^21
                 ids[pos] = id_base + owner;
             }
         }
         written += (uint32_t)__popcll(pmask);
         wave_lds_fence();
     }
-    return hits[lane];
+    // a splat without items takes the prefix of the splats before it
+    const uint32_t through = wave_incl_max_u32(ends[lane]);
+    owner_slot[lane] = through;
+    wave_lds_fence();
+    const uint32_t before = lane ? owner_slot[lane - 1u] : 0u;
+    return through - before;
 }
 
 }  // namespace bh

@@ -108,7 +108,8 @@ __device__ __forceinline__ void load_sh_row(const float* __restrict__ sh, uint32
 }
 
 // A visible splat's projected row (project_visible.rs:22-89) in its global-id
-// slot: 12 floats, x y c00 c01 | c11 opac r g | b depth - -.  Slots are packed
+// slot: 12 floats, x y c00 c01 | c11 opac r g | b depth pt -, pt being the
+// tile predicate's power threshold ln(255 opac) for the map's walk.  Slots are packed
 // (48 bytes): a wave's stores cover whole lines, where 48 bytes of a 64-byte
 // slot cost partial-line writes.
 // project_forward reads the parameters and SH rows in global-id order
@@ -129,7 +130,7 @@ __device__ __forceinline__ void write_row_from_coeffs(const bh_project_uniforms&
     float4* dst = rows + (size_t)gid * 3;
     dst[0] = make_float4(p.m.x, p.m.y, p.conic.c00, p.conic.c01);
     dst[1] = make_float4(p.conic.c11, p.opac, r, g);
-    dst[2] = make_float4(b, p.depth, 0.0f, 0.0f);
+    dst[2] = make_float4(b, p.depth, p.pt, 0.0f);
 }
 
 template <bool MIP, int CAM, int TH, int DEG>
@@ -398,7 +399,7 @@ __global__ __launch_bounds__(256) void map_intersects_kernel(uint32_t tile_bw, u
         if (!emit) return;
         m = v2(a.x, a.y);
         conic = S2{a.z, a.w, b.x};
-        pt = bh_logf(b.y * 255.0f);
+        pt = d.z;  // bh_logf(b.y * 255), as the counting walk used it
         bb = tile_bbox<TH>(m, bbox_extent(conic, pt), tile_bw, tile_bh);
         base = c == 0 ? 0u : cum[c - 1];
         budget = cum[c] - base;
