@@ -164,6 +164,12 @@ __global__ __launch_bounds__(256, DEG >= 4 ? 4 : 5) void project_forward_kernel(
         vis = project_cull<MIP, CAM, TH>(u, t, raw_opac[gid], p);
         mean = v3(t[0], t[1], t[2]);
     }
+    // Every parameter load has landed here (vmcnt(0); they have long since,
+    // but a cull that exits early leaves some unread).  Without it, the merge
+    // after the conditional SH loads below makes the compiler's first reuse of
+    // such a register wait for all outstanding loads, the SH row included, and
+    // the tile walk would no longer hide the row's latency.
+    __builtin_amdgcn_s_waitcnt(0x0F70);
     constexpr int NC = (DEG + 1) * (DEG + 1);
     float coeffs[3 * NC];
     if (vis) load_sh_row<NC>(sh, gid, coeffs);
