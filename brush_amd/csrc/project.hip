@@ -161,7 +161,11 @@ __global__ __launch_bounds__(256, DEG >= 4 ? 4 : 5) void project_forward_kernel(
             t[2 * i] = q.x;
             t[2 * i + 1] = q.y;
         }
-        vis = project_cull<MIP, CAM, TH>(u, t, raw_opac[gid], p);
+        // the cull fills q only for a splat it keeps: its early exits then
+        // carry no copies of p's zeros
+        Projected q;
+        vis = project_cull<MIP, CAM, TH>(u, t, raw_opac[gid], q);
+        if (vis) p = q;
         mean = v3(t[0], t[1], t[2]);
     }
     // Every parameter load has landed here (vmcnt(0); they have long since,
