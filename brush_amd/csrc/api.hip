@@ -670,23 +670,37 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
             launch_fill_u32(ctx, (uint32_t*)projected, 0u, 10);
         }
         if (p.m) {
-            uint32_t *ut, *uc, *tk, *tv;
-            char* scr;
-            BH_TRY(ws.get(&ut, p.m));
-            BH_TRY(ws.get(&uc, p.m));
-            BH_TRY(ws.get(&tk, p.m));
-            BH_TRY(ws.get(&tv, p.m));
             // tile sort over bits(num_tiles) bits (render.rs:392-395); the map
-            // kernel zeroes the sort's scratch
+            // kernel zeroes the sort's scratch.  Below 2^16 tiles (sentinel
+            // included: 16 key bits) the map's tile ids and the sort's
+            // intermediate keys are 16-bit, the sorted ones 32-bit.
             const uint32_t bits = bit_length(num_tiles);
+            const bool k16 = bits <= 16;
+            uint32_t *uc, *tv;
+            void *ut, *tk;
+            char* scr;
+            if (k16) {
+                BH_TRY(ws.get((uint16_t**)&ut, p.m));
+                BH_TRY(ws.get((uint16_t**)&tk, p.m));
+            } else {
+                BH_TRY(ws.get((uint32_t**)&ut, p.m));
+                BH_TRY(ws.get((uint32_t**)&tk, p.m));
+            }
+            BH_TRY(ws.get(&uc, p.m));
+            BH_TRY(ws.get(&tv, p.m));
             BH_TRY(ws.get(&scr, radix_sort_scratch_bytes(p.m, bits)));
             launch_map_intersects(ctx, u.tile_bw, u.tile_bh, tile_h, vis_rows, gfc, num_splats, cum, p.v, projected,
-                                  depths, ut, uc, (uint32_t*)scr, (uint32_t)radix_sort_zeroed_words(p.m, bits), dc);
+                                  depths, ut, k16, uc, (uint32_t*)scr, (uint32_t)radix_sort_zeroed_words(p.m, bits),
+                                  dc);
             BH_TRY(check_launch(ctx, "map_intersects"));
             SortDevice dev;
             if (dc) dev.n = dc + 7;
-            BH_TRY(radix_sort_pairs(ctx, ut, uc, p.m, bits, 0u, 0xFFFFFFFFu, tile_ids, cgids, tk, tv, scr, "tile_sort",
-                                    true, nullptr, nullptr, dev));
+            if (k16)
+                BH_TRY(radix_sort_pairs_k16(ctx, (const uint16_t*)ut, uc, p.m, bits, tile_ids, cgids, (uint16_t*)tk,
+                                            tv, scr, "tile_sort", true, dev));
+            else
+                BH_TRY(radix_sort_pairs(ctx, (const uint32_t*)ut, uc, p.m, bits, 0u, 0xFFFFFFFFu, tile_ids, cgids,
+                                        (uint32_t*)tk, tv, scr, "tile_sort", true, nullptr, nullptr, dev));
         } else {
             launch_fill_u32(ctx, tile_ids, 0u, 1);
             launch_fill_u32(ctx, cgids, 0u, 1);

@@ -171,6 +171,12 @@ bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t*
                            const char* tag = "radix", bool scratch_zeroed = false,
                            const uint32_t* gather_src = nullptr, uint32_t* gather_out = nullptr,
                            const SortDevice& dev = SortDevice{});
+// The same over 16-bit keys (key_bits <= 16, no key transform): keys_in and
+// tmp_keys hold uint16_t, the sorted keys land in keys_out as uint32_t.
+bh_status radix_sort_pairs_k16(bh_ctx* ctx, const uint16_t* keys_in, const uint32_t* vals_in, uint32_t n,
+                               uint32_t key_bits, uint32_t* keys_out, uint32_t* vals_out, uint16_t* tmp_keys,
+                               uint32_t* tmp_vals, void* scratch, const char* tag = "radix",
+                               bool scratch_zeroed = false, const SortDevice& dev = SortDevice{});
 // out[i] = in[i] & mask
 void launch_mask_u32(bh_ctx* ctx, const uint32_t* in, uint32_t mask, uint32_t n, uint32_t* out);
 // keys_out[i] = keys_in[perm[i]], vals_out[i] = vals_in[perm[i]]
@@ -197,10 +203,12 @@ void launch_project_visible(bh_ctx* ctx, const float* rows, const uint32_t* gfc,
 // (the tile sort's scratch).  With dev (the context counters after
 // project_forward), num_visible is a capacity: the kernel reads the visible
 // count from dev[0] and writes intersections only when they fit the buffers.
+// The tile ids are written as uint16_t when tile_ids16 is set (fewer than
+// 2^16 tiles, the sentinel included), else as uint32_t.
 void launch_map_intersects(bh_ctx* ctx, uint32_t tile_bw, uint32_t tile_bh, uint32_t tile_h, const float* rows,
                            const uint32_t* gfc, uint32_t num_splats, const uint32_t* cum, uint32_t num_visible,
-                           float* projected, float* depths, uint32_t* tile_ids, uint32_t* cgids, uint32_t* zero,
-                           uint32_t zero_words, const uint32_t* dev = nullptr);
+                           float* projected, float* depths, void* tile_ids, bool tile_ids16, uint32_t* cgids,
+                           uint32_t* zero, uint32_t zero_words, const uint32_t* dev = nullptr);
 
 // raster.hip
 // With dev_m, m is a capacity and the ids are tile_ids[0, min(m, *dev_m)).

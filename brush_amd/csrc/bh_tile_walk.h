@@ -126,13 +126,13 @@ __device__ __forceinline__ uint32_t bbox_items(const TileBox& bb) {
 //
 // Returns the number of passing tiles of this lane's splat.  With WRITE, the
 // passing items are stored at out_base + (passing items before it in walk
-// order): tile id tx + ty * tile_bw into tile_ids and id_base + owner lane into
-// ids, skipping positions >= out_end.
-template <bool WRITE, int TH = 16>
+// order): tile id tx + ty * tile_bw into tile_ids (as TileT) and id_base +
+// owner lane into ids, skipping positions >= out_end.
+template <bool WRITE, int TH, typename TileT>
 __device__ uint32_t wave_tile_walk(uint32_t lane, uint32_t items, V2 m, const S2& conic, float pt,
                                    const TileBox& bb, WalkRec* rec, uint32_t* owner_slot, uint32_t* ends,
                                    uint32_t tile_bw, uint32_t out_base, uint32_t out_end, uint32_t id_base,
-                                   uint32_t* __restrict__ tile_ids, uint32_t* __restrict__ ids) {
+                                   TileT* __restrict__ tile_ids, uint32_t* __restrict__ ids) {
     const uint32_t incl = wave_incl_add_u32(items);
     const uint32_t start = incl - items;
     const uint32_t total = __builtin_amdgcn_readlane(incl, 63);
@@ -176,7 +176,7 @@ __device__ uint32_t wave_tile_walk(uint32_t lane, uint32_t items, V2 m, const S2
         if (WRITE && pass) {
             const uint32_t pos = out_base + written + below;
             if (pos < out_end) {
-                tile_ids[pos] = tx + __umul24(ty, tile_bw);  // a tile id < 2^21
+                tile_ids[pos] = (TileT)(tx + __umul24(ty, tile_bw));  // a tile id < 2^21
                 ids[pos] = id_base + owner;
             }
         }

@@ -178,7 +178,7 @@ __global__ __launch_bounds__(256, DEG >= 4 ? 4 : 5) void project_forward_kernel(
     float coeffs[3 * NC];
     if (vis) load_sh_row<NC>(sh, gid, coeffs);
     // count_contributing_tiles (project_forward.rs:120-128) for the whole wave
-    const uint32_t hits = wave_tile_walk<false, TH>(lane, vis ? bbox_items(p.bb) : 0u, p.m, p.conic, p.pt, p.bb,
+    const uint32_t hits = wave_tile_walk<false, TH, uint32_t>(lane, vis ? bbox_items(p.bb) : 0u, p.m, p.conic, p.pt, p.bb,
                                                 s_rec[wave], s_slot[wave], s_count[wave], u.tile_bw, 0u, 0u, 0u,
                                                 nullptr, nullptr);
     if (gid < n) {
@@ -366,14 +366,14 @@ void launch_project_visible(bh_ctx* ctx, const float* rows, const uint32_t* gfc,
 // intersections are written only when their count fits the output
 // (dev[7] == dev[2..3], set by project_reduce), so every store stays inside
 // buffers sized for the capacity.
-template <int TH>
+template <int TH, typename TileT>
 __global__ __launch_bounds__(256) void map_intersects_kernel(uint32_t tile_bw, uint32_t tile_bh,
                                                               const float4* __restrict__ rows,
                                                               const uint32_t* __restrict__ gfc, uint32_t num_splats,
                                                               const uint32_t* __restrict__ cum, uint32_t num_visible,
                                                               float* __restrict__ projected,
                                                               float* __restrict__ depths,
-                                                              uint32_t* __restrict__ tile_ids,
+                                                              TileT* __restrict__ tile_ids,
                                                               uint32_t* __restrict__ cgids,
                                                               uint32_t* __restrict__ zero, uint32_t zero_words,
                                                               const uint32_t* __restrict__ dev) {
@@ -420,7 +420,7 @@ __global__ __launch_bounds__(256) void map_intersects_kernel(uint32_t tile_bw, u
     const uint32_t last = min(c0 + 63u, num_visible - 1u);
     const uint32_t out_base = c0 == 0 ? 0u : cum[c0 - 1];
     const uint32_t out_end = cum[last];
-    const uint32_t hits = wave_tile_walk<true, TH>(lane, active ? bbox_items(bb) : 0u, m, conic, pt, bb, s_rec[wave],
+    const uint32_t hits = wave_tile_walk<true, TH, TileT>(lane, active ? bbox_items(bb) : 0u, m, conic, pt, bb, s_rec[wave],
                                                s_slot[wave], s_count[wave], tile_bw, out_base, out_end, c0, tile_ids,
                                                cgids);
     if (__ballot(active && hits != budget) == 0ull) return;
@@ -434,32 +434,34 @@ __global__ __launch_bounds__(256) void map_intersects_kernel(uint32_t tile_bw, u
     for (uint32_t ty = bb.min_y; ty < bb.max_y && k < budget; ty++)
         for (uint32_t tx = bb.min_x; tx < bb.max_x && k < budget; tx++)
             if (will_contribute<TH>(tx, ty, m, conic, pt)) {
-                tile_ids[base + k] = tx + ty * tile_bw;
+                tile_ids[base + k] = (TileT)(tx + ty * tile_bw);
                 cgids[base + k] = c;
                 k++;
             }
     for (; k < budget; k++) {
-        tile_ids[base + k] = tile_bw * tile_bh;
+        tile_ids[base + k] = (TileT)(tile_bw * tile_bh);
         cgids[base + k] = c;
     }
 }
 
 void launch_map_intersects(bh_ctx* ctx, uint32_t tile_bw, uint32_t tile_bh, uint32_t tile_h, const float* rows,
                            const uint32_t* gfc, uint32_t num_splats, const uint32_t* cum, uint32_t num_visible,
-                           float* projected, float* depths, uint32_t* tile_ids, uint32_t* cgids, uint32_t* zero,
-                           uint32_t zero_words, const uint32_t* dev) {
+                           float* projected, float* depths, void* tile_ids, bool tile_ids16, uint32_t* cgids,
+                           uint32_t* zero, uint32_t zero_words, const uint32_t* dev) {
     if (num_visible == 0) return;
     KernelTimer t(ctx, "map_intersects");
     const uint32_t blocks = div_up(num_visible, 256);
     const float4* r4 = reinterpret_cast<const float4*>(rows);
-    if (tile_h == 8)
-        map_intersects_kernel<8><<<blocks, 256, 0, ctx->stream>>>(tile_bw, tile_bh, r4, gfc, num_splats, cum,
-                                                                 num_visible, projected, depths, tile_ids, cgids, zero,
-                                                                 zero_words, dev);
-    else
-        map_intersects_kernel<16><<<blocks, 256, 0, ctx->stream>>>(tile_bw, tile_bh, r4, gfc, num_splats, cum,
-                                                                  num_visible, projected, depths, tile_ids, cgids, zero,
-                                                                  zero_words, dev);
+#define BH_MAP(TH, T)                                                                                            \
+    map_intersects_kernel<TH, T><<<blocks, 256, 0, ctx->stream>>>(tile_bw, tile_bh, r4, gfc, num_splats, cum,     \
+                                                                  num_visible, projected, depths, (T*)tile_ids,  \
+                                                                  cgids, zero, zero_words, dev)
+    if (tile_h == 8) {
+        if (tile_ids16) BH_MAP(8, uint16_t); else BH_MAP(8, uint32_t);
+    } else {
+        if (tile_ids16) BH_MAP(16, uint16_t); else BH_MAP(16, uint32_t);
+    }
+#undef BH_MAP
 }
 
 }  // namespace bh

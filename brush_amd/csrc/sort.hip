@@ -186,10 +186,11 @@ static ScanPlan scan_plan(uint32_t n, const DigitPlan& d) {
 // ---- reduce-then-scan: digit counts of each partition ----------------------------
 
 // One workgroup per partition: the digit counts of its keys (per-wave LDS
-// copies, 16-byte loads for a whole aligned partition) go to its row of
-// `counts` and are added to its block's sums.
-template <bool FIRST, int ITEMS>
-__global__ __launch_bounds__(kThreads) void radix_upsweep_kernel(const uint32_t* __restrict__ keys, uint32_t n,
+// copies, 16-byte loads for a whole aligned partition; 8-byte ones for four
+// 16-bit keys) go to its row of `counts` and are added to its block's sums.
+// K is the stored key type: uint32_t, or uint16_t for keys below 2^16.
+template <bool FIRST, int ITEMS, typename K>
+__global__ __launch_bounds__(kThreads) void radix_upsweep_kernel(const K* __restrict__ keys, uint32_t n,
                                                                   uint32_t shift, uint32_t digit_bits,
                                                                   uint32_t key_sub, uint32_t key_cap, uint32_t radix,
                                                                   uint32_t rows, uint32_t* __restrict__ counts,
@@ -211,25 +212,39 @@ __global__ __launch_bounds__(kThreads) void radix_upsweep_kernel(const uint32_t*
     // the first pass of a dropping sort does not count capped keys
     const bool drop = FIRST && dev.drop_capped;
     if (base + PART <= n && (reinterpret_cast<uintptr_t>(keys) & 15u) == 0u) {
-        const uint4* k4 = reinterpret_cast<const uint4*>(keys + base);
-        uint4 q[ITEMS / 4];
+        // this thread's ITEMS keys as 32-bit words: 16-byte loads (8-byte
+        // ones for four 16-bit keys), interleaved across the threads
+        constexpr int WORDS = ITEMS * (int)sizeof(K) / 4;
+        constexpr int VW = WORDS >= 4 ? 4 : 2;
+        uint32_t w[WORDS];
+        if constexpr (VW == 4) {
+            const uint4* k4 = reinterpret_cast<const uint4*>(keys + base);
 #pragma unroll
-        for (int j = 0; j < ITEMS / 4; j++) q[j] = k4[j * kThreads + tid];
-#pragma unroll
-        for (int j = 0; j < ITEMS / 4; j++) {
-            const uint32_t kk[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const uint32_t k = FIRST ? min(kk[e] - key_sub, key_cap) : kk[e];
-                if (!(drop && k == key_cap)) atomicAdd(&mine[(k >> shift) & dmask], 1u);
+            for (int j = 0; j < WORDS / 4; j++) {
+                const uint4 q = k4[j * kThreads + tid];
+                w[4 * j] = q.x, w[4 * j + 1] = q.y, w[4 * j + 2] = q.z, w[4 * j + 3] = q.w;
             }
+        } else {
+            const uint2* k2 = reinterpret_cast<const uint2*>(keys + base);
+#pragma unroll
+            for (int j = 0; j < WORDS / 2; j++) {
+                const uint2 q = k2[j * kThreads + tid];
+                w[2 * j] = q.x, w[2 * j + 1] = q.y;
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < ITEMS; e++) {
+            const uint32_t kw = sizeof(K) == 4 ? w[e] : (w[e / 2] >> (16 * (e & 1))) & 0xFFFFu;
+            const uint32_t k = FIRST ? min(kw - key_sub, key_cap) : kw;
+            if (!(drop && k == key_cap)) atomicAdd(&mine[(k >> shift) & dmask], 1u);
         }
     } else {
 #pragma unroll
         for (int j = 0; j < ITEMS; j++) {
             const uint64_t idx = base + (uint64_t)j * kThreads + tid;
             if (idx < n) {
-                const uint32_t k = FIRST ? min(keys[idx] - key_sub, key_cap) : keys[idx];
+                const uint32_t kw = keys[idx];
+                const uint32_t k = FIRST ? min(kw - key_sub, key_cap) : kw;
                 if (!(drop && k == key_cap)) atomicAdd(&mine[(k >> shift) & dmask], 1u);
             }
         }
@@ -338,10 +353,10 @@ __device__ __forceinline__ uint32_t xcd_partition(uint32_t b, uint32_t g) {
 // each output value v also writes gather_out[g] = gather_src[v]: the gather
 // loads are issued with the pair loads (their latency hides behind the
 // ranking) and go out through LDS like the values.
-template <bool FIRST, int ITEMS, bool GATHER>
-__global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __restrict__ keys_in,
+template <bool FIRST, int ITEMS, bool GATHER, typename KI, typename KO>
+__global__ __launch_bounds__(kThreads) void onesweep_kernel(const KI* __restrict__ keys_in,
                                                              const uint32_t* __restrict__ vals_in,
-                                                             uint32_t* __restrict__ keys_out,
+                                                             KO* __restrict__ keys_out,
                                                              uint32_t* __restrict__ vals_out, uint32_t n,
                                                              uint32_t shift, uint32_t digit_bits, uint32_t key_sub,
                                                              uint32_t key_cap, uint32_t radix,
@@ -448,7 +463,7 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
             const uint32_t dd = (key >> shift) & dmask;
             const uint32_t g = s_global_off[dd] + (i - s_local_start[dd]);
             if (g < n) {  // always true: the offsets partition [0, n)
-                keys_out[g] = key;
+                keys_out[g] = (KO)key;
                 dst[j] = g;
             }
         }
@@ -491,34 +506,81 @@ size_t radix_sort_zeroed_words(uint32_t n, uint32_t key_bits) {
     return (size_t)plan.passes * sp.blocks * sp.radix;
 }
 
-template <bool FIRST, int ITEMS>
-static void launch_digit_pass(bh_ctx* ctx, uint32_t parts, const uint32_t* src_k, const uint32_t* src_v,
-                              uint32_t* dk, uint32_t* dv, uint32_t n, uint32_t sh, uint32_t bits, uint32_t sub,
-                              uint32_t cap, uint32_t radix, const uint32_t* offs, const uint32_t* gs, uint32_t* go,
+template <bool FIRST, int ITEMS, typename KI, typename KO>
+static void launch_digit_pass(bh_ctx* ctx, uint32_t parts, const KI* src_k, const uint32_t* src_v, KO* dk,
+                              uint32_t* dv, uint32_t n, uint32_t sh, uint32_t bits, uint32_t sub, uint32_t cap,
+                              uint32_t radix, const uint32_t* offs, const uint32_t* gs, uint32_t* go,
                               const SortDevice& dev) {
-    if (go)
-        onesweep_kernel<FIRST, ITEMS, true><<<parts, kThreads, 0, ctx->stream>>>(src_k, src_v, dk, dv, n, sh, bits, sub,
-                                                                              cap, radix, offs, gs, go, dev);
-    else
-        onesweep_kernel<FIRST, ITEMS, false><<<parts, kThreads, 0, ctx->stream>>>(src_k, src_v, dk, dv, n, sh, bits,
-                                                                               sub, cap, radix, offs, gs, go, dev);
+    if constexpr (sizeof(KI) == 4 && sizeof(KO) == 4) {
+        if (go) {
+            onesweep_kernel<FIRST, ITEMS, true, KI, KO><<<parts, kThreads, 0, ctx->stream>>>(
+                src_k, src_v, dk, dv, n, sh, bits, sub, cap, radix, offs, gs, go, dev);
+            return;
+        }
+    }
+    onesweep_kernel<FIRST, ITEMS, false, KI, KO><<<parts, kThreads, 0, ctx->stream>>>(
+        src_k, src_v, dk, dv, n, sh, bits, sub, cap, radix, offs, nullptr, nullptr, dev);
 }
 
-bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t* vals_in, uint32_t n,
-                           uint32_t key_bits, uint32_t key_sub, uint32_t key_cap, uint32_t* keys_out,
-                           uint32_t* vals_out, uint32_t* tmp_keys, uint32_t* tmp_vals, void* scratch,
-                           const char* tag, bool scratch_zeroed, const uint32_t* gather_src,
-                           uint32_t* gather_out, const SortDevice& dev) {
+// One digit pass: upsweep, offset scan, scatter.  Keys are read as uint16_t
+// or uint32_t (in_w bytes) and written as out_w bytes; 16-bit keys carry at
+// most 16 key bits.
+template <bool FIRST, int I>
+static bh_status sort_pass(bh_ctx* ctx, const ScanPlan& sp, const std::string& up_name,
+                           const std::string& scan_name, const std::string& pass_name, const void* src_k,
+                           int in_w, const uint32_t* src_v, void* dk, int out_w, uint32_t* dv, uint32_t n,
+                           uint32_t sh, uint32_t bits, uint32_t sub, uint32_t cap, uint32_t* offs, uint32_t* pblk,
+                           const uint32_t* gs, uint32_t* go, const SortDevice& pdev) {
+    const dim3 grid(sp.parts), block(kThreads);
+    {
+        KernelTimer t(ctx, up_name.c_str());
+        if (in_w == 2)
+            radix_upsweep_kernel<FIRST, I, uint16_t><<<grid, block, 0, ctx->stream>>>(
+                (const uint16_t*)src_k, n, sh, bits, sub, cap, sp.radix, sp.rows, offs, pblk, pdev);
+        else
+            radix_upsweep_kernel<FIRST, I, uint32_t><<<grid, block, 0, ctx->stream>>>(
+                (const uint32_t*)src_k, n, sh, bits, sub, cap, sp.radix, sp.rows, offs, pblk, pdev);
+    }
+    {
+        KernelTimer t(ctx, scan_name.c_str());
+        radix_scan_kernel<<<sp.blocks, kScanThreads, 0, ctx->stream>>>(offs, pblk, sp.parts, sp.rows, sp.blocks,
+                                                                       sp.radix);
+    }
+    KernelTimer t(ctx, pass_name.c_str());
+    if (in_w == 4 && out_w == 4)
+        launch_digit_pass<FIRST, I, uint32_t, uint32_t>(ctx, sp.parts, (const uint32_t*)src_k, src_v, (uint32_t*)dk,
+                                                        dv, n, sh, bits, sub, cap, sp.radix, offs, gs, go, pdev);
+    else if (in_w == 2 && out_w == 2 && !go)
+        launch_digit_pass<FIRST, I, uint16_t, uint16_t>(ctx, sp.parts, (const uint16_t*)src_k, src_v, (uint16_t*)dk,
+                                                        dv, n, sh, bits, sub, cap, sp.radix, offs, gs, go, pdev);
+    else if (in_w == 2 && out_w == 4 && !go)
+        launch_digit_pass<FIRST, I, uint16_t, uint32_t>(ctx, sp.parts, (const uint16_t*)src_k, src_v, (uint32_t*)dk,
+                                                        dv, n, sh, bits, sub, cap, sp.radix, offs, gs, go, pdev);
+    else
+        return set_error(ctx, BH_ERR_INVALID_ARG, "radix sort: unsupported key widths");
+    return BH_OK;
+}
+
+// The sort over keys stored as in_w / tmp_w / out_w bytes (keys_in, the
+// temporaries and keys_out).
+static bh_status radix_sort_impl(bh_ctx* ctx, const void* keys_in, int in_w, const uint32_t* vals_in, uint32_t n,
+                                 uint32_t key_bits, uint32_t key_sub, uint32_t key_cap, void* keys_out, int out_w,
+                                 uint32_t* vals_out, void* tmp_keys, int tmp_w, uint32_t* tmp_vals, void* scratch,
+                                 const char* tag, bool scratch_zeroed, const uint32_t* gather_src,
+                                 uint32_t* gather_out, const SortDevice& dev) {
     const std::string up_name = std::string(tag) + "_up", scan_name = std::string(tag) + "_scan",
                       pass_name = std::string(tag) + "_onesweep";
     if (n == 0) return BH_OK;
     if (key_bits > 32) return set_error(ctx, BH_ERR_INVALID_ARG, "radix sort: more than 32 key bits");
+    if (std::min(std::min(in_w, out_w), tmp_w) < 4 && (key_bits > 16 || key_sub != 0u))
+        return set_error(ctx, BH_ERR_INVALID_ARG, "radix sort: 16-bit keys carry at most 16 key bits");
     const DigitPlan plan = digit_plan(key_bits);
     const ScanPlan sp = scan_plan(n, plan);
     uint32_t* blk = (uint32_t*)scratch;
     uint32_t* offs = blk + (size_t)plan.passes * sp.blocks * sp.radix;
     if (!scratch_zeroed) launch_fill_u32(ctx, blk, 0u, radix_sort_zeroed_words(n, key_bits));
-    const uint32_t* src_k = keys_in;
+    const void* src_k = keys_in;
+    int src_w = in_w;
     const uint32_t* src_v = vals_in;
     // a dropping sort: the first pass sees n pairs, the later ones n_rest
     SortDevice dev_rest = dev;
@@ -530,7 +592,8 @@ bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t*
         n = p == 0 ? n_first : n_later;
         // the last pass lands in the output buffers
         bool to_out = ((plan.passes - 1 - p) % 2) == 0;
-        uint32_t* dk = to_out ? keys_out : tmp_keys;
+        void* dk = to_out ? keys_out : tmp_keys;
+        const int dst_w = to_out ? out_w : tmp_w;
         uint32_t* dv = to_out ? vals_out : tmp_vals;
         uint32_t* pblk = blk + (size_t)p * sp.blocks * sp.radix;
         const uint32_t sh = plan.shift(p), bits = plan.bits(p);
@@ -538,44 +601,40 @@ bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t*
         const bool last = p + 1 == plan.passes;
         const uint32_t* gs = last ? gather_src : nullptr;
         uint32_t* go = last ? gather_out : nullptr;
-        const dim3 grid(sp.parts), block(kThreads);
-#define BH_SORT_PASS(I)                                                                                          \
-    do {                                                                                                        \
-        {                                                                                                       \
-            KernelTimer t(ctx, up_name.c_str());                                                                \
-            if (p == 0)                                                                                         \
-                radix_upsweep_kernel<true, I><<<grid, block, 0, ctx->stream>>>(src_k, n, sh, bits, sub, cap,   \
-                                                                               sp.radix, sp.rows, offs, pblk,  \
-                                                                               pdev);                          \
-            else                                                                                                \
-                radix_upsweep_kernel<false, I><<<grid, block, 0, ctx->stream>>>(src_k, n, sh, bits, sub, cap,  \
-                                                                                sp.radix, sp.rows, offs, pblk, \
-                                                                                pdev);                         \
-        }                                                                                                       \
-        {                                                                                                       \
-            KernelTimer t(ctx, scan_name.c_str());                                                              \
-            radix_scan_kernel<<<sp.blocks, kScanThreads, 0, ctx->stream>>>(offs, pblk, sp.parts, sp.rows,       \
-                                                                           sp.blocks, sp.radix);               \
-        }                                                                                                       \
-        {                                                                                                       \
-            KernelTimer t(ctx, pass_name.c_str());                                                              \
-            if (p == 0)                                                                                         \
-                launch_digit_pass<true, I>(ctx, sp.parts, src_k, src_v, dk, dv, n, sh, bits, sub, cap, sp.radix,  \
-                                           offs, gs, go, pdev);                                                 \
-            else                                                                                                \
-                launch_digit_pass<false, I>(ctx, sp.parts, src_k, src_v, dk, dv, n, sh, bits, sub, cap,          \
-                                            sp.radix, offs, gs, go, pdev);                                      \
-        }                                                                                                       \
+#define BH_SORT_PASS(F, I)                                                                                   \
+    do {                                                                                                         \
+        const bh_status st_ = sort_pass<F, I>(ctx, sp, up_name, scan_name, pass_name, src_k, src_w, src_v, dk,   \
+                                              dst_w, dv, n, sh, bits, sub, cap, offs, pblk, gs, go, pdev);      \
+        if (st_ != BH_OK) return st_;                                                                            \
     } while (0)
-        if (sp.items == 8)
-            BH_SORT_PASS(8);
-        else
-            BH_SORT_PASS(4);
+        if (sp.items == 8) {
+            if (p == 0) BH_SORT_PASS(true, 8); else BH_SORT_PASS(false, 8);
+        } else {
+            if (p == 0) BH_SORT_PASS(true, 4); else BH_SORT_PASS(false, 4);
+        }
 #undef BH_SORT_PASS
         src_k = dk;
+        src_w = dst_w;
         src_v = dv;
     }
     return check_launch(ctx, "radix sort");
+}
+
+bh_status radix_sort_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t* vals_in, uint32_t n,
+                           uint32_t key_bits, uint32_t key_sub, uint32_t key_cap, uint32_t* keys_out,
+                           uint32_t* vals_out, uint32_t* tmp_keys, uint32_t* tmp_vals, void* scratch,
+                           const char* tag, bool scratch_zeroed, const uint32_t* gather_src,
+                           uint32_t* gather_out, const SortDevice& dev) {
+    return radix_sort_impl(ctx, keys_in, 4, vals_in, n, key_bits, key_sub, key_cap, keys_out, 4, vals_out, tmp_keys,
+                           4, tmp_vals, scratch, tag, scratch_zeroed, gather_src, gather_out, dev);
+}
+
+bh_status radix_sort_pairs_k16(bh_ctx* ctx, const uint16_t* keys_in, const uint32_t* vals_in, uint32_t n,
+                               uint32_t key_bits, uint32_t* keys_out, uint32_t* vals_out, uint16_t* tmp_keys,
+                               uint32_t* tmp_vals, void* scratch, const char* tag, bool scratch_zeroed,
+                               const SortDevice& dev) {
+    return radix_sort_impl(ctx, keys_in, 2, vals_in, n, key_bits, 0u, 0xFFFFFFFFu, keys_out, 4, vals_out, tmp_keys,
+                           2, tmp_vals, scratch, tag, scratch_zeroed, nullptr, nullptr, dev);
 }
 
 __global__ void mask_u32_kernel(const uint32_t* __restrict__ in, uint32_t mask, uint32_t n,
