@@ -103,8 +103,9 @@ def algorithmic_bytes(name: str, n: int, v: int, m: int, m_post: int, t: int, p:
     if name == "scan":
         return 12.0 * v                                  # gid + gathered count in, cum out
     if name == "map_intersects":
-        # gid + global-id row slot (48 B) + cum in; ordered row + depth out; (tile, id) pairs out
-        return (4.0 + 48.0 + 8.0) * v + 44.0 * v + 8.0 * m
+        # gid + global-id row slot (48 B) + cum in; ordered row + depth out; (tile, id) pairs out,
+        # the tile ids 16-bit below 2^16 tiles
+        return (4.0 + 48.0 + 8.0) * v + 44.0 * v + (6.0 if t < 65536 else 8.0) * m
     if name == "tile_offsets":
         return 4.0 * m + 8.0 * t
     if name == "rasterize":
@@ -128,19 +129,25 @@ def algorithmic_bytes(name: str, n: int, v: int, m: int, m_post: int, t: int, p:
     return 0.0
 
 
-def sort_bytes_per_launch(name: str, passes: float, n: int, m: int) -> float:
+def sort_bytes_per_launch(name: str, passes: float, n: int, m: int, t: int) -> float:
     """Algorithmic bytes of one launch of a sort kernel: every digit pass reads
-    and writes (u32 key, u32 value) once; the depth sort's first pass generates
+    and writes (key, u32 value) once; the depth sort's first pass generates
     its values (global ids) instead of reading them; each pass's upsweep reads
-    the keys (the offset scan's few counters are not counted)."""
+    the keys (the offset scan's few counters are not counted).  Below 2^16
+    tiles the tile sort's keys are 16-bit until its last pass writes the
+    32-bit sorted ids."""
+    k16 = t < 65536
     if name == "depth_sort_up":
         return 4.0 * n
     if name == "tile_sort_up":
-        return 4.0 * m
+        return (2.0 if k16 else 4.0) * m
     if name == "depth_sort_onesweep":
         return (16.0 * passes - 4.0) * n / max(passes, 1.0)
     if name == "tile_sort_onesweep":
-        return 16.0 * m
+        if not k16:
+            return 16.0 * m
+        # 12 B per pair in the earlier passes, 14 B in the last
+        return (12.0 * passes + 2.0) * m / max(passes, 1.0)
     return 0.0
 
 
@@ -477,7 +484,7 @@ def main():
             per_step_launches = launches / steps
             avg = total / max(launches, 1)
             if name.endswith(("_onesweep", "_up", "_scan")):
-                b = sort_bytes_per_launch(name, per_step_launches / poses, n, m)
+                b = sort_bytes_per_launch(name, per_step_launches / poses, n, m, tiles)
             else:
                 b = algorithmic_bytes(name, n, v, m, m_post, tiles, pixels, c, contributing)
             table[name] = {"launches_per_step": round(per_step_launches, 2), "avg_ms": round(avg, 4),
