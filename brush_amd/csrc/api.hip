@@ -599,7 +599,17 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
         };
         launch_fill_multi(ctx, zero, (int)(sizeof(zero) / sizeof(zero[0])));
     };
-    zero_outputs(true);
+    // with splats, project_forward zeroes these beside its own work (its
+    // reduction writes the counters, flags word included)
+    ZeroRanges pf_zero{};
+    if (num_splats) {
+        pf_zero.p[0] = (uint32_t*)visible, pf_zero.count[0] = bwd ? (uint64_t)num_splats : 0u;
+        pf_zero.p[1] = (uint32_t*)depth_scr, pf_zero.count[1] = radix_sort_zeroed_words(num_splats, 32);
+        pf_zero.p[2] = off_pre, pf_zero.count[2] = (uint64_t)num_tiles * 2;
+        pf_zero.p[3] = tile_offsets, pf_zero.count[3] = bwd ? (uint64_t)num_tiles * 2 : 0u;
+    } else {
+        zero_outputs(true);
+    }
 
     uint32_t num_visible = 0, kmin = 0, kmax = 0;
     uint64_t num_isect = 0;
@@ -621,7 +631,7 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
         BH_STRY(ws.get(&vis_rows, (size_t)num_splats * 12));
         launch_project_forward(ctx, u, transforms, raw_opacities, sh_coeffs, sh_degree, num_splats, mip, tile_h, counts,
                                max_radius, depth_keys, vis_rows, partials, ctx->d_counters,
-                               planned ? ctx->plan_isect_cap : 0u);
+                               planned ? ctx->plan_isect_cap : 0u, pf_zero);
         BH_STRY(check_launch(ctx, "project_forward"));
         BH_STRY(hip_check(ctx, hipMemcpyAsync(ctx->h_counters, ctx->d_counters, 32, hipMemcpyDeviceToHost, ctx->stream),
                           "count readback"));

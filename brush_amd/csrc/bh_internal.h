@@ -126,6 +126,12 @@ struct FillRange {
 };
 constexpr int kMaxFillRanges = 8;
 void launch_fill_multi(bh_ctx* ctx, const FillRange* ranges, int k);
+// Ranges a kernel zeroes beside its own work (a grid-stride loop per range;
+// unused ranges have count 0), in place of a fill launch of their own.
+struct ZeroRanges {
+    uint32_t* p[4];
+    uint64_t count[4];
+};
 // Debug validation: first[j] (u64, ~0 when none) = the index of the first NaN
 // or infinity in float array j; first holds kMaxFiniteArrays entries.
 constexpr int kMaxFiniteArrays = 4;
@@ -195,7 +201,8 @@ size_t project_partials_bytes(uint32_t n);
 void launch_project_forward(bh_ctx* ctx, const bh_project_uniforms& u, const float* transforms,
                             const float* raw_opac, const float* sh, uint32_t sh_degree, uint32_t n, bool mip,
                             uint32_t tile_h, uint32_t* intersect_counts, float* max_radius, uint32_t* depth_keys,
-                            float* rows, uint32_t* partials, uint32_t* counters, uint32_t isect_cap = 0);
+                            float* rows, uint32_t* partials, uint32_t* counters, uint32_t isect_cap = 0,
+                            const ZeroRanges& zero = ZeroRanges{});
 void launch_project_visible(bh_ctx* ctx, const float* rows, const uint32_t* gfc, uint32_t num_visible,
                             uint32_t num_splats, float* projected, float* depths);
 // Also writes compact rows `projected` [V,10] and `depths` [V] from the

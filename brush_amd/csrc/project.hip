@@ -142,7 +142,7 @@ __global__ __launch_bounds__(256, DEG >= 4 ? 4 : 5) void project_forward_kernel(
                                                                float* __restrict__ max_radius,
                                                                uint32_t* __restrict__ depth_keys,
                                                                float4* __restrict__ rows,
-                                                               uint32_t* __restrict__ partials) {
+                                                               uint32_t* __restrict__ partials, ZeroRanges zero) {
     __shared__ uint32_t s_vis[4], s_kmin[4], s_kmax[4];
     __shared__ unsigned long long s_hits[4];
     __shared__ WalkRec s_rec[4][64];
@@ -215,6 +215,11 @@ __global__ __launch_bounds__(256, DEG >= 4 ? 4 : 5) void project_forward_kernel(
         out[3] = mn;
         out[4] = mx;
     }
+    // the forward's zero-fills (visible mask, sort scratch, tile offsets),
+    // last, when the splat's registers are free
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        for (uint64_t i = gid; i < zero.count[j]; i += (uint64_t)gridDim.x * 256u) zero.p[j][i] = 0u;
 }
 
 // Folds the per-block totals of project_forward into the context counters
@@ -256,6 +261,7 @@ __global__ __launch_bounds__(1024) void project_reduce_kernel(const uint32_t* __
             mx = max(mx, s_mx[w]);
         }
         counters[0] = v;
+        counters[1] = 0u;  // no device error
         counters[2] = (uint32_t)h;
         counters[3] = (uint32_t)(h >> 32);
         counters[4] = mn;
@@ -270,11 +276,12 @@ size_t project_partials_bytes(uint32_t n) { return (size_t)div_up(n, 256) * 8 * 
 template <bool MIP, int TH, int DEG>
 static void launch_pf(bh_ctx* ctx, uint32_t blocks, const bh_project_uniforms& u, const float* transforms,
                       const float* raw_opac, const float* sh, uint32_t n, uint32_t* intersect_counts,
-                      float* max_radius, uint32_t* depth_keys, float4* rows, uint32_t* partials) {
+                      float* max_radius, uint32_t* depth_keys, float4* rows, uint32_t* partials,
+                      const ZeroRanges& zero) {
 #define BH_PF(C)                                                                                             \
     project_forward_kernel<MIP, C, TH, DEG><<<blocks, 256, 0, ctx->stream>>>(u, transforms, raw_opac, sh, n, \
                                                                              intersect_counts, max_radius,   \
-                                                                             depth_keys, rows, partials)
+                                                                             depth_keys, rows, partials, zero)
     switch (u.camera_model) {
         case kCamKB4: BH_PF(kCamKB4); break;
         case kCamRT8: BH_PF(kCamRT8); break;
@@ -288,10 +295,10 @@ template <int DEG>
 static void launch_pf_deg(bh_ctx* ctx, uint32_t blocks, const bh_project_uniforms& u, const float* transforms,
                           const float* raw_opac, const float* sh, uint32_t n, bool mip, uint32_t tile_h,
                           uint32_t* intersect_counts, float* max_radius, uint32_t* depth_keys, float4* rows,
-                          uint32_t* partials) {
+                          uint32_t* partials, const ZeroRanges& zero) {
 #define BH_PFM(M, T)                                                                                               \
     launch_pf<M, T, DEG>(ctx, blocks, u, transforms, raw_opac, sh, n, intersect_counts, max_radius, depth_keys, rows, \
-                         partials)
+                         partials, zero)
     if (tile_h == 8) {
         if (mip) BH_PFM(true, 8); else BH_PFM(false, 8);
     } else {
@@ -303,7 +310,8 @@ static void launch_pf_deg(bh_ctx* ctx, uint32_t blocks, const bh_project_uniform
 void launch_project_forward(bh_ctx* ctx, const bh_project_uniforms& u, const float* transforms,
                             const float* raw_opac, const float* sh, uint32_t sh_degree, uint32_t n, bool mip,
                             uint32_t tile_h, uint32_t* intersect_counts, float* max_radius, uint32_t* depth_keys,
-                            float* rows, uint32_t* partials, uint32_t* counters, uint32_t isect_cap) {
+                            float* rows, uint32_t* partials, uint32_t* counters, uint32_t isect_cap,
+                            const ZeroRanges& zero) {
     if (n == 0) return;
     uint32_t blocks = div_up(n, 256);
     {
@@ -311,7 +319,7 @@ void launch_project_forward(bh_ctx* ctx, const bh_project_uniforms& u, const flo
         float4* r4 = reinterpret_cast<float4*>(rows);
 #define BH_PFD(D) \
     launch_pf_deg<D>(ctx, blocks, u, transforms, raw_opac, sh, n, mip, tile_h, intersect_counts, max_radius, depth_keys, \
-                     r4, partials)
+                     r4, partials, zero)
         switch (sh_degree) {
             case 0: BH_PFD(0); break;
             case 1: BH_PFD(1); break;
