@@ -347,14 +347,14 @@ def test_render_backward_rejects_flags_of_another_forward(gpu, fwd_flags, bwd_fl
     out.state.release()
 
 
-@pytest.mark.parametrize("tile16x8", [False, True])
-def test_more_than_16384_tiles(gpu, tile16x8):
+@pytest.mark.parametrize("w,h,tile16x8", [(3840, 2160, False), (2048, 1080, True), (4096, 2160, True)])
+def test_more_than_16384_tiles(gpu, w, h, tile16x8):
     """Frames with more tiles than the tile-order kernel keeps in registers
-    (16 x 1024): 3840x2160 with 16x16 tiles (32400 tiles) and 2048x1080 with
-    16x8 tiles (17280 tiles).  Forward bit for bit, every tile's offsets
-    before and after the blend, and the fused backward to rtol 1e-3, against
-    the CPU restatement."""
-    w, h = (2048, 1080) if tile16x8 else (3840, 2160)
+    (16 x 1024): 3840x2160 with 16x16 tiles (32400 tiles), 2048x1080 with
+    16x8 tiles (17280 tiles), and 4096x2160 with 16x8 tiles (69120 tiles:
+    from 2^16 tiles the tile sort's keys are 32-bit throughout).  Forward bit
+    for bit, every tile's offsets before and after the blend, and the fused
+    backward to rtol 1e-3, against the CPU restatement."""
     print(f"[case] {w}x{h} tiles 16x{8 if tile16x8 else 16}", flush=True)
     tr, sh, opac = random_scene(57, 20_000, 1, mean_range=1.2, log_scale=(-3.5, 0.6))
     cam = Camera.from_focal((0.0, 0.0, -3.0), (0.0, 0.0, 0.0, 1.0), 0.45 * w, w, h)
