@@ -22,6 +22,11 @@ struct bh_fwd_state {
     // the blend's record of contributing pairs (forward with BWD_INFO and
     // intersections), read by bh_render_backward
     bh::SplatRecord record;
+    // gradient rows [N, 11] the forward zeroed for the backward (beside its
+    // tile-order launch, which leaves the rest of the GPU idle); the first
+    // backward takes them, a later one zeroes its own
+    float* bwd_rows = nullptr;
+    mutable bool bwd_rows_clean = false;
 };
 
 namespace bh {
@@ -722,6 +727,11 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
             BH_TRY(ws.get(&order, num_tiles));
             launch_tile_order(ctx, off_pre, num_tiles, order);
         }
+        // with BWD_INFO and intersections, the blend's last workgroups zero
+        // the backward's gradient rows in the blend's tail
+        st->bwd_rows = nullptr;
+        st->bwd_rows_clean = false;
+        if (bwd && p.m) BH_TRY(sget((void**)&st->bwd_rows, (size_t)num_splats * 11 * 4));
         rec = SplatRecord{};
         if (bwd) {
             // which pairs the blend used, for the fused backward.  Every BWD_INFO
@@ -732,7 +742,9 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
             BH_TRY(sget((void**)&rec.block_end, (size_t)num_tiles * bpt * 4));
         }
         launch_rasterize(ctx, u.img_w, u.img_h, u.tile_bw, u.tile_bh, background, p.v, projected, cgids, gfc, off_pre,
-                         order, flags, out_img, visible, tile_offsets, true, rec);
+                         order, flags, out_img, visible, tile_offsets, true, rec, (uint32_t*)st->bwd_rows,
+                         st->bwd_rows ? (uint64_t)num_splats * 11 : 0u);
+        st->bwd_rows_clean = st->bwd_rows != nullptr;
         return check_launch(ctx, "rasterize");
     };
     auto exact_plan = [&]() {
@@ -876,21 +888,30 @@ bh_status bh_render_backward(bh_ctx* ctx, const bh_fwd_state* state, const float
     // them in order (no inverse permutation, no gathered rows)
     Scratch ws(ctx);
     float* rows;
-    BH_TRY(ws.get(&rows, (size_t)n * 11));
+    const bool pre_zeroed = state->bwd_rows && state->bwd_rows_clean;
+    if (pre_zeroed) {
+        rows = state->bwd_rows;
+        state->bwd_rows_clean = false;
+    } else {
+        BH_TRY(ws.get(&rows, (size_t)n * 11));
+    }
     const uint32_t raster_flags = (in.flags & (fwd_owned | BH_FLAG_TILE_16X8)) | (flags & BH_FLAG_REFINE_WEIGHT);
     if (in.num_visible && in.num_intersections && state->record.masks) {
         // the longest tiles (most splats the forward blended) start first;
         // the order is computed while the gradient rows are zeroed
         uint32_t* order;
         BH_TRY(ws.get(&order, in.num_tiles));
-        launch_zero_and_tile_order(ctx, (uint32_t*)rows, (uint64_t)n * 11, tile_offsets, in.num_tiles, order);
+        if (pre_zeroed)
+            launch_tile_order(ctx, tile_offsets, in.num_tiles, order);
+        else
+            launch_zero_and_tile_order(ctx, (uint32_t*)rows, (uint64_t)n * 11, tile_offsets, in.num_tiles, order);
         launch_rasterize_backward_recorded(ctx, in.img_w, in.img_h, in.tile_bw, in.tile_bh, background, in.num_visible,
                                            out_img, in.projected, in.compact_gid_from_isect, in.tile_offsets_pre,
                                            state->record, v_output, raster_flags, in.global_from_compact_gid, order,
                                            rows);
     } else {
         // no intersections: no pixel blended a splat, every gradient is zero
-        launch_fill_u32(ctx, (uint32_t*)rows, 0u, (uint64_t)n * 11);
+        if (!pre_zeroed) launch_fill_u32(ctx, (uint32_t*)rows, 0u, (uint64_t)n * 11);
     }
     BH_TRY(check_launch(ctx, "rasterize_backward"));
     launch_project_backward(ctx, in.uniforms, transforms, sh_coeffs, raw_opacities, nullptr, n, in.sh_degree,

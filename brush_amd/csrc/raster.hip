@@ -218,6 +218,8 @@ void launch_zero_and_tile_order(bh_ctx* ctx, uint32_t* p, uint64_t words, const 
     zero_and_tile_order_kernel<<<fill_blocks + 1u, 1024, 0, ctx->stream>>>(p, words, offsets, num_tiles, order);
 }
 
+constexpr uint32_t kFillQuadsPerLane = 16;
+
 template <bool BWD_INFO, bool SMOOTH, bool DEPTH, int TH>
 __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t img_h, uint32_t tile_bw,
                                                         uint32_t num_tiles, float bg_r, float bg_g, float bg_b,
@@ -227,12 +229,28 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
                                                         const uint32_t* __restrict__ off_pre,
                                                         const uint32_t* __restrict__ order,
                                                         void* __restrict__ out_img, float* __restrict__ visible,
-                                                        uint32_t* __restrict__ off_post, SplatRecord rec) {
+                                                        uint32_t* __restrict__ off_post, SplatRecord rec,
+                                                        uint32_t* __restrict__ fill, uint64_t fill_words,
+                                                        uint32_t blend_groups) {
     // the conic scaled for the power in base 2 (bh_conic_log2: a, b, c)
     __shared__ float4 s_xyco[64];  // x, y, a, b
     __shared__ float4 s_c11a[64];  // c, opacity, cutoff on the power in base 2
     __shared__ float4 s_rgbd[64];  // r, g, b (staged_colour), depth
 
+    if (BWD_INFO && blockIdx.x >= blend_groups) {
+        // the backward's gradient rows: 16 KB per trailing workgroup, which
+        // the dispatcher starts as the blend's blocks drain
+        const uint64_t q0 = (uint64_t)(blockIdx.x - blend_groups) * (64u * kFillQuadsPerLane);
+        uint4* q = reinterpret_cast<uint4*>(fill);
+        const uint64_t quads = fill_words / 4u;
+#pragma unroll
+        for (uint32_t k = 0; k < kFillQuadsPerLane; k++) {
+            const uint64_t i = q0 + k * 64u + threadIdx.x;
+            if (i < quads) q[i] = make_uint4(0u, 0u, 0u, 0u);
+        }
+        if (q0 == 0u && threadIdx.x < fill_words % 4u) fill[quads * 4u + threadIdx.x] = 0u;
+        return;
+    }
     uint32_t tile, blk;
     raster_block_of_workgroup<TH>(blockIdx.x, tile, blk);
     if (tile >= num_tiles) return;
@@ -438,7 +456,8 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
 void launch_rasterize(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,
                       const float* bg, uint32_t num_visible, const float* projected, const uint32_t* cgids, const uint32_t* gfc,
                       const uint32_t* off_pre, const uint32_t* order, uint32_t flags, void* out_img, float* visible,
-                      uint32_t* off_post, bool off_post_zeroed, SplatRecord rec) {
+                      uint32_t* off_post, bool off_post_zeroed, SplatRecord rec, uint32_t* fill,
+                      uint64_t fill_words) {
     const uint32_t num_tiles = tile_bw * tile_bh;
     if (num_tiles == 0) return;
     const bool bwd = (flags & BH_FLAG_BWD_INFO) != 0;
@@ -452,11 +471,14 @@ void launch_rasterize(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile
     const bool fine = (flags & BH_FLAG_TILE_16X8) != 0;
     // 8 tiles per group of workgroup ids, 4 (16x16) or 2 (16x8) blocks per tile
     const uint32_t groups = div_up(num_tiles, 8) * (fine ? 16u : 32u);
+    // trailing zero-fill workgroups (BWD_INFO only)
+    if (!bwd || !fill) fill_words = 0;
+    const uint32_t fill_groups = (uint32_t)div_up(div_up(fill_words, 4u), 64u * kFillQuadsPerLane);
     KernelTimer t(ctx, "rasterize");
 #define BH_RASTER_T(B, S, D, T)                                                                                    \
-    rasterize_kernel<B, S, D, T><<<groups, 64, 0, ctx->stream>>>(img_w, img_h, tile_bw, num_tiles, bg[0], bg[1], \
-                                                                 bg[2], nv, projected, cgids, gfc, off_pre, order, \
-                                                                 out_img, visible, off_post, rec)
+    rasterize_kernel<B, S, D, T><<<groups + fill_groups, 64, 0, ctx->stream>>>(                                  \
+        img_w, img_h, tile_bw, num_tiles, bg[0], bg[1], bg[2], nv, projected, cgids, gfc, off_pre, order, out_img,    \
+        visible, off_post, rec, fill, fill_words, groups)
 #define BH_RASTER(B, S, D) \
     do {                   \
         if (fine)          \
