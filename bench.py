@@ -109,7 +109,9 @@ def algorithmic_bytes(name: str, n: int, v: int, m: int, m_post: int, t: int, p:
     if name == "tile_offsets":
         return 4.0 * m + 8.0 * t
     if name == "rasterize":
-        return 44.0 * m_post + 16.0 * p + 4.0 * v + 16.0 * t  # id+row per used isect, image, visible, offsets
+        # id+row per used isect, image, visible, offsets; its trailing workgroups zero the
+        # backward's [N, 11] gradient rows (a forward with the backward's record)
+        return 44.0 * m_post + 16.0 * p + 4.0 * v + 16.0 * t + 44.0 * n
     if name == "rasterize_backward":
         return 44.0 * m_post + 32.0 * p + 40.0 * m_post  # id+row, image+grad image, atomics per isect
     if name == "project_backward":
