@@ -380,3 +380,32 @@ def test_more_than_16384_tiles(gpu, w, h, tile16x8):
     grad_close("v_transforms", t.grad.cpu().numpy(), vt, mt)
     grad_close("v_coeffs", s.grad.cpu().numpy(), vcoef, mc)
     grad_close("v_raw_opac", op.grad.cpu().numpy(), vo, mo)
+
+
+def test_second_backward_of_one_forward(gpu):
+    """The forward zeroes the gradient rows its first backward uses; a second
+    backward of the same forward (retain_graph) zeroes its own and matches the
+    first (float atomics: equal to rtol 1e-5 of each array's largest entry)."""
+    import torch
+    from brush_amd import render as R
+
+    w, h = 320, 240
+    print(f"[case] two backwards of one forward, {w}x{h}", flush=True)
+    tr, sh, opac = random_scene(61, 3000, 1, mean_range=1.0, log_scale=(-3.0, 0.5))
+    cam = Camera.from_focal((0.0, 0.0, -3.0), (0.0, 0.0, 0.0, 1.0), 0.8 * w, w, h)
+    t = torch.from_numpy(tr).to(gpu).requires_grad_(True)
+    s = torch.from_numpy(sh).to(gpu).requires_grad_(True)
+    op = torch.from_numpy(opac).to(gpu).requires_grad_(True)
+    res = R.render_splats_diff(R.Splats(t, s, op), cam, (w, h))
+    v_out = torch.from_numpy(np.random.default_rng(5).standard_normal((h, w, 4)).astype(np.float32)).to(gpu)
+    res.img.backward(v_out, retain_graph=True)
+    first = [x.grad.clone() for x in (t, s, op)]
+    for x in (t, s, op):
+        x.grad = None
+    res.img.backward(v_out)
+    for name, a, b in zip(("v_transforms", "v_coeffs", "v_raw_opac"), first, (t.grad, s.grad, op.grad)):
+        a, b = a.cpu().numpy(), b.cpu().numpy()
+        assert np.all(np.isfinite(b)), name
+        scale = max(float(np.abs(a).max()), 1e-30)
+        assert np.abs(a - b).max() <= 1e-5 * scale, name
+        assert np.abs(a).max() > 0.0, name
