@@ -483,7 +483,13 @@ class _DiffConfig:
         self.raster_mode = raster_mode
         self.raster_pass = raster_pass
         self.compute_refine_weight = compute_refine_weight
-        self.output = None
+        # the forward's state and aux, not its RenderOutput: the output image
+        # is the autograd node's own output, and a reference to it from here
+        # would close a cycle (image -> grad_fn -> ctx -> cfg -> image) that
+        # keeps every step's state and image alive until the cyclic garbage
+        # collector runs
+        self.state = None
+        self.aux = None
         self.refine_weight = None
 
 
@@ -494,7 +500,8 @@ class _RenderSplatsFn(torch.autograd.Function):
     def forward(ctx, transforms, sh_coeffs, raw_opac, cfg: _DiffConfig):
         out = render(cfg.camera, cfg.img_size, transforms.detach(), sh_coeffs.detach(), raw_opac.detach(),
                      cfg.render_mode, cfg.raster_mode, cfg.background, cfg.raster_pass, rasterizer=cfg.rasterizer)
-        cfg.output = out
+        cfg.state = out.state
+        cfg.aux = out.aux
         ctx.cfg = cfg
         ctx.save_for_backward(transforms, sh_coeffs, raw_opac, out.out_img, out.aux.tile_offsets)
         return out.out_img
@@ -506,7 +513,6 @@ class _RenderSplatsFn(torch.autograd.Function):
         workspace, as v_combined stays inside RenderBackwards::backward."""
         cfg = ctx.cfg
         transforms, sh_coeffs, raw_opac, out_img, tile_offsets = ctx.saved_tensors
-        out = cfg.output
         n = transforms.shape[0]
         dev = transforms.device
         nc = sh_coeffs.shape[1]
@@ -524,7 +530,7 @@ class _RenderSplatsFn(torch.autograd.Function):
         bg = (ctypes.c_float * 3)(*[float(x) for x in cfg.background])
         with torch.cuda.device(dev):
             c = context()
-            st = lib().bh_render_backward(c.handle, out.state.handle, ptr(out_img), ptr(tile_offsets), bg,
+            st = lib().bh_render_backward(c.handle, cfg.state.handle, ptr(out_img), ptr(tile_offsets), bg,
                                           ptr(transforms.detach().contiguous()),
                                           ptr(sh_coeffs.detach().contiguous()), ptr(raw_opac.detach().contiguous()),
                                           ptr(v_img.contiguous()), flags, ptr(v_t), ptr(v_c), ptr(v_o), ptr(v_r))
@@ -546,7 +552,7 @@ def render_splats_diff(splats: Splats, camera: Camera, img_size, background=(0.0
                       rasterizer)
     transforms, raw_opacities = splats.folded()  # burn_glue.rs:631-641, differentiable through the fold
     img = _RenderSplatsFn.apply(transforms, splats.sh_coeffs, raw_opacities, cfg)
-    aux = cfg.output.aux
+    aux = cfg.aux
     res = SplatOutputDiff(img, aux.num_visible, aux.visible, aux.max_radius, aux)
     res._cfg = cfg
 

@@ -104,3 +104,53 @@ def test_render_rejects_bad_arguments_without_gpu():
         R.render(Camera(), (16, 16), t, torch.zeros((4, 1, 3)), torch.zeros(4))  # CPU tensors
     with pytest.raises(ValueError):
         R.sh_degree_from_coeffs(5)
+
+
+def test_diff_render_frees_its_state_without_the_cycle_collector(monkeypatch):
+    """The differentiable render's autograd node must not close a reference
+    cycle through its own output image: a step's forward state (and the
+    image) are released when the caller drops the result, not when Python's
+    cyclic garbage collector happens to run.  Otherwise every step of a
+    training or benchmark loop keeps its count-sized buffers until a
+    collection, and the library and torch allocate afresh each step.  The
+    render is stubbed with CPU tensors (only the host-side object graph is
+    under test)."""
+    import gc
+    import weakref
+
+    import torch
+
+    from brush_amd import render as R
+
+    class FakeState:
+        handle = None
+
+        def release(self):
+            pass
+
+    states = []
+
+    def fake_render(camera, img_size, transforms, sh, opac, mode, rmode, bg, rpass, rasterizer=None, **kw):
+        st = FakeState()
+        states.append(weakref.ref(st))
+        w, h = img_size
+        aux = R.RenderAux(1, 1, torch.zeros(transforms.shape[0]), torch.zeros(transforms.shape[0]),
+                          torch.zeros((1, 1, 2), dtype=torch.int32), (w, h))
+        return R.RenderOutput(torch.zeros((h, w, 4)), aux, {}, st)
+
+    monkeypatch.setattr(R, "render", fake_render)
+    t = torch.zeros((3, 10), requires_grad=True)
+    s = torch.zeros((3, 1, 3), requires_grad=True)
+    o = torch.zeros((3,), requires_grad=True)
+    was_enabled = gc.isenabled()
+    gc.disable()
+    try:
+        res = R.render_splats_diff(R.Splats(t, s, o), None, (4, 2))
+        img_ref = weakref.ref(res.img)
+        assert states[0]() is not None
+        del res
+        assert states[0]() is None, "the forward state outlived its result (reference cycle)"
+        assert img_ref() is None, "the rendered image outlived its result (reference cycle)"
+    finally:
+        if was_enabled:
+            gc.enable()
