@@ -34,6 +34,7 @@ FLAG_TILE_16X8 = 32
 DEBUG_POISON = 1
 DEBUG_VALIDATE = 2
 DEBUG_EXACT_SIZES = 4
+DEBUG_KEEP_LANES = 8
 
 PROJECTED_LANES = 10
 COMPACT_GRAD_LANES = 11
@@ -46,7 +47,7 @@ EXPORTED = [
     "bh_ctx_read_timings", "bh_ctx_reset_timings", "bh_ctx_workspace_bytes", "bh_ctx_release_workspace",
     "bh_ctx_set_debug",
     "bh_radix_argsort", "bh_radix_argsort_noalloc",
-    "bh_prefix_sum", "bh_get_tile_offsets", "bh_render_forward", "bh_fwd_state_info",
+    "bh_prefix_sum", "bh_get_tile_offsets", "bh_render_forward", "bh_fwd_state_info", "bh_fwd_state_backward_lanes",
     "bh_fwd_state_release", "bh_rasterize_backward", "bh_render_backward", "bh_project_backward",
     "bh_image_loss_forward", "bh_image_loss_backward", "bh_adam_scaled_step", "bh_copy_to_host",
     "bh_copy_to_device", "bh_copy_device", "bh_device_alloc", "bh_device_free", "bh_synchronize",
@@ -208,6 +209,7 @@ def lib() -> ctypes.CDLL:
         "bh_get_tile_offsets": (S, [P, P, U32, U32, P]),
         "bh_render_forward": (S, [P, UP, P, P, P, P, U32, U32, U32, P, P, P, P, PP]),
         "bh_fwd_state_info": (S, [P, ctypes.POINTER(FwdInfo)]),
+        "bh_fwd_state_backward_lanes": (S, [P, PP]),
         "bh_fwd_state_release": (None, [P]),
         "bh_rasterize_backward": (S, [P, P, P, P, P, U32, P, U32, U32, P, U32, P]),
         "bh_render_backward": (S, [P, P, P, P, P, P, P, P, P, U32, P, P, P, P]),
@@ -274,15 +276,18 @@ class Context:
         self.check(lib().bh_ctx_read_timings(self.handle, arr, 64, ctypes.byref(n)), "bh_ctx_read_timings")
         return {arr[i].name.decode(): (int(arr[i].launches), float(arr[i].total_ms)) for i in range(n.value)}
 
-    def set_debug(self, poison: bool = False, validate: bool = False, exact_sizes: bool = False):
+    def set_debug(self, poison: bool = False, validate: bool = False, exact_sizes: bool = False,
+                  keep_lanes: bool = False):
         """BH_DEBUG_POISON: workspace blocks start as 0xFF bytes;
         BH_DEBUG_VALIDATE: NaN / Inf splat parameters (forward) and gradients
         (fused backward) raise BH_ERR_NOT_FINITE;
         BH_DEBUG_EXACT_SIZES: every forward waits for its counts before it
         queues the launches that depend on them (no plan from the previous
-        forward)."""
+        forward);
+        BH_DEBUG_KEEP_LANES: the fused backward keeps its per-splat gradient
+        lanes in the forward state (ForwardState.backward_lanes)."""
         flags = ((DEBUG_POISON if poison else 0) | (DEBUG_VALIDATE if validate else 0)
-                 | (DEBUG_EXACT_SIZES if exact_sizes else 0))
+                 | (DEBUG_EXACT_SIZES if exact_sizes else 0) | (DEBUG_KEEP_LANES if keep_lanes else 0))
         self.check(lib().bh_ctx_set_debug(self.handle, flags), "bh_ctx_set_debug")
 
     def workspace_bytes(self) -> int:

@@ -26,7 +26,19 @@ struct bh_fwd_state {
     // tile-order launch, which leaves the rest of the GPU idle); the first
     // backward takes them, a later one zeroes its own
     float* bwd_rows = nullptr;
-    mutable bool bwd_rows_clean = false;
+    bool bwd_rows_clean = false;
+    // BH_DEBUG_KEEP_LANES: the gradient lanes the latest backward accumulated
+    float* kept_lanes = nullptr;
+
+    // returns one of the state's buffers to the pool (stream ordered: later
+    // users of the block run after the work already queued on it)
+    void drop(void* p) {
+        if (!p) return;
+        auto it = std::find(buffers.begin(), buffers.end(), p);
+        if (it == buffers.end()) return;
+        buffers.erase(it);
+        ctx->pool.release(p);
+    }
 };
 
 namespace bh {
@@ -422,7 +434,7 @@ bh_status bh_ctx_reset_timings(bh_ctx* ctx) {
 
 bh_status bh_ctx_set_debug(bh_ctx* ctx, uint32_t flags) {
     if (!ctx) return BH_ERR_INVALID_ARG;
-    if (flags & ~(BH_DEBUG_POISON | BH_DEBUG_VALIDATE | BH_DEBUG_EXACT_SIZES))
+    if (flags & ~(BH_DEBUG_POISON | BH_DEBUG_VALIDATE | BH_DEBUG_EXACT_SIZES | BH_DEBUG_KEEP_LANES))
         return set_error(ctx, BH_ERR_INVALID_ARG, "set_debug: unknown flag");
     ctx->debug = flags;
     return BH_OK;
@@ -816,6 +828,12 @@ bh_status bh_fwd_state_info(const bh_fwd_state* state, bh_fwd_info* out) {
     return BH_OK;
 }
 
+bh_status bh_fwd_state_backward_lanes(const bh_fwd_state* state, const float** lanes) {
+    if (!state || !lanes) return BH_ERR_INVALID_ARG;
+    *lanes = state->kept_lanes;
+    return BH_OK;
+}
+
 void bh_fwd_state_release(bh_fwd_state* state) {
     if (!state) return;
     for (void* p : state->buffers) state->ctx->pool.release(p);
@@ -885,15 +903,33 @@ bh_status bh_render_backward(bh_ctx* ctx, const bh_fwd_state* state, const float
         !v_transforms || !v_coeffs || !v_raw_opac || !v_refine)
         return set_error(ctx, BH_ERR_INVALID_ARG, "render_backward: null argument");
     // gradient lanes accumulated per global id, so project backward reads
-    // them in order (no inverse permutation, no gathered rows)
+    // them in order (no inverse permutation, no gathered rows).  The first
+    // backward of a state takes the rows its forward zeroed and returns them
+    // to the pool once project backward is queued; a later backward zeroes
+    // rows of its own.  The call changes the state (it consumes those rows),
+    // so backwards of one state are serialised like every call on a context.
+    bh_fwd_state* st = const_cast<bh_fwd_state*>(state);
+    const bool keep = (ctx->debug & BH_DEBUG_KEEP_LANES) != 0;
     Scratch ws(ctx);
     float* rows;
-    const bool pre_zeroed = state->bwd_rows && state->bwd_rows_clean;
+    const bool pre_zeroed = st->bwd_rows && st->bwd_rows_clean;
     if (pre_zeroed) {
-        rows = state->bwd_rows;
-        state->bwd_rows_clean = false;
+        rows = st->bwd_rows;
+        st->bwd_rows = nullptr;
+        st->bwd_rows_clean = false;
+    } else if (keep) {
+        void* p = nullptr;
+        hipError_t e = ctx->pool.alloc(&p, (size_t)n * 11 * sizeof(float));
+        if (e != hipSuccess) return hip_check(ctx, e, "workspace allocation");
+        st->buffers.push_back(p);
+        poison(ctx, p, (size_t)n * 11 * sizeof(float));
+        rows = (float*)p;
     } else {
         BH_TRY(ws.get(&rows, (size_t)n * 11));
+    }
+    if (st->kept_lanes) {
+        st->drop(st->kept_lanes);
+        st->kept_lanes = nullptr;
     }
     const uint32_t raster_flags = (in.flags & (fwd_owned | BH_FLAG_TILE_16X8)) | (flags & BH_FLAG_REFINE_WEIGHT);
     if (in.num_visible && in.num_intersections && state->record.masks) {
@@ -917,6 +953,10 @@ bh_status bh_render_backward(bh_ctx* ctx, const bh_fwd_state* state, const float
     launch_project_backward(ctx, in.uniforms, transforms, sh_coeffs, raw_opacities, nullptr, n, in.sh_degree,
                             (in.flags & BH_FLAG_MIP) != 0, rows, v_transforms, v_coeffs, v_raw_opac, v_refine);
     BH_TRY(check_launch(ctx, "project_backward"));
+    if (keep)
+        st->kept_lanes = rows;
+    else if (pre_zeroed)
+        st->drop(rows);
     if (ctx->debug & BH_DEBUG_VALIDATE) {
         // Splats::bwd_validate (gaussian_splats.rs:384-415)
         const uint32_t nc = (in.sh_degree + 1u) * (in.sh_degree + 1u);

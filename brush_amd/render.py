@@ -144,6 +144,20 @@ class ForwardState:
                            "bh_copy_device")
         return out
 
+    def backward_lanes(self) -> torch.Tensor | None:
+        """A copy of the [N, 11] per-splat gradient lanes (row = global id)
+        of this state's latest fused backward, when it ran with the
+        context's keep_lanes debug mode; None otherwise."""
+        p = ctypes.c_void_p()
+        self.ctx.check(lib().bh_fwd_state_backward_lanes(self.handle, ctypes.byref(p)), "bh_fwd_state_backward_lanes")
+        if not p.value:
+            return None
+        n = int(self.info.num_splats)
+        out = torch.empty((n, _lib.COMPACT_GRAD_LANES), dtype=torch.float32, device=f"cuda:{self.ctx.device}")
+        self.ctx.use_current_stream()
+        self.ctx.check(lib().bh_copy_device(self.ctx.handle, ptr(out), p, out.numel() * 4), "bh_copy_device")
+        return out
+
     def release(self):
         if self.handle:
             lib().bh_fwd_state_release(self.handle)

@@ -194,6 +194,11 @@ bh_status bh_ctx_reset_timings(bh_ctx* ctx);
 #define BH_DEBUG_POISON 1u
 #define BH_DEBUG_VALIDATE 2u
 #define BH_DEBUG_EXACT_SIZES 4u
+/* BH_DEBUG_KEEP_LANES: bh_render_backward keeps the per-splat gradient lanes
+ *   it accumulated in the forward state (bh_fwd_state_backward_lanes) instead
+ *   of returning them to the workspace pool, so a test can compare them with
+ *   rasterize_bwd's v_combined lane by lane. */
+#define BH_DEBUG_KEEP_LANES 8u
 bh_status bh_ctx_set_debug(bh_ctx* ctx, uint32_t flags);
 /* Bytes currently cached by the context's workspace pool. */
 uint64_t bh_ctx_workspace_bytes(const bh_ctx* ctx);
@@ -266,6 +271,13 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* u, const flo
                             uint32_t* tile_offsets, bh_fwd_state** state);
 
 bh_status bh_fwd_state_info(const bh_fwd_state* state, bh_fwd_info* out);
+/* Debug: the per-splat gradient lanes f32 [N,11] (row = global id, lanes as
+ * v_combined) that the state's latest bh_render_backward accumulated, when
+ * that backward ran with BH_DEBUG_KEEP_LANES set; *lanes is NULL otherwise.
+ * Valid until the state's next backward or its release.  No counterpart in
+ * the reference (its v_combined is an ordinary tensor, rasterize_bwd's
+ * output). */
+bh_status bh_fwd_state_backward_lanes(const bh_fwd_state* state, const float** lanes);
 /* Returns the state's buffers to the context pool (stream ordered). */
 void bh_fwd_state_release(bh_fwd_state* state);
 
@@ -287,11 +299,19 @@ bh_status bh_rasterize_backward(bh_ctx* ctx, const float* out_img, const float* 
 /* Both backward operations of one forward state in one call: the backward of
  * RenderBackwards (brush-render-bwd/src/burn_glue.rs:292-378), which runs
  * rasterize_bwd then project_bwd and keeps v_combined internal.  Here the
- * gradient lanes are accumulated per global id in library workspace, so
- * project backward reads them in order.  `state` comes from a forward with
- * BH_FLAG_BWD_INFO; out_img and tile_offsets are that forward's outputs;
- * flags: BH_FLAG_SMOOTH_CUTOFF, BH_FLAG_REFINE_WEIGHT, BH_FLAG_RENDER_DEPTH
- * (BH_FLAG_MIP follows the forward).  Outputs as bh_project_backward. */
+ * gradient lanes are accumulated per global id, so project backward reads
+ * them in order.  `state` comes from a forward with BH_FLAG_BWD_INFO;
+ * out_img and tile_offsets are that forward's outputs; flags:
+ * BH_FLAG_SMOOTH_CUTOFF, BH_FLAG_REFINE_WEIGHT, BH_FLAG_RENDER_DEPTH
+ * (BH_FLAG_MIP follows the forward).  Outputs as bh_project_backward.
+ *
+ * The call changes the state: the first backward of a state accumulates into
+ * the [N,11] lane rows that the forward zeroed (held by the state until
+ * then) and returns them to the context's workspace pool once its work is
+ * queued; a later backward of the same state zeroes workspace rows of its
+ * own.  Backwards of one state must therefore not overlap; since a state
+ * belongs to one context, and calls on a context are externally
+ * synchronised, this is the context's rule. */
 bh_status bh_render_backward(bh_ctx* ctx, const bh_fwd_state* state, const float* out_img,
                              const uint32_t* tile_offsets, const float background[3],
                              const float* transforms, const float* sh_coeffs,

@@ -9,6 +9,7 @@
  */
 #include "bh_oracle.h"
 
+#include <math.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -884,16 +885,24 @@ void or_rasterize_reference(const float* projected, uint32_t n, uint32_t w, uint
 /* in pixel order, then strip 0 + strip 1 + strip 2 + strip 3.  The GPU adds */
 /* the per-tile sums with atomics, so only the cross-tile order differs.     */
 /* ------------------------------------------------------------------------ */
-void or_rasterize_backward(uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,
-                           const float* bg, const float* out_img, const float* projected,
-                           const uint32_t* cgid_from_isect, const uint32_t* offsets,
-                           uint32_t num_visible, const float* v_output, uint32_t flags,
-                           float* v_combined) {
+/* check: OR_CHECK_DROP_LAST_BATCH plants a mistake for the tests of the
+ * gradient tolerance (the last 64 entries of every tile's list, or the
+ * partial batch that ends it, are skipped).  v_abs (may be NULL) receives,
+ * per lane, the sum over the lane's per-pixel terms of a bound on each
+ * term's magnitude that also bounds the magnitudes it is computed from (see
+ * or_rasterize_backward_check in bh_oracle.h). */
+static void rasterize_backward_impl(uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,
+                                    const float* bg, const float* out_img, const float* projected,
+                                    const uint32_t* cgid_from_isect, const uint32_t* offsets,
+                                    uint32_t num_visible, const float* v_output, uint32_t flags,
+                                    float* v_combined, float* v_abs, float* v_sq, uint32_t check) {
     int smooth = (flags & BH_FLAG_SMOOTH_CUTOFF) != 0;
     int refine = (flags & BH_FLAG_REFINE_WEIGHT) != 0;
     int depth = (flags & BH_FLAG_RENDER_DEPTH) != 0;
     uint32_t chans = depth ? 5u : 4u;
     memset(v_combined, 0, (size_t)(num_visible ? num_visible : 1) * 11 * sizeof(float));
+    if (v_abs) memset(v_abs, 0, (size_t)(num_visible ? num_visible : 1) * 11 * sizeof(float));
+    if (v_abs) memset(v_sq, 0, (size_t)(num_visible ? num_visible : 1) * 11 * sizeof(float));
     float img_wf = (float)img_w, img_hf = (float)img_h;
     int64_t num_tiles = (int64_t)tile_bw * tile_bh;
     const uint32_t th = (flags & BH_FLAG_TILE_16X8) ? 8u : 16u;
@@ -901,8 +910,12 @@ void or_rasterize_backward(uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uin
     for (int64_t tile = 0; tile < num_tiles; tile++) {
         uint32_t lo = offsets[2 * tile], hi = offsets[2 * tile + 1];
         if (hi <= lo) continue;
+        if (check & OR_CHECK_DROP_LAST_BATCH) hi = lo + (hi - lo - 1u) / 64u * 64u;
         uint32_t ox = (uint32_t)(tile % tile_bw) * 16u, oy = (uint32_t)(tile / tile_bw) * th;
         float st[256][5];
+        /* per pixel: the sum of squares of the magnitudes the remaining
+         * colour has been rounded at along the walk (per channel) */
+        double se[256][3];
         for (uint32_t p = 0; p < 16u * th; p++) {
             uint32_t px = ox + (p & 15u), py = oy + (p >> 4);
             if (px < img_w && py < img_h) {
@@ -916,6 +929,7 @@ void or_rasterize_backward(uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uin
             } else {
                 st[p][0] = st[p][1] = st[p][2] = st[p][3] = st[p][4] = 0.0f;
             }
+            se[p][0] = se[p][1] = se[p][2] = 0.0;
         }
         for (uint32_t i = lo; i < hi; i++) {
             uint32_t cg = cgid_from_isect[i];
@@ -925,6 +939,7 @@ void or_rasterize_backward(uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uin
             bh_conic_log2(c.c00, c.c01, c.c11, &ca, &cbc, &cc);
             float cr = bh_maxf(s[6], 0.0f), cgc = bh_maxf(s[7], 0.0f), cb = bh_maxf(s[8], 0.0f);
             float gs[4][11] = {{0}};
+            double ga[11] = {0}, gq[11] = {0};
             for (uint32_t p = 0; p < 16u * th; p++) {
                 float* gr = gs[p >> 6];
                 float sx = st[p][0], sy = st[p][1], sz = st[p][2], sw = st[p][3];
@@ -979,6 +994,60 @@ void or_rasterize_backward(uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uin
                         gr[9] += len / bh_maxf(final_a, 1.0e-5f);
                     }
                 }
+                if (v_abs) {
+                    /* the scale of the rounding noise in each term: the
+                     * colour gap T c - S rounded once at its operands'
+                     * magnitudes, plus the rounding S has gathered along the
+                     * pixel's walk as a random walk (each step rounds a
+                     * product |vis c| and a difference |S'|; the root sum of
+                     * their squares), times |v_out| */
+                    double m_alpha =
+                        fabs((double)w + (double)alpha * dw) * (double)ra *
+                        ((fabs((double)sw * cr) + fabs((double)sx) + sqrt(se[p][0])) * fabs((double)vox) +
+                         (fabs((double)sw * cgc) + fabs((double)sy) + sqrt(se[p][1])) * fabs((double)voy) +
+                         (fabs((double)sw * cb) + fabs((double)sz) + sqrt(se[p][2])) * fabs((double)voz) +
+                         fabs((double)vow));
+                    double m_sigma = (double)alpha * m_alpha;
+                    double ddx = fabs((double)dx), ddy = fabs((double)dy);
+                    double mt[11] = {0};
+                    mt[5] = s[6] >= 0.0f ? (double)vis * fabs((double)vox) : 0.0;
+                    mt[6] = s[7] >= 0.0f ? (double)vis * fabs((double)voy) : 0.0;
+                    mt[7] = s[8] >= 0.0f ? (double)vis * fabs((double)voz) : 0.0;
+                    if (depth) mt[10] = (double)vis * fabs((double)vo[4]);
+                    if (s[5] * gaussian <= 0.999f) {
+                        mt[0] = m_sigma * (fabs((double)c.c00) * ddx + fabs((double)c.c01) * ddy);
+                        mt[1] = m_sigma * (fabs((double)c.c01) * ddx + fabs((double)c.c11) * ddy);
+                        mt[2] = 0.5 * m_sigma * ddx * ddx;
+                        mt[3] = m_sigma * ddx * ddy;
+                        mt[4] = 0.5 * m_sigma * ddy * ddy;
+                        mt[8] = m_alpha * (double)gaussian;
+                        if (refine)
+                            mt[9] = sqrt(mt[0] * img_wf * mt[0] * img_wf + mt[1] * img_hf * mt[1] * img_hf) /
+                                    (double)bh_maxf(final_a, 1.0e-5f);
+                    }
+                    /* the terms' own magnitudes, for the summation order (the
+                     * 2D-mean lanes as sums of v_sigma dx and v_sigma dy
+                     * times the conic, the GPU's grouping) */
+                    double at[11] = {0};
+                    at[5] = mt[5], at[6] = mt[6], at[7] = mt[7], at[10] = mt[10];
+                    if (s[5] * gaussian <= 0.999f) {
+                        double vs = fabs((double)v_sigma);
+                        at[0] = vs * (fabs((double)c.c00) * ddx + fabs((double)c.c01) * ddy);
+                        at[1] = vs * (fabs((double)c.c01) * ddx + fabs((double)c.c11) * ddy);
+                        at[2] = 0.5 * vs * ddx * ddx;
+                        at[3] = vs * ddx * ddy;
+                        at[4] = 0.5 * vs * ddy * ddy;
+                        at[8] = fabs((double)v_alpha * (double)gaussian);
+                        if (refine)
+                            at[9] = sqrt(at[0] * img_wf * at[0] * img_wf + at[1] * img_hf * at[1] * img_hf) /
+                                    (double)bh_maxf(final_a, 1.0e-5f);
+                    }
+                    for (int k = 0; k < 11; k++) ga[k] += at[k], gq[k] += mt[k] * mt[k];
+                    double pr = (double)vis * cr, pg = (double)vis * cgc, pb = (double)vis * cb;
+                    se[p][0] += pr * pr + (double)nrx * nrx;
+                    se[p][1] += pg * pg + (double)nry * nry;
+                    se[p][2] += pb * pb + (double)nrz * nrz;
+                }
                 st[p][0] = nrx;
                 st[p][1] = nry;
                 st[p][2] = nrz;
@@ -987,18 +1056,162 @@ void or_rasterize_backward(uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uin
             float gr[11];
             for (int k = 0; k < 11; k++) gr[k] = ((gs[0][k] + gs[1][k]) + gs[2][k]) + gs[3][k];
             float* out = v_combined + (size_t)cg * 11;
+            float* oa = v_abs ? v_abs + (size_t)cg * 11 : NULL;
+            float* oq = v_sq ? v_sq + (size_t)cg * 11 : NULL;
             for (int k = 0; k < 11; k++) {
                 if (k == 9 && !refine) continue;
                 if (k == 10 && !depth) continue;
                 if (g_threads > 1) {
 #pragma omp atomic
                     out[k] += gr[k];
+                    if (oa) {
+#pragma omp atomic
+                        oa[k] += (float)ga[k];
+#pragma omp atomic
+                        oq[k] += (float)gq[k];
+                    }
                 } else {
                     out[k] += gr[k];
+                    if (oa) oa[k] += (float)ga[k], oq[k] += (float)gq[k];
                 }
             }
         }
     }
+}
+
+void or_rasterize_backward(uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,
+                           const float* bg, const float* out_img, const float* projected,
+                           const uint32_t* cgid_from_isect, const uint32_t* offsets,
+                           uint32_t num_visible, const float* v_output, uint32_t flags,
+                           float* v_combined) {
+    rasterize_backward_impl(img_w, img_h, tile_bw, tile_bh, bg, out_img, projected, cgid_from_isect, offsets,
+                            num_visible, v_output, flags, v_combined, NULL, NULL, 0u);
+}
+
+void or_rasterize_backward_check(uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,
+                                 const float* bg, const float* out_img, const float* projected,
+                                 const uint32_t* cgid_from_isect, const uint32_t* offsets,
+                                 uint32_t num_visible, const float* v_output, uint32_t flags, uint32_t check,
+                                 float* v_combined, float* v_abs, float* v_sq) {
+    rasterize_backward_impl(img_w, img_h, tile_bw, tile_bh, bg, out_img, projected, cgid_from_isect, offsets,
+                            num_visible, v_output, flags, v_combined, v_abs, v_abs ? v_sq : NULL, check);
+}
+
+/* The same backward with every gradient quantity in double: transmittance,
+ * remaining colour, the per-pixel terms and every sum.  The decisions (which
+ * pairs contribute, where a pixel's walk ends) are the f32 ones above, and
+ * alpha is the forward's f32 alpha, so both evaluate the gradient of the
+ * same rendered image; they differ only by the f32 rounding of the
+ * gradient arithmetic and of its sums.  Test infrastructure: it calibrates
+ * the tolerance that the GPU backward is held to. */
+void or_rasterize_backward_f64(uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,
+                               const float* bg, const float* out_img, const float* projected,
+                               const uint32_t* cgid_from_isect, const uint32_t* offsets,
+                               uint32_t num_visible, const float* v_output, uint32_t flags,
+                               float* v_combined) {
+    int smooth = (flags & BH_FLAG_SMOOTH_CUTOFF) != 0;
+    int refine = (flags & BH_FLAG_REFINE_WEIGHT) != 0;
+    int depth = (flags & BH_FLAG_RENDER_DEPTH) != 0;
+    uint32_t chans = depth ? 5u : 4u;
+    size_t rows = (size_t)(num_visible ? num_visible : 1);
+    double* acc = (double*)calloc(rows * 11, sizeof(double));
+    double img_wd = (double)img_w, img_hd = (double)img_h;
+    int64_t num_tiles = (int64_t)tile_bw * tile_bh;
+    const uint32_t th = (flags & BH_FLAG_TILE_16X8) ? 8u : 16u;
+#pragma omp parallel for schedule(dynamic, 2) num_threads(g_threads)
+    for (int64_t tile = 0; tile < num_tiles; tile++) {
+        uint32_t lo = offsets[2 * tile], hi = offsets[2 * tile + 1];
+        if (hi <= lo) continue;
+        uint32_t ox = (uint32_t)(tile % tile_bw) * 16u, oy = (uint32_t)(tile / tile_bw) * th;
+        float tf[256];      /* f32 transmittance: the decisions */
+        double sd[256][5];  /* remaining colour, transmittance, remaining depth */
+        for (uint32_t p = 0; p < 16u * th; p++) {
+            uint32_t px = ox + (p & 15u), py = oy + (p >> 4);
+            if (px < img_w && py < img_h) {
+                const float* o = out_img + ((size_t)py * img_w + px) * chans;
+                double t_final = 1.0 - (double)o[3];
+                for (int k = 0; k < 3; k++) sd[p][k] = (double)o[k] - t_final * (double)bg[k];
+                sd[p][3] = 1.0;
+                sd[p][4] = depth ? (double)o[4] : 0.0;
+                tf[p] = 1.0f;
+            } else {
+                for (int k = 0; k < 5; k++) sd[p][k] = 0.0;
+                tf[p] = 0.0f;
+            }
+        }
+        for (uint32_t i = lo; i < hi; i++) {
+            uint32_t cg = cgid_from_isect[i];
+            const float* s = projected + (size_t)cg * 10;
+            float ca, cbc, cc;
+            bh_conic_log2(s[2], s[3], s[4], &ca, &cbc, &cc);
+            double col[3] = {(double)bh_maxf(s[6], 0.0f), (double)bh_maxf(s[7], 0.0f), (double)bh_maxf(s[8], 0.0f)};
+            double g[11] = {0};
+            for (uint32_t p = 0; p < 16u * th; p++) {
+                float sw = tf[p];
+                if (!(sw > 1.0e-4f)) continue;
+                uint32_t px = ox + (p & 15u), py = oy + (p >> 4);
+                float pcx = (float)px + 0.5f, pcy = (float)py + 0.5f;
+                float dxf = s[0] - pcx, dyf = s[1] - pcy;
+                float power = bh_power_log2(ca, cbc, cc, dxf, dyf);
+                float gaussian = bh_exp2_neg(-power);
+                float alpha = bh_minf(0.999f, s[5] * gaussian);
+                float w = smooth ? cutoff_weight(alpha) : (alpha >= CUT_MID ? 1.0f : 0.0f);
+                if (!(power >= 0.0f && w > 0.0f)) continue;
+                float aef = alpha * w;
+                float next_tf = sw * (1.0f - aef);
+                if (next_tf <= 1.0e-4f) {
+                    tf[p] = 0.0f;
+                    continue;
+                }
+                tf[p] = next_tf;
+                double T = sd[p][3], ae = (double)alpha * (double)w;
+                double vis = ae * T;
+                const float* vo = v_output + ((size_t)py * img_w + px) * chans;
+                double vod[4] = {(double)vo[0], (double)vo[1], (double)vo[2], (double)vo[3]};
+                double final_a = (double)out_img[((size_t)py * img_w + px) * chans + 3];
+                double t_final = 1.0 - final_a;
+                double vow = (vod[3] - ((double)bg[0] * vod[0] + (double)bg[1] * vod[1] + (double)bg[2] * vod[2])) *
+                             t_final;
+                for (int k = 0; k < 3; k++)
+                    if (s[6 + k] >= 0.0f) g[5 + k] += vis * vod[k];
+                double ra = 1.0 / (1.0 - ae);
+                double dot_rgb = 0.0;
+                for (int k = 0; k < 3; k++) dot_rgb += (T * col[k] - sd[p][k]) * vod[k];
+                dot_rgb *= ra;
+                if (depth) {
+                    g[10] += vis * (double)vo[4];
+                    sd[p][4] -= vis * (double)s[9];
+                }
+                double dw = smooth ? (double)cutoff_weight_deriv(alpha) : 0.0;
+                double v_alpha = (dot_rgb + vow * ra) * ((double)w + (double)alpha * dw);
+                double v_sigma = -(double)alpha * v_alpha;
+                double dx = (double)dxf, dy = (double)dyf;
+                double vx = v_sigma * ((double)s[2] * dx + (double)s[3] * dy);
+                double vy = v_sigma * ((double)s[3] * dx + (double)s[4] * dy);
+                if (s[5] * gaussian <= 0.999f) {
+                    g[2] += 0.5 * v_sigma * dx * dx;
+                    g[3] += v_sigma * dx * dy;
+                    g[4] += 0.5 * v_sigma * dy * dy;
+                    g[0] += vx;
+                    g[1] += vy;
+                    g[8] += v_alpha * (double)gaussian;
+                    if (refine) g[9] += sqrt(vx * img_wd * vx * img_wd + vy * img_hd * vy * img_hd) /
+                                        (double)bh_maxf((float)final_a, 1.0e-5f);
+                }
+                for (int k = 0; k < 3; k++) sd[p][k] -= vis * col[k];
+                sd[p][3] = T * (1.0 - ae);
+            }
+            double* out = acc + (size_t)cg * 11;
+            for (int k = 0; k < 11; k++) {
+                if (k == 9 && !refine) continue;
+                if (k == 10 && !depth) continue;
+#pragma omp atomic
+                out[k] += g[k];
+            }
+        }
+    }
+    for (size_t i = 0; i < rows * 11; i++) v_combined[i] = (float)acc[i];
+    free(acc);
 }
 
 /* ------------------------------------------------------------------------ */

@@ -86,6 +86,35 @@ void or_rasterize_backward(uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uin
                            const uint32_t* tile_offsets, uint32_t num_visible,
                            const float* v_output, uint32_t flags, float* v_combined);
 
+/* Test support for the gradient tolerance.  or_rasterize_backward_check is
+ * or_rasterize_backward with additions:
+ *   check: OR_CHECK_DROP_LAST_BATCH plants a mistake (the last batch of 64
+ *     entries of every tile's list is skipped);
+ *   v_abs [max(V,1),11] (may be NULL): per lane, the sum of its per-pixel
+ *     terms' magnitudes (the 2D-mean lanes as |c00 v_sigma dx| + |c01 v_sigma
+ *     dy| and the like): a sum in another order differs by a small multiple
+ *     of the unit roundoff times this;
+ *   v_sq [max(V,1),11] (used when v_abs is given): per lane, the sum of the
+ *     squares of its per-pixel terms' rounding scales: the magnitudes each
+ *     term is formed from (the colour gap |T c| + |S| with the rounding the
+ *     remaining colour S has gathered along the walk, as a root sum of
+ *     squares of the magnitudes it was rounded at, then |v_out| and the
+ *     alpha, conic and offset factors).  Another f32 evaluation of the terms
+ *     moves the lane by a small multiple of the unit roundoff times the root
+ *     of this.
+ * or_rasterize_backward_f64 evaluates the same backward in double (the same
+ * decisions and the same f32 alpha). */
+#define OR_CHECK_DROP_LAST_BATCH 1u
+void or_rasterize_backward_check(uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,
+                                 const float* background, const float* out_img, const float* projected,
+                                 const uint32_t* compact_gid_from_isect, const uint32_t* tile_offsets,
+                                 uint32_t num_visible, const float* v_output, uint32_t flags, uint32_t check,
+                                 float* v_combined, float* v_abs, float* v_sq);
+void or_rasterize_backward_f64(uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,
+                               const float* background, const float* out_img, const float* projected,
+                               const uint32_t* compact_gid_from_isect, const uint32_t* tile_offsets,
+                               uint32_t num_visible, const float* v_output, uint32_t flags, float* v_combined);
+
 void or_project_backward(const bh_project_uniforms* u, const float* transforms,
                          const float* sh_coeffs, const float* raw_opac,
                          const uint32_t* global_from_compact_gid, uint32_t num_visible,

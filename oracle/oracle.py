@@ -126,6 +126,8 @@ def lib():
         L.or_rasterize.argtypes = [U32, U32, U32, U32, P, P, P, P, P, U32, P, P, P]
         L.or_rasterize_reference.argtypes = [P, U32, U32, U32, P, U32, P]
         L.or_rasterize_backward.argtypes = [U32, U32, U32, U32, P, P, P, P, P, U32, P, U32, P]
+        L.or_rasterize_backward_check.argtypes = [U32, U32, U32, U32, P, P, P, P, P, U32, P, U32, U32, P, P, P]
+        L.or_rasterize_backward_f64.argtypes = [U32, U32, U32, U32, P, P, P, P, P, U32, P, U32, P]
         L.or_project_backward.argtypes = [UP, P, P, P, P, U32, U32, U32, U32, P, P, P, P, P]
         L.or_gauss_taps.argtypes = [P]
         L.or_image_loss_forward.argtypes = [P, U32, U32, P, U32, U32, ctypes.POINTER(LossConfig), P]
@@ -369,6 +371,48 @@ def rasterize_backward(fwd: ForwardResult, v_output: np.ndarray, flags: int = FL
                                 _p(fwd.compact_gid_from_isect),
                                 _p(np.ascontiguousarray(fwd.tile_offsets).reshape(-1)),
                                 fwd.num_visible, _p(v_output), flags, _p(v_comb))
+    return v_comb
+
+
+CHECK_DROP_LAST_BATCH = 1
+
+
+def _raster_bwd_args(fwd: ForwardResult, v_output, flags, background):
+    ud = fwd.uniforms
+    if ud.get("tile_h", 16) == 8:
+        flags |= FLAG_TILE_16X8
+    bg = np.asarray(background, dtype=np.float32)
+    v_output = np.ascontiguousarray(v_output, dtype=np.float32)
+    keep = (bg, v_output, np.ascontiguousarray(fwd.out_img), np.ascontiguousarray(fwd.tile_offsets).reshape(-1))
+    args = [ud["img_w"], ud["img_h"], ud["tile_bw"], ud["tile_bh"], _p(keep[0]), _p(keep[2]), _p(fwd.projected),
+            _p(fwd.compact_gid_from_isect), _p(keep[3]), fwd.num_visible, _p(keep[1]), flags]
+    return args, keep
+
+
+def rasterize_backward_check(fwd: ForwardResult, v_output: np.ndarray, flags: int = FLAG_REFINE_WEIGHT,
+                             background=(0.0, 0.0, 0.0), check: int = 0):
+    """Test support for the gradient tolerance: the f32 backward (as
+    rasterize_backward, or with a planted mistake: ``check`` =
+    CHECK_DROP_LAST_BATCH) and, per lane, the sum of the magnitude bounds of
+    the lane's per-pixel terms (or_rasterize_backward_check in
+    bh_oracle.h).  Returns (v_combined, v_abs), both [max(V, 1), 11]."""
+    args, keep = _raster_bwd_args(fwd, v_output, flags, background)
+    rows = max(fwd.num_visible, 1)
+    v_comb = np.zeros((rows, 11), np.float32)
+    v_abs = np.zeros((rows, 11), np.float32)
+    v_sq = np.zeros((rows, 11), np.float32)
+    lib().or_rasterize_backward_check(*args, check, _p(v_comb), _p(v_abs), _p(v_sq))
+    return v_comb, v_abs, np.sqrt(v_sq)
+
+
+def rasterize_backward_f64(fwd: ForwardResult, v_output: np.ndarray, flags: int = FLAG_REFINE_WEIGHT,
+                           background=(0.0, 0.0, 0.0)) -> np.ndarray:
+    """The backward with every gradient quantity in double (the f32
+    decisions and alpha): a second, more accurate evaluation of the same
+    gradient, for calibrating tolerances."""
+    args, keep = _raster_bwd_args(fwd, v_output, flags, background)
+    v_comb = np.zeros((max(fwd.num_visible, 1), 11), np.float32)
+    lib().or_rasterize_backward_f64(*args, _p(v_comb))
     return v_comb
 
 

@@ -21,8 +21,8 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
-from tests.helpers import (assert_bits_equal, compare_forward, gpu_forward, grad_close, gradient_term_magnitudes,
-                           rel_close, uniforms_for)
+from tests.helpers import (OracleGrads, assert_bits_equal, check_fused_backward, compare_forward, gpu_forward,
+                           keep_lanes, uniforms_for)
 from brush_amd.synthetic import CONFIGS, generate_splats, generate_v_output  # noqa: F401
 
 pytestmark = pytest.mark.gpu
@@ -140,34 +140,26 @@ def test_full_size_forward_and_backward(gpu, w_id):
 
 def _compare_gradients(gpu, w, cam, tr, sh, opac, o):
     """The fused backward of render_splats_diff against the restatement's
-    rasterize + project backward, for the config's upstream gradient, to
-    rtol 1e-3 plus the entry's sensitivity to f32 summation differences in its
-    lanes (grad_close / gradient_term_magnitudes): in the clustered config a
-    few scale and rotation gradients are small differences of conic terms
-    1e4-1e5 times larger, where two correct f32 evaluations (the restatement
-    and the GPU's replay path, whose lanes agree to 7 digits) differ by
-    percents, and a float64 evaluation puts the restatement itself up to 1 %
-    away."""
+    rasterize + project backward for the config's upstream gradient: its
+    per-splat lanes entry by entry, its dense gradients bit for bit against
+    the restatement's project backward of those lanes, and entry by entry
+    against the restatement's own dense gradients; every entry within rtol
+    1e-3 plus its own f32 rounding noise (tests/helpers.py), with the worst
+    err / tol printed per array."""
     import torch
     from brush_amd import render as R
 
     t = torch.from_numpy(tr).to(gpu).requires_grad_(True)
     s = torch.from_numpy(sh).to(gpu).requires_grad_(True)
     op = torch.from_numpy(opac).to(gpu).requires_grad_(True)
-    res = R.render_splats_diff(R.Splats(t, s, op), cam, (w.img_w, w.img_h))
     v_out = generate_v_output(w)
-    res.img.backward(torch.from_numpy(v_out).to(gpu))
-    vc = O.rasterize_backward(o, v_out, O.FLAG_REFINE_WEIGHT)
-    vt, vcoef, vo, vr = O.project_backward(o, tr, sh, opac, vc)
-    # A full-size lane sums up to ~2000 per-pixel terms (64 pixels a block,
-    # tens of blocks) in an order that differs between the restatement and
-    # the GPU (and between GPU runs: float atomics); the sum of n terms is
-    # exact to n ulp of the terms' scale, 1e-4 relative for n ~ 2000.
-    mt, mc, mo = gradient_term_magnitudes(o, tr, sh, opac, vc, rel=1e-4)
-    grad_close("v_transforms", t.grad.cpu().numpy(), vt, mt)
-    grad_close("v_coeffs", s.grad.cpu().numpy(), vcoef, mc)
-    grad_close("v_raw_opac", op.grad.cpu().numpy(), vo, mo)
-    rel_close("refine", res._cfg.refine_weight.cpu().numpy(), vr, rtol=1e-3, atol_frac=1e-4)
+    with keep_lanes():
+        res = R.render_splats_diff(R.Splats(t, s, op), cam, (w.img_w, w.img_h))
+        res.img.backward(torch.from_numpy(v_out).to(gpu))
+    want = OracleGrads(o, tr, sh, opac, v_out, O.FLAG_REFINE_WEIGHT)
+    grads = {"v_transforms": t.grad.cpu().numpy(), "v_coeffs": s.grad.cpu().numpy(),
+             "v_raw_opac": op.grad.cpu().numpy(), "v_refine": res._cfg.refine_weight.cpu().numpy()}
+    check_fused_backward(w.name, res._cfg.state, tr, sh, opac, grads, want)
 
 
 def test_config2_clustered_full_size(gpu):
@@ -209,3 +201,20 @@ def test_config3_4k_forward_full_size(gpu, pose):
     _check_sort_structure(g, u["tile_bw"] * u["tile_bh"])
     _check_subset(g, u, tr, sh, opac, 0, seed=30 + pose, size=10000)
     assert g["out_img"].shape == (w.img_h, w.img_w)
+
+
+def test_config3_4k_pose_bit_exact(gpu):
+    """Config 3's first pose (6M SH3 splats, 3840x2160, forward only): every
+    output, the packed RGBA8 image included, bit for bit against the CPU
+    restatement."""
+    w_id = 3
+    w = CONFIGS[w_id]
+    print(f"[case] {w.name} pose 0 against the restatement", flush=True)
+    tr, sh, opac = _scene(w_id)
+    cam = w.camera(0, 8)
+    u = uniforms_for(cam, w.img_w, w.img_h, w.n, w.sh_degree)
+    g = gpu_forward(u, tr, sh, opac, 0)
+    o = O.render_forward(u, tr, sh, opac, 0)
+    assert o.num_intersections > 10_000_000
+    compare_forward(g, o)
+    assert g["out_img"].dtype == np.uint32 and g["out_img"].shape == (w.img_h, w.img_w)

@@ -16,7 +16,9 @@ bit for bit the same either way:
 * at the north-star size (config 1, 1M splats at 1080p), where the timed loop
   of the benchmark runs the planned launches;
 * for the fused backward of a planned forward (the record of contributing
-  pairs sized for the plan), to the order of float atomics.
+  pairs sized for the plan), and of a planned forward that outgrew its plan
+  and was queued again (its gradient rows allocated and zeroed anew), to the
+  order of float atomics.
 """
 import numpy as np
 import pytest
@@ -24,7 +26,7 @@ import pytest
 from brush_amd.camera import Camera
 from brush_amd.synthetic import CONFIGS, generate_splats
 from oracle import oracle as O
-from tests.helpers import gpu_forward, grad_close, gradient_term_magnitudes, rng_scene, uniforms_for
+from tests.helpers import OracleGrads, check_close, check_fused_backward, gpu_forward, keep_lanes, rng_scene, uniforms_for
 
 pytestmark = pytest.mark.gpu
 
@@ -132,34 +134,73 @@ def test_north_star_planned_forward_matches_exact(ctx):
         _assert_same(f"config 1 planned #{rep}", ref, g)
 
 
-def test_backward_of_a_planned_forward(ctx, gpu):
+def _diff(ctx, gpu, scene, cam, v_out, exact, lanes=False):
+    """render_splats_diff + backward, exact or planned; returns the image,
+    the dense gradients and the result (its forward state)."""
     import torch
     from brush_amd import render as R
 
-    print("[case] backward after planned forward", flush=True)
-    tr, sh, opac = rng_scene(20_000, 1.5, (-2.5, -0.5), (-1.0, 2.0), 0x55)
-    cam = _cam()
-    v_out = np.random.default_rng(3).standard_normal((SIZE[1], SIZE[0], 4)).astype(np.float32)
+    tr, sh, opac = scene
+    ctx.set_debug(exact_sizes=exact, keep_lanes=lanes)
+    t = torch.from_numpy(tr).to(gpu).requires_grad_(True)
+    s = torch.from_numpy(sh).to(gpu).requires_grad_(True)
+    o = torch.from_numpy(opac).to(gpu).requires_grad_(True)
+    res = R.render_splats_diff(R.Splats(t, s, o), cam, SIZE)
+    res.img.backward(torch.from_numpy(v_out).to(gpu))
+    torch.cuda.synchronize()
+    ctx.set_debug()
+    grads = {"v_transforms": t.grad.cpu().numpy(), "v_coeffs": s.grad.cpu().numpy(),
+             "v_raw_opac": o.grad.cpu().numpy(), "v_refine": res._cfg.refine_weight.cpu().numpy()}
+    return res.img.detach().cpu().numpy(), grads, res
 
-    def run(exact):
-        ctx.set_debug(exact_sizes=exact)
-        t = torch.from_numpy(tr).to(gpu).requires_grad_(True)
-        s = torch.from_numpy(sh).to(gpu).requires_grad_(True)
-        o = torch.from_numpy(opac).to(gpu).requires_grad_(True)
-        res = R.render_splats_diff(R.Splats(t, s, o), cam, SIZE)
-        res.img.backward(torch.from_numpy(v_out).to(gpu))
-        torch.cuda.synchronize()
-        ctx.set_debug()
-        return res.img.detach().cpu().numpy(), (t.grad.cpu().numpy(), s.grad.cpu().numpy(), o.grad.cpu().numpy())
 
-    img0, g0 = run(True)
-    run(False)  # plans this scene
-    img1, g1 = run(False)
-    assert np.array_equal(img0.view(np.uint32), img1.view(np.uint32))
+def _oracle(scene, cam, v_out):
+    tr, sh, opac = scene
     uo = uniforms_for(cam, SIZE[0], SIZE[1], tr.shape[0], 0)
     o = O.render_forward(uo, tr, sh, opac, O.FLAG_BWD_INFO)
-    vc = O.rasterize_backward(o, v_out, O.FLAG_REFINE_WEIGHT)
-    mags = gradient_term_magnitudes(o, tr, sh, opac, vc)
-    for name, a, b, m in zip(("v_transforms", "v_coeffs", "v_raw_opac"), g0, g1, mags):
-        assert np.all(np.isfinite(b)), name
-        grad_close(name, b, a, m, rtol=1e-4, atol_frac=1e-6)
+    return OracleGrads(o, tr, sh, opac, v_out, O.FLAG_REFINE_WEIGHT)
+
+
+def test_backward_of_a_planned_forward(ctx, gpu):
+    print("[case] backward after planned forward", flush=True)
+    scene = rng_scene(20_000, 1.5, (-2.5, -0.5), (-1.0, 2.0), 0x55)
+    cam = _cam()
+    v_out = np.random.default_rng(3).standard_normal((SIZE[1], SIZE[0], 4)).astype(np.float32)
+    img0, g0, _ = _diff(ctx, gpu, scene, cam, v_out, True)
+    _diff(ctx, gpu, scene, cam, v_out, False)  # plans this scene
+    img1, g1, res = _diff(ctx, gpu, scene, cam, v_out, False, lanes=True)
+    assert np.array_equal(img0.view(np.uint32), img1.view(np.uint32))
+    want = _oracle(scene, cam, v_out)
+    noise = {"v_transforms": want.noise_transforms, "v_coeffs": want.noise_coeffs,
+             "v_raw_opac": want.noise_raw_opac, "v_refine": want.noise_refine}
+    for name in ("v_transforms", "v_coeffs", "v_raw_opac"):
+        assert np.all(np.isfinite(g1[name])), name
+        check_close(f"{name} planned vs exact", g1[name], g0[name], noise[name], rtol=1e-4)
+    check_fused_backward("planned", res._cfg.state, *scene, g1, want)
+
+
+def test_backward_of_a_forward_that_outgrew_its_plan(ctx, gpu):
+    """A planned forward whose scene has four times the intersections its plan
+    was made for is queued again with exact sizes (its state's buffers,
+    gradient rows included, released and allocated anew); its backward
+    matches the backward of an exact-size forward and the restatement."""
+    print("[case] backward after a forward that outgrew its plan", flush=True)
+    small = rng_scene(2_000, 1.5, (-3.0, -1.5), (-1.0, 2.0), 0x51)
+    large = rng_scene(20_000, 1.5, (-2.5, -0.5), (-1.0, 2.0), 0x52)
+    cam = _cam()
+    v_out = np.random.default_rng(4).standard_normal((SIZE[1], SIZE[0], 4)).astype(np.float32)
+    img0, g0, _ = _diff(ctx, gpu, large, cam, v_out, True)
+    _diff(ctx, gpu, small, cam, v_out, False)  # the plan: the small scene
+    ctx.reset_timings()
+    ctx.set_timing(True, only="rasterize")
+    img1, g1, res = _diff(ctx, gpu, large, cam, v_out, False, lanes=True)
+    launches = ctx.read_timings().get("rasterize", (0, 0.0))[0]
+    ctx.set_timing(False)
+    assert launches == 2, "the large scene must outgrow the small scene's plan"
+    assert np.array_equal(img0.view(np.uint32), img1.view(np.uint32))
+    want = _oracle(large, cam, v_out)
+    noise = {"v_transforms": want.noise_transforms, "v_coeffs": want.noise_coeffs,
+             "v_raw_opac": want.noise_raw_opac}
+    for name in ("v_transforms", "v_coeffs", "v_raw_opac"):
+        check_close(f"{name} re-queued vs exact", g1[name], g0[name], noise[name], rtol=1e-4)
+    check_fused_backward("re-queued", res._cfg.state, *large, g1, want)

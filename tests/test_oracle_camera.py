@@ -304,3 +304,144 @@ def test_render_backward_matches_finite_differences(name):
             minus[i, k] -= eps
             fd = (loss(plus) - loss(minus)) / (2 * eps)
             assert abs(vt[i, k] - fd) <= 0.03 * abs(fd) + 0.03, f"{name} t[{i},{k}]: {vt[i, k]} vs {fd}"
+
+
+# ---- beyond the Jacobian clamp ------------------------------------------------------------------------
+#
+# Splats centred beyond 1.15 W (or -0.15 W, and likewise for H) get a
+# Jacobian evaluated at the clamped direction (camera.rs:200-254,
+# pinhole.rs:32-56, radial_tangential_8.rs:67-130).  The pinhole VJP
+# (pinhole.rs:58-123) is the exact derivative of that forward: the screen
+# position uses the unclamped point, the covariance the clamped Jacobian, so
+# d/dx of the Jacobian is zero and d/dz goes through the clamped x.  RT8's VJP
+# (radial_tangential_8.rs:155-330) differentiates a surrogate instead: the
+# projection of the clamped point c(p) = (clamp(x/z) z, clamp(y/z) z, z), and a
+# covariance J(c(p)) S V S^T J(c(p))^T with S = dc/dp (constant inside a
+# clamped region), so that no gradient moves a clamped splat along the
+# clamped axis.  Both are checked against float64 central differences, at
+# points whose normalised coordinate is 20-80 % of the limit beyond it, so no
+# step crosses the kink.
+
+
+def _clamp_points(rng, n, u, axes):
+    """Camera-space points beyond the clamp limit on the given axes ("x", "y"
+    or both), on either side, inside the limit on the others."""
+    z = rng.uniform(1.0, 6.0, n)
+    out = []
+    for ax in ("x", "y"):
+        pos, neg = float(u[f"lim_pos_{ax}"]), float(u[f"lim_neg_{ax}"])
+        if ax in axes:
+            side = rng.integers(0, 2, n)
+            t = np.where(side == 1, pos + rng.uniform(0.2, 0.8, n) * abs(pos),
+                         neg - rng.uniform(0.2, 0.8, n) * abs(neg))
+        else:
+            t = rng.uniform(0.1, 0.9, n) * np.where(rng.integers(0, 2, n) == 1, pos, neg)
+        out.append(t * z)
+    return np.stack([out[0], out[1], z], 1).astype(np.float32)
+
+
+def _clampmap(u, p):
+    """c(p) and S = dc/dp at p (float64)."""
+    lims = {ax: (float(np.float32(u[f"lim_neg_{ax}"])), float(np.float32(u[f"lim_pos_{ax}"]))) for ax in "xy"}
+    c = p.copy()
+    S = np.eye(3)
+    for i, ax in enumerate("xy"):
+        t = p[i] / p[2]
+        lo, hi = lims[ax]
+        if t < lo or t > hi:
+            tc = min(max(t, lo), hi)
+            c[i] = tc * p[2]
+            S[i, i], S[i, 2] = 0.0, tc
+    return c, S
+
+
+def _pinhole64(u, p):
+    fx, fy, cx, cy = (float(u[k]) for k in ("fx", "fy", "cx", "cy"))
+    return np.array([fx * p[0] / p[2] + cx, fy * p[1] / p[2] + cy])
+
+
+def _pinhole_jac_clamped64(u, p):
+    fx, fy = float(u["fx"]), float(u["fy"])
+    c, _ = _clampmap(u, p)
+    tx, ty = c[0] / p[2], c[1] / p[2]
+    return np.array([[fx / p[2], 0.0, -fx * tx / p[2]], [0.0, fy / p[2], -fy * ty / p[2]]])
+
+
+@pytest.mark.parametrize("axes", ["x", "y", "xy"])
+def test_clamped_pinhole_vjp_is_the_derivative_of_the_forward(axes):
+    u = _uniforms(C.PINHOLE)
+    rng = np.random.default_rng(40 + len(axes))
+    pts = _clamp_points(rng, 80, u, axes)
+    cov6, vc, vm = _vjp_inputs(rng, len(pts))
+    # the forward's Jacobian is the clamped one
+    got_j = O.camera_jacobian(u, pts)
+    for i in range(len(pts)):
+        want_j = _pinhole_jac_clamped64(u, pts[i].astype(np.float64))
+        assert np.max(np.abs(got_j[i] - want_j)) <= 1e-5 * np.abs(want_j).max(), (i, got_j[i], want_j)
+    got = O.camera_vjp(u, pts, cov6, vc, vm)
+    for i in range(len(pts)):
+        c = cov6[i].astype(np.float64)
+        S = np.array([[c[0], c[1], c[2]], [c[1], c[3], c[4]], [c[2], c[4], c[5]]])
+        V = np.array([[vc[i, 0], vc[i, 1]], [vc[i, 1], vc[i, 2]]], np.float64)
+
+        def loss(p):
+            J = _pinhole_jac_clamped64(u, p)
+            return float(vm[i].astype(np.float64) @ _pinhole64(u, p) + np.trace(V @ J @ S @ J.T))
+
+        p0 = pts[i].astype(np.float64)
+        h = 1e-5 * max(1.0, float(np.abs(p0).max()))
+        want = np.array([(loss(p0 + h * e) - loss(p0 - h * e)) / (2 * h) for e in np.eye(3)])
+        assert np.max(np.abs(got[i] - want)) <= 2e-4 * np.abs(want).max() + 1e-6, (i, got[i], want)
+    # through the covariance alone a clamped axis gets exactly zero
+    zero_vm = np.zeros_like(vm)
+    g0 = O.camera_vjp(u, pts, cov6, vc, zero_vm)
+    for i, p in enumerate(pts):
+        for k, ax in enumerate("xy"):
+            t = float(p[k]) / float(p[2])
+            if t > float(u[f"lim_pos_{ax}"]) or t < float(u[f"lim_neg_{ax}"]):
+                assert g0[i, k] == 0.0, (i, ax, g0[i])
+
+
+@pytest.mark.parametrize("heavy", [False, True])
+@pytest.mark.parametrize("axes", ["x", "y", "xy"])
+def test_clamped_rt8_vjp_is_the_derivative_of_its_surrogate(heavy, axes):
+    model = HEAVY["rt8"] if heavy else MODELS["rt8"]
+    u = _uniforms(model)
+    rng = np.random.default_rng(50 + len(axes) + (7 if heavy else 0))
+    pts = _clamp_points(rng, 60, u, axes)
+    cov6, vc, vm = _vjp_inputs(rng, len(pts))
+    got = O.camera_vjp(u, pts, cov6, vc, vm)
+    f = (float(u["fx"]), float(u["fy"]), float(u["cx"]), float(u["cy"]))
+    for i in range(len(pts)):
+        c6 = cov6[i].astype(np.float64)
+        Sig = np.array([[c6[0], c6[1], c6[2]], [c6[1], c6[3], c6[4]], [c6[2], c6[4], c6[5]]])
+        V = np.array([[vc[i, 0], vc[i, 1]], [vc[i, 1], vc[i, 2]]], np.float64)
+        p0 = pts[i].astype(np.float64)
+        _, S0 = _clampmap(u, p0)
+        # the forward's Jacobian is the model's Jacobian at the clamped point
+        c0, _ = _clampmap(u, p0)
+        want_j = _jac64("rt8", model, u, c0)
+        assert np.max(np.abs(O.camera_jacobian(u, pts[i:i + 1])[0] - want_j)) <= 1e-5 * np.abs(want_j).max()
+
+        def loss(p):
+            c, _ = _clampmap(u, p)
+            J = _jac64("rt8", model, u, c)
+            return float(vm[i].astype(np.float64) @ _project64("rt8", model, *f, c[None])[0] +
+                         np.trace(V @ J @ S0 @ Sig @ S0.T @ J.T))
+
+        def loss_open(p):
+            # the same terms without the clamp's routing: the size of what
+            # cancels when both axes are clamped (J(c(p)) S is then zero)
+            J = _jac64("rt8", model, u, p)
+            return float(vm[i].astype(np.float64) @ _project64("rt8", model, *f, p[None])[0] +
+                         np.trace(V @ J @ Sig @ J.T))
+
+        h = 1e-4 * max(1.0, float(np.abs(p0).max()))
+        want = np.array([(loss(p0 + h * e) - loss(p0 - h * e)) / (2 * h) for e in np.eye(3)])
+        terms = np.array([(loss_open(c0 + h * e) - loss_open(c0 - h * e)) / (2 * h) for e in np.eye(3)])
+        tol = 2e-3 * np.abs(want).max() + 1e-5 * np.abs(terms).max() + 1e-6
+        assert np.max(np.abs(got[i] - want)) <= tol, (i, got[i], want)
+        # a clamped axis gets no gradient at all
+        for k in range(2):
+            if S0[k, k] == 0.0:
+                assert got[i, k] == 0.0, (i, k, got[i])
