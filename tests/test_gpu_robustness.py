@@ -418,3 +418,74 @@ def test_second_backward_of_one_forward(gpu):
         assert np.abs(a).max() > 0.0, name
         check_close(f"{name} (second backward vs first)", b, a, n, rtol=1e-5)
         check_close(f"{name} (second backward)", b, ref, n)
+
+
+def _validated_diff(gpu, tr, sh, opac, cam, size, mip=False):
+    """render_splats_diff + backward of mean(image) on a context in
+    BH_DEBUG_VALIDATE mode: a non-finite parameter or gradient raises."""
+    import torch
+    from brush_amd import render as R
+
+    t = torch.from_numpy(np.ascontiguousarray(tr)).to(gpu).requires_grad_(True)
+    s = torch.from_numpy(np.ascontiguousarray(sh)).to(gpu).requires_grad_(True)
+    o = torch.from_numpy(np.ascontiguousarray(opac)).to(gpu).requires_grad_(True)
+    res = R.render_splats_diff(R.Splats(t, s, o, render_mip=mip), cam, size)
+    res.img.mean().backward()
+    torch.cuda.synchronize()
+    grads = (t.grad.cpu().numpy(), s.grad.cpu().numpy(), o.grad.cpu().numpy(), res._cfg.refine_weight.cpu().numpy())
+    for g in grads:
+        assert np.all(np.isfinite(g))
+    return res, grads
+
+
+@pytest.mark.parametrize("ls", [-20.0, -5.0, 0.0, 5.0, 15.0, 30.0, 40.0])
+def test_bwd_extreme_inputs_stay_finite(gpu, debug_ctx, ls):
+    """fuzz.rs:519-551 on the fused backward, under BH_DEBUG_VALIDATE: eight
+    splats at the origin with log-scales up to 40 and SH DC magnitudes up to
+    f32::MAX / 2 render with every splat visible and every gradient finite;
+    the forward is bit for bit the restatement's."""
+    from tests.test_oracle import STD_CAM
+
+    print(f"[case] extreme inputs log_scale={ls}", flush=True)
+    n = 8
+    tr = np.tile(np.array([0, 0, 3, 1, 0, 0, 0, ls, ls, ls], np.float32), (n, 1))
+    debug_ctx.set_debug(validate=True)
+    for mag in (0.1, 10.0, 1e6, 3.4028235e38 / 2):
+        sh = np.tile(np.array([mag, -mag, mag], np.float32), (n, 1)).reshape(n, 1, 3)
+        opac = np.full(n, 2.0, np.float32)
+        res, _ = _validated_diff(gpu, tr, sh, opac, STD_CAM, (64, 64))
+        assert res.num_visible == n, (ls, mag)
+        u = uniforms_for(STD_CAM, 64, 64, n, 0)
+        o = O.render_forward(u, tr, sh, opac, O.FLAG_BWD_INFO)
+        assert np.array_equal(res.img.detach().cpu().numpy().view(np.uint32), o.out_img.view(np.uint32)), (ls, mag)
+
+
+def test_bwd_random_scenes_gradients_are_finite(gpu, debug_ctx):
+    """fuzz.rs:492-517 on the fused backward, under BH_DEBUG_VALIDATE: 100
+    random scenes (4-255 splats) seen from cameras anywhere, image sides
+    16-127, Mip mode 30 % of the time; every gradient finite and equal to
+    the restatement's to rtol 1e-3 plus its rounding noise."""
+    from brush_amd.camera import project_uniforms
+    from tests.helpers import OracleGrads, compare_dense
+    from tests.test_oracle import _fuzz_finite_scene, _fuzz_rand_cam
+    from tests.test_oracle_fuzz import MASK64, Sm64
+
+    debug_ctx.set_debug(validate=True)
+    live = 0
+    for seed in range(100):
+        rng = Sm64(0xBDBDBDBD ^ ((seed * 0xA5A5CAFE) & MASK64))
+        n = rng.usize_in(4, 256)
+        w, h = rng.usize_in(16, 128), rng.usize_in(16, 128)
+        cam = _fuzz_rand_cam(rng)
+        mip = bool(rng.f01() < 0.3)
+        tr, sh, opac = _fuzz_finite_scene(seed, n)
+        res, g = _validated_diff(gpu, tr, sh, opac, cam, (w, h), mip)
+        u = project_uniforms(cam, w, h, n, 0)
+        flags = O.FLAG_BWD_INFO | (O.FLAG_MIP if mip else 0)
+        o = O.render_forward(u, tr, sh, opac, flags)
+        assert res.num_visible == o.num_visible, seed
+        want = OracleGrads(o, tr, sh, opac, np.full((h, w, 4), 1.0 / (h * w * 4), np.float32),
+                           O.FLAG_REFINE_WEIGHT, mip=mip)
+        compare_dense(f"seed {seed} ", {"v_transforms": g[0], "v_coeffs": g[1], "v_raw_opac": g[2]}, want)
+        live += bool(np.any(g[0] != 0))
+    assert live > 10
