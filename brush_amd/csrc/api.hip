@@ -334,7 +334,11 @@ bh_status bh_ctx_create(int device, bh_ctx** out) {
     // the allocation-free entry point's scratch on this device (looked up
     // once per device; a failure only disables that entry point)
     if (noalloc_scratch_address(device, &ctx->noalloc_scratch) != hipSuccess) ctx->noalloc_scratch = nullptr;
-    if (hipMalloc(&ctx->d_counters, 64) != hipSuccess || hipHostMalloc(&ctx->h_counters, 64) != hipSuccess ||
+    // the counters' pinned host copy is written by the reduction kernel itself
+    // (mapped, coherent host memory), so no copy runs between it and the reads
+    if (hipMalloc(&ctx->d_counters, 64) != hipSuccess ||
+        hipHostMalloc(&ctx->h_counters, 64, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess ||
+        hipHostGetDevicePointer((void**)&ctx->h_counters_dev, ctx->h_counters, 0) != hipSuccess ||
         hipEventCreateWithFlags(&ctx->counters_ready, hipEventDisableTiming) != hipSuccess) {
         (void)hipGetLastError();
         if (ctx->d_counters) (void)hipFree(ctx->d_counters);
@@ -648,10 +652,8 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
         BH_STRY(ws.get(&vis_rows, (size_t)num_splats * 12));
         launch_project_forward(ctx, u, transforms, raw_opacities, sh_coeffs, sh_degree, num_splats, mip, tile_h, counts,
                                max_radius, depth_keys, vis_rows, partials, ctx->d_counters,
-                               planned ? ctx->plan_isect_cap : 0u, pf_zero);
+                               planned ? ctx->plan_isect_cap : 0u, pf_zero, ctx->h_counters_dev);
         BH_STRY(check_launch(ctx, "project_forward"));
-        BH_STRY(hip_check(ctx, hipMemcpyAsync(ctx->h_counters, ctx->d_counters, 32, hipMemcpyDeviceToHost, ctx->stream),
-                          "count readback"));
         BH_STRY(hip_check(ctx, hipEventRecord(ctx->counters_ready, ctx->stream), "count readback"));
     }
 

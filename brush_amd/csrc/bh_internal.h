@@ -82,7 +82,8 @@ struct bh_ctx {
     // [6] depth key cap, [7] intersections when they fit the planned capacity
     uint32_t* d_counters = nullptr;
     uint32_t* h_counters = nullptr;  // pinned
-    hipEvent_t counters_ready = nullptr;  // recorded after the counters' copy to h_counters
+    uint32_t* h_counters_dev = nullptr;  // h_counters as the device addresses it
+    hipEvent_t counters_ready = nullptr;  // recorded after the reduction wrote h_counters
     // The forward's plan for the launches that depend on its counts, taken
     // from the previous forward on this context: the depth key width and the
     // intersection capacity (valid once a forward with splats has run).
@@ -202,7 +203,7 @@ void launch_project_forward(bh_ctx* ctx, const bh_project_uniforms& u, const flo
                             const float* raw_opac, const float* sh, uint32_t sh_degree, uint32_t n, bool mip,
                             uint32_t tile_h, uint32_t* intersect_counts, float* max_radius, uint32_t* depth_keys,
                             float* rows, uint32_t* partials, uint32_t* counters, uint32_t isect_cap = 0,
-                            const ZeroRanges& zero = ZeroRanges{});
+                            const ZeroRanges& zero = ZeroRanges{}, uint32_t* host_counters = nullptr);
 void launch_project_visible(bh_ctx* ctx, const float* rows, const uint32_t* gfc, uint32_t num_visible,
                             uint32_t num_splats, float* projected, float* depths);
 // Also writes compact rows `projected` [V,10] and `depths` [V] from the

@@ -226,10 +226,14 @@ __global__ __launch_bounds__(256, DEG >= 4 ? 4 : 5) void project_forward_kernel(
 // ([0] visible, [2..3] intersections, [4] min depth key, [5] max depth key),
 // and writes what launches sized before the host reads them take from there:
 // [6] the depth sort's key cap (max - min + 1) and [7] the intersection
-// count when it fits `isect_cap` (else 0).
+// count when it fits `isect_cap` (else 0).  The same eight words also go to
+// `host` (mapped, coherent pinned host memory, or null), which the host reads
+// once an event after this kernel has completed: no copy kernel runs between
+// the reduction and the host's read.
 __global__ __launch_bounds__(1024) void project_reduce_kernel(const uint32_t* __restrict__ partials,
                                                               uint32_t num_blocks, uint32_t isect_cap,
-                                                              uint32_t* __restrict__ counters) {
+                                                              uint32_t* __restrict__ counters,
+                                                              uint32_t* __restrict__ host) {
     __shared__ uint32_t s_v[16], s_mn[16], s_mx[16];
     __shared__ unsigned long long s_h[16];
     uint32_t v = 0, mn = 0xFFFFFFFFu, mx = 0u;
@@ -260,14 +264,15 @@ __global__ __launch_bounds__(1024) void project_reduce_kernel(const uint32_t* __
             mn = min(mn, s_mn[w]);
             mx = max(mx, s_mx[w]);
         }
-        counters[0] = v;
-        counters[1] = 0u;  // no device error
-        counters[2] = (uint32_t)h;
-        counters[3] = (uint32_t)(h >> 32);
-        counters[4] = mn;
-        counters[5] = mx;
-        counters[6] = mx - mn + 1u;
-        counters[7] = h <= (unsigned long long)isect_cap ? (uint32_t)h : 0u;
+        const uint32_t c[8] = {v, 0u /* no device error */, (uint32_t)h, (uint32_t)(h >> 32), mn, mx, mx - mn + 1u,
+                               h <= (unsigned long long)isect_cap ? (uint32_t)h : 0u};
+        reinterpret_cast<uint4*>(counters)[0] = make_uint4(c[0], c[1], c[2], c[3]);
+        reinterpret_cast<uint4*>(counters)[1] = make_uint4(c[4], c[5], c[6], c[7]);
+        if (host) {
+            reinterpret_cast<uint4*>(host)[0] = make_uint4(c[0], c[1], c[2], c[3]);
+            reinterpret_cast<uint4*>(host)[1] = make_uint4(c[4], c[5], c[6], c[7]);
+            __threadfence_system();
+        }
     }
 }
 
@@ -311,7 +316,7 @@ void launch_project_forward(bh_ctx* ctx, const bh_project_uniforms& u, const flo
                             const float* raw_opac, const float* sh, uint32_t sh_degree, uint32_t n, bool mip,
                             uint32_t tile_h, uint32_t* intersect_counts, float* max_radius, uint32_t* depth_keys,
                             float* rows, uint32_t* partials, uint32_t* counters, uint32_t isect_cap,
-                            const ZeroRanges& zero) {
+                            const ZeroRanges& zero, uint32_t* host_counters) {
     if (n == 0) return;
     uint32_t blocks = div_up(n, 256);
     {
@@ -330,7 +335,7 @@ void launch_project_forward(bh_ctx* ctx, const bh_project_uniforms& u, const flo
 #undef BH_PFD
     }
     KernelTimer t(ctx, "project_reduce");
-    project_reduce_kernel<<<1, 1024, 0, ctx->stream>>>(partials, blocks, isect_cap, counters);
+    project_reduce_kernel<<<1, 1024, 0, ctx->stream>>>(partials, blocks, isect_cap, counters, host_counters);
 }
 
 // ---- project_visible ------------------------------------------------------------
