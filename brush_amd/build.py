@@ -33,6 +33,8 @@ FLAGS = [
     # per-kernel VGPRs, LDS, occupancy and scratch, checked below
     "-Rpass-analysis=kernel-resource-usage",
 ]
+# the stage ranges (roctx, recorded by rocprofv3 --marker-trace)
+LINK_LIBS = ["-L/opt/rocm/lib", "-lrocprofiler-sdk-roctx", "-Wl,-rpath,/opt/rocm/lib"]
 
 
 def kernel_resources(stderr: str) -> dict:
@@ -91,7 +93,7 @@ def build(verbose: bool = True) -> str:
         for k in sorted(res):
             f.write(k + " " + " | ".join(f"{a}={b}" for a, b in res[k].items()) + "\n")
     tmp = OUT + ".tmp"
-    res = _run([HIPCC, "--offload-arch=gfx950", "-fPIC", "-shared", "-o", tmp, *[obj for obj, _ in jobs]])
+    res = _run([HIPCC, "--offload-arch=gfx950", "-fPIC", "-shared", "-o", tmp, *[obj for obj, _ in jobs], *LINK_LIBS])
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
         raise RuntimeError("hipcc failed to link libbrush_hip.so")

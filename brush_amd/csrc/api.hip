@@ -13,6 +13,8 @@
 #include <new>
 #include <string>
 
+#include <rocprofiler-sdk-roctx/roctx.h>
+
 #include "bh_internal.h"
 
 struct bh_fwd_state {
@@ -111,6 +113,9 @@ void Pool::trim() {
     free_blocks.clear();
     cached_bytes = 0;
 }
+
+StageRange::StageRange(const char* name) { roctxRangePushA(name); }
+StageRange::~StageRange() { roctxRangePop(); }
 
 KernelTimer::KernelTimer(bh_ctx* c, const char* n) : ctx(c), name(n) {
     if (!ctx->timing) return;
@@ -650,6 +655,7 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
         BH_STRY(ws.get(&depth_keys, num_splats));
         BH_STRY(ws.get((char**)&partials, project_partials_bytes(num_splats)));
         BH_STRY(ws.get(&vis_rows, (size_t)num_splats * 12));
+        StageRange stage("ProjectSplats");
         launch_project_forward(ctx, u, transforms, raw_opacities, sh_coeffs, sh_degree, num_splats, mip, tile_h, counts,
                                max_radius, depth_keys, vis_rows, partials, ctx->d_counters,
                                planned ? ctx->plan_isect_cap : 0u, pf_zero, ctx->h_counters_dev);
@@ -681,6 +687,7 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
             if (dc) dev.key_sub = dc + 4, dev.key_cap = dc + 6, dev.n_rest = dc + 0;
             dev.drop_capped = true;
             dev.n_rest_host = p.v;
+            StageRange stage("DepthSort");
             BH_TRY(radix_sort_pairs(ctx, depth_keys, nullptr, num_splats, p.key_bits, p.kmin, p.kcap, sk, gfc, tk, tv,
                                     depth_scr, "depth_sort", true, counts, counts_sorted, dev));
         }
@@ -690,10 +697,16 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
         BH_TRY(sget((void**)&tile_ids, (size_t)std::max<uint32_t>(p.m, 1u) * 4));
         BH_TRY(sget((void**)&cgids, (size_t)std::max<uint32_t>(p.m, 1u) * 4));
         if (p.v) {
-            BH_TRY(inclusive_scan(ctx, counts_sorted, cum, p.v, scan_scr, dc));
+            {
+                StageRange stage("PrefixSumGaussHits");
+                BH_TRY(inclusive_scan(ctx, counts_sorted, cum, p.v, scan_scr, dc));
+            }
             // with intersections (and always under a device plan, which sizes
             // them for at least one), map_intersects orders the rows as it reads them
-            if (p.m == 0) launch_project_visible(ctx, vis_rows, gfc, p.v, num_splats, projected, depths);
+            if (p.m == 0) {
+                StageRange stage("ProjectVisible");
+                launch_project_visible(ctx, vis_rows, gfc, p.v, num_splats, projected, depths);
+            }
             BH_TRY(check_launch(ctx, "project_visible"));
         } else {
             launch_fill_u32(ctx, (uint32_t*)projected, 0u, 10);
@@ -718,10 +731,15 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
             BH_TRY(ws.get(&uc, p.m));
             BH_TRY(ws.get(&tv, p.m));
             BH_TRY(ws.get(&scr, radix_sort_scratch_bytes(p.m, bits)));
-            launch_map_intersects(ctx, u.tile_bw, u.tile_bh, tile_h, vis_rows, gfc, num_splats, cum, p.v, projected,
+            {
+                // project_visible's rows are ordered here too (ProjectVisible)
+                StageRange stage("MapGaussiansToIntersect");
+                launch_map_intersects(ctx, u.tile_bw, u.tile_bh, tile_h, vis_rows, gfc, num_splats, cum, p.v, projected,
                                   depths, ut, k16, uc, (uint32_t*)scr, (uint32_t)radix_sort_zeroed_words(p.m, bits),
                                   dc);
+            }
             BH_TRY(check_launch(ctx, "map_intersects"));
+            StageRange stage("Tile sort");
             SortDevice dev;
             if (dc) dev.n = dc + 7;
             if (k16)
@@ -734,7 +752,11 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
             launch_fill_u32(ctx, tile_ids, 0u, 1);
             launch_fill_u32(ctx, cgids, 0u, 1);
         }
-        launch_tile_offsets(ctx, tile_ids, p.m, num_tiles, off_pre, true, dc ? dc + 7 : nullptr);
+        {
+            StageRange stage("GetTileOffsets");
+            launch_tile_offsets(ctx, tile_ids, p.m, num_tiles, off_pre, true, dc ? dc + 7 : nullptr);
+        }
+        StageRange raster_stage(p.m ? "Rasterize" : "RasterizeEmpty");
         // the blend kernel starts the tiles with the most candidates first
         uint32_t* order = nullptr;
         if (p.m) {
@@ -853,6 +875,7 @@ bh_status bh_rasterize_backward(bh_ctx* ctx, const float* out_img, const float* 
         return set_error(ctx, BH_ERR_INVALID_ARG, "rasterize_backward: null argument");
     const uint32_t tbw = div_up(img_w, BH_TILE_WIDTH);
     const uint32_t tbh = div_up(img_h, (flags & BH_FLAG_TILE_16X8) ? 8u : BH_TILE_WIDTH);
+    StageRange stage("RasterizeBackwards");
     launch_fill_u32(ctx, (uint32_t*)v_combined, 0u, (uint64_t)std::max<uint32_t>(num_visible, 1) * 11);
     if (num_visible)
         launch_rasterize_backward(ctx, img_w, img_h, tbw, tbh, background, num_visible, out_img, projected,
@@ -877,6 +900,7 @@ bh_status bh_project_backward(bh_ctx* ctx, const bh_project_uniforms* u, const f
     Scratch ws(ctx);
     uint32_t* cfg;
     BH_TRY(ws.get(&cfg, n));
+    StageRange stage("ProjectBackwards");
     launch_invert_permutation(ctx, global_from_compact_gid, u->num_visible, n, cfg);
     launch_project_backward(ctx, *u, transforms, sh_coeffs, raw_opacities, cfg, n, u->sh_degree,
                             (flags & BH_FLAG_MIP) != 0, v_combined, v_transforms, v_coeffs, v_raw_opac, v_refine);
@@ -934,6 +958,7 @@ bh_status bh_render_backward(bh_ctx* ctx, const bh_fwd_state* state, const float
         st->kept_lanes = nullptr;
     }
     const uint32_t raster_flags = (in.flags & (fwd_owned | BH_FLAG_TILE_16X8)) | (flags & BH_FLAG_REFINE_WEIGHT);
+    StageRange raster_stage("RasterizeBackwards");
     if (in.num_visible && in.num_intersections && state->record.masks) {
         // the longest tiles (most splats the forward blended) start first;
         // the order is computed while the gradient rows are zeroed
@@ -952,8 +977,11 @@ bh_status bh_render_backward(bh_ctx* ctx, const bh_fwd_state* state, const float
         if (!pre_zeroed) launch_fill_u32(ctx, (uint32_t*)rows, 0u, (uint64_t)n * 11);
     }
     BH_TRY(check_launch(ctx, "rasterize_backward"));
-    launch_project_backward(ctx, in.uniforms, transforms, sh_coeffs, raw_opacities, nullptr, n, in.sh_degree,
-                            (in.flags & BH_FLAG_MIP) != 0, rows, v_transforms, v_coeffs, v_raw_opac, v_refine);
+    {
+        StageRange stage("ProjectBackwards");
+        launch_project_backward(ctx, in.uniforms, transforms, sh_coeffs, raw_opacities, nullptr, n, in.sh_degree,
+                                (in.flags & BH_FLAG_MIP) != 0, rows, v_transforms, v_coeffs, v_raw_opac, v_refine);
+    }
     BH_TRY(check_launch(ctx, "project_backward"));
     if (keep)
         st->kept_lanes = rows;

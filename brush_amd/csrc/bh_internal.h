@@ -31,6 +31,18 @@ struct Pool {
     void trim();  // hipFree everything in the free list
 };
 
+// A named host-side range around the launches of one stage of the path,
+// named as the reference's tracing spans name them (render.rs:187-459,
+// render_bwd.rs:106-366), so a profile of this library lines up with one of
+// the reference.  rocprofv3 --marker-trace records them; without a tool
+// attached a range costs two calls that return at once.
+struct StageRange {
+    explicit StageRange(const char* name);
+    ~StageRange();
+    StageRange(const StageRange&) = delete;
+    StageRange& operator=(const StageRange&) = delete;
+};
+
 struct Timing {
     std::string name;
     hipEvent_t start, stop;

@@ -96,7 +96,7 @@ def test_c_abi_host_code_under_asan_and_ubsan(tmp_path):
     others = [o for o in objs if not o.endswith("api.o")]
     res = subprocess.run([HIPCC, "--offload-arch=gfx950", "-fPIC", "-shared", "-Xarch_host", "-fsanitize=address",
                           "-Xarch_host", "-fsanitize=undefined", "-Xarch_host", "-shared-libsan", "-o", lib, api_o,
-                          *others], capture_output=True, text=True)
+                          *others, *B.LINK_LIBS], capture_output=True, text=True)
     assert res.returncode == 0, res.stderr[-3000:]
     res = _run([sys.executable, "-m", "pytest", "-q", "-x", "-p", "no:cacheprovider", "-m", "not gpu",
                 os.path.join("tests", "test_cabi.py")], {"LD_PRELOAD": preload, "BH_LIB_PATH": lib})
