@@ -631,83 +631,70 @@ BH_DEV void sh_basis(V3 v, float* basis) {
     }
 }
 
-// sh_color_viewdir_vjp (sh.rs:249-381)
+// The z factor F(z) of the degree-l, order-m basis functions and dF/dz.
+// Every basis function of sh_to_color above is F(z) times Re or Im of
+// (x + i y)^m (cosine part at index l^2 + l + m, sine part at l^2 + l - m),
+// with these F (the forward's constants; the m = 0 one of degree 4 is its
+// recursion over degrees 3 and 2).
+BH_DEV void sh_z_factor(int l, int m, float z, float& f, float& df) {
+    const float z2 = z * z;
+    switch (l * 8 + m) {
+        case 8: f = 0.4886025f * z, df = 0.4886025f; break;
+        case 9: f = -0.4886025f, df = 0.0f; break;
+        case 16: f = 0.9461747f * z2 - 0.31539157f, df = 1.8923494f * z; break;
+        case 17: f = -1.0925485f * z, df = -1.0925485f; break;
+        case 18: f = 0.54627424f, df = 0.0f; break;
+        case 24: f = z * (1.8658817f * z2 - 1.119529f), df = 5.5976451f * z2 - 1.119529f; break;
+        case 25: f = -2.285229f * z2 + 0.4570458f, df = -4.570458f * z; break;
+        case 26: f = 1.4453057f * z, df = 1.4453057f; break;
+        case 27: f = -0.5900436f, df = 0.0f; break;
+        case 32: {
+            const float f3 = z * (1.8658817f * z2 - 1.119529f), d3 = 5.5976451f * z2 - 1.119529f;
+            const float f2 = 0.9461747f * z2 - 0.31539157f, d2 = 1.8923494f * z;
+            f = 1.9843135f * z * f3 - 1.0062306f * f2;
+            df = 1.9843135f * (f3 + z * d3) - 1.0062306f * d2;
+            break;
+        }
+        case 33: f = z * (-4.683326f * z2 + 2.0071396f), df = -14.049978f * z2 + 2.0071396f; break;
+        case 34: f = 3.3116114f * z2 - 0.47308735f, df = 6.6232228f * z; break;
+        case 35: f = -1.7701308f * z, df = -1.7701308f; break;
+        default: f = 0.62583575f, df = 0.0f; break;  // l = m = 4
+    }
+}
+
+// The colour's gradient with respect to the (unnormalised) view direction v
+// for the upstream colour gradient vc: sum over basis functions of
+// (c_k . vc) grad Y_k (sh_color_viewdir_vjp, sh.rs:249-381, computes the same
+// derivative term by term).  With Y = F(z) P_m(x, y), P_m = Re or Im of
+// (x + i y)^m: d/dx (x + i y)^m = m (x + i y)^(m-1) and d/dy = i m
+// (x + i y)^(m-1), so a cosine/sine pair of order m with weights wc, ws adds
+// F m (wc C + ws S, ws C - wc S) with C + i S = (x + i y)^(m-1) to the x and
+// y components and F' (wc Re + ws Im)((x + i y)^m) to z.
 template <int DEG>
 BH_DEV V3 sh_viewdir_vjp(const float* c, V3 v, V3 vc) {
+    // re[m] + i im[m] = (x + i y)^m
+    float re[DEG + 1], im[DEG + 1];
+    re[0] = 1.0f, im[0] = 0.0f;
+#pragma unroll
+    for (int m = 1; m <= DEG; m++) {
+        re[m] = v.x * re[m - 1] - v.y * im[m - 1];
+        im[m] = v.x * im[m - 1] + v.y * re[m - 1];
+    }
     float gx = 0.0f, gy = 0.0f, gz = 0.0f;
-    if (DEG >= 1) {
-        const float f0a = 0.4886025f;
-        float s_n1 = dot(rd3(c, 1), vc), s_z0 = dot(rd3(c, 2), vc), s_p1 = dot(rd3(c, 3), vc);
-        gx += -f0a * s_p1;
-        gy += -f0a * s_n1;
-        gz += f0a * s_z0;
-        if (DEG >= 2) {
-            float z = v.z, x = v.x, y = v.y;
-            const float c2 = -1.0925485f;
-            const float f1a = 0.54627424f;
-            float s_n2 = dot(rd3(c, 4), vc);
-            s_n1 = dot(rd3(c, 5), vc);
-            s_z0 = dot(rd3(c, 6), vc);
-            s_p1 = dot(rd3(c, 7), vc);
-            float s_p2 = dot(rd3(c, 8), vc);
-            gx += 2.0f * f1a * y * s_n2 + c2 * z * s_p1 + 2.0f * f1a * x * s_p2;
-            gy += 2.0f * f1a * x * s_n2 + c2 * z * s_n1 - 2.0f * f1a * y * s_p2;
-            gz += c2 * y * s_n1 + 2.0f * 0.9461747f * z * s_z0 + c2 * x * s_p1;
-            if (DEG >= 3) {
-                float z2 = z * z, x2 = x * x, y2 = y * y;
-                const float f2a = -0.5900436f;
-                const float c1b = 1.4453057f;
-                float f1b = c1b * z;
-                const float c0c = -2.285229f;
-                float f0c = c0c * z2 + 0.4570458f;
-                float f0c_dz = 2.0f * c0c * z;
-                float s_n3 = dot(rd3(c, 9), vc);
-                s_n2 = dot(rd3(c, 10), vc);
-                s_n1 = dot(rd3(c, 11), vc);
-                s_z0 = dot(rd3(c, 12), vc);
-                s_p1 = dot(rd3(c, 13), vc);
-                s_p2 = dot(rd3(c, 14), vc);
-                float s_p3 = dot(rd3(c, 15), vc);
-                float d12_z = 3.0f * 1.8658817f * z2 - 1.119529f;
-                gx += f2a * 6.0f * x * y * s_n3 + 2.0f * f1b * y * s_n2 + f0c * s_p1 + 2.0f * f1b * x * s_p2 +
-                      f2a * 3.0f * (x2 - y2) * s_p3;
-                gy += f2a * 3.0f * (x2 - y2) * s_n3 + 2.0f * f1b * x * s_n2 + f0c * s_n1 + (-2.0f) * f1b * y * s_p2 +
-                      f2a * (-6.0f) * x * y * s_p3;
-                gz += 2.0f * c1b * x * y * s_n2 + f0c_dz * y * s_n1 + d12_z * s_z0 + f0c_dz * x * s_p1 +
-                      c1b * (x2 - y2) * s_p2;
-                if (DEG >= 4) {
-                    float fc1 = x2 - y2;
-                    float fs1 = 2.0f * x * y;
-                    float fc2 = x * fc1 - y * fs1;
-                    float fs2 = x * fs1 + y * fc1;
-                    float f0d = z * (-4.683326f * z2 + 2.0071396f);
-                    float f0d_dz = -14.049978f * z2 + 2.0071396f;
-                    float f1c = 3.3116114f * z2 - 0.47308735f;
-                    float f1c_dz = 2.0f * 3.3116114f * z;
-                    const float f2b_dz = -1.7701308f;
-                    float f2b = f2b_dz * z;
-                    const float f3a = 0.62583575f;
-                    float p12 = z * (1.8658817f * z2 - 1.119529f);
-                    float dp12 = 3.0f * 1.8658817f * z2 - 1.119529f;
-                    float dp6 = 2.0f * 0.9461747f * z;
-                    float dp20 = 1.9843135f * (p12 + z * dp12) - 1.0062306f * dp6;
-                    float s_n4 = dot(rd3(c, 16), vc);
-                    s_n3 = dot(rd3(c, 17), vc);
-                    s_n2 = dot(rd3(c, 18), vc);
-                    s_n1 = dot(rd3(c, 19), vc);
-                    s_z0 = dot(rd3(c, 20), vc);
-                    s_p1 = dot(rd3(c, 21), vc);
-                    s_p2 = dot(rd3(c, 22), vc);
-                    s_p3 = dot(rd3(c, 23), vc);
-                    float s_p4 = dot(rd3(c, 24), vc);
-                    gx += f3a * 4.0f * fs2 * s_n4 + f2b * 3.0f * fs1 * s_n3 + f1c * 2.0f * y * s_n2 + f0d * s_p1 +
-                          f1c * 2.0f * x * s_p2 + f2b * 3.0f * fc1 * s_p3 + f3a * 4.0f * fc2 * s_p4;
-                    gy += f3a * 4.0f * fc2 * s_n4 + f2b * 3.0f * fc1 * s_n3 + f1c * 2.0f * x * s_n2 + f0d * s_n1 +
-                          f1c * (-2.0f) * y * s_p2 + f2b * (-3.0f) * fs1 * s_p3 + f3a * (-4.0f) * fs2 * s_p4;
-                    gz += f2b_dz * fs2 * s_n3 + f1c_dz * fs1 * s_n2 + f0d_dz * y * s_n1 + dp20 * s_z0 +
-                          f0d_dz * x * s_p1 + f1c_dz * fc1 * s_p2 + f2b_dz * fc2 * s_p3;
-                }
-            }
+#pragma unroll
+    for (int l = 1; l <= DEG; l++) {
+        const int k0 = l * l + l;
+        float f, df;
+        sh_z_factor(l, 0, v.z, f, df);
+        gz += df * dot(rd3(c, k0), vc);
+#pragma unroll
+        for (int m = 1; m <= l; m++) {
+            sh_z_factor(l, m, v.z, f, df);
+            const float wc = dot(rd3(c, k0 + m), vc), ws = dot(rd3(c, k0 - m), vc);
+            const float fm = f * (float)m;
+            gx += fm * (wc * re[m - 1] + ws * im[m - 1]);
+            gy += fm * (ws * re[m - 1] - wc * im[m - 1]);
+            gz += df * (wc * re[m] + ws * im[m]);
         }
     }
     return v3(gx, gy, gz);
@@ -715,36 +702,40 @@ BH_DEV V3 sh_viewdir_vjp(const float* c, V3 v, V3 vc) {
 
 // ---- projection backward pieces (project_backwards.rs) -------------------------
 
-// apply_normalize_vjp (:19-52)
+// Gradient through q -> q / |q| (apply_normalize_vjp, project_backwards.rs:
+// 19-52): the Jacobian (I - q q^T / |q|^2) / |q| applied to g, i.e.
+// (|q|^2 g - (q . g) q) / |q|^3.
 BH_DEV Q4 normalize_vjp(Q4 q, Q4 g) {
-    float lsq = qdot(q, q);
-    float l = sqrtf(lsq);
-    float inv = 1.0f / (l * lsq);
-    float cc0 = -q.w * q.x, cc1 = -q.x * q.y, cc2 = -q.y * q.w;
-    float cs0 = -q.w * q.z, cs1 = -q.x * q.z, cs2 = -q.y * q.z;
-    float sw = q.w * q.w, sx = q.x * q.x, sy = q.y * q.y, sz = q.z * q.z;
-    Q4 r;
-    r.w = ((lsq - sw) * g.w + cc0 * g.x + cc2 * g.y + cs0 * g.z) * inv;
-    r.x = (cc0 * g.w + (lsq - sx) * g.x + cc1 * g.y + cs1 * g.z) * inv;
-    r.y = (cc2 * g.w + cc1 * g.x + (lsq - sy) * g.y + cs2 * g.z) * inv;
-    r.z = (cs0 * g.w + cs1 * g.x + cs2 * g.y + (lsq - sz) * g.z) * inv;
-    return r;
+    const float n2 = qdot(q, q);
+    const float qg = qdot(q, g);
+    const float s = 1.0f / (sqrtf(n2) * n2);
+    return Q4{(n2 * g.w - qg * q.w) * s, (n2 * g.x - qg * q.x) * s, (n2 * g.y - qg * q.y) * s,
+              (n2 * g.z - qg * q.z) * s};
 }
-// quat_to_mat_vjp (:54-79)
+// Gradient of sum_ab V_ab R_ab(q) through the rotation matrix of a unit
+// quaternion (quat_to_mat_vjp, project_backwards.rs:54-79).  The entries of R
+// are 1 - 2(y^2 + z^2) on the diagonal and 2(xy -+ wz), 2(xz +- wy),
+// 2(yz -+ wx) off it, so w meets only the antisymmetric part of V and each of
+// x, y, z the symmetric part plus its own diagonal pair.  V is column-major
+// (cI_R = V[R][I]).
 BH_DEV Q4 quat_to_mat_vjp(Q4 q, const M3& v) {
-    float w_grad = q.x * (v.c1z - v.c2y) + q.y * (v.c2x - v.c0z) + q.z * (v.c0y - v.c1x);
-    float x_grad = -2.0f * q.x * (v.c1y + v.c2z) + q.y * (v.c0y + v.c1x) + q.z * (v.c0z + v.c2x) + q.w * (v.c1z - v.c2y);
-    float y_grad = q.x * (v.c0y + v.c1x) - 2.0f * q.y * (v.c0x + v.c2z) + q.z * (v.c1z + v.c2y) + q.w * (v.c2x - v.c0z);
-    float z_grad = q.x * (v.c0z + v.c2x) + q.y * (v.c1z + v.c2y) - 2.0f * q.z * (v.c0x + v.c1y) + q.w * (v.c0y - v.c1x);
-    return Q4{2.0f * w_grad, 2.0f * x_grad, 2.0f * y_grad, 2.0f * z_grad};
+    const float a_zy = v.c1z - v.c2y, a_xz = v.c2x - v.c0z, a_yx = v.c0y - v.c1x;  // V - V^T
+    const float s_xy = v.c1x + v.c0y, s_xz = v.c2x + v.c0z, s_yz = v.c2y + v.c1z;  // V + V^T
+    const float gw = q.x * a_zy + q.y * a_xz + q.z * a_yx;
+    const float gx = q.w * a_zy + q.y * s_xy + q.z * s_xz - 2.0f * q.x * (v.c1y + v.c2z);
+    const float gy = q.w * a_xz + q.x * s_xy + q.z * s_yz - 2.0f * q.y * (v.c0x + v.c2z);
+    const float gz = q.w * a_yx + q.x * s_xz + q.y * s_yz - 2.0f * q.z * (v.c0x + v.c1y);
+    return Q4{2.0f * gw, 2.0f * gx, 2.0f * gy, 2.0f * gz};
 }
-// inverse2x2_vjp (:81-99)
+// Gradient through the inverse of a symmetric 2x2 matrix (inverse2x2_vjp,
+// project_backwards.rs:81-99): with C = M^-1 (here `m`, the conic) and V the
+// symmetric gradient with respect to C, dL/dM = -C V C, expanded entry by
+// entry for C = [[a, b], [b, c]], V = [[p, q], [q, r]].
 BH_DEV S2 inverse2x2_vjp(const S2& m, const S2& v) {
-    float t00 = -m.c00 * v.c00 + -m.c01 * v.c01;
-    float t01 = -m.c01 * v.c00 + -m.c11 * v.c01;
-    float t10 = -m.c00 * v.c01 + -m.c01 * v.c11;
-    float t11 = -m.c01 * v.c01 + -m.c11 * v.c11;
-    return S2{t00 * m.c00 + t10 * m.c01, t01 * m.c00 + t11 * m.c01, t01 * m.c01 + t11 * m.c11};
+    const float a = m.c00, b = m.c01, c = m.c11, p = v.c00, q = v.c01, r = v.c11;
+    const float ab = a * b, bc = b * c;
+    return S2{-(a * a * p + 2.0f * ab * q + b * b * r), -(ab * p + (b * b + a * c) * q + bc * r),
+              -(b * b * p + 2.0f * bc * q + c * c * r)};
 }
 // calculate_projection_vjp_pinhole (camera_model/pinhole.rs:58-123)
 BH_DEV V3 projection_vjp_pinhole(const bh_project_uniforms& u, const M23& J, V3 mean_c, const S3& cov_c, const S2& v_cov2d,

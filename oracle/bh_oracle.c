@@ -1218,38 +1218,39 @@ void or_rasterize_backward_f64(uint32_t img_w, uint32_t img_h, uint32_t tile_bw,
 /* project_backwards (brush-render-bwd/src/kernels/project_backwards.rs)     */
 /* ------------------------------------------------------------------------ */
 
-/* apply_normalize_vjp (:19-52) */
+/* Gradient through q -> q / |q| (apply_normalize_vjp, :19-52): the Jacobian
+ * (I - q q^T / |q|^2) / |q| applied to g, (|q|^2 g - (q . g) q) / |q|^3.
+ * Written as the product's kernels write it, so both give the same bits. */
 static qt normalize_vjp(qt q, qt g) {
-    float lsq = qdot(q, q);
-    float l = sqrtf(lsq);
-    float inv = 1.0f / (l * lsq);
-    float cc0 = -q.w * q.x, cc1 = -q.x * q.y, cc2 = -q.y * q.w;
-    float cs0 = -q.w * q.z, cs1 = -q.x * q.z, cs2 = -q.y * q.z;
-    float sw = q.w * q.w, sx = q.x * q.x, sy = q.y * q.y, sz = q.z * q.z;
-    qt r;
-    r.w = ((lsq - sw) * g.w + cc0 * g.x + cc2 * g.y + cs0 * g.z) * inv;
-    r.x = (cc0 * g.w + (lsq - sx) * g.x + cc1 * g.y + cs1 * g.z) * inv;
-    r.y = (cc2 * g.w + cc1 * g.x + (lsq - sy) * g.y + cs2 * g.z) * inv;
-    r.z = (cs0 * g.w + cs1 * g.x + cs2 * g.y + (lsq - sz) * g.z) * inv;
+    float n2 = qdot(q, q);
+    float qg = qdot(q, g);
+    float s = 1.0f / (sqrtf(n2) * n2);
+    qt r = {(n2 * g.w - qg * q.w) * s, (n2 * g.x - qg * q.x) * s, (n2 * g.y - qg * q.y) * s,
+            (n2 * g.z - qg * q.z) * s};
     return r;
 }
-/* quat_to_mat_vjp (:54-79) */
+/* Gradient of sum_ab V_ab R_ab(q) through the rotation matrix of a unit
+ * quaternion (quat_to_mat_vjp, :54-79): w meets the antisymmetric part of V,
+ * x, y, z the symmetric part plus their own diagonal pairs. */
 static qt quat_to_mat_vjp(qt q, m3 v) {
-    float w_grad = q.x * (v.c1z - v.c2y) + q.y * (v.c2x - v.c0z) + q.z * (v.c0y - v.c1x);
-    float x_grad = -2.0f * q.x * (v.c1y + v.c2z) + q.y * (v.c0y + v.c1x) + q.z * (v.c0z + v.c2x) + q.w * (v.c1z - v.c2y);
-    float y_grad = q.x * (v.c0y + v.c1x) - 2.0f * q.y * (v.c0x + v.c2z) + q.z * (v.c1z + v.c2y) + q.w * (v.c2x - v.c0z);
-    float z_grad = q.x * (v.c0z + v.c2x) + q.y * (v.c1z + v.c2y) - 2.0f * q.z * (v.c0x + v.c1y) + q.w * (v.c0y - v.c1x);
-    qt r = {2.0f * w_grad, 2.0f * x_grad, 2.0f * y_grad, 2.0f * z_grad};
+    float a_zy = v.c1z - v.c2y, a_xz = v.c2x - v.c0z, a_yx = v.c0y - v.c1x;
+    float s_xy = v.c1x + v.c0y, s_xz = v.c2x + v.c0z, s_yz = v.c2y + v.c1z;
+    float gw = q.x * a_zy + q.y * a_xz + q.z * a_yx;
+    float gx = q.w * a_zy + q.y * s_xy + q.z * s_xz - 2.0f * q.x * (v.c1y + v.c2z);
+    float gy = q.w * a_xz + q.x * s_xy + q.z * s_yz - 2.0f * q.y * (v.c0x + v.c2z);
+    float gz = q.w * a_yx + q.x * s_xz + q.y * s_yz - 2.0f * q.z * (v.c0x + v.c1y);
+    qt r = {2.0f * gw, 2.0f * gx, 2.0f * gy, 2.0f * gz};
     return r;
 }
-/* inverse2x2_vjp (:81-99) */
+/* Gradient through the inverse of a symmetric 2x2 matrix (inverse2x2_vjp,
+ * :81-99): dL/dM = -C V C with C = M^-1 = [[a, b], [b, c]] and V = [[p, q],
+ * [q, r]], expanded entry by entry. */
 static s2 inverse2x2_vjp(s2 m, s2 v) {
-    float t00 = -m.c00 * v.c00 + -m.c01 * v.c01;
-    float t01 = -m.c01 * v.c00 + -m.c11 * v.c01;
-    float t10 = -m.c00 * v.c01 + -m.c01 * v.c11;
-    float t11 = -m.c01 * v.c01 + -m.c11 * v.c11;
-    s2 r = {t00 * m.c00 + t10 * m.c01, t01 * m.c00 + t11 * m.c01, t01 * m.c01 + t11 * m.c11};
-    return r;
+    float a = m.c00, b = m.c01, c = m.c11, p = v.c00, q = v.c01, r = v.c11;
+    float ab = a * b, bc = b * c;
+    s2 o = {-(a * a * p + 2.0f * ab * q + b * b * r), -(ab * p + (b * b + a * c) * q + bc * r),
+            -(b * b * p + 2.0f * bc * q + c * c * r)};
+    return o;
 }
 /* calculate_projection_vjp_pinhole (camera_model/pinhole.rs:58-123) */
 static v3 pinhole_projection_vjp(const bh_project_uniforms* u, m23 J, v3 mean_c, s3 cov_c, s2 v_cov2d,
@@ -1582,76 +1583,59 @@ static void sh_color_vjp(float* o, uint32_t deg, v3 v, v3 vc) {
         }
     }
 }
-/* sh_color_viewdir_vjp (kernels/sh.rs:249-381) */
+/* The z factor F(z) of the degree-l, order-m SH basis functions and dF/dz:
+ * every basis function of sh_to_color is F(z) times Re or Im of (x + i y)^m
+ * (cosine part at index l^2 + l + m, sine part at l^2 + l - m). */
+static void sh_z_factor(int l, int m, float z, float* f, float* df) {
+    float z2 = z * z;
+    switch (l * 8 + m) {
+        case 8: *f = 0.4886025f * z, *df = 0.4886025f; break;
+        case 9: *f = -0.4886025f, *df = 0.0f; break;
+        case 16: *f = 0.9461747f * z2 - 0.31539157f, *df = 1.8923494f * z; break;
+        case 17: *f = -1.0925485f * z, *df = -1.0925485f; break;
+        case 18: *f = 0.54627424f, *df = 0.0f; break;
+        case 24: *f = z * (1.8658817f * z2 - 1.119529f), *df = 5.5976451f * z2 - 1.119529f; break;
+        case 25: *f = -2.285229f * z2 + 0.4570458f, *df = -4.570458f * z; break;
+        case 26: *f = 1.4453057f * z, *df = 1.4453057f; break;
+        case 27: *f = -0.5900436f, *df = 0.0f; break;
+        case 32: {
+            float f3 = z * (1.8658817f * z2 - 1.119529f), d3 = 5.5976451f * z2 - 1.119529f;
+            float f2 = 0.9461747f * z2 - 0.31539157f, d2 = 1.8923494f * z;
+            *f = 1.9843135f * z * f3 - 1.0062306f * f2;
+            *df = 1.9843135f * (f3 + z * d3) - 1.0062306f * d2;
+            break;
+        }
+        case 33: *f = z * (-4.683326f * z2 + 2.0071396f), *df = -14.049978f * z2 + 2.0071396f; break;
+        case 34: *f = 3.3116114f * z2 - 0.47308735f, *df = 6.6232228f * z; break;
+        case 35: *f = -1.7701308f * z, *df = -1.7701308f; break;
+        default: *f = 0.62583575f, *df = 0.0f; break;
+    }
+}
+/* The colour's gradient with respect to the view direction (the derivative
+ * sh_color_viewdir_vjp, kernels/sh.rs:249-381, takes term by term): a pair of
+ * order m with weights wc, ws (the coefficient rows dotted with the colour
+ * gradient) adds F m (wc C + ws S, ws C - wc S) with C + i S = (x + i y)^(m-1)
+ * to x and y, and F' (wc Re + ws Im)((x + i y)^m) to z. */
 static v3 sh_viewdir_vjp(const float* c, uint32_t deg, v3 v, v3 vc) {
+    float re[5], im[5];
+    re[0] = 1.0f, im[0] = 0.0f;
+    for (uint32_t m = 1; m <= deg; m++) {
+        re[m] = v.x * re[m - 1] - v.y * im[m - 1];
+        im[m] = v.x * im[m - 1] + v.y * re[m - 1];
+    }
     float gx = 0.0f, gy = 0.0f, gz = 0.0f;
-    if (deg >= 1) {
-        float f0a = 0.4886025f;
-        float s_n1 = dot3(rd3(c, 1), vc), s_z0 = dot3(rd3(c, 2), vc), s_p1 = dot3(rd3(c, 3), vc);
-        gx += -f0a * s_p1;
-        gy += -f0a * s_n1;
-        gz += f0a * s_z0;
-        if (deg >= 2) {
-            float z = v.z, x = v.x, y = v.y;
-            float c2 = -1.0925485f;
-            float f1a = 0.54627424f;
-            float s_n2 = dot3(rd3(c, 4), vc);
-            s_n1 = dot3(rd3(c, 5), vc);
-            s_z0 = dot3(rd3(c, 6), vc);
-            s_p1 = dot3(rd3(c, 7), vc);
-            float s_p2 = dot3(rd3(c, 8), vc);
-            gx += 2.0f * f1a * y * s_n2 + c2 * z * s_p1 + 2.0f * f1a * x * s_p2;
-            gy += 2.0f * f1a * x * s_n2 + c2 * z * s_n1 - 2.0f * f1a * y * s_p2;
-            gz += c2 * y * s_n1 + 2.0f * 0.9461747f * z * s_z0 + c2 * x * s_p1;
-            if (deg >= 3) {
-                float z2 = z * z, x2 = x * x, y2 = y * y;
-                float f2a = -0.5900436f;
-                float c1b = 1.4453057f;
-                float f1b = c1b * z;
-                float c0c = -2.285229f;
-                float f0c = c0c * z2 + 0.4570458f;
-                float f0c_dz = 2.0f * c0c * z;
-                float s_n3 = dot3(rd3(c, 9), vc);
-                s_n2 = dot3(rd3(c, 10), vc);
-                s_n1 = dot3(rd3(c, 11), vc);
-                s_z0 = dot3(rd3(c, 12), vc);
-                s_p1 = dot3(rd3(c, 13), vc);
-                s_p2 = dot3(rd3(c, 14), vc);
-                float s_p3 = dot3(rd3(c, 15), vc);
-                float d12_z = 3.0f * 1.8658817f * z2 - 1.119529f;
-                gx += f2a * 6.0f * x * y * s_n3 + 2.0f * f1b * y * s_n2 + f0c * s_p1 + 2.0f * f1b * x * s_p2 + f2a * 3.0f * (x2 - y2) * s_p3;
-                gy += f2a * 3.0f * (x2 - y2) * s_n3 + 2.0f * f1b * x * s_n2 + f0c * s_n1 + (-2.0f) * f1b * y * s_p2 + f2a * (-6.0f) * x * y * s_p3;
-                gz += 2.0f * c1b * x * y * s_n2 + f0c_dz * y * s_n1 + d12_z * s_z0 + f0c_dz * x * s_p1 + c1b * (x2 - y2) * s_p2;
-                if (deg >= 4) {
-                    float fc1 = x2 - y2;
-                    float fs1 = 2.0f * x * y;
-                    float fc2 = x * fc1 - y * fs1;
-                    float fs2 = x * fs1 + y * fc1;
-                    float f0d = z * (-4.683326f * z2 + 2.0071396f);
-                    float f0d_dz = -14.049978f * z2 + 2.0071396f;
-                    float f1c = 3.3116114f * z2 - 0.47308735f;
-                    float f1c_dz = 2.0f * 3.3116114f * z;
-                    float f2b_dz_const = -1.7701308f;
-                    float f2b = f2b_dz_const * z;
-                    float f3a = 0.62583575f;
-                    float p12 = z * (1.8658817f * z2 - 1.119529f);
-                    float dp12 = 3.0f * 1.8658817f * z2 - 1.119529f;
-                    float dp6 = 2.0f * 0.9461747f * z;
-                    float dp20 = 1.9843135f * (p12 + z * dp12) - 1.0062306f * dp6;
-                    float s_n4 = dot3(rd3(c, 16), vc);
-                    s_n3 = dot3(rd3(c, 17), vc);
-                    s_n2 = dot3(rd3(c, 18), vc);
-                    s_n1 = dot3(rd3(c, 19), vc);
-                    s_z0 = dot3(rd3(c, 20), vc);
-                    s_p1 = dot3(rd3(c, 21), vc);
-                    s_p2 = dot3(rd3(c, 22), vc);
-                    s_p3 = dot3(rd3(c, 23), vc);
-                    float s_p4 = dot3(rd3(c, 24), vc);
-                    gx += f3a * 4.0f * fs2 * s_n4 + f2b * 3.0f * fs1 * s_n3 + f1c * 2.0f * y * s_n2 + f0d * s_p1 + f1c * 2.0f * x * s_p2 + f2b * 3.0f * fc1 * s_p3 + f3a * 4.0f * fc2 * s_p4;
-                    gy += f3a * 4.0f * fc2 * s_n4 + f2b * 3.0f * fc1 * s_n3 + f1c * 2.0f * x * s_n2 + f0d * s_n1 + f1c * (-2.0f) * y * s_p2 + f2b * (-3.0f) * fs1 * s_p3 + f3a * (-4.0f) * fs2 * s_p4;
-                    gz += f2b_dz_const * fs2 * s_n3 + f1c_dz * fs1 * s_n2 + f0d_dz * y * s_n1 + dp20 * s_z0 + f0d_dz * x * s_p1 + f1c_dz * fc1 * s_p2 + f2b_dz_const * fc2 * s_p3;
-                }
-            }
+    for (int l = 1; l <= (int)deg; l++) {
+        int k0 = l * l + l;
+        float f, df;
+        sh_z_factor(l, 0, v.z, &f, &df);
+        gz += df * dot3(rd3(c, (uint32_t)k0), vc);
+        for (int m = 1; m <= l; m++) {
+            sh_z_factor(l, m, v.z, &f, &df);
+            float wc = dot3(rd3(c, (uint32_t)(k0 + m)), vc), ws = dot3(rd3(c, (uint32_t)(k0 - m)), vc);
+            float fm = f * (float)m;
+            gx += fm * (wc * re[m - 1] + ws * im[m - 1]);
+            gy += fm * (ws * re[m - 1] - wc * im[m - 1]);
+            gz += df * (wc * re[m] + ws * im[m]);
         }
     }
     return mk3(gx, gy, gz);
