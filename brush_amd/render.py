@@ -189,11 +189,16 @@ class RenderAux:
 @dataclass
 class RenderOutput:
     """render_aux.rs:17-26.  The count-sized buffers are copied out of the
-    forward state on first access."""
+    forward state on first access, and the uniforms turned into a dict on
+    first access."""
     out_img: torch.Tensor
     aux: RenderAux
-    project_uniforms: dict
+    uniforms: _lib.Uniforms = field(repr=False)
     state: ForwardState = field(repr=False)
+
+    @property
+    def project_uniforms(self) -> dict:
+        return self.uniforms.to_dict()
 
     @property
     def projected_splats(self) -> torch.Tensor:
@@ -230,6 +235,35 @@ class RenderOutput:
         return self.state.tensor("tile_offsets_pre", (tbh, tbw, 2), torch.int32)
 
 
+_UNIFORMS_CACHE: dict = {}
+_UNIFORMS_CACHE_MAX = 64
+
+
+def _camera_uniforms(camera: Camera, img_w: int, img_h: int, n: int, degree: int, tile_h: int) -> Uniforms:
+    """ProjectUniforms of a camera and frame (camera.rs:63-119, 200-254 in
+    project_uniforms), kept for the last few cameras: a training or viewer
+    loop renders the same camera many times, and the host-side camera maths
+    (float64 fov/focal conversions, the world-to-camera inverse, the clamp
+    limits) would otherwise run every call.  The key holds every field the
+    uniforms depend on; the cached struct is read-only to its users."""
+    try:
+        key = (tuple(float(x) for x in camera.position), tuple(float(x) for x in camera.rotation),
+               float(camera.fov_x), float(camera.fov_y), tuple(float(x) for x in camera.center_uv),
+               repr(camera.camera_model), img_w, img_h, n, degree, tile_h)
+    except TypeError:
+        key = None
+    u = _UNIFORMS_CACHE.get(key) if key is not None else None
+    if u is None:
+        ud = project_uniforms(camera, img_w, img_h, n, degree)
+        ud["tile_bw"], ud["tile_bh"] = tile_bounds(img_w, img_h, tile_h)
+        u = Uniforms.from_dict(ud)
+        if key is not None:
+            if len(_UNIFORMS_CACHE) >= _UNIFORMS_CACHE_MAX:
+                _UNIFORMS_CACHE.pop(next(iter(_UNIFORMS_CACHE)))
+            _UNIFORMS_CACHE[key] = u
+    return u
+
+
 def render(camera: Camera, img_size, transforms: torch.Tensor, sh_coeffs: torch.Tensor,
            raw_opacities: torch.Tensor, render_mode: SplatRenderMode = SplatRenderMode.Default,
            raster_mode: RasterizationMode = RasterizationMode.Rgba, background=(0.0, 0.0, 0.0),
@@ -258,10 +292,13 @@ def render(camera: Camera, img_size, transforms: torch.Tensor, sh_coeffs: torch.
     sh_coeffs = sh_coeffs.contiguous()
     raw_opacities = raw_opacities.contiguous()
 
-    ud = dict(uniforms) if uniforms is not None else project_uniforms(camera, img_w, img_h, n, degree)
-    ud["img_w"], ud["img_h"] = img_w, img_h
-    ud["tile_bw"], ud["tile_bh"] = tile_bounds(img_w, img_h, rasterizer.tile_height)
-    u = Uniforms.from_dict(ud)
+    if uniforms is not None:
+        ud = dict(uniforms)
+        ud["img_w"], ud["img_h"] = img_w, img_h
+        ud["tile_bw"], ud["tile_bh"] = tile_bounds(img_w, img_h, rasterizer.tile_height)
+        u = Uniforms.from_dict(ud)
+    else:
+        u = _camera_uniforms(camera, img_w, img_h, n, degree, rasterizer.tile_height)
     flags = _flags(render_mode, raster_mode, raster_pass) | rasterizer.flag
     depth = (flags & _lib.FLAG_RENDER_DEPTH) != 0
     with torch.cuda.device(device):
@@ -286,8 +323,7 @@ def render(camera: Camera, img_size, transforms: torch.Tensor, sh_coeffs: torch.
     info = state.info
     aux = RenderAux(int(info.num_visible), int(info.num_intersections), visible, max_radius, tile_offsets,
                     (img_w, img_h))
-    pu = info.uniforms.to_dict()
-    return RenderOutput(out_img, aux, pu, state)
+    return RenderOutput(out_img, aux, info.uniforms, state)
 
 
 @dataclass
