@@ -17,8 +17,8 @@ backward, AdamScaled on every splat parameter) at 1600x1064.
 
 Prints one JSON line (the driver's contract).  ``roofline`` reports the kernel
 with the largest share of the step: its algorithmic bytes per launch divided by
-its mean launch time (HIP events on the library's stream, recorded in the timed
-region around that kernel only), against 8 TB/s; ``traffic`` is the HBM bytes
+its mean launch time (HIP events on the library's stream bound to that kernel's
+dispatch, in the timed region, on every fifth step by default), against 8 TB/s; ``traffic`` is the HBM bytes
 per launch that rocprofv3 FETCH_SIZE / WRITE_SIZE measured for it
 (profiles/cfg1_hbm_traffic.md).  ``kernels`` is a per-kernel table from a short
 separate pass with every launch bracketed by events.  ``cpu_baseline`` times the
@@ -360,7 +360,89 @@ def bench_ply(args):
     print(json.dumps(line))
 
 
+def _trace_dispatches(path: str) -> list:
+    """(start_ns, end_ns, kernel name) of every dispatch in a rocprofv3 kernel
+    trace: a rocpd database (``*_results.db``, the default output) or a csv
+    kernel trace (``*_kernel_trace.csv``), in start order."""
+    import re
+
+    rows = []
+    if path.endswith(".db"):
+        import sqlite3
+
+        con = sqlite3.connect(f"file:{path}?mode=ro", uri=True)
+        for name, start, end in con.execute("select name, start, end from kernels"):
+            rows.append((int(start), int(end), name))
+        con.close()
+    else:
+        import csv
+
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
+    short = lambda n: re.sub(r"[<(].*", "", n.replace("void ", "")).strip()
+    typed = lambda n: re.sub(r"\(.*", "", n.replace("void ", "")).strip()
+    return sorted((a, b, short(n), typed(n)) for a, b, n in rows)
+
+
+def split_trace(path: str, steps: int, first_kernel: str = "bh::project_forward_kernel") -> str:
+    """Split the last ``steps`` steps of a bench.py run's kernel trace into the
+    time the GPU ran kernels and the time it sat idle, as a markdown summary
+    (with each kernel's share of the timed steps).
+
+    A step starts at its ``first_kernel`` dispatch and lasts until the next
+    step's (the last one until its final dispatch ends); bench.py launches no
+    GPU work after its timed region, so the last ``steps`` steps of the trace
+    are the timed ones.  Idle time is grouped by the pair of kernels around
+    each gap, which names the host work the GPU waited for."""
+    rows = _trace_dispatches(path)
+    starts = [i for i, r in enumerate(rows) if r[2] == first_kernel]
+    if len(starts) < steps:
+        raise SystemExit(f"{path}: {len(starts)} steps in the trace, fewer than {steps}")
+    sel = starts[-steps:]
+    spans, busys, gaps, counts, per_kernel = [], [], {}, {}, {}
+    for k, s in enumerate(sel):
+        e = sel[k + 1] if k + 1 < len(sel) else len(rows)
+        seg = rows[s:e]
+        stop = rows[e][0] if e < len(rows) else max(r[1] for r in seg)
+        busy, cur = 0, seg[0][0]
+        for a, b, _, name in seg:
+            busy += max(0, b - max(a, cur))
+            cur = max(cur, b)
+            n, t = per_kernel.get(name, (0, 0))
+            per_kernel[name] = (n + 1, t + (b - a))
+        spans.append(stop - seg[0][0])
+        busys.append(busy)
+        ends = seg[1:] + ([rows[e]] if e < len(rows) else [])
+        for (a0, b0, n0, _), (a1, _, n1, _) in zip(seg, ends):
+            if a1 > b0:
+                gaps[(n0, n1)] = gaps.get((n0, n1), 0) + (a1 - b0)
+                counts[(n0, n1)] = counts.get((n0, n1), 0) + 1
+    us = lambda ns: ns / 1000.0
+    span, busy = sum(spans) / steps, sum(busys) / steps
+    out = [f"trace: `{os.path.basename(path)}`: {len(rows)} dispatches, {len(starts)} steps; "
+           f"the last {steps} (the timed region) are split below.", "",
+           "| per step | us |", "|---|---|",
+           f"| step (first dispatch to the next step's first dispatch) | {us(span):.1f} |",
+           f"| kernels running | {us(busy):.1f} |",
+           f"| GPU idle | {us(span - busy):.1f} ({100.0 * (span - busy) / span:.1f} %) |", "",
+           "Step by step (us): " + ", ".join(f"{us(a):.0f}/{us(b):.0f}" for a, b in zip(spans, busys))
+           + " (span/kernels).", "",
+           "| idle gap between | total us over the timed steps | gaps | us per step |", "|---|---|---|---|"]
+    for key, g in sorted(gaps.items(), key=lambda kv: -kv[1])[:10]:
+        out.append(f"| `{key[0]}` -> `{key[1]}` | {us(g):.1f} | {counts[key]} | {us(g) / steps:.2f} |")
+    out += ["", "| kernel (timed steps) | launches per step | avg us | us per step |", "|---|---|---|---|"]
+    for name, (n, t) in sorted(per_kernel.items(), key=lambda kv: -kv[1][1]):
+        out.append(f"| `{name}` | {n / steps:g} | {us(t) / n:.2f} | {us(t) / steps:.2f} |")
+    return "\n".join(out)
+
+
 def main():
+    if len(sys.argv) > 1 and sys.argv[1] == "--split-trace":
+        # bench.py --split-trace RESULTS [STEPS]: summarise a rocprofv3 kernel
+        # trace of a bench.py run (no GPU used)
+        print(split_trace(sys.argv[2], int(sys.argv[3]) if len(sys.argv) > 3 else 20))
+        return
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     # 200 timed steps after 20 warm-up steps: shorter runs (20 after 3) read
@@ -370,6 +452,8 @@ def main():
     ap.add_argument("--config", type=int, default=1)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget in seconds (0 = skip)")
     ap.add_argument("--no-timing", action="store_true", help="do not bracket kernels with HIP events")
+    ap.add_argument("--sample-every", type=int, default=5,
+                    help="bracket the dominant kernel with events on every Nth timed step (1 = all)")
     ap.add_argument("--profile-steps", type=int, default=5,
                     help="untimed steps with every kernel bracketed by events (per-kernel table)")
     ap.add_argument("--rasterizer", choices=["legacy", "candidate"], default="legacy",
@@ -509,15 +593,22 @@ def main():
         ctx.set_timing(False)
         dominant = max(kernels.items(), key=lambda kv: kv[1]["ms_per_step"])[0] if kernels else None
 
+    # The timed region brackets the dominant kernel with events on every
+    # --sample-every-th step: a timed launch leaves the GPU idle for ~5 us on
+    # each side of the kernel, which would otherwise be part of every step.
+    every = max(1, args.sample_every)
     ctx.reset_timings()
     ctx.set_timing(dominant is not None, only=dominant)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for k in range(args.steps):
+        if dominant is not None and every > 1:
+            ctx.enable_timing(k % every == 0)
         step()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    timed = kernel_table(ctx.read_timings(), args.steps) if dominant else {}
+    sampled = -(-args.steps // every)  # the steps whose dominant launch was timed
+    timed = kernel_table(ctx.read_timings(), sampled) if dominant else {}
     ctx.set_timing(False)
     ms = (t1 - t0) * 1000.0 / args.steps
     mpix = pixels * poses / (ms / 1000.0) / 1e6
@@ -529,7 +620,8 @@ def main():
         roofline = {"bound": "hbm", "kernel": dominant, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dominant, w.name),
                     "avg_ms": kd["avg_ms"], "algorithmic_mb": kd["algorithmic_mb"],
-                    "timed_launches": int(round(kd["launches_per_step"] * args.steps))}
+                    "timed_launches": int(round(kd["launches_per_step"] * sampled)),
+                    "timed_steps": f"every {every}th of the {args.steps} timed steps" if every > 1 else "all"}
         # the blend kernels are bound by VALU issue, not HBM: the dominant
         # kernel's instructions per launch (committed SQ counter summary) over
         # the issue slots of its live-measured duration

@@ -267,6 +267,10 @@ class Context:
         self.check(lib().bh_ctx_set_timing_filter(self.handle, (only or "").encode()), "bh_ctx_set_timing_filter")
         self.check(lib().bh_ctx_set_timing(self.handle, int(enable)), "bh_ctx_set_timing")
 
+    def enable_timing(self, enable: bool):
+        """Switches the event brackets on or off, keeping the kernel filter."""
+        self.check(lib().bh_ctx_set_timing(self.handle, int(enable)), "bh_ctx_set_timing")
+
     def reset_timings(self):
         self.check(lib().bh_ctx_reset_timings(self.handle), "bh_ctx_reset_timings")
 

@@ -255,12 +255,11 @@ bh_status launch_adam_step(bh_ctx* ctx, float* param, const float* grad, float* 
                                                   reinterpret_cast<uintptr_t>(m1)) &
                                                  15u) == 0u;
         if (vec4)
-            adam_row_reduced_vec4_kernel<kAdamChunk / 4 / kAdamThreads>
-                <<<div_up(rows, rpb), kAdamThreads, 0, ctx->stream>>>(a, param, grad, m1, m2, scaling, rows, row_len,
-                                                                      rpb);
+            launch(ctx, adam_row_reduced_vec4_kernel<kAdamChunk / 4 / kAdamThreads>, dim3(div_up(rows, rpb)),
+                   dim3(kAdamThreads), 0u, a, param, grad, m1, m2, scaling, rows, row_len, rpb);
         else
-            adam_row_reduced_kernel<<<div_up(rows, rpb), kAdamThreads, 0, ctx->stream>>>(a, param, grad, m1, m2,
-                                                                                           scaling, rows, row_len, rpb);
+            launch(ctx, adam_row_reduced_kernel, dim3(div_up(rows, rpb)), dim3(kAdamThreads), 0u, a, param, grad, m1,
+                   m2, scaling, rows, row_len, rpb);
     } else {
         const bool vec4 = count >= 4 && ((reinterpret_cast<uintptr_t>(param) | reinterpret_cast<uintptr_t>(grad) |
                                           reinterpret_cast<uintptr_t>(m1) | reinterpret_cast<uintptr_t>(m2)) &
@@ -268,11 +267,11 @@ bh_status launch_adam_step(bh_ctx* ctx, float* param, const float* grad, float* 
         const uint32_t blocks =
             (uint32_t)std::max<uint64_t>(1u, std::min<uint64_t>(div_up(vec4 ? count / 4 : count, kAdamThreads), 1u << 20));
         if (vec4)
-            adam_elementwise_kernel<true><<<blocks, kAdamThreads, 0, ctx->stream>>>(a, param, grad, m1, m2, scaling,
-                                                                                     count, row_len);
+            launch(ctx, adam_elementwise_kernel<true>, dim3(blocks), dim3(kAdamThreads), 0u, a, param, grad, m1, m2,
+                   scaling, count, row_len);
         else
-            adam_elementwise_kernel<false><<<blocks, kAdamThreads, 0, ctx->stream>>>(a, param, grad, m1, m2, scaling,
-                                                                                      count, row_len);
+            launch(ctx, adam_elementwise_kernel<false>, dim3(blocks), dim3(kAdamThreads), 0u, a, param, grad, m1, m2,
+                   scaling, count, row_len);
     }
     return check_launch(ctx, "adam step");
 }

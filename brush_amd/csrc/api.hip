@@ -9,6 +9,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <chrono>
 #include <mutex>
 #include <new>
 #include <string>
@@ -117,7 +118,8 @@ void Pool::trim() {
 StageRange::StageRange(const char* name) { roctxRangePushA(name); }
 StageRange::~StageRange() { roctxRangePop(); }
 
-KernelTimer::KernelTimer(bh_ctx* c, const char* n) : ctx(c), name(n) {
+KernelTimer::KernelTimer(bh_ctx* c, const char* n) : ctx(c), name(n), outer(c->timer) {
+    ctx->timer = this;
     if (!ctx->timing) return;
     if (!ctx->timing_filter.empty() && ctx->timing_filter != n) return;
     auto get = [&]() {
@@ -134,13 +136,16 @@ KernelTimer::KernelTimer(bh_ctx* c, const char* n) : ctx(c), name(n) {
     };
     e0 = get();
     e1 = get();
-    if (e0) (void)hipEventRecord(e0, ctx->stream);
 }
 
 KernelTimer::~KernelTimer() {
-    if (!e0 || !e1) return;
-    (void)hipEventRecord(e1, ctx->stream);
-    ctx->pending.push_back(Timing{name, e0, e1});
+    ctx->timer = outer;
+    if (bound) {
+        ctx->pending.push_back(Timing{name, e0, e1});
+        return;
+    }
+    if (e0) ctx->event_cache.push_back(e0);
+    if (e1) ctx->event_cache.push_back(e1);
 }
 
 bh_status set_error(bh_ctx* ctx, bh_status st, const std::string& msg) {
@@ -160,6 +165,27 @@ static bh_status hip_check(bh_ctx* ctx, hipError_t e, const char* what) {
     (void)hipGetLastError();
     return set_error(ctx, e == hipErrorOutOfMemory ? BH_ERR_OOM : BH_ERR_DEVICE,
                      std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// Waits for the counts of the reduction of generation `gen`: the kernel stores
+// the eight counters in mapped host memory and then, after a system-scope
+// fence, `gen` in word 8, so the host polls that word (no event marker on the
+// stream).  A spin that has not seen it after 20 ms (the stream is far
+// behind, or a launch failed) synchronises the stream instead, which reports
+// a failed kernel; after that the word must be there.
+static bh_status wait_counters(bh_ctx* ctx, uint32_t gen) {
+    const auto seen = [&]() { return __atomic_load_n(ctx->h_counters + 8, __ATOMIC_ACQUIRE) == gen; };
+    const auto t0 = std::chrono::steady_clock::now();
+    for (uint32_t i = 1; !seen(); i++) {
+        if ((i & 255u) == 0u && std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(20)) {
+            const bh_status st = hip_check(ctx, hipStreamSynchronize(ctx->stream), "count readback");
+            if (st != BH_OK) return st;
+            if (!seen()) return set_error(ctx, BH_ERR_INTERNAL, "count readback: the reduction stored no counts");
+            break;
+        }
+        __builtin_ia32_pause();
+    }
+    return BH_OK;
 }
 
 #define BH_TRY(expr)                      \
@@ -343,14 +369,14 @@ bh_status bh_ctx_create(int device, bh_ctx** out) {
     // (mapped, coherent host memory), so no copy runs between it and the reads
     if (hipMalloc(&ctx->d_counters, 64) != hipSuccess ||
         hipHostMalloc(&ctx->h_counters, 64, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess ||
-        hipHostGetDevicePointer((void**)&ctx->h_counters_dev, ctx->h_counters, 0) != hipSuccess ||
-        hipEventCreateWithFlags(&ctx->counters_ready, hipEventDisableTiming) != hipSuccess) {
+        hipHostGetDevicePointer((void**)&ctx->h_counters_dev, ctx->h_counters, 0) != hipSuccess) {
         (void)hipGetLastError();
         if (ctx->d_counters) (void)hipFree(ctx->d_counters);
         if (ctx->h_counters) (void)hipHostFree(ctx->h_counters);
         delete ctx;
         return BH_ERR_OOM;
     }
+    memset(ctx->h_counters, 0, 64);  // generation 0: no reduction has stored counts
     *out = ctx;
     return BH_OK;
 }
@@ -367,7 +393,6 @@ void bh_ctx_destroy(bh_ctx* ctx) {
     for (auto& kv : ctx->pool.live) (void)hipFree(kv.first);
     (void)hipFree(ctx->d_counters);
     (void)hipHostFree(ctx->h_counters);
-    (void)hipEventDestroy(ctx->counters_ready);
     delete ctx;
 }
 
@@ -640,7 +665,7 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
     uint32_t num_visible = 0, kmin = 0, kmax = 0;
     uint64_t num_isect = 0;
     auto read_counts = [&]() -> bh_status {
-        BH_TRY(hip_check(ctx, hipEventSynchronize(ctx->counters_ready), "count readback"));
+        BH_TRY(wait_counters(ctx, ctx->count_generation));
         num_visible = ctx->h_counters[0];
         num_isect = (uint64_t)ctx->h_counters[2] | ((uint64_t)ctx->h_counters[3] << 32);
         kmin = ctx->h_counters[4];
@@ -658,9 +683,9 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
         StageRange stage("ProjectSplats");
         launch_project_forward(ctx, u, transforms, raw_opacities, sh_coeffs, sh_degree, num_splats, mip, tile_h, counts,
                                max_radius, depth_keys, vis_rows, partials, ctx->d_counters,
-                               planned ? ctx->plan_isect_cap : 0u, pf_zero, ctx->h_counters_dev);
+                               planned ? ctx->plan_isect_cap : 0u, pf_zero, ctx->h_counters_dev,
+                               ++ctx->count_generation);
         BH_STRY(check_launch(ctx, "project_forward"));
-        BH_STRY(hip_check(ctx, hipEventRecord(ctx->counters_ready, ctx->stream), "count readback"));
     }
 
     uint32_t *gfc = nullptr, *cum = nullptr, *tile_ids = nullptr, *cgids = nullptr;

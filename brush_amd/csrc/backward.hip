@@ -287,9 +287,8 @@ void launch_rasterize_backward(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint
     const uint32_t groups = div_up(num_tiles, 8) * (fine ? 16u : 32u);
     KernelTimer t(ctx, "rasterize_backward");
 #define BH_RB_T(S, R, D, T)                                                                                      \
-    rasterize_backward_kernel<S, R, D, T><<<groups, 64, 0, ctx->stream>>>(                                       \
-        img_w, img_h, tile_bw, num_tiles, bg[0], bg[1], bg[2], num_visible, out_img, projected, cgids, offsets, \
-        v_output, row_of, order, v_combined)
+    launch(ctx, rasterize_backward_kernel<S, R, D, T>, dim3(groups), dim3(64), 0u, img_w, img_h, tile_bw, num_tiles,   \
+           bg[0], bg[1], bg[2], num_visible, out_img, projected, cgids, offsets, v_output, row_of, order, v_combined)
 #define BH_RB(S, R, D) \
     do {               \
         if (fine)      \
@@ -660,9 +659,9 @@ static void launch_recorded_t(bh_ctx* ctx, uint32_t groups, uint32_t img_w, uint
                               const float* projected, const uint32_t* cgids, const uint32_t* off_pre,
                               const SplatRecord& rec, const float* v_output, const uint32_t* row_of,
                               const uint32_t* order, float* v_rows) {
-    rasterize_backward_recorded_kernel<S, R, D, T><<<groups, 64, 0, ctx->stream>>>(
-        img_w, img_h, tile_bw, num_tiles, bg[0], bg[1], bg[2], num_visible, out_img, projected, cgids, off_pre, rec,
-        v_output, row_of, order, v_rows);
+    launch(ctx, rasterize_backward_recorded_kernel<S, R, D, T>, dim3(groups), dim3(64), 0u, img_w, img_h, tile_bw,
+           num_tiles, bg[0], bg[1], bg[2], num_visible, out_img, projected, cgids, off_pre, rec, v_output, row_of,
+           order, v_rows);
 }
 
 void launch_rasterize_backward_recorded(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile_bw,
@@ -722,8 +721,8 @@ void launch_invert_permutation(bh_ctx* ctx, const uint32_t* gfc, uint32_t num_vi
     launch_fill_u32(ctx, compact_from_global, 0xFFFFFFFFu, n);
     if (num_visible == 0) return;
     KernelTimer t(ctx, "invert_permutation");
-    invert_permutation_kernel<<<div_up(num_visible, 256), 256, 0, ctx->stream>>>(gfc, num_visible, n,
-                                                                                    compact_from_global);
+    launch(ctx, invert_permutation_kernel, dim3(div_up(num_visible, 256)), dim3(256), 0u, gfc, num_visible, n,
+           compact_from_global);
 }
 
 template <int NC>
@@ -937,9 +936,8 @@ static void launch_pb_cam(bh_ctx* ctx, const bh_project_uniforms& u, const float
                           float* v_transforms, float* v_coeffs, float* v_raw_opac, float* v_refine) {
     const uint32_t blocks = div_up(n, PB_SPLATS);
 #define BH_PB(C)                                                                                                  \
-    project_backward_kernel<DEG, MIP, C><<<blocks, 256, 0, ctx->stream>>>(u, transforms, sh, raw_opac, cfg, n,     \
-                                                                          v_combined, v_transforms, v_coeffs,     \
-                                                                          v_raw_opac, v_refine)
+    launch(ctx, project_backward_kernel<DEG, MIP, C>, dim3(blocks), dim3(256), 0u, u, transforms, sh, raw_opac, cfg,   \
+           n, v_combined, v_transforms, v_coeffs, v_raw_opac, v_refine)
     switch (u.camera_model) {
         case kCamKB4: BH_PB(kCamKB4); break;
         case kCamRT8: BH_PB(kCamRT8); break;

@@ -2,6 +2,7 @@
 // C-ABI implementation and the kernel translation units.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -42,6 +43,8 @@ struct StageRange {
     StageRange(const StageRange&) = delete;
     StageRange& operator=(const StageRange&) = delete;
 };
+
+struct KernelTimer;
 
 struct Timing {
     std::string name;
@@ -89,13 +92,16 @@ struct bh_ctx {
     std::vector<bh::Timing> pending;
     std::vector<hipEvent_t> event_cache;
     std::vector<std::pair<std::string, bh::TimingTotal>> totals;
+    bh::KernelTimer* timer = nullptr;  // the timer whose scope is open (bh::launch binds its events)
     // small device scratch: [0] num_visible, [1] error flags,
     // [2..3] num_intersections (u64), [4] min depth key, [5] max depth key,
     // [6] depth key cap, [7] intersections when they fit the planned capacity
     uint32_t* d_counters = nullptr;
-    uint32_t* h_counters = nullptr;  // pinned
+    // pinned, mapped host copy of the eight counters; word 8 is the
+    // generation of the reduction that wrote them, stored after them
+    uint32_t* h_counters = nullptr;
     uint32_t* h_counters_dev = nullptr;  // h_counters as the device addresses it
-    hipEvent_t counters_ready = nullptr;  // recorded after the reduction wrote h_counters
+    uint32_t count_generation = 0;       // of the last reduction queued
     // The forward's plan for the launches that depend on its counts, taken
     // from the previous forward on this context: the depth key width and the
     // intersection capacity (valid once a forward with splats has run).
@@ -113,14 +119,37 @@ namespace bh {
 
 constexpr uint32_t kErrOverflow = 2u;  // a count exceeded its field
 
-// Scoped timing of one kernel launch on the context's stream.
+// Scoped timing of one kernel launch on the context's stream.  The timer
+// takes two events from the context and `launch` binds them to the kernel's
+// own dispatch: hipExtLaunchKernel sets them from the kernel's start and end
+// timestamps, so a timed kernel has no marker packets around it (a marker
+// between two kernels left the GPU idle for ~5 us).  A launch binds the
+// innermost open timer, and a timer binds only the first launch in its scope.
 struct KernelTimer {
     bh_ctx* ctx;
     const char* name;
     hipEvent_t e0 = nullptr, e1 = nullptr;
+    bool bound = false;
+    KernelTimer* outer = nullptr;
     KernelTimer(bh_ctx* c, const char* n);
     ~KernelTimer();
+    KernelTimer(const KernelTimer&) = delete;
+    KernelTimer& operator=(const KernelTimer&) = delete;
 };
+
+// Every kernel of the library is launched through here, on the context's
+// stream, so that an open KernelTimer times it.
+template <typename F, typename... Args>
+inline void launch(bh_ctx* ctx, F kernel, dim3 grid, dim3 block, uint32_t lds, Args... args) {
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    KernelTimer* t = ctx->timer;
+    if (t && t->e0 && t->e1 && !t->bound) {
+        e0 = t->e0;
+        e1 = t->e1;
+        t->bound = true;
+    }
+    hipExtLaunchKernelGGL(kernel, grid, block, lds, ctx->stream, e0, e1, 0u, args...);
+}
 
 bh_status set_error(bh_ctx* ctx, bh_status st, const std::string& msg);
 bh_status check_launch(bh_ctx* ctx, const char* what);
@@ -210,12 +239,15 @@ bh_status inclusive_scan(bh_ctx* ctx, const uint32_t* in, uint32_t* out, uint32_
 // project.hip
 size_t project_partials_bytes(uint32_t n);
 // Also writes each visible splat's projected row into rows [n, 16] (its
-// global-id slot), for launch_project_visible to order by depth.
+// global-id slot), for launch_project_visible to order by depth.  With
+// host_counters (device address of mapped host memory), the reduction also
+// stores the eight counters there and then `generation` in word 8.
 void launch_project_forward(bh_ctx* ctx, const bh_project_uniforms& u, const float* transforms,
                             const float* raw_opac, const float* sh, uint32_t sh_degree, uint32_t n, bool mip,
                             uint32_t tile_h, uint32_t* intersect_counts, float* max_radius, uint32_t* depth_keys,
                             float* rows, uint32_t* partials, uint32_t* counters, uint32_t isect_cap = 0,
-                            const ZeroRanges& zero = ZeroRanges{}, uint32_t* host_counters = nullptr);
+                            const ZeroRanges& zero = ZeroRanges{}, uint32_t* host_counters = nullptr,
+                            uint32_t generation = 0);
 void launch_project_visible(bh_ctx* ctx, const float* rows, const uint32_t* gfc, uint32_t num_visible,
                             uint32_t num_splats, float* projected, float* depths);
 // Also writes compact rows `projected` [V,10] and `depths` [V] from the

@@ -380,9 +380,9 @@ void launch_image_loss_forward(bh_ctx* ctx, const float* pred, uint32_t stride, 
     const dim3 grid(div_up(w, kLTile), div_up(h, kLTile), channels);
     KernelTimer t(ctx, "image_loss_forward");
     if (cfg.ssim_weight != 0.0f)
-        image_loss_forward_kernel<true><<<grid, 256, 0, ctx->stream>>>(p, pred, gt, map);
+        launch(ctx, image_loss_forward_kernel<true>, grid, dim3(256), 0u, p, pred, gt, map);
     else
-        image_loss_forward_kernel<false><<<grid, 256, 0, ctx->stream>>>(p, pred, gt, map);
+        launch(ctx, image_loss_forward_kernel<false>, grid, dim3(256), 0u, p, pred, gt, map);
 }
 
 void launch_image_loss_backward(bh_ctx* ctx, const float* pred, uint32_t stride, uint32_t channels,
@@ -393,9 +393,9 @@ void launch_image_loss_backward(bh_ctx* ctx, const float* pred, uint32_t stride,
     const dim3 grid(div_up(w, kLTile), div_up(h, kLTile), channels);
     KernelTimer t(ctx, "image_loss_backward");
     if (cfg.ssim_weight != 0.0f)
-        image_loss_backward_kernel<true><<<grid, 256, 0, ctx->stream>>>(p, pred, gt, dl_dmap, dl_dpred);
+        launch(ctx, image_loss_backward_kernel<true>, grid, dim3(256), 0u, p, pred, gt, dl_dmap, dl_dpred);
     else
-        image_loss_backward_kernel<false><<<grid, 256, 0, ctx->stream>>>(p, pred, gt, dl_dmap, dl_dpred);
+        launch(ctx, image_loss_backward_kernel<false>, grid, dim3(256), 0u, p, pred, gt, dl_dmap, dl_dpred);
 }
 
 }  // namespace bh

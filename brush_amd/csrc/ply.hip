@@ -423,8 +423,8 @@ template <int NC, bool CONTIG, bool F32>
 void launch_decode_variant(bh_ctx* ctx, uint32_t blocks, uint32_t lds, const uint8_t* rows, uint64_t rows_bytes,
                            uint32_t row_bytes, uint64_t n_out, uint32_t subsample, uint32_t big, uint32_t nr,
                            uint32_t slot_dwords, const PlyColumns& cols, float* transforms, float* sh, float* opac) {
-    ply_decode_rows_kernel<NC, CONTIG, F32><<<blocks, kPlyThreads, lds, ctx->stream>>>(
-        rows, rows_bytes, row_bytes, n_out, subsample, big, nr, slot_dwords, cols, transforms, sh, opac);
+    launch(ctx, ply_decode_rows_kernel<NC, CONTIG, F32>, dim3(blocks), dim3(kPlyThreads), lds, rows, rows_bytes,
+           row_bytes, n_out, subsample, big, nr, slot_dwords, cols, transforms, sh, opac);
 }
 
 template <int NC>
@@ -500,8 +500,8 @@ bh_status launch_ply_decode_compressed(bh_ctx* ctx, const float* chunks, const u
                                        uint64_t n_out, uint32_t subsample, uint32_t flags,
                                        const bh_ply_compressed_layout& L, float* transforms, float* sh, float* opac) {
     KernelTimer t(ctx, "ply_decode_compressed");
-    ply_decode_compressed_kernel<<<div_up(n_out, kPlyThreads), kPlyThreads, 0, ctx->stream>>>(
-        chunks, vrows, srows, n_out, subsample, (flags & BH_PLY_BIG_ENDIAN) ? 1u : 0u, L, transforms, sh, opac);
+    launch(ctx, ply_decode_compressed_kernel, dim3(div_up(n_out, kPlyThreads)), dim3(kPlyThreads), 0u, chunks, vrows,
+           srows, n_out, subsample, (flags & BH_PLY_BIG_ENDIAN) ? 1u : 0u, L, transforms, sh, opac);
     return check_launch(ctx, "ply_decode_compressed");
 }
 
@@ -521,9 +521,11 @@ bh_status launch_ply_encode_rows(bh_ctx* ctx, const float* transforms, const flo
     KernelTimer t(ctx, "ply_encode_rows");
 #define BH_PLY_ENCODE(NC)                                                                                            \
     if (vec)                                                                                                         \
-        ply_encode_rows_kernel<NC, true><<<blocks, kPlyThreads, lds, ctx->stream>>>(transforms, sh, opac, n, nr, rows); \
+        launch(ctx, ply_encode_rows_kernel<NC, true>, dim3(blocks), dim3(kPlyThreads), lds, transforms, sh, opac, n,   \
+               nr, rows);                                                                                              \
     else                                                                                                             \
-        ply_encode_rows_kernel<NC, false><<<blocks, kPlyThreads, lds, ctx->stream>>>(transforms, sh, opac, n, nr, rows)
+        launch(ctx, ply_encode_rows_kernel<NC, false>, dim3(blocks), dim3(kPlyThreads), lds, transforms, sh, opac, n,  \
+               nr, rows)
     switch (num_coeffs) {
         case 1: BH_PLY_ENCODE(1); break;
         case 4: BH_PLY_ENCODE(4); break;

@@ -227,13 +227,14 @@ __global__ __launch_bounds__(256, DEG >= 4 ? 4 : 5) void project_forward_kernel(
 // and writes what launches sized before the host reads them take from there:
 // [6] the depth sort's key cap (max - min + 1) and [7] the intersection
 // count when it fits `isect_cap` (else 0).  The same eight words also go to
-// `host` (mapped, coherent pinned host memory, or null), which the host reads
-// once an event after this kernel has completed: no copy kernel runs between
-// the reduction and the host's read.
+// `host` (mapped, coherent pinned host memory, or null), followed, after a
+// system-scope fence, by `generation` in host[8]: the host polls that word,
+// so neither a copy nor an event marker runs between the reduction and the
+// host's read.
 __global__ __launch_bounds__(1024) void project_reduce_kernel(const uint32_t* __restrict__ partials,
                                                               uint32_t num_blocks, uint32_t isect_cap,
                                                               uint32_t* __restrict__ counters,
-                                                              uint32_t* __restrict__ host) {
+                                                              uint32_t* __restrict__ host, uint32_t generation) {
     __shared__ uint32_t s_v[16], s_mn[16], s_mx[16];
     __shared__ unsigned long long s_h[16];
     uint32_t v = 0, mn = 0xFFFFFFFFu, mx = 0u;
@@ -272,6 +273,7 @@ __global__ __launch_bounds__(1024) void project_reduce_kernel(const uint32_t* __
             reinterpret_cast<uint4*>(host)[0] = make_uint4(c[0], c[1], c[2], c[3]);
             reinterpret_cast<uint4*>(host)[1] = make_uint4(c[4], c[5], c[6], c[7]);
             __threadfence_system();
+            __hip_atomic_store(host + 8, generation, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         }
     }
 }
@@ -283,10 +285,9 @@ static void launch_pf(bh_ctx* ctx, uint32_t blocks, const bh_project_uniforms& u
                       const float* raw_opac, const float* sh, uint32_t n, uint32_t* intersect_counts,
                       float* max_radius, uint32_t* depth_keys, float4* rows, uint32_t* partials,
                       const ZeroRanges& zero) {
-#define BH_PF(C)                                                                                             \
-    project_forward_kernel<MIP, C, TH, DEG><<<blocks, 256, 0, ctx->stream>>>(u, transforms, raw_opac, sh, n, \
-                                                                             intersect_counts, max_radius,   \
-                                                                             depth_keys, rows, partials, zero)
+#define BH_PF(C)                                                                                              \
+    launch(ctx, project_forward_kernel<MIP, C, TH, DEG>, dim3(blocks), dim3(256), 0u, u, transforms, raw_opac, sh, \
+           n, intersect_counts, max_radius, depth_keys, rows, partials, zero)
     switch (u.camera_model) {
         case kCamKB4: BH_PF(kCamKB4); break;
         case kCamRT8: BH_PF(kCamRT8); break;
@@ -316,7 +317,7 @@ void launch_project_forward(bh_ctx* ctx, const bh_project_uniforms& u, const flo
                             const float* raw_opac, const float* sh, uint32_t sh_degree, uint32_t n, bool mip,
                             uint32_t tile_h, uint32_t* intersect_counts, float* max_radius, uint32_t* depth_keys,
                             float* rows, uint32_t* partials, uint32_t* counters, uint32_t isect_cap,
-                            const ZeroRanges& zero, uint32_t* host_counters) {
+                            const ZeroRanges& zero, uint32_t* host_counters, uint32_t generation) {
     if (n == 0) return;
     uint32_t blocks = div_up(n, 256);
     {
@@ -335,7 +336,8 @@ void launch_project_forward(bh_ctx* ctx, const bh_project_uniforms& u, const flo
 #undef BH_PFD
     }
     KernelTimer t(ctx, "project_reduce");
-    project_reduce_kernel<<<1, 1024, 0, ctx->stream>>>(partials, blocks, isect_cap, counters, host_counters);
+    launch(ctx, project_reduce_kernel, dim3(1), dim3(1024), 0u, partials, blocks, isect_cap, counters, host_counters,
+           generation);
 }
 
 // ---- project_visible ------------------------------------------------------------
@@ -366,8 +368,8 @@ void launch_project_visible(bh_ctx* ctx, const float* rows, const uint32_t* gfc,
                             uint32_t num_splats, float* projected, float* depths) {
     if (num_visible == 0) return;
     KernelTimer t(ctx, "project_visible");
-    project_gather_kernel<<<div_up(num_visible, 256), 256, 0, ctx->stream>>>(
-        reinterpret_cast<const float4*>(rows), gfc, num_visible, num_splats, projected, depths);
+    launch(ctx, project_gather_kernel, dim3(div_up(num_visible, 256)), dim3(256), 0u,
+           reinterpret_cast<const float4*>(rows), gfc, num_visible, num_splats, projected, depths);
 }
 
 // ---- map_intersects ----------------------------------------------------------------
@@ -465,10 +467,9 @@ void launch_map_intersects(bh_ctx* ctx, uint32_t tile_bw, uint32_t tile_bh, uint
     KernelTimer t(ctx, "map_intersects");
     const uint32_t blocks = div_up(num_visible, 256);
     const float4* r4 = reinterpret_cast<const float4*>(rows);
-#define BH_MAP(TH, T)                                                                                            \
-    map_intersects_kernel<TH, T><<<blocks, 256, 0, ctx->stream>>>(tile_bw, tile_bh, r4, gfc, num_splats, cum,     \
-                                                                  num_visible, projected, depths, (T*)tile_ids,  \
-                                                                  cgids, zero, zero_words, dev)
+#define BH_MAP(TH, T)                                                                                           \
+    launch(ctx, map_intersects_kernel<TH, T>, dim3(blocks), dim3(256), 0u, tile_bw, tile_bh, r4, gfc, num_splats, \
+           cum, num_visible, projected, depths, (T*)tile_ids, cgids, zero, zero_words, dev)
     if (tile_h == 8) {
         if (tile_ids16) BH_MAP(8, uint16_t); else BH_MAP(8, uint32_t);
     } else {

@@ -65,8 +65,8 @@ void launch_tile_offsets(bh_ctx* ctx, const uint32_t* tile_ids, uint32_t m, uint
     if (!zeroed) launch_fill_u32(ctx, offsets, 0u, (uint64_t)num_tiles * 2);
     if (m == 0) return;
     KernelTimer t(ctx, "tile_offsets");
-    tile_offsets_kernel<<<div_up(div_up(m, 4), 256), 256, 0, ctx->stream>>>(tile_ids, m, num_tiles, offsets,
-                                                                         dev_m);
+    launch(ctx, tile_offsets_kernel, dim3(div_up(div_up(m, 4), 256)), dim3(256), 0u, tile_ids, m, num_tiles, offsets,
+           dev_m);
 }
 
 // v_writelane_b32: writes the wave-uniform `value` into lane `lane` of `old`,
@@ -204,7 +204,7 @@ __global__ __launch_bounds__(1024) void zero_and_tile_order_kernel(uint32_t* __r
 void launch_tile_order(bh_ctx* ctx, const uint32_t* offsets, uint32_t num_tiles, uint32_t* order) {
     if (num_tiles == 0) return;
     KernelTimer t(ctx, "tile_order");
-    tile_order_kernel<<<1, 1024, 0, ctx->stream>>>(offsets, num_tiles, order);
+    launch(ctx, tile_order_kernel, dim3(1), dim3(1024), 0u, offsets, num_tiles, order);
 }
 
 void launch_zero_and_tile_order(bh_ctx* ctx, uint32_t* p, uint64_t words, const uint32_t* offsets,
@@ -215,7 +215,8 @@ void launch_zero_and_tile_order(bh_ctx* ctx, uint32_t* p, uint64_t words, const 
     }
     KernelTimer t(ctx, "zero_and_tile_order");
     const uint32_t fill_blocks = (uint32_t)std::min<uint64_t>((words / 4u + 1023u) / 1024u + 1u, 1024u);
-    zero_and_tile_order_kernel<<<fill_blocks + 1u, 1024, 0, ctx->stream>>>(p, words, offsets, num_tiles, order);
+    launch(ctx, zero_and_tile_order_kernel, dim3(fill_blocks + 1u), dim3(1024), 0u, p, words, offsets, num_tiles,
+           order);
 }
 
 constexpr uint32_t kFillQuadsPerLane = 16;
@@ -476,9 +477,9 @@ void launch_rasterize(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile
     const uint32_t fill_groups = (uint32_t)div_up(div_up(fill_words, 4u), 64u * kFillQuadsPerLane);
     KernelTimer t(ctx, "rasterize");
 #define BH_RASTER_T(B, S, D, T)                                                                                    \
-    rasterize_kernel<B, S, D, T><<<groups + fill_groups, 64, 0, ctx->stream>>>(                                  \
-        img_w, img_h, tile_bw, num_tiles, bg[0], bg[1], bg[2], nv, projected, cgids, gfc, off_pre, order, out_img,    \
-        visible, off_post, rec, fill, fill_words, groups)
+    launch(ctx, rasterize_kernel<B, S, D, T>, dim3(groups + fill_groups), dim3(64), 0u, img_w, img_h, tile_bw,         \
+           num_tiles, bg[0], bg[1], bg[2], nv, projected, cgids, gfc, off_pre, order, out_img, visible, off_post, rec, \
+           fill, fill_words, groups)
 #define BH_RASTER(B, S, D) \
     do {                   \
         if (fine)          \

@@ -71,7 +71,7 @@ void launch_fill_u32(bh_ctx* ctx, uint32_t* p, uint32_t value, uint64_t count) {
     if (count == 0) return;
     KernelTimer t(ctx, "fill");
     uint32_t blocks = (uint32_t)std::min<uint64_t>((count / 4 + 255) / 256 + 1, 2048);
-    fill_u32_kernel<<<blocks, 256, 0, ctx->stream>>>(p, value, count);
+    launch(ctx, fill_u32_kernel, dim3(blocks), dim3(256), 0u, p, value, count);
 }
 
 struct FillRanges {
@@ -113,7 +113,7 @@ void launch_fill_multi(bh_ctx* ctx, const FillRange* ranges, int k) {
     if (fr.k == 0) return;
     KernelTimer t(ctx, "fill");
     const uint32_t blocks = (uint32_t)std::min<uint64_t>((total / 4 + 255) / 256 + 1, 2048);
-    fill_multi_kernel<<<blocks, 256, 0, ctx->stream>>>(fr);
+    launch(ctx, fill_multi_kernel, dim3(blocks), dim3(256), 0u, fr);
 }
 
 // ---- debug validation: the first non-finite value of each array ----------------------
@@ -137,7 +137,7 @@ void launch_first_non_finite(bh_ctx* ctx, const FiniteArrays& a, unsigned long l
     if (total == 0) return;
     KernelTimer t(ctx, "first_non_finite");
     const uint32_t blocks = (uint32_t)std::min<uint64_t>((total + 255) / 256, 4096);
-    first_non_finite_kernel<<<blocks, 256, 0, ctx->stream>>>(a, first);
+    launch(ctx, first_non_finite_kernel, dim3(blocks), dim3(256), 0u, a, first);
 }
 
 // Digit layout of a sort by the low `key_bits` bits: ceil(key_bits / 8)
@@ -513,13 +513,13 @@ static void launch_digit_pass(bh_ctx* ctx, uint32_t parts, const KI* src_k, cons
                               const SortDevice& dev) {
     if constexpr (sizeof(KI) == 4 && sizeof(KO) == 4) {
         if (go) {
-            onesweep_kernel<FIRST, ITEMS, true, KI, KO><<<parts, kThreads, 0, ctx->stream>>>(
-                src_k, src_v, dk, dv, n, sh, bits, sub, cap, radix, offs, gs, go, dev);
+            launch(ctx, onesweep_kernel<FIRST, ITEMS, true, KI, KO>, dim3(parts), dim3(kThreads), 0u, src_k, src_v, dk,
+                   dv, n, sh, bits, sub, cap, radix, offs, gs, go, dev);
             return;
         }
     }
-    onesweep_kernel<FIRST, ITEMS, false, KI, KO><<<parts, kThreads, 0, ctx->stream>>>(
-        src_k, src_v, dk, dv, n, sh, bits, sub, cap, radix, offs, nullptr, nullptr, dev);
+    launch(ctx, onesweep_kernel<FIRST, ITEMS, false, KI, KO>, dim3(parts), dim3(kThreads), 0u, src_k, src_v, dk, dv, n,
+           sh, bits, sub, cap, radix, offs, nullptr, nullptr, dev);
 }
 
 // One digit pass: upsweep, offset scan, scatter.  Keys are read as uint16_t
@@ -535,16 +535,16 @@ static bh_status sort_pass(bh_ctx* ctx, const ScanPlan& sp, const std::string& u
     {
         KernelTimer t(ctx, up_name.c_str());
         if (in_w == 2)
-            radix_upsweep_kernel<FIRST, I, uint16_t><<<grid, block, 0, ctx->stream>>>(
-                (const uint16_t*)src_k, n, sh, bits, sub, cap, sp.radix, sp.rows, offs, pblk, pdev);
+            launch(ctx, radix_upsweep_kernel<FIRST, I, uint16_t>, grid, block, 0u, (const uint16_t*)src_k, n, sh, bits,
+                   sub, cap, sp.radix, sp.rows, offs, pblk, pdev);
         else
-            radix_upsweep_kernel<FIRST, I, uint32_t><<<grid, block, 0, ctx->stream>>>(
-                (const uint32_t*)src_k, n, sh, bits, sub, cap, sp.radix, sp.rows, offs, pblk, pdev);
+            launch(ctx, radix_upsweep_kernel<FIRST, I, uint32_t>, grid, block, 0u, (const uint32_t*)src_k, n, sh, bits,
+                   sub, cap, sp.radix, sp.rows, offs, pblk, pdev);
     }
     {
         KernelTimer t(ctx, scan_name.c_str());
-        radix_scan_kernel<<<sp.blocks, kScanThreads, 0, ctx->stream>>>(offs, pblk, sp.parts, sp.rows, sp.blocks,
-                                                                       sp.radix);
+        launch(ctx, radix_scan_kernel, dim3(sp.blocks), dim3(kScanThreads), 0u, offs, pblk, sp.parts, sp.rows,
+               sp.blocks, sp.radix);
     }
     KernelTimer t(ctx, pass_name.c_str());
     if (in_w == 4 && out_w == 4)
@@ -646,7 +646,7 @@ __global__ void mask_u32_kernel(const uint32_t* __restrict__ in, uint32_t mask, 
 void launch_mask_u32(bh_ctx* ctx, const uint32_t* in, uint32_t mask, uint32_t n, uint32_t* out) {
     if (n == 0) return;
     KernelTimer t(ctx, "mask");
-    mask_u32_kernel<<<div_up(n, 256), 256, 0, ctx->stream>>>(in, mask, n, out);
+    launch(ctx, mask_u32_kernel, dim3(div_up(n, 256)), dim3(256), 0u, in, mask, n, out);
 }
 
 __global__ void gather_pairs_kernel(const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
@@ -664,7 +664,8 @@ void launch_gather_pairs(bh_ctx* ctx, const uint32_t* keys_in, const uint32_t* v
                          uint32_t n, uint32_t* keys_out, uint32_t* vals_out) {
     if (n == 0) return;
     KernelTimer t(ctx, "gather_pairs");
-    gather_pairs_kernel<<<div_up(n, 256), 256, 0, ctx->stream>>>(keys_in, vals_in, perm, n, keys_out, vals_out);
+    launch(ctx, gather_pairs_kernel, dim3(div_up(n, 256)), dim3(256), 0u, keys_in, vals_in, perm, n, keys_out,
+           vals_out);
 }
 
 // ---- inclusive scan (reduce-then-scan) -------------------------------------------
@@ -762,11 +763,11 @@ bh_status inclusive_scan(bh_ctx* ctx, const uint32_t* in, uint32_t* out, uint32_
     uint32_t* sums = (uint32_t*)scratch;
     {
         KernelTimer t(ctx, "scan_reduce");
-        scan_reduce_kernel<<<g.parts, kThreads, 0, ctx->stream>>>(in, n, g.chunks, sums, dev_n);
+        launch(ctx, scan_reduce_kernel, dim3(g.parts), dim3(kThreads), 0u, in, n, g.chunks, sums, dev_n);
     }
     {
         KernelTimer t(ctx, "scan");
-        scan_down_kernel<<<g.parts, kThreads, 0, ctx->stream>>>(in, out, n, g.chunks, sums, dev_n);
+        launch(ctx, scan_down_kernel, dim3(g.parts), dim3(kThreads), 0u, in, out, n, g.chunks, sums, dev_n);
     }
     return check_launch(ctx, "scan");
 }

@@ -154,3 +154,31 @@ def test_diff_render_frees_its_state_without_the_cycle_collector(monkeypatch):
     finally:
         if was_enabled:
             gc.enable()
+
+
+def test_bench_splits_a_kernel_trace_into_kernel_and_idle_time(tmp_path):
+    """bench.py --split-trace on a hand-made csv trace: two steps that start at
+    project_forward, with a 5 us gap before the second kernel of each step and
+    overlapping dispatches counted once."""
+    import bench
+
+    rows = [  # (start ns, end ns, name)
+        (0, 10_000, "void bh::project_forward_kernel<false, 0, 16, 3>(float const*)"),
+        (15_000, 20_000, "bh::tile_order_kernel(unsigned int const*)"),
+        (18_000, 30_000, "void bh::rasterize_kernel<true>(float)"),
+        (30_000, 40_000, "void bh::project_forward_kernel<false, 0, 16, 3>(float const*)"),
+        (45_000, 50_000, "bh::tile_order_kernel(unsigned int const*)"),
+        (50_000, 60_000, "void bh::rasterize_kernel<true>(float)"),
+    ]
+    p = tmp_path / "run_kernel_trace.csv"
+    p.write_text("Kernel_Name,Start_Timestamp,End_Timestamp\n"
+                 + "".join(f'"{n}",{a},{b}\n' for a, b, n in rows))
+    out = bench.split_trace(str(p), 2)
+    # step 1 spans 0..30 us with 25 us of kernels, step 2 spans 30..60 us with 25 us
+    assert "| step (first dispatch to the next step's first dispatch) | 30.0 |" in out
+    assert "| kernels running | 25.0 |" in out
+    assert "| GPU idle | 5.0 (16.7 %) |" in out
+    assert "| `bh::project_forward_kernel` -> `bh::tile_order_kernel` | 10.0 | 2 | 5.00 |" in out
+    assert "| `bh::rasterize_kernel<true>` | 1 | 11.00 | 11.00 |" in out
+    with pytest.raises(SystemExit):
+        bench.split_trace(str(p), 3)
