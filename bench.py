@@ -28,6 +28,7 @@ sample of the same workload.
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import sys
@@ -597,6 +598,11 @@ def main():
     # --sample-every-th step: a timed launch leaves the GPU idle for ~5 us on
     # each side of the kernel, which would otherwise be part of every step.
     every = max(1, args.sample_every)
+    # the objects alive now (torch's, the inputs) leave the collector's
+    # generations, so a collection inside the timed region scans only the
+    # steps' own short-lived objects
+    gc.collect()
+    gc.freeze()
     ctx.reset_timings()
     ctx.set_timing(dominant is not None, only=dominant)
     torch.cuda.synchronize()

@@ -609,9 +609,13 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
     } while (0)
 
     Scratch ws(ctx);
+    // off_pre [T, 2], and with BWD_INFO the backward order's per-tile words
+    // [T] (u64) and bucket counts behind it: one range that starts at zero
+    // (bh_splat_record.h)
     uint32_t *counts = nullptr, *off_pre = nullptr;
+    const uint64_t off_pre_words = (uint64_t)num_tiles * 2 + (bwd ? (uint64_t)num_tiles * 2 + kOrderBuckets : 0u);
     BH_STRY(sget((void**)&counts, (size_t)num_splats * 4));
-    BH_STRY(sget((void**)&off_pre, (size_t)num_tiles * 8));
+    BH_STRY(sget((void**)&off_pre, (size_t)off_pre_words * 4));
 
     // The launches after project_forward depend on its counts (visible
     // splats, intersections, depth-key range).  A plan sizes them: the counts
@@ -645,7 +649,7 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
             {ctx->d_counters + 1, 0u, counters && num_splats ? 1u : 0u},
             {(uint32_t*)visible, 0u, bwd ? (uint64_t)num_splats : 0u},
             {(uint32_t*)depth_scr, 0u, num_splats ? radix_sort_zeroed_words(num_splats, 32) : 0u},
-            {off_pre, 0u, (uint64_t)num_tiles * 2},
+            {off_pre, 0u, off_pre_words},
             {tile_offsets, 0u, bwd ? (uint64_t)num_tiles * 2 : 0u},
         };
         launch_fill_multi(ctx, zero, (int)(sizeof(zero) / sizeof(zero[0])));
@@ -656,7 +660,7 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
     if (num_splats) {
         pf_zero.p[0] = (uint32_t*)visible, pf_zero.count[0] = bwd ? (uint64_t)num_splats : 0u;
         pf_zero.p[1] = (uint32_t*)depth_scr, pf_zero.count[1] = radix_sort_zeroed_words(num_splats, 32);
-        pf_zero.p[2] = off_pre, pf_zero.count[2] = (uint64_t)num_tiles * 2;
+        pf_zero.p[2] = off_pre, pf_zero.count[2] = off_pre_words;
         pf_zero.p[3] = tile_offsets, pf_zero.count[3] = bwd ? (uint64_t)num_tiles * 2 : 0u;
     } else {
         zero_outputs(true);
@@ -801,6 +805,12 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
             const uint32_t bpt = 2u * tile_h / 8u;
             BH_TRY(sget((void**)&rec.masks, std::max<size_t>(record_masks(p.m, bpt), 1) * sizeof(uint2)));
             BH_TRY(sget((void**)&rec.block_end, (size_t)num_tiles * bpt * 4));
+            if (p.m) {
+                // the backward's dispatch order, appended by the blend
+                rec.order.word = reinterpret_cast<unsigned long long*>(off_pre + (size_t)num_tiles * 2);
+                rec.order.count = off_pre + (size_t)num_tiles * 4;
+                BH_TRY(sget((void**)&rec.order.list, (size_t)kOrderBuckets * num_tiles * 4));
+            }
         }
         launch_rasterize(ctx, u.img_w, u.img_h, u.tile_bw, u.tile_bh, background, p.v, projected, cgids, gfc, off_pre,
                          order, flags, out_img, visible, tile_offsets, true, rec, (uint32_t*)st->bwd_rows,
@@ -985,14 +995,19 @@ bh_status bh_render_backward(bh_ctx* ctx, const bh_fwd_state* state, const float
     const uint32_t raster_flags = (in.flags & (fwd_owned | BH_FLAG_TILE_16X8)) | (flags & BH_FLAG_REFINE_WEIGHT);
     StageRange raster_stage("RasterizeBackwards");
     if (in.num_visible && in.num_intersections && state->record.masks) {
-        // the longest tiles (most splats the forward blended) start first;
-        // the order is computed while the gradient rows are zeroed
-        uint32_t* order;
-        BH_TRY(ws.get(&order, in.num_tiles));
-        if (pre_zeroed)
-            launch_tile_order(ctx, tile_offsets, in.num_tiles, order);
-        else
-            launch_zero_and_tile_order(ctx, (uint32_t*)rows, (uint64_t)n * 11, tile_offsets, in.num_tiles, order);
+        // the longest tiles (most splats the forward blended) start first: in
+        // the order the forward's blend recorded, or one computed here (while
+        // the gradient rows are zeroed)
+        uint32_t* order = nullptr;
+        if (state->record.order.list) {
+            if (!pre_zeroed) launch_fill_u32(ctx, (uint32_t*)rows, 0u, (uint64_t)n * 11);
+        } else {
+            BH_TRY(ws.get(&order, in.num_tiles));
+            if (pre_zeroed)
+                launch_tile_order(ctx, tile_offsets, in.num_tiles, order);
+            else
+                launch_zero_and_tile_order(ctx, (uint32_t*)rows, (uint64_t)n * 11, tile_offsets, in.num_tiles, order);
+        }
         launch_rasterize_backward_recorded(ctx, in.img_w, in.img_h, in.tile_bw, in.tile_bh, background, in.num_visible,
                                            out_img, in.projected, in.compact_gid_from_isect, in.tile_offsets_pre,
                                            state->record, v_output, raster_flags, in.global_from_compact_gid, order,

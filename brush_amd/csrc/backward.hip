@@ -389,7 +389,13 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
     uint32_t tile, blk;
     block_of_workgroup<TH>(blockIdx.x, tile, blk);
     if (tile >= num_tiles) return;
-    if (order) tile = order[tile];
+    if (order)
+        tile = order[tile];
+    else if (rec.order.list) {
+        // the order the forward blend recorded (tiles some pixel blended)
+        tile = ordered_tile(tile, rec.order.count, rec.order.list, num_tiles);
+        if (tile >= num_tiles) return;
+    }
     const uint32_t lo = off_pre[2 * tile], hi = off_pre[2 * tile + 1];
     const uint32_t end = rec.block_end[tile * BPT + blk];
     if (end <= lo) return;

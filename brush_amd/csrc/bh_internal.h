@@ -273,13 +273,14 @@ void launch_tile_order(bh_ctx* ctx, const uint32_t* offsets, uint32_t num_tiles,
 void launch_zero_and_tile_order(bh_ctx* ctx, uint32_t* p, uint64_t words, const uint32_t* offsets,
                                 uint32_t num_tiles, uint32_t* order);
 // With BWD_INFO and rec.masks set, the blend also records its contributing
-// pairs for the fused backward (bh_splat_record.h).  With BWD_INFO, workgroups
-// after the blend's zero fill[0, fill_words) (16-byte aligned) in its tail.
+// pairs for the fused backward (bh_splat_record.h), and with rec.order.list
+// the backward's dispatch order.  With BWD_INFO, workgroups after the blend's
+// zero fill[0, fill_words) (16-byte aligned) in its tail.
 void launch_rasterize(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,
-                      const float* bg, uint32_t num_visible, const float* projected, const uint32_t* cgids, const uint32_t* gfc,
-                      const uint32_t* off_pre, const uint32_t* order, uint32_t flags, void* out_img, float* visible,
-                      uint32_t* off_post, bool off_post_zeroed = false, SplatRecord rec = SplatRecord{},
-                      uint32_t* fill = nullptr, uint64_t fill_words = 0);
+                      const float* bg, uint32_t num_visible, const float* projected, const uint32_t* cgids,
+                      const uint32_t* gfc, const uint32_t* off_pre, const uint32_t* order, uint32_t flags,
+                      void* out_img, float* visible, uint32_t* off_post, bool off_post_zeroed = false,
+                      SplatRecord rec = SplatRecord{}, uint32_t* fill = nullptr, uint64_t fill_words = 0);
 
 // backward.hip
 void launch_rasterize_backward(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t tile_bh,

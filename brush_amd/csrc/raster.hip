@@ -447,6 +447,18 @@ __global__ __launch_bounds__(64) void rasterize_kernel(uint32_t img_w, uint32_t 
         const uint32_t m = last;  // wave-uniform: one past the block's last blended candidate
         if (lane == 0) atomicMax(&off_post[2 * tile + 1], m);
         if (record && lane == 0) rec.block_end[tile * BPT + blk] = m;
+        if (record && lane == 0 && rec.order.list) {
+            // the backward's order (bh_splat_record.h): the tile's last block
+            // appends it under its longest block's bucket
+            const unsigned long long add = (1ull << 32) | ((unsigned long long)order_bucket(m - lo) << (8u * blk));
+            const unsigned long long w = atomicAdd(&rec.order.word[tile], add) + add;
+            if ((uint32_t)(w >> 32) == BPT) {
+                uint32_t b = kOrderBuckets - 1u;
+#pragma unroll
+                for (uint32_t k = 0; k < BPT; ++k) b = min(b, (uint32_t)(w >> (8u * k)) & 0xFFu);
+                if (b != kOrderBuckets - 1u) order_append(rec.order, b, tile, num_tiles);
+            }
+        }
     }
     if (lane == 0 && blk == 0) {
         off_post[2 * tile] = lo;
