@@ -301,6 +301,8 @@ struct Bump {
 };
 
 static uint32_t bit_length(uint32_t x) { return x ? 32u - (uint32_t)__builtin_clz(x) : 0u; }
+// the largest splat count the depth sort's bucket path takes
+constexpr uint32_t kBucketSortMaxSplats = 1u << 21;
 
 // bh_radix_argsort's body over a workspace provider (the pool, or the fixed
 // scratch of the allocation-free entry point).
@@ -717,8 +719,15 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
             dev.drop_capped = true;
             dev.n_rest_host = p.v;
             StageRange stage("DepthSort");
-            BH_TRY(radix_sort_pairs(ctx, depth_keys, nullptr, num_splats, p.key_bits, p.kmin, p.kcap, sk, gfc, tk, tv,
-                                    depth_scr, "depth_sort", true, counts, counts_sorted, dev));
+            // up to 2^21 splats: one top-digit pass and a per-bucket sort
+            // (four launches); above, the LSD passes (each bucket would hold
+            // more than 8192 splats of an even spread of depths)
+            if (num_splats <= kBucketSortMaxSplats)
+                BH_TRY(depth_sort_buckets(ctx, depth_keys, num_splats, p.kmin, p.kcap, sk, gfc, tk, tv, depth_scr,
+                                          true, counts, counts_sorted, dev));
+            else
+                BH_TRY(radix_sort_pairs(ctx, depth_keys, nullptr, num_splats, p.key_bits, p.kmin, p.kcap, sk, gfc, tk,
+                                        tv, depth_scr, "depth_sort", true, counts, counts_sorted, dev));
         }
         BH_TRY(sget((void**)&cum, (size_t)p.v * 4));
         BH_TRY(sget((void**)&projected, (size_t)std::max<uint32_t>(p.v, 1u) * 40));
@@ -765,7 +774,7 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
                 StageRange stage("MapGaussiansToIntersect");
                 launch_map_intersects(ctx, u.tile_bw, u.tile_bh, tile_h, vis_rows, gfc, num_splats, cum, p.v, projected,
                                   depths, ut, k16, uc, (uint32_t*)scr, (uint32_t)radix_sort_zeroed_words(p.m, bits),
-                                  dc);
+                                  dc, p.m);
             }
             BH_TRY(check_launch(ctx, "map_intersects"));
             StageRange stage("Tile sort");

@@ -225,6 +225,18 @@ bh_status radix_sort_pairs_k16(bh_ctx* ctx, const uint16_t* keys_in, const uint3
                                uint32_t key_bits, uint32_t* keys_out, uint32_t* vals_out, uint16_t* tmp_keys,
                                uint32_t* tmp_vals, void* scratch, const char* tag = "radix",
                                bool scratch_zeroed = false, const SortDevice& dev = SortDevice{});
+// Stable sort of (key', index) pairs as radix_sort_pairs sorts them (key' =
+// min(key - key_sub, key_cap), the first pass's drop of capped keys, the
+// sorted indices to vals_out and gather_out[i] = gather_src[vals_out[i]]),
+// for any key width: one pass by the top 8 bits of key_cap's range, then
+// every bucket sorted by one workgroup (in LDS up to 16384 pairs).  keys_tmp,
+// tmp_keys and tmp_vals are n-element buffers; the scratch is
+// radix_sort_scratch_bytes(n, 8), its first radix_sort_zeroed_words(n, 8)
+// words zero (or zeroed here unless scratch_zeroed).
+bh_status depth_sort_buckets(bh_ctx* ctx, const uint32_t* keys_in, uint32_t n, uint32_t key_sub, uint32_t key_cap,
+                             uint32_t* keys_tmp, uint32_t* vals_out, uint32_t* tmp_keys, uint32_t* tmp_vals,
+                             void* scratch, bool scratch_zeroed, const uint32_t* gather_src, uint32_t* gather_out,
+                             const SortDevice& dev);
 // out[i] = in[i] & mask
 void launch_mask_u32(bh_ctx* ctx, const uint32_t* in, uint32_t mask, uint32_t n, uint32_t* out);
 // keys_out[i] = keys_in[perm[i]], vals_out[i] = vals_in[perm[i]]
@@ -256,11 +268,12 @@ void launch_project_visible(bh_ctx* ctx, const float* rows, const uint32_t* gfc,
 // project_forward), num_visible is a capacity: the kernel reads the visible
 // count from dev[0] and writes intersections only when they fit the buffers.
 // The tile ids are written as uint16_t when tile_ids16 is set (fewer than
-// 2^16 tiles, the sentinel included), else as uint32_t.
+// 2^16 tiles, the sentinel included), else as uint32_t.  m_cap is the pair
+// buffers' size: no pair is stored at or past it.
 void launch_map_intersects(bh_ctx* ctx, uint32_t tile_bw, uint32_t tile_bh, uint32_t tile_h, const float* rows,
                            const uint32_t* gfc, uint32_t num_splats, const uint32_t* cum, uint32_t num_visible,
                            float* projected, float* depths, void* tile_ids, bool tile_ids16, uint32_t* cgids,
-                           uint32_t* zero, uint32_t zero_words, const uint32_t* dev = nullptr);
+                           uint32_t* zero, uint32_t zero_words, const uint32_t* dev, uint32_t m_cap);
 
 // raster.hip
 // With dev_m, m is a capacity and the ids are tile_ids[0, min(m, *dev_m)).

@@ -391,7 +391,7 @@ __global__ __launch_bounds__(256) void map_intersects_kernel(uint32_t tile_bw, u
                                                               TileT* __restrict__ tile_ids,
                                                               uint32_t* __restrict__ cgids,
                                                               uint32_t* __restrict__ zero, uint32_t zero_words,
-                                                              const uint32_t* __restrict__ dev) {
+                                                              const uint32_t* __restrict__ dev, uint32_t m_cap) {
     __shared__ WalkRec s_rec[4][64];
     __shared__ uint32_t s_slot[4][64], s_count[4][64];
     const uint32_t c = blockIdx.x * 256u + threadIdx.x;
@@ -434,7 +434,8 @@ __global__ __launch_bounds__(256) void map_intersects_kernel(uint32_t tile_bw, u
     // the walk emits their tiles in that order.
     const uint32_t last = min(c0 + 63u, num_visible - 1u);
     const uint32_t out_base = c0 == 0 ? 0u : cum[c0 - 1];
-    const uint32_t out_end = cum[last];
+    // no store lands past the pair buffers (m_cap pairs), whatever cum holds
+    const uint32_t out_end = min(cum[last], m_cap);
     const uint32_t hits = wave_tile_walk<true, TH, TileT>(lane, active ? bbox_items(bb) : 0u, m, conic, pt, bb, s_rec[wave],
                                                s_slot[wave], s_count[wave], tile_bw, out_base, out_end, c0, tile_ids,
                                                cgids);
@@ -446,6 +447,7 @@ __global__ __launch_bounds__(256) void map_intersects_kernel(uint32_t tile_bw, u
     __threadfence();
     if (!active) return;
     uint32_t k = 0;
+    budget = base < m_cap ? min(budget, m_cap - base) : 0u;
     for (uint32_t ty = bb.min_y; ty < bb.max_y && k < budget; ty++)
         for (uint32_t tx = bb.min_x; tx < bb.max_x && k < budget; tx++)
             if (will_contribute<TH>(tx, ty, m, conic, pt)) {
@@ -462,14 +464,14 @@ __global__ __launch_bounds__(256) void map_intersects_kernel(uint32_t tile_bw, u
 void launch_map_intersects(bh_ctx* ctx, uint32_t tile_bw, uint32_t tile_bh, uint32_t tile_h, const float* rows,
                            const uint32_t* gfc, uint32_t num_splats, const uint32_t* cum, uint32_t num_visible,
                            float* projected, float* depths, void* tile_ids, bool tile_ids16, uint32_t* cgids,
-                           uint32_t* zero, uint32_t zero_words, const uint32_t* dev) {
+                           uint32_t* zero, uint32_t zero_words, const uint32_t* dev, uint32_t m_cap) {
     if (num_visible == 0) return;
     KernelTimer t(ctx, "map_intersects");
     const uint32_t blocks = div_up(num_visible, 256);
     const float4* r4 = reinterpret_cast<const float4*>(rows);
 #define BH_MAP(TH, T)                                                                                           \
     launch(ctx, map_intersects_kernel<TH, T>, dim3(blocks), dim3(256), 0u, tile_bw, tile_bh, r4, gfc, num_splats, \
-           cum, num_visible, projected, depths, (T*)tile_ids, cgids, zero, zero_words, dev)
+           cum, num_visible, projected, depths, (T*)tile_ids, cgids, zero, zero_words, dev, m_cap)
     if (tile_h == 8) {
         if (tile_ids16) BH_MAP(8, uint16_t); else BH_MAP(8, uint32_t);
     } else {

@@ -53,6 +53,49 @@ __device__ inline uint32_t block_exclusive_scan(uint32_t v, uint32_t* s_wave_tot
     return off + x - v;
 }
 
+// Stable ranks of a wave's pairs among its pairs of the same digit
+// (k >> sh) & (2^bits - 1): item j of lane l is the wave's (64 j + l)-th pair,
+// valid where bit j of `valid` is set, for j < items (wave-uniform).  On
+// return pos[j] = hist[d] before the call plus the wave's earlier pairs of
+// digit d, and hist[d] (the wave's running count in LDS) has advanced by the
+// wave's pairs of each digit.  A lane's peers (the lanes that share its
+// digit) come from a match over the digit's bit planes; the highest lane of
+// each peer group advances the running count.  BITS > 0 matches exactly BITS
+// planes, unrolled (digits must be below 2^BITS); BITS == 0 the runtime `bits`.
+template <int ITEMS, int BITS = 0>
+__device__ __forceinline__ void wave_rank(const uint32_t (&k)[ITEMS], uint32_t valid, uint32_t items, uint32_t sh,
+                                          uint32_t bits, uint32_t* hist, uint32_t (&pos)[ITEMS]) {
+    const int lane = threadIdx.x & 63;
+    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    const uint32_t dmask = (1u << bits) - 1u;
+#pragma unroll
+    for (int j = 0; j < ITEMS; j++) {
+        if ((uint32_t)j < items) {
+            const bool ok = (valid >> j) & 1u;
+            const uint32_t d = (k[j] >> sh) & dmask;
+            uint64_t peers = __ballot(ok);
+            if constexpr (BITS > 0) {
+#pragma unroll
+                for (int b = 0; b < BITS; b++) {
+                    const bool bit = (d >> b) & 1u;
+                    const uint64_t bal = __ballot(bit);
+                    peers &= bit ? bal : ~bal;
+                }
+            } else {
+                for (uint32_t b = 0; b < bits; b++) {
+                    const bool bit = (d >> b) & 1u;
+                    const uint64_t bal = __ballot(bit);
+                    peers &= bit ? bal : ~bal;
+                }
+            }
+            uint32_t prefix = 0;
+            if (ok) prefix = hist[d];
+            pos[j] = prefix + (uint32_t)__popcll(peers & lt_mask);
+            if (ok && (peers >> lane) == 1ull) hist[d] = prefix + (uint32_t)__popcll(peers);
+        }
+    }
+}
+
 // p[0, count) = value: 16-byte stores from the first 16-byte boundary, single
 // words for the unaligned head and the tail.
 __global__ void fill_u32_kernel(uint32_t* p, uint32_t value, uint64_t count) {
@@ -183,6 +226,16 @@ static ScanPlan scan_plan(uint32_t n, const DigitPlan& d) {
     return s;
 }
 
+// A first pass whose shift is kShiftTop sorts by the top 8 bits of the
+// transformed key range instead: bit_length(key_cap) - 8 (0 below 9 bits),
+// taken from the key cap the kernel reads, so the digit follows a device-held
+// range.
+constexpr uint32_t kShiftTop = 0xFFFFFFFFu;
+__device__ __forceinline__ uint32_t top_digit_shift(uint32_t cap) {
+    const uint32_t bl = cap ? 32u - (uint32_t)__clz((int)cap) : 0u;
+    return bl > 8u ? bl - 8u : 0u;
+}
+
 // ---- reduce-then-scan: digit counts of each partition ----------------------------
 
 // One workgroup per partition: the digit counts of its keys (per-wave LDS
@@ -202,6 +255,7 @@ __global__ __launch_bounds__(kThreads) void radix_upsweep_kernel(const K* __rest
         key_sub = *dev.key_sub;
         key_cap = *dev.key_cap;
     }
+    if (FIRST && shift == kShiftTop) shift = top_digit_shift(key_cap);
     for (int i = tid; i < kWaves * kRadix; i += kThreads) (&s_hist[0][0])[i] = 0;
     __syncthreads();
     constexpr int PART = kThreads * ITEMS;
@@ -377,6 +431,7 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const KI* __restrict
         key_sub = *dev.key_sub;
         key_cap = *dev.key_cap;
     }
+    if (FIRST && shift == kShiftTop) shift = top_digit_shift(key_cap);
     // a partition past a device-held count has no pairs (the grid is sized
     // for the capacity); the upsweep wrote its counts as zeros
     if ((uint64_t)part * (kThreads * ITEMS) >= n) return;
@@ -408,23 +463,7 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const KI* __restrict
 #pragma unroll
         for (int j = 0; j < ITEMS; j++) gv[j] = (kept >> j) & 1u ? gather_src[v[j]] : 0u;
     }
-    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-#pragma unroll
-    for (int j = 0; j < ITEMS; j++) {
-        const bool valid = (kept >> j) & 1u;
-        uint32_t d = (k[j] >> shift) & dmask;
-        uint64_t peers = __ballot(valid);
-        for (uint32_t b = 0; b < digit_bits; b++) {
-            bool bit = (d >> b) & 1u;
-            uint64_t bal = __ballot(bit);
-            peers &= bit ? bal : ~bal;
-        }
-        uint32_t prefix = 0;
-        if (valid) prefix = s_wave_hist[wave][d];
-        pos[j] = prefix + (uint32_t)__popcll(peers & lt_mask);
-        // the highest lane of each peer group advances the wave's running count
-        if (valid && (peers >> lane) == 1ull) s_wave_hist[wave][d] = prefix + (uint32_t)__popcll(peers);
-    }
+    wave_rank<ITEMS>(k, kept, ITEMS, shift, digit_bits, s_wave_hist[wave], pos);
     __syncthreads();
 
     // per-digit counts of the partition and each wave's offset inside them
@@ -489,6 +528,331 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const KI* __restrict
             const uint32_t i = (uint32_t)(j * kThreads + tid);
             if (dst[j] != 0xFFFFFFFFu) gather_out[dst[j]] = s_buf[i];
         }
+    }
+}
+
+// ---- depth sort: one top-digit pass, then each bucket sorted by one workgroup -------
+//
+// A stable pass by the top 8 bits of the key range (the digit passes above, with
+// kShiftTop) leaves 256 buckets, each the run of one top digit in input order.
+// One workgroup per bucket then sorts it stably by the key bits below that
+// digit, in 8-bit LSD passes: a bucket of up to kBsCap pairs is ranked and
+// reordered in LDS without touching memory between passes; a larger one makes
+// the same passes over its chunks through global memory (ping-ponging with
+// the temporaries).  The result is the stable sort by the whole key, in four
+// launches instead of three per 8-bit digit.
+constexpr int kBsThreads = 1024;
+constexpr int kBsWaves = kBsThreads / 64;
+constexpr int kBsItems = 16;
+constexpr uint32_t kBsCap = kBsThreads * kBsItems;
+constexpr uint32_t kBsBuckets = 256;
+
+// Stable rank of the chunk of `cnt` pairs the workgroup holds (item j of a
+// lane is chunk element e = wave * 64 * iw + j * 64 + lane, j < iw, valid
+// below cnt) by the digit (k >> sh) & (2^bits - 1).  On return pos[j] is the
+// element's position in the digit-ordered chunk, and s_start[d] / s_cnt[d]
+// the chunk's first position and count of digit d.
+__device__ __forceinline__ void bucket_rank(const uint32_t (&k)[kBsItems], uint32_t (&pos)[kBsItems], uint32_t iw,
+                                            uint32_t cnt, uint32_t sh, uint32_t bits,
+                                            uint32_t (*s_hist)[kRadix], uint32_t* s_start, uint32_t* s_cnt,
+                                            uint32_t* s_tot) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int i = tid; i < kBsWaves * kRadix; i += kBsThreads) (&s_hist[0][0])[i] = 0;
+    __syncthreads();
+    const uint32_t dmask = (1u << bits) - 1u;
+    const uint32_t wbase = (uint32_t)wave * 64u * iw;
+    uint32_t valid = 0;
+#pragma unroll
+    for (int j = 0; j < kBsItems; j++)
+        if (wbase + (uint32_t)j * 64u + (uint32_t)lane < cnt) valid |= 1u << j;
+    wave_rank<kBsItems, 8>(k, valid, iw, sh, bits, s_hist[wave], pos);
+    __syncthreads();
+    // digit d = tid: each wave's offset inside the digit, the digit's total
+    uint32_t total = 0;
+    if (tid < kRadix) {
+#pragma unroll
+        for (int w = 0; w < kBsWaves; w++) {
+            const uint32_t c = s_hist[w][tid];
+            s_hist[w][tid] = total;
+            total += c;
+        }
+    }
+    uint32_t all;
+    const uint32_t start = block_exclusive_scan<kBsThreads>(total, s_tot, &all);
+    if (tid < kRadix) {
+        s_start[tid] = start;
+        s_cnt[tid] = total;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kBsItems; j++) {
+        if ((uint32_t)j >= iw) break;
+        if (wbase + (uint32_t)j * 64u + (uint32_t)lane < cnt) {
+            const uint32_t d = (k[j] >> sh) & dmask;
+            pos[j] += s_start[d] + s_hist[wave][d];
+        }
+    }
+}
+
+// Longest run of equal keys that the counting path orders (one thread per
+// run, insertion sort in LDS), and the widest key it counts: a bucket with a
+// longer run or wider keys takes the LSD passes instead.
+constexpr uint32_t kBsMaxRun = 32;
+constexpr uint32_t kBsCountBits = 15;
+
+// Counting sort of a bucket of `size` <= kBsCap pairs whose keys (their low
+// `low` <= 15 bits) lie in k[] (wave-major items, as bucket_rank lays them
+// out): a histogram of the keys in packed 16-bit LDS counters, their
+// exclusive scan, and one returning LDS add per pair for its slot.  Pairs of
+// equal keys (a run of slots) are then put in input order by the thread that
+// holds the run's first slot.  The sorted values and gathered counts go out
+// in place.  Returns false, having written nothing, when a key occurs more
+// than kBsMaxRun times.  s_raw holds the counters (up to 16384 words), then
+// each slot's input position and key (16384 uint16_t each).
+__device__ bool bucket_count_sort(uint32_t (&k)[kBsItems], uint32_t iw, uint32_t size, uint32_t low,
+                                  uint32_t start, uint32_t* __restrict__ vals,
+                                  const uint32_t* __restrict__ gather_src, uint32_t* __restrict__ gather_out,
+                                  uint32_t* s_raw, uint32_t* s_tot, uint32_t* s_flag) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t wbase = (uint32_t)wave * 64u * iw;
+    uint32_t* words = s_raw;                                         // counters, two per word
+    uint16_t* s_idx = reinterpret_cast<uint16_t*>(s_raw + 16384);  // slot -> input position
+    uint16_t* s_bin = s_idx + kBsCap;                                // slot -> key
+    const uint32_t lowmask = (1u << low) - 1u;
+    const uint32_t nwords = 1u << (low - 1u);
+    // counter word i lives at word swz(i): the scan's threads each read 16
+    // consecutive words, which would put a wave's 64 lanes on 4 LDS banks;
+    // the swizzle (inside each aligned group of 16) spreads them over all
+    auto swz = [](uint32_t i) { return (i & ~15u) | ((i & 15u) ^ ((i >> 6) & 15u)); };
+    for (uint32_t i = (uint32_t)tid; i < nwords; i += kBsThreads) words[i] = 0u;
+    if (tid == 0) *s_flag = 0u;
+#pragma unroll
+    for (int j = 0; j < kBsItems; j++)
+        if ((uint32_t)j < iw) k[j] &= lowmask;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kBsItems; j++) {
+        if ((uint32_t)j >= iw) break;
+        if (wbase + (uint32_t)j * 64u + (uint32_t)lane < size)
+            atomicAdd(&words[swz(k[j] >> 1)], 1u << ((k[j] & 1u) * 16u));
+    }
+    __syncthreads();
+    // exclusive scan of the counters (thread t: words [t * wpt, (t + 1) * wpt))
+    // and the largest count
+    const uint32_t wpt = (nwords + kBsThreads - 1u) / kBsThreads;  // <= 16
+    uint32_t loc[16], sum = 0u, mx = 0u;
+#pragma unroll
+    for (uint32_t w = 0; w < 16u; w++) {
+        const uint32_t i = (uint32_t)tid * wpt + w;
+        loc[w] = w < wpt && i < nwords ? words[swz(i)] : 0u;
+        const uint32_t lo = loc[w] & 0xFFFFu, hi = loc[w] >> 16;
+        sum += lo + hi;
+        mx = max(mx, max(lo, hi));
+    }
+    if (mx > kBsMaxRun) *s_flag = 1u;
+    uint32_t all;
+    uint32_t run = block_exclusive_scan<kBsThreads>(sum, s_tot, &all);
+#pragma unroll
+    for (uint32_t w = 0; w < 16u; w++) {
+        const uint32_t i = (uint32_t)tid * wpt + w;
+        if (w < wpt && i < nwords) {
+            const uint32_t lo = loc[w] & 0xFFFFu, hi = loc[w] >> 16;
+            words[swz(i)] = run | ((run + lo) << 16);
+            run += lo + hi;
+        }
+    }
+    __syncthreads();
+    if (*s_flag) return false;  // uniform: a run too long for one thread
+    // every pair takes its key's next slot (any order among equal keys)
+#pragma unroll
+    for (int j = 0; j < kBsItems; j++) {
+        if ((uint32_t)j >= iw) break;
+        const uint32_t e = wbase + (uint32_t)j * 64u + (uint32_t)lane;
+        if (e < size) {
+            const uint32_t half = (k[j] & 1u) * 16u;
+            const uint32_t slot = (atomicAdd(&words[swz(k[j] >> 1)], 1u << half) >> half) & 0xFFFFu;
+            s_idx[slot] = (uint16_t)e;
+            s_bin[slot] = (uint16_t)k[j];
+        }
+    }
+    __syncthreads();
+    // runs of equal keys into input order
+    for (uint32_t i = (uint32_t)tid; i < size; i += kBsThreads) {
+        const uint32_t key = s_bin[i];
+        const bool first = i == 0u || s_bin[i - 1u] != key;
+        if (!first || i + 1u >= size || s_bin[i + 1u] != key) continue;
+        uint32_t r = 2u;
+        while (i + r < size && s_bin[i + r] == key) r++;
+        for (uint32_t a = i + 1u; a < i + r; a++) {
+            const uint32_t x = s_idx[a];
+            uint32_t c = a;
+            while (c > i && s_idx[c - 1u] > x) {
+                s_idx[c] = s_idx[c - 1u];
+                c--;
+            }
+            s_idx[c] = (uint16_t)x;
+        }
+    }
+    __syncthreads();
+    // values in sorted order (read before any is overwritten), then out
+    uint32_t vv[kBsItems];
+#pragma unroll
+    for (int j = 0; j < kBsItems; j++) {
+        const uint32_t i = (uint32_t)j * kBsThreads + (uint32_t)tid;
+        vv[j] = (uint32_t)j < iw && i < size ? vals[start + s_idx[i]] : 0u;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kBsItems; j++) {
+        const uint32_t i = (uint32_t)j * kBsThreads + (uint32_t)tid;
+        if ((uint32_t)j < iw && i < size) {
+            vals[start + i] = vv[j];
+            gather_out[start + i] = gather_src[vv[j]];
+        }
+    }
+    return true;
+}
+
+// Workgroup b sorts bucket b = [offs[b], offs[b + 1]) (the last one ends at
+// the pair count) of (keys, vals) by the key bits below the top digit, then
+// writes vals in place and gather_out[i] = gather_src[vals[i]].  n and cap
+// are the pair count and the key cap (from n_dev / cap_dev when given).
+__global__ __launch_bounds__(kBsThreads) void bucket_sort_kernel(uint32_t* __restrict__ keys,
+                                                                  uint32_t* __restrict__ vals,
+                                                                  const uint32_t* __restrict__ offs, uint32_t n,
+                                                                  const uint32_t* __restrict__ n_dev, uint32_t cap,
+                                                                  const uint32_t* __restrict__ cap_dev,
+                                                                  const uint32_t* __restrict__ gather_src,
+                                                                  uint32_t* __restrict__ gather_out,
+                                                                  uint32_t* __restrict__ tmp_k,
+                                                                  uint32_t* __restrict__ tmp_v) {
+    // LSD passes: keys, values and per-wave histograms; counting path: bins,
+    // slots and keys (bucket_count_sort)
+    __shared__ uint32_t s_raw[2 * kBsCap + kBsWaves * kRadix];
+    uint32_t* s_k = s_raw;
+    uint32_t* s_v = s_raw + kBsCap;
+    uint32_t(*s_hist)[kRadix] = reinterpret_cast<uint32_t(*)[kRadix]>(s_raw + 2 * kBsCap);
+    __shared__ uint32_t s_start[kRadix], s_cnt[kRadix], s_run[kRadix];
+    __shared__ uint32_t s_tot[kBsWaves];
+    __shared__ uint32_t s_flag;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t b = blockIdx.x;
+    if (n_dev) n = min(n, *n_dev);
+    if (cap_dev) cap = *cap_dev;
+    const uint32_t low = top_digit_shift(cap);  // key bits below the top digit
+    const uint32_t end = min(n, b + 1u < kBsBuckets ? offs[b + 1] : n);
+    const uint32_t start = min(offs[b], end);
+    if (end == start) return;
+    const uint32_t size = end - start, passes = (low + 7u) / 8u;
+    uint32_t k[kBsItems], v[kBsItems], pos[kBsItems];
+
+    if (size <= kBsCap) {
+        // the whole bucket in registers: counted into order, or reordered
+        // through LDS by each LSD pass
+        const uint32_t iw = (size + kBsThreads - 1u) / kBsThreads;
+        const uint32_t wbase = (uint32_t)wave * 64u * iw;
+#pragma unroll
+        for (int j = 0; j < kBsItems; j++) {
+            if ((uint32_t)j >= iw) break;
+            const uint32_t e = wbase + (uint32_t)j * 64u + (uint32_t)lane;
+            k[j] = e < size ? keys[start + e] : 0u;
+        }
+        if (low > 0u && low <= kBsCountBits &&
+            bucket_count_sort(k, iw, size, low, start, vals, gather_src, gather_out, s_raw, s_tot, &s_flag))
+            return;
+#pragma unroll
+        for (int j = 0; j < kBsItems; j++) {
+            if ((uint32_t)j >= iw) break;
+            const uint32_t e = wbase + (uint32_t)j * 64u + (uint32_t)lane;
+            v[j] = e < size ? vals[start + e] : 0u;
+        }
+        for (uint32_t p = 0; p < passes; p++) {
+            const uint32_t sh = 8u * p, bits = min(8u, low - sh);
+            bucket_rank(k, pos, iw, size, sh, bits, s_hist, s_start, s_cnt, s_tot);
+#pragma unroll
+            for (int j = 0; j < kBsItems; j++) {
+                if ((uint32_t)j >= iw) break;
+                if (wbase + (uint32_t)j * 64u + (uint32_t)lane < size) {
+                    s_k[pos[j]] = k[j];
+                    s_v[pos[j]] = v[j];
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int j = 0; j < kBsItems; j++) {
+                if ((uint32_t)j >= iw) break;
+                const uint32_t e = wbase + (uint32_t)j * 64u + (uint32_t)lane;
+                if (e < size) {
+                    k[j] = s_k[e];
+                    v[j] = s_v[e];
+                }
+            }
+            __syncthreads();
+        }
+#pragma unroll
+        for (int j = 0; j < kBsItems; j++) {
+            if ((uint32_t)j >= iw) break;
+            const uint32_t e = wbase + (uint32_t)j * 64u + (uint32_t)lane;
+            if (e < size) {
+                vals[start + e] = v[j];
+                gather_out[start + e] = gather_src[v[j]];
+            }
+        }
+        return;
+    }
+
+    // A bucket above the LDS capacity: each pass counts the bucket's digits,
+    // then ranks its chunks in order and writes every pair to the digit's
+    // running offset, from (keys, vals) to (tmp_k, tmp_v) and back.
+    uint32_t *src_k = keys, *src_v = vals, *dst_k = tmp_k, *dst_v = tmp_v;
+    for (uint32_t p = 0; p < passes; p++) {
+        const uint32_t sh = 8u * p, bits = min(8u, low - sh), dmask = (1u << bits) - 1u;
+        if (tid < kRadix) s_run[tid] = 0u;
+        __syncthreads();
+        for (uint32_t e = (uint32_t)tid; e < size; e += kBsThreads) atomicAdd(&s_run[(src_k[start + e] >> sh) & dmask], 1u);
+        __syncthreads();
+        const uint32_t c = tid < kRadix ? s_run[tid] : 0u;
+        uint32_t all;
+        const uint32_t before = block_exclusive_scan<kBsThreads>(c, s_tot, &all);
+        if (tid < kRadix) s_run[tid] = before;
+        __syncthreads();
+        for (uint32_t c0 = 0; c0 < size; c0 += kBsCap) {
+            const uint32_t cnt = min(kBsCap, size - c0);
+            const uint32_t iw = (cnt + kBsThreads - 1u) / kBsThreads;
+            const uint32_t wbase = (uint32_t)wave * 64u * iw;
+#pragma unroll
+            for (int j = 0; j < kBsItems; j++) {
+                if ((uint32_t)j >= iw) break;
+                const uint32_t e = wbase + (uint32_t)j * 64u + (uint32_t)lane;
+                k[j] = e < cnt ? src_k[start + c0 + e] : 0u;
+                v[j] = e < cnt ? src_v[start + c0 + e] : 0u;
+            }
+            bucket_rank(k, pos, iw, cnt, sh, bits, s_hist, s_start, s_cnt, s_tot);
+#pragma unroll
+            for (int j = 0; j < kBsItems; j++) {
+                if ((uint32_t)j >= iw) break;
+                if (wbase + (uint32_t)j * 64u + (uint32_t)lane < cnt) {
+                    const uint32_t d = (k[j] >> sh) & dmask;
+                    const uint32_t dst = start + s_run[d] + (pos[j] - s_start[d]);
+                    dst_k[dst] = k[j];
+                    dst_v[dst] = v[j];
+                }
+            }
+            __syncthreads();
+            if (tid < kRadix) s_run[tid] += s_cnt[tid];
+            __syncthreads();
+        }
+        uint32_t* t = src_k;
+        src_k = dst_k;
+        dst_k = t;
+        t = src_v;
+        src_v = dst_v;
+        dst_v = t;
+    }
+    for (uint32_t e = (uint32_t)tid; e < size; e += kBsThreads) {
+        const uint32_t g = src_v[start + e];
+        vals[start + e] = g;
+        gather_out[start + e] = gather_src[g];
     }
 }
 
@@ -635,6 +999,36 @@ bh_status radix_sort_pairs_k16(bh_ctx* ctx, const uint16_t* keys_in, const uint3
                                const SortDevice& dev) {
     return radix_sort_impl(ctx, keys_in, 2, vals_in, n, key_bits, 0u, 0xFFFFFFFFu, keys_out, 4, vals_out, tmp_keys,
                            2, tmp_vals, scratch, tag, scratch_zeroed, nullptr, nullptr, dev);
+}
+
+bh_status depth_sort_buckets(bh_ctx* ctx, const uint32_t* keys_in, uint32_t n, uint32_t key_sub, uint32_t key_cap,
+                             uint32_t* keys_tmp, uint32_t* vals_out, uint32_t* tmp_keys, uint32_t* tmp_vals,
+                             void* scratch, bool scratch_zeroed, const uint32_t* gather_src, uint32_t* gather_out,
+                             const SortDevice& dev) {
+    if (n == 0) return BH_OK;
+    const DigitPlan plan = digit_plan(8);
+    const ScanPlan sp = scan_plan(n, plan);
+    uint32_t* blk = (uint32_t*)scratch;
+    uint32_t* offs = blk + (size_t)plan.passes * sp.blocks * sp.radix;
+    if (!scratch_zeroed) launch_fill_u32(ctx, blk, 0u, radix_sort_zeroed_words(n, 8));
+    // the top-digit pass: keys to keys_tmp, values (input indices) to vals_out
+    bh_status st;
+    if (sp.items == 8)
+        st = sort_pass<true, 8>(ctx, sp, "depth_sort_up", "depth_sort_scan", "depth_sort_onesweep", keys_in, 4,
+                                nullptr, keys_tmp, 4, vals_out, n, kShiftTop, 8u, key_sub, key_cap, offs, blk, nullptr,
+                                nullptr, dev);
+    else
+        st = sort_pass<true, 4>(ctx, sp, "depth_sort_up", "depth_sort_scan", "depth_sort_onesweep", keys_in, 4,
+                                nullptr, keys_tmp, 4, vals_out, n, kShiftTop, 8u, key_sub, key_cap, offs, blk, nullptr,
+                                nullptr, dev);
+    if (st != BH_OK) return st;
+    {
+        KernelTimer t(ctx, "depth_sort_buckets");
+        const uint32_t n_rest = dev.drop_capped ? std::min(n, dev.n_rest_host) : n;
+        launch(ctx, bucket_sort_kernel, dim3(kBsBuckets), dim3(kBsThreads), 0u, keys_tmp, vals_out, offs, n_rest,
+               dev.drop_capped ? dev.n_rest : dev.n, key_cap, dev.key_cap, gather_src, gather_out, tmp_keys, tmp_vals);
+    }
+    return check_launch(ctx, "depth sort");
 }
 
 __global__ void mask_u32_kernel(const uint32_t* __restrict__ in, uint32_t mask, uint32_t n,
