@@ -701,41 +701,44 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
         const uint32_t* dc = p.device ? ctx->d_counters : nullptr;
         uint32_t* counts_sorted = nullptr;
         BH_TRY(sget((void**)&gfc, (size_t)std::max<uint32_t>(num_splats, 1u) * 4));
+        BH_TRY(sget((void**)&cum, (size_t)p.v * 4));
+        // up to 2^21 splats the depth sort is one top-digit pass and a
+        // per-bucket sort that also writes cum_tiles_hit (four launches);
+        // above, the LSD passes (each bucket would hold more than 8192 splats
+        // of an even spread of depths) and the scan
+        const bool buckets = num_splats <= kBucketSortMaxSplats;
         if (p.v) {
             // depth sort: key' = min(bits - kmin, kmax - kmin + 1); culled splats
             // (all-ones key) map to the cap, and the first pass drops them, so
             // the later passes sort only the visible splats (render.rs:339-346
-            // sorts the visible depths).  The last pass also gathers each
-            // splat's tile count in depth order, so the scan below reads them
-            // contiguously.  A plan with more key bits than the range needs
-            // sorts the same: its extra passes see digit 0 only.
+            // sorts the visible depths).  The LSD sort's last pass also gathers
+            // each splat's tile count in depth order, so the scan below reads
+            // them contiguously.  A plan with more key bits than the range
+            // needs sorts the same: its extra passes see digit 0 only.
             uint32_t *sk, *tk, *tv;
             BH_TRY(ws.get(&sk, num_splats));
             BH_TRY(ws.get(&tk, num_splats));
             BH_TRY(ws.get(&tv, num_splats));
-            BH_TRY(ws.get(&counts_sorted, num_splats));
             SortDevice dev;
             if (dc) dev.key_sub = dc + 4, dev.key_cap = dc + 6, dev.n_rest = dc + 0;
             dev.drop_capped = true;
             dev.n_rest_host = p.v;
             StageRange stage("DepthSort");
-            // up to 2^21 splats: one top-digit pass and a per-bucket sort
-            // (four launches); above, the LSD passes (each bucket would hold
-            // more than 8192 splats of an even spread of depths)
-            if (num_splats <= kBucketSortMaxSplats)
+            if (buckets) {
                 BH_TRY(depth_sort_buckets(ctx, depth_keys, num_splats, p.kmin, p.kcap, sk, gfc, tk, tv, depth_scr,
-                                          true, counts, counts_sorted, dev));
-            else
+                                          true, counts, cum, dev));
+            } else {
+                BH_TRY(ws.get(&counts_sorted, num_splats));
                 BH_TRY(radix_sort_pairs(ctx, depth_keys, nullptr, num_splats, p.key_bits, p.kmin, p.kcap, sk, gfc, tk,
                                         tv, depth_scr, "depth_sort", true, counts, counts_sorted, dev));
+            }
         }
-        BH_TRY(sget((void**)&cum, (size_t)p.v * 4));
         BH_TRY(sget((void**)&projected, (size_t)std::max<uint32_t>(p.v, 1u) * 40));
         BH_TRY(sget((void**)&depths, (size_t)p.v * 4));
         BH_TRY(sget((void**)&tile_ids, (size_t)std::max<uint32_t>(p.m, 1u) * 4));
         BH_TRY(sget((void**)&cgids, (size_t)std::max<uint32_t>(p.m, 1u) * 4));
         if (p.v) {
-            {
+            if (!buckets) {
                 StageRange stage("PrefixSumGaussHits");
                 BH_TRY(inclusive_scan(ctx, counts_sorted, cum, p.v, scan_scr, dc));
             }

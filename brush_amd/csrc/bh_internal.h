@@ -202,6 +202,10 @@ struct SortDevice {
     // (the depth sort's culled splats), so later passes sort n_rest pairs
     bool drop_capped = false;
     uint32_t n_rest_host = 0;
+    // the first pass's upsweep also adds weight[index] of each counted key to
+    // wsum[block][digit] (depth_sort_buckets: a digit's sum of tile counts)
+    const uint32_t* weight = nullptr;
+    uint32_t* wsum = nullptr;
 };
 // Stable sort of (key', value) pairs by the low key_bits bits of
 // key' = min(key - key_sub, key_cap), in ceil(key_bits / 8) passes of equal
@@ -227,16 +231,19 @@ bh_status radix_sort_pairs_k16(bh_ctx* ctx, const uint16_t* keys_in, const uint3
                                bool scratch_zeroed = false, const SortDevice& dev = SortDevice{});
 // Stable sort of (key', index) pairs as radix_sort_pairs sorts them (key' =
 // min(key - key_sub, key_cap), the first pass's drop of capped keys, the
-// sorted indices to vals_out and gather_out[i] = gather_src[vals_out[i]]),
-// for any key width: one pass by the top 8 bits of key_cap's range, then
-// every bucket sorted by one workgroup (in LDS up to 16384 pairs).  keys_tmp,
-// tmp_keys and tmp_vals are n-element buffers; the scratch is
-// radix_sort_scratch_bytes(n, 8), its first radix_sort_zeroed_words(n, 8)
-// words zero (or zeroed here unless scratch_zeroed).
+// sorted indices to vals_out), for any key width: one pass by the top 8 bits
+// of key_cap's range, then every bucket sorted by one workgroup (in LDS up to
+// 16384 pairs), which also writes cum[i] = the inclusive prefix sum of
+// weight[vals_out[.]] through i (the forward's tile counts in depth order).
+// keys_tmp, tmp_keys and tmp_vals are n-element buffers; the scratch is
+// radix_sort_scratch_bytes(n, 32), its first depth_sort_buckets_zeroed_words(n)
+// words zero (or zeroed here unless scratch_zeroed; at most
+// radix_sort_zeroed_words(n, 32)).
 bh_status depth_sort_buckets(bh_ctx* ctx, const uint32_t* keys_in, uint32_t n, uint32_t key_sub, uint32_t key_cap,
                              uint32_t* keys_tmp, uint32_t* vals_out, uint32_t* tmp_keys, uint32_t* tmp_vals,
-                             void* scratch, bool scratch_zeroed, const uint32_t* gather_src, uint32_t* gather_out,
+                             void* scratch, bool scratch_zeroed, const uint32_t* weight, uint32_t* cum,
                              const SortDevice& dev);
+size_t depth_sort_buckets_zeroed_words(uint32_t n);
 // out[i] = in[i] & mask
 void launch_mask_u32(bh_ctx* ctx, const uint32_t* in, uint32_t mask, uint32_t n, uint32_t* out);
 // keys_out[i] = keys_in[perm[i]], vals_out[i] = vals_in[perm[i]]

@@ -21,6 +21,7 @@
 #include <hip/hip_runtime.h>
 
 #include "bh_internal.h"
+#include "bh_wave.h"
 
 namespace bh {
 
@@ -249,6 +250,9 @@ __global__ __launch_bounds__(kThreads) void radix_upsweep_kernel(const K* __rest
                                                                   uint32_t rows, uint32_t* __restrict__ counts,
                                                                   uint32_t* __restrict__ blk, SortDevice dev) {
     __shared__ uint32_t s_hist[kWaves][kRadix];
+    // with dev.weight, each digit's sum of the keys' weights (weight[index])
+    constexpr bool WEIGHTS = FIRST && sizeof(K) == 4;
+    __shared__ uint32_t s_whist[WEIGHTS ? kWaves : 1][kRadix];
     const int tid = threadIdx.x, wave = tid >> 6;
     if (dev.n) n = min(n, *dev.n);
     if (FIRST && dev.key_sub) {
@@ -256,7 +260,10 @@ __global__ __launch_bounds__(kThreads) void radix_upsweep_kernel(const K* __rest
         key_cap = *dev.key_cap;
     }
     if (FIRST && shift == kShiftTop) shift = top_digit_shift(key_cap);
+    const uint32_t* __restrict__ weight = WEIGHTS ? dev.weight : nullptr;
     for (int i = tid; i < kWaves * kRadix; i += kThreads) (&s_hist[0][0])[i] = 0;
+    if (WEIGHTS && weight)
+        for (int i = tid; i < kWaves * kRadix; i += kThreads) (&s_whist[0][0])[i] = 0;
     __syncthreads();
     constexpr int PART = kThreads * ITEMS;
     const uint32_t part = blockIdx.x;
@@ -265,18 +272,31 @@ __global__ __launch_bounds__(kThreads) void radix_upsweep_kernel(const K* __rest
     uint32_t* mine = s_hist[wave];
     // the first pass of a dropping sort does not count capped keys
     const bool drop = FIRST && dev.drop_capped;
-    if (base + PART <= n && (reinterpret_cast<uintptr_t>(keys) & 15u) == 0u) {
+    if (base + PART <= n && (reinterpret_cast<uintptr_t>(keys) & 15u) == 0u &&
+        (reinterpret_cast<uintptr_t>(weight) & 15u) == 0u) {
         // this thread's ITEMS keys as 32-bit words: 16-byte loads (8-byte
         // ones for four 16-bit keys), interleaved across the threads
         constexpr int WORDS = ITEMS * (int)sizeof(K) / 4;
         constexpr int VW = WORDS >= 4 ? 4 : 2;
         uint32_t w[WORDS];
+        uint32_t wt[WEIGHTS ? ITEMS : 1];
         if constexpr (VW == 4) {
             const uint4* k4 = reinterpret_cast<const uint4*>(keys + base);
 #pragma unroll
             for (int j = 0; j < WORDS / 4; j++) {
                 const uint4 q = k4[j * kThreads + tid];
                 w[4 * j] = q.x, w[4 * j + 1] = q.y, w[4 * j + 2] = q.z, w[4 * j + 3] = q.w;
+            }
+            if constexpr (WEIGHTS) {
+                // weights of the same indices (keys are 32-bit here: item e is word e)
+                if (weight) {
+                    const uint4* w4 = reinterpret_cast<const uint4*>(weight + base);
+#pragma unroll
+                    for (int j = 0; j < ITEMS / 4; j++) {
+                        const uint4 q = w4[j * kThreads + tid];
+                        wt[4 * j] = q.x, wt[4 * j + 1] = q.y, wt[4 * j + 2] = q.z, wt[4 * j + 3] = q.w;
+                    }
+                }
             }
         } else {
             const uint2* k2 = reinterpret_cast<const uint2*>(keys + base);
@@ -290,7 +310,11 @@ __global__ __launch_bounds__(kThreads) void radix_upsweep_kernel(const K* __rest
         for (int e = 0; e < ITEMS; e++) {
             const uint32_t kw = sizeof(K) == 4 ? w[e] : (w[e / 2] >> (16 * (e & 1))) & 0xFFFFu;
             const uint32_t k = FIRST ? min(kw - key_sub, key_cap) : kw;
-            if (!(drop && k == key_cap)) atomicAdd(&mine[(k >> shift) & dmask], 1u);
+            if (!(drop && k == key_cap)) {
+                atomicAdd(&mine[(k >> shift) & dmask], 1u);
+                if constexpr (WEIGHTS)
+                    if (weight && wt[e]) atomicAdd(&s_whist[wave][(k >> shift) & dmask], wt[e]);
+            }
         }
     } else {
 #pragma unroll
@@ -299,7 +323,11 @@ __global__ __launch_bounds__(kThreads) void radix_upsweep_kernel(const K* __rest
             if (idx < n) {
                 const uint32_t kw = keys[idx];
                 const uint32_t k = FIRST ? min(kw - key_sub, key_cap) : kw;
-                if (!(drop && k == key_cap)) atomicAdd(&mine[(k >> shift) & dmask], 1u);
+                if (!(drop && k == key_cap)) {
+                    atomicAdd(&mine[(k >> shift) & dmask], 1u);
+                    if constexpr (WEIGHTS)
+                        if (weight && weight[idx]) atomicAdd(&s_whist[wave][(k >> shift) & dmask], weight[idx]);
+                }
             }
         }
     }
@@ -310,6 +338,14 @@ __global__ __launch_bounds__(kThreads) void radix_upsweep_kernel(const K* __rest
         for (int w = 0; w < kWaves; w++) c += s_hist[w][tid];
         counts[(size_t)part * radix + tid] = c;
         if (c) atomicAdd(&blk[(size_t)(part / rows) * radix + tid], c);
+        if constexpr (WEIGHTS) {
+            if (weight) {
+                uint32_t ws = 0;
+#pragma unroll
+                for (int w = 0; w < kWaves; w++) ws += s_whist[w][tid];
+                if (ws) atomicAdd(&dev.wsum[(size_t)(part / rows) * radix + tid], ws);
+            }
+        }
     }
 }
 
@@ -609,10 +645,9 @@ constexpr uint32_t kBsCountBits = 15;
 // in place.  Returns false, having written nothing, when a key occurs more
 // than kBsMaxRun times.  s_raw holds the counters (up to 16384 words), then
 // each slot's input position and key (16384 uint16_t each).
-__device__ bool bucket_count_sort(uint32_t (&k)[kBsItems], uint32_t iw, uint32_t size, uint32_t low,
-                                  uint32_t start, uint32_t* __restrict__ vals,
-                                  const uint32_t* __restrict__ gather_src, uint32_t* __restrict__ gather_out,
-                                  uint32_t* s_raw, uint32_t* s_tot, uint32_t* s_flag) {
+__device__ bool bucket_count_sort(uint32_t (&k)[kBsItems], uint32_t (&v)[kBsItems], uint32_t iw, uint32_t size,
+                                  uint32_t low, uint32_t start, uint32_t* __restrict__ vals, uint32_t* s_raw,
+                                  uint32_t* s_tot, uint32_t* s_flag) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t wbase = (uint32_t)wave * 64u * iw;
     uint32_t* words = s_raw;                                         // counters, two per word
@@ -694,36 +729,85 @@ __device__ bool bucket_count_sort(uint32_t (&k)[kBsItems], uint32_t iw, uint32_t
         }
     }
     __syncthreads();
-    // values in sorted order (read before any is overwritten), then out
-    uint32_t vv[kBsItems];
+    // values in sorted order into v[] (wave-major, as the items were laid
+    // out), read before any is overwritten, then out
 #pragma unroll
     for (int j = 0; j < kBsItems; j++) {
-        const uint32_t i = (uint32_t)j * kBsThreads + (uint32_t)tid;
-        vv[j] = (uint32_t)j < iw && i < size ? vals[start + s_idx[i]] : 0u;
+        const uint32_t i = wbase + (uint32_t)j * 64u + (uint32_t)lane;
+        v[j] = (uint32_t)j < iw && i < size ? vals[start + s_idx[i]] : 0u;
     }
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < kBsItems; j++) {
-        const uint32_t i = (uint32_t)j * kBsThreads + (uint32_t)tid;
-        if ((uint32_t)j < iw && i < size) {
-            vals[start + i] = vv[j];
-            gather_out[start + i] = gather_src[vv[j]];
-        }
+        const uint32_t i = wbase + (uint32_t)j * 64u + (uint32_t)lane;
+        if ((uint32_t)j < iw && i < size) vals[start + i] = v[j];
     }
     return true;
 }
 
+// One chunk of cum_tiles_hit: vv holds the chunk's sorted values (cnt <=
+// kBsCap of them, wave-major items, ipt per lane); out[e] = offset + the
+// workgroup's sum of `part` + the inclusive prefix sum of weight[vv] through
+// chunk element e (a wave scan per item row, the waves' totals and shares of
+// `part` through LDS).  Returns the chunk's weight plus the sum of `part`.
+__device__ uint32_t cum_chunk(const uint32_t (&vv)[kBsItems], uint32_t ipt, uint32_t cnt,
+                              const uint32_t* __restrict__ weight, uint32_t* __restrict__ out, uint32_t offset,
+                              uint32_t part, uint32_t* s_w) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t wb = (uint32_t)wave * 64u * ipt;
+    uint32_t w[kBsItems];
+#pragma unroll
+    for (int j = 0; j < kBsItems; j++) {
+        const uint32_t e = wb + (uint32_t)j * 64u + (uint32_t)lane;
+        w[j] = (uint32_t)j < ipt && e < cnt ? weight[vv[j]] : 0u;
+    }
+    uint32_t run = 0u;  // the wave's running total (uniform)
+#pragma unroll
+    for (int j = 0; j < kBsItems; j++) {
+        if ((uint32_t)j < ipt) {  // uniform
+            const uint32_t x = wave_incl_add_u32(w[j]);
+            w[j] = x + run;
+            run += (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
+        }
+    }
+    const uint32_t pw = (uint32_t)__builtin_amdgcn_readlane((int)wave_incl_add_u32(part), 63);
+    if (lane == 0) {
+        s_w[wave] = run;
+        s_w[kBsWaves + wave] = pw;
+    }
+    __syncthreads();
+    uint32_t before = 0u, all = 0u, base = 0u;
+#pragma unroll
+    for (int q = 0; q < kBsWaves; q++) {
+        const uint32_t t = s_w[q];
+        before += q < wave ? t : 0u;
+        all += t;
+        base += s_w[kBsWaves + q];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kBsItems; j++) {
+        const uint32_t e = wb + (uint32_t)j * 64u + (uint32_t)lane;
+        if ((uint32_t)j < ipt && e < cnt) out[e] = offset + base + before + w[j];
+    }
+    return all + base;
+}
+
 // Workgroup b sorts bucket b = [offs[b], offs[b + 1]) (the last one ends at
-// the pair count) of (keys, vals) by the key bits below the top digit, then
-// writes vals in place and gather_out[i] = gather_src[vals[i]].  n and cap
-// are the pair count and the key cap (from n_dev / cap_dev when given).
+// the pair count) of (keys, vals) by the key bits below the top digit, writes
+// vals in place and cum[i] = the inclusive prefix sum of weight[vals[.]] over
+// the whole sorted order: the bucket's own prefix plus the weights of the
+// buckets before it, from the first pass's per-block digit sums wsum
+// [wsum_words / 256][256].  n and cap are the pair count and the key cap
+// (from n_dev / cap_dev when given).
 __global__ __launch_bounds__(kBsThreads) void bucket_sort_kernel(uint32_t* __restrict__ keys,
                                                                   uint32_t* __restrict__ vals,
                                                                   const uint32_t* __restrict__ offs, uint32_t n,
                                                                   const uint32_t* __restrict__ n_dev, uint32_t cap,
                                                                   const uint32_t* __restrict__ cap_dev,
-                                                                  const uint32_t* __restrict__ gather_src,
-                                                                  uint32_t* __restrict__ gather_out,
+                                                                  const uint32_t* __restrict__ weight,
+                                                                  const uint32_t* __restrict__ wsum,
+                                                                  uint32_t wsum_words, uint32_t* __restrict__ cum,
                                                                   uint32_t* __restrict__ tmp_k,
                                                                   uint32_t* __restrict__ tmp_v) {
     // LSD passes: keys, values and per-wave histograms; counting path: bins,
@@ -734,6 +818,7 @@ __global__ __launch_bounds__(kBsThreads) void bucket_sort_kernel(uint32_t* __res
     uint32_t(*s_hist)[kRadix] = reinterpret_cast<uint32_t(*)[kRadix]>(s_raw + 2 * kBsCap);
     __shared__ uint32_t s_start[kRadix], s_cnt[kRadix], s_run[kRadix];
     __shared__ uint32_t s_tot[kBsWaves];
+    __shared__ uint32_t s_w[2 * kBsWaves];
     __shared__ uint32_t s_flag;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t b = blockIdx.x;
@@ -745,6 +830,12 @@ __global__ __launch_bounds__(kBsThreads) void bucket_sort_kernel(uint32_t* __res
     if (end == start) return;
     const uint32_t size = end - start, passes = (low + 7u) / 8u;
     uint32_t k[kBsItems], v[kBsItems], pos[kBsItems];
+    // the weights of the buckets before this one: wsum[block][digit] summed
+    // over the blocks and the digits below b
+    // over the blocks and the digits below b (this thread's share; summed
+    // over the workgroup by bucket_cum)
+    uint32_t part = 0u;
+    for (uint32_t i = (uint32_t)tid; i < wsum_words; i += kBsThreads) part += (i & (kBsBuckets - 1u)) < b ? wsum[i] : 0u;
 
     if (size <= kBsCap) {
         // the whole bucket in registers: counted into order, or reordered
@@ -757,16 +848,17 @@ __global__ __launch_bounds__(kBsThreads) void bucket_sort_kernel(uint32_t* __res
             const uint32_t e = wbase + (uint32_t)j * 64u + (uint32_t)lane;
             k[j] = e < size ? keys[start + e] : 0u;
         }
-        if (low > 0u && low <= kBsCountBits &&
-            bucket_count_sort(k, iw, size, low, start, vals, gather_src, gather_out, s_raw, s_tot, &s_flag))
-            return;
+        const bool counted = low > 0u && low <= kBsCountBits &&
+                             bucket_count_sort(k, v, iw, size, low, start, vals, s_raw, s_tot, &s_flag);
+        if (!counted) {
 #pragma unroll
-        for (int j = 0; j < kBsItems; j++) {
-            if ((uint32_t)j >= iw) break;
-            const uint32_t e = wbase + (uint32_t)j * 64u + (uint32_t)lane;
-            v[j] = e < size ? vals[start + e] : 0u;
+            for (int j = 0; j < kBsItems; j++) {
+                if ((uint32_t)j >= iw) break;
+                const uint32_t e = wbase + (uint32_t)j * 64u + (uint32_t)lane;
+                v[j] = e < size ? vals[start + e] : 0u;
+            }
         }
-        for (uint32_t p = 0; p < passes; p++) {
+        for (uint32_t p = 0; p < (counted ? 0u : passes); p++) {
             const uint32_t sh = 8u * p, bits = min(8u, low - sh);
             bucket_rank(k, pos, iw, size, sh, bits, s_hist, s_start, s_cnt, s_tot);
 #pragma unroll
@@ -789,33 +881,67 @@ __global__ __launch_bounds__(kBsThreads) void bucket_sort_kernel(uint32_t* __res
             }
             __syncthreads();
         }
+        if (!counted) {
 #pragma unroll
-        for (int j = 0; j < kBsItems; j++) {
-            if ((uint32_t)j >= iw) break;
-            const uint32_t e = wbase + (uint32_t)j * 64u + (uint32_t)lane;
-            if (e < size) {
-                vals[start + e] = v[j];
-                gather_out[start + e] = gather_src[v[j]];
+            for (int j = 0; j < kBsItems; j++) {
+                if ((uint32_t)j >= iw) break;
+                const uint32_t e = wbase + (uint32_t)j * 64u + (uint32_t)lane;
+                if (e < size) vals[start + e] = v[j];
             }
         }
-        return;
-    }
-
-    // A bucket above the LDS capacity: each pass counts the bucket's digits,
-    // then ranks its chunks in order and writes every pair to the digit's
-    // running offset, from (keys, vals) to (tmp_k, tmp_v) and back.
-    uint32_t *src_k = keys, *src_v = vals, *dst_k = tmp_k, *dst_v = tmp_v;
-    for (uint32_t p = 0; p < passes; p++) {
-        const uint32_t sh = 8u * p, bits = min(8u, low - sh), dmask = (1u << bits) - 1u;
-        if (tid < kRadix) s_run[tid] = 0u;
-        __syncthreads();
-        for (uint32_t e = (uint32_t)tid; e < size; e += kBsThreads) atomicAdd(&s_run[(src_k[start + e] >> sh) & dmask], 1u);
-        __syncthreads();
-        const uint32_t c = tid < kRadix ? s_run[tid] : 0u;
-        uint32_t all;
-        const uint32_t before = block_exclusive_scan<kBsThreads>(c, s_tot, &all);
-        if (tid < kRadix) s_run[tid] = before;
-        __syncthreads();
+        // cum_tiles_hit from the sorted values still in registers
+        cum_chunk(v, iw, size, weight, cum + start, 0u, part, s_w);
+    } else {
+        // A bucket above the LDS capacity: each pass counts the bucket's digits,
+        // then ranks its chunks in order and writes every pair to the digit's
+        // running offset, from (keys, vals) to (tmp_k, tmp_v) and back.
+        uint32_t *src_k = keys, *src_v = vals, *dst_k = tmp_k, *dst_v = tmp_v;
+        for (uint32_t p = 0; p < passes; p++) {
+            const uint32_t sh = 8u * p, bits = min(8u, low - sh), dmask = (1u << bits) - 1u;
+            if (tid < kRadix) s_run[tid] = 0u;
+            __syncthreads();
+            for (uint32_t e = (uint32_t)tid; e < size; e += kBsThreads) atomicAdd(&s_run[(src_k[start + e] >> sh) & dmask], 1u);
+            __syncthreads();
+            const uint32_t c = tid < kRadix ? s_run[tid] : 0u;
+            uint32_t all;
+            const uint32_t before = block_exclusive_scan<kBsThreads>(c, s_tot, &all);
+            if (tid < kRadix) s_run[tid] = before;
+            __syncthreads();
+            for (uint32_t c0 = 0; c0 < size; c0 += kBsCap) {
+                const uint32_t cnt = min(kBsCap, size - c0);
+                const uint32_t iw = (cnt + kBsThreads - 1u) / kBsThreads;
+                const uint32_t wbase = (uint32_t)wave * 64u * iw;
+    #pragma unroll
+                for (int j = 0; j < kBsItems; j++) {
+                    if ((uint32_t)j >= iw) break;
+                    const uint32_t e = wbase + (uint32_t)j * 64u + (uint32_t)lane;
+                    k[j] = e < cnt ? src_k[start + c0 + e] : 0u;
+                    v[j] = e < cnt ? src_v[start + c0 + e] : 0u;
+                }
+                bucket_rank(k, pos, iw, cnt, sh, bits, s_hist, s_start, s_cnt, s_tot);
+    #pragma unroll
+                for (int j = 0; j < kBsItems; j++) {
+                    if ((uint32_t)j >= iw) break;
+                    if (wbase + (uint32_t)j * 64u + (uint32_t)lane < cnt) {
+                        const uint32_t d = (k[j] >> sh) & dmask;
+                        const uint32_t dst = start + s_run[d] + (pos[j] - s_start[d]);
+                        dst_k[dst] = k[j];
+                        dst_v[dst] = v[j];
+                    }
+                }
+                __syncthreads();
+                if (tid < kRadix) s_run[tid] += s_cnt[tid];
+                __syncthreads();
+            }
+            uint32_t* t = src_k;
+            src_k = dst_k;
+            dst_k = t;
+            t = src_v;
+            src_v = dst_v;
+            dst_v = t;
+        }
+        // the sorted values into vals, and cum_tiles_hit over them, by chunks
+        uint32_t carry = 0u;
         for (uint32_t c0 = 0; c0 < size; c0 += kBsCap) {
             const uint32_t cnt = min(kBsCap, size - c0);
             const uint32_t iw = (cnt + kBsThreads - 1u) / kBsThreads;
@@ -824,35 +950,11 @@ __global__ __launch_bounds__(kBsThreads) void bucket_sort_kernel(uint32_t* __res
             for (int j = 0; j < kBsItems; j++) {
                 if ((uint32_t)j >= iw) break;
                 const uint32_t e = wbase + (uint32_t)j * 64u + (uint32_t)lane;
-                k[j] = e < cnt ? src_k[start + c0 + e] : 0u;
                 v[j] = e < cnt ? src_v[start + c0 + e] : 0u;
+                if (e < cnt && src_v != vals) vals[start + c0 + e] = v[j];
             }
-            bucket_rank(k, pos, iw, cnt, sh, bits, s_hist, s_start, s_cnt, s_tot);
-#pragma unroll
-            for (int j = 0; j < kBsItems; j++) {
-                if ((uint32_t)j >= iw) break;
-                if (wbase + (uint32_t)j * 64u + (uint32_t)lane < cnt) {
-                    const uint32_t d = (k[j] >> sh) & dmask;
-                    const uint32_t dst = start + s_run[d] + (pos[j] - s_start[d]);
-                    dst_k[dst] = k[j];
-                    dst_v[dst] = v[j];
-                }
-            }
-            __syncthreads();
-            if (tid < kRadix) s_run[tid] += s_cnt[tid];
-            __syncthreads();
+            carry += cum_chunk(v, iw, cnt, weight, cum + start + c0, carry, c0 == 0u ? part : 0u, s_w);
         }
-        uint32_t* t = src_k;
-        src_k = dst_k;
-        dst_k = t;
-        t = src_v;
-        src_v = dst_v;
-        dst_v = t;
-    }
-    for (uint32_t e = (uint32_t)tid; e < size; e += kBsThreads) {
-        const uint32_t g = src_v[start + e];
-        vals[start + e] = g;
-        gather_out[start + e] = gather_src[g];
     }
 }
 
@@ -1003,32 +1105,44 @@ bh_status radix_sort_pairs_k16(bh_ctx* ctx, const uint16_t* keys_in, const uint3
 
 bh_status depth_sort_buckets(bh_ctx* ctx, const uint32_t* keys_in, uint32_t n, uint32_t key_sub, uint32_t key_cap,
                              uint32_t* keys_tmp, uint32_t* vals_out, uint32_t* tmp_keys, uint32_t* tmp_vals,
-                             void* scratch, bool scratch_zeroed, const uint32_t* gather_src, uint32_t* gather_out,
+                             void* scratch, bool scratch_zeroed, const uint32_t* weight, uint32_t* cum,
                              const SortDevice& dev) {
     if (n == 0) return BH_OK;
     const DigitPlan plan = digit_plan(8);
     const ScanPlan sp = scan_plan(n, plan);
+    // block sums | per-block digit weight sums (both zeroed) | offsets
+    const size_t blk_words = (size_t)sp.blocks * sp.radix;
     uint32_t* blk = (uint32_t*)scratch;
-    uint32_t* offs = blk + (size_t)plan.passes * sp.blocks * sp.radix;
-    if (!scratch_zeroed) launch_fill_u32(ctx, blk, 0u, radix_sort_zeroed_words(n, 8));
+    uint32_t* wsum = blk + blk_words;
+    uint32_t* offs = wsum + blk_words;
+    if (!scratch_zeroed) launch_fill_u32(ctx, blk, 0u, 2 * blk_words);
+    SortDevice d = dev;
+    d.weight = weight;
+    d.wsum = wsum;
     // the top-digit pass: keys to keys_tmp, values (input indices) to vals_out
     bh_status st;
     if (sp.items == 8)
         st = sort_pass<true, 8>(ctx, sp, "depth_sort_up", "depth_sort_scan", "depth_sort_onesweep", keys_in, 4,
                                 nullptr, keys_tmp, 4, vals_out, n, kShiftTop, 8u, key_sub, key_cap, offs, blk, nullptr,
-                                nullptr, dev);
+                                nullptr, d);
     else
         st = sort_pass<true, 4>(ctx, sp, "depth_sort_up", "depth_sort_scan", "depth_sort_onesweep", keys_in, 4,
                                 nullptr, keys_tmp, 4, vals_out, n, kShiftTop, 8u, key_sub, key_cap, offs, blk, nullptr,
-                                nullptr, dev);
+                                nullptr, d);
     if (st != BH_OK) return st;
     {
         KernelTimer t(ctx, "depth_sort_buckets");
         const uint32_t n_rest = dev.drop_capped ? std::min(n, dev.n_rest_host) : n;
         launch(ctx, bucket_sort_kernel, dim3(kBsBuckets), dim3(kBsThreads), 0u, keys_tmp, vals_out, offs, n_rest,
-               dev.drop_capped ? dev.n_rest : dev.n, key_cap, dev.key_cap, gather_src, gather_out, tmp_keys, tmp_vals);
+               dev.drop_capped ? dev.n_rest : dev.n, key_cap, dev.key_cap, weight, wsum, (uint32_t)blk_words, cum,
+               tmp_keys, tmp_vals);
     }
     return check_launch(ctx, "depth sort");
+}
+
+size_t depth_sort_buckets_zeroed_words(uint32_t n) {
+    const ScanPlan sp = scan_plan(n, digit_plan(8));
+    return 2 * (size_t)sp.blocks * sp.radix;
 }
 
 __global__ void mask_u32_kernel(const uint32_t* __restrict__ in, uint32_t mask, uint32_t n,
