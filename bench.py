@@ -103,6 +103,9 @@ def algorithmic_bytes(name: str, n: int, v: int, m: int, m_post: int, t: int, p:
         return v * (4 + 48) + v * (40 + 4)               # gid + row slot in; ordered row, depth out
     if name == "scan":
         return 12.0 * v                                  # gid + gathered count in, cum out
+    if name == "depth_sort_buckets":
+        # (key, gid) in, the gid's tile count gathered, (gid, cum_tiles_hit) out
+        return 20.0 * v
     if name == "map_intersects":
         # gid + global-id row slot (48 B) + cum in; ordered row + depth out; (tile, id) pairs out,
         # the tile ids 16-bit below 2^16 tiles
@@ -132,16 +135,20 @@ def algorithmic_bytes(name: str, n: int, v: int, m: int, m_post: int, t: int, p:
     return 0.0
 
 
+BUCKET_SORT_MAX_SPLATS = 1 << 21  # the depth sort's bucket path (brush_amd/csrc/api.hip)
+
+
 def sort_bytes_per_launch(name: str, passes: float, n: int, m: int, t: int) -> float:
     """Algorithmic bytes of one launch of a sort kernel: every digit pass reads
     and writes (key, u32 value) once; the depth sort's first pass generates
     its values (global ids) instead of reading them; each pass's upsweep reads
-    the keys (the offset scan's few counters are not counted).  Below 2^16
-    tiles the tile sort's keys are 16-bit until its last pass writes the
-    32-bit sorted ids."""
+    the keys (the offset scan's few counters are not counted), and the bucket
+    path's one upsweep also each splat's tile count.  Below 2^16 tiles the
+    tile sort's keys are 16-bit until its last pass writes the 32-bit sorted
+    ids."""
     k16 = t < 65536
     if name == "depth_sort_up":
-        return 4.0 * n
+        return (8.0 if n <= BUCKET_SORT_MAX_SPLATS else 4.0) * n
     if name == "tile_sort_up":
         return (2.0 if k16 else 4.0) * m
     if name == "depth_sort_onesweep":

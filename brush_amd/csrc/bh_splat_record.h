@@ -24,6 +24,8 @@
 // block_end only, all of which lie in walked batches.
 #pragma once
 
+#include "bh_wave.h"
+
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -71,20 +73,19 @@ __device__ __forceinline__ uint32_t order_bucket(uint32_t len) {
 }
 
 // The tile of dispatch slot `slot`, or num_tiles when the slot lies past the
-// last recorded tile.  The bucket counts are wave-uniform: scalar loads, all
-// issued before the first comparison, and a scalar walk over the buckets.
+// last recorded tile.  Called by a whole wave (64 lanes) with a uniform slot:
+// lane b holds bucket b's count, a wave scan gives each bucket's end, and the
+// slot's bucket is the first whose end lies past it.
+static_assert(kOrderBuckets == 64, "one order bucket per lane of a wave");
 __device__ __forceinline__ uint32_t ordered_tile(uint32_t slot, const uint32_t* __restrict__ count,
                                                  const uint32_t* __restrict__ list, uint32_t num_tiles) {
-    uint32_t c[kOrderBuckets];
-#pragma unroll
-    for (uint32_t b = 0; b < kOrderBuckets; ++b) c[b] = count[b];
-    uint32_t start = 0, bucket = kOrderBuckets;
-#pragma unroll
-    for (uint32_t b = 0; b < kOrderBuckets; ++b) {
-        if (bucket == kOrderBuckets && slot - start < c[b]) bucket = b;
-        if (bucket == kOrderBuckets) start += c[b];
-    }
-    if (bucket == kOrderBuckets) return num_tiles;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t c = count[lane];
+    const uint32_t end = wave_incl_add_u32(c);
+    const uint64_t past = __builtin_amdgcn_ballot_w64(slot < end);
+    if (past == 0ull) return num_tiles;
+    const uint32_t bucket = (uint32_t)__builtin_ctzll(past);
+    const uint32_t start = (uint32_t)__builtin_amdgcn_readlane((int)(end - c), (int)bucket);
     return list[(size_t)bucket * num_tiles + (slot - start)];
 }
 
