@@ -227,10 +227,10 @@ static ScanPlan scan_plan(uint32_t n, const DigitPlan& d) {
     return s;
 }
 
-// A first pass whose shift is kShiftTop sorts by the top 8 bits of the
-// transformed key range instead: bit_length(key_cap) - 8 (0 below 9 bits),
-// taken from the key cap the kernel reads, so the digit follows a device-held
-// range.
+// A first pass over 32-bit keys whose shift is kShiftTop sorts by the top 8
+// bits of the transformed key range instead: bit_length(key_cap) - 8 (0 below
+// 9 bits), taken from the key cap the kernel reads, so the digit follows a
+// device-held range.
 constexpr uint32_t kShiftTop = 0xFFFFFFFFu;
 __device__ __forceinline__ uint32_t top_digit_shift(uint32_t cap) {
     const uint32_t bl = cap ? 32u - (uint32_t)__clz((int)cap) : 0u;
@@ -259,7 +259,8 @@ __global__ __launch_bounds__(kThreads) void radix_upsweep_kernel(const K* __rest
         key_sub = *dev.key_sub;
         key_cap = *dev.key_cap;
     }
-    if (FIRST && shift == kShiftTop) shift = top_digit_shift(key_cap);
+    if constexpr (FIRST && sizeof(K) == 4)
+        if (shift == kShiftTop) shift = top_digit_shift(key_cap);
     const uint32_t* __restrict__ weight = WEIGHTS ? dev.weight : nullptr;
     for (int i = tid; i < kWaves * kRadix; i += kThreads) (&s_hist[0][0])[i] = 0;
     if (WEIGHTS && weight)
@@ -467,7 +468,8 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const KI* __restrict
         key_sub = *dev.key_sub;
         key_cap = *dev.key_cap;
     }
-    if (FIRST && shift == kShiftTop) shift = top_digit_shift(key_cap);
+    if constexpr (FIRST && sizeof(KI) == 4)
+        if (shift == kShiftTop) shift = top_digit_shift(key_cap);
     // a partition past a device-held count has no pairs (the grid is sized
     // for the capacity); the upsweep wrote its counts as zeros
     if ((uint64_t)part * (kThreads * ITEMS) >= n) return;
@@ -499,7 +501,23 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const KI* __restrict
 #pragma unroll
         for (int j = 0; j < ITEMS; j++) gv[j] = (kept >> j) & 1u ? gather_src[v[j]] : 0u;
     }
-    wave_rank<ITEMS>(k, kept, ITEMS, shift, digit_bits, s_wave_hist[wave], pos);
+    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+#pragma unroll
+    for (int j = 0; j < ITEMS; j++) {
+        const bool valid = (kept >> j) & 1u;
+        uint32_t d = (k[j] >> shift) & dmask;
+        uint64_t peers = __ballot(valid);
+        for (uint32_t b = 0; b < digit_bits; b++) {
+            bool bit = (d >> b) & 1u;
+            uint64_t bal = __ballot(bit);
+            peers &= bit ? bal : ~bal;
+        }
+        uint32_t prefix = 0;
+        if (valid) prefix = s_wave_hist[wave][d];
+        pos[j] = prefix + (uint32_t)__popcll(peers & lt_mask);
+        // the highest lane of each peer group advances the wave's running count
+        if (valid && (peers >> lane) == 1ull) s_wave_hist[wave][d] = prefix + (uint32_t)__popcll(peers);
+    }
     __syncthreads();
 
     // per-digit counts of the partition and each wave's offset inside them
