@@ -301,8 +301,9 @@ struct Bump {
 };
 
 static uint32_t bit_length(uint32_t x) { return x ? 32u - (uint32_t)__builtin_clz(x) : 0u; }
-// the largest splat count the depth sort's bucket path takes
+// the largest splat count and depth-key width the depth sort's bucket path takes
 constexpr uint32_t kBucketSortMaxSplats = 1u << 21;
+constexpr uint32_t kBucketSortMaxKeyBits = 24;
 
 // bh_radix_argsort's body over a workspace provider (the pool, or the fixed
 // scratch of the allocation-free entry point).
@@ -702,11 +703,14 @@ bh_status bh_render_forward(bh_ctx* ctx, const bh_project_uniforms* uin, const f
         uint32_t* counts_sorted = nullptr;
         BH_TRY(sget((void**)&gfc, (size_t)std::max<uint32_t>(num_splats, 1u) * 4));
         BH_TRY(sget((void**)&cum, (size_t)p.v * 4));
-        // up to 2^21 splats the depth sort is one top-digit pass and a
+        // up to 2^21 splats and a key range of up to 24 bits (depths within a
+        // factor of about four), the depth sort is one top-digit pass and a
         // per-bucket sort that also writes cum_tiles_hit (four launches);
-        // above, the LSD passes (each bucket would hold more than 8192 splats
-        // of an even spread of depths) and the scan
-        const bool buckets = num_splats <= kBucketSortMaxSplats;
+        // otherwise the LSD passes and the scan.  More splats would put more
+        // than 8192 in a bucket at an even spread of depths; a wider range
+        // (near floaters in front of a scene) leaves most splats in a few
+        // top digits, buckets far above the 16384 pairs sorted in LDS.
+        const bool buckets = num_splats <= kBucketSortMaxSplats && p.key_bits <= kBucketSortMaxKeyBits;
         if (p.v) {
             // depth sort: key' = min(bits - kmin, kmax - kmin + 1); culled splats
             // (all-ones key) map to the cap, and the first pass drops them, so

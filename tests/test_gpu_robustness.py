@@ -190,19 +190,21 @@ def test_mostly_culled_scene_sorts_only_visible(gpu):
         compare_forward(g, o)
 
 
-@pytest.mark.parametrize("case", ["crowded_bucket", "one_depth", "chunked_bucket"])
+@pytest.mark.parametrize("case", ["crowded_bucket", "one_depth", "chunked_bucket", "wide_range"])
 def test_depth_sort_bucket_extremes(gpu, case):
     """The depth sort's bucket path (one pass by the top 8 bits of the key
-    range, then each bucket sorted by one workgroup) at its extremes, bit for
-    bit against the restatement's stable sort, from a fresh context (counts
-    read first) and from a plan:
+    range, then each bucket sorted by one workgroup) at its extremes, and the
+    switch to the LSD passes, bit for bit against the restatement's stable
+    sort, from a fresh context (counts read first) and from a plan:
     * crowded_bucket: 150k of 200k splats share one depth, so one bucket holds
       them all (above the 16384 pairs sorted in LDS) among spread buckets;
     * one_depth: every splat at one depth (a one-key range: the top-digit
       pass alone sorts, no bits below it);
     * chunked_bucket: 40k splats within 1e-3 of one depth among 20k spread
       over [4, 6], so one or two buckets of ~40k pairs are sorted in chunks
-      by the key bits below the top digit."""
+      by the key bits below the top digit;
+    * wide_range: depths from ~0.3 to ~50 (a key range above 24 bits), which
+      takes the LSD passes; the second run queues them from the plan."""
     print(f"[case] depth sort buckets: {case}", flush=True)
     cam = _cam()
     if case == "crowded_bucket":
@@ -211,9 +213,15 @@ def test_depth_sort_bucket_extremes(gpu, case):
     elif case == "one_depth":
         tr, sh, op = rng_scene(60_000, 1.0, (-5.0, -4.0), (0.0, 3.0), 0xD6)
         tr[:, 2] = -0.5
-    else:
+    elif case == "chunked_bucket":
         tr, sh, op = rng_scene(60_000, 1.0, (-5.0, -4.0), (0.0, 3.0), 0xD7)
         tr[:40_000, 2] = np.linspace(0.0, 1e-3, 40_000, dtype=np.float32)[np.random.default_rng(3).permutation(40_000)]
+    else:
+        tr, sh, op = rng_scene(60_000, 1.0, (-5.0, -4.0), (0.0, 3.0), 0xD8)
+        # depth z + 5 from ~0.3 to ~50, the x, y spread with it so they stay on screen
+        z = np.exp(np.random.default_rng(4).uniform(np.log(0.3), np.log(50.0), 60_000)).astype(np.float32) - 5.0
+        tr[:, 0:2] *= ((z + 5.0) / 5.0)[:, None]
+        tr[:, 2] = z
     u = uniforms_for(cam, 256, 256, tr.shape[0], 0)
     o = O.render_forward(u, tr, sh, op, O.FLAG_BWD_INFO)
     assert o.num_visible > 0.9 * tr.shape[0], o.num_visible
