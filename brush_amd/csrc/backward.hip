@@ -30,9 +30,10 @@
 #include "bh_splat_record.h"
 #include "bh_tile_walk.h"
 
-// Candidates staged per batch by the recorded backward (32 or 64).
+// Candidates staged per batch by the recorded backward (32 or 64).  32
+// keeps its LDS at 9 KB (17 workgroups per CU) with three summing slots.
 #ifndef BH_BWD_BATCH
-#define BH_BWD_BATCH 64
+#define BH_BWD_BATCH 32
 #endif
 
 namespace bh {
@@ -342,14 +343,14 @@ void launch_rasterize_backward(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint
 // The gradient-only products use FMA contraction.
 //
 // A splat's K gradient sums are formed through LDS: every lane writes its K
-// values into rows of 64 (one row per sum), and once two splats are queued
-// (the candidate loop alternates two register sets, set a filling slot 0 and
-// set b slot 1), two lanes per row sum its halves (a float4 loop) and one
+// values into rows of 64 (one row per sum) of a slot, and once three splats
+// are queued (two where K = 11: the rows of three slots must fit the wave's
+// 32 row pairs), two lanes per row sum its halves (a float4 loop) and one
 // lane per row applies the splat's factor and adds the total to the splat's
 // gradient row in HBM: about one VALU add per value and one atomic
-// instruction per two splats.  A slot's rows start at an even row, so its two
-// mean rows lie in one lane quad and a quad permute brings each the other's
-// total.
+// instruction per three splats.  A slot's rows start at an even row, so its
+// two mean rows lie in one lane quad and a quad permute brings each the
+// other's total.
 template <bool SMOOTH, bool REFINE, bool DEPTH, int TH>
 __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
     uint32_t img_w, uint32_t img_h, uint32_t tile_bw, uint32_t num_tiles, float bg_r, float bg_g, float bg_b,
@@ -363,8 +364,11 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
     // v_sigma dy dy, vis v_r, vis v_g, vis v_b, the opacity lane, (refine), (depth)
     constexpr int K = 9 + (REFINE ? 1 : 0) + (DEPTH ? 1 : 0);
     constexpr int KP = (K + 1) & ~1;  // rows per slot (even)
-    constexpr int R = 2 * KP;         // rows in use: two slots
-    static_assert(R <= 32, "flush geometry: two slots of at most 16 rows");
+    // slots summed per flush: three where their rows fit the 32 row pairs of
+    // a wave (K <= 10), else two
+    constexpr int NS = 3 * KP <= 32 ? 3 : 2;
+    constexpr int R = NS * KP;  // rows in use
+    static_assert(R <= 32, "flush geometry: at most 32 rows, two lanes each");
     // the conic from its scaled form (bh_conic_log2): c00 = 2 ln2 a,
     // c01 = ln2 b, c11 = 2 ln2 c
     constexpr float kLn2 = 0.69314718055994530942f;
@@ -379,10 +383,10 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
     // row (global id): the candidate's three 16-byte records share one
     // address
     __shared__ uint4 s_aux[BATCH];
-    // R rows of two 32-float halves, each padded by 4 floats: a row's stores
-    // and the summing lanes' 16-byte reads are free of bank conflicts
-    constexpr int SSTR = 36;      // half-row stride in floats
-    constexpr int RS = 2 * SSTR;  // row stride in floats
+    // R rows of 64 floats, lane l's value in column l (conflict-free
+    // stores); the summing lanes' reads are spread over the banks by their
+    // order (below)
+    constexpr int RS = 64;  // row stride in floats
     __shared__ float4 s_red4[R * RS / 4];
     float* s_red = reinterpret_cast<float*>(s_red4);
 
@@ -444,22 +448,31 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
     // v_sigma dx row), c11 (its v_sigma dy row), 0.5 (the dx dx and dy dy
     // rows), the colour gate (a colour row) or 1, plus the quad partner row's
     // total times c01 (the two mean rows)
-    const uint32_t wcol = (lane >> 5) * SSTR + (lane & 31u);
     // byte offsets of this lane's column in rows 0, 4 and 8 of each slot: a
     // row store's offset from them fits the 8-bit dword offsets of paired
-    // LDS stores (rows 72 floats apart); kept in registers (opaque to the
+    // LDS stores (rows 64 floats apart); kept in registers (opaque to the
     // compiler, which would otherwise rebuild them with an add per store pair)
-    uint32_t wbase[2][3];
+    uint32_t wbase[NS][3];
 #pragma unroll
-    for (int sl = 0; sl < 2; ++sl)
+    for (int sl = 0; sl < NS; ++sl)
 #pragma unroll
         for (int gr = 0; gr < 3; ++gr) {
-            wbase[sl][gr] = ((uint32_t)(sl * KP + 4 * gr) * RS + wcol) * 4u;
+            wbase[sl][gr] = ((uint32_t)(sl * KP + 4 * gr) * RS + lane) * 4u;
             __asm__ volatile("" : "+v"(wbase[sl][gr]));
         }
     const uint32_t frow = lane >> 1, fq = lane & 1u;
     const uint32_t fslot = frow / (uint32_t)KP, fk = frow % (uint32_t)KP;
-    const float4* fsrc = reinterpret_cast<const float4*>(s_red + frow * RS + fq * SSTR);
+    // the byte offsets of the eight float4 groups of its row's half a summing
+    // lane reads, group 8 h + ((q + r + 4 h) mod 8) at step q (row r, half
+    // h): the 16 lanes of a read phase (8 rows, both halves) read 16
+    // distinct groups of four banks, the 8 of a narrower phase (4 rows)
+    // groups distinct modulo 8 (in registers, computed once)
+    uint32_t faddr[8];
+#pragma unroll
+    for (uint32_t q = 0; q < 8u; ++q) {
+        faddr[q] = (frow * (uint32_t)RS + 4u * (8u * fq + ((q + frow + 4u * fq) & 7u))) * 4u;
+        __asm__ volatile("" : "+v"(faddr[q]));
+    }
     // the factors as weights of the staged a, c, b and a constant (exact
     // products by 0: a splat's conic is finite)
     const float f00 = fk == 0u ? kTwoLn2 : 0.0f, f11 = fk == 1u ? kTwoLn2 : 0.0f;
@@ -473,7 +486,7 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
     // totals to the splats' gradient rows.  A slot holds the candidate index
     // of its splat in the current batch (the staging arrays outlive the
     // slot: pending slots are flushed before the next batch is staged).
-    uint32_t slot_js = 0;  // queued candidate indices: slot 0 in bits 0-5, slot 1 in bits 6-11
+    uint32_t slot_js = 0;  // queued candidate indices: slot s in bits 6 s to 6 s + 5
     auto flush = [&](uint32_t nslots) {
         wave_lds_fence();
         const bool active = fslot < nslots && fk < (uint32_t)K;
@@ -485,11 +498,11 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
         const uint32_t gates = aux.y, row = aux.z;
         float acc = 0.0f;
         if (active) {
-            float4 v = fsrc[0];
+            float4 v = *reinterpret_cast<const float4*>(reinterpret_cast<const char*>(s_red4) + faddr[0]);
             acc = (v.x + v.y) + (v.z + v.w);
 #pragma unroll
             for (int q = 1; q < 8; ++q) {
-                v = fsrc[q];
+                v = *reinterpret_cast<const float4*>(reinterpret_cast<const char*>(s_red4) + faddr[q]);
                 acc += (v.x + v.y) + (v.z + v.w);
             }
         }
@@ -539,10 +552,10 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
                                (r3.x >= 0.0f ? 1u : 0u) | (r3.y >= 0.0f ? 2u : 0u) | (r4.x >= 0.0f ? 4u : 0u), grow, 0u);
         uint64_t todo = __builtin_amdgcn_ballot_w64(any);
         wave_lds_fence();
-        // One candidate: its gradient values into slot SLOT (0 for register
-        // set a, 1 for set b).  The loop below reads the next candidate's
-        // parameters while the current one is evaluated, two register sets
-        // in turn, and sums the two slots after every set-b candidate.
+        // One candidate: its gradient values into slot SLOT.  The loop below
+        // reads the next candidate's parameters while the current one is
+        // evaluated, two register sets in turn, and sums the slots once all
+        // NS are filled.
         auto eval_one = [&](auto slot, uint32_t j, const float4& geo, const float4& op, float cb) {
             constexpr uint32_t SLOT = decltype(slot)::value;
             // candidate j's mask, read into scalar registers, is the lane condition
@@ -613,47 +626,66 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
             if (SLOT == 0u)
                 slot_js = j;
             else
-                slot_js |= j << 6;
+                slot_js |= j << (6u * SLOT);
         };
         using Slot0 = std::integral_constant<uint32_t, 0u>;
         using Slot1 = std::integral_constant<uint32_t, 1u>;
-        // an odd count leaves the batch's last candidate alone in slot 0
-        const bool odd = (__builtin_popcountll(todo) & 1) != 0;
-        if (todo) {
-            uint32_t ja = (uint32_t)__builtin_ctzll(todo);
+        using Slot2 = std::integral_constant<uint32_t, 2u>;
+        // reads the next candidate of the batch into a register set; false
+        // (and the set untouched) when none is left
+        auto next = [&](uint32_t& j, float4& geo, float4& op, float& cb) -> bool {
+            if (todo == 0ull) return false;
+            j = (uint32_t)__builtin_ctzll(todo);
             todo &= todo - 1ull;
-            float4 geoa = s_geo[ja], opa = s_op[ja];
-            float cba = __uint_as_float(s_aux[ja].x);
-            while (true) {
-                const bool has_b = todo != 0ull;
-                uint32_t jb = 0u;
-                float4 geob, opb;
-                float cbb = 0.0f;
-                if (has_b) {
-                    jb = (uint32_t)__builtin_ctzll(todo);
-                    todo &= todo - 1ull;
-                    geob = s_geo[jb];
-                    opb = s_op[jb];
-                    cbb = __uint_as_float(s_aux[jb].x);
+            geo = s_geo[j];
+            op = s_op[j];
+            cb = __uint_as_float(s_aux[j].x);
+            return true;
+        };
+        uint32_t pend = 0u;  // slots filled since the last flush
+        uint32_t ja = 0u, jb = 0u;
+        float4 geoa, opa, geob, opb;
+        float cba = 0.0f, cbb = 0.0f;
+        if (next(ja, geoa, opa, cba)) {
+            if constexpr (NS == 2) {
+                while (true) {
+                    const bool hb = next(jb, geob, opb, cbb);
+                    eval_one(Slot0{}, ja, geoa, opa, cba);
+                    if (!hb) { pend = 1u; break; }
+                    const bool ha = next(ja, geoa, opa, cba);
+                    eval_one(Slot1{}, jb, geob, opb, cbb);
+                    flush(2u);
+                    if (!ha) break;
                 }
-                eval_one(Slot0{}, ja, geoa, opa, cba);
-                if (!has_b) break;
-                const bool has_a = todo != 0ull;
-                if (has_a) {
-                    ja = (uint32_t)__builtin_ctzll(todo);
-                    todo &= todo - 1ull;
-                    geoa = s_geo[ja];
-                    opa = s_op[ja];
-                    cba = __uint_as_float(s_aux[ja].x);
+            } else {
+                // slots 0, 1, 2 from sets a, b, a, then b, a, b
+                while (true) {
+                    bool hb = next(jb, geob, opb, cbb);
+                    eval_one(Slot0{}, ja, geoa, opa, cba);
+                    if (!hb) { pend = 1u; break; }
+                    bool ha = next(ja, geoa, opa, cba);
+                    eval_one(Slot1{}, jb, geob, opb, cbb);
+                    if (!ha) { pend = 2u; break; }
+                    hb = next(jb, geob, opb, cbb);
+                    eval_one(Slot2{}, ja, geoa, opa, cba);
+                    flush(3u);
+                    if (!hb) break;
+                    ha = next(ja, geoa, opa, cba);
+                    eval_one(Slot0{}, jb, geob, opb, cbb);
+                    if (!ha) { pend = 1u; break; }
+                    hb = next(jb, geob, opb, cbb);
+                    eval_one(Slot1{}, ja, geoa, opa, cba);
+                    if (!hb) { pend = 2u; break; }
+                    ha = next(ja, geoa, opa, cba);
+                    eval_one(Slot2{}, jb, geob, opb, cbb);
+                    flush(3u);
+                    if (!ha) break;
                 }
-                eval_one(Slot1{}, jb, geob, opb, cbb);
-                flush(2u);
-                if (!has_a) break;
             }
         }
-        // sum it before the next batch overwrites the staging arrays the
-        // slots refer to
-        if (odd) flush(1u);
+        // sum the rest before the next batch overwrites the staging arrays
+        // the slots refer to
+        if (pend) flush(pend);
         wave_lds_fence();
     }
 }
