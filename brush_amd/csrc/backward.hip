@@ -466,11 +466,13 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
     // lane reads, group 8 h + ((q + r + 4 h) mod 8) at step q (row r, half
     // h): the 16 lanes of a read phase (8 rows, both halves) read 16
     // distinct groups of four banks, the 8 of a narrower phase (4 rows)
-    // groups distinct modulo 8 (in registers, computed once)
+    // groups distinct modulo 8 (in registers, computed once; the lanes past
+    // the R rows read row R - 1 and discard it)
     uint32_t faddr[8];
+    const uint32_t frow_c = min(frow, (uint32_t)R - 1u);
 #pragma unroll
     for (uint32_t q = 0; q < 8u; ++q) {
-        faddr[q] = (frow * (uint32_t)RS + 4u * (8u * fq + ((q + frow + 4u * fq) & 7u))) * 4u;
+        faddr[q] = (frow_c * (uint32_t)RS + 4u * (8u * fq + ((q + frow_c + 4u * fq) & 7u))) * 4u;
         __asm__ volatile("" : "+v"(faddr[q]));
     }
     // the factors as weights of the staged a, c, b and a constant (exact
@@ -495,17 +497,18 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
         const float4 geo = s_geo[js];
         const float c11 = s_op[js].x;
         const uint4 aux = s_aux[js];
-        const uint32_t gates = aux.y, row = aux.z;
-        float acc = 0.0f;
-        if (active) {
-            float4 v = *reinterpret_cast<const float4*>(reinterpret_cast<const char*>(s_red4) + faddr[0]);
-            acc = (v.x + v.y) + (v.z + v.w);
+        // all eight reads of the row half in flight before the first add
+        // (every lane reads; an inactive lane's sum is discarded)
+        float4 rv[8];
 #pragma unroll
-            for (int q = 1; q < 8; ++q) {
-                v = *reinterpret_cast<const float4*>(reinterpret_cast<const char*>(s_red4) + faddr[q]);
-                acc += (v.x + v.y) + (v.z + v.w);
-            }
-        }
+        for (int q = 0; q < 8; ++q)
+            rv[q] = *reinterpret_cast<const float4*>(reinterpret_cast<const char*>(s_red4) + faddr[q]);
+        __builtin_amdgcn_sched_barrier(0);
+        const uint32_t gates = aux.y, row = aux.z;
+        float acc = (rv[0].x + rv[0].y) + (rv[0].z + rv[0].w);
+#pragma unroll
+        for (int q = 1; q < 8; ++q) acc += (rv[q].x + rv[q].y) + (rv[q].z + rv[q].w);
+        acc = active ? acc : 0.0f;
         acc = dpp_add<0xB1>(acc);  // quad_perm [1, 0, 3, 2]: the row's two halves
         // quad_perm [2, 3, 0, 1]: the other row of the lane quad (a slot's
         // v_sigma dx row for its v_sigma dy row and back)
