@@ -130,6 +130,11 @@ __device__ uint32_t wave_tile_walk(uint32_t lane, uint32_t items, V2 m, const S2
         const uint32_t item = base + lane;
         const bool valid = item < total;
         const WalkRec r = rec[owner & 63u];
+        // the owner's item prefix, read with the rest of its record (left to
+        // itself the compiler reads it again inside the branch below: one
+        // more LDS round trip per step)
+        uint32_t r_incl = __float_as_uint(r.b.w);
+        __asm__ volatile("" : "+v"(r_incl));
         const uint32_t local = item - r.c.w;
         // row = local / width, exactly, through the float reciprocal: with
         // w = width and 1/w rounded, (local + 0.5) / w lies at least 0.5 / w
@@ -147,7 +152,7 @@ __device__ uint32_t wave_tile_walk(uint32_t lane, uint32_t items, V2 m, const S2
         // the wave's passing items up to and including this one, kept at a
         // splat's last item
         const uint32_t below = lanes_below(pmask);
-        if (valid && item + 1u == __float_as_uint(r.b.w)) ends[owner & 63u] = written + below + (pass ? 1u : 0u);
+        if (valid && item + 1u == r_incl) ends[owner & 63u] = written + below + (pass ? 1u : 0u);
         if (WRITE && pass) {
             const uint32_t pos = out_base + written + below;
             if (pos < out_end) {
