@@ -485,16 +485,24 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const KI* __restrict
     // the first pass of a dropping sort neither ranks nor writes capped keys
     const bool drop = FIRST && dev.drop_capped;
     uint32_t kept = 0;  // bit j: item j is a pair of this pass
+    // every key and value load first, none conditional on a loaded key (a
+    // value load behind the drop test would wait for its key: one memory
+    // round trip per item), then the transform and the drop test
 #pragma unroll
     for (int j = 0; j < ITEMS; j++) {
-        uint64_t idx = wave_base + (uint64_t)j * 64 + lane;
-        bool valid = idx < n;
-        uint32_t kk = valid ? keys_in[idx] : 0u;
-        if (FIRST) kk = min(kk - key_sub, key_cap);
-        if (drop && kk == key_cap) valid = false;
-        if (valid) kept |= 1u << j;
-        k[j] = kk;
-        v[j] = valid ? (vals_in ? vals_in[idx] : (uint32_t)idx) : 0u;
+        const uint64_t idx = wave_base + (uint64_t)j * 64 + lane;
+        const bool in_range = idx < n;
+        k[j] = in_range ? keys_in[idx] : 0u;
+        v[j] = in_range ? (vals_in ? vals_in[idx] : (uint32_t)idx) : 0u;
+        if (in_range) kept |= 1u << j;
+    }
+#pragma unroll
+    for (int j = 0; j < ITEMS; j++) {
+        if (FIRST) k[j] = min(k[j] - key_sub, key_cap);
+        if (drop && k[j] == key_cap) {
+            kept &= ~(1u << j);
+            v[j] = 0u;
+        }
     }
     uint32_t gv[GATHER ? ITEMS : 1];
     if (GATHER) {
