@@ -92,8 +92,8 @@ __device__ __forceinline__ void raster_block_of_workgroup(uint32_t g, uint32_t& 
 // Dispatch order of the tiles: by descending splat count, in buckets of a
 // quarter octave (exact order inside a bucket is not needed), so the longest
 // blocks start first.  One workgroup; order[i] is the i-th tile to dispatch.
-__device__ __forceinline__ uint32_t tile_load_bucket(const uint32_t* __restrict__ offsets, uint32_t t) {
-    const uint32_t lo = offsets[2 * t], hi = offsets[2 * t + 1];
+__device__ __forceinline__ uint32_t tile_bucket(uint2 off) {
+    const uint32_t lo = off.x, hi = off.y;
     const uint32_t c = hi > lo ? hi - lo : 0u;
     uint32_t b = c;
     if (c >= 4u) {
@@ -101,6 +101,9 @@ __device__ __forceinline__ uint32_t tile_load_bucket(const uint32_t* __restrict_
         b = msb * 4u + ((c >> (msb - 2u)) & 3u);
     }
     return 127u - min(b, 127u);
+}
+__device__ __forceinline__ uint32_t tile_load_bucket(const uint32_t* __restrict__ offsets, uint32_t t) {
+    return tile_bucket(make_uint2(offsets[2 * t], offsets[2 * t + 1]));
 }
 
 // Adds one to s[b] for each lane of the (fully active) wave whose b is a
@@ -133,12 +136,18 @@ __device__ __forceinline__ void tile_order_block(const uint32_t* __restrict__ of
     __shared__ uint32_t s_cur[128];
     const uint32_t t = threadIdx.x;
     if (t < 128u) s_cur[t] = 0u;
-    uint32_t bk[K];
+    // every load issued before the first wait: unconditional, at indices
+    // clamped into the tiles (a load behind `i < num_tiles` is a branch of its
+    // own with its own wait, one memory round trip per k)
+    uint2 off[K];
 #pragma unroll
     for (uint32_t k = 0; k < K; ++k) {
-        const uint32_t i = k * 1024u + t;
-        bk[k] = i < num_tiles ? tile_load_bucket(offsets, i) : NONE;
+        const uint32_t i = min(k * 1024u + t, num_tiles - 1u);
+        off[k] = make_uint2(offsets[2 * i], offsets[2 * i + 1]);
     }
+    uint32_t bk[K];
+#pragma unroll
+    for (uint32_t k = 0; k < K; ++k) bk[k] = k * 1024u + t < num_tiles ? tile_bucket(off[k]) : NONE;
     __syncthreads();
 #pragma unroll
     for (uint32_t k = 0; k < K; ++k)
