@@ -919,15 +919,18 @@ __global__ __launch_bounds__(256) void project_backward_kernel(
         const size_t gid = g0 + p * 256u + t;
         cs[p] = gid < n ? (cfg ? cfg[gid] : (uint32_t)gid) : 0xFFFFFFFFu;
     }
+    // every lane of every pass loaded unconditionally (an id without a row
+    // reads row 0 and is discarded), then tested with one OR: a short-circuit
+    // test makes each load wait for the one before it, eleven memory round
+    // trips per pass for a splat without gradient (most of them)
 #pragma unroll
     for (uint32_t p = 0; p < PASSES; ++p) {
-        bool a = false;
-        if (cs[p] != 0xFFFFFFFFu) {
-            const float* src = v_combined + (size_t)cs[p] * 11;
+        const bool have = cs[p] != 0xFFFFFFFFu;
+        const float* src = v_combined + (size_t)(have ? cs[p] : 0u) * 11;
+        uint32_t bits = 0u;
 #pragma unroll
-            for (int k = 0; k < 11; k++) a = a || src[k] != 0.0f;
-        }
-        any[p] = a;
+        for (int k = 0; k < 11; k++) bits |= __float_as_uint(src[k]) << 1;  // any lane other than +-0 (NaN counts)
+        any[p] = have && bits != 0u;
     }
     uint64_t masks[PASSES];
 #pragma unroll
