@@ -121,9 +121,15 @@ def algorithmic_bytes(name: str, n: int, v: int, m: int, m_post: int, t: int, p:
     if name == "project_backward":
         # gradient lanes [N, 11] in, dense rows out (transforms, SH, opacity,
         # refine); the parameters are read only for the splats with a
-        # gradient, those some pixel blended
+        # gradient, those some pixel blended.  From SIDE_FILL_MIN_SPLATS on,
+        # the other rows are zeroed by dense_zero on the side stream and
+        # project backward writes only the rows with a gradient.
         k = v if contributing is None else contributing
-        return 44.0 * n + (40 + 12 * c + 4) * k + (40 + 12 * c + 8) * n
+        rows = k if n >= SIDE_FILL_MIN_SPLATS else n
+        return 44.0 * n + (40 + 12 * c + 4) * k + (40 + 12 * c + 8) * rows
+    if name == "dense_zero":
+        # the dense gradient rows zeroed beside the rasterize backward
+        return (40 + 12 * c + 8) * n
     if name == "image_loss_forward":
         return 28.0 * p                                  # RGB + packed GT in, RGB map out
     if name == "image_loss_backward":
@@ -136,6 +142,7 @@ def algorithmic_bytes(name: str, n: int, v: int, m: int, m_post: int, t: int, p:
 
 
 BUCKET_SORT_MAX_SPLATS = 1 << 21  # the depth sort's bucket path (brush_amd/csrc/api.hip)
+SIDE_FILL_MIN_SPLATS = 1 << 19  # dense gradients zeroed on the side stream (brush_amd/csrc/api.hip)
 
 
 def sort_bytes_per_launch(name: str, passes: float, n: int, m: int, t: int) -> float:

@@ -902,7 +902,7 @@ __global__ __launch_bounds__(256) void project_backward_kernel(
     bh_project_uniforms u, const float* __restrict__ transforms, const float* __restrict__ sh,
     const float* __restrict__ raw_opac, const uint32_t* __restrict__ cfg, uint32_t n,
     const float* __restrict__ v_combined, float* __restrict__ v_transforms, float* __restrict__ v_coeffs,
-    float* __restrict__ v_raw_opac, float* __restrict__ v_refine) {
+    float* __restrict__ v_raw_opac, float* __restrict__ v_refine, bool zeroed) {
     constexpr int NC = (DEG + 1) * (DEG + 1);
     constexpr uint32_t PASSES = PB_SPLATS / 256u;
     __shared__ uint32_t s_gid[PB_SPLATS];
@@ -938,10 +938,12 @@ __global__ __launch_bounds__(256) void project_backward_kernel(
         masks[p] = __ballot(any[p]);
         if (lane == 0) s_count[p][wave] = (uint32_t)__popcll(masks[p]);
     }
-    block_zero(v_transforms, g0 * 10u, g1 * 10u);
-    block_zero(v_coeffs, g0 * (3u * NC), g1 * (3u * NC));
-    block_zero(v_raw_opac, g0, g1);
-    block_zero(v_refine, g0, g1);
+    if (!zeroed) {  // (uniform) else the caller zeroed the rows
+        block_zero(v_transforms, g0 * 10u, g1 * 10u);
+        block_zero(v_coeffs, g0 * (3u * NC), g1 * (3u * NC));
+        block_zero(v_raw_opac, g0, g1);
+        block_zero(v_refine, g0, g1);
+    }
     __syncthreads();
     // compact the ids with gradient: list order = pass, wave, lane
     uint32_t base = 0;
@@ -977,11 +979,11 @@ __global__ __launch_bounds__(256) void project_backward_kernel(
 template <int DEG, bool MIP>
 static void launch_pb_cam(bh_ctx* ctx, const bh_project_uniforms& u, const float* transforms, const float* sh,
                           const float* raw_opac, const uint32_t* cfg, uint32_t n, const float* v_combined,
-                          float* v_transforms, float* v_coeffs, float* v_raw_opac, float* v_refine) {
+                          float* v_transforms, float* v_coeffs, float* v_raw_opac, float* v_refine, bool zeroed) {
     const uint32_t blocks = div_up(n, PB_SPLATS);
 #define BH_PB(C)                                                                                                  \
     launch(ctx, project_backward_kernel<DEG, MIP, C>, dim3(blocks), dim3(256), 0u, u, transforms, sh, raw_opac, cfg,   \
-           n, v_combined, v_transforms, v_coeffs, v_raw_opac, v_refine)
+           n, v_combined, v_transforms, v_coeffs, v_raw_opac, v_refine, zeroed)
     switch (u.camera_model) {
         case kCamKB4: BH_PB(kCamKB4); break;
         case kCamRT8: BH_PB(kCamRT8); break;
@@ -990,32 +992,33 @@ static void launch_pb_cam(bh_ctx* ctx, const bh_project_uniforms& u, const float
     }
 #undef BH_PB
 }
-
 template <int DEG>
 static void launch_pb(bh_ctx* ctx, bool mip, const bh_project_uniforms& u, const float* transforms, const float* sh,
                       const float* raw_opac, const uint32_t* cfg, uint32_t n, const float* v_combined,
-                      float* v_transforms, float* v_coeffs, float* v_raw_opac, float* v_refine) {
+                      float* v_transforms, float* v_coeffs, float* v_raw_opac, float* v_refine, bool zeroed) {
     if (mip)
         launch_pb_cam<DEG, true>(ctx, u, transforms, sh, raw_opac, cfg, n, v_combined, v_transforms, v_coeffs,
-                                 v_raw_opac, v_refine);
+                                 v_raw_opac, v_refine, zeroed);
     else
         launch_pb_cam<DEG, false>(ctx, u, transforms, sh, raw_opac, cfg, n, v_combined, v_transforms, v_coeffs,
-                                  v_raw_opac, v_refine);
+                                  v_raw_opac, v_refine, zeroed);
 }
-
 void launch_project_backward(bh_ctx* ctx, const bh_project_uniforms& u, const float* transforms, const float* sh,
                              const float* raw_opac, const uint32_t* cfg, uint32_t n, uint32_t sh_degree, bool mip,
                              const float* v_combined, float* v_transforms, float* v_coeffs, float* v_raw_opac,
-                             float* v_refine) {
+                             float* v_refine, bool zeroed) {
     if (n == 0) return;
     KernelTimer t(ctx, "project_backward");
+#define BH_PBD(D) \
+    launch_pb<D>(ctx, mip, u, transforms, sh, raw_opac, cfg, n, v_combined, v_transforms, v_coeffs, v_raw_opac, v_refine, zeroed)
     switch (sh_degree) {
-        case 0: launch_pb<0>(ctx, mip, u, transforms, sh, raw_opac, cfg, n, v_combined, v_transforms, v_coeffs, v_raw_opac, v_refine); break;
-        case 1: launch_pb<1>(ctx, mip, u, transforms, sh, raw_opac, cfg, n, v_combined, v_transforms, v_coeffs, v_raw_opac, v_refine); break;
-        case 2: launch_pb<2>(ctx, mip, u, transforms, sh, raw_opac, cfg, n, v_combined, v_transforms, v_coeffs, v_raw_opac, v_refine); break;
-        case 3: launch_pb<3>(ctx, mip, u, transforms, sh, raw_opac, cfg, n, v_combined, v_transforms, v_coeffs, v_raw_opac, v_refine); break;
-        default: launch_pb<4>(ctx, mip, u, transforms, sh, raw_opac, cfg, n, v_combined, v_transforms, v_coeffs, v_raw_opac, v_refine); break;
+        case 0: BH_PBD(0); break;
+        case 1: BH_PBD(1); break;
+        case 2: BH_PBD(2); break;
+        case 3: BH_PBD(3); break;
+        default: BH_PBD(4); break;
     }
+#undef BH_PBD
 }
 
 }  // namespace bh

@@ -113,6 +113,12 @@ struct bh_ctx {
     void* noalloc_scratch = nullptr;
     // BH_DEBUG_* flags (bh_ctx_set_debug)
     uint32_t debug = 0;
+    // A second stream (default priority, created on first use) for work that
+    // overlaps kernels of `stream`: side_fork / side_join.
+    hipStream_t side = nullptr;
+    hipEvent_t side_fork_ev = nullptr, side_join_ev = nullptr;
+    bool side_join_pending = false;  // `stream` has not yet waited for the side work
+    bool side_unavailable = false;   // creating it failed: side work runs on `stream`
 };
 
 namespace bh {
@@ -138,9 +144,10 @@ struct KernelTimer {
 };
 
 // Every kernel of the library is launched through here, on the context's
-// stream, so that an open KernelTimer times it.
+// stream (or, launch_on, the stream side_fork returned), so that an open
+// KernelTimer times it.
 template <typename F, typename... Args>
-inline void launch(bh_ctx* ctx, F kernel, dim3 grid, dim3 block, uint32_t lds, Args... args) {
+inline void launch_on(bh_ctx* ctx, hipStream_t stream, F kernel, dim3 grid, dim3 block, uint32_t lds, Args... args) {
     hipEvent_t e0 = nullptr, e1 = nullptr;
     KernelTimer* t = ctx->timer;
     if (t && t->e0 && t->e1 && !t->bound) {
@@ -148,8 +155,21 @@ inline void launch(bh_ctx* ctx, F kernel, dim3 grid, dim3 block, uint32_t lds, A
         e1 = t->e1;
         t->bound = true;
     }
-    hipExtLaunchKernelGGL(kernel, grid, block, lds, ctx->stream, e0, e1, 0u, args...);
+    hipExtLaunchKernelGGL(kernel, grid, block, lds, stream, e0, e1, 0u, args...);
 }
+template <typename F, typename... Args>
+inline void launch(bh_ctx* ctx, F kernel, dim3 grid, dim3 block, uint32_t lds, Args... args) {
+    launch_on(ctx, ctx->stream, kernel, grid, block, lds, args...);
+}
+
+// Side work: side_fork returns a stream whose work starts after everything
+// queued on ctx->stream so far (the side stream, or ctx->stream itself when
+// no side stream can be had); side_record_join marks the end of the side work
+// queued on it, and side_join makes ctx->stream wait for that end (a no-op
+// when nothing is pending).  Every call that forks joins before it returns.
+hipStream_t side_fork(bh_ctx* ctx);
+void side_record_join(bh_ctx* ctx, hipStream_t side);
+void side_join(bh_ctx* ctx);
 
 bh_status set_error(bh_ctx* ctx, bh_status st, const std::string& msg);
 bh_status check_launch(bh_ctx* ctx, const char* what);
@@ -167,7 +187,10 @@ struct FillRange {
     uint64_t count;
 };
 constexpr int kMaxFillRanges = 8;
-void launch_fill_multi(bh_ctx* ctx, const FillRange* ranges, int k);
+// On `stream` (ctx->stream when null), with at most max_blocks workgroups,
+// timed under `name`.
+void launch_fill_multi(bh_ctx* ctx, const FillRange* ranges, int k, hipStream_t stream = nullptr,
+                       uint32_t max_blocks = 2048, const char* name = "fill");
 // Ranges a kernel zeroes beside its own work (a grid-stride loop per range;
 // unused ranges have count 0), in place of a fill launch of their own.
 struct ZeroRanges {
@@ -316,10 +339,12 @@ void launch_rasterize_backward_recorded(bh_ctx* ctx, uint32_t img_w, uint32_t im
                                         const uint32_t* row_of, const uint32_t* order, float* v_rows);
 void launch_invert_permutation(bh_ctx* ctx, const uint32_t* gfc, uint32_t num_visible, uint32_t n,
                                uint32_t* compact_from_global);
-// compact_from_global == nullptr: v_combined is indexed by global id.
+// compact_from_global == nullptr: v_combined is indexed by global id.  With
+// zeroed the four gradient arrays are already zero (the splats without a
+// gradient are skipped instead of zero-filled).
 void launch_project_backward(bh_ctx* ctx, const bh_project_uniforms& u, const float* transforms, const float* sh,
                              const float* raw_opac, const uint32_t* compact_from_global, uint32_t n,
                              uint32_t sh_degree, bool mip, const float* v_combined, float* v_transforms,
-                             float* v_coeffs, float* v_raw_opac, float* v_refine);
+                             float* v_coeffs, float* v_raw_opac, float* v_refine, bool zeroed = false);
 
 }  // namespace bh

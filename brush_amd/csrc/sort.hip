@@ -142,22 +142,23 @@ __global__ void fill_multi_kernel(FillRanges ranges) {
     }
 }
 
-void launch_fill_multi(bh_ctx* ctx, const FillRange* ranges, int k) {
+void launch_fill_multi(bh_ctx* ctx, const FillRange* ranges, int k, hipStream_t stream, uint32_t max_blocks,
+                       const char* name) {
     FillRanges fr{};
     uint64_t total = 0;
     for (int j = 0; j < k; j++) {
         if (ranges[j].count == 0 || !ranges[j].p) continue;
         if (fr.k == kMaxFillRanges) {  // more than one launch holds
-            launch_fill_multi(ctx, ranges + j, k - j);
+            launch_fill_multi(ctx, ranges + j, k - j, stream, max_blocks, name);
             break;
         }
         fr.r[fr.k++] = ranges[j];
         total += ranges[j].count;
     }
     if (fr.k == 0) return;
-    KernelTimer t(ctx, "fill");
-    const uint32_t blocks = (uint32_t)std::min<uint64_t>((total / 4 + 255) / 256 + 1, 2048);
-    launch(ctx, fill_multi_kernel, dim3(blocks), dim3(256), 0u, fr);
+    KernelTimer t(ctx, name);
+    const uint32_t blocks = (uint32_t)std::min<uint64_t>((total / 4 + 255) / 256 + 1, std::max(max_blocks, 1u));
+    launch_on(ctx, stream ? stream : ctx->stream, fill_multi_kernel, dim3(blocks), dim3(256), 0u, fr);
 }
 
 // ---- debug validation: the first non-finite value of each array ----------------------
