@@ -395,6 +395,10 @@ static bh_status radix_argsort_with(bh_ctx* ctx, Ws& ws, const uint32_t* keys_in
 #define BH_SIDE_FILL_BLOCKS 64
 #endif
 constexpr uint32_t kSideFillBlocks = BH_SIDE_FILL_BLOCKS;
+#ifndef BH_SIDE_FILL_NT
+#define BH_SIDE_FILL_NT true
+#endif
+constexpr bool kSideFillNontemporal = BH_SIDE_FILL_NT;
 // below this many splats project backward zero-fills its own rows (config 0,
 // 100k splats: the fork and join cost more than the fill, 0.2353 vs 0.2396 ms)
 constexpr uint32_t kSideFillMinSplats = 1u << 19;
@@ -1091,7 +1095,8 @@ bh_status bh_render_backward(bh_ctx* ctx, const bh_fwd_state* state, const float
                                    {(uint32_t*)v_raw_opac, 0u, (uint64_t)n},
                                    {(uint32_t*)v_refine, 0u, (uint64_t)n}};
         const hipStream_t side = side_fork(ctx);
-        launch_fill_multi(ctx, dense, 4, side, std::min(512u, kSideFillBlocks * div_up(n, 1u << 20)), "dense_zero");
+        launch_fill_multi(ctx, dense, 4, side, std::min(512u, kSideFillBlocks * div_up(n, 1u << 20)), "dense_zero",
+                          kSideFillNontemporal);
         side_record_join(ctx, side);
     }
     StageRange raster_stage("RasterizeBackwards");

@@ -188,9 +188,9 @@ struct FillRange {
 };
 constexpr int kMaxFillRanges = 8;
 // On `stream` (ctx->stream when null), with at most max_blocks workgroups,
-// timed under `name`.
+// timed under `name`; with nontemporal its 16-byte stores are non-temporal.
 void launch_fill_multi(bh_ctx* ctx, const FillRange* ranges, int k, hipStream_t stream = nullptr,
-                       uint32_t max_blocks = 2048, const char* name = "fill");
+                       uint32_t max_blocks = 2048, const char* name = "fill", bool nontemporal = false);
 // Ranges a kernel zeroes beside its own work (a grid-stride loop per range;
 // unused ranges have count 0), in place of a fill launch of their own.
 struct ZeroRanges {

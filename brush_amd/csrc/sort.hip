@@ -124,7 +124,9 @@ struct FillRanges {
 };
 
 // Every range filled by the whole grid in turn (the range index is uniform),
-// each as fill_u32_kernel fills one.
+// each as fill_u32_kernel fills one; with NT the 16-byte stores are
+// non-temporal (streamed past the caches other kernels are using).
+template <bool NT>
 __global__ void fill_multi_kernel(FillRanges ranges) {
     const uint64_t tid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
@@ -137,19 +139,26 @@ __global__ void fill_multi_kernel(FillRanges ranges) {
         const uint64_t quads = (count - head) / 4u;
         uint4* q = reinterpret_cast<uint4*>(p + head);
         const uint4 v4 = make_uint4(value, value, value, value);
-        for (uint64_t i = tid; i < quads; i += stride) q[i] = v4;
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        const u32x4 n4 = {value, value, value, value};
+        for (uint64_t i = tid; i < quads; i += stride) {
+            if (NT)
+                __builtin_nontemporal_store(n4, reinterpret_cast<u32x4*>(q + i));
+            else
+                q[i] = v4;
+        }
         for (uint64_t i = head + quads * 4u + tid; i < count; i += stride) p[i] = value;
     }
 }
 
 void launch_fill_multi(bh_ctx* ctx, const FillRange* ranges, int k, hipStream_t stream, uint32_t max_blocks,
-                       const char* name) {
+                       const char* name, bool nontemporal) {
     FillRanges fr{};
     uint64_t total = 0;
     for (int j = 0; j < k; j++) {
         if (ranges[j].count == 0 || !ranges[j].p) continue;
         if (fr.k == kMaxFillRanges) {  // more than one launch holds
-            launch_fill_multi(ctx, ranges + j, k - j, stream, max_blocks, name);
+            launch_fill_multi(ctx, ranges + j, k - j, stream, max_blocks, name, nontemporal);
             break;
         }
         fr.r[fr.k++] = ranges[j];
@@ -158,7 +167,10 @@ void launch_fill_multi(bh_ctx* ctx, const FillRange* ranges, int k, hipStream_t 
     if (fr.k == 0) return;
     KernelTimer t(ctx, name);
     const uint32_t blocks = (uint32_t)std::min<uint64_t>((total / 4 + 255) / 256 + 1, std::max(max_blocks, 1u));
-    launch_on(ctx, stream ? stream : ctx->stream, fill_multi_kernel, dim3(blocks), dim3(256), 0u, fr);
+    if (nontemporal)
+        launch_on(ctx, stream ? stream : ctx->stream, fill_multi_kernel<true>, dim3(blocks), dim3(256), 0u, fr);
+    else
+        launch_on(ctx, stream ? stream : ctx->stream, fill_multi_kernel<false>, dim3(blocks), dim3(256), 0u, fr);
 }
 
 // ---- debug validation: the first non-finite value of each array ----------------------
