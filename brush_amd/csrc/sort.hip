@@ -220,7 +220,8 @@ static DigitPlan digit_plan(uint32_t key_bits) {
 
 // Offset geometry of a sort: `parts` partitions of 256 * `items` pairs,
 // `radix` counters per partition (2^width), and partitions grouped into
-// `blocks` of `rows` (a power of two >= sqrt(parts)) for the offset scan, so
+// `blocks` of `rows` (a power of two >= sqrt(parts), or >= sqrt(parts / 2)
+// above 2^14 partitions) for the offset scan, so
 // that both the block sums every scan workgroup reads and the rows it walks
 // stay short.  Partitions hold 2048 pairs from 2M keys (the 10M-pair tile
 // sort of a 1080p frame: 4096-pair partitions need 112 VGPRs, four waves per
@@ -233,8 +234,12 @@ static ScanPlan scan_plan(uint32_t n, const DigitPlan& d) {
     ScanPlan s;
     s.items = n >= (2048u << 10) ? 8u : 4u;
     s.parts = div_up(n, (uint64_t)kThreads * s.items);
+    // above 2^14 partitions (a 4K frame's tile sort) rows ~ sqrt(parts / 2):
+    // twice the scan workgroups, so more of the chip walks the counts
     s.rows = 16;
-    while ((uint64_t)s.rows * s.rows < s.parts) s.rows *= 2;
+    while ((uint64_t)s.rows * s.rows < s.parts &&
+           (s.parts <= (1u << 14) || (uint64_t)s.rows * s.rows * 2u < s.parts))
+        s.rows *= 2;
     s.blocks = div_up(s.parts, s.rows);
     s.radix = 1u << d.width;
     return s;
