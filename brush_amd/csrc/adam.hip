@@ -174,15 +174,20 @@ __global__ __launch_bounds__(kAdamThreads) void adam_row_reduced_vec4_kernel(
     float4* p4 = reinterpret_cast<float4*>(param) + base;
     float4* m14 = reinterpret_cast<float4*>(m1) + base;
     float4 g[ITEMS], pv[ITEMS], v1[ITEMS];
+    // every load first (unconditional, at indices clamped into the block's
+    // run: a load in a branch that also stores to LDS waits before the next
+    // item's loads), then the LDS stores
+#pragma unroll
+    for (int i = 0; i < ITEMS; i++) {
+        const uint32_t q = min(threadIdx.x + (uint32_t)i * kAdamThreads, quads - 1u);
+        g[i] = g4[q];
+        pv[i] = p4[q];
+        v1[i] = a.first ? make_float4(0.0f, 0.0f, 0.0f, 0.0f) : m14[q];
+    }
 #pragma unroll
     for (int i = 0; i < ITEMS; i++) {
         const uint32_t q = threadIdx.x + (uint32_t)i * kAdamThreads;
-        if (q < quads) {
-            g[i] = g4[q];
-            pv[i] = p4[q];
-            v1[i] = a.first ? make_float4(0.0f, 0.0f, 0.0f, 0.0f) : m14[q];
-            s_g[q] = g[i];
-        }
+        if (q < quads) s_g[q] = g[i];
     }
     __syncthreads();
     // mean_trailing_dims (adam_scaled.rs:287-300): row sum of g^2 in index order / row length

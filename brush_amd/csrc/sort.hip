@@ -525,7 +525,9 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const KI* __restrict
     uint32_t gv[GATHER ? ITEMS : 1];
     if (GATHER) {
 #pragma unroll
-        for (int j = 0; j < ITEMS; j++) gv[j] = (kept >> j) & 1u ? gather_src[v[j]] : 0u;
+        for (int j = 0; j < ITEMS; j++) gv[j] = gather_src[v[j]];  // v = 0 where not kept: in bounds
+#pragma unroll
+        for (int j = 0; j < ITEMS; j++) gv[j] = (kept >> j) & 1u ? gv[j] : 0u;
     }
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 #pragma unroll
