@@ -389,6 +389,55 @@ def test_render_backward_rejects_flags_of_another_forward(gpu, fwd_flags, bwd_fl
     out.state.release()
 
 
+@pytest.mark.parametrize("n", [300_000, 600_000])
+def test_render_backward_writes_every_output_entry(gpu, n):
+    """The fused backward writes every entry of its four output arrays: below
+    2^19 splats project backward zero-fills the rows of splats without a
+    gradient itself, from 2^19 on a fill on the context's second stream does,
+    beside the rasterize backward.  Outputs poisoned with NaN before the call
+    come back finite, zero in exactly the rows that are zero when the outputs
+    start at zero, and equal to those elsewhere up to the float atomics'
+    order (two backwards of one forward)."""
+    import torch
+    from brush_amd import _lib
+    from brush_amd import render as R
+
+    print(f"[case] backward over poisoned outputs, {n} splats", flush=True)
+    tr, sh, opac = random_scene(47, n, 1, log_scale=(-4.5, 0.5))
+    cam = Camera.from_focal((0.0, 0.0, -3.0), (0.0, 0.0, 0.0, 1.0), 200.0, 256, 192)
+    t = torch.from_numpy(tr).to(gpu)
+    s = torch.from_numpy(sh).to(gpu)
+    o = torch.from_numpy(opac).to(gpu)
+    out = R.render(cam, (256, 192), t, s, o, R.SplatRenderMode.Default, R.RasterizationMode.Rgba, (0.0, 0.0, 0.0),
+                   R.RasterPass.Backward)
+    g = torch.Generator(device=gpu).manual_seed(5)
+    v_out = torch.randn(out.out_img.shape, generator=g, device=gpu)
+    ctx = _lib.context()
+    bg = (ctypes.c_float * 3)(0.0, 0.0, 0.0)
+
+    def backward(fill):
+        grads = [torch.full(shape, fill, device=gpu) for shape in ((n, 10), (n, 4, 3), (n,), (n,))]
+        st = _lib.lib().bh_render_backward(ctx.handle, out.state.handle, _lib.ptr(out.out_img),
+                                           _lib.ptr(out.aux.tile_offsets), bg, _lib.ptr(t), _lib.ptr(s),
+                                           _lib.ptr(o), _lib.ptr(v_out), 0, *[_lib.ptr(x) for x in grads])
+        torch.cuda.synchronize()
+        assert st == 0, _lib.lib().bh_last_error(ctx.handle).decode()
+        return [x.reshape(n, -1).cpu().numpy() for x in grads]
+
+    poisoned = backward(float("nan"))
+    clean = backward(0.0)
+    out.state.release()
+    with_gradient = np.zeros(n, bool)
+    for a, b in zip(poisoned, clean):
+        assert np.isfinite(a).all()
+        zero_a, zero_b = ~np.any(a != 0.0, axis=1), ~np.any(b != 0.0, axis=1)
+        assert (zero_a == zero_b).all()
+        with_gradient |= ~zero_b
+        np.testing.assert_allclose(a, b, rtol=1e-3, atol=1e-6 * float(np.abs(b).max()))
+    print(f"[tol] {with_gradient.sum()} of {n} splats with a gradient", flush=True)
+    assert 0 < with_gradient.sum() < n
+
+
 @pytest.mark.parametrize("w,h,tile16x8", [(3840, 2160, False), (2048, 1080, True), (4096, 2160, True)])
 def test_more_than_16384_tiles(gpu, w, h, tile16x8):
     """Frames with more tiles than the tile-order kernel keeps in registers
