@@ -428,11 +428,18 @@ def split_trace(path: str, steps: int, first_kernel: str = "bh::project_forward_
             per_kernel[name] = (n + 1, t + (b - a))
         spans.append(stop - seg[0][0])
         busys.append(busy)
+        # a gap is time with no kernel running (kernels of a second stream
+        # overlap): from the latest end so far to the next start, named by
+        # the kernel that ended last and the one that starts
         ends = seg[1:] + ([rows[e]] if e < len(rows) else [])
+        last_end, last_name = seg[0][1], seg[0][2]
         for (a0, b0, n0, _), (a1, _, n1, _) in zip(seg, ends):
-            if a1 > b0:
-                gaps[(n0, n1)] = gaps.get((n0, n1), 0) + (a1 - b0)
-                counts[(n0, n1)] = counts.get((n0, n1), 0) + 1
+            if b0 > last_end:
+                last_end, last_name = b0, n0
+            if a1 > last_end:
+                key = (last_name, n1)
+                gaps[key] = gaps.get(key, 0) + (a1 - last_end)
+                counts[key] = counts.get(key, 0) + 1
     us = lambda ns: ns / 1000.0
     span, busy = sum(spans) / steps, sum(busys) / steps
     out = [f"trace: `{os.path.basename(path)}`: {len(rows)} dispatches, {len(starts)} steps; "
