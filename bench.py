@@ -117,19 +117,19 @@ def algorithmic_bytes(name: str, n: int, v: int, m: int, m_post: int, t: int, p:
         # backward's [N, 11] gradient rows (a forward with the backward's record)
         return 44.0 * m_post + 16.0 * p + 4.0 * v + 16.0 * t + 44.0 * n
     if name == "rasterize_backward":
-        return 44.0 * m_post + 32.0 * p + 40.0 * m_post  # id+row, image+grad image, atomics per isect
+        # id+row, image+grad image, atomics per isect; its fill workgroups zero
+        # the dense gradient rows (transforms, SH, opacity, refine)
+        fill = (40 + 12 * c + 8) * n if n >= FUSED_FILL_MIN_SPLATS else 0
+        return 44.0 * m_post + 32.0 * p + 40.0 * m_post + fill
     if name == "project_backward":
         # gradient lanes [N, 11] in, dense rows out (transforms, SH, opacity,
         # refine); the parameters are read only for the splats with a
-        # gradient, those some pixel blended.  From SIDE_FILL_MIN_SPLATS on,
-        # the other rows are zeroed by dense_zero on the side stream and
-        # project backward writes only the rows with a gradient.
+        # gradient, those some pixel blended.  From FUSED_FILL_MIN_SPLATS on,
+        # the rasterize backward zeroes the dense rows and project backward
+        # writes only the rows with a gradient.
         k = v if contributing is None else contributing
-        rows = k if n >= SIDE_FILL_MIN_SPLATS else n
+        rows = k if n >= FUSED_FILL_MIN_SPLATS else n
         return 44.0 * n + (40 + 12 * c + 4) * k + (40 + 12 * c + 8) * rows
-    if name == "dense_zero":
-        # the dense gradient rows zeroed beside the rasterize backward
-        return (40 + 12 * c + 8) * n
     if name == "image_loss_forward":
         return 28.0 * p                                  # RGB + packed GT in, RGB map out
     if name == "image_loss_backward":
@@ -142,7 +142,7 @@ def algorithmic_bytes(name: str, n: int, v: int, m: int, m_post: int, t: int, p:
 
 
 BUCKET_SORT_MAX_SPLATS = 1 << 21  # the depth sort's bucket path (brush_amd/csrc/api.hip)
-SIDE_FILL_MIN_SPLATS = 1 << 19  # dense gradients zeroed on the side stream (brush_amd/csrc/api.hip)
+FUSED_FILL_MIN_SPLATS = 0  # dense gradients zeroed by the rasterize backward (brush_amd/csrc/api.hip)
 
 
 def sort_bytes_per_launch(name: str, passes: float, n: int, m: int, t: int) -> float:

@@ -148,51 +148,6 @@ KernelTimer::~KernelTimer() {
     if (e1) ctx->event_cache.push_back(e1);
 }
 
-hipStream_t side_fork(bh_ctx* ctx) {
-    if (!ctx->side && !ctx->side_unavailable) {
-        // synchronisation-only events: no timestamps, no system-scope fence
-        const unsigned flags = hipEventDisableTiming | hipEventDisableSystemFence;
-        if (hipStreamCreateWithFlags(&ctx->side, hipStreamNonBlocking) != hipSuccess ||
-            hipEventCreateWithFlags(&ctx->side_fork_ev, flags) != hipSuccess ||
-            hipEventCreateWithFlags(&ctx->side_join_ev, flags) != hipSuccess) {
-            (void)hipGetLastError();
-            if (ctx->side) (void)hipStreamDestroy(ctx->side);
-            if (ctx->side_fork_ev) (void)hipEventDestroy(ctx->side_fork_ev);
-            if (ctx->side_join_ev) (void)hipEventDestroy(ctx->side_join_ev);
-            ctx->side = nullptr;
-            ctx->side_fork_ev = ctx->side_join_ev = nullptr;
-            ctx->side_unavailable = true;
-        }
-    }
-    if (!ctx->side) return ctx->stream;
-    side_join(ctx);  // one side span at a time
-    if (hipEventRecord(ctx->side_fork_ev, ctx->stream) != hipSuccess ||
-        hipStreamWaitEvent(ctx->side, ctx->side_fork_ev, 0) != hipSuccess) {
-        (void)hipGetLastError();
-        return ctx->stream;
-    }
-    return ctx->side;
-}
-
-void side_record_join(bh_ctx* ctx, hipStream_t side) {
-    if (side == ctx->stream) return;
-    if (hipEventRecord(ctx->side_join_ev, side) != hipSuccess) {
-        (void)hipGetLastError();
-        (void)hipStreamSynchronize(side);  // the host waits for the side work instead
-        return;
-    }
-    ctx->side_join_pending = true;
-}
-
-void side_join(bh_ctx* ctx) {
-    if (!ctx->side_join_pending) return;
-    ctx->side_join_pending = false;
-    if (hipStreamWaitEvent(ctx->stream, ctx->side_join_ev, 0) != hipSuccess) {
-        (void)hipGetLastError();
-        (void)hipStreamSynchronize(ctx->side);
-    }
-}
-
 bh_status set_error(bh_ctx* ctx, bh_status st, const std::string& msg) {
     if (ctx) ctx->last_error = msg;
     return st;
@@ -387,21 +342,12 @@ static bh_status radix_argsort_with(bh_ctx* ctx, Ws& ws, const uint32_t* keys_in
                             digit_scratch);
 }
 
-// workgroups of the dense-gradient zero-fill on the side stream, per 2^20
-// splats (at most 512): at config 1 64 of them spread the 244 MB fill over
-// most of the rasterize backward (2 paired rounds: 32, 64, 128 and 512
-// workgroups measured 0.5985, 0.5982, 0.6027 and 0.6099 ms per step)
-#ifndef BH_SIDE_FILL_BLOCKS
-#define BH_SIDE_FILL_BLOCKS 64
+// Below this many splats project backward zero-fills the dense gradients
+// itself instead of the rasterize backward's fill workgroups.
+#ifndef BH_FUSED_FILL_MIN
+#define BH_FUSED_FILL_MIN 0
 #endif
-constexpr uint32_t kSideFillBlocks = BH_SIDE_FILL_BLOCKS;
-#ifndef BH_SIDE_FILL_NT
-#define BH_SIDE_FILL_NT true
-#endif
-constexpr bool kSideFillNontemporal = BH_SIDE_FILL_NT;
-// below this many splats project backward zero-fills its own rows (config 0,
-// 100k splats: the fork and join cost more than the fill, 0.2353 vs 0.2396 ms)
-constexpr uint32_t kSideFillMinSplats = 1u << 19;
+constexpr uint32_t kFusedFillMinSplats = BH_FUSED_FILL_MIN;
 
 static bh_status check_device_error(bh_ctx* ctx, uint32_t flags) {
     if (flags & kErrOverflow) return set_error(ctx, BH_ERR_INTERNAL, "a device count overflowed");
@@ -448,12 +394,6 @@ bh_status bh_ctx_create(int device, bh_ctx** out) {
 void bh_ctx_destroy(bh_ctx* ctx) {
     if (!ctx) return;
     (void)hipStreamSynchronize(ctx->stream);
-    if (ctx->side) {
-        (void)hipStreamSynchronize(ctx->side);
-        (void)hipStreamDestroy(ctx->side);
-        (void)hipEventDestroy(ctx->side_fork_ev);
-        (void)hipEventDestroy(ctx->side_join_ev);
-    }
     for (auto& t : ctx->pending) {
         (void)hipEventDestroy(t.start);
         (void)hipEventDestroy(t.stop);
@@ -470,7 +410,6 @@ bh_status bh_ctx_set_stream(bh_ctx* ctx, void* hip_stream) {
     if (!ctx) return BH_ERR_INVALID_ARG;
     hipStream_t s = (hipStream_t)hip_stream;
     if (s != ctx->stream) {
-        side_join(ctx);
         BH_TRY(hip_check(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize"));
         ctx->stream = s;
     }
@@ -1056,11 +995,6 @@ bh_status bh_render_backward(bh_ctx* ctx, const bh_fwd_state* state, const float
     bh_fwd_state* st = const_cast<bh_fwd_state*>(state);
     const bool keep = (ctx->debug & BH_DEBUG_KEEP_LANES) != 0;
     Scratch ws(ctx);
-    // the side stream's zero-fill is joined on every path out
-    struct SideJoin {
-        bh_ctx* c;
-        ~SideJoin() { side_join(c); }
-    } side_guard{ctx};
     float* rows;
     const bool pre_zeroed = st->bwd_rows && st->bwd_rows_clean;
     if (pre_zeroed) {
@@ -1082,24 +1016,8 @@ bh_status bh_render_backward(bh_ctx* ctx, const bh_fwd_state* state, const float
         st->kept_lanes = nullptr;
     }
     const uint32_t raster_flags = (in.flags & (fwd_owned | BH_FLAG_TILE_16X8)) | (flags & BH_FLAG_REFINE_WEIGHT);
-    const bool side_fill = n >= kSideFillMinSplats;
-    if (side_fill) {
-        // The dense gradients start as zeros, filled on the side stream while
-        // the rasterize backward (bound by instruction issue, not memory)
-        // runs; project backward then writes only the rows of splats with a
-        // gradient.  A small grid spreads the fill over the blend, whose
-        // atomics slow down under a faster one.
-        const uint32_t nc = (in.sh_degree + 1u) * (in.sh_degree + 1u);
-        const FillRange dense[] = {{(uint32_t*)v_transforms, 0u, (uint64_t)n * 10u},
-                                   {(uint32_t*)v_coeffs, 0u, (uint64_t)n * 3u * nc},
-                                   {(uint32_t*)v_raw_opac, 0u, (uint64_t)n},
-                                   {(uint32_t*)v_refine, 0u, (uint64_t)n}};
-        const hipStream_t side = side_fork(ctx);
-        launch_fill_multi(ctx, dense, 4, side, std::min(512u, kSideFillBlocks * div_up(n, 1u << 20)), "dense_zero",
-                          kSideFillNontemporal);
-        side_record_join(ctx, side);
-    }
     StageRange raster_stage("RasterizeBackwards");
+    bool dense_zeroed = false;  // the four gradient arrays hold zeros
     if (in.num_visible && in.num_intersections && state->record.masks) {
         // the longest tiles (most splats the forward blended) start first: in
         // the order the forward's blend recorded, or one computed here (while
@@ -1114,10 +1032,21 @@ bh_status bh_render_backward(bh_ctx* ctx, const bh_fwd_state* state, const float
             else
                 launch_zero_and_tile_order(ctx, (uint32_t*)rows, (uint64_t)n * 11, tile_offsets, in.num_tiles, order);
         }
-        launch_rasterize_backward_recorded(ctx, in.img_w, in.img_h, in.tile_bw, in.tile_bh, background, in.num_visible,
-                                           out_img, in.projected, in.compact_gid_from_isect, in.tile_offsets_pre,
-                                           state->record, v_output, raster_flags, in.global_from_compact_gid, order,
-                                           rows);
+        // The dense gradients start as zeros, stored by workgroups of the
+        // rasterize backward (bound by instruction issue, not memory) spread
+        // among its blend's; project backward then writes only the rows of
+        // splats with a gradient.
+        const uint32_t nc = (in.sh_degree + 1u) * (in.sh_degree + 1u);
+        const FillRange dense[] = {{(uint32_t*)v_transforms, 0u, (uint64_t)n * 10u},
+                                   {(uint32_t*)v_coeffs, 0u, (uint64_t)n * 3u * nc},
+                                   {(uint32_t*)v_raw_opac, 0u, (uint64_t)n},
+                                   {(uint32_t*)v_refine, 0u, (uint64_t)n}};
+        const int dense_k = n >= kFusedFillMinSplats ? 4 : 0;
+        dense_zeroed = launch_rasterize_backward_recorded(
+                           ctx, in.img_w, in.img_h, in.tile_bw, in.tile_bh, background, in.num_visible, out_img,
+                           in.projected, in.compact_gid_from_isect, in.tile_offsets_pre, state->record, v_output,
+                           raster_flags, in.global_from_compact_gid, order, rows, dense, dense_k) &&
+                       dense_k != 0;
     } else {
         // no intersections: no pixel blended a splat, every gradient is zero
         if (!pre_zeroed) launch_fill_u32(ctx, (uint32_t*)rows, 0u, (uint64_t)n * 11);
@@ -1125,10 +1054,9 @@ bh_status bh_render_backward(bh_ctx* ctx, const bh_fwd_state* state, const float
     BH_TRY(check_launch(ctx, "rasterize_backward"));
     {
         StageRange stage("ProjectBackwards");
-        side_join(ctx);  // the dense rows are zero (with side_fill)
         launch_project_backward(ctx, in.uniforms, transforms, sh_coeffs, raw_opacities, nullptr, n, in.sh_degree,
                                 (in.flags & BH_FLAG_MIP) != 0, rows, v_transforms, v_coeffs, v_raw_opac, v_refine,
-                                side_fill);
+                                dense_zeroed);
     }
     BH_TRY(check_launch(ctx, "project_backward"));
     if (keep)

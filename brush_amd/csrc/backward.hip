@@ -357,7 +357,7 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
     uint32_t num_visible, const float* __restrict__ out_img, const float* __restrict__ projected,
     const uint32_t* __restrict__ cgids, const uint32_t* __restrict__ off_pre, SplatRecord rec,
     const float* __restrict__ v_output, const uint32_t* __restrict__ row_of, const uint32_t* __restrict__ order,
-    float* __restrict__ v_rows) {
+    float* __restrict__ v_rows, FillRanges fill, uint32_t fill_slots, uint32_t all_slots) {
     constexpr uint32_t CH = DEPTH ? 5u : 4u;
     constexpr uint32_t BPT = 2u * (uint32_t)TH / 8u;
     // sums per splat: v_sigma dx, v_sigma dy, v_sigma dx dx, v_sigma dx dy,
@@ -390,8 +390,24 @@ __global__ __launch_bounds__(64) void rasterize_backward_recorded_kernel(
     __shared__ float4 s_red4[R * RS / 4];
     float* s_red = reinterpret_cast<float*>(s_red4);
 
+    // fill_slots of the all_slots slots of 8 workgroups (one per XCD) zero
+    // the fill ranges, spread evenly among the blend's: slot s is a fill
+    // slot where floor((s + 1) F / T) > floor(s F / T), the fill slot
+    // floor(s F / T), else blend slot s - floor(s F / T)
+    uint32_t g = blockIdx.x;
+    if (fill_slots) {
+        const uint32_t s = g >> 3;
+        const uint32_t f0 = (uint32_t)((uint64_t)s * fill_slots / all_slots);
+        const uint32_t f1 = (uint32_t)((uint64_t)(s + 1u) * fill_slots / all_slots);
+        if (f1 > f0) {
+            fill_ranges_strided<true>(fill, (uint64_t)(f0 * 8u + (g & 7u)) * 64u + threadIdx.x,
+                                      (uint64_t)fill_slots * 512u);
+            return;
+        }
+        g = ((s - f0) << 3) | (g & 7u);
+    }
     uint32_t tile, blk;
-    block_of_workgroup<TH>(blockIdx.x, tile, blk);
+    block_of_workgroup<TH>(g, tile, blk);
     if (tile >= num_tiles) return;
     if (order)
         tile = order[tile];
@@ -699,19 +715,39 @@ static void launch_recorded_t(bh_ctx* ctx, uint32_t groups, uint32_t img_w, uint
                               uint32_t num_tiles, const float* bg, uint32_t num_visible, const float* out_img,
                               const float* projected, const uint32_t* cgids, const uint32_t* off_pre,
                               const SplatRecord& rec, const float* v_output, const uint32_t* row_of,
-                              const uint32_t* order, float* v_rows) {
-    launch(ctx, rasterize_backward_recorded_kernel<S, R, D, T>, dim3(groups), dim3(64), 0u, img_w, img_h, tile_bw,
-           num_tiles, bg[0], bg[1], bg[2], num_visible, out_img, projected, cgids, off_pre, rec, v_output, row_of,
-           order, v_rows);
+                              const uint32_t* order, float* v_rows, const FillRanges& fill, uint32_t fill_slots) {
+    const uint32_t all_slots = groups / 8u + fill_slots;
+    launch(ctx, rasterize_backward_recorded_kernel<S, R, D, T>, dim3(all_slots * 8u), dim3(64), 0u, img_w, img_h,
+           tile_bw, num_tiles, bg[0], bg[1], bg[2], num_visible, out_img, projected, cgids, off_pre, rec, v_output,
+           row_of, order, v_rows, fill, fill_slots, all_slots);
 }
 
-void launch_rasterize_backward_recorded(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile_bw,
+// 16-byte stores per lane of a workgroup that zeroes the fill ranges inside the
+// rasterize backward (about 64 KiB a workgroup)
+#ifndef BH_FUSED_FILL_ITERS
+#define BH_FUSED_FILL_ITERS 64
+#endif
+constexpr uint64_t kFusedFillIters = BH_FUSED_FILL_ITERS;
+
+bool launch_rasterize_backward_recorded(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile_bw,
                                         uint32_t tile_bh, const float* bg, uint32_t num_visible, const float* out_img,
                                         const float* projected, const uint32_t* cgids, const uint32_t* off_pre,
                                         const SplatRecord& rec, const float* v_output, uint32_t flags,
-                                        const uint32_t* row_of, const uint32_t* order, float* v_rows) {
+                                        const uint32_t* row_of, const uint32_t* order, float* v_rows,
+                                        const FillRange* zero, int zero_k) {
     const uint32_t num_tiles = tile_bw * tile_bh;
-    if (num_tiles == 0 || num_visible == 0 || !rec.masks) return;
+    if (num_tiles == 0 || num_visible == 0 || !rec.masks) return false;
+    FillRanges fill{};
+    uint64_t quads = 0;
+    const bool fits = zero_k <= kMaxFillRanges;  // else the caller zeroes them
+    for (int j = 0; fits && j < zero_k; j++) {
+        if (zero[j].count == 0 || !zero[j].p) continue;
+        fill.r[fill.k++] = zero[j];
+        quads += div_up(zero[j].count, (uint64_t)4);
+    }
+    // a fill workgroup stores about kFusedFillIters 16-byte words per lane
+    const uint32_t fill_slots =
+        (uint32_t)std::min<uint64_t>(div_up(quads, (uint64_t)512 * kFusedFillIters), 1u << 20);
     const bool smooth = (flags & BH_FLAG_SMOOTH_CUTOFF) != 0;
     const bool refine = (flags & BH_FLAG_REFINE_WEIGHT) != 0;
     const bool depth = (flags & BH_FLAG_RENDER_DEPTH) != 0;
@@ -720,7 +756,7 @@ void launch_rasterize_backward_recorded(bh_ctx* ctx, uint32_t img_w, uint32_t im
     KernelTimer t(ctx, "rasterize_backward");
 #define BH_RBR_T(S, R, D, T)                                                                                      \
     launch_recorded_t<S, R, D, T>(ctx, groups, img_w, img_h, tile_bw, num_tiles, bg, num_visible, out_img,       \
-                                  projected, cgids, off_pre, rec, v_output, row_of, order, v_rows)
+                                  projected, cgids, off_pre, rec, v_output, row_of, order, v_rows, fill, fill_slots)
 #define BH_RBR(S, R, D)              \
     do {                             \
         if (fine)                    \
@@ -743,6 +779,7 @@ void launch_rasterize_backward_recorded(bh_ctx* ctx, uint32_t img_w, uint32_t im
     }
 #undef BH_RBR
 #undef BH_RBR_T
+    return fits;
 }
 
 // ---- project backward ---------------------------------------------------------------

@@ -113,12 +113,6 @@ struct bh_ctx {
     void* noalloc_scratch = nullptr;
     // BH_DEBUG_* flags (bh_ctx_set_debug)
     uint32_t debug = 0;
-    // A second stream (default priority, created on first use) for work that
-    // overlaps kernels of `stream`: side_fork / side_join.
-    hipStream_t side = nullptr;
-    hipEvent_t side_fork_ev = nullptr, side_join_ev = nullptr;
-    bool side_join_pending = false;  // `stream` has not yet waited for the side work
-    bool side_unavailable = false;   // creating it failed: side work runs on `stream`
 };
 
 namespace bh {
@@ -144,10 +138,9 @@ struct KernelTimer {
 };
 
 // Every kernel of the library is launched through here, on the context's
-// stream (or, launch_on, the stream side_fork returned), so that an open
-// KernelTimer times it.
+// stream, so that an open KernelTimer times it.
 template <typename F, typename... Args>
-inline void launch_on(bh_ctx* ctx, hipStream_t stream, F kernel, dim3 grid, dim3 block, uint32_t lds, Args... args) {
+inline void launch(bh_ctx* ctx, F kernel, dim3 grid, dim3 block, uint32_t lds, Args... args) {
     hipEvent_t e0 = nullptr, e1 = nullptr;
     KernelTimer* t = ctx->timer;
     if (t && t->e0 && t->e1 && !t->bound) {
@@ -155,21 +148,8 @@ inline void launch_on(bh_ctx* ctx, hipStream_t stream, F kernel, dim3 grid, dim3
         e1 = t->e1;
         t->bound = true;
     }
-    hipExtLaunchKernelGGL(kernel, grid, block, lds, stream, e0, e1, 0u, args...);
+    hipExtLaunchKernelGGL(kernel, grid, block, lds, ctx->stream, e0, e1, 0u, args...);
 }
-template <typename F, typename... Args>
-inline void launch(bh_ctx* ctx, F kernel, dim3 grid, dim3 block, uint32_t lds, Args... args) {
-    launch_on(ctx, ctx->stream, kernel, grid, block, lds, args...);
-}
-
-// Side work: side_fork returns a stream whose work starts after everything
-// queued on ctx->stream so far (the side stream, or ctx->stream itself when
-// no side stream can be had); side_record_join marks the end of the side work
-// queued on it, and side_join makes ctx->stream wait for that end (a no-op
-// when nothing is pending).  Every call that forks joins before it returns.
-hipStream_t side_fork(bh_ctx* ctx);
-void side_record_join(bh_ctx* ctx, hipStream_t side);
-void side_join(bh_ctx* ctx);
 
 bh_status set_error(bh_ctx* ctx, bh_status st, const std::string& msg);
 bh_status check_launch(bh_ctx* ctx, const char* what);
@@ -187,10 +167,36 @@ struct FillRange {
     uint64_t count;
 };
 constexpr int kMaxFillRanges = 8;
-// On `stream` (ctx->stream when null), with at most max_blocks workgroups,
-// timed under `name`; with nontemporal its 16-byte stores are non-temporal.
-void launch_fill_multi(bh_ctx* ctx, const FillRange* ranges, int k, hipStream_t stream = nullptr,
-                       uint32_t max_blocks = 2048, const char* name = "fill", bool nontemporal = false);
+struct FillRanges {
+    FillRange r[kMaxFillRanges];
+    int k;
+};
+// Thread `tid` of `stride` threads fills its share of every range in turn (the
+// range index is uniform): single words up to each range's first 16-byte
+// boundary and after its last, 16-byte stores between (non-temporal with NT:
+// streamed past the caches other kernels are using).
+template <bool NT>
+__device__ __forceinline__ void fill_ranges_strided(const FillRanges& ranges, uint64_t tid, uint64_t stride) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    for (int j = 0; j < ranges.k; j++) {
+        uint32_t* p = ranges.r[j].p;
+        const uint32_t value = ranges.r[j].value;
+        const uint64_t count = ranges.r[j].count;
+        const uint64_t head = min<uint64_t>(count, ((16u - (reinterpret_cast<uintptr_t>(p) & 15u)) & 15u) / 4u);
+        if (tid < head) p[tid] = value;
+        const uint64_t quads = (count - head) / 4u;
+        u32x4* q = reinterpret_cast<u32x4*>(p + head);
+        const u32x4 v4 = {value, value, value, value};
+        for (uint64_t i = tid; i < quads; i += stride) {
+            if (NT)
+                __builtin_nontemporal_store(v4, q + i);
+            else
+                q[i] = v4;
+        }
+        for (uint64_t i = head + quads * 4u + tid; i < count; i += stride) p[i] = value;
+    }
+}
+void launch_fill_multi(bh_ctx* ctx, const FillRange* ranges, int k);
 // Ranges a kernel zeroes beside its own work (a grid-stride loop per range;
 // unused ranges have count 0), in place of a fill launch of their own.
 struct ZeroRanges {
@@ -331,12 +337,16 @@ void launch_rasterize_backward(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint
                                const uint32_t* cgids, const uint32_t* offsets, const float* v_output,
                                uint32_t flags, const uint32_t* row_of, const uint32_t* order, float* v_combined);
 // The fused backward's rasterize step from the forward's record; v_rows is
-// indexed by row_of[compact id] (the global id).
-void launch_rasterize_backward_recorded(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile_bw,
+// indexed by row_of[compact id] (the global id).  Workgroups of the same
+// launch, spread among the blend's, zero the zero_k ranges of `zero` (the
+// blend neither reads nor writes them); returns whether they were zeroed
+// (false when nothing was launched or more than kMaxFillRanges were given).
+bool launch_rasterize_backward_recorded(bh_ctx* ctx, uint32_t img_w, uint32_t img_h, uint32_t tile_bw,
                                         uint32_t tile_bh, const float* bg, uint32_t num_visible, const float* out_img,
                                         const float* projected, const uint32_t* cgids, const uint32_t* off_pre,
                                         const SplatRecord& rec, const float* v_output, uint32_t flags,
-                                        const uint32_t* row_of, const uint32_t* order, float* v_rows);
+                                        const uint32_t* row_of, const uint32_t* order, float* v_rows,
+                                        const FillRange* zero = nullptr, int zero_k = 0);
 void launch_invert_permutation(bh_ctx* ctx, const uint32_t* gfc, uint32_t num_visible, uint32_t n,
                                uint32_t* compact_from_global);
 // compact_from_global == nullptr: v_combined is indexed by global id.  With

@@ -118,59 +118,28 @@ void launch_fill_u32(bh_ctx* ctx, uint32_t* p, uint32_t value, uint64_t count) {
     launch(ctx, fill_u32_kernel, dim3(blocks), dim3(256), 0u, p, value, count);
 }
 
-struct FillRanges {
-    FillRange r[kMaxFillRanges];
-    int k;
-};
-
-// Every range filled by the whole grid in turn (the range index is uniform),
-// each as fill_u32_kernel fills one; with NT the 16-byte stores are
-// non-temporal (streamed past the caches other kernels are using).
-template <bool NT>
+// Every range filled by the whole grid in turn (fill_ranges_strided).
 __global__ void fill_multi_kernel(FillRanges ranges) {
-    const uint64_t tid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-    for (int j = 0; j < ranges.k; j++) {
-        uint32_t* p = ranges.r[j].p;
-        const uint32_t value = ranges.r[j].value;
-        const uint64_t count = ranges.r[j].count;
-        const uint64_t head = min<uint64_t>(count, ((16u - (reinterpret_cast<uintptr_t>(p) & 15u)) & 15u) / 4u);
-        if (tid < head) p[tid] = value;
-        const uint64_t quads = (count - head) / 4u;
-        uint4* q = reinterpret_cast<uint4*>(p + head);
-        const uint4 v4 = make_uint4(value, value, value, value);
-        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-        const u32x4 n4 = {value, value, value, value};
-        for (uint64_t i = tid; i < quads; i += stride) {
-            if (NT)
-                __builtin_nontemporal_store(n4, reinterpret_cast<u32x4*>(q + i));
-            else
-                q[i] = v4;
-        }
-        for (uint64_t i = head + quads * 4u + tid; i < count; i += stride) p[i] = value;
-    }
+    fill_ranges_strided<false>(ranges, (uint64_t)blockIdx.x * blockDim.x + threadIdx.x,
+                               (uint64_t)gridDim.x * blockDim.x);
 }
 
-void launch_fill_multi(bh_ctx* ctx, const FillRange* ranges, int k, hipStream_t stream, uint32_t max_blocks,
-                       const char* name, bool nontemporal) {
+void launch_fill_multi(bh_ctx* ctx, const FillRange* ranges, int k) {
     FillRanges fr{};
     uint64_t total = 0;
     for (int j = 0; j < k; j++) {
         if (ranges[j].count == 0 || !ranges[j].p) continue;
         if (fr.k == kMaxFillRanges) {  // more than one launch holds
-            launch_fill_multi(ctx, ranges + j, k - j, stream, max_blocks, name, nontemporal);
+            launch_fill_multi(ctx, ranges + j, k - j);
             break;
         }
         fr.r[fr.k++] = ranges[j];
         total += ranges[j].count;
     }
     if (fr.k == 0) return;
-    KernelTimer t(ctx, name);
-    const uint32_t blocks = (uint32_t)std::min<uint64_t>((total / 4 + 255) / 256 + 1, std::max(max_blocks, 1u));
-    if (nontemporal)
-        launch_on(ctx, stream ? stream : ctx->stream, fill_multi_kernel<true>, dim3(blocks), dim3(256), 0u, fr);
-    else
-        launch_on(ctx, stream ? stream : ctx->stream, fill_multi_kernel<false>, dim3(blocks), dim3(256), 0u, fr);
+    KernelTimer t(ctx, "fill");
+    const uint32_t blocks = (uint32_t)std::min<uint64_t>((total / 4 + 255) / 256 + 1, 2048);
+    launch(ctx, fill_multi_kernel, dim3(blocks), dim3(256), 0u, fr);
 }
 
 // ---- debug validation: the first non-finite value of each array ----------------------

@@ -150,8 +150,7 @@ typedef struct bh_adam_config {
 bh_status bh_ctx_create(int device, bh_ctx** out);
 void bh_ctx_destroy(bh_ctx* ctx);
 /* Use `hip_stream` (a hipStream_t) for all later work.  If it differs from the
- * current stream, the current stream (and the context's second stream, which
- * bh_render_backward joins into it) is synchronised first so that cached
+ * current stream, the current stream is synchronised first so that cached
  * workspace is not reused across streams. */
 bh_status bh_ctx_set_stream(bh_ctx* ctx, void* hip_stream);
 const char* bh_last_error(const bh_ctx* ctx);
@@ -314,12 +313,8 @@ bh_status bh_rasterize_backward(bh_ctx* ctx, const float* out_img, const float* 
  * belongs to one context, and calls on a context are externally
  * synchronised, this is the context's rule.
  *
- * From 2^19 splats on, the call zeroes the four output arrays on a second
- * stream that the context owns (created on first use, default priority),
- * beside the rasterize backward on the context's stream, and makes the
- * context's stream wait for it before project backward: every output is
- * ordered on the context's stream as with a single stream, and nothing of
- * the call runs after the context's stream has passed it. */
+ * Every entry of the four output arrays is written (zeros for splats without
+ * a gradient), all of it on the context's stream. */
 bh_status bh_render_backward(bh_ctx* ctx, const bh_fwd_state* state, const float* out_img,
                              const uint32_t* tile_offsets, const float background[3],
                              const float* transforms, const float* sh_coeffs,

@@ -391,10 +391,9 @@ def test_render_backward_rejects_flags_of_another_forward(gpu, fwd_flags, bwd_fl
 
 @pytest.mark.parametrize("n", [300_000, 600_000])
 def test_render_backward_writes_every_output_entry(gpu, n):
-    """The fused backward writes every entry of its four output arrays: below
-    2^19 splats project backward zero-fills the rows of splats without a
-    gradient itself, from 2^19 on a fill on the context's second stream does,
-    beside the rasterize backward.  Outputs poisoned with NaN before the call
+    """The fused backward writes every entry of its four output arrays: fill
+    workgroups of the rasterize backward zero them and project backward
+    writes the rows of splats with a gradient.  Outputs poisoned with NaN before the call
     come back finite, zero in exactly the rows that are zero when the outputs
     start at zero, and equal to those elsewhere up to the float atomics'
     order (two backwards of one forward)."""
@@ -436,6 +435,38 @@ def test_render_backward_writes_every_output_entry(gpu, n):
         np.testing.assert_allclose(a, b, rtol=1e-3, atol=1e-6 * float(np.abs(b).max()))
     print(f"[tol] {with_gradient.sum()} of {n} splats with a gradient", flush=True)
     assert 0 < with_gradient.sum() < n
+
+
+def test_render_backward_without_intersections_zeroes_outputs(gpu):
+    """With every splat behind the camera there is no rasterize backward to
+    zero the outputs: project backward writes zeros into every row of outputs
+    poisoned with NaN."""
+    import torch
+    from brush_amd import _lib
+    from brush_amd import render as R
+
+    print("[case] backward over poisoned outputs, no splat in view", flush=True)
+    n = 5000
+    tr, sh, opac = random_scene(48, n, 1)
+    cam = Camera.from_focal((0.0, 0.0, 3.0), (0.0, 0.0, 0.0, 1.0), 200.0, 256, 192)
+    t = torch.from_numpy(tr).to(gpu)
+    s = torch.from_numpy(sh).to(gpu)
+    o = torch.from_numpy(opac).to(gpu)
+    out = R.render(cam, (256, 192), t, s, o, R.SplatRenderMode.Default, R.RasterizationMode.Rgba, (0.0, 0.0, 0.0),
+                   R.RasterPass.Backward)
+    assert int(out.aux.num_visible) == 0
+    v_out = torch.ones_like(out.out_img)
+    ctx = _lib.context()
+    bg = (ctypes.c_float * 3)(0.0, 0.0, 0.0)
+    grads = [torch.full(shape, float("nan"), device=gpu) for shape in ((n, 10), (n, 4, 3), (n,), (n,))]
+    st = _lib.lib().bh_render_backward(ctx.handle, out.state.handle, _lib.ptr(out.out_img),
+                                       _lib.ptr(out.aux.tile_offsets), bg, _lib.ptr(t), _lib.ptr(s), _lib.ptr(o),
+                                       _lib.ptr(v_out), 0, *[_lib.ptr(x) for x in grads])
+    torch.cuda.synchronize()
+    assert st == 0, _lib.lib().bh_last_error(ctx.handle).decode()
+    out.state.release()
+    for x in grads:
+        assert bool((x == 0.0).all())
 
 
 @pytest.mark.parametrize("w,h,tile16x8", [(3840, 2160, False), (2048, 1080, True), (4096, 2160, True)])
