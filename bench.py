@@ -103,9 +103,14 @@ def algorithmic_bytes(name: str, n: int, v: int, m: int, m_post: int, t: int, p:
         return v * (4 + 48) + v * (40 + 4)               # gid + row slot in; ordered row, depth out
     if name == "scan":
         return 12.0 * v                                  # gid + gathered count in, cum out
-    if name == "depth_sort_buckets":
-        # (key, gid) in, the gid's tile count gathered, (gid, cum_tiles_hit) out
+    if name == "depth_sort_count":
+        # (key, gid, tile count) in, (gid, cum_tiles_hit) out, for every pair.  The count kernel sorts the buckets with 1 to
+        # 15 key bits below the top digit and at most 8192 pairs (every
+        # bucket at configs 0, 1 and 4), the LSD kernel the others (most of
+        # them at configs 2 and 3); the pairs' bytes are credited here.
         return 20.0 * v
+    if name == "depth_sort_buckets":
+        return 0.0
     if name == "map_intersects":
         # gid + global-id row slot (48 B) + cum in; ordered row + depth out; (tile, id) pairs out,
         # the tile ids 16-bit below 2^16 tiles
@@ -159,6 +164,10 @@ def sort_bytes_per_launch(name: str, passes: float, n: int, m: int, t: int) -> f
     if name == "tile_sort_up":
         return (2.0 if k16 else 4.0) * m
     if name == "depth_sort_onesweep":
+        if n <= BUCKET_SORT_MAX_SPLATS:
+            # the top-digit pass: key in, (key, gid) out, each gid's tile
+            # count in and out beside it
+            return 20.0 * n
         return (16.0 * passes - 4.0) * n / max(passes, 1.0)
     if name == "tile_sort_onesweep":
         if not k16:

@@ -469,11 +469,12 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const KI* __restrict
     const uint32_t dmask = (1u << digit_bits) - 1u;
 
     uint32_t k[ITEMS], v[ITEMS], pos[ITEMS];
+    uint32_t gv[GATHER ? ITEMS : 1];
     // the first pass of a dropping sort neither ranks nor writes capped keys
     const bool drop = FIRST && dev.drop_capped;
     uint32_t kept = 0;  // bit j: item j is a pair of this pass
-    // every key and value load first, none conditional on a loaded key (a
-    // value load behind the drop test would wait for its key: one memory
+    // every key, value and gather load first, none conditional on a loaded
+    // key (a load behind the drop test would wait for its key: one memory
     // round trip per item), then the transform and the drop test
 #pragma unroll
     for (int j = 0; j < ITEMS; j++) {
@@ -481,6 +482,7 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const KI* __restrict
         const bool in_range = idx < n;
         k[j] = in_range ? keys_in[idx] : 0u;
         v[j] = in_range ? (vals_in ? vals_in[idx] : (uint32_t)idx) : 0u;
+        if (GATHER) gv[j] = gather_src[v[j]];  // v = 0 out of range: in bounds
         if (in_range) kept |= 1u << j;
     }
 #pragma unroll
@@ -490,13 +492,7 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const KI* __restrict
             kept &= ~(1u << j);
             v[j] = 0u;
         }
-    }
-    uint32_t gv[GATHER ? ITEMS : 1];
-    if (GATHER) {
-#pragma unroll
-        for (int j = 0; j < ITEMS; j++) gv[j] = gather_src[v[j]];  // v = 0 where not kept: in bounds
-#pragma unroll
-        for (int j = 0; j < ITEMS; j++) gv[j] = (kept >> j) & 1u ? gv[j] : 0u;
+        if (GATHER) gv[j] = (kept >> j) & 1u ? gv[j] : 0u;
     }
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 #pragma unroll
@@ -637,10 +633,11 @@ __device__ __forceinline__ void bucket_rank(const uint32_t (&k)[kBsItems], uint3
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < kBsItems; j++) {
-        if ((uint32_t)j >= iw) break;
-        if (wbase + (uint32_t)j * 64u + (uint32_t)lane < cnt) {
-            const uint32_t d = (k[j] >> sh) & dmask;
-            pos[j] += s_start[d] + s_hist[wave][d];
+        if ((uint32_t)j < iw) {
+            if (wbase + (uint32_t)j * 64u + (uint32_t)lane < cnt) {
+                const uint32_t d = (k[j] >> sh) & dmask;
+                pos[j] += s_start[d] + s_hist[wave][d];
+            }
         }
     }
 }
@@ -651,134 +648,43 @@ __device__ __forceinline__ void bucket_rank(const uint32_t (&k)[kBsItems], uint3
 constexpr uint32_t kBsMaxRun = 32;
 constexpr uint32_t kBsCountBits = 15;
 
-// Counting sort of a bucket of `size` <= kBsCap pairs whose keys (their low
-// `low` <= 15 bits) lie in k[] (wave-major items, as bucket_rank lays them
-// out): a histogram of the keys in packed 16-bit LDS counters, their
-// exclusive scan, and one returning LDS add per pair for its slot.  Pairs of
-// equal keys (a run of slots) are then put in input order by the thread that
-// holds the run's first slot.  The sorted values and gathered counts go out
-// in place.  Returns false, having written nothing, when a key occurs more
-// than kBsMaxRun times.  s_raw holds the counters (up to 16384 words), then
-// each slot's input position and key (16384 uint16_t each).
-__device__ bool bucket_count_sort(uint32_t (&k)[kBsItems], uint32_t (&v)[kBsItems], uint32_t iw, uint32_t size,
-                                  uint32_t low, uint32_t start, uint32_t* __restrict__ vals, uint32_t* s_raw,
-                                  uint32_t* s_tot, uint32_t* s_flag) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t wbase = (uint32_t)wave * 64u * iw;
-    uint32_t* words = s_raw;                                         // counters, two per word
-    uint16_t* s_idx = reinterpret_cast<uint16_t*>(s_raw + 16384);  // slot -> input position
-    uint16_t* s_bin = s_idx + kBsCap;                                // slot -> key
-    const uint32_t lowmask = (1u << low) - 1u;
-    const uint32_t nwords = 1u << (low - 1u);
-    // counter word i lives at word swz(i): the scan's threads each read 16
-    // consecutive words, which would put a wave's 64 lanes on 4 LDS banks;
-    // the swizzle (inside each aligned group of 16) spreads them over all
-    auto swz = [](uint32_t i) { return (i & ~15u) | ((i & 15u) ^ ((i >> 6) & 15u)); };
-    for (uint32_t i = (uint32_t)tid; i < nwords; i += kBsThreads) words[i] = 0u;
-    if (tid == 0) *s_flag = 0u;
-#pragma unroll
-    for (int j = 0; j < kBsItems; j++)
-        if ((uint32_t)j < iw) k[j] &= lowmask;
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < kBsItems; j++) {
-        if ((uint32_t)j >= iw) break;
-        if (wbase + (uint32_t)j * 64u + (uint32_t)lane < size)
-            atomicAdd(&words[swz(k[j] >> 1)], 1u << ((k[j] & 1u) * 16u));
-    }
-    __syncthreads();
-    // exclusive scan of the counters (thread t: words [t * wpt, (t + 1) * wpt))
-    // and the largest count
-    const uint32_t wpt = (nwords + kBsThreads - 1u) / kBsThreads;  // <= 16
-    uint32_t loc[16], sum = 0u, mx = 0u;
-#pragma unroll
-    for (uint32_t w = 0; w < 16u; w++) {
-        const uint32_t i = (uint32_t)tid * wpt + w;
-        loc[w] = w < wpt && i < nwords ? words[swz(i)] : 0u;
-        const uint32_t lo = loc[w] & 0xFFFFu, hi = loc[w] >> 16;
-        sum += lo + hi;
-        mx = max(mx, max(lo, hi));
-    }
-    if (mx > kBsMaxRun) *s_flag = 1u;
-    uint32_t all;
-    uint32_t run = block_exclusive_scan<kBsThreads>(sum, s_tot, &all);
-#pragma unroll
-    for (uint32_t w = 0; w < 16u; w++) {
-        const uint32_t i = (uint32_t)tid * wpt + w;
-        if (w < wpt && i < nwords) {
-            const uint32_t lo = loc[w] & 0xFFFFu, hi = loc[w] >> 16;
-            words[swz(i)] = run | ((run + lo) << 16);
-            run += lo + hi;
-        }
-    }
-    __syncthreads();
-    if (*s_flag) return false;  // uniform: a run too long for one thread
-    // every pair takes its key's next slot (any order among equal keys)
-#pragma unroll
-    for (int j = 0; j < kBsItems; j++) {
-        if ((uint32_t)j >= iw) break;
-        const uint32_t e = wbase + (uint32_t)j * 64u + (uint32_t)lane;
-        if (e < size) {
-            const uint32_t half = (k[j] & 1u) * 16u;
-            const uint32_t slot = (atomicAdd(&words[swz(k[j] >> 1)], 1u << half) >> half) & 0xFFFFu;
-            s_idx[slot] = (uint16_t)e;
-            s_bin[slot] = (uint16_t)k[j];
-        }
-    }
-    __syncthreads();
-    // runs of equal keys into input order
-    for (uint32_t i = (uint32_t)tid; i < size; i += kBsThreads) {
-        const uint32_t key = s_bin[i];
-        const bool first = i == 0u || s_bin[i - 1u] != key;
-        if (!first || i + 1u >= size || s_bin[i + 1u] != key) continue;
-        uint32_t r = 2u;
-        while (i + r < size && s_bin[i + r] == key) r++;
-        for (uint32_t a = i + 1u; a < i + r; a++) {
-            const uint32_t x = s_idx[a];
-            uint32_t c = a;
-            while (c > i && s_idx[c - 1u] > x) {
-                s_idx[c] = s_idx[c - 1u];
-                c--;
-            }
-            s_idx[c] = (uint16_t)x;
-        }
-    }
-    __syncthreads();
-    // values in sorted order into v[] (wave-major, as the items were laid
-    // out), read before any is overwritten, then out
-#pragma unroll
-    for (int j = 0; j < kBsItems; j++) {
-        const uint32_t i = wbase + (uint32_t)j * 64u + (uint32_t)lane;
-        v[j] = (uint32_t)j < iw && i < size ? vals[start + s_idx[i]] : 0u;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < kBsItems; j++) {
-        const uint32_t i = wbase + (uint32_t)j * 64u + (uint32_t)lane;
-        if ((uint32_t)j < iw && i < size) vals[start + i] = v[j];
-    }
-    return true;
-}
-
 // One chunk of cum_tiles_hit: vv holds the chunk's sorted values (cnt <=
 // kBsCap of them, wave-major items, ipt per lane); out[e] = offset + the
 // workgroup's sum of `part` + the inclusive prefix sum of weight[vv] through
 // chunk element e (a wave scan per item row, the waves' totals and shares of
 // `part` through LDS).  Returns the chunk's weight plus the sum of `part`.
-__device__ uint32_t cum_chunk(const uint32_t (&vv)[kBsItems], uint32_t ipt, uint32_t cnt,
+template <int N>
+__device__ uint32_t cum_chunk_w(uint32_t (&w)[N], uint32_t ipt, uint32_t cnt, uint32_t* __restrict__ out,
+                                uint32_t offset, uint32_t part, uint32_t* s_w);
+
+template <int N>
+__device__ uint32_t cum_chunk(const uint32_t (&vv)[N], uint32_t ipt, uint32_t cnt,
                               const uint32_t* __restrict__ weight, uint32_t* __restrict__ out, uint32_t offset,
                               uint32_t part, uint32_t* s_w) {
+    // (every item's weight load issued before the first is used: vv holds a
+    // valid index, 0, past the chunk's end)
+    uint32_t w[N];
+#pragma unroll
+    for (int j = 0; j < N; j++)
+        if ((uint32_t)j < ipt) w[j] = weight[vv[j]];
+    return cum_chunk_w<N>(w, ipt, cnt, out, offset, part, s_w);
+}
+
+// cum_chunk from the weights of the chunk's sorted elements, w[j] (item j of
+// the lane, as vv above; entries past the chunk are ignored).
+template <int N>
+__device__ uint32_t cum_chunk_w(uint32_t (&w)[N], uint32_t ipt, uint32_t cnt, uint32_t* __restrict__ out,
+                                uint32_t offset, uint32_t part, uint32_t* s_w) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t wb = (uint32_t)wave * 64u * ipt;
-    uint32_t w[kBsItems];
 #pragma unroll
-    for (int j = 0; j < kBsItems; j++) {
+    for (int j = 0; j < N; j++) {
         const uint32_t e = wb + (uint32_t)j * 64u + (uint32_t)lane;
-        w[j] = (uint32_t)j < ipt && e < cnt ? weight[vv[j]] : 0u;
+        if ((uint32_t)j >= ipt || e >= cnt) w[j] = 0u;
     }
     uint32_t run = 0u;  // the wave's running total (uniform)
 #pragma unroll
-    for (int j = 0; j < kBsItems; j++) {
+    for (int j = 0; j < N; j++) {
         if ((uint32_t)j < ipt) {  // uniform
             const uint32_t x = wave_incl_add_u32(w[j]);
             w[j] = x + run;
@@ -801,20 +707,242 @@ __device__ uint32_t cum_chunk(const uint32_t (&vv)[kBsItems], uint32_t ipt, uint
     }
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < kBsItems; j++) {
+    for (int j = 0; j < N; j++) {
         const uint32_t e = wb + (uint32_t)j * 64u + (uint32_t)lane;
         if ((uint32_t)j < ipt && e < cnt) out[e] = offset + base + before + w[j];
     }
     return all + base;
 }
 
-// Workgroup b sorts bucket b = [offs[b], offs[b + 1]) (the last one ends at
-// the pair count) of (keys, vals) by the key bits below the top digit, writes
-// vals in place and cum[i] = the inclusive prefix sum of weight[vals[.]] over
-// the whole sorted order: the bucket's own prefix plus the weights of the
-// buckets before it, from the first pass's per-block digit sums wsum
-// [wsum_words / 256][256].  n and cap are the pair count and the key cap
-// (from n_dev / cap_dev when given).
+// Counting sort of a bucket of `size` <= IW * kBsThreads pairs by the low
+// `low` <= 15 bits of its keys, and everything the bucket needs after it.
+// Items are wave-major, IW per lane (element e = wave * 64 * IW + j * 64 +
+// lane), and every item loop is unrolled over IW with no per-item branch, so
+// each phase's loads and LDS operations are in flight together:
+//   * the keys (loads clamped into the bucket);
+//   * a histogram of the keys in packed 16-bit LDS counters (lanes past the
+//     bucket add 0 to a counter of their own) and its exclusive scan;
+//   * one returning LDS add per pair for its slot;
+//   * the runs of equal keys (a run of slots) put back in input order, each
+//     by the thread that holds its first slot, after every thread has read
+//     the keys around its slots at once;
+//   * the values and their weights (wts: the weights in the bucket's input
+//     order, which the top-digit pass wrote beside the values) gathered into
+//     sorted order from the bucket's own range, the values written in place,
+//     and cum_tiles_hit formed over the weights (cum_chunk_w).
+// Returns false, having written nothing, when a key occurs more than
+// kBsMaxRun times.  s_raw holds the counters (up to 16384 words), then each
+// slot's input position and key (16384 uint16_t each).
+template <int IW>
+__device__ bool bucket_counted(const uint32_t* __restrict__ keys, uint32_t* __restrict__ vals, uint32_t start,
+                               uint32_t size, uint32_t low, const uint32_t* __restrict__ wts,
+                               uint32_t* __restrict__ cum, uint32_t part, uint32_t* s_raw, uint32_t* s_tot,
+                               uint32_t* s_flag, uint32_t* s_w) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t wbase = (uint32_t)wave * 64u * IW;
+    uint32_t* words = s_raw;                                         // counters, two per word
+    uint16_t* s_idx = reinterpret_cast<uint16_t*>(s_raw + 16384);  // slot -> input position
+    uint16_t* s_bin = s_idx + kBsCap;                                // slot -> key
+    const uint32_t lowmask = (1u << low) - 1u;
+    const uint32_t nwords = 1u << (low - 1u);
+    // counter word i lives at word swz(i): the scan's threads each read 16
+    // consecutive words, which would put a wave's 64 lanes on 4 LDS banks;
+    // the swizzle (inside each aligned group of 16) spreads them over all
+    auto swz = [](uint32_t i) { return (i & ~15u) | ((i & 15u) ^ ((i >> 6) & 15u)); };
+    uint32_t k[IW];
+#pragma unroll
+    for (int j = 0; j < IW; j++) k[j] = keys[start + min(wbase + (uint32_t)j * 64u + (uint32_t)lane, size - 1u)];
+    for (uint32_t i = (uint32_t)tid; i < nwords; i += kBsThreads) words[i] = 0u;
+    if (tid == 0) *s_flag = 0u;
+    // an item's counter word and increment (past the bucket: 0, added to a
+    // word of the lane's own, so that no item needs a branch)
+    auto word_of = [&](int j) {
+        return wbase + (uint32_t)j * 64u + (uint32_t)lane < size ? swz(k[j] >> 1)
+                                                                 : swz((uint32_t)tid & (nwords - 1u));
+    };
+    auto inc_of = [&](int j) {
+        return wbase + (uint32_t)j * 64u + (uint32_t)lane < size ? 1u << ((k[j] & 1u) * 16u) : 0u;
+    };
+#pragma unroll
+    for (int j = 0; j < IW; j++) k[j] &= lowmask;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < IW; j++) atomicAdd(&words[word_of(j)], inc_of(j));
+    __syncthreads();
+    // exclusive scan of the counters (thread t: words [t * wpt, (t + 1) * wpt))
+    // and the largest count
+    const uint32_t wpt = (nwords + kBsThreads - 1u) / kBsThreads;  // <= 16
+    uint32_t loc[16], sum = 0u, mx = 0u;
+#pragma unroll
+    for (uint32_t w = 0; w < 16u; w++) loc[w] = words[swz(min((uint32_t)tid * wpt + w, nwords - 1u))];
+#pragma unroll
+    for (uint32_t w = 0; w < 16u; w++) {
+        if (w >= wpt || (uint32_t)tid * wpt + w >= nwords) loc[w] = 0u;
+        const uint32_t lo = loc[w] & 0xFFFFu, hi = loc[w] >> 16;
+        sum += lo + hi;
+        mx = max(mx, max(lo, hi));
+    }
+    if (mx > kBsMaxRun) *s_flag = 1u;
+    uint32_t all;
+    uint32_t run = block_exclusive_scan<kBsThreads>(sum, s_tot, &all);
+#pragma unroll
+    for (uint32_t w = 0; w < 16u; w++) {
+        const uint32_t i = (uint32_t)tid * wpt + w;
+        if (w < wpt && i < nwords) {
+            const uint32_t lo = loc[w] & 0xFFFFu, hi = loc[w] >> 16;
+            words[swz(i)] = run | ((run + lo) << 16);
+            run += lo + hi;
+        }
+    }
+    __syncthreads();
+    if (*s_flag) return false;  // uniform: a run too long for one thread
+    // every pair takes its key's next slot (any order among equal keys)
+    uint32_t slot[IW];
+#pragma unroll
+    for (int j = 0; j < IW; j++) {
+        const uint32_t half = (k[j] & 1u) * 16u;
+        slot[j] = (atomicAdd(&words[word_of(j)], inc_of(j)) >> half) & 0xFFFFu;
+    }
+#pragma unroll
+    for (int j = 0; j < IW; j++) {
+        const uint32_t e = wbase + (uint32_t)j * 64u + (uint32_t)lane;
+        if (e < size) {
+            s_idx[slot[j]] = (uint16_t)e;
+            s_bin[slot[j]] = (uint16_t)k[j];
+        }
+    }
+    __syncthreads();
+    // runs of equal keys into input order: thread t looks at slots t + q *
+    // kBsThreads, reading the keys of up to eight slots and of their
+    // neighbours at once
+    constexpr int RQ = IW < 8 ? IW : 8;
+#pragma unroll
+    for (int q0 = 0; q0 < IW; q0 += RQ) {
+        uint32_t bq[RQ], bl[RQ], br[RQ];
+#pragma unroll
+        for (int q = 0; q < RQ; q++) {
+            const uint32_t i = min((uint32_t)tid + (uint32_t)(q0 + q) * kBsThreads, size - 1u);
+            bq[q] = s_bin[i];
+            bl[q] = s_bin[i ? i - 1u : 0u];
+            br[q] = s_bin[min(i + 1u, size - 1u)];
+        }
+#pragma unroll
+        for (int q = 0; q < RQ; q++) {
+            const uint32_t i = (uint32_t)tid + (uint32_t)(q0 + q) * kBsThreads;
+            if (i + 1u < size && br[q] == bq[q] && (i == 0u || bl[q] != bq[q])) {
+                uint32_t r = 2u;
+                while (i + r < size && s_bin[i + r] == bq[q]) r++;
+                for (uint32_t a = i + 1u; a < i + r; a++) {
+                    const uint32_t x = s_idx[a];
+                    uint32_t c = a;
+                    while (c > i && s_idx[c - 1u] > x) {
+                        s_idx[c] = s_idx[c - 1u];
+                        c--;
+                    }
+                    s_idx[c] = (uint16_t)x;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    // values and weights in sorted order (past the bucket: the last slot's),
+    // read before any value is overwritten, then out
+    uint32_t v[IW], w[IW];
+#pragma unroll
+    for (int j = 0; j < IW; j++) v[j] = s_idx[min(wbase + (uint32_t)j * 64u + (uint32_t)lane, size - 1u)];
+#pragma unroll
+    for (int j = 0; j < IW; j++) {
+        w[j] = wts[start + v[j]];
+        v[j] = vals[start + v[j]];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < IW; j++) {
+        const uint32_t i = wbase + (uint32_t)j * 64u + (uint32_t)lane;
+        if (i < size) vals[start + i] = v[j];
+    }
+    // cum_tiles_hit from the sorted weights
+    cum_chunk_w<IW>(w, IW, size, cum + start, 0u, part, s_w);
+    return true;
+}
+
+// Bucket b = [offs[b], offs[b + 1]) (the last one ends at the pair count; n
+// and cap are the pair count and the key cap, from n_dev / cap_dev when
+// given) and its key bits below the top digit.
+struct BucketSpan {
+    uint32_t start, size, low;
+};
+__device__ __forceinline__ BucketSpan bucket_span(uint32_t b, const uint32_t* __restrict__ offs, uint32_t n,
+                                                  const uint32_t* __restrict__ n_dev, uint32_t cap,
+                                                  const uint32_t* __restrict__ cap_dev) {
+    if (n_dev) n = min(n, *n_dev);
+    if (cap_dev) cap = *cap_dev;
+    const uint32_t end = min(n, b + 1u < kBsBuckets ? offs[b + 1] : n);
+    const uint32_t start = min(offs[b], end);
+    return BucketSpan{start, end - start, top_digit_shift(cap)};
+}
+
+// This thread's share of the weights of the buckets before bucket b: the
+// first pass's per-block digit sums wsum[wsum_words / 256][256] over the
+// blocks and the digits below b (summed over the workgroup by cum_chunk;
+// eight loads in flight per round, at clamped indices).
+__device__ __forceinline__ uint32_t bucket_part(uint32_t b, const uint32_t* __restrict__ wsum, uint32_t wsum_words) {
+    const uint32_t tid = threadIdx.x;
+    uint32_t part = 0u;
+    if ((tid & (kBsBuckets - 1u)) < b && wsum_words) {
+        for (uint32_t i0 = tid; i0 < wsum_words; i0 += 8u * kBsThreads) {
+            uint32_t x[8];
+#pragma unroll
+            for (int q = 0; q < 8; q++) x[q] = wsum[min(i0 + (uint32_t)q * kBsThreads, wsum_words - 1u)];
+#pragma unroll
+            for (int q = 0; q < 8; q++) part += i0 + (uint32_t)q * kBsThreads < wsum_words ? x[q] : 0u;
+        }
+    }
+    return part;
+}
+
+// Workgroup b counts bucket b into order (bucket_counted, with wts the
+// weights in the order of the top-digit pass's output) when its keys have
+// 1 to 15 bits below the top digit and it holds at most kBcItems pairs a
+// lane, and sets done[b] (also for an empty bucket); otherwise, or when a
+// key occurs too often, it writes nothing but done[b] = 0 and
+// bucket_sort_kernel sorts the bucket.
+constexpr uint32_t kBcItems = 8;  // (12 or 16 items a lane spill registers)
+__global__ __launch_bounds__(kBsThreads) void bucket_count_kernel(const uint32_t* __restrict__ keys,
+                                                                   uint32_t* __restrict__ vals,
+                                                                   const uint32_t* __restrict__ offs, uint32_t n,
+                                                                   const uint32_t* __restrict__ n_dev, uint32_t cap,
+                                                                   const uint32_t* __restrict__ cap_dev,
+                                                                   const uint32_t* __restrict__ wts,
+                                                                   const uint32_t* __restrict__ wsum,
+                                                                   uint32_t wsum_words, uint32_t* __restrict__ cum,
+                                                                   uint32_t* __restrict__ done) {
+    // the counters (up to 16384 words), then each slot's input position and
+    // key (16384 uint16_t each)
+    __shared__ uint32_t s_raw[2 * kBsCap];
+    __shared__ uint32_t s_tot[kBsWaves];
+    __shared__ uint32_t s_w[2 * kBsWaves];
+    __shared__ uint32_t s_flag;
+    const uint32_t b = blockIdx.x;
+    const BucketSpan sp = bucket_span(b, offs, n, n_dev, cap, cap_dev);
+    bool ok = sp.size == 0u;
+    if (sp.size && sp.low > 0u && sp.low <= kBsCountBits && sp.size <= kBcItems * kBsThreads) {
+        const uint32_t part = bucket_part(b, wsum, wsum_words);
+        const uint32_t iw = (sp.size + kBsThreads - 1u) / kBsThreads;
+        if (iw <= 4u)
+            ok = bucket_counted<4>(keys, vals, sp.start, sp.size, sp.low, wts, cum, part, s_raw, s_tot, &s_flag, s_w);
+        else
+            ok = bucket_counted<kBcItems>(keys, vals, sp.start, sp.size, sp.low, wts, cum, part, s_raw, s_tot,
+                                          &s_flag, s_w);
+    }
+    if (threadIdx.x == 0) done[b] = ok ? 1u : 0u;
+}
+
+// Workgroup b sorts bucket b, unless bucket_count_kernel has (done[b]), stably
+// by the key bits below the top digit in 8-bit LSD passes, writes vals in
+// place and cum[i] = the inclusive prefix sum of weight[vals[.]] over the
+// whole sorted order: the bucket's own prefix plus the weights of the buckets
+// before it (bucket_part).
 __global__ __launch_bounds__(kBsThreads) void bucket_sort_kernel(uint32_t* __restrict__ keys,
                                                                   uint32_t* __restrict__ vals,
                                                                   const uint32_t* __restrict__ offs, uint32_t n,
@@ -824,9 +952,9 @@ __global__ __launch_bounds__(kBsThreads) void bucket_sort_kernel(uint32_t* __res
                                                                   const uint32_t* __restrict__ wsum,
                                                                   uint32_t wsum_words, uint32_t* __restrict__ cum,
                                                                   uint32_t* __restrict__ tmp_k,
-                                                                  uint32_t* __restrict__ tmp_v) {
-    // LSD passes: keys, values and per-wave histograms; counting path: bins,
-    // slots and keys (bucket_count_sort)
+                                                                  uint32_t* __restrict__ tmp_v,
+                                                                  const uint32_t* __restrict__ done) {
+    // keys, values and per-wave histograms
     __shared__ uint32_t s_raw[2 * kBsCap + kBsWaves * kRadix];
     uint32_t* s_k = s_raw;
     uint32_t* s_v = s_raw + kBsCap;
@@ -834,78 +962,63 @@ __global__ __launch_bounds__(kBsThreads) void bucket_sort_kernel(uint32_t* __res
     __shared__ uint32_t s_start[kRadix], s_cnt[kRadix], s_run[kRadix];
     __shared__ uint32_t s_tot[kBsWaves];
     __shared__ uint32_t s_w[2 * kBsWaves];
-    __shared__ uint32_t s_flag;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t b = blockIdx.x;
-    if (n_dev) n = min(n, *n_dev);
-    if (cap_dev) cap = *cap_dev;
-    const uint32_t low = top_digit_shift(cap);  // key bits below the top digit
-    const uint32_t end = min(n, b + 1u < kBsBuckets ? offs[b + 1] : n);
-    const uint32_t start = min(offs[b], end);
-    if (end == start) return;
-    const uint32_t size = end - start, passes = (low + 7u) / 8u;
+    if (done[b]) return;
+    const BucketSpan sp = bucket_span(b, offs, n, n_dev, cap, cap_dev);
+    if (sp.size == 0u) return;
+    const uint32_t start = sp.start, size = sp.size, low = sp.low, passes = (low + 7u) / 8u;
     uint32_t k[kBsItems], v[kBsItems], pos[kBsItems];
-    // the weights of the buckets before this one: wsum[block][digit] summed
-    // over the blocks and the digits below b
-    // over the blocks and the digits below b (this thread's share; summed
-    // over the workgroup by bucket_cum)
-    uint32_t part = 0u;
-    for (uint32_t i = (uint32_t)tid; i < wsum_words; i += kBsThreads) part += (i & (kBsBuckets - 1u)) < b ? wsum[i] : 0u;
+    const uint32_t part = bucket_part(b, wsum, wsum_words);
 
     if (size <= kBsCap) {
-        // the whole bucket in registers: counted into order, or reordered
-        // through LDS by each LSD pass
+        // the whole bucket in registers, reordered through LDS by each LSD pass
         const uint32_t iw = (size + kBsThreads - 1u) / kBsThreads;
-        const uint32_t wbase = (uint32_t)wave * 64u * iw;
-#pragma unroll
-        for (int j = 0; j < kBsItems; j++) {
-            if ((uint32_t)j >= iw) break;
-            const uint32_t e = wbase + (uint32_t)j * 64u + (uint32_t)lane;
-            k[j] = e < size ? keys[start + e] : 0u;
-        }
-        const bool counted = low > 0u && low <= kBsCountBits &&
-                             bucket_count_sort(k, v, iw, size, low, start, vals, s_raw, s_tot, &s_flag);
-        if (!counted) {
+        {
+            const uint32_t wbase = (uint32_t)wave * 64u * iw;
 #pragma unroll
             for (int j = 0; j < kBsItems; j++) {
-                if ((uint32_t)j >= iw) break;
-                const uint32_t e = wbase + (uint32_t)j * 64u + (uint32_t)lane;
-                v[j] = e < size ? vals[start + e] : 0u;
-            }
-        }
-        for (uint32_t p = 0; p < (counted ? 0u : passes); p++) {
-            const uint32_t sh = 8u * p, bits = min(8u, low - sh);
-            bucket_rank(k, pos, iw, size, sh, bits, s_hist, s_start, s_cnt, s_tot);
-#pragma unroll
-            for (int j = 0; j < kBsItems; j++) {
-                if ((uint32_t)j >= iw) break;
-                if (wbase + (uint32_t)j * 64u + (uint32_t)lane < size) {
-                    s_k[pos[j]] = k[j];
-                    s_v[pos[j]] = v[j];
+                if ((uint32_t)j < iw) {
+                    const uint32_t e = wbase + (uint32_t)j * 64u + (uint32_t)lane;
+                    k[j] = e < size ? keys[start + e] : 0u;
+                    v[j] = e < size ? vals[start + e] : 0u;
                 }
             }
-            __syncthreads();
+            for (uint32_t p = 0; p < passes; p++) {
+                const uint32_t sh = 8u * p, bits = min(8u, low - sh);
+                bucket_rank(k, pos, iw, size, sh, bits, s_hist, s_start, s_cnt, s_tot);
+#pragma unroll
+                for (int j = 0; j < kBsItems; j++) {
+                    if ((uint32_t)j < iw) {
+                        if (wbase + (uint32_t)j * 64u + (uint32_t)lane < size) {
+                            s_k[pos[j]] = k[j];
+                            s_v[pos[j]] = v[j];
+                        }
+                    }
+                }
+                __syncthreads();
+#pragma unroll
+                for (int j = 0; j < kBsItems; j++) {
+                    if ((uint32_t)j < iw) {
+                        const uint32_t e = wbase + (uint32_t)j * 64u + (uint32_t)lane;
+                        if (e < size) {
+                            k[j] = s_k[e];
+                            v[j] = s_v[e];
+                        }
+                    }
+                }
+                __syncthreads();
+            }
 #pragma unroll
             for (int j = 0; j < kBsItems; j++) {
-                if ((uint32_t)j >= iw) break;
-                const uint32_t e = wbase + (uint32_t)j * 64u + (uint32_t)lane;
-                if (e < size) {
-                    k[j] = s_k[e];
-                    v[j] = s_v[e];
+                if ((uint32_t)j < iw) {
+                    const uint32_t e = wbase + (uint32_t)j * 64u + (uint32_t)lane;
+                    if (e < size) vals[start + e] = v[j];
                 }
             }
-            __syncthreads();
+            // cum_tiles_hit from the sorted values still in registers
+            cum_chunk(v, iw, size, weight, cum + start, 0u, part, s_w);
         }
-        if (!counted) {
-#pragma unroll
-            for (int j = 0; j < kBsItems; j++) {
-                if ((uint32_t)j >= iw) break;
-                const uint32_t e = wbase + (uint32_t)j * 64u + (uint32_t)lane;
-                if (e < size) vals[start + e] = v[j];
-            }
-        }
-        // cum_tiles_hit from the sorted values still in registers
-        cum_chunk(v, iw, size, weight, cum + start, 0u, part, s_w);
     } else {
         // A bucket above the LDS capacity: each pass counts the bucket's digits,
         // then ranks its chunks in order and writes every pair to the digit's
@@ -928,20 +1041,22 @@ __global__ __launch_bounds__(kBsThreads) void bucket_sort_kernel(uint32_t* __res
                 const uint32_t wbase = (uint32_t)wave * 64u * iw;
     #pragma unroll
                 for (int j = 0; j < kBsItems; j++) {
-                    if ((uint32_t)j >= iw) break;
-                    const uint32_t e = wbase + (uint32_t)j * 64u + (uint32_t)lane;
-                    k[j] = e < cnt ? src_k[start + c0 + e] : 0u;
-                    v[j] = e < cnt ? src_v[start + c0 + e] : 0u;
+                    if ((uint32_t)j < iw) {
+                        const uint32_t e = wbase + (uint32_t)j * 64u + (uint32_t)lane;
+                        k[j] = e < cnt ? src_k[start + c0 + e] : 0u;
+                        v[j] = e < cnt ? src_v[start + c0 + e] : 0u;
+                    }
                 }
                 bucket_rank(k, pos, iw, cnt, sh, bits, s_hist, s_start, s_cnt, s_tot);
     #pragma unroll
                 for (int j = 0; j < kBsItems; j++) {
-                    if ((uint32_t)j >= iw) break;
-                    if (wbase + (uint32_t)j * 64u + (uint32_t)lane < cnt) {
-                        const uint32_t d = (k[j] >> sh) & dmask;
-                        const uint32_t dst = start + s_run[d] + (pos[j] - s_start[d]);
-                        dst_k[dst] = k[j];
-                        dst_v[dst] = v[j];
+                    if ((uint32_t)j < iw) {
+                        if (wbase + (uint32_t)j * 64u + (uint32_t)lane < cnt) {
+                            const uint32_t d = (k[j] >> sh) & dmask;
+                            const uint32_t dst = start + s_run[d] + (pos[j] - s_start[d]);
+                            dst_k[dst] = k[j];
+                            dst_v[dst] = v[j];
+                        }
                     }
                 }
                 __syncthreads();
@@ -963,10 +1078,11 @@ __global__ __launch_bounds__(kBsThreads) void bucket_sort_kernel(uint32_t* __res
             const uint32_t wbase = (uint32_t)wave * 64u * iw;
 #pragma unroll
             for (int j = 0; j < kBsItems; j++) {
-                if ((uint32_t)j >= iw) break;
-                const uint32_t e = wbase + (uint32_t)j * 64u + (uint32_t)lane;
-                v[j] = e < cnt ? src_v[start + c0 + e] : 0u;
-                if (e < cnt && src_v != vals) vals[start + c0 + e] = v[j];
+                if ((uint32_t)j < iw) {
+                    const uint32_t e = wbase + (uint32_t)j * 64u + (uint32_t)lane;
+                    v[j] = e < cnt ? src_v[start + c0 + e] : 0u;
+                    if (e < cnt && src_v != vals) vals[start + c0 + e] = v[j];
+                }
             }
             carry += cum_chunk(v, iw, cnt, weight, cum + start + c0, carry, c0 == 0u ? part : 0u, s_w);
         }
@@ -1130,27 +1246,38 @@ bh_status depth_sort_buckets(bh_ctx* ctx, const uint32_t* keys_in, uint32_t n, u
     uint32_t* blk = (uint32_t*)scratch;
     uint32_t* wsum = blk + blk_words;
     uint32_t* offs = wsum + blk_words;
+    // the buckets bucket_count_kernel sorted, after the offsets
+    uint32_t* done = offs + (size_t)sp.parts * sp.radix;
+    if ((2 * blk_words + (size_t)sp.parts * sp.radix + kBsBuckets) * 4 > radix_sort_scratch_bytes(n, 32))
+        return set_error(ctx, BH_ERR_INTERNAL, "depth sort: scratch too small for the bucket flags");
     if (!scratch_zeroed) launch_fill_u32(ctx, blk, 0u, 2 * blk_words);
     SortDevice d = dev;
     d.weight = weight;
     d.wsum = wsum;
-    // the top-digit pass: keys to keys_tmp, values (input indices) to vals_out
+    // the top-digit pass: keys to keys_tmp, values (input indices) to
+    // vals_out, their weights beside them to tmp_vals (read by the count
+    // kernel; the LSD kernel's larger buckets reuse their own ranges of it)
     bh_status st;
     if (sp.items == 8)
         st = sort_pass<true, 8>(ctx, sp, "depth_sort_up", "depth_sort_scan", "depth_sort_onesweep", keys_in, 4,
-                                nullptr, keys_tmp, 4, vals_out, n, kShiftTop, 8u, key_sub, key_cap, offs, blk, nullptr,
-                                nullptr, d);
+                                nullptr, keys_tmp, 4, vals_out, n, kShiftTop, 8u, key_sub, key_cap, offs, blk, weight,
+                                tmp_vals, d);
     else
         st = sort_pass<true, 4>(ctx, sp, "depth_sort_up", "depth_sort_scan", "depth_sort_onesweep", keys_in, 4,
-                                nullptr, keys_tmp, 4, vals_out, n, kShiftTop, 8u, key_sub, key_cap, offs, blk, nullptr,
-                                nullptr, d);
+                                nullptr, keys_tmp, 4, vals_out, n, kShiftTop, 8u, key_sub, key_cap, offs, blk, weight,
+                                tmp_vals, d);
     if (st != BH_OK) return st;
     {
-        KernelTimer t(ctx, "depth_sort_buckets");
         const uint32_t n_rest = dev.drop_capped ? std::min(n, dev.n_rest_host) : n;
+        const uint32_t* n_dev = dev.drop_capped ? dev.n_rest : dev.n;
+        {
+            KernelTimer t(ctx, "depth_sort_count");
+            launch(ctx, bucket_count_kernel, dim3(kBsBuckets), dim3(kBsThreads), 0u, keys_tmp, vals_out, offs, n_rest,
+                   n_dev, key_cap, dev.key_cap, (const uint32_t*)tmp_vals, wsum, (uint32_t)blk_words, cum, done);
+        }
+        KernelTimer t(ctx, "depth_sort_buckets");
         launch(ctx, bucket_sort_kernel, dim3(kBsBuckets), dim3(kBsThreads), 0u, keys_tmp, vals_out, offs, n_rest,
-               dev.drop_capped ? dev.n_rest : dev.n, key_cap, dev.key_cap, weight, wsum, (uint32_t)blk_words, cum,
-               tmp_keys, tmp_vals);
+               n_dev, key_cap, dev.key_cap, weight, wsum, (uint32_t)blk_words, cum, tmp_keys, tmp_vals, done);
     }
     return check_launch(ctx, "depth sort");
 }

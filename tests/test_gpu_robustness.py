@@ -190,7 +190,7 @@ def test_mostly_culled_scene_sorts_only_visible(gpu):
         compare_forward(g, o)
 
 
-@pytest.mark.parametrize("case", ["crowded_bucket", "one_depth", "chunked_bucket", "wide_range"])
+@pytest.mark.parametrize("case", ["crowded_bucket", "one_depth", "chunked_bucket", "wide_range", "counted_sizes"])
 def test_depth_sort_bucket_extremes(gpu, case):
     """The depth sort's bucket path (one pass by the top 8 bits of the key
     range, then each bucket sorted by one workgroup) at its extremes, and the
@@ -204,7 +204,13 @@ def test_depth_sort_bucket_extremes(gpu, case):
       over [4, 6], so one or two buckets of ~40k pairs are sorted in chunks
       by the key bits below the top digit;
     * wide_range: depths from ~0.3 to ~50 (a key range above 24 bits), which
-      takes the LSD passes; the second run queues them from the plan."""
+      takes the LSD passes; the second run queues them from the plan;
+    * counted_sizes: depths in [4, 6] (15 key bits below the top digit, so a
+      bucket is 1/64 of depth wide and is counted), with buckets of ~3k, ~7k
+      and ~11k pairs (4, 8 and 12 items a lane), one of ~14k (more than 12 a
+      lane: the LSD passes), runs of 2 to 20 equal depths (put back in input
+      order), and a small bucket with 40 equal depths (longer than a counted
+      run may be: that bucket takes the LSD passes)."""
     print(f"[case] depth sort buckets: {case}", flush=True)
     cam = _cam()
     if case == "crowded_bucket":
@@ -216,6 +222,22 @@ def test_depth_sort_bucket_extremes(gpu, case):
     elif case == "chunked_bucket":
         tr, sh, op = rng_scene(60_000, 1.0, (-5.0, -4.0), (0.0, 3.0), 0xD7)
         tr[:40_000, 2] = np.linspace(0.0, 1e-3, 40_000, dtype=np.float32)[np.random.default_rng(3).permutation(40_000)]
+    elif case == "counted_sizes":
+        rng = np.random.default_rng(5)
+        # the key range from 4 to 6 exactly: 2^22 keys, 15 bits below the top digit
+        parts = [np.array([4.0, 6.0]), rng.uniform(4.0, 5.999, 20_000)]
+        for b, cnt in ((10, 3_000), (30, 7_000), (50, 11_000), (70, 14_000)):
+            parts.append(4.0 + (b + rng.uniform(0.02, 0.98, cnt)) / 64.0)
+        # runs of equal depths inside the 7k bucket, and 40 equal ones in a small bucket
+        for r in range(2, 21):
+            parts.append(np.full(r, 4.0 + (30 + 0.01 * r + 0.05) / 64.0))
+        parts.append(np.full(40, 4.0 + (90 + 0.5) / 64.0))
+        depth = np.concatenate(parts).astype(np.float32)
+        depth = depth[rng.permutation(depth.shape[0])]
+        tr, sh, op = rng_scene(depth.shape[0], 1.0, (-5.0, -4.0), (0.0, 3.0), 0xD9)
+        z = depth - 5.0
+        tr[:, 0:2] *= ((z + 5.0) / 5.0)[:, None]
+        tr[:, 2] = z
     else:
         tr, sh, op = rng_scene(60_000, 1.0, (-5.0, -4.0), (0.0, 3.0), 0xD8)
         # depth z + 5 from ~0.3 to ~50, the x, y spread with it so they stay on screen
